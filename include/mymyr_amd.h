@@ -1,0 +1,154 @@
+/* mymyr_amd: the MI355X-native state-expansion path of a lifted classical planner (applicable-action testing,
+ * effect application on packed u64 bitset states, goal and reward evaluation, 64-bit state hashing and device
+ * dedup), exposed as a C ABI: plain pointers and sizes, int status returns, no Python or torch types.
+ *
+ * Conventions
+ *   - Every function returns 0 on success and a negative value on failure; mya_last_error() then holds the message
+ *     (thread-local). Argument errors name the argument, as the reference's "mymyr: ..." exceptions do
+ *     (src/mymyr/rl/env.cpp:102-135).
+ *   - Pointers documented "device" are HIP device memory; "stream" is a hipStream_t (null: the default stream).
+ *     Calls on a stream are asynchronous unless documented otherwise.
+ *   - States are rows of `words` little-endian u64 words; slot i is bit i & 63 of word i >> 6 (the reference's state
+ *     contract, include/mymyr/core/bitset.hpp:2-5).
+ *   - Caller-owned output arrays that are null are not written (include/mymyr/rl/env.hpp:137).
+ */
+#ifndef MYMYR_AMD_H
+#define MYMYR_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mya_task mya_task;
+typedef struct mya_env mya_env;
+typedef struct mya_hashset mya_hashset;
+
+/* ---------------------------------------------------------------------------------------------------------- misc */
+
+/* The last error message of the calling thread ("" if none). */
+const char* mya_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+#define MYA_ABI_VERSION 1
+int mya_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------------------- tasks */
+
+/* Atom slot modes (reference TaskOptions::Atoms, include/mymyr/task/task.hpp:88-101). */
+#define MYA_ATOMS_AUTO 0
+#define MYA_ATOMS_REACHABLE 1
+#define MYA_ATOMS_DENSE 2
+
+/* Loads a task from the reference's text format (replaces Task::from_text_file / Task::create over
+ * read_task_text, include/mymyr/task/task.hpp:166-167, include/mymyr/formalism/text_format.hpp:23-24).
+ * Host-only: compiles the canonical layout, atom slots, initial state, goal and the device tables. */
+int mya_task_load_text(const char* text, size_t len, int atoms, mya_task** out);
+int mya_task_load_file(const char* path, int atoms, mya_task** out);
+void mya_task_free(mya_task* task);
+
+typedef struct mya_task_info
+{
+    uint32_t words;         /* state words W (Task::words(), at least 1) */
+    uint32_t fluent_slots;  /* atom slots */
+    uint32_t atom_mode;     /* 0 reachable, 1 dense (AtomMode) */
+    uint32_t num_schemas;
+    uint32_t label_width;   /* largest schema arity */
+    uint32_t num_objects;
+    uint32_t max_arity;     /* largest fluent predicate arity */
+    uint32_t goal_unsat;    /* the goal can never hold */
+    uint64_t dense_fluent;  /* size of the typed-dense canonical fluent space */
+    uint64_t reachable_fluent; /* relaxed-reachable fluent atoms (0 when not computed: dense option) */
+    uint32_t view_words;    /* per-state device view size in u64 words */
+    uint32_t reserved;
+} mya_task_info;
+
+int mya_task_info_get(const mya_task* task, mya_task_info* out);
+
+/* Slot records: rec [fluent_slots, 1 + max(1, max_arity)] u32 = predicate then arguments (zero padded);
+ * cid [fluent_slots] u64 canonical ids (AtomIndex::record / canonical, include/mymyr/task/atom_index.hpp:167-172).
+ * Either may be null. */
+int mya_task_slots(const mya_task* task, uint32_t* rec, uint64_t* cid);
+
+/* The initial state, zero padded to `words` (>= the task's words). Host memory. */
+int mya_task_initial(const mya_task* task, uint64_t* row, uint32_t words);
+
+/* ---------------------------------------------------------------------------------------------------------- hashing */
+
+/* hash_state of `n` rows of `words` words: the reference's public state hash over the trimmed words
+ * (hash::state, include/mymyr/core/hash.hpp:56-60; device hash_rows, python/src/cuda_bindings.cpp:1289-1320).
+ * rows, out: device. */
+int mya_hash_rows(const uint64_t* rows, uint64_t n, uint32_t words, uint64_t* out, void* stream);
+
+/* Host versions (C API hash_words, include/mymyr/ext.h:104). */
+uint64_t mya_hash_words(const uint64_t* w, uint32_t n, uint64_t seed);
+uint64_t mya_hash_state(const uint64_t* w, uint32_t n);
+
+/* Philox-4x32-10 block of (seed; draw, env, purpose) and the random-policy index (include/mymyr/rl/rng.hpp:45-83),
+ * host versions of the device code. */
+void mya_philox(uint64_t seed, uint64_t env, uint64_t draw, uint32_t purpose, uint32_t out[4]);
+uint32_t mya_successor_index(uint64_t seed, uint64_t env, uint64_t draw, uint32_t count);
+
+/* ---------------------------------------------------------------------------------------------------------- state set */
+
+/* A device-resident open-addressing set of rows of `words` words with capacity ceil(max_states / max_load) slots
+ * (replaces the state_set launchers, include/mymyr/cuda/state_set.hpp:52-91). batch: the most rows one insert
+ * processes at once (larger inserts are split). */
+int mya_hashset_create(uint64_t max_states, uint32_t words, double max_load, uint64_t batch, mya_hashset** out);
+void mya_hashset_free(mya_hashset* set);
+
+/* Inserts n rows (device). ids (device, optional) receives each row's state id (the first-inserted equal row's id:
+ * smallest batch index wins within a batch, new ids in row order); is_new (device, optional) 1 for rows that added a
+ * state. new_count (host, optional) receives the number of new states. Synchronizes the stream. */
+int mya_hashset_insert(mya_hashset* set, const uint64_t* rows, uint64_t n, int64_t* ids, uint8_t* is_new,
+                       uint64_t* new_count, void* stream);
+int mya_hashset_size(const mya_hashset* set, uint64_t* size);
+/* Device pointer to the stored rows [size, words] in id order. */
+int mya_hashset_rows(const mya_hashset* set, const uint64_t** rows);
+int mya_hashset_clear(mya_hashset* set, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------- BrFS */
+
+/* Options of brfs(Task, BrfsOptions) (include/mymyr/search/brfs.hpp:62-101) that the device search takes. */
+typedef struct mya_brfs_options
+{
+    uint32_t max_depth;      /* expand only states of depth < max_depth (UINT32_MAX: unbounded) */
+    int32_t witness_pruning; /* reference default 1 */
+    uint64_t max_states;     /* stop (OutOfStates) once this many states are stored (UINT64_MAX: unbounded) */
+    uint64_t max_expanded;   /* stop before the expansion that would exceed this many (UINT64_MAX: unbounded) */
+    int32_t stop_at_goal;    /* reference default 1 */
+    int32_t fingerprint;     /* compute BrfsResult::fingerprint */
+    uint64_t chunk;          /* candidates per device batch (0: automatic) */
+    uint64_t memory_states;  /* state capacity when max_states is unbounded (0: 2^26) */
+} mya_brfs_options;
+
+/* BrfsResult fields (include/mymyr/search/brfs.hpp:103-138). status: the reference's SearchStatus codes
+ * (0 solved, 1 exhausted, 2 out of states, 5 failed, 6 unsolvable). */
+typedef struct mya_brfs_result
+{
+    int32_t status;
+    int32_t solved;
+    int32_t exhausted;
+    uint32_t layers;
+    uint64_t states;
+    uint64_t expanded;
+    uint64_t generated;
+    uint64_t goal_states;
+    uint64_t fingerprint;
+    int64_t first_goal; /* id of the first goal state tested (-1: none) */
+    double search_s;    /* wall time of the whole call */
+    double device_s;    /* wall time from the start state's insert to the end of the search */
+} mya_brfs_result;
+
+/* Layer-synchronous BrFS on the current device (replaces brfs(), include/mymyr/search/brfs.hpp:140, and
+ * cuda::brfs, include/mymyr/cuda/brfs.hpp:89-123). layer_counts [cap, 3] (host, optional) receives
+ * {expanded, generated, new} per expanded layer. Returns the number of layers, or -1. Synchronous. */
+int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts,
+             uint32_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,166 @@
+"""ctypes binding of libmymyr_amd.so (the C ABI declared in include/mymyr_amd.h).
+
+The library is built in-tree (``make -C mymyr_amd``); importing this module without it raises ImportError, so no
+caller can silently run without the HIP path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int64, c_size_t, c_uint8, c_uint32, c_uint64, c_void_p
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
+
+
+class MyaError(RuntimeError):
+    """A failed mymyr_amd call; the message is the library's mya_last_error()."""
+
+
+class TaskInfo(Structure):
+    _fields_ = [
+        ("words", c_uint32),
+        ("fluent_slots", c_uint32),
+        ("atom_mode", c_uint32),
+        ("num_schemas", c_uint32),
+        ("label_width", c_uint32),
+        ("num_objects", c_uint32),
+        ("max_arity", c_uint32),
+        ("goal_unsat", c_uint32),
+        ("dense_fluent", c_uint64),
+        ("reachable_fluent", c_uint64),
+        ("view_words", c_uint32),
+        ("reserved", c_uint32),
+    ]
+
+
+class EnvConfig(Structure):
+    _fields_ = [
+        ("seed", c_uint64),
+        ("max_steps", c_uint32),
+        ("step_reward", ctypes.c_float),
+        ("goal_reward", ctypes.c_float),
+        ("dead_end_reward", ctypes.c_float),
+        ("dead_end", c_int32),
+        ("dead_end_terminal", c_int32),
+        ("autoreset", c_int32),
+        ("canonical_order", c_int32),
+        ("witness_pruning", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+class EnvBatch(Structure):
+    _fields_ = [
+        ("states", c_void_p),
+        ("rows", c_uint64),
+        ("words", c_uint32),
+        ("reserved", c_uint32),
+        ("steps", c_void_p),
+        ("draws", c_void_p),
+        ("at_goal", c_void_p),
+        ("first_env", c_uint64),
+    ]
+
+
+class StepOutputs(Structure):
+    _fields_ = [
+        ("reward", c_void_p),
+        ("terminated", c_void_p),
+        ("truncated", c_void_p),
+        ("count", c_void_p),
+        ("final_states", c_void_p),
+        ("schema", c_void_p),
+        ("binding", c_void_p),
+        ("label_width", c_uint32),
+        ("final_words", c_uint32),
+        ("invalid", c_void_p),
+        ("goal", c_void_p),
+    ]
+
+
+class BrfsOptions(Structure):
+    _fields_ = [
+        ("max_depth", c_uint32),
+        ("witness_pruning", c_int32),
+        ("max_states", c_uint64),
+        ("max_expanded", c_uint64),
+        ("stop_at_goal", c_int32),
+        ("fingerprint", c_int32),
+        ("chunk", c_uint64),
+        ("memory_states", c_uint64),
+    ]
+
+
+class BrfsResult(Structure):
+    _fields_ = [
+        ("status", c_int32),
+        ("solved", c_int32),
+        ("exhausted", c_int32),
+        ("layers", c_uint32),
+        ("states", c_uint64),
+        ("expanded", c_uint64),
+        ("generated", c_uint64),
+        ("goal_states", c_uint64),
+        ("fingerprint", c_uint64),
+        ("first_goal", c_int64),
+        ("search_s", c_double),
+        ("device_s", c_double),
+    ]
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"mymyr_amd: {LIB_PATH} is not built (run `make -C mymyr_amd` or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    sigs = {
+        "mya_last_error": (c_char_p, []),
+        "mya_abi_version": (c_int, []),
+        "mya_task_load_text": (c_int, [c_char_p, c_size_t, c_int, POINTER(c_void_p)]),
+        "mya_task_load_file": (c_int, [c_char_p, c_int, POINTER(c_void_p)]),
+        "mya_task_free": (None, [c_void_p]),
+        "mya_task_info_get": (c_int, [c_void_p, POINTER(TaskInfo)]),
+        "mya_task_slots": (c_int, [c_void_p, c_void_p, c_void_p]),
+        "mya_task_initial": (c_int, [c_void_p, c_void_p, c_uint32]),
+        "mya_hash_rows": (c_int, [c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),
+        "mya_hash_words": (c_uint64, [c_void_p, c_uint32, c_uint64]),
+        "mya_hash_state": (c_uint64, [c_void_p, c_uint32]),
+        "mya_philox": (None, [c_uint64, c_uint64, c_uint64, c_uint32, c_void_p]),
+        "mya_successor_index": (c_uint32, [c_uint64, c_uint64, c_uint64, c_uint32]),
+        "mya_hashset_create": (c_int, [c_uint64, c_uint32, c_double, c_uint64, POINTER(c_void_p)]),
+        "mya_hashset_free": (None, [c_void_p]),
+        "mya_hashset_insert": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p, POINTER(c_uint64), c_void_p]),
+        "mya_hashset_size": (c_int, [c_void_p, POINTER(c_uint64)]),
+        "mya_hashset_rows": (c_int, [c_void_p, POINTER(c_void_p)]),
+        "mya_hashset_clear": (c_int, [c_void_p, c_void_p]),
+    }
+    optional = {
+        "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),
+        "mya_env_free": (None, [c_void_p]),
+        "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_void_p]),
+        "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p]),
+        "mya_env_check": (c_int, [c_void_p]),
+        "mya_env_initial_count": (c_int, [c_void_p, POINTER(c_uint32), POINTER(c_uint8)]),
+        "mya_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
+        "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p]),
+        "mya_schema_masks": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),
+        "mya_successors": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
+    }
+    for name, (res, args) in list(sigs.items()) + list(optional.items()):
+        fn = getattr(lib, name, None)
+        if fn is None:
+            if name in sigs:
+                raise ImportError(f"mymyr_amd: {LIB_PATH} lacks {name}")
+            continue
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise MyaError(lib.mya_last_error().decode())

@@ -1,0 +1,54 @@
+#pragma once
+// Layer-synchronous breadth-first search on the device, bit-exact with the reference's BrFS (src/mymyr/search/brfs.cpp:
+// run_flat 274-404 and brfs() 1809-1931): ids are ranks of first discovery by (parent id, successor index), every
+// expanded state is goal-tested, layer_counts[d] = {expanded, generated, new}, max_states stops at the state that fills
+// the store inside its parent's expansion, max_depth stores but does not expand the states of depth max_depth, and
+// fingerprint = XOR over ids of mix64(id * phi ^ canonical_hash(state)) (brfs.cpp:34-37, task.cpp:387-404).
+
+#include "task.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <vector>
+
+namespace mya
+{
+struct BrfsOptionsC
+{
+    u32 max_depth = ~u32{0};
+    i32 witness_pruning = 1;
+    u64 max_states = ~u64{0};
+    u64 max_expanded = ~u64{0};
+    i32 stop_at_goal = 1;
+    i32 fingerprint = 0;
+    u64 chunk = 0;          // candidates per device batch (0: automatic)
+    u64 memory_states = 0;  // arena capacity when max_states is unbounded (0: automatic)
+};
+
+struct BrfsResultC
+{
+    i32 status = 0;  // SearchStatus of the reference (search/control.hpp:28-37)
+    i32 solved = 0;
+    i32 exhausted = 0;
+    u32 layers = 0;
+    u64 states = 0, expanded = 0, generated = 0, goal_states = 0, fingerprint = 0;
+    i64 first_goal = -1;
+    double search_s = 0;
+    double device_s = 0;
+};
+
+enum SearchStatus : i32
+{
+    kSolved = 0,
+    kExhausted = 1,
+    kOutOfStates = 2,
+    kOutOfTime = 3,
+    kCancelled = 4,
+    kFailed = 5,
+    kUnsolvable = 6,
+};
+
+/// Runs the BrFS on the current device; fills layer_counts with {expanded, generated, new} per expanded layer.
+BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts);
+}  // namespace mya

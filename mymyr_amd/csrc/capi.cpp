@@ -1,0 +1,296 @@
+// The C ABI (include/mymyr_amd.h): argument checks, exception-to-status translation, and the calls into the task
+// compiler, the state set and the drivers.
+
+#include "../../include/mymyr_amd.h"
+
+#include "brfs.hpp"
+#include "capi_internal.hpp"
+#include "device_common.hpp"
+#include "runtime.hpp"
+#include "state_set.hpp"
+#include "task.hpp"
+
+#include <cstring>
+#include <fstream>
+#include <sstream>
+
+namespace mya
+{
+thread_local std::string g_error;
+
+void set_error(const std::string& m) { g_error = m; }
+
+const DeviceTask& device_task(mya_task* t)
+{
+    std::lock_guard lock(t->mutex);
+    if (!t->dev.image)
+    {
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        const auto& img = t->compiled->image;
+        t->dev.image = dev_alloc<u64>(img.size(), "task image");
+        hip_check(hipMemcpy(t->dev.image, img.data(), img.size() * sizeof(u64), hipMemcpyHostToDevice), "upload task image");
+        t->dev.device = dev;
+        t->dev.words = img.size();
+    }
+    return t->dev;
+}
+}  // namespace mya
+
+using namespace mya;
+
+struct mya_hashset
+{
+    StateSet set;
+};
+
+extern "C" {
+
+const char* mya_last_error(void) { return g_error.c_str(); }
+
+int mya_abi_version(void) { return MYA_ABI_VERSION; }
+
+int mya_task_load_text(const char* text, size_t len, int atoms, mya_task** out)
+{
+    return guarded([&] {
+        if (!text || !out)
+            throw std::invalid_argument("mymyr_amd: task_load_text: null argument");
+        if (atoms < 0 || atoms > 2)
+            throw std::invalid_argument("mymyr_amd: task_load_text: atoms must be 0 (auto), 1 (reachable) or 2 (dense)");
+        auto t = std::make_unique<mya_task>();
+        t->compiled = compile_task(parse_task_text(std::string_view(text, len)), static_cast<AtomsOption>(atoms));
+        *out = t.release();
+    });
+}
+
+int mya_task_load_file(const char* path, int atoms, mya_task** out)
+{
+    return guarded([&] {
+        if (!path)
+            throw std::invalid_argument("mymyr_amd: task_load_file: null path");
+        std::ifstream in(path, std::ios::binary);
+        if (!in)
+            throw std::invalid_argument(std::string("mymyr_amd: cannot open ") + path);
+        std::stringstream ss;
+        ss << in.rdbuf();
+        const std::string s = ss.str();
+        if (mya_task_load_text(s.data(), s.size(), atoms, out) != 0)
+            throw std::runtime_error(g_error);
+    });
+}
+
+void mya_task_free(mya_task* task)
+{
+    if (!task)
+        return;
+    dev_free(task->dev.image);
+    delete task;
+}
+
+int mya_task_info_get(const mya_task* task, mya_task_info* out)
+{
+    return guarded([&] {
+        if (!task || !out)
+            throw std::invalid_argument("mymyr_amd: task_info: null argument");
+        const CompiledTask& c = *task->compiled;
+        std::memset(out, 0, sizeof(*out));
+        out->words = c.words;
+        out->fluent_slots = c.fluent_slots;
+        out->atom_mode = static_cast<uint32_t>(c.mode);
+        out->num_schemas = static_cast<uint32_t>(c.text.schemas.size());
+        out->label_width = c.label_width;
+        out->num_objects = c.n;
+        u32 ma = 0;
+        for (const auto& p : c.text.preds)
+            if (p.kind == 'F')
+                ma = std::max(ma, p.arity);
+        out->max_arity = ma;
+        out->goal_unsat = c.goal_unsat ? 1 : 0;
+        out->dense_fluent = c.layout.fluent_count;
+        out->reachable_fluent = c.reachable_fluent;
+        out->view_words = c.header().view_words;
+    });
+}
+
+int mya_task_slots(const mya_task* task, uint32_t* rec, uint64_t* cid)
+{
+    return guarded([&] {
+        if (!task)
+            throw std::invalid_argument("mymyr_amd: task_slots: null task");
+        const CompiledTask& c = *task->compiled;
+        u32 ma = 0;
+        for (const auto& p : c.text.preds)
+            if (p.kind == 'F')
+                ma = std::max(ma, p.arity);
+        const u32 stride = 1 + std::max<u32>(1, ma);
+        for (u32 s = 0; s < c.fluent_slots; ++s)
+        {
+            const u64 id = c.slot_cid[s];
+            if (cid)
+                cid[s] = id;
+            if (!rec)
+                continue;
+            // decode: the predicate whose block holds the id, then mixed-radix ranks (last position stride 1)
+            u32 p = kNone;
+            for (u32 q = 0; q < c.text.preds.size(); ++q)
+                if (c.text.preds[q].kind == 'F' && c.layout.size[q] > 0 && c.layout.offset[q] <= id && id < c.layout.offset[q] + c.layout.size[q])
+                    p = q;
+            u32* r = rec + static_cast<size_t>(s) * stride;
+            std::memset(r, 0, stride * sizeof(u32));
+            r[0] = p;
+            u64 rem = id - c.layout.offset[p];
+            const u32 ar = c.text.preds[p].arity;
+            for (u32 i = ar; i-- > 0;)
+            {
+                const auto& dom = c.layout.domain[c.layout.pos_begin[p] + i];
+                r[1 + i] = dom[rem % dom.size()];
+                rem /= dom.size();
+            }
+        }
+    });
+}
+
+int mya_task_initial(const mya_task* task, uint64_t* row, uint32_t words)
+{
+    return guarded([&] {
+        if (!task || !row)
+            throw std::invalid_argument("mymyr_amd: task_initial: null argument");
+        const CompiledTask& c = *task->compiled;
+        if (words < c.words)
+            throw std::invalid_argument("mymyr_amd: task_initial: rows of " + std::to_string(words) + " words; the task needs " +
+                                        std::to_string(c.words));
+        std::memset(row, 0, words * sizeof(uint64_t));
+        std::memcpy(row, c.initial.data(), c.words * sizeof(uint64_t));
+    });
+}
+
+int mya_hash_rows(const uint64_t* rows, uint64_t n, uint32_t words, uint64_t* out, void* stream)
+{
+    return guarded([&] {
+        if (n && (!rows || !out))
+            throw std::invalid_argument("mymyr_amd: hash_rows: null array");
+        launch_hash_rows(rows, n, words, out, static_cast<hipStream_t>(stream));
+    });
+}
+
+uint64_t mya_hash_words(const uint64_t* w, uint32_t n, uint64_t seed) { return hash_words(w, n, seed); }
+uint64_t mya_hash_state(const uint64_t* w, uint32_t n) { return hash_state(w, n); }
+
+void mya_philox(uint64_t seed, uint64_t env, uint64_t draw, uint32_t purpose, uint32_t out[4])
+{
+    const Block4 b = philox4x32_10(Block4{{static_cast<u32>(draw), static_cast<u32>(draw >> 32), static_cast<u32>(env), purpose}},
+                                   static_cast<u32>(seed), static_cast<u32>(seed >> 32));
+    for (int i = 0; i < 4; ++i)
+        out[i] = b.v[i];
+}
+
+uint32_t mya_successor_index(uint64_t seed, uint64_t env, uint64_t draw, uint32_t count)
+{
+    return successor_index(seed, env, draw, count);
+}
+
+int mya_hashset_create(uint64_t max_states, uint32_t words, double max_load, uint64_t batch, mya_hashset** out)
+{
+    return guarded([&] {
+        if (!out)
+            throw std::invalid_argument("mymyr_amd: hashset_create: null output");
+        auto h = std::make_unique<mya_hashset>();
+        state_set_create(h->set, max_states, words, max_load, batch ? batch : (u64{1} << 20), nullptr);
+        hip_check(hipStreamSynchronize(nullptr), "hashset create");
+        *out = h.release();
+    });
+}
+
+void mya_hashset_free(mya_hashset* set)
+{
+    if (!set)
+        return;
+    state_set_destroy(set->set);
+    delete set;
+}
+
+int mya_hashset_insert(mya_hashset* set, const uint64_t* rows, uint64_t n, int64_t* ids, uint8_t* is_new, uint64_t* new_count,
+                       void* stream)
+{
+    return guarded([&] {
+        if (!set || (n && !rows))
+            throw std::invalid_argument("mymyr_amd: hashset_insert: null argument");
+        state_set_insert(set->set, rows, nullptr, n, ids, is_new, new_count, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_hashset_size(const mya_hashset* set, uint64_t* size)
+{
+    return guarded([&] {
+        if (!set || !size)
+            throw std::invalid_argument("mymyr_amd: hashset_size: null argument");
+        *size = set->set.size;
+    });
+}
+
+int mya_hashset_rows(const mya_hashset* set, const uint64_t** rows)
+{
+    return guarded([&] {
+        if (!set || !rows)
+            throw std::invalid_argument("mymyr_amd: hashset_rows: null argument");
+        *rows = set->set.v.arena;
+    });
+}
+
+int mya_hashset_clear(mya_hashset* set, void* stream)
+{
+    return guarded([&] {
+        if (!set)
+            throw std::invalid_argument("mymyr_amd: hashset_clear: null set");
+        state_set_clear(set->set, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts, uint32_t cap)
+{
+    int layers = -1;
+    const int rc = guarded([&] {
+        if (!task || !options || !result)
+            throw std::invalid_argument("mymyr_amd: brfs: null argument");
+        BrfsOptionsC o;
+        o.max_depth = options->max_depth;
+        o.witness_pruning = options->witness_pruning;
+        o.max_states = options->max_states;
+        o.max_expanded = options->max_expanded;
+        o.stop_at_goal = options->stop_at_goal;
+        o.fingerprint = options->fingerprint;
+        o.chunk = options->chunk;
+        o.memory_states = options->memory_states;
+        std::vector<std::array<u64, 3>> lc;
+        BrfsResultC r;
+        if (o.stop_at_goal && task->compiled->goal_unsat)
+        {
+            // no state is a goal: the start state alone, nothing expanded (brfs.cpp:1864-1876)
+            r.status = kUnsolvable;
+            r.states = 1;
+        }
+        else
+            r = brfs_device(*task->compiled, o, lc);
+        std::memset(result, 0, sizeof(*result));
+        result->status = r.status;
+        result->solved = r.solved;
+        result->exhausted = r.exhausted;
+        result->layers = r.layers;
+        result->states = r.states;
+        result->expanded = r.expanded;
+        result->generated = r.generated;
+        result->goal_states = r.goal_states;
+        result->fingerprint = r.fingerprint;
+        result->first_goal = r.first_goal;
+        result->search_s = r.search_s;
+        result->device_s = r.device_s;
+        if (layer_counts)
+            for (size_t i = 0; i < lc.size() && i < cap; ++i)
+                for (int j = 0; j < 3; ++j)
+                    layer_counts[i * 3 + j] = lc[i][j];
+        layers = static_cast<int>(lc.size());
+    });
+    return rc == 0 ? layers : -1;
+}
+
+}  // extern "C"

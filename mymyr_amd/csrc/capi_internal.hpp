@@ -1,0 +1,55 @@
+#pragma once
+// Internals shared by the C-ABI translation units: the opaque handle types and the exception guard.
+
+#include "task.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <exception>
+#include <memory>
+#include <mutex>
+#include <string>
+
+namespace mya
+{
+void set_error(const std::string& m);
+
+/// A task's device image, uploaded on first device use.
+struct DeviceTask
+{
+    u64* image = nullptr;
+    u64 words = 0;
+    int device = -1;
+};
+
+template<class F>
+int guarded(F&& f)
+{
+    try
+    {
+        f();
+        return 0;
+    }
+    catch (const std::exception& e)
+    {
+        set_error(e.what());
+    }
+    catch (...)
+    {
+        set_error("mymyr_amd: unknown error");
+    }
+    return -1;
+}
+}  // namespace mya
+
+struct mya_task
+{
+    std::unique_ptr<mya::CompiledTask> compiled;
+    mya::DeviceTask dev;
+    std::mutex mutex;
+};
+
+namespace mya
+{
+const DeviceTask& device_task(mya_task* t);
+}

@@ -1,0 +1,118 @@
+#pragma once
+// Integer primitives shared by every kernel (and usable on the host): the state hash, Philox-4x32-10 and the index
+// draw. Bit-identical to the reference definitions:
+//   mix64 / mulfold / words / state_words  include/mymyr/core/hash.hpp:12-53
+//   philox4x32_10 / block / bits64 / below include/mymyr/rl/rng.hpp:45-83
+// The 64x64->128 product uses __umul64hi on the device and unsigned __int128 on the host.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mya
+{
+using u8 = std::uint8_t;
+using u32 = std::uint32_t;
+using u64 = std::uint64_t;
+using i32 = std::int32_t;
+using i64 = std::int64_t;
+
+#define MYA_HD __host__ __device__ __forceinline__
+
+constexpr u64 kHashSeed = 0x2d358dccaa6c78a5ULL;
+constexpr u64 kHashP1 = 0x8bb84b93962eacc9ULL;
+constexpr u64 kHashP2 = 0x4b33a62ed433d4a3ULL;
+
+MYA_HD u64 mix64(u64 x)
+{
+    x ^= x >> 30;
+    x *= 0xbf58476d1ce4e5b9ULL;
+    x ^= x >> 27;
+    x *= 0x94d049bb133111ebULL;
+    x ^= x >> 31;
+    return x;
+}
+
+MYA_HD u64 mulfold(u64 a, u64 b)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return (a * b) ^ __umul64hi(a, b);
+#else
+    const unsigned __int128 r = static_cast<unsigned __int128>(a) * b;
+    return static_cast<u64>(r) ^ static_cast<u64>(r >> 64);
+#endif
+}
+
+/// Hash of n words (order- and length-sensitive).
+MYA_HD u64 hash_words(const u64* w, u32 n, u64 seed = kHashSeed)
+{
+    u64 h = seed ^ (static_cast<u64>(n) * kHashP1);
+    u32 i = 0;
+    for (; i + 1 < n; i += 2)
+        h = mulfold(h ^ w[i] ^ kHashP1, w[i + 1] ^ kHashP2);
+    if (i < n)
+        h = mulfold(h ^ w[i] ^ kHashP1, kHashP2);
+    return mix64(h);
+}
+
+MYA_HD u32 trimmed(const u64* w, u32 n)
+{
+    while (n > 0 && w[n - 1] == 0)
+        --n;
+    return n;
+}
+
+/// The public state hash: hash_words over the trimmed words.
+MYA_HD u64 hash_state(const u64* w, u32 n) { return hash_words(w, trimmed(w, n)); }
+
+// ------------------------------------------------------------------------------------------------------ Philox
+struct Block4
+{
+    u32 v[4];
+};
+
+MYA_HD u32 mulhi32(u32 a, u32 b) { return static_cast<u32>((static_cast<u64>(a) * b) >> 32); }
+
+MYA_HD Block4 philox4x32_10(Block4 c, u32 k0, u32 k1)
+{
+    constexpr u32 m0 = 0xD2511F53u, m1 = 0xCD9E8D57u, w0 = 0x9E3779B9u, w1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r)
+    {
+        const u32 hi0 = mulhi32(m0, c.v[0]), lo0 = m0 * c.v[0];
+        const u32 hi1 = mulhi32(m1, c.v[2]), lo1 = m1 * c.v[2];
+        c = Block4{{hi1 ^ c.v[1] ^ k0, lo1, hi0 ^ c.v[3] ^ k1, lo0}};
+        k0 += w0;
+        k1 += w1;
+    }
+    return c;
+}
+
+/// 64 random bits of (seed; draw, env, purpose): the block's first two words, low first.
+MYA_HD u64 philox_bits64(u64 seed, u64 env, u64 draw, u32 purpose)
+{
+    const Block4 b = philox4x32_10(Block4{{static_cast<u32>(draw), static_cast<u32>(draw >> 32), static_cast<u32>(env), purpose}},
+                                   static_cast<u32>(seed), static_cast<u32>(seed >> 32));
+    return static_cast<u64>(b.v[0]) | (static_cast<u64>(b.v[1]) << 32);
+}
+
+/// high64(x * n) from 32x32-bit partial products: an index in [0, n).
+MYA_HD u32 below(u64 x, u32 n)
+{
+    const u64 hi = (x >> 32) * n, lo = (x & 0xFFFFFFFFull) * n;
+    return static_cast<u32>((hi + (lo >> 32)) >> 32);
+}
+
+MYA_HD u32 successor_index(u64 seed, u64 env, u64 draw, u32 count) { return below(philox_bits64(seed, env, draw, 0), count); }
+
+// ------------------------------------------------------------------------------------------------------ errors
+/// Sticky device status bits (OR-ed into a device word, read by the host after the stream drains).
+enum StatusBit : u32
+{
+    kStatusTableFull = 1u << 0,     // a hash-set probe wrapped around the whole table
+    kStatusCapacity = 1u << 1,      // an output buffer was too small
+    kStatusWideRow = 1u << 2,       // a state has bits beyond the task's words
+    kStatusNoSlot = 1u << 3,        // an add effect without an atom slot
+    kStatusPickFailed = 1u << 4,    // the chosen successor index was not found (internal inconsistency)
+};
+}  // namespace mya

@@ -1,0 +1,131 @@
+// Device-wide exclusive scan of u32 counts into u64 offsets (see scan.hpp).
+
+#include "scan.hpp"
+
+namespace mya
+{
+namespace
+{
+constexpr int kScanBlock = 256;
+constexpr int kPerThread = 4;  // 1024 elements per block
+
+__global__ __launch_bounds__(kScanBlock) void k_block_sums(const u32* __restrict__ counts, u64 n, u64* __restrict__ sums)
+{
+    __shared__ u64 lds[kScanBlock / kWave];
+    const u64 base = static_cast<u64>(blockIdx.x) * kScanBlock * kPerThread;
+    u64 s = 0;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        const u64 i = base + static_cast<u64>(k) * kScanBlock + threadIdx.x;
+        if (i < n)
+            s += counts[i];
+    }
+    s = wave_sum64(s);
+    if (lane_id() == 0)
+        lds[threadIdx.x / kWave] = s;
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        u64 t = 0;
+        for (int w = 0; w < kScanBlock / kWave; ++w)
+            t += lds[w];
+        sums[blockIdx.x] = t;
+    }
+}
+
+// One block scans the block sums in place (exclusive) and writes the grand total.
+__global__ __launch_bounds__(1024) void k_scan_sums(u64* __restrict__ sums, u64 nb, u64* __restrict__ total)
+{
+    __shared__ u64 lds[1024 / kWave + 1];
+    __shared__ u64 carry;
+    if (threadIdx.x == 0)
+        carry = 0;
+    __syncthreads();
+    for (u64 base = 0; base < nb; base += 1024)
+    {
+        const u64 i = base + threadIdx.x;
+        const u64 v = i < nb ? sums[i] : 0;
+        const u64 inc = wave_inclusive64(v);
+        const u32 wave = threadIdx.x / kWave;
+        if (lane_id() == kWave - 1)
+            lds[wave] = inc;
+        __syncthreads();
+        if (threadIdx.x == 0)
+        {
+            u64 run = 0;
+            for (int w = 0; w < 1024 / kWave; ++w)
+            {
+                const u64 t = lds[w];
+                lds[w] = run;
+                run += t;
+            }
+            lds[1024 / kWave] = run;
+        }
+        __syncthreads();
+        if (i < nb)
+            sums[i] = carry + lds[wave] + inc - v;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            carry += lds[1024 / kWave];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        *total = carry;
+}
+
+__global__ __launch_bounds__(kScanBlock) void k_offsets(const u32* __restrict__ counts, u64 n, const u64* __restrict__ sums,
+                                                       u64* __restrict__ offsets)
+{
+    __shared__ u64 lds[kScanBlock / kWave + 1];
+    const u64 base = static_cast<u64>(blockIdx.x) * kScanBlock * kPerThread;
+    // each thread owns kPerThread consecutive elements
+    const u64 first = base + static_cast<u64>(threadIdx.x) * kPerThread;
+    u32 v[kPerThread];
+    u64 s = 0;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        v[k] = first + k < n ? counts[first + k] : 0;
+        s += v[k];
+    }
+    const u64 inc = wave_inclusive64(s);
+    const u32 wave = threadIdx.x / kWave;
+    if (lane_id() == kWave - 1)
+        lds[wave] = inc;
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        u64 run = 0;
+        for (int w = 0; w < kScanBlock / kWave; ++w)
+        {
+            const u64 t = lds[w];
+            lds[w] = run;
+            run += t;
+        }
+    }
+    __syncthreads();
+    u64 off = sums[blockIdx.x] + lds[wave] + inc - s;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        if (first + k < n)
+            offsets[first + k] = off;
+        off += v[k];
+    }
+}
+}  // namespace
+
+void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream)
+{
+    const u64 nb = (n + kScanBlock * kPerThread - 1) / (kScanBlock * kPerThread);
+    if (nb == 0)
+    {
+        hipMemsetAsync(total, 0, sizeof(u64), stream);
+        return;
+    }
+    hipLaunchKernelGGL(k_block_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, counts, n, scratch);
+    hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, stream, scratch, nb, total);
+    hipLaunchKernelGGL(k_offsets, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, counts, n, scratch, offsets);
+}
+}  // namespace mya

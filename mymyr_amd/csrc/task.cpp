@@ -1,0 +1,1470 @@
+// Task text reader and task compiler (host C++). See task.hpp for the reference semantics each part follows.
+
+#include "task.hpp"
+
+#include <algorithm>
+#include <bit>
+#include <charconv>
+#include <cstring>
+#include <numeric>
+#include <set>
+#include <functional>
+#include <unordered_set>
+
+namespace mya
+{
+namespace
+{
+// ------------------------------------------------------------------------------------------------- text reader
+// Token grammar of the reference reader (src/mymyr/formalism/text_format.cpp:22-197): O, P, SI, FI, G, A, then the
+// optional X, C and EG sections. Numeric tasks (the N section) are refused.
+class Reader
+{
+public:
+    explicit Reader(std::string_view s) : m_s(s) {}
+
+    TaskText read()
+    {
+        TaskText t;
+        expect("O");
+        t.objects = u();
+        expect("P");
+        const u32 np = u();
+        for (u32 i = 0; i < np; ++i)
+        {
+            const std::string_view k = word();
+            PredicateText p;
+            if (k == "S")
+                p.kind = 'S';
+            else if (k == "F")
+                p.kind = 'F';
+            else if (k == "D" || k == "C" || k == "P")
+                p.kind = 'D';
+            else
+                fail("bad predicate kind " + std::string(k));
+            p.arity = u();
+            p.name = std::string(word());
+            t.preds.push_back(std::move(p));
+        }
+        std::string_view tag = word();
+        if (tag == "N")
+            fail("numeric tasks are not supported by the device path");
+        if (tag != "SI")
+            fail("expected SI, got " + std::string(tag));
+        atoms(t, t.static_init);
+        expect("FI");
+        atoms(t, t.fluent_init);
+        expect("G");
+        const u32 ng = u();
+        for (u32 i = 0; i < ng; ++i)
+            t.goal.push_back(literal(t, true));
+        expect("A");
+        const u32 ns = u();
+        for (u32 i = 0; i < ns; ++i)
+            t.schemas.push_back(schema(t));
+        while (!at_end())
+        {
+            tag = word();
+            if (tag == "X")
+            {
+                if (u() != 0)
+                    fail("axioms (derived predicates) are not supported by the device path");
+            }
+            else if (tag == "C")
+            {
+                // collapsed parameters: the schemas bind the other parameters only (labels as the reference's)
+                const u32 k = u();
+                for (u32 i = 0; i < k; ++i)
+                {
+                    const u32 s = u();
+                    if (s >= t.schemas.size())
+                        fail("collapsed parameter of an unknown schema");
+                    (void)u();
+                    (void)u();
+                    (void)i32v();
+                }
+            }
+            else if (tag == "EG")
+            {
+                (void)u();
+                const u32 k = u();
+                for (u32 i = 0; i < k; ++i)
+                {
+                    const u32 p = u();
+                    if (p >= t.preds.size())
+                        fail("encoding goal literal of an unknown predicate");
+                    (void)u();
+                    for (u32 j = 0; j < t.preds[p].arity; ++j)
+                        (void)u();
+                }
+            }
+            else
+                fail("unexpected section " + std::string(tag));
+        }
+        for (const auto& p : t.preds)
+            if (p.kind == 'D')
+                fail("derived predicates are not supported by the device path");
+        return t;
+    }
+
+private:
+    [[noreturn]] void fail(const std::string& m) { throw Error("task text: " + m); }
+    void skip_ws()
+    {
+        while (m_pos < m_s.size() && (m_s[m_pos] == ' ' || m_s[m_pos] == '\n' || m_s[m_pos] == '\t' || m_s[m_pos] == '\r'))
+            ++m_pos;
+    }
+    bool at_end()
+    {
+        skip_ws();
+        return m_pos >= m_s.size();
+    }
+    std::string_view word()
+    {
+        skip_ws();
+        if (m_pos >= m_s.size())
+            fail("unexpected end of input");
+        const size_t b = m_pos;
+        while (m_pos < m_s.size() && !(m_s[m_pos] == ' ' || m_s[m_pos] == '\n' || m_s[m_pos] == '\t' || m_s[m_pos] == '\r'))
+            ++m_pos;
+        return m_s.substr(b, m_pos - b);
+    }
+    void expect(const char* s)
+    {
+        const std::string_view w = word();
+        if (w != s)
+            fail(std::string("expected ") + s + ", got '" + std::string(w) + "'");
+    }
+    u32 u()
+    {
+        const std::string_view w = word();
+        u32 v = 0;
+        auto [p, ec] = std::from_chars(w.data(), w.data() + w.size(), v);
+        if (ec != std::errc{} || p != w.data() + w.size())
+            fail("expected unsigned integer, got '" + std::string(w) + "'");
+        return v;
+    }
+    i32 i32v()
+    {
+        const std::string_view w = word();
+        i32 v = 0;
+        auto [p, ec] = std::from_chars(w.data(), w.data() + w.size(), v);
+        if (ec != std::errc{} || p != w.data() + w.size())
+            fail("expected integer, got '" + std::string(w) + "'");
+        return v;
+    }
+    u32 pred(const TaskText& t)
+    {
+        const u32 p = u();
+        if (p >= t.preds.size())
+            fail("unknown predicate " + std::to_string(p));
+        return p;
+    }
+    void atoms(const TaskText& t, std::vector<std::vector<u32>>& out)
+    {
+        const u32 k = u();
+        for (u32 i = 0; i < k; ++i)
+        {
+            std::vector<u32> a{pred(t)};
+            for (u32 j = 0; j < t.preds[a[0]].arity; ++j)
+            {
+                const u32 o = u();
+                if (o >= t.objects)
+                    fail("object out of range");
+                a.push_back(o);
+            }
+            out.push_back(std::move(a));
+        }
+    }
+    Literal literal(const TaskText& t, bool ground, u32 params = 0)
+    {
+        Literal l;
+        l.pred = pred(t);
+        l.positive = u() != 0;
+        for (u32 j = 0; j < t.preds[l.pred].arity; ++j)
+        {
+            i32 x;
+            if (ground)
+            {
+                const u32 o = u();
+                if (o >= t.objects)
+                    fail("object out of range");
+                x = -static_cast<i32>(o) - 1;
+            }
+            else
+            {
+                x = i32v();
+                if (x >= 0 && static_cast<u32>(x) >= params)
+                    fail("parameter out of range");
+                if (x < 0 && static_cast<u32>(-(x + 1)) >= t.objects)
+                    fail("object out of range");
+            }
+            l.terms.push_back(x);
+        }
+        return l;
+    }
+    SchemaText schema(const TaskText& t)
+    {
+        SchemaText s;
+        s.name = std::string(word());
+        s.arity = u();
+        expect("L");
+        const u32 np = u();
+        for (u32 i = 0; i < np; ++i)
+            s.pre.push_back(literal(t, false, s.arity));
+        expect("E");
+        const u32 ne = u();
+        for (u32 i = 0; i < ne; ++i)
+        {
+            const u32 extra = u();
+            expect("L");
+            const u32 nc = u();
+            if (extra != 0 || nc != 0)
+                fail("conditional effects are not supported by the device path (schema " + s.name + ")");
+            expect("F");
+            const u32 nf = u();
+            for (u32 j = 0; j < nf; ++j)
+            {
+                Literal l = literal(t, false, s.arity);
+                if (t.preds[l.pred].kind != 'F')
+                    fail("effect on a non-fluent predicate");
+                s.eff.push_back(std::move(l));
+            }
+        }
+        return s;
+    }
+
+    std::string_view m_s;
+    size_t m_pos = 0;
+};
+
+u64 sat_mul(u64 a, u64 b)
+{
+    constexpr u64 cap = u64{1} << 62;
+    if (a == 0 || b == 0)
+        return 0;
+    if (a > cap / b)
+        return cap;
+    return std::min(cap, a * b);
+}
+
+using Bits = std::vector<u64>;
+inline void set_bit(Bits& b, u32 i) { b[i >> 6] |= u64{1} << (i & 63); }
+inline bool test_bit(const Bits& b, u32 i) { return (b[i >> 6] >> (i & 63)) & 1; }
+inline bool any_bit(const Bits& b)
+{
+    for (u64 w : b)
+        if (w)
+            return true;
+    return false;
+}
+inline u32 popcount(const Bits& b)
+{
+    u32 c = 0;
+    for (u64 w : b)
+        c += static_cast<u32>(std::popcount(w));
+    return c;
+}
+
+bool is_object(i32 t) { return t < 0; }
+u32 term_object(i32 t) { return static_cast<u32>(-(t + 1)); }
+
+std::vector<u32> distinct_params(const std::vector<i32>& terms)
+{
+    std::vector<u32> v;
+    for (i32 x : terms)
+        if (x >= 0 && std::find(v.begin(), v.end(), static_cast<u32>(x)) == v.end())
+            v.push_back(static_cast<u32>(x));
+    return v;
+}
+
+// Packed static key: sum obj_i * n^(ar-1-i).
+u64 static_key(const u32* objs, u32 ar, u32 n)
+{
+    u64 k = 0;
+    for (u32 i = 0; i < ar; ++i)
+        k = k * n + objs[i];
+    return k;
+}
+
+class Compiler
+{
+public:
+    Compiler(TaskText text, AtomsOption atoms) : m_opt(atoms)
+    {
+        C = std::make_unique<CompiledTask>();
+        C->text = std::move(text);
+    }
+
+    std::unique_ptr<CompiledTask> run()
+    {
+        T = &C->text;
+        n = T->objects;
+        if (n == 0)
+            n = 0;
+        ow = std::max<u32>(1, words_for(n));
+        C->n = n;
+        C->ow = ow;
+        const u32 m = static_cast<u32>(T->preds.size());
+        for (const auto& p : T->preds)
+            if (p.arity > 6)
+                throw Error("predicate " + p.name + " has arity above 6 (unsupported by the device path)");
+        // static key packing must fit 64 bits
+        for (u32 p = 0; p < m; ++p)
+            if (T->preds[p].kind == 'S')
+            {
+                long double sp = 1;
+                for (u32 i = 0; i < T->preds[p].arity; ++i)
+                    sp *= std::max<u32>(n, 1);
+                if (sp >= 1.8e19L)
+                    throw Error("static predicate " + T->preds[p].name + " has a key space beyond 64 bits");
+            }
+        setup_statics();
+        compute_dom0();
+        build_layout();
+        choose_mode();
+        build_state_tables();
+        build_image();
+        C->static_keys.assign(T->preds.size(), {});
+        for (u32 p = 0; p < T->preds.size(); ++p)
+        {
+            C->static_keys[p].assign(static_keys[p].begin(), static_keys[p].end());
+            std::sort(C->static_keys[p].begin(), C->static_keys[p].end());
+        }
+        return std::move(C);
+    }
+
+private:
+    // --------------------------------------------------------------------------------------------- statics
+    void setup_statics()
+    {
+        const u32 m = static_cast<u32>(T->preds.size());
+        static_atoms.assign(m, {});
+        static_keys.assign(m, {});
+        s_unary.assign(m, Bits(ow, 0));
+        for (const auto& a : T->static_init)
+        {
+            if (T->preds[a[0]].kind != 'S')
+                throw Error("static initial atom of a non-static predicate");
+            static_atoms[a[0]].push_back(&a);
+            static_keys[a[0]].insert(static_key(a.data() + 1, T->preds[a[0]].arity, std::max<u32>(n, 1)));
+            if (T->preds[a[0]].arity == 1)
+                set_bit(s_unary[a[0]], a[1]);
+        }
+        for (const auto& a : T->fluent_init)
+            if (T->preds[a[0]].kind != 'F')
+                throw Error("fluent initial atom of a non-fluent predicate");
+    }
+
+    bool static_holds(u32 p, const u32* objs) const
+    {
+        return static_keys[p].count(static_key(objs, T->preds[p].arity, std::max<u32>(n, 1))) != 0;
+    }
+    bool static_ground_holds(const Literal& l) const
+    {
+        std::vector<u32> objs;
+        for (i32 x : l.terms)
+            objs.push_back(term_object(x));
+        return static_holds(l.pred, objs.data());
+    }
+
+    /// Row table of static `pred`: row(a[from]) has bit a[to] (n rows of ow words, object space).
+    u32 static_rows(u32 pred, u32 from, u32 to)
+    {
+        const auto key = std::make_tuple(pred, from, to);
+        if (auto it = m_row_tables.find(key); it != m_row_tables.end())
+            return it->second;
+        const u32 id = static_cast<u32>(m_row_data.size());
+        Bits rows(static_cast<size_t>(std::max<u32>(n, 1)) * ow, 0);
+        for (const auto* a : static_atoms[pred])
+        {
+            const u32 f = (*a)[1 + from], t = (*a)[1 + to];
+            rows[static_cast<size_t>(f) * ow + (t >> 6)] |= u64{1} << (t & 63);
+        }
+        m_row_data.push_back(std::move(rows));
+        m_row_tables.emplace(key, id);
+        return id;
+    }
+
+    // --------------------------------------------------------------------------------------------- dom0
+    // The static domain of each schema parameter: every object, AND static unary literals, AND static binary
+    // literals with one constant, AND projections of positive static k-ary literals (compile.cpp:803-915).
+    void compute_dom0()
+    {
+        C->dom0.resize(T->schemas.size());
+        C->never.assign(T->schemas.size(), 0);
+        for (u32 si = 0; si < T->schemas.size(); ++si)
+        {
+            const SchemaText& s = T->schemas[si];
+            if (s.arity > kMaxParams)
+                throw Error("schema " + s.name + " has " + std::to_string(s.arity) + " parameters; the device path supports at most " +
+                            std::to_string(kMaxParams));
+            auto& dom = C->dom0[si];
+            dom.assign(s.arity, Bits(ow, 0));
+            for (u32 v = 0; v < s.arity; ++v)
+                for (u32 o = 0; o < n; ++o)
+                    set_bit(dom[v], o);
+            bool never = false;
+            for (const Literal& l : s.pre)
+            {
+                const PredicateText& P = T->preds[l.pred];
+                if (P.kind == 'D')
+                    throw Error("derived precondition literals are not supported");
+                const bool fluent = P.kind != 'S';
+                const auto vars = distinct_params(l.terms);
+                if (vars.empty())
+                {
+                    if (!fluent && static_ground_holds(l) != l.positive)
+                        never = true;
+                    continue;
+                }
+                if (P.arity == 1)
+                {
+                    if (!fluent)
+                        and_bits(dom[vars[0]], s_unary[l.pred], !l.positive);
+                    continue;
+                }
+                if (P.arity == 2 && l.terms[0] != l.terms[1])
+                {
+                    const bool f0 = l.terms[0] >= 0, f1 = l.terms[1] >= 0;
+                    if (f0 && f1)
+                        continue;
+                    const u32 fpos = f0 ? 0 : 1, opos = 1 - fpos;
+                    const u32 v = static_cast<u32>(l.terms[fpos]);
+                    const u32 cobj = term_object(l.terms[opos]);
+                    if (!fluent)
+                    {
+                        const u32 tab = static_rows(l.pred, opos, fpos);
+                        Bits row(m_row_data[tab].begin() + static_cast<size_t>(cobj) * ow,
+                                 m_row_data[tab].begin() + static_cast<size_t>(cobj + 1) * ow);
+                        and_bits(dom[v], row, !l.positive);
+                    }
+                    continue;
+                }
+                if (!fluent && l.positive && P.arity >= 3)
+                {
+                    for (u32 i = 0; i < P.arity; ++i)
+                        if (l.terms[i] >= 0)
+                        {
+                            Bits proj(ow, 0);
+                            for (const auto* a : static_atoms[l.pred])
+                            {
+                                bool ok = true;
+                                for (u32 j = 0; j < P.arity && ok; ++j)
+                                    if (l.terms[j] < 0 && (*a)[1 + j] != term_object(l.terms[j]))
+                                        ok = false;
+                                if (ok)
+                                    set_bit(proj, (*a)[1 + i]);
+                            }
+                            and_bits(dom[static_cast<u32>(l.terms[i])], proj, false);
+                        }
+                }
+            }
+            for (u32 v = 0; v < s.arity; ++v)
+                if (!any_bit(dom[v]))
+                    never = true;
+            C->never[si] = never ? 1 : 0;
+        }
+    }
+    void and_bits(Bits& d, const Bits& s, bool neg)
+    {
+        for (u32 w = 0; w < ow; ++w)
+            d[w] &= neg ? ~s[w] : s[w];
+    }
+
+    // --------------------------------------------------------------------------------------------- layout
+    // Position domains: the objects the add effects can put there (a constant, or the dom0 of the parameter) plus
+    // the initial atoms' objects; ranks in object order; the last position has stride 1 (compile.cpp:1363-1455).
+    void build_layout()
+    {
+        const u32 m = static_cast<u32>(T->preds.size());
+        std::vector<std::vector<Bits>> bits(m);
+        for (u32 p = 0; p < m; ++p)
+            if (T->preds[p].kind == 'F')
+                bits[p].assign(T->preds[p].arity, Bits(ow, 0));
+        for (u32 si = 0; si < T->schemas.size(); ++si)
+            for (const Literal& l : T->schemas[si].eff)
+                if (l.positive)
+                    for (u32 i = 0; i < l.terms.size(); ++i)
+                    {
+                        if (l.terms[i] < 0)
+                            set_bit(bits[l.pred][i], term_object(l.terms[i]));
+                        else
+                            for (u32 w = 0; w < ow; ++w)
+                                bits[l.pred][i][w] |= C->dom0[si][static_cast<u32>(l.terms[i])][w];
+                    }
+        for (const auto& a : T->fluent_init)
+            for (u32 i = 0; i + 1 < a.size(); ++i)
+                set_bit(bits[a[0]][i], a[1 + i]);
+
+        Layout& L = C->layout;
+        L.offset.assign(m, kNone64);
+        L.size.assign(m, 0);
+        L.pos_begin.assign(m, 0);
+        u32 positions = 0;
+        for (u32 p = 0; p < m; ++p)
+            if (T->preds[p].kind == 'F')
+            {
+                L.pos_begin[p] = positions;
+                positions += T->preds[p].arity;
+            }
+        L.rs.assign(positions, std::vector<u64>(n, Layout::kOutside));
+        L.domain.assign(positions, {});
+        u64 running = 0;
+        for (u32 p = 0; p < m; ++p)
+        {
+            if (T->preds[p].kind != 'F')
+                continue;
+            const u32 ar = T->preds[p].arity;
+            u64 size = 1;
+            for (u32 i = 0; i < ar; ++i)
+            {
+                const u32 pos = L.pos_begin[p] + i;
+                for (u32 o = 0; o < n; ++o)
+                    if (test_bit(bits[p][i], o))
+                        L.domain[pos].push_back(o);
+                size = sat_mul(size, L.domain[pos].size());
+            }
+            u64 st = 1;
+            for (u32 i = ar; i-- > 0;)
+            {
+                const u32 pos = L.pos_begin[p] + i;
+                for (u32 r = 0; r < L.domain[pos].size(); ++r)
+                    L.rs[pos][L.domain[pos][r]] = r * st;
+                st = sat_mul(st, std::max<u64>(1, L.domain[pos].size()));
+            }
+            L.size[p] = size;
+            L.offset[p] = running;
+            running = std::min<u64>(running + size, u64{1} << 62);
+        }
+        L.fluent_count = running;
+    }
+
+    u64 cid_of(u32 p, const u32* args) const { return C->layout.encode(p, args, T->preds[p].arity); }
+
+    // --------------------------------------------------------------------------------------------- reachability
+    // The delete-relaxed fixpoint: one rule per (schema, add literal) with the positive fluent preconditions and every
+    // static precondition as its body; negative fluent literals dropped; "=" by object identity; a variable no
+    // positive literal binds ranges over every object (relaxed_reachability.hpp:3-12). Evaluated by naive rounds of
+    // a bitset join until no new atom appears.
+    std::vector<u64> reachable_fluents()
+    {
+        const u32 m = static_cast<u32>(T->preds.size());
+        std::vector<u8> reached(C->layout.fluent_count, 0);
+        std::vector<u64> list;
+        // per fluent predicate: unary bits, binary fwd/bwd rows (object space)
+        std::vector<Bits> unary(m);
+        std::vector<Bits> fwd(m), bwd(m);
+        for (u32 p = 0; p < m; ++p)
+            if (T->preds[p].kind == 'F')
+            {
+                if (T->preds[p].arity == 1)
+                    unary[p].assign(ow, 0);
+                if (T->preds[p].arity == 2)
+                {
+                    fwd[p].assign(static_cast<size_t>(std::max<u32>(n, 1)) * ow, 0);
+                    bwd[p].assign(static_cast<size_t>(std::max<u32>(n, 1)) * ow, 0);
+                }
+            }
+        auto add_atom = [&](u32 p, const u32* args) -> bool
+        {
+            const u64 c = cid_of(p, args);
+            if (c >= C->layout.fluent_count)
+                return false;  // outside every position domain: no canonical id
+            if (reached[c])
+                return false;
+            reached[c] = 1;
+            list.push_back(c);
+            const u32 ar = T->preds[p].arity;
+            if (ar == 1)
+                set_bit(unary[p], args[0]);
+            else if (ar == 2)
+            {
+                fwd[p][static_cast<size_t>(args[0]) * ow + (args[1] >> 6)] |= u64{1} << (args[1] & 63);
+                bwd[p][static_cast<size_t>(args[1]) * ow + (args[0] >> 6)] |= u64{1} << (args[0] & 63);
+            }
+            return true;
+        };
+        auto holds = [&](u32 p, const u32* args) -> bool
+        {
+            const u64 c = cid_of(p, args);
+            return c < C->layout.fluent_count && reached[c];
+        };
+        for (const auto& a : T->fluent_init)
+            add_atom(a[0], a.data() + 1);
+
+        const u32 eq = equality_pred();
+        for (bool changed = true; changed;)
+        {
+            changed = false;
+            for (u32 si = 0; si < T->schemas.size(); ++si)
+            {
+                const SchemaText& s = T->schemas[si];
+                std::vector<const Literal*> body;
+                bool has_head = false;
+                for (const Literal& l : s.eff)
+                    has_head |= l.positive;
+                if (!has_head)
+                    continue;
+                for (const Literal& l : s.pre)
+                {
+                    const bool fluent = T->preds[l.pred].kind != 'S';
+                    if (fluent && !l.positive)
+                        continue;  // the delete relaxation
+                    body.push_back(&l);
+                }
+                // variables: everything the body or a head mentions
+                std::vector<u8> mentioned(s.arity, 0);
+                for (const Literal* l : body)
+                    for (i32 x : l->terms)
+                        if (x >= 0)
+                            mentioned[x] = 1;
+                for (const Literal& l : s.eff)
+                    if (l.positive)
+                        for (i32 x : l.terms)
+                            if (x >= 0)
+                                mentioned[x] = 1;
+                std::vector<u32> vars;
+                for (u32 v = 0; v < s.arity; ++v)
+                    if (mentioned[v])
+                        vars.push_back(v);
+                // ground body literals
+                bool ok = true;
+                for (const Literal* l : body)
+                    if (distinct_params(l->terms).empty())
+                    {
+                        std::vector<u32> objs;
+                        for (i32 x : l->terms)
+                            objs.push_back(term_object(x));
+                        const bool fluent = T->preds[l->pred].kind != 'S';
+                        bool h;
+                        if (fluent)
+                            h = holds(l->pred, objs.data());
+                        else if (l->pred == eq)
+                            h = objs[0] == objs[1];
+                        else
+                            h = static_holds(l->pred, objs.data());
+                        if (h != l->positive)
+                            ok = false;
+                    }
+                if (!ok)
+                    continue;
+                // order: greedy by constraints to placed variables
+                std::vector<u32> order;
+                std::vector<u8> placed(s.arity, 0);
+                while (order.size() < vars.size())
+                {
+                    int best = -1;
+                    long best_score = 0;
+                    for (u32 v : vars)
+                    {
+                        if (placed[v])
+                            continue;
+                        long links = 0, un = 0;
+                        for (const Literal* l : body)
+                        {
+                            const auto ps = distinct_params(l->terms);
+                            if (std::find(ps.begin(), ps.end(), v) == ps.end())
+                                continue;
+                            if (ps.size() == 1)
+                                ++un;
+                            for (u32 q : ps)
+                                if (q != v && placed[q])
+                                    ++links;
+                        }
+                        const long score = links * 1000000 + un * 10000;
+                        if (best < 0 || score > best_score)
+                            best = static_cast<int>(v), best_score = score;
+                    }
+                    placed[best] = 1;
+                    order.push_back(static_cast<u32>(best));
+                }
+                std::vector<u32> bind(s.arity, 0);
+                std::vector<u8> bound(s.arity, 0);
+                std::vector<std::vector<u32>> heads;
+                enumerate(s, body, order, 0, bind, bound, unary, fwd, bwd, reached, eq, heads);
+                for (const auto& h : heads)
+                    if (add_atom(h[0], h.data() + 1))
+                        changed = true;
+            }
+        }
+        std::sort(list.begin(), list.end());
+        return list;
+    }
+
+    u32 equality_pred() const
+    {
+        for (u32 p = 0; p < T->preds.size(); ++p)
+            if (T->preds[p].kind == 'S' && T->preds[p].name == "=" && T->preds[p].arity == 2)
+                return p;
+        return kNone;
+    }
+
+    void enumerate(const SchemaText& s, const std::vector<const Literal*>& body, const std::vector<u32>& order, u32 d,
+                   std::vector<u32>& bind, std::vector<u8>& bound, const std::vector<Bits>& unary,
+                   const std::vector<Bits>& fwd, const std::vector<Bits>& bwd, const std::vector<u8>& reached, u32 eq,
+                   std::vector<std::vector<u32>>& heads)
+    {
+        if (d == order.size())
+        {
+            for (const Literal& l : s.eff)
+                if (l.positive)
+                {
+                    std::vector<u32> h{l.pred};
+                    for (i32 x : l.terms)
+                        h.push_back(x < 0 ? term_object(x) : bind[x]);
+                    heads.push_back(std::move(h));
+                }
+            return;
+        }
+        const u32 v = order[d];
+        Bits cand(ow, 0);
+        for (u32 o = 0; o < n; ++o)
+            set_bit(cand, o);
+        std::vector<const Literal*> checks;
+        for (const Literal* l : body)
+        {
+            const auto ps = distinct_params(l->terms);
+            if (std::find(ps.begin(), ps.end(), v) == ps.end())
+                continue;
+            bool rest_bound = true;
+            for (u32 q : ps)
+                if (q != v && !bound[q])
+                    rest_bound = false;
+            if (!rest_bound)
+                continue;
+            const bool fluent = T->preds[l->pred].kind != 'S';
+            const u32 ar = T->preds[l->pred].arity;
+            if (ar == 1 && l->pred != eq)
+            {
+                and_bits(cand, fluent ? unary[l->pred] : s_unary[l->pred], !l->positive);
+                continue;
+            }
+            if (ar == 2 && l->terms[0] != l->terms[1] && l->pred != eq)
+            {
+                const u32 vpos = l->terms[0] == static_cast<i32>(v) ? 0 : 1, opos = 1 - vpos;
+                const i32 ot = l->terms[opos];
+                const u32 oobj = ot < 0 ? term_object(ot) : bind[ot];
+                Bits row(ow, 0);
+                if (fluent)
+                {
+                    const Bits& tab = opos == 0 ? fwd[l->pred] : bwd[l->pred];
+                    std::copy(tab.begin() + static_cast<size_t>(oobj) * ow, tab.begin() + static_cast<size_t>(oobj + 1) * ow, row.begin());
+                }
+                else
+                {
+                    const u32 t = static_rows(l->pred, opos, vpos);
+                    std::copy(m_row_data[t].begin() + static_cast<size_t>(oobj) * ow,
+                              m_row_data[t].begin() + static_cast<size_t>(oobj + 1) * ow, row.begin());
+                }
+                and_bits(cand, row, !l->positive);
+                continue;
+            }
+            checks.push_back(l);
+        }
+        bound[v] = 1;
+        for (u32 w = 0; w < ow; ++w)
+        {
+            u64 word = cand[w];
+            while (word)
+            {
+                const u32 o = w * 64 + static_cast<u32>(std::countr_zero(word));
+                word &= word - 1;
+                bind[v] = o;
+                bool ok = true;
+                for (const Literal* l : checks)
+                {
+                    std::vector<u32> objs;
+                    for (i32 x : l->terms)
+                        objs.push_back(x < 0 ? term_object(x) : bind[x]);
+                    bool h;
+                    if (T->preds[l->pred].kind != 'S')
+                    {
+                        const u64 c = cid_of(l->pred, objs.data());
+                        h = c < C->layout.fluent_count && reached[c];
+                    }
+                    else if (l->pred == eq)
+                        h = objs[0] == objs[1];
+                    else
+                        h = static_holds(l->pred, objs.data());
+                    if (h != l->positive)
+                    {
+                        ok = false;
+                        break;
+                    }
+                }
+                if (ok)
+                    enumerate(s, body, order, d + 1, bind, bound, unary, fwd, bwd, reached, eq, heads);
+            }
+        }
+        bound[v] = 0;
+    }
+
+    // --------------------------------------------------------------------------------------------- atom mode
+    // Dense where it is not wider than the reachable slots (task.cpp:106-143).
+    void choose_mode()
+    {
+        const Layout& L = C->layout;
+        if (L.fluent_count > (u64{1} << 28))
+            throw Error("the typed-dense canonical space of " + std::to_string(L.fluent_count) + " atoms exceeds 2^28");
+        u32 max_arity = 0;
+        for (const auto& p : T->preds)
+            if (p.kind == 'F')
+                max_arity = std::max(max_arity, p.arity);
+        auto frozen_bytes = [&](u64 atoms)
+        {
+            const u64 per = (1 + std::max<u64>(1, max_arity)) * 4 + 16 + 8;
+            return atoms * per + (L.fluent_count + 1) * 4;
+        };
+        constexpr u64 kMaxBytes = u64{4} << 30;
+        std::vector<u64> reach;
+        AtomMode mode = AtomMode::Dense;
+        if (m_opt != AtomsOption::Dense)
+        {
+            reach = reachable_fluents();
+            C->reachable_fluent = reach.size();
+            const bool dense_fits = words_for(L.fluent_count) <= words_for(reach.size()) && frozen_bytes(L.fluent_count) <= kMaxBytes;
+            mode = m_opt == AtomsOption::Auto && dense_fits ? AtomMode::Dense : AtomMode::Reachable;
+        }
+        if (frozen_bytes(mode == AtomMode::Dense ? L.fluent_count : reach.size()) > kMaxBytes)
+            throw Error("atom slots need more than 4 GiB of records");
+        C->mode = mode;
+        C->slot_of.assign(L.fluent_count, kNone);
+        if (mode == AtomMode::Dense)
+        {
+            C->fluent_slots = static_cast<u32>(L.fluent_count);
+            C->slot_cid.resize(L.fluent_count);
+            for (u64 c = 0; c < L.fluent_count; ++c)
+            {
+                C->slot_of[c] = static_cast<u32>(c);
+                C->slot_cid[c] = c;
+            }
+        }
+        else
+        {
+            C->fluent_slots = static_cast<u32>(reach.size());
+            C->slot_cid = reach;
+            for (u32 s = 0; s < reach.size(); ++s)
+                C->slot_of[reach[s]] = s;
+        }
+        C->words = std::max<u32>(1, words_for(C->fluent_slots));
+    }
+
+    u32 slot_of_cid(u64 c) const { return c < C->layout.fluent_count ? C->slot_of[c] : kNone; }
+
+    void build_state_tables()
+    {
+        C->initial.assign(C->words, 0);
+        for (const auto& a : T->fluent_init)
+        {
+            const u32 s = slot_of_cid(cid_of(a[0], a.data() + 1));
+            if (s == kNone)
+                throw Error("an initial atom has no slot");
+            C->initial[s >> 6] |= u64{1} << (s & 63);
+        }
+        // goal: static literals folded, fluent ones as slot masks (a positive atom without a slot never holds)
+        std::set<std::vector<u32>> pos_atoms;
+        for (const Literal& l : T->goal)
+        {
+            std::vector<u32> objs;
+            for (i32 x : l.terms)
+                objs.push_back(term_object(x));
+            if (T->preds[l.pred].kind == 'S')
+            {
+                if (static_holds(l.pred, objs.data()) != l.positive)
+                    C->goal_unsat = true;
+                continue;
+            }
+            std::vector<u32> key{l.pred};
+            key.insert(key.end(), objs.begin(), objs.end());
+            if (l.positive)
+                pos_atoms.insert(key);
+            const u32 s = slot_of_cid(cid_of(l.pred, objs.data()));
+            if (s == kNone)
+            {
+                if (l.positive)
+                    C->goal_unsat = true;
+                continue;
+            }
+            (l.positive ? C->goal_pos : C->goal_neg).push_back(s);
+        }
+        for (const Literal& l : T->goal)
+            if (!l.positive && T->preds[l.pred].kind != 'S')
+            {
+                std::vector<u32> key{l.pred};
+                for (i32 x : l.terms)
+                    key.push_back(term_object(x));
+                if (pos_atoms.count(key))
+                    C->goal_unsat = true;
+            }
+        C->label_width = 0;
+        for (const auto& s : T->schemas)
+            C->label_width = std::max(C->label_width, s.arity);
+    }
+
+    // --------------------------------------------------------------------------------------------- device image
+    struct PairKey
+    {
+        u32 pred, dir;
+        bool operator<(const PairKey& o) const { return pred != o.pred ? pred < o.pred : dir < o.dir; }
+    };
+
+    u32 pair_of(u32 pred, u32 dir)
+    {
+        const PairKey k{pred, dir};
+        if (auto it = m_pairs.find(k); it != m_pairs.end())
+            return it->second;
+        const u32 id = static_cast<u32>(m_pair_list.size());
+        m_pairs.emplace(k, id);
+        m_pair_list.push_back(k);
+        return id;
+    }
+
+    // object window [lo, hi] of a layout position's domain (empty domain: lo = hi + 1)
+    std::pair<u32, u32> position_window(u32 pos) const
+    {
+        const auto& d = C->layout.domain[pos];
+        if (d.empty())
+            return {0, 0};
+        return {d.front(), d.back() - d.front() + 1};
+    }
+
+    void build_image()
+    {
+        const u32 m = static_cast<u32>(T->preds.size());
+        const u32 eq = equality_pred();
+        (void)eq;
+        std::vector<DevSchema> schemas;
+        std::vector<DevStep> steps;
+        std::vector<DevCons> cons;
+        std::vector<DevCheck> checks;
+        std::vector<DevEffect> effects;
+        std::vector<u64> dom0_words;
+        // static k-ary relations used by checks
+        std::map<u32, u32> static_rel;  // pred -> index
+        std::vector<DevStaticMeta> static_meta;
+        std::vector<u64> static_key_words;
+        auto rel_of = [&](u32 p) -> u32
+        {
+            if (auto it = static_rel.find(p); it != static_rel.end())
+                return it->second;
+            const u32 id = static_cast<u32>(static_meta.size());
+            DevStaticMeta meta{};
+            meta.arity = T->preds[p].arity;
+            std::vector<u64> keys(static_keys[p].begin(), static_keys[p].end());
+            std::sort(keys.begin(), keys.end());
+            meta.keys = static_key_words.size();  // relative; fixed up below
+            meta.count = keys.size();
+            static_key_words.insert(static_key_words.end(), keys.begin(), keys.end());
+            static_meta.push_back(meta);
+            static_rel.emplace(p, id);
+            return id;
+        };
+
+        for (u32 si = 0; si < T->schemas.size(); ++si)
+        {
+            const SchemaText& s = T->schemas[si];
+            DevSchema ds{};
+            ds.arity = s.arity;
+            ds.never = C->never[si];
+            // windows and dom0 (window-aligned)
+            std::vector<u32> lo(s.arity, 0), wwords(s.arity, 1), dom_off(s.arity, 0);
+            for (u32 v = 0; v < s.arity; ++v)
+            {
+                const Bits& d = C->dom0[si][v];
+                u32 first = kNone, last = 0;
+                for (u32 o = 0; o < n; ++o)
+                    if (test_bit(d, o))
+                    {
+                        if (first == kNone)
+                            first = o;
+                        last = o;
+                    }
+                if (first == kNone)
+                    first = last = 0;
+                lo[v] = first;
+                wwords[v] = words_for(last - first + 1);
+                dom_off[v] = static_cast<u32>(dom0_words.size());
+                Bits wbits(wwords[v], 0);
+                for (u32 o = first; o <= last && o < n; ++o)
+                    if (test_bit(d, o))
+                        wbits[(o - first) >> 6] |= u64{1} << ((o - first) & 63);
+                dom0_words.insert(dom0_words.end(), wbits.begin(), wbits.end());
+            }
+            // ground fluent checks
+            ds.ground_begin = static_cast<u32>(checks.size());
+            for (const Literal& l : s.pre)
+                if (distinct_params(l.terms).empty() && T->preds[l.pred].kind == 'F')
+                    checks.push_back(make_check(l, rel_of));
+            ds.ground_end = static_cast<u32>(checks.size());
+
+            // a step binding `v` after the parameters marked in `bound`
+            auto make_step = [&](u32 v, const std::vector<u8>& bound)
+            {
+                DevStep st{};
+                st.param = v;
+                st.lo = lo[v];
+                st.words = wwords[v];
+                st.cons_begin = static_cast<u32>(cons.size());
+                cons.push_back(DevCons{static_cast<u32>(ConsKind::Dom0), 0, kNone, 0, dom_off[v], 0});
+                st.check_begin = kNone;
+                std::vector<DevCheck> mine;
+                for (const Literal& l : s.pre)
+                {
+                    const PredicateText& P = T->preds[l.pred];
+                    const auto ps = distinct_params(l.terms);
+                    if (std::find(ps.begin(), ps.end(), v) == ps.end())
+                        continue;
+                    bool rest = true;
+                    for (u32 q : ps)
+                        if (q != v && !bound[q])
+                            rest = false;
+                    if (!rest)
+                        continue;
+                    const bool fluent = P.kind == 'F';
+                    if (P.arity == 1)
+                    {
+                        if (fluent)
+                            cons.push_back(DevCons{static_cast<u32>(ConsKind::ViewUnary), l.positive ? 0u : 1u, kNone, 0,
+                                                   pair_of(l.pred, 0), 0});
+                        continue;  // static unary: in dom0
+                    }
+                    if (P.arity == 2 && l.terms[0] != l.terms[1])
+                    {
+                        const u32 vpos = l.terms[0] == static_cast<i32>(v) ? 0 : 1, opos = 1 - vpos;
+                        const i32 ot = l.terms[opos];
+                        if (ot < 0)
+                        {
+                            if (fluent)  // the row of the constant: forward if the constant is at position 0
+                                cons.push_back(DevCons{static_cast<u32>(ConsKind::ViewRow), l.positive ? 0u : 1u, kNone,
+                                                       term_object(ot), pair_of(l.pred, opos == 0 ? 0 : 1), 0});
+                            continue;  // static with a constant: in dom0
+                        }
+                        if (fluent)
+                            cons.push_back(DevCons{static_cast<u32>(ConsKind::ViewRow), l.positive ? 0u : 1u,
+                                                   static_cast<u32>(ot), 0, pair_of(l.pred, opos == 0 ? 0 : 1), 0});
+                        else
+                            cons.push_back(DevCons{static_cast<u32>(ConsKind::StaticRow), l.positive ? 0u : 1u,
+                                                   static_cast<u32>(ot), 0, static_rows(l.pred, opos, vpos), 0});
+                        continue;
+                    }
+                    mine.push_back(make_check(l, rel_of));
+                }
+                st.cons_end = static_cast<u32>(cons.size());
+                st.check_begin = static_cast<u32>(checks.size());
+                checks.insert(checks.end(), mine.begin(), mine.end());
+                st.check_end = static_cast<u32>(checks.size());
+                return st;
+            };
+
+            // plans P_j: parameters [0, j) bound, the rest in greedy order
+            for (u32 j = 0; j <= s.arity; ++j)
+            {
+                ds.plan_begin[j] = static_cast<u32>(steps.size());
+                std::vector<u8> bound(s.arity, 0);
+                for (u32 v = 0; v < j; ++v)
+                    bound[v] = 1;
+                for (u32 placed = j; placed < s.arity; ++placed)
+                {
+                    int best = -1;
+                    long best_score = 0;
+                    for (u32 v = 0; v < s.arity; ++v)
+                    {
+                        if (bound[v])
+                            continue;
+                        long links = 0, un = 0;
+                        for (const Literal& l : s.pre)
+                        {
+                            const auto ps = distinct_params(l.terms);
+                            if (std::find(ps.begin(), ps.end(), v) == ps.end())
+                                continue;
+                            if (T->preds[l.pred].kind == 'F' && ps.size() == 1)
+                                ++un;
+                            if (ps.size() == 2)
+                                for (u32 q : ps)
+                                    if (q != v && bound[q])
+                                        ++links;
+                        }
+                        const long score = links * 1000000 + un * 10000 - static_cast<long>(popcount(C->dom0[si][v]));
+                        if (best < 0 || score > best_score)
+                            best = static_cast<int>(v), best_score = score;
+                    }
+                    steps.push_back(make_step(static_cast<u32>(best), bound));
+                    bound[best] = 1;
+                }
+            }
+            ds.plan_begin[s.arity + 1] = static_cast<u32>(steps.size());
+            for (u32 j = s.arity + 2; j < kMaxParams + 2; ++j)
+                ds.plan_begin[j] = ds.plan_begin[s.arity + 1];
+            // filters F_i
+            for (u32 i = 0; i < s.arity; ++i)
+            {
+                std::vector<u8> bound(s.arity, 0);
+                for (u32 v = 0; v < i; ++v)
+                    bound[v] = 1;
+                ds.filter_step[i] = static_cast<u32>(steps.size());
+                steps.push_back(make_step(i, bound));
+            }
+            // effects: adds first, then deletes
+            ds.eff_begin = static_cast<u32>(effects.size());
+            for (int pass = 0; pass < 2; ++pass)
+                for (const Literal& l : s.eff)
+                {
+                    if (l.positive != (pass == 0))
+                        continue;
+                    DevEffect e{};
+                    e.pred = l.pred;
+                    e.base = C->layout.offset[l.pred];
+                    if (l.terms.size() > 4)
+                        throw Error("effect literals of arity above 4 are not supported by the device path");
+                    for (u32 i = 0; i < l.terms.size(); ++i)
+                    {
+                        const u32 pos = C->layout.pos_begin[l.pred] + i;
+                        if (l.terms[i] < 0)
+                            e.base += C->layout.rs[pos][term_object(l.terms[i])];
+                        else
+                        {
+                            e.var_param[e.nvar] = static_cast<u32>(l.terms[i]);
+                            e.var_pos[e.nvar] = pos;
+                            ++e.nvar;
+                        }
+                    }
+                    effects.push_back(e);
+                }
+            ds.eff_end = static_cast<u32>(effects.size());
+            ds.nadd = 0;
+            for (const Literal& l : s.eff)
+                ds.nadd += l.positive ? 1 : 0;
+            schemas.push_back(ds);
+        }
+
+        // view pairs: windows and offsets
+        std::vector<DevPair> pairs;
+        u32 view_words = 0;
+        for (const PairKey& k : m_pair_list)
+        {
+            DevPair p{};
+            p.pred = k.pred;
+            p.dir = k.dir;
+            const u32 pb = C->layout.pos_begin[k.pred];
+            if (T->preds[k.pred].arity == 1)
+            {
+                p.src_lo = 0;
+                p.src_n = 1;
+                const auto [dl, dn] = position_window(pb);
+                p.dst_lo = dl;
+                p.dst_words = std::max<u32>(1, words_for(dn));
+            }
+            else
+            {
+                const u32 spos = pb + (k.dir == 0 ? 0 : 1), dpos = pb + (k.dir == 0 ? 1 : 0);
+                const auto [sl, sn] = position_window(spos);
+                const auto [dl, dn] = position_window(dpos);
+                p.src_lo = sl;
+                p.src_n = std::max<u32>(1, sn);
+                p.dst_lo = dl;
+                p.dst_words = std::max<u32>(1, words_for(dn));
+            }
+            p.offset = view_words;
+            view_words += p.src_n * p.dst_words;
+            pairs.push_back(p);
+        }
+
+        // slot records (pred | a0 << 16 | a1 << 32 | a2 << 48) for the view build and the atom listing
+        std::vector<u64> records(C->fluent_slots, 0);
+        {
+            std::vector<u32> by_offset;
+            for (u32 p = 0; p < m; ++p)
+                if (T->preds[p].kind == 'F' && C->layout.size[p] > 0)
+                    by_offset.push_back(p);
+            for (u32 s = 0; s < C->fluent_slots; ++s)
+            {
+                const u64 c = C->slot_cid[s];
+                u32 p = by_offset[0];
+                for (u32 q : by_offset)
+                    if (C->layout.offset[q] <= c)
+                        p = q;
+                u64 rem = c - C->layout.offset[p];
+                const u32 ar = T->preds[p].arity;
+                u64 rec = p;
+                // decode ranks: last position has stride 1
+                std::vector<u32> args(ar, 0);
+                for (u32 i = ar; i-- > 0;)
+                {
+                    const auto& dom = C->layout.domain[C->layout.pos_begin[p] + i];
+                    const u64 dsz = std::max<u64>(1, dom.size());
+                    args[i] = dom[rem % dsz];
+                    rem /= dsz;
+                }
+                for (u32 i = 0; i < ar && i < 3; ++i)
+                {
+                    if (args[i] >= 65536)
+                        throw Error("objects beyond 65535 are not supported by the device path");
+                    rec |= static_cast<u64>(args[i]) << (16 * (i + 1));
+                }
+                records[s] = rec;
+            }
+        }
+
+        // per predicate: its view pairs (unary/forward, backward) for the view build
+        std::vector<u64> pred_pairs(m, ~u64{0});
+        for (u32 i = 0; i < pairs.size(); ++i)
+        {
+            u64& e = pred_pairs[pairs[i].pred];
+            if (pairs[i].dir == 0)
+                e = (e & 0xFFFFFFFF00000000ull) | i;
+            else
+                e = (e & 0x00000000FFFFFFFFull) | (static_cast<u64>(i) << 32);
+        }
+
+        // assemble the image
+        std::vector<u64> img;
+        auto reserve_words = [&](size_t w)
+        {
+            const u64 off = img.size();
+            img.resize(img.size() + w, 0);
+            return off;
+        };
+        auto put = [&](const void* src, size_t bytes) -> u64
+        {
+            const u64 off = reserve_words((bytes + 7) / 8);
+            if (bytes)
+                std::memcpy(img.data() + off, src, bytes);
+            return off;
+        };
+        reserve_words((sizeof(DevTaskHeader) + 7) / 8);
+        DevTaskHeader h{};
+        h.num_objects = n;
+        h.ow = ow;
+        h.words = C->words;
+        h.fluent_slots = C->fluent_slots;
+        h.dense = C->mode == AtomMode::Dense ? 1 : 0;
+        h.num_schemas = static_cast<u32>(schemas.size());
+        h.label_width = C->label_width;
+        h.num_pairs = static_cast<u32>(pairs.size());
+        h.view_words = view_words;
+        h.num_goal_pos = static_cast<u32>(C->goal_pos.size());
+        h.num_goal_neg = static_cast<u32>(C->goal_neg.size());
+        h.goal_unsat = C->goal_unsat ? 1 : 0;
+        h.fluent_count = C->layout.fluent_count;
+        h.off_schemas = put(schemas.data(), schemas.size() * sizeof(DevSchema));
+        h.off_steps = put(steps.data(), steps.size() * sizeof(DevStep));
+        h.off_cons = put(cons.data(), cons.size() * sizeof(DevCons));
+        h.off_checks = put(checks.data(), checks.size() * sizeof(DevCheck));
+        h.off_effects = put(effects.data(), effects.size() * sizeof(DevEffect));
+        h.off_pairs = put(pairs.data(), pairs.size() * sizeof(DevPair));
+        // rs tables: per position n entries (u64)
+        h.num_positions = static_cast<u32>(C->layout.rs.size());
+        h.off_rs = reserve_words(static_cast<size_t>(h.num_positions) * n);
+        for (u32 pos = 0; pos < h.num_positions; ++pos)
+            std::copy(C->layout.rs[pos].begin(), C->layout.rs[pos].end(), img.begin() + h.off_rs + static_cast<size_t>(pos) * n);
+        {
+            std::vector<u32> so(C->mode == AtomMode::Dense ? 0 : C->layout.fluent_count);
+            for (size_t c = 0; c < so.size(); ++c)
+                so[c] = C->slot_of[c];
+            h.off_slot_of = put(so.data(), so.size() * sizeof(u32));
+        }
+        h.off_records = put(records.data(), records.size() * sizeof(u64));
+        h.off_dom0 = put(dom0_words.data(), dom0_words.size() * sizeof(u64));
+        {
+            // static row tables back to back (n * ow words each); DevCons.table holds the table index, the kernel
+            // multiplies by n * ow
+            h.off_static_rows = img.size();
+            for (const auto& t : m_row_data)
+                img.insert(img.end(), t.begin(), t.end());
+        }
+        h.off_static_keys = put(static_key_words.data(), static_key_words.size() * sizeof(u64));
+        for (auto& meta : static_meta)
+            meta.keys += h.off_static_keys;
+        h.off_static_meta = put(static_meta.data(), static_meta.size() * sizeof(DevStaticMeta));
+        h.off_goal_pos = put(C->goal_pos.data(), C->goal_pos.size() * sizeof(u32));
+        h.off_goal_neg = put(C->goal_neg.data(), C->goal_neg.size() * sizeof(u32));
+        h.off_initial = put(C->initial.data(), C->initial.size() * sizeof(u64));
+        {
+            std::vector<u32> ar(m);
+            for (u32 p = 0; p < m; ++p)
+                ar[p] = T->preds[p].arity;
+            h.off_pred_arity = put(ar.data(), ar.size() * sizeof(u32));
+            h.off_pos_begin = put(C->layout.pos_begin.data(), C->layout.pos_begin.size() * sizeof(u32));
+        }
+        h.off_pred_pairs = put(pred_pairs.data(), pred_pairs.size() * sizeof(u64));
+        {
+            std::vector<u64> offs(m, 0);
+            for (u32 p = 0; p < m; ++p)
+                offs[p] = C->layout.offset[p] == kNone64 ? 0 : C->layout.offset[p];
+            h.off_pred_offset = put(offs.data(), offs.size() * sizeof(u64));
+        }
+        std::memcpy(img.data(), &h, sizeof(h));
+        C->image = std::move(img);
+    }
+
+    template<class RelOf>
+    DevCheck make_check(const Literal& l, RelOf&& rel_of)
+    {
+        DevCheck c{};
+        c.pos = l.positive ? 1 : 0;
+        c.nterms = static_cast<u32>(l.terms.size());
+        if (c.nterms > 6)
+            throw Error("literal arity above 6");
+        for (u32 i = 0; i < c.nterms; ++i)
+            c.terms[i] = l.terms[i];
+        if (T->preds[l.pred].kind == 'F')
+        {
+            c.kind = static_cast<u32>(CheckKind::Fluent);
+            c.pred = l.pred;
+        }
+        else
+        {
+            c.kind = static_cast<u32>(CheckKind::Static);
+            c.pred = rel_of(l.pred);
+        }
+        return c;
+    }
+
+    AtomsOption m_opt;
+    std::unique_ptr<CompiledTask> C;
+    const TaskText* T = nullptr;
+    u32 n = 0, ow = 1;
+    std::vector<std::vector<const std::vector<u32>*>> static_atoms;
+    std::vector<std::unordered_set<u64>> static_keys;
+    std::vector<Bits> s_unary;
+    std::map<std::tuple<u32, u32, u32>, u32> m_row_tables;
+    std::vector<Bits> m_row_data;
+    std::map<PairKey, u32> m_pairs;
+    std::vector<PairKey> m_pair_list;
+};
+}  // namespace
+
+TaskText parse_task_text(std::string_view text) { return Reader(text).read(); }
+
+bool CompiledTask::static_holds(u32 pred, const u32* objs) const
+{
+    const u64 k = static_key(objs, text.preds[pred].arity, std::max<u32>(n, 1));
+    return std::binary_search(static_keys[pred].begin(), static_keys[pred].end(), k);
+}
+
+u32 CompiledTask::slot_of_atom(u32 pred, const u32* objs) const
+{
+    const u64 c = layout.encode(pred, objs, text.preds[pred].arity);
+    return c < layout.fluent_count ? slot_of[c] : kNone;
+}
+
+GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit)
+{
+    const TaskText& T = task.text;
+    GroundActions g;
+    g.label_width = task.label_width;
+    const u32 eq = [&] {
+        for (u32 p = 0; p < T.preds.size(); ++p)
+            if (T.preds[p].kind == 'S' && T.preds[p].name == "=" && T.preds[p].arity == 2)
+                return p;
+        return kNone;
+    }();
+    (void)eq;  // the successor engine reads "=" as a static relation over its initial atoms, as the reference does
+    for (u32 si = 0; si < T.schemas.size(); ++si)
+    {
+        const SchemaText& s = T.schemas[si];
+        if (witness_pruning)
+        {
+            std::vector<u8> rel(s.arity, 0);
+            for (const Literal& l : s.eff)
+                for (i32 x : l.terms)
+                    if (x >= 0)
+                        rel[x] = 1;
+            for (u32 v = 0; v < s.arity; ++v)
+                if (!rel[v])
+                    throw Error("schema " + s.name + " has a parameter no effect mentions; device witness pruning is not implemented "
+                                "(run with witness_pruning off)");
+        }
+        if (task.never[si])
+            continue;
+        // lexicographic enumeration over dom0, static literals checked once their parameters are bound
+        std::vector<u32> bind(s.arity, 0);
+        std::vector<std::vector<const Literal*>> statics_at(s.arity + 1);
+        for (const Literal& l : s.pre)
+        {
+            if (T.preds[l.pred].kind != 'S')
+                continue;
+            i32 last = -1;
+            for (i32 x : l.terms)
+                last = std::max(last, x);
+            statics_at[static_cast<u32>(last + 1)].push_back(&l);
+        }
+        auto lit_objs = [&](const Literal& l) {
+            std::vector<u32> o;
+            for (i32 x : l.terms)
+                o.push_back(x < 0 ? term_object(x) : bind[x]);
+            return o;
+        };
+        auto statics_ok = [&](u32 level) {
+            for (const Literal* l : statics_at[level])
+            {
+                const auto o = lit_objs(*l);
+                if (task.static_holds(l->pred, o.data()) != l->positive)
+                    return false;
+            }
+            return true;
+        };
+        if (!statics_ok(0))
+            continue;
+        std::function<void(u32)> rec = [&](u32 d) {
+            if (d == s.arity)
+            {
+                std::vector<u32> pos, neg, add, del;
+                for (const Literal& l : s.pre)
+                {
+                    if (T.preds[l.pred].kind == 'S')
+                        continue;
+                    const auto o = lit_objs(l);
+                    const u32 slot = task.slot_of_atom(l.pred, o.data());
+                    if (slot == kNone)
+                    {
+                        if (l.positive)
+                            return;  // never applicable
+                        continue;
+                    }
+                    (l.positive ? pos : neg).push_back(slot);
+                }
+                for (const Literal& l : s.eff)
+                {
+                    const auto o = lit_objs(l);
+                    const u32 slot = task.slot_of_atom(l.pred, o.data());
+                    if (slot == kNone)
+                    {
+                        if (l.positive)
+                            throw Error("an add effect of " + s.name + " has no atom slot");
+                        continue;
+                    }
+                    (l.positive ? add : del).push_back(slot);
+                }
+                if (pos.size() > 255 || neg.size() > 255 || add.size() > 255 || del.size() > 255)
+                    throw Error("ground action with more than 255 atoms in one list");
+                if (g.meta.size() >= limit)
+                    throw Error("more than " + std::to_string(limit) + " ground actions");
+                g.meta.push_back(static_cast<u32>(pos.size()) | static_cast<u32>(neg.size()) << 8 | static_cast<u32>(add.size()) << 16 |
+                                 static_cast<u32>(del.size()) << 24);
+                g.off.push_back(static_cast<u32>(g.slots.size()));
+                for (auto* v : {&pos, &neg, &add, &del})
+                    g.slots.insert(g.slots.end(), v->begin(), v->end());
+                g.schema.push_back(si);
+                for (u32 k = 0; k < g.label_width; ++k)
+                    g.binding.push_back(k < s.arity ? bind[k] : kNone);
+                return;
+            }
+            const auto& dom = task.dom0[si][d];
+            for (u32 o = 0; o < task.n; ++o)
+            {
+                if (!((dom[o >> 6] >> (o & 63)) & 1))
+                    continue;
+                bind[d] = o;
+                if (statics_ok(d + 1))
+                    rec(d + 1);
+            }
+        };
+        rec(0);
+    }
+    return g;
+}
+
+std::unique_ptr<CompiledTask> compile_task(TaskText text, AtomsOption atoms) { return Compiler(std::move(text), atoms).run(); }
+}  // namespace mya

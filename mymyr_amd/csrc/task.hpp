@@ -1,0 +1,273 @@
+#pragma once
+// Host side of a planning task: the text reader, the task compiler (typed-dense canonical atom layout, relaxed
+// reachability, atom slots, initial state, goal) and the device image the HIP kernels read.
+//
+// Semantics follow the reference task build (maichmueller/mymyr):
+//   text format                 src/mymyr/formalism/text_format.cpp:22-197
+//   dom0 of a parameter         src/mymyr/task/compile.cpp:803-915 (the matcher's static domain)
+//   canonical layout            src/mymyr/task/compile.cpp:1363-1455 (build_layout)
+//   atom mode (dense/reachable) src/mymyr/task/task.cpp:106-143 (choose_atom_mode)
+//   relaxed reachability        include/mymyr/reachability/relaxed_reachability.hpp:3-12 (rule semantics)
+//   initial state               src/mymyr/task/task.cpp:216-232
+// The code is this project's own: a single-threaded host compiler producing flat tables for the device.
+
+#include <array>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <string_view>
+#include <vector>
+
+namespace mya
+{
+using u8 = std::uint8_t;
+using u16 = std::uint16_t;
+using u32 = std::uint32_t;
+using u64 = std::uint64_t;
+using i32 = std::int32_t;
+using i64 = std::int64_t;
+
+struct Error : std::runtime_error
+{
+    using std::runtime_error::runtime_error;
+};
+
+constexpr u32 kNone = ~u32{0};
+constexpr u64 kNone64 = ~u64{0};
+
+/// A literal: terms >= 0 are parameter indices, < 0 encode object o as -(o + 1).
+struct Literal
+{
+    u32 pred = 0;
+    bool positive = true;
+    std::vector<i32> terms;
+};
+
+struct SchemaText
+{
+    std::string name;
+    u32 arity = 0;
+    std::vector<Literal> pre;
+    std::vector<Literal> eff;  // positive = add, negative = delete
+};
+
+struct PredicateText
+{
+    char kind = 'S';  // S static, F fluent, D derived
+    u32 arity = 0;
+    std::string name;
+};
+
+struct TaskText
+{
+    u32 objects = 0;
+    std::vector<PredicateText> preds;
+    std::vector<std::vector<u32>> static_init, fluent_init;  // [pred, args...]
+    std::vector<Literal> goal;                                // ground
+    std::vector<SchemaText> schemas;
+};
+
+/// Parses the reference's task text format (classical subset: no numeric sections, no axioms, no conditional
+/// effects). Throws mya::Error naming what is unsupported or malformed.
+TaskText parse_task_text(std::string_view text);
+
+enum class AtomMode : u32
+{
+    Reachable = 0,
+    Dense = 1,
+};
+enum class AtomsOption : u32
+{
+    Auto = 0,
+    Reachable = 1,
+    Dense = 2,
+};
+
+/// Typed-dense canonical ids: cid(p, a) = offset[p] + sum_i rs[pos_begin[p] + i][a_i].
+struct Layout
+{
+    static constexpr u64 kOutside = u64{1} << 40;
+    std::vector<u64> offset;     // per predicate (kNone64 for static predicates)
+    std::vector<u64> size;       // per predicate
+    std::vector<u32> pos_begin;  // per predicate
+    std::vector<std::vector<u64>> rs;      // per position: rank * stride or kOutside, per object
+    std::vector<std::vector<u32>> domain;  // per position: objects in rank order
+    u64 fluent_count = 0;
+    [[nodiscard]] u64 encode(u32 p, const u32* args, u32 arity) const
+    {
+        u64 c = offset[p];
+        for (u32 i = 0; i < arity; ++i)
+            c += rs[pos_begin[p] + i][args[i]];
+        return c;
+    }
+};
+
+/// One constraint on the candidate objects of a parameter (an AND term of its candidate bitset).
+enum class ConsKind : u32
+{
+    Dom0 = 0,        // the static domain (dom0) of the parameter
+    ViewUnary = 1,   // the view row of a unary fluent predicate
+    ViewRow = 2,     // a row of a binary fluent predicate, indexed by a bound parameter or a constant
+    StaticRow = 3,   // a row of a binary static predicate, indexed by a bound parameter
+};
+
+/// A literal checked once all its parameters are bound (k-ary literals, repeated variables, ground fluents).
+enum class CheckKind : u32
+{
+    Fluent = 0,  // canonical key -> slot -> state bit
+    Static = 1,  // static relation membership (sorted keys)
+};
+
+// ---------------------------------------------------------------------------------------------------------------
+// Device image. Everything below is POD and copied verbatim into one device buffer; offsets are in u64 words from
+// the image start. The kernels index it directly.
+
+struct DevCons
+{
+    u32 kind;   // ConsKind
+    u32 neg;    // 1: AND with the complement (negative literal)
+    u32 src;    // ViewRow / StaticRow: the source parameter, or kNone when `obj` is a constant
+    u32 obj;    // constant source object (ViewRow with src == kNone)
+    u32 table;  // Dom0: word offset of the dom0 bits; ViewUnary / ViewRow: view pair index; StaticRow: static row table
+    u32 pad;
+};
+
+struct DevCheck
+{
+    u32 kind;  // CheckKind
+    u32 pos;   // literal polarity
+    u32 pred;  // predicate (Static: its relation index)
+    u32 nterms;
+    i32 terms[6];
+};
+
+/// One parameter to bind: its object window and the AND terms of its candidate set.
+struct DevStep
+{
+    u32 param;
+    u32 lo;      // first object of the window
+    u32 words;   // window words
+    u32 cons_begin, cons_end;    // into the schema's DevCons
+    u32 check_begin, check_end;  // into the schema's DevCheck
+    u32 pad;
+};
+
+constexpr u32 kMaxParams = 6;
+
+/// Per schema: plans P_j (j = 0..arity) count the bindings with parameters [0, j) bound; filters F_i (i < arity) give
+/// the candidates of parameter i with [0, i) bound (the lexicographic pick).
+struct DevSchema
+{
+    u32 arity;
+    u32 never;       // a static precondition fails, or a dom0 is empty
+    u32 ground_begin, ground_end;  // ground fluent checks (DevCheck) of the precondition
+    u32 plan_begin[kMaxParams + 2];  // into steps: plan j occupies [plan_begin[j], plan_begin[j + 1])
+    u32 filter_step[kMaxParams];     // the DevStep of filter i
+    u32 eff_begin, eff_end;          // into effects
+    u32 nadd;                        // effects [eff_begin, eff_begin + nadd) add, the rest delete
+    u32 pad;
+};
+
+/// An effect pattern: cid = base + sum over parameter terms of rs[pos][object].
+struct DevEffect
+{
+    u32 pred;
+    u32 nvar;
+    u64 base;
+    u32 var_param[4];
+    u32 var_pos[4];  // global position index into the rs tables
+};
+
+/// A view pair: the rows of a fluent predicate of arity 1 (one row) or 2 (forward: source position 0, or backward).
+struct DevPair
+{
+    u32 pred;
+    u32 dir;      // 0 forward (rows by position 0's object, bits of position 1), 1 backward; unary: 0
+    u32 src_lo, src_n;   // source object window (rows)
+    u32 dst_lo, dst_words;  // destination object window
+    u32 offset;   // word offset of the pair's rows in the per-state view
+    u32 pad;
+};
+
+struct DevTaskHeader
+{
+    u32 num_objects;
+    u32 ow;             // words_for(num_objects)
+    u32 words;          // state words W
+    u32 fluent_slots;
+    u32 dense;          // 1: slot = cid
+    u32 num_schemas;
+    u32 label_width;
+    u32 num_pairs;
+    u32 view_words;     // per-state view size (u64 words)
+    u32 num_goal_pos, num_goal_neg;
+    u32 goal_unsat;
+    u64 fluent_count;
+    // word offsets into the image
+    u64 off_schemas, off_steps, off_cons, off_checks, off_effects, off_pairs;
+    u64 off_rs, off_slot_of, off_records, off_dom0, off_static_rows, off_static_keys, off_static_meta;
+    u64 off_goal_pos, off_goal_neg, off_initial;
+    u64 off_pred_arity, off_pos_begin;
+    u64 off_pred_pairs;   // per predicate: view pair of the unary / forward rows (low 32 bits), backward (high)
+    u64 off_pred_offset;  // per predicate: first canonical id (u64)
+    u32 num_positions;
+    u32 init_count;     // successors of the initial state (filled once the device has counted them)
+};
+
+/// Static k-ary relation: sorted keys sum(obj_i * n^(ar-1-i)) at [keys, keys + count).
+struct DevStaticMeta
+{
+    u64 keys;
+    u64 count;
+    u32 arity;
+    u32 pad;
+};
+
+struct CompiledTask
+{
+    TaskText text;
+    u32 n = 0, ow = 1;
+    Layout layout;
+    AtomMode mode = AtomMode::Dense;
+    u64 reachable_fluent = 0;
+    u32 fluent_slots = 0, words = 1;
+    std::vector<u32> slot_of;     // per cid (fluent_count entries): slot or kNone
+    std::vector<u64> slot_cid;    // per slot
+    std::vector<u64> initial;     // [words]
+    std::vector<u32> goal_pos, goal_neg;  // goal slots
+    bool goal_unsat = false;
+    u32 label_width = 0;
+    std::vector<std::vector<std::vector<u64>>> dom0;  // per schema, per parameter: object bits (ow words)
+    std::vector<u8> never;                            // per schema
+    std::vector<std::vector<u64>> static_keys;        // per static predicate: sorted packed keys of its atoms
+    std::vector<u64> image;                           // the device image (DevTaskHeader first)
+    [[nodiscard]] const DevTaskHeader& header() const { return *reinterpret_cast<const DevTaskHeader*>(image.data()); }
+    [[nodiscard]] bool static_holds(u32 pred, const u32* objs) const;
+    [[nodiscard]] u32 slot_of_atom(u32 pred, const u32* objs) const;  // kNone: no slot
+};
+
+std::unique_ptr<CompiledTask> compile_task(TaskText text, AtomsOption atoms);
+
+/// Ground actions in canonical order (schema, then lexicographic binding), with their static preconditions evaluated
+/// and fluent ones resolved to slots. An action whose positive fluent precondition has no slot is dropped (it never
+/// applies); a negative one without a slot always holds.
+struct GroundActions
+{
+    std::vector<u32> meta;   // npos | nneg << 8 | nadd << 16 | ndel << 24
+    std::vector<u32> off;    // into slots
+    std::vector<u32> slots;  // pos..., neg..., add..., del...
+    std::vector<u32> schema;
+    std::vector<u32> binding;  // [num, label_width]
+    u32 label_width = 0;
+    [[nodiscard]] u32 size() const { return static_cast<u32>(meta.size()); }
+};
+
+/// Grounds every schema (static literals filter the bindings). Throws if more than `limit` actions result, if an
+/// action has more than 255 atoms in one list, or if `witness_pruning` is set and some schema has a parameter that no
+/// effect mentions (device witness pruning is not implemented).
+GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit);
+
+inline u32 words_for(u64 bits) { return static_cast<u32>((bits + 63) >> 6); }
+}  // namespace mya

@@ -1,0 +1,55 @@
+"""``search.brfs`` on the device: the drop-in for the reference's ``mymyr.search.brfs`` / ``mymyr.cuda.brfs``
+(python/src/search_bindings.cpp:3348, python/src/cuda_bindings.cpp:2716; C++ brfs(), include/mymyr/search/brfs.hpp:140).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+from .task import Task
+
+STATUS = {0: "solved", 1: "exhausted", 2: "out_of_states", 3: "out_of_time", 4: "cancelled", 5: "failed", 6: "unsolvable"}
+UNBOUNDED32 = 0xFFFFFFFF
+UNBOUNDED64 = (1 << 64) - 1
+
+
+@dataclass
+class BrfsResult:
+    """The fields of the reference's BrfsResult (include/mymyr/search/brfs.hpp:103-138) that the device search fills."""
+
+    status: str
+    states: int
+    expanded: int
+    generated: int
+    num_goal_states: int
+    layers: int
+    exhausted: bool
+    solved: bool
+    fingerprint: int
+    first_goal: int
+    search_s: float
+    device_s: float
+    layer_counts: list = field(default_factory=list)
+
+
+def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None, max_expanded: int | None = None,
+         witness_pruning: bool = True, stop_at_goal: bool = True, fingerprint: bool = False, layer_stats: bool = True,
+         chunk: int = 0, memory_states: int = 0) -> BrfsResult:
+    """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
+    (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer."""
+    o = _lib.BrfsOptions(UNBOUNDED32 if max_depth is None else max_depth, int(witness_pruning),
+                         UNBOUNDED64 if max_states is None else max_states, UNBOUNDED64 if max_expanded is None else max_expanded,
+                         int(stop_at_goal), int(fingerprint), chunk, memory_states)
+    r = _lib.BrfsResult()
+    lc = np.zeros((4096, 3), dtype=np.uint64)
+    n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096)
+    if n < 0:
+        check(-1)
+    return BrfsResult(STATUS.get(r.status, str(r.status)), r.states, r.expanded, r.generated, r.goal_states, r.layers,
+                      bool(r.exhausted), bool(r.solved), r.fingerprint, r.first_goal, r.search_s, r.device_s,
+                      lc[:n].tolist() if layer_stats else [])

@@ -1,0 +1,257 @@
+"""Test infrastructure, not product code: ctypes binding of oracle/_ref/libmymyr_ref.so, the reference CPU core
+(maichmueller/mymyr) compiled from its own sources by oracle/Makefile, with the harness oracle/ref_harness.cpp.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, as the checker or the timed CPU
+baseline; the product never imports it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_ref", "libmymyr_ref.so")
+
+
+class EnvConfig(Structure):
+    _fields_ = [
+        ("seed", c_uint64),
+        ("max_steps", c_uint32),
+        ("step_reward", c_float),
+        ("goal_reward", c_float),
+        ("dead_end_reward", c_float),
+        ("dead_end", c_int32),
+        ("dead_end_terminal", c_int32),
+        ("autoreset", c_int32),
+        ("canonical_order", c_int32),
+        ("witness_pruning", c_int32),
+    ]
+
+
+class BrfsOptions(Structure):
+    _fields_ = [
+        ("threads", c_uint32),
+        ("max_depth", c_uint32),
+        ("max_states", c_uint64),
+        ("witness_pruning", c_int32),
+        ("canonical_order", c_int32),
+        ("stop_at_goal", c_int32),
+        ("fingerprint", c_int32),
+    ]
+
+
+class BrfsResult(Structure):
+    _fields_ = [
+        ("states", c_uint64),
+        ("expanded", c_uint64),
+        ("generated", c_uint64),
+        ("goal_states", c_uint64),
+        ("fingerprint", c_uint64),
+        ("layers", c_uint32),
+        ("status", c_int32),
+        ("solved", c_int32),
+        ("exhausted", c_int32),
+        ("seconds", c_double),
+    ]
+
+
+def available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not available():
+            raise ImportError(f"reference build missing: {LIB_PATH} (make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "mref_last_error": (c_char_p, []),
+            "mref_task_load": (c_void_p, [c_char_p, c_int]),
+            "mref_task_free": (None, [c_void_p]),
+            "mref_task_info": (c_int, [c_void_p, c_void_p]),
+            "mref_task_slots": (c_int, [c_void_p, c_void_p, c_void_p]),
+            "mref_task_initial": (c_int, [c_void_p, c_void_p, c_uint32]),
+            "mref_task_goal": (c_int, [c_void_p, c_void_p, c_uint32]),
+            "mref_canonical_hash": (c_uint64, [c_void_p, c_void_p, c_uint32]),
+            "mref_successors": (c_int64, [c_void_p, c_void_p, c_uint32, c_int, c_int, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_uint64]),
+            "mref_hash_words": (c_uint64, [c_void_p, c_uint32, c_uint64]),
+            "mref_hash_state": (c_uint64, [c_void_p, c_uint32]),
+            "mref_hash_mix64": (c_uint64, [c_uint64]),
+            "mref_philox": (None, [c_uint64, c_uint64, c_uint64, c_uint32, c_void_p]),
+            "mref_philox_raw": (None, [c_void_p, c_uint32, c_uint32, c_void_p]),
+            "mref_successor_index": (c_uint32, [c_uint64, c_uint64, c_uint64, c_uint32]),
+            "mref_env_create": (c_void_p, [c_void_p, POINTER(EnvConfig), c_uint32]),
+            "mref_env_free": (None, [c_void_p]),
+            "mref_env_reset": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64]),
+            "mref_env_step": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
+                                      c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p]),
+            "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
+            "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _err() -> str:
+    return lib().mref_last_error().decode()
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+class RefTask:
+    """A reference Task (Task::from_text_file) plus its one-instance TaskTable."""
+
+    MODES = {"auto": 0, "reachable": 1, "dense": 2}
+
+    def __init__(self, path: str, atoms: str = "auto"):
+        h = lib().mref_task_load(str(path).encode(), self.MODES[atoms])
+        if not h:
+            raise RuntimeError(_err())
+        self._h = c_void_p(h)
+        info = np.zeros(9, dtype=np.uint64)
+        assert lib().mref_task_info(self._h, info.ctypes.data) == 0
+        (self.words, self.fluent_slots, mode, self.num_schemas, self.label_width, self.num_objects, self.max_arity,
+         self.table_words, self.dense_fluent) = (int(x) for x in info)
+        self.atom_mode = {0: "reachable", 1: "dense", 2: "lazy"}[mode]
+
+    def slot_records(self):
+        stride = 1 + max(1, self.max_arity)
+        rec = np.zeros((self.fluent_slots, stride), dtype=np.uint32)
+        cid = np.zeros(self.fluent_slots, dtype=np.uint64)
+        if lib().mref_task_slots(self._h, rec.ctypes.data, cid.ctypes.data) != 0:
+            raise RuntimeError(_err())
+        return rec, cid
+
+    def initial_state(self, words: int | None = None) -> np.ndarray:
+        w = self.table_words if words is None else words
+        row = np.zeros(w, dtype=np.uint64)
+        if lib().mref_task_initial(self._h, row.ctypes.data, w) != 0:
+            raise RuntimeError(_err())
+        return row
+
+    def is_goal(self, row: np.ndarray) -> bool:
+        row = np.ascontiguousarray(row, dtype=np.uint64)
+        return lib().mref_task_goal(self._h, row.ctypes.data, row.size) == 1
+
+    def canonical_hash(self, row: np.ndarray) -> int:
+        row = np.ascontiguousarray(row, dtype=np.uint64)
+        return int(lib().mref_canonical_hash(self._h, row.ctypes.data, row.size))
+
+    def successors(self, row: np.ndarray, witness: bool = False, canonical: bool = True, cap: int = 1 << 16):
+        """(schema [k], binding [k, L], rows [k, W]) in the reference generator's order."""
+        row = np.ascontiguousarray(row, dtype=np.uint64)
+        L = max(1, self.label_width)
+        W = self.table_words
+        schema = np.zeros(cap, dtype=np.int32)
+        binding = np.zeros((cap, L), dtype=np.int32)
+        rows = np.zeros((cap, W), dtype=np.uint64)
+        k = lib().mref_successors(self._h, row.ctypes.data, row.size, int(witness), int(canonical), schema.ctypes.data,
+                                  binding.ctypes.data, L, rows.ctypes.data, W, cap)
+        if k < 0:
+            raise RuntimeError(_err())
+        if k > cap:
+            return self.successors(row, witness, canonical, cap=int(k))
+        return schema[:k], binding[:k], rows[:k]
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().mref_task_free(self._h)
+            self._h = c_void_p()
+
+
+class RefEnv:
+    """rl::HostEnv over a one-instance table (reference env step semantics)."""
+
+    def __init__(self, task: RefTask, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, canonical_order=True,
+                 witness_pruning=False, threads=1):
+        self.task = task
+        self.cfg = EnvConfig(seed, max_steps, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
+                             int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning))
+        h = lib().mref_env_create(task._h, ctypes.byref(self.cfg), threads)
+        if not h:
+            raise RuntimeError(_err())
+        self._h = c_void_p(h)
+
+    def reset(self, states, steps, draws, at_goal, count, first_env=0):
+        rows, words = states.shape
+        if lib().mref_env_reset(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), _p(count), first_env) != 0:
+            raise RuntimeError(_err())
+
+    def step(self, states, steps, draws, at_goal, first_env=0, actions=None, reward=None, terminated=None, truncated=None,
+             count=None, schema=None, binding=None, goal=None, invalid=None, final_states=None):
+        rows, words = states.shape
+        lw = 0 if binding is None else binding.shape[1]
+        rc = lib().mref_env_step(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), first_env, _p(actions),
+                                 _p(reward), _p(terminated), _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal),
+                                 _p(invalid), _p(final_states))
+        if rc != 0:
+            raise RuntimeError(_err())
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().mref_env_free(self._h)
+            self._h = c_void_p()
+
+
+def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> tuple[float, int]:
+    """CpuEnvPool (threads workers): reset, then `steps` random-policy steps of every env. (seconds, checksum)."""
+    e = RefEnv.__new__(RefEnv)
+    c = EnvConfig(cfg.get("seed", 0), cfg.get("max_steps", 0), cfg.get("step_reward", 0.0), cfg.get("goal_reward", 1.0),
+                  cfg.get("dead_end_reward", 0.0), 1 if cfg.get("dead_end") == "none" else 0,
+                  int(cfg.get("dead_end_terminal", True)), int(cfg.get("autoreset", True)), 1, 0)
+    secs = c_double()
+    chk = c_uint64()
+    if lib().mref_pool_run(task._h, ctypes.byref(c), num_envs, threads, steps, ctypes.byref(secs), ctypes.byref(chk)) != 0:
+        raise RuntimeError(_err())
+    del e
+    return secs.value, chk.value
+
+
+def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
+         stop_at_goal=False, fingerprint=True):
+    o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint))
+    r = BrfsResult()
+    lc = np.zeros((4096, 3), dtype=np.uint64)
+    n = lib().mref_brfs(task._h, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096)
+    if n < 0:
+        raise RuntimeError(_err())
+    return {
+        "states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.goal_states,
+        "fingerprint": r.fingerprint, "layers": r.layers, "status": r.status, "solved": bool(r.solved),
+        "exhausted": bool(r.exhausted), "seconds": r.seconds, "layer_counts": lc[:n].tolist(),
+    }
+
+
+def hash_words(w: np.ndarray, seed: int = 0x2D358DCCAA6C78A5) -> int:
+    w = np.ascontiguousarray(w, dtype=np.uint64)
+    return int(lib().mref_hash_words(w.ctypes.data, w.size, seed))
+
+
+def hash_state(w: np.ndarray) -> int:
+    w = np.ascontiguousarray(w, dtype=np.uint64)
+    return int(lib().mref_hash_state(w.ctypes.data, w.size))
+
+
+def philox(seed: int, env: int, draw: int, purpose: int = 0) -> list[int]:
+    out = np.zeros(4, dtype=np.uint32)
+    lib().mref_philox(seed, env, draw, purpose, out.ctypes.data)
+    return [int(x) for x in out]
+
+
+def successor_index(seed: int, env: int, draw: int, count: int) -> int:
+    return int(lib().mref_successor_index(seed, env, draw, count))

@@ -1,0 +1,419 @@
+// Test infrastructure, not product code: a C-ABI harness over the reference CPU core (maichmueller/mymyr), compiled
+// together with the reference's own sources by oracle/Makefile into oracle/_ref/libmymyr_ref.so. Only tests/,
+// the smoke check and bench.py's CPU-baseline leg load it; the product library never links or calls it.
+//
+// Every entry point is a thin call into the reference API it names:
+//   task loading          Task::from_text_file           include/mymyr/task/task.hpp:166-167
+//   slot records          AtomIndex::record / canonical  include/mymyr/task/atom_index.hpp:167-172
+//   successors            Successors::generate           include/mymyr/successor/successors.hpp:154-248
+//   hashes                hash::words / hash::state      include/mymyr/core/hash.hpp:38-60
+//   Philox                rl::rng::block                 include/mymyr/rl/rng.hpp:45-83
+//   env step / reset      rl::HostEnv                    include/mymyr/rl/env.hpp:181-278
+//   env pool              rl::CpuEnvPool                 include/mymyr/rl/pool.hpp:114-172
+//   BrFS                  brfs(Task, BrfsOptions)        include/mymyr/search/brfs.hpp:140
+// Errors: functions return a negative value (or null) and mref_last_error() holds the message.
+
+#include "mymyr/core/hash.hpp"
+#include "mymyr/rl/env.hpp"
+#include "mymyr/rl/pool.hpp"
+#include "mymyr/rl/rng.hpp"
+#include "mymyr/rl/task_table.hpp"
+#include "mymyr/search/brfs.hpp"
+#include "mymyr/successor/successors.hpp"
+#include "mymyr/task/task.hpp"
+#include "mymyr/task/workspace.hpp"
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+#include <vector>
+
+using namespace mymyr;
+
+namespace
+{
+thread_local std::string g_error;
+
+template<class F>
+auto guarded(F&& f, decltype(f()) on_error) -> decltype(f())
+{
+    try
+    {
+        return f();
+    }
+    catch (const std::exception& e)
+    {
+        g_error = e.what();
+    }
+    catch (...)
+    {
+        g_error = "unknown exception";
+    }
+    return on_error;
+}
+}  // namespace
+
+struct mref_task
+{
+    TaskPtr task;
+    rl::TaskTablePtr table;
+};
+
+struct mref_env
+{
+    std::unique_ptr<rl::HostEnv> env;
+    std::unique_ptr<ThreadPool> pool;
+};
+
+extern "C" {
+
+struct mref_env_config
+{
+    uint64_t seed;
+    uint32_t max_steps;
+    float step_reward;
+    float goal_reward;
+    float dead_end_reward;
+    int32_t dead_end;  // 0 no_successors, 1 none
+    int32_t dead_end_terminal;
+    int32_t autoreset;
+    int32_t canonical_order;
+    int32_t witness_pruning;
+};
+
+struct mref_brfs_options
+{
+    uint32_t threads;
+    uint32_t max_depth;
+    uint64_t max_states;
+    int32_t witness_pruning;
+    int32_t canonical_order;
+    int32_t stop_at_goal;
+    int32_t fingerprint;
+};
+
+struct mref_brfs_result
+{
+    uint64_t states, expanded, generated, goal_states, fingerprint;
+    uint32_t layers;
+    int32_t status;
+    int32_t solved;
+    int32_t exhausted;
+    double seconds;
+};
+
+const char* mref_last_error() { return g_error.c_str(); }
+
+// atoms: 0 auto, 1 reachable, 2 dense
+mref_task* mref_task_load(const char* path, int atoms)
+{
+    return guarded(
+        [&]() -> mref_task*
+        {
+            TaskOptions o;
+            o.atoms = atoms == 1 ? TaskOptions::Atoms::Reachable : atoms == 2 ? TaskOptions::Atoms::Dense : TaskOptions::Atoms::Auto;
+            auto t = new mref_task;
+            t->task = Task::from_text_file(path, o);
+            t->table = rl::TaskTable::single(t->task);
+            return t;
+        },
+        nullptr);
+}
+
+void mref_task_free(mref_task* t) { delete t; }
+
+// out: words, fluent_slots, mode (0 reachable, 1 dense, 2 lazy), num_schemas, label_width, num_objects, max_arity,
+// table_words, dense_fluent (typed-dense canonical fluent count)
+int mref_task_info(mref_task* t, uint64_t* out)
+{
+    return guarded(
+        [&]() -> int
+        {
+            const Task& k = *t->task;
+            out[0] = k.words();
+            out[1] = k.atoms().fluent_slots();
+            out[2] = static_cast<uint64_t>(k.atoms().mode());
+            out[3] = k.num_schemas();
+            out[4] = t->table->label_width();
+            out[5] = k.data().num_objects();
+            out[6] = k.atoms().layout().max_arity;
+            out[7] = t->table->words();
+            out[8] = k.atoms().layout().fluent_count;
+            return 0;
+        },
+        -1);
+}
+
+// rec: [fluent_slots, 1 + max(1, max_arity)] = predicate then arguments; cid: [fluent_slots]
+int mref_task_slots(mref_task* t, uint32_t* rec, uint64_t* cid)
+{
+    return guarded(
+        [&]() -> int
+        {
+            const AtomIndex& a = t->task->atoms();
+            const u32 n = a.fluent_slots();
+            const u32 stride = 1 + std::max<u32>(1, a.layout().max_arity);
+            for (u32 s = 0; s < n; ++s)
+            {
+                const u32* r = a.record(AtomKind::Fluent, s);
+                for (u32 j = 0; j < stride; ++j)
+                    rec[static_cast<usize>(s) * stride + j] = j <= a.layout().arity[r[0]] ? r[j] : 0;
+                cid[s] = a.canonical(AtomKind::Fluent, s);
+            }
+            return 0;
+        },
+        -1);
+}
+
+// the initial state, zero-padded to `words`
+int mref_task_initial(mref_task* t, uint64_t* row, uint32_t words)
+{
+    return guarded(
+        [&]() -> int
+        {
+            const State& s = t->task->initial_state();
+            std::memset(row, 0, words * sizeof(uint64_t));
+            const auto w = s.words();
+            if (w.size() > words)
+                throw std::length_error("initial state wider than the row");
+            std::memcpy(row, w.data(), w.size() * sizeof(uint64_t));
+            return 0;
+        },
+        -1);
+}
+
+int mref_task_goal(mref_task* t, const uint64_t* row, uint32_t nw)
+{
+    return guarded([&]() -> int { return t->task->is_goal(StateView{row, bits::trimmed_size(row, nw), nullptr, 0}) ? 1 : 0; }, -1);
+}
+
+uint64_t mref_canonical_hash(mref_task* t, const uint64_t* row, uint32_t nw)
+{
+    return t->task->canonical_hash(StateView{row, bits::trimmed_size(row, nw), nullptr, 0});
+}
+
+// The successors of a state in the generator's order: schema [cap], binding [cap, L] (-1 padded), rows [cap, W]
+// (zero padded; W >= the task's words). Returns the successor count (which may exceed cap; only cap are written).
+int64_t mref_successors(mref_task* t, const uint64_t* row, uint32_t nw, int witness, int canonical, int32_t* schema,
+                        int32_t* binding, uint32_t L, uint64_t* rows, uint32_t W, uint64_t cap)
+{
+    return guarded(
+        [&]() -> int64_t
+        {
+            const WorkspaceLease lease = t->task->workspace();
+            Successors& succ = lease->successors();
+            const u32 n = bits::trimmed_size(row, nw);
+            succ.prepare(StateView{row, n, nullptr, 0});
+            std::vector<u64> next;
+            int64_t count = 0;
+            succ.generate<false>(
+                [&](u32 s, const ObjectId* b, const Delta& d) -> bool
+                {
+                    if (static_cast<uint64_t>(count) < cap)
+                    {
+                        if (schema)
+                            schema[count] = static_cast<int32_t>(s);
+                        if (binding)
+                            for (u32 k = 0; k < L; ++k)
+                                binding[count * L + k] = k < succ.arity(s) ? static_cast<int32_t>(b[k].v) : -1;
+                        if (rows)
+                        {
+                            const u32 m = apply_delta(row, n, d, next);
+                            if (m > W)
+                                throw std::length_error("successor wider than the row");
+                            uint64_t* dst = rows + count * W;
+                            std::memset(dst, 0, W * sizeof(uint64_t));
+                            std::memcpy(dst, next.data(), m * sizeof(uint64_t));
+                        }
+                    }
+                    ++count;
+                    return true;
+                },
+                witness != 0, canonical != 0);
+            return count;
+        },
+        -1);
+}
+
+uint64_t mref_hash_words(const uint64_t* w, uint32_t n, uint64_t seed) { return hash::words(w, n, seed); }
+uint64_t mref_hash_state(const uint64_t* w, uint32_t n) { return hash::state(w, n, nullptr, 0); }
+uint64_t mref_hash_mix64(uint64_t x) { return hash::mix64(x); }
+
+void mref_philox(uint64_t seed, uint64_t env, uint64_t draw, uint32_t purpose, uint32_t* out)
+{
+    const rl::rng::Block4 b = rl::rng::block(seed, env, draw, purpose);
+    for (int i = 0; i < 4; ++i)
+        out[i] = b.v[i];
+}
+
+void mref_philox_raw(const uint32_t* counter, uint32_t k0, uint32_t k1, uint32_t* out)
+{
+    const rl::rng::Block4 b = rl::rng::philox4x32_10(rl::rng::Block4{{counter[0], counter[1], counter[2], counter[3]}}, k0, k1);
+    for (int i = 0; i < 4; ++i)
+        out[i] = b.v[i];
+}
+
+uint32_t mref_successor_index(uint64_t seed, uint64_t env, uint64_t draw, uint32_t count)
+{
+    return rl::rng::successor_index(seed, env, draw, count);
+}
+
+static rl::EnvConfig env_config(const mref_env_config* c)
+{
+    rl::EnvConfig e;
+    e.seed = c->seed;
+    e.max_steps = c->max_steps;
+    e.step_reward = c->step_reward;
+    e.goal_reward = c->goal_reward;
+    e.dead_end_reward = c->dead_end_reward;
+    e.dead_end = c->dead_end == 1 ? rl::DeadEnd::None : rl::DeadEnd::NoSuccessors;
+    e.dead_end_terminal = c->dead_end_terminal != 0;
+    e.autoreset = c->autoreset != 0;
+    e.canonical_order = c->canonical_order != 0;
+    e.witness_pruning = c->witness_pruning != 0;
+    return e;
+}
+
+mref_env* mref_env_create(mref_task* t, const mref_env_config* c, uint32_t threads)
+{
+    return guarded(
+        [&]() -> mref_env*
+        {
+            auto e = new mref_env;
+            e->env = std::make_unique<rl::HostEnv>(t->table, env_config(c));
+            if (threads > 1)
+                e->pool = std::make_unique<ThreadPool>(threads);
+            return e;
+        },
+        nullptr);
+}
+
+void mref_env_free(mref_env* e) { delete e; }
+
+int mref_env_reset(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws,
+                   uint8_t* at_goal, int32_t* count, uint64_t first_env)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::EnvBatch b;
+            b.states = states;
+            b.rows = rows;
+            b.words = words;
+            b.steps = steps;
+            b.draws = draws;
+            b.at_goal = at_goal;
+            b.first_env = first_env;
+            e->env->reset(b, nullptr, count);
+            return 0;
+        },
+        -1);
+}
+
+// actions: null for the random policy
+int mref_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws,
+                  uint8_t* at_goal, uint64_t first_env, const int64_t* actions, float* reward, uint8_t* terminated,
+                  uint8_t* truncated, int32_t* count, int32_t* schema, int32_t* binding, uint32_t label_width,
+                  uint8_t* goal, uint8_t* invalid, uint64_t* final_states)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::EnvBatch b;
+            b.states = states;
+            b.rows = rows;
+            b.words = words;
+            b.steps = steps;
+            b.draws = draws;
+            b.at_goal = at_goal;
+            b.first_env = first_env;
+            rl::StepOutputs o;
+            o.reward = reward;
+            o.terminated = terminated;
+            o.truncated = truncated;
+            o.count = count;
+            o.schema = schema;
+            o.binding = binding;
+            o.label_width = label_width;
+            o.goal = goal;
+            o.invalid = invalid;
+            o.final_states = final_states;
+            rl::Actions a;
+            a.v64 = actions;
+            e->env->step(b, o, a, nullptr, e->pool.get());
+            return 0;
+        },
+        -1);
+}
+
+// The CPU env pool (CpuEnvPool, `threads` workers) over `num_envs` envs: reset, then `steps` random-policy steps of
+// every env. seconds: wall time of the steps only. checksum: hash of the final pool states, rewards and counts.
+int mref_pool_run(mref_task* t, const mref_env_config* c, uint32_t num_envs, uint32_t threads, uint32_t steps,
+                  double* seconds, uint64_t* checksum)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::PoolOptions po;
+            po.threads = threads;
+            rl::CpuEnvPool pool(t->table, env_config(c), num_envs, po);
+            rl::PoolBatch b = pool.reset(nullptr, 0, nullptr);
+            pool.recycle(std::move(b));
+            u64 h = 0;
+            const auto t0 = std::chrono::steady_clock::now();
+            for (u32 k = 0; k < steps; ++k)
+            {
+                rl::PoolBatch r = pool.step(nullptr, 0, rl::Actions{}, nullptr);
+                if (k + 1 == steps)
+                {
+                    h = hash::words(r.states.data(), static_cast<u32>(r.states.size()));
+                    h = hash::combine(h, hash::words(reinterpret_cast<const u64*>(r.count.data()), static_cast<u32>(r.count.size() / 2)));
+                }
+                pool.recycle(std::move(r));
+            }
+            *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            *checksum = h;
+            return 0;
+        },
+        -1);
+}
+
+// BrFS over the task; layer_counts [cap, 3] receives {expanded, generated, new} per expanded layer.
+int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uint64_t* layer_counts, uint32_t cap)
+{
+    return guarded(
+        [&]() -> int
+        {
+            BrfsOptions b;
+            b.threads = o->threads;
+            b.max_depth = o->max_depth;
+            b.max_states = o->max_states;
+            b.witness_pruning = o->witness_pruning != 0;
+            b.canonical_order = o->canonical_order != 0;
+            b.stop_at_goal = o->stop_at_goal != 0;
+            b.fingerprint = o->fingerprint != 0;
+            b.layer_stats = true;
+            const auto t0 = std::chrono::steady_clock::now();
+            const BrfsResult x = brfs(*t->task, b);
+            r->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            r->states = x.states;
+            r->expanded = x.expanded;
+            r->generated = x.generated;
+            r->goal_states = x.num_goal_states;
+            r->fingerprint = x.fingerprint;
+            r->layers = x.layers;
+            r->status = static_cast<int32_t>(x.status);
+            r->solved = x.solved;
+            r->exhausted = x.exhausted;
+            for (u32 i = 0; i < x.layer_counts.size() && i < cap; ++i)
+                for (u32 j = 0; j < 3; ++j)
+                    layer_counts[i * 3 + j] = x.layer_counts[i][j];
+            return static_cast<int>(x.layer_counts.size());
+        },
+        -1);
+}
+
+}  // extern "C"
