@@ -109,6 +109,78 @@ int mya_hashset_size(const mya_hashset* set, uint64_t* size);
 int mya_hashset_rows(const mya_hashset* set, const uint64_t** rows);
 int mya_hashset_clear(mya_hashset* set, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------- env */
+
+/* EnvConfig (include/mymyr/rl/env.hpp:76-92), index action space. dead_end: 0 no_successors, 1 none.
+ * canonical_order must be 1 and witness_pruning 0 (the reference env defaults; the device step implements those). */
+typedef struct mya_env_config
+{
+    uint64_t seed;
+    uint32_t max_steps;
+    float step_reward;
+    float goal_reward;
+    float dead_end_reward;
+    int32_t dead_end;
+    int32_t dead_end_terminal;
+    int32_t autoreset;
+    int32_t canonical_order;
+    int32_t witness_pruning;
+    int32_t reserved;
+} mya_env_config;
+
+/* EnvBatch (include/mymyr/rl/env.hpp:96-135), device pointers: states [rows, words] (required), steps i32 [rows],
+ * draws u64 [rows] (required for the random policy), at_goal u8 [rows] (required, as for the reference device env). */
+typedef struct mya_env_batch
+{
+    uint64_t* states;
+    uint64_t rows;
+    uint32_t words;
+    uint32_t reserved;
+    int32_t* steps;
+    uint64_t* draws;
+    uint8_t* at_goal;
+    uint64_t first_env;
+} mya_env_batch;
+
+/* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
+ * final_states [rows, final_words] (final_words 0: the batch's words). */
+typedef struct mya_step_outputs
+{
+    float* reward;
+    uint8_t* terminated;
+    uint8_t* truncated;
+    int32_t* count;
+    uint64_t* final_states;
+    int32_t* schema;
+    int32_t* binding;
+    uint32_t label_width;
+    uint32_t final_words;
+    uint8_t* invalid;
+    uint8_t* goal;
+} mya_step_outputs;
+
+/* A device environment over one task (replaces cuda::DeviceEnv, include/mymyr/cuda/env.hpp:89, and
+ * rl::HostEnv, include/mymyr/rl/env.hpp:181). Uploads the task and counts the initial state's successors. */
+int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out);
+void mya_env_free(mya_env* env);
+/* Initial state's successor count and goal flag. */
+int mya_env_initial_count(const mya_env* env, uint32_t* count, uint8_t* goal);
+/* HostEnv::reset (env.cpp:207-240): rows with mask[i] != 0 (device, optional) to the initial state, steps 0,
+ * at_goal and count (device, optional) of the initial state; draws kept. Async on the stream. */
+int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, void* stream);
+/* HostEnv::step (env.cpp:530-548 / step_row_impl 351-528): actions (device, int64 [rows], optional: the random policy
+ * when null). Async on the stream; device-side failures set the sticky status that mya_env_check reports. */
+int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
+                 void* stream);
+/* Reads and clears the sticky device status (synchronizes the env's status copy); -1 with a message if a step failed. */
+int mya_env_check(mya_env* env);
+
+/* Successors of rows in canonical order, witness pruning off (Successors::generate, successors.hpp:154-248):
+ * count [rows] i32; schema [rows, cap] i32; binding [rows, cap, label_width] i32 (-1 padded); succ [rows, cap, words]
+ * u64. Device pointers (each optional but count). Entries past cap are counted, not written. Synchronous. */
+int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, int32_t cap, int32_t* count,
+                   int32_t* schema, int32_t* binding, uint64_t* succ, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------- BrFS */
 
 /* Options of brfs(Task, BrfsOptions) (include/mymyr/search/brfs.hpp:62-101) that the device search takes. */

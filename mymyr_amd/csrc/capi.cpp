@@ -8,6 +8,7 @@
 #include "device_common.hpp"
 #include "runtime.hpp"
 #include "state_set.hpp"
+#include "lifted.hpp"
 #include "task.hpp"
 
 #include <cstring>
@@ -32,6 +33,9 @@ const DeviceTask& device_task(mya_task* t)
         hip_check(hipMemcpy(t->dev.image, img.data(), img.size() * sizeof(u64), hipMemcpyHostToDevice), "upload task image");
         t->dev.device = dev;
         t->dev.words = img.size();
+        t->dev.thost = std::make_unique<TaskDev>(task_dev(t->dev.image, t->compiled->header()));
+        t->dev.tdev = dev_alloc<TaskDev>(1, "task pointer table");
+        hip_check(hipMemcpy(t->dev.tdev, t->dev.thost.get(), sizeof(TaskDev), hipMemcpyHostToDevice), "upload task table");
     }
     return t->dev;
 }
@@ -84,6 +88,7 @@ void mya_task_free(mya_task* task)
     if (!task)
         return;
     dev_free(task->dev.image);
+    dev_free(task->dev.tdev);
     delete task;
 }
 

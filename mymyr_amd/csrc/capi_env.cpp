@@ -1,0 +1,219 @@
+// C ABI of the device environment and the successor listing (include/mymyr_amd.h, "env" section). Argument checks
+// follow the reference's check_env / check_step messages (src/mymyr/rl/env.cpp:102-135, 403-421).
+
+#include "../../include/mymyr_amd.h"
+
+#include "capi_internal.hpp"
+#include "env.hpp"
+#include "runtime.hpp"
+
+#include <cstring>
+
+using namespace mya;
+
+struct mya_env
+{
+    mya_task* task = nullptr;
+    TaskDev T{};                // host copy of the pointer table
+    const TaskDev* Td = nullptr;  // device copy
+    EnvCfg cfg{};
+    u32 init_count = 0;
+    u32 init_goal = 0;
+    u32* d_status = nullptr;
+    u32* h_status = nullptr;
+};
+
+namespace
+{
+void check_batch(const mya_env* e, const mya_env_batch* b)
+{
+    if (!b)
+        throw std::invalid_argument("mymyr_amd: env: null batch");
+    if (b->rows && !b->states)
+        throw std::invalid_argument("mymyr: env: null state array");
+    if (b->rows > 0x7FFFFFFFull)
+        throw std::invalid_argument("mymyr: env: more than 2^31 - 1 environments in one batch");
+    if (b->words < e->T.W)
+        throw std::invalid_argument("mymyr: env: state rows of " + std::to_string(b->words) + " words; the task needs " +
+                                    std::to_string(e->T.W) + " (its widest instance's words)");
+}
+}  // namespace
+
+extern "C" {
+
+int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
+{
+    return guarded([&] {
+        if (!task || !config || !out)
+            throw std::invalid_argument("mymyr_amd: env_create: null argument");
+        if (!config->canonical_order || config->witness_pruning)
+            throw std::invalid_argument("mymyr_amd: env: the device step takes canonical_order on and witness_pruning off");
+        if (config->dead_end != 0 && config->dead_end != 1)
+            throw std::invalid_argument("mymyr_amd: env: dead_end must be 0 (no_successors) or 1 (none)");
+        auto e = std::make_unique<mya_env>();
+        e->task = task;
+        const DeviceTask& d = device_task(task);
+        e->T = *d.thost;
+        e->Td = d.tdev;
+        e->cfg.seed = config->seed;
+        e->cfg.max_steps = config->max_steps;
+        e->cfg.step_reward = config->step_reward;
+        e->cfg.goal_reward = config->goal_reward;
+        e->cfg.dead_end_reward = config->dead_end_reward;
+        e->cfg.dead_end_none = config->dead_end == 1 ? 1 : 0;
+        e->cfg.dead_end_terminal = config->dead_end_terminal;
+        e->cfg.autoreset = config->autoreset;
+        e->d_status = dev_alloc<u32>(1, "env status");
+        hip_check(hipHostMalloc(reinterpret_cast<void**>(&e->h_status), sizeof(u32), hipHostMallocDefault), "pinned status");
+        hip_check(hipMemset(e->d_status, 0, sizeof(u32)), "env status");
+        // the initial state's successor count and goal flag
+        const u32 W = e->T.W;
+        u64* row = dev_alloc<u64>(W, "initial row");
+        i32* cnt = dev_alloc<i32>(1, "initial count");
+        u8* gl = dev_alloc<u8>(1, "initial goal");
+        hip_check(hipMemcpy(row, task->compiled->initial.data(), W * sizeof(u64), hipMemcpyHostToDevice), "initial row");
+        launch_env_count(e->Td, e->T, row, 1, W, cnt, gl, nullptr);
+        i32 hc = 0;
+        u8 hg = 0;
+        hip_check(hipMemcpy(&hc, cnt, sizeof(i32), hipMemcpyDeviceToHost), "initial count");
+        hip_check(hipMemcpy(&hg, gl, sizeof(u8), hipMemcpyDeviceToHost), "initial goal");
+        dev_free(row);
+        dev_free(cnt);
+        dev_free(gl);
+        e->init_count = static_cast<u32>(hc);
+        e->init_goal = hg;
+        *out = e.release();
+    });
+}
+
+void mya_env_free(mya_env* env)
+{
+    if (!env)
+        return;
+    dev_free(env->d_status);
+    if (env->h_status)
+        (void)hipHostFree(env->h_status);
+    delete env;
+}
+
+int mya_env_initial_count(const mya_env* env, uint32_t* count, uint8_t* goal)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        if (count)
+            *count = env->init_count;
+        if (goal)
+            *goal = static_cast<uint8_t>(env->init_goal);
+    });
+}
+
+int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        check_batch(env, batch);
+        launch_env_reset(env->Td, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, env->init_count,
+                         env->init_goal, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions, void* stream)
+{
+    return guarded([&] {
+        if (!env || !out)
+            throw std::invalid_argument("mymyr_amd: env: null argument");
+        check_batch(env, batch);
+        if (batch->rows && !batch->at_goal)
+            throw std::invalid_argument("mymyr_amd: env: the device step needs the at_goal array");
+        if (!actions && batch->rows && !batch->draws)
+            throw std::invalid_argument("mymyr: env: the random policy needs the draw counters");
+        if (env->cfg.max_steps && batch->rows && !batch->steps)
+            throw std::invalid_argument("mymyr: env: truncation (max_steps) needs the step counters");
+        if (out->binding && out->label_width < env->T.label_width)
+            throw std::invalid_argument("mymyr: env: label width " + std::to_string(out->label_width) + " is below the largest schema arity " +
+                                        std::to_string(env->T.label_width));
+        const u32 fw = out->final_words ? out->final_words : batch->words;
+        if (out->final_states && fw < env->T.W)
+            throw std::invalid_argument("mymyr: env: final state rows of " + std::to_string(fw) + " words; the task has " +
+                                        std::to_string(env->T.W));
+        EnvArgs a{};
+        a.T = env->Td;
+        a.W = env->T.W;
+        a.view_words = env->T.view_words;
+        a.cfg = env->cfg;
+        a.states = batch->states;
+        a.rows = batch->rows;
+        a.words = batch->words;
+        a.steps = batch->steps;
+        a.draws = batch->draws;
+        a.at_goal = batch->at_goal;
+        a.first_env = batch->first_env;
+        a.actions = actions;
+        a.reward = out->reward;
+        a.terminated = out->terminated;
+        a.truncated = out->truncated;
+        a.count = out->count;
+        a.final_states = out->final_states;
+        a.final_words = fw;
+        a.schema = out->schema;
+        a.binding = out->binding;
+        a.label_width = out->label_width;
+        a.invalid = out->invalid;
+        a.goal = out->goal;
+        a.init_count = env->init_count;
+        a.init_goal = env->init_goal;
+        a.status = env->d_status;
+        launch_env_step(a, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_check(mya_env* env)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        hip_check(hipMemcpy(env->h_status, env->d_status, sizeof(u32), hipMemcpyDeviceToHost), "env status");
+        const u32 s = *env->h_status;
+        if (s)
+        {
+            hip_check(hipMemset(env->d_status, 0, sizeof(u32)), "env status");
+            std::string m = "mymyr_amd: env: device status";
+            if (s & kStatusCapacity)
+                m += " capacity";
+            if (s & kStatusNoSlot)
+                m += " add-effect-without-slot";
+            if (s & kStatusPickFailed)
+                m += " pick-failed";
+            throw std::runtime_error(m);
+        }
+    });
+}
+
+int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, int32_t cap, int32_t* count, int32_t* schema,
+                   int32_t* binding, uint64_t* succ, void* stream)
+{
+    return guarded([&] {
+        if (!task || (rows && (!states || !count)))
+            throw std::invalid_argument("mymyr_amd: successors: null argument");
+        if (cap < 0)
+            throw std::invalid_argument("mymyr_amd: successors: negative cap");
+        const DeviceTask& d = device_task(task);
+        const TaskDev& T = *d.thost;
+        if (words < T.W)
+            throw std::invalid_argument("mymyr_amd: successors: rows of " + std::to_string(words) + " words; the task needs " +
+                                        std::to_string(T.W));
+        u32* st = dev_alloc<u32>(1, "status");
+        hip_check(hipMemsetAsync(st, 0, sizeof(u32), static_cast<hipStream_t>(stream)), "status");
+        launch_successors(d.tdev, T, states, rows, words, static_cast<u32>(cap), count, schema, binding, succ, st, static_cast<hipStream_t>(stream));
+        u32 hs = 0;
+        hip_check(hipMemcpyAsync(&hs, st, sizeof(u32), hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)), "status");
+        hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "successors");
+        dev_free(st);
+        if (hs)
+            throw std::runtime_error("mymyr_amd: successors: device status " + std::to_string(hs));
+    });
+}
+
+}  // extern "C"

@@ -14,12 +14,16 @@ namespace mya
 {
 void set_error(const std::string& m);
 
-/// A task's device image, uploaded on first device use.
+struct TaskDev;
+
+/// A task's device image, uploaded on first device use, plus the pointer table into it (host and device copies).
 struct DeviceTask
 {
     u64* image = nullptr;
     u64 words = 0;
     int device = -1;
+    TaskDev* tdev = nullptr;         // device copy of the pointer table
+    std::unique_ptr<TaskDev> thost;  // host copy
 };
 
 template<class F>

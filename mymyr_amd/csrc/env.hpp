@@ -1,0 +1,69 @@
+#pragma once
+// The batched environment step on the device, bit-exact with HostEnv::step_row_impl (src/mymyr/rl/env.cpp:351-528):
+// choose (given index or Philox draw over the canonical successor order), move, goal, dead end, reward, termination,
+// truncation, successor count of the reached state, SAME_STEP autoreset. One wavefront per environment row.
+
+#include "lifted.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace mya
+{
+struct EnvCfg
+{
+    u64 seed;
+    u32 max_steps;
+    float step_reward, goal_reward, dead_end_reward;
+    i32 dead_end_none;      // DeadEnd::None
+    i32 dead_end_terminal;
+    i32 autoreset;
+};
+
+struct EnvArgs
+{
+    const TaskDev* T;  // device copy (kernels read it through scalar loads)
+    u32 W;             // the task's words
+    u32 view_words;
+    EnvCfg cfg;
+    u64* states;
+    u64 rows;
+    u32 words;  // row words of the batch (>= T.W)
+    i32* steps;
+    u64* draws;
+    u8* at_goal;
+    u64 first_env;
+    const i64* actions;  // null: the random policy
+    float* reward;
+    u8* terminated;
+    u8* truncated;
+    i32* count;
+    u64* final_states;
+    u32 final_words;
+    i32* schema;
+    i32* binding;
+    u32 label_width;
+    u8* invalid;
+    u8* goal;
+    u32 init_count;
+    u32 init_goal;
+    u32* status;
+};
+
+void launch_env_step(const EnvArgs& a, hipStream_t stream);
+
+/// count[i] (successors) and goal[i] of rows (either may be null). Td: the device copy, Th: the host copy.
+void launch_env_count(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
+                      hipStream_t stream);
+
+/// Resets the rows with mask[i] != 0 (all if mask is null) to the initial state: steps 0, at_goal = init_goal,
+/// count = init_count; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).
+void launch_env_reset(const TaskDev* Td, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal,
+                      i32* count, u32 init_count, u32 init_goal, hipStream_t stream);
+
+/// Per-row successor listing in canonical order (schema [rows, cap], binding [rows, cap, L], successor rows
+/// [rows, cap, words]) and counts [rows]; entries past cap are counted but not written.
+void launch_successors(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, u32 cap, i32* count,
+                       i32* schema, i32* binding, u64* succ, u32* status, hipStream_t stream);
+
+size_t env_lds_bytes(const DevTaskHeader& h);
+}  // namespace mya

@@ -1,0 +1,136 @@
+"""Batched environments on the device: the drop-in for the reference's ``rl.CpuEnvPool`` (python/src/rl_bindings.cpp:
+2465-2600, include/mymyr/rl/pool.hpp:114-172) and its device env (include/mymyr/cuda/env.hpp), with the same keyword
+arguments and defaults (seed 0, step_reward 0, goal_reward 1, dead_end "no_successors", autoreset True,
+canonical_order True, witness_pruning False, first_env 0).
+
+Every array lives on the device as a torch tensor (uint64 state words are carried as int64 tensors with the same
+bits); step() runs on torch's current stream and returns views of the pool's own buffers (a PoolBatch-like dict), which
+the next call overwrites, as the reference's recycled batches.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+from .task import Task
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+class DeviceEnvPool:
+    """num_envs environments over one task, stepped together on the device (random policy unless actions are given)."""
+
+    def __init__(self, task: Task, num_envs: int, *, seed: int = 0, max_steps: int | None = None, step_reward: float = 0.0,
+                 goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
+                 dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
+                 witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda"):
+        if num_envs < 1 or num_envs > 0x7FFFFFFF:
+            raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
+        if dead_end not in ("no_successors", "none"):
+            raise ValueError("mymyr: dead_end must be 'no_successors' or 'none'")
+        self.task = task
+        self.num_envs = num_envs
+        self.first_env = first_env
+        self.words = task.words if words is None else words
+        if self.words < task.words:
+            raise ValueError(f"mymyr: env: state rows of {self.words} words; the task needs {task.words}")
+        self.label_width = max(1, task.label_width)
+        self.device = torch.device(device)
+        cfg = _lib.EnvConfig(seed, max_steps or 0, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
+                             int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning), 0)
+        h = ctypes.c_void_p()
+        check(lib.mya_env_create(task.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        N, W, L, dev = num_envs, self.words, self.label_width, self.device
+        self.states = torch.zeros((N, W), dtype=torch.int64, device=dev)
+        self.steps = torch.zeros(N, dtype=torch.int32, device=dev)
+        self.draws = torch.zeros(N, dtype=torch.int64, device=dev)
+        self.at_goal = torch.zeros(N, dtype=torch.uint8, device=dev)
+        self.count = torch.zeros(N, dtype=torch.int32, device=dev)
+        self.reward = torch.zeros(N, dtype=torch.float32, device=dev)
+        self.terminated = torch.zeros(N, dtype=torch.uint8, device=dev)
+        self.truncated = torch.zeros(N, dtype=torch.uint8, device=dev)
+        self.goal = torch.zeros(N, dtype=torch.uint8, device=dev)
+        self.invalid = torch.zeros(N, dtype=torch.uint8, device=dev)
+        self.schema = torch.zeros(N, dtype=torch.int32, device=dev)
+        self.binding = torch.zeros((N, L), dtype=torch.int32, device=dev)
+        self.final_states: torch.Tensor | None = None
+        self._batch = _lib.EnvBatch(self.states.data_ptr(), N, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
+                                    self.at_goal.data_ptr(), first_env)
+
+    def initial_count(self) -> tuple[int, bool]:
+        c = ctypes.c_uint32()
+        g = ctypes.c_uint8()
+        check(lib.mya_env_initial_count(self._h, ctypes.byref(c), ctypes.byref(g)))
+        return c.value, bool(g.value)
+
+    def reset(self, mask: torch.Tensor | None = None) -> dict:
+        """Resets every env (or those with mask != 0) to the initial state; draws are kept."""
+        if mask is not None:
+            mask = mask.to(device=self.device, dtype=torch.uint8).contiguous()
+        check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), _stream()))
+        return {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
+
+    def step(self, actions: torch.Tensor | None = None, final_states: bool = False, labels: bool = True) -> dict:
+        """One step of every env: actions [num_envs] int64 indices into the canonical successor order (None: the random
+        policy). Returns the step's arrays (views, overwritten by the next step)."""
+        if actions is not None:
+            actions = actions.to(device=self.device, dtype=torch.int64).contiguous()
+            if actions.shape != (self.num_envs,):
+                raise ValueError(f"mymyr: env: actions must have shape ({self.num_envs},)")
+        if final_states and self.final_states is None:
+            self.final_states = torch.zeros((self.num_envs, self.words), dtype=torch.int64, device=self.device)
+        fs = self.final_states if final_states else None
+        out = _lib.StepOutputs(self.reward.data_ptr(), self.terminated.data_ptr(), self.truncated.data_ptr(), self.count.data_ptr(),
+                               _p(fs), self.schema.data_ptr() if labels else None, self.binding.data_ptr() if labels else None,
+                               self.label_width, self.words, self.invalid.data_ptr(), self.goal.data_ptr())
+        check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(out), _p(actions), _stream()))
+        r = {"states": self.states, "reward": self.reward, "terminated": self.terminated, "truncated": self.truncated,
+             "count": self.count, "steps": self.steps, "at_goal": self.at_goal, "goal": self.goal, "invalid": self.invalid}
+        if labels:
+            r["schema"] = self.schema
+            r["binding"] = self.binding
+        if fs is not None:
+            r["final_states"] = fs
+        return r
+
+    def check(self) -> None:
+        """Raises if a step set the device's sticky error status."""
+        check(lib.mya_env_check(self._h))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        try:
+            if h is not None and h.value:
+                lib.mya_env_free(h)
+                self._h = ctypes.c_void_p()
+        except Exception:
+            pass
+
+
+def successors(task: Task, states: torch.Tensor, cap: int = 4096) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Canonical successor listing of each row (witness pruning off): (count [n], schema [n, cap], binding [n, cap, L],
+    rows [n, cap, words]); entries past count are unspecified."""
+    s = states.view(torch.int64) if states.dtype == torch.uint64 else states
+    if not s.is_cuda or s.dim() != 2:
+        raise ValueError("mymyr_amd: successors: states must be a 2-d device tensor")
+    s = s.contiguous()
+    n, w = s.shape
+    L = max(1, task.label_width)
+    count = torch.zeros(n, dtype=torch.int32, device=s.device)
+    schema = torch.full((n, cap), -1, dtype=torch.int32, device=s.device)
+    binding = torch.full((n, cap, L), -1, dtype=torch.int32, device=s.device)
+    rows = torch.zeros((n, cap, w), dtype=torch.int64, device=s.device)
+    check(lib.mya_successors(task.handle, s.data_ptr(), n, w, cap, count.data_ptr(), schema.data_ptr(), binding.data_ptr(),
+                             rows.data_ptr(), _stream()))
+    return count, schema, binding, rows
