@@ -109,6 +109,11 @@ int mya_hashset_size(const mya_hashset* set, uint64_t* size);
 int mya_hashset_rows(const mya_hashset* set, const uint64_t** rows);
 int mya_hashset_clear(mya_hashset* set, void* stream);
 
+/* No reference counterpart: the synthetic input of the dedup workload. Rows [start, start + count) of the seeded
+ * stream in which row i > 0 is, with probability dup, an exact copy of an earlier row, else fresh words
+ * mix64(seed + (16 i + k + 1) * 0x9E3779B97F4A7C15). out [count, words]: device. Async on the stream. */
+int mya_dedup_rows(uint64_t start, uint64_t count, uint32_t words, uint64_t seed, double dup, uint64_t* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------- env */
 
 /* EnvConfig (include/mymyr/rl/env.hpp:76-92), index action space. dead_end: 0 no_successors, 1 none.
@@ -143,7 +148,10 @@ typedef struct mya_env_batch
 } mya_env_batch;
 
 /* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
- * final_states [rows, final_words] (final_words 0: the batch's words). */
+ * final_states [rows, final_words] (final_words 0: the batch's words).
+ * atoms [rows, max_atoms] int32 and masks [rows, num_schemas] uint8 encode the observed state after the step (and
+ * the autoreset): its true-atom slots ascending, -1 padded (State::slots, include/mymyr/state/state.hpp:96-101), and
+ * the schemas with an applicable binding (rl::schema_masks, include/mymyr/rl/masks.hpp:9-11). */
 typedef struct mya_step_outputs
 {
     float* reward;
@@ -157,6 +165,10 @@ typedef struct mya_step_outputs
     uint32_t final_words;
     uint8_t* invalid;
     uint8_t* goal;
+    int32_t* atoms;
+    uint8_t* masks;
+    uint32_t max_atoms;
+    uint32_t reserved;
 } mya_step_outputs;
 
 /* A device environment over one task (replaces cuda::DeviceEnv, include/mymyr/cuda/env.hpp:89, and
@@ -174,6 +186,15 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
                  void* stream);
 /* Reads and clears the sticky device status (synchronizes the env's status copy); -1 with a message if a step failed. */
 int mya_env_check(mya_env* env);
+
+/* The true-atom slots of rows, ascending, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101);
+ * states [rows, words], out [rows, max_atoms] int32: device. Async on the stream; more atoms than max_atoms set the
+ * env's sticky status (mya_env_check). */
+int mya_encode_atoms(mya_env* env, const uint64_t* states, uint64_t rows, uint32_t words, int32_t* out, uint32_t max_atoms,
+                     void* stream);
+/* Per row and schema, whether some binding is applicable (rl::schema_masks, include/mymyr/rl/masks.hpp:9-11);
+ * masks [rows, num_schemas] uint8, device. Async on the stream. */
+int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32_t words, uint8_t* masks, void* stream);
 
 /* Successors of rows in canonical order, witness pruning off (Successors::generate, successors.hpp:154-248):
  * count [rows] i32; schema [rows, cap] i32; binding [rows, cap, label_width] i32 (-1 padded); succ [rows, cap, words]

@@ -77,6 +77,10 @@ class StepOutputs(Structure):
         ("final_words", c_uint32),
         ("invalid", c_void_p),
         ("goal", c_void_p),
+        ("atoms", c_void_p),
+        ("masks", c_void_p),
+        ("max_atoms", c_uint32),
+        ("reserved", c_uint32),
     ]
 
 
@@ -134,6 +138,7 @@ def _load() -> ctypes.CDLL:
         "mya_hashset_size": (c_int, [c_void_p, POINTER(c_uint64)]),
         "mya_hashset_rows": (c_int, [c_void_p, POINTER(c_void_p)]),
         "mya_hashset_clear": (c_int, [c_void_p, c_void_p]),
+        "mya_dedup_rows": (c_int, [c_uint64, c_uint64, c_uint32, c_uint64, c_double, c_void_p, c_void_p]),
     }
     optional = {
         "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),
@@ -143,7 +148,7 @@ def _load() -> ctypes.CDLL:
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_initial_count": (c_int, [c_void_p, POINTER(c_uint32), POINTER(c_uint8)]),
         "mya_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
-        "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p, c_void_p]),
+        "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p]),
         "mya_schema_masks": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),
         "mya_successors": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     }

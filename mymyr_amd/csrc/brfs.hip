@@ -23,6 +23,8 @@ struct GroundDev
     const u32* meta;
     const u32* off;
     const u32* slots;
+    const u32* dom_off;  // witness pruning: dominators of each action (null: none)
+    const u32* dom;
     u32 num;
 };
 
@@ -53,6 +55,22 @@ __device__ __forceinline__ bool applicable(const u64 (*st)[kGB], const u32* __re
     return true;
 }
 
+/// Whether action a is a successor: applicable, and (witness pruning) no dominator is.
+template<int W>
+__device__ __forceinline__ bool emitted(const u64 (*st)[kGB], const GroundDev& g, u32 a, u32 m, u32 o)
+{
+    if (!applicable<W>(st, g.slots, m, o))
+        return false;
+    if (g.dom_off)
+        for (u32 k = g.dom_off[a], e = g.dom_off[a + 1]; k < e; ++k)
+        {
+            const u32 d = g.dom[k];
+            if (applicable<W>(st, g.slots, g.meta[d], g.off[d]))
+                return false;
+        }
+    return true;
+}
+
 template<int W>
 __global__ __launch_bounds__(kGB) void k_ground_count(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g, GoalDev goal,
                                                      u32* __restrict__ counts, u8* __restrict__ goal_flags)
@@ -71,7 +89,7 @@ __global__ __launch_bounds__(kGB) void k_ground_count(const u64* __restrict__ ar
         gl = gl && !lds_bit<W>(st, goal.neg[i]);
     u32 cnt = 0;
     for (u32 a = 0; a < g.num; ++a)
-        cnt += applicable<W>(st, g.slots, g.meta[a], g.off[a]) ? 1u : 0u;
+        cnt += emitted<W>(st, g, a, g.meta[a], g.off[a]) ? 1u : 0u;
     if (valid)
     {
         counts[t] = cnt;
@@ -122,7 +140,7 @@ __global__ __launch_bounds__(kGB) void k_ground_generate(const u64* __restrict__
     for (u32 a = 0; a < g.num; ++a)
     {
         const u32 m = g.meta[a], o = g.off[a];
-        if (!valid || !applicable<W>(st, g.slots, m, o))
+        if (!valid || !emitted<W>(st, g, a, m, o))
             continue;
         const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF, nadd = (m >> 16) & 0xFF, ndel = m >> 24;
         u64 v[W];
@@ -270,6 +288,8 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     u32* d_meta = dev_alloc<u32>(ga.meta.size(), "ground meta");
     u32* d_off = dev_alloc<u32>(ga.off.size(), "ground offsets");
     u32* d_slots = dev_alloc<u32>(ga.slots.size(), "ground slots");
+    u32* d_dom_off = ga.dom_off.empty() ? nullptr : dev_alloc<u32>(ga.dom_off.size(), "ground dominators");
+    u32* d_dom = ga.dom_off.empty() ? nullptr : dev_alloc<u32>(ga.dom.size(), "ground dominators");
     u32* d_gpos = dev_alloc<u32>(task.goal_pos.size(), "goal");
     u32* d_gneg = dev_alloc<u32>(task.goal_neg.size(), "goal");
     u64* d_slot_cid = task.mode == AtomMode::Dense ? nullptr : dev_alloc<u64>(task.slot_cid.size(), "slot cids");
@@ -281,7 +301,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             for (void* x : p)
                 dev_free(x);
         }
-    } fa{{d_meta, d_off, d_slots, d_gpos, d_gneg, d_slot_cid}};
+    } fa{{d_meta, d_off, d_slots, d_gpos, d_gneg, d_slot_cid, d_dom_off, d_dom}};
     auto up = [&](void* d, const void* h, size_t b) {
         if (b)
             hip_check(hipMemcpyAsync(d, h, b, hipMemcpyHostToDevice, stream), "upload");
@@ -289,11 +309,16 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     up(d_meta, ga.meta.data(), ga.meta.size() * 4);
     up(d_off, ga.off.data(), ga.off.size() * 4);
     up(d_slots, ga.slots.data(), ga.slots.size() * 4);
+    if (d_dom_off)
+    {
+        up(d_dom_off, ga.dom_off.data(), ga.dom_off.size() * 4);
+        up(d_dom, ga.dom.data(), ga.dom.size() * 4);
+    }
     up(d_gpos, task.goal_pos.data(), task.goal_pos.size() * 4);
     up(d_gneg, task.goal_neg.data(), task.goal_neg.size() * 4);
     if (d_slot_cid)
         up(d_slot_cid, task.slot_cid.data(), task.slot_cid.size() * 8);
-    const GroundDev g{d_meta, d_off, d_slots, ga.size()};
+    const GroundDev g{d_meta, d_off, d_slots, d_dom_off, d_dom, ga.size()};
     const GoalDev goal{d_gpos, d_gneg, static_cast<u32>(task.goal_pos.size()), static_cast<u32>(task.goal_neg.size()),
                        task.goal_unsat ? 1u : 0u};
 

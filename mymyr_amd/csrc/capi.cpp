@@ -251,6 +251,19 @@ int mya_hashset_clear(mya_hashset* set, void* stream)
     });
 }
 
+int mya_dedup_rows(uint64_t start, uint64_t count, uint32_t words, uint64_t seed, double dup, uint64_t* out, void* stream)
+{
+    return guarded([&] {
+        if (count && !out)
+            throw std::invalid_argument("mymyr_amd: dedup_rows: null output");
+        if (!(dup >= 0.0 && dup < 1.0))
+            throw std::invalid_argument("mymyr_amd: dedup_rows: dup must be in [0, 1)");
+        if (start + count > (u64{1} << 32))
+            throw std::invalid_argument("mymyr_amd: dedup_rows: rows beyond 2^32");
+        launch_dedup_rows(start, count, words, seed, dup, out, static_cast<hipStream_t>(stream));
+    });
+}
+
 int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts, uint32_t cap)
 {
     int layers = -1;

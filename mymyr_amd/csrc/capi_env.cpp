@@ -19,6 +19,7 @@ struct mya_env
     EnvCfg cfg{};
     u32 init_count = 0;
     u32 init_goal = 0;
+    u8* init_masks = nullptr;  // device [num_schemas]
     u32* d_status = nullptr;
     u32* h_status = nullptr;
 };
@@ -72,7 +73,8 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
         i32* cnt = dev_alloc<i32>(1, "initial count");
         u8* gl = dev_alloc<u8>(1, "initial goal");
         hip_check(hipMemcpy(row, task->compiled->initial.data(), W * sizeof(u64), hipMemcpyHostToDevice), "initial row");
-        launch_env_count(e->Td, e->T, row, 1, W, cnt, gl, nullptr);
+        e->init_masks = dev_alloc<u8>(std::max<u32>(1, e->T.num_schemas), "initial masks");
+        launch_env_count(e->Td, e->T, row, 1, W, cnt, gl, e->init_masks, nullptr);
         i32 hc = 0;
         u8 hg = 0;
         hip_check(hipMemcpy(&hc, cnt, sizeof(i32), hipMemcpyDeviceToHost), "initial count");
@@ -91,6 +93,7 @@ void mya_env_free(mya_env* env)
     if (!env)
         return;
     dev_free(env->d_status);
+    dev_free(env->init_masks);
     if (env->h_status)
         (void)hipHostFree(env->h_status);
     delete env;
@@ -162,6 +165,12 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.label_width = out->label_width;
         a.invalid = out->invalid;
         a.goal = out->goal;
+        a.atoms = out->atoms;
+        a.max_atoms = out->max_atoms;
+        a.masks = out->masks;
+        a.init_masks = env->init_masks;
+        if (out->atoms && out->max_atoms == 0)
+            throw std::invalid_argument("mymyr_amd: env: atoms output needs max_atoms > 0");
         a.init_count = env->init_count;
         a.init_goal = env->init_goal;
         a.status = env->d_status;
@@ -188,6 +197,28 @@ int mya_env_check(mya_env* env)
                 m += " pick-failed";
             throw std::runtime_error(m);
         }
+    });
+}
+
+int mya_encode_atoms(mya_env* env, const uint64_t* states, uint64_t rows, uint32_t words, int32_t* out, uint32_t max_atoms, void* stream)
+{
+    return guarded([&] {
+        if (!env || (rows && (!states || !out)))
+            throw std::invalid_argument("mymyr_amd: encode_atoms: null argument");
+        if (words < env->T.W)
+            throw std::invalid_argument("mymyr_amd: encode_atoms: rows narrower than the task");
+        launch_encode_atoms(states, rows, words, env->T.W, out, max_atoms, env->d_status, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32_t words, uint8_t* masks, void* stream)
+{
+    return guarded([&] {
+        if (!env || (rows && (!states || !masks)))
+            throw std::invalid_argument("mymyr_amd: schema_masks: null argument");
+        if (words < env->T.W)
+            throw std::invalid_argument("mymyr_amd: schema_masks: rows narrower than the task");
+        launch_env_count(env->Td, env->T, states, rows, words, nullptr, nullptr, masks, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -445,6 +445,33 @@ __device__ void build_view(const TaskDev& T, const Lds& L, const u64* row, u32 l
     __syncthreads();
 }
 
+/// The ascending set-bit slots of `row` (W words) into out[0, max_atoms), -1 padded (all lanes).
+__device__ void encode_row(const u64* row, u32 W, i32* out, u32 max_atoms, u32 lane, u32* status)
+{
+    u32 base = 0;
+    for (u32 w0 = 0; w0 < W; w0 += kWave)
+    {
+        const u32 w = w0 + lane;
+        u64 x = w < W ? row[w] : 0;
+        const u32 c = static_cast<u32>(__popcll(x));
+        const u32 incl = wave_inclusive(c);
+        u32 k = base + incl - c;
+        while (x)
+        {
+            const u32 b = static_cast<u32>(__builtin_ctzll(x));
+            x &= x - 1;
+            if (k < max_atoms)
+                out[k] = static_cast<i32>(w * 64 + b);
+            ++k;
+        }
+        base += __shfl(incl, kWave - 1, kWave);
+    }
+    for (u32 k = base + lane; k < max_atoms; k += kWave)
+        out[k] = -1;
+    if (base > max_atoms && lane == 0)
+        atomicOr(status, kStatusCapacity);
+}
+
 __device__ bool goal_test(const TaskDev& T, const u64* row, u32 lane)
 {
     bool ok = true;
@@ -595,7 +622,8 @@ __global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
                 f[k] = k < T.W ? row[k] : 0;
         }
         // 5. the autoreset, or the bookkeeping of the move (the row already holds s')
-        if (A.cfg.autoreset && (term || trunc))
+        const bool reset = A.cfg.autoreset && (term || trunc);
+        if (reset)
         {
             for (u32 k = lane; k < A.words; k += kWave)
                 row[k] = k < T.W ? T.initial[k] : 0;
@@ -616,12 +644,45 @@ __global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
             if (A.count)
                 A.count[i] = static_cast<i32>(c2);
         }
+        // 6. the observation's encoding: true-atom slots and applicable-schema masks (LDS holds the per-schema counts
+        // of the state the row holds unless the row was reset)
+        if (A.atoms || A.masks)
+        {
+            __threadfence_block();
+            __syncthreads();
+            if (A.atoms)
+                encode_row(row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
+            if (A.masks)
+                for (u32 s = lane; s < T.num_schemas; s += kWave)
+                {
+                    u8 m;
+                    if (reset)
+                        m = A.init_masks[s];
+                    else
+                        m = (s < kCountCache ? L.counts[s] : 1u) > 0 ? 1 : 0;
+                    A.masks[i * T.num_schemas + s] = m;
+                }
+            if (A.masks && !reset && T.num_schemas > kCountCache)
+                for (u32 s = kCountCache; s < T.num_schemas; ++s)
+                {
+                    const u32 c = schema_count(T, L, row, s, lane);
+                    if (lane == 0)
+                        A.masks[i * T.num_schemas + s] = c > 0 ? 1 : 0;
+                }
+        }
         __syncthreads();
     }
 }
 
+__global__ __launch_bounds__(kEB) void k_encode(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status)
+{
+    const u32 lane = threadIdx.x;
+    for (u64 i = blockIdx.x; i < rows; i += gridDim.x)
+        encode_row(states + i * words, W, out + i * max_atoms, max_atoms, lane, status);
+}
+
 __global__ __launch_bounds__(kEB) void k_env_count(const TaskDev* __restrict__ Tp, const u64* states, u64 rows, u32 words, i32* count,
-                                                   u8* goal)
+                                                   u8* goal, u8* masks)
 {
     extern __shared__ u64 smem[];
     const TaskDev& T = *Tp;
@@ -640,6 +701,13 @@ __global__ __launch_bounds__(kEB) void k_env_count(const TaskDev* __restrict__ T
             if (goal)
                 goal[i] = g ? 1 : 0;
         }
+        if (masks)
+            for (u32 s = 0; s < T.num_schemas; ++s)
+            {
+                const u32 cs = s < kCountCache ? L.counts[s] : schema_count(T, L, row, s, lane);
+                if (lane == 0)
+                    masks[i * T.num_schemas + s] = cs > 0 ? 1 : 0;
+            }
         __syncthreads();
     }
 }
@@ -751,15 +819,23 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
     launch_check("env step");
 }
 
-void launch_env_count(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
+void launch_env_count(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks,
                       hipStream_t stream)
 {
     if (rows == 0)
         return;
     const size_t lds = static_cast<size_t>(Th.view_words + kLdsExtraWords) * sizeof(u64);
     set_lds(reinterpret_cast<const void*>(&k_env_count), lds);
-    hipLaunchKernelGGL(k_env_count, dim3(grid_for(rows)), dim3(kEB), lds, stream, Td, states, rows, words, count, goal);
+    hipLaunchKernelGGL(k_env_count, dim3(grid_for(rows)), dim3(kEB), lds, stream, Td, states, rows, words, count, goal, masks);
     launch_check("env count");
+}
+
+void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream)
+{
+    if (rows == 0)
+        return;
+    hipLaunchKernelGGL(k_encode, dim3(grid_for(rows)), dim3(kEB), 0, stream, states, rows, words, W, out, max_atoms, status);
+    launch_check("encode atoms");
 }
 
 void launch_env_reset(const TaskDev* Td, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,

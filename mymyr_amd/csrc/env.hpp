@@ -44,6 +44,10 @@ struct EnvArgs
     u32 label_width;
     u8* invalid;
     u8* goal;
+    i32* atoms;       // [rows, max_atoms]: ascending true-atom slots of the observed state, -1 padded (optional)
+    u32 max_atoms;
+    u8* masks;        // [rows, num_schemas]: schemas with an applicable binding in the observed state (optional)
+    const u8* init_masks;  // [num_schemas]: the initial state's masks (device)
     u32 init_count;
     u32 init_goal;
     u32* status;
@@ -51,9 +55,13 @@ struct EnvArgs
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream);
 
-/// count[i] (successors) and goal[i] of rows (either may be null). Td: the device copy, Th: the host copy.
+/// count[i] (successors), goal[i] and masks [rows, num_schemas] of rows (each may be null). Td: the device copy, Th:
+/// the host copy.
 void launch_env_count(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
-                      hipStream_t stream);
+                      u8* masks, hipStream_t stream);
+
+/// Ascending true-atom slots of each row, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101).
+void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream);
 
 /// Resets the rows with mask[i] != 0 (all if mask is null) to the initial state: steps 0, at_goal = init_goal,
 /// count = init_count; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).

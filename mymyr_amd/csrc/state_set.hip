@@ -134,7 +134,34 @@ __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u6
     const u32 code = static_cast<u32>(s.table[cs & ~kDupSettled]);
     ids[j] = (code & kPending) ? -1 : static_cast<i64>(code) - 1;
 }
+// The dedup stream: row i is, with probability `dup` (i > 0), an exact copy of row src(i) < i, else fresh words
+// mix64(seed + (16 i + k + 1) * gamma). Counter-based, so any range of rows is generated independently.
+constexpr u64 kGamma = 0x9E3779B97F4A7C15ULL;
+constexpr u64 kDupKey = 0xD1B54A32D192ED03ULL;
+constexpr u64 kSrcKey = 0x8CB92BA72F3D8DD7ULL;
+
+__global__ __launch_bounds__(kBlock) void k_dedup_rows(u64 start, u64 count, u32 words, u64 seed, u64 thr, u64* __restrict__ out)
+{
+    const u64 j = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    if (j >= count)
+        return;
+    u64 cur = start + j;
+    while (cur > 0 && (mix64((seed ^ kDupKey) ^ (cur * kGamma)) >> 32) < thr)
+        cur = ((mix64((seed ^ kSrcKey) ^ (cur * kGamma)) & 0xFFFFFFFFull) * cur) >> 32;
+    u64* row = out + j * words;
+    for (u32 k = 0; k < words; ++k)
+        row[k] = mix64(seed + (cur * 16 + k + 1) * kGamma);
+}
 }  // namespace
+
+void launch_dedup_rows(u64 start, u64 count, u32 words, u64 seed, double dup, u64* out, hipStream_t stream)
+{
+    if (count == 0)
+        return;
+    const u64 thr = static_cast<u64>(dup * 4294967296.0);
+    hipLaunchKernelGGL(k_dedup_rows, dim3(blocks_for(count, kBlock)), dim3(kBlock), 0, stream, start, count, words, seed, thr, out);
+    launch_check("dedup rows");
+}
 
 void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t stream)
 {

@@ -65,4 +65,7 @@ void state_set_compact(StateSet& s, const u64* rows, const u64* hashes, u64 n, u
 
 /// hash_state of every row (thread per row).
 void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t stream);
+
+/// Rows [start, start + count) of the seeded dedup stream (the dedup workload's synthetic input).
+void launch_dedup_rows(u64 start, u64 count, u32 words, u64 seed, double dup, u64* out, hipStream_t stream);
 }  // namespace mya

@@ -1361,9 +1361,11 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
         return kNone;
     }();
     (void)eq;  // the successor engine reads "=" as a static relation over its initial atoms, as the reference does
+    std::map<std::vector<u32>, std::vector<u32>> groups;  // (schema, relevant objects) -> members, witness ascending
     for (u32 si = 0; si < T.schemas.size(); ++si)
     {
         const SchemaText& s = T.schemas[si];
+        i32 witness = -1;
         if (witness_pruning)
         {
             std::vector<u8> rel(s.arity, 0);
@@ -1373,11 +1375,16 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
                         rel[x] = 1;
             for (u32 v = 0; v < s.arity; ++v)
                 if (!rel[v])
-                    throw Error("schema " + s.name + " has a parameter no effect mentions; device witness pruning is not implemented "
-                                "(run with witness_pruning off)");
+                {
+                    if (witness >= 0)
+                        throw Error("schema " + s.name + " has several parameters no effect mentions; the device BrFS prunes one "
+                                    "witness parameter per schema (run with witness_pruning off)");
+                    witness = static_cast<i32>(v);
+                }
         }
         if (task.never[si])
             continue;
+        const u32 first_action = static_cast<u32>(g.meta.size());
         // lexicographic enumeration over dom0, static literals checked once their parameters are bound
         std::vector<u32> bind(s.arity, 0);
         std::vector<std::vector<const Literal*>> statics_at(s.arity + 1);
@@ -1462,6 +1469,31 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
             }
         };
         rec(0);
+        if (witness >= 0)
+            for (u32 a = first_action; a < g.meta.size(); ++a)
+            {
+                std::vector<u32> key{si};
+                for (u32 v = 0; v < s.arity; ++v)
+                    if (static_cast<i32>(v) != witness)
+                        key.push_back(g.binding[static_cast<size_t>(a) * g.label_width + v]);
+                groups[key].push_back(a);
+            }
+    }
+    if (witness_pruning)
+    {
+        // dominators: the group's members with a smaller witness object. Members are in lexicographic binding order,
+        // so within a group (fixed effect-relevant objects) they ascend in the witness object.
+        std::vector<std::vector<u32>> doms(g.meta.size());
+        for (const auto& [key, members] : groups)
+            for (size_t i = 1; i < members.size(); ++i)
+                doms[members[i]].assign(members.begin(), members.begin() + static_cast<long>(i));
+        g.dom_off.assign(g.meta.size() + 1, 0);
+        for (u32 a = 0; a < g.meta.size(); ++a)
+        {
+            g.dom_off[a] = static_cast<u32>(g.dom.size());
+            g.dom.insert(g.dom.end(), doms[a].begin(), doms[a].end());
+        }
+        g.dom_off[g.meta.size()] = static_cast<u32>(g.dom.size());
     }
     return g;
 }

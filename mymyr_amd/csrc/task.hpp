@@ -260,13 +260,19 @@ struct GroundActions
     std::vector<u32> slots;  // pos..., neg..., add..., del...
     std::vector<u32> schema;
     std::vector<u32> binding;  // [num, label_width]
+    /// Witness pruning: action a is emitted only if none of dom[dom_off[a], dom_off[a + 1]) applies (the actions with
+    /// its effect-relevant binding and a smaller witness object). Empty without witness pruning.
+    std::vector<u32> dom_off;
+    std::vector<u32> dom;
     u32 label_width = 0;
     [[nodiscard]] u32 size() const { return static_cast<u32>(meta.size()); }
 };
 
-/// Grounds every schema (static literals filter the bindings). Throws if more than `limit` actions result, if an
-/// action has more than 255 atoms in one list, or if `witness_pruning` is set and some schema has a parameter that no
-/// effect mentions (device witness pruning is not implemented).
+/// Grounds every schema (static literals filter the bindings). Throws if more than `limit` actions result, or if an
+/// action has more than 255 atoms in one list. With `witness_pruning`, a schema may have at most one parameter that
+/// no effect mentions (a witness): among the applicable actions with one effect-relevant binding the one with the
+/// smallest witness object is the successor, the binding the reference's matcher finds first when the witness is its
+/// only unbound parameter (include/mymyr/successor/detail/engine.hpp:345-356). More witnesses throw.
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit);
 
 inline u32 words_for(u64 bits) { return static_cast<u32>((bits + 63) >> 6); }

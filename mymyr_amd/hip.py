@@ -43,6 +43,13 @@ def hash_rows(states: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def dedup_rows(start: int, count: int, words: int = 16, seed: int = 0, dup: float = 0.3, device="cuda") -> torch.Tensor:
+    """Rows [start, start + count) of the seeded dedup stream, generated on the device ([count, words] int64)."""
+    out = torch.empty((count, words), dtype=torch.int64, device=device)
+    check(lib.mya_dedup_rows(start, count, words, seed, dup, out.data_ptr(), _stream()))
+    return out
+
+
 class StateSet:
     """Device-resident open-addressing state set (rows of `words` u64 words)."""
 

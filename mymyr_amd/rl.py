@@ -81,9 +81,12 @@ class DeviceEnvPool:
         check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), _stream()))
         return {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
 
-    def step(self, actions: torch.Tensor | None = None, final_states: bool = False, labels: bool = True) -> dict:
+    def step(self, actions: torch.Tensor | None = None, final_states: bool = False, labels: bool = True,
+             encode: int = 0) -> dict:
         """One step of every env: actions [num_envs] int64 indices into the canonical successor order (None: the random
-        policy). Returns the step's arrays (views, overwritten by the next step)."""
+        policy). encode > 0 also emits the observed states' true-atom slots ("atoms", int32 [num_envs, encode], -1
+        padded) and applicable-schema masks ("masks", uint8 [num_envs, num_schemas]). Returns the step's arrays
+        (views, overwritten by the next step)."""
         if actions is not None:
             actions = actions.to(device=self.device, dtype=torch.int64).contiguous()
             if actions.shape != (self.num_envs,):
@@ -91,9 +94,16 @@ class DeviceEnvPool:
         if final_states and self.final_states is None:
             self.final_states = torch.zeros((self.num_envs, self.words), dtype=torch.int64, device=self.device)
         fs = self.final_states if final_states else None
+        atoms = masks = None
+        if encode:
+            if getattr(self, "_atoms", None) is None or self._atoms.shape[1] != encode:
+                self._atoms = torch.empty((self.num_envs, encode), dtype=torch.int32, device=self.device)
+                self._masks = torch.empty((self.num_envs, max(1, self.task.num_schemas)), dtype=torch.uint8, device=self.device)
+            atoms, masks = self._atoms, self._masks
         out = _lib.StepOutputs(self.reward.data_ptr(), self.terminated.data_ptr(), self.truncated.data_ptr(), self.count.data_ptr(),
                                _p(fs), self.schema.data_ptr() if labels else None, self.binding.data_ptr() if labels else None,
-                               self.label_width, self.words, self.invalid.data_ptr(), self.goal.data_ptr())
+                               self.label_width, self.words, self.invalid.data_ptr(), self.goal.data_ptr(), _p(atoms), _p(masks),
+                               encode, 0)
         check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(out), _p(actions), _stream()))
         r = {"states": self.states, "reward": self.reward, "terminated": self.terminated, "truncated": self.truncated,
              "count": self.count, "steps": self.steps, "at_goal": self.at_goal, "goal": self.goal, "invalid": self.invalid}
@@ -102,7 +112,24 @@ class DeviceEnvPool:
             r["binding"] = self.binding
         if fs is not None:
             r["final_states"] = fs
+        if encode:
+            r["atoms"] = atoms
+            r["masks"] = masks
         return r
+
+    def encode_atoms(self, states: torch.Tensor, max_atoms: int) -> torch.Tensor:
+        """True-atom slots of each row, ascending, -1 padded (int32 [rows, max_atoms])."""
+        s = states.view(torch.int64) if states.dtype == torch.uint64 else states.contiguous()
+        out = torch.empty((s.shape[0], max_atoms), dtype=torch.int32, device=s.device)
+        check(lib.mya_encode_atoms(self._h, s.data_ptr(), s.shape[0], s.shape[1], out.data_ptr(), max_atoms, _stream()))
+        return out
+
+    def schema_masks(self, states: torch.Tensor) -> torch.Tensor:
+        """Per row and schema, whether some binding is applicable (uint8 [rows, num_schemas])."""
+        s = states.view(torch.int64) if states.dtype == torch.uint64 else states.contiguous()
+        out = torch.empty((s.shape[0], max(1, self.task.num_schemas)), dtype=torch.uint8, device=s.device)
+        check(lib.mya_schema_masks(self._h, s.data_ptr(), s.shape[0], s.shape[1], out.data_ptr(), _stream()))
+        return out
 
     def check(self) -> None:
         """Raises if a step set the device's sticky error status."""

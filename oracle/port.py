@@ -1,0 +1,709 @@
+"""Test infrastructure, not product code: a CPU restatement of the reference algorithm of the state-expansion path
+(maichmueller/mymyr), written from the reference's semantics in plain Python with numpy for row arithmetic. Only
+tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, as the checker; the product never imports it.
+
+Every function cites the reference file:line it restates. How each part is pinned (tests/test_oracle.py):
+  hash_words / hash_state / mix64   closed form (include/mymyr/core/hash.hpp:12-60) + the compiled reference
+                                    (oracle/_ref) on random rows + golden vectors in tests/golden/hash.json
+  philox / successor_index          Random123 known-answer vectors (tests/cpp/rl/test_env.cpp:167-194) + the
+                                    compiled reference
+  read_task / compile (layout)      slot tables of the compiled reference for 18 suite tasks and the 5 workloads
+                                    (tests/golden/slots.json)
+  successors                        the compiled reference's canonical successor lists on random-walk states
+  env_step                          the compiled reference's HostEnv trajectories (tests/golden/env_*.json)
+  brfs                              the reference suite's exhaustive counts (tests/cpp/support/suite.hpp:33-56)
+                                    and layer counts / fingerprints of the compiled reference
+  dedup unique count                closed form: the number of fresh rows of the generator
+  encode_atoms / schema_masks       closed form (ascending set bits; any applicable binding per schema)
+Limitation: witness pruning is restated only where it is vacuous (every parameter in some effect); a task with
+witness parameters raises NotImplementedError ("parity unpinned" for that case).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+M64 = (1 << 64) - 1
+M32 = (1 << 32) - 1
+HASH_SEED = 0x2D358DCCAA6C78A5
+HASH_P1 = 0x8BB84B93962EACC9
+HASH_P2 = 0x4B33A62ED433D4A3
+OUTSIDE = 1 << 40
+
+
+# ------------------------------------------------------------------------------------------------- hashing
+def mix64(x: int) -> int:
+    """splitmix64 finalizer (include/mymyr/core/hash.hpp:12-20)."""
+    x &= M64
+    x ^= x >> 30
+    x = (x * 0xBF58476D1CE4E5B9) & M64
+    x ^= x >> 27
+    x = (x * 0x94D049BB133111EB) & M64
+    x ^= x >> 31
+    return x
+
+
+def mulfold(a: int, b: int) -> int:
+    """64x64->128 product folded to 64 bits (hash.hpp:23-31)."""
+    r = (a & M64) * (b & M64)
+    return (r & M64) ^ (r >> 64)
+
+
+def hash_words(w, seed: int = HASH_SEED) -> int:
+    """Hash of n words (hash.hpp:37-47)."""
+    w = [int(x) for x in w]
+    n = len(w)
+    h = (seed ^ (n * HASH_P1)) & M64
+    i = 0
+    while i + 1 < n:
+        h = mulfold(h ^ w[i] ^ HASH_P1, w[i + 1] ^ HASH_P2)
+        i += 2
+    if i < n:
+        h = mulfold(h ^ w[i] ^ HASH_P1, HASH_P2)
+    return mix64(h)
+
+
+def trimmed(w) -> int:
+    """bits::trimmed_size (include/mymyr/core/bitset.hpp:49-55)."""
+    n = len(w)
+    while n > 0 and int(w[n - 1]) == 0:
+        n -= 1
+    return n
+
+
+def hash_state(w) -> int:
+    """hash::state_words: hash over the trimmed words (hash.hpp:49-53)."""
+    return hash_words(list(w)[: trimmed(w)])
+
+
+# ------------------------------------------------------------------------------------------------- Philox
+def philox4x32_10(c, k0: int, k1: int):
+    """Philox-4x32-10 (include/mymyr/rl/rng.hpp:45-57)."""
+    c = [x & M32 for x in c]
+    k0 &= M32
+    k1 &= M32
+    for _ in range(10):
+        p0 = 0xD2511F53 * c[0]
+        p1 = 0xCD9E8D57 * c[2]
+        c = [((p1 >> 32) ^ c[1] ^ k0) & M32, p1 & M32, ((p0 >> 32) ^ c[3] ^ k1) & M32, p0 & M32]
+        k0 = (k0 + 0x9E3779B9) & M32
+        k1 = (k1 + 0xBB67AE85) & M32
+    return c
+
+
+def philox_block(seed: int, env: int, draw: int, purpose: int):
+    """rng::block: counter (draw lo, draw hi, env, purpose), key = seed (rng.hpp:59-64)."""
+    return philox4x32_10([draw & M32, (draw >> 32) & M32, env & M32, purpose], seed & M32, (seed >> 32) & M32)
+
+
+def below(x: int, n: int) -> int:
+    """high64(x * n) from 32x32 partial products (rng.hpp:73-78)."""
+    hi = (x >> 32) * n
+    lo = (x & M32) * n
+    return ((hi + (lo >> 32)) >> 32) & M32
+
+
+def successor_index(seed: int, env: int, draw: int, count: int) -> int:
+    """rng::successor_index (rng.hpp:80-84)."""
+    b = philox_block(seed, env, draw, 0)
+    return below(b[0] | (b[1] << 32), count)
+
+
+# ------------------------------------------------------------------------------------------------- task text
+class Task:
+    """A classical task read from the text format (src/mymyr/formalism/text_format.cpp:22-197) and compiled to atom
+    slots (src/mymyr/task/compile.cpp:803-915, 1363-1455; src/mymyr/task/task.cpp:106-143, 216-232)."""
+
+    def __init__(self, text: str, atoms: str = "auto"):
+        self._read(text)
+        self._compile(atoms)
+
+    # ---------------------------------------------------------------------------- reader
+    def _read(self, text: str) -> None:
+        tok = text.split()
+        pos = 0
+
+        def word():
+            nonlocal pos
+            pos += 1
+            return tok[pos - 1]
+
+        def num():
+            return int(word())
+
+        assert word() == "O"
+        self.n = num()
+        assert word() == "P"
+        self.preds = []  # (kind, arity, name)
+        for _ in range(num()):
+            k = word()
+            a = num()
+            nm = word()
+            if k not in ("S", "F"):
+                raise NotImplementedError("derived predicates")
+            self.preds.append((k, a, nm))
+        tag = word()
+        if tag != "SI":
+            raise NotImplementedError("numeric tasks")
+
+        def atoms():
+            out = []
+            for _ in range(num()):
+                p = num()
+                out.append((p, tuple(num() for _ in range(self.preds[p][1]))))
+            return out
+
+        self.static_init = atoms()
+        assert word() == "FI"
+        self.fluent_init = atoms()
+        assert word() == "G"
+        self.goal = []
+        for _ in range(num()):
+            p = num()
+            s = num() != 0
+            self.goal.append((p, s, tuple(num() for _ in range(self.preds[p][1]))))
+        assert word() == "A"
+        self.schemas = []  # (name, arity, pre [(p, pos, terms)], eff [(p, pos, terms)])
+        for _ in range(num()):
+            name = word()
+            ar = num()
+            assert word() == "L"
+            pre = []
+            for _ in range(num()):
+                p = num()
+                s = num() != 0
+                pre.append((p, s, tuple(int(word()) for _ in range(self.preds[p][1]))))
+            assert word() == "E"
+            eff = []
+            for _ in range(num()):
+                extra = num()
+                assert word() == "L"
+                nc = num()
+                if extra or nc:
+                    raise NotImplementedError("conditional effects")
+                assert word() == "F"
+                for _ in range(num()):
+                    p = num()
+                    s = num() != 0
+                    eff.append((p, s, tuple(int(word()) for _ in range(self.preds[p][1]))))
+            self.schemas.append((name, ar, pre, eff))
+        while pos < len(tok):
+            t = word()
+            if t == "X":
+                if num():
+                    raise NotImplementedError("axioms")
+            elif t == "C":
+                for _ in range(num()):
+                    num(); num(); num(); int(word())
+            elif t == "EG":
+                num()
+                for _ in range(num()):
+                    p = num(); num()
+                    for _ in range(self.preds[p][1]):
+                        num()
+            else:
+                raise ValueError("unexpected section " + t)
+        self.statics = {}
+        for p, args in self.static_init:
+            self.statics.setdefault(p, set()).add(args)
+        self.label_width = max([s[1] for s in self.schemas] + [0])
+
+    # ---------------------------------------------------------------------------- compile
+    def _static(self, p: int, args) -> bool:
+        return tuple(args) in self.statics.get(p, ())
+
+    def _dom0(self, s):
+        """The matcher's static domain of every parameter (compile.cpp:803-915)."""
+        name, ar, pre, eff = s
+        dom = [set(range(self.n)) for _ in range(ar)]
+        never = False
+        for p, pos, terms in pre:
+            kind, arity, _ = self.preds[p]
+            params = sorted({t for t in terms if t >= 0})
+            if not params:
+                if kind == "S" and self._static(p, [-(t + 1) for t in terms]) != pos:
+                    never = True
+                continue
+            if arity == 1:
+                if kind == "S":
+                    sat = {a[0] for a in self.statics.get(p, ())}
+                    dom[params[0]] = dom[params[0]] & sat if pos else dom[params[0]] - sat
+                continue
+            if arity == 2 and terms[0] != terms[1]:
+                f0, f1 = terms[0] >= 0, terms[1] >= 0
+                if f0 and f1:
+                    continue
+                fpos = 0 if f0 else 1
+                opos = 1 - fpos
+                v = terms[fpos]
+                c = -(terms[opos] + 1)
+                if kind == "S":
+                    row = {a[fpos] for a in self.statics.get(p, ()) if a[opos] == c}
+                    dom[v] = dom[v] & row if pos else dom[v] - row
+                continue
+            if kind == "S" and pos and arity >= 3:
+                for i in range(arity):
+                    if terms[i] >= 0:
+                        proj = {a[i] for a in self.statics.get(p, ())
+                                if all(terms[j] >= 0 or a[j] == -(terms[j] + 1) for j in range(arity))}
+                        dom[terms[i]] &= proj
+        if any(not d for d in dom):
+            never = True
+        return dom, never
+
+    def _compile(self, atoms: str) -> None:
+        self.dom0 = []
+        self.never = []
+        for s in self.schemas:
+            d, nv = self._dom0(s)
+            self.dom0.append(d)
+            self.never.append(nv)
+        # canonical layout (compile.cpp:1363-1455)
+        pos_dom = {}
+        for p, (k, a, _) in enumerate(self.preds):
+            if k == "F":
+                pos_dom[p] = [set() for _ in range(a)]
+        for si, (_, _, _, eff) in enumerate(self.schemas):
+            for p, positive, terms in eff:
+                if positive:
+                    for i, t in enumerate(terms):
+                        pos_dom[p][i] |= {-(t + 1)} if t < 0 else self.dom0[si][t]
+        for p, args in self.fluent_init:
+            for i, o in enumerate(args):
+                pos_dom[p][i].add(o)
+        self.offset, self.rank, self.stride, self.domain = {}, {}, {}, {}
+        running = 0
+        for p, (k, a, _) in enumerate(self.preds):
+            if k != "F":
+                continue
+            doms = [sorted(d) for d in pos_dom[p]]
+            self.domain[p] = doms
+            self.rank[p] = [{o: r for r, o in enumerate(d)} for d in doms]
+            st = [0] * a
+            acc = 1
+            for i in range(a - 1, -1, -1):
+                st[i] = acc
+                acc *= max(1, len(doms[i]))
+            self.stride[p] = st
+            size = 1
+            for d in doms:
+                size *= len(d)
+            self.offset[p] = running
+            running += size
+        self.fluent_count = running
+        # atom mode (task.cpp:106-143)
+        words_for = lambda x: (x + 63) // 64
+        if atoms == "dense":
+            self.mode = "dense"
+        else:
+            reach = sorted(self._reachable())
+            self.reachable = reach
+            dense_fits = words_for(self.fluent_count) <= words_for(len(reach))
+            self.mode = "dense" if atoms == "auto" and dense_fits else "reachable"
+        if self.mode == "dense":
+            self.slot_cid = list(range(self.fluent_count))
+        else:
+            self.slot_cid = self.reachable
+        self.slot_of = {c: s for s, c in enumerate(self.slot_cid)}
+        self.slots = len(self.slot_cid)
+        self.words = max(1, words_for(self.slots))
+        self.initial = self.row_of([(p, a) for p, a in self.fluent_init])
+        self.goal_unsat = False
+        self.goal_pos, self.goal_neg = [], []
+        posset = set()
+        for p, pos, args in self.goal:
+            if self.preds[p][0] == "S":
+                if self._static(p, args) != pos:
+                    self.goal_unsat = True
+                continue
+            if pos:
+                posset.add((p, args))
+            s = self.slot(p, args)
+            if s is None:
+                if pos:
+                    self.goal_unsat = True
+                continue
+            (self.goal_pos if pos else self.goal_neg).append(s)
+        for p, pos, args in self.goal:
+            if not pos and self.preds[p][0] == "F" and (p, args) in posset:
+                self.goal_unsat = True
+
+    def cid(self, p: int, args) -> int | None:
+        """CanonicalLayout::encode (include/mymyr/task/atom_index.hpp:89-95); None outside the position domains."""
+        c = self.offset[p]
+        for i, o in enumerate(args):
+            r = self.rank[p][i].get(o)
+            if r is None:
+                return None
+            c += r * self.stride[p][i]
+        return c
+
+    def slot(self, p: int, args) -> int | None:
+        c = self.cid(p, args)
+        return None if c is None else self.slot_of.get(c)
+
+    def record(self, s: int):
+        """(predicate, args) of slot s (AtomIndex::record)."""
+        c = self.slot_cid[s]
+        p = next(q for q in self.offset if self.offset[q] <= c < self.offset[q] + self._size(q))
+        rem = c - self.offset[p]
+        args = []
+        for i, d in enumerate(self.domain[p]):
+            args.append(d[rem // self.stride[p][i]])
+            rem %= self.stride[p][i]
+        return p, tuple(args)
+
+    def _size(self, p: int) -> int:
+        s = 1
+        for d in self.domain[p]:
+            s *= len(d)
+        return s
+
+    def row_of(self, atoms, words: int | None = None) -> np.ndarray:
+        w = self.words if words is None else words
+        row = np.zeros(w, dtype=np.uint64)
+        for p, args in atoms:
+            s = self.slot(p, args)
+            row[s >> 6] |= np.uint64(1 << (s & 63))
+        return row
+
+    def true_atoms(self, row) -> list:
+        out = []
+        for wi, x in enumerate(row):
+            x = int(x)
+            while x:
+                b = (x & -x).bit_length() - 1
+                x &= x - 1
+                s = wi * 64 + b
+                if s < self.slots:
+                    out.append(self.record(s))
+        return out
+
+    # ---------------------------------------------------------------------------- reachability
+    def _reachable(self) -> set:
+        """The delete-relaxed fixpoint (include/mymyr/reachability/relaxed_reachability.hpp:3-12): rules per add
+        effect, bodies of positive fluent and all static literals, '=' by identity; naive rounds."""
+        eq = next((p for p, (k, a, nm) in enumerate(self.preds) if k == "S" and nm == "=" and a == 2), None)
+        reached = set()
+        for p, args in self.fluent_init:
+            c = self.cid(p, args)
+            if c is not None:
+                reached.add((p, args))
+        changed = True
+        while changed:
+            changed = False
+            state = Index(reached)
+            for si, (name, ar, pre, eff) in enumerate(self.schemas):
+                heads = [e for e in eff if e[1]]
+                if not heads:
+                    continue
+                body = [(p, pos, t) for p, pos, t in pre if not (self.preds[p][0] == "F" and not pos)]
+                for b in self._bindings(ar, body, state, eq, dom=self.dom0[si]):
+                    for p, _, terms in heads:
+                        args = tuple(-(t + 1) if t < 0 else b[t] for t in terms)
+                        if self.cid(p, args) is not None and (p, args) not in reached:
+                            reached.add((p, args))
+                            changed = True
+        return {self.cid(p, a) for p, a in reached}
+
+    # ---------------------------------------------------------------------------- bindings
+    def _holds(self, p, args, state, eq) -> bool:
+        if self.preds[p][0] == "S":
+            return args[0] == args[1] if (eq is not None and p == eq) else tuple(args) in self.statics.get(p, ())
+        return (p, tuple(args)) in state.atoms
+
+    def _bindings(self, ar, lits, state, eq, dom):
+        """Every binding (parameters in index order, so lexicographic) under which all `lits` hold: brute force over
+        the parameters' domains, where a positive literal whose other parameters are already bound narrows the
+        candidates of its last parameter to the objects that make it true (an index lookup), and every literal is
+        checked once its last parameter is bound."""
+        b = [0] * ar
+        filters = [[] for _ in range(ar)]
+        checks = [[] for _ in range(ar)]
+        for p, pos, terms in lits:
+            ps = [t for t in terms if t >= 0]
+            if not ps:
+                if self._holds(p, tuple(-(t + 1) for t in terms), state, eq) != pos:
+                    return
+                continue
+            last = max(ps)
+            checks[last].append((p, pos, terms))
+            if pos and terms.count(last) == 1 and not (eq is not None and p == eq):
+                filters[last].append((p, terms.index(last), terms))
+
+        def rec(i):
+            if i == ar:
+                yield list(b)
+                return
+            cands = set(dom[i]) if dom is not None else set(range(self.n))
+            for p, at, terms in filters[i]:
+                key = tuple(-(t + 1) if t < 0 else b[t] for j, t in enumerate(terms) if j != at)
+                cands &= state.objects(self, p, at, key)
+            for o in sorted(cands):
+                b[i] = o
+                if all(self._holds(p, tuple(-(t + 1) if t < 0 else b[t] for t in terms), state, eq) == pos
+                       for p, pos, terms in checks[i]):
+                    yield from rec(i + 1)
+
+        yield from rec(0)
+
+
+class Index:
+    """A set of fluent atoms with per-(predicate, position) lookups; static predicates read the task's atoms."""
+
+    def __init__(self, atoms):
+        self.atoms = set(atoms)
+        self._idx = {}
+
+    def objects(self, task: Task, p: int, at: int, key) -> set:
+        k = (p, at)
+        if k not in self._idx:
+            d = {}
+            src = [(p, a) for a in task.statics.get(p, ())] if task.preds[p][0] == "S" else [x for x in self.atoms if x[0] == p]
+            for _, args in src:
+                d.setdefault(args[:at] + args[at + 1:], set()).add(args[at])
+            self._idx[k] = d
+        return self._idx[k].get(key, set())
+
+
+def successors(task: Task, row, witness: bool = False):
+    """Successors in canonical order: schemas in id order, bindings lexicographic over the parameter list; effects as
+    delete, then add (include/mymyr/successor/successors.hpp:154-248, 423-451). Returns [(schema, binding, row)]."""
+    state = Index(task.true_atoms(row))
+    out = []
+    for si, (name, ar, pre, eff) in enumerate(task.schemas):
+        if task.never[si]:
+            continue
+        rel = sorted({t for _, _, terms in eff for t in terms if t >= 0})
+        if witness and len(rel) < ar - 1:
+            raise NotImplementedError("witness pruning with several witness parameters (parity unpinned)")
+        seen = set()
+        for b in task._bindings(ar, pre, state, None, task.dom0[si]):
+            if witness and len(rel) < ar:
+                # one witness: the matcher's first witness is the smallest object, which is the lexicographically
+                # first binding of the effect-relevant values (engine.hpp:345-356)
+                key = tuple(b[v] for v in rel)
+                if key in seen:
+                    continue
+                seen.add(key)
+            nxt = np.array(row, dtype=np.uint64, copy=True)
+            for p, pos, terms in eff:
+                if not pos:
+                    s = task.slot(p, tuple(-(t + 1) if t < 0 else b[t] for t in terms))
+                    if s is not None:
+                        nxt[s >> 6] &= np.uint64(~(1 << (s & 63)) & M64)
+            for p, pos, terms in eff:
+                if pos:
+                    s = task.slot(p, tuple(-(t + 1) if t < 0 else b[t] for t in terms))
+                    nxt[s >> 6] |= np.uint64(1 << (s & 63))
+            out.append((si, b, nxt))
+    return out
+
+
+def is_goal(task: Task, row) -> bool:
+    """Successors::goal_holds over the compiled goal (successors.hpp:129-141)."""
+    if task.goal_unsat:
+        return False
+    bit = lambda s: (int(row[s >> 6]) >> (s & 63)) & 1
+    return all(bit(s) for s in task.goal_pos) and not any(bit(s) for s in task.goal_neg)
+
+
+# ------------------------------------------------------------------------------------------------- env
+class Env:
+    """HostEnv over one task, index action space (src/mymyr/rl/env.cpp:351-528): per-row state, steps, draws, at_goal."""
+
+    def __init__(self, task: Task, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True):
+        self.t = task
+        self.seed, self.max_steps = seed, max_steps
+        self.step_reward = np.float32(step_reward)
+        self.goal_reward = np.float32(goal_reward)
+        self.dead_end_reward = np.float32(dead_end_reward)
+        self.dead_end, self.dead_end_terminal, self.autoreset = dead_end, dead_end_terminal, autoreset
+        self.init_count = len(successors(task, task.initial))
+        self.init_goal = is_goal(task, task.initial)
+
+    def reset(self, n: int, words: int | None = None) -> dict:
+        """HostEnv::reset (env.cpp:207-240): every row to the initial state, steps 0, draws 0."""
+        w = self.t.words if words is None else words
+        states = np.zeros((n, w), dtype=np.uint64)
+        states[:, : self.t.words] = self.t.initial
+        return {"states": states, "steps": np.zeros(n, np.int32), "draws": np.zeros(n, np.uint64),
+                "at_goal": np.full(n, 1 if self.init_goal else 0, np.uint8), "count": np.full(n, self.init_count, np.int32)}
+
+    def step(self, b: dict, first_env: int = 0, actions=None) -> dict:
+        n = b["states"].shape[0]
+        L = max(1, self.t.label_width)
+        out = {"reward": np.zeros(n, np.float32), "terminated": np.zeros(n, np.uint8), "truncated": np.zeros(n, np.uint8),
+               "count": np.zeros(n, np.int32), "schema": np.full(n, -1, np.int32), "binding": np.full((n, L), -1, np.int32),
+               "goal": np.zeros(n, np.uint8), "invalid": np.zeros(n, np.uint8),
+               "final_states": np.zeros_like(b["states"])}
+        W = self.t.words
+        for i in range(n):
+            row = b["states"][i, :W].copy()
+            already = bool(b["at_goal"][i])
+            succ = successors(self.t, row)
+            c = len(succ)
+            st = "goal" if already else "ok"
+            a = 0
+            if not already and c == 0:
+                st = "stuck"
+            elif not already and actions is not None:
+                if actions[i] < 0 or actions[i] >= c:
+                    st = "invalid"
+                else:
+                    a = int(actions[i])
+            elif not already:
+                a = successor_index(self.seed, first_env + i, int(b["draws"][i]), c)
+            b["draws"][i] += np.uint64(1)
+            if st == "ok":
+                out["schema"][i] = succ[a][0]
+                for k, o in enumerate(succ[a][1]):
+                    out["binding"][i, k] = o
+            out["invalid"][i] = 1 if st == "invalid" else 0
+            s2 = succ[a][2] if st == "ok" else row
+            g = already
+            c2 = c
+            if st == "ok":
+                g = is_goal(self.t, s2)
+                c2 = len(successors(self.t, s2))
+            dead = self.dead_end == "no_successors" and not g and ((st == "ok" and c2 == 0) or st == "stuck")
+            term = g or (dead and self.dead_end_terminal)
+            absorbed = already or (st == "stuck" and dead and self.dead_end_terminal)
+            t2 = int(b["steps"][i]) + (0 if absorbed else 1)
+            trunc = (not term) and self.max_steps and t2 >= self.max_steps
+            if absorbed:
+                r = np.float32(0.0)
+            else:
+                r = np.float32(self.step_reward + (self.goal_reward if g else np.float32(0.0)))
+                r = np.float32(r + (self.dead_end_reward if dead else np.float32(0.0)))
+            out["reward"][i] = r
+            out["terminated"][i] = 1 if term else 0
+            out["truncated"][i] = 1 if trunc else 0
+            out["goal"][i] = 1 if g else 0
+            out["final_states"][i, :W] = s2
+            if self.autoreset and (term or trunc):
+                b["states"][i, :] = 0
+                b["states"][i, :W] = self.t.initial
+                b["steps"][i] = 0
+                b["at_goal"][i] = 1 if self.init_goal else 0
+                out["count"][i] = self.init_count
+                continue
+            b["at_goal"][i] = 1 if g else 0
+            b["states"][i, :W] = s2
+            b["steps"][i] = t2
+            out["count"][i] = c2
+        return out
+
+
+# ------------------------------------------------------------------------------------------------- BrFS
+def brfs(task: Task, max_depth=None, max_states=None, max_expanded=None, stop_at_goal=True, fingerprint=True) -> dict:
+    """run_flat (src/mymyr/search/brfs.cpp:274-404) with Control::finish (brfs.cpp:194-203): ids by first discovery,
+    layer_counts {expanded, generated, new}, fingerprint = XOR mix64(id * phi ^ canonical_hash) (brfs.cpp:34-37,
+    task.cpp:387-404)."""
+    INF = float("inf")
+    md = INF if max_depth is None else max_depth
+    ms = INF if max_states is None else max_states
+    me = INF if max_expanded is None else max_expanded
+    rows = [task.initial.copy()]
+    ids = {task.initial.tobytes(): 0}
+    expanded = generated = goals = 0
+    layers = 0
+    layer_end = 0
+    pos = 0
+    first_goal = None
+    lc = []
+    cur = None
+    stopped_budget = False
+    full = False
+    while pos < len(rows) and len(rows) < ms:
+        if expanded >= me:
+            stopped_budget = True
+            break
+        if pos == layer_end:
+            if cur is not None:
+                lc.append([expanded - cur[0], generated - cur[1], len(rows) - cur[2]])
+                cur = None
+            if layers == md:
+                break
+            layers += 1
+            layer_end = len(rows)
+            cur = (expanded, generated, len(rows))
+        row = rows[pos]
+        g = is_goal(task, row)
+        goals += g
+        if g and first_goal is None:
+            first_goal = pos
+        if g and stop_at_goal:
+            break
+        expanded += 1
+        for _, _, nxt in successors(task, row, witness=True):
+            generated += 1
+            key = nxt.tobytes()
+            if key not in ids:
+                ids[key] = len(rows)
+                rows.append(nxt)
+                if len(rows) >= ms:
+                    full = True
+                    break
+        if full:
+            break
+        pos += 1
+    if cur is not None:
+        lc.append([expanded - cur[0], generated - cur[1], len(rows) - cur[2]])
+    exhausted = pos == len(rows)
+    fp = 0
+    if fingerprint:
+        for i, r in enumerate(rows):
+            fp ^= mix64((i * 0x9E3779B97F4A7C15 & M64) ^ canonical_hash(task, r))
+    solved = first_goal is not None
+    status = 0 if solved else (2 if stopped_budget else (1 if exhausted or layers >= md else 2))
+    return {"states": len(rows), "expanded": expanded, "generated": generated, "goal_states": goals, "layers": layers,
+            "layer_counts": lc, "exhausted": exhausted, "solved": solved, "status": status, "fingerprint": fp}
+
+
+def canonical_hash(task: Task, row) -> int:
+    """Task::canonical_hash (src/mymyr/task/task.cpp:387-404), classical part."""
+    x = 0
+    for wi, w in enumerate(row):
+        w = int(w)
+        while w:
+            b = (w & -w).bit_length() - 1
+            w &= w - 1
+            x ^= mix64(task.slot_cid[wi * 64 + b] + 0x1234567)
+    return x
+
+
+# ------------------------------------------------------------------------------------------------- encoding
+def encode_atoms(row, max_atoms: int) -> np.ndarray:
+    """Ascending slot indices of the set bits (State::slots, include/mymyr/state/state.hpp:96-101), -1 padded
+    (the padded-array convention, include/mymyr/rl/task_arrays.hpp:4-8)."""
+    out = np.full(max_atoms, -1, np.int32)
+    k = 0
+    for wi, w in enumerate(row):
+        w = int(w)
+        while w and k < max_atoms:
+            b = (w & -w).bit_length() - 1
+            w &= w - 1
+            out[k] = wi * 64 + b
+            k += 1
+    return out
+
+
+def schema_masks(task: Task, row) -> np.ndarray:
+    """Per schema, whether some binding is applicable (rl::schema_masks, include/mymyr/rl/masks.hpp:9-11)."""
+    m = np.zeros(len(task.schemas), np.uint8)
+    for si, _, _ in successors(task, row):
+        m[si] = 1
+    return m
+
+
+def dedup_unique(rows: np.ndarray) -> tuple[int, np.ndarray]:
+    """Unique count and first-occurrence ids of rows inserted in order (FlatStateStore::insert ids,
+    include/mymyr/state/flat_store.hpp:73-115)."""
+    seen = {}
+    ids = np.zeros(rows.shape[0], np.int64)
+    for i in range(rows.shape[0]):
+        k = rows[i, : trimmed(rows[i])].tobytes()
+        ids[i] = seen.setdefault(k, len(seen))
+    return len(seen), ids

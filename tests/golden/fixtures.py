@@ -1,0 +1,66 @@
+"""Fixture helpers shared by tests/golden/make_golden.py and the tests: file locations and the per-step digest of env
+trajectories."""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+
+import numpy as np
+
+GOLDEN = os.path.dirname(os.path.abspath(__file__))
+TASKS = os.path.join(GOLDEN, "tasks")
+
+# suite tasks of the reference (tests/data/tasks) that the device path supports, with the reference's published
+# exhaustive BrFS counts {states, generated (witness pruning on), goal_states} (tests/cpp/support/suite.hpp:33-56)
+SUITE_COUNTS = {
+    "gripper__prob05": (376832, 2031616, 2),
+    "blocks__probBLOCKS-8-0": (695417, 2094752, 1),
+    "logistics00__probLOGISTICS-6-1": (941192, 10487568, 8),
+    "miconic__s7-4": (229376, 3153920, 1792),
+    "visitall__visitall_x-6_y-3_r-100": (193456, 597411, 18),
+    "sokoban-opt08-strips__p14": (348955, 866027, 27),
+    "depot__p02": (40320, 376560, 9),
+    "driverlog__p03": (348750, 2826000, 40),
+    "zenotravel__p05": (1016064, 17224704, 784),
+    "transport-opt08-strips__p23": (1185759, 6993720, 81),
+    "snake-opt18-strips__p05": (1320037, 2200339, 88669),
+    "parcprinter-opt11-strips__p03": (173942, 488868, 1),
+    "pegsol-08-strips__p22": (99457, 189967, 2),
+    "pathways__p02": (669078, 11237052, 12288),
+}
+# rovers__p02 has schemas with two witness parameters (device witness pruning takes one): env and layout only
+LAYOUT_ONLY = ["rovers__p02"]
+
+# the reference's own determinism digests of search.brfs(max_states=20000, fingerprint=True, stop_at_goal=False):
+# sha256(json.dumps([states, expanded, generated, layers, fingerprint], sort_keys=True))[:16]
+# (tests/data/determinism.json, tests/python/test_determinism.py:63-104)
+DETERMINISM_BRFS = {
+    "blocks__probBLOCKS-8-0": "4a2c176284577ee8",
+    "depot__p02": "a8bc749fad052dbe",
+    "gripper__prob05": "393197c282f5c1d2",
+    "logistics00__probLOGISTICS-6-1": "ab1c7b50f936cad0",
+}
+
+
+def determinism_digest(states, expanded, generated, layers, fingerprint) -> str:
+    return hashlib.sha256(json.dumps([states, expanded, generated, layers, fingerprint], sort_keys=True).encode()).hexdigest()[:16]
+
+
+def step_digest(n: int, states, reward, terminated, truncated, count, schema, binding, goal) -> str:
+    """sha256 of the first n rows of one step's arrays, in a fixed order and dtype."""
+    h = hashlib.sha256()
+    for a, dt in ((states, np.uint64), (reward, np.float32), (terminated, np.uint8), (truncated, np.uint8), (count, np.int32),
+                  (schema, np.int32), (binding, np.int32), (goal, np.uint8)):
+        h.update(np.ascontiguousarray(np.asarray(a)[:n]).astype(dt, copy=False).tobytes())
+    return h.hexdigest()[:16]
+
+
+def load(name: str):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return json.load(f)
+
+
+def task_path(name: str) -> str:
+    return os.path.join(TASKS, f"{name}.txt")

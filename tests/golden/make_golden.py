@@ -1,0 +1,204 @@
+"""Writes the golden fixtures under tests/golden/ from the compiled reference (oracle/_ref, built by oracle/Makefile from
+the reference's sources). Run in a container that has the reference checkout:
+
+    make -C oracle && python tests/golden/make_golden.py [--quick]
+
+Outputs (JSON): hash.json, philox.json, slots.json, successors.json, env_<workload>.json, brfs.json, plus the
+workload task files under tests/golden/tasks/. --quick skips the slow BrFS fixtures.
+"""
+
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from mymyr_amd import workloads  # noqa: E402
+from oracle import ref  # noqa: E402
+from tests.golden import fixtures as fx  # noqa: E402
+
+M64 = (1 << 64) - 1
+
+
+def dump(name, obj):
+    with open(os.path.join(fx.GOLDEN, name), "w") as f:
+        json.dump(obj, f, indent=1, sort_keys=True)
+    print("wrote", name, flush=True)
+
+
+def hex_row(r):
+    return [f"{int(x):016x}" for x in r]
+
+
+def make_hash():
+    rng = np.random.default_rng(12345)
+    cases = []
+    for n in [0, 1, 2, 3, 7, 8, 13, 16, 33, 176]:
+        for k in range(3):
+            w = rng.integers(0, 2**63, size=n, dtype=np.int64).view(np.uint64) ^ rng.integers(0, 2, size=n, dtype=np.uint64) << np.uint64(63)
+            if k == 1 and n > 2:
+                w[n // 2:] = 0  # trailing zero words: the state hash ignores them
+            seed = int(rng.integers(0, 2**63)) if k == 2 else 0x2D358DCCAA6C78A5
+            cases.append({"words": hex_row(w), "seed": f"{seed:016x}", "hash_words": f"{ref.hash_words(w, seed):016x}",
+                          "hash_state": f"{ref.hash_state(w):016x}"})
+    mix = [{"x": f"{x:016x}", "mix64": f"{int(ref.lib().mref_hash_mix64(x)):016x}"} for x in
+           [0, 1, 0x9E3779B97F4A7C15, M64, 0x123456789ABCDEF0]]
+    dump("hash.json", {"cases": cases, "mix64": mix})
+
+
+def make_philox():
+    # Random123 kat_vectors, philox4x32 10 (the reference's tests/cpp/rl/test_env.cpp:167-194)
+    kats = [
+        {"ctr": [0, 0, 0, 0], "key": [0, 0], "out": [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]},
+        {"ctr": [0xFFFFFFFF] * 4, "key": [0xFFFFFFFF] * 2, "out": [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]},
+        {"ctr": [0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], "key": [0xA4093822, 0x299F31D0],
+         "out": [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]},
+    ]
+    rng = np.random.default_rng(7)
+    draws = []
+    for _ in range(64):
+        seed = int(rng.integers(0, 2**63))
+        env = int(rng.integers(0, 2**32))
+        draw = int(rng.integers(0, 2**40))
+        count = int(rng.integers(1, 5000))
+        draws.append({"seed": seed, "env": env, "draw": draw, "block": ref.philox(seed, env, draw, 0), "count": count,
+                      "index": ref.successor_index(seed, env, draw, count)})
+    dump("philox.json", {"kats": kats, "draws": draws})
+
+
+def workload_tasks():
+    for name in workloads.TASKS:
+        workloads.task_file(name, fx.TASKS)
+
+
+def make_slots():
+    out = {}
+    names = sorted(list(fx.SUITE_COUNTS) + fx.LAYOUT_ONLY)
+    for name in names + list(workloads.TASKS):
+        for atoms in ["auto", "dense", "reachable"]:
+            t = ref.RefTask(fx.task_path(name), atoms)
+            rec, cid = t.slot_records()
+            out[f"{name}:{atoms}"] = {
+                "words": t.words, "mode": t.atom_mode, "slots": t.fluent_slots, "dense_fluent": t.dense_fluent,
+                "cid_sha": hashlib.sha256(cid.astype(np.uint64).tobytes()).hexdigest(),
+                "rec_sha": hashlib.sha256(rec.astype(np.uint32).tobytes()).hexdigest(),
+                "cid_head": [int(x) for x in cid[:32]], "initial": hex_row(t.initial_state(t.words)),
+            }
+    dump("slots.json", out)
+
+
+def make_successors():
+    out = {}
+    for name, steps in [("gripper__prob05", 12), ("blocks__probBLOCKS-8-0", 12), ("depot__p02", 8), ("gridworld", 12),
+                        ("transport", 8), ("strips", 4), ("transport_xl", 3)]:
+        t = ref.RefTask(fx.task_path(name), "dense" if name == "strips" else "auto")
+        rng = np.random.default_rng(3)
+        row = t.initial_state()
+        states = []
+        for _ in range(steps):
+            sc, bd, rs = t.successors(row)
+            states.append({"row": hex_row(row), "count": int(len(sc)), "schema": [int(x) for x in sc],
+                           "binding": bd.tolist(), "succ_hash": [f"{ref.hash_state(r):016x}" for r in rs],
+                           "goal": t.is_goal(row)})
+            if len(sc) == 0:
+                break
+            row = rs[int(rng.integers(len(sc)))]
+        out[name] = states
+    dump("successors.json", out)
+
+
+def env_trajectory(w: workloads.EnvWorkload, rows: int, steps: int, threads: int = 8):
+    t = ref.RefTask(fx.task_path(w.name), w.atoms)
+    e = ref.RefEnv(t, threads=threads, **w.env)
+    N, W, L = rows, t.table_words, max(1, t.label_width)
+    S = np.zeros((N, W), np.uint64)
+    st = np.zeros(N, np.int32)
+    dr = np.zeros(N, np.uint64)
+    ag = np.zeros(N, np.uint8)
+    cnt = np.zeros(N, np.int32)
+    e.reset(S, st, dr, ag, cnt)
+    digests = []
+    totals = {"terminated": 0, "truncated": 0, "reward": 0.0}
+    t0 = time.time()
+    for k in range(steps):
+        R = np.zeros(N, np.float32)
+        term = np.zeros(N, np.uint8)
+        trunc = np.zeros(N, np.uint8)
+        c = np.zeros(N, np.int32)
+        sch = np.zeros(N, np.int32)
+        bnd = np.zeros((N, L), np.int32)
+        g = np.zeros(N, np.uint8)
+        e.step(S, st, dr, ag, reward=R, terminated=term, truncated=trunc, count=c, schema=sch, binding=bnd, goal=g)
+        digests.append(fx.step_digest(N, S, R, term, trunc, c, sch, bnd, g))
+        totals["terminated"] += int(term.sum())
+        totals["truncated"] += int(trunc.sum())
+        totals["reward"] += float(R.astype(np.float64).sum())
+    return {"workload": w.name, "rows": N, "steps": steps, "env": w.env, "digests": digests, "totals": totals,
+            "ref_seconds": time.time() - t0}
+
+
+def make_env():
+    g = workloads.GRIDWORLD
+    dump("env_gridworld.json", env_trajectory(g, g.num_envs, g.steps))
+    dump("env_transport.json", env_trajectory(workloads.TRANSPORT, 2048, 64))
+    dump("env_transport_xl.json", env_trajectory(workloads.TRANSPORT_XL, 128, 32))
+    # small instances with goals, truncation and dead ends reached often
+    small = workloads.EnvWorkload("gridworld", 256, 200, {"seed": 3, "max_steps": 40, "step_reward": -1.0, "goal_reward": 5.0})
+    dump("env_gridworld_truncated.json", env_trajectory(small, 256, 200))
+    make_env_small()
+
+
+def make_env_small():
+    # a trajectory short enough for the oracle's pure-Python restatement
+    tiny = workloads.EnvWorkload("gridworld", 16, 60, {"seed": 3, "max_steps": 20, "step_reward": -1.0, "goal_reward": 5.0})
+    dump("env_gridworld_small.json", env_trajectory(tiny, 16, 60))
+
+
+def brfs_record(name, atoms="auto", **kw):
+    t = ref.RefTask(fx.task_path(name), atoms)
+    r = ref.brfs(t, **kw)
+    r.pop("seconds")
+    r["options"] = kw
+    return r
+
+
+def make_brfs(quick: bool):
+    out = {"suite": {}, "budget": {}, "strips": {}}
+    for name in fx.SUITE_COUNTS:
+        if quick and fx.SUITE_COUNTS[name][0] > 200000:
+            continue
+        out["suite"][name] = brfs_record(name, stop_at_goal=False)
+        out["budget"][name] = brfs_record(name, stop_at_goal=False, max_states=20000)
+        out["budget"][name + ":goal"] = brfs_record(name, stop_at_goal=True)
+        print(name, out["suite"][name]["states"], flush=True)
+    for ms in ([1 << 20] if quick else [1 << 20, 1 << 22, 1 << 24]):
+        out["strips"][str(ms)] = brfs_record("strips", "dense", max_depth=12, max_states=ms, stop_at_goal=False)
+        print("strips", ms, flush=True)
+    out["strips"]["depth3"] = brfs_record("strips", "dense", max_depth=3, stop_at_goal=False)
+    out["strips"]["expanded5000"] = brfs_record("strips", "dense", max_depth=12, max_states=1 << 22, stop_at_goal=False)
+    dump("brfs.json", out)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--only", default="")
+    a = ap.parse_args()
+    workload_tasks()
+    steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
+             "env_small": make_env_small, "brfs": lambda: make_brfs(a.quick)}
+    for k, f in steps.items():
+        if not a.only or k in a.only.split(","):
+            f()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,79 @@
+"""The device BrFS against the reference: the suite's published exhaustive counts (tests/cpp/support/suite.hpp:33-56),
+the reference's own determinism digests (tests/data/determinism.json), and the compiled reference's layer counts,
+fingerprints and statuses (tests/golden/brfs.json), including the strips workload's max_states cuts."""
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+pytest.importorskip("torch")
+
+KEYS = ["states", "expanded", "generated", "goal_states", "layers", "fingerprint", "status", "layer_counts", "exhausted", "solved"]
+STATUS = {0: "solved", 1: "exhausted", 2: "out_of_states"}
+
+
+def device(golden, name, atoms="auto", **kw):
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path(name), atoms)
+    r = search.brfs(t, fingerprint=True, **kw)
+    return {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
+            "layers": r.layers, "fingerprint": r.fingerprint, "status": r.status, "layer_counts": r.layer_counts,
+            "exhausted": r.exhausted, "solved": r.solved}
+
+
+def same(r, exp):
+    bad = {k: (r[k], exp[k] if k != "status" else STATUS.get(exp[k], exp[k])) for k in KEYS
+           if (r[k] != (STATUS.get(exp[k], exp[k]) if k == "status" else exp[k]))}
+    return bad
+
+
+@pytest.mark.parametrize("name", ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "miconic__s7-4", "pegsol-08-strips__p22",
+                                  "parcprinter-opt11-strips__p03", "visitall__visitall_x-6_y-3_r-100", "sokoban-opt08-strips__p14",
+                                  "driverlog__p03", "logistics00__probLOGISTICS-6-1", "pathways__p02", "zenotravel__p05",
+                                  "transport-opt08-strips__p23", "snake-opt18-strips__p05"])
+def test_suite_exhaustive(golden, name):
+    states, generated, goals = golden.SUITE_COUNTS[name]
+    r = device(golden, name, stop_at_goal=False)
+    assert (r["states"], r["generated"], r["goal_states"]) == (states, generated, goals)
+    exp = golden.load("brfs.json")["suite"].get(name)
+    if exp:
+        assert not same(r, exp), same(r, exp)
+
+
+@pytest.mark.parametrize("name", list(__import__("tests.golden.fixtures", fromlist=["x"]).DETERMINISM_BRFS))
+def test_reference_determinism_digests(golden, name):
+    r = device(golden, name, stop_at_goal=False, max_states=20000)
+    assert golden.determinism_digest(r["states"], r["expanded"], r["generated"], r["layers"], r["fingerprint"]) == \
+        golden.DETERMINISM_BRFS[name]
+
+
+def test_budget_and_goal_stops(golden):
+    g = golden.load("brfs.json")["budget"]
+    for key, exp in g.items():
+        name = key.split(":")[0]
+        kw = dict(exp["options"])
+        r = device(golden, name, **kw)
+        assert not same(r, exp), (key, same(r, exp))
+
+
+def test_strips_workload_cuts(golden):
+    g = golden.load("brfs.json")["strips"]
+    for key, exp in g.items():
+        r = device(golden, "strips", "dense", **exp["options"])
+        assert not same(r, exp), (key, same(r, exp))
+
+
+def test_small_chunks_do_not_change_results(golden):
+    """Chunked layers (tiny candidate buffers) give the same ids and counts."""
+    a = device(golden, "gripper__prob05", stop_at_goal=False)
+    b = device(golden, "gripper__prob05", stop_at_goal=False, chunk=64)
+    assert a == b
+
+
+def test_unsupported_witness_pattern_refused(golden):
+    from mymyr_amd._lib import MyaError
+
+    with pytest.raises(MyaError, match="witness"):
+        device(golden, "rovers__p02", stop_at_goal=False)

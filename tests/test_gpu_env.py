@@ -1,0 +1,137 @@
+"""The device env step against the reference HostEnv's trajectories (per-step digests of states, rewards,
+terminations, truncations, counts, labels and goals written by the compiled reference), the canonical successor
+listing against the reference's, and the per-step encodings against the oracle's closed forms.
+
+An env's trajectory depends only on its row, its actions and its RNG stream (env id), so a full-size batch is checked
+on its first rows against the reference's trajectory of a smaller batch (include/mymyr/rl/env.hpp:46-48)."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0):
+    from mymyr_amd import rl, workloads
+    from mymyr_amd.task import Task
+
+    g = golden.load(fixture)
+    atoms = "dense" if g["workload"] == "strips" else "auto"
+    t = Task.from_text_file(golden.task_path(g["workload"]), atoms)
+    n = num_envs or g["rows"]
+    pool = rl.DeviceEnvPool(t, n, **g["env"])
+    pool.reset()
+    rows = g["rows"]
+    for k in range(g["steps"]):
+        o = pool.step(encode=encode)
+        d = golden.step_digest(rows, host(o["states"]).view(np.uint64), host(o["reward"]), host(o["terminated"]),
+                               host(o["truncated"]), host(o["count"]), host(o["schema"]), host(o["binding"])[:, : max(1, t.label_width)],
+                               host(o["goal"]))
+        assert d == g["digests"][k], f"{fixture}: step {k} differs from the reference"
+    pool.check()
+    return pool, t
+
+
+def test_gridworld_full_workload(golden):
+    """The gridworld workload at its full size (1024 envs x 256 steps), bit-exact every step."""
+    run_env(golden, "env_gridworld.json")
+
+
+def test_gridworld_truncation_goals_resets(golden):
+    g = golden.load("env_gridworld_truncated.json")
+    assert g["totals"]["truncated"] > 0 and g["totals"]["terminated"] > 0  # the fixture exercises both
+    run_env(golden, "env_gridworld_truncated.json")
+
+
+def test_transport_full_batch_first_rows(golden):
+    """65536 envs (the transport workload's batch) stepped on the device; the first 2048 rows match the reference."""
+    run_env(golden, "env_transport.json", num_envs=65536)
+
+
+def test_transport_xl_first_rows_with_encoding(golden):
+    """transport_xl with the encoding outputs on; the first rows match the reference's trajectory."""
+    pool, t = run_env(golden, "env_transport_xl.json", num_envs=4096, encode=600)
+
+
+def test_encoding_closed_form(golden):
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+    from oracle import port
+
+    text = open(golden.task_path("transport")).read()
+    t = Task.from_text(text)
+    pt = port.Task(text)
+    pool = rl.DeviceEnvPool(t, 64, seed=11)
+    pool.reset()
+    for _ in range(5):
+        o = pool.step(encode=160)
+    states = host(o["states"]).view(np.uint64)
+    atoms, masks = host(o["atoms"]), host(o["masks"])
+    for i in range(0, 64, 7):
+        assert np.array_equal(atoms[i], port.encode_atoms(states[i, : pt.words], 160))
+        assert np.array_equal(masks[i], port.schema_masks(pt, states[i, : pt.words]))
+    # the standalone ops agree with the fused outputs
+    assert np.array_equal(host(pool.encode_atoms(o["states"], 160)), atoms)
+    assert np.array_equal(host(pool.schema_masks(o["states"])), masks)
+
+
+@pytest.mark.parametrize("name", ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "gridworld", "transport", "strips",
+                                  "transport_xl"])
+def test_successor_listing_golden(golden, name):
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+    from oracle import port
+
+    g = golden.load("successors.json")[name]
+    t = Task.from_text_file(golden.task_path(name), "dense" if name == "strips" else "auto")
+    rows = np.array([[int(x, 16) for x in s["row"]][: t.words] for s in g], dtype=np.uint64)
+    cap = max(s["count"] for s in g) + 1
+    cnt, sch, bnd, succ = rl.successors(t, torch.from_numpy(rows.view(np.int64)).cuda(), cap=cap)
+    cnt, sch, bnd, succ = host(cnt), host(sch), host(bnd), host(succ).view(np.uint64)
+    for i, s in enumerate(g):
+        k = s["count"]
+        assert cnt[i] == k
+        assert list(sch[i, :k]) == s["schema"]
+        if k:
+            assert bnd[i, :k, : len(s["binding"][0])].tolist() == s["binding"]
+        assert [f"{port.hash_state(r):016x}" for r in succ[i, :k]] == s["succ_hash"]
+
+
+def test_given_actions_and_invalid(golden):
+    """Index actions: in-range ones move to that successor; out-of-range ones do not move and set invalid."""
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("gridworld"))
+    pool = rl.DeviceEnvPool(t, 8, seed=0)
+    pool.reset()
+    s0 = host(pool.states).copy()
+    cnt, _, _, succ = rl.successors(t, pool.states, cap=8)
+    acts = torch.tensor([0, 1, -1, 100, 0, 0, 0, 0], dtype=torch.int64)
+    o = pool.step(actions=acts)
+    inv = host(o["invalid"])
+    assert list(inv[:4]) == [0, int(host(cnt)[1] <= 1), 1, 1]
+    assert np.array_equal(host(o["states"])[0], host(succ)[0, 0])
+    assert np.array_equal(host(o["states"])[2], s0[2])
+    assert host(o["reward"])[2] == 0.0  # step_reward 0: an invalid action earns it, not the goal reward
+
+
+def test_env_argument_errors(golden):
+    from mymyr_amd import rl
+    from mymyr_amd._lib import MyaError
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("transport"))
+    with pytest.raises(MyaError, match="witness_pruning"):
+        rl.DeviceEnvPool(t, 4, witness_pruning=True)
+    with pytest.raises(ValueError, match="words"):
+        rl.DeviceEnvPool(t, 4, words=2)
+    pool = rl.DeviceEnvPool(t, 4)
+    with pytest.raises(ValueError, match="shape"):
+        pool.step(actions=torch.zeros(3, dtype=torch.int64))

@@ -1,0 +1,96 @@
+"""Device hashing and the device state set against the golden hash vectors, the oracle and closed forms."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a: np.ndarray) -> "torch.Tensor":
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int64)).cuda()
+
+
+def host(t) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint64)
+
+
+def test_hash_rows_golden(golden):
+    from mymyr_amd import hip
+
+    g = golden.load("hash.json")
+    by_len = {}
+    for c in g["cases"]:
+        by_len.setdefault(len(c["words"]), []).append(c)
+    for n, cases in by_len.items():
+        if n == 0:
+            continue
+        rows = np.array([[int(x, 16) for x in c["words"]] for c in cases], dtype=np.uint64)
+        h = host(hip.hash_rows(dev(rows)))
+        assert [f"{int(x):016x}" for x in h] == [c["hash_state"] for c in cases], n
+
+
+def test_hash_rows_random_vs_oracle():
+    from mymyr_amd import hip
+    from oracle import port
+
+    rng = np.random.default_rng(1)
+    for words in (1, 3, 8, 13, 16, 176):
+        rows = rng.integers(0, 2**63, size=(257, words), dtype=np.int64).view(np.uint64)
+        rows[::4, words // 2:] = 0
+        rows[7] = 0
+        h = host(hip.hash_rows(dev(rows)))
+        assert all(int(h[i]) == port.hash_state(rows[i]) for i in range(0, 257, 16))
+
+
+def test_dedup_stream_matches_generator():
+    from mymyr_amd import gen, hip
+
+    d = host(hip.dedup_rows(1000, 3000, 16, seed=9))
+    assert np.array_equal(d, gen.dedup_rows(1000, 3000, 16, seed=9))
+
+
+def test_state_set_ids_and_unique_count():
+    from mymyr_amd import gen, hip
+    from oracle import port
+
+    rows = gen.dedup_rows(0, 20000, 16, seed=4)
+    s = hip.StateSet(40000, 16, 0.5, batch=4096)  # several batches
+    n, ids, is_new = s.insert(dev(rows))
+    exp_n, exp_ids = port.dedup_unique(rows)
+    assert n == exp_n == len(s)
+    assert np.array_equal(ids.cpu().numpy(), exp_ids)
+    first = np.zeros(len(rows), np.uint8)
+    first[np.unique(exp_ids, return_index=True)[1]] = 1
+    assert np.array_equal(is_new.cpu().numpy(), first)
+    # a second insert of the same rows adds nothing and returns the same ids
+    n2, ids2, _ = s.insert(dev(rows))
+    assert n2 == 0 and np.array_equal(ids2.cpu().numpy(), exp_ids)
+
+
+def test_state_set_dedup_closed_form_large():
+    """2^22 rows of 1024 bits in 2^20-row batches at load 0.5: the unique count is the generator's fresh-row count."""
+    from mymyr_amd import gen, hip
+
+    total, batch = 1 << 22, 1 << 20
+    s = hip.StateSet(total, 16, 0.5, batch=batch)
+    new = 0
+    for b in range(0, total, batch):
+        n, _, _ = s.insert(hip.dedup_rows(b, batch, 16, seed=0), want_ids=False)
+        new += n
+    fresh = int(gen.dedup_is_fresh(np.arange(total, dtype=np.uint64), seed=0).sum())
+    assert new == fresh == len(s)
+
+
+def test_state_set_errors():
+    from mymyr_amd import hip
+    from mymyr_amd._lib import MyaError
+
+    s = hip.StateSet(10, 4, 0.5, batch=16)
+    with pytest.raises(ValueError):
+        s.insert(torch.zeros((3, 5), dtype=torch.int64, device="cuda"))
+    with pytest.raises(MyaError, match="state set full"):
+        s.insert(torch.arange(64, dtype=torch.int64, device="cuda").view(16, 4))
+    with pytest.raises(MyaError, match="load"):
+        hip.StateSet(10, 4, 1.5)

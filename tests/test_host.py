@@ -1,0 +1,102 @@
+"""Host-side checks of the product library (no GPU needed): the C ABI loads and exports every symbol that
+include/mymyr_amd.h declares, the task compiler reproduces the reference's atom slots, host hash / Philox functions
+match the golden vectors, and argument errors surface as MyaError with the reference's messages."""
+
+import ctypes
+import hashlib
+import os
+import re
+
+import numpy as np
+import pytest
+
+from mymyr_amd import _lib, gen, workloads
+from mymyr_amd._lib import MyaError, lib
+from mymyr_amd.task import Task
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "mymyr_amd.h")).read()
+    return sorted(set(re.findall(r"\b(mya_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = declared_symbols()
+    assert len(syms) >= 25
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+    assert lib.mya_abi_version() == 1
+
+
+def test_symbols_are_plain_c():
+    # no C++ types cross the boundary: the exported names are unmangled
+    dll = ctypes.CDLL(_lib.LIB_PATH)
+    for s in declared_symbols():
+        assert getattr(dll, s) is not None
+
+
+ALL_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "driverlog__p03", "logistics00__probLOGISTICS-6-1",
+             "miconic__s7-4", "parcprinter-opt11-strips__p03", "pathways__p02", "pegsol-08-strips__p22", "rovers__p02",
+             "snake-opt18-strips__p05", "sokoban-opt08-strips__p14", "transport-opt08-strips__p23",
+             "visitall__visitall_x-6_y-3_r-100", "zenotravel__p05", "gridworld", "strips", "transport", "transport_xl"]
+
+
+@pytest.mark.parametrize("name", ALL_TASKS)
+def test_slot_tables_match_reference(golden, name):
+    slots = golden.load("slots.json")
+    for atoms in ["auto", "dense", "reachable"]:
+        t = Task.from_text_file(golden.task_path(name), atoms)
+        g = slots[f"{name}:{atoms}"]
+        assert (t.words, t.atom_mode, t.fluent_slots, t.dense_fluent) == (g["words"], g["mode"], g["slots"], g["dense_fluent"])
+        rec, cid = t.slot_records()
+        assert hashlib.sha256(cid.astype(np.uint64).tobytes()).hexdigest() == g["cid_sha"]
+        assert hashlib.sha256(rec.astype(np.uint32).tobytes()).hexdigest() == g["rec_sha"]
+        assert [f"{int(x):016x}" for x in t.initial_state()] == g["initial"]
+
+
+def test_workload_task_files_are_reproducible(golden):
+    for name in workloads.TASKS:
+        assert open(golden.task_path(name)).read() == workloads.TASKS[name](), name
+
+
+def test_host_hash_and_philox(golden):
+    g = golden.load("hash.json")
+    for c in g["cases"]:
+        w = np.array([int(x, 16) for x in c["words"]], dtype=np.uint64)
+        assert lib.mya_hash_words(w.ctypes.data, w.size, int(c["seed"], 16)) == int(c["hash_words"], 16)
+        assert lib.mya_hash_state(w.ctypes.data, w.size) == int(c["hash_state"], 16)
+    p = golden.load("philox.json")
+    out = np.zeros(4, np.uint32)
+    for d in p["draws"]:
+        lib.mya_philox(d["seed"], d["env"], d["draw"], 0, out.ctypes.data)
+        assert list(out) == d["block"]
+        assert lib.mya_successor_index(d["seed"], d["env"], d["draw"], d["count"]) == d["index"]
+
+
+def test_task_errors():
+    with pytest.raises(MyaError, match="expected"):
+        Task.from_text("O 1\nQ 0\n")
+    with pytest.raises(MyaError, match="numeric"):
+        Task.from_text("O 0\nP 0\nN 0\n")
+    with pytest.raises(MyaError, match="cannot open"):
+        Task.from_text_file("/nonexistent/task.txt")
+    with pytest.raises(MyaError, match="object out of range"):
+        Task.from_text("O 1\nP 1\nF 1 p\nSI 0\nFI 1\n0 3\nG 0\nA 0\n")
+    with pytest.raises(MyaError, match="parameters; the device path supports at most"):
+        Task.from_text("O 2\nP 1\nF 1 p\nSI 0\nFI 0\nG 0\nA 1\nbig 7\nL 0\nE 1\n0\nL 0\nF 1\n0 1 0\n")
+
+
+def test_conditional_effects_and_axioms_refused():
+    txt = "O 1\nP 1\nF 1 p\nSI 0\nFI 0\nG 0\nA 1\nx 1\nL 0\nE 1\n0\nL 1\n0 1 0\nF 1\n0 1 0\n"
+    with pytest.raises(MyaError, match="conditional effects"):
+        Task.from_text(txt)
+
+
+def test_generators_deterministic():
+    assert gen.gridworld(8, 8, 0.2, seed=1) == gen.gridworld(8, 8, 0.2, seed=1)
+    assert gen.gridworld(8, 8, 0.2, seed=1) != gen.gridworld(8, 8, 0.2, seed=2)
+    a = gen.dedup_rows(100, 50, 16, seed=3)
+    b = gen.dedup_rows(0, 150, 16, seed=3)[100:]
+    assert np.array_equal(a, b)

@@ -1,0 +1,144 @@
+"""The oracle's CPU restatement (oracle/port.py) pinned against the reference: the golden vectors the compiled
+reference wrote (tests/golden/*.json), the reference's own fixtures (Random123 vectors, determinism digests, suite
+counts) and closed forms. When oracle/_ref is built here, it is also compared directly on fresh inputs."""
+
+import numpy as np
+import pytest
+
+from mymyr_amd import gen, workloads
+from oracle import port
+
+
+def test_hash_golden(golden):
+    g = golden.load("hash.json")
+    for c in g["cases"]:
+        w = [int(x, 16) for x in c["words"]]
+        assert port.hash_words(w, int(c["seed"], 16)) == int(c["hash_words"], 16)
+        assert port.hash_state(w) == int(c["hash_state"], 16)
+    for m in g["mix64"]:
+        assert port.mix64(int(m["x"], 16)) == int(m["mix64"], 16)
+
+
+def test_hash_properties():
+    # the state hash ignores trailing zero words and separates single-bit states (tests/cpp/core/test_hash.cpp:12-75)
+    w = [0x1234, 0, 0xFFFF, 0, 0]
+    assert port.hash_state(w) == port.hash_state(w[:3])
+    assert port.hash_words(w) != port.hash_words(w[:3])
+    seen = {port.hash_state([1 << b if i == k else 0 for i in range(4)]) for k in range(4) for b in range(64)}
+    assert len(seen) == 256
+
+
+def test_philox_known_answers(golden):
+    g = golden.load("philox.json")
+    for k in g["kats"]:
+        assert port.philox4x32_10(k["ctr"], *k["key"]) == k["out"]
+    # the draw layout: counter (draw lo, draw hi, env, purpose), key (seed lo, seed hi) (test_env.cpp:190-193)
+    assert port.philox_block(0x0123456789ABCDEF, 7, 0x100000002, 0) == port.philox4x32_10([2, 1, 7, 0], 0x89ABCDEF, 0x01234567)
+    for d in g["draws"]:
+        assert port.philox_block(d["seed"], d["env"], d["draw"], 0) == d["block"]
+        assert port.successor_index(d["seed"], d["env"], d["draw"], d["count"]) == d["index"]
+
+
+def test_index_in_range():
+    for n in (1, 2, 3, 7, 1000, 0xFFFFFFFF):
+        for d in range(50):
+            assert port.successor_index(42, d % 13, d, n) < n
+
+
+SMALL_LAYOUTS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "driverlog__p03", "rovers__p02",
+                 "sokoban-opt08-strips__p14", "snake-opt18-strips__p05", "gridworld", "strips", "transport"]
+
+
+@pytest.mark.parametrize("name", SMALL_LAYOUTS)
+def test_layout_golden(golden, name):
+    import hashlib
+
+    slots = golden.load("slots.json")
+    text = open(golden.task_path(name)).read()
+    for atoms in ["auto", "dense", "reachable"]:
+        t = port.Task(text, atoms)
+        g = slots[f"{name}:{atoms}"]
+        assert t.words == g["words"] and t.mode == g["mode"] and t.slots == g["slots"], (name, atoms)
+        assert t.fluent_count == g["dense_fluent"]
+        assert hashlib.sha256(np.array(t.slot_cid, dtype=np.uint64).tobytes()).hexdigest() == g["cid_sha"]
+        assert [f"{int(x):016x}" for x in t.initial] == g["initial"]
+
+
+@pytest.mark.parametrize("name", ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "gridworld", "transport", "strips"])
+def test_successors_golden(golden, name):
+    g = golden.load("successors.json")[name]
+    t = port.Task(open(golden.task_path(name)).read(), "dense" if name == "strips" else "auto")
+    for s in g:
+        row = np.array([int(x, 16) for x in s["row"]], dtype=np.uint64)[: t.words]
+        succ = port.successors(t, row)
+        assert len(succ) == s["count"]
+        assert [x[0] for x in succ] == s["schema"]
+        assert [list(x[1]) + [-1] * (len(s["binding"][0]) - len(x[1])) for x in succ] == s["binding"] if succ else True
+        assert [f"{port.hash_state(x[2]):016x}" for x in succ] == s["succ_hash"]
+        assert port.is_goal(t, row) == s["goal"]
+
+
+def test_env_golden_small(golden):
+    """The restated HostEnv step against the reference's trajectory (first rows of the truncating gridworld)."""
+    g = golden.load("env_gridworld_small.json")
+    t = port.Task(open(golden.task_path("gridworld")).read())
+    e = port.Env(t, **g["env"])
+    b = e.reset(g["rows"])
+    for k in range(g["steps"]):
+        o = e.step(b)
+        assert golden.step_digest(g["rows"], b["states"], o["reward"], o["terminated"], o["truncated"], o["count"],
+                                  o["schema"], o["binding"], o["goal"]) == g["digests"][k], k
+
+
+def test_brfs_determinism_digests(golden):
+    """The reference's own determinism fixture (tests/data/determinism.json) for two suite tasks."""
+    for name in ["gripper__prob05", "depot__p02"]:
+        t = port.Task(open(golden.task_path(name)).read())
+        r = port.brfs(t, max_states=20000, stop_at_goal=False)
+        d = golden.determinism_digest(r["states"], r["expanded"], r["generated"], r["layers"], r["fingerprint"])
+        assert d == golden.DETERMINISM_BRFS[name], name
+
+
+def test_brfs_golden_budget(golden):
+    g = golden.load("brfs.json")["budget"]
+    for name in ["depot__p02", "miconic__s7-4"]:
+        t = port.Task(open(golden.task_path(name)).read())
+        r = port.brfs(t, max_states=20000, stop_at_goal=False)
+        exp = g[name]
+        for k in ["states", "expanded", "generated", "goal_states", "layers", "fingerprint", "status", "layer_counts"]:
+            assert r[k] == exp[k], (name, k)
+
+
+def test_dedup_closed_form():
+    rows = gen.dedup_rows(0, 4000, 16, seed=5)
+    n, ids = port.dedup_unique(rows)
+    assert n == int(gen.dedup_is_fresh(np.arange(4000, dtype=np.uint64), seed=5).sum())
+    # an exact duplicate maps to the id of its source's first occurrence
+    assert all(ids[i] <= i for i in range(len(ids)))
+
+
+def test_encode_closed_form():
+    t = port.Task(workloads.TASKS["transport"]())
+    row = t.initial
+    idx = port.encode_atoms(row, 200)
+    ones = [s for s in range(t.slots) if (int(row[s >> 6]) >> (s & 63)) & 1]
+    assert list(idx[: len(ones)]) == ones and (idx[len(ones):] == -1).all()
+    m = port.schema_masks(t, row)
+    assert list(m) == [1 if any(x[0] == s for x in port.successors(t, row)) else 0 for s in range(len(t.schemas))]
+
+
+ref = pytest.importorskip("oracle.ref")
+
+
+@pytest.mark.skipif(not ref.available(), reason="oracle/_ref not built (make -C oracle)")
+def test_port_against_reference_random_rows():
+    rng = np.random.default_rng(99)
+    for n in range(0, 40):
+        w = rng.integers(0, 2**63, size=n, dtype=np.int64).view(np.uint64)
+        if n > 3:
+            w[-2:] = 0
+        assert port.hash_state(w) == ref.hash_state(w)
+        assert port.hash_words(w) == ref.hash_words(w)
+    for _ in range(200):
+        s, e, d, c = (int(x) for x in rng.integers(1, 2**31, size=4))
+        assert port.successor_index(s, e, d, c) == ref.successor_index(s, e, d, c)
