@@ -1,0 +1,250 @@
+"""Benchmark of the state-expansion path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only strips,gridworld,...] [--no-cpu]
+
+Prints ONE JSON line. The headline (`value`) is the strips workload: BrFS expanded states per second of a random
+ground STRIPS task (512 fluents, 4096 actions) from its initial state, depth bound 12, stopped by max_states = 2^26
+(the frontier grows ~40x per layer, so the depth bound is never reached; the stop is the reference's own max_states
+rule). One step = one whole BrFS. The other workloads (gridworld / transport / transport_xl env pools, dedup) are
+reported under "workloads", each with env-steps/s (or rows/s) and the achieved HBM bandwidth of its dominant kernel.
+
+roofline: the dominant kernel class of the BrFS (by summed HIP-event time on the search's own stream): its
+algorithmic bytes (per launch, summed) / its summed duration, against the 8 TB/s HBM peak of MI355X.
+cpu_baseline: the reference's own CPU BrFS (oracle/_ref: ParallelBrfs with deterministic ids) on a bounded sample of
+the same task, timed on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "env steps/sec + BrFS expanded states/sec on 1 GPU; % of HBM roofline"
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch measured by rocprofv3 PMC counters (profiles/pmc_<kernel>.json), if committed."""
+    p = os.path.join(ROOT, "profiles", f"pmc_{kernel}.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
+def bench_strips(steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from mymyr_amd import search, workloads
+    from mymyr_amd.task import Task
+
+    w = workloads.STRIPS
+    path = workloads.task_file("strips", os.path.join(ROOT, "tests", "golden", "tasks"))
+    t = Task.from_text_file(path, w.atoms)
+    kw = dict(max_depth=w.max_depth, max_states=w.max_states, stop_at_goal=False)
+    for _ in range(warmup):
+        search.brfs(t, **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    results = [search.brfs(t, timings=True, **kw) for _ in range(steps)]
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    r = results[0]
+    expanded = sum(x.expanded for x in results)
+    value = expanded / wall
+    # the dominant kernel class over the timed region
+    classes = ["count", "generate", "probe", "rank", "compact"]
+    ms = {c: sum(x.kernels[c]["ms"] for x in results) for c in classes}
+    by = {c: sum(x.kernels[c]["bytes"] for x in results) for c in classes}
+    launches = {c: sum(x.kernels[c]["launches"] for x in results) for c in classes}
+    dom = max(classes, key=lambda c: ms[c])
+    achieved = by[dom] / (ms[dom] * 1e-3) / 1e9 if ms[dom] > 0 else 0.0
+    traffic = load_traffic(f"brfs_{dom}")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": f"brfs {dom}",
+                "bytes_per_launch": int(by[dom] / max(1, launches[dom])), "ms_per_launch": round(ms[dom] / max(1, launches[dom]), 4)}
+    out = {
+        "value": value, "unit": "expanded states/s", "ms_per_step": wall * 1e3 / steps, "roofline": roofline,
+        "detail": {"states": r.states, "expanded": r.expanded, "generated": r.generated, "layers": r.layers, "status": r.status,
+                   "layer_counts": r.layer_counts, "generated_per_s": sum(x.generated for x in results) / wall,
+                   "kernel_ms_per_step": {c: round(ms[c] / steps, 3) for c in classes},
+                   "kernel_gbs": {c: round(by[c] / (ms[c] * 1e-3) / 1e9, 1) if ms[c] else None for c in classes},
+                   "whole_search_gbs": round(sum(by.values()) / wall / 1e9, 1)},
+    }
+    if cpu:
+        out["cpu_baseline"] = cpu_strips(path, w)
+    return out
+
+
+def cpu_strips(path, w):
+    from oracle import ref
+
+    if not ref.available():
+        return None
+    T = cpu_threads()
+    rt = ref.RefTask(path, w.atoms)
+    sample = 1 << 22
+    r = ref.brfs(rt, threads=T, max_depth=w.max_depth, max_states=sample, stop_at_goal=False, fingerprint=False)
+    return {"value": r["expanded"] / r["seconds"], "unit": "expanded states/s", "cores": T, "kind": "reference",
+            "sample": f"reference ParallelBrfs (deterministic ids) on the strips task, depth 12, max_states 2^22: "
+                      f"{r['expanded']} expanded, {r['generated']} generated in {r['seconds']:.2f} s"}
+
+
+def bench_env(name: str, steps: int, warmup: int, cpu: bool, num_envs: int | None = None):
+    import torch
+
+    from mymyr_amd import rl, workloads
+    from mymyr_amd.task import Task
+
+    w = {"gridworld": workloads.GRIDWORLD, "transport": workloads.TRANSPORT, "transport_xl": workloads.TRANSPORT_XL}[name]
+    path = workloads.task_file(name, os.path.join(ROOT, "tests", "golden", "tasks"))
+    t = Task.from_text_file(path, w.atoms)
+    N = num_envs or w.num_envs
+    encode = 600 if w.encode else 0
+    pool = rl.DeviceEnvPool(t, N, **w.env)
+    pool.reset()
+    for _ in range(warmup):
+        pool.step(encode=encode, labels=False)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record()
+        pool.step(encode=encode, labels=False)
+        b.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    pool.check()
+    kms = sum(a.elapsed_time(b) for a, b in evs) / steps
+    R = t.words * 8
+    per_step = 2 * R + 36 + (encode * 4 + t.num_schemas if encode else 0)
+    achieved = per_step * N / (kms * 1e-3) / 1e9
+    out = {"env_steps_per_s": N * steps / wall, "num_envs": N, "steps_timed": steps, "ms_per_step": wall * 1e3 / steps,
+           "words": t.words, "bytes_per_env_step": per_step,
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "env step", "ms_per_launch": round(kms, 4),
+                        "traffic": load_traffic(f"env_{name}")}}
+    if cpu:
+        out["cpu_baseline"] = cpu_env(path, w)
+    return out
+
+
+def cpu_env(path, w):
+    from oracle import ref
+
+    if not ref.available():
+        return None
+    T = cpu_threads()
+    rt = ref.RefTask(path, w.atoms)
+    n, k = {"gridworld": (1024, 256), "transport": (16384, 16), "transport_xl": (4096, 4)}[w.name]
+    secs, _ = ref.pool_run(rt, n, T, k, **w.env)
+    return {"value": n * k / secs, "unit": "env steps/s", "cores": T, "kind": "reference",
+            "sample": f"reference CpuEnvPool, {n} envs x {k} steps, {T} worker threads"}
+
+
+def bench_dedup(steps: int, warmup: int, cpu: bool):
+    import torch
+
+    from mymyr_amd import gen, hip, workloads
+
+    total, batch, words = workloads.DEDUP_ROWS, workloads.DEDUP_BATCH, workloads.DEDUP_WORDS
+    rows = hip.dedup_rows(0, total, words, seed=workloads.SEED, dup=workloads.DEDUP_DUP)
+    times = []
+    unique = 0
+    for it in range(warmup + steps):
+        s = hip.StateSet(total, words, 0.5, batch=batch)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        unique = 0
+        for b in range(0, total, batch):
+            n, _, _ = s.insert(rows[b: b + batch], want_ids=False)
+            unique += n
+        torch.cuda.synchronize()
+        if it >= warmup:
+            times.append(time.perf_counter() - t0)
+        del s
+    wall = sum(times) / len(times)
+    R = words * 8
+    alg = total * (R + 8) + unique * (R + 8) + (total - unique) * R
+    out = {"rows_per_s": total / wall, "unique": unique, "rows": total, "ms_per_step": wall * 1e3,
+           "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4), "kernel": "state-set insert pipeline (hash, probe, rank, compact)",
+                        "traffic": load_traffic("state_set_probe")}}
+    if cpu:
+        from oracle import port
+
+        sample = 1 << 16
+        r = gen.dedup_rows(0, sample, words, seed=workloads.SEED, dup=workloads.DEDUP_DUP)
+        t0 = time.perf_counter()
+        port.dedup_unique(r)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": sample / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+                               "sample": f"oracle restatement (dict-based first-occurrence ids), {sample} rows"}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--only", default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the env pool shards by env range and the "
+              f"BrFS by state-hash owner, but no multi-GPU path is built", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    only = set(x for x in a.only.split(",") if x)
+    cpu = not a.no_cpu
+    steps, warmup = max(1, a.steps), max(0, a.warmup)
+    head = bench_strips(steps, warmup, cpu) if (not only or "strips" in only) else None
+    wl = {}
+    if not only or "gridworld" in only:
+        wl["gridworld"] = bench_env("gridworld", 256, 16, cpu)
+    if not only or "transport" in only:
+        wl["transport"] = bench_env("transport", 32, 4, cpu)
+    if not only or "transport_xl" in only:
+        wl["transport_xl"] = bench_env("transport_xl", 4, 1, cpu)
+    if not only or "dedup" in only:
+        wl["dedup"] = bench_dedup(steps, min(warmup, 1), cpu)
+    line = {
+        "metric": METRIC,
+        "value": head["value"] if head else None,
+        "unit": head["unit"] if head else "expanded states/s",
+        "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": head["ms_per_step"] if head else None,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+        "config": {"workload": "strips: random ground STRIPS (512 fluents, 4096 actions, seed 0), BrFS from the initial "
+                               "state, max_depth 12, max_states 2^26, witness pruning on, dense atoms",
+                   "parallelism": "single GPU"},
+        "roofline": head["roofline"] if head else None,
+        "cpu_baseline": head.get("cpu_baseline") if head else None,
+        "detail": head["detail"] if head else None,
+        "workloads": wl,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -215,6 +215,8 @@ typedef struct mya_brfs_options
     int32_t fingerprint;     /* compute BrfsResult::fingerprint */
     uint64_t chunk;          /* candidates per device batch (0: automatic) */
     uint64_t memory_states;  /* state capacity when max_states is unbounded (0: 2^26) */
+    int32_t timings;         /* time each kernel class with HIP events (mya_brfs_result.kernel_ms) */
+    int32_t reserved;
 } mya_brfs_options;
 
 /* BrfsResult fields (include/mymyr/search/brfs.hpp:103-138). status: the reference's SearchStatus codes
@@ -233,6 +235,11 @@ typedef struct mya_brfs_result
     int64_t first_goal; /* id of the first goal state tested (-1: none) */
     double search_s;    /* wall time of the whole call */
     double device_s;    /* wall time from the start state's insert to the end of the search */
+    /* per kernel class (0 count, 1 generate, 2 probe, 3 rank, 4 compact, 5 other): summed HIP-event durations (with
+     * options.timings), algorithmic bytes and launches */
+    double kernel_ms[6];
+    uint64_t kernel_bytes[6];
+    uint64_t kernel_launches[6];
 } mya_brfs_result;
 
 /* Layer-synchronous BrFS on the current device (replaces brfs(), include/mymyr/search/brfs.hpp:140, and

@@ -94,6 +94,8 @@ class BrfsOptions(Structure):
         ("fingerprint", c_int32),
         ("chunk", c_uint64),
         ("memory_states", c_uint64),
+        ("timings", c_int32),
+        ("reserved", c_int32),
     ]
 
 
@@ -111,6 +113,9 @@ class BrfsResult(Structure):
         ("first_goal", c_int64),
         ("search_s", c_double),
         ("device_s", c_double),
+        ("kernel_ms", c_double * 6),
+        ("kernel_bytes", c_uint64 * 6),
+        ("kernel_launches", c_uint64 * 6),
     ]
 
 

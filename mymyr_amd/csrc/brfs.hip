@@ -271,6 +271,64 @@ struct Buffers
 
 using Clock = std::chrono::steady_clock;
 
+/// HIP-event timing of kernel classes on one stream; durations are read once the stream has drained.
+class Timers
+{
+public:
+    Timers(bool on, hipStream_t s, BrfsResultC& r) : m_on(on), m_s(s), m_r(r) {}
+    ~Timers()
+    {
+        for (auto& e : m_ev)
+        {
+            (void)hipEventDestroy(e.a);
+            (void)hipEventDestroy(e.b);
+        }
+    }
+    void begin(int k)
+    {
+        if (!m_on)
+            return;
+        Pair p{k, nullptr, nullptr};
+        hip_check(hipEventCreate(&p.a), "event");
+        hip_check(hipEventCreate(&p.b), "event");
+        hip_check(hipEventRecord(p.a, m_s), "event");
+        m_ev.push_back(p);
+    }
+    void end(int k, u64 bytes)
+    {
+        m_r.kernel_bytes[k] += bytes;
+        m_r.kernel_launches[k] += 1;
+        if (!m_on)
+            return;
+        hip_check(hipEventRecord(m_ev.back().b, m_s), "event");
+    }
+    void bytes(int k, u64 b) { m_r.kernel_bytes[k] += b; }
+    /// Adds the durations of the recorded pairs (the stream must have drained).
+    void collect()
+    {
+        for (auto& e : m_ev)
+        {
+            float ms = 0;
+            hip_check(hipEventElapsedTime(&ms, e.a, e.b), "event time");
+            m_r.kernel_ms[e.k] += ms;
+            (void)hipEventDestroy(e.a);
+            (void)hipEventDestroy(e.b);
+        }
+        m_ev.clear();
+    }
+
+private:
+    struct Pair
+    {
+        int k;
+        hipEvent_t a, b;
+    };
+    bool m_on;
+    hipStream_t m_s;
+    BrfsResultC& m_r;
+    std::vector<Pair> m_ev;
+};
+
 template<int W>
 BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc)
 {
@@ -283,6 +341,8 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         hipStream_t s;
         ~StreamGuard() { (void)hipStreamDestroy(s); }
     } sg{stream};
+    Timers tm(o.timings != 0, stream, r);
+    constexpr u64 R = W * 8;  // row bytes
 
     // ground table and goal
     u32* d_meta = dev_alloc<u32>(ga.meta.size(), "ground meta");
@@ -389,10 +449,14 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         std::array<u64, 3> row{0, 0, 0};
         const u64 size0 = set.size;
         // counts and goal flags of the whole layer
+        tm.begin(kKCount);
         hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(ln, kGB)), dim3(kGB), 0, stream, set.v.arena, layer_begin,
                            static_cast<u32>(ln), g, goal, b.counts, b.goal);
         launch_check("ground count");
+        tm.end(kKCount, ln * (R + 5));
+        tm.begin(kKOther);
         launch_exclusive_scan(b.counts, b.offsets, ln, b.scan_scratch, b.small + 0, stream);
+        tm.end(kKOther, 0);
         // offsets[ln] = total (for chunk searches)
         hip_check(hipMemcpyAsync(b.offsets + ln, b.small + 0, sizeof(u64), hipMemcpyDeviceToDevice, stream), "total");
         // the parents this layer expands: up to the first goal (stop_at_goal) and the expansion budget
@@ -430,17 +494,24 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             hip_check(hipStreamSynchronize(stream), "sync");
             const u64 m = b.host[4] - base;
             const u32 np = static_cast<u32>(p1 - p0);
+            tm.begin(kKGenerate);
             hipLaunchKernelGGL(k_ground_generate<W>, dim3(blocks_for(np, kGB)), dim3(kGB), 0, stream, set.v.arena, layer_begin + p0, np,
                                g, b.offsets + p0, base, b.cand, b.cand_hash, b.cand_parent, b.cand_action);
             launch_check("ground generate");
+            tm.end(kKGenerate, np * (R + 8) + m * (R + 16));
+            tm.begin(kKProbe);
             state_set_probe(set, b.cand, b.cand_hash, m, stream);
+            tm.end(kKProbe, m * (R + 24));
+            tm.begin(kKRank);
             state_set_rank(set, m, stream);
+            tm.end(kKRank, m * 32);
             hip_check(hipMemcpyAsync(b.host + 5, set.d_total, sizeof(u64), hipMemcpyDeviceToHost, stream), "new");
             hip_check(hipMemcpyAsync(b.host + 6, set.d_status, sizeof(u32), hipMemcpyDeviceToHost, stream), "status");
             hip_check(hipStreamSynchronize(stream), "sync");
             if (static_cast<u32>(b.host[6]) & kStatusTableFull)
                 throw std::length_error("mymyr_amd: brfs: state table full");
             const u64 fresh = b.host[5];
+            tm.bytes(kKProbe, (m - fresh) * R);  // a duplicate compares its row with the stored one
             const u64 room = (bounded ? o.max_states : cap_states) - set.size;
             if (fresh >= room && fresh > 0 && bounded)
             {
@@ -451,7 +522,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 hip_check(hipMemcpyAsync(b.host + 3, b.cand_parent + jcut, sizeof(u32), hipMemcpyDeviceToHost, stream), "parent");
                 hip_check(hipStreamSynchronize(stream), "sync");
                 const u64 pcut = static_cast<u32>(b.host[3]) - layer_begin;  // index in the layer
+                tm.begin(kKCompact);
                 state_set_compact(set, b.cand, b.cand_hash, m, set.size, o.max_states, nullptr, nullptr, stream);
+                tm.end(kKCompact, m * 12 + room * (2 * R + 24));
                 row[0] += pcut - p0 + 1;
                 row[1] += jcut + 1;
                 set_small(0, 0);
@@ -466,7 +539,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             if (fresh > room)
                 throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
                                         " states of device memory (set max_states or memory_states)");
+            tm.begin(kKCompact);
             state_set_compact(set, b.cand, b.cand_hash, m, set.size, cap_states, nullptr, nullptr, stream);
+            tm.end(kKCompact, m * 12 + fresh * (2 * R + 24));
             set.size += fresh;
             row[0] += np;
             row[1] += m;
@@ -507,6 +582,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         r.status = kSolved;
     else if (!budget_stopped)
         r.status = (r.exhausted || r.layers >= o.max_depth) ? kExhausted : kOutOfStates;
+    hip_check(hipStreamSynchronize(stream), "brfs");
+    r.device_s = std::chrono::duration<double>(Clock::now() - td0).count();
+    tm.collect();
     if (o.fingerprint)
     {
         set_small(0, 0);
@@ -515,8 +593,6 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         launch_check("fingerprint");
         r.fingerprint = read_small(0);
     }
-    hip_check(hipStreamSynchronize(stream), "brfs");
-    r.device_s = std::chrono::duration<double>(Clock::now() - td0).count();
     r.search_s = std::chrono::duration<double>(Clock::now() - t0).count();
     return r;
 }

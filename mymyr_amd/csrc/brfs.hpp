@@ -24,6 +24,19 @@ struct BrfsOptionsC
     i32 fingerprint = 0;
     u64 chunk = 0;          // candidates per device batch (0: automatic)
     u64 memory_states = 0;  // arena capacity when max_states is unbounded (0: automatic)
+    i32 timings = 0;        // time every kernel class with HIP events on the search's stream
+};
+
+/// Kernel classes of the device BrFS (timed with HIP events when BrfsOptionsC::timings is set).
+enum BrfsKernel : int
+{
+    kKCount = 0,     // applicability counts and goal flags of a layer's parents
+    kKGenerate = 1,  // successor rows, hashes and (parent, action) records
+    kKProbe = 2,     // state-set probe with the min-candidate winner
+    kKRank = 3,      // winner flags and their exclusive scan
+    kKCompact = 4,   // new states into the arena and the table
+    kKOther = 5,     // scans of counts, goal searches, chunk bounds, fingerprint
+    kKClasses = 6,
 };
 
 struct BrfsResultC
@@ -36,6 +49,9 @@ struct BrfsResultC
     i64 first_goal = -1;
     double search_s = 0;
     double device_s = 0;
+    double kernel_ms[kKClasses] = {};
+    u64 kernel_bytes[kKClasses] = {};  // algorithmic bytes (see DevBytes in brfs.hip)
+    u64 kernel_launches[kKClasses] = {};
 };
 
 enum SearchStatus : i32

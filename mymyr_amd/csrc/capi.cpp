@@ -279,6 +279,7 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         o.fingerprint = options->fingerprint;
         o.chunk = options->chunk;
         o.memory_states = options->memory_states;
+        o.timings = options->timings;
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
         if (o.stop_at_goal && task->compiled->goal_unsat)
@@ -302,6 +303,12 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         result->first_goal = r.first_goal;
         result->search_s = r.search_s;
         result->device_s = r.device_s;
+        for (int k = 0; k < kKClasses; ++k)
+        {
+            result->kernel_ms[k] = r.kernel_ms[k];
+            result->kernel_bytes[k] = r.kernel_bytes[k];
+            result->kernel_launches[k] = r.kernel_launches[k];
+        }
         if (layer_counts)
             for (size_t i = 0; i < lc.size() && i < cap; ++i)
                 for (int j = 0; j < 3; ++j)

@@ -35,21 +35,27 @@ class BrfsResult:
     search_s: float
     device_s: float
     layer_counts: list = field(default_factory=list)
+    kernels: dict = field(default_factory=dict)  # class -> {"ms", "bytes", "launches"} (ms with timings=True)
+
+
+KERNEL_CLASSES = ["count", "generate", "probe", "rank", "compact", "other"]
 
 
 def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None, max_expanded: int | None = None,
          witness_pruning: bool = True, stop_at_goal: bool = True, fingerprint: bool = False, layer_stats: bool = True,
-         chunk: int = 0, memory_states: int = 0) -> BrfsResult:
+         chunk: int = 0, memory_states: int = 0, timings: bool = False) -> BrfsResult:
     """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
     (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer."""
     o = _lib.BrfsOptions(UNBOUNDED32 if max_depth is None else max_depth, int(witness_pruning),
                          UNBOUNDED64 if max_states is None else max_states, UNBOUNDED64 if max_expanded is None else max_expanded,
-                         int(stop_at_goal), int(fingerprint), chunk, memory_states)
+                         int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096)
     if n < 0:
         check(-1)
+    kernels = {c: {"ms": r.kernel_ms[i], "bytes": r.kernel_bytes[i], "launches": r.kernel_launches[i]}
+               for i, c in enumerate(KERNEL_CLASSES)}
     return BrfsResult(STATUS.get(r.status, str(r.status)), r.states, r.expanded, r.generated, r.goal_states, r.layers,
                       bool(r.exhausted), bool(r.solved), r.fingerprint, r.first_goal, r.search_s, r.device_s,
-                      lc[:n].tolist() if layer_stats else [])
+                      lc[:n].tolist() if layer_stats else [], kernels)
