@@ -67,7 +67,7 @@ def bench_strips(steps: int, warmup: int, cpu: bool):
     expanded = sum(x.expanded for x in results)
     value = expanded / wall
     # the dominant kernel class over the timed region
-    classes = ["count", "generate", "probe", "rank", "compact"]
+    classes = ["count", "emit", "lookup", "probe", "rank", "compact", "other"]
     ms = {c: sum(x.kernels[c]["ms"] for x in results) for c in classes}
     by = {c: sum(x.kernels[c]["bytes"] for x in results) for c in classes}
     launches = {c: sum(x.kernels[c]["launches"] for x in results) for c in classes}
@@ -197,6 +197,26 @@ def bench_dedup(steps: int, warmup: int, cpu: bool):
     return out
 
 
+def copy_calibration(steps: int):
+    """A plain device copy of a known size (1 GiB read, 1 GiB written per launch): the PMC counters FETCH_SIZE and
+    WRITE_SIZE read on it give the scale factor between counter units and bytes."""
+    import torch
+
+    n = 1 << 28
+    x = torch.ones(n, dtype=torch.int32, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        y.copy_(x)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "ms_per_launch": ms,
+                      "gbs": 2 * n * 4 / (ms * 1e-3) / 1e9}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,6 +224,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 1 GiB device copy (the reference kernel for scaling PMC byte counters)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the env pool shards by env range and the "
@@ -215,6 +237,9 @@ def main():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if a.copy_calibration:
+        copy_calibration(max(1, a.steps))
+        return
     only = set(x for x in a.only.split(",") if x)
     cpu = not a.no_cpu
     steps, warmup = max(1, a.steps), max(0, a.warmup)

@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 1
+#define MYA_ABI_VERSION 2
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -235,11 +235,11 @@ typedef struct mya_brfs_result
     int64_t first_goal; /* id of the first goal state tested (-1: none) */
     double search_s;    /* wall time of the whole call */
     double device_s;    /* wall time from the start state's insert to the end of the search */
-    /* per kernel class (0 count, 1 generate, 2 probe, 3 rank, 4 compact, 5 other): summed HIP-event durations (with
-     * options.timings), algorithmic bytes and launches */
-    double kernel_ms[6];
-    uint64_t kernel_bytes[6];
-    uint64_t kernel_launches[6];
+    /* per kernel class (0 count, 1 emit, 2 lookup, 3 probe, 4 rank, 5 compact, 6 other, 7 unused): summed HIP-event
+     * durations (with options.timings), algorithmic bytes and launches */
+    double kernel_ms[8];
+    uint64_t kernel_bytes[8];
+    uint64_t kernel_launches[8];
 } mya_brfs_result;
 
 /* Layer-synchronous BrFS on the current device (replaces brfs(), include/mymyr/search/brfs.hpp:140, and

@@ -12,6 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
+ABI_VERSION = 2  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -113,9 +114,9 @@ class BrfsResult(Structure):
         ("first_goal", c_int64),
         ("search_s", c_double),
         ("device_s", c_double),
-        ("kernel_ms", c_double * 6),
-        ("kernel_bytes", c_uint64 * 6),
-        ("kernel_launches", c_uint64 * 6),
+        ("kernel_ms", c_double * 8),
+        ("kernel_bytes", c_uint64 * 8),
+        ("kernel_launches", c_uint64 * 8),
     ]
 
 
@@ -123,6 +124,10 @@ def _load() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"mymyr_amd: {LIB_PATH} is not built (run `make -C mymyr_amd` or __graft_entry__.build())")
     lib = ctypes.CDLL(LIB_PATH)
+    lib.mya_abi_version.restype = c_int
+    if lib.mya_abi_version() != ABI_VERSION:
+        raise ImportError(f"mymyr_amd: {LIB_PATH} has ABI version {lib.mya_abi_version()}, this binding expects {ABI_VERSION} "
+                          f"(rebuild with `make -C mymyr_amd`)")
     sigs = {
         "mya_last_error": (c_char_p, []),
         "mya_abi_version": (c_int, []),

@@ -1,7 +1,19 @@
-// Device BrFS over ground actions (brfs.hpp). One thread per parent state: the parent row sits in LDS (transposed,
-// conflict-free per lane) and in registers; the action loop is wave-uniform, so action records come through scalar
-// loads. Per layer chunk: count -> exclusive scan -> generate (rows, hashes, parent, action) -> probe -> rank ->
-// compact, all on one stream; the host reads a handful of counters per chunk.
+// Device BrFS over ground actions (brfs.hpp).
+//
+// A layer's parents are expanded in chunks whose successors fit the candidate buffers. Per chunk, on one stream:
+//   count   (thread per parent)     applicable-action counts and goal flags, for blocks of parents counted just ahead of
+//                                   the expansion; a piecewise exclusive scan gives layer-relative successor offsets
+//   emit    (thread per parent)     each parent's successors in action order as (parent, action) records at its
+//                                   offsets: candidate index = order of first discovery (parent id, successor index)
+//   lookup  (thread per candidate)  successor row = parent row with the action's delete and add masks, its state hash,
+//                                   and a read-only probe of the stored states: a successor already stored is dropped
+//                                   here, the others (fresh) keep their row and hash at their candidate index
+//   probe / rank / compact          the state set's batch insert of the fresh candidates (the smallest candidate index
+//                                   wins among equal rows; new ids follow candidate order)
+// The applicability test reads the parent from LDS byte planes (plane b holds byte b of every thread's row, so a
+// wave reads 64 consecutive bytes per test) and the action records through scalar loads, eight actions at a time:
+// an action with at most four positive preconditions, no negative one and no witness dominators is a single record
+// of four precondition slots; the others take a general path over their slot lists.
 
 #include "brfs.hpp"
 #include "runtime.hpp"
@@ -16,16 +28,23 @@ namespace mya
 {
 namespace
 {
-constexpr int kGB = 128;  // threads per block of the ground kernels
+constexpr int kPB = 64;       // parents per block of the per-parent kernels (one lane each)
+constexpr int kMaxSlices = 8; // waves per block of the per-parent kernels: wave s scans action slice s
+constexpr int kLB = 256;      // threads per block of the per-candidate kernels
+constexpr u64 kGeneral = 0x8000;  // fast-record flag: the action takes the general test
 
 struct GroundDev
 {
-    const u32* meta;
-    const u32* off;
-    const u32* slots;
+    const u64* fast;     // [num_padded] four u16 precondition slots per action (kGeneral in the first)
+    const u32* meta;     // npos | nneg << 8 | nadd << 16 | ndel << 24
+    const u32* off;      // into slots
+    const u32* slots;    // pos..., neg..., add..., del...
     const u32* dom_off;  // witness pruning: dominators of each action (null: none)
     const u32* dom;
     u32 num;
+    u32 num_padded;      // a multiple of 8; the padding records never apply
+    u32 slices;          // action slices per parent (waves per block)
+    u32 slice_len;       // actions per slice, a multiple of 8
 };
 
 struct GoalDev
@@ -36,64 +55,141 @@ struct GoalDev
     u32 unsat;
 };
 
+/// Byte planes of one row per thread: plane b (b < 8W) holds byte b of the thread's row, plane 8W is all ones and
+/// plane 8W + 1 all zeros (the always-true and never-true slots 64W and 64W + 8).
 template<int W>
-__device__ __forceinline__ bool lds_bit(const u64 (*st)[kGB], u32 slot)
+struct Planes
 {
-    return (st[slot >> 6][threadIdx.x] >> (slot & 63)) & 1;
-}
+    static constexpr u32 kCount = W * 8 + 2;
+    static constexpr u32 kOneSlot = W * 64;
+    static constexpr u32 kZeroSlot = W * 64 + 8;
+};
 
 template<int W>
-__device__ __forceinline__ bool applicable(const u64 (*st)[kGB], const u32* __restrict__ slots, u32 m, u32 o)
+__device__ __forceinline__ void load_planes(u8* planes, const u64* row, bool valid)
+{
+    const u32 t = threadIdx.x & (kPB - 1);
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+    {
+        const u64 x = valid ? row[w] : 0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            planes[(w * 8 + b) * kPB + t] = static_cast<u8>(x >> (8 * b));
+    }
+    planes[(W * 8) * kPB + t] = 0xFF;
+    planes[(W * 8 + 1) * kPB + t] = 0;
+}
+
+/// Bit s of the row of the block's parent in this lane.
+__device__ __forceinline__ u32 pbit(const u8* planes, u32 s)
+{
+    return (planes[(s >> 3) * kPB + (threadIdx.x & (kPB - 1))] >> (s & 7)) & 1u;
+}
+
+__device__ __forceinline__ bool applicable(const u8* planes, const u32* __restrict__ slots, u32 m, u32 o)
 {
     const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF;
     for (u32 i = 0; i < npos; ++i)
-        if (!lds_bit<W>(st, slots[o + i]))
+        if (!pbit(planes, slots[o + i]))
             return false;
     for (u32 i = 0; i < nneg; ++i)
-        if (lds_bit<W>(st, slots[o + npos + i]))
+        if (pbit(planes, slots[o + npos + i]))
             return false;
     return true;
 }
 
-/// Whether action a is a successor: applicable, and (witness pruning) no dominator is.
-template<int W>
-__device__ __forceinline__ bool emitted(const u64 (*st)[kGB], const GroundDev& g, u32 a, u32 m, u32 o)
+/// The general test: applicable, and (witness pruning) no dominator is.
+__device__ __noinline__ bool general_emitted(const u8* planes, const GroundDev& g, u32 a)
 {
-    if (!applicable<W>(st, g.slots, m, o))
+    if (!applicable(planes, g.slots, g.meta[a], g.off[a]))
         return false;
     if (g.dom_off)
         for (u32 k = g.dom_off[a], e = g.dom_off[a + 1]; k < e; ++k)
         {
             const u32 d = g.dom[k];
-            if (applicable<W>(st, g.slots, g.meta[d], g.off[d]))
+            if (applicable(planes, g.slots, g.meta[d], g.off[d]))
                 return false;
         }
     return true;
 }
 
-template<int W>
-__global__ __launch_bounds__(kGB) void k_ground_count(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g, GoalDev goal,
-                                                     u32* __restrict__ counts, u8* __restrict__ goal_flags)
+/// Whether action a (record rec, wave-uniform) is a successor of the thread's row.
+__device__ __forceinline__ u32 action_ok(const u8* planes, const GroundDev& g, u64 rec, u32 a)
 {
-    __shared__ u64 st[W][kGB];
-    const u32 t = blockIdx.x * kGB + threadIdx.x;
+    if (rec & kGeneral)
+        return general_emitted(planes, g, a) ? 1u : 0u;
+    const u32 s0 = static_cast<u32>(rec & 0x7FFF), s1 = static_cast<u32>((rec >> 16) & 0xFFFF);
+    const u32 s2 = static_cast<u32>((rec >> 32) & 0xFFFF), s3 = static_cast<u32>(rec >> 48);
+    return pbit(planes, s0) & pbit(planes, s1) & pbit(planes, s2) & pbit(planes, s3);
+}
+
+// Counts of the parents [first, first + n): a block holds 64 parents (one per lane) and `slices` waves; wave s counts the
+// successors among actions [s * slice_len, (s + 1) * slice_len) into counts[t * slices + s]; wave 0 writes the goal flag.
+template<int W>
+__global__ __launch_bounds__(kPB * kMaxSlices) void k_ground_count(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
+                                                                  GoalDev goal, u32* __restrict__ counts, u8* __restrict__ goal_flags)
+{
+    __shared__ u8 planes[Planes<W>::kCount * kPB];
+    const u32 lane = threadIdx.x & (kPB - 1), s = threadIdx.x / kPB;
+    const u32 t = blockIdx.x * kPB + lane;
     const bool valid = t < n;
-    const u64* row = arena + (first + t) * W;
-#pragma unroll
-    for (int w = 0; w < W; ++w)
-        st[w][threadIdx.x] = valid ? row[w] : 0;
-    bool gl = !goal.unsat;
-    for (u32 i = 0; i < goal.npos; ++i)
-        gl = gl && lds_bit<W>(st, goal.pos[i]);
-    for (u32 i = 0; i < goal.nneg; ++i)
-        gl = gl && !lds_bit<W>(st, goal.neg[i]);
-    u32 cnt = 0;
-    for (u32 a = 0; a < g.num; ++a)
-        cnt += emitted<W>(st, g, a, g.meta[a], g.off[a]) ? 1u : 0u;
-    if (valid)
+    if (s == 0)
+        load_planes<W>(planes, arena + (first + t) * W, valid);
+    __syncthreads();
+    if (s == 0)
     {
-        counts[t] = cnt;
-        goal_flags[t] = gl ? 1 : 0;
+        bool gl = !goal.unsat;
+        for (u32 i = 0; i < goal.npos; ++i)
+            gl = gl && pbit(planes, goal.pos[i]);
+        for (u32 i = 0; i < goal.nneg; ++i)
+            gl = gl && !pbit(planes, goal.neg[i]);
+        if (valid)
+            goal_flags[t] = gl ? 1 : 0;
+    }
+    const u32 a0 = min(s * g.slice_len, g.num_padded), a1 = min(a0 + g.slice_len, g.num_padded);
+    u32 cnt = 0;
+    for (u32 a = a0; a < a1; a += 8)
+    {
+        u64 rec[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            rec[j] = g.fast[a + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            cnt += action_ok(planes, g, rec[j], a + j);
+    }
+    if (valid)
+        counts[static_cast<u64>(t) * g.slices + s] = cnt;
+}
+
+// (parent, action) records of the successors of parents [first, first + n), in the layout of k_ground_count: wave s
+// writes the successors of its action slice at offsets[t * slices + s] - cand_base on, the parent index relative to
+// `first` in the high 32 bits, the action in the low.
+template<int W>
+__global__ __launch_bounds__(kPB * kMaxSlices) void k_ground_emit(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
+                                                                 const u64* __restrict__ offsets, u64 cand_base, u64* __restrict__ cand_pa)
+{
+    __shared__ u8 planes[Planes<W>::kCount * kPB];
+    const u32 lane = threadIdx.x & (kPB - 1), s = threadIdx.x / kPB;
+    const u32 t = blockIdx.x * kPB + lane;
+    const bool valid = t < n;
+    if (s == 0)
+        load_planes<W>(planes, arena + (first + t) * W, valid);
+    __syncthreads();
+    u64 k = valid ? offsets[static_cast<u64>(t) * g.slices + s] - cand_base : 0;
+    const u64 hi = static_cast<u64>(t) << 32;
+    const u32 a0 = min(s * g.slice_len, g.num_padded), a1 = min(a0 + g.slice_len, g.num_padded);
+    for (u32 a = a0; a < a1; a += 8)
+    {
+        u64 rec[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            rec[j] = g.fast[a + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (action_ok(planes, g, rec[j], a + j) && valid)
+                cand_pa[k++] = hi | (a + j);
     }
 }
 
@@ -117,63 +213,67 @@ __device__ __forceinline__ u64 hash_fixed(const u64 (&v)[W])
     return mix64(h);
 }
 
-// Writes the successors of parents [first, first + n) at candidate positions offsets[t] - cand_base.
+/// Whether the set holds row v (hash h) as a stored state. Read-only: the table holds no pending entries between
+/// batches.
 template<int W>
-__global__ __launch_bounds__(kGB) void k_ground_generate(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
-                                                        const u64* __restrict__ offsets, u64 cand_base, u64* __restrict__ cand,
-                                                        u64* __restrict__ cand_hash, u32* __restrict__ cand_parent,
-                                                        u32* __restrict__ cand_action)
+__device__ bool stored(const StateSetView& s, const u64 (&v)[W], u64 h)
 {
-    __shared__ u64 st[W][kGB];
-    const u32 t = blockIdx.x * kGB + threadIdx.x;
-    const bool valid = t < n;
-    const u64* row = arena + (first + t) * W;
-    u64 r[W];
+    const u64 tag = h >> 32;
+    u64 slot = slot_of_hash(h, s.capacity);
+    for (u64 probes = 0; probes < s.capacity; ++probes)
+    {
+        const u64 e = s.table[slot];
+        if (e == 0)
+            return false;
+        const u32 code = static_cast<u32>(e);
+        if ((e >> 32) == tag && !(code & kPending))
+        {
+            const u64* o = s.arena + static_cast<u64>(code - 1) * W;
+            bool eq = true;
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-    {
-        r[w] = valid ? row[w] : 0;
-        st[w][threadIdx.x] = r[w];
+            for (int w = 0; w < W; ++w)
+                eq = eq && o[w] == v[w];
+            if (eq)
+                return true;
+        }
+        slot = slot + 1 == s.capacity ? 0 : slot + 1;
     }
-    u64 k = valid ? offsets[t] - cand_base : 0;
-    const u32 parent = static_cast<u32>(first + t);
-    for (u32 a = 0; a < g.num; ++a)
+    return false;
+}
+
+// Candidates [0, m): successor rows and hashes; fresh[j] = the row is not a stored state; fresh rows and hashes are
+// kept at their candidate index; *nfresh += the number of fresh candidates.
+template<int W>
+__global__ __launch_bounds__(kLB) void k_ground_lookup(StateSetView s, u64 first, const u64* __restrict__ cand_pa, u64 m,
+                                                      const u64* __restrict__ masks, u64* __restrict__ cand,
+                                                      u64* __restrict__ cand_hash, u8* __restrict__ fresh, u64* __restrict__ nfresh)
+{
+    const u64 j = static_cast<u64>(blockIdx.x) * kLB + threadIdx.x;
+    bool fr = false;
+    if (j < m)
     {
-        const u32 m = g.meta[a], o = g.off[a];
-        if (!valid || !emitted<W>(st, g, a, m, o))
-            continue;
-        const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF, nadd = (m >> 16) & 0xFF, ndel = m >> 24;
+        const u64 pa = cand_pa[j];
+        const u64* row = s.arena + (first + (pa >> 32)) * W;
+        const u64* mk = masks + static_cast<u64>(static_cast<u32>(pa)) * (2 * W);
         u64 v[W];
 #pragma unroll
         for (int w = 0; w < W; ++w)
-            v[w] = r[w];
-        const u32* adds = g.slots + o + npos + nneg;
-        const u32* dels = adds + nadd;
-        for (u32 i = 0; i < ndel; ++i)
+            v[w] = (row[w] & ~mk[w]) | mk[W + w];
+        const u64 h = hash_fixed<W>(v);
+        fr = !stored<W>(s, v, h);
+        fresh[j] = fr ? 1 : 0;
+        if (fr)
         {
-            const u32 s = dels[i];
+            u64* dst = cand + j * W;
 #pragma unroll
             for (int w = 0; w < W; ++w)
-                if (static_cast<u32>(w) == (s >> 6))
-                    v[w] &= ~(u64{1} << (s & 63));
+                dst[w] = v[w];
+            cand_hash[j] = h;
         }
-        for (u32 i = 0; i < nadd; ++i)
-        {
-            const u32 s = adds[i];
-#pragma unroll
-            for (int w = 0; w < W; ++w)
-                if (static_cast<u32>(w) == (s >> 6))
-                    v[w] |= u64{1} << (s & 63);
-        }
-        u64* dst = cand + k * W;
-#pragma unroll
-        for (int w = 0; w < W; ++w)
-            dst[w] = v[w];
-        cand_hash[k] = hash_fixed<W>(v);
-        cand_parent[k] = parent;
-        cand_action[k] = a;
-        ++k;
     }
+    const u64 c = static_cast<u64>(__popcll(__ballot(fr)));
+    if (lane_id() == 0 && c)
+        atomicAdd(reinterpret_cast<unsigned long long*>(nfresh), static_cast<unsigned long long>(c));
 }
 
 // The winner whose exclusive rank equals `rank`: its candidate index.
@@ -184,20 +284,22 @@ __global__ void k_find_rank(const u32* __restrict__ flags, const u64* __restrict
         *out = j;
 }
 
-// The first index i in [lo, hi) with offsets[i] - base > limit (or hi): the parents whose successors fit a chunk.
-__global__ void k_upper(const u64* __restrict__ offsets, u64 lo, u64 hi, u64 bound, u64* __restrict__ out)
+// The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
+// p0 + 1 (one parent's successors always fit). out[0] = p, out[1] = offsets[p * stride].
+__global__ void k_chunk_end(const u64* __restrict__ offsets, u32 stride, u64 p0, u64 hi, u64 bound, u64* __restrict__ out)
 {
-    // one thread: binary search
-    u64 a = lo, b = hi;
+    u64 a = p0 + 1, b = hi + 1;  // the first parent in [p0 + 1, hi + 1) past the bound
     while (a < b)
     {
         const u64 mid = a + (b - a) / 2;
-        if (offsets[mid] <= bound)
+        if (offsets[mid * stride] <= bound)
             a = mid + 1;
         else
             b = mid;
     }
-    *out = a;
+    const u64 p = a - 1 < p0 + 1 ? p0 + 1 : a - 1;
+    out[0] = p;
+    out[1] = offsets[p * stride];
 }
 
 __global__ void k_sum_u8(const u8* __restrict__ v, u64 n, u64* __restrict__ out)
@@ -246,23 +348,22 @@ __global__ void k_fingerprint(const u64* __restrict__ arena, u64 n, u32 W, const
 
 __global__ void k_set_u64(u64* p, u64 v) { *p = v; }
 
+constexpr int kSmall = 16;  // device scalars of the driver
+
 struct Buffers
 {
-    u32* counts = nullptr;
-    u8* goal = nullptr;
-    u64* offsets = nullptr;
-    u64* scan_scratch = nullptr;
-    u64* cand = nullptr;
-    u64* cand_hash = nullptr;
-    u32* cand_parent = nullptr;
-    u32* cand_action = nullptr;
-    u64* small = nullptr;  // device scalars
-    u64* host = nullptr;   // pinned mirror
+    std::vector<void*> owned;
+    u64* host = nullptr;  // pinned mirror of the device scalars
+    template<class T>
+    T* alloc(size_t n, const char* what)
+    {
+        T* p = dev_alloc<T>(n, what);
+        owned.push_back(p);
+        return p;
+    }
     ~Buffers()
     {
-        for (void* p : {static_cast<void*>(counts), static_cast<void*>(goal), static_cast<void*>(offsets), static_cast<void*>(scan_scratch),
-                        static_cast<void*>(cand), static_cast<void*>(cand_hash), static_cast<void*>(cand_parent),
-                        static_cast<void*>(cand_action), static_cast<void*>(small)})
+        for (void* p : owned)
             dev_free(p);
         if (host)
             (void)hipHostFree(host);
@@ -329,6 +430,41 @@ private:
     std::vector<Pair> m_ev;
 };
 
+/// The fast records and the delete / add masks of the ground actions (host).
+template<int W>
+void build_action_tables(const GroundActions& ga, std::vector<u64>& fast, std::vector<u64>& masks)
+{
+    const u32 num = ga.size();
+    const u32 padded = (num + 7) & ~7u;
+    constexpr u64 one = Planes<W>::kOneSlot, zero = Planes<W>::kZeroSlot;
+    fast.assign(padded, zero | (zero << 16) | (zero << 32) | (zero << 48));
+    masks.assign(static_cast<size_t>(num) * 2 * W, 0);
+    for (u32 a = 0; a < num; ++a)
+    {
+        const u32 m = ga.meta[a], o = ga.off[a];
+        const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF, nadd = (m >> 16) & 0xFF, ndel = m >> 24;
+        const bool dominated = !ga.dom_off.empty() && ga.dom_off[a + 1] > ga.dom_off[a];
+        u64 rec = 0;
+        for (u32 i = 0; i < 4; ++i)
+            rec |= (i < npos ? static_cast<u64>(ga.slots[o + i]) : one) << (16 * i);
+        if (nneg || npos > 4 || dominated)
+            rec = (rec & ~u64{0xFFFF}) | one | kGeneral;
+        fast[a] = rec;
+        u64* del = masks.data() + static_cast<size_t>(a) * 2 * W;
+        u64* add = del + W;
+        for (u32 i = 0; i < ndel; ++i)
+        {
+            const u32 s = ga.slots[o + npos + nneg + nadd + i];
+            del[s >> 6] |= u64{1} << (s & 63);
+        }
+        for (u32 i = 0; i < nadd; ++i)
+        {
+            const u32 s = ga.slots[o + npos + nneg + i];
+            add[s >> 6] |= u64{1} << (s & 63);
+        }
+    }
+}
+
 template<int W>
 BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc)
 {
@@ -343,44 +479,29 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     } sg{stream};
     Timers tm(o.timings != 0, stream, r);
     constexpr u64 R = W * 8;  // row bytes
+    Buffers b;
 
-    // ground table and goal
-    u32* d_meta = dev_alloc<u32>(ga.meta.size(), "ground meta");
-    u32* d_off = dev_alloc<u32>(ga.off.size(), "ground offsets");
-    u32* d_slots = dev_alloc<u32>(ga.slots.size(), "ground slots");
-    u32* d_dom_off = ga.dom_off.empty() ? nullptr : dev_alloc<u32>(ga.dom_off.size(), "ground dominators");
-    u32* d_dom = ga.dom_off.empty() ? nullptr : dev_alloc<u32>(ga.dom.size(), "ground dominators");
-    u32* d_gpos = dev_alloc<u32>(task.goal_pos.size(), "goal");
-    u32* d_gneg = dev_alloc<u32>(task.goal_neg.size(), "goal");
-    u64* d_slot_cid = task.mode == AtomMode::Dense ? nullptr : dev_alloc<u64>(task.slot_cid.size(), "slot cids");
-    struct FreeAll
-    {
-        std::vector<void*> p;
-        ~FreeAll()
-        {
-            for (void* x : p)
-                dev_free(x);
-        }
-    } fa{{d_meta, d_off, d_slots, d_gpos, d_gneg, d_slot_cid, d_dom_off, d_dom}};
-    auto up = [&](void* d, const void* h, size_t b) {
-        if (b)
-            hip_check(hipMemcpyAsync(d, h, b, hipMemcpyHostToDevice, stream), "upload");
+    // ground tables and goal
+    std::vector<u64> fast, masks;
+    build_action_tables<W>(ga, fast, masks);
+    auto upload = [&](const auto& v, const char* what) {
+        using T = std::decay_t<decltype(v[0])>;
+        if (v.empty())
+            return static_cast<T*>(nullptr);
+        T* d = b.alloc<T>(v.size(), what);
+        hip_check(hipMemcpyAsync(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, stream), what);
+        return d;
     };
-    up(d_meta, ga.meta.data(), ga.meta.size() * 4);
-    up(d_off, ga.off.data(), ga.off.size() * 4);
-    up(d_slots, ga.slots.data(), ga.slots.size() * 4);
-    if (d_dom_off)
-    {
-        up(d_dom_off, ga.dom_off.data(), ga.dom_off.size() * 4);
-        up(d_dom, ga.dom.data(), ga.dom.size() * 4);
-    }
-    up(d_gpos, task.goal_pos.data(), task.goal_pos.size() * 4);
-    up(d_gneg, task.goal_neg.data(), task.goal_neg.size() * 4);
-    if (d_slot_cid)
-        up(d_slot_cid, task.slot_cid.data(), task.slot_cid.size() * 8);
-    const GroundDev g{d_meta, d_off, d_slots, d_dom_off, d_dom, ga.size()};
-    const GoalDev goal{d_gpos, d_gneg, static_cast<u32>(task.goal_pos.size()), static_cast<u32>(task.goal_neg.size()),
-                       task.goal_unsat ? 1u : 0u};
+    // action slices: one wave per slice of at least 512 actions (up to kMaxSlices waves per 64 parents)
+    const u32 S = std::clamp<u32>(static_cast<u32>(fast.size()) / 512, 1, kMaxSlices);
+    const u32 slice_len = ((static_cast<u32>(fast.size()) / 8 + S - 1) / S) * 8;
+    const GroundDev g{upload(fast, "action records"), upload(ga.meta, "ground meta"), upload(ga.off, "ground offsets"),
+                      upload(ga.slots, "ground slots"), upload(ga.dom_off, "ground dominators"), upload(ga.dom, "ground dominators"),
+                      ga.size(), static_cast<u32>(fast.size()), S, slice_len};
+    const u64* d_masks = upload(masks, "action masks");
+    const GoalDev goal{upload(task.goal_pos, "goal"), upload(task.goal_neg, "goal"), static_cast<u32>(task.goal_pos.size()),
+                       static_cast<u32>(task.goal_neg.size()), task.goal_unsat ? 1u : 0u};
+    const u64* d_slot_cid = task.mode == AtomMode::Dense ? nullptr : upload(task.slot_cid, "slot cids");
 
     // capacity: the arena holds every stored state
     const bool bounded = o.max_states != ~u64{0};
@@ -393,38 +514,75 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         StateSet& s;
         ~SetGuard() { state_set_destroy(s); }
     } setg{set};
-    Buffers b;
-    b.counts = dev_alloc<u32>(cap_states, "layer counts");
-    b.goal = dev_alloc<u8>(cap_states, "layer goal flags");
-    b.offsets = dev_alloc<u64>(cap_states + 1, "layer offsets");
-    b.scan_scratch = dev_alloc<u64>(scan_scratch_words(cap_states), "scan scratch");
-    b.cand = dev_alloc<u64>(chunk * W, "candidate rows");
-    b.cand_hash = dev_alloc<u64>(chunk, "candidate hashes");
-    b.cand_parent = dev_alloc<u32>(chunk, "candidate parents");
-    b.cand_action = dev_alloc<u32>(chunk, "candidate actions");
-    b.small = dev_alloc<u64>(8, "scalars");
-    hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), 8 * sizeof(u64), hipHostMallocDefault), "pinned");
-
-    auto read_small = [&](int idx) -> u64 {
-        hip_check(hipMemcpyAsync(b.host + idx, b.small + idx, sizeof(u64), hipMemcpyDeviceToHost, stream), "read");
+    // per-layer arrays (grown with the largest layer): counts [parents * S] per (parent, slice), goal flags per parent,
+    // successor offsets [parents * S + 1] (layer-relative candidate indices)
+    u32* counts = nullptr;
+    u8* goal_flags = nullptr;
+    u64* offsets = nullptr;
+    u64* scan_scratch = nullptr;
+    u64 layer_cap = 0;
+    auto ensure_layer = [&](u64 ln) {
+        if (ln <= layer_cap)
+            return;
         hip_check(hipStreamSynchronize(stream), "sync");
-        return b.host[idx];
+        for (void* q : {static_cast<void*>(counts), static_cast<void*>(goal_flags), static_cast<void*>(offsets), static_cast<void*>(scan_scratch)})
+            dev_free(q);
+        layer_cap = std::max<u64>(ln, std::min<u64>(cap_states, layer_cap * 2));
+        counts = dev_alloc<u32>(layer_cap * S, "layer counts");
+        goal_flags = dev_alloc<u8>(layer_cap, "layer goal flags");
+        offsets = dev_alloc<u64>(layer_cap * S + 1, "layer offsets");
+        scan_scratch = dev_alloc<u64>(scan_scratch_words(layer_cap * S), "scan scratch");
     };
-    auto set_small = [&](int idx, u64 v) { hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, b.small + idx, v); };
+    struct LayerGuard
+    {
+        u32*& c;
+        u8*& g;
+        u64*& o;
+        u64*& s;
+        ~LayerGuard()
+        {
+            dev_free(c);
+            dev_free(g);
+            dev_free(o);
+            dev_free(s);
+        }
+    } layer_guard{counts, goal_flags, offsets, scan_scratch};
+    u64* cand = b.alloc<u64>(chunk * W, "candidate rows");
+    u64* cand_hash = b.alloc<u64>(chunk, "candidate hashes");
+    u64* cand_pa = b.alloc<u64>(chunk, "candidate records");
+    u8* fresh = b.alloc<u8>(chunk, "candidate fresh flags");
+    u64* small = b.alloc<u64>(kSmall, "scalars");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
+    enum
+    {
+        kGoalSum = 0,   // goal states among the layer's expanded parents
+        kFirstGoal = 1, // first goal flag of a counted block
+        kChunkP = 2,    // chunk end parent, then its offset
+        kChunkOff = 3,
+        kFresh = 4,     // fresh candidates of the chunk
+        kCut = 5,       // the candidate of the state that fills the store
+        kBlockTotal = 6,
+        kFingerprint = 7,
+    };
+    auto set_small = [&](int idx, u64 v) { hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, small + idx, v); };
+    auto sync_small = [&] {
+        hip_check(hipMemcpyAsync(b.host, small, kSmall * sizeof(u64), hipMemcpyDeviceToHost, stream), "read scalars");
+        hip_check(hipStreamSynchronize(stream), "sync");
+    };
 
     // the start state
     {
         std::vector<u64> s0(W, 0);
         std::copy(task.initial.begin(), task.initial.end(), s0.begin());
-        hip_check(hipMemcpyAsync(b.cand, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
+        hip_check(hipMemcpyAsync(cand, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
         u64 nn = 0;
-        state_set_insert(set, b.cand, nullptr, 1, nullptr, nullptr, &nn, stream);
+        state_set_insert(set, cand, nullptr, 1, nullptr, nullptr, &nn, stream);
     }
     const auto td0 = Clock::now();
-    u64 layer_begin = 0, layer_end = 1;
     bool stopped = false, budget_stopped = false;
     r.status = kExhausted;
-    u64 pos = 0;  // states expanded or passed (the reference's queue position)
+    u64 pos = 0;                           // states expanded or passed (the reference's queue position)
+    u64 seen_parents = 0, seen_cands = 0;  // counted so far (the successors-per-parent estimate)
     while (!stopped)
     {
         if (pos >= set.size)
@@ -443,113 +601,142 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         if (r.layers == o.max_depth)
             break;
         ++r.layers;
-        layer_begin = pos;
-        layer_end = set.size;
+        const u64 layer_begin = pos, layer_end = set.size;
         const u64 ln = layer_end - layer_begin;
         std::array<u64, 3> row{0, 0, 0};
         const u64 size0 = set.size;
-        // counts and goal flags of the whole layer
-        tm.begin(kKCount);
-        hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(ln, kGB)), dim3(kGB), 0, stream, set.v.arena, layer_begin,
-                           static_cast<u32>(ln), g, goal, b.counts, b.goal);
-        launch_check("ground count");
-        tm.end(kKCount, ln * (R + 5));
-        tm.begin(kKOther);
-        launch_exclusive_scan(b.counts, b.offsets, ln, b.scan_scratch, b.small + 0, stream);
-        tm.end(kKOther, 0);
-        // offsets[ln] = total (for chunk searches)
-        hip_check(hipMemcpyAsync(b.offsets + ln, b.small + 0, sizeof(u64), hipMemcpyDeviceToDevice, stream), "total");
-        // the parents this layer expands: up to the first goal (stop_at_goal) and the expansion budget
-        u64 expand_n = ln;
-        set_small(1, ~u64{0});
-        hipLaunchKernelGGL(k_first_u8, dim3(std::min<u64>(blocks_for(ln, 256), 4096)), dim3(256), 0, stream, b.goal, ln, b.small + 1);
-        const u64 first_goal = read_small(1);
-        bool goal_stop = false, budget_stop = false;
-        if (o.stop_at_goal && first_goal != ~u64{0})
+        // the budget check precedes the goal test of each state (brfs.cpp:138-144): parents at or past the remaining
+        // budget are neither tested nor expanded
+        const u64 budget = o.max_expanded == ~u64{0} ? ~u64{0} : o.max_expanded - r.expanded;
+        u64 lim = std::min(ln, budget);
+        ensure_layer(ln);
+        u64 counted = 0, counted_total = 0;  // parents [0, counted) counted; offsets[counted * S] on the host
+        u64 first_goal = ~u64{0};
+        bool goal_stop = false;
+        set_small(kGoalSum, 0);
+        u64 p0 = 0, base = 0;  // base = offsets[p0 * S]
+        while (p0 < lim && !stopped)
         {
-            expand_n = first_goal;
-            goal_stop = true;
-        }
-        // the budget check precedes the goal test of each state (brfs.cpp:138-144)
-        if (o.max_expanded != ~u64{0} &&
-            (goal_stop ? r.expanded + expand_n >= o.max_expanded : r.expanded + expand_n > o.max_expanded))
-        {
-            expand_n = o.max_expanded - r.expanded;
-            budget_stop = true;
-            goal_stop = false;
-        }
-        // chunks of parents whose successors fit the candidate buffers
-        u64 p0 = 0;
-        while (p0 < expand_n && !stopped)
-        {
-            set_small(2, 0);
-            hip_check(hipMemcpyAsync(b.host + 3, b.offsets + p0, sizeof(u64), hipMemcpyDeviceToHost, stream), "offset");
-            hip_check(hipStreamSynchronize(stream), "sync");
-            const u64 base = b.host[3];
-            // parents [p0, p1) end at offsets[p1] <= base + chunk: p1 + 1 is the first index past the bound
-            hipLaunchKernelGGL(k_upper, dim3(1), dim3(1), 0, stream, b.offsets, p0, expand_n + 1, base + chunk, b.small + 2);
-            u64 p1 = read_small(2) - 1;
-            p1 = std::min<u64>(std::max<u64>(p1, p0 + 1), expand_n);
-            hip_check(hipMemcpyAsync(b.host + 4, b.offsets + p1, sizeof(u64), hipMemcpyDeviceToHost, stream), "offset");
-            hip_check(hipStreamSynchronize(stream), "sync");
-            const u64 m = b.host[4] - base;
+            // count ahead until the counted parents past p0 hold a full chunk (or the layer's rest)
+            while (counted < lim && counted_total - base < chunk)
+            {
+                const u64 est = seen_parents ? std::max<u64>(1, (seen_cands + seen_parents - 1) / seen_parents) : 1;
+                const u64 nb = std::min<u64>(lim - counted, std::max<u64>(u64{1} << 16, chunk / est));
+                tm.begin(kKCount);
+                hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kPB)), dim3(kPB * S), 0, stream, set.v.arena, layer_begin + counted,
+                                   static_cast<u32>(nb), g, goal, counts + counted * S, goal_flags + counted);
+                launch_check("ground count");
+                tm.end(kKCount, nb * (R + 5));
+                tm.begin(kKOther);
+                launch_exclusive_scan(counts + counted * S, offsets + counted * S, nb * S, scan_scratch, offsets + (counted + nb) * S, stream,
+                                      counted ? offsets + counted * S : nullptr);
+                set_small(kFirstGoal, ~u64{0});
+                hipLaunchKernelGGL(k_first_u8, dim3(std::min<u64>(blocks_for(nb, 256), 4096)), dim3(256), 0, stream, goal_flags + counted, nb,
+                                   small + kFirstGoal);
+                hip_check(hipMemcpyAsync(small + kBlockTotal, offsets + (counted + nb) * S, sizeof(u64), hipMemcpyDeviceToDevice, stream), "total");
+                launch_check("count scan");
+                tm.end(kKOther, 0);
+                sync_small();
+                const u64 total = b.host[kBlockTotal];
+                seen_parents += nb;
+                seen_cands += total - counted_total;
+                counted_total = total;
+                if (b.host[kFirstGoal] != ~u64{0})
+                {
+                    const u64 gi = counted + b.host[kFirstGoal];
+                    if (first_goal == ~u64{0})
+                        first_goal = gi;
+                    if (o.stop_at_goal && gi < lim)
+                    {
+                        lim = gi;
+                        goal_stop = true;
+                    }
+                }
+                counted += nb;
+            }
+            if (p0 >= lim)
+                break;
+            hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, std::min(counted, lim), base + chunk, small + kChunkP);
+            launch_check("chunk end");
+            sync_small();
+            const u64 p1 = b.host[kChunkP], end_off = b.host[kChunkOff];
+            const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
-            tm.begin(kKGenerate);
-            hipLaunchKernelGGL(k_ground_generate<W>, dim3(blocks_for(np, kGB)), dim3(kGB), 0, stream, set.v.arena, layer_begin + p0, np,
-                               g, b.offsets + p0, base, b.cand, b.cand_hash, b.cand_parent, b.cand_action);
-            launch_check("ground generate");
-            tm.end(kKGenerate, np * (R + 8) + m * (R + 16));
-            tm.begin(kKProbe);
-            state_set_probe(set, b.cand, b.cand_hash, m, stream);
-            tm.end(kKProbe, m * (R + 24));
-            tm.begin(kKRank);
-            state_set_rank(set, m, stream);
-            tm.end(kKRank, m * 32);
-            hip_check(hipMemcpyAsync(b.host + 5, set.d_total, sizeof(u64), hipMemcpyDeviceToHost, stream), "new");
-            hip_check(hipMemcpyAsync(b.host + 6, set.d_status, sizeof(u32), hipMemcpyDeviceToHost, stream), "status");
-            hip_check(hipStreamSynchronize(stream), "sync");
-            if (static_cast<u32>(b.host[6]) & kStatusTableFull)
-                throw std::length_error("mymyr_amd: brfs: state table full");
-            const u64 fresh = b.host[5];
-            tm.bytes(kKProbe, (m - fresh) * R);  // a duplicate compares its row with the stored one
+            u64 nfresh = 0, winners = 0;
+            if (m > 0)
+            {
+                tm.begin(kKEmit);
+                hipLaunchKernelGGL(k_ground_emit<W>, dim3(blocks_for(np, kPB)), dim3(kPB * S), 0, stream, set.v.arena, layer_begin + p0, np, g,
+                                   offsets + p0 * S, base, cand_pa);
+                launch_check("ground emit");
+                tm.end(kKEmit, np * (R + 8) + m * 8);
+                set_small(kFresh, 0);
+                tm.begin(kKLookup);
+                hipLaunchKernelGGL(k_ground_lookup<W>, dim3(blocks_for(m, kLB)), dim3(kLB), 0, stream, set.v, layer_begin + p0, cand_pa, m,
+                                   d_masks, cand, cand_hash, fresh, small + kFresh);
+                launch_check("ground lookup");
+                tm.end(kKLookup, 0);
+                tm.begin(kKProbe);
+                state_set_probe(set, cand, cand_hash, m, stream, fresh);
+                tm.end(kKProbe, 0);
+                tm.begin(kKRank);
+                state_set_rank(set, m, stream);
+                tm.end(kKRank, m * 24);
+                hip_check(hipMemcpyAsync(small + kBlockTotal, set.d_total, sizeof(u64), hipMemcpyDeviceToDevice, stream), "new");
+                hip_check(hipMemcpyAsync(small + kCut, set.d_status, sizeof(u32), hipMemcpyDeviceToDevice, stream), "status");
+                sync_small();
+                if (static_cast<u32>(b.host[kCut]) & kStatusTableFull)
+                    throw std::length_error("mymyr_amd: brfs: state table full");
+                nfresh = b.host[kFresh];
+                winners = b.host[kBlockTotal];
+                // lookup: records, table entries and flags of every candidate, parent rows, the stored row each dropped
+                // candidate matched, fresh rows and hashes; probe: the fresh candidates' rows, hashes, entries and slots,
+                // and the pending row each non-winner matched
+                tm.bytes(kKLookup, m * 17 + u64{np} * R + (m - nfresh) * R + nfresh * (R + 8));
+                tm.bytes(kKProbe, nfresh * (R + 24) + (nfresh - winners) * R);
+            }
             const u64 room = (bounded ? o.max_states : cap_states) - set.size;
-            if (fresh >= room && fresh > 0 && bounded)
+            if (winners >= room && winners > 0 && bounded)
             {
                 // the store fills at the winner of rank room - 1: stop inside its parent's expansion
-                set_small(7, ~u64{0});
-                hipLaunchKernelGGL(k_find_rank, dim3(blocks_for(m, 256)), dim3(256), 0, stream, set.flags, set.offsets, m, room - 1, b.small + 7);
-                const u64 jcut = read_small(7);
-                hip_check(hipMemcpyAsync(b.host + 3, b.cand_parent + jcut, sizeof(u32), hipMemcpyDeviceToHost, stream), "parent");
+                set_small(kCut, ~u64{0});
+                hipLaunchKernelGGL(k_find_rank, dim3(blocks_for(m, 256)), dim3(256), 0, stream, set.flags, set.offsets, m, room - 1, small + kCut);
+                sync_small();
+                const u64 jcut = b.host[kCut];
+                hip_check(hipMemcpyAsync(b.host + kCut, cand_pa + jcut, sizeof(u64), hipMemcpyDeviceToHost, stream), "parent");
                 hip_check(hipStreamSynchronize(stream), "sync");
-                const u64 pcut = static_cast<u32>(b.host[3]) - layer_begin;  // index in the layer
+                const u64 pc = b.host[kCut] >> 32;  // the parent, relative to p0
                 tm.begin(kKCompact);
-                state_set_compact(set, b.cand, b.cand_hash, m, set.size, o.max_states, nullptr, nullptr, stream);
+                state_set_compact(set, cand, cand_hash, m, set.size, o.max_states, nullptr, nullptr, stream);
                 tm.end(kKCompact, m * 12 + room * (2 * R + 24));
-                row[0] += pcut - p0 + 1;
+                row[0] += pc + 1;
                 row[1] += jcut + 1;
-                set_small(0, 0);
-                hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pcut - p0 + 1, 256), 1024)), dim3(256), 0, stream, b.goal + p0,
-                                   pcut - p0 + 1, b.small + 0);
-                r.goal_states += read_small(0);
+                hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pc + 1, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, pc + 1,
+                                   small + kGoalSum);
                 set.size = o.max_states;
                 r.status = kOutOfStates;
                 stopped = true;
                 break;
             }
-            if (fresh > room)
+            if (winners > room)
                 throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
                                         " states of device memory (set max_states or memory_states)");
-            tm.begin(kKCompact);
-            state_set_compact(set, b.cand, b.cand_hash, m, set.size, cap_states, nullptr, nullptr, stream);
-            tm.end(kKCompact, m * 12 + fresh * (2 * R + 24));
-            set.size += fresh;
+            if (m > 0)
+            {
+                tm.begin(kKCompact);
+                state_set_compact(set, cand, cand_hash, m, set.size, cap_states, nullptr, nullptr, stream);
+                tm.end(kKCompact, m * 12 + winners * (2 * R + 24));
+            }
+            set.size += winners;
             row[0] += np;
             row[1] += m;
-            set_small(0, 0);
-            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(np, 256), 1024)), dim3(256), 0, stream, b.goal + p0, np, b.small + 0);
-            r.goal_states += read_small(0);
+            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(np, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, np,
+                               small + kGoalSum);
             p0 = p1;
+            base = end_off;
         }
+        sync_small();
+        r.goal_states += b.host[kGoalSum];
         pos = layer_begin + row[0];
         r.expanded += row[0];
         r.generated += row[1];
@@ -564,8 +751,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             r.status = kSolved;
             stopped = true;
         }
-        if (budget_stop && !stopped)
+        if (!goal_stop && !stopped && lim < ln)
         {
+            // the expansion budget ran out inside this layer
             r.status = kOutOfStates;
             budget_stopped = true;
             stopped = true;
@@ -587,11 +775,12 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     tm.collect();
     if (o.fingerprint)
     {
-        set_small(0, 0);
+        set_small(kFingerprint, 0);
         hipLaunchKernelGGL(k_fingerprint, dim3(std::min<u64>(blocks_for(set.size, 256), 2048)), dim3(256), 0, stream, set.v.arena,
-                           set.size, static_cast<u32>(W), d_slot_cid, b.small + 0);
+                           set.size, static_cast<u32>(W), d_slot_cid, small + kFingerprint);
         launch_check("fingerprint");
-        r.fingerprint = read_small(0);
+        sync_small();
+        r.fingerprint = b.host[kFingerprint];
     }
     r.search_s = std::chrono::duration<double>(Clock::now() - t0).count();
     return r;

@@ -30,13 +30,14 @@ struct BrfsOptionsC
 /// Kernel classes of the device BrFS (timed with HIP events when BrfsOptionsC::timings is set).
 enum BrfsKernel : int
 {
-    kKCount = 0,     // applicability counts and goal flags of a layer's parents
-    kKGenerate = 1,  // successor rows, hashes and (parent, action) records
-    kKProbe = 2,     // state-set probe with the min-candidate winner
-    kKRank = 3,      // winner flags and their exclusive scan
-    kKCompact = 4,   // new states into the arena and the table
-    kKOther = 5,     // scans of counts, goal searches, chunk bounds, fingerprint
-    kKClasses = 6,
+    kKCount = 0,    // applicability counts and goal flags of a block of parents
+    kKEmit = 1,     // (parent, action) records of the successors, in candidate order
+    kKLookup = 2,   // successor rows and hashes; read-only probe of the stored states; fresh rows kept
+    kKProbe = 3,    // state-set probe of the fresh candidates with the min-candidate winner
+    kKRank = 4,     // winner flags and their exclusive scan
+    kKCompact = 5,  // new states into the arena and the table
+    kKOther = 6,    // scans of counts, goal searches, chunk bounds, fingerprint
+    kKClasses = 7,
 };
 
 struct BrfsResultC
@@ -50,7 +51,7 @@ struct BrfsResultC
     double search_s = 0;
     double device_s = 0;
     double kernel_ms[kKClasses] = {};
-    u64 kernel_bytes[kKClasses] = {};  // algorithmic bytes (see DevBytes in brfs.hip)
+    u64 kernel_bytes[kKClasses] = {};  // algorithmic bytes per class (the per-launch formulas in brfs.hip)
     u64 kernel_launches[kKClasses] = {};
 };
 

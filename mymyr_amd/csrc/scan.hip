@@ -35,12 +35,12 @@ __global__ __launch_bounds__(kScanBlock) void k_block_sums(const u32* __restrict
 }
 
 // One block scans the block sums in place (exclusive) and writes the grand total.
-__global__ __launch_bounds__(1024) void k_scan_sums(u64* __restrict__ sums, u64 nb, u64* __restrict__ total)
+__global__ __launch_bounds__(1024) void k_scan_sums(u64* __restrict__ sums, u64 nb, u64* total, const u64* base)
 {
     __shared__ u64 lds[1024 / kWave + 1];
     __shared__ u64 carry;
     if (threadIdx.x == 0)
-        carry = 0;
+        carry = base ? *base : 0;
     __syncthreads();
     for (u64 base = 0; base < nb; base += 1024)
     {
@@ -116,16 +116,17 @@ __global__ __launch_bounds__(kScanBlock) void k_offsets(const u32* __restrict__ 
 }
 }  // namespace
 
-void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream)
+void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream, const u64* base)
 {
     const u64 nb = (n + kScanBlock * kPerThread - 1) / (kScanBlock * kPerThread);
     if (nb == 0)
     {
-        hipMemsetAsync(total, 0, sizeof(u64), stream);
+        // the total of an empty piece is its base
+        hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, stream, scratch, u64{0}, total, base);
         return;
     }
     hipLaunchKernelGGL(k_block_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, counts, n, scratch);
-    hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, stream, scratch, nb, total);
+    hipLaunchKernelGGL(k_scan_sums, dim3(1), dim3(1024), 0, stream, scratch, nb, total, base);
     hipLaunchKernelGGL(k_offsets, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, counts, n, scratch, offsets);
 }
 }  // namespace mya

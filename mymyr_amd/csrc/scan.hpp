@@ -80,6 +80,9 @@ __device__ __forceinline__ u32 block_exclusive(u32 v, u32* lds, u32* total)
 
 /// Device-wide exclusive scan of u32 counts into u64 offsets, in three launches: per-block sums, a one-block scan of
 /// the sums, then the per-element offsets. `scratch` holds blocks(n) + 1 u64 words; `total` (device) receives the sum.
-void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream);
+/// With `base` (device, optional) every offset and the total start at *base instead of 0 (`total` may be the element
+/// after the last offset, and `base` the total of the previous piece, to scan a sequence piece by piece).
+void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream,
+                           const u64* base = nullptr);
 inline u64 scan_scratch_words(u64 n) { return (n + 1023) / 1024 + 2; }
 }  // namespace mya

@@ -13,9 +13,9 @@ namespace
 {
 constexpr u64 kDupSettled = u64{1} << 63;
 constexpr u64 kProbeFailed = ~u64{0};
+constexpr u64 kProbeSkipped = ~u64{0} - 1;  // a candidate outside the probe mask
 constexpr int kBlock = 256;
 
-__device__ __forceinline__ u64 slot_of_hash(u64 h, u64 cap) { return ((h & 0xFFFFFFFFull) * cap) >> 32; }
 
 __device__ __forceinline__ bool rows_equal(const u64* __restrict__ a, const u64* __restrict__ b, u32 w)
 {
@@ -34,11 +34,17 @@ __global__ __launch_bounds__(kBlock) void k_hash_rows(const u64* __restrict__ ro
 }
 
 __global__ __launch_bounds__(kBlock) void k_probe(StateSetView s, const u64* __restrict__ rows, const u64* __restrict__ hashes,
-                                                 u64 n, u64* __restrict__ cand_slot, u32* __restrict__ status)
+                                                 const u8* __restrict__ mask, u64 n, u64* __restrict__ cand_slot,
+                                                 u32* __restrict__ status)
 {
     const u64 j = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
     if (j >= n)
         return;
+    if (mask && !mask[j])
+    {
+        cand_slot[j] = kProbeSkipped;
+        return;
+    }
     const u64 h = hashes[j];
     const u64 tag = h >> 32;
     const u32 W = s.words;
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(kBlock) void k_flags(StateSetView s, const u64* __r
         return;
     const u64 cs = cand_slot[j];
     u32 win = 0;
-    if (cs != kProbeFailed && !(cs & kDupSettled))
+    if (cs < kProbeSkipped && !(cs & kDupSettled))
         win = static_cast<u32>(s.table[cs]) == (kPending | static_cast<u32>(j)) ? 1u : 0u;
     flags[j] = win;
 }
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u6
     if (j >= n)
         return;
     const u64 cs = cand_slot[j];
-    if (cs == kProbeFailed)
+    if (cs >= kProbeSkipped)
     {
         ids[j] = -1;
         return;
@@ -224,11 +230,12 @@ void state_set_clear(StateSet& s, hipStream_t stream)
     s.size = 0;
 }
 
-void state_set_probe(StateSet& s, const u64* rows, const u64* hashes, u64 n, hipStream_t stream)
+void state_set_probe(StateSet& s, const u64* rows, const u64* hashes, u64 n, hipStream_t stream, const u8* mask)
 {
     if (n == 0)
         return;
-    hipLaunchKernelGGL(k_probe, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, rows, hashes, n, s.cand_slot, s.d_status);
+    hipLaunchKernelGGL(k_probe, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, rows, hashes, mask, n, s.cand_slot,
+                       s.d_status);
     launch_check("state set probe");
 }
 

@@ -14,6 +14,9 @@ namespace mya
 {
 constexpr u32 kPending = 0x80000000u;
 
+/// Slot of a state hash: fastrange of its low 32 bits over the capacity (the tag is the high 32 bits).
+__host__ __device__ inline u64 slot_of_hash(u64 h, u64 cap) { return ((h & 0xFFFFFFFFull) * cap) >> 32; }
+
 struct StateSetView
 {
     u64* table;
@@ -57,8 +60,9 @@ void state_set_insert(StateSet& s, const u64* rows, const u64* hashes, u64 n, i6
 
 /// Launch pieces of an insert for drivers that keep the batch on the device (BrFS): probe (after which winners are
 /// those whose entry holds their candidate), flags + scan, and compaction at base id `base`. Candidate rows and
-/// hashes stay readable until compaction ends.
-void state_set_probe(StateSet& s, const u64* rows, const u64* hashes, u64 n, hipStream_t stream);
+/// hashes stay readable until compaction ends. With `mask` (device, optional) the probe takes only the candidates j
+/// with mask[j] != 0; the others are neither inserted nor winners (their rows and hashes are not read).
+void state_set_probe(StateSet& s, const u64* rows, const u64* hashes, u64 n, hipStream_t stream, const u8* mask = nullptr);
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream);  // d_total[0] = winners
 void state_set_compact(StateSet& s, const u64* rows, const u64* hashes, u64 n, u64 base, u64 limit, i64* ids, u8* is_new,
                        hipStream_t stream);

@@ -929,6 +929,19 @@ private:
         return {d.front(), d.back() - d.front() + 1};
     }
 
+    // every position of predicate p has a domain that is a contiguous object range (rank = object - first)
+    bool pred_contiguous(u32 p) const
+    {
+        const u32 pb = C->layout.pos_begin[p];
+        for (u32 i = 0; i < T->preds[p].arity; ++i)
+        {
+            const auto& d = C->layout.domain[pb + i];
+            if (d.empty() || d.back() - d.front() + 1 != d.size())
+                return false;
+        }
+        return true;
+    }
+
     void build_image()
     {
         const u32 m = static_cast<u32>(T->preds.size());
@@ -1165,9 +1178,41 @@ private:
                 p.dst_lo = dl;
                 p.dst_words = std::max<u32>(1, words_for(dn));
             }
+            // forward rows (and unary rows) of a dense predicate over contiguous domains are slices of the state
+            if (C->mode == AtomMode::Dense && k.dir == 0 && pred_contiguous(k.pred) && C->layout.size[k.pred] > 0)
+            {
+                p.bulk = 1;
+                p.bit0 = C->layout.offset[k.pred];
+                const u32 last = pb + T->preds[k.pred].arity - 1;
+                p.row_bits = static_cast<u32>(C->layout.domain[last].size());
+            }
             p.offset = view_words;
             view_words += p.src_n * p.dst_words;
             pairs.push_back(p);
+        }
+        // slot decoding per fluent predicate (ascending offset)
+        std::vector<DevPredDecode> decode;
+        bool decode_arith = C->mode == AtomMode::Dense;
+        for (u32 p = 0; p < m; ++p)
+        {
+            if (T->preds[p].kind != 'F' || C->layout.size[p] == 0)
+                continue;
+            DevPredDecode d{};
+            d.offset = C->layout.offset[p];
+            d.size = C->layout.size[p];
+            d.pred = p;
+            d.arity = T->preds[p].arity;
+            const u32 pb = C->layout.pos_begin[p];
+            d.d1 = d.arity >= 2 ? static_cast<u32>(C->layout.domain[pb + 1].size()) : 1;
+            d.lo0 = d.arity >= 1 ? C->layout.domain[pb][0] : 0;
+            d.lo1 = d.arity >= 2 ? C->layout.domain[pb + 1][0] : 0;
+            d.contiguous = pred_contiguous(p) ? 1 : 0;
+            if (d.arity > 2 || !d.contiguous)
+                decode_arith = false;
+            for (const DevPair& q : pairs)
+                if (q.pred == p && !q.bulk)
+                    d.has_scatter = 1;
+            decode.push_back(d);
         }
 
         // slot records (pred | a0 << 16 | a1 << 32 | a2 << 48) for the view build and the atom listing
@@ -1247,39 +1292,19 @@ private:
         h.num_goal_neg = static_cast<u32>(C->goal_neg.size());
         h.goal_unsat = C->goal_unsat ? 1 : 0;
         h.fluent_count = C->layout.fluent_count;
+        // hot sections first: everything read per state by the step and count kernels
         h.off_schemas = put(schemas.data(), schemas.size() * sizeof(DevSchema));
         h.off_steps = put(steps.data(), steps.size() * sizeof(DevStep));
         h.off_cons = put(cons.data(), cons.size() * sizeof(DevCons));
         h.off_checks = put(checks.data(), checks.size() * sizeof(DevCheck));
         h.off_effects = put(effects.data(), effects.size() * sizeof(DevEffect));
         h.off_pairs = put(pairs.data(), pairs.size() * sizeof(DevPair));
-        // rs tables: per position n entries (u64)
-        h.num_positions = static_cast<u32>(C->layout.rs.size());
-        h.off_rs = reserve_words(static_cast<size_t>(h.num_positions) * n);
-        for (u32 pos = 0; pos < h.num_positions; ++pos)
-            std::copy(C->layout.rs[pos].begin(), C->layout.rs[pos].end(), img.begin() + h.off_rs + static_cast<size_t>(pos) * n);
-        {
-            std::vector<u32> so(C->mode == AtomMode::Dense ? 0 : C->layout.fluent_count);
-            for (size_t c = 0; c < so.size(); ++c)
-                so[c] = C->slot_of[c];
-            h.off_slot_of = put(so.data(), so.size() * sizeof(u32));
-        }
-        h.off_records = put(records.data(), records.size() * sizeof(u64));
+        h.num_decode = static_cast<u32>(decode.size());
+        h.decode_arith = decode_arith ? 1 : 0;
+        h.off_decode = put(decode.data(), decode.size() * sizeof(DevPredDecode));
         h.off_dom0 = put(dom0_words.data(), dom0_words.size() * sizeof(u64));
-        {
-            // static row tables back to back (n * ow words each); DevCons.table holds the table index, the kernel
-            // multiplies by n * ow
-            h.off_static_rows = img.size();
-            for (const auto& t : m_row_data)
-                img.insert(img.end(), t.begin(), t.end());
-        }
-        h.off_static_keys = put(static_key_words.data(), static_key_words.size() * sizeof(u64));
-        for (auto& meta : static_meta)
-            meta.keys += h.off_static_keys;
-        h.off_static_meta = put(static_meta.data(), static_meta.size() * sizeof(DevStaticMeta));
         h.off_goal_pos = put(C->goal_pos.data(), C->goal_pos.size() * sizeof(u32));
         h.off_goal_neg = put(C->goal_neg.data(), C->goal_neg.size() * sizeof(u32));
-        h.off_initial = put(C->initial.data(), C->initial.size() * sizeof(u64));
         {
             std::vector<u32> ar(m);
             for (u32 p = 0; p < m; ++p)
@@ -1294,6 +1319,31 @@ private:
                 offs[p] = C->layout.offset[p] == kNone64 ? 0 : C->layout.offset[p];
             h.off_pred_offset = put(offs.data(), offs.size() * sizeof(u64));
         }
+        h.hot_words = img.size();
+        // rs tables: per position n entries (u64)
+        h.num_positions = static_cast<u32>(C->layout.rs.size());
+        h.off_rs = reserve_words(static_cast<size_t>(h.num_positions) * n);
+        for (u32 pos = 0; pos < h.num_positions; ++pos)
+            std::copy(C->layout.rs[pos].begin(), C->layout.rs[pos].end(), img.begin() + h.off_rs + static_cast<size_t>(pos) * n);
+        {
+            std::vector<u32> so(C->mode == AtomMode::Dense ? 0 : C->layout.fluent_count);
+            for (size_t c = 0; c < so.size(); ++c)
+                so[c] = C->slot_of[c];
+            h.off_slot_of = put(so.data(), so.size() * sizeof(u32));
+        }
+        h.off_records = put(records.data(), records.size() * sizeof(u64));
+        {
+            // static row tables back to back (n * ow words each); DevCons.table holds the table index, the kernel
+            // multiplies by n * ow
+            h.off_static_rows = img.size();
+            for (const auto& t : m_row_data)
+                img.insert(img.end(), t.begin(), t.end());
+        }
+        h.off_static_keys = put(static_key_words.data(), static_key_words.size() * sizeof(u64));
+        for (auto& meta : static_meta)
+            meta.keys += h.off_static_keys;
+        h.off_static_meta = put(static_meta.data(), static_meta.size() * sizeof(DevStaticMeta));
+        h.off_initial = put(C->initial.data(), C->initial.size() * sizeof(u64));
         std::memcpy(img.data(), &h, sizeof(h));
         C->image = std::move(img);
     }

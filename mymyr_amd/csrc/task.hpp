@@ -188,6 +188,24 @@ struct DevPair
     u32 src_lo, src_n;   // source object window (rows)
     u32 dst_lo, dst_words;  // destination object window
     u32 offset;   // word offset of the pair's rows in the per-state view
+    u32 bulk;     // 1: row r is the state's bits [bit0 + r * row_bits, + row_bits) (dense slots, contiguous domains)
+    u64 bit0;     // bulk: first state bit of row 0
+    u32 row_bits; // bulk: bits per row (the destination domain's size)
+    u32 pad;
+};
+
+/// Slot decoding of a fluent predicate for the view build: a slot s in [offset, offset + size) is the atom with
+/// position ranks (s - offset) / d1 and (s - offset) % d1; with contiguous domains the objects are lo0 + r0, lo1 + r1.
+struct DevPredDecode
+{
+    u64 offset;
+    u64 size;
+    u32 pred;
+    u32 arity;
+    u32 d1;        // size of position 1's domain (1 for arity < 2)
+    u32 lo0, lo1;
+    u32 contiguous;  // every position's domain is a contiguous object range
+    u32 has_scatter; // some view pair of the predicate is built by scattering set bits
     u32 pad;
 };
 
@@ -212,7 +230,12 @@ struct DevTaskHeader
     u64 off_pred_arity, off_pos_begin;
     u64 off_pred_pairs;   // per predicate: view pair of the unary / forward rows (low 32 bits), backward (high)
     u64 off_pred_offset;  // per predicate: first canonical id (u64)
+    u64 off_decode;       // DevPredDecode per fluent predicate with atoms, ascending offset
+    u64 hot_words;        // the image's first hot_words words hold everything the kernels read per state
+                          // (staged in LDS); rs tables, slot tables, records, static rows and keys follow
     u32 num_positions;
+    u32 num_decode;
+    u32 decode_arith;     // 1: slots decode arithmetically (dense slots, contiguous domains)
     u32 init_count;     // successors of the initial state (filled once the device has counted them)
 };
 
