@@ -100,11 +100,14 @@ int mya_hashset_create(uint64_t max_states, uint32_t words, double max_load, uin
 void mya_hashset_free(mya_hashset* set);
 
 /* Inserts n rows (device). ids (device, optional) receives each row's state id (the first-inserted equal row's id:
- * smallest batch index wins within a batch, new ids in row order); is_new (device, optional) 1 for rows that added a
- * state. new_count (host, optional) receives the number of new states. Synchronizes the stream. */
+ * smallest batch index wins within a batch, new ids in row order; -1 for a row whose state did not fit); is_new
+ * (device, optional) 1 for rows that added a state. With new_count (host) the call synchronizes the stream, returns
+ * the number of new states and fails if the set overflowed; without it the insert is asynchronous and an overflow is
+ * reported by the next mya_hashset_size. A set that overflowed must be cleared. */
 int mya_hashset_insert(mya_hashset* set, const uint64_t* rows, uint64_t n, int64_t* ids, uint8_t* is_new,
                        uint64_t* new_count, void* stream);
-int mya_hashset_size(const mya_hashset* set, uint64_t* size);
+/* The number of stored states; waits for the set's last insert and fails if an insert overflowed the set. */
+int mya_hashset_size(mya_hashset* set, uint64_t* size);
 /* Device pointer to the stored rows [size, words] in id order. */
 int mya_hashset_rows(const mya_hashset* set, const uint64_t** rows);
 int mya_hashset_clear(mya_hashset* set, void* stream);
@@ -235,7 +238,7 @@ typedef struct mya_brfs_result
     int64_t first_goal; /* id of the first goal state tested (-1: none) */
     double search_s;    /* wall time of the whole call */
     double device_s;    /* wall time from the start state's insert to the end of the search */
-    /* per kernel class (0 count, 1 emit, 2 lookup, 3 probe, 4 rank, 5 compact, 6 other, 7 unused): summed HIP-event
+    /* per kernel class (0 count, 1 emit, 2 insert, 3 unused, 4 rank, 5 compact, 6 other, 7 unused): summed HIP-event
      * durations (with options.timings), algorithmic bytes and launches */
     double kernel_ms[8];
     uint64_t kernel_bytes[8];

@@ -5,11 +5,12 @@
 //                                   the expansion; a piecewise exclusive scan gives layer-relative successor offsets
 //   emit    (thread per parent)     each parent's successors in action order as (parent, action) records at its
 //                                   offsets: candidate index = order of first discovery (parent id, successor index)
-//   lookup  (thread per candidate)  successor row = parent row with the action's delete and add masks, its state hash,
-//                                   and a read-only probe of the stored states: a successor already stored is dropped
-//                                   here, the others (fresh) keep their row and hash at their candidate index
-//   probe / rank / compact          the state set's batch insert of the fresh candidates (the smallest candidate index
-//                                   wins among equal rows; new ids follow candidate order)
+//   insert  (group per candidate)   successor row = parent row with the action's delete and add masks, its state hash,
+//                                   and the state set's probe: a successor equal to a stored state is dropped, equal
+//                                   candidates keep the smallest index (rows of pending entries are recomputed from
+//                                   their records, never stored)
+//   rank / compact                  exclusive scan of the winner flags (new ids follow candidate order), winner rows
+//                                   into the arena and their table entries settled
 // The applicability test reads the parent from LDS byte planes (plane b holds byte b of every thread's row, so a
 // wave reads 64 consecutive bytes per test) and the action records through scalar loads, eight actions at a time:
 // an action with at most four positive preconditions, no negative one and no witness dominators is a single record
@@ -193,87 +194,68 @@ __global__ __launch_bounds__(kPB * kMaxSlices) void k_ground_emit(const u64* __r
     }
 }
 
+/// The successor rows of (parent, action) records as the row source of the state set's probe and compaction:
+/// candidate c's row = (parent row & ~delete mask) | add mask, recomputed wherever it is needed (the probe compares a
+/// pending entry against it, the compaction writes it), so candidate rows are never stored before they are new states.
 template<int W>
-__device__ __forceinline__ u64 hash_fixed(const u64 (&v)[W])
+struct ParentRows
 {
-    u32 n = W;
-#pragma unroll
-    for (int i = W - 1; i >= 0; --i)
-        if (n == static_cast<u32>(i + 1) && v[i] == 0)
-            n = i;
-    u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
-#pragma unroll
-    for (int i = 0; i < W; i += 2)
+    const u64* arena;
+    u64 first;            // arena id of the chunk's first parent (records hold the parent relative to it)
+    const u64* cand_pa;   // (parent << 32) | action
+    const u64* masks;     // [actions, 2W]: delete mask, then add mask
+    template<int G, int K>
+    __device__ __forceinline__ void load(u64 c, u32 q, Slice<G, K>& o) const
     {
-        if (static_cast<u32>(i + 1) < n)
-            h = mulfold(h ^ v[i] ^ kHashP1, v[i + 1] ^ kHashP2);
-        else if (static_cast<u32>(i) < n)
-            h = mulfold(h ^ v[i] ^ kHashP1, kHashP2);
-    }
-    return mix64(h);
-}
-
-/// Whether the set holds row v (hash h) as a stored state. Read-only: the table holds no pending entries between
-/// batches.
-template<int W>
-__device__ bool stored(const StateSetView& s, const u64 (&v)[W], u64 h)
-{
-    const u64 tag = h >> 32;
-    u64 slot = slot_of_hash(h, s.capacity);
-    for (u64 probes = 0; probes < s.capacity; ++probes)
-    {
-        const u64 e = s.table[slot];
-        if (e == 0)
-            return false;
-        const u32 code = static_cast<u32>(e);
-        if ((e >> 32) == tag && !(code & kPending))
-        {
-            const u64* o = s.arena + static_cast<u64>(code - 1) * W;
-            bool eq = true;
-#pragma unroll
-            for (int w = 0; w < W; ++w)
-                eq = eq && o[w] == v[w];
-            if (eq)
-                return true;
-        }
-        slot = slot + 1 == s.capacity ? 0 : slot + 1;
-    }
-    return false;
-}
-
-// Candidates [0, m): successor rows and hashes; fresh[j] = the row is not a stored state; fresh rows and hashes are
-// kept at their candidate index; *nfresh += the number of fresh candidates.
-template<int W>
-__global__ __launch_bounds__(kLB) void k_ground_lookup(StateSetView s, u64 first, const u64* __restrict__ cand_pa, u64 m,
-                                                      const u64* __restrict__ masks, u64* __restrict__ cand,
-                                                      u64* __restrict__ cand_hash, u8* __restrict__ fresh, u64* __restrict__ nfresh)
-{
-    const u64 j = static_cast<u64>(blockIdx.x) * kLB + threadIdx.x;
-    bool fr = false;
-    if (j < m)
-    {
-        const u64 pa = cand_pa[j];
-        const u64* row = s.arena + (first + (pa >> 32)) * W;
+        const u64 pa = cand_pa[c];
+        const u64* row = arena + (first + (pa >> 32)) * W;
         const u64* mk = masks + static_cast<u64>(static_cast<u32>(pa)) * (2 * W);
-        u64 v[W];
+        Slice<G, K> r, d, a;
+        load_row<G, K>(row, W, q, r);
+        load_row<G, K>(mk, W, q, d);
+        load_row<G, K>(mk + W, W, q, a);
 #pragma unroll
-        for (int w = 0; w < W; ++w)
-            v[w] = (row[w] & ~mk[w]) | mk[W + w];
-        const u64 h = hash_fixed<W>(v);
-        fr = !stored<W>(s, v, h);
-        fresh[j] = fr ? 1 : 0;
-        if (fr)
+        for (int k = 0; k < K; ++k)
         {
-            u64* dst = cand + j * W;
-#pragma unroll
-            for (int w = 0; w < W; ++w)
-                dst[w] = v[w];
-            cand_hash[j] = h;
+            o.lo[k] = (r.lo[k] & ~d.lo[k]) | a.lo[k];
+            o.hi[k] = (r.hi[k] & ~d.hi[k]) | a.hi[k];
         }
     }
-    const u64 c = static_cast<u64>(__popcll(__ballot(fr)));
-    if (lane_id() == 0 && c)
-        atomicAdd(reinterpret_cast<unsigned long long*>(nfresh), static_cast<unsigned long long>(c));
+};
+
+template<int W>
+constexpr int kGroup = W >= 2 ? W / 2 : 1;  // lanes per candidate row (16 bytes each)
+
+// Candidates [0, m) of a chunk into the state set: a group of lanes per candidate forms its row, hashes it and probes
+// the table (a stored equal row drops it; a pending equal row takes part in the smallest-index rule; an empty slot
+// takes it as pending).
+template<int W>
+__global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W> src, u64 m, u64* __restrict__ cand_slot,
+                                                      u32* __restrict__ flags, u32* __restrict__ status)
+{
+    constexpr int G = kGroup<W>;
+    const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
+    const u32 q = lane_id() % G, gbase = lane_id() - q;
+    if (j >= m)
+        return;
+    Slice<G, 1> me;
+    src.load(j, q, me);
+    const u64 h = group_hash<G, 1>(me, q, gbase);
+    probe_insert<G, 1>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
+}
+
+// The chunk's winners with ids below `limit` into the arena (rows recomputed from their records) and the table.
+template<int W>
+__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 m, const u64* __restrict__ cand_slot,
+                                                       u32* __restrict__ flags, const u64* __restrict__ offsets, u64 limit,
+                                                       u32* __restrict__ status)
+{
+    constexpr int G = kGroup<W>;
+    const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
+    const u32 q = lane_id() % G, gbase = lane_id() - q;
+    if (j >= m)
+        return;
+    compact_one<G, 1>(s, src, j, q, gbase, cand_slot, flags, offsets, limit, nullptr, status);
 }
 
 // The winner whose exclusive rank equals `rank`: its candidate index.
@@ -547,10 +529,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             dev_free(s);
         }
     } layer_guard{counts, goal_flags, offsets, scan_scratch};
-    u64* cand = b.alloc<u64>(chunk * W, "candidate rows");
-    u64* cand_hash = b.alloc<u64>(chunk, "candidate hashes");
     u64* cand_pa = b.alloc<u64>(chunk, "candidate records");
-    u8* fresh = b.alloc<u8>(chunk, "candidate fresh flags");
     u64* small = b.alloc<u64>(kSmall, "scalars");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
     enum
@@ -559,7 +538,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         kFirstGoal = 1, // first goal flag of a counted block
         kChunkP = 2,    // chunk end parent, then its offset
         kChunkOff = 3,
-        kFresh = 4,     // fresh candidates of the chunk
+        kSizeNow = 4,   // the set's size before the chunk's insert, then after it
+        kSizeNext = 8,
+        kSpare = 9,     // the capacity status of a cut chunk's compaction (expected there, not an error)
         kCut = 5,       // the candidate of the state that fills the store
         kBlockTotal = 6,
         kFingerprint = 7,
@@ -574,9 +555,10 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     {
         std::vector<u64> s0(W, 0);
         std::copy(task.initial.begin(), task.initial.end(), s0.begin());
-        hip_check(hipMemcpyAsync(cand, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
+        u64* d_s0 = b.alloc<u64>(W, "start state");
+        hip_check(hipMemcpyAsync(d_s0, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
         u64 nn = 0;
-        state_set_insert(set, cand, nullptr, 1, nullptr, nullptr, &nn, stream);
+        state_set_insert(set, d_s0, 1, nullptr, nullptr, &nn, stream);
     }
     const auto td0 = Clock::now();
     bool stopped = false, budget_stopped = false;
@@ -662,7 +644,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             const u64 p1 = b.host[kChunkP], end_off = b.host[kChunkOff];
             const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
-            u64 nfresh = 0, winners = 0;
+            u64 winners = 0;
+            const ParentRows<W> src{set.v.arena, layer_begin + p0, cand_pa, d_masks};
+            constexpr int G = kGroup<W>;
             if (m > 0)
             {
                 tm.begin(kKEmit);
@@ -670,45 +654,43 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                                    offsets + p0 * S, base, cand_pa);
                 launch_check("ground emit");
                 tm.end(kKEmit, np * (R + 8) + m * 8);
-                set_small(kFresh, 0);
-                tm.begin(kKLookup);
-                hipLaunchKernelGGL(k_ground_lookup<W>, dim3(blocks_for(m, kLB)), dim3(kLB), 0, stream, set.v, layer_begin + p0, cand_pa, m,
-                                   d_masks, cand, cand_hash, fresh, small + kFresh);
-                launch_check("ground lookup");
-                tm.end(kKLookup, 0);
-                tm.begin(kKProbe);
-                state_set_probe(set, cand, cand_hash, m, stream, fresh);
-                tm.end(kKProbe, 0);
+                tm.begin(kKInsert);
+                hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
+                                   set.flags, set.d_status);
+                launch_check("ground insert");
+                tm.end(kKInsert, 0);
                 tm.begin(kKRank);
                 state_set_rank(set, m, stream);
-                tm.end(kKRank, m * 24);
-                hip_check(hipMemcpyAsync(small + kBlockTotal, set.d_total, sizeof(u64), hipMemcpyDeviceToDevice, stream), "new");
+                tm.end(kKRank, m * 16);
+                hip_check(hipMemcpyAsync(small + kSizeNow, state_set_size_now(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
+                hip_check(hipMemcpyAsync(small + kSizeNext, state_set_size_next(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
                 hip_check(hipMemcpyAsync(small + kCut, set.d_status, sizeof(u32), hipMemcpyDeviceToDevice, stream), "status");
                 sync_small();
                 if (static_cast<u32>(b.host[kCut]) & kStatusTableFull)
                     throw std::length_error("mymyr_amd: brfs: state table full");
-                nfresh = b.host[kFresh];
-                winners = b.host[kBlockTotal];
-                // lookup: records, table entries and flags of every candidate, parent rows, the stored row each dropped
-                // candidate matched, fresh rows and hashes; probe: the fresh candidates' rows, hashes, entries and slots,
-                // and the pending row each non-winner matched
-                tm.bytes(kKLookup, m * 17 + u64{np} * R + (m - nfresh) * R + nfresh * (R + 8));
-                tm.bytes(kKProbe, nfresh * (R + 24) + (nfresh - winners) * R);
+                winners = b.host[kSizeNext] - b.host[kSizeNow];
+                // insert: every candidate's record, its probe entry and its slot, the parent rows, and the row each
+                // non-winner compared equal to
+                tm.bytes(kKInsert, m * 24 + u64{np} * R + (m - winners) * R);
             }
             const u64 room = (bounded ? o.max_states : cap_states) - set.size;
             if (winners >= room && winners > 0 && bounded)
             {
-                // the store fills at the winner of rank room - 1: stop inside its parent's expansion
+                // the store fills at the winner of id max_states - 1: stop inside its parent's expansion
                 set_small(kCut, ~u64{0});
-                hipLaunchKernelGGL(k_find_rank, dim3(blocks_for(m, 256)), dim3(256), 0, stream, set.flags, set.offsets, m, room - 1, small + kCut);
+                hipLaunchKernelGGL(k_find_rank, dim3(blocks_for(m, 256)), dim3(256), 0, stream, set.flags, set.offsets, m, o.max_states - 1,
+                                   small + kCut);
                 sync_small();
                 const u64 jcut = b.host[kCut];
                 hip_check(hipMemcpyAsync(b.host + kCut, cand_pa + jcut, sizeof(u64), hipMemcpyDeviceToHost, stream), "parent");
                 hip_check(hipStreamSynchronize(stream), "sync");
                 const u64 pc = b.host[kCut] >> 32;  // the parent, relative to p0
                 tm.begin(kKCompact);
-                state_set_compact(set, cand, cand_hash, m, set.size, o.max_states, nullptr, nullptr, stream);
-                tm.end(kKCompact, m * 12 + room * (2 * R + 24));
+                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
+                                   set.flags, set.offsets, o.max_states, reinterpret_cast<u32*>(small + kSpare));
+                launch_check("ground compact");
+                tm.end(kKCompact, m * 12 + room * (2 * R + 16));
+                state_set_flip(set);
                 row[0] += pc + 1;
                 row[1] += jcut + 1;
                 hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pc + 1, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, pc + 1,
@@ -724,8 +706,12 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             if (m > 0)
             {
                 tm.begin(kKCompact);
-                state_set_compact(set, cand, cand_hash, m, set.size, cap_states, nullptr, nullptr, stream);
-                tm.end(kKCompact, m * 12 + winners * (2 * R + 24));
+                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
+                                   set.flags, set.offsets, cap_states, set.d_status);
+                launch_check("ground compact");
+                // flags, ids and slots of every candidate; the winners' records, parent rows (in L2), arena rows and entries
+                tm.end(kKCompact, m * 12 + winners * (2 * R + 16));
+                state_set_flip(set);
             }
             set.size += winners;
             row[0] += np;

@@ -32,8 +32,8 @@ enum BrfsKernel : int
 {
     kKCount = 0,    // applicability counts and goal flags of a block of parents
     kKEmit = 1,     // (parent, action) records of the successors, in candidate order
-    kKLookup = 2,   // successor rows and hashes; read-only probe of the stored states; fresh rows kept
-    kKProbe = 3,    // state-set probe of the fresh candidates with the min-candidate winner
+    kKInsert = 2,   // successor rows, hashes and the state-set probe (stored and pending equals, min-candidate winner)
+    kKUnused = 3,
     kKRank = 4,     // winner flags and their exclusive scan
     kKCompact = 5,  // new states into the arena and the table
     kKOther = 6,    // scans of counts, goal searches, chunk bounds, fingerprint

@@ -220,15 +220,16 @@ int mya_hashset_insert(mya_hashset* set, const uint64_t* rows, uint64_t n, int64
     return guarded([&] {
         if (!set || (n && !rows))
             throw std::invalid_argument("mymyr_amd: hashset_insert: null argument");
-        state_set_insert(set->set, rows, nullptr, n, ids, is_new, new_count, static_cast<hipStream_t>(stream));
+        state_set_insert(set->set, rows, n, ids, is_new, new_count, static_cast<hipStream_t>(stream));
     });
 }
 
-int mya_hashset_size(const mya_hashset* set, uint64_t* size)
+int mya_hashset_size(mya_hashset* set, uint64_t* size)
 {
     return guarded([&] {
         if (!set || !size)
             throw std::invalid_argument("mymyr_amd: hashset_size: null argument");
+        state_set_sync(set->set);
         *size = set->set.size;
     });
 }

@@ -1,7 +1,6 @@
-// Device state set (state_set.hpp): row hashing, CAS probing with a min-candidate winner, ranking, compaction.
+// Device state set (state_set.hpp): the batch insert of rows held in a buffer, row hashing, the dedup stream.
 
 #include "runtime.hpp"
-#include "scan.hpp"
 #include "state_set.hpp"
 
 #include <algorithm>
@@ -11,119 +10,73 @@ namespace mya
 {
 namespace
 {
-constexpr u64 kDupSettled = u64{1} << 63;
-constexpr u64 kProbeFailed = ~u64{0};
-constexpr u64 kProbeSkipped = ~u64{0} - 1;  // a candidate outside the probe mask
 constexpr int kBlock = 256;
 
-
-__device__ __forceinline__ bool rows_equal(const u64* __restrict__ a, const u64* __restrict__ b, u32 w)
+/// Rows of a device buffer as the row source of the probe and the compaction.
+struct BufferRows
 {
-    for (u32 i = 0; i < w; ++i)
-        if (a[i] != b[i])
-            return false;
-    return true;
+    const u64* rows;
+    u32 W;
+    template<int G, int K>
+    __device__ __forceinline__ void load(u64 c, u32 q, Slice<G, K>& o) const
+    {
+        load_row<G, K>(rows + c * W, W, q, o);
+    }
+};
+
+/// The group of this lane: (candidate, lane in group, first lane of the group in the wave).
+template<int G>
+__device__ __forceinline__ void group_of(u64& j, u32& q, u32& gbase)
+{
+    const u64 t = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    const u32 lane = lane_id();
+    j = t / G;
+    q = lane % G;
+    gbase = lane - q;
 }
 
+template<int G, int K>
 __global__ __launch_bounds__(kBlock) void k_hash_rows(const u64* __restrict__ rows, u64 n, u32 words, u64* __restrict__ out)
 {
-    const u64 i = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= n)
-        return;
-    out[i] = hash_state(rows + i * words, words);
-}
-
-__global__ __launch_bounds__(kBlock) void k_probe(StateSetView s, const u64* __restrict__ rows, const u64* __restrict__ hashes,
-                                                 const u8* __restrict__ mask, u64 n, u64* __restrict__ cand_slot,
-                                                 u32* __restrict__ status)
-{
-    const u64 j = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    u64 j;
+    u32 q, gbase;
+    group_of<G>(j, q, gbase);
     if (j >= n)
         return;
-    if (mask && !mask[j])
-    {
-        cand_slot[j] = kProbeSkipped;
-        return;
-    }
-    const u64 h = hashes[j];
-    const u64 tag = h >> 32;
-    const u32 W = s.words;
-    const u64* row = rows + j * W;
-    u64 slot = slot_of_hash(h, s.capacity);
-    for (u64 probes = 0; probes < s.capacity; ++probes)
-    {
-        u64 e = __hip_atomic_load(s.table + slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (e == 0)
-        {
-            const u64 mine = (tag << 32) | kPending | j;
-            const u64 old = atomicCAS(reinterpret_cast<unsigned long long*>(s.table + slot), 0ull, static_cast<unsigned long long>(mine));
-            if (old == 0)
-            {
-                cand_slot[j] = slot;
-                return;
-            }
-            e = old;
-        }
-        if ((e >> 32) == tag)
-        {
-            const u32 code = static_cast<u32>(e);
-            const bool pending = (code & kPending) != 0;
-            const u64* other = pending ? rows + static_cast<u64>(code & ~kPending) * W : s.arena + static_cast<u64>(code - 1) * W;
-            if (rows_equal(row, other, W))
-            {
-                if (pending)
-                {
-                    atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>((tag << 32) | kPending | j));
-                    cand_slot[j] = slot;
-                }
-                else
-                    cand_slot[j] = slot | kDupSettled;
-                return;
-            }
-        }
-        slot = slot + 1 == s.capacity ? 0 : slot + 1;
-    }
-    atomicOr(status, kStatusTableFull);
-    cand_slot[j] = kProbeFailed;
+    Slice<G, K> r;
+    load_row<G, K>(rows + j * words, words, q, r);
+    const u64 h = group_hash<G, K>(r, q, gbase);
+    if (q == 0)
+        out[j] = h;
 }
 
-__global__ __launch_bounds__(kBlock) void k_flags(StateSetView s, const u64* __restrict__ cand_slot, u64 n, u32* __restrict__ flags)
+template<int G, int K>
+__global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __restrict__ rows, u64 n, u64* __restrict__ cand_slot,
+                                                  u32* __restrict__ flags, u32* __restrict__ status)
 {
-    const u64 j = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    u64 j;
+    u32 q, gbase;
+    group_of<G>(j, q, gbase);
     if (j >= n)
         return;
-    const u64 cs = cand_slot[j];
-    u32 win = 0;
-    if (cs < kProbeSkipped && !(cs & kDupSettled))
-        win = static_cast<u32>(s.table[cs]) == (kPending | static_cast<u32>(j)) ? 1u : 0u;
-    flags[j] = win;
+    const BufferRows src{rows, s.words};
+    Slice<G, K> me;
+    src.load(j, q, me);
+    const u64 h = group_hash<G, K>(me, q, gbase);
+    probe_insert<G, K>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
 }
 
-__global__ __launch_bounds__(kBlock) void k_compact(StateSetView s, const u64* __restrict__ rows, const u64* __restrict__ hashes,
-                                                   const u64* __restrict__ cand_slot, const u32* __restrict__ flags,
-                                                   const u64* __restrict__ offsets, u64 n, u64 base, u64 limit, u8* __restrict__ is_new)
+template<int G, int K>
+__global__ __launch_bounds__(kBlock) void k_compact(StateSetView s, const u64* __restrict__ rows, u64 n, const u64* __restrict__ cand_slot,
+                                                   u32* __restrict__ flags, const u64* __restrict__ offsets, u64 limit,
+                                                   u8* __restrict__ is_new, u32* __restrict__ status)
 {
-    const u64 j = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    u64 j;
+    u32 q, gbase;
+    group_of<G>(j, q, gbase);
     if (j >= n)
         return;
-    const bool win = flags[j] != 0;
-    if (is_new)
-        is_new[j] = 0;
-    if (!win)
-        return;
-    const u64 id = base + offsets[j];
-    if (id >= limit)
-        return;
-    const u32 W = s.words;
-    const u64* src = rows + j * W;
-    u64* dst = s.arena + id * W;
-    for (u32 i = 0; i < W; ++i)
-        dst[i] = src[i];
-    const u64 h = hashes[j];
-    s.hashes[id] = h;
-    s.table[cand_slot[j]] = ((h >> 32) << 32) | static_cast<u32>(id + 1);
-    if (is_new)
-        is_new[j] = 1;
+    compact_one<G, K>(s, BufferRows{rows, s.words}, j, q, gbase, cand_slot, flags, offsets, limit, is_new, status);
 }
 
 __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u64* __restrict__ cand_slot, u64 n, i64* __restrict__ ids)
@@ -132,14 +85,32 @@ __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u6
     if (j >= n)
         return;
     const u64 cs = cand_slot[j];
-    if (cs >= kProbeSkipped)
+    i64 id = -1;
+    if (cs == kProbeFailed)
+        id = -1;
+    else if (cand_is_stored(cs))
+        id = static_cast<i64>(cs >> 32);
+    else
     {
-        ids[j] = -1;
-        return;
+        const u32 code = static_cast<u32>(s.table[static_cast<u32>(cs)]);
+        id = (code & kPending) ? -1 : static_cast<i64>(code) - 1;
     }
-    const u32 code = static_cast<u32>(s.table[cs & ~kDupSettled]);
-    ids[j] = (code & kPending) ? -1 : static_cast<i64>(code) - 1;
+    ids[j] = id;
 }
+
+__global__ __launch_bounds__(kBlock) void k_fill_u32(u32* __restrict__ p, u64 n, u32 v)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += static_cast<u64>(gridDim.x) * kBlock)
+        p[i] = v;
+}
+
+__global__ void k_set_words(u64* p, u64 a, u64 b, u32* status)
+{
+    p[0] = a;
+    p[1] = b;
+    *status = 0;
+}
+
 // The dedup stream: row i is, with probability `dup` (i > 0), an exact copy of row src(i) < i, else fresh words
 // mix64(seed + (16 i + k + 1) * gamma). Counter-based, so any range of rows is generated independently.
 constexpr u64 kGamma = 0x9E3779B97F4A7C15ULL;
@@ -148,24 +119,66 @@ constexpr u64 kSrcKey = 0x8CB92BA72F3D8DD7ULL;
 
 __global__ __launch_bounds__(kBlock) void k_dedup_rows(u64 start, u64 count, u32 words, u64 seed, u64 thr, u64* __restrict__ out)
 {
-    const u64 j = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    const u64 t = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    const u64 j = t / words;
+    const u32 k = static_cast<u32>(t - j * words);
     if (j >= count)
         return;
     u64 cur = start + j;
     while (cur > 0 && (mix64((seed ^ kDupKey) ^ (cur * kGamma)) >> 32) < thr)
         cur = ((mix64((seed ^ kSrcKey) ^ (cur * kGamma)) & 0xFFFFFFFFull) * cur) >> 32;
-    u64* row = out + j * words;
-    for (u32 k = 0; k < words; ++k)
-        row[k] = mix64(seed + (cur * 16 + k + 1) * kGamma);
+    out[t] = mix64(seed + (cur * 16 + k + 1) * kGamma);
+}
+
+/// Calls f.template operator()<G, K>() for the lane-group shape of rows of W words.
+template<class F>
+void with_shape(u32 W, F&& f)
+{
+    if (W <= 2)
+        f.template operator()<1, 1>();
+    else if (W <= 4)
+        f.template operator()<2, 1>();
+    else if (W <= 8)
+        f.template operator()<4, 1>();
+    else if (W <= 16)
+        f.template operator()<8, 1>();
+    else if (W <= 32)
+        f.template operator()<16, 1>();
+    else if (W <= 128)
+        f.template operator()<64, 1>();
+    else if (W <= 256)
+        f.template operator()<64, 2>();
+    else if (W <= 512)
+        f.template operator()<64, 4>();
+    else if (W <= 1024)
+        f.template operator()<64, 8>();
+    else if (W <= 2048)
+        f.template operator()<64, 16>();
+    else
+        throw std::invalid_argument("mymyr_amd: state set rows hold at most 2048 words");
+}
+
+template<int G>
+unsigned group_blocks(u64 n)
+{
+    return blocks_for(n * G, kBlock);
 }
 }  // namespace
+
+void launch_fill_u32(u32* p, u64 n, u32 v, hipStream_t stream)
+{
+    if (n == 0)
+        return;
+    hipLaunchKernelGGL(k_fill_u32, dim3(std::min<u64>(blocks_for(n, kBlock), 8192)), dim3(kBlock), 0, stream, p, n, v);
+    launch_check("fill");
+}
 
 void launch_dedup_rows(u64 start, u64 count, u32 words, u64 seed, double dup, u64* out, hipStream_t stream)
 {
     if (count == 0)
         return;
     const u64 thr = static_cast<u64>(dup * 4294967296.0);
-    hipLaunchKernelGGL(k_dedup_rows, dim3(blocks_for(count, kBlock)), dim3(kBlock), 0, stream, start, count, words, seed, thr, out);
+    hipLaunchKernelGGL(k_dedup_rows, dim3(blocks_for(count * words, kBlock)), dim3(kBlock), 0, stream, start, count, words, seed, thr, out);
     launch_check("dedup rows");
 }
 
@@ -173,7 +186,9 @@ void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t s
 {
     if (n == 0)
         return;
-    hipLaunchKernelGGL(k_hash_rows, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, rows, n, words, out);
+    with_shape(words, [&]<int G, int K>() {
+        hipLaunchKernelGGL((k_hash_rows<G, K>), dim3(group_blocks<G>(n)), dim3(kBlock), 0, stream, rows, n, words, out);
+    });
     launch_check("hash_rows");
 }
 
@@ -181,42 +196,45 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
 {
     if (words == 0)
         throw std::invalid_argument("mymyr_amd: state set rows need at least one word");
+    if (words > 2048)
+        throw std::invalid_argument("mymyr_amd: state set rows hold at most 2048 words");
     if (!(max_load > 0.0 && max_load <= 0.95))
         throw std::invalid_argument("mymyr_amd: state set load must be in (0, 0.95]");
     if (max_states >= (u64{1} << 31) - 1)
         throw std::invalid_argument("mymyr_amd: state set holds at most 2^31 - 2 states");
+    if (batch_cap >= (u64{1} << 31))
+        throw std::invalid_argument("mymyr_amd: state set batches hold fewer than 2^31 rows");
     const u64 cap = std::max<u64>(64, static_cast<u64>(std::ceil(static_cast<double>(max_states + pending) / max_load)));
-    if (cap >= (u64{1} << 32))
-        throw std::invalid_argument("mymyr_amd: state set table capacity above 2^32 slots");
+    if (cap >= (u64{1} << 32) - 1)
+        throw std::invalid_argument("mymyr_amd: state set table capacity above 2^32 - 2 slots");
     s.v.words = words;
     s.v.capacity = cap;
     s.max_states = max_states;
     s.batch_cap = std::max<u64>(1, batch_cap);
     s.v.table = dev_alloc<u64>(cap, "state set table");
     s.v.arena = dev_alloc<u64>(max_states * words, "state set arena");
-    s.v.hashes = dev_alloc<u64>(max_states, "state set hashes");
     s.cand_slot = dev_alloc<u64>(s.batch_cap, "state set batch slots");
     s.flags = dev_alloc<u32>(s.batch_cap, "state set batch flags");
     s.offsets = dev_alloc<u64>(s.batch_cap, "state set batch offsets");
-    s.hashes_tmp = dev_alloc<u64>(s.batch_cap, "state set batch hashes");
     s.scan_scratch = dev_alloc<u64>(scan_scratch_words(s.batch_cap), "state set scan scratch");
-    s.d_total = dev_alloc<u64>(2, "state set totals");
+    s.d_size = dev_alloc<u64>(2, "state set size");
     s.d_status = dev_alloc<u32>(1, "state set status");
-    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s.h_pinned), sizeof(u64) * 2, hipHostMallocDefault), "pinned count");
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s.h_pinned), sizeof(u64) * 4, hipHostMallocDefault), "pinned words");
+    launch_fill_u32(s.flags, s.batch_cap, 1, stream);
     state_set_clear(s, stream);
 }
 
 void state_set_destroy(StateSet& s)
 {
+    if (s.last)
+        (void)hipStreamSynchronize(s.last);
     dev_free(s.v.table);
     dev_free(s.v.arena);
-    dev_free(s.v.hashes);
     dev_free(s.cand_slot);
     dev_free(s.flags);
     dev_free(s.offsets);
-    dev_free(s.hashes_tmp);
     dev_free(s.scan_scratch);
-    dev_free(s.d_total);
+    dev_free(s.d_size);
     dev_free(s.d_status);
     if (s.h_pinned)
         (void)hipHostFree(s.h_pinned);
@@ -226,77 +244,64 @@ void state_set_destroy(StateSet& s)
 void state_set_clear(StateSet& s, hipStream_t stream)
 {
     hip_check(hipMemsetAsync(s.v.table, 0, s.v.capacity * sizeof(u64), stream), "clear state set");
-    hip_check(hipMemsetAsync(s.d_status, 0, sizeof(u32), stream), "clear state set status");
+    hipLaunchKernelGGL(k_set_words, dim3(1), dim3(1), 0, stream, s.d_size, u64{0}, u64{0}, s.d_status);
+    launch_check("clear state set");
+    s.cur = 0;
     s.size = 0;
-}
-
-void state_set_probe(StateSet& s, const u64* rows, const u64* hashes, u64 n, hipStream_t stream, const u8* mask)
-{
-    if (n == 0)
-        return;
-    hipLaunchKernelGGL(k_probe, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, rows, hashes, mask, n, s.cand_slot,
-                       s.d_status);
-    launch_check("state set probe");
+    s.last = stream;
 }
 
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream)
 {
-    if (n == 0)
-    {
-        hip_check(hipMemsetAsync(s.d_total, 0, sizeof(u64), stream), "rank");
-        return;
-    }
-    hipLaunchKernelGGL(k_flags, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, s.cand_slot, n, s.flags);
-    launch_check("state set flags");
-    launch_exclusive_scan(s.flags, s.offsets, n, s.scan_scratch, s.d_total, stream);
-    launch_check("state set scan");
+    launch_exclusive_scan(s.flags, s.offsets, n, s.scan_scratch, state_set_size_next(s), stream, state_set_size_now(s));
+    launch_check("state set rank");
 }
 
-void state_set_compact(StateSet& s, const u64* rows, const u64* hashes, u64 n, u64 base, u64 limit, i64* ids, u8* is_new,
-                       hipStream_t stream)
+void state_set_sync(StateSet& s)
 {
-    if (n == 0)
-        return;
-    hipLaunchKernelGGL(k_compact, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, rows, hashes, s.cand_slot, s.flags,
-                       s.offsets, n, base, limit, is_new);
-    launch_check("state set compact");
-    if (ids)
-    {
-        hipLaunchKernelGGL(k_resolve_ids, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, s.cand_slot, n, ids);
-        launch_check("state set ids");
-    }
+    hip_check(hipStreamSynchronize(s.last), "state set");
+    const u32 status = static_cast<u32>(s.h_pinned[2]);
+    const u64 after = s.h_pinned[1];
+    s.size = std::min(after, s.max_states);
+    if (status & kStatusTableFull)
+        throw std::length_error("mymyr_amd: state set table full");
+    if (status & kStatusCapacity)
+        throw std::length_error("mymyr_amd: state set full (" + std::to_string(s.max_states) + " states; the inserts needed " +
+                                std::to_string(after) + ")");
 }
 
-void state_set_insert(StateSet& s, const u64* rows, const u64* hashes, u64 n, i64* ids, u8* is_new, u64* new_count,
-                      hipStream_t stream)
+void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new, u64* new_count, hipStream_t stream)
 {
-    u64 done = 0, added = 0;
-    while (done < n)
-    {
-        const u64 m = std::min(n - done, s.batch_cap);
-        if (s.size + m > s.max_states)
-            throw std::length_error("mymyr_amd: state set full (" + std::to_string(s.size) + " of " + std::to_string(s.max_states) +
-                                    " states; the batch could add " + std::to_string(m) + ")");
-        const u64* r = rows + done * s.v.words;
-        const u64* h = hashes ? hashes + done : s.hashes_tmp;
-        if (!hashes)
-            launch_hash_rows(r, m, s.v.words, s.hashes_tmp, stream);
-        state_set_probe(s, r, h, m, stream);
-        state_set_rank(s, m, stream);
-        state_set_compact(s, r, h, m, s.size, s.max_states, ids ? ids + done : nullptr, is_new ? is_new + done : nullptr, stream);
-        hip_check(hipMemcpyAsync(s.h_pinned, s.d_total, sizeof(u64), hipMemcpyDeviceToHost, stream), "read new count");
-        u32 status = 0;
-        hip_check(hipMemcpyAsync(reinterpret_cast<u32*>(s.h_pinned + 1), s.d_status, sizeof(u32), hipMemcpyDeviceToHost, stream),
-                  "read status");
-        hip_check(hipStreamSynchronize(stream), "state set insert");
-        status = *reinterpret_cast<u32*>(s.h_pinned + 1);
-        if (status & kStatusTableFull)
-            throw std::length_error("mymyr_amd: state set table full");
-        s.size += s.h_pinned[0];
-        added += s.h_pinned[0];
-        done += m;
-    }
+    const u32 W = s.v.words;
+    hip_check(hipMemcpyAsync(s.h_pinned, state_set_size_now(s), sizeof(u64), hipMemcpyDeviceToHost, stream), "read size");
+    with_shape(W, [&]<int G, int K>() {
+        for (u64 done = 0; done < n;)
+        {
+            const u64 m = std::min(n - done, s.batch_cap);
+            const u64* r = rows + done * W;
+            hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, s.cand_slot, s.flags,
+                               s.d_status);
+            launch_check("state set probe");
+            state_set_rank(s, m, stream);
+            hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, s.cand_slot, s.flags,
+                               s.offsets, s.max_states, is_new ? is_new + done : nullptr, s.d_status);
+            launch_check("state set compact");
+            if (ids)
+            {
+                hipLaunchKernelGGL(k_resolve_ids, dim3(blocks_for(m, kBlock)), dim3(kBlock), 0, stream, s.v, s.cand_slot, m, ids + done);
+                launch_check("state set ids");
+            }
+            state_set_flip(s);
+            done += m;
+        }
+    });
+    hip_check(hipMemcpyAsync(s.h_pinned + 1, state_set_size_now(s), sizeof(u64), hipMemcpyDeviceToHost, stream), "read size");
+    hip_check(hipMemcpyAsync(s.h_pinned + 2, s.d_status, sizeof(u32), hipMemcpyDeviceToHost, stream), "read status");
+    s.last = stream;
     if (new_count)
-        *new_count = added;
+    {
+        state_set_sync(s);
+        *new_count = s.h_pinned[1] - s.h_pinned[0];
+    }
 }
 }  // namespace mya

@@ -7,40 +7,34 @@
 // candidate index wins (64-bit atomicMin on the pending entry), and new ids follow candidate order (an exclusive scan
 // of the winner flags). The probe hash is the public state hash (hash_state); slot = fastrange of its low 32 bits over
 // the capacity, tag = its high 32 bits, linear probing.
+//
+// A batch is three launches on one stream: probe (group of lanes per row: hash, probe, CAS or atomicMin, loser
+// flags), the exclusive scan of the winner flags (ids = the set's size + rank), and compaction (winner rows into the
+// arena, entries settled). The set's size lives on the device in two words used alternately (the scan of a batch
+// writes next = current + winners), so batches need no host synchronization; the host copy is refreshed by the
+// calls that synchronize.
 
-#include "device_common.hpp"
+#include "state_set_device.hpp"
+
+#include <hip/hip_runtime.h>
 
 namespace mya
 {
-constexpr u32 kPending = 0x80000000u;
-
-/// Slot of a state hash: fastrange of its low 32 bits over the capacity (the tag is the high 32 bits).
-__host__ __device__ inline u64 slot_of_hash(u64 h, u64 cap) { return ((h & 0xFFFFFFFFull) * cap) >> 32; }
-
-struct StateSetView
-{
-    u64* table;
-    u64 capacity;
-    u64* arena;   // [max_states, W]
-    u64* hashes;  // [max_states]
-    u32 words;
-};
-
 struct StateSet
 {
     StateSetView v{};
     u64 max_states = 0;
-    u64 size = 0;  // host copy, updated by insert
-    // batch scratch
+    u64 size = 0;       // host copy of the size (exact after a synchronizing call)
     u64 batch_cap = 0;
-    u64* cand_slot = nullptr;  // [batch_cap]
-    u32* flags = nullptr;      // [batch_cap]
-    u64* offsets = nullptr;    // [batch_cap]
-    u64* hashes_tmp = nullptr; // [batch_cap]
+    u64* cand_slot = nullptr;  // [batch_cap] probe result per candidate (state_set_device.hpp encodings)
+    u32* flags = nullptr;      // [batch_cap] winner flags, 1 at rest
+    u64* offsets = nullptr;    // [batch_cap] ids of the winners (size + exclusive rank)
     u64* scan_scratch = nullptr;
-    u64* d_total = nullptr;    // [2]: new count, spare
-    u32* d_status = nullptr;
-    u64* h_pinned = nullptr;   // pinned host word for the new count
+    u64* d_size = nullptr;     // [2] the size, alternating per batch
+    u32* d_status = nullptr;   // sticky kStatus* bits
+    u64* h_pinned = nullptr;   // [4] size before, size after, status of the last insert
+    int cur = 0;               // d_size[cur] is the current size
+    hipStream_t last = nullptr;
 };
 
 /// Allocates a set for up to max_states rows of `words` words at the given maximum load: capacity =
@@ -52,23 +46,29 @@ void state_set_destroy(StateSet& s);
 /// Clears the set (size 0) without freeing.
 void state_set_clear(StateSet& s, hipStream_t stream);
 
-/// Inserts rows [n, W] (device). hashes: the rows' state hashes (device, optional: computed when null). Optional
-/// outputs: ids [n] (i64 id of each row's state), is_new [n]. new_count: host out (synchronizes the stream).
-/// Throws on capacity overflow (the set is left with the rows it had).
-void state_set_insert(StateSet& s, const u64* rows, const u64* hashes, u64 n, i64* ids, u8* is_new, u64* new_count,
-                      hipStream_t stream);
+/// Inserts rows [n, W] (device), in batches of at most batch_cap rows, asynchronously on the stream. Optional outputs:
+/// ids [n] (i64 id of each row's state; -1 for a row past the capacity), is_new [n]. With new_count (host) the call
+/// synchronizes and returns the number of new states, throwing on a full set or table. Without it, a capacity
+/// overflow is reported by the next synchronizing call (state_set_sync); the set must then be cleared.
+void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new, u64* new_count, hipStream_t stream);
 
-/// Launch pieces of an insert for drivers that keep the batch on the device (BrFS): probe (after which winners are
-/// those whose entry holds their candidate), flags + scan, and compaction at base id `base`. Candidate rows and
-/// hashes stay readable until compaction ends. With `mask` (device, optional) the probe takes only the candidates j
-/// with mask[j] != 0; the others are neither inserted nor winners (their rows and hashes are not read).
-void state_set_probe(StateSet& s, const u64* rows, const u64* hashes, u64 n, hipStream_t stream, const u8* mask = nullptr);
-void state_set_rank(StateSet& s, u64 n, hipStream_t stream);  // d_total[0] = winners
-void state_set_compact(StateSet& s, const u64* rows, const u64* hashes, u64 n, u64 base, u64 limit, i64* ids, u8* is_new,
-                       hipStream_t stream);
+/// Waits for the set's last insert and refreshes s.size; throws if a batch overflowed the set or its table.
+void state_set_sync(StateSet& s);
 
-/// hash_state of every row (thread per row).
+/// Device words of the current and the next size, for drivers that run their own probe and compaction kernels: the
+/// scan of a batch reads the current size and writes the next; state_set_flip then makes the next current.
+inline u64* state_set_size_now(StateSet& s) { return s.d_size + s.cur; }
+inline u64* state_set_size_next(StateSet& s) { return s.d_size + (s.cur ^ 1); }
+inline void state_set_flip(StateSet& s) { s.cur ^= 1; }
+
+/// The winner scan of a batch of n candidates: offsets[j] = size + rank of winner j; next size = size + winners.
+void state_set_rank(StateSet& s, u64 n, hipStream_t stream);
+
+/// hash_state of every row (a group of lanes per row).
 void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t stream);
+
+/// Fills n u32 words with v.
+void launch_fill_u32(u32* p, u64 n, u32 v, hipStream_t stream);
 
 /// Rows [start, start + count) of the seeded dedup stream (the dedup workload's synthetic input).
 void launch_dedup_rows(u64 start, u64 count, u32 words, u64 seed, double dup, u64* out, hipStream_t stream);

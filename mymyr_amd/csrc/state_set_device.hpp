@@ -1,0 +1,275 @@
+#pragma once
+// Device building blocks of the state set, shared by the generic batch insert (rows in a buffer) and the BrFS insert
+// (rows recomputed from (parent, action) records): a row is handled by a group of G lanes, lane q of the group holding
+// the word pairs p = k * G + q (k < K) of the row as (word 2p, word 2p + 1). A random row access is then one
+// coalesced request of the whole group, and the group's lanes follow one control path (every branch depends on
+// group-uniform values only).
+//
+// The state hash is the public hash_state (include/mymyr/core/hash.hpp:38-60) over the trimmed words, chained over the
+// pairs in order with the pair broadcast from its lane; the table probe keeps the reference's id rule
+// (include/mymyr/cuda/state_set.hpp:2-18): among equal candidates the smallest candidate index wins (64-bit atomicMin
+// on the pending entry), new ids follow candidate order.
+//
+// Winner flags need no second pass over the table: every candidate starts at flag 1 (set by the previous kernel on
+// the stream), and only zeros are written during the probe: a candidate equal to a stored state, and the larger
+// index of every atomicMin exchange between two pending candidates. Every candidate but the smallest of its
+// content is the larger index of exactly one exchange, so the flags that stay 1 are exactly the winners. Rows of
+// other candidates are never read back from memory written in the same kernel (a row source recomputes them), so no
+// release fence is needed between a row write and the entry that publishes it.
+
+#include "device_common.hpp"
+#include "scan.hpp"
+
+namespace mya
+{
+constexpr u32 kPending = 0x80000000u;
+constexpr u32 kNoSlot = 0xFFFFFFFFu;
+constexpr u64 kProbeFailed = ~u64{0};
+
+/// Slot of a state hash: fastrange of its low 32 bits over the capacity (the tag is the high 32 bits).
+__host__ __device__ inline u64 slot_of_hash(u64 h, u64 cap) { return ((h & 0xFFFFFFFFull) * cap) >> 32; }
+
+struct StateSetView
+{
+    u64* table;
+    u64 capacity;
+    u64* arena;  // [max_states, words]
+    u32 words;
+};
+
+/// cand_slot encodings written by the probe: (tag << 32) | slot for a candidate that holds or held a pending entry;
+/// (id << 32) | kNoSlot for a candidate equal to the stored state `id`; kProbeFailed when the table was full.
+__host__ __device__ inline bool cand_is_stored(u64 cs) { return static_cast<u32>(cs) == kNoSlot; }
+
+template<int G, int K>
+struct Slice
+{
+    u64 lo[K], hi[K];  // pair k * G + q: words 2p (lo) and 2p + 1 (hi)
+};
+
+/// Lane q's words of a row of W words (zeros past W).
+template<int G, int K>
+__device__ __forceinline__ void load_row(const u64* __restrict__ row, u32 W, u32 q, Slice<G, K>& s)
+{
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+    {
+        const u32 w = 2 * (k * G + q);
+        if (w + 1 < W && (W & 1) == 0)
+        {
+            const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(row + w);
+            s.lo[k] = v.x;
+            s.hi[k] = v.y;
+        }
+        else
+        {
+            s.lo[k] = w < W ? row[w] : 0;
+            s.hi[k] = w + 1 < W ? row[w + 1] : 0;
+        }
+    }
+}
+
+template<int G, int K>
+__device__ __forceinline__ void store_row(u64* __restrict__ row, u32 W, u32 q, const Slice<G, K>& s)
+{
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+    {
+        const u32 w = 2 * (k * G + q);
+        if (w + 1 < W && (W & 1) == 0)
+            *reinterpret_cast<ulonglong2*>(row + w) = ulonglong2{s.lo[k], s.hi[k]};
+        else
+        {
+            if (w < W)
+                row[w] = s.lo[k];
+            if (w + 1 < W)
+                row[w + 1] = s.hi[k];
+        }
+    }
+}
+
+/// Value of lane `src` of the group (all lanes of the wave must execute this).
+template<int G>
+__device__ __forceinline__ u64 group_bcast(u64 v, u32 gbase, u32 src)
+{
+    if constexpr (G == 1)
+        return v;
+    else
+        return __shfl(v, static_cast<int>(gbase + src), kWave);
+}
+
+template<int G>
+__device__ __forceinline__ u32 group_max(u32 v)
+{
+#pragma unroll
+    for (int d = 1; d < G; d <<= 1)
+        v = max(v, static_cast<u32>(__shfl_xor(static_cast<int>(v), d, kWave)));
+    return v;
+}
+
+/// Whether every lane of the group has `ok` (group-uniform result).
+template<int G>
+__device__ __forceinline__ bool group_all(bool ok, u32 gbase)
+{
+    if constexpr (G == 1)
+        return ok;
+    else
+    {
+        const u64 bad = __ballot(!ok);
+        const u64 mask = G == 64 ? ~u64{0} : (((u64{1} << G) - 1) << gbase);
+        return (bad & mask) == 0;
+    }
+}
+
+template<int G, int K>
+__device__ __forceinline__ bool group_equal(const Slice<G, K>& a, const Slice<G, K>& b, u32 gbase)
+{
+    bool eq = true;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        eq = eq && a.lo[k] == b.lo[k] && a.hi[k] == b.hi[k];
+    return group_all<G>(eq, gbase);
+}
+
+/// hash_state of the group's row (group-uniform).
+template<int G, int K>
+__device__ __forceinline__ u64 group_hash(const Slice<G, K>& s, u32 q, u32 gbase)
+{
+    u32 top = 0;  // 1 + index of the lane's highest nonzero word
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+    {
+        const u32 w = 2 * (k * G + q);
+        if (s.hi[k])
+            top = w + 2;
+        else if (s.lo[k])
+            top = w + 1;
+    }
+    const u32 n = group_max<G>(top);
+    u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int r = 0; r < G; ++r)
+        {
+            const u32 p = k * G + r;
+            const u64 a = group_bcast<G>(s.lo[k], gbase, r);
+            const u64 b = group_bcast<G>(s.hi[k], gbase, r);
+            if (2 * p < n)
+                h = mulfold(h ^ a ^ kHashP1, b ^ kHashP2);
+        }
+    return mix64(h);
+}
+
+__device__ __forceinline__ u64 load_entry(const u64* e) { return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+/// Probes the table for the group's row `me` (candidate j, hash h) and inserts it as pending if no equal row is there.
+/// Src::load(c, q, out) gives lane q's words of candidate c. Writes cand_slot[j] and, for losers, flags = 0.
+template<int G, int K, class Src>
+__device__ void probe_insert(const StateSetView& s, const Src& src, u64 j, const Slice<G, K>& me, u64 h, u32 q, u32 gbase,
+                             u64* __restrict__ cand_slot, u32* __restrict__ flags, u32* __restrict__ status)
+{
+    const u64 tag = h >> 32;
+    const u64 mine = (tag << 32) | kPending | j;
+    u64 slot = slot_of_hash(h, s.capacity);
+    for (u64 probes = 0; probes < s.capacity; ++probes)
+    {
+        u64 e = q == 0 ? load_entry(s.table + slot) : 0;
+        e = group_bcast<G>(e, gbase, 0);
+        if (e == 0)
+        {
+            u64 old = 0;
+            if (q == 0)
+                old = atomicCAS(reinterpret_cast<unsigned long long*>(s.table + slot), 0ull, static_cast<unsigned long long>(mine));
+            old = group_bcast<G>(old, gbase, 0);
+            if (old == 0)
+            {
+                if (q == 0)
+                    cand_slot[j] = (tag << 32) | slot;
+                return;
+            }
+            e = old;
+        }
+        if ((e >> 32) == tag)
+        {
+            const u32 code = static_cast<u32>(e);
+            Slice<G, K> o;
+            const bool pending = (code & kPending) != 0;
+            if (pending)
+                src.load(code & ~kPending, q, o);
+            else
+                load_row<G, K>(s.arena + static_cast<u64>(code - 1) * s.words, s.words, q, o);
+            if (group_equal<G, K>(me, o, gbase))
+            {
+                if (pending)
+                {
+                    u64 old = 0;
+                    if (q == 0)
+                        old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
+                    old = group_bcast<G>(old, gbase, 0);
+                    if (q == 0)
+                    {
+                        const u64 other = static_cast<u32>(old) & ~kPending;
+                        flags[other > j ? other : j] = 0;
+                        cand_slot[j] = (tag << 32) | slot;
+                    }
+                }
+                else if (q == 0)
+                {
+                    flags[j] = 0;
+                    cand_slot[j] = (static_cast<u64>(code - 1) << 32) | kNoSlot;
+                }
+                return;
+            }
+        }
+        slot = slot + 1 == s.capacity ? 0 : slot + 1;
+    }
+    if (q == 0)
+    {
+        atomicOr(status, kStatusTableFull);
+        flags[j] = 0;
+        cand_slot[j] = kProbeFailed;
+    }
+}
+
+/// Winner j with id offsets[j] < limit: its row into the arena and its entry settled to id + 1. Resets flags[j] to 1
+/// for the next batch. Ids at or past limit set kStatusCapacity.
+template<int G, int K, class Src>
+__device__ __forceinline__ void compact_one(const StateSetView& s, const Src& src, u64 j, u32 q, u32 gbase,
+                                            const u64* __restrict__ cand_slot, u32* __restrict__ flags,
+                                            const u64* __restrict__ offsets, u64 limit, u8* __restrict__ is_new,
+                                            u32* __restrict__ status)
+{
+    const bool win = flags[j] != 0;
+    if (q == 0)
+    {
+        if (!win)
+            flags[j] = 1;
+        if (is_new)
+            is_new[j] = 0;
+    }
+    if (!win)
+        return;
+    const u64 id = offsets[j];
+    if (id >= limit)
+    {
+        if (q == 0)
+        {
+            atomicOr(status, kStatusCapacity);
+            flags[j] = 1;
+        }
+        return;
+    }
+    Slice<G, K> r;
+    src.load(j, q, r);
+    store_row<G, K>(s.arena + id * s.words, s.words, q, r);
+    if (q == 0)
+    {
+        const u64 cs = cand_slot[j];
+        s.table[static_cast<u32>(cs)] = (cs & 0xFFFFFFFF00000000ull) | static_cast<u32>(id + 1);
+        flags[j] = 1;
+        if (is_new)
+            is_new[j] = 1;
+    }
+}
+}  // namespace mya

@@ -59,8 +59,9 @@ class StateSet:
         self._h = h
         self.words = words
 
-    def insert(self, rows: torch.Tensor, want_ids: bool = True) -> tuple[int, torch.Tensor | None, torch.Tensor]:
-        """Inserts rows; returns (new states, ids [n] int64 or None, is_new [n] uint8)."""
+    def insert(self, rows: torch.Tensor, want_ids: bool = True, count: bool = True) -> tuple[int | None, torch.Tensor | None, torch.Tensor]:
+        """Inserts rows; returns (new states, ids [n] int64 or None, is_new [n] uint8). With count=False the insert is
+        asynchronous on torch's current stream and the first item is None (len() synchronizes and reports overflow)."""
         r = _u64(rows)
         _require(r, "rows", torch.int64, 2)
         if r.shape[1] != self.words:
@@ -70,8 +71,8 @@ class StateSet:
         is_new = torch.empty(n, dtype=torch.uint8, device=r.device)
         cnt = ctypes.c_uint64()
         check(lib.mya_hashset_insert(self._h, r.data_ptr(), n, None if ids is None else ids.data_ptr(), is_new.data_ptr(),
-                                     ctypes.byref(cnt), _stream()))
-        return cnt.value, ids, is_new
+                                     ctypes.byref(cnt) if count else None, _stream()))
+        return (cnt.value if count else None), ids, is_new
 
     def __len__(self) -> int:
         s = ctypes.c_uint64()

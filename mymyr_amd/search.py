@@ -38,7 +38,7 @@ class BrfsResult:
     kernels: dict = field(default_factory=dict)  # class -> {"ms", "bytes", "launches"} (ms with timings=True)
 
 
-KERNEL_CLASSES = ["count", "emit", "lookup", "probe", "rank", "compact", "other"]
+KERNEL_CLASSES = ["count", "emit", "insert", "unused", "rank", "compact", "other"]
 
 
 def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None, max_expanded: int | None = None,
