@@ -34,8 +34,6 @@ const DeviceTask& device_task(mya_task* t)
         t->dev.device = dev;
         t->dev.words = img.size();
         t->dev.thost = std::make_unique<TaskDev>(task_dev(t->dev.image, t->compiled->header()));
-        t->dev.tdev = dev_alloc<TaskDev>(1, "task pointer table");
-        hip_check(hipMemcpy(t->dev.tdev, t->dev.thost.get(), sizeof(TaskDev), hipMemcpyHostToDevice), "upload task table");
     }
     return t->dev;
 }
@@ -88,7 +86,6 @@ void mya_task_free(mya_task* task)
     if (!task)
         return;
     dev_free(task->dev.image);
-    dev_free(task->dev.tdev);
     delete task;
 }
 

@@ -15,7 +15,6 @@ struct mya_env
 {
     mya_task* task = nullptr;
     TaskDev T{};                // host copy of the pointer table
-    const TaskDev* Td = nullptr;  // device copy
     EnvCfg cfg{};
     u32 init_count = 0;
     u32 init_goal = 0;
@@ -55,7 +54,6 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
         e->task = task;
         const DeviceTask& d = device_task(task);
         e->T = *d.thost;
-        e->Td = d.tdev;
         e->cfg.seed = config->seed;
         e->cfg.max_steps = config->max_steps;
         e->cfg.step_reward = config->step_reward;
@@ -74,7 +72,7 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
         u8* gl = dev_alloc<u8>(1, "initial goal");
         hip_check(hipMemcpy(row, task->compiled->initial.data(), W * sizeof(u64), hipMemcpyHostToDevice), "initial row");
         e->init_masks = dev_alloc<u8>(std::max<u32>(1, e->T.num_schemas), "initial masks");
-        launch_env_count(e->Td, e->T, row, 1, W, cnt, gl, e->init_masks, nullptr);
+        launch_env_count(e->T, row, 1, W, cnt, gl, e->init_masks, nullptr);
         i32 hc = 0;
         u8 hg = 0;
         hip_check(hipMemcpy(&hc, cnt, sizeof(i32), hipMemcpyDeviceToHost), "initial count");
@@ -117,7 +115,7 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         if (!env)
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
-        launch_env_reset(env->Td, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, env->init_count,
+        launch_env_reset(env->T, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, env->init_count,
                          env->init_goal, static_cast<hipStream_t>(stream));
     });
 }
@@ -142,9 +140,7 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
             throw std::invalid_argument("mymyr: env: final state rows of " + std::to_string(fw) + " words; the task has " +
                                         std::to_string(env->T.W));
         EnvArgs a{};
-        a.T = env->Td;
-        a.W = env->T.W;
-        a.view_words = env->T.view_words;
+        a.T = env->T;
         a.cfg = env->cfg;
         a.states = batch->states;
         a.rows = batch->rows;
@@ -218,7 +214,7 @@ int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32
             throw std::invalid_argument("mymyr_amd: schema_masks: null argument");
         if (words < env->T.W)
             throw std::invalid_argument("mymyr_amd: schema_masks: rows narrower than the task");
-        launch_env_count(env->Td, env->T, states, rows, words, nullptr, nullptr, masks, static_cast<hipStream_t>(stream));
+        launch_env_count(env->T, states, rows, words, nullptr, nullptr, masks, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -237,7 +233,7 @@ int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32
                                         std::to_string(T.W));
         u32* st = dev_alloc<u32>(1, "status");
         hip_check(hipMemsetAsync(st, 0, sizeof(u32), static_cast<hipStream_t>(stream)), "status");
-        launch_successors(d.tdev, T, states, rows, words, static_cast<u32>(cap), count, schema, binding, succ, st, static_cast<hipStream_t>(stream));
+        launch_successors(T, states, rows, words, static_cast<u32>(cap), count, schema, binding, succ, st, static_cast<hipStream_t>(stream));
         u32 hs = 0;
         hip_check(hipMemcpyAsync(&hs, st, sizeof(u32), hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)), "status");
         hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "successors");

@@ -22,7 +22,6 @@ struct DeviceTask
     u64* image = nullptr;
     u64 words = 0;
     int device = -1;
-    TaskDev* tdev = nullptr;         // device copy of the pointer table
     std::unique_ptr<TaskDev> thost;  // host copy
 };
 

@@ -1,34 +1,42 @@
-// Lifted matching (lifted.hpp) and the device env step (env.hpp). One 64-lane block per state row.
+// Lifted matching (lifted.hpp) and the device env step (env.hpp). A block holds up to kMaxWaves wavefronts that share
+// the LDS copy of the task's hot tables; each wave steps one environment at a time in its own LDS region. Waves of a
+// block run different environments, so every barrier inside the per-environment work is a wavefront barrier.
 
 #include "env.hpp"
 #include "runtime.hpp"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace mya
 {
 TaskDev task_dev(const u64* img, const DevTaskHeader& h)
 {
     TaskDev t{};
-    t.schemas = reinterpret_cast<const DevSchema*>(img + h.off_schemas);
-    t.steps = reinterpret_cast<const DevStep*>(img + h.off_steps);
-    t.cons = reinterpret_cast<const DevCons*>(img + h.off_cons);
-    t.checks = reinterpret_cast<const DevCheck*>(img + h.off_checks);
-    t.effects = reinterpret_cast<const DevEffect*>(img + h.off_effects);
-    t.pairs = reinterpret_cast<const DevPair*>(img + h.off_pairs);
+    t.off_schemas = h.off_schemas;
+    t.off_steps = h.off_steps;
+    t.off_cons = h.off_cons;
+    t.off_checks = h.off_checks;
+    t.off_effects = h.off_effects;
+    t.off_pairs = h.off_pairs;
+    t.off_decode = h.off_decode;
+    t.off_dom0 = h.off_dom0;
+    t.off_goal_pos = h.off_goal_pos;
+    t.off_goal_neg = h.off_goal_neg;
+    t.off_pred_arity = h.off_pred_arity;
+    t.off_pos_begin = h.off_pos_begin;
+    t.off_pred_pairs = h.off_pred_pairs;
+    t.off_pred_offset = h.off_pred_offset;
+    t.image = img;
     t.rs = img + h.off_rs;
     t.slot_of = reinterpret_cast<const u32*>(img + h.off_slot_of);
     t.records = img + h.off_records;
-    t.dom0 = img + h.off_dom0;
     t.static_rows = img + h.off_static_rows;
     t.static_meta = reinterpret_cast<const DevStaticMeta*>(img + h.off_static_meta);
     t.static_words = img;
-    t.goal_pos = reinterpret_cast<const u32*>(img + h.off_goal_pos);
-    t.goal_neg = reinterpret_cast<const u32*>(img + h.off_goal_neg);
     t.initial = img + h.off_initial;
-    t.pred_arity = reinterpret_cast<const u32*>(img + h.off_pred_arity);
-    t.pos_begin = reinterpret_cast<const u32*>(img + h.off_pos_begin);
-    t.pred_pairs = img + h.off_pred_pairs;
-    t.pred_offset = img + h.off_pred_offset;
     t.fluent_count = h.fluent_count;
+    t.hot_words = static_cast<u32>(h.hot_words);
     t.n = h.num_objects;
     t.ow = h.ow;
     t.W = h.words;
@@ -41,48 +49,183 @@ TaskDev task_dev(const u64* img, const DevTaskHeader& h)
     t.dense = h.dense;
     t.label_width = h.label_width;
     t.fluent_slots = h.fluent_slots;
+    t.num_decode = h.num_decode;
+    t.decode_arith = h.decode_arith;
+    t.max_step_words = h.max_step_words;
     return t;
 }
 
-size_t env_lds_bytes(const DevTaskHeader& h) { return static_cast<size_t>(lds_words(h)) * sizeof(u64); }
-
 namespace
 {
-constexpr int kEB = 64;  // one wavefront per block
+constexpr int kMaxWaves = 4;
+constexpr u64 kHotMax = 48 * 1024;  // hot tables above this size stay in global memory (read through the caches)
+constexpr u32 kMaxEff = 32;  // effects per schema the step applies (more set kStatusCapacity)
+static_assert(kCap == 64, "a level of the level-synchronous count holds one item per lane");
 
-struct Lds
+/// LDS-qualified types: their pointers are 32-bit LDS addresses.
+template<class X>
+using lds = __attribute__((address_space(3))) X;
+
+/// A copy of the record at p (LDS or global).
+template<class X>
+__device__ __forceinline__ X ld(const X* p)
 {
-    u64* view;    // [view_words]
-    u32* bind;    // [kMaxParams][64]: lane columns
-    u32* counts;  // [kCountCache]
-    u64* cur_m;   // [kMaxParams][64]: enumeration cursors (candidate bits left)
-    u32* cur_w;   // [kMaxParams][64]: enumeration cursors (word index)
-    u32* eff;     // [64]: effect slots (lane 0)
-    u32* before;  // [64]: effect atoms' bits before the move (lane 0)
+    return *p;
+}
+template<class X>
+__device__ __forceinline__ X ld(lds<const X>* p)
+{
+    static_assert(sizeof(X) % 4 == 0, "records are whole 32-bit words");
+    u32 w[sizeof(X) / 4];
+    const lds<const u32>* src = (const lds<const u32>*)p;
+#pragma unroll
+    for (u32 i = 0; i < sizeof(X) / 4; ++i)
+        w[i] = src[i];
+    X x;
+    __builtin_memcpy(&x, w, sizeof(X));
+    return x;
+}
+
+/// The hot tables: in LDS (kStaged) or in the image in global memory.
+template<bool kStaged>
+struct Tab
+{
+    template<class X>
+    using ptr = std::conditional_t<kStaged, lds<const X>*, const X*>;
+    ptr<DevSchema> schemas;
+    ptr<DevStep> steps;
+    ptr<DevCons> cons;
+    ptr<DevCheck> checks;
+    ptr<DevEffect> effects;
+    ptr<DevPair> pairs;
+    ptr<DevPredDecode> decode;
+    ptr<u64> dom0;
+    ptr<u32> goal_pos;
+    ptr<u32> goal_neg;
+    ptr<u32> pred_arity;
+    ptr<u32> pos_begin;
+    ptr<u64> pred_pairs;
+    ptr<u64> pred_offset;
 };
 
-__device__ __forceinline__ Lds lds_layout(u64* base, const TaskDev& T)
+template<bool kStaged, class Base>
+__device__ __forceinline__ Tab<kStaged> tab_of(Base hot, const TaskDev& T)
 {
+    using H = Tab<kStaged>;
+    H t;
+    t.schemas = reinterpret_cast<typename H::template ptr<DevSchema>>(hot + T.off_schemas);
+    t.steps = reinterpret_cast<typename H::template ptr<DevStep>>(hot + T.off_steps);
+    t.cons = reinterpret_cast<typename H::template ptr<DevCons>>(hot + T.off_cons);
+    t.checks = reinterpret_cast<typename H::template ptr<DevCheck>>(hot + T.off_checks);
+    t.effects = reinterpret_cast<typename H::template ptr<DevEffect>>(hot + T.off_effects);
+    t.pairs = reinterpret_cast<typename H::template ptr<DevPair>>(hot + T.off_pairs);
+    t.decode = reinterpret_cast<typename H::template ptr<DevPredDecode>>(hot + T.off_decode);
+    t.dom0 = hot + T.off_dom0;
+    t.goal_pos = reinterpret_cast<typename H::template ptr<u32>>(hot + T.off_goal_pos);
+    t.goal_neg = reinterpret_cast<typename H::template ptr<u32>>(hot + T.off_goal_neg);
+    t.pred_arity = reinterpret_cast<typename H::template ptr<u32>>(hot + T.off_pred_arity);
+    t.pos_begin = reinterpret_cast<typename H::template ptr<u32>>(hot + T.off_pos_begin);
+    t.pred_pairs = hot + T.off_pred_pairs;
+    t.pred_offset = hot + T.off_pred_offset;
+    return t;
+}
+
+/// A wave's LDS region.
+struct Lds
+{
+    lds<u64>* row;     // [W] the state
+    lds<u64>* view;    // [view_words] rows of the non-bulk view pairs
+    lds<u32>* qa;      // [kCap][A] item bindings of the current level of a level-synchronous count
+    lds<u32>* qb;      // [kCap][A] the next level
+    lds<u32>* ra;      // [kCap] root of each current item
+    lds<u32>* rb;      // [kCap]
+    lds<u32>* rc;      // [kCap] per-root counts
+    lds<u32>* robj;    // [kCap] the objects of a pick round's roots
+    lds<u32>* own;     // [kCap] the lane that makes each item of a level-expansion round
+    lds<u32>* ub;      // [8] the wave-uniform binding (pick prefix, then the picked action)
+    lds<u32>* bind;    // [A][64]: lane columns of the per-lane nested loop (count_from)
+    lds<u64>* cur_m;   // [A][64]: its enumeration cursors (candidate bits left)
+    lds<u32>* cur_w;   // [A][64]: its enumeration cursors (word index)
+    lds<u32>* eff;     // [kMaxEff]: effect slots (lane 0)
+    lds<u32>* before;  // [kMaxEff]: effect atoms' bits before the move (lane 0)
+    lds<u32>* counts;  // [num_schemas]
+};
+
+template<bool kLevels>
+__device__ __forceinline__ Lds lds_of(lds<u64>* base, const TaskDev& T)
+{
+    const u32 A = T.label_width ? T.label_width : 1;
     Lds l;
-    u64* p = base;
+    lds<u64>* p = base;
+    l.row = p;
+    p += T.W;
     l.view = p;
     p += T.view_words;
-    l.bind = reinterpret_cast<u32*>(p);
-    p += (kMaxParams * 64) / 2;
-    l.counts = reinterpret_cast<u32*>(p);
-    p += kCountCache / 2;
+    l.ub = reinterpret_cast<lds<u32>*>(p);
+    p += 4;
+    l.bind = reinterpret_cast<lds<u32>*>(p);
+    p += 32 * A;
     l.cur_m = p;
-    p += kMaxParams * 64;
-    l.cur_w = reinterpret_cast<u32*>(p);
-    p += (kMaxParams * 64) / 2;
-    l.eff = reinterpret_cast<u32*>(p);
-    p += 32;
-    l.before = reinterpret_cast<u32*>(p);
+    p += 64 * A;
+    l.cur_w = reinterpret_cast<lds<u32>*>(p);
+    p += 32 * A;
+    l.eff = reinterpret_cast<lds<u32>*>(p);
+    p += kMaxEff / 2;
+    l.before = reinterpret_cast<lds<u32>*>(p);
+    p += kMaxEff / 2;
+    l.counts = reinterpret_cast<lds<u32>*>(p);
+    p += (T.num_schemas + 1) / 2;
+    if constexpr (kLevels)
+    {
+        l.qa = reinterpret_cast<lds<u32>*>(p);
+        p += kCap * A / 2;
+        l.qb = reinterpret_cast<lds<u32>*>(p);
+        p += kCap * A / 2;
+        l.ra = reinterpret_cast<lds<u32>*>(p);
+        p += kCap / 2;
+        l.rb = reinterpret_cast<lds<u32>*>(p);
+        p += kCap / 2;
+        l.rc = reinterpret_cast<lds<u32>*>(p);
+        p += kCap / 2;
+        l.robj = reinterpret_cast<lds<u32>*>(p);
+        p += kCap / 2;
+        l.own = reinterpret_cast<lds<u32>*>(p);
+    }
     return l;
 }
 
+/// Orders the wave's LDS accesses before and after this point (lanes of one wave run in lockstep).
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/// The hot tables of the block: copied into LDS at kernel start (whole block), or the image itself when they do not
+/// fit. Returns the start of the waves' LDS regions.
+template<bool kStaged>
+__device__ __forceinline__ lds<u64>* stage_hot(u64* smem_generic, const TaskDev& T, Tab<kStaged>* H)
+{
+    lds<u64>* smem = (lds<u64>*)(smem_generic);
+    if constexpr (kStaged)
+    {
+        for (u32 k = threadIdx.x; k < T.hot_words; k += blockDim.x)
+            smem[k] = T.image[k];
+        __syncthreads();
+        *H = tab_of<true>(static_cast<lds<const u64>*>(smem), T);
+        return smem + T.hot_words;
+    }
+    else
+    {
+        *H = tab_of<false>(T.image, T);
+        return smem;
+    }
+}
+
 /// 64 bits of a row (bit 0 = object row_lo, `words` words) for objects [obj_start, obj_start + 64); zeros outside.
-__device__ __forceinline__ u64 extract64(const u64* row, u32 words, u32 row_lo, u32 obj_start)
+template<class P>
+__device__ __forceinline__ u64 extract64(P row, u32 words, u32 row_lo, u32 obj_start)
 {
     const i64 bitpos = static_cast<i64>(obj_start) - static_cast<i64>(row_lo);
     const i64 wi = bitpos >> 6;
@@ -94,55 +237,82 @@ __device__ __forceinline__ u64 extract64(const u64* row, u32 words, u32 row_lo, 
     return (lo >> sh) | (hi << (64 - sh));
 }
 
-__device__ __forceinline__ bool row_bit(const u64* row, u32 slot) { return (row[slot >> 6] >> (slot & 63)) & 1; }
+/// Bits [rel, rel + 64) of the `len`-bit segment that starts at bit `base` of the W-word row (zeros outside it).
+template<class P>
+__device__ __forceinline__ u64 seg_bits(P row, u32 W, u64 base, i64 rel, u32 len)
+{
+    if (rel >= static_cast<i64>(len) || rel <= -64)
+        return 0;
+    const i64 a = static_cast<i64>(base) + rel;
+    const i64 wi = a >> 6;
+    const u32 sh = static_cast<u32>(a & 63);
+    const u64 lo = (wi >= 0 && wi < static_cast<i64>(W)) ? row[wi] : 0;
+    u64 v = lo;
+    if (sh)
+    {
+        const u64 hi = (wi + 1 >= 0 && wi + 1 < static_cast<i64>(W)) ? row[wi + 1] : 0;
+        v = (lo >> sh) | (hi << (64 - sh));
+    }
+    if (rel < 0)
+        v &= ~u64{0} << static_cast<u32>(-rel);
+    const i64 keep = static_cast<i64>(len) - rel;  // valid bits from position 0
+    if (keep < 64)
+        v &= (u64{1} << static_cast<u32>(keep)) - 1;
+    return v;
+}
 
-/// The candidate bits of step `st` for objects [st.lo + 64 w, + 64) under the lane's bindings.
-__device__ u64 cand_word(const TaskDev& T, const Lds& L, const DevStep& st, u32 w, u32 lane)
+template<class P>
+__device__ __forceinline__ bool row_bit(P row, u32 slot) { return (row[slot >> 6] >> (slot & 63)) & 1; }
+
+/// The candidate bits of step `st` for objects [st.lo + 64 w, + 64) under the binding b (parameter p at b[p * bs]).
+__device__ __forceinline__ u64 cand_word(const TaskDev& T, const auto& H, const Lds& L, const auto& st, u32 w, auto b, u32 bs)
 {
     u64 a = ~u64{0};
     const u32 obj0 = st.lo + 64 * w;
     for (u32 ci = st.cons_begin; ci < st.cons_end; ++ci)
     {
-        const DevCons c = T.cons[ci];
+        const DevCons c = ld(H.cons + ci);
         u64 v;
         if (c.kind == static_cast<u32>(ConsKind::Dom0))
-            v = T.dom0[c.table + w];
-        else if (c.kind == static_cast<u32>(ConsKind::ViewUnary))
+            v = H.dom0[c.table + w];
+        else if (c.kind == static_cast<u32>(ConsKind::StaticRow))
         {
-            const DevPair p = T.pairs[c.table];
-            v = extract64(L.view + p.offset, p.dst_words, p.dst_lo, obj0);
-        }
-        else if (c.kind == static_cast<u32>(ConsKind::ViewRow))
-        {
-            const DevPair p = T.pairs[c.table];
-            const u32 so = c.src == kNone ? c.obj : L.bind[c.src * 64 + lane];
-            const u32 ri = so - p.src_lo;
-            v = ri < p.src_n ? extract64(L.view + p.offset + static_cast<u64>(ri) * p.dst_words, p.dst_words, p.dst_lo, obj0) : 0;
+            const u32 so = b[c.src * bs];
+            v = extract64(T.static_rows + (static_cast<u64>(c.table) * T.n + so) * T.ow, T.ow, 0, obj0);
         }
         else
         {
-            const u32 so = L.bind[c.src * 64 + lane];
-            v = extract64(T.static_rows + (static_cast<u64>(c.table) * T.n + so) * T.ow, T.ow, 0, obj0);
+            const auto& p = H.pairs[c.table];
+            u32 ri = 0;
+            if (c.kind == static_cast<u32>(ConsKind::ViewRow))
+                ri = (c.src == kNone ? c.obj : b[c.src * bs]) - p.src_lo;
+            if (ri >= p.src_n)
+                v = 0;
+            else if (p.bulk)
+                v = seg_bits(L.row, T.W, p.bit0 + static_cast<u64>(ri) * p.row_bits, static_cast<i64>(obj0) - static_cast<i64>(p.dst_lo),
+                             p.row_bits);
+            else
+                v = extract64(L.view + p.offset + static_cast<u64>(ri) * p.dst_words, p.dst_words, p.dst_lo, obj0);
         }
         a &= c.neg ? ~v : v;
     }
     return a;
 }
 
-__device__ bool check_holds(const TaskDev& T, const Lds& L, const DevCheck& c, const u64* row, u32 lane)
+__device__ __forceinline__ bool check_holds(const TaskDev& T, const auto& H, const Lds& L, const auto& c, auto b, u32 bs)
 {
     u32 objs[6];
 #pragma unroll
     for (int i = 0; i < 6; ++i)
     {
         const i32 t = c.terms[i];
-        objs[i] = (static_cast<u32>(i) < c.nterms) ? (t < 0 ? static_cast<u32>(-(t + 1)) : L.bind[t * 64 + lane]) : 0;
+        objs[i] = (static_cast<u32>(i) < c.nterms) ? (t < 0 ? static_cast<u32>(-(t + 1)) : b[t * bs]) : 0;
     }
     bool h;
     if (c.kind == static_cast<u32>(CheckKind::Fluent))
     {
-        u64 key = T.pred_offset[c.pred];
-        const u32 pb = T.pos_begin[c.pred];
+        u64 key = H.pred_offset[c.pred];
+        const u32 pb = H.pos_begin[c.pred];
 #pragma unroll
         for (int i = 0; i < 6; ++i)
             if (static_cast<u32>(i) < c.nterms)
@@ -152,7 +322,7 @@ __device__ bool check_holds(const TaskDev& T, const Lds& L, const DevCheck& c, c
         else
         {
             const u32 slot = T.dense ? static_cast<u32>(key) : T.slot_of[key];
-            h = slot != kNone && row_bit(row, slot);
+            h = slot != kNone && row_bit(L.row, slot);
         }
     }
     else
@@ -178,27 +348,29 @@ __device__ bool check_holds(const TaskDev& T, const Lds& L, const DevCheck& c, c
     return h == (c.pos != 0);
 }
 
-__device__ __forceinline__ bool checks_ok(const TaskDev& T, const Lds& L, u32 b, u32 e, const u64* row, u32 lane)
+__device__ __forceinline__ bool checks_ok(const TaskDev& T, const auto& H, const Lds& L, u32 cb, u32 ce, auto b, u32 bs)
 {
-    for (u32 k = b; k < e; ++k)
-        if (!check_holds(T, L, T.checks[k], row, lane))
+    for (u32 k = cb; k < ce; ++k)
+        if (!check_holds(T, H, L, H.checks[k], b, bs))
             return false;
     return true;
 }
 
-/// Bindings completing steps [si, se) sequentially in this lane (its own binding column): an iterative nested loop
-/// whose per-level cursor (current word index and remaining candidate bits) lives in the lane's LDS columns.
-__device__ u32 count_from(const TaskDev& T, const Lds& L, const u64* row, u32 si, u32 se, u32 lane)
+/// Bindings completing steps [si, se) sequentially in this lane (its own binding column L.bind[p * 64 + lane]): an
+/// iterative nested loop whose per-level cursor (current word index and remaining candidate bits) lives in the lane's
+/// LDS columns. The fallback of count_multi for levels wider than its item capacity.
+__device__ __forceinline__ u32 count_from(const TaskDev& T, const auto& H, const Lds& L, u32 si, u32 se, u32 lane)
 {
     if (si == se)
         return 1;
+    const auto b = L.bind + lane;
     u32 total = 0;
     u32 d = 0;  // level: step si + d
     L.cur_w[lane] = 0;
-    L.cur_m[lane] = cand_word(T, L, T.steps[si], 0, lane);
+    L.cur_m[lane] = cand_word(T, H, L, H.steps[si], 0, b, 64);
     for (;;)
     {
-        const DevStep st = T.steps[si + d];
+        const auto& st = H.steps[si + d];
         u64 m = L.cur_m[d * 64 + lane];
         const bool last = si + d + 1 == se;
         const bool chk = st.check_begin != st.check_end;
@@ -210,11 +382,11 @@ __device__ u32 count_from(const TaskDev& T, const Lds& L, const u64* row, u32 si
         if (m == 0)
         {
             // next word of this level, or back to the level above
-            u32 w = L.cur_w[d * 64 + lane] + 1;
+            const u32 w = L.cur_w[d * 64 + lane] + 1;
             if (w < st.words)
             {
                 L.cur_w[d * 64 + lane] = w;
-                L.cur_m[d * 64 + lane] = cand_word(T, L, st, w, lane);
+                L.cur_m[d * 64 + lane] = cand_word(T, H, L, st, w, b, 64);
                 continue;
             }
             if (d == 0)
@@ -222,10 +394,10 @@ __device__ u32 count_from(const TaskDev& T, const Lds& L, const u64* row, u32 si
             --d;
             continue;
         }
-        const u32 b = static_cast<u32>(__builtin_ctzll(m));
+        const u32 bit = static_cast<u32>(__builtin_ctzll(m));
         L.cur_m[d * 64 + lane] = m & (m - 1);
-        L.bind[st.param * 64 + lane] = st.lo + 64 * L.cur_w[d * 64 + lane] + b;
-        if (chk && !checks_ok(T, L, st.check_begin, st.check_end, row, lane))
+        L.bind[st.param * 64 + lane] = st.lo + 64 * L.cur_w[d * 64 + lane] + bit;
+        if (chk && !checks_ok(T, H, L, st.check_begin, st.check_end, b, 64))
             continue;
         if (last)
         {
@@ -234,62 +406,305 @@ __device__ u32 count_from(const TaskDev& T, const Lds& L, const u64* row, u32 si
         }
         ++d;
         L.cur_w[d * 64 + lane] = 0;
-        L.cur_m[d * 64 + lane] = cand_word(T, L, T.steps[si + d], 0, lane);
+        L.cur_m[d * 64 + lane] = cand_word(T, H, L, H.steps[si + d], 0, b, 64);
     }
     return total;
 }
 
-/// Bindings completing steps [si, se), the first step's candidates split over the lanes (one bit per lane); the
-/// bound prefix must be in every lane's column. Wave-uniform result.
-__device__ u32 count_wave(const TaskDev& T, const Lds& L, const u64* row, u32 si, u32 se, u32 lane)
+/// The candidates m of step st for item binding b that pass the step's k-ary checks (each bit bound in the lane's
+/// column and checked).
+__device__ __forceinline__ u64 checked(const TaskDev& T, const auto& H, const Lds& L, const auto& st, u32 w, u64 m, auto b,
+                                       u32 A, u32 lane)
+{
+    for (u32 p = 0; p < A; ++p)
+        L.bind[p * 64 + lane] = b[p];
+    u64 keep = 0;
+    for (u64 x = m; x;)
+    {
+        const u32 bit = static_cast<u32>(__builtin_ctzll(x));
+        x &= x - 1;
+        L.bind[st.param * 64 + lane] = st.lo + 64 * w + bit;
+        if (checks_ok(T, H, L, st.check_begin, st.check_end, L.bind + lane, 64))
+            keep |= u64{1} << bit;
+    }
+    return keep;
+}
+
+/// Position of the k-th (from 0) set bit of m (k < popcount(m)).
+__device__ __forceinline__ u32 kth_bit(u64 m, u32 k)
+{
+    u32 pos = 0;
+    u32 c = static_cast<u32>(__popc(static_cast<u32>(m)));
+    if (k >= c)
+    {
+        k -= c;
+        m >>= 32;
+        pos += 32;
+    }
+#pragma unroll
+    for (u32 sh = 16; sh; sh >>= 1)
+    {
+        c = static_cast<u32>(__popc(static_cast<u32>(m) & ((1u << sh) - 1)));
+        if (k >= c)
+        {
+            k -= c;
+            m >>= sh;
+            pos += sh;
+        }
+    }
+    return pos;
+}
+
+/// The OR of v over the wave.
+__device__ __forceinline__ u64 wave_or64(u64 v)
+{
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1)
+        v |= __shfl_xor(v, d, kWave);
+    return v;
+}
+
+/// (item, word) of pair p of a level with `words` words per item (p < 2^20): p / words by a float estimate and one
+/// correction step.
+__device__ __forceinline__ void pair_of(u32 p, u32 words, float rcp, u32* item, u32* w)
+{
+    if (words == 1)
+    {
+        *item = p;
+        *w = 0;
+        return;
+    }
+    u32 q = static_cast<u32>(static_cast<float>(p) * rcp);
+    if (q * words > p)
+        --q;
+    else if ((q + 1) * words <= p)
+        ++q;
+    *item = q;
+    *w = p - q * words;
+}
+
+/// Level-synchronous count: for each of the nroots roots (bindings L.qa[r * A ...], every parameter that steps
+/// [si, se) read already bound), the number of full bindings completing steps [si, se) into L.rc[r]. Each level
+/// spreads its (item, candidate word) pairs over the lanes; a non-last level turns the candidate bits into the next
+/// level's items (their order does not matter for counting; item j of a round is made by lane j, which selects its
+/// bit from the pair that holds it), the last level adds popcounts to the items' roots. A level with more than kCap
+/// items continues in the lanes' nested loops (count_from) from the current items.
+__device__ __forceinline__ void count_multi(const TaskDev& T, const auto& H, const Lds& L, u32 si, u32 se, u32 nroots, u32 lane)
+{
+    const u32 A = T.label_width ? T.label_width : 1;
+    if (lane < kCap)
+    {
+        L.rc[lane] = (si == se && lane < nroots) ? 1u : 0u;
+        L.ra[lane] = lane;
+    }
+    wave_sync();
+    if (si == se || nroots == 0)
+        return;
+    lds<u32>* qa = L.qa;
+    lds<u32>* qb = L.qb;
+    lds<u32>* ra = L.ra;
+    lds<u32>* rb = L.rb;
+    u32 n = nroots;
+    for (u32 k = si; k < se; ++k)
+    {
+        const DevStep st = ld(H.steps + k);
+        const bool last = k + 1 == se;
+        const bool chk = st.check_begin != st.check_end;
+        const u32 pairs = n * st.words;
+        const float rcp = 1.0f / static_cast<float>(st.words);
+        u32 total1 = 0;  // a single root's count (a wave sum instead of LDS atomics)
+        if (last)
+        {
+            for (u32 p0 = 0; p0 < pairs; p0 += kWave)
+            {
+                const u32 p = p0 + lane;
+                if (p < pairs)
+                {
+                    u32 item, w;
+                    pair_of(p, st.words, rcp, &item, &w);
+                    u64 m = cand_word(T, H, L, st, w, qa + item * A, 1);
+                    if (chk && m)
+                        m = checked(T, H, L, st, w, m, qa + item * A, A, lane);
+                    const u32 c = static_cast<u32>(__popcll(m));
+                    if (c && nroots > 1)
+                        __hip_atomic_fetch_add(L.rc + ra[item], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                    if (nroots == 1)
+                        total1 += c;
+                }
+            }
+            if (nroots == 1)
+            {
+                const u32 t1 = wave_sum(total1);
+                if (lane == 0)
+                    L.rc[0] = t1;
+            }
+            wave_sync();
+            return;
+        }
+        // the next level's items: the current item's binding with the step's parameter bound to each candidate
+        u32 base = 0;
+        bool wide = false;
+        for (u32 p0 = 0; p0 < pairs && !wide; p0 += kWave)
+        {
+            const u32 p = p0 + lane;
+            u64 m = 0;
+            u32 item = 0, w = 0;
+            if (p < pairs)
+            {
+                pair_of(p, st.words, rcp, &item, &w);
+                m = cand_word(T, H, L, st, w, qa + item * A, 1);
+                if (chk && m)
+                    m = checked(T, H, L, st, w, m, qa + item * A, A, lane);
+            }
+            const u32 c = static_cast<u32>(__popcll(m));
+            const u32 incl = wave_inclusive(c);
+            const u32 round = __shfl(incl, kWave - 1, kWave);
+            if (base + round > kCap)
+            {
+                wide = true;
+                break;
+            }
+            if (round == 0)
+                continue;
+            const u32 o = incl - c;
+            if (__ballot(c > 4) == 0)
+            {
+                // few candidates per pair: each lane writes its own items
+                u32 dst = base + o;
+                for (u64 x = m; x; ++dst)
+                {
+                    const u32 bit = static_cast<u32>(__builtin_ctzll(x));
+                    x &= x - 1;
+                    for (u32 q = 0; q < A; ++q)
+                        qb[dst * A + q] = qa[item * A + q];
+                    qb[dst * A + st.param] = st.lo + 64 * w + bit;
+                    rb[dst] = ra[item];
+                }
+                base += round;
+                wave_sync();
+                continue;
+            }
+            // output j of the round comes from the lane whose range [incl - c, incl) holds j
+            const u64 starts = wave_or64(c ? u64{1} << o : 0);
+            if (c)
+                L.own[o] = lane;
+            wave_sync();
+            u32 src = 0, sp = 0;
+            if (lane < round)
+            {
+                const u64 le = lane == 63 ? ~u64{0} : (u64{2} << lane) - 1;
+                sp = 63u - static_cast<u32>(__clzll(starts & le));
+                src = L.own[sp];
+            }
+            const u64 sm = __shfl(m, static_cast<int>(src), kWave);
+            const u32 sitem = __shfl(item, static_cast<int>(src), kWave);
+            const u32 sw = __shfl(w, static_cast<int>(src), kWave);
+            if (lane < round)
+            {
+                const u32 bit = kth_bit(sm, lane - sp);
+                const u32 dst = base + lane;
+                for (u32 q = 0; q < A; ++q)
+                    qb[dst * A + q] = qa[sitem * A + q];
+                qb[dst * A + st.param] = st.lo + 64 * sw + bit;
+                rb[dst] = ra[sitem];
+            }
+            base += round;
+            wave_sync();
+        }
+        if (wide)
+        {
+            // too wide for the item levels: each lane completes its items with the nested loop
+            for (u32 item = lane; item < n; item += kWave)
+            {
+                for (u32 q = 0; q < A; ++q)
+                    L.bind[q * 64 + lane] = qa[item * A + q];
+                const u32 c = count_from(T, H, L, k, se, lane);
+                if (c)
+                    __hip_atomic_fetch_add(L.rc + ra[item], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            }
+            wave_sync();
+            return;
+        }
+        if (base == 0)
+            return;
+        lds<u32>* t = qa;
+        qa = qb;
+        qb = t;
+        t = ra;
+        ra = rb;
+        rb = t;
+        n = base;
+    }
+}
+
+/// Bindings completing steps [si, se) from the empty binding: the first step's candidates split over the lanes (one
+/// bit per lane), each lane completing its own with the nested loop. Wave-uniform result.
+__device__ __forceinline__ u32 count_wave(const TaskDev& T, const auto& H, const Lds& L, u32 si, u32 se, u32 lane)
 {
     if (si == se)
         return 1;
-    const DevStep st = T.steps[si];
+    const DevStep st = ld(H.steps + si);
     const bool chk = st.check_begin != st.check_end;
+    const bool last = si + 1 == se;
     u32 mine = 0;
     for (u32 w = 0; w < st.words; ++w)
     {
-        const u64 m = cand_word(T, L, st, w, lane);
+        const u64 m = cand_word(T, H, L, st, w, L.bind + lane, 64);
+        if (last && !chk)
+        {
+            mine += lane == 0 ? static_cast<u32>(__popcll(m)) : 0;
+            continue;
+        }
         if (!((m >> lane) & 1))
             continue;
         L.bind[st.param * 64 + lane] = st.lo + 64 * w + lane;
-        if (chk && !checks_ok(T, L, st.check_begin, st.check_end, row, lane))
+        if (chk && !checks_ok(T, H, L, st.check_begin, st.check_end, L.bind + lane, 64))
             continue;
-        mine += count_from(T, L, row, si + 1, se, lane);
+        mine += count_from(T, H, L, si + 1, se, lane);
     }
     return wave_sum(mine);
 }
 
-__device__ __forceinline__ u32 schema_count(const TaskDev& T, const Lds& L, const u64* row, u32 s, u32 lane)
+/// The successors of schema s: level-synchronous (kLevels) or split over the first step's candidates.
+template<bool kLevels>
+__device__ __forceinline__ u32 schema_count(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane)
 {
-    const DevSchema& S = T.schemas[s];
-    if (S.never || !checks_ok(T, L, S.ground_begin, S.ground_end, row, lane))
+    const auto& S = H.schemas[s];
+    if (S.never || !checks_ok(T, H, L, S.ground_begin, S.ground_end, L.ub, 1))
         return 0;
-    return count_wave(T, L, row, S.plan_begin[0], S.plan_begin[1], lane);
+    if constexpr (kLevels)
+    {
+        count_multi(T, H, L, S.plan_begin[0], S.plan_begin[1], 1, lane);
+        const u32 c = L.rc[0];
+        wave_sync();
+        return c;
+    }
+    else
+        return count_wave(T, H, L, S.plan_begin[0], S.plan_begin[1], lane);
 }
 
-/// Successors of the state (witness pruning off); per-schema counts of the first kCountCache schemas into LDS.
-__device__ u32 count_all(const TaskDev& T, const Lds& L, const u64* row, u32 lane)
+/// Successors of the state (witness pruning off); the per-schema counts into LDS.
+template<bool kLevels>
+__device__ __forceinline__ u32 count_all(const TaskDev& T, const auto& H, const Lds& L, u32 lane)
 {
     u32 total = 0;
     for (u32 s = 0; s < T.num_schemas; ++s)
     {
-        const u32 c = schema_count(T, L, row, s, lane);
-        if (s < kCountCache && lane == 0)
+        const u32 c = schema_count<kLevels>(T, H, L, s, lane);
+        if (lane == 0)
             L.counts[s] = c;
         total += c;
     }
-    __syncthreads();
+    wave_sync();
     return total;
 }
 
 /// The schema holding successor `a` (< total) and the rank within it.
-__device__ void select_schema(const TaskDev& T, const Lds& L, const u64* row, u32 a, u32 lane, u32* schema, u32* rank)
+__device__ __forceinline__ void select_schema(const TaskDev& T, const Lds& L, u32 a, u32* schema, u32* rank)
 {
     for (u32 s = 0; s < T.num_schemas; ++s)
     {
-        const u32 c = s < kCountCache ? L.counts[s] : schema_count(T, L, row, s, lane);
+        const u32 c = L.counts[s];
         if (a < c)
         {
             *schema = s;
@@ -302,28 +717,95 @@ __device__ void select_schema(const TaskDev& T, const Lds& L, const u64* row, u3
     *rank = 0;
 }
 
-__device__ __forceinline__ void set_bind_all(const Lds& L, u32 param, u32 obj, u32 lane) { L.bind[param * 64 + lane] = obj; }
-
-/// The rank-th applicable binding of schema s in lexicographic order into every lane's column. false: not found.
-__device__ bool pick(const TaskDev& T, const Lds& L, const u64* row, u32 s, u32 rank, u32 lane)
+/// The rank-th applicable binding of schema s in lexicographic order into L.ub. false: not found. Per parameter i in
+/// order, each window word of its candidates (given parameters [0, i) in L.ub) makes up to 64 roots whose completions
+/// count_multi counts; the prefix over the roots in object order locates the rank.
+__device__ __forceinline__ bool pick_levels(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 rank, u32 lane)
 {
-    const DevSchema& S = T.schemas[s];
+    const auto& S = H.schemas[s];
+    const u32 A = T.label_width ? T.label_width : 1;
     u32 a = rank;
     for (u32 i = 0; i < S.arity; ++i)
     {
-        const DevStep F = T.steps[S.filter_step[i]];
+        const DevStep F = ld(H.steps + S.filter_step[i]);
         const u32 pb = S.plan_begin[i + 1], pe = S.plan_begin[i + 2];
         const bool chk = F.check_begin != F.check_end;
         bool found = false;
         for (u32 w = 0; w < F.words && !found; ++w)
         {
-            const u64 m = cand_word(T, L, F, w, lane);
+            u64 m = cand_word(T, H, L, F, w, L.ub, 1);
+            if (chk && m)
+            {
+                // lane b checks candidate b
+                bool ok = false;
+                if ((m >> lane) & 1)
+                {
+                    for (u32 q = 0; q < A; ++q)
+                        L.bind[q * 64 + lane] = L.ub[q];
+                    L.bind[i * 64 + lane] = F.lo + 64 * w + lane;
+                    ok = checks_ok(T, H, L, F.check_begin, F.check_end, L.bind + lane, 64);
+                }
+                m = __ballot(ok);
+            }
+            if (m == 0)
+                continue;
+            const u32 nr = static_cast<u32>(__popcll(m));
+            // root r = the r-th candidate in object order
+            if ((m >> lane) & 1)
+            {
+                const u32 r = static_cast<u32>(__popcll(m & ((u64{1} << lane) - 1)));
+                for (u32 q = 0; q < A; ++q)
+                    L.qa[r * A + q] = L.ub[q];
+                L.qa[r * A + i] = F.lo + 64 * w + lane;
+                L.robj[r] = F.lo + 64 * w + lane;
+            }
+            wave_sync();
+            count_multi(T, H, L, pb, pe, nr, lane);
+            const u32 c = lane < nr ? L.rc[lane] : 0;
+            const u32 incl = wave_inclusive(c);
+            const u32 tot = __shfl(incl, kWave - 1, kWave);
+            if (a < tot)
+            {
+                const u64 over = __ballot(incl > a);
+                const u32 win = static_cast<u32>(__builtin_ctzll(over));
+                a -= __shfl(incl - c, win, kWave);
+                const u32 obj = L.robj[win];
+                wave_sync();
+                if (lane == 0)
+                    L.ub[i] = obj;
+                found = true;
+            }
+            else
+                a -= tot;
+            wave_sync();
+        }
+        if (!found)
+            return false;
+    }
+    return true;
+}
+
+/// The rank-th applicable binding of schema s in lexicographic order into L.ub, by prefix counting over the lanes:
+/// per parameter i, lane b takes candidate b of each window word and completes it with the nested loop.
+__device__ __forceinline__ bool pick_lanes(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 rank, u32 lane)
+{
+    const auto& S = H.schemas[s];
+    u32 a = rank;
+    for (u32 i = 0; i < S.arity; ++i)
+    {
+        const DevStep F = ld(H.steps + S.filter_step[i]);
+        const u32 pb = S.plan_begin[i + 1], pe = S.plan_begin[i + 2];
+        const bool chk = F.check_begin != F.check_end;
+        bool found = false;
+        for (u32 w = 0; w < F.words && !found; ++w)
+        {
+            const u64 m = cand_word(T, H, L, F, w, L.bind + lane, 64);
             u32 c = 0;
             if ((m >> lane) & 1)
             {
                 L.bind[i * 64 + lane] = F.lo + 64 * w + lane;
-                if (!chk || checks_ok(T, L, F.check_begin, F.check_end, row, lane))
-                    c = count_from(T, L, row, pb, pe, lane);
+                if (!chk || checks_ok(T, H, L, F.check_begin, F.check_end, L.bind + lane, 64))
+                    c = count_from(T, H, L, pb, pe, lane);
             }
             const u32 incl = wave_inclusive(c);
             const u32 tot = __shfl(incl, kWave - 1, kWave);
@@ -331,9 +813,8 @@ __device__ bool pick(const TaskDev& T, const Lds& L, const u64* row, u32 s, u32 
             {
                 const u64 over = __ballot(incl > a);
                 const u32 win = static_cast<u32>(__builtin_ctzll(over));
-                const u32 before = __shfl(incl - c, win, kWave);
-                a -= before;
-                set_bind_all(L, i, F.lo + 64 * w + win, lane);
+                a -= __shfl(incl - c, win, kWave);
+                L.bind[i * 64 + lane] = F.lo + 64 * w + win;
                 found = true;
             }
             else
@@ -342,32 +823,79 @@ __device__ bool pick(const TaskDev& T, const Lds& L, const u64* row, u32 s, u32 
         if (!found)
             return false;
     }
+    wave_sync();
+    if (lane < S.arity)
+        L.ub[lane] = L.bind[lane * 64];
+    wave_sync();
     return true;
 }
 
-__device__ __forceinline__ u32 effect_slot(const TaskDev& T, const Lds& L, const DevEffect& e, u32 lane)
+template<bool kLevels>
+__device__ __forceinline__ bool pick(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 rank, u32 lane)
+{
+    if constexpr (kLevels)
+        return pick_levels(T, H, L, s, rank, lane);
+    else
+        return pick_lanes(T, H, L, s, rank, lane);
+}
+
+__device__ __forceinline__ u32 effect_slot(const TaskDev& T, const Lds& L, const auto& e)
 {
     u64 cid = e.base;
     for (u32 v = 0; v < e.nvar; ++v)
-        cid += T.rs[static_cast<u64>(e.var_pos[v]) * T.n + L.bind[e.var_param[v] * 64 + lane]];
+        cid += T.rs[static_cast<u64>(e.var_pos[v]) * T.n + L.ub[e.var_param[v]]];
     if (cid >= T.fluent_count)
         return kNone;
     return T.dense ? static_cast<u32>(cid) : T.slot_of[cid];
 }
 
-/// Sets (on) or clears the view bits of atom slot s (one lane).
-__device__ void view_update(const TaskDev& T, const Lds& L, u32 s, bool on)
+/// Predicate and the first two arguments of atom slot s: arithmetic for dense slots over contiguous domains, else the
+/// slot's record.
+__device__ __forceinline__ void decode_slot(const TaskDev& T, const auto& H, u32 s, u32* pred, u32* a0, u32* a1)
 {
+    if (T.decode_arith)
+    {
+        u32 k = 0;
+        while (k + 1 < T.num_decode && H.decode[k + 1].offset <= s)
+            ++k;
+        const auto& d = H.decode[k];
+        const u32 rem = static_cast<u32>(s - d.offset);
+        *pred = d.pred;
+        if (d.arity >= 2)
+        {
+            const u32 r0 = rem / d.d1;
+            *a0 = d.lo0 + r0;
+            *a1 = d.lo1 + (rem - r0 * d.d1);
+        }
+        else
+        {
+            *a0 = d.lo0 + rem;
+            *a1 = 0;
+        }
+        return;
+    }
     const u64 rec = T.records[s];
-    const u32 pred = static_cast<u32>(rec & 0xFFFF), a0 = static_cast<u32>((rec >> 16) & 0xFFFF), a1 = static_cast<u32>((rec >> 32) & 0xFFFF);
-    const u64 pp = T.pred_pairs[pred];
-    const u32 ar = T.pred_arity[pred];
+    *pred = static_cast<u32>(rec & 0xFFFF);
+    *a0 = static_cast<u32>((rec >> 16) & 0xFFFF);
+    *a1 = static_cast<u32>((rec >> 32) & 0xFFFF);
+}
+
+/// The view word and bit of atom (pred, a0, a1) in the non-bulk pairs of its predicate: calls f(word pointer, bit).
+template<class F>
+__device__ __forceinline__ void for_view_bits(const auto& H, const Lds& L, u32 pred, u32 a0, u32 a1, F&& f)
+{
+    const u64 pp = H.pred_pairs[pred];
+    if (pp == ~u64{0})
+        return;
+    const u32 ar = H.pred_arity[pred];
     for (int d = 0; d < 2; ++d)
     {
         const u32 pi = d == 0 ? static_cast<u32>(pp) : static_cast<u32>(pp >> 32);
         if (pi == kNone)
             continue;
-        const DevPair P = T.pairs[pi];
+        const auto& P = H.pairs[pi];
+        if (P.bulk)
+            continue;
         u32 ri, bi;
         if (ar == 1)
         {
@@ -384,69 +912,46 @@ __device__ void view_update(const TaskDev& T, const Lds& L, u32 s, bool on)
             ri = a1 - P.src_lo;
             bi = a0 - P.dst_lo;
         }
-        u64* w = L.view + P.offset + static_cast<u64>(ri) * P.dst_words + (bi >> 6);
-        const u64 bit = u64{1} << (bi & 63);
-        if (on)
-            *w |= bit;
-        else
-            *w &= ~bit;
+        f(L.view + P.offset + static_cast<u64>(ri) * P.dst_words + (bi >> 6), u64{1} << (bi & 63));
     }
 }
 
-/// Builds the view of `row` (all lanes).
-__device__ void build_view(const TaskDev& T, const Lds& L, const u64* row, u32 lane)
+/// Builds the view of the wave's row (all lanes).
+__device__ __forceinline__ void build_view(const TaskDev& T, const auto& H, const Lds& L, u32 lane)
 {
     for (u32 k = lane; k < T.view_words; k += kWave)
         L.view[k] = 0;
-    __syncthreads();
+    wave_sync();
     for (u32 w = lane; w < T.W; w += kWave)
     {
-        u64 x = row[w];
+        u64 x = L.row[w];
         while (x)
         {
             const u32 s = w * 64 + static_cast<u32>(__builtin_ctzll(x));
             x &= x - 1;
             if (s >= T.fluent_slots)
                 break;  // bits past the task's slots belong to no atom
-            const u64 rec = T.records[s];
-            const u32 pred = static_cast<u32>(rec & 0xFFFF);
-            const u64 pp = T.pred_pairs[pred];
-            if (pp == ~u64{0})
-                continue;
-            const u32 a0 = static_cast<u32>((rec >> 16) & 0xFFFF), a1 = static_cast<u32>((rec >> 32) & 0xFFFF);
-            const u32 ar = T.pred_arity[pred];
-            for (int d = 0; d < 2; ++d)
-            {
-                const u32 pi = d == 0 ? static_cast<u32>(pp) : static_cast<u32>(pp >> 32);
-                if (pi == kNone)
-                    continue;
-                const DevPair P = T.pairs[pi];
-                u32 ri, bi;
-                if (ar == 1)
-                {
-                    ri = 0;
-                    bi = a0 - P.dst_lo;
-                }
-                else if (d == 0)
-                {
-                    ri = a0 - P.src_lo;
-                    bi = a1 - P.dst_lo;
-                }
-                else
-                {
-                    ri = a1 - P.src_lo;
-                    bi = a0 - P.dst_lo;
-                }
-                atomicOr(reinterpret_cast<unsigned long long*>(L.view + P.offset + static_cast<u64>(ri) * P.dst_words + (bi >> 6)),
-                         1ull << (bi & 63));
-            }
+            u32 pred, a0, a1;
+            decode_slot(T, H, s, &pred, &a0, &a1);
+            for_view_bits(H, L, pred, a0, a1, [](lds<u64>* word, u64 bit) {
+                __hip_atomic_fetch_or(word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            });
         }
     }
-    __syncthreads();
+    wave_sync();
+}
+
+/// Loads row i (W words of `words`) into the wave's LDS row.
+__device__ __forceinline__ void load_row_lds(const TaskDev& T, const Lds& L, const u64* src, u32 lane)
+{
+    for (u32 k = lane; k < T.W; k += kWave)
+        L.row[k] = src[k];
+    wave_sync();
 }
 
 /// The ascending set-bit slots of `row` (W words) into out[0, max_atoms), -1 padded (all lanes).
-__device__ void encode_row(const u64* row, u32 W, i32* out, u32 max_atoms, u32 lane, u32* status)
+template<class P>
+__device__ __forceinline__ void encode_row(P row, u32 W, i32* out, u32 max_atoms, u32 lane, u32* status)
 {
     u32 base = 0;
     for (u32 w0 = 0; w0 < W; w0 += kWave)
@@ -472,66 +977,111 @@ __device__ void encode_row(const u64* row, u32 W, i32* out, u32 max_atoms, u32 l
         atomicOr(status, kStatusCapacity);
 }
 
-__device__ bool goal_test(const TaskDev& T, const u64* row, u32 lane)
+template<class P>
+__device__ __forceinline__ bool goal_test(const TaskDev& T, const auto& H, P row, u32 lane)
 {
     bool ok = true;
     for (u32 i = lane; i < T.ngp; i += kWave)
-        ok = ok && row_bit(row, T.goal_pos[i]);
+        ok = ok && row_bit(row, H.goal_pos[i]);
     for (u32 i = lane; i < T.ngn; i += kWave)
-        ok = ok && !row_bit(row, T.goal_neg[i]);
+        ok = ok && !row_bit(row, H.goal_neg[i]);
     return !T.goal_unsat && __ballot(!ok) == 0;
 }
 
-/// Applies the effects of the picked binding of schema s to `row` (global) and the view: delete, then add.
-__device__ void apply_effects(const TaskDev& T, const Lds& L, u64* row, u32 s, u32 lane, u32* status)
+/// Applies the effects of the picked binding of schema s to the LDS row and the view: delete, then add.
+__device__ __forceinline__ void apply_effects(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane, u32* status)
 {
-    const DevSchema& S = T.schemas[s];
+    const auto& S = H.schemas[s];
     if (lane == 0)
     {
-        constexpr u32 kMaxEff = 64;
-        u32* slot = L.eff;
-        u32* before = L.before;
+        lds<u32>* slot = L.eff;
+        lds<u32>* before = L.before;
         const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
         if (S.eff_end - S.eff_begin > kMaxEff)
             atomicOr(status, kStatusCapacity);
         for (u32 k = 0; k < ne; ++k)
         {
-            slot[k] = effect_slot(T, L, T.effects[S.eff_begin + k], lane);
-            before[k] = slot[k] != kNone && row_bit(row, slot[k]);
+            slot[k] = effect_slot(T, L, H.effects[S.eff_begin + k]);
+            before[k] = slot[k] != kNone && row_bit(L.row, slot[k]);
             if (k < S.nadd && slot[k] == kNone)
                 atomicOr(status, kStatusNoSlot);
         }
         for (u32 k = S.nadd; k < ne; ++k)
             if (slot[k] != kNone)
-                row[slot[k] >> 6] &= ~(u64{1} << (slot[k] & 63));
+                L.row[slot[k] >> 6] &= ~(u64{1} << (slot[k] & 63));
         for (u32 k = 0; k < S.nadd && k < ne; ++k)
             if (slot[k] != kNone)
-                row[slot[k] >> 6] |= u64{1} << (slot[k] & 63);
-        for (u32 k = S.nadd; k < ne; ++k)
-            if (slot[k] != kNone && before[k] && !row_bit(row, slot[k]))
-                view_update(T, L, slot[k], false);
-        for (u32 k = 0; k < S.nadd && k < ne; ++k)
-            if (slot[k] != kNone && !before[k])
-                view_update(T, L, slot[k], true);
+                L.row[slot[k] >> 6] |= u64{1} << (slot[k] & 63);
+        // the view follows the atoms whose bit changed
+        for (u32 k = 0; k < ne; ++k)
+        {
+            const u32 sl = slot[k];
+            if (sl == kNone || sl >= T.fluent_slots)
+                continue;
+            const bool now = row_bit(L.row, sl);
+            if (now == (before[k] != 0))
+                continue;
+            before[k] = now ? 1u : 0u;  // a slot listed twice changes once
+            u32 pred, a0, a1;
+            decode_slot(T, H, sl, &pred, &a0, &a1);
+            for_view_bits(H, L, pred, a0, a1, [now](lds<u64>* word, u64 bit) {
+                if (now)
+                    *word |= bit;
+                else
+                    *word &= ~bit;
+            });
+        }
     }
-    __threadfence_block();
-    __syncthreads();
+    wave_sync();
 }
 
-__global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
+/// Whether the task's hot tables are staged in LDS.
+bool staged(const TaskDev& T) { return static_cast<u64>(T.hot_words) * 8 <= kHotMax; }
+
+/// Whether counts and picks run level-synchronously (candidate windows of several words, where the lanes' nested
+/// loops would walk long word sequences) or split over the lanes.
+bool levels(const TaskDev& T) { return T.max_step_words >= 4; }
+
+/// The kernel variant for the task.
+template<class F>
+F variant(const TaskDev& T, F ss, F sl, F gs, F gl)
+{
+    return staged(T) ? (levels(T) ? sl : ss) : (levels(T) ? gl : gs);
+}
+
+bool levels(const TaskDev& T);
+
+unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
+{
+    if (T.num_schemas > kMaxEnvSchemas)
+        throw std::invalid_argument("mymyr_amd: env: the device step keeps the successor counts of at most " + std::to_string(kMaxEnvSchemas) +
+                                    " schemas (the task has " + std::to_string(T.num_schemas) + ")");
+    const size_t hot = staged(T) ? static_cast<size_t>(T.hot_words) * 8 : 0, wave = static_cast<size_t>(wave_lds_words(T, levels(T))) * 8;
+    int nw = static_cast<int>((64 * 1024 - std::min<size_t>(hot, 64 * 1024)) / wave);
+    nw = std::clamp(nw, 1, kMaxWaves);
+    *lds_bytes = hot + static_cast<size_t>(nw) * wave;
+    if (*lds_bytes > 160 * 1024)
+        throw std::invalid_argument("mymyr_amd: env: the task's per-state LDS (" + std::to_string(*lds_bytes) +
+                                    " bytes) exceeds the 160 KiB of a gfx950 workgroup");
+    return static_cast<unsigned>(nw);
+}
+
+template<bool kStaged, bool kLevels>
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
 {
     extern __shared__ u64 smem[];
-    const TaskDev& T = *A.T;
-    const Lds L = lds_layout(smem, T);
-    const u32 lane = threadIdx.x;
+    const TaskDev& T = A.T;
+    Tab<kStaged> H;
+    lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
     const u32 Lw = A.label_width;
-    for (u64 i = blockIdx.x; i < A.rows; i += gridDim.x)
+    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
     {
-        u64* row = A.states + i * A.words;
-        build_view(T, L, row, lane);
+        u64* grow = A.states + i * A.words;
+        load_row_lds(T, L, grow, lane);
+        build_view(T, H, L, lane);
         const bool already_goal = A.at_goal[i] != 0;
-        const u32 c = count_all(T, L, row, lane);
-        // 2. the choice (env.cpp:416-440)
         enum
         {
             kOk = 0,
@@ -539,54 +1089,64 @@ __global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
             kInvalid = 2,
             kGoal = 3
         };
-        u32 st = already_goal ? kGoal : kOk;
-        u32 a = 0;
-        if (!already_goal && c == 0)
-            st = kStuck;
-        else if (!already_goal && A.actions)
-        {
-            const i64 act = A.actions[i];
-            if (act < 0 || static_cast<u64>(act) >= c)
-                st = kInvalid;
-            else
-                a = static_cast<u32>(act);
-        }
-        else if (!already_goal)
-            a = successor_index(A.cfg.seed, A.first_env + i, A.draws[i], c);
-        u32 schema = kNone, rank = 0;
-        if (st == kOk)
-        {
-            select_schema(T, L, row, a, lane, &schema, &rank);
-            if (schema == kNone || !pick(T, L, row, schema, rank, lane))
-            {
-                if (lane == 0)
-                    atomicOr(A.status, kStatusPickFailed);
-                st = kStuck;
-            }
-        }
-        if (lane == 0)
-        {
-            if (A.draws)
-                A.draws[i] += 1;
-            if (A.schema)
-                A.schema[i] = st == kOk ? static_cast<i32>(schema) : -1;
-            if (A.invalid)
-                A.invalid[i] = st == kInvalid ? 1 : 0;
-        }
-        if (A.binding)
-        {
-            const u32 arity = st == kOk ? T.schemas[schema].arity : 0;
-            for (u32 k = lane; k < Lw; k += kWave)
-                A.binding[i * Lw + k] = (st == kOk && k < arity) ? static_cast<i32>(L.bind[k * 64 + lane]) : -1;
-        }
-        // 3. the move, goal and successor count of the reached state
+        // phase 0 counts s, chooses, picks and moves; phase 1 counts the reached state s' (one copy of the count)
+        u32 c = 0, c2 = 0, st = kOk, schema = kNone;
         bool g = already_goal;
-        u32 c2 = c;
-        if (st == kOk)
+        for (u32 phase = 0; phase < 2; ++phase)
         {
-            apply_effects(T, L, row, schema, lane, A.status);
-            g = goal_test(T, row, lane);
-            c2 = count_all(T, L, row, lane);
+            const u32 cc = count_all<kLevels>(T, H, L, lane);
+            if (phase == 1)
+            {
+                c2 = cc;
+                break;
+            }
+            c = c2 = cc;
+            // 2. the choice (env.cpp:416-440)
+            st = already_goal ? kGoal : kOk;
+            u32 a = 0;
+            if (!already_goal && c == 0)
+                st = kStuck;
+            else if (!already_goal && A.actions)
+            {
+                const i64 act = A.actions[i];
+                if (act < 0 || static_cast<u64>(act) >= c)
+                    st = kInvalid;
+                else
+                    a = static_cast<u32>(act);
+            }
+            else if (!already_goal)
+                a = successor_index(A.cfg.seed, A.first_env + i, A.draws[i], c);
+            u32 rank = 0;
+            if (st == kOk)
+            {
+                select_schema(T, L, a, &schema, &rank);
+                if (schema == kNone || !pick<kLevels>(T, H, L, schema, rank, lane))
+                {
+                    if (lane == 0)
+                        atomicOr(A.status, kStatusPickFailed);
+                    st = kStuck;
+                }
+            }
+            if (lane == 0)
+            {
+                if (A.draws)
+                    A.draws[i] += 1;
+                if (A.schema)
+                    A.schema[i] = st == kOk ? static_cast<i32>(schema) : -1;
+                if (A.invalid)
+                    A.invalid[i] = st == kInvalid ? 1 : 0;
+            }
+            if (A.binding)
+            {
+                const u32 arity = st == kOk ? H.schemas[schema].arity : 0;
+                for (u32 k = lane; k < Lw; k += kWave)
+                    A.binding[i * Lw + k] = (st == kOk && k < arity) ? static_cast<i32>(L.ub[k]) : -1;
+            }
+            if (st != kOk)
+                break;
+            // 3. the move, goal and (next phase) the successor count of the reached state
+            apply_effects(T, H, L, schema, lane, A.status);
+            g = goal_test(T, H, L.row, lane);
         }
         // 4. rewards, termination, truncation (env.cpp:466-485)
         const bool dead = !A.cfg.dead_end_none && !g && ((st == kOk && c2 == 0) || st == kStuck);
@@ -619,14 +1179,17 @@ __global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
             const u32 FW = A.final_words;
             u64* f = A.final_states + i * FW;
             for (u32 k = lane; k < FW; k += kWave)
-                f[k] = k < T.W ? row[k] : 0;
+                f[k] = k < T.W ? L.row[k] : 0;
         }
-        // 5. the autoreset, or the bookkeeping of the move (the row already holds s')
+        // 5. the autoreset, or the bookkeeping of the move (the LDS row holds s')
         const bool reset = A.cfg.autoreset && (term || trunc);
         if (reset)
         {
             for (u32 k = lane; k < A.words; k += kWave)
-                row[k] = k < T.W ? T.initial[k] : 0;
+                grow[k] = k < T.W ? T.initial[k] : 0;
+            if (A.atoms)
+                for (u32 k = lane; k < T.W; k += kWave)
+                    L.row[k] = T.initial[k];
             if (lane == 0)
             {
                 if (A.count)
@@ -636,22 +1199,27 @@ __global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
                     A.steps[i] = 0;
             }
         }
-        else if (lane == 0)
+        else
         {
-            A.at_goal[i] = g ? 1 : 0;
-            if (A.steps)
-                A.steps[i] = t2;
-            if (A.count)
-                A.count[i] = static_cast<i32>(c2);
+            if (st == kOk)
+                for (u32 k = lane; k < T.W; k += kWave)
+                    grow[k] = L.row[k];
+            if (lane == 0)
+            {
+                A.at_goal[i] = g ? 1 : 0;
+                if (A.steps)
+                    A.steps[i] = t2;
+                if (A.count)
+                    A.count[i] = static_cast<i32>(c2);
+            }
         }
         // 6. the observation's encoding: true-atom slots and applicable-schema masks (LDS holds the per-schema counts
         // of the state the row holds unless the row was reset)
         if (A.atoms || A.masks)
         {
-            __threadfence_block();
-            __syncthreads();
+            wave_sync();
             if (A.atoms)
-                encode_row(row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
+                encode_row(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
             if (A.masks)
                 for (u32 s = lane; s < T.num_schemas; s += kWave)
                 {
@@ -659,41 +1227,36 @@ __global__ __launch_bounds__(kEB) void k_env_step(EnvArgs A)
                     if (reset)
                         m = A.init_masks[s];
                     else
-                        m = (s < kCountCache ? L.counts[s] : 1u) > 0 ? 1 : 0;
+                        m = L.counts[s] > 0 ? 1 : 0;
                     A.masks[i * T.num_schemas + s] = m;
                 }
-            if (A.masks && !reset && T.num_schemas > kCountCache)
-                for (u32 s = kCountCache; s < T.num_schemas; ++s)
-                {
-                    const u32 c = schema_count(T, L, row, s, lane);
-                    if (lane == 0)
-                        A.masks[i * T.num_schemas + s] = c > 0 ? 1 : 0;
-                }
         }
-        __syncthreads();
+        wave_sync();
     }
 }
 
-__global__ __launch_bounds__(kEB) void k_encode(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status)
+__global__ __launch_bounds__(kWave) void k_encode(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status)
 {
     const u32 lane = threadIdx.x;
     for (u64 i = blockIdx.x; i < rows; i += gridDim.x)
         encode_row(states + i * words, W, out + i * max_atoms, max_atoms, lane, status);
 }
 
-__global__ __launch_bounds__(kEB) void k_env_count(const TaskDev* __restrict__ Tp, const u64* states, u64 rows, u32 words, i32* count,
-                                                   u8* goal, u8* masks)
+template<bool kStaged, bool kLevels>
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(TaskDev T, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
+                                                                 u8* masks)
 {
     extern __shared__ u64 smem[];
-    const TaskDev& T = *Tp;
-    const Lds L = lds_layout(smem, T);
-    const u32 lane = threadIdx.x;
-    for (u64 i = blockIdx.x; i < rows; i += gridDim.x)
+    Tab<kStaged> H;
+    lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < rows; i += static_cast<u64>(gridDim.x) * nw)
     {
-        const u64* row = states + i * words;
-        build_view(T, L, row, lane);
-        const u32 c = count_all(T, L, row, lane);
-        const bool g = goal_test(T, row, lane);
+        load_row_lds(T, L, states + i * words, lane);
+        build_view(T, H, L, lane);
+        const u32 c = count_all<kLevels>(T, H, L, lane);
+        const bool g = goal_test(T, H, L.row, lane);
         if (lane == 0)
         {
             if (count)
@@ -704,18 +1267,17 @@ __global__ __launch_bounds__(kEB) void k_env_count(const TaskDev* __restrict__ T
         if (masks)
             for (u32 s = 0; s < T.num_schemas; ++s)
             {
-                const u32 cs = s < kCountCache ? L.counts[s] : schema_count(T, L, row, s, lane);
+                const u32 cs = L.counts[s];
                 if (lane == 0)
                     masks[i * T.num_schemas + s] = cs > 0 ? 1 : 0;
             }
-        __syncthreads();
+        wave_sync();
     }
 }
 
-__global__ void k_env_reset(const TaskDev* __restrict__ Tp, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal,
-                            i32* count, u32 init_count, u32 init_goal)
+__global__ void k_env_reset(TaskDev T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
+                            u32 init_count, u32 init_goal)
 {
-    const TaskDev& T = *Tp;
     const u64 total = rows * words;
     for (u64 k = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; k < total; k += static_cast<u64>(gridDim.x) * blockDim.x)
     {
@@ -737,26 +1299,28 @@ __global__ void k_env_reset(const TaskDev* __restrict__ Tp, u64* states, u64 row
 }
 
 // Successor listing: successor k of row i is pick(k) applied to a copy of the row.
-__global__ __launch_bounds__(kEB) void k_successors(const TaskDev* __restrict__ Tp, const u64* states, u64 rows, u32 words, u32 cap,
-                                                   i32* count, i32* schema, i32* binding, u64* succ, u32* status)
+template<bool kStaged, bool kLevels>
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, const u64* states, u64 rows, u32 words, u32 cap, i32* count,
+                                                                  i32* schema, i32* binding, u64* succ, u32* status)
 {
     extern __shared__ u64 smem[];
-    const TaskDev& T = *Tp;
-    const Lds L = lds_layout(smem, T);
-    const u32 lane = threadIdx.x;
+    Tab<kStaged> H;
+    lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
     const u32 Lw = T.label_width;
-    for (u64 i = blockIdx.x; i < rows; i += gridDim.x)
+    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < rows; i += static_cast<u64>(gridDim.x) * nw)
     {
-        const u64* row = states + i * words;
-        build_view(T, L, row, lane);
-        const u32 c = count_all(T, L, row, lane);
+        load_row_lds(T, L, states + i * words, lane);
+        build_view(T, H, L, lane);
+        const u32 c = count_all<kLevels>(T, H, L, lane);
         if (lane == 0 && count)
             count[i] = static_cast<i32>(c);
         for (u32 k = 0; k < c && k < cap; ++k)
         {
             u32 s = kNone, rank = 0;
-            select_schema(T, L, row, k, lane, &s, &rank);
-            const bool ok = s != kNone && pick(T, L, row, s, rank, lane);
+            select_schema(T, L, k, &s, &rank);
+            const bool ok = s != kNone && pick<kLevels>(T, H, L, s, rank, lane);
             if (!ok)
             {
                 if (lane == 0)
@@ -766,67 +1330,70 @@ __global__ __launch_bounds__(kEB) void k_successors(const TaskDev* __restrict__ 
             const u64 o = i * cap + k;
             if (lane == 0 && schema)
                 schema[o] = static_cast<i32>(s);
-            const DevSchema& S = T.schemas[s];
+            const auto& S = H.schemas[s];
             if (binding)
                 for (u32 q = lane; q < Lw; q += kWave)
-                    binding[o * Lw + q] = q < S.arity ? static_cast<i32>(L.bind[q * 64 + lane]) : -1;
+                    binding[o * Lw + q] = q < S.arity ? static_cast<i32>(L.ub[q]) : -1;
             if (succ)
             {
                 u64* dst = succ + o * words;
                 for (u32 q = lane; q < words; q += kWave)
-                    dst[q] = q < T.W ? row[q] : 0;
+                    dst[q] = q < T.W ? L.row[q] : 0;
                 __threadfence_block();
-                __syncthreads();
+                wave_sync();
                 if (lane == 0)
                 {
                     // delete, then add, on the copy
                     for (u32 e = S.eff_begin + S.nadd; e < S.eff_end; ++e)
                     {
-                        const u32 sl = effect_slot(T, L, T.effects[e], lane);
+                        const u32 sl = effect_slot(T, L, H.effects[e]);
                         if (sl != kNone)
                             dst[sl >> 6] &= ~(u64{1} << (sl & 63));
                     }
                     for (u32 e = S.eff_begin; e < S.eff_begin + S.nadd; ++e)
                     {
-                        const u32 sl = effect_slot(T, L, T.effects[e], lane);
+                        const u32 sl = effect_slot(T, L, H.effects[e]);
                         if (sl != kNone)
                             dst[sl >> 6] |= u64{1} << (sl & 63);
                     }
                 }
             }
-            __syncthreads();
+            wave_sync();
         }
-        __syncthreads();
+        wave_sync();
     }
 }
 
-unsigned grid_for(u64 rows) { return static_cast<unsigned>(std::min<u64>(rows, u64{1} << 20)); }
-}  // namespace
+unsigned grid_for(u64 rows, unsigned nw) { return static_cast<unsigned>(std::min<u64>((rows + nw - 1) / nw, u64{1} << 20)); }
 
-static void set_lds(const void* fn, size_t bytes)
+void set_lds(const void* fn, size_t bytes)
 {
     if (bytes > 64 * 1024)
         hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)), "LDS size");
 }
+}  // namespace
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream)
 {
     if (a.rows == 0)
         return;
-    const size_t lds = static_cast<size_t>(a.view_words + kLdsExtraWords) * sizeof(u64);
-    set_lds(reinterpret_cast<const void*>(&k_env_step), lds);
-    hipLaunchKernelGGL(k_env_step, dim3(grid_for(a.rows)), dim3(kEB), lds, stream, a);
+    size_t lds = 0;
+    const unsigned nw = waves_per_block(a.T, &lds);
+    const auto fn = variant(a.T, k_env_step<true, false>, k_env_step<true, true>, k_env_step<false, false>, k_env_step<false, true>);
+    set_lds(reinterpret_cast<const void*>(fn), lds);
+    hipLaunchKernelGGL(fn, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), lds, stream, a);
     launch_check("env step");
 }
 
-void launch_env_count(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks,
-                      hipStream_t stream)
+void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, hipStream_t stream)
 {
     if (rows == 0)
         return;
-    const size_t lds = static_cast<size_t>(Th.view_words + kLdsExtraWords) * sizeof(u64);
-    set_lds(reinterpret_cast<const void*>(&k_env_count), lds);
-    hipLaunchKernelGGL(k_env_count, dim3(grid_for(rows)), dim3(kEB), lds, stream, Td, states, rows, words, count, goal, masks);
+    size_t lds = 0;
+    const unsigned nw = waves_per_block(T, &lds);
+    const auto fn = variant(T, k_env_count<true, false>, k_env_count<true, true>, k_env_count<false, false>, k_env_count<false, true>);
+    set_lds(reinterpret_cast<const void*>(fn), lds);
+    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks);
     launch_check("env count");
 }
 
@@ -834,30 +1401,32 @@ void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out
 {
     if (rows == 0)
         return;
-    hipLaunchKernelGGL(k_encode, dim3(grid_for(rows)), dim3(kEB), 0, stream, states, rows, words, W, out, max_atoms, status);
+    hipLaunchKernelGGL(k_encode, dim3(grid_for(rows, 1)), dim3(kWave), 0, stream, states, rows, words, W, out, max_atoms, status);
     launch_check("encode atoms");
 }
 
-void launch_env_reset(const TaskDev* Td, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
+void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
                       u32 init_count, u32 init_goal, hipStream_t stream)
 {
     if (rows == 0)
         return;
     const u64 total = rows * words;
-    hipLaunchKernelGGL(k_env_reset, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(total, 256), 65536))), dim3(256), 0, stream, Td,
+    hipLaunchKernelGGL(k_env_reset, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(total, 256), 65536))), dim3(256), 0, stream, T,
                        states, rows, words, mask, steps, at_goal, count, init_count, init_goal);
     launch_check("env reset");
 }
 
-void launch_successors(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, u32 cap, i32* count, i32* schema,
-                       i32* binding, u64* succ, u32* status, hipStream_t stream)
+void launch_successors(const TaskDev& T, const u64* states, u64 rows, u32 words, u32 cap, i32* count, i32* schema, i32* binding,
+                       u64* succ, u32* status, hipStream_t stream)
 {
     if (rows == 0)
         return;
-    const size_t lds = static_cast<size_t>(Th.view_words + kLdsExtraWords) * sizeof(u64);
-    set_lds(reinterpret_cast<const void*>(&k_successors), lds);
-    hipLaunchKernelGGL(k_successors, dim3(grid_for(rows)), dim3(kEB), lds, stream, Td, states, rows, words, cap, count, schema, binding,
-                       succ, status);
+    size_t lds = 0;
+    const unsigned nw = waves_per_block(T, &lds);
+    const auto fn = variant(T, k_successors<true, false>, k_successors<true, true>, k_successors<false, false>, k_successors<false, true>);
+    set_lds(reinterpret_cast<const void*>(fn), lds);
+    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, cap, count, schema,
+                       binding, succ, status);
     launch_check("successors");
 }
 }  // namespace mya

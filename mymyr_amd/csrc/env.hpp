@@ -1,7 +1,8 @@
 #pragma once
 // The batched environment step on the device, bit-exact with HostEnv::step_row_impl (src/mymyr/rl/env.cpp:351-528):
 // choose (given index or Philox draw over the canonical successor order), move, goal, dead end, reward, termination,
-// truncation, successor count of the reached state, SAME_STEP autoreset. One wavefront per environment row.
+// truncation, successor count of the reached state, SAME_STEP autoreset. One wavefront per environment row, several
+// waves per block sharing the LDS copy of the task's hot tables.
 
 #include "lifted.hpp"
 
@@ -21,9 +22,7 @@ struct EnvCfg
 
 struct EnvArgs
 {
-    const TaskDev* T;  // device copy (kernels read it through scalar loads)
-    u32 W;             // the task's words
-    u32 view_words;
+    TaskDev T;
     EnvCfg cfg;
     u64* states;
     u64 rows;
@@ -55,23 +54,19 @@ struct EnvArgs
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream);
 
-/// count[i] (successors), goal[i] and masks [rows, num_schemas] of rows (each may be null). Td: the device copy, Th:
-/// the host copy.
-void launch_env_count(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
-                      u8* masks, hipStream_t stream);
+/// count[i] (successors), goal[i] and masks [rows, num_schemas] of rows (each may be null).
+void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, hipStream_t stream);
 
 /// Ascending true-atom slots of each row, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101).
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream);
 
 /// Resets the rows with mask[i] != 0 (all if mask is null) to the initial state: steps 0, at_goal = init_goal,
 /// count = init_count; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).
-void launch_env_reset(const TaskDev* Td, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal,
-                      i32* count, u32 init_count, u32 init_goal, hipStream_t stream);
+void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
+                      u32 init_count, u32 init_goal, hipStream_t stream);
 
 /// Per-row successor listing in canonical order (schema [rows, cap], binding [rows, cap, L], successor rows
 /// [rows, cap, words]) and counts [rows]; entries past cap are counted but not written.
-void launch_successors(const TaskDev* Td, const TaskDev& Th, const u64* states, u64 rows, u32 words, u32 cap, i32* count,
-                       i32* schema, i32* binding, u64* succ, u32* status, hipStream_t stream);
-
-size_t env_lds_bytes(const DevTaskHeader& h);
+void launch_successors(const TaskDev& T, const u64* states, u64 rows, u32 words, u32 cap, i32* count, i32* schema, i32* binding,
+                       u64* succ, u32* status, hipStream_t stream);
 }  // namespace mya

@@ -1186,8 +1186,10 @@ private:
                 const u32 last = pb + T->preds[k.pred].arity - 1;
                 p.row_bits = static_cast<u32>(C->layout.domain[last].size());
             }
+            // bulk rows are read from the state itself: only the other pairs take view words
             p.offset = view_words;
-            view_words += p.src_n * p.dst_words;
+            if (!p.bulk)
+                view_words += p.src_n * p.dst_words;
             pairs.push_back(p);
         }
         // slot decoding per fluent predicate (ascending offset)
@@ -1320,6 +1322,8 @@ private:
             h.off_pred_offset = put(offs.data(), offs.size() * sizeof(u64));
         }
         h.hot_words = img.size();
+        for (const DevStep& st : steps)
+            h.max_step_words = std::max(h.max_step_words, st.words);
         // rs tables: per position n entries (u64)
         h.num_positions = static_cast<u32>(C->layout.rs.size());
         h.off_rs = reserve_words(static_cast<size_t>(h.num_positions) * n);

@@ -187,7 +187,7 @@ struct DevPair
     u32 dir;      // 0 forward (rows by position 0's object, bits of position 1), 1 backward; unary: 0
     u32 src_lo, src_n;   // source object window (rows)
     u32 dst_lo, dst_words;  // destination object window
-    u32 offset;   // word offset of the pair's rows in the per-state view
+    u32 offset;   // word offset of the pair's rows in the per-state view (not bulk)
     u32 bulk;     // 1: row r is the state's bits [bit0 + r * row_bits, + row_bits) (dense slots, contiguous domains)
     u64 bit0;     // bulk: first state bit of row 0
     u32 row_bits; // bulk: bits per row (the destination domain's size)
@@ -237,6 +237,8 @@ struct DevTaskHeader
     u32 num_decode;
     u32 decode_arith;     // 1: slots decode arithmetically (dense slots, contiguous domains)
     u32 init_count;     // successors of the initial state (filled once the device has counted them)
+    u32 max_step_words; // the widest candidate window of any plan or filter step, in words
+    u32 pad_header;
 };
 
 /// Static k-ary relation: sorted keys sum(obj_i * n^(ar-1-i)) at [keys, keys + count).
