@@ -29,8 +29,7 @@ namespace mya
 {
 namespace
 {
-constexpr int kPB = 64;       // parents per block of the per-parent kernels (one lane each)
-constexpr int kMaxSlices = 8; // waves per block of the per-parent kernels: wave s scans action slice s
+constexpr int kTW = 4;        // waves per block of the per-parent kernels (64 parents per wave, one per lane)
 constexpr int kLB = 256;      // threads per block of the per-candidate kernels
 constexpr u64 kGeneral = 0x8000;  // fast-record flag: the action takes the general test
 
@@ -43,9 +42,7 @@ struct GroundDev
     const u32* dom_off;  // witness pruning: dominators of each action (null: none)
     const u32* dom;
     u32 num;
-    u32 num_padded;      // a multiple of 8; the padding records never apply
-    u32 slices;          // action slices per parent (waves per block)
-    u32 slice_len;       // actions per slice, a multiple of 8
+    u32 num_padded;      // a multiple of 64; the padding records never apply
 };
 
 struct GoalDev
@@ -56,141 +53,176 @@ struct GoalDev
     u32 unsat;
 };
 
-/// Byte planes of one row per thread: plane b (b < 8W) holds byte b of the thread's row, plane 8W is all ones and
-/// plane 8W + 1 all zeros (the always-true and never-true slots 64W and 64W + 8).
+/// Slot words of 64 parents, bit-sliced: word s holds bit s of each of the wave's 64 parents (bit t: parent t), for
+/// s < 64W; word kOneSlot (= 64W) holds the wave's valid parents and word kZeroSlot (= 64W + 8) nothing, so a fast record
+/// pads unused precondition slots with kOneSlot and padding actions with kZeroSlot.
 template<int W>
-struct Planes
+struct Slices
 {
-    static constexpr u32 kCount = W * 8 + 2;
     static constexpr u32 kOneSlot = W * 64;
     static constexpr u32 kZeroSlot = W * 64 + 8;
+    static constexpr u32 kWords = W * 64 + 16;
 };
 
-template<int W>
-__device__ __forceinline__ void load_planes(u8* planes, const u64* row, bool valid)
+/// 64x64 bit transpose across the wave: bit t of the result in lane s = bit s of x in lane t.
+__device__ __forceinline__ u64 transpose64(u64 x, u32 lane)
 {
-    const u32 t = threadIdx.x & (kPB - 1);
+#pragma unroll
+    for (int j = 32; j >= 1; j >>= 1)
+    {
+        const u64 m = j == 32 ? 0x00000000FFFFFFFFull
+                      : j == 16 ? 0x0000FFFF0000FFFFull
+                      : j == 8  ? 0x00FF00FF00FF00FFull
+                      : j == 4  ? 0x0F0F0F0F0F0F0F0Full
+                      : j == 2  ? 0x3333333333333333ull
+                                : 0x5555555555555555ull;
+        const u64 y = __shfl_xor(x, j, kWave);
+        x = (lane & j) ? ((x & ~m) | ((y & ~m) >> j)) : ((x & m) | ((y & m) << j));
+    }
+    return x;
+}
+
+/// Loads the rows of parents [first + base, + 64) (lane t: parent base + t, rows past n zero) bit-sliced into B.
+/// Returns the mask of the valid parents.
+template<int W>
+__device__ __forceinline__ u64 load_slices(u64* B, const u64* __restrict__ arena, u64 first, u32 base, u32 n, u32 lane)
+{
+    const u32 t = base + lane;
+    const bool valid = t < n;
+    const u64* row = arena + (first + (valid ? t : 0)) * W;
 #pragma unroll
     for (int w = 0; w < W; ++w)
-    {
-        const u64 x = valid ? row[w] : 0;
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-            planes[(w * 8 + b) * kPB + t] = static_cast<u8>(x >> (8 * b));
-    }
-    planes[(W * 8) * kPB + t] = 0xFF;
-    planes[(W * 8 + 1) * kPB + t] = 0;
+        B[w * 64 + lane] = transpose64(valid ? row[w] : 0, lane);
+    const u64 vm = __ballot(valid);
+    if (lane < 16)
+        B[W * 64 + lane] = lane < 8 ? vm : 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return vm;
 }
 
-/// Bit s of the row of the block's parent in this lane.
-__device__ __forceinline__ u32 pbit(const u8* planes, u32 s)
-{
-    return (planes[(s >> 3) * kPB + (threadIdx.x & (kPB - 1))] >> (s & 7)) & 1u;
-}
-
-__device__ __forceinline__ bool applicable(const u8* planes, const u32* __restrict__ slots, u32 m, u32 o)
+/// The parents (bit mask) for which action a's precondition list holds.
+__device__ __forceinline__ u64 holds_mask(const u64* B, const u32* __restrict__ slots, u32 m, u32 o, u64 vm)
 {
     const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF;
+    u64 r = vm;
     for (u32 i = 0; i < npos; ++i)
-        if (!pbit(planes, slots[o + i]))
-            return false;
+        r &= B[slots[o + i]];
     for (u32 i = 0; i < nneg; ++i)
-        if (pbit(planes, slots[o + npos + i]))
-            return false;
-    return true;
+        r &= ~B[slots[o + npos + i]];
+    return r;
 }
 
-/// The general test: applicable, and (witness pruning) no dominator is.
-__device__ __noinline__ bool general_emitted(const u8* planes, const GroundDev& g, u32 a)
+/// The parents for which action a is a successor: its preconditions hold and (witness pruning) no dominator's do.
+__device__ __noinline__ u64 general_mask(const u64* B, const u32* __restrict__ slots, const u32* __restrict__ meta, const u32* __restrict__ off,
+                                        const u32* __restrict__ dom_off, const u32* __restrict__ dom, u32 a, u64 vm)
 {
-    if (!applicable(planes, g.slots, g.meta[a], g.off[a]))
-        return false;
-    if (g.dom_off)
-        for (u32 k = g.dom_off[a], e = g.dom_off[a + 1]; k < e; ++k)
+    u64 r = holds_mask(B, slots, meta[a], off[a], vm);
+    if (dom_off && r)
+        for (u32 k = dom_off[a], e = dom_off[a + 1]; k < e; ++k)
         {
-            const u32 d = g.dom[k];
-            if (applicable(planes, g.slots, g.meta[d], g.off[d]))
-                return false;
+            const u32 d = dom[k];
+            r &= ~holds_mask(B, slots, meta[d], off[d], vm);
         }
-    return true;
+    return r;
 }
 
-/// Whether action a (record rec, wave-uniform) is a successor of the thread's row.
-__device__ __forceinline__ u32 action_ok(const u8* planes, const GroundDev& g, u64 rec, u32 a)
+/// The successor mask over the wave's parents of the action in this lane (record rec).
+template<int W>
+__device__ __forceinline__ u64 action_mask(const u64* B, const GroundDev& g, u64 rec, u32 a, u64 vm)
 {
     if (rec & kGeneral)
-        return general_emitted(planes, g, a) ? 1u : 0u;
-    const u32 s0 = static_cast<u32>(rec & 0x7FFF), s1 = static_cast<u32>((rec >> 16) & 0xFFFF);
-    const u32 s2 = static_cast<u32>((rec >> 32) & 0xFFFF), s3 = static_cast<u32>(rec >> 48);
-    return pbit(planes, s0) & pbit(planes, s1) & pbit(planes, s2) & pbit(planes, s3);
+        return general_mask(B, g.slots, g.meta, g.off, g.dom_off, g.dom, a, vm);
+    return B[rec & 0x7FFF] & B[(rec >> 16) & 0xFFFF] & B[(rec >> 32) & 0xFFFF] & B[rec >> 48];
 }
 
-// Counts of the parents [first, first + n): a block holds 64 parents (one per lane) and `slices` waves; wave s counts the
-// successors among actions [s * slice_len, (s + 1) * slice_len) into counts[t * slices + s]; wave 0 writes the goal flag.
+// Successor counts and goal flags of parents [first, first + n): a wave takes 64 parents bit-sliced in LDS; each lane
+// tests one action of a group of 64 against all 64 parents at once (an AND of the action's precondition slot words),
+// and a transpose turns the group's masks into each parent's 64 action bits.
 template<int W>
-__global__ __launch_bounds__(kPB * kMaxSlices) void k_ground_count(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
-                                                                  GoalDev goal, u32* __restrict__ counts, u8* __restrict__ goal_flags)
+__global__ __launch_bounds__(kTW * kWave) void k_ground_count(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g, GoalDev goal,
+                                                             u32* __restrict__ counts, u8* __restrict__ goal_flags)
 {
-    __shared__ u8 planes[Planes<W>::kCount * kPB];
-    const u32 lane = threadIdx.x & (kPB - 1), s = threadIdx.x / kPB;
-    const u32 t = blockIdx.x * kPB + lane;
-    const bool valid = t < n;
-    if (s == 0)
-        load_planes<W>(planes, arena + (first + t) * W, valid);
-    __syncthreads();
-    if (s == 0)
-    {
-        bool gl = !goal.unsat;
-        for (u32 i = 0; i < goal.npos; ++i)
-            gl = gl && pbit(planes, goal.pos[i]);
-        for (u32 i = 0; i < goal.nneg; ++i)
-            gl = gl && !pbit(planes, goal.neg[i]);
-        if (valid)
-            goal_flags[t] = gl ? 1 : 0;
-    }
-    const u32 a0 = min(s * g.slice_len, g.num_padded), a1 = min(a0 + g.slice_len, g.num_padded);
+    __shared__ u64 Bs[kTW][Slices<W>::kWords];
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave;
+    const u32 base = (blockIdx.x * kTW + wave) * kWave;
+    if (base >= n)
+        return;
+    u64* B = Bs[wave];
+    const u64 vm = load_slices<W>(B, arena, first, base, n, lane);
+    u64 gm = goal.unsat ? 0 : vm;
+    for (u32 i = 0; i < goal.npos; ++i)
+        gm &= B[goal.pos[i]];
+    for (u32 i = 0; i < goal.nneg; ++i)
+        gm &= ~B[goal.neg[i]];
     u32 cnt = 0;
-    for (u32 a = a0; a < a1; a += 8)
+    u32 a0 = 0;
+    for (; a0 + 4 * kWave <= g.num_padded; a0 += 4 * kWave)
     {
-        u64 rec[8];
+        // four independent groups in flight
+        u64 m[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            rec[j] = g.fast[a + j];
+        for (int k = 0; k < 4; ++k)
+            m[k] = action_mask<W>(B, g, g.fast[a0 + k * kWave + lane], a0 + k * kWave + lane, vm);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            cnt += action_ok(planes, g, rec[j], a + j);
+        for (int k = 0; k < 4; ++k)
+            cnt += static_cast<u32>(__popcll(transpose64(m[k], lane)));
     }
-    if (valid)
-        counts[static_cast<u64>(t) * g.slices + s] = cnt;
+    for (; a0 < g.num_padded; a0 += kWave)
+    {
+        const u32 a = a0 + lane;
+        cnt += static_cast<u32>(__popcll(transpose64(action_mask<W>(B, g, g.fast[a], a, vm), lane)));
+    }
+    const u32 t = base + lane;
+    if (t < n)
+    {
+        counts[t] = cnt;
+        goal_flags[t] = static_cast<u8>((gm >> lane) & 1);
+    }
 }
 
-// (parent, action) records of the successors of parents [first, first + n), in the layout of k_ground_count: wave s
-// writes the successors of its action slice at offsets[t * slices + s] - cand_base on, the parent index relative to
-// `first` in the high 32 bits, the action in the low.
+// (parent, action) records of the successors of parents [first, first + n) at their offsets (candidate index =
+// offsets[t] - cand_base + rank in action order): the parent index relative to `first` in the high 32 bits, the action in
+// the low.
 template<int W>
-__global__ __launch_bounds__(kPB * kMaxSlices) void k_ground_emit(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
-                                                                 const u64* __restrict__ offsets, u64 cand_base, u64* __restrict__ cand_pa)
+__global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
+                                                            const u64* __restrict__ offsets, u64 cand_base, u64* __restrict__ cand_pa)
 {
-    __shared__ u8 planes[Planes<W>::kCount * kPB];
-    const u32 lane = threadIdx.x & (kPB - 1), s = threadIdx.x / kPB;
-    const u32 t = blockIdx.x * kPB + lane;
+    __shared__ u64 Bs[kTW][Slices<W>::kWords];
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave;
+    const u32 base = (blockIdx.x * kTW + wave) * kWave;
+    if (base >= n)
+        return;
+    u64* B = Bs[wave];
+    const u64 vm = load_slices<W>(B, arena, first, base, n, lane);
+    const u32 t = base + lane;
     const bool valid = t < n;
-    if (s == 0)
-        load_planes<W>(planes, arena + (first + t) * W, valid);
-    __syncthreads();
-    u64 k = valid ? offsets[static_cast<u64>(t) * g.slices + s] - cand_base : 0;
+    u64 k = valid ? offsets[t] - cand_base : 0;
     const u64 hi = static_cast<u64>(t) << 32;
-    const u32 a0 = min(s * g.slice_len, g.num_padded), a1 = min(a0 + g.slice_len, g.num_padded);
-    for (u32 a = a0; a < a1; a += 8)
+    for (u32 a0 = 0; a0 < g.num_padded; a0 += 4 * kWave)
     {
-        u64 rec[8];
+        // four groups in flight (num_padded is a multiple of 64; groups past it are empty)
+        u64 mt[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            rec[j] = g.fast[a + j];
+        for (int q = 0; q < 4; ++q)
+        {
+            const u32 a = a0 + q * kWave + lane;
+            mt[q] = a0 + q * kWave < g.num_padded ? action_mask<W>(B, g, g.fast[a], a, vm) : 0;
+        }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (action_ok(planes, g, rec[j], a + j) && valid)
-                cand_pa[k++] = hi | (a + j);
+        for (int q = 0; q < 4; ++q)
+            mt[q] = transpose64(mt[q], lane);
+        if (!valid)
+            continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            while (mt[q])
+            {
+                const u32 bit = static_cast<u32>(__builtin_ctzll(mt[q]));
+                mt[q] &= mt[q] - 1;
+                cand_pa[k++] = hi | (a0 + q * kWave + bit);
+            }
     }
 }
 
@@ -244,26 +276,19 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     probe_insert<G, 1>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
 }
 
-// The chunk's winners with ids below `limit` into the arena (rows recomputed from their records) and the table.
+// The chunk's winners (list order, ids from *size_now) below `limit` into the arena (rows recomputed from their records)
+// and the table.
 template<int W>
-__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 m, const u64* __restrict__ cand_slot,
-                                                       u32* __restrict__ flags, const u64* __restrict__ offsets, u64 limit,
+__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 winners, const u32* __restrict__ list,
+                                                       const u64* __restrict__ cand_slot, const u64* __restrict__ size_now, u64 limit,
                                                        u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
-    const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
-    const u32 q = lane_id() % G, gbase = lane_id() - q;
-    if (j >= m)
+    const u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
+    const u32 q = lane_id() % G;
+    if (w >= winners)
         return;
-    compact_one<G, 1>(s, src, j, q, gbase, cand_slot, flags, offsets, limit, nullptr, status);
-}
-
-// The winner whose exclusive rank equals `rank`: its candidate index.
-__global__ void k_find_rank(const u32* __restrict__ flags, const u64* __restrict__ ranks, u64 n, u64 rank, u64* __restrict__ out)
-{
-    const u64 j = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (j < n && flags[j] && ranks[j] == rank)
-        *out = j;
+    compact_winner<G, 1>(s, src, w, q, list, cand_slot, *size_now, limit, nullptr, status);
 }
 
 // The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
@@ -417,8 +442,8 @@ template<int W>
 void build_action_tables(const GroundActions& ga, std::vector<u64>& fast, std::vector<u64>& masks)
 {
     const u32 num = ga.size();
-    const u32 padded = (num + 7) & ~7u;
-    constexpr u64 one = Planes<W>::kOneSlot, zero = Planes<W>::kZeroSlot;
+    const u32 padded = (num + 63) & ~63u;
+    constexpr u64 one = Slices<W>::kOneSlot, zero = Slices<W>::kZeroSlot;
     fast.assign(padded, zero | (zero << 16) | (zero << 32) | (zero << 48));
     masks.assign(static_cast<size_t>(num) * 2 * W, 0);
     for (u32 a = 0; a < num; ++a)
@@ -474,12 +499,10 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         hip_check(hipMemcpyAsync(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, stream), what);
         return d;
     };
-    // action slices: one wave per slice of at least 512 actions (up to kMaxSlices waves per 64 parents)
-    const u32 S = std::clamp<u32>(static_cast<u32>(fast.size()) / 512, 1, kMaxSlices);
-    const u32 slice_len = ((static_cast<u32>(fast.size()) / 8 + S - 1) / S) * 8;
+    constexpr u32 S = 1;  // one count and one offset per parent
     const GroundDev g{upload(fast, "action records"), upload(ga.meta, "ground meta"), upload(ga.off, "ground offsets"),
                       upload(ga.slots, "ground slots"), upload(ga.dom_off, "ground dominators"), upload(ga.dom, "ground dominators"),
-                      ga.size(), static_cast<u32>(fast.size()), S, slice_len};
+                      ga.size(), static_cast<u32>(fast.size())};
     const u64* d_masks = upload(masks, "action masks");
     const GoalDev goal{upload(task.goal_pos, "goal"), upload(task.goal_neg, "goal"), static_cast<u32>(task.goal_pos.size()),
                        static_cast<u32>(task.goal_neg.size()), task.goal_unsat ? 1u : 0u};
@@ -488,7 +511,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     // capacity: the arena holds every stored state
     const bool bounded = o.max_states != ~u64{0};
     const u64 cap_states = bounded ? std::max<u64>(1, o.max_states) : (o.memory_states ? o.memory_states : (u64{1} << 26));
-    const u64 chunk = std::max<u64>(o.chunk ? o.chunk : (u64{1} << 23), ga.size() + 1);
+    const u64 chunk = std::max<u64>(o.chunk ? o.chunk : (u64{1} << 25), ga.size() + 1);
     StateSet set;
     state_set_create(set, cap_states, W, 0.5, chunk, stream, chunk);
     struct SetGuard
@@ -603,9 +626,9 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             while (counted < lim && counted_total - base < chunk)
             {
                 const u64 est = seen_parents ? std::max<u64>(1, (seen_cands + seen_parents - 1) / seen_parents) : 1;
-                const u64 nb = std::min<u64>(lim - counted, std::max<u64>(u64{1} << 16, chunk / est));
+                const u64 nb = std::min<u64>(lim - counted, std::max<u64>(u64{1} << 18, chunk / est));
                 tm.begin(kKCount);
-                hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kPB)), dim3(kPB * S), 0, stream, set.v.arena, layer_begin + counted,
+                hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kTW * kWave)), dim3(kTW * kWave), 0, stream, set.v.arena, layer_begin + counted,
                                    static_cast<u32>(nb), g, goal, counts + counted * S, goal_flags + counted);
                 launch_check("ground count");
                 tm.end(kKCount, nb * (R + 5));
@@ -650,7 +673,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             if (m > 0)
             {
                 tm.begin(kKEmit);
-                hipLaunchKernelGGL(k_ground_emit<W>, dim3(blocks_for(np, kPB)), dim3(kPB * S), 0, stream, set.v.arena, layer_begin + p0, np, g,
+                hipLaunchKernelGGL(k_ground_emit<W>, dim3(blocks_for(np, kTW * kWave)), dim3(kTW * kWave), 0, stream, set.v.arena, layer_begin + p0, np, g,
                                    offsets + p0 * S, base, cand_pa);
                 launch_check("ground emit");
                 tm.end(kKEmit, np * (R + 8) + m * 8);
@@ -661,7 +684,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 tm.end(kKInsert, 0);
                 tm.begin(kKRank);
                 state_set_rank(set, m, stream);
-                tm.end(kKRank, m * 16);
+                tm.end(kKRank, m * 9 + winners * 4);
                 hip_check(hipMemcpyAsync(small + kSizeNow, state_set_size_now(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
                 hip_check(hipMemcpyAsync(small + kSizeNext, state_set_size_next(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
                 hip_check(hipMemcpyAsync(small + kCut, set.d_status, sizeof(u32), hipMemcpyDeviceToDevice, stream), "status");
@@ -676,20 +699,19 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             const u64 room = (bounded ? o.max_states : cap_states) - set.size;
             if (winners >= room && winners > 0 && bounded)
             {
-                // the store fills at the winner of id max_states - 1: stop inside its parent's expansion
-                set_small(kCut, ~u64{0});
-                hipLaunchKernelGGL(k_find_rank, dim3(blocks_for(m, 256)), dim3(256), 0, stream, set.flags, set.offsets, m, o.max_states - 1,
-                                   small + kCut);
-                sync_small();
-                const u64 jcut = b.host[kCut];
+                // the store fills at winner room - 1 (id max_states - 1): stop inside its parent's expansion
+                u32 jc = 0;
+                hip_check(hipMemcpyAsync(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost, stream), "cut");
+                hip_check(hipStreamSynchronize(stream), "sync");
+                const u64 jcut = jc;
                 hip_check(hipMemcpyAsync(b.host + kCut, cand_pa + jcut, sizeof(u64), hipMemcpyDeviceToHost, stream), "parent");
                 hip_check(hipStreamSynchronize(stream), "sync");
                 const u64 pc = b.host[kCut] >> 32;  // the parent, relative to p0
                 tm.begin(kKCompact);
-                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
-                                   set.flags, set.offsets, o.max_states, reinterpret_cast<u32*>(small + kSpare));
+                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(winners * G, kLB)), dim3(kLB), 0, stream, set.v, src, winners, set.list,
+                                   set.cand_slot, state_set_size_now(set), o.max_states, reinterpret_cast<u32*>(small + kSpare));
                 launch_check("ground compact");
-                tm.end(kKCompact, m * 12 + room * (2 * R + 16));
+                tm.end(kKCompact, room * (2 * R + 28));
                 state_set_flip(set);
                 row[0] += pc + 1;
                 row[1] += jcut + 1;
@@ -706,11 +728,14 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             if (m > 0)
             {
                 tm.begin(kKCompact);
-                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
-                                   set.flags, set.offsets, cap_states, set.d_status);
-                launch_check("ground compact");
-                // flags, ids and slots of every candidate; the winners' records, parent rows (in L2), arena rows and entries
-                tm.end(kKCompact, m * 12 + winners * (2 * R + 16));
+                if (winners > 0)
+                {
+                    hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(winners * G, kLB)), dim3(kLB), 0, stream, set.v, src, winners,
+                                       set.list, set.cand_slot, state_set_size_now(set), cap_states, set.d_status);
+                    launch_check("ground compact");
+                }
+                // per winner: its list entry, record, slot and parent row (in L2 across a parent's winners), arena row and entry
+                tm.end(kKCompact, winners * (2 * R + 28));
                 state_set_flip(set);
             }
             set.size += winners;

@@ -114,7 +114,104 @@ __global__ __launch_bounds__(kScanBlock) void k_offsets(const u32* __restrict__ 
         off += v[k];
     }
 }
+// One block scans the block sums in place (exclusive, from 0) and writes *total = *total_base + the grand total.
+__global__ __launch_bounds__(1024) void k_scan_sums_rel(u64* __restrict__ sums, u64 nb, u64* total, const u64* total_base)
+{
+    __shared__ u64 lds[1024 / kWave + 1];
+    __shared__ u64 carry;
+    if (threadIdx.x == 0)
+        carry = 0;
+    __syncthreads();
+    for (u64 b0 = 0; b0 < nb; b0 += 1024)
+    {
+        const u64 i = b0 + threadIdx.x;
+        const u64 v = i < nb ? sums[i] : 0;
+        const u64 inc = wave_inclusive64(v);
+        const u32 wave = threadIdx.x / kWave;
+        if (lane_id() == kWave - 1)
+            lds[wave] = inc;
+        __syncthreads();
+        if (threadIdx.x == 0)
+        {
+            u64 run = 0;
+            for (int w = 0; w < 1024 / kWave; ++w)
+            {
+                const u64 t = lds[w];
+                lds[w] = run;
+                run += t;
+            }
+            lds[1024 / kWave] = run;
+        }
+        __syncthreads();
+        if (i < nb)
+            sums[i] = carry + lds[wave] + inc - v;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            carry += lds[1024 / kWave];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        *total = (total_base ? *total_base : 0) + carry;
+}
+
+// The winners' indices in order (list[rank] = j for flags[j] != 0), is_new[j] = flags[j] (optional), and the losers'
+// flags reset to 1.
+__global__ __launch_bounds__(kScanBlock) void k_winner_list(u32* __restrict__ flags, u64 n, const u64* __restrict__ sums,
+                                                           u32* __restrict__ list, u8* __restrict__ is_new)
+{
+    __shared__ u64 lds[kScanBlock / kWave + 1];
+    const u64 base = static_cast<u64>(blockIdx.x) * kScanBlock * kPerThread;
+    const u64 first = base + static_cast<u64>(threadIdx.x) * kPerThread;
+    u32 v[kPerThread];
+    u64 s = 0;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        v[k] = first + k < n ? flags[first + k] : 0;
+        s += v[k];
+    }
+    const u64 inc = wave_inclusive64(s);
+    const u32 wave = threadIdx.x / kWave;
+    if (lane_id() == kWave - 1)
+        lds[wave] = inc;
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        u64 run = 0;
+        for (int w = 0; w < kScanBlock / kWave; ++w)
+        {
+            const u64 t = lds[w];
+            lds[w] = run;
+            run += t;
+        }
+    }
+    __syncthreads();
+    u64 off = sums[blockIdx.x] + lds[wave] + inc - s;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        const u64 j = first + k;
+        if (j >= n)
+            break;
+        if (v[k])
+            list[off++] = static_cast<u32>(j);
+        else
+            flags[j] = 1;
+        if (is_new)
+            is_new[j] = static_cast<u8>(v[k]);
+    }
+}
 }  // namespace
+
+void launch_winner_list(u32* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u8* is_new, hipStream_t stream)
+{
+    const u64 nb = (n + kScanBlock * kPerThread - 1) / (kScanBlock * kPerThread);
+    if (nb > 0)
+        hipLaunchKernelGGL(k_block_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch);
+    hipLaunchKernelGGL(k_scan_sums_rel, dim3(1), dim3(1024), 0, stream, scratch, nb, total, total_base);
+    if (nb > 0)
+        hipLaunchKernelGGL(k_winner_list, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, list, is_new);
+}
 
 void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream, const u64* base)
 {

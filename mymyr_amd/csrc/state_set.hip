@@ -66,17 +66,20 @@ __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __
     probe_insert<G, K>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
 }
 
+// Compaction over the batch's winners (their count: size_next - size_now, read on the device).
 template<int G, int K>
-__global__ __launch_bounds__(kBlock) void k_compact(StateSetView s, const u64* __restrict__ rows, u64 n, const u64* __restrict__ cand_slot,
-                                                   u32* __restrict__ flags, const u64* __restrict__ offsets, u64 limit,
-                                                   u8* __restrict__ is_new, u32* __restrict__ status)
+__global__ __launch_bounds__(kBlock) void k_compact(StateSetView s, const u64* __restrict__ rows, const u32* __restrict__ list,
+                                                   const u64* __restrict__ cand_slot, const u64* __restrict__ size_now,
+                                                   const u64* __restrict__ size_next, u64 limit, u8* __restrict__ is_new,
+                                                   u32* __restrict__ status)
 {
-    u64 j;
+    u64 w;
     u32 q, gbase;
-    group_of<G>(j, q, gbase);
-    if (j >= n)
+    group_of<G>(w, q, gbase);
+    const u64 id0 = *size_now;
+    if (w >= *size_next - id0)
         return;
-    compact_one<G, K>(s, BufferRows{rows, s.words}, j, q, gbase, cand_slot, flags, offsets, limit, is_new, status);
+    compact_winner<G, K>(s, BufferRows{rows, s.words}, w, q, list, cand_slot, id0, limit, is_new, status);
 }
 
 __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u64* __restrict__ cand_slot, u64 n, i64* __restrict__ ids)
@@ -215,7 +218,7 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
     s.v.arena = dev_alloc<u64>(max_states * words, "state set arena");
     s.cand_slot = dev_alloc<u64>(s.batch_cap, "state set batch slots");
     s.flags = dev_alloc<u32>(s.batch_cap, "state set batch flags");
-    s.offsets = dev_alloc<u64>(s.batch_cap, "state set batch offsets");
+    s.list = dev_alloc<u32>(s.batch_cap, "state set batch winners");
     s.scan_scratch = dev_alloc<u64>(scan_scratch_words(s.batch_cap), "state set scan scratch");
     s.d_size = dev_alloc<u64>(2, "state set size");
     s.d_status = dev_alloc<u32>(1, "state set status");
@@ -232,7 +235,7 @@ void state_set_destroy(StateSet& s)
     dev_free(s.v.arena);
     dev_free(s.cand_slot);
     dev_free(s.flags);
-    dev_free(s.offsets);
+    dev_free(s.list);
     dev_free(s.scan_scratch);
     dev_free(s.d_size);
     dev_free(s.d_status);
@@ -251,9 +254,9 @@ void state_set_clear(StateSet& s, hipStream_t stream)
     s.last = stream;
 }
 
-void state_set_rank(StateSet& s, u64 n, hipStream_t stream)
+void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
 {
-    launch_exclusive_scan(s.flags, s.offsets, n, s.scan_scratch, state_set_size_next(s), stream, state_set_size_now(s));
+    launch_winner_list(s.flags, n, s.scan_scratch, state_set_size_next(s), state_set_size_now(s), s.list, is_new, stream);
     launch_check("state set rank");
 }
 
@@ -282,9 +285,9 @@ void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new,
             hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, s.cand_slot, s.flags,
                                s.d_status);
             launch_check("state set probe");
-            state_set_rank(s, m, stream);
-            hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, s.cand_slot, s.flags,
-                               s.offsets, s.max_states, is_new ? is_new + done : nullptr, s.d_status);
+            state_set_rank(s, m, stream, is_new ? is_new + done : nullptr);
+            hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, s.list, s.cand_slot,
+                               state_set_size_now(s), state_set_size_next(s), s.max_states, is_new ? is_new + done : nullptr, s.d_status);
             launch_check("state set compact");
             if (ids)
             {

@@ -8,9 +8,9 @@
 // of the winner flags). The probe hash is the public state hash (hash_state); slot = fastrange of its low 32 bits over
 // the capacity, tag = its high 32 bits, linear probing.
 //
-// A batch is three launches on one stream: probe (group of lanes per row: hash, probe, CAS or atomicMin, loser
-// flags), the exclusive scan of the winner flags (ids = the set's size + rank), and compaction (winner rows into the
-// arena, entries settled). The set's size lives on the device in two words used alternately (the scan of a batch
+// A batch is three steps on one stream: probe (group of lanes per row: hash, probe, CAS or atomicMin, loser flags),
+// the winner list (a scan of the flags: winner w gets id = the set's size + w), and compaction over the winners
+// (rows into the arena, entries settled). The set's size lives on the device in two words used alternately (the scan of a batch
 // writes next = current + winners), so batches need no host synchronization; the host copy is refreshed by the
 // calls that synchronize.
 
@@ -28,7 +28,7 @@ struct StateSet
     u64 batch_cap = 0;
     u64* cand_slot = nullptr;  // [batch_cap] probe result per candidate (state_set_device.hpp encodings)
     u32* flags = nullptr;      // [batch_cap] winner flags, 1 at rest
-    u64* offsets = nullptr;    // [batch_cap] ids of the winners (size + exclusive rank)
+    u32* list = nullptr;       // [batch_cap] the winners' candidate indices in order (winner w gets id size + w)
     u64* scan_scratch = nullptr;
     u64* d_size = nullptr;     // [2] the size, alternating per batch
     u32* d_status = nullptr;   // sticky kStatus* bits
@@ -61,8 +61,9 @@ inline u64* state_set_size_now(StateSet& s) { return s.d_size + s.cur; }
 inline u64* state_set_size_next(StateSet& s) { return s.d_size + (s.cur ^ 1); }
 inline void state_set_flip(StateSet& s) { s.cur ^= 1; }
 
-/// The winner scan of a batch of n candidates: offsets[j] = size + rank of winner j; next size = size + winners.
-void state_set_rank(StateSet& s, u64 n, hipStream_t stream);
+/// The winners of a batch of n candidates in order into s.list (losers' flags reset), is_new[j] (optional) the flags,
+/// and next size = size + winners.
+void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new = nullptr);
 
 /// hash_state of every row (a group of lanes per row).
 void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t stream);

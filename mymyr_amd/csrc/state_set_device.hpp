@@ -10,8 +10,8 @@
 // (include/mymyr/cuda/state_set.hpp:2-18): among equal candidates the smallest candidate index wins (64-bit atomicMin
 // on the pending entry), new ids follow candidate order.
 //
-// Winner flags need no second pass over the table: every candidate starts at flag 1 (set by the previous kernel on
-// the stream), and only zeros are written during the probe: a candidate equal to a stored state, and the larger
+// Winner flags need no second pass over the table: every candidate starts at flag 1 (the winner list of the previous
+// batch resets the zeros), and only zeros are written during the probe: a candidate equal to a stored state, and the larger
 // index of every atomicMin exchange between two pending candidates. Every candidate but the smallest of its
 // content is the larger index of exactly one exchange, so the flags that stay 1 are exactly the winners. Rows of
 // other candidates are never read back from memory written in the same kernel (a row source recomputes them), so no
@@ -232,31 +232,22 @@ __device__ void probe_insert(const StateSetView& s, const Src& src, u64 j, const
     }
 }
 
-/// Winner j with id offsets[j] < limit: its row into the arena and its entry settled to id + 1. Resets flags[j] to 1
-/// for the next batch. Ids at or past limit set kStatusCapacity.
+/// Winner w of the batch (candidate j = list[w], id = id0 + w): below `limit` its row into the arena and its entry settled
+/// to id + 1; at or past it, kStatusCapacity (and is_new[j] = 0).
 template<int G, int K, class Src>
-__device__ __forceinline__ void compact_one(const StateSetView& s, const Src& src, u64 j, u32 q, u32 gbase,
-                                            const u64* __restrict__ cand_slot, u32* __restrict__ flags,
-                                            const u64* __restrict__ offsets, u64 limit, u8* __restrict__ is_new,
-                                            u32* __restrict__ status)
+__device__ __forceinline__ void compact_winner(const StateSetView& s, const Src& src, u64 w, u32 q, const u32* __restrict__ list,
+                                               const u64* __restrict__ cand_slot, u64 id0, u64 limit, u8* __restrict__ is_new,
+                                               u32* __restrict__ status)
 {
-    const bool win = flags[j] != 0;
-    if (q == 0)
-    {
-        if (!win)
-            flags[j] = 1;
-        if (is_new)
-            is_new[j] = 0;
-    }
-    if (!win)
-        return;
-    const u64 id = offsets[j];
+    const u64 j = list[w];
+    const u64 id = id0 + w;
     if (id >= limit)
     {
         if (q == 0)
         {
             atomicOr(status, kStatusCapacity);
-            flags[j] = 1;
+            if (is_new)
+                is_new[j] = 0;
         }
         return;
     }
@@ -267,9 +258,6 @@ __device__ __forceinline__ void compact_one(const StateSetView& s, const Src& sr
     {
         const u64 cs = cand_slot[j];
         s.table[static_cast<u32>(cs)] = (cs & 0xFFFFFFFF00000000ull) | static_cast<u32>(id + 1);
-        flags[j] = 1;
-        if (is_new)
-            is_new[j] = 1;
     }
 }
 }  // namespace mya
