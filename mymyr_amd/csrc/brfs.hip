@@ -256,7 +256,9 @@ struct ParentRows
 };
 
 template<int W>
-constexpr int kGroup = W >= 2 ? W / 2 : 1;  // lanes per candidate row (16 bytes each)
+constexpr int kGroup = W >= 4 ? W / 4 : 1;  // lanes per candidate row (32 bytes each)
+template<int W>
+constexpr int kPairs = W >= 4 ? 2 : 1;  // word pairs per lane
 
 // Candidates [0, m) of a chunk into the state set: a group of lanes per candidate forms its row, hashes it and probes
 // the table (a stored equal row drops it; a pending equal row takes part in the smallest-index rule; an empty slot
@@ -270,10 +272,10 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     const u32 q = lane_id() % G, gbase = lane_id() - q;
     if (j >= m)
         return;
-    Slice<G, 1> me;
+    Slice<G, kPairs<W>> me;
     src.load(j, q, me);
-    const u64 h = group_hash<G, 1>(me, q, gbase);
-    probe_insert<G, 1>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
+    const u64 h = group_hash<G, kPairs<W>>(me, q, gbase);
+    probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
 }
 
 // The chunk's winners (list order, ids from *size_now) below `limit` into the arena (rows recomputed from their records)
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
     const u32 q = lane_id() % G;
     if (w >= winners)
         return;
-    compact_winner<G, 1>(s, src, w, q, list, cand_slot, *size_now, limit, nullptr, status);
+    compact_winner<G, kPairs<W>>(s, src, w, q, list, cand_slot, *size_now, limit, nullptr, status);
 }
 
 // The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
