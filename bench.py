@@ -38,12 +38,14 @@ def cpu_threads() -> int:
 
 
 def load_traffic(kernel: str):
-    """HBM bytes per launch measured by rocprofv3 PMC counters (profiles/pmc_<kernel>.json), if committed."""
-    p = os.path.join(ROOT, "profiles", f"pmc_{kernel}.json")
+    """HBM bytes per launch of a kernel, measured by rocprofv3 PMC counters (FETCH_SIZE, WRITE_SIZE, scaled by a plain
+    copy of known size) and committed in profiles/pmc_traffic.json; None if not measured."""
+    p = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        k = json.load(f).get("kernels", {}).get(kernel)
+    return k.get("traffic_bytes_per_launch") if k else None
 
 
 def bench_strips(steps: int, warmup: int, cpu: bool):
@@ -179,10 +181,13 @@ def bench_dedup(steps: int, warmup: int, cpu: bool):
     wall = sum(times) / len(times)
     R = words * 8
     alg = total * (R + 8) + unique * (R + 8) + (total - unique) * R
+    nb = total // batch
     out = {"rows_per_s": total / wall, "unique": unique, "rows": total, "ms_per_step": wall * 1e3,
            "roofline": {"bound": "hbm", "achieved": round(alg / wall / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4), "kernel": "state-set insert pipeline (hash, probe, rank, compact)",
-                        "traffic": load_traffic("state_set_probe")}}
+                        "frac": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4),
+                        "kernel": "state-set batch insert (probe, winner scan, compaction) per 2^20-row batch",
+                        "bytes_per_launch": int(alg / nb), "ms_per_launch": round(wall * 1e3 / nb, 4),
+                        "traffic": load_traffic("dedup_batch")}}
     if cpu:
         from oracle import port
 
