@@ -85,7 +85,9 @@ def bench_strips(steps: int, warmup: int, cpu: bool):
                    "layer_counts": r.layer_counts, "generated_per_s": sum(x.generated for x in results) / wall,
                    "kernel_ms_per_step": {c: round(ms[c] / steps, 3) for c in classes},
                    "kernel_gbs": {c: round(by[c] / (ms[c] * 1e-3) / 1e9, 1) if ms[c] else None for c in classes},
-                   "whole_search_gbs": round(sum(by.values()) / wall / 1e9, 1)},
+                   "whole_search_gbs": round(sum(by.values()) / wall / 1e9, 1),
+                   "search_ms": round(sum(x.search_s for x in results) * 1e3 / steps, 3),
+                   "device_ms": round(sum(x.device_s for x in results) * 1e3 / steps, 3)},
     }
     if cpu:
         out["cpu_baseline"] = cpu_strips(path, w)

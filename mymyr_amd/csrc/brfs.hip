@@ -278,19 +278,20 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
 }
 
-// The chunk's winners (list order, ids from *size_now) below `limit` into the arena (rows recomputed from their records)
-// and the table.
+// The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena
+// (rows recomputed from their records) and the table.
 template<int W>
-__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 winners, const u32* __restrict__ list,
-                                                       const u64* __restrict__ cand_slot, const u64* __restrict__ size_now, u64 limit,
-                                                       u32* __restrict__ status)
+__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 m, const u32* __restrict__ list,
+                                                       const u64* __restrict__ cand_slot, const u64* __restrict__ size_now,
+                                                       const u64* __restrict__ size_next, u64 limit, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
     const u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
     const u32 q = lane_id() % G;
-    if (w >= winners)
+    const u64 id0 = *size_now;
+    if (w >= m || w >= *size_next - id0)
         return;
-    compact_winner<G, kPairs<W>>(s, src, w, q, list, cand_slot, *size_now, limit, nullptr, status);
+    compact_winner<G, kPairs<W>>(s, src, w, q, list, cand_slot, id0, limit, nullptr, status);
 }
 
 // The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
@@ -390,8 +391,8 @@ public:
     {
         for (auto& e : m_ev)
         {
-            (void)hipEventDestroy(e.a);
-            (void)hipEventDestroy(e.b);
+            event_release(e.a);
+            event_release(e.b);
         }
     }
     void begin(int k)
@@ -399,8 +400,8 @@ public:
         if (!m_on)
             return;
         Pair p{k, nullptr, nullptr};
-        hip_check(hipEventCreate(&p.a), "event");
-        hip_check(hipEventCreate(&p.b), "event");
+        p.a = event_acquire();
+        p.b = event_acquire();
         hip_check(hipEventRecord(p.a, m_s), "event");
         m_ev.push_back(p);
     }
@@ -421,8 +422,8 @@ public:
             float ms = 0;
             hip_check(hipEventElapsedTime(&ms, e.a, e.b), "event time");
             m_r.kernel_ms[e.k] += ms;
-            (void)hipEventDestroy(e.a);
-            (void)hipEventDestroy(e.b);
+            event_release(e.a);
+            event_release(e.b);
         }
         m_ev.clear();
     }
@@ -622,13 +623,73 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         bool goal_stop = false;
         set_small(kGoalSum, 0);
         u64 p0 = 0, base = 0;  // base = offsets[p0 * S]
+        constexpr int G = kGroup<W>;
+        // The chunk whose kernels are queued but whose outcome (its winners) the host has not read yet: it is confirmed
+        // at the next synchronization, which precedes the next chunk's emit and rank (its records and winner list are
+        // intact until then), so the driver synchronizes once per chunk.
+        struct Pending
+        {
+            bool live = false;
+            u64 p0 = 0, np = 0, m = 0;
+        } pend;
+        // confirms the pending chunk from the set's size and status read at the last synchronization; true if the
+        // store filled inside it (the search stops there)
+        auto confirm = [&](u64 size_dev, u32 status) {
+            if (!pend.live)
+                return false;
+            pend.live = false;
+            if (status & kStatusTableFull)
+                throw std::length_error("mymyr_amd: brfs: state table full");
+            const u64 winners = size_dev - set.size;
+            const u64 room = (bounded ? o.max_states : cap_states) - set.size;
+            // insert: every candidate's record, probe entry and slot, the parent rows, and the row each non-winner
+            // compared equal to; compaction: per winner its list entry, record, slot, arena row and entry
+            tm.bytes(kKInsert, pend.m * 24 + pend.np * R + (pend.m - std::min(winners, pend.m)) * R);
+            tm.bytes(kKRank, pend.m * 9 + winners * 4);
+            if (bounded && winners >= room && winners > 0)
+            {
+                // the store filled at winner room - 1 (id max_states - 1): the search stops inside its parent's
+                // expansion; the compaction wrote ids below max_states only
+                tm.bytes(kKCompact, room * (2 * R + 28));
+                u32 jc = 0;
+                hip_check(hipMemcpyAsync(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost, stream), "cut");
+                hip_check(hipStreamSynchronize(stream), "sync");
+                hip_check(hipMemcpyAsync(b.host + kCut, cand_pa + jc, sizeof(u64), hipMemcpyDeviceToHost, stream), "parent");
+                hip_check(hipStreamSynchronize(stream), "sync");
+                const u64 pc = b.host[kCut] >> 32;  // the parent, relative to the chunk's first
+                row[0] += pc + 1;
+                row[1] += u64{jc} + 1;
+                hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pc + 1, 256), 1024)), dim3(256), 0, stream, goal_flags + pend.p0,
+                                   pc + 1, small + kGoalSum);
+                set.size = o.max_states;
+                r.status = kOutOfStates;
+                stopped = true;
+                return true;
+            }
+            if (winners > room)
+                throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
+                                        " states of device memory (set max_states or memory_states)");
+            tm.bytes(kKCompact, winners * (2 * R + 28));
+            set.size = size_dev;
+            row[0] += pend.np;
+            row[1] += pend.m;
+            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pend.np, 256), 1024)), dim3(256), 0, stream, goal_flags + pend.p0,
+                               pend.np, small + kGoalSum);
+            return false;
+        };
+        auto read_state = [&] {
+            hip_check(hipMemcpyAsync(small + kSizeNow, state_set_size_now(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
+            hip_check(hipMemcpyAsync(small + kCut, set.d_status, sizeof(u32), hipMemcpyDeviceToDevice, stream), "status");
+        };
         while (p0 < lim && !stopped)
         {
-            // count ahead until the counted parents past p0 hold a full chunk (or the layer's rest)
-            while (counted < lim && counted_total - base < chunk)
+            // count ahead when the counted parents past p0 hold less than a full chunk (and the layer has more)
+            const bool count_now = counted < lim && counted_total - base < chunk;
+            u64 nb = 0;
+            if (count_now)
             {
                 const u64 est = seen_parents ? std::max<u64>(1, (seen_cands + seen_parents - 1) / seen_parents) : 1;
-                const u64 nb = std::min<u64>(lim - counted, std::max<u64>(u64{1} << 18, chunk / est));
+                nb = std::min<u64>(lim - counted, std::max<u64>(u64{1} << 18, chunk / est));
                 tm.begin(kKCount);
                 hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kTW * kWave)), dim3(kTW * kWave), 0, stream, set.v.arena, layer_begin + counted,
                                    static_cast<u32>(nb), g, goal, counts + counted * S, goal_flags + counted);
@@ -643,7 +704,14 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 hip_check(hipMemcpyAsync(small + kBlockTotal, offsets + (counted + nb) * S, sizeof(u64), hipMemcpyDeviceToDevice, stream), "total");
                 launch_check("count scan");
                 tm.end(kKOther, 0);
-                sync_small();
+            }
+            // the chunk end over what is counted, and the pending chunk's outcome, in one synchronization
+            hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, std::min(counted + nb, lim), base + chunk, small + kChunkP);
+            launch_check("chunk end");
+            read_state();
+            sync_small();
+            if (count_now)
+            {
                 const u64 total = b.host[kBlockTotal];
                 seen_parents += nb;
                 seen_cands += total - counted_total;
@@ -661,17 +729,24 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 }
                 counted += nb;
             }
+            if (confirm(b.host[kSizeNow], static_cast<u32>(b.host[kCut])))
+                break;
             if (p0 >= lim)
                 break;
-            hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, std::min(counted, lim), base + chunk, small + kChunkP);
-            launch_check("chunk end");
-            sync_small();
-            const u64 p1 = b.host[kChunkP], end_off = b.host[kChunkOff];
+            if (counted < lim && counted_total - base < chunk)
+                continue;  // count more parents before this chunk
+            u64 p1 = b.host[kChunkP], end_off = b.host[kChunkOff];
+            if (p1 > lim)
+            {
+                // a goal found by this count ends the layer's expansion before the chunk end: the chunk ends there
+                p1 = lim;
+                hip_check(hipMemcpyAsync(b.host + kChunkOff, offsets + lim * S, sizeof(u64), hipMemcpyDeviceToHost, stream), "chunk end");
+                hip_check(hipStreamSynchronize(stream), "sync");
+                end_off = b.host[kChunkOff];
+            }
             const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
-            u64 winners = 0;
             const ParentRows<W> src{set.v.arena, layer_begin + p0, cand_pa, d_masks};
-            constexpr int G = kGroup<W>;
             if (m > 0)
             {
                 tm.begin(kKEmit);
@@ -686,67 +761,26 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 tm.end(kKInsert, 0);
                 tm.begin(kKRank);
                 state_set_rank(set, m, stream);
-                tm.end(kKRank, m * 9 + winners * 4);
-                hip_check(hipMemcpyAsync(small + kSizeNow, state_set_size_now(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
-                hip_check(hipMemcpyAsync(small + kSizeNext, state_set_size_next(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
-                hip_check(hipMemcpyAsync(small + kCut, set.d_status, sizeof(u32), hipMemcpyDeviceToDevice, stream), "status");
-                sync_small();
-                if (static_cast<u32>(b.host[kCut]) & kStatusTableFull)
-                    throw std::length_error("mymyr_amd: brfs: state table full");
-                winners = b.host[kSizeNext] - b.host[kSizeNow];
-                // insert: every candidate's record, its probe entry and its slot, the parent rows, and the row each
-                // non-winner compared equal to
-                tm.bytes(kKInsert, m * 24 + u64{np} * R + (m - winners) * R);
-            }
-            const u64 room = (bounded ? o.max_states : cap_states) - set.size;
-            if (winners >= room && winners > 0 && bounded)
-            {
-                // the store fills at winner room - 1 (id max_states - 1): stop inside its parent's expansion
-                u32 jc = 0;
-                hip_check(hipMemcpyAsync(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost, stream), "cut");
-                hip_check(hipStreamSynchronize(stream), "sync");
-                const u64 jcut = jc;
-                hip_check(hipMemcpyAsync(b.host + kCut, cand_pa + jcut, sizeof(u64), hipMemcpyDeviceToHost, stream), "parent");
-                hip_check(hipStreamSynchronize(stream), "sync");
-                const u64 pc = b.host[kCut] >> 32;  // the parent, relative to p0
+                tm.end(kKRank, 0);
+                // the winners' count is on the device (size next - size now); ids from max_states on are not written
+                // (the store filled: the confirmation finds the cut)
                 tm.begin(kKCompact);
-                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(winners * G, kLB)), dim3(kLB), 0, stream, set.v, src, winners, set.list,
-                                   set.cand_slot, state_set_size_now(set), o.max_states, reinterpret_cast<u32*>(small + kSpare));
+                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.list,
+                                   set.cand_slot, state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states,
+                                   bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
                 launch_check("ground compact");
-                tm.end(kKCompact, room * (2 * R + 28));
-                state_set_flip(set);
-                row[0] += pc + 1;
-                row[1] += jcut + 1;
-                hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pc + 1, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, pc + 1,
-                                   small + kGoalSum);
-                set.size = o.max_states;
-                r.status = kOutOfStates;
-                stopped = true;
-                break;
-            }
-            if (winners > room)
-                throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
-                                        " states of device memory (set max_states or memory_states)");
-            if (m > 0)
-            {
-                tm.begin(kKCompact);
-                if (winners > 0)
-                {
-                    hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(winners * G, kLB)), dim3(kLB), 0, stream, set.v, src, winners,
-                                       set.list, set.cand_slot, state_set_size_now(set), cap_states, set.d_status);
-                    launch_check("ground compact");
-                }
-                // per winner: its list entry, record, slot and parent row (in L2 across a parent's winners), arena row and entry
-                tm.end(kKCompact, winners * (2 * R + 28));
+                tm.end(kKCompact, 0);
                 state_set_flip(set);
             }
-            set.size += winners;
-            row[0] += np;
-            row[1] += m;
-            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(np, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, np,
-                               small + kGoalSum);
+            pend = Pending{true, p0, np, m};
             p0 = p1;
             base = end_off;
+        }
+        if (!stopped && pend.live)
+        {
+            read_state();
+            sync_small();
+            confirm(b.host[kSizeNow], static_cast<u32>(b.host[kCut]));
         }
         sync_small();
         r.goal_states += b.host[kGoalSum];
