@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 2
+#define MYA_ABI_VERSION 3
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -250,6 +250,100 @@ typedef struct mya_brfs_result
  * {expanded, generated, new} per expanded layer. Returns the number of layers, or -1. Synchronous. */
 int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts,
              uint32_t cap);
+
+/* ---------------------------------------------------------------------------------------------------------- DLPack */
+
+/* Device arrays handed to other frameworks without a copy (replaces the reference's DLArray export,
+ * python/src/arrays.cpp:100-235, and its stream handoff, python/src/dlpack.hpp:1-94). The structs below have the
+ * layout of DLPack 1.x's DLDevice, DLDataType, DLTensor, DLManagedTensor (legacy) and DLManagedTensorVersioned,
+ * under this library's names so that the header can sit beside a caller's own dlpack.h. */
+#define MYA_DL_ROCM 10 /* kDLROCM */
+#define MYA_DL_INT 0
+#define MYA_DL_UINT 1
+#define MYA_DL_FLOAT 2
+#define MYA_DL_BOOL 6
+#define MYA_DL_FLAG_READ_ONLY 1u /* DLPACK_FLAG_BITMASK_READ_ONLY */
+#define MYA_DL_MAJOR 1
+#define MYA_DL_MINOR 0
+/* Consumer streams follow the DLPack convention for ROCm: -1 no synchronization, 0 the default stream, any other
+ * value a hipStream_t. */
+#define MYA_DL_STREAM_NONE (-1)
+
+typedef struct
+{
+    int32_t device_type;
+    int32_t device_id;
+} mya_dl_device;
+
+typedef struct
+{
+    uint8_t code;
+    uint8_t bits;
+    uint16_t lanes;
+} mya_dl_dtype;
+
+typedef struct
+{
+    void* data;
+    mya_dl_device device;
+    int32_t ndim;
+    mya_dl_dtype dtype;
+    int64_t* shape;
+    int64_t* strides; /* in elements */
+    uint64_t byte_offset;
+} mya_dl_tensor;
+
+typedef struct mya_dl_managed
+{
+    mya_dl_tensor dl_tensor;
+    void* manager_ctx;
+    void (*deleter)(struct mya_dl_managed* self);
+} mya_dl_managed;
+
+typedef struct
+{
+    uint32_t major;
+    uint32_t minor;
+} mya_dl_version;
+
+typedef struct mya_dl_managed_versioned
+{
+    mya_dl_version version;
+    void* manager_ctx;
+    void (*deleter)(struct mya_dl_managed_versioned* self);
+    uint64_t flags;
+    mya_dl_tensor dl_tensor;
+} mya_dl_managed_versioned;
+
+/* Device memory owned by the library, reference-counted (the reference's DLArray blocks, python/src/arrays.cpp): the
+ * creator holds one reference and every exported tensor another; the memory is freed when the last is dropped.
+ * Contents start undefined. Allocated on the current device. */
+typedef struct mya_buffer mya_buffer;
+int mya_buffer_create(uint64_t bytes, mya_buffer** out);
+void* mya_buffer_data(const mya_buffer* buffer);
+uint64_t mya_buffer_bytes(const mya_buffer* buffer);
+/* Drops the caller's reference. */
+void mya_buffer_release(mya_buffer* buffer);
+
+/* Exports a view of a buffer: element type (code, bits), ndim (0..8) extents `shape` and element strides `strides`
+ * (null: row-major), starting byte_offset bytes into the buffer (aligned to the element size; folded into the data
+ * pointer). Every element of the view must lie inside the buffer; strides must be non-negative. flags: 0 or
+ * MYA_DL_FLAG_READ_ONLY (versioned only). Work on producer_stream (a hipStream_t) is made to precede later work on
+ * consumer_stream (see MYA_DL_STREAM_NONE). *out receives a mya_dl_managed_versioned* (versioned != 0) or a
+ * mya_dl_managed*, which holds a reference to the buffer until its deleter is called. */
+int mya_buffer_export(mya_buffer* buffer, uint64_t byte_offset, uint8_t code, uint8_t bits, int32_t ndim,
+                      const int64_t* shape, const int64_t* strides, uint64_t flags, void* producer_stream,
+                      int64_t consumer_stream, int versioned, void** out);
+
+/* Exports the stored rows of a state set as a uint64 [size, words] tensor (waits for the set's last insert, like
+ * mya_hashset_size). The tensor holds a reference to the set: it stays valid after mya_hashset_free until its deleter
+ * runs; a later mya_hashset_clear makes its contents undefined. */
+int mya_hashset_export_rows(mya_hashset* set, uint64_t flags, int64_t consumer_stream, int versioned, void** out);
+
+/* For Python hosts: a PyCapsule destructor for capsules named "dltensor" or "dltensor_versioned" that hold a tensor
+ * exported above. It calls the tensor's deleter unless a consumer has taken the tensor (renamed the capsule), as the
+ * DLPack Python protocol specifies. It finds the CPython API in the running process and does nothing outside one. */
+void mya_dlpack_capsule_destructor(void* capsule);
 
 #ifdef __cplusplus
 }

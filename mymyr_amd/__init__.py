@@ -7,6 +7,7 @@ this package is the Python mirror of the reference's entry points for that path:
   search.brfs                                device BrFS (reference search.brfs / cuda.brfs)
   rl.DeviceEnvPool                           batched env step on the device (reference rl.CpuEnvPool / DeviceEnv)
   hip.hash_rows, hip.StateSet                hashing and the device dedup set
+  dlpack.DeviceBuffer / DeviceArray          library-owned device arrays exported over DLPack (reference DLArray)
   gen                                        seeded synthetic task generators
 """
 

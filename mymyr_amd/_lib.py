@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 2  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 3  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -121,6 +121,13 @@ class BrfsResult(Structure):
 
 
 def _load() -> ctypes.CDLL:
+    # torch-ROCm ships its own libamdhip64.so.7. Loaded first, the library would bind the system's copy and the
+    # process would hold two HIP runtimes (torch's then finds no device); with torch imported first, the library
+    # binds to the runtime already loaded under that soname, and both share one runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"mymyr_amd: {LIB_PATH} is not built (run `make -C mymyr_amd` or __graft_entry__.build())")
     lib = ctypes.CDLL(LIB_PATH)
@@ -149,6 +156,14 @@ def _load() -> ctypes.CDLL:
         "mya_hashset_rows": (c_int, [c_void_p, POINTER(c_void_p)]),
         "mya_hashset_clear": (c_int, [c_void_p, c_void_p]),
         "mya_dedup_rows": (c_int, [c_uint64, c_uint64, c_uint32, c_uint64, c_double, c_void_p, c_void_p]),
+        "mya_buffer_create": (c_int, [c_uint64, POINTER(c_void_p)]),
+        "mya_buffer_data": (c_void_p, [c_void_p]),
+        "mya_buffer_bytes": (c_uint64, [c_void_p]),
+        "mya_buffer_release": (None, [c_void_p]),
+        "mya_buffer_export": (c_int, [c_void_p, c_uint64, c_uint8, c_uint8, c_int32, c_void_p, c_void_p, c_uint64, c_void_p,
+                                      c_int64, c_int, POINTER(c_void_p)]),
+        "mya_hashset_export_rows": (c_int, [c_void_p, c_uint64, c_int64, c_int, POINTER(c_void_p)]),
+        "mya_dlpack_capsule_destructor": (None, [c_void_p]),
     }
     optional = {
         "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),

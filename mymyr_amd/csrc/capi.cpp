@@ -41,11 +41,6 @@ const DeviceTask& device_task(mya_task* t)
 
 using namespace mya;
 
-struct mya_hashset
-{
-    StateSet set;
-};
-
 extern "C" {
 
 const char* mya_last_error(void) { return g_error.c_str(); }
@@ -205,10 +200,8 @@ int mya_hashset_create(uint64_t max_states, uint32_t words, double max_load, uin
 
 void mya_hashset_free(mya_hashset* set)
 {
-    if (!set)
-        return;
-    state_set_destroy(set->set);
-    delete set;
+    if (set)
+        hashset_unref(set);
 }
 
 int mya_hashset_insert(mya_hashset* set, const uint64_t* rows, uint64_t n, int64_t* ids, uint8_t* is_new, uint64_t* new_count,

@@ -1,10 +1,12 @@
 #pragma once
 // Internals shared by the C-ABI translation units: the opaque handle types and the exception guard.
 
+#include "state_set.hpp"
 #include "task.hpp"
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <exception>
 #include <memory>
 #include <mutex>
@@ -55,4 +57,16 @@ struct mya_task
 namespace mya
 {
 const DeviceTask& device_task(mya_task* t);
+}
+
+/// A state set handle; mya_hashset_free drops the creator's reference and every exported rows tensor holds another.
+struct mya_hashset
+{
+    mya::StateSet set;
+    std::atomic<int> refs{1};
+};
+
+namespace mya
+{
+void hashset_unref(mya_hashset* h);
 }

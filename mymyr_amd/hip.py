@@ -2,7 +2,8 @@
 
   hash_rows(states)        the public state hash of each row (reference: mymyr.cuda hash_rows,
                            python/src/cuda_bindings.cpp:1289-1320)
-  StateSet                 the device dedup set (reference: include/mymyr/cuda/state_set.hpp)
+  StateSet                 the device dedup set (reference: include/mymyr/cuda/state_set.hpp); StateSet.rows()
+                           exports the stored rows over DLPack
 """
 
 from __future__ import annotations
@@ -81,6 +82,19 @@ class StateSet:
 
     def clear(self) -> None:
         check(lib.mya_hashset_clear(self._h, _stream()))
+
+    def rows(self, read_only: bool = False):
+        """The stored rows [len, words] (uint64) as a DLPack-exportable device array, without a copy:
+        ``torch.from_dlpack(s.rows())``. Waits for the last insert. The export holds the set's memory until the consumer
+        drops it; a later clear() makes its contents undefined."""
+        from .dlpack import DeviceArray
+        flags = 1 if read_only else 0
+        n = len(self)
+
+        def export(consumer: int, versioned: int, out: ctypes.c_void_p) -> int:
+            return lib.mya_hashset_export_rows(self._h, flags, consumer, versioned, ctypes.byref(out))
+
+        return DeviceArray(export, torch.cuda.current_device(), (n, self.words), "uint64", owner=self)
 
     def __del__(self):
         h = getattr(self, "_h", None)

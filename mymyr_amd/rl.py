@@ -85,8 +85,8 @@ class DeviceEnvPool:
              encode: int = 0) -> dict:
         """One step of every env: actions [num_envs] int64 indices into the canonical successor order (None: the random
         policy). encode > 0 also emits the observed states' true-atom slots ("atoms", int32 [num_envs, encode], -1
-        padded) and applicable-schema masks ("masks", uint8 [num_envs, num_schemas]). Returns the step's arrays
-        (views, overwritten by the next step)."""
+        padded) and applicable-schema masks ("masks", uint8 [num_envs, num_schemas]), both in library-owned device
+        buffers taken over DLPack. Returns the step's arrays (views, overwritten by the next step)."""
         if actions is not None:
             actions = actions.to(device=self.device, dtype=torch.int64).contiguous()
             if actions.shape != (self.num_envs,):
@@ -97,8 +97,7 @@ class DeviceEnvPool:
         atoms = masks = None
         if encode:
             if getattr(self, "_atoms", None) is None or self._atoms.shape[1] != encode:
-                self._atoms = torch.empty((self.num_envs, encode), dtype=torch.int32, device=self.device)
-                self._masks = torch.empty((self.num_envs, max(1, self.task.num_schemas)), dtype=torch.uint8, device=self.device)
+                self._atoms, self._masks = self._encoding_outputs(encode)
             atoms, masks = self._atoms, self._masks
         out = _lib.StepOutputs(self.reward.data_ptr(), self.terminated.data_ptr(), self.truncated.data_ptr(), self.count.data_ptr(),
                                _p(fs), self.schema.data_ptr() if labels else None, self.binding.data_ptr() if labels else None,
@@ -116,6 +115,20 @@ class DeviceEnvPool:
             r["atoms"] = atoms
             r["masks"] = masks
         return r
+
+    def _encoding_outputs(self, encode: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The atom-index and mask outputs live in library-owned device buffers that torch takes over DLPack without a
+        copy (the reference's pool arrays are DLPack-exported blocks, python/src/arrays.cpp:100-235)."""
+        from .dlpack import DeviceBuffer
+        S = max(1, self.task.num_schemas)
+        with torch.cuda.device(self.device):
+            ab = DeviceBuffer(self.num_envs * encode * 4)
+            mb = DeviceBuffer(self.num_envs * S)
+            atoms = torch.from_dlpack(ab.array("int32", (self.num_envs, encode)))
+            masks = torch.from_dlpack(mb.array("uint8", (self.num_envs, S)))
+        ab.release()
+        mb.release()
+        return atoms, masks
 
     def encode_atoms(self, states: torch.Tensor, max_atoms: int) -> torch.Tensor:
         """True-atom slots of each row, ascending, -1 padded (int32 [rows, max_atoms])."""

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     assert len(syms) >= 25
     missing = [s for s in syms if not hasattr(lib, s)]
     assert not missing, missing
-    assert lib.mya_abi_version() == 2
+    assert lib.mya_abi_version() == _lib.ABI_VERSION
 
 
 def test_symbols_are_plain_c():
