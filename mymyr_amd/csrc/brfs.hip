@@ -32,6 +32,7 @@ namespace
 constexpr int kTW = 4;        // waves per block of the per-parent kernels (64 parents per wave, one per lane)
 constexpr int kLB = 256;      // threads per block of the per-candidate kernels
 constexpr u64 kGeneral = 0x8000;  // fast-record flag: the action takes the general test
+constexpr int kCountPlanes = 7;    // bit planes of the per-lane successor counters (counts up to 64 between flushes)
 
 struct GroundDev
 {
@@ -156,7 +157,30 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_count(const u64* __restr
         gm &= B[goal.pos[i]];
     for (u32 i = 0; i < goal.nneg; ++i)
         gm &= ~B[goal.neg[i]];
-    u32 cnt = 0;
+    // Per lane (one action of each group), a bit-sliced counter over the 64 parents: plane k holds bit k of how many of
+    // the lane's actions so far apply to each parent. Adding a group's mask is a ripple carry through the planes, and
+    // only the final planes are transposed (bit k of parent t's count over the lanes = popcount of plane k's column t),
+    // instead of one transpose per group. 64 groups at most between flushes keep every counter below 2^7.
+    u64 plane[kCountPlanes] = {};
+    u32 cnt = 0, groups = 0;
+    auto add = [&](u64 m) {
+#pragma unroll
+        for (int k = 0; k < kCountPlanes; ++k)
+        {
+            const u64 c = plane[k] & m;
+            plane[k] ^= m;
+            m = c;
+        }
+    };
+    auto flush = [&]() {
+#pragma unroll
+        for (int k = 0; k < kCountPlanes; ++k)
+        {
+            cnt += static_cast<u32>(__popcll(transpose64(plane[k], lane))) << k;
+            plane[k] = 0;
+        }
+        groups = 0;
+    };
     u32 a0 = 0;
     for (; a0 + 4 * kWave <= g.num_padded; a0 += 4 * kWave)
     {
@@ -167,13 +191,19 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_count(const u64* __restr
             m[k] = action_mask<W>(B, g, g.fast[a0 + k * kWave + lane], a0 + k * kWave + lane, vm);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            cnt += static_cast<u32>(__popcll(transpose64(m[k], lane)));
+            add(m[k]);
+        groups += 4;
+        if (groups == 64)
+            flush();
     }
     for (; a0 < g.num_padded; a0 += kWave)
     {
         const u32 a = a0 + lane;
-        cnt += static_cast<u32>(__popcll(transpose64(action_mask<W>(B, g, g.fast[a], a, vm), lane)));
+        add(action_mask<W>(B, g, g.fast[a], a, vm));
+        if (++groups == 64)
+            flush();
     }
+    flush();
     const u32 t = base + lane;
     if (t < n)
     {
@@ -275,7 +305,13 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     Slice<G, kPairs<W>> me;
     src.load(j, q, me);
     const u64 h = group_hash<G, kPairs<W>>(me, q, gbase);
-    probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
+    const ProbeResult r = probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, flags, status);
+    if (q == 0)
+    {
+        cand_slot[j] = r.cand_slot;
+        if (r.lose)
+            flags[j] = 0;
+    }
 }
 
 // The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena

@@ -63,7 +63,13 @@ __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __
     Slice<G, K> me;
     src.load(j, q, me);
     const u64 h = group_hash<G, K>(me, q, gbase);
-    probe_insert<G, K>(s, src, j, me, h, q, gbase, cand_slot, flags, status);
+    const ProbeResult r = probe_insert<G, K>(s, src, j, me, h, q, gbase, flags, status);
+    if (q == 0)
+    {
+        cand_slot[j] = r.cand_slot;
+        if (r.lose)
+            flags[j] = 0;
+    }
 }
 
 // Compaction over the batch's winners (their count: size_next - size_now, read on the device).

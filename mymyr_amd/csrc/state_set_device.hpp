@@ -165,11 +165,19 @@ __device__ __forceinline__ u64 group_hash(const Slice<G, K>& s, u32 q, u32 gbase
 
 __device__ __forceinline__ u64 load_entry(const u64* e) { return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+struct ProbeResult
+{
+    u64 cand_slot;  // the cand_slot encoding of the candidate
+    bool lose;      // the candidate is not the winner of its content (its flag must be cleared)
+};
+
 /// Probes the table for the group's row `me` (candidate j, hash h) and inserts it as pending if no equal row is there.
-/// Src::load(c, q, out) gives lane q's words of candidate c. Writes cand_slot[j] and, for losers, flags = 0.
+/// Src::load(c, q, out) gives lane q's words of candidate c. Returns the candidate's own outputs, which the caller
+/// stores once the wave has reconverged (one coalesced store per wave instead of one per divergent path); the only
+/// store made here is the flag of another candidate that this one displaces from a pending entry.
 template<int G, int K, class Src>
-__device__ void probe_insert(const StateSetView& s, const Src& src, u64 j, const Slice<G, K>& me, u64 h, u32 q, u32 gbase,
-                             u64* __restrict__ cand_slot, u32* __restrict__ flags, u32* __restrict__ status)
+__device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const Src& src, u64 j, const Slice<G, K>& me, u64 h,
+                                                    u32 q, u32 gbase, u32* __restrict__ flags, u32* __restrict__ status)
 {
     const u64 tag = h >> 32;
     const u64 mine = (tag << 32) | kPending | j;
@@ -185,11 +193,7 @@ __device__ void probe_insert(const StateSetView& s, const Src& src, u64 j, const
                 old = atomicCAS(reinterpret_cast<unsigned long long*>(s.table + slot), 0ull, static_cast<unsigned long long>(mine));
             old = group_bcast<G>(old, gbase, 0);
             if (old == 0)
-            {
-                if (q == 0)
-                    cand_slot[j] = (tag << 32) | slot;
-                return;
-            }
+                return {(tag << 32) | slot, false};
             e = old;
         }
         if ((e >> 32) == tag)
@@ -203,45 +207,27 @@ __device__ void probe_insert(const StateSetView& s, const Src& src, u64 j, const
                 load_row<G, K>(s.arena + static_cast<u64>(code - 1) * s.words, s.words, q, o);
             if (group_equal<G, K>(me, o, gbase))
             {
-                if (pending && (code & ~kPending) < j)
-                {
-                    // a smaller candidate holds the entry already: this one loses without an atomic (a pending entry
-                    // only ever decreases, so a stale read shows a value at least as large as the current one)
-                    if (q == 0)
-                    {
-                        flags[j] = 0;
-                        cand_slot[j] = (tag << 32) | slot;
-                    }
-                }
-                else if (pending)
-                {
-                    u64 old = 0;
-                    if (q == 0)
-                        old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
-                    old = group_bcast<G>(old, gbase, 0);
-                    if (q == 0)
-                    {
-                        const u64 other = static_cast<u32>(old) & ~kPending;
-                        flags[other > j ? other : j] = 0;
-                        cand_slot[j] = (tag << 32) | slot;
-                    }
-                }
-                else if (q == 0)
-                {
-                    flags[j] = 0;
-                    cand_slot[j] = (static_cast<u64>(code - 1) << 32) | kNoSlot;
-                }
-                return;
+                if (!pending)
+                    return {(static_cast<u64>(code - 1) << 32) | kNoSlot, true};
+                // a smaller candidate holding the entry already makes this one lose without an atomic (a pending
+                // entry only ever decreases, so a stale read shows a value at least as large as the current one)
+                if ((code & ~kPending) < j)
+                    return {(tag << 32) | slot, true};
+                u64 old = 0;
+                if (q == 0)
+                    old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
+                old = group_bcast<G>(old, gbase, 0);
+                const u64 other = static_cast<u32>(old) & ~kPending;
+                if (other > j && q == 0)
+                    flags[other] = 0;
+                return {(tag << 32) | slot, other < j};
             }
         }
         slot = slot + 1 == s.capacity ? 0 : slot + 1;
     }
     if (q == 0)
-    {
         atomicOr(status, kStatusTableFull);
-        flags[j] = 0;
-        cand_slot[j] = kProbeFailed;
-    }
+    return {kProbeFailed, true};
 }
 
 /// Winner w of the batch (candidate j = list[w], id = id0 + w): below `limit` its row into the arena and its entry settled
