@@ -65,22 +65,50 @@ struct Slices
     static constexpr u32 kWords = W * 64 + 16;
 };
 
-/// 64x64 bit transpose across the wave: bit t of the result in lane s = bit s of x in lane t.
+/// Lane l ^ J's value, for J < 32: quad permutations (DPP) for 1 and 2, a bitmask swizzle within 32 lanes above.
+template<int J>
+__device__ __forceinline__ u32 xor_lane(u32 v)
+{
+    if constexpr (J == 1)
+        return static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    else if constexpr (J == 2)
+        return static_cast<u32>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    else
+        return static_cast<u32>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x1F | (J << 10)));  // and 31, xor J
+}
+
+/// One step of a 32x32 bit transpose over each half wave: lanes l and l ^ J swap the J-bit blocks that sit in the
+/// wrong lane (the high J bits of each 2J-bit block of the lane without bit J, the low J bits of the other).
+template<int J>
+__device__ __forceinline__ u32 transpose_step(u32 x, u32 lane)
+{
+    constexpr u32 m = J == 16 ? 0x0000FFFFu : J == 8 ? 0x00FF00FFu : J == 4 ? 0x0F0F0F0Fu : J == 2 ? 0x33333333u : 0x55555555u;
+    const u32 y = xor_lane<J>(x);
+    const bool low = (lane & J) == 0;
+    const u32 keep = low ? x : (y >> J), take = low ? (y << J) : x;
+    return (keep & m) | (take & ~m);
+}
+
+/// 64x64 bit transpose across the wave: bit t of the result in lane s = bit s of x in lane t. The 32-bit halves
+/// swap across the half waves first (the high word of lanes 0-31 with the low word of lanes 32-63, one lane-swap
+/// instruction), then each word is a 32x32 transpose within its half wave; every step is branch-free.
 __device__ __forceinline__ u64 transpose64(u64 x, u32 lane)
 {
-#pragma unroll
-    for (int j = 32; j >= 1; j >>= 1)
-    {
-        const u64 m = j == 32 ? 0x00000000FFFFFFFFull
-                      : j == 16 ? 0x0000FFFF0000FFFFull
-                      : j == 8  ? 0x00FF00FF00FF00FFull
-                      : j == 4  ? 0x0F0F0F0F0F0F0F0Full
-                      : j == 2  ? 0x3333333333333333ull
-                                : 0x5555555555555555ull;
-        const u64 y = __shfl_xor(x, j, kWave);
-        x = (lane & j) ? ((x & ~m) | ((y & ~m) >> j)) : ((x & m) | ((y & m) << j));
-    }
-    return x;
+    u32 lo = static_cast<u32>(x), hi = static_cast<u32>(x >> 32);
+    const auto sw = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);  // lo of lanes 32-63 <-> hi of lanes 0-31
+    lo = sw[0];
+    hi = sw[1];
+    lo = transpose_step<16>(lo, lane);
+    hi = transpose_step<16>(hi, lane);
+    lo = transpose_step<8>(lo, lane);
+    hi = transpose_step<8>(hi, lane);
+    lo = transpose_step<4>(lo, lane);
+    hi = transpose_step<4>(hi, lane);
+    lo = transpose_step<2>(lo, lane);
+    hi = transpose_step<2>(hi, lane);
+    lo = transpose_step<1>(lo, lane);
+    hi = transpose_step<1>(hi, lane);
+    return static_cast<u64>(lo) | (static_cast<u64>(hi) << 32);
 }
 
 /// Loads the rows of parents [first + base, + 64) (lane t: parent base + t, rows past n zero) bit-sliced into B.
