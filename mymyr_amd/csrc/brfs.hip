@@ -32,6 +32,7 @@ namespace
 constexpr int kTW = 4;        // waves per block of the per-parent kernels (64 parents per wave, one per lane)
 constexpr int kLB = 256;      // threads per block of the per-candidate kernels
 constexpr u64 kGeneral = 0x8000;  // fast-record flag: the action takes the general test
+constexpr u64 kStrideBlocks = 4096;  // grid of the grid-stride kernels (16 blocks of 256 threads per CU)
 constexpr int kCountPlanes = 7;    // bit planes of the per-lane successor counters (counts up to 64 between flushes)
 
 struct GroundDev
@@ -323,7 +324,7 @@ constexpr int kPairs = W >= 4 ? 2 : 1;  // word pairs per lane
 // takes it as pending).
 template<int W>
 __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W> src, u64 m, u64* __restrict__ cand_slot,
-                                                      u32* __restrict__ flags, u32* __restrict__ status)
+                                                      u8* __restrict__ flags, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
     const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
@@ -350,12 +351,12 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
                                                        const u64* __restrict__ size_next, u64 limit, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
-    const u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
     const u32 q = lane_id() % G;
     const u64 id0 = *size_now;
-    if (w >= m || w >= *size_next - id0)
-        return;
-    compact_winner<G, kPairs<W>>(s, src, w, q, list, cand_slot, id0, limit, nullptr, status);
+    const u64 winners = min(m, *size_next - id0);
+    // a grid sized for the whole chunk would mostly start waves that find no winner: a bounded grid strides instead
+    for (u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G; w < winners; w += static_cast<u64>(gridDim.x) * (kLB / G))
+        compact_winner<G, kPairs<W>>(s, src, w, q, list, cand_slot, id0, limit, nullptr, status);
 }
 
 // The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
@@ -829,7 +830,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 // the winners' count is on the device (size next - size now); ids from max_states on are not written
                 // (the store filled: the confirmation finds the cut)
                 tm.begin(kKCompact);
-                hipLaunchKernelGGL(k_ground_compact<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.list,
+                hipLaunchKernelGGL(k_ground_compact<W>, dim3(std::min<u64>(blocks_for(m * G, kLB), kStrideBlocks)), dim3(kLB), 0, stream, set.v, src, m, set.list,
                                    set.cand_slot, state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states,
                                    bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
                 launch_check("ground compact");

@@ -114,7 +114,10 @@ __global__ __launch_bounds__(kScanBlock) void k_offsets(const u32* __restrict__ 
         off += v[k];
     }
 }
-// One block scans the block sums in place (exclusive, from 0) and writes *total = *total_base + the grand total.
+// One block scans the block sums in place (exclusive, from 0) and writes *total = *total_base + the grand total. Each
+// thread takes kSumsPerThread consecutive sums per pass.
+constexpr int kSumsPerThread = 8;
+
 __global__ __launch_bounds__(1024) void k_scan_sums_rel(u64* __restrict__ sums, u64 nb, u64* total, const u64* total_base)
 {
     __shared__ u64 lds[1024 / kWave + 1];
@@ -122,11 +125,18 @@ __global__ __launch_bounds__(1024) void k_scan_sums_rel(u64* __restrict__ sums, 
     if (threadIdx.x == 0)
         carry = 0;
     __syncthreads();
-    for (u64 b0 = 0; b0 < nb; b0 += 1024)
+    for (u64 b0 = 0; b0 < nb; b0 += 1024 * kSumsPerThread)
     {
-        const u64 i = b0 + threadIdx.x;
-        const u64 v = i < nb ? sums[i] : 0;
-        const u64 inc = wave_inclusive64(v);
+        const u64 i0 = b0 + static_cast<u64>(threadIdx.x) * kSumsPerThread;
+        u64 v[kSumsPerThread];
+        u64 s = 0;
+#pragma unroll
+        for (int k = 0; k < kSumsPerThread; ++k)
+        {
+            v[k] = i0 + k < nb ? sums[i0 + k] : 0;
+            s += v[k];
+        }
+        const u64 inc = wave_inclusive64(s);
         const u32 wave = threadIdx.x / kWave;
         if (lane_id() == kWave - 1)
             lds[wave] = inc;
@@ -143,8 +153,14 @@ __global__ __launch_bounds__(1024) void k_scan_sums_rel(u64* __restrict__ sums, 
             lds[1024 / kWave] = run;
         }
         __syncthreads();
-        if (i < nb)
-            sums[i] = carry + lds[wave] + inc - v;
+        u64 run = carry + lds[wave] + inc - s;
+#pragma unroll
+        for (int k = 0; k < kSumsPerThread; ++k)
+        {
+            if (i0 + k < nb)
+                sums[i0 + k] = run;
+            run += v[k];
+        }
         __syncthreads();
         if (threadIdx.x == 0)
             carry += lds[1024 / kWave];
@@ -154,60 +170,87 @@ __global__ __launch_bounds__(1024) void k_scan_sums_rel(u64* __restrict__ sums, 
         *total = (total_base ? *total_base : 0) + carry;
 }
 
-// The winners' indices in order (list[rank] = j for flags[j] != 0), is_new[j] = flags[j] (optional), and the losers'
-// flags reset to 1.
-__global__ __launch_bounds__(kScanBlock) void k_winner_list(u32* __restrict__ flags, u64 n, const u64* __restrict__ sums,
-                                                           u32* __restrict__ list, u8* __restrict__ is_new)
+// Winner flags are bytes (0 or 1), 16 per thread (one 16-byte access), 4096 per block.
+constexpr int kFlagsPerThread = 16;
+constexpr u64 kFlagsPerBlock = static_cast<u64>(kScanBlock) * kFlagsPerThread;
+
+/// The thread's 16 flags (zeros past n) and their sum; `full` when all 16 lie below n (one 16-byte load).
+__device__ __forceinline__ u32 load_flags(const u8* __restrict__ flags, u64 first, u64 n, uint4& v, bool& full)
 {
-    __shared__ u64 lds[kScanBlock / kWave + 1];
-    const u64 base = static_cast<u64>(blockIdx.x) * kScanBlock * kPerThread;
-    const u64 first = base + static_cast<u64>(threadIdx.x) * kPerThread;
-    u32 v[kPerThread];
-    u64 s = 0;
-#pragma unroll
-    for (int k = 0; k < kPerThread; ++k)
+    full = first + kFlagsPerThread <= n;
+    if (full)
+        v = *reinterpret_cast<const uint4*>(flags + first);
+    else
     {
-        v[k] = first + k < n ? flags[first + k] : 0;
-        s += v[k];
+        u32 w[4] = {0, 0, 0, 0};
+        for (int k = 0; k < kFlagsPerThread; ++k)
+            if (first + k < n)
+                w[k / 4] |= static_cast<u32>(flags[first + k]) << (8 * (k % 4));
+        v = uint4{w[0], w[1], w[2], w[3]};
     }
-    const u64 inc = wave_inclusive64(s);
-    const u32 wave = threadIdx.x / kWave;
-    if (lane_id() == kWave - 1)
-        lds[wave] = inc;
+    // bytes are 0 or 1: x * 0x01010101 sums the four bytes into the top byte
+    return ((v.x * 0x01010101u) >> 24) + ((v.y * 0x01010101u) >> 24) + ((v.z * 0x01010101u) >> 24) + ((v.w * 0x01010101u) >> 24);
+}
+
+__global__ __launch_bounds__(kScanBlock) void k_flag_sums(const u8* __restrict__ flags, u64 n, u64* __restrict__ sums)
+{
+    __shared__ u32 lds[kScanBlock / kWave];
+    uint4 v;
+    bool full;
+    u32 s = load_flags(flags, static_cast<u64>(blockIdx.x) * kFlagsPerBlock + threadIdx.x * kFlagsPerThread, n, v, full);
+    s = wave_sum(s);
+    if (lane_id() == 0)
+        lds[threadIdx.x / kWave] = s;
     __syncthreads();
     if (threadIdx.x == 0)
     {
-        u64 run = 0;
+        u32 t = 0;
         for (int w = 0; w < kScanBlock / kWave; ++w)
-        {
-            const u64 t = lds[w];
-            lds[w] = run;
-            run += t;
-        }
+            t += lds[w];
+        sums[blockIdx.x] = t;
     }
-    __syncthreads();
-    u64 off = sums[blockIdx.x] + lds[wave] + inc - s;
+}
+
+// The winners' indices in order (list[rank] = j for flags[j] != 0), is_new[j] = flags[j] (optional), and the losers'
+// flags reset to 1.
+__global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ flags, u64 n, const u64* __restrict__ sums,
+                                                           u32* __restrict__ list, u8* __restrict__ is_new)
+{
+    __shared__ u32 lds[kScanBlock / kWave + 1];
+    const u64 first = static_cast<u64>(blockIdx.x) * kFlagsPerBlock + threadIdx.x * kFlagsPerThread;
+    uint4 v;
+    bool full;
+    const u32 s = load_flags(flags, first, n, v, full);
+    u32 total;
+    const u32 excl = block_exclusive<kScanBlock>(s, lds, &total);
+    u64 off = sums[blockIdx.x] + excl;
+    const u32 w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int k = 0; k < kPerThread; ++k)
+    for (int k = 0; k < kFlagsPerThread; ++k)
+        if ((w[k / 4] >> (8 * (k % 4))) & 1)
+            list[off++] = static_cast<u32>(first + k);
+    if (full)
     {
-        const u64 j = first + k;
-        if (j >= n)
-            break;
-        if (v[k])
-            list[off++] = static_cast<u32>(j);
-        else
-            flags[j] = 1;
+        if (s != kFlagsPerThread)
+            *reinterpret_cast<uint4*>(flags + first) = uint4{0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
         if (is_new)
-            is_new[j] = static_cast<u8>(v[k]);
+            *reinterpret_cast<uint4*>(is_new + first) = v;
     }
+    else
+        for (int k = 0; k < kFlagsPerThread && first + k < n; ++k)
+        {
+            flags[first + k] = 1;
+            if (is_new)
+                is_new[first + k] = static_cast<u8>((w[k / 4] >> (8 * (k % 4))) & 1);
+        }
 }
 }  // namespace
 
-void launch_winner_list(u32* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u8* is_new, hipStream_t stream)
+void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u8* is_new, hipStream_t stream)
 {
-    const u64 nb = (n + kScanBlock * kPerThread - 1) / (kScanBlock * kPerThread);
+    const u64 nb = (n + kFlagsPerBlock - 1) / kFlagsPerBlock;
     if (nb > 0)
-        hipLaunchKernelGGL(k_block_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch);
+        hipLaunchKernelGGL(k_flag_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch);
     hipLaunchKernelGGL(k_scan_sums_rel, dim3(1), dim3(1024), 0, stream, scratch, nb, total, total_base);
     if (nb > 0)
         hipLaunchKernelGGL(k_winner_list, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, list, is_new);

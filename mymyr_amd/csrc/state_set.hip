@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kBlock) void k_hash_rows(const u64* __restrict__ ro
 
 template<int G, int K>
 __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __restrict__ rows, u64 n, u64* __restrict__ cand_slot,
-                                                  u32* __restrict__ flags, u32* __restrict__ status)
+                                                  u8* __restrict__ flags, u32* __restrict__ status)
 {
     u64 j;
     u32 q, gbase;
@@ -223,13 +223,13 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
     s.v.table = dev_alloc<u64>(cap, "state set table");
     s.v.arena = dev_alloc<u64>(max_states * words, "state set arena");
     s.cand_slot = dev_alloc<u64>(s.batch_cap, "state set batch slots");
-    s.flags = dev_alloc<u32>(s.batch_cap, "state set batch flags");
+    s.flags = dev_alloc<u8>((s.batch_cap + 15) / 16 * 16, "state set batch flags");
     s.list = dev_alloc<u32>(s.batch_cap, "state set batch winners");
     s.scan_scratch = dev_alloc<u64>(scan_scratch_words(s.batch_cap), "state set scan scratch");
     s.d_size = dev_alloc<u64>(2, "state set size");
     s.d_status = dev_alloc<u32>(1, "state set status");
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&s.h_pinned), sizeof(u64) * 4, hipHostMallocDefault), "pinned words");
-    launch_fill_u32(s.flags, s.batch_cap, 1, stream);
+    launch_fill_u32(reinterpret_cast<u32*>(s.flags), (s.batch_cap + 15) / 16 * 4, 0x01010101u, stream);  // flag bytes 1
     state_set_clear(s, stream);
 }
 

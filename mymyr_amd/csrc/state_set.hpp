@@ -27,7 +27,7 @@ struct StateSet
     u64 size = 0;       // host copy of the size (exact after a synchronizing call)
     u64 batch_cap = 0;
     u64* cand_slot = nullptr;  // [batch_cap] probe result per candidate (state_set_device.hpp encodings)
-    u32* flags = nullptr;      // [batch_cap] winner flags, 1 at rest
+    u8* flags = nullptr;       // [batch_cap] winner flag bytes, 1 at rest
     u32* list = nullptr;       // [batch_cap] the winners' candidate indices in order (winner w gets id size + w)
     u64* scan_scratch = nullptr;
     u64* d_size = nullptr;     // [2] the size, alternating per batch

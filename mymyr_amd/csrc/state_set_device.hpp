@@ -177,7 +177,7 @@ struct ProbeResult
 /// store made here is the flag of another candidate that this one displaces from a pending entry.
 template<int G, int K, class Src>
 __device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const Src& src, u64 j, const Slice<G, K>& me, u64 h,
-                                                    u32 q, u32 gbase, u32* __restrict__ flags, u32* __restrict__ status)
+                                                    u32 q, u32 gbase, u8* __restrict__ flags, u32* __restrict__ status)
 {
     const u64 tag = h >> 32;
     const u64 mine = (tag << 32) | kPending | j;
