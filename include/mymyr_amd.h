@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 3
+#define MYA_ABI_VERSION 4
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -148,6 +148,12 @@ typedef struct mya_env_batch
     uint64_t* draws;
     uint8_t* at_goal;
     uint64_t first_env;
+    /* The count cache (the reference device env's EnvBatch::counts, include/mymyr/rl/env.hpp:106-110), optional:
+     * [rows, num_schemas + 2] uint32, each row's per-schema successor counts of its current state, then a 64-bit
+     * fingerprint of that state (low word first). reset, refresh and step keep it current, and a step takes the
+     * counts of a row from it instead of counting the row's successors when the fingerprint matches the row's state
+     * (a state written directly is counted again; refresh brings at_goal up to date for it). Null: every step counts. */
+    uint32_t* counts;
 } mya_env_batch;
 
 /* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
@@ -189,6 +195,10 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
                  void* stream);
 /* Reads and clears the sticky device status (synchronizes the env's status copy); -1 with a message if a step failed. */
 int mya_env_check(mya_env* env);
+/* Recomputes at_goal and the count cache (when the batch has one) of every row from its state, after the caller wrote
+ * states directly (DeviceEnv::refresh, include/mymyr/cuda/env.hpp:170-174); count (device, optional) receives the
+ * successor counts. Async on the stream. */
+int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, void* stream);
 
 /* The true-atom slots of rows, ascending, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101);
  * states [rows, words], out [rows, max_atoms] int32: device. Async on the stream; more atoms than max_atoms set the

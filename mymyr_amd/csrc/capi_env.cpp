@@ -19,6 +19,7 @@ struct mya_env
     u32 init_count = 0;
     u32 init_goal = 0;
     u8* init_masks = nullptr;  // device [num_schemas]
+    u32* init_cache = nullptr; // device [num_schemas + 2]: the initial state's count-cache row
     u32* d_status = nullptr;
     u32* h_status = nullptr;
 };
@@ -72,7 +73,8 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
         u8* gl = dev_alloc<u8>(1, "initial goal");
         hip_check(hipMemcpy(row, task->compiled->initial.data(), W * sizeof(u64), hipMemcpyHostToDevice), "initial row");
         e->init_masks = dev_alloc<u8>(std::max<u32>(1, e->T.num_schemas), "initial masks");
-        launch_env_count(e->T, row, 1, W, cnt, gl, e->init_masks, nullptr);
+        e->init_cache = dev_alloc<u32>(cache_width(e->T), "initial count cache");
+        launch_env_count(e->T, row, 1, W, cnt, gl, e->init_masks, e->init_cache, nullptr);
         i32 hc = 0;
         u8 hg = 0;
         hip_check(hipMemcpy(&hc, cnt, sizeof(i32), hipMemcpyDeviceToHost), "initial count");
@@ -92,6 +94,7 @@ void mya_env_free(mya_env* env)
         return;
     dev_free(env->d_status);
     dev_free(env->init_masks);
+    dev_free(env->init_cache);
     if (env->h_status)
         (void)hipHostFree(env->h_status);
     delete env;
@@ -115,8 +118,8 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         if (!env)
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
-        launch_env_reset(env->T, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, env->init_count,
-                         env->init_goal, static_cast<hipStream_t>(stream));
+        launch_env_reset(env->T, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, batch->counts,
+                         env->init_cache, env->init_count, env->init_goal, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -165,12 +168,25 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.max_atoms = out->max_atoms;
         a.masks = out->masks;
         a.init_masks = env->init_masks;
+        a.counts = batch->counts;
+        a.init_counts = env->init_cache;
         if (out->atoms && out->max_atoms == 0)
             throw std::invalid_argument("mymyr_amd: env: atoms output needs max_atoms > 0");
         a.init_count = env->init_count;
         a.init_goal = env->init_goal;
         a.status = env->d_status;
         launch_env_step(a, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        check_batch(env, batch);
+        launch_env_count(env->T, batch->states, batch->rows, batch->words, count, batch->at_goal, nullptr, batch->counts,
+                         static_cast<hipStream_t>(stream));
     });
 }
 
@@ -214,7 +230,7 @@ int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32
             throw std::invalid_argument("mymyr_amd: schema_masks: null argument");
         if (words < env->T.W)
             throw std::invalid_argument("mymyr_amd: schema_masks: rows narrower than the task");
-        launch_env_count(env->T, states, rows, words, nullptr, nullptr, masks, static_cast<hipStream_t>(stream));
+        launch_env_count(env->T, states, rows, words, nullptr, nullptr, masks, nullptr, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -699,6 +699,42 @@ __device__ __forceinline__ u32 count_all(const TaskDev& T, const auto& H, const 
     return total;
 }
 
+/// A 64-bit fingerprint of the state (the count cache's check that a row still holds the state its counts are of).
+__device__ __forceinline__ u64 state_fingerprint(const lds<u64>* row, u32 W, u32 lane)
+{
+    u64 acc = 0;
+    for (u32 w = lane; w < W; w += kWave)
+        acc += mix64(row[w] ^ (static_cast<u64>(w + 1) * 0x9E3779B97F4A7C15ull));
+    return wave_sum64(acc);
+}
+
+/// The per-schema counts of a count-cache row into LDS; returns their total.
+__device__ __forceinline__ u32 load_counts(const TaskDev& T, const Lds& L, const u32* crow, u32 lane)
+{
+    u32 part = 0;
+    for (u32 s = lane; s < T.num_schemas; s += kWave)
+    {
+        const u32 c = crow[s];
+        L.counts[s] = c;
+        part += c;
+    }
+    wave_sync();
+    return wave_sum(part);
+}
+
+/// A count-cache row from the per-schema counts in LDS and the fingerprint of the LDS state.
+__device__ __forceinline__ void store_counts(const TaskDev& T, const Lds& L, u32* crow, u32 lane)
+{
+    const u64 fp = state_fingerprint(L.row, T.W, lane);
+    for (u32 s = lane; s < T.num_schemas; s += kWave)
+        crow[s] = L.counts[s];
+    if (lane == 0)
+    {
+        crow[T.num_schemas] = static_cast<u32>(fp);
+        crow[T.num_schemas + 1] = static_cast<u32>(fp >> 32);
+    }
+}
+
 /// The schema holding successor `a` (< total) and the rank within it.
 __device__ __forceinline__ void select_schema(const TaskDev& T, const Lds& L, u32 a, u32* schema, u32* rank)
 {
@@ -1082,6 +1118,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
         load_row_lds(T, L, grow, lane);
         build_view(T, H, L, lane);
         const bool already_goal = A.at_goal[i] != 0;
+        // the count cache row: its counts stand for the row's state when its fingerprint matches (reset, refresh and
+        // step write it; a state written directly since is counted again)
+        u32* crow = A.counts ? A.counts + i * cache_width(T) : nullptr;
+        bool cached = false;
+        if (crow)
+        {
+            const u64 fp = state_fingerprint(L.row, T.W, lane);
+            cached = (static_cast<u64>(crow[T.num_schemas]) | (static_cast<u64>(crow[T.num_schemas + 1]) << 32)) == fp;
+        }
         enum
         {
             kOk = 0,
@@ -1094,7 +1139,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
         bool g = already_goal;
         for (u32 phase = 0; phase < 2; ++phase)
         {
-            const u32 cc = count_all<kLevels>(T, H, L, lane);
+            const u32 cc = (phase == 0 && cached) ? load_counts(T, L, crow, lane) : count_all<kLevels>(T, H, L, lane);
             if (phase == 1)
             {
                 c2 = cc;
@@ -1213,6 +1258,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
                     A.count[i] = static_cast<i32>(c2);
             }
         }
+        // the count cache of the state the row now holds: the initial state's after a reset, else the counts in LDS
+        // (of s' after a move, of s otherwise) unless they came from the cache
+        if (crow)
+        {
+            if (reset)
+                for (u32 k = lane; k < cache_width(T); k += kWave)
+                    crow[k] = A.init_counts[k];
+            else if (st == kOk || !cached)
+                store_counts(T, L, crow, lane);
+        }
         // 6. the observation's encoding: true-atom slots and applicable-schema masks (LDS holds the per-schema counts
         // of the state the row holds unless the row was reset)
         if (A.atoms || A.masks)
@@ -1244,7 +1299,7 @@ __global__ __launch_bounds__(kWave) void k_encode(const u64* states, u64 rows, u
 
 template<bool kStaged, bool kLevels>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(TaskDev T, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
-                                                                 u8* masks)
+                                                                 u8* masks, u32* cache)
 {
     extern __shared__ u64 smem[];
     Tab<kStaged> H;
@@ -1271,6 +1326,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(TaskDev T, cons
                 if (lane == 0)
                     masks[i * T.num_schemas + s] = cs > 0 ? 1 : 0;
             }
+        if (cache)
+            store_counts(T, L, cache + i * cache_width(T), lane);
         wave_sync();
     }
 }
@@ -1295,6 +1352,18 @@ __global__ void k_env_reset(TaskDev T, u64* states, u64 rows, u32 words, const u
             if (count)
                 count[i] = static_cast<i32>(init_count);
         }
+    }
+}
+
+__global__ void k_env_reset_cache(u64 rows, u32 width, const u8* mask, u32* cache, const u32* init_cache)
+{
+    const u64 total = rows * width;
+    for (u64 k = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; k < total; k += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        const u64 i = k / width;
+        if (mask && !mask[i])
+            continue;
+        cache[k] = init_cache[k - i * width];
     }
 }
 
@@ -1385,7 +1454,8 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
     launch_check("env step");
 }
 
-void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, hipStream_t stream)
+void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
+                      hipStream_t stream)
 {
     if (rows == 0)
         return;
@@ -1393,7 +1463,7 @@ void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, 
     const unsigned nw = waves_per_block(T, &lds);
     const auto fn = variant(T, k_env_count<true, false>, k_env_count<true, true>, k_env_count<false, false>, k_env_count<false, true>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks);
+    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks, cache);
     launch_check("env count");
 }
 
@@ -1406,7 +1476,7 @@ void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out
 }
 
 void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
-                      u32 init_count, u32 init_goal, hipStream_t stream)
+                      u32* cache, const u32* init_cache, u32 init_count, u32 init_goal, hipStream_t stream)
 {
     if (rows == 0)
         return;
@@ -1414,6 +1484,13 @@ void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const 
     hipLaunchKernelGGL(k_env_reset, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(total, 256), 65536))), dim3(256), 0, stream, T,
                        states, rows, words, mask, steps, at_goal, count, init_count, init_goal);
     launch_check("env reset");
+    if (cache)
+    {
+        const u64 cells = rows * cache_width(T);
+        hipLaunchKernelGGL(k_env_reset_cache, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(cells, 256), 65536))), dim3(256), 0,
+                           stream, rows, cache_width(T), mask, cache, init_cache);
+        launch_check("env reset cache");
+    }
 }
 
 void launch_successors(const TaskDev& T, const u64* states, u64 rows, u32 words, u32 cap, i32* count, i32* schema, i32* binding,

@@ -46,6 +46,8 @@ struct EnvArgs
     i32* atoms;       // [rows, max_atoms]: ascending true-atom slots of the observed state, -1 padded (optional)
     u32 max_atoms;
     u8* masks;        // [rows, num_schemas]: schemas with an applicable binding in the observed state (optional)
+    u32* counts;      // [rows, num_schemas + 2]: the count cache (per-schema counts, then the state's fingerprint), optional
+    const u32* init_counts;  // [num_schemas + 2]: the initial state's cache row (device)
     const u8* init_masks;  // [num_schemas]: the initial state's masks (device)
     u32 init_count;
     u32 init_goal;
@@ -54,16 +56,21 @@ struct EnvArgs
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream);
 
-/// count[i] (successors), goal[i] and masks [rows, num_schemas] of rows (each may be null).
-void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, hipStream_t stream);
+/// count[i] (successors), goal[i], masks [rows, num_schemas] and the count cache [rows, num_schemas + 2] of rows (each
+/// may be null).
+void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
+                      hipStream_t stream);
 
 /// Ascending true-atom slots of each row, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101).
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream);
 
 /// Resets the rows with mask[i] != 0 (all if mask is null) to the initial state: steps 0, at_goal = init_goal,
-/// count = init_count; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).
+/// count = init_count, the count cache row = init_cache; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).
 void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
-                      u32 init_count, u32 init_goal, hipStream_t stream);
+                      u32* cache, const u32* init_cache, u32 init_count, u32 init_goal, hipStream_t stream);
+
+/// Words of a count-cache row: the per-schema counts, then the 64-bit state fingerprint.
+__host__ __device__ inline u32 cache_width(const TaskDev& T) { return T.num_schemas + 2; }
 
 /// Per-row successor listing in canonical order (schema [rows, cap], binding [rows, cap, L], successor rows
 /// [rows, cap, words]) and counts [rows]; entries past cap are counted but not written.

@@ -33,7 +33,8 @@ class DeviceEnvPool:
     def __init__(self, task: Task, num_envs: int, *, seed: int = 0, max_steps: int | None = None, step_reward: float = 0.0,
                  goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
-                 witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda"):
+                 witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda",
+                 count_cache: bool = True):
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
@@ -65,8 +66,11 @@ class DeviceEnvPool:
         self.schema = torch.zeros(N, dtype=torch.int32, device=dev)
         self.binding = torch.zeros((N, L), dtype=torch.int32, device=dev)
         self.final_states: torch.Tensor | None = None
+        # the count cache (the reference device env's EnvBatch::counts): per-schema successor counts of each row's
+        # state plus its fingerprint, so a step counts only the reached states; zeros match no state
+        self.counts_cache = (torch.zeros((N, task.num_schemas + 2), dtype=torch.int32, device=dev) if count_cache else None)
         self._batch = _lib.EnvBatch(self.states.data_ptr(), N, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
-                                    self.at_goal.data_ptr(), first_env)
+                                    self.at_goal.data_ptr(), first_env, _p(self.counts_cache))
 
     def initial_count(self) -> tuple[int, bool]:
         c = ctypes.c_uint32()
@@ -143,6 +147,12 @@ class DeviceEnvPool:
         out = torch.empty((s.shape[0], max(1, self.task.num_schemas)), dtype=torch.uint8, device=s.device)
         check(lib.mya_schema_masks(self._h, s.data_ptr(), s.shape[0], s.shape[1], out.data_ptr(), _stream()))
         return out
+
+    def refresh(self) -> torch.Tensor:
+        """Recomputes at_goal and the count cache from the current states after they were written directly
+        (DeviceEnv::refresh); returns the successor counts."""
+        check(lib.mya_env_refresh(self._h, ctypes.byref(self._batch), self.count.data_ptr(), _stream()))
+        return self.count
 
     def check(self) -> None:
         """Raises if a step set the device's sticky error status."""

@@ -17,7 +17,7 @@ def host(t):
     return t.cpu().numpy()
 
 
-def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0):
+def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0, **pool_kw):
     from mymyr_amd import rl, workloads
     from mymyr_amd.task import Task
 
@@ -25,7 +25,7 @@ def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0):
     atoms = "dense" if g["workload"] == "strips" else "auto"
     t = Task.from_text_file(golden.task_path(g["workload"]), atoms)
     n = num_envs or g["rows"]
-    pool = rl.DeviceEnvPool(t, n, **g["env"])
+    pool = rl.DeviceEnvPool(t, n, **g["env"], **pool_kw)
     pool.reset()
     rows = g["rows"]
     for k in range(g["steps"]):
@@ -135,3 +135,48 @@ def test_env_argument_errors(golden):
     pool = rl.DeviceEnvPool(t, 4)
     with pytest.raises(ValueError, match="shape"):
         pool.step(actions=torch.zeros(3, dtype=torch.int64))
+
+
+def test_without_count_cache(golden):
+    """The step without the count cache (every step counts its state's successors) gives the same trajectories."""
+    run_env(golden, "env_gridworld_truncated.json", count_cache=False)
+    run_env(golden, "env_transport.json", count_cache=False)
+
+
+def test_count_cache_with_states_written_directly(golden):
+    """Rows whose states are written directly, without refresh, are counted again (their cache fingerprints no longer
+    match), and refresh() rebuilds at_goal and the cache: the cached pool follows the uncached one step for step."""
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+
+    g = golden.load("env_gridworld_truncated.json")
+    t = Task.from_text_file(golden.task_path(g["workload"]), "auto")
+    a = rl.DeviceEnvPool(t, 512, **g["env"])
+    b = rl.DeviceEnvPool(t, 512, **g["env"], count_cache=False)
+    a.reset()
+    b.reset()
+    keys = ("states", "reward", "terminated", "truncated", "count", "schema", "binding", "goal", "steps", "at_goal")
+
+    def step_both(k):
+        oa, ob = a.step(), b.step()
+        for key in keys:
+            assert torch.equal(oa[key], ob[key]), f"step {k}: {key} differs"
+
+    for k in range(6):
+        step_both(k)
+    # rows take other rows' states (with their goal flags), written directly: the cache rows no longer match them
+    for p in (a, b):
+        p.states.copy_(p.states.roll(7, dims=0))
+        p.at_goal.copy_(p.at_goal.roll(7, dims=0))
+    for k in range(6, 12):
+        step_both(k)
+    # a write followed by refresh(): at_goal and the cache are recomputed from the states
+    init = torch.from_numpy(t.initial_state().view(np.int64)).cuda()
+    for p in (a, b):
+        p.states[::3] = init
+        p.refresh()
+    assert torch.equal(a.at_goal, b.at_goal) and torch.equal(a.count, b.count)
+    for k in range(12, 20):
+        step_both(k)
+    a.check()
+    b.check()
