@@ -347,7 +347,7 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
 // (rows recomputed from their records) and the table.
 template<int W>
 __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 m, const u32* __restrict__ list,
-                                                       const u64* __restrict__ cand_slot, const u64* __restrict__ size_now,
+                                                       const u64* __restrict__ size_now,
                                                        const u64* __restrict__ size_next, u64 limit, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
     const u64 winners = min(m, *size_next - id0);
     // a grid sized for the whole chunk would mostly start waves that find no winner: a bounded grid strides instead
     for (u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G; w < winners; w += static_cast<u64>(gridDim.x) * (kLB / G))
-        compact_winner<G, kPairs<W>>(s, src, w, q, list, cand_slot, id0, limit, nullptr, status);
+        compact_winner<G, kPairs<W>>(s, src, w, q, list, id0, limit, nullptr, status);
 }
 
 // The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
@@ -579,7 +579,10 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     // capacity: the arena holds every stored state
     const bool bounded = o.max_states != ~u64{0};
     const u64 cap_states = bounded ? std::max<u64>(1, o.max_states) : (o.memory_states ? o.memory_states : (u64{1} << 26));
-    const u64 chunk = std::max<u64>(o.chunk ? o.chunk : (u64{1} << 25), ga.size() + 1);
+    // a chunk holds at most kMaxBatch candidates (the state set's candidate-coded entries) and one parent's successors
+    if (ga.size() + 1 > kMaxBatch)
+        throw std::invalid_argument("mymyr_amd: brfs: more than 2^25 - 1 ground actions");
+    const u64 chunk = std::min<u64>(std::max<u64>(o.chunk ? o.chunk : kMaxBatch, ga.size() + 1), kMaxBatch);
     StateSet set;
     state_set_create(set, cap_states, W, 0.5, chunk, stream, chunk);
     struct SetGuard
@@ -820,6 +823,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 launch_check("ground emit");
                 tm.end(kKEmit, np * (R + 8) + m * 8);
                 tm.begin(kKInsert);
+                state_set_begin_batch(set, stream);
                 hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
                                    set.flags, set.d_status);
                 launch_check("ground insert");
@@ -831,7 +835,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 // (the store filled: the confirmation finds the cut)
                 tm.begin(kKCompact);
                 hipLaunchKernelGGL(k_ground_compact<W>, dim3(std::min<u64>(blocks_for(m * G, kLB), kStrideBlocks)), dim3(kLB), 0, stream, set.v, src, m, set.list,
-                                   set.cand_slot, state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states,
+                                   state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states,
                                    bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
                 launch_check("ground compact");
                 tm.end(kKCompact, 0);

@@ -211,10 +211,11 @@ __global__ __launch_bounds__(kScanBlock) void k_flag_sums(const u8* __restrict__
     }
 }
 
-// The winners' indices in order (list[rank] = j for flags[j] != 0), is_new[j] = flags[j] (optional), and the losers'
-// flags reset to 1.
+// The winners' indices in order (list[rank] = j for flags[j] != 0), their ids base + rank into id_of[j] (optional),
+// is_new[j] = flags[j] (optional), and the losers' flags reset to 1.
 __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ flags, u64 n, const u64* __restrict__ sums,
-                                                           u32* __restrict__ list, u8* __restrict__ is_new)
+                                                           const u64* __restrict__ base, u32* __restrict__ list,
+                                                           u32* __restrict__ id_of, u8* __restrict__ is_new)
 {
     __shared__ u32 lds[kScanBlock / kWave + 1];
     const u64 first = static_cast<u64>(blockIdx.x) * kFlagsPerBlock + threadIdx.x * kFlagsPerThread;
@@ -224,11 +225,16 @@ __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ fla
     u32 total;
     const u32 excl = block_exclusive<kScanBlock>(s, lds, &total);
     u64 off = sums[blockIdx.x] + excl;
+    const u64 id0 = base ? *base : 0;
     const u32 w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int k = 0; k < kFlagsPerThread; ++k)
         if ((w[k / 4] >> (8 * (k % 4))) & 1)
+        {
+            if (id_of)
+                id_of[first + k] = static_cast<u32>(id0 + off);
             list[off++] = static_cast<u32>(first + k);
+        }
     if (full)
     {
         if (s != kFlagsPerThread)
@@ -246,14 +252,16 @@ __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ fla
 }
 }  // namespace
 
-void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u8* is_new, hipStream_t stream)
+void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u32* id_of, u8* is_new,
+                        hipStream_t stream)
 {
     const u64 nb = (n + kFlagsPerBlock - 1) / kFlagsPerBlock;
     if (nb > 0)
         hipLaunchKernelGGL(k_flag_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch);
     hipLaunchKernelGGL(k_scan_sums_rel, dim3(1), dim3(1024), 0, stream, scratch, nb, total, total_base);
     if (nb > 0)
-        hipLaunchKernelGGL(k_winner_list, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, list, is_new);
+        hipLaunchKernelGGL(k_winner_list, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, total_base, list,
+                           id_of, is_new);
 }
 
 void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream, const u64* base)

@@ -87,7 +87,8 @@ void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch,
 inline u64 scan_scratch_words(u64 n) { return (n + 1023) / 1024 + 2; }
 
 /// The indices j of the nonzero flags in order into list[0, winners) (flag bytes are 0 or 1; zero flags are reset to 1),
-/// is_new[j] = flags[j] (optional), and *total = *total_base + winners. Three launches; scratch as for
-/// launch_exclusive_scan. flags must be 16-byte aligned.
-void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u8* is_new, hipStream_t stream);
+/// id_of[j] = *total_base + rank for the winners (optional), is_new[j] = flags[j] (optional), and *total = *total_base +
+/// winners. Three launches; scratch as for launch_exclusive_scan. flags must be 16-byte aligned.
+void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u32* id_of, u8* is_new,
+                        hipStream_t stream);
 }  // namespace mya

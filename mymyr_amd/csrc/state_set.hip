@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __
 // Compaction over the batch's winners (their count: size_next - size_now, read on the device).
 template<int G, int K>
 __global__ __launch_bounds__(kBlock) void k_compact(StateSetView s, const u64* __restrict__ rows, const u32* __restrict__ list,
-                                                   const u64* __restrict__ cand_slot, const u64* __restrict__ size_now,
+                                                   const u64* __restrict__ size_now,
                                                    const u64* __restrict__ size_next, u64 limit, u8* __restrict__ is_new,
                                                    u32* __restrict__ status)
 {
@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kBlock) void k_compact(StateSetView s, const u64* _
     const u64 id0 = *size_now;
     if (w >= *size_next - id0)
         return;
-    compact_winner<G, K>(s, BufferRows{rows, s.words}, w, q, list, cand_slot, id0, limit, is_new, status);
+    compact_winner<G, K>(s, BufferRows{rows, s.words}, w, q, list, id0, limit, is_new, status);
 }
 
 __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u64* __restrict__ cand_slot, u64 n, i64* __restrict__ ids)
@@ -101,10 +101,33 @@ __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u6
         id = static_cast<i64>(cs >> 32);
     else
     {
-        const u32 code = static_cast<u32>(s.table[static_cast<u32>(cs)]);
-        id = (code & kPending) ? -1 : static_cast<i64>(code) - 1;
+        const u64 c = committed_id(s, static_cast<u32>(s.table[static_cast<u32>(cs)]));
+        id = c < s.max_rows ? static_cast<i64>(c) : -1;
     }
     ids[j] = id;
+}
+
+// Settles every candidate-coded entry to id + 1 (two entries per thread per step).
+__global__ __launch_bounds__(kBlock) void k_settle(u64* __restrict__ table, u64 capacity, const u32* __restrict__ id_of, u64 stride)
+{
+    const u64 pairs = capacity / 2;
+    for (u64 i = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x; i < pairs; i += static_cast<u64>(gridDim.x) * kBlock)
+    {
+        const ulonglong2 v = reinterpret_cast<const ulonglong2*>(table)[i];
+        u64 e[2] = {v.x, v.y};
+        bool dirty = false;
+        for (int k = 0; k < 2; ++k)
+        {
+            const u32 code = static_cast<u32>(e[k]);
+            if (code & kPending)
+            {
+                e[k] = (e[k] & 0xFFFFFFFF00000000ull) | (id_of[code_epoch(code) * stride + (code & kJMask)] + 1u);
+                dirty = true;
+            }
+        }
+        if (dirty)
+            reinterpret_cast<ulonglong2*>(table)[i] = ulonglong2{e[0], e[1]};
+    }
 }
 
 __global__ __launch_bounds__(kBlock) void k_fill_u32(u32* __restrict__ p, u64 n, u32 v)
@@ -213,13 +236,21 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
         throw std::invalid_argument("mymyr_amd: state set holds at most 2^31 - 2 states");
     if (batch_cap >= (u64{1} << 31))
         throw std::invalid_argument("mymyr_amd: state set batches hold fewer than 2^31 rows");
-    const u64 cap = std::max<u64>(64, static_cast<u64>(std::ceil(static_cast<double>(max_states + pending) / max_load)));
+    // an even capacity of at least 64 slots (the epoch settling streams the table two entries at a time)
+    u64 cap = std::max<u64>(64, static_cast<u64>(std::ceil(static_cast<double>(max_states + pending) / max_load)));
+    cap += cap & 1;
     if (cap >= (u64{1} << 32) - 1)
         throw std::invalid_argument("mymyr_amd: state set table capacity above 2^32 - 2 slots");
     s.v.words = words;
     s.v.capacity = cap;
     s.max_states = max_states;
-    s.batch_cap = std::max<u64>(1, batch_cap);
+    s.batch_cap = std::clamp<u64>(batch_cap, 1, kMaxBatch);
+    // epochs in rotation: as many as fit 2 GiB of id maps (the 2^25-candidate batches of the BrFS: 16), at least 4
+    s.epochs = static_cast<u32>(std::clamp<u64>((u64{1} << 31) / (s.batch_cap * sizeof(u32)), 4, kMaxEpochs));
+    s.id_of = dev_alloc<u32>(s.epochs * s.batch_cap, "state set epoch ids");
+    s.v.id_of = s.id_of;
+    s.v.id_stride = s.batch_cap;
+    s.v.max_rows = max_states;
     s.v.table = dev_alloc<u64>(cap, "state set table");
     s.v.arena = dev_alloc<u64>(max_states * words, "state set arena");
     s.cand_slot = dev_alloc<u64>(s.batch_cap, "state set batch slots");
@@ -245,6 +276,7 @@ void state_set_destroy(StateSet& s)
     dev_free(s.scan_scratch);
     dev_free(s.d_size);
     dev_free(s.d_status);
+    dev_free(s.id_of);
     if (s.h_pinned)
         (void)hipHostFree(s.h_pinned);
     s = StateSet{};
@@ -252,17 +284,34 @@ void state_set_destroy(StateSet& s)
 
 void state_set_clear(StateSet& s, hipStream_t stream)
 {
-    hip_check(hipMemsetAsync(s.v.table, 0, s.v.capacity * sizeof(u64), stream), "clear state set");
+    // a fill kernel rather than a memset node, so that a captured clear replays correctly
+    launch_fill_u32(reinterpret_cast<u32*>(s.v.table), s.v.capacity * 2, 0u, stream);
     hipLaunchKernelGGL(k_set_words, dim3(1), dim3(1), 0, stream, s.d_size, u64{0}, u64{0}, s.d_status);
     launch_check("clear state set");
     s.cur = 0;
     s.size = 0;
+    s.batches = 0;
+    s.v.epoch = 0;
     s.last = stream;
+}
+
+void state_set_begin_batch(StateSet& s, hipStream_t stream)
+{
+    if (s.batches == s.epochs)
+    {
+        // every epoch is taken: one streaming pass settles all candidate-coded entries, and the rotation restarts
+        hipLaunchKernelGGL(k_settle, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(s.v.capacity / 2, kBlock), 8192))), dim3(kBlock),
+                           0, stream, s.v.table, s.v.capacity, s.id_of, s.batch_cap);
+        launch_check("state set settle");
+        s.batches = 0;
+    }
+    s.v.epoch = static_cast<u32>(s.batches++);
 }
 
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
 {
-    launch_winner_list(s.flags, n, s.scan_scratch, state_set_size_next(s), state_set_size_now(s), s.list, is_new, stream);
+    launch_winner_list(s.flags, n, s.scan_scratch, state_set_size_next(s), state_set_size_now(s), s.list,
+                       s.id_of + static_cast<u64>(s.v.epoch) * s.batch_cap, is_new, stream);
     launch_check("state set rank");
 }
 
@@ -288,11 +337,12 @@ void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new,
         {
             const u64 m = std::min(n - done, s.batch_cap);
             const u64* r = rows + done * W;
+            state_set_begin_batch(s, stream);
             hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, s.cand_slot, s.flags,
                                s.d_status);
             launch_check("state set probe");
             state_set_rank(s, m, stream, is_new ? is_new + done : nullptr);
-            hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, s.list, s.cand_slot,
+            hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, s.list,
                                state_set_size_now(s), state_set_size_next(s), s.max_states, is_new ? is_new + done : nullptr, s.d_status);
             launch_check("state set compact");
             if (ids)

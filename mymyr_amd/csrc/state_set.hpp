@@ -1,6 +1,7 @@
 #pragma once
 // Device-resident open-addressing state set: rows of W u64 words in an arena (ids in insertion order), one u64 table
-// entry per slot = (tag32 << 32) | code, code = id + 1 (settled) or kPending | candidate (pending within a batch).
+// entry per slot = (tag32 << 32) | code, code = id + 1 (settled) or kPending | epoch | candidate (a candidate of a
+// batch: pending while that batch is inserted, then standing for the id the batch's epoch maps it to).
 //
 // A batch insert keeps the reference's id rule (include/mymyr/cuda/state_set.hpp:2-18, the CPU stores'
 // first-discovery ids: src/mymyr/search/brfs.cpp:1657-1780): among equal candidates of one batch the smallest
@@ -9,8 +10,8 @@
 // the capacity, tag = its high 32 bits, linear probing.
 //
 // A batch is three steps on one stream: probe (group of lanes per row: hash, probe, CAS or atomicMin, loser flags),
-// the winner list (a scan of the flags: winner w gets id = the set's size + w), and compaction over the winners
-// (rows into the arena, entries settled). The set's size lives on the device in two words used alternately (the scan of a batch
+// the winner list (a scan of the flags: winner w gets id = the set's size + w, recorded per candidate in the batch's
+// epoch of id_of), and compaction over the winners (rows into the arena; the entries keep their epoch codes). The set's size lives on the device in two words used alternately (the scan of a batch
 // writes next = current + winners), so batches need no host synchronization; the host copy is refreshed by the
 // calls that synchronize.
 
@@ -35,6 +36,9 @@ struct StateSet
     u64* h_pinned = nullptr;   // [4] size before, size after, status of the last insert
     int cur = 0;               // d_size[cur] is the current size
     hipStream_t last = nullptr;
+    u32* id_of = nullptr;      // [epochs, batch_cap] winner ids per epoch (v.id_of)
+    u32 epochs = 0;            // epochs in rotation (at most kMaxEpochs)
+    u64 batches = 0;           // epochs taken since the last clear or settling pass
 };
 
 /// Allocates a set for up to max_states rows of `words` words at the given maximum load: capacity =
@@ -45,6 +49,10 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
 void state_set_destroy(StateSet& s);
 /// Clears the set (size 0) without freeing.
 void state_set_clear(StateSet& s, hipStream_t stream);
+
+/// Starts a batch: takes the next free epoch into s.v.epoch (when all are taken, one pass over the table settles every
+/// candidate-coded entry to id + 1 first). Drivers with their own probe kernels call it before each batch's probe.
+void state_set_begin_batch(StateSet& s, hipStream_t stream);
 
 /// Inserts rows [n, W] (device), in batches of at most batch_cap rows, asynchronously on the stream. Optional outputs:
 /// ids [n] (i64 id of each row's state; -1 for a row past the capacity), is_new [n]. With new_count (host) the call
@@ -61,8 +69,8 @@ inline u64* state_set_size_now(StateSet& s) { return s.d_size + s.cur; }
 inline u64* state_set_size_next(StateSet& s) { return s.d_size + (s.cur ^ 1); }
 inline void state_set_flip(StateSet& s) { s.cur ^= 1; }
 
-/// The winners of a batch of n candidates in order into s.list (losers' flags reset), is_new[j] (optional) the flags,
-/// and next size = size + winners.
+/// The winners of a batch of n candidates in order into s.list (losers' flags reset), their ids into the batch's
+/// epoch of id_of, is_new[j] (optional) the flags, and next size = size + winners.
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new = nullptr);
 
 /// hash_state of every row (a group of lanes per row).

@@ -10,6 +10,12 @@
 // (include/mymyr/cuda/state_set.hpp:2-18): among equal candidates the smallest candidate index wins (64-bit atomicMin
 // on the pending entry), new ids follow candidate order.
 //
+// Entries are never rewritten after the probe: a batch's pending entries keep the candidate code of their winner, and
+// the batch's epoch (one of up to 64, 6 bits of the code) maps candidate indices to ids through id_of, written by the
+// winner list. When every epoch is taken, one streaming pass settles all entries to id + 1. This trades the random
+// 8-byte rewrite of every new state's entry (a read-modify-write of a memory line) for a 4-byte id_of read on the
+// probes that compare against a recent state.
+//
 // Winner flags need no second pass over the table: every candidate starts at flag 1 (the winner list of the previous
 // batch resets the zeros), and only zeros are written during the probe: a candidate equal to a stored state, a candidate
 // that finds a smaller equal one already pending (no atomic: a pending entry only decreases), and the larger index of
@@ -24,9 +30,18 @@
 
 namespace mya
 {
-constexpr u32 kPending = 0x80000000u;
+constexpr u32 kPending = 0x80000000u;  // a candidate-coded entry: epoch and candidate index instead of id + 1
+constexpr u32 kJBits = 25;             // candidate index bits of a candidate-coded entry (batches of at most 2^25)
+constexpr u32 kJMask = (1u << kJBits) - 1;
+constexpr u32 kEpochMask = (1u << (31 - kJBits)) - 1;
+constexpr u32 kMaxEpochs = kEpochMask + 1;
+constexpr u64 kMaxBatch = u64{1} << kJBits;
 constexpr u32 kNoSlot = 0xFFFFFFFFu;
 constexpr u64 kProbeFailed = ~u64{0};
+
+/// The entry code of candidate j of the batch of the given epoch.
+__host__ __device__ inline u32 cand_code(u32 epoch, u64 j) { return kPending | (epoch << kJBits) | static_cast<u32>(j); }
+__host__ __device__ inline u32 code_epoch(u32 code) { return (code >> kJBits) & kEpochMask; }
 
 /// Slot of a state hash: fastrange of its low 32 bits over the capacity (the tag is the high 32 bits).
 __host__ __device__ inline u64 slot_of_hash(u64 h, u64 cap) { return ((h & 0xFFFFFFFFull) * cap) >> 32; }
@@ -35,9 +50,19 @@ struct StateSetView
 {
     u64* table;
     u64 capacity;
-    u64* arena;  // [max_states, words]
+    u64* arena;         // [max_rows, words]
     u32 words;
+    u32 epoch;          // the epoch of the batch being inserted
+    const u32* id_of;   // [epochs, id_stride]: the id of each batch winner j of the epoch (written by the winner list)
+    u64 id_stride;
+    u64 max_rows;       // rows of the arena: ids at or past it were never stored
 };
+
+/// The id a committed entry code stands for: id + 1 for settled codes, the epoch's winner id for candidate codes.
+__device__ __forceinline__ u64 committed_id(const StateSetView& s, u32 code)
+{
+    return (code & kPending) ? s.id_of[code_epoch(code) * s.id_stride + (code & kJMask)] : static_cast<u64>(code) - 1;
+}
 
 /// cand_slot encodings written by the probe: (tag << 32) | slot for a candidate that holds or held a pending entry;
 /// (id << 32) | kNoSlot for a candidate equal to the stored state `id`; kProbeFailed when the table was full.
@@ -180,7 +205,7 @@ __device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const
                                                     u32 q, u32 gbase, u8* __restrict__ flags, u32* __restrict__ status)
 {
     const u64 tag = h >> 32;
-    const u64 mine = (tag << 32) | kPending | j;
+    const u64 mine = (tag << 32) | cand_code(s.epoch, j);
     u64 slot = slot_of_hash(h, s.capacity);
     for (u64 probes = 0; probes < s.capacity; ++probes)
     {
@@ -198,26 +223,30 @@ __device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const
         }
         if ((e >> 32) == tag)
         {
+            // a pending entry holds a candidate of this batch (its row comes from the row source); any other entry a
+            // stored state (its row is in the arena; an id past the arena was cut by a capacity overflow and matches
+            // nothing)
             const u32 code = static_cast<u32>(e);
+            const bool pending = (code & kPending) && code_epoch(code) == s.epoch;
+            const u64 id = pending ? 0 : committed_id(s, code);
             Slice<G, K> o;
-            const bool pending = (code & kPending) != 0;
             if (pending)
-                src.load(code & ~kPending, q, o);
-            else
-                load_row<G, K>(s.arena + static_cast<u64>(code - 1) * s.words, s.words, q, o);
-            if (group_equal<G, K>(me, o, gbase))
+                src.load(code & kJMask, q, o);
+            else if (id < s.max_rows)
+                load_row<G, K>(s.arena + id * s.words, s.words, q, o);
+            if ((pending || id < s.max_rows) && group_equal<G, K>(me, o, gbase))
             {
                 if (!pending)
-                    return {(static_cast<u64>(code - 1) << 32) | kNoSlot, true};
+                    return {(id << 32) | kNoSlot, true};
                 // a smaller candidate holding the entry already makes this one lose without an atomic (a pending
                 // entry only ever decreases, so a stale read shows a value at least as large as the current one)
-                if ((code & ~kPending) < j)
+                if ((code & kJMask) < j)
                     return {(tag << 32) | slot, true};
                 u64 old = 0;
                 if (q == 0)
                     old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
                 old = group_bcast<G>(old, gbase, 0);
-                const u64 other = static_cast<u32>(old) & ~kPending;
+                const u64 other = static_cast<u32>(old) & kJMask;
                 if (other > j && q == 0)
                     flags[other] = 0;
                 return {(tag << 32) | slot, other < j};
@@ -230,12 +259,12 @@ __device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const
     return {kProbeFailed, true};
 }
 
-/// Winner w of the batch (candidate j = list[w], id = id0 + w): below `limit` its row into the arena and its entry settled
-/// to id + 1; at or past it, kStatusCapacity (and is_new[j] = 0).
+/// Winner w of the batch (candidate j = list[w], id = id0 + w): below `limit` its row into the arena; at or past it,
+/// kStatusCapacity (and is_new[j] = 0). The winner's table entry keeps its candidate code: the batch's epoch maps it to
+/// the id (id_of), so no entry is rewritten.
 template<int G, int K, class Src>
 __device__ __forceinline__ void compact_winner(const StateSetView& s, const Src& src, u64 w, u32 q, const u32* __restrict__ list,
-                                               const u64* __restrict__ cand_slot, u64 id0, u64 limit, u8* __restrict__ is_new,
-                                               u32* __restrict__ status)
+                                               u64 id0, u64 limit, u8* __restrict__ is_new, u32* __restrict__ status)
 {
     const u64 j = list[w];
     const u64 id = id0 + w;
@@ -252,10 +281,5 @@ __device__ __forceinline__ void compact_winner(const StateSetView& s, const Src&
     Slice<G, K> r;
     src.load(j, q, r);
     store_row<G, K>(s.arena + id * s.words, s.words, q, r);
-    if (q == 0)
-    {
-        const u64 cs = cand_slot[j];
-        s.table[static_cast<u32>(cs)] = (cs & 0xFFFFFFFF00000000ull) | static_cast<u32>(id + 1);
-    }
 }
 }  // namespace mya

@@ -69,6 +69,28 @@ def test_state_set_ids_and_unique_count():
     assert n2 == 0 and np.array_equal(ids2.cpu().numpy(), exp_ids)
 
 
+def test_state_set_ids_across_epoch_settling():
+    """Batches of 128 rows use up the state set's 64 epochs several times: the passes that settle candidate-coded
+    entries to ids keep every id and the unique count equal to the oracle's, and rows inserted again later find them."""
+    from mymyr_amd import gen, hip
+    from oracle import port
+
+    rows = gen.dedup_rows(0, 30000, 8, seed=6)
+    s = hip.StateSet(30000, 8, 0.5, batch=128)  # 235 batches: 3 settling passes
+    n, ids, _ = s.insert(dev(rows))
+    exp_n, exp_ids = port.dedup_unique(rows)
+    assert n == exp_n == len(s)
+    assert np.array_equal(ids.cpu().numpy(), exp_ids)
+    # rows from the start and the end of the stream again, in one more batch sequence
+    again = np.concatenate([rows[:5000], rows[-5000:]])
+    n2, ids2, is_new2 = s.insert(dev(again))
+    assert n2 == 0 and not is_new2.any()
+    assert np.array_equal(ids2.cpu().numpy(), np.concatenate([exp_ids[:5000], exp_ids[-5000:]]))
+    # the stored rows are the first occurrences in id order
+    stored = torch.from_dlpack(s.rows()).cpu().numpy().view(np.uint64)
+    assert np.array_equal(stored, rows[np.unique(exp_ids, return_index=True)[1]])
+
+
 def test_state_set_dedup_closed_form_large():
     """2^22 rows of 1024 bits in 2^20-row batches at load 0.5: the unique count is the generator's fresh-row count."""
     from mymyr_amd import gen, hip
