@@ -317,6 +317,9 @@ void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
 
 void state_set_sync(StateSet& s)
 {
+    // the size and status words are read here only (an asynchronous insert copies nothing back)
+    hip_check(hipMemcpyAsync(s.h_pinned + 1, state_set_size_now(s), sizeof(u64), hipMemcpyDeviceToHost, s.last), "read size");
+    hip_check(hipMemcpyAsync(s.h_pinned + 2, s.d_status, sizeof(u32), hipMemcpyDeviceToHost, s.last), "read status");
     hip_check(hipStreamSynchronize(s.last), "state set");
     const u32 status = static_cast<u32>(s.h_pinned[2]);
     const u64 after = s.h_pinned[1];
@@ -331,7 +334,8 @@ void state_set_sync(StateSet& s)
 void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new, u64* new_count, hipStream_t stream)
 {
     const u32 W = s.v.words;
-    hip_check(hipMemcpyAsync(s.h_pinned, state_set_size_now(s), sizeof(u64), hipMemcpyDeviceToHost, stream), "read size");
+    if (new_count)
+        hip_check(hipMemcpyAsync(s.h_pinned, state_set_size_now(s), sizeof(u64), hipMemcpyDeviceToHost, stream), "read size");
     with_shape(W, [&]<int G, int K>() {
         for (u64 done = 0; done < n;)
         {
@@ -354,8 +358,6 @@ void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new,
             done += m;
         }
     });
-    hip_check(hipMemcpyAsync(s.h_pinned + 1, state_set_size_now(s), sizeof(u64), hipMemcpyDeviceToHost, stream), "read size");
-    hip_check(hipMemcpyAsync(s.h_pinned + 2, s.d_status, sizeof(u32), hipMemcpyDeviceToHost, stream), "read status");
     s.last = stream;
     if (new_count)
     {
