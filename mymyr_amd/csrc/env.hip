@@ -6,7 +6,9 @@
 #include "runtime.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 namespace mya
 {
@@ -1435,10 +1437,20 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
 
 unsigned grid_for(u64 rows, unsigned nw) { return static_cast<unsigned>(std::min<u64>((rows + nw - 1) / nw, u64{1} << 20)); }
 
+/// Raises a kernel's dynamic LDS limit once per (kernel, size): later launches make no runtime call besides the launch,
+/// so a step recorded into a HIP graph after a first eager call holds kernel nodes only.
 void set_lds(const void* fn, size_t bytes)
 {
-    if (bytes > 64 * 1024)
-        hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)), "LDS size");
+    if (bytes <= 64 * 1024)
+        return;
+    static std::mutex mu;
+    static std::unordered_map<const void*, size_t> done;
+    std::lock_guard lock(mu);
+    size_t& have = done[fn];
+    if (bytes <= have)
+        return;
+    hip_check(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)), "LDS size");
+    have = bytes;
 }
 }  // namespace
 
