@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 4
+#define MYA_ABI_VERSION 5
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -214,6 +214,46 @@ int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32
  * u64. Device pointers (each optional but count). Entries past cap are counted, not written. Synchronous. */
 int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, int32_t cap, int32_t* count,
                    int32_t* schema, int32_t* binding, uint64_t* succ, void* stream);
+
+/* rl::expand over one task (include/mymyr/rl/expand.hpp:1-130, ExpandOptions and Expansion): the flat CSR
+ * expansion of rows [rows, words] (device). Device arrays of the expansion (each optional, null: not written):
+ * succ [capacity, words] successor rows, parent / schema / index [capacity] int32, binding [capacity, label_width]
+ * int32 (-1 past the schema's arity), goal / noop [capacity] uint8, succ_hash [capacity] uint64 (hash_state of the
+ * successor), offsets [rows + 1] int32 (successors of row i are [offsets[i], offsets[i+1])). Rows past the capacity are
+ * counted, not written: generated (all successors) > capacity is the overflow. With drop_noops the no-op successors of
+ * a row are removed unless all of its successors are no-ops (then all are kept), index gives each kept row's position
+ * in its row's full order, and an overflow reports the counts before dropping (offsets[rows] == total == generated).
+ * Successors in canonical order; witness pruning off. Synchronous: generated, total and words_needed are set on return. */
+typedef struct mya_expand_options
+{
+    int32_t canonical_order; /* must be 1 */
+    int32_t witness_pruning; /* must be 0 */
+    int32_t validate;        /* reject rows with atoms past the task's slots */
+    int32_t drop_noops;
+} mya_expand_options;
+
+typedef struct mya_expansion
+{
+    uint64_t capacity;
+    uint32_t words;       /* words of the succ rows */
+    uint32_t label_width; /* columns of binding (at least the largest schema arity) */
+    uint64_t* succ;
+    int32_t* parent;
+    int32_t* schema;
+    int32_t* binding;
+    uint8_t* goal;        /* needs succ */
+    int32_t* offsets;
+    uint64_t* succ_hash;
+    uint8_t* noop;
+    int32_t* index;       /* required with drop_noops when capacity > 0 */
+    uint64_t generated;   /* out: successors before dropping */
+    uint64_t total;       /* out: kept successors */
+    uint32_t words_needed; /* out: widest trimmed successor that did not fit `words` (0 if all fit) */
+    uint32_t reserved;
+} mya_expansion;
+
+int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, const mya_expand_options* options,
+               mya_expansion* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------- BrFS */
 

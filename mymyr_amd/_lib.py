@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 4  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 5  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -121,6 +121,36 @@ class BrfsResult(Structure):
     ]
 
 
+class ExpandOptions(Structure):
+    _fields_ = [
+        ("canonical_order", c_int32),
+        ("witness_pruning", c_int32),
+        ("validate", c_int32),
+        ("drop_noops", c_int32),
+    ]
+
+
+class Expansion(Structure):
+    _fields_ = [
+        ("capacity", c_uint64),
+        ("words", c_uint32),
+        ("label_width", c_uint32),
+        ("succ", c_void_p),
+        ("parent", c_void_p),
+        ("schema", c_void_p),
+        ("binding", c_void_p),
+        ("goal", c_void_p),
+        ("offsets", c_void_p),
+        ("succ_hash", c_void_p),
+        ("noop", c_void_p),
+        ("index", c_void_p),
+        ("generated", c_uint64),
+        ("total", c_uint64),
+        ("words_needed", c_uint32),
+        ("reserved", c_uint32),
+    ]
+
+
 def _load() -> ctypes.CDLL:
     # torch-ROCm ships its own libamdhip64.so.7. Loaded first, the library would bind the system's copy and the
     # process would hold two HIP runtimes (torch's then finds no device); with torch imported first, the library
@@ -177,6 +207,7 @@ def _load() -> ctypes.CDLL:
         "mya_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
         "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p]),
         "mya_schema_masks": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),
+        "mya_expand": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion), c_void_p]),
         "mya_successors": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     }
     for name, (res, args) in list(sigs.items()) + list(optional.items()):

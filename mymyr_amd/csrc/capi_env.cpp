@@ -6,8 +6,11 @@
 #include "capi_internal.hpp"
 #include "env.hpp"
 #include "runtime.hpp"
+#include "scan.hpp"
+#include "state_set.hpp"
 
 #include <cstring>
+#include <vector>
 
 using namespace mya;
 
@@ -256,6 +259,122 @@ int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32
         dev_free(st);
         if (hs)
             throw std::runtime_error("mymyr_amd: successors: device status " + std::to_string(hs));
+    });
+}
+
+int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, const mya_expand_options* options,
+               mya_expansion* out, void* stream_)
+{
+    return guarded([&] {
+        if (!task || !options || !out || (rows && !states))
+            throw std::invalid_argument("mymyr_amd: expand: null argument");
+        if (!options->canonical_order || options->witness_pruning)
+            throw std::invalid_argument("mymyr_amd: expand: the device expansion takes canonical_order on and witness_pruning off");
+        const DeviceTask& d = device_task(task);
+        const TaskDev& T = *d.thost;
+        constexpr u64 kMaxRows = (u64{1} << 31) - 1;
+        if (rows > kMaxRows)
+            throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 states in one batch");
+        if (words < T.W)
+            throw std::invalid_argument("mymyr: expand: state rows of " + std::to_string(words) + " words; the task needs " +
+                                        std::to_string(T.W));
+        if (out->binding && out->label_width < T.label_width)
+            throw std::invalid_argument("mymyr: expand: label width " + std::to_string(out->label_width) +
+                                        " is below the largest schema arity " + std::to_string(T.label_width));
+        if (out->capacity > kMaxRows)
+            throw std::invalid_argument("mymyr: expand: capacity above 2^31 - 1 rows");
+        if (out->succ && out->words == 0 && out->capacity)
+            throw std::invalid_argument("mymyr: expand: successor rows of zero words");
+        if (out->goal && !out->succ)
+            throw std::invalid_argument("mymyr: expand: goal flags need the successor rows");
+        if (options->drop_noops && out->capacity && !out->index)
+            throw std::invalid_argument("mymyr: expand: drop_noops requires index");
+        const auto stream = static_cast<hipStream_t>(stream_);
+        out->generated = out->total = 0;
+        out->words_needed = 0;
+        // scratch: per-row counts and no-op counts, offsets before and after dropping, scan scratch, status words
+        const u64 n = std::max<u64>(rows, 1);
+        u32* counts = dev_alloc<u32>(n, "expand counts");
+        u32* noops = dev_alloc<u32>(n, "expand no-op counts");
+        u32* kept = dev_alloc<u32>(n, "expand kept counts");
+        u64* pre = dev_alloc<u64>(n + 1, "expand offsets");
+        u64* fin = dev_alloc<u64>(n + 1, "expand kept offsets");
+        u64* scratch = dev_alloc<u64>(scan_scratch_words(n), "expand scan scratch");
+        u32* words_status = dev_alloc<u32>(2, "expand status");  // [0] words needed, [1] status
+        struct Free
+        {
+            std::vector<void*> p;
+            ~Free()
+            {
+                for (void* q : p)
+                    dev_free(q);
+            }
+        } freeing{{counts, noops, kept, pre, fin, scratch, words_status}};
+        launch_fill_u32(words_status, 2, 0, stream);
+        ExpandArgs a{};
+        a.T = T;
+        a.states = states;
+        a.rows = rows;
+        a.words = words;
+        a.drop_noops = options->drop_noops ? 1 : 0;
+        a.out_words = out->words;
+        a.label_width = out->label_width;
+        a.counts = counts;
+        a.noops = noops;
+        a.words_needed = words_status;
+        a.status = words_status + 1;
+        a.pass = 0;
+        launch_expand(a, stream);
+        launch_exclusive_scan(counts, pre, rows, scratch, pre + rows, stream);
+        if (a.drop_noops)
+        {
+            launch_kept_counts(counts, noops, rows, kept, stream);
+            launch_exclusive_scan(kept, fin, rows, scratch, fin + rows, stream);
+        }
+        u64 totals[2] = {0, 0};
+        u32 st[2] = {0, 0};
+        hip_check(hipMemcpyAsync(&totals[0], pre + rows, sizeof(u64), hipMemcpyDeviceToHost, stream), "expand total");
+        if (a.drop_noops)
+            hip_check(hipMemcpyAsync(&totals[1], fin + rows, sizeof(u64), hipMemcpyDeviceToHost, stream), "expand total");
+        hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
+        hip_check(hipStreamSynchronize(stream), "expand");
+        if (options->validate && (st[1] & kStatusWideRow))
+            throw std::invalid_argument("mymyr: expand: a state has atoms past the task's slots");
+        if (st[1] & ~kStatusWideRow)
+            throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
+        const u64 generated = totals[0];
+        if (generated > kMaxRows)
+            throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 successors in one batch");
+        // an overflow with drop_noops reports the counts before dropping
+        const bool dropping = a.drop_noops && generated <= out->capacity;
+        const u64* offs = dropping ? fin : pre;
+        out->generated = generated;
+        out->total = dropping ? totals[1] : generated;
+        if (out->offsets)
+            launch_offsets_i32(offs, rows + 1, out->offsets, stream);
+        const bool rows_out = out->succ || out->parent || out->schema || out->binding || out->goal || out->succ_hash || out->noop ||
+                              out->index;
+        if ((rows_out && out->capacity) || (out->succ && out->words < T.W))
+        {
+            a.pass = 1;
+            a.drop_noops = dropping ? 1 : 0;
+            a.offsets = offs;
+            a.capacity = out->capacity;
+            a.succ = out->succ;
+            a.parent = out->parent;
+            a.schema = out->schema;
+            a.binding = out->binding;
+            a.goal = out->goal;
+            a.succ_hash = out->succ_hash;
+            a.noop = out->noop;
+            a.index = out->index;
+            launch_expand(a, stream);
+        }
+        hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
+        hip_check(hipStreamSynchronize(stream), "expand");
+        if (st[1] & ~kStatusWideRow)
+            throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
+        out->words_needed = st[0];
     });
 }
 

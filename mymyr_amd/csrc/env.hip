@@ -1369,6 +1369,197 @@ __global__ void k_env_reset_cache(u64 rows, u32 width, const u8* mask, u32* cach
     }
 }
 
+/// Applies the effects of the picked binding of schema s to the LDS row only (the view stays the parent's), keeping
+/// the effect slots and their prior bits for succ_revert. Returns whether no bit changed (a no-op successor).
+__device__ __forceinline__ bool succ_apply(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane, u32* status)
+{
+    const auto& S = H.schemas[s];
+    bool noop = true;
+    if (lane == 0)
+    {
+        const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
+        if (S.eff_end - S.eff_begin > kMaxEff)
+            atomicOr(status, kStatusCapacity);
+        for (u32 k = 0; k < ne; ++k)
+        {
+            L.eff[k] = effect_slot(T, L, H.effects[S.eff_begin + k]);
+            L.before[k] = L.eff[k] != kNone && row_bit(L.row, L.eff[k]);
+            if (k < S.nadd && L.eff[k] == kNone)
+                atomicOr(status, kStatusNoSlot);
+        }
+        for (u32 k = S.nadd; k < ne; ++k)
+            if (L.eff[k] != kNone)
+                L.row[L.eff[k] >> 6] &= ~(u64{1} << (L.eff[k] & 63));
+        for (u32 k = 0; k < S.nadd && k < ne; ++k)
+            if (L.eff[k] != kNone)
+                L.row[L.eff[k] >> 6] |= u64{1} << (L.eff[k] & 63);
+        for (u32 k = 0; k < ne; ++k)
+            if (L.eff[k] != kNone && row_bit(L.row, L.eff[k]) != (L.before[k] != 0))
+                noop = false;
+    }
+    wave_sync();
+    return __shfl(noop ? 1 : 0, 0, kWave) != 0;
+}
+
+/// Restores the parent row after succ_apply.
+__device__ __forceinline__ void succ_revert(const auto& H, const Lds& L, u32 s, u32 lane)
+{
+    if (lane == 0)
+    {
+        const auto& S = H.schemas[s];
+        const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
+        for (u32 k = 0; k < ne; ++k)
+        {
+            const u32 sl = L.eff[k];
+            if (sl == kNone)
+                continue;
+            if (L.before[k])
+                L.row[sl >> 6] |= u64{1} << (sl & 63);
+            else
+                L.row[sl >> 6] &= ~(u64{1} << (sl & 63));
+        }
+    }
+    wave_sync();
+}
+
+/// 1 + the index of the highest nonzero word of the LDS row (0 for an empty row), on every lane.
+__device__ __forceinline__ u32 trimmed_words(const lds<u64>* row, u32 W, u32 lane)
+{
+    u32 top = 0;
+    for (u32 w = lane; w < W; w += kWave)
+        if (row[w])
+            top = w + 1;
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1)
+        top = max(top, static_cast<u32>(__shfl_xor(static_cast<int>(top), d, kWave)));
+    return top;
+}
+
+template<bool kStaged, bool kLevels>
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_expand(ExpandArgs A)
+{
+    extern __shared__ u64 smem[];
+    const TaskDev& T = A.T;
+    Tab<kStaged> H;
+    lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+    const u32 Lw = A.label_width;
+    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
+    {
+        const u64* src = A.states + i * A.words;
+        if (A.pass == 0)
+        {
+            // rows must hold no atoms past the task's slots (ExpandOptions::validate)
+            bool wide = false;
+            for (u32 w = lane; w < A.words; w += kWave)
+            {
+                const u64 x = src[w];
+                if (w >= T.W)
+                    wide = wide || x != 0;
+                else if (w == T.W - 1 && (T.fluent_slots & 63))
+                    wide = wide || (x >> (T.fluent_slots & 63)) != 0;
+            }
+            if (__ballot(wide) && lane == 0)
+                atomicOr(A.status, kStatusWideRow);
+        }
+        load_row_lds(T, L, src, lane);
+        build_view(T, H, L, lane);
+        const u32 c = count_all<kLevels>(T, H, L, lane);
+        if (A.pass == 0 && !A.drop_noops)
+        {
+            if (lane == 0)
+                A.counts[i] = c;
+            continue;
+        }
+        const bool keep_all = A.pass == 1 && A.drop_noops && A.noops[i] == c;
+        u32 noops = 0, kept = 0;
+        for (u32 k = 0; k < c; ++k)
+        {
+            u32 s = kNone, rank = 0;
+            select_schema(T, L, k, &s, &rank);
+            if (s == kNone || !pick<kLevels>(T, H, L, s, rank, lane))
+            {
+                if (lane == 0)
+                    atomicOr(A.status, kStatusPickFailed);
+                break;
+            }
+            const bool noop = succ_apply(T, H, L, s, lane, A.status);
+            noops += noop ? 1 : 0;
+            if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
+            {
+                const u64 pos = A.offsets[i] + (A.drop_noops ? kept : k);
+                ++kept;
+                const u32 n = (A.succ || A.succ_hash) ? trimmed_words(L.row, T.W, lane) : 0;
+                const bool fits = n <= A.out_words;
+                if (A.succ && !fits && lane == 0)
+                    atomicMax(A.words_needed, n);
+                if (pos < A.capacity)
+                {
+                    if (A.succ)
+                    {
+                        u64* dst = A.succ + pos * A.out_words;
+                        for (u32 w = lane; w < A.out_words; w += kWave)
+                            dst[w] = (fits && w < T.W) ? L.row[w] : 0;
+                    }
+                    if (A.goal)
+                    {
+                        const bool g = goal_test(T, H, L.row, lane);
+                        if (lane == 0)
+                            A.goal[pos] = g ? 1 : 0;
+                    }
+                    if (lane == 0)
+                    {
+                        if (A.succ_hash)
+                        {
+                            // hash_state over the trimmed words: the pairs chained in order
+                            u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
+                            for (u32 w = 0; w < n; w += 2)
+                                h = mulfold(h ^ L.row[w] ^ kHashP1, (w + 1 < n ? L.row[w + 1] : 0) ^ kHashP2);
+                            A.succ_hash[pos] = mix64(h);
+                        }
+                        if (A.noop)
+                            A.noop[pos] = noop ? 1 : 0;
+                        if (A.index)
+                            A.index[pos] = static_cast<i32>(k);
+                        if (A.parent)
+                            A.parent[pos] = static_cast<i32>(i);
+                        if (A.schema)
+                            A.schema[pos] = static_cast<i32>(s);
+                    }
+                    if (A.binding)
+                    {
+                        const u32 arity = H.schemas[s].arity;
+                        for (u32 q = lane; q < Lw; q += kWave)
+                            A.binding[pos * Lw + q] = q < arity ? static_cast<i32>(L.ub[q]) : -1;
+                    }
+                }
+            }
+            succ_revert(H, L, s, lane);
+        }
+        if (A.pass == 0 && lane == 0)
+        {
+            A.counts[i] = c;
+            A.noops[i] = noops;
+        }
+        wave_sync();
+    }
+}
+
+__global__ void k_offsets_i32(const u64* src, u64 n, i32* dst)
+{
+    const u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n)
+        dst[i] = static_cast<i32>(src[i]);
+}
+
+__global__ void k_kept_counts(const u32* counts, const u32* noops, u64 rows, u32* kept)
+{
+    const u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < rows)
+        kept[i] = noops[i] == counts[i] ? counts[i] : counts[i] - noops[i];
+}
+
 // Successor listing: successor k of row i is pick(k) applied to a copy of the row.
 template<bool kStaged, bool kLevels>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, const u64* states, u64 rows, u32 words, u32 cap, i32* count,
@@ -1477,6 +1668,32 @@ void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, 
     set_lds(reinterpret_cast<const void*>(fn), lds);
     hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks, cache);
     launch_check("env count");
+}
+
+void launch_expand(const ExpandArgs& a, hipStream_t stream)
+{
+    if (a.rows == 0)
+        return;
+    size_t lds = 0;
+    const unsigned nw = waves_per_block(a.T, &lds);
+    const auto fn = variant(a.T, k_expand<true, false>, k_expand<true, true>, k_expand<false, false>, k_expand<false, true>);
+    set_lds(reinterpret_cast<const void*>(fn), lds);
+    hipLaunchKernelGGL(fn, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), lds, stream, a);
+    launch_check("expand");
+}
+
+void launch_offsets_i32(const u64* src, u64 n, i32* dst, hipStream_t stream)
+{
+    hipLaunchKernelGGL(k_offsets_i32, dim3(blocks_for(n, 256)), dim3(256), 0, stream, src, n, dst);
+    launch_check("expand offsets");
+}
+
+void launch_kept_counts(const u32* counts, const u32* noops, u64 rows, u32* kept, hipStream_t stream)
+{
+    if (rows == 0)
+        return;
+    hipLaunchKernelGGL(k_kept_counts, dim3(blocks_for(rows, 256)), dim3(256), 0, stream, counts, noops, rows, kept);
+    launch_check("expand kept counts");
 }
 
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream)

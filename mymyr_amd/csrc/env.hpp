@@ -72,6 +72,41 @@ void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const 
 /// Words of a count-cache row: the per-schema counts, then the 64-bit state fingerprint.
 __host__ __device__ inline u32 cache_width(const TaskDev& T) { return T.num_schemas + 2; }
 
+/// The flat expansion of rows (rl::expand, include/mymyr/rl/expand.hpp:1-130). Pass 0 counts each row's successors
+/// (and, with drop_noops, its no-op successors) and checks that rows have no atoms past the task's slots; pass 1 writes
+/// the successors of row i from offsets[i] on (kept rows only with drop_noops), up to capacity.
+struct ExpandArgs
+{
+    TaskDev T;
+    const u64* states;
+    u64 rows;
+    u32 words;
+    u32 pass;
+    u32 drop_noops;
+    u32 out_words;    // words of the succ rows
+    u32 label_width;  // columns of binding
+    u32* counts;      // [rows]
+    u32* noops;       // [rows]
+    const u64* offsets;  // [rows]
+    u64 capacity;
+    u64* succ;
+    i32* parent;
+    i32* schema;
+    i32* binding;
+    u8* goal;
+    u64* succ_hash;
+    u8* noop;
+    i32* index;
+    u32* words_needed;  // device word: the widest trimmed successor that did not fit out_words
+    u32* status;
+};
+
+void launch_expand(const ExpandArgs& a, hipStream_t stream);
+/// kept[i] = counts[i] - noops[i], or counts[i] when every successor of row i is a no-op.
+void launch_kept_counts(const u32* counts, const u32* noops, u64 rows, u32* kept, hipStream_t stream);
+/// dst[i] = src[i] for i < n (offsets fit int32 after the caller's checks).
+void launch_offsets_i32(const u64* src, u64 n, i32* dst, hipStream_t stream);
+
 /// Per-row successor listing in canonical order (schema [rows, cap], binding [rows, cap, L], successor rows
 /// [rows, cap, words]) and counts [rows]; entries past cap are counted but not written.
 void launch_successors(const TaskDev& T, const u64* states, u64 rows, u32 words, u32 cap, i32* count, i32* schema, i32* binding,

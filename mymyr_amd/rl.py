@@ -184,3 +184,49 @@ def successors(task: Task, states: torch.Tensor, cap: int = 4096) -> tuple[torch
     check(lib.mya_successors(task.handle, s.data_ptr(), n, w, cap, count.data_ptr(), schema.data_ptr(), binding.data_ptr(),
                              rows.data_ptr(), _stream()))
     return count, schema, binding, rows
+
+
+def expand(task: Task, states: torch.Tensor, *, capacity: int | None = None, goal: bool = False, hashes: bool = False,
+           noops: bool = False, drop_noops: bool = False, index: bool = False, validate: bool = True,
+           words: int | None = None) -> dict:
+    """The flat expansion of states [N, W] on the device (rl.expand, include/mymyr/rl/expand.hpp:1-130): successor rows
+    "succ" [M, words], "parent", "schema" [M] int32, "binding" [M, label_width] int32 (-1 padded), "offsets" [N + 1]
+    int32, with goal=True "goal" [M] uint8, hashes=True "succ_hash" [M] (uint64 bits in int64), noops=True "noop" [M]
+    uint8, and "index" [M] int32 (the position in the parent's full successor order) with drop_noops or index=True;
+    plus "generated", "total", "words_needed" and "overflow". capacity None sizes the buffers to every successor (a
+    first call counts them). Canonical order, witness pruning off; drop_noops removes a state's no-op successors unless
+    all of them are no-ops."""
+    s = states.view(torch.int64) if states.dtype == torch.uint64 else states
+    if not s.is_cuda or s.dim() != 2 or s.dtype != torch.int64:
+        raise ValueError("mymyr_amd: expand: states must be a 2-d int64/uint64 device tensor")
+    s = s.contiguous()
+    rows, w = s.shape
+    ow = task.words if words is None else words
+    L = max(1, task.label_width)
+    opts = _lib.ExpandOptions(1, 0, int(validate), int(drop_noops))
+    if capacity is None:
+        probe = _lib.Expansion()
+        check(lib.mya_expand(task.handle, s.data_ptr(), rows, w, ctypes.byref(opts), ctypes.byref(probe), _stream()))
+        capacity = probe.generated
+    dev = s.device
+    cap = int(capacity)
+    succ = torch.zeros((cap, ow), dtype=torch.int64, device=dev)
+    parent = torch.empty(cap, dtype=torch.int32, device=dev)
+    schema = torch.empty(cap, dtype=torch.int32, device=dev)
+    binding = torch.empty((cap, L), dtype=torch.int32, device=dev)
+    offsets = torch.empty(rows + 1, dtype=torch.int32, device=dev)
+    gl = torch.empty(cap, dtype=torch.uint8, device=dev) if goal else None
+    sh = torch.empty(cap, dtype=torch.int64, device=dev) if hashes else None
+    np_ = torch.empty(cap, dtype=torch.uint8, device=dev) if noops else None
+    ix = torch.empty(cap, dtype=torch.int32, device=dev) if (drop_noops or index) else None
+    x = _lib.Expansion(cap, ow, L, succ.data_ptr(), parent.data_ptr(), schema.data_ptr(), binding.data_ptr(), _p(gl),
+                       offsets.data_ptr(), _p(sh), _p(np_), _p(ix), 0, 0, 0, 0)
+    check(lib.mya_expand(task.handle, s.data_ptr(), rows, w, ctypes.byref(opts), ctypes.byref(x), _stream()))
+    kept = min(x.total, cap)
+    out = {"succ": succ[:kept], "parent": parent[:kept], "schema": schema[:kept], "binding": binding[:kept],
+           "offsets": offsets, "generated": x.generated, "total": x.total, "words_needed": x.words_needed,
+           "overflow": x.generated > cap or x.total > cap or x.words_needed > ow}
+    for name, t in (("goal", gl), ("succ_hash", sh), ("noop", np_), ("index", ix)):
+        if t is not None:
+            out[name] = t[:kept]
+    return out

@@ -500,6 +500,42 @@ def successors(task: Task, row, witness: bool = False):
     return out
 
 
+def expand(task: Task, rows, capacity: int | None = None, drop_noops: bool = False) -> dict:
+    """The flat expansion of rows (rl::expand over one task, expand_impl: src/mymyr/rl/expand.cpp:560-620, the
+    no-op filter of DirectSink::compact: 340-377): per state its successors in canonical order, each with its parent,
+    schema, binding, goal flag, hash_state, no-op flag (the successor equals the parent) and index (its position in
+    the parent's full order). With drop_noops a state keeps its non-no-op successors, or all of them when every one is
+    a no-op. generated counts every successor; an overflow with drop_noops (generated > capacity) reports the counts
+    before dropping in offsets and total."""
+    out = {k: [] for k in ("succ", "parent", "schema", "binding", "goal", "succ_hash", "noop", "index")}
+    offsets, per_state = [0], []
+    for i, row in enumerate(rows):
+        entries = []
+        for k, (si, b, nxt) in enumerate(successors(task, row)):
+            entries.append((k, si, b, nxt, bool(np.array_equal(nxt, row))))
+        per_state.append(len(entries))
+        kept = [e for e in entries if not e[4]] if drop_noops else entries
+        if drop_noops and not kept:
+            kept = entries
+        for k, si, b, nxt, noop in kept:
+            out["succ"].append(nxt)
+            out["parent"].append(i)
+            out["schema"].append(si)
+            out["binding"].append(list(b))
+            out["goal"].append(is_goal(task, nxt))
+            out["succ_hash"].append(hash_state(nxt))
+            out["noop"].append(noop)
+            out["index"].append(k)
+        offsets.append(len(out["parent"]))
+    generated = sum(per_state)
+    total = offsets[-1]
+    if drop_noops and capacity is not None and generated > capacity:
+        offsets = [0] + list(np.cumsum(per_state))
+        total = generated
+    out.update(offsets=offsets, generated=generated, total=total)
+    return out
+
+
 def is_goal(task: Task, row) -> bool:
     """Successors::goal_holds over the compiled goal (successors.hpp:129-141)."""
     if task.goal_unsat:

@@ -142,3 +142,26 @@ def test_port_against_reference_random_rows():
     for _ in range(200):
         s, e, d, c = (int(x) for x in rng.integers(1, 2**31, size=4))
         assert port.successor_index(s, e, d, c) == ref.successor_index(s, e, d, c)
+
+
+def test_expand_noop_filter_closed_form(golden):
+    """The switches task (two idle schemas, stop, set; the reference's no-op test domain, tests/python/test_rl_noops.py)
+    from its initial state: four successors in schema order, the idle ones no-ops; dropping them keeps stop and set at
+    their full-order positions 2 and 3; a state whose successors are all no-ops keeps them all."""
+    t = port.Task(open(golden.task_path("noop_switches")).read())
+    row = np.zeros(t.words, np.uint64)
+    row[0] = 1  # live
+    full = port.expand(t, [row])
+    assert full["schema"] == [0, 1, 2, 3] and full["noop"] == [True, True, False, False]
+    assert full["offsets"] == [0, 4] and full["generated"] == full["total"] == 4
+    assert [port.hash_state(r) for r in full["succ"]][:2] == [port.hash_state(row)] * 2
+    kept = port.expand(t, [row], drop_noops=True)
+    assert kept["schema"] == [2, 3] and kept["index"] == [2, 3] and kept["offsets"] == [0, 2] and kept["total"] == 2
+    assert kept["generated"] == 4 and kept["goal"] == [False, True]
+    # live and p: only the idle schemas apply, all no-ops, so all are kept
+    both = np.array([3], np.uint64)
+    k2 = port.expand(t, [both], drop_noops=True)
+    assert k2["schema"] == [0, 1] and k2["noop"] == [True, True] and k2["offsets"] == [0, 2]
+    # an overflow with drop_noops reports the counts before dropping
+    k3 = port.expand(t, [row, row], capacity=5, drop_noops=True)
+    assert k3["generated"] == 8 and k3["total"] == 8 and k3["offsets"] == [0, 4, 8]
