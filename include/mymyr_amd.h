@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 5
+#define MYA_ABI_VERSION 6
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -154,6 +154,11 @@ typedef struct mya_env_batch
      * counts of a row from it instead of counting the row's successors when the fingerprint matches the row's state
      * (a state written directly is counted again; refresh brings at_goal up to date for it). Null: every step counts. */
     uint32_t* counts;
+    /* Per-env goal masks (EnvBatch::goal_pos / goal_neg, include/mymyr/rl/env.hpp:103-104), optional, both or neither:
+     * [rows, words] each. A row's goal is (s & goal_pos) == goal_pos and (s & goal_neg) == 0 (mask_goal,
+     * src/mymyr/rl/env.cpp:55-61). reset writes the task's goal into them unless keep_goals; an autoreset writes it. */
+    uint64_t* goal_pos;
+    uint64_t* goal_neg;
 } mya_env_batch;
 
 /* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
@@ -186,9 +191,12 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out);
 void mya_env_free(mya_env* env);
 /* Initial state's successor count and goal flag. */
 int mya_env_initial_count(const mya_env* env, uint32_t* count, uint8_t* goal);
-/* HostEnv::reset (env.cpp:207-240): rows with mask[i] != 0 (device, optional) to the initial state, steps 0,
- * at_goal and count (device, optional) of the initial state; draws kept. Async on the stream. */
-int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, void* stream);
+/* HostEnv::reset (env.cpp:223-255): rows with mask[i] != 0 (device, optional) to the initial state, steps 0,
+ * at_goal and count (device, optional) of the initial state; draws kept. With per-env goal masks, the task's goal is
+ * written into them unless keep_goals, in which case the given masks stay, at_goal is their test on the initial state,
+ * and masks that set fluent slots the task does not have set the sticky status (mya_env_check). Async on the stream. */
+int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals,
+                  void* stream);
 /* HostEnv::step (env.cpp:530-548 / step_row_impl 351-528): actions (device, int64 [rows], optional: the random policy
  * when null). Async on the stream; device-side failures set the sticky status that mya_env_check reports. */
 int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 5  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 6  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -63,6 +63,8 @@ class EnvBatch(Structure):
         ("at_goal", c_void_p),
         ("first_env", c_uint64),
         ("counts", c_void_p),
+        ("goal_pos", c_void_p),
+        ("goal_neg", c_void_p),
     ]
 
 
@@ -199,7 +201,7 @@ def _load() -> ctypes.CDLL:
     optional = {
         "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),
         "mya_env_free": (None, [c_void_p]),
-        "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_void_p]),
+        "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_void_p]),
         "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p]),
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_refresh": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),

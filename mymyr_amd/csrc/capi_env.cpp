@@ -23,6 +23,7 @@ struct mya_env
     u32 init_goal = 0;
     u8* init_masks = nullptr;  // device [num_schemas]
     u32* init_cache = nullptr; // device [num_schemas + 2]: the initial state's count-cache row
+    u64* goal_masks = nullptr; // device [2, W]: the task's goal as masks (positive, then negative)
     u32* d_status = nullptr;
     u32* h_status = nullptr;
 };
@@ -40,6 +41,11 @@ void check_batch(const mya_env* e, const mya_env_batch* b)
     if (b->words < e->T.W)
         throw std::invalid_argument("mymyr: env: state rows of " + std::to_string(b->words) + " words; the task needs " +
                                     std::to_string(e->T.W) + " (its widest instance's words)");
+    if ((b->goal_pos == nullptr) != (b->goal_neg == nullptr))
+        throw std::invalid_argument("mymyr: env: per-env goals need both goal_pos and goal_neg");
+    if (b->goal_pos && e->T.goal_unsat)
+        throw std::invalid_argument("mymyr: env: per-env goal masks cannot express the goal of instance 0 (it is statically "
+                                    "unsatisfiable); use the instances' goal tests (no goal masks)");
 }
 }  // namespace
 
@@ -77,6 +83,16 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
         hip_check(hipMemcpy(row, task->compiled->initial.data(), W * sizeof(u64), hipMemcpyHostToDevice), "initial row");
         e->init_masks = dev_alloc<u8>(std::max<u32>(1, e->T.num_schemas), "initial masks");
         e->init_cache = dev_alloc<u32>(cache_width(e->T), "initial count cache");
+        {
+            // the task's goal as masks over its words
+            std::vector<u64> gm(2 * static_cast<size_t>(W), 0);
+            for (u32 sl : task->compiled->goal_pos)
+                gm[sl >> 6] |= u64{1} << (sl & 63);
+            for (u32 sl : task->compiled->goal_neg)
+                gm[W + (sl >> 6)] |= u64{1} << (sl & 63);
+            e->goal_masks = dev_alloc<u64>(gm.size(), "goal masks");
+            hip_check(hipMemcpy(e->goal_masks, gm.data(), gm.size() * sizeof(u64), hipMemcpyHostToDevice), "goal masks");
+        }
         launch_env_count(e->T, row, 1, W, cnt, gl, e->init_masks, e->init_cache, nullptr);
         i32 hc = 0;
         u8 hg = 0;
@@ -98,6 +114,7 @@ void mya_env_free(mya_env* env)
     dev_free(env->d_status);
     dev_free(env->init_masks);
     dev_free(env->init_cache);
+    dev_free(env->goal_masks);
     if (env->h_status)
         (void)hipHostFree(env->h_status);
     delete env;
@@ -115,7 +132,7 @@ int mya_env_initial_count(const mya_env* env, uint32_t* count, uint8_t* goal)
     });
 }
 
-int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, void* stream)
+int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals, void* stream)
 {
     return guarded([&] {
         if (!env)
@@ -123,6 +140,10 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         check_batch(env, batch);
         launch_env_reset(env->T, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, batch->counts,
                          env->init_cache, env->init_count, env->init_goal, static_cast<hipStream_t>(stream));
+        if (batch->goal_pos)
+            launch_env_reset_goals(env->T, batch->rows, batch->words, mask, batch->goal_pos, batch->goal_neg, env->goal_masks,
+                                   env->goal_masks + env->T.W, keep_goals != 0, batch->at_goal, env->d_status,
+                                   static_cast<hipStream_t>(stream));
     });
 }
 
@@ -173,6 +194,10 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.init_masks = env->init_masks;
         a.counts = batch->counts;
         a.init_counts = env->init_cache;
+        a.goal_pos = batch->goal_pos;
+        a.goal_neg = batch->goal_neg;
+        a.task_goal_pos = env->goal_masks;
+        a.task_goal_neg = env->goal_masks + env->T.W;
         if (out->atoms && out->max_atoms == 0)
             throw std::invalid_argument("mymyr_amd: env: atoms output needs max_atoms > 0");
         a.init_count = env->init_count;
@@ -189,7 +214,7 @@ int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, vo
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
         launch_env_count(env->T, batch->states, batch->rows, batch->words, count, batch->at_goal, nullptr, batch->counts,
-                         static_cast<hipStream_t>(stream));
+                         static_cast<hipStream_t>(stream), batch->goal_pos, batch->goal_neg, env->d_status);
     });
 }
 
@@ -210,6 +235,8 @@ int mya_env_check(mya_env* env)
                 m += " add-effect-without-slot";
             if (s & kStatusPickFailed)
                 m += " pick-failed";
+            if (s & kStatusGoalMask)
+                m = "mymyr: env: goal masks set fluent slots the task does not have; supply goals for the task's slots";
             throw std::runtime_error(m);
         }
     });

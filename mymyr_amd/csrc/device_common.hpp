@@ -114,5 +114,6 @@ enum StatusBit : u32
     kStatusWideRow = 1u << 2,       // a state has bits beyond the task's words
     kStatusNoSlot = 1u << 3,        // an add effect without an atom slot
     kStatusPickFailed = 1u << 4,    // the chosen successor index was not found (internal inconsistency)
+    kStatusGoalMask = 1u << 5,      // per-env goal masks set bits past the task's fluent slots
 };
 }  // namespace mya

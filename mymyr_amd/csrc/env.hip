@@ -701,6 +701,33 @@ __device__ __forceinline__ u32 count_all(const TaskDev& T, const auto& H, const 
     return total;
 }
 
+/// The per-env goal test (mask_goal, src/mymyr/rl/env.cpp:55-61): the LDS row against a row of goal masks.
+__device__ __forceinline__ bool mask_goal(const lds<u64>* row, const u64* gp, const u64* gn, u32 W, u32 lane)
+{
+    bool ok = true;
+    for (u32 w = lane; w < W; w += kWave)
+    {
+        const u64 x = row[w];
+        ok = ok && (x & gp[w]) == gp[w] && (x & gn[w]) == 0;
+    }
+    return __ballot(!ok) == 0;
+}
+
+/// Whether a row of goal masks sets only the task's fluent slots (words past W and bits past the last slot clear).
+__device__ __forceinline__ bool goal_masks_fit(const u64* gp, const u64* gn, u32 words, const TaskDev& T, u32 lane)
+{
+    bool fit = true;
+    for (u32 w = lane; w < words; w += kWave)
+    {
+        const u64 x = gp[w] | gn[w];
+        if (w >= T.W)
+            fit = fit && x == 0;
+        else if (w == T.W - 1 && (T.fluent_slots & 63))
+            fit = fit && (x >> (T.fluent_slots & 63)) == 0;
+    }
+    return __ballot(!fit) == 0;
+}
+
 /// A 64-bit fingerprint of the state (the count cache's check that a row still holds the state its counts are of).
 __device__ __forceinline__ u64 state_fingerprint(const lds<u64>* row, u32 W, u32 lane)
 {
@@ -1193,7 +1220,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
                 break;
             // 3. the move, goal and (next phase) the successor count of the reached state
             apply_effects(T, H, L, schema, lane, A.status);
-            g = goal_test(T, H, L.row, lane);
+            g = A.goal_pos ? mask_goal(L.row, A.goal_pos + i * A.words, A.goal_neg + i * A.words, T.W, lane)
+                           : goal_test(T, H, L.row, lane);
         }
         // 4. rewards, termination, truncation (env.cpp:466-485)
         const bool dead = !A.cfg.dead_end_none && !g && ((st == kOk && c2 == 0) || st == kStuck);
@@ -1234,6 +1262,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
         {
             for (u32 k = lane; k < A.words; k += kWave)
                 grow[k] = k < T.W ? T.initial[k] : 0;
+            if (A.goal_pos)
+                for (u32 k = lane; k < A.words; k += kWave)
+                {
+                    A.goal_pos[i * A.words + k] = k < T.W ? A.task_goal_pos[k] : 0;
+                    A.goal_neg[i * A.words + k] = k < T.W ? A.task_goal_neg[k] : 0;
+                }
             if (A.atoms)
                 for (u32 k = lane; k < T.W; k += kWave)
                     L.row[k] = T.initial[k];
@@ -1301,7 +1335,8 @@ __global__ __launch_bounds__(kWave) void k_encode(const u64* states, u64 rows, u
 
 template<bool kStaged, bool kLevels>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(TaskDev T, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
-                                                                 u8* masks, u32* cache)
+                                                                 u8* masks, u32* cache, const u64* goal_pos, const u64* goal_neg,
+                                                                 u32* status)
 {
     extern __shared__ u64 smem[];
     Tab<kStaged> H;
@@ -1313,7 +1348,17 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(TaskDev T, cons
         load_row_lds(T, L, states + i * words, lane);
         build_view(T, H, L, lane);
         const u32 c = count_all<kLevels>(T, H, L, lane);
-        const bool g = goal_test(T, H, L.row, lane);
+        bool g;
+        if (goal_pos)
+        {
+            const u64* gp = goal_pos + i * words;
+            const u64* gn = goal_neg + i * words;
+            if (!goal_masks_fit(gp, gn, words, T, lane) && lane == 0 && status)
+                atomicOr(status, kStatusGoalMask);
+            g = mask_goal(L.row, gp, gn, T.W, lane);
+        }
+        else
+            g = goal_test(T, H, L.row, lane);
         if (lane == 0)
         {
             if (count)
@@ -1354,6 +1399,41 @@ __global__ void k_env_reset(TaskDev T, u64* states, u64 rows, u32 words, const u
             if (count)
                 count[i] = static_cast<i32>(init_count);
         }
+    }
+}
+
+__global__ void k_env_reset_goals(TaskDev T, u64 rows, u32 words, const u8* mask, u64* goal_pos, u64* goal_neg, const u64* task_pos,
+                                  const u64* task_neg, u32 keep, u8* at_goal, u32* status)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        if (mask && !mask[i])
+            continue;
+        u64* gp = goal_pos + i * words;
+        u64* gn = goal_neg + i * words;
+        if (!keep)
+        {
+            for (u32 w = 0; w < words; ++w)
+            {
+                gp[w] = w < T.W ? task_pos[w] : 0;
+                gn[w] = w < T.W ? task_neg[w] : 0;
+            }
+            continue;
+        }
+        bool ok = true, fit = true;
+        for (u32 w = 0; w < words; ++w)
+        {
+            const u64 p = gp[w], n = gn[w], x = w < T.W ? T.initial[w] : 0;
+            ok = ok && (x & p) == p && (x & n) == 0;
+            if (w >= T.W)
+                fit = fit && (p | n) == 0;
+            else if (w == T.W - 1 && (T.fluent_slots & 63))
+                fit = fit && ((p | n) >> (T.fluent_slots & 63)) == 0;
+        }
+        if (!fit)
+            atomicOr(status, kStatusGoalMask);
+        if (at_goal)
+            at_goal[i] = ok ? 1 : 0;
     }
 }
 
@@ -1658,7 +1738,7 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
 }
 
 void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
-                      hipStream_t stream)
+                      hipStream_t stream, const u64* goal_pos, const u64* goal_neg, u32* status)
 {
     if (rows == 0)
         return;
@@ -1666,7 +1746,8 @@ void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, 
     const unsigned nw = waves_per_block(T, &lds);
     const auto fn = variant(T, k_env_count<true, false>, k_env_count<true, true>, k_env_count<false, false>, k_env_count<false, true>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks, cache);
+    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks, cache,
+                       goal_pos, goal_neg, status);
     launch_check("env count");
 }
 
@@ -1720,6 +1801,16 @@ void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const 
                            stream, rows, cache_width(T), mask, cache, init_cache);
         launch_check("env reset cache");
     }
+}
+
+void launch_env_reset_goals(const TaskDev& T, u64 rows, u32 words, const u8* mask, u64* goal_pos, u64* goal_neg, const u64* task_pos,
+                            const u64* task_neg, bool keep_goals, u8* at_goal, u32* status, hipStream_t stream)
+{
+    if (rows == 0)
+        return;
+    hipLaunchKernelGGL(k_env_reset_goals, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream, T,
+                       rows, words, mask, goal_pos, goal_neg, task_pos, task_neg, keep_goals ? 1u : 0u, at_goal, status);
+    launch_check("env reset goals");
 }
 
 void launch_successors(const TaskDev& T, const u64* states, u64 rows, u32 words, u32 cap, i32* count, i32* schema, i32* binding,

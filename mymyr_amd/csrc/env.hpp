@@ -47,6 +47,10 @@ struct EnvArgs
     u32 max_atoms;
     u8* masks;        // [rows, num_schemas]: schemas with an applicable binding in the observed state (optional)
     u32* counts;      // [rows, num_schemas + 2]: the count cache (per-schema counts, then the state's fingerprint), optional
+    u64* goal_pos;    // [rows, words]: per-env goal masks (optional, with goal_neg)
+    u64* goal_neg;
+    const u64* task_goal_pos;  // [W]: the task's goal as masks (device), written by an autoreset
+    const u64* task_goal_neg;
     const u32* init_counts;  // [num_schemas + 2]: the initial state's cache row (device)
     const u8* init_masks;  // [num_schemas]: the initial state's masks (device)
     u32 init_count;
@@ -59,7 +63,7 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream);
 /// count[i] (successors), goal[i], masks [rows, num_schemas] and the count cache [rows, num_schemas + 2] of rows (each
 /// may be null).
 void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
-                      hipStream_t stream);
+                      hipStream_t stream, const u64* goal_pos = nullptr, const u64* goal_neg = nullptr, u32* status = nullptr);
 
 /// Ascending true-atom slots of each row, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101).
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream);
@@ -68,6 +72,12 @@ void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out
 /// count = init_count, the count cache row = init_cache; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).
 void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
                       u32* cache, const u32* init_cache, u32 init_count, u32 init_goal, hipStream_t stream);
+
+/// Per-env goal masks at a reset of the rows with mask[i] != 0: the task's goal (task_pos / task_neg [W]) written into
+/// them, or with keep_goals the given masks kept, checked against the task's fluent slots (kStatusGoalMask) and
+/// at_goal tested on the initial state with them.
+void launch_env_reset_goals(const TaskDev& T, u64 rows, u32 words, const u8* mask, u64* goal_pos, u64* goal_neg, const u64* task_pos,
+                            const u64* task_neg, bool keep_goals, u8* at_goal, u32* status, hipStream_t stream);
 
 /// Words of a count-cache row: the per-schema counts, then the 64-bit state fingerprint.
 __host__ __device__ inline u32 cache_width(const TaskDev& T) { return T.num_schemas + 2; }

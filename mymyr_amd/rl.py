@@ -34,7 +34,7 @@ class DeviceEnvPool:
                  goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
                  witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda",
-                 count_cache: bool = True):
+                 count_cache: bool = True, goals: bool = False):
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
@@ -69,8 +69,12 @@ class DeviceEnvPool:
         # the count cache (the reference device env's EnvBatch::counts): per-schema successor counts of each row's
         # state plus its fingerprint, so a step counts only the reached states; zeros match no state
         self.counts_cache = (torch.zeros((N, task.num_schemas + 2), dtype=torch.int32, device=dev) if count_cache else None)
+        # per-env goal masks (goals=True, CpuEnvPool's `goals`): goal_pos / goal_neg [N, W], the task's goal after a reset
+        self.goal_pos = torch.zeros((N, W), dtype=torch.int64, device=dev) if goals else None
+        self.goal_neg = torch.zeros((N, W), dtype=torch.int64, device=dev) if goals else None
         self._batch = _lib.EnvBatch(self.states.data_ptr(), N, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
-                                    self.at_goal.data_ptr(), first_env, _p(self.counts_cache))
+                                    self.at_goal.data_ptr(), first_env, _p(self.counts_cache), _p(self.goal_pos),
+                                    _p(self.goal_neg))
 
     def initial_count(self) -> tuple[int, bool]:
         c = ctypes.c_uint32()
@@ -78,12 +82,18 @@ class DeviceEnvPool:
         check(lib.mya_env_initial_count(self._h, ctypes.byref(c), ctypes.byref(g)))
         return c.value, bool(g.value)
 
-    def reset(self, mask: torch.Tensor | None = None) -> dict:
-        """Resets every env (or those with mask != 0) to the initial state; draws are kept."""
+    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False) -> dict:
+        """Resets every env (or those with mask != 0) to the initial state; draws are kept. With per-env goals the task's
+        goal is written into goal_pos / goal_neg unless keep_goals (the masks written there stay, and at_goal is their
+        test on the initial state)."""
         if mask is not None:
             mask = mask.to(device=self.device, dtype=torch.uint8).contiguous()
-        check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), _stream()))
-        return {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
+        check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), int(keep_goals), _stream()))
+        r = {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
+        if self.goal_pos is not None:
+            r["goal_pos"] = self.goal_pos
+            r["goal_neg"] = self.goal_neg
+        return r
 
     def step(self, actions: torch.Tensor | None = None, final_states: bool = False, labels: bool = True,
              encode: int = 0) -> dict:

@@ -536,6 +536,12 @@ def expand(task: Task, rows, capacity: int | None = None, drop_noops: bool = Fal
     return out
 
 
+def mask_goal(row, gp, gn) -> bool:
+    """The per-env goal test over the words of the masks (mask_goal, src/mymyr/rl/env.cpp:55-61)."""
+    row, gp, gn = (np.asarray(x, np.uint64) for x in (row, gp, gn))
+    return bool(np.all((row & gp) == gp) and np.all((row & gn) == 0))
+
+
 def is_goal(task: Task, row) -> bool:
     """Successors::goal_holds over the compiled goal (successors.hpp:129-141)."""
     if task.goal_unsat:
@@ -559,13 +565,39 @@ class Env:
         self.init_count = len(successors(task, task.initial))
         self.init_goal = is_goal(task, task.initial)
 
-    def reset(self, n: int, words: int | None = None) -> dict:
-        """HostEnv::reset (env.cpp:207-240): every row to the initial state, steps 0, draws 0."""
+    def goal_masks(self, words: int):
+        """The task's goal as masks over `words` words (TaskTable::Instance::goal_pos / goal_neg)."""
+        gp, gn = np.zeros(words, np.uint64), np.zeros(words, np.uint64)
+        for s in self.t.goal_pos:
+            gp[s >> 6] |= np.uint64(1 << (s & 63))
+        for s in self.t.goal_neg:
+            gn[s >> 6] |= np.uint64(1 << (s & 63))
+        return gp, gn
+
+    def reset(self, n: int, words: int | None = None, goals: bool = False) -> dict:
+        """HostEnv::reset (env.cpp:223-255): every row to the initial state, steps 0, draws 0; with per-env goals the
+        task's goal masks in every row (reset_row, env.cpp:179-200)."""
         w = self.t.words if words is None else words
         states = np.zeros((n, w), dtype=np.uint64)
         states[:, : self.t.words] = self.t.initial
-        return {"states": states, "steps": np.zeros(n, np.int32), "draws": np.zeros(n, np.uint64),
-                "at_goal": np.full(n, 1 if self.init_goal else 0, np.uint8), "count": np.full(n, self.init_count, np.int32)}
+        b = {"states": states, "steps": np.zeros(n, np.int32), "draws": np.zeros(n, np.uint64),
+             "at_goal": np.full(n, 1 if self.init_goal else 0, np.uint8), "count": np.full(n, self.init_count, np.int32)}
+        if goals:
+            gp, gn = self.goal_masks(w)
+            b["goal_pos"] = np.tile(gp, (n, 1))
+            b["goal_neg"] = np.tile(gn, (n, 1))
+        return b
+
+    def keep_goals_reset(self, b: dict) -> None:
+        """reset(keep_goals=True) of every row: the initial state, the given masks kept, at_goal their test on it."""
+        n = b["states"].shape[0]
+        W = self.t.words
+        b["states"][:] = 0
+        b["states"][:, :W] = self.t.initial
+        b["steps"][:] = 0
+        b["count"][:] = self.init_count
+        for i in range(n):
+            b["at_goal"][i] = 1 if mask_goal(self.t.initial, b["goal_pos"][i, :W], b["goal_neg"][i, :W]) else 0
 
     def step(self, b: dict, first_env: int = 0, actions=None) -> dict:
         n = b["states"].shape[0]
@@ -601,7 +633,7 @@ class Env:
             g = already
             c2 = c
             if st == "ok":
-                g = is_goal(self.t, s2)
+                g = (mask_goal(s2, b["goal_pos"][i, :W], b["goal_neg"][i, :W]) if "goal_pos" in b else is_goal(self.t, s2))
                 c2 = len(successors(self.t, s2))
             dead = self.dead_end == "no_successors" and not g and ((st == "ok" and c2 == 0) or st == "stuck")
             term = g or (dead and self.dead_end_terminal)
@@ -623,6 +655,9 @@ class Env:
                 b["states"][i, :W] = self.t.initial
                 b["steps"][i] = 0
                 b["at_goal"][i] = 1 if self.init_goal else 0
+                if "goal_pos" in b:  # an autoreset writes the task's goal (reset_row with keep_goals off)
+                    gp, gn = self.goal_masks(b["goal_pos"].shape[1])
+                    b["goal_pos"][i], b["goal_neg"][i] = gp, gn
                 out["count"][i] = self.init_count
                 continue
             b["at_goal"][i] = 1 if g else 0

@@ -213,3 +213,92 @@ def test_step_replayed_from_a_hip_graph(golden):
             assert torch.equal(oa[key], ob[key]), f"replay {k}: {key} differs"
     a.check()
     b.check()
+
+
+def test_per_env_goals_default_to_the_task_goal(golden):
+    """With per-env goal masks holding the task's goal (what reset writes), trajectories equal the reference's."""
+    pool, t = run_env(golden, "env_gridworld_truncated.json", goals=True)
+    from oracle import port
+
+    pt = port.Task(open(golden.task_path("gridworld")).read())
+    gp, gn = port.Env(pt).goal_masks(t.words)
+    assert np.array_equal(host(pool.goal_pos).view(np.uint64), np.tile(gp, (pool.num_envs, 1)))
+    assert not host(pool.goal_neg).any()
+
+
+def _single(pt, slot):
+    row = np.zeros(pt.words, np.uint64)
+    row[slot >> 6] = np.uint64(1) << np.uint64(slot & 63)
+    return row
+
+
+def test_per_env_goals_against_the_oracle(golden):
+    """Each env gets its own goal cell (mask_goal over per-env masks, kept by reset(keep_goals=True)); the steps,
+    rewards, terminations, goal flags, autoresets (which write the task's goal back) and masks follow the oracle."""
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+    from oracle import port
+
+    text = open(golden.task_path("gridworld")).read()
+    t, pt = Task.from_text(text), port.Task(text)
+    n, steps = 96, 24
+    cfg = dict(seed=11, step_reward=-0.5, goal_reward=2.0, max_steps=40)
+    pool = rl.DeviceEnvPool(t, n, goals=True, **cfg)
+    env = port.Env(pt, **cfg)
+    b = env.reset(n, goals=True)
+    pool.reset()
+    rng = np.random.default_rng(3)
+    # goals: at(c) for cells near the start (reachable in a few steps), one per env
+    def bits(row):
+        return {w * 64 + k for w in range(len(row)) for k in range(64) if (int(row[w]) >> k) & 1}
+
+    near = set(bits(pt.initial))
+    for _ in range(2):
+        near |= {s for sl in list(near) for r in port.successors(pt, _single(pt, sl)) for s in bits(r[2])}
+    cand = sorted(near)
+    gp = np.zeros((n, t.words), np.uint64)
+    for i in range(n):
+        sl = cand[rng.integers(len(cand))]
+        gp[i, sl >> 6] = np.uint64(1) << np.uint64(sl & 63)
+    b["goal_pos"][:] = gp
+    b["goal_neg"][:] = 0
+    env.keep_goals_reset(b)
+    pool.goal_pos.copy_(torch.from_numpy(gp.view(np.int64)))
+    pool.goal_neg.zero_()
+    pool.reset(keep_goals=True)
+    assert np.array_equal(host(pool.at_goal), b["at_goal"])
+    hits = int(b["at_goal"].sum())
+    for k in range(steps):
+        o = pool.step()
+        e = env.step(b)
+        hits += int(e["goal"].sum())
+        for key in ("reward", "terminated", "truncated", "count", "goal"):
+            assert np.array_equal(host(o[key]), e[key]), f"step {k}: {key}"
+        assert np.array_equal(host(o["states"]).view(np.uint64), b["states"]), f"step {k}: states"
+        assert np.array_equal(host(pool.at_goal), b["at_goal"]), f"step {k}: at_goal"
+        assert np.array_equal(host(pool.goal_pos).view(np.uint64), b["goal_pos"]), f"step {k}: goal masks"
+    assert hits > 0  # the per-env goals are reached (55 times in this setup)
+    pool.check()
+
+
+def test_goal_masks_past_the_slots_and_refresh(golden):
+    from mymyr_amd import rl
+    from mymyr_amd._lib import MyaError
+    from mymyr_amd.task import Task
+    from oracle import port
+
+    text = open(golden.task_path("gridworld")).read()
+    t, pt = Task.from_text(text), port.Task(text)
+    pool = rl.DeviceEnvPool(t, 8, goals=True)
+    pool.reset()
+    if pt.slots % 64:
+        pool.goal_pos[3, t.words - 1] = -1  # bits past the last fluent slot
+        pool.reset(keep_goals=True)
+        with pytest.raises(MyaError, match="goal masks set fluent slots"):
+            pool.check()
+    # refresh tests the current states against the masks written since
+    pool.reset()
+    pool.goal_pos.copy_(pool.states)  # every env's goal: its own current state
+    pool.refresh()
+    assert host(pool.at_goal).all()
+    pool.check()
