@@ -377,6 +377,17 @@ __global__ void k_chunk_end(const u64* __restrict__ offsets, u32 stride, u64 p0,
     out[1] = offsets[p * stride];
 }
 
+// The driver's scalars that a synchronization reads, gathered in one launch: the set's current size and status, and
+// (optional) a counted block's offset total.
+__global__ void k_gather_small(u64* __restrict__ small, int size_at, const u64* __restrict__ size_now, int status_at,
+                               const u32* __restrict__ status, int total_at, const u64* __restrict__ total)
+{
+    small[size_at] = *size_now;
+    small[status_at] = *status;
+    if (total)
+        small[total_at] = *total;
+}
+
 __global__ void k_sum_u8(const u8* __restrict__ v, u64 n, u64* __restrict__ out)
 {
     u64 s = 0;
@@ -596,19 +607,12 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     u8* goal_flags = nullptr;
     u64* offsets = nullptr;
     u64* scan_scratch = nullptr;
-    u64 layer_cap = 0;
-    auto ensure_layer = [&](u64 ln) {
-        if (ln <= layer_cap)
-            return;
-        hip_check(hipStreamSynchronize(stream), "sync");
-        for (void* q : {static_cast<void*>(counts), static_cast<void*>(goal_flags), static_cast<void*>(offsets), static_cast<void*>(scan_scratch)})
-            dev_free(q);
-        layer_cap = std::max<u64>(ln, std::min<u64>(cap_states, layer_cap * 2));
-        counts = dev_alloc<u32>(layer_cap * S, "layer counts");
-        goal_flags = dev_alloc<u8>(layer_cap, "layer goal flags");
-        offsets = dev_alloc<u64>(layer_cap * S + 1, "layer offsets");
-        scan_scratch = dev_alloc<u64>(scan_scratch_words(layer_cap * S), "scan scratch");
-    };
+    // sized once for the largest layer (no layer outgrows the store), so that no layer start waits for reallocation
+    const u64 layer_cap = cap_states;
+    counts = dev_alloc<u32>(layer_cap * S, "layer counts");
+    goal_flags = dev_alloc<u8>(layer_cap, "layer goal flags");
+    offsets = dev_alloc<u64>(layer_cap * S + 1, "layer offsets");
+    scan_scratch = dev_alloc<u64>(scan_scratch_words(layer_cap * S), "scan scratch");
     struct LayerGuard
     {
         u32*& c;
@@ -634,6 +638,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         kChunkOff = 3,
         kSizeNow = 4,   // the set's size before the chunk's insert, then after it
         kSizeNext = 8,
+        kChunkGoal = 10,  // goal states among a chunk's parents (read at the synchronization that confirms the chunk)
         kSpare = 9,     // the capacity status of a cut chunk's compaction (expected there, not an error)
         kCut = 5,       // the candidate of the state that fills the store
         kBlockTotal = 6,
@@ -685,11 +690,10 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
         // budget are neither tested nor expanded
         const u64 budget = o.max_expanded == ~u64{0} ? ~u64{0} : o.max_expanded - r.expanded;
         u64 lim = std::min(ln, budget);
-        ensure_layer(ln);
         u64 counted = 0, counted_total = 0;  // parents [0, counted) counted; offsets[counted * S] on the host
         u64 first_goal = ~u64{0};
         bool goal_stop = false;
-        set_small(kGoalSum, 0);
+        u64 layer_goals = 0;   // goal states among the layer's expanded parents (confirmed chunks)
         u64 p0 = 0, base = 0;  // base = offsets[p0 * S]
         constexpr int G = kGroup<W>;
         // The chunk whose kernels are queued but whose outcome (its winners) the host has not read yet: it is confirmed
@@ -727,8 +731,11 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 const u64 pc = b.host[kCut] >> 32;  // the parent, relative to the chunk's first
                 row[0] += pc + 1;
                 row[1] += u64{jc} + 1;
+                set_small(kGoalSum, 0);
                 hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pc + 1, 256), 1024)), dim3(256), 0, stream, goal_flags + pend.p0,
                                    pc + 1, small + kGoalSum);
+                sync_small();
+                layer_goals += b.host[kGoalSum];
                 set.size = o.max_states;
                 r.status = kOutOfStates;
                 stopped = true;
@@ -741,13 +748,13 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             set.size = size_dev;
             row[0] += pend.np;
             row[1] += pend.m;
-            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pend.np, 256), 1024)), dim3(256), 0, stream, goal_flags + pend.p0,
-                               pend.np, small + kGoalSum);
+            layer_goals += b.host[kChunkGoal];
             return false;
         };
-        auto read_state = [&] {
-            hip_check(hipMemcpyAsync(small + kSizeNow, state_set_size_now(set), sizeof(u64), hipMemcpyDeviceToDevice, stream), "size");
-            hip_check(hipMemcpyAsync(small + kCut, set.d_status, sizeof(u32), hipMemcpyDeviceToDevice, stream), "status");
+        auto read_state = [&](const u64* block_total = nullptr) {
+            hipLaunchKernelGGL(k_gather_small, dim3(1), dim3(1), 0, stream, small, int{kSizeNow}, state_set_size_now(set), int{kCut},
+                               set.d_status, int{kBlockTotal}, block_total);
+            launch_check("gather");
         };
         while (p0 < lim && !stopped)
         {
@@ -769,14 +776,13 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 set_small(kFirstGoal, ~u64{0});
                 hipLaunchKernelGGL(k_first_u8, dim3(std::min<u64>(blocks_for(nb, 256), 4096)), dim3(256), 0, stream, goal_flags + counted, nb,
                                    small + kFirstGoal);
-                hip_check(hipMemcpyAsync(small + kBlockTotal, offsets + (counted + nb) * S, sizeof(u64), hipMemcpyDeviceToDevice, stream), "total");
                 launch_check("count scan");
                 tm.end(kKOther, 0);
             }
             // the chunk end over what is counted, and the pending chunk's outcome, in one synchronization
             hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, std::min(counted + nb, lim), base + chunk, small + kChunkP);
             launch_check("chunk end");
-            read_state();
+            read_state(count_now ? offsets + (counted + nb) * S : nullptr);
             sync_small();
             if (count_now)
             {
@@ -841,9 +847,15 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
                 tm.end(kKCompact, 0);
                 state_set_flip(set);
             }
+            // the chunk's goal states, read at the synchronization that confirms it
+            set_small(kChunkGoal, 0);
+            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(np, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, u64{np},
+                               small + kChunkGoal);
             pend = Pending{true, p0, np, m};
             p0 = p1;
             base = end_off;
+            if (p0 >= lim)
+                break;  // the layer's last chunk: its confirmation is the layer's last synchronization
         }
         if (!stopped && pend.live)
         {
@@ -851,8 +863,7 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
             sync_small();
             confirm(b.host[kSizeNow], static_cast<u32>(b.host[kCut]));
         }
-        sync_small();
-        r.goal_states += b.host[kGoalSum];
+        r.goal_states += layer_goals;
         pos = layer_begin + row[0];
         r.expanded += row[0];
         r.generated += row[1];
