@@ -551,9 +551,64 @@ void build_action_tables(const GroundActions& ga, std::vector<u64>& fast, std::v
     }
 }
 
-template<int W>
-BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc)
+}  // namespace
+
+struct BrfsTables
 {
+    int device = -1;
+    u32 W = 0;
+    GroundActions ga;
+    GroundDev g{};
+    GoalDev goal{};
+    const u64* masks = nullptr;
+    const u64* slot_cid = nullptr;
+    std::vector<void*> owned;
+
+    template<class T>
+    const T* upload(const std::vector<T>& v)
+    {
+        if (v.empty())
+            return nullptr;
+        T* d = dev_alloc<T>(v.size(), "brfs tables");
+        owned.push_back(d);
+        hip_check(hipMemcpy(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "brfs tables");
+        return d;
+    }
+    ~BrfsTables()
+    {
+        for (void* p : owned)
+            dev_free(p);
+    }
+};
+
+BrfsCache::BrfsCache() = default;
+BrfsCache::~BrfsCache() = default;
+
+namespace
+{
+template<int W>
+std::unique_ptr<BrfsTables> build_tables(const CompiledTask& task, bool witness, int device)
+{
+    auto tb = std::make_unique<BrfsTables>();
+    tb->device = device;
+    tb->W = W;
+    tb->ga = ground_actions(task, witness, u64{1} << 24);
+    const GroundActions& ga = tb->ga;
+    std::vector<u64> fast, masks;
+    build_action_tables<W>(ga, fast, masks);
+    tb->g = GroundDev{tb->upload(fast), tb->upload(ga.meta), tb->upload(ga.off), tb->upload(ga.slots), tb->upload(ga.dom_off),
+                      tb->upload(ga.dom), ga.size(), static_cast<u32>(fast.size())};
+    tb->masks = tb->upload(masks);
+    tb->goal = GoalDev{tb->upload(task.goal_pos), tb->upload(task.goal_neg), static_cast<u32>(task.goal_pos.size()),
+                       static_cast<u32>(task.goal_neg.size()), task.goal_unsat ? 1u : 0u};
+    tb->slot_cid = task.mode == AtomMode::Dense ? nullptr : tb->upload(task.slot_cid);
+    return tb;
+}
+
+template<int W>
+BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc)
+{
+    const GroundActions& ga = tb.ga;
     BrfsResultC r;
     const auto t0 = Clock::now();
     hipStream_t stream = nullptr;
@@ -567,25 +622,12 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
     constexpr u64 R = W * 8;  // row bytes
     Buffers b;
 
-    // ground tables and goal
-    std::vector<u64> fast, masks;
-    build_action_tables<W>(ga, fast, masks);
-    auto upload = [&](const auto& v, const char* what) {
-        using T = std::decay_t<decltype(v[0])>;
-        if (v.empty())
-            return static_cast<T*>(nullptr);
-        T* d = b.alloc<T>(v.size(), what);
-        hip_check(hipMemcpyAsync(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice, stream), what);
-        return d;
-    };
+    // ground tables and goal (device copies kept with the task)
     constexpr u32 S = 1;  // one count and one offset per parent
-    const GroundDev g{upload(fast, "action records"), upload(ga.meta, "ground meta"), upload(ga.off, "ground offsets"),
-                      upload(ga.slots, "ground slots"), upload(ga.dom_off, "ground dominators"), upload(ga.dom, "ground dominators"),
-                      ga.size(), static_cast<u32>(fast.size())};
-    const u64* d_masks = upload(masks, "action masks");
-    const GoalDev goal{upload(task.goal_pos, "goal"), upload(task.goal_neg, "goal"), static_cast<u32>(task.goal_pos.size()),
-                       static_cast<u32>(task.goal_neg.size()), task.goal_unsat ? 1u : 0u};
-    const u64* d_slot_cid = task.mode == AtomMode::Dense ? nullptr : upload(task.slot_cid, "slot cids");
+    const GroundDev& g = tb.g;
+    const u64* d_masks = tb.masks;
+    const GoalDev& goal = tb.goal;
+    const u64* d_slot_cid = tb.slot_cid;
 
     // capacity: the arena holds every stored state
     const bool bounded = o.max_states != ~u64{0};
@@ -914,20 +956,52 @@ BrfsResultC run(const CompiledTask& task, const GroundActions& ga, const BrfsOpt
 }
 }  // namespace
 
-BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts)
+namespace
 {
-    const GroundActions ga = ground_actions(task, o.witness_pruning != 0, u64{1} << 24);
+template<int W>
+BrfsResultC run_cached(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc, BrfsCache* cache)
+{
+    int device = 0;
+    hip_check(hipGetDevice(&device), "hipGetDevice");
+    const bool witness = o.witness_pruning != 0;
+    if (!cache)
+    {
+        const auto tb = build_tables<W>(task, witness, device);
+        return run<W>(task, *tb, o, lc);
+    }
+    const BrfsTables* tb = nullptr;
+    std::unique_ptr<BrfsTables> local;
+    {
+        std::lock_guard lock(cache->mutex);
+        std::unique_ptr<BrfsTables>& slot = cache->tables[witness ? 1 : 0];
+        if (!slot)
+            slot = build_tables<W>(task, witness, device);
+        if (slot->device == device && slot->W == W)
+            tb = slot.get();
+    }
+    if (!tb)
+    {
+        // another device than the cached tables': tables of its own for this search
+        local = build_tables<W>(task, witness, device);
+        tb = local.get();
+    }
+    return run<W>(task, *tb, o, lc);
+}
+}  // namespace
+
+BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts, BrfsCache* cache)
+{
     const u32 W = task.words;
     if (W <= 1)
-        return run<1>(task, ga, o, layer_counts);
+        return run_cached<1>(task, o, layer_counts, cache);
     if (W <= 2)
-        return run<2>(task, ga, o, layer_counts);
+        return run_cached<2>(task, o, layer_counts, cache);
     if (W <= 4)
-        return run<4>(task, ga, o, layer_counts);
+        return run_cached<4>(task, o, layer_counts, cache);
     if (W <= 8)
-        return run<8>(task, ga, o, layer_counts);
+        return run_cached<8>(task, o, layer_counts, cache);
     if (W <= 16)
-        return run<16>(task, ga, o, layer_counts);
+        return run_cached<16>(task, o, layer_counts, cache);
     throw std::invalid_argument("mymyr_amd: brfs: states of " + std::to_string(W) + " words (the device BrFS takes at most 16)");
 }
 }  // namespace mya

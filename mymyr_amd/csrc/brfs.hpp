@@ -10,6 +10,8 @@
 #include <hip/hip_runtime.h>
 
 #include <array>
+#include <memory>
+#include <mutex>
 #include <vector>
 
 namespace mya
@@ -67,5 +69,18 @@ enum SearchStatus : i32
 };
 
 /// Runs the BrFS on the current device; fills layer_counts with {expanded, generated, new} per expanded layer.
-BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts);
+/// The device tables of a task's ground actions (grounding, witness dominators, fast precondition records, effect
+/// masks, goal and slot tables), built on the first search per witness-pruning setting and device and kept with the
+/// task: repeated searches skip grounding and uploads. Built under the mutex; read-only afterwards.
+struct BrfsTables;
+struct BrfsCache
+{
+    std::mutex mutex;
+    std::unique_ptr<BrfsTables> tables[2];
+    BrfsCache();
+    ~BrfsCache();
+};
+
+BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts,
+                        BrfsCache* cache = nullptr);
 }  // namespace mya

@@ -1,6 +1,7 @@
 #pragma once
 // Internals shared by the C-ABI translation units: the opaque handle types and the exception guard.
 
+#include "brfs.hpp"
 #include "state_set.hpp"
 #include "task.hpp"
 
@@ -52,6 +53,7 @@ struct mya_task
     std::unique_ptr<mya::CompiledTask> compiled;
     mya::DeviceTask dev;
     std::mutex mutex;
+    mya::BrfsCache brfs;  // the BrFS's device tables of the task's ground actions
 };
 
 namespace mya
