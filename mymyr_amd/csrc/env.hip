@@ -1122,8 +1122,23 @@ unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
         throw std::invalid_argument("mymyr_amd: env: the device step keeps the successor counts of at most " + std::to_string(kMaxEnvSchemas) +
                                     " schemas (the task has " + std::to_string(T.num_schemas) + ")");
     const size_t hot = staged(T) ? static_cast<size_t>(T.hot_words) * 8 : 0, wave = static_cast<size_t>(wave_lds_words(T, levels(T))) * 8;
-    int nw = static_cast<int>((64 * 1024 - std::min<size_t>(hot, 64 * 1024)) / wave);
-    nw = std::clamp(nw, 1, kMaxWaves);
+    // the waves per block that keep the most waves resident on a CU (its 160 KiB of LDS shared by whole blocks); a
+    // smaller block is taken only for at least 1/8 more resident waves (a larger one stages the hot tables fewer times)
+    constexpr size_t kCuLds = 160 * 1024;
+    constexpr int kCuWaves = 24;  // waves per CU the kernels' register use allows
+    int nw = 1, best = 0;
+    for (int k = kMaxWaves; k >= 1; --k)
+    {
+        const size_t block = hot + static_cast<size_t>(k) * wave;
+        if (block > kCuLds)
+            continue;
+        const int resident = std::min(kCuWaves, k * static_cast<int>(kCuLds / block));
+        if (8 * resident > 9 * best)
+        {
+            best = resident;
+            nw = k;
+        }
+    }
     *lds_bytes = hot + static_cast<size_t>(nw) * wave;
     if (*lds_bytes > 160 * 1024)
         throw std::invalid_argument("mymyr_amd: env: the task's per-state LDS (" + std::to_string(*lds_bytes) +
