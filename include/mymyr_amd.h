@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 6
+#define MYA_ABI_VERSION 7
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -159,6 +159,12 @@ typedef struct mya_env_batch
      * src/mymyr/rl/env.cpp:55-61). reset writes the task's goal into them unless keep_goals; an autoreset writes it. */
     uint64_t* goal_pos;
     uint64_t* goal_neg;
+    /* Each row's instance (EnvBatch::task_ids, include/mymyr/rl/env.hpp:102), device int32 [rows], optional: null puts
+     * every row in instance 0 (required over several instances). reset puts a row in the instance its entry names; an
+     * autoreset writes the instance the row restarts in. A row's words past its instance's are padding: a step
+     * neither reads nor writes them, and a reset zeroes the words it may have dirtied (TaskSuite::initial_row,
+     * src/mymyr/rl/task_suite.cpp:130-138). */
+    int32_t* task_ids;
 } mya_env_batch;
 
 /* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
@@ -186,26 +192,42 @@ typedef struct mya_step_outputs
 } mya_step_outputs;
 
 /* A device environment over one task (replaces cuda::DeviceEnv, include/mymyr/cuda/env.hpp:89, and
- * rl::HostEnv, include/mymyr/rl/env.hpp:181). Uploads the task and counts the initial state's successors. */
+ * rl::HostEnv, include/mymyr/rl/env.hpp:181). Uploads the task and counts the initial state's successors. The same
+ * as mya_env_create_table over a table of one instance. */
 int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out);
+/* A device environment over a task table: `count` instances of one domain (TaskTable::create,
+ * include/mymyr/rl/task_table.hpp:69-75), at most 65,536. Fails with the reference's message ("mymyr: TaskTable:
+ * instance i is not of the domain of instance 0: ...", src/mymyr/rl/task_table.cpp:75-100) unless every instance has
+ * instance 0's action schemas (names, arities) and predicates (names, arities, kinds) in the same order. A batch's rows
+ * are at least the widest instance's words; the label width is the largest schema arity. The env keeps the tasks'
+ * device images alive by reference: free the env before the tasks. */
+int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out);
 void mya_env_free(mya_env* env);
-/* Initial state's successor count and goal flag. */
-int mya_env_initial_count(const mya_env* env, uint32_t* count, uint8_t* goal);
-/* HostEnv::reset (env.cpp:223-255): rows with mask[i] != 0 (device, optional) to the initial state, steps 0,
- * at_goal and count (device, optional) of the initial state; draws kept. With per-env goal masks, the task's goal is
- * written into them unless keep_goals, in which case the given masks stay, at_goal is their test on the initial state,
- * and masks that set fluent slots the task does not have set the sticky status (mya_env_check). Async on the stream. */
+/* The initial state's successor count and goal flag of an instance (DeviceEnv::initial_count,
+ * include/mymyr/cuda/env.hpp:161-162). */
+int mya_env_initial_count(const mya_env* env, uint32_t instance, uint32_t* count, uint8_t* goal);
+/* HostEnv::reset (env.cpp:179-205, 223-255): rows with mask[i] != 0 (device, optional) to the initial state of their
+ * instance (batch->task_ids; an id outside the table resets the row into instance 0, writes 0 there and sets the sticky
+ * status, as DeviceEnv::reset, include/mymyr/cuda/env.hpp:163-168), steps 0, at_goal and count (device, optional) of
+ * that initial state; draws kept. With per-env goal masks, the instance's goal is written into them unless keep_goals,
+ * in which case the given masks stay, at_goal is their test on the initial state, and masks that set fluent slots the
+ * instance does not have set the sticky status (mya_env_check). Async on the stream. */
 int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals,
                   void* stream);
 /* HostEnv::step (env.cpp:530-548 / step_row_impl 351-528): actions (device, int64 [rows], optional: the random policy
- * when null). Async on the stream; device-side failures set the sticky status that mya_env_check reports. */
+ * when null); next_task_ids (device, int32 [rows], optional: the instance an autoresetting row restarts in; null: its
+ * own). Async on the stream; device-side failures set the sticky status that mya_env_check reports: among them a
+ * task id outside the table in batch->task_ids (the row is not stepped) or in next_task_ids (an autoresetting row
+ * keeps its instance; DeviceEnv::step, include/mymyr/cuda/env.hpp:180-184). Over several instances the rows are
+ * grouped by instance on the device first (a counting sort of task_ids into env-owned scratch, allocated on the
+ * first call with a larger batch). */
 int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
-                 void* stream);
+                 const int32_t* next_task_ids, void* stream);
 /* Reads and clears the sticky device status (synchronizes the env's status copy); -1 with a message if a step failed. */
 int mya_env_check(mya_env* env);
-/* Recomputes at_goal and the count cache (when the batch has one) of every row from its state, after the caller wrote
- * states directly (DeviceEnv::refresh, include/mymyr/cuda/env.hpp:170-174); count (device, optional) receives the
- * successor counts. Async on the stream. */
+/* Recomputes at_goal and the count cache (when the batch has one) of every row from its state and instance, after the
+ * caller wrote states, task ids or goal masks directly (DeviceEnv::refresh, include/mymyr/cuda/env.hpp:170-174);
+ * count (device, optional) receives the successor counts. Async on the stream. */
 int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, void* stream);
 
 /* The true-atom slots of rows, ascending, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101);
@@ -214,7 +236,7 @@ int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, vo
 int mya_encode_atoms(mya_env* env, const uint64_t* states, uint64_t rows, uint32_t words, int32_t* out, uint32_t max_atoms,
                      void* stream);
 /* Per row and schema, whether some binding is applicable (rl::schema_masks, include/mymyr/rl/masks.hpp:9-11);
- * masks [rows, num_schemas] uint8, device. Async on the stream. */
+ * masks [rows, num_schemas] uint8, device; the rows are states of instance 0. Async on the stream. */
 int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32_t words, uint8_t* masks, void* stream);
 
 /* Successors of rows in canonical order, witness pruning off (Successors::generate, successors.hpp:154-248):

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 6  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 7  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -65,6 +65,7 @@ class EnvBatch(Structure):
         ("counts", c_void_p),
         ("goal_pos", c_void_p),
         ("goal_neg", c_void_p),
+        ("task_ids", c_void_p),
     ]
 
 
@@ -200,12 +201,13 @@ def _load() -> ctypes.CDLL:
     }
     optional = {
         "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),
+        "mya_env_create_table": (c_int, [c_void_p, c_uint32, POINTER(EnvConfig), POINTER(c_void_p)]),
         "mya_env_free": (None, [c_void_p]),
         "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_void_p]),
-        "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p]),
+        "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p, c_void_p]),
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_refresh": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),
-        "mya_env_initial_count": (c_int, [c_void_p, POINTER(c_uint32), POINTER(c_uint8)]),
+        "mya_env_initial_count": (c_int, [c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_uint8)]),
         "mya_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
         "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p]),
         "mya_schema_masks": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),

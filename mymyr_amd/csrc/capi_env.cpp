@@ -10,22 +10,56 @@
 #include "state_set.hpp"
 
 #include <cstring>
+#include <initializer_list>
+#include <mutex>
+#include <string>
 #include <vector>
 
 using namespace mya;
 
-struct mya_env
+/// One instance of an env's table: its task, tables and initial-state facts (host copies).
+struct EnvInstance
 {
     mya_task* task = nullptr;
-    TaskDev T{};                // host copy of the pointer table
-    EnvCfg cfg{};
+    TaskDev T{};
     u32 init_count = 0;
     u32 init_goal = 0;
-    u8* init_masks = nullptr;  // device [num_schemas]
-    u32* init_cache = nullptr; // device [num_schemas + 2]: the initial state's count-cache row
-    u64* goal_masks = nullptr; // device [2, W]: the task's goal as masks (positive, then negative)
+    u32 variant = 0;
+};
+
+struct mya_env
+{
+    std::vector<EnvInstance> inst;
+    EnvCfg cfg{};
+    u32 words = 1;        // the widest instance's words
+    u32 label_width = 0;  // the largest schema arity
+    u32 num_schemas = 0;
+    InstDev* d_inst = nullptr;    // device [instances]
+    TaskDev* d_tasks = nullptr;   // device [instances]
+    u64* d_init = nullptr;        // device: per instance its goal masks (positive, then negative) over its words
+    u32* d_init_cache = nullptr;  // device [instances, num_schemas + 2]: the initial states' count-cache rows
+    u8* d_init_masks = nullptr;   // device [instances, num_schemas]
     u32* d_status = nullptr;
     u32* h_status = nullptr;
+    // grouped launches: per variant present, its block shape
+    struct Launch
+    {
+        u32 variant;
+        unsigned nw;
+        size_t lds;
+        u32 wave_words;
+    };
+    std::vector<Launch> launches;
+    // the row groups of the last grouped call (device scratch, grown to the largest batch)
+    u64 group_rows = 0;
+    u32* d_hist = nullptr;   // [instances + 1]
+    u32* d_starts = nullptr;  // [instances + 1]
+    u32* d_chunks = nullptr;  // [instances + 1]
+    u32* d_order = nullptr;   // [group_rows]
+    std::mutex mutex;         // guards the scratch growth
+
+    [[nodiscard]] u32 instances() const { return static_cast<u32>(inst.size()); }
+    [[nodiscard]] const TaskDev& T0() const { return inst[0].T; }
 };
 
 namespace
@@ -38,32 +72,104 @@ void check_batch(const mya_env* e, const mya_env_batch* b)
         throw std::invalid_argument("mymyr: env: null state array");
     if (b->rows > 0x7FFFFFFFull)
         throw std::invalid_argument("mymyr: env: more than 2^31 - 1 environments in one batch");
-    if (b->words < e->T.W)
-        throw std::invalid_argument("mymyr: env: state rows of " + std::to_string(b->words) + " words; the task needs " +
-                                    std::to_string(e->T.W) + " (its widest instance's words)");
+    if (b->words < e->words)
+        throw std::invalid_argument("mymyr: env: state rows of " + std::to_string(b->words) + " words; the " +
+                                    (e->instances() > 1 ? "table" : "task") + " needs " + std::to_string(e->words) +
+                                    " (its widest instance's words)");
     if ((b->goal_pos == nullptr) != (b->goal_neg == nullptr))
         throw std::invalid_argument("mymyr: env: per-env goals need both goal_pos and goal_neg");
-    if (b->goal_pos && e->T.goal_unsat)
-        throw std::invalid_argument("mymyr: env: per-env goal masks cannot express the goal of instance 0 (it is statically "
-                                    "unsatisfiable); use the instances' goal tests (no goal masks)");
+    if (b->goal_pos)
+        for (u32 i = 0; i < e->instances(); ++i)
+            if (e->inst[i].T.goal_unsat)
+                throw std::invalid_argument("mymyr: env: per-env goal masks cannot express the goal of instance " + std::to_string(i) +
+                                            " (it is statically unsatisfiable); use the instances' goal tests (no goal masks)");
+    if (!b->task_ids && b->rows && e->instances() > 1)
+        throw std::invalid_argument("mymyr: env: a batch over a table of " + std::to_string(e->instances()) +
+                                    " instances needs task ids");
+}
+
+/// Whether a call runs grouped by instance: over several instances (a one-instance batch runs in batch order, checking
+/// its task ids on the way).
+bool grouped(const mya_env* e) { return e->instances() > 1; }
+
+/// Groups the batch's rows by instance into the env's scratch (grown under the env's lock; a call with a batch no
+/// larger than before allocates nothing).
+RowGroups group_rows(mya_env* e, const mya_env_batch* b, hipStream_t stream)
+{
+    {
+        std::lock_guard lock(e->mutex);
+        if (b->rows > e->group_rows)
+        {
+            dev_free(e->d_order);
+            e->d_order = nullptr;
+            e->group_rows = 0;
+            e->d_order = dev_alloc<u32>(b->rows, "env row groups");
+            e->group_rows = b->rows;
+        }
+    }
+    launch_group_rows(b->task_ids, b->rows, e->instances(), e->d_hist, e->d_order, e->d_starts, e->d_chunks, e->d_status, stream);
+    return RowGroups{e->d_order, e->d_starts, e->d_chunks};
+}
+
+/// The table's domain check (TaskTable::domain_mismatch, src/mymyr/rl/task_table.cpp:75-100): empty if `t` has the
+/// action schemas (names, arities) and predicates (names, arities, kinds) of `r` in the same order.
+std::string domain_mismatch(const TaskText& r, const TaskText& t)
+{
+    if (t.schemas.size() != r.schemas.size())
+        return std::to_string(t.schemas.size()) + " action schemas, instance 0 has " + std::to_string(r.schemas.size());
+    for (size_t s = 0; s < t.schemas.size(); ++s)
+        if (t.schemas[s].name != r.schemas[s].name || t.schemas[s].arity != r.schemas[s].arity)
+            return "action schema " + std::to_string(s) + " is " + t.schemas[s].name + "/" + std::to_string(t.schemas[s].arity) +
+                   ", instance 0 has " + r.schemas[s].name + "/" + std::to_string(r.schemas[s].arity);
+    auto kind = [](char k) { return std::string(k == 'S' ? "static" : k == 'F' ? "fluent" : "derived"); };
+    for (size_t d = 0; d < t.preds.size(); ++d)
+        if (d >= r.preds.size() || r.preds[d].name != t.preds[d].name || r.preds[d].arity != t.preds[d].arity ||
+            r.preds[d].kind != t.preds[d].kind)
+            return "domain predicate " + std::to_string(d) + " is " + t.preds[d].name + "/" + std::to_string(t.preds[d].arity) + " (" +
+                   kind(t.preds[d].kind) + "), instance 0 has " +
+                   (d < r.preds.size() ? r.preds[d].name + "/" + std::to_string(r.preds[d].arity) + " (" + kind(r.preds[d].kind) + ")"
+                                       : std::string("no more"));
+    if (t.preds.size() != r.preds.size())
+        return std::to_string(t.preds.size()) + " domain predicates, instance 0 has " + std::to_string(r.preds.size());
+    return {};
+}
+
+void free_env(mya_env* e)
+{
+    for (void* p : std::initializer_list<void*>{e->d_status, e->d_inst, e->d_tasks, e->d_init, e->d_init_cache, e->d_init_masks, e->d_hist,
+                                                e->d_starts, e->d_chunks, e->d_order})
+        dev_free(p);
+    if (e->h_status)
+        (void)hipHostFree(e->h_status);
+    delete e;
 }
 }  // namespace
 
 extern "C" {
 
-int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
+int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out)
 {
     return guarded([&] {
-        if (!task || !config || !out)
+        if (!tasks || !config || !out)
             throw std::invalid_argument("mymyr_amd: env_create: null argument");
+        if (count == 0)
+            throw std::invalid_argument("mymyr: TaskTable: no instances");
+        if (count > kMaxInstances)
+            throw std::invalid_argument("mymyr_amd: env: the device env takes at most " + std::to_string(kMaxInstances) + " instances");
+        for (u32 i = 0; i < count; ++i)
+            if (!tasks[i])
+                throw std::invalid_argument("mymyr: TaskTable: instance " + std::to_string(i) + " is null");
+        for (u32 i = 1; i < count; ++i)
+        {
+            const std::string why = domain_mismatch(tasks[0]->compiled->text, tasks[i]->compiled->text);
+            if (!why.empty())
+                throw std::invalid_argument("mymyr: TaskTable: instance " + std::to_string(i) + " is not of the domain of instance 0: " + why);
+        }
         if (!config->canonical_order || config->witness_pruning)
             throw std::invalid_argument("mymyr_amd: env: the device step takes canonical_order on and witness_pruning off");
         if (config->dead_end != 0 && config->dead_end != 1)
             throw std::invalid_argument("mymyr_amd: env: dead_end must be 0 (no_successors) or 1 (none)");
-        auto e = std::make_unique<mya_env>();
-        e->task = task;
-        const DeviceTask& d = device_task(task);
-        e->T = *d.thost;
+        std::unique_ptr<mya_env, void (*)(mya_env*)> e(new mya_env, free_env);
         e->cfg.seed = config->seed;
         e->cfg.max_steps = config->max_steps;
         e->cfg.step_reward = config->step_reward;
@@ -72,63 +178,126 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
         e->cfg.dead_end_none = config->dead_end == 1 ? 1 : 0;
         e->cfg.dead_end_terminal = config->dead_end_terminal;
         e->cfg.autoreset = config->autoreset;
+        e->inst.resize(count);
+        for (u32 i = 0; i < count; ++i)
+        {
+            EnvInstance& in = e->inst[i];
+            in.task = tasks[i];
+            in.T = *device_task(tasks[i]).thost;
+            in.variant = env_variant(in.T);
+            e->words = std::max(e->words, in.T.W);
+            e->label_width = std::max(e->label_width, in.T.label_width);
+        }
+        e->num_schemas = e->T0().num_schemas;
+        const u32 S = e->num_schemas, cw = cache_width(e->T0());
         e->d_status = dev_alloc<u32>(1, "env status");
         hip_check(hipHostMalloc(reinterpret_cast<void**>(&e->h_status), sizeof(u32), hipHostMallocDefault), "pinned status");
         hip_check(hipMemset(e->d_status, 0, sizeof(u32)), "env status");
-        // the initial state's successor count and goal flag
-        const u32 W = e->T.W;
-        u64* row = dev_alloc<u64>(W, "initial row");
-        i32* cnt = dev_alloc<i32>(1, "initial count");
-        u8* gl = dev_alloc<u8>(1, "initial goal");
-        hip_check(hipMemcpy(row, task->compiled->initial.data(), W * sizeof(u64), hipMemcpyHostToDevice), "initial row");
-        e->init_masks = dev_alloc<u8>(std::max<u32>(1, e->T.num_schemas), "initial masks");
-        e->init_cache = dev_alloc<u32>(cache_width(e->T), "initial count cache");
+        // per instance: the goal as masks over its words; then the initial states' counts, goal flags, masks and
+        // count-cache rows (one count launch per instance)
+        std::vector<size_t> goal_at(count);
+        std::vector<u64> gm;
+        for (u32 i = 0; i < count; ++i)
         {
-            // the task's goal as masks over its words
-            std::vector<u64> gm(2 * static_cast<size_t>(W), 0);
-            for (u32 sl : task->compiled->goal_pos)
-                gm[sl >> 6] |= u64{1} << (sl & 63);
-            for (u32 sl : task->compiled->goal_neg)
-                gm[W + (sl >> 6)] |= u64{1} << (sl & 63);
-            e->goal_masks = dev_alloc<u64>(gm.size(), "goal masks");
-            hip_check(hipMemcpy(e->goal_masks, gm.data(), gm.size() * sizeof(u64), hipMemcpyHostToDevice), "goal masks");
+            const u32 W = e->inst[i].T.W;
+            goal_at[i] = gm.size();
+            gm.resize(gm.size() + 2 * static_cast<size_t>(W), 0);
+            for (u32 sl : tasks[i]->compiled->goal_pos)
+                gm[goal_at[i] + (sl >> 6)] |= u64{1} << (sl & 63);
+            for (u32 sl : tasks[i]->compiled->goal_neg)
+                gm[goal_at[i] + W + (sl >> 6)] |= u64{1} << (sl & 63);
         }
-        launch_env_count(e->T, row, 1, W, cnt, gl, e->init_masks, e->init_cache, nullptr);
-        i32 hc = 0;
-        u8 hg = 0;
-        hip_check(hipMemcpy(&hc, cnt, sizeof(i32), hipMemcpyDeviceToHost), "initial count");
-        hip_check(hipMemcpy(&hg, gl, sizeof(u8), hipMemcpyDeviceToHost), "initial goal");
-        dev_free(row);
-        dev_free(cnt);
-        dev_free(gl);
-        e->init_count = static_cast<u32>(hc);
-        e->init_goal = hg;
+        e->d_init = dev_alloc<u64>(gm.size(), "goal masks");
+        hip_check(hipMemcpy(e->d_init, gm.data(), gm.size() * sizeof(u64), hipMemcpyHostToDevice), "goal masks");
+        e->d_init_masks = dev_alloc<u8>(static_cast<size_t>(count) * std::max<u32>(1, S), "initial masks");
+        e->d_init_cache = dev_alloc<u32>(static_cast<size_t>(count) * cw, "initial count caches");
+        std::vector<i32> hc(count);
+        std::vector<u8> hg(count);
+        {
+            i32* cnt = dev_alloc<i32>(count, "initial counts");
+            u8* gl = dev_alloc<u8>(count, "initial goals");
+            for (u32 i = 0; i < count; ++i)
+            {
+                const TaskDev& T = e->inst[i].T;
+                launch_env_count(T, T.initial, 1, T.W, cnt + i, gl + i, e->d_init_masks + static_cast<size_t>(i) * std::max<u32>(1, S),
+                                 e->d_init_cache + static_cast<size_t>(i) * cw, nullptr, nullptr, nullptr, nullptr, i);
+            }
+            hip_check(hipMemcpy(hc.data(), cnt, count * sizeof(i32), hipMemcpyDeviceToHost), "initial counts");
+            hip_check(hipMemcpy(hg.data(), gl, count * sizeof(u8), hipMemcpyDeviceToHost), "initial goals");
+            dev_free(cnt);
+            dev_free(gl);
+        }
+        std::vector<InstDev> hi(count);
+        std::vector<TaskDev> ht(count);
+        for (u32 i = 0; i < count; ++i)
+        {
+            EnvInstance& in = e->inst[i];
+            in.init_count = static_cast<u32>(hc[i]);
+            in.init_goal = hg[i];
+            InstDev& d = hi[i];
+            d.initial = in.T.initial;
+            d.init_cache = e->d_init_cache + static_cast<size_t>(i) * cw;
+            d.init_masks = e->d_init_masks + static_cast<size_t>(i) * std::max<u32>(1, S);
+            d.goal_pos = e->d_init + goal_at[i];
+            d.goal_neg = e->d_init + goal_at[i] + in.T.W;
+            d.W = in.T.W;
+            d.init_count = in.init_count;
+            d.init_goal = in.init_goal;
+            d.fluent_slots = in.T.fluent_slots;
+            d.variant = in.variant;
+            ht[i] = in.T;
+        }
+        e->d_inst = dev_alloc<InstDev>(count, "env instances");
+        hip_check(hipMemcpy(e->d_inst, hi.data(), count * sizeof(InstDev), hipMemcpyHostToDevice), "env instances");
+        e->d_tasks = dev_alloc<TaskDev>(count, "env instance tables");
+        hip_check(hipMemcpy(e->d_tasks, ht.data(), count * sizeof(TaskDev), hipMemcpyHostToDevice), "env instance tables");
+        if (count > 1)
+        {
+            for (u32 v = 0; v < 4; ++v)
+            {
+                std::vector<const TaskDev*> of;
+                for (const EnvInstance& in : e->inst)
+                    if (in.variant == v)
+                        of.push_back(&in.T);
+                if (of.empty())
+                    continue;
+                mya_env::Launch l{v, 0, 0, 0};
+                l.nw = grouped_shape(of.data(), static_cast<u32>(of.size()), &l.lds, &l.wave_words);
+                e->launches.push_back(l);
+            }
+            e->d_hist = dev_alloc<u32>(count + 1, "env group counters");
+            e->d_starts = dev_alloc<u32>(count + 1, "env group starts");
+            e->d_chunks = dev_alloc<u32>(count + 1, "env group chunks");
+        }
         *out = e.release();
     });
 }
 
-void mya_env_free(mya_env* env)
+int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
 {
-    if (!env)
-        return;
-    dev_free(env->d_status);
-    dev_free(env->init_masks);
-    dev_free(env->init_cache);
-    dev_free(env->goal_masks);
-    if (env->h_status)
-        (void)hipHostFree(env->h_status);
-    delete env;
+    if (!task)
+        return guarded([] { throw std::invalid_argument("mymyr_amd: env_create: null argument"); });
+    return mya_env_create_table(&task, 1, config, out);
 }
 
-int mya_env_initial_count(const mya_env* env, uint32_t* count, uint8_t* goal)
+void mya_env_free(mya_env* env)
+{
+    if (env)
+        free_env(env);
+}
+
+int mya_env_initial_count(const mya_env* env, uint32_t instance, uint32_t* count, uint8_t* goal)
 {
     return guarded([&] {
         if (!env)
             throw std::invalid_argument("mymyr_amd: env: null env");
+        if (instance >= env->instances())
+            throw std::invalid_argument("mymyr: env: instance " + std::to_string(instance) + " is outside the table's " +
+                                        std::to_string(env->instances()) + " instances");
         if (count)
-            *count = env->init_count;
+            *count = env->inst[instance].init_count;
         if (goal)
-            *goal = static_cast<uint8_t>(env->init_goal);
+            *goal = static_cast<uint8_t>(env->inst[instance].init_goal);
     });
 }
 
@@ -138,16 +307,17 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         if (!env)
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
-        launch_env_reset(env->T, batch->states, batch->rows, batch->words, mask, batch->steps, batch->at_goal, count, batch->counts,
-                         env->init_cache, env->init_count, env->init_goal, static_cast<hipStream_t>(stream));
+        const auto s = static_cast<hipStream_t>(stream);
+        launch_env_reset(env->d_inst, env->instances(), batch->states, batch->rows, batch->words, mask, batch->task_ids, batch->steps,
+                         batch->at_goal, count, batch->counts, cache_width(env->T0()), env->d_status, s);
         if (batch->goal_pos)
-            launch_env_reset_goals(env->T, batch->rows, batch->words, mask, batch->goal_pos, batch->goal_neg, env->goal_masks,
-                                   env->goal_masks + env->T.W, keep_goals != 0, batch->at_goal, env->d_status,
-                                   static_cast<hipStream_t>(stream));
+            launch_env_reset_goals(env->d_inst, env->instances(), batch->rows, batch->words, mask, batch->task_ids, batch->goal_pos,
+                                   batch->goal_neg, keep_goals != 0, batch->at_goal, env->d_status, s);
     });
 }
 
-int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions, void* stream)
+int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
+                 const int32_t* next_task_ids, void* stream)
 {
     return guarded([&] {
         if (!env || !out)
@@ -159,19 +329,28 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
             throw std::invalid_argument("mymyr: env: the random policy needs the draw counters");
         if (env->cfg.max_steps && batch->rows && !batch->steps)
             throw std::invalid_argument("mymyr: env: truncation (max_steps) needs the step counters");
-        if (out->binding && out->label_width < env->T.label_width)
+        if (next_task_ids && batch->rows && !batch->task_ids && env->cfg.autoreset)
+            throw std::invalid_argument("mymyr_amd: env: next_task_ids needs the batch's task_ids (an autoreset writes the new instance)");
+        if (out->binding && out->label_width < env->label_width)
             throw std::invalid_argument("mymyr: env: label width " + std::to_string(out->label_width) + " is below the largest schema arity " +
-                                        std::to_string(env->T.label_width));
+                                        std::to_string(env->label_width));
         const u32 fw = out->final_words ? out->final_words : batch->words;
-        if (out->final_states && fw < env->T.W)
-            throw std::invalid_argument("mymyr: env: final state rows of " + std::to_string(fw) + " words; the task has " +
-                                        std::to_string(env->T.W));
+        if (out->final_states && fw < env->words)
+            throw std::invalid_argument("mymyr: env: final state rows of " + std::to_string(fw) + " words; the widest instance has " +
+                                        std::to_string(env->words));
+        if (out->atoms && out->max_atoms == 0)
+            throw std::invalid_argument("mymyr_amd: env: atoms output needs max_atoms > 0");
         EnvArgs a{};
-        a.T = env->T;
+        a.T = env->T0();
+        a.tasks = env->d_tasks;
+        a.inst = env->d_inst;
+        a.instances = env->instances();
         a.cfg = env->cfg;
         a.states = batch->states;
         a.rows = batch->rows;
         a.words = batch->words;
+        a.task_ids = batch->task_ids;
+        a.next_task_ids = next_task_ids;
         a.steps = batch->steps;
         a.draws = batch->draws;
         a.at_goal = batch->at_goal;
@@ -191,19 +370,22 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.atoms = out->atoms;
         a.max_atoms = out->max_atoms;
         a.masks = out->masks;
-        a.init_masks = env->init_masks;
         a.counts = batch->counts;
-        a.init_counts = env->init_cache;
         a.goal_pos = batch->goal_pos;
         a.goal_neg = batch->goal_neg;
-        a.task_goal_pos = env->goal_masks;
-        a.task_goal_neg = env->goal_masks + env->T.W;
-        if (out->atoms && out->max_atoms == 0)
-            throw std::invalid_argument("mymyr_amd: env: atoms output needs max_atoms > 0");
-        a.init_count = env->init_count;
-        a.init_goal = env->init_goal;
         a.status = env->d_status;
-        launch_env_step(a, static_cast<hipStream_t>(stream));
+        const auto s = static_cast<hipStream_t>(stream);
+        if (!grouped(env))
+        {
+            launch_env_step(a, s);
+            return;
+        }
+        a.groups = group_rows(env, batch, s);
+        for (const mya_env::Launch& l : env->launches)
+        {
+            a.wave_words = l.wave_words;
+            launch_env_step_grouped(a, l.variant, l.nw, l.lds, s);
+        }
     });
 }
 
@@ -213,8 +395,33 @@ int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, vo
         if (!env)
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
-        launch_env_count(env->T, batch->states, batch->rows, batch->words, count, batch->at_goal, nullptr, batch->counts,
-                         static_cast<hipStream_t>(stream), batch->goal_pos, batch->goal_neg, env->d_status);
+        CountArgs a{};
+        a.T = env->T0();
+        a.tasks = env->d_tasks;
+        a.inst = env->d_inst;
+        a.instances = env->instances();
+        a.states = batch->states;
+        a.rows = batch->rows;
+        a.words = batch->words;
+        a.task_ids = batch->task_ids;
+        a.count = count;
+        a.goal = batch->at_goal;
+        a.cache = batch->counts;
+        a.goal_pos = batch->goal_pos;
+        a.goal_neg = batch->goal_neg;
+        a.status = env->d_status;
+        const auto s = static_cast<hipStream_t>(stream);
+        if (!grouped(env))
+        {
+            launch_env_count(a, s);
+            return;
+        }
+        a.groups = group_rows(env, batch, s);
+        for (const mya_env::Launch& l : env->launches)
+        {
+            a.wave_words = l.wave_words;
+            launch_env_count_grouped(a, l.variant, l.nw, l.lds, s);
+        }
     });
 }
 
@@ -237,6 +444,9 @@ int mya_env_check(mya_env* env)
                 m += " pick-failed";
             if (s & kStatusGoalMask)
                 m = "mymyr: env: goal masks set fluent slots the task does not have; supply goals for the task's slots";
+            if (s & kStatusTaskId)
+                m = "mymyr: env: a task id is outside the table's " + std::to_string(env->instances()) +
+                    " instances (a reset put its row in instance 0; a step left its row unstepped or kept an autoresetting row's instance)";
             throw std::runtime_error(m);
         }
     });
@@ -247,9 +457,9 @@ int mya_encode_atoms(mya_env* env, const uint64_t* states, uint64_t rows, uint32
     return guarded([&] {
         if (!env || (rows && (!states || !out)))
             throw std::invalid_argument("mymyr_amd: encode_atoms: null argument");
-        if (words < env->T.W)
-            throw std::invalid_argument("mymyr_amd: encode_atoms: rows narrower than the task");
-        launch_encode_atoms(states, rows, words, env->T.W, out, max_atoms, env->d_status, static_cast<hipStream_t>(stream));
+        if (words < env->words)
+            throw std::invalid_argument("mymyr_amd: encode_atoms: rows narrower than the widest instance");
+        launch_encode_atoms(states, rows, words, env->words, out, max_atoms, env->d_status, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -258,9 +468,9 @@ int mya_schema_masks(mya_env* env, const uint64_t* states, uint64_t rows, uint32
     return guarded([&] {
         if (!env || (rows && (!states || !masks)))
             throw std::invalid_argument("mymyr_amd: schema_masks: null argument");
-        if (words < env->T.W)
+        if (words < env->T0().W)
             throw std::invalid_argument("mymyr_amd: schema_masks: rows narrower than the task");
-        launch_env_count(env->T, states, rows, words, nullptr, nullptr, masks, nullptr, static_cast<hipStream_t>(stream));
+        launch_env_count(env->T0(), states, rows, words, nullptr, nullptr, masks, nullptr, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -115,5 +115,6 @@ enum StatusBit : u32
     kStatusNoSlot = 1u << 3,        // an add effect without an atom slot
     kStatusPickFailed = 1u << 4,    // the chosen successor index was not found (internal inconsistency)
     kStatusGoalMask = 1u << 5,      // per-env goal masks set bits past the task's fluent slots
+    kStatusTaskId = 1u << 6,        // a task id (of a row or of next_task_ids) names no instance of the table
 };
 }  // namespace mya

@@ -4,6 +4,7 @@
 
 #include "env.hpp"
 #include "runtime.hpp"
+#include "state_set.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -751,10 +752,10 @@ __device__ __forceinline__ u32 load_counts(const TaskDev& T, const Lds& L, const
     return wave_sum(part);
 }
 
-/// A count-cache row from the per-schema counts in LDS and the fingerprint of the LDS state.
-__device__ __forceinline__ void store_counts(const TaskDev& T, const Lds& L, u32* crow, u32 lane)
+/// A count-cache row from the per-schema counts in LDS and the fingerprint of the LDS state (plus the instance's salt).
+__device__ __forceinline__ void store_counts(const TaskDev& T, const Lds& L, u32* crow, u32 lane, u64 salt)
 {
-    const u64 fp = state_fingerprint(L.row, T.W, lane);
+    const u64 fp = state_fingerprint(L.row, T.W, lane) + salt;
     for (u32 s = lane; s < T.num_schemas; s += kWave)
         crow[s] = L.counts[s];
     if (lane == 0)
@@ -1116,14 +1117,11 @@ F variant(const TaskDev& T, F ss, F sl, F gs, F gl)
 
 bool levels(const TaskDev& T);
 
-unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
+/// The waves per block that keep the most waves resident on a CU (its 160 KiB of LDS shared by whole blocks), for
+/// hot tables of `hot` bytes staged once per block and `wave` bytes per wave; a smaller block is taken only for at
+/// least 1/8 more resident waves (a larger one stages the hot tables fewer times).
+unsigned block_shape(size_t hot, size_t wave, size_t* lds_bytes)
 {
-    if (T.num_schemas > kMaxEnvSchemas)
-        throw std::invalid_argument("mymyr_amd: env: the device step keeps the successor counts of at most " + std::to_string(kMaxEnvSchemas) +
-                                    " schemas (the task has " + std::to_string(T.num_schemas) + ")");
-    const size_t hot = staged(T) ? static_cast<size_t>(T.hot_words) * 8 : 0, wave = static_cast<size_t>(wave_lds_words(T, levels(T))) * 8;
-    // the waves per block that keep the most waves resident on a CU (its 160 KiB of LDS shared by whole blocks); a
-    // smaller block is taken only for at least 1/8 more resident waves (a larger one stages the hot tables fewer times)
     constexpr size_t kCuLds = 160 * 1024;
     constexpr int kCuWaves = 24;  // waves per CU the kernels' register use allows
     int nw = 1, best = 0;
@@ -1140,12 +1138,230 @@ unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
         }
     }
     *lds_bytes = hot + static_cast<size_t>(nw) * wave;
-    if (*lds_bytes > 160 * 1024)
+    if (*lds_bytes > kCuLds)
         throw std::invalid_argument("mymyr_amd: env: the task's per-state LDS (" + std::to_string(*lds_bytes) +
                                     " bytes) exceeds the 160 KiB of a gfx950 workgroup");
     return static_cast<unsigned>(nw);
 }
 
+void check_schemas(const TaskDev& T)
+{
+    if (T.num_schemas > kMaxEnvSchemas)
+        throw std::invalid_argument("mymyr_amd: env: the device step keeps the successor counts of at most " + std::to_string(kMaxEnvSchemas) +
+                                    " schemas (the task has " + std::to_string(T.num_schemas) + ")");
+}
+
+unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
+{
+    check_schemas(T);
+    const size_t hot = staged(T) ? static_cast<size_t>(T.hot_words) * 8 : 0, wave = static_cast<size_t>(wave_lds_words(T, levels(T))) * 8;
+    return block_shape(hot, wave, lds_bytes);
+}
+
+/// One environment's step (HostEnv::step_row_impl, src/mymyr/rl/env.cpp:351-528): row i of instance k, whose tables
+/// are T / H and whose wave region is L. An autoreset restarts the row in next_task_ids[i] when that names an instance
+/// (else in k), writing the new instance's initial state and goal masks over the words the row may have dirtied
+/// (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138) and its id into task_ids.
+template<bool kLevels>
+__device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane)
+{
+    const u32 Lw = A.label_width;
+    u64* grow = A.states + i * A.words;
+    load_row_lds(T, L, grow, lane);
+    build_view(T, H, L, lane);
+    const bool already_goal = A.at_goal[i] != 0;
+    // the count cache row: its counts stand for the row's state (and instance) when its fingerprint matches (reset,
+    // refresh and step write it; a state written directly since is counted again)
+    const u32 cw = cache_width(T);
+    u32* crow = A.counts ? A.counts + i * cw : nullptr;
+    const u64 salt = instance_salt(k);
+    bool cached = false;
+    if (crow)
+    {
+        const u64 fp = state_fingerprint(L.row, T.W, lane) + salt;
+        cached = (static_cast<u64>(crow[T.num_schemas]) | (static_cast<u64>(crow[T.num_schemas + 1]) << 32)) == fp;
+    }
+    // the instance an autoreset restarts in; an id outside the table sets the status (every row's, as the reference
+    // checks next_task_ids over the whole batch) and keeps the row's instance
+    u32 next = k;
+    if (A.next_task_ids)
+    {
+        const i32 v = A.next_task_ids[i];
+        if (v < 0 || static_cast<u32>(v) >= A.instances)
+        {
+            if (lane == 0)
+                atomicOr(A.status, kStatusTaskId);
+        }
+        else
+            next = static_cast<u32>(v);
+    }
+    enum
+    {
+        kOk = 0,
+        kStuck = 1,
+        kInvalid = 2,
+        kGoal = 3
+    };
+    // phase 0 counts s, chooses, picks and moves; phase 1 counts the reached state s' (one copy of the count)
+    u32 c = 0, c2 = 0, st = kOk, schema = kNone;
+    bool g = already_goal;
+    for (u32 phase = 0; phase < 2; ++phase)
+    {
+        const u32 cc = (phase == 0 && cached) ? load_counts(T, L, crow, lane) : count_all<kLevels>(T, H, L, lane);
+        if (phase == 1)
+        {
+            c2 = cc;
+            break;
+        }
+        c = c2 = cc;
+        // 2. the choice (env.cpp:416-440)
+        st = already_goal ? kGoal : kOk;
+        u32 a = 0;
+        if (!already_goal && c == 0)
+            st = kStuck;
+        else if (!already_goal && A.actions)
+        {
+            const i64 act = A.actions[i];
+            if (act < 0 || static_cast<u64>(act) >= c)
+                st = kInvalid;
+            else
+                a = static_cast<u32>(act);
+        }
+        else if (!already_goal)
+            a = successor_index(A.cfg.seed, A.first_env + i, A.draws[i], c);
+        u32 rank = 0;
+        if (st == kOk)
+        {
+            select_schema(T, L, a, &schema, &rank);
+            if (schema == kNone || !pick<kLevels>(T, H, L, schema, rank, lane))
+            {
+                if (lane == 0)
+                    atomicOr(A.status, kStatusPickFailed);
+                st = kStuck;
+            }
+        }
+        if (lane == 0)
+        {
+            if (A.draws)
+                A.draws[i] += 1;
+            if (A.schema)
+                A.schema[i] = st == kOk ? static_cast<i32>(schema) : -1;
+            if (A.invalid)
+                A.invalid[i] = st == kInvalid ? 1 : 0;
+        }
+        if (A.binding)
+        {
+            const u32 arity = st == kOk ? H.schemas[schema].arity : 0;
+            for (u32 q = lane; q < Lw; q += kWave)
+                A.binding[i * Lw + q] = (st == kOk && q < arity) ? static_cast<i32>(L.ub[q]) : -1;
+        }
+        if (st != kOk)
+            break;
+        // 3. the move, goal and (next phase) the successor count of the reached state
+        apply_effects(T, H, L, schema, lane, A.status);
+        g = A.goal_pos ? mask_goal(L.row, A.goal_pos + i * A.words, A.goal_neg + i * A.words, T.W, lane)
+                       : goal_test(T, H, L.row, lane);
+    }
+    // 4. rewards, termination, truncation (env.cpp:466-485)
+    const bool dead = !A.cfg.dead_end_none && !g && ((st == kOk && c2 == 0) || st == kStuck);
+    const bool term = g || (dead && A.cfg.dead_end_terminal);
+    const bool absorbed = already_goal || (st == kStuck && dead && A.cfg.dead_end_terminal);
+    const i32 steps0 = A.steps ? A.steps[i] : 0;
+    const i32 t2 = A.steps ? steps0 + (absorbed ? 0 : 1) : 0;
+    const bool trunc = !term && A.cfg.max_steps && t2 >= static_cast<i32>(A.cfg.max_steps);
+    if (lane == 0)
+    {
+        if (A.reward)
+        {
+            float r = 0.0f;
+            if (!absorbed)
+            {
+                r = A.cfg.step_reward + (g ? A.cfg.goal_reward : 0.0f);
+                r = r + (dead ? A.cfg.dead_end_reward : 0.0f);
+            }
+            A.reward[i] = r;
+        }
+        if (A.terminated)
+            A.terminated[i] = term ? 1 : 0;
+        if (A.truncated)
+            A.truncated[i] = trunc ? 1 : 0;
+        if (A.goal)
+            A.goal[i] = g ? 1 : 0;
+    }
+    if (A.final_states)
+    {
+        const u32 FW = A.final_words;
+        u64* f = A.final_states + i * FW;
+        for (u32 q = lane; q < FW; q += kWave)
+            f[q] = q < T.W ? L.row[q] : 0;
+    }
+    // 5. the autoreset, or the bookkeeping of the move (the LDS row holds s')
+    const bool reset = A.cfg.autoreset && (term || trunc);
+    if (reset)
+    {
+        const InstDev& J = A.inst[next];
+        const u32 z = min(A.words, max(J.W, T.W));  // the words the row may have dirtied: its old and new instance's
+        for (u32 q = lane; q < z; q += kWave)
+            grow[q] = q < J.W ? J.initial[q] : 0;
+        if (A.goal_pos)
+            for (u32 q = lane; q < z; q += kWave)
+            {
+                A.goal_pos[i * A.words + q] = q < J.W ? J.goal_pos[q] : 0;
+                A.goal_neg[i * A.words + q] = q < J.W ? J.goal_neg[q] : 0;
+            }
+        if (lane == 0)
+        {
+            if (A.task_ids)
+                A.task_ids[i] = static_cast<i32>(next);
+            if (A.count)
+                A.count[i] = static_cast<i32>(J.init_count);
+            A.at_goal[i] = J.init_goal ? 1 : 0;
+            if (A.steps)
+                A.steps[i] = 0;
+        }
+        if (crow)
+            for (u32 q = lane; q < cw; q += kWave)
+                crow[q] = J.init_cache[q];
+    }
+    else
+    {
+        if (st == kOk)
+            for (u32 q = lane; q < T.W; q += kWave)
+                grow[q] = L.row[q];
+        if (lane == 0)
+        {
+            A.at_goal[i] = g ? 1 : 0;
+            if (A.steps)
+                A.steps[i] = t2;
+            if (A.count)
+                A.count[i] = static_cast<i32>(c2);
+        }
+        // the count cache of the state the row now holds: the counts in LDS (of s' after a move, of s otherwise)
+        // unless they came from the cache
+        if (crow && (st == kOk || !cached))
+            store_counts(T, L, crow, lane, salt);
+    }
+    // 6. the observation's encoding: true-atom slots and applicable-schema masks (LDS holds the per-schema counts of
+    // the state the row holds unless the row was reset)
+    if (A.atoms || A.masks)
+    {
+        wave_sync();
+        if (A.atoms)
+        {
+            if (reset)
+                encode_row(A.inst[next].initial, A.inst[next].W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
+            else
+                encode_row(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
+        }
+        if (A.masks)
+            for (u32 q = lane; q < T.num_schemas; q += kWave)
+                A.masks[i * T.num_schemas + q] = reset ? A.inst[next].init_masks[q] : (L.counts[q] > 0 ? 1 : 0);
+    }
+    wave_sync();
+}
+
+/// The step of a batch of one instance: every row in batch order with the kernel-argument tables. A row whose task id
+/// is not 0 names no instance: it sets kStatusTaskId and is not stepped.
 template<bool kStaged, bool kLevels>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
 {
@@ -1155,189 +1371,55 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
     lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
     const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
     const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
-    const u32 Lw = A.label_width;
     for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
     {
-        u64* grow = A.states + i * A.words;
-        load_row_lds(T, L, grow, lane);
-        build_view(T, H, L, lane);
-        const bool already_goal = A.at_goal[i] != 0;
-        // the count cache row: its counts stand for the row's state when its fingerprint matches (reset, refresh and
-        // step write it; a state written directly since is counted again)
-        u32* crow = A.counts ? A.counts + i * cache_width(T) : nullptr;
-        bool cached = false;
-        if (crow)
+        if (A.task_ids && A.task_ids[i] != 0)
         {
-            const u64 fp = state_fingerprint(L.row, T.W, lane);
-            cached = (static_cast<u64>(crow[T.num_schemas]) | (static_cast<u64>(crow[T.num_schemas + 1]) << 32)) == fp;
-        }
-        enum
-        {
-            kOk = 0,
-            kStuck = 1,
-            kInvalid = 2,
-            kGoal = 3
-        };
-        // phase 0 counts s, chooses, picks and moves; phase 1 counts the reached state s' (one copy of the count)
-        u32 c = 0, c2 = 0, st = kOk, schema = kNone;
-        bool g = already_goal;
-        for (u32 phase = 0; phase < 2; ++phase)
-        {
-            const u32 cc = (phase == 0 && cached) ? load_counts(T, L, crow, lane) : count_all<kLevels>(T, H, L, lane);
-            if (phase == 1)
-            {
-                c2 = cc;
-                break;
-            }
-            c = c2 = cc;
-            // 2. the choice (env.cpp:416-440)
-            st = already_goal ? kGoal : kOk;
-            u32 a = 0;
-            if (!already_goal && c == 0)
-                st = kStuck;
-            else if (!already_goal && A.actions)
-            {
-                const i64 act = A.actions[i];
-                if (act < 0 || static_cast<u64>(act) >= c)
-                    st = kInvalid;
-                else
-                    a = static_cast<u32>(act);
-            }
-            else if (!already_goal)
-                a = successor_index(A.cfg.seed, A.first_env + i, A.draws[i], c);
-            u32 rank = 0;
-            if (st == kOk)
-            {
-                select_schema(T, L, a, &schema, &rank);
-                if (schema == kNone || !pick<kLevels>(T, H, L, schema, rank, lane))
-                {
-                    if (lane == 0)
-                        atomicOr(A.status, kStatusPickFailed);
-                    st = kStuck;
-                }
-            }
             if (lane == 0)
-            {
-                if (A.draws)
-                    A.draws[i] += 1;
-                if (A.schema)
-                    A.schema[i] = st == kOk ? static_cast<i32>(schema) : -1;
-                if (A.invalid)
-                    A.invalid[i] = st == kInvalid ? 1 : 0;
-            }
-            if (A.binding)
-            {
-                const u32 arity = st == kOk ? H.schemas[schema].arity : 0;
-                for (u32 k = lane; k < Lw; k += kWave)
-                    A.binding[i * Lw + k] = (st == kOk && k < arity) ? static_cast<i32>(L.ub[k]) : -1;
-            }
-            if (st != kOk)
-                break;
-            // 3. the move, goal and (next phase) the successor count of the reached state
-            apply_effects(T, H, L, schema, lane, A.status);
-            g = A.goal_pos ? mask_goal(L.row, A.goal_pos + i * A.words, A.goal_neg + i * A.words, T.W, lane)
-                           : goal_test(T, H, L.row, lane);
+                atomicOr(A.status, kStatusTaskId);
+            continue;
         }
-        // 4. rewards, termination, truncation (env.cpp:466-485)
-        const bool dead = !A.cfg.dead_end_none && !g && ((st == kOk && c2 == 0) || st == kStuck);
-        const bool term = g || (dead && A.cfg.dead_end_terminal);
-        const bool absorbed = already_goal || (st == kStuck && dead && A.cfg.dead_end_terminal);
-        const i32 steps0 = A.steps ? A.steps[i] : 0;
-        const i32 t2 = A.steps ? steps0 + (absorbed ? 0 : 1) : 0;
-        const bool trunc = !term && A.cfg.max_steps && t2 >= static_cast<i32>(A.cfg.max_steps);
-        if (lane == 0)
-        {
-            if (A.reward)
-            {
-                float r = 0.0f;
-                if (!absorbed)
-                {
-                    r = A.cfg.step_reward + (g ? A.cfg.goal_reward : 0.0f);
-                    r = r + (dead ? A.cfg.dead_end_reward : 0.0f);
-                }
-                A.reward[i] = r;
-            }
-            if (A.terminated)
-                A.terminated[i] = term ? 1 : 0;
-            if (A.truncated)
-                A.truncated[i] = trunc ? 1 : 0;
-            if (A.goal)
-                A.goal[i] = g ? 1 : 0;
-        }
-        if (A.final_states)
-        {
-            const u32 FW = A.final_words;
-            u64* f = A.final_states + i * FW;
-            for (u32 k = lane; k < FW; k += kWave)
-                f[k] = k < T.W ? L.row[k] : 0;
-        }
-        // 5. the autoreset, or the bookkeeping of the move (the LDS row holds s')
-        const bool reset = A.cfg.autoreset && (term || trunc);
-        if (reset)
-        {
-            for (u32 k = lane; k < A.words; k += kWave)
-                grow[k] = k < T.W ? T.initial[k] : 0;
-            if (A.goal_pos)
-                for (u32 k = lane; k < A.words; k += kWave)
-                {
-                    A.goal_pos[i * A.words + k] = k < T.W ? A.task_goal_pos[k] : 0;
-                    A.goal_neg[i * A.words + k] = k < T.W ? A.task_goal_neg[k] : 0;
-                }
-            if (A.atoms)
-                for (u32 k = lane; k < T.W; k += kWave)
-                    L.row[k] = T.initial[k];
-            if (lane == 0)
-            {
-                if (A.count)
-                    A.count[i] = static_cast<i32>(A.init_count);
-                A.at_goal[i] = A.init_goal ? 1 : 0;
-                if (A.steps)
-                    A.steps[i] = 0;
-            }
-        }
+        step_row<kLevels>(A, T, H, L, i, 0, lane);
+    }
+}
+
+/// The instance of chunk c: the last k with chunk_start[k] <= c (chunk_start is non-decreasing, chunk_start[0] = 0).
+__device__ __forceinline__ u32 chunk_instance(const u32* chunk_start, u32 instances, u32 c)
+{
+    u32 lo = 0, hi = instances;
+    while (hi - lo > 1)
+    {
+        const u32 mid = (lo + hi) / 2;
+        if (chunk_start[mid] <= c)
+            lo = mid;
         else
-        {
-            if (st == kOk)
-                for (u32 k = lane; k < T.W; k += kWave)
-                    grow[k] = L.row[k];
-            if (lane == 0)
-            {
-                A.at_goal[i] = g ? 1 : 0;
-                if (A.steps)
-                    A.steps[i] = t2;
-                if (A.count)
-                    A.count[i] = static_cast<i32>(c2);
-            }
-        }
-        // the count cache of the state the row now holds: the initial state's after a reset, else the counts in LDS
-        // (of s' after a move, of s otherwise) unless they came from the cache
-        if (crow)
-        {
-            if (reset)
-                for (u32 k = lane; k < cache_width(T); k += kWave)
-                    crow[k] = A.init_counts[k];
-            else if (st == kOk || !cached)
-                store_counts(T, L, crow, lane);
-        }
-        // 6. the observation's encoding: true-atom slots and applicable-schema masks (LDS holds the per-schema counts
-        // of the state the row holds unless the row was reset)
-        if (A.atoms || A.masks)
-        {
-            wave_sync();
-            if (A.atoms)
-                encode_row(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
-            if (A.masks)
-                for (u32 s = lane; s < T.num_schemas; s += kWave)
-                {
-                    u8 m;
-                    if (reset)
-                        m = A.init_masks[s];
-                    else
-                        m = L.counts[s] > 0 ? 1 : 0;
-                    A.masks[i * T.num_schemas + s] = m;
-                }
-        }
-        wave_sync();
+            hi = mid;
+    }
+    return lo;
+}
+
+/// The step of the rows of the instances of variant kVariant of a batch grouped by instance: each block takes chunks
+/// of kChunkRows rows of one instance, stages that instance's hot tables and steps the chunk's rows (one per wave).
+template<bool kStaged, bool kLevels>
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step_grouped(EnvArgs A, u32 variant)
+{
+    extern __shared__ u64 smem[];
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const u32 chunks = A.groups.chunk_start[A.instances];
+    for (u32 c = blockIdx.x; c < chunks; c += gridDim.x)
+    {
+        const u32 k = chunk_instance(A.groups.chunk_start, A.instances, c);
+        if (A.inst[k].variant != variant)
+            continue;
+        const TaskDev T = A.tasks[k];
+        __syncthreads();  // every wave is done with the tables of the block's previous chunk
+        Tab<kStaged> H;
+        lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+        const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * A.wave_words, T);
+        const u32 r0 = A.groups.starts[k] + (c - A.groups.chunk_start[k]) * kChunkRows;
+        const u32 r1 = min(r0 + kChunkRows, A.groups.starts[k + 1]);
+        for (u32 j = r0 + wave; j < r1; j += nw)
+            step_row<kLevels>(A, T, H, L, A.groups.order[j], k, lane);
     }
 }
 
@@ -1348,102 +1430,160 @@ __global__ __launch_bounds__(kWave) void k_encode(const u64* states, u64 rows, u
         encode_row(states + i * words, W, out + i * max_atoms, max_atoms, lane, status);
 }
 
+/// The count of row i of instance k (HostEnv::refresh / count_row, src/mymyr/rl/env.cpp:283-322): successors, goal
+/// (per-env masks, checked against the instance's slots, or the instance's goal test), masks and the count cache.
+template<bool kLevels>
+__device__ __forceinline__ void count_row(const CountArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane)
+{
+    load_row_lds(T, L, A.states + i * A.words, lane);
+    build_view(T, H, L, lane);
+    const u32 c = count_all<kLevels>(T, H, L, lane);
+    bool g;
+    if (A.goal_pos)
+    {
+        const u64* gp = A.goal_pos + i * A.words;
+        const u64* gn = A.goal_neg + i * A.words;
+        if (!goal_masks_fit(gp, gn, A.words, T, lane) && lane == 0 && A.status)
+            atomicOr(A.status, kStatusGoalMask);
+        g = mask_goal(L.row, gp, gn, T.W, lane);
+    }
+    else
+        g = goal_test(T, H, L.row, lane);
+    if (lane == 0)
+    {
+        if (A.count)
+            A.count[i] = static_cast<i32>(c);
+        if (A.goal)
+            A.goal[i] = g ? 1 : 0;
+    }
+    if (A.masks)
+        for (u32 q = lane; q < T.num_schemas; q += kWave)
+            A.masks[i * T.num_schemas + q] = L.counts[q] > 0 ? 1 : 0;
+    if (A.cache)
+        store_counts(T, L, A.cache + i * cache_width(T), lane, instance_salt(k));
+    wave_sync();
+}
+
+/// The count of a batch of one instance (A.instance) in batch order; rows whose task id is not 0 set kStatusTaskId and
+/// are not counted.
 template<bool kStaged, bool kLevels>
-__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(TaskDev T, const u64* states, u64 rows, u32 words, i32* count, u8* goal,
-                                                                 u8* masks, u32* cache, const u64* goal_pos, const u64* goal_neg,
-                                                                 u32* status)
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(CountArgs A)
 {
     extern __shared__ u64 smem[];
+    const TaskDev& T = A.T;
     Tab<kStaged> H;
     lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
     const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
     const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
-    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < rows; i += static_cast<u64>(gridDim.x) * nw)
+    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
     {
-        load_row_lds(T, L, states + i * words, lane);
-        build_view(T, H, L, lane);
-        const u32 c = count_all<kLevels>(T, H, L, lane);
-        bool g;
-        if (goal_pos)
+        if (A.task_ids && A.task_ids[i] != 0)
         {
-            const u64* gp = goal_pos + i * words;
-            const u64* gn = goal_neg + i * words;
-            if (!goal_masks_fit(gp, gn, words, T, lane) && lane == 0 && status)
-                atomicOr(status, kStatusGoalMask);
-            g = mask_goal(L.row, gp, gn, T.W, lane);
+            if (lane == 0 && A.status)
+                atomicOr(A.status, kStatusTaskId);
+            continue;
         }
-        else
-            g = goal_test(T, H, L.row, lane);
-        if (lane == 0)
-        {
-            if (count)
-                count[i] = static_cast<i32>(c);
-            if (goal)
-                goal[i] = g ? 1 : 0;
-        }
-        if (masks)
-            for (u32 s = 0; s < T.num_schemas; ++s)
-            {
-                const u32 cs = L.counts[s];
-                if (lane == 0)
-                    masks[i * T.num_schemas + s] = cs > 0 ? 1 : 0;
-            }
-        if (cache)
-            store_counts(T, L, cache + i * cache_width(T), lane);
-        wave_sync();
+        count_row<kLevels>(A, T, H, L, i, A.instance, lane);
     }
 }
 
-__global__ void k_env_reset(TaskDev T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
-                            u32 init_count, u32 init_goal)
+/// The count of the rows of the instances of variant `variant` of a batch grouped by instance (as k_env_step_grouped).
+template<bool kStaged, bool kLevels>
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count_grouped(CountArgs A, u32 variant)
+{
+    extern __shared__ u64 smem[];
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const u32 chunks = A.groups.chunk_start[A.instances];
+    for (u32 c = blockIdx.x; c < chunks; c += gridDim.x)
+    {
+        const u32 k = chunk_instance(A.groups.chunk_start, A.instances, c);
+        if (A.inst[k].variant != variant)
+            continue;
+        const TaskDev T = A.tasks[k];
+        __syncthreads();
+        Tab<kStaged> H;
+        lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+        const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * A.wave_words, T);
+        const u32 r0 = A.groups.starts[k] + (c - A.groups.chunk_start[k]) * kChunkRows;
+        const u32 r1 = min(r0 + kChunkRows, A.groups.starts[k + 1]);
+        for (u32 j = r0 + wave; j < r1; j += nw)
+            count_row<kLevels>(A, T, H, L, A.groups.order[j], k, lane);
+    }
+}
+
+/// The instance a reset puts row i in: task_ids[i] (null: 0); an id outside the table resets into instance 0.
+__device__ __forceinline__ u32 reset_instance(const i32* task_ids, u64 i, u32 instances, bool* bad)
+{
+    const i32 v = task_ids ? task_ids[i] : 0;
+    *bad = v < 0 || static_cast<u32>(v) >= instances;
+    return *bad ? 0u : static_cast<u32>(v);
+}
+
+/// One thread per state word of the batch (reset_row with a dirtied row: zeros up to the batch's words).
+__global__ void k_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows, u32 words, const u8* mask, i32* task_ids,
+                            i32* steps, u8* at_goal, i32* count, u32* status)
 {
     const u64 total = rows * words;
-    for (u64 k = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; k < total; k += static_cast<u64>(gridDim.x) * blockDim.x)
+    for (u64 e = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += static_cast<u64>(gridDim.x) * blockDim.x)
     {
-        const u64 i = k / words;
-        const u32 w = static_cast<u32>(k - i * words);
+        const u64 i = e / words;
+        const u32 w = static_cast<u32>(e - i * words);
         if (mask && !mask[i])
             continue;
-        states[k] = w < T.W ? T.initial[w] : 0;
+        // the word-0 thread writes a corrected id (0) while the row's other threads may read it: either value they
+        // see resets the row into instance 0
+        bool bad = false;
+        const u32 k = reset_instance(task_ids, i, instances, &bad);
+        const InstDev& J = inst[k];
+        states[e] = w < J.W ? J.initial[w] : 0;
         if (w == 0)
         {
+            if (bad)
+            {
+                atomicOr(status, kStatusTaskId);
+                task_ids[i] = 0;
+            }
             if (steps)
                 steps[i] = 0;
             if (at_goal)
-                at_goal[i] = init_goal ? 1 : 0;
+                at_goal[i] = J.init_goal ? 1 : 0;
             if (count)
-                count[i] = static_cast<i32>(init_count);
+                count[i] = static_cast<i32>(J.init_count);
         }
     }
 }
 
-__global__ void k_env_reset_goals(TaskDev T, u64 rows, u32 words, const u8* mask, u64* goal_pos, u64* goal_neg, const u64* task_pos,
-                                  const u64* task_neg, u32 keep, u8* at_goal, u32* status)
+/// Per row: the instance's goal into the row's goal masks, or (keep) the given masks checked against the instance's
+/// fluent slots and tested on its initial state. Runs after k_env_reset, so task ids are valid.
+__global__ void k_env_reset_goals(const InstDev* inst, u32 instances, u64 rows, u32 words, const u8* mask, const i32* task_ids,
+                                  u64* goal_pos, u64* goal_neg, u32 keep, u8* at_goal, u32* status)
 {
     for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
     {
         if (mask && !mask[i])
             continue;
+        bool bad = false;
+        const InstDev& J = inst[reset_instance(task_ids, i, instances, &bad)];
         u64* gp = goal_pos + i * words;
         u64* gn = goal_neg + i * words;
         if (!keep)
         {
             for (u32 w = 0; w < words; ++w)
             {
-                gp[w] = w < T.W ? task_pos[w] : 0;
-                gn[w] = w < T.W ? task_neg[w] : 0;
+                gp[w] = w < J.W ? J.goal_pos[w] : 0;
+                gn[w] = w < J.W ? J.goal_neg[w] : 0;
             }
             continue;
         }
         bool ok = true, fit = true;
         for (u32 w = 0; w < words; ++w)
         {
-            const u64 p = gp[w], n = gn[w], x = w < T.W ? T.initial[w] : 0;
+            const u64 p = gp[w], n = gn[w], x = w < J.W ? J.initial[w] : 0;
             ok = ok && (x & p) == p && (x & n) == 0;
-            if (w >= T.W)
+            if (w >= J.W)
                 fit = fit && (p | n) == 0;
-            else if (w == T.W - 1 && (T.fluent_slots & 63))
-                fit = fit && ((p | n) >> (T.fluent_slots & 63)) == 0;
+            else if (w == J.W - 1 && (J.fluent_slots & 63))
+                fit = fit && ((p | n) >> (J.fluent_slots & 63)) == 0;
         }
         if (!fit)
             atomicOr(status, kStatusGoalMask);
@@ -1452,16 +1592,152 @@ __global__ void k_env_reset_goals(TaskDev T, u64 rows, u32 words, const u8* mask
     }
 }
 
-__global__ void k_env_reset_cache(u64 rows, u32 width, const u8* mask, u32* cache, const u32* init_cache)
+/// One thread per count-cache word: the initial state's row of the row's instance. Runs after k_env_reset.
+__global__ void k_env_reset_cache(const InstDev* inst, u32 instances, u64 rows, u32 width, const u8* mask, const i32* task_ids, u32* cache)
 {
     const u64 total = rows * width;
-    for (u64 k = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; k < total; k += static_cast<u64>(gridDim.x) * blockDim.x)
+    for (u64 e = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += static_cast<u64>(gridDim.x) * blockDim.x)
     {
-        const u64 i = k / width;
+        const u64 i = e / width;
         if (mask && !mask[i])
             continue;
-        cache[k] = init_cache[k - i * width];
+        bool bad = false;
+        cache[e] = inst[reset_instance(task_ids, i, instances, &bad)].init_cache[e - i * width];
     }
+}
+
+// ------------------------------------------------------------------------------------------ grouping by instance
+constexpr u32 kGroupBlock = 1024;
+constexpr u32 kGroupRowsPerThread = 4;
+constexpr u32 kLdsInstances = 4096;  // instances whose block-local counters fit LDS
+
+/// hist[k] += rows with task id k (block-local counters in LDS when the table is small); ids outside the table set
+/// kStatusTaskId.
+__global__ __launch_bounds__(kGroupBlock) void k_group_count(const i32* task_ids, u64 rows, u32 instances, u32* hist, u32* status)
+{
+    __shared__ u32 sh[kLdsInstances];
+    const bool local = instances <= kLdsInstances;
+    if (local)
+    {
+        for (u32 k = threadIdx.x; k < instances; k += blockDim.x)
+            sh[k] = 0;
+        __syncthreads();
+    }
+    const u64 base = static_cast<u64>(blockIdx.x) * blockDim.x * kGroupRowsPerThread;
+    bool bad = false;
+    for (u32 r = 0; r < kGroupRowsPerThread; ++r)
+    {
+        const u64 i = base + static_cast<u64>(r) * blockDim.x + threadIdx.x;
+        if (i >= rows)
+            break;
+        const i32 v = task_ids[i];
+        if (v < 0 || static_cast<u32>(v) >= instances)
+        {
+            bad = true;
+            continue;
+        }
+        if (local)
+            atomicAdd(&sh[v], 1u);
+        else
+            atomicAdd(&hist[v], 1u);
+    }
+    if (bad)
+        atomicOr(status, kStatusTaskId);
+    if (local)
+    {
+        __syncthreads();
+        for (u32 k = threadIdx.x; k < instances; k += blockDim.x)
+            if (sh[k])
+                atomicAdd(&hist[k], sh[k]);
+    }
+}
+
+/// One block: starts = exclusive scan of hist, chunk_start = exclusive scan of ceil(hist / kChunkRows) (both
+/// [instances + 1]); hist becomes each group's write cursor (its start).
+__global__ __launch_bounds__(kGroupBlock) void k_group_scan(u32* hist, u32 instances, u32* starts, u32* chunk_start)
+{
+    __shared__ u32 sr[kGroupBlock], sc[kGroupBlock];
+    const u32 per = (instances + kGroupBlock - 1) / kGroupBlock;
+    const u32 lo = min(instances, threadIdx.x * per), hi = min(instances, lo + per);
+    u32 r = 0, c = 0;
+    for (u32 k = lo; k < hi; ++k)
+    {
+        r += hist[k];
+        c += (hist[k] + kChunkRows - 1) / kChunkRows;
+    }
+    sr[threadIdx.x] = r;
+    sc[threadIdx.x] = c;
+    __syncthreads();
+    // inclusive Hillis-Steele scan of the per-thread sums
+    for (u32 d = 1; d < kGroupBlock; d <<= 1)
+    {
+        const u32 ar = threadIdx.x >= d ? sr[threadIdx.x - d] : 0;
+        const u32 ac = threadIdx.x >= d ? sc[threadIdx.x - d] : 0;
+        __syncthreads();
+        sr[threadIdx.x] += ar;
+        sc[threadIdx.x] += ac;
+        __syncthreads();
+    }
+    r = sr[threadIdx.x] - r;
+    c = sc[threadIdx.x] - c;
+    for (u32 k = lo; k < hi; ++k)
+    {
+        const u32 h = hist[k];
+        starts[k] = r;
+        chunk_start[k] = c;
+        hist[k] = r;
+        r += h;
+        c += (h + kChunkRows - 1) / kChunkRows;
+    }
+    if (threadIdx.x == kGroupBlock - 1)
+    {
+        starts[instances] = sr[kGroupBlock - 1];
+        chunk_start[instances] = sc[kGroupBlock - 1];
+    }
+}
+
+/// order[cursor[k]++] = i for each row i of instance k (block-local ranks in LDS, one global reservation per block and
+/// instance, when the table is small). Rows in a group come in no particular order; each row's results do not depend
+/// on it.
+__global__ __launch_bounds__(kGroupBlock) void k_group_scatter(const i32* task_ids, u64 rows, u32 instances, u32* cursor, u32* order)
+{
+    __shared__ u32 sh[kLdsInstances];
+    const bool local = instances <= kLdsInstances;
+    if (local)
+    {
+        for (u32 k = threadIdx.x; k < instances; k += blockDim.x)
+            sh[k] = 0;
+        __syncthreads();
+    }
+    const u64 base = static_cast<u64>(blockIdx.x) * blockDim.x * kGroupRowsPerThread;
+    u32 pos[kGroupRowsPerThread];
+    i32 ids[kGroupRowsPerThread];
+    for (u32 r = 0; r < kGroupRowsPerThread; ++r)
+    {
+        const u64 i = base + static_cast<u64>(r) * blockDim.x + threadIdx.x;
+        ids[r] = -1;
+        if (i >= rows)
+            continue;
+        const i32 v = task_ids[i];
+        if (v < 0 || static_cast<u32>(v) >= instances)
+            continue;
+        ids[r] = v;
+        pos[r] = local ? atomicAdd(&sh[v], 1u) : atomicAdd(&cursor[v], 1u);
+    }
+    if (local)
+    {
+        __syncthreads();
+        for (u32 k = threadIdx.x; k < instances; k += blockDim.x)
+        {
+            const u32 n = sh[k];
+            if (n)
+                sh[k] = atomicAdd(&cursor[k], n);
+        }
+        __syncthreads();
+    }
+    for (u32 r = 0; r < kGroupRowsPerThread; ++r)
+        if (ids[r] >= 0)
+            order[(local ? sh[ids[r]] : 0u) + pos[r]] = static_cast<u32>(base + static_cast<u64>(r) * blockDim.x + threadIdx.x);
 }
 
 /// Applies the effects of the picked binding of schema s to the LDS row only (the view stays the parent's), keeping
@@ -1752,18 +2028,114 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
     launch_check("env step");
 }
 
-void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
-                      hipStream_t stream, const u64* goal_pos, const u64* goal_neg, u32* status)
+void launch_env_count(const CountArgs& a, hipStream_t stream)
 {
-    if (rows == 0)
+    if (a.rows == 0)
         return;
     size_t lds = 0;
-    const unsigned nw = waves_per_block(T, &lds);
-    const auto fn = variant(T, k_env_count<true, false>, k_env_count<true, true>, k_env_count<false, false>, k_env_count<false, true>);
+    const unsigned nw = waves_per_block(a.T, &lds);
+    const auto fn = variant(a.T, k_env_count<true, false>, k_env_count<true, true>, k_env_count<false, false>, k_env_count<false, true>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(grid_for(rows, nw)), dim3(nw * kWave), lds, stream, T, states, rows, words, count, goal, masks, cache,
-                       goal_pos, goal_neg, status);
+    hipLaunchKernelGGL(fn, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), lds, stream, a);
     launch_check("env count");
+}
+
+void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
+                      hipStream_t stream, const u64* goal_pos, const u64* goal_neg, u32* status, u32 instance)
+{
+    CountArgs a{};
+    a.T = T;
+    a.instances = 1;
+    a.states = states;
+    a.rows = rows;
+    a.words = words;
+    a.count = count;
+    a.goal = goal;
+    a.masks = masks;
+    a.cache = cache;
+    a.goal_pos = goal_pos;
+    a.goal_neg = goal_neg;
+    a.status = status;
+    a.instance = instance;
+    launch_env_count(a, stream);
+}
+
+u32 env_variant(const TaskDev& T)
+{
+    check_schemas(T);
+    return (staged(T) ? 1u : 0u) | (levels(T) ? 2u : 0u);
+}
+
+unsigned grouped_shape(const TaskDev* const* tasks, u32 n, size_t* lds_bytes, u32* wave_words)
+{
+    size_t hot = 0;
+    u32 wave = 0;
+    for (u32 k = 0; k < n; ++k)
+    {
+        const TaskDev& T = *tasks[k];
+        check_schemas(T);
+        if (staged(T))
+            hot = std::max(hot, static_cast<size_t>(T.hot_words) * 8);
+        wave = std::max(wave, wave_lds_words(T, levels(T)));
+    }
+    *wave_words = wave;
+    return block_shape(hot, static_cast<size_t>(wave) * 8, lds_bytes);
+}
+
+namespace
+{
+/// Blocks of a grouped launch: at most one chunk per block (chunks number at most rows / kChunkRows + instances).
+unsigned grouped_grid(u64 rows, u32 instances)
+{
+    return static_cast<unsigned>(std::min<u64>((rows + kChunkRows - 1) / kChunkRows + instances, u64{1} << 20));
+}
+
+template<class F>
+F variant_of(u32 v, F gs, F ss, F gl, F sl)
+{
+    return v == 0 ? gs : v == 1 ? ss : v == 2 ? gl : sl;
+}
+}  // namespace
+
+void launch_env_step_grouped(const EnvArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream)
+{
+    if (a.rows == 0)
+        return;
+    const auto fn = variant_of(v, k_env_step_grouped<false, false>, k_env_step_grouped<true, false>, k_env_step_grouped<false, true>,
+                               k_env_step_grouped<true, true>);
+    set_lds(reinterpret_cast<const void*>(fn), lds);
+    hipLaunchKernelGGL(fn, dim3(grouped_grid(a.rows, a.instances)), dim3(nw * kWave), lds, stream, a, v);
+    launch_check("env step (grouped)");
+}
+
+void launch_env_count_grouped(const CountArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream)
+{
+    if (a.rows == 0)
+        return;
+    const auto fn = variant_of(v, k_env_count_grouped<false, false>, k_env_count_grouped<true, false>, k_env_count_grouped<false, true>,
+                               k_env_count_grouped<true, true>);
+    set_lds(reinterpret_cast<const void*>(fn), lds);
+    hipLaunchKernelGGL(fn, dim3(grouped_grid(a.rows, a.instances)), dim3(nw * kWave), lds, stream, a, v);
+    launch_check("env count (grouped)");
+}
+
+void launch_group_rows(const i32* task_ids, u64 rows, u32 instances, u32* hist, u32* order, u32* starts, u32* chunk_start, u32* status,
+                       hipStream_t stream)
+{
+    launch_fill_u32(hist, instances + 1, 0, stream);
+    const unsigned blocks = static_cast<unsigned>(std::max<u64>(1, (rows + kGroupBlock * kGroupRowsPerThread - 1) / (kGroupBlock * kGroupRowsPerThread)));
+    if (rows)
+    {
+        hipLaunchKernelGGL(k_group_count, dim3(blocks), dim3(kGroupBlock), 0, stream, task_ids, rows, instances, hist, status);
+        launch_check("group count");
+    }
+    hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(kGroupBlock), 0, stream, hist, instances, starts, chunk_start);
+    launch_check("group scan");
+    if (rows)
+    {
+        hipLaunchKernelGGL(k_group_scatter, dim3(blocks), dim3(kGroupBlock), 0, stream, task_ids, rows, instances, hist, order);
+        launch_check("group scatter");
+    }
 }
 
 void launch_expand(const ExpandArgs& a, hipStream_t stream)
@@ -1800,31 +2172,31 @@ void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out
     launch_check("encode atoms");
 }
 
-void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
-                      u32* cache, const u32* init_cache, u32 init_count, u32 init_goal, hipStream_t stream)
+void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows, u32 words, const u8* mask, i32* task_ids, i32* steps,
+                      u8* at_goal, i32* count, u32* cache, u32 cache_width, u32* status, hipStream_t stream)
 {
     if (rows == 0)
         return;
     const u64 total = rows * words;
-    hipLaunchKernelGGL(k_env_reset, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(total, 256), 65536))), dim3(256), 0, stream, T,
-                       states, rows, words, mask, steps, at_goal, count, init_count, init_goal);
+    hipLaunchKernelGGL(k_env_reset, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(total, 256), 65536))), dim3(256), 0, stream, inst,
+                       instances, states, rows, words, mask, task_ids, steps, at_goal, count, status);
     launch_check("env reset");
     if (cache)
     {
-        const u64 cells = rows * cache_width(T);
+        const u64 cells = rows * cache_width;
         hipLaunchKernelGGL(k_env_reset_cache, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(cells, 256), 65536))), dim3(256), 0,
-                           stream, rows, cache_width(T), mask, cache, init_cache);
+                           stream, inst, instances, rows, cache_width, mask, task_ids, cache);
         launch_check("env reset cache");
     }
 }
 
-void launch_env_reset_goals(const TaskDev& T, u64 rows, u32 words, const u8* mask, u64* goal_pos, u64* goal_neg, const u64* task_pos,
-                            const u64* task_neg, bool keep_goals, u8* at_goal, u32* status, hipStream_t stream)
+void launch_env_reset_goals(const InstDev* inst, u32 instances, u64 rows, u32 words, const u8* mask, const i32* task_ids, u64* goal_pos,
+                            u64* goal_neg, bool keep_goals, u8* at_goal, u32* status, hipStream_t stream)
 {
     if (rows == 0)
         return;
-    hipLaunchKernelGGL(k_env_reset_goals, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream, T,
-                       rows, words, mask, goal_pos, goal_neg, task_pos, task_neg, keep_goals ? 1u : 0u, at_goal, status);
+    hipLaunchKernelGGL(k_env_reset_goals, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream, inst,
+                       instances, rows, words, mask, task_ids, goal_pos, goal_neg, keep_goals ? 1u : 0u, at_goal, status);
     launch_check("env reset goals");
 }
 

@@ -20,13 +20,49 @@ struct EnvCfg
     i32 autoreset;
 };
 
+/// What a step and a reset need of an instance besides its tables (device): the initial state, its count-cache row
+/// and schema masks, and the goal as masks over the instance's words.
+struct InstDev
+{
+    const u64* initial;     // [W]
+    const u32* init_cache;  // [num_schemas + 2]
+    const u8* init_masks;   // [num_schemas]
+    const u64* goal_pos;    // [W]
+    const u64* goal_neg;    // [W]
+    u32 W;
+    u32 init_count;
+    u32 init_goal;
+    u32 fluent_slots;
+    u32 variant;  // the kernel variant that runs the instance's rows (staged | levels << 1)
+    u32 reserved;
+};
+
+/// Rows of a batch over several instances grouped by instance (a counting sort of the task ids): order lists the rows
+/// of instance 0, then of instance 1, ...; instance k's rows are order[starts[k], starts[k + 1]), cut into chunks of
+/// kChunkRows rows numbered from chunk_start[k]. Rows whose task id names no instance are in no group.
+struct RowGroups
+{
+    const u32* order;
+    const u32* starts;       // [instances + 1]
+    const u32* chunk_start;  // [instances + 1]
+};
+constexpr u32 kChunkRows = 4;  // rows of a chunk: one block's share (one per wave of a block of 4 waves)
+constexpr u32 kMaxInstances = 65536;
+
 struct EnvArgs
 {
-    TaskDev T;
+    TaskDev T;             // the instance of a one-instance batch
+    const TaskDev* tasks;  // [instances] (device): every instance's tables, for a grouped launch
+    const InstDev* inst;   // [instances] (device)
+    u32 instances;
+    u32 wave_words;        // LDS words per wave of a grouped launch (the largest of its instances)
+    RowGroups groups;
     EnvCfg cfg;
     u64* states;
     u64 rows;
-    u32 words;  // row words of the batch (>= T.W)
+    u32 words;  // row words of the batch (>= every instance's W)
+    i32* task_ids;             // [rows]: each row's instance (null: instance 0); an autoreset writes the new one
+    const i32* next_task_ids;  // [rows]: the instance an autoresetting row restarts in (null: its own)
     i32* steps;
     u64* draws;
     u8* at_goal;
@@ -49,35 +85,74 @@ struct EnvArgs
     u32* counts;      // [rows, num_schemas + 2]: the count cache (per-schema counts, then the state's fingerprint), optional
     u64* goal_pos;    // [rows, words]: per-env goal masks (optional, with goal_neg)
     u64* goal_neg;
-    const u64* task_goal_pos;  // [W]: the task's goal as masks (device), written by an autoreset
-    const u64* task_goal_neg;
-    const u32* init_counts;  // [num_schemas + 2]: the initial state's cache row (device)
-    const u8* init_masks;  // [num_schemas]: the initial state's masks (device)
-    u32 init_count;
-    u32 init_goal;
     u32* status;
 };
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream);
 
-/// count[i] (successors), goal[i], masks [rows, num_schemas] and the count cache [rows, num_schemas + 2] of rows (each
-/// may be null).
+/// The arguments of a count over rows (refresh, the initial states, schema masks): count[i] (successors), goal[i],
+/// masks [rows, num_schemas] and the count cache [rows, num_schemas + 2] of the rows (each may be null); goal_pos /
+/// goal_neg [rows, words]: per-env goal masks (null: the instances' goal tests).
+struct CountArgs
+{
+    TaskDev T;
+    const TaskDev* tasks;
+    const InstDev* inst;
+    u32 instances;
+    u32 wave_words;
+    RowGroups groups;
+    const u64* states;
+    u64 rows;
+    u32 words;
+    const i32* task_ids;
+    i32* count;
+    u8* goal;
+    u8* masks;
+    u32* cache;
+    const u64* goal_pos;
+    const u64* goal_neg;
+    u32* status;
+    u32 instance;  // the instance of a one-instance count (its fingerprint salt)
+};
+
+void launch_env_count(const CountArgs& a, hipStream_t stream);
+/// A one-instance count of rows of instance `instance` (the common case of launch_env_count).
 void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
-                      hipStream_t stream, const u64* goal_pos = nullptr, const u64* goal_neg = nullptr, u32* status = nullptr);
+                      hipStream_t stream, const u64* goal_pos = nullptr, const u64* goal_neg = nullptr, u32* status = nullptr,
+                      u32 instance = 0);
+
+/// Groups the rows by task id (RowGroups): hist [instances + 1] and the three group arrays are device scratch; rows
+/// with a task id outside [0, instances) set kStatusTaskId.
+void launch_group_rows(const i32* task_ids, u64 rows, u32 instances, u32* hist, u32* order, u32* starts, u32* chunk_start,
+                       u32* status, hipStream_t stream);
+
+/// The kernel variant of an instance (InstDev::variant) and the block shape of a grouped launch over the instances of
+/// one variant: waves per block and dynamic LDS bytes, from the largest hot tables and per-wave region among them.
+u32 env_variant(const TaskDev& T);
+unsigned grouped_shape(const TaskDev* const* tasks, u32 n, size_t* lds_bytes, u32* wave_words);
+/// The grouped step / count of the rows of the instances of variant v (grid: enough blocks for every chunk).
+void launch_env_step_grouped(const EnvArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream);
+void launch_env_count_grouped(const CountArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream);
 
 /// Ascending true-atom slots of each row, -1 padded to max_atoms (State::slots, include/mymyr/state/state.hpp:96-101).
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream);
 
-/// Resets the rows with mask[i] != 0 (all if mask is null) to the initial state: steps 0, at_goal = init_goal,
-/// count = init_count, the count cache row = init_cache; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:207-240).
-void launch_env_reset(const TaskDev& T, u64* states, u64 rows, u32 words, const u8* mask, i32* steps, u8* at_goal, i32* count,
-                      u32* cache, const u32* init_cache, u32 init_count, u32 init_goal, hipStream_t stream);
+/// Resets the rows with mask[i] != 0 (all if mask is null) to the initial state of their instance task_ids[i] (null:
+/// instance 0; an id outside [0, instances) resets the row into instance 0, writes 0 there and sets kStatusTaskId):
+/// the instance's initial state in its words and zeros up to the batch's, steps 0, at_goal, count and the count cache
+/// row of the initial state; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:179-205, 223-255).
+void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows, u32 words, const u8* mask, i32* task_ids, i32* steps,
+                      u8* at_goal, i32* count, u32* cache, u32 cache_width, u32* status, hipStream_t stream);
 
-/// Per-env goal masks at a reset of the rows with mask[i] != 0: the task's goal (task_pos / task_neg [W]) written into
-/// them, or with keep_goals the given masks kept, checked against the task's fluent slots (kStatusGoalMask) and
-/// at_goal tested on the initial state with them.
-void launch_env_reset_goals(const TaskDev& T, u64 rows, u32 words, const u8* mask, u64* goal_pos, u64* goal_neg, const u64* task_pos,
-                            const u64* task_neg, bool keep_goals, u8* at_goal, u32* status, hipStream_t stream);
+/// Per-env goal masks at a reset of the rows with mask[i] != 0: the instance's goal written into them, or with
+/// keep_goals the given masks kept, checked against the instance's fluent slots (kStatusGoalMask) and at_goal tested
+/// on the initial state with them. Runs after launch_env_reset (it reads the rows' instances from task_ids).
+void launch_env_reset_goals(const InstDev* inst, u32 instances, u64 rows, u32 words, const u8* mask, const i32* task_ids, u64* goal_pos,
+                            u64* goal_neg, bool keep_goals, u8* at_goal, u32* status, hipStream_t stream);
+
+/// The count cache's fingerprint salt of an instance: 0 for instance 0, so a row's cache entry stands for its state
+/// and its instance.
+__host__ __device__ inline u64 instance_salt(u32 k) { return static_cast<u64>(k) * 0xD6E8FEB86659FD93ull; }
 
 /// Words of a count-cache row: the per-schema counts, then the 64-bit state fingerprint.
 __host__ __device__ inline u32 cache_width(const TaskDev& T) { return T.num_schemas + 2; }

@@ -28,29 +28,38 @@ def _p(t: torch.Tensor | None):
 
 
 class DeviceEnvPool:
-    """num_envs environments over one task, stepped together on the device (random policy unless actions are given)."""
+    """num_envs environments over one task, or over a task table (a list of instances of one domain: TaskTable,
+    include/mymyr/rl/task_table.hpp:1-28), stepped together on the device (random policy unless actions are given).
+    Over a table every env has an instance ("task_ids", int32 [num_envs], initially `task_ids` or all 0) and its rows
+    are the widest instance's words; reset(task_ids=...) moves envs to other instances and step(next_task_ids=...)
+    names the instance an autoresetting env restarts in."""
 
-    def __init__(self, task: Task, num_envs: int, *, seed: int = 0, max_steps: int | None = None, step_reward: float = 0.0,
+    def __init__(self, task: Task | list[Task], num_envs: int, *, seed: int = 0, max_steps: int | None = None, step_reward: float = 0.0,
                  goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
                  witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda",
-                 count_cache: bool = True, goals: bool = False):
+                 count_cache: bool = True, goals: bool = False, task_ids=None):
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
             raise ValueError("mymyr: dead_end must be 'no_successors' or 'none'")
-        self.task = task
+        self.tasks = list(task) if isinstance(task, (list, tuple)) else [task]
+        if not self.tasks:
+            raise ValueError("mymyr: TaskTable: no instances")
+        self.task = self.tasks[0]
         self.num_envs = num_envs
         self.first_env = first_env
-        self.words = task.words if words is None else words
-        if self.words < task.words:
-            raise ValueError(f"mymyr: env: state rows of {self.words} words; the task needs {task.words}")
-        self.label_width = max(1, task.label_width)
+        widest = max(t.words for t in self.tasks)
+        self.words = widest if words is None else words
+        if self.words < widest:
+            raise ValueError(f"mymyr: env: state rows of {self.words} words; the task needs {widest}")
+        self.label_width = max(1, max(t.label_width for t in self.tasks))
         self.device = torch.device(device)
         cfg = _lib.EnvConfig(seed, max_steps or 0, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
                              int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning), 0)
         h = ctypes.c_void_p()
-        check(lib.mya_env_create(task.handle, ctypes.byref(cfg), ctypes.byref(h)))
+        handles = (ctypes.c_void_p * len(self.tasks))(*[t.handle.value for t in self.tasks])
+        check(lib.mya_env_create_table(handles, len(self.tasks), ctypes.byref(cfg), ctypes.byref(h)))
         self._h = h
         N, W, L, dev = num_envs, self.words, self.label_width, self.device
         self.states = torch.zeros((N, W), dtype=torch.int64, device=dev)
@@ -68,37 +77,54 @@ class DeviceEnvPool:
         self.final_states: torch.Tensor | None = None
         # the count cache (the reference device env's EnvBatch::counts): per-schema successor counts of each row's
         # state plus its fingerprint, so a step counts only the reached states; zeros match no state
-        self.counts_cache = (torch.zeros((N, task.num_schemas + 2), dtype=torch.int32, device=dev) if count_cache else None)
+        self.counts_cache = (torch.zeros((N, self.task.num_schemas + 2), dtype=torch.int32, device=dev) if count_cache else None)
         # per-env goal masks (goals=True, CpuEnvPool's `goals`): goal_pos / goal_neg [N, W], the task's goal after a reset
         self.goal_pos = torch.zeros((N, W), dtype=torch.int64, device=dev) if goals else None
         self.goal_neg = torch.zeros((N, W), dtype=torch.int64, device=dev) if goals else None
+        # each env's instance (a table of several instances only)
+        self.task_ids = None
+        if len(self.tasks) > 1:
+            self.task_ids = torch.zeros(N, dtype=torch.int32, device=dev)
+            if task_ids is not None:
+                self.task_ids.copy_(torch.as_tensor(task_ids, dtype=torch.int32))
         self._batch = _lib.EnvBatch(self.states.data_ptr(), N, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
                                     self.at_goal.data_ptr(), first_env, _p(self.counts_cache), _p(self.goal_pos),
-                                    _p(self.goal_neg))
+                                    _p(self.goal_neg), _p(self.task_ids))
 
-    def initial_count(self) -> tuple[int, bool]:
+    def initial_count(self, instance: int = 0) -> tuple[int, bool]:
         c = ctypes.c_uint32()
         g = ctypes.c_uint8()
-        check(lib.mya_env_initial_count(self._h, ctypes.byref(c), ctypes.byref(g)))
+        check(lib.mya_env_initial_count(self._h, instance, ctypes.byref(c), ctypes.byref(g)))
         return c.value, bool(g.value)
 
-    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False) -> dict:
-        """Resets every env (or those with mask != 0) to the initial state; draws are kept. With per-env goals the task's
-        goal is written into goal_pos / goal_neg unless keep_goals (the masks written there stay, and at_goal is their
-        test on the initial state)."""
+    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False, task_ids=None) -> dict:
+        """Resets every env (or those with mask != 0) to the initial state of its instance; draws are kept. task_ids
+        (over a table) first sets the instances of the envs being reset. With per-env goals the instance's goal is
+        written into goal_pos / goal_neg unless keep_goals (the masks written there stay, and at_goal is their test on
+        the initial state)."""
         if mask is not None:
             mask = mask.to(device=self.device, dtype=torch.uint8).contiguous()
+        if task_ids is not None:
+            if self.task_ids is None:
+                raise ValueError("mymyr: env: task ids need a table of several instances")
+            ids = torch.as_tensor(task_ids, dtype=torch.int32).to(self.device)
+            if mask is None:
+                self.task_ids.copy_(ids)
+            else:
+                self.task_ids.copy_(torch.where(mask != 0, ids, self.task_ids))
         check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), int(keep_goals), _stream()))
         r = {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
+        if self.task_ids is not None:
+            r["task_ids"] = self.task_ids
         if self.goal_pos is not None:
             r["goal_pos"] = self.goal_pos
             r["goal_neg"] = self.goal_neg
         return r
 
     def step(self, actions: torch.Tensor | None = None, final_states: bool = False, labels: bool = True,
-             encode: int = 0) -> dict:
+             encode: int = 0, next_task_ids=None) -> dict:
         """One step of every env: actions [num_envs] int64 indices into the canonical successor order (None: the random
-        policy). encode > 0 also emits the observed states' true-atom slots ("atoms", int32 [num_envs, encode], -1
+        policy). next_task_ids [num_envs] (over a table): the instance each autoresetting env restarts in. encode > 0 also emits the observed states' true-atom slots ("atoms", int32 [num_envs, encode], -1
         padded) and applicable-schema masks ("masks", uint8 [num_envs, num_schemas]), both in library-owned device
         buffers taken over DLPack. Returns the step's arrays (views, overwritten by the next step)."""
         if actions is not None:
@@ -117,9 +143,18 @@ class DeviceEnvPool:
                                _p(fs), self.schema.data_ptr() if labels else None, self.binding.data_ptr() if labels else None,
                                self.label_width, self.words, self.invalid.data_ptr(), self.goal.data_ptr(), _p(atoms), _p(masks),
                                encode, 0)
-        check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(out), _p(actions), _stream()))
+        nxt = None
+        if next_task_ids is not None:
+            if self.task_ids is None:
+                raise ValueError("mymyr: env: next_task_ids needs a table of several instances")
+            nxt = torch.as_tensor(next_task_ids, dtype=torch.int32).to(self.device).contiguous()
+            if nxt.shape != (self.num_envs,):
+                raise ValueError(f"mymyr: env: next_task_ids must have shape ({self.num_envs},)")
+        check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(out), _p(actions), _p(nxt), _stream()))
         r = {"states": self.states, "reward": self.reward, "terminated": self.terminated, "truncated": self.truncated,
              "count": self.count, "steps": self.steps, "at_goal": self.at_goal, "goal": self.goal, "invalid": self.invalid}
+        if self.task_ids is not None:
+            r["task_ids"] = self.task_ids
         if labels:
             r["schema"] = self.schema
             r["binding"] = self.binding

@@ -50,6 +50,15 @@ TASKS = {
     "transport_xl": lambda: gen.transport(128, 32, 512, goals=32, seed=SEED),
 }
 
+# task tables: several instances of one domain (different sizes, so different row widths), stepped in one batch with a
+# per-row instance
+TABLES = {
+    "gridworld_table": [lambda: gen.gridworld(6, 6, 0.2, seed=1), lambda: gen.gridworld(12, 10, 0.2, seed=2),
+                        lambda: gen.gridworld(16, 16, 0.15, seed=3)],
+    "transport_table": [lambda: gen.transport(8, 2, 4, goals=3, seed=1), lambda: gen.transport(24, 6, 40, goals=6, seed=2),
+                        lambda: gen.transport(6, 2, 3, goals=2, seed=3)],
+}
+
 GRIDWORLD = EnvWorkload("gridworld", 1024, 256, {"seed": SEED, "step_reward": -1.0, "goal_reward": 0.0})
 TRANSPORT = EnvWorkload("transport", 65536, 512, {"seed": SEED})
 TRANSPORT_XL = EnvWorkload("transport_xl", 262144, 128, {"seed": SEED}, encode=True)
@@ -60,12 +69,20 @@ DEDUP_WORDS = 16
 DEDUP_DUP = 0.3
 
 
-def task_file(name: str, directory: str) -> str:
-    """Writes the workload's task text to directory/name.txt (once) and returns the path."""
-    path = os.path.join(directory, f"{name}.txt")
+def _write_once(path: str, text) -> str:
     if not os.path.exists(path):
-        os.makedirs(directory, exist_ok=True)
+        os.makedirs(os.path.dirname(path), exist_ok=True)
         with open(path + ".tmp", "w") as f:
-            f.write(TASKS[name]())
+            f.write(text())
         os.replace(path + ".tmp", path)
     return path
+
+
+def task_file(name: str, directory: str) -> str:
+    """Writes the workload's task text to directory/name.txt (once) and returns the path."""
+    return _write_once(os.path.join(directory, f"{name}.txt"), TASKS[name])
+
+
+def table_files(name: str, directory: str) -> list[str]:
+    """Writes the instances of task table `name` to directory/name_<i>.txt (once) and returns the paths."""
+    return [_write_once(os.path.join(directory, f"{name}_{i}.txt"), t) for i, t in enumerate(TABLES[name])]

@@ -208,6 +208,10 @@ class Task:
             self.statics.setdefault(p, set()).add(args)
         self.label_width = max([s[1] for s in self.schemas] + [0])
 
+    def pred_info(self) -> list:
+        """The predicates as (name, arity, kind) in declaration order."""
+        return [(nm, a, k) for k, a, nm in self.preds]
+
     # ---------------------------------------------------------------------------- compile
     def _static(self, p: int, args) -> bool:
         return tuple(args) in self.statics.get(p, ())
@@ -665,6 +669,184 @@ class Env:
             b["steps"][i] = t2
             out["count"][i] = c2
         return out
+
+
+class TableEnv:
+    """HostEnv over a task table: several instances of one domain, each row in the instance task_ids[i] names
+    (TaskTable, include/mymyr/rl/task_table.hpp:1-28; src/mymyr/rl/env.cpp:179-255, 351-528). Rows are `words` wide
+    (at least the widest instance); a row's words past its own instance's are padding that a step neither reads nor
+    writes, and a reset zeroes only what it may have dirtied (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138)."""
+
+    def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True):
+        if not tasks:
+            raise ValueError("mymyr: TaskTable: no instances")
+        for i, t in enumerate(tasks[1:], 1):
+            why = domain_mismatch(tasks[0], t)
+            if why:
+                raise ValueError(f"mymyr: TaskTable: instance {i} is not of the domain of instance 0: {why}")
+        self.envs = [Env(t, seed, max_steps, step_reward, goal_reward, dead_end_reward, dead_end, dead_end_terminal, autoreset)
+                     for t in tasks]
+        self.tasks = tasks
+        self.words = max(t.words for t in tasks)
+        self.label_width = max(1, max(t.label_width for t in tasks))
+        e = self.envs[0]
+        self.seed, self.max_steps, self.autoreset = seed, max_steps, autoreset
+        self.step_reward, self.goal_reward, self.dead_end_reward = e.step_reward, e.goal_reward, e.dead_end_reward
+        self.dead_end, self.dead_end_terminal = dead_end, dead_end_terminal
+
+    def _check_ids(self, ids) -> None:
+        bad = [(r, int(x)) for r, x in enumerate(ids) if x < 0 or x >= len(self.tasks)]
+        if bad:
+            r, x = bad[0]
+            raise ValueError(f"mymyr: task id {x} of row {r} is outside the table's {len(self.tasks)} instances")
+
+    def _reset_row(self, b: dict, i: int, inst: int, keep_goals: bool, dirty: int) -> None:
+        """reset_row (env.cpp:179-205) with TaskSuite::initial_row: the instance's initial state in its own words,
+        zeros up to the words the row may have dirtied."""
+        t = self.tasks[inst]
+        W = b["states"].shape[1]
+        w = t.words
+        z = min(W, max(w, dirty))
+        b["states"][i, :w] = t.initial
+        b["states"][i, w:z] = 0
+        b["task_ids"][i] = inst
+        b["steps"][i] = 0
+        if "goal_pos" in b and not keep_goals:
+            gp, gn = self.envs[inst].goal_masks(w)
+            b["goal_pos"][i, :w], b["goal_neg"][i, :w] = gp, gn
+            b["goal_pos"][i, w:z] = 0
+            b["goal_neg"][i, w:z] = 0
+
+    def _goal_row(self, b: dict, i: int) -> bool:
+        t = self.tasks[int(b["task_ids"][i])]
+        w = min(b["states"].shape[1], t.words)
+        if "goal_pos" in b:
+            return mask_goal(b["states"][i, :w], b["goal_pos"][i, :w], b["goal_neg"][i, :w])
+        return is_goal(t, b["states"][i, :w])
+
+    def reset(self, b: dict, mask=None, keep_goals: bool = False) -> None:
+        """HostEnv::reset (env.cpp:223-255) of the rows with mask[i] != 0 into their instances task_ids[i]: count
+        receives the initial states' successor counts; with keep_goals the rows' goal masks stay (checked against the
+        instance's fluent slots) and at_goal is their test on the initial state."""
+        n = b["states"].shape[0]
+        self._check_ids(b["task_ids"])
+        if keep_goals and "goal_pos" in b:
+            for i in range(n):
+                if mask is None or mask[i]:
+                    t = self.tasks[int(b["task_ids"][i])]
+                    if not goal_masks_fit(b["goal_pos"][i], b["goal_neg"][i], t.slots):
+                        raise ValueError(f"mymyr: env: goal masks in row {i} set fluent slots its instance does not have; "
+                                         "supply goals for the written instance")
+        W = b["states"].shape[1]
+        for i in range(n):
+            if mask is not None and not mask[i]:
+                continue
+            inst = int(b["task_ids"][i])
+            self._reset_row(b, i, inst, keep_goals, W)
+            b["count"][i] = self.envs[inst].init_count
+            b["at_goal"][i] = 1 if (self._goal_row(b, i) if "goal_pos" in b else self.envs[inst].init_goal) else 0
+
+    def step(self, b: dict, first_env: int = 0, actions=None, next_task_ids=None, final_words: int | None = None) -> dict:
+        """HostEnv::step (env.cpp:351-528) of every row in its own instance; an autoreset restarts a row in
+        next_task_ids[i] when given, else in its instance."""
+        n, W = b["states"].shape
+        self._check_ids(b["task_ids"])
+        if next_task_ids is not None:
+            self._check_ids(next_task_ids)
+        L = self.label_width
+        FW = W if final_words is None else final_words
+        out = {"reward": np.zeros(n, np.float32), "terminated": np.zeros(n, np.uint8), "truncated": np.zeros(n, np.uint8),
+               "count": np.zeros(n, np.int32), "schema": np.full(n, -1, np.int32), "binding": np.full((n, L), -1, np.int32),
+               "goal": np.zeros(n, np.uint8), "invalid": np.zeros(n, np.uint8),
+               "final_states": np.zeros((n, FW), np.uint64)}
+        goals = "goal_pos" in b
+        for i in range(n):
+            inst = int(b["task_ids"][i])
+            t = self.tasks[inst]
+            w = min(W, t.words)
+            row = b["states"][i, :w].copy()
+            already = bool(b["at_goal"][i])
+            succ = successors(t, row)
+            c = len(succ)
+            st = "goal" if already else "ok"
+            a = 0
+            if not already and c == 0:
+                st = "stuck"
+            elif not already and actions is not None:
+                if actions[i] < 0 or actions[i] >= c:
+                    st = "invalid"
+                else:
+                    a = int(actions[i])
+            elif not already:
+                a = successor_index(self.seed, first_env + i, int(b["draws"][i]), c)
+            b["draws"][i] += np.uint64(1)
+            if st == "ok":
+                out["schema"][i] = succ[a][0]
+                for k, o in enumerate(succ[a][1]):
+                    out["binding"][i, k] = o
+            out["invalid"][i] = 1 if st == "invalid" else 0
+            s2 = succ[a][2] if st == "ok" else row
+            g, c2 = already, c
+            if st == "ok":
+                g = mask_goal(s2, b["goal_pos"][i, :w], b["goal_neg"][i, :w]) if goals else is_goal(t, s2)
+                c2 = len(successors(t, s2))
+            dead = self.dead_end == "no_successors" and not g and ((st == "ok" and c2 == 0) or st == "stuck")
+            term = g or (dead and self.dead_end_terminal)
+            absorbed = already or (st == "stuck" and dead and self.dead_end_terminal)
+            t2 = int(b["steps"][i]) + (0 if absorbed else 1)
+            trunc = (not term) and self.max_steps and t2 >= self.max_steps
+            if absorbed:
+                r = np.float32(0.0)
+            else:
+                r = np.float32(self.step_reward + (self.goal_reward if g else np.float32(0.0)))
+                r = np.float32(r + (self.dead_end_reward if dead else np.float32(0.0)))
+            out["reward"][i] = r
+            out["terminated"][i] = 1 if term else 0
+            out["truncated"][i] = 1 if trunc else 0
+            out["goal"][i] = 1 if g else 0
+            out["final_states"][i, :w] = s2
+            if self.autoreset and (term or trunc):
+                nxt = int(next_task_ids[i]) if next_task_ids is not None else inst
+                self._reset_row(b, i, nxt, False, w)
+                out["count"][i] = self.envs[nxt].init_count
+                b["at_goal"][i] = 1 if (self._goal_row(b, i) if goals else self.envs[nxt].init_goal) else 0
+                continue
+            b["at_goal"][i] = 1 if g else 0
+            b["states"][i, :w] = s2
+            b["steps"][i] = t2
+            out["count"][i] = c2
+        return out
+
+
+def goal_masks_fit(gp, gn, fluent_slots: int) -> bool:
+    """Whether goal masks set no bit at or past fluent_slots (rl::goal_masks_fit, include/mymyr/rl/goal_masks.hpp:8-21)."""
+    for wi, (p, q) in enumerate(zip(np.asarray(gp, np.uint64), np.asarray(gn, np.uint64))):
+        x = int(p) | int(q)
+        lo = 64 * wi
+        if x and (x.bit_length() - 1 + lo) >= fluent_slots:
+            return False
+    return True
+
+
+def domain_mismatch(ref: Task, task: Task) -> str:
+    """Empty if `task` is of the domain of `ref`: the same action schemas (names, arities) and predicates (names,
+    arities, kinds) in the same order (TaskTable::domain_mismatch, src/mymyr/rl/task_table.cpp:75-100; text tasks
+    have no problem-local predicates)."""
+    if len(task.schemas) != len(ref.schemas):
+        return f"{len(task.schemas)} action schemas, instance 0 has {len(ref.schemas)}"
+    for s, (a, b) in enumerate(zip(task.schemas, ref.schemas)):
+        if a[0] != b[0] or a[1] != b[1]:
+            return f"action schema {s} is {a[0]}/{a[1]}, instance 0 has {b[0]}/{b[1]}"
+    kinds = {"S": "static", "F": "fluent", "D": "derived"}
+    rp, dp = ref.pred_info(), task.pred_info()
+    for d, (name, ar, kind) in enumerate(dp):
+        if d >= len(rp) or rp[d] != (name, ar, kind):
+            have = f"{rp[d][0]}/{rp[d][1]} ({kinds[rp[d][2]]})" if d < len(rp) else "no more"
+            return f"domain predicate {d} is {name}/{ar} ({kinds[kind]}), instance 0 has {have}"
+    if len(dp) != len(rp):
+        return f"{len(dp)} domain predicates, instance 0 has {len(rp)}"
+    return ""
 
 
 # ------------------------------------------------------------------------------------------------- BrFS

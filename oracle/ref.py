@@ -93,6 +93,12 @@ def lib() -> ctypes.CDLL:
             "mref_env_reset": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64]),
             "mref_env_step": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p]),
+            "mref_table_env_create": (c_void_p, [c_void_p, c_uint32, POINTER(EnvConfig)]),
+            "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                             c_void_p, c_void_p, c_void_p, c_int]),
+            "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32]),
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
             "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
         }
@@ -199,6 +205,45 @@ class RefEnv:
         rc = lib().mref_env_step(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), first_env, _p(actions),
                                  _p(reward), _p(terminated), _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal),
                                  _p(invalid), _p(final_states))
+        if rc != 0:
+            raise RuntimeError(_err())
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().mref_env_free(self._h)
+            self._h = c_void_p()
+
+
+class RefTableEnv:
+    """rl::HostEnv over TaskTable::create(tasks): several instances of one domain, per-row task ids."""
+
+    def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True):
+        self.tasks = tasks
+        self.cfg = EnvConfig(seed, max_steps, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
+                             int(dead_end_terminal), int(autoreset), 1, 0)
+        arr = (c_void_p * len(tasks))(*[t._h.value for t in tasks])
+        h = lib().mref_table_env_create(arr, len(tasks), ctypes.byref(self.cfg))
+        if not h:
+            raise RuntimeError(_err())
+        self._h = c_void_p(h)
+
+    def reset(self, states, steps, draws, at_goal, count, task_ids, goal_pos=None, goal_neg=None, mask=None, keep_goals=False):
+        rows, words = states.shape
+        if lib().mref_table_env_reset(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), _p(count),
+                                      _p(task_ids), _p(goal_pos), _p(goal_neg), _p(mask), int(keep_goals)) != 0:
+            raise RuntimeError(_err())
+
+    def step(self, states, steps, draws, at_goal, task_ids, goal_pos=None, goal_neg=None, first_env=0, actions=None,
+             next_task_ids=None, reward=None, terminated=None, truncated=None, count=None, schema=None, binding=None, goal=None,
+             invalid=None, final_states=None):
+        rows, words = states.shape
+        lw = 0 if binding is None else binding.shape[1]
+        fw = 0 if final_states is None else final_states.shape[1]
+        rc = lib().mref_table_env_step(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), first_env,
+                                       _p(task_ids), _p(goal_pos), _p(goal_neg), _p(actions), _p(next_task_ids), _p(reward),
+                                       _p(terminated), _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal), _p(invalid),
+                                       _p(final_states), fw)
         if rc != 0:
             raise RuntimeError(_err())
 

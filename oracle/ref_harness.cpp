@@ -349,6 +349,88 @@ int mref_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, 
         -1);
 }
 
+// A HostEnv over TaskTable::create(tasks) (include/mymyr/rl/task_table.hpp:69-75): several instances of one domain.
+// Null (and the table's message in mref_last_error) when the tasks are not of one domain.
+mref_env* mref_table_env_create(mref_task* const* tasks, uint32_t n, const mref_env_config* c)
+{
+    return guarded(
+        [&]() -> mref_env*
+        {
+            std::vector<TaskPtr> v;
+            for (uint32_t i = 0; i < n; ++i)
+                v.push_back(tasks[i]->task);
+            auto e = new mref_env;
+            e->env = std::make_unique<rl::HostEnv>(rl::TaskTable::create(std::move(v)), env_config(c));
+            return e;
+        },
+        nullptr);
+}
+
+// The batch of a table env: task_ids [rows] (null: instance 0), goal_pos / goal_neg [rows, words] (both or neither).
+static rl::EnvBatch table_batch(uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws, uint8_t* at_goal,
+                                uint64_t first_env, int32_t* task_ids, uint64_t* goal_pos, uint64_t* goal_neg)
+{
+    rl::EnvBatch b;
+    b.states = states;
+    b.rows = rows;
+    b.words = words;
+    b.steps = steps;
+    b.draws = draws;
+    b.at_goal = at_goal;
+    b.first_env = first_env;
+    b.task_ids = task_ids;
+    b.goal_pos = goal_pos;
+    b.goal_neg = goal_neg;
+    return b;
+}
+
+// HostEnv::reset over a table batch: mask [rows] (null: all), keep_goals.
+int mref_table_env_reset(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws,
+                         uint8_t* at_goal, int32_t* count, int32_t* task_ids, uint64_t* goal_pos, uint64_t* goal_neg,
+                         const uint8_t* mask, int keep_goals)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::EnvBatch b = table_batch(states, rows, words, steps, draws, at_goal, 0, task_ids, goal_pos, goal_neg);
+            e->env->reset(b, mask, count, keep_goals != 0);
+            return 0;
+        },
+        -1);
+}
+
+// HostEnv::step over a table batch: actions (null: the random policy), next_task_ids [rows] (null: an autoreset keeps
+// the row's instance); final_states [rows, final_words] (final_words 0: the batch's words).
+int mref_table_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws,
+                        uint8_t* at_goal, uint64_t first_env, int32_t* task_ids, uint64_t* goal_pos, uint64_t* goal_neg,
+                        const int64_t* actions, const int32_t* next_task_ids, float* reward, uint8_t* terminated,
+                        uint8_t* truncated, int32_t* count, int32_t* schema, int32_t* binding, uint32_t label_width,
+                        uint8_t* goal, uint8_t* invalid, uint64_t* final_states, uint32_t final_words)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::EnvBatch b = table_batch(states, rows, words, steps, draws, at_goal, first_env, task_ids, goal_pos, goal_neg);
+            rl::StepOutputs o;
+            o.reward = reward;
+            o.terminated = terminated;
+            o.truncated = truncated;
+            o.count = count;
+            o.schema = schema;
+            o.binding = binding;
+            o.label_width = label_width;
+            o.goal = goal;
+            o.invalid = invalid;
+            o.final_states = final_states;
+            o.words = final_words;
+            rl::Actions a;
+            a.v64 = actions;
+            e->env->step(b, o, a, next_task_ids, nullptr);
+            return 0;
+        },
+        -1);
+}
+
 // The CPU env pool (CpuEnvPool, `threads` workers) over `num_envs` envs: reset, then `steps` random-policy steps of
 // every env. seconds: wall time of the steps only. checksum: hash of the final pool states, rewards and counts.
 int mref_pool_run(mref_task* t, const mref_env_config* c, uint32_t num_envs, uint32_t threads, uint32_t steps,

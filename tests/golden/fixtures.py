@@ -64,3 +64,56 @@ def load(name: str):
 
 def task_path(name: str) -> str:
     return os.path.join(TASKS, f"{name}.txt")
+
+
+def arrays_digest(*arrays) -> str:
+    """sha256 of the arrays' bytes in order (each as given: the caller fixes the dtypes)."""
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(np.asarray(a)).tobytes())
+    return h.hexdigest()[:16]
+
+
+# Task-table env trajectories (rl::HostEnv over TaskTable::create, src/mymyr/rl/env.cpp:179-255, 351-528): per-row
+# instances, autoresets into the instances of next_task_ids, masked resets that move rows to other instances, and
+# keep_goals resets with per-env goal masks. Every input of a case is drawn here from numpy's PCG64 with the case's
+# seed, so the golden script, the oracle test and the device test replay the same trajectory.
+TABLE_CASES = {
+    # name: (table, rows, steps, env config, per-env goals, policy, seed)
+    "gridworld_ids": ("gridworld_table", 48, 40, {"seed": 3, "max_steps": 14, "step_reward": -1.0, "goal_reward": 5.0}, False,
+                      "random", 21),
+    "gridworld_goals": ("gridworld_table", 48, 40, {"seed": 4, "max_steps": 10, "step_reward": -0.5, "goal_reward": 2.0,
+                                                    "dead_end_reward": -3.0}, True, "given", 22),
+    "transport_ids": ("transport_table", 24, 16, {"seed": 5, "max_steps": 6}, True, "random", 23),
+    "gridworld_large": ("gridworld_table", 4096, 96, {"seed": 6, "max_steps": 30, "step_reward": -1.0, "goal_reward": 0.0}, False,
+                        "random", 24),
+    "transport_large": ("transport_table", 2048, 48, {"seed": 7, "max_steps": 16}, True, "given", 25),
+}
+# cases small enough for the oracle's pure-Python restatement
+TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids"]
+
+
+def table_inputs(case: str, instances: int) -> dict:
+    """The inputs of a table case: initial task ids, per step the next_task_ids (even steps; None on odd ones) and the
+    uniforms behind the given actions, and the two masked resets (step -> (mask, new task ids, keep_goals))."""
+    _, rows, steps, _, goals, _, seed = TABLE_CASES[case]
+    rng = np.random.default_rng(seed)
+    out = {"task_ids": rng.integers(0, instances, rows, dtype=np.int32), "next": [], "u": []}
+    for k in range(steps):
+        nxt = rng.integers(0, instances, rows, dtype=np.int32)
+        out["next"].append(nxt if k % 2 == 0 else None)
+        out["u"].append(rng.random(rows))
+    resets = {}
+    m = rng.random(rows) < 0.25
+    resets[steps // 2] = (m.astype(np.uint8), rng.integers(0, instances, rows, dtype=np.int32), False)
+    if goals:
+        m = rng.random(rows) < 0.25
+        resets[steps // 4] = (m.astype(np.uint8), None, True)
+    out["resets"] = resets
+    return out
+
+
+def given_actions(u, count) -> np.ndarray:
+    """The given policy's actions: uniform over [-1, count] (so some are invalid: -1 and count)."""
+    c = np.asarray(count, np.int64)
+    return np.floor(np.asarray(u) * (c + 2)).astype(np.int64) - 1

@@ -162,6 +162,67 @@ def make_env_small():
     dump("env_gridworld_small.json", env_trajectory(tiny, 16, 60))
 
 
+def table_trajectory(case: str) -> dict:
+    """A task-table env trajectory of the compiled reference (rl::HostEnv over TaskTable::create): the digest of the
+    batch after the first reset, after each masked reset and after every step."""
+    table, rows, steps, env, goals, policy, _ = fx.TABLE_CASES[case]
+    ts = [ref.RefTask(p) for p in workloads.table_files(table, fx.TASKS)]
+    I, W = len(ts), max(t.words for t in ts)
+    L = max(1, max(t.label_width for t in ts))
+    inp = fx.table_inputs(case, I)
+    e = ref.RefTableEnv(ts, **env)
+    S = np.zeros((rows, W), np.uint64)
+    st, dr, ag, cnt = np.zeros(rows, np.int32), np.zeros(rows, np.uint64), np.zeros(rows, np.uint8), np.zeros(rows, np.int32)
+    tid = inp["task_ids"].copy()
+    gp = np.zeros((rows, W), np.uint64) if goals else None
+    gn = np.zeros((rows, W), np.uint64) if goals else None
+    init = [t.initial_state(W) for t in ts]
+    e.reset(S, st, dr, ag, cnt, tid, gp, gn)
+    batch = lambda: [S, tid, st, dr, ag] + ([gp, gn] if goals else [])
+    resets = {"initial": fx.arrays_digest(*batch(), cnt)}
+    digests = []
+    totals = {"terminated": 0, "truncated": 0, "invalid": 0, "goal": 0, "instance_rows": [0] * I}
+    for k in range(steps):
+        if k in inp["resets"]:
+            mask, new_ids, keep = inp["resets"][k]
+            if new_ids is not None:
+                tid[mask == 1] = new_ids[mask == 1]
+            if keep:
+                for i in np.nonzero(mask)[0]:
+                    gp[i] = init[tid[i]]
+                    gn[i] = 0
+            e.reset(S, st, dr, ag, cnt, tid, gp, gn, mask=mask, keep_goals=keep)
+            resets[str(k)] = fx.arrays_digest(*batch(), cnt)
+        actions = fx.given_actions(inp["u"][k], cnt) if policy == "given" else None
+        R, term, trunc = np.zeros(rows, np.float32), np.zeros(rows, np.uint8), np.zeros(rows, np.uint8)
+        c, sch, bnd = np.zeros(rows, np.int32), np.zeros(rows, np.int32), np.zeros((rows, L), np.int32)
+        g, inv, fs = np.zeros(rows, np.uint8), np.zeros(rows, np.uint8), np.zeros((rows, W), np.uint64)
+        e.step(S, st, dr, ag, tid, gp, gn, first_env=5, actions=actions, next_task_ids=inp["next"][k], reward=R, terminated=term,
+               truncated=trunc, count=c, schema=sch, binding=bnd, goal=g, invalid=inv, final_states=fs)
+        digests.append(fx.arrays_digest(*batch(), R, term, trunc, c, sch, bnd, g, inv, fs))
+        cnt = c
+        for key, a in (("terminated", term), ("truncated", trunc), ("invalid", inv), ("goal", g)):
+            totals[key] += int(a.sum())
+        for i in range(I):
+            totals["instance_rows"][i] += int((tid == i).sum())
+    return {"case": case, "table": table, "rows": rows, "steps": steps, "words": W, "label_width": L, "resets": resets,
+            "digests": digests, "totals": totals}
+
+
+def make_env_table():
+    out = {case: table_trajectory(case) for case in fx.TABLE_CASES}
+    for case, r in out.items():
+        print(case, r["totals"], flush=True)
+    # the table's domain check (TaskTable::domain_mismatch, src/mymyr/rl/task_table.cpp:75-100)
+    mixed = [ref.RefTask(workloads.table_files("gridworld_table", fx.TASKS)[0]), ref.RefTask(workloads.table_files("transport_table", fx.TASKS)[0])]
+    try:
+        ref.RefTableEnv(mixed)
+        out["mismatch"] = None
+    except RuntimeError as ex:
+        out["mismatch"] = str(ex)
+    dump("env_table.json", out)
+
+
 def brfs_record(name, atoms="auto", **kw):
     t = ref.RefTask(fx.task_path(name), atoms)
     r = ref.brfs(t, **kw)
@@ -194,7 +255,7 @@ def main():
     a = ap.parse_args()
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
-             "env_small": make_env_small, "brfs": lambda: make_brfs(a.quick)}
+             "env_small": make_env_small, "env_table": make_env_table, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -1,0 +1,157 @@
+"""The device env over task tables (several instances of one domain, rows grouped by instance on the device) against
+the compiled reference's rl::HostEnv over TaskTable::create: every reset and step of the fixture's trajectories
+(tests/golden/env_table.json, from 24 to 4096 envs) digest-equal, through the C ABI (mymyr_amd.rl.DeviceEnvPool).
+Also: a table whose rows all sit in one instance steps exactly as a one-instance env of that task, task ids outside
+the table raise through the sticky status, and a grouped step replays from a HIP graph."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def u64(t):
+    return host(t).view(np.uint64)
+
+
+def load_tasks(golden, table):
+    from mymyr_amd import workloads
+    from mymyr_amd.task import Task
+
+    return [Task.from_text_file(p) for p in workloads.table_files(table, golden.TASKS)]
+
+
+def initial_rows(ts, W):
+    return [t.initial_state(W) for t in ts]
+
+
+def replay(golden, case: str):
+    from mymyr_amd import rl
+
+    g = golden.load("env_table.json")[case]
+    table, rows, steps, env, goals, policy, _ = golden.TABLE_CASES[case]
+    ts = load_tasks(golden, table)
+    inp = golden.table_inputs(case, len(ts))
+    print(f"table case {case}: {rows} envs x {steps} steps", flush=True)
+    pool = rl.DeviceEnvPool(ts, rows, first_env=5, goals=goals, task_ids=inp["task_ids"], **env)
+    assert (pool.words, pool.label_width) == (g["words"], g["label_width"])
+    W = pool.words
+    init = initial_rows(ts, W)
+
+    def batch():
+        b = [u64(pool.states), host(pool.task_ids), host(pool.steps), u64(pool.draws), host(pool.at_goal)]
+        return b + ([u64(pool.goal_pos), u64(pool.goal_neg)] if goals else [])
+
+    pool.reset()
+    assert golden.arrays_digest(*batch(), host(pool.count)) == g["resets"]["initial"], f"{case}: initial reset"
+    for k in range(steps):
+        if k in inp["resets"]:
+            mask, new, keep = inp["resets"][k]
+            if keep:
+                gp = u64(pool.goal_pos).copy()
+                ids = host(pool.task_ids)
+                for i in np.nonzero(mask)[0]:
+                    gp[i] = init[ids[i]]
+                pool.goal_pos.copy_(torch.from_numpy(gp.view(np.int64)))
+                pool.goal_neg[torch.from_numpy(mask.astype(bool)).to(pool.device)] = 0
+            pool.reset(torch.from_numpy(mask), keep_goals=keep, task_ids=None if new is None else torch.from_numpy(new))
+            assert golden.arrays_digest(*batch(), host(pool.count)) == g["resets"][str(k)], f"{case}: reset at step {k}"
+        acts = None
+        if policy == "given":
+            acts = torch.from_numpy(golden.given_actions(inp["u"][k], host(pool.count)))
+        nxt = inp["next"][k]
+        o = pool.step(actions=acts, final_states=True, next_task_ids=None if nxt is None else torch.from_numpy(nxt))
+        d = golden.arrays_digest(*batch(), host(o["reward"]), host(o["terminated"]), host(o["truncated"]), host(o["count"]),
+                                 host(o["schema"]), host(o["binding"]), host(o["goal"]), host(o["invalid"]), u64(o["final_states"]))
+        assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
+    pool.check()
+    return pool
+
+
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_large", "transport_large"])
+def test_table_env_matches_reference(golden, case):
+    replay(golden, case)
+
+
+@pytest.mark.parametrize("table", ["gridworld_table", "transport_table"])
+def test_one_instance_rows_step_as_the_task(golden, table):
+    """Rows that all sit in instance k (next_task_ids = k) step exactly as a one-instance env of task k with rows as
+    wide as the table's: the grouped kernels and the batch-order kernels agree word for word."""
+    from mymyr_amd import rl
+
+    ts = load_tasks(golden, table)
+    W = max(t.words for t in ts)
+    n = 1000
+    for k, t in enumerate(ts):
+        a = rl.DeviceEnvPool(ts, n, seed=9, max_steps=25, task_ids=np.full(n, k, np.int32), first_env=3)
+        b = rl.DeviceEnvPool(t, n, seed=9, max_steps=25, words=W, first_env=3)
+        a.reset()
+        b.reset()
+        nxt = torch.full((n,), k, dtype=torch.int32)
+        for step in range(30):
+            oa = a.step(next_task_ids=nxt, final_states=True)
+            ob = b.step(final_states=True)
+            for key in ("states", "reward", "terminated", "truncated", "count", "schema", "binding", "goal", "at_goal", "final_states"):
+                assert torch.equal(oa[key], ob[key]), f"{table} instance {k} step {step}: {key}"
+        a.check()
+        b.check()
+
+
+def test_task_ids_outside_the_table(golden):
+    from mymyr_amd import rl
+    from mymyr_amd._lib import MyaError
+
+    ts = load_tasks(golden, "gridworld_table")
+    pool = rl.DeviceEnvPool(ts, 64, task_ids=np.arange(64) % 3)
+    pool.reset()
+    pool.check()
+    # a reset into an id outside the table puts the row in instance 0 and raises at the check
+    with pytest.raises(MyaError, match="task id is outside the table's 3 instances"):
+        pool.reset(task_ids=np.where(np.arange(64) == 7, 5, np.arange(64) % 3))
+        pool.check()
+    assert int(pool.task_ids[7]) == 0
+    init0 = initial_rows(ts, pool.words)[0]
+    assert np.array_equal(u64(pool.states)[7], init0)
+    pool.check()
+    # next_task_ids outside the table: reported, the row keeps its instance
+    with pytest.raises(MyaError, match="task id is outside"):
+        pool.step(next_task_ids=np.full(64, -1, np.int32))
+        pool.check()
+    assert np.array_equal(host(pool.task_ids), np.where(np.arange(64) == 7, 0, np.arange(64) % 3))
+    pool.check()
+
+
+def test_grouped_step_graph_replay(golden):
+    """A grouped step (grouping kernels + per-variant step launches) captured into a HIP graph replays as eager steps."""
+    from mymyr_amd import rl
+
+    ts = load_tasks(golden, "transport_table")
+    n = 3000
+    ids = (np.arange(n) * 7) % 3
+    kw = dict(seed=4, max_steps=12, task_ids=ids)
+    a, b = rl.DeviceEnvPool(ts, n, **kw), rl.DeviceEnvPool(ts, n, **kw)
+    a.reset()
+    b.reset()
+    nxt = torch.from_numpy(((np.arange(n) * 5) % 3).astype(np.int32)).cuda()
+    a.step(next_task_ids=nxt)  # eager first call: scratch and LDS limits set up outside the capture
+    b.step(next_task_ids=nxt)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        a.step(next_task_ids=nxt)
+    for r in range(6):
+        graph.replay()
+        torch.cuda.synchronize()
+        ob = b.step(next_task_ids=nxt)
+        extra = (a.states.sum() + 1).item()  # eager work on the pool's arrays between replays
+        assert extra is not None
+        for key in ("states", "reward", "terminated", "truncated", "count", "at_goal", "task_ids"):
+            assert torch.equal(getattr(a, key), ob[key]), f"replay {r}: {key}"
+    a.check()
+    b.check()

@@ -1,0 +1,95 @@
+"""The oracle's task-table env (oracle/port.py TableEnv: several instances of one domain, per-row instances,
+autoresets into next_task_ids, masked resets into other instances, keep_goals resets with per-env masks) against the
+compiled reference's rl::HostEnv over TaskTable::create: every reset and every step of the fixture's trajectories
+(tests/golden/env_table.json) digest-equal, and the table's domain check with the reference's message."""
+
+import numpy as np
+import pytest
+
+from mymyr_amd import workloads
+from oracle import port
+
+
+def load_table(golden, table: str):
+    return [port.Task(open(p).read()) for p in workloads.table_files(table, golden.TASKS)]
+
+
+def replay_oracle(golden, case: str) -> None:
+    g = golden.load("env_table.json")[case]
+    table, rows, steps, env, goals, policy, _ = golden.TABLE_CASES[case]
+    ts = load_table(golden, table)
+    e = port.TableEnv(ts, **env)
+    assert (e.words, e.label_width) == (g["words"], g["label_width"])
+    inp = golden.table_inputs(case, len(ts))
+    W = e.words
+    b = {"states": np.zeros((rows, W), np.uint64), "steps": np.zeros(rows, np.int32), "draws": np.zeros(rows, np.uint64),
+         "at_goal": np.zeros(rows, np.uint8), "count": np.zeros(rows, np.int32), "task_ids": inp["task_ids"].copy()}
+    if goals:
+        b["goal_pos"] = np.zeros((rows, W), np.uint64)
+        b["goal_neg"] = np.zeros((rows, W), np.uint64)
+    batch = lambda: [b["states"], b["task_ids"], b["steps"], b["draws"], b["at_goal"]] + ([b["goal_pos"], b["goal_neg"]] if goals else [])
+    e.reset(b)
+    assert golden.arrays_digest(*batch(), b["count"]) == g["resets"]["initial"]
+    for k in range(steps):
+        if k in inp["resets"]:
+            mask, new, keep = inp["resets"][k]
+            if new is not None:
+                b["task_ids"][mask == 1] = new[mask == 1]
+            if keep:
+                for i in np.nonzero(mask)[0]:
+                    t = ts[b["task_ids"][i]]
+                    b["goal_pos"][i] = 0
+                    b["goal_pos"][i, : t.words] = t.initial
+                    b["goal_neg"][i] = 0
+            e.reset(b, mask=mask, keep_goals=keep)
+            assert golden.arrays_digest(*batch(), b["count"]) == g["resets"][str(k)], f"{case}: reset at step {k}"
+        acts = golden.given_actions(inp["u"][k], b["count"]) if policy == "given" else None
+        o = e.step(b, first_env=5, actions=acts, next_task_ids=inp["next"][k])
+        d = golden.arrays_digest(*batch(), o["reward"], o["terminated"], o["truncated"], o["count"], o["schema"], o["binding"],
+                                 o["goal"], o["invalid"], o["final_states"])
+        assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
+        b["count"] = o["count"]
+
+
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids"])
+def test_table_env_matches_reference(golden, case):
+    replay_oracle(golden, case)
+
+
+def test_table_fixture_exercises_the_rules(golden):
+    """The fixture's trajectories move rows between instances, truncate, terminate, and take invalid actions."""
+    g = golden.load("env_table.json")
+    for case in golden.TABLE_CASES:
+        t = g[case]["totals"]
+        assert all(n > 0 for n in t["instance_rows"]), case
+        assert t["truncated"] > 0, case
+    assert g["gridworld_goals"]["totals"]["invalid"] > 0 and g["gridworld_large"]["totals"]["terminated"] > 0
+    # instances of different widths: padding words exist in every table
+    for table in workloads.TABLES:
+        ts = load_table(golden, table)
+        assert len({t.words for t in ts}) > 1
+
+
+def test_domain_mismatch_message(golden):
+    g = golden.load("env_table.json")
+    grid = load_table(golden, "gridworld_table")[0]
+    trans = load_table(golden, "transport_table")[0]
+    with pytest.raises(ValueError) as ex:
+        port.TableEnv([grid, trans])
+    assert str(ex.value) == g["mismatch"]
+    # a planted change in one schema name or predicate kind is caught
+    assert port.domain_mismatch(grid, grid) == ""
+    other = load_table(golden, "gridworld_table")[1]
+    other.schemas[0] = ("walk",) + other.schemas[0][1:]
+    assert port.domain_mismatch(grid, other) == "action schema 0 is walk/2, instance 0 has move/2"
+    other = load_table(golden, "gridworld_table")[1]
+    other.preds[0] = ("F",) + other.preds[0][1:]
+    assert port.domain_mismatch(grid, other) == "domain predicate 0 is adj/2 (fluent), instance 0 has adj/2 (static)"
+
+
+def test_task_id_checks(golden):
+    e = port.TableEnv(load_table(golden, "gridworld_table"))
+    b = {"states": np.zeros((2, e.words), np.uint64), "steps": np.zeros(2, np.int32), "draws": np.zeros(2, np.uint64),
+         "at_goal": np.zeros(2, np.uint8), "count": np.zeros(2, np.int32), "task_ids": np.array([0, 3], np.int32)}
+    with pytest.raises(ValueError, match="task id 3 of row 1 is outside the table's 3 instances"):
+        e.reset(b)
