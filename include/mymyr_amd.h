@@ -90,6 +90,11 @@ uint64_t mya_hash_state(const uint64_t* w, uint32_t n);
  * host versions of the device code. */
 void mya_philox(uint64_t seed, uint64_t env, uint64_t draw, uint32_t purpose, uint32_t out[4]);
 uint32_t mya_successor_index(uint64_t seed, uint64_t env, uint64_t draw, uint32_t count);
+/* The instance of env `env`'s draw number `reset_count` under `seed` (rl::rng::instance_draw,
+ * include/mymyr/rl/rng.hpp:94-115): uniform over `instances` when m is 0, else indices[k] with k the number of the
+ * m - 1 ascending thresholds at most the draw's 32 bits (host arrays). */
+int32_t mya_instance_draw(uint64_t seed, uint64_t env, uint32_t reset_count, uint32_t instances, const uint32_t* thresholds,
+                          const int32_t* indices, uint32_t m);
 
 /* ---------------------------------------------------------------------------------------------------------- state set */
 
@@ -165,6 +170,16 @@ typedef struct mya_env_batch
      * neither reads nor writes them, and a reset zeroes the words it may have dirtied (TaskSuite::initial_row,
      * src/mymyr/rl/task_suite.cpp:130-138). */
     int32_t* task_ids;
+    /* Per-row RNG keys and env ids of the random policy (EnvBatch::seeds / env_ids, include/mymyr/rl/env.hpp:114-115),
+     * device, optional: null uses the config's seed and first_env + row. */
+    const uint64_t* seeds;
+    const uint32_t* env_ids;
+    /* The instance sampler's per-row counters and keys (EnvBatch::reset_counts / sampling_seeds, rl/env.hpp:116-120),
+     * device, optional: a row's next sampled instance is the draw of (its sampling key or the config's seed, its env
+     * id, reset_counts[row]); every reset and autoreset of the row advances its counter, sampled or not. Null
+     * reset_counts: no counting and no sampling. */
+    uint32_t* reset_counts;
+    const uint64_t* sampling_seeds;
 } mya_env_batch;
 
 /* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
@@ -203,20 +218,27 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out);
  * device images alive by reference: free the env before the tasks. */
 int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out);
 void mya_env_free(mya_env* env);
+/* The env's instance sampler (EnvConfig::sampling, include/mymyr/rl/env.hpp:89-91; rl/sampling.hpp): `instances`
+ * 0 turns it off, else it must be the table's instance count; m = 0 draws uniformly, else thresholds [m - 1]
+ * (ascending) and indices [m] (instances) are mymyr.rl.InstanceSampler's arrays (host memory, copied). Autoresets
+ * without next_task_ids, and resets with `sample`, of batches with reset counters draw from it. Errors follow
+ * check_sampling (src/mymyr/rl/env.cpp:137-153). Not while a step of the env is in flight on another stream. */
+int mya_env_set_sampling(mya_env* env, uint32_t instances, const uint32_t* thresholds, const int32_t* indices, uint32_t m);
 /* The initial state's successor count and goal flag of an instance (DeviceEnv::initial_count,
  * include/mymyr/cuda/env.hpp:161-162). */
 int mya_env_initial_count(const mya_env* env, uint32_t instance, uint32_t* count, uint8_t* goal);
 /* HostEnv::reset (env.cpp:179-205, 223-255): rows with mask[i] != 0 (device, optional) to the initial state of their
- * instance (batch->task_ids; an id outside the table resets the row into instance 0, writes 0 there and sets the sticky
- * status, as DeviceEnv::reset, include/mymyr/cuda/env.hpp:163-168), steps 0, at_goal and count (device, optional) of
- * that initial state; draws kept. With per-env goal masks, the instance's goal is written into them unless keep_goals,
+ * instance (batch->task_ids, or with `sample` the rows' next sampled instances, written there; an id outside the
+ * table resets the row into instance 0, writes 0 there and sets the sticky status, as DeviceEnv::reset,
+ * include/mymyr/cuda/env.hpp:163-168), steps 0, at_goal and count (device, optional) of that initial state; draws
+ * kept, reset counters advanced. With per-env goal masks, the instance's goal is written into them unless keep_goals,
  * in which case the given masks stay, at_goal is their test on the initial state, and masks that set fluent slots the
  * instance does not have set the sticky status (mya_env_check). Async on the stream. */
-int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals,
+int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals, int sample,
                   void* stream);
 /* HostEnv::step (env.cpp:530-548 / step_row_impl 351-528): actions (device, int64 [rows], optional: the random policy
  * when null); next_task_ids (device, int32 [rows], optional: the instance an autoresetting row restarts in; null: its
- * own). Async on the stream; device-side failures set the sticky status that mya_env_check reports: among them a
+ * next sampled instance when the env has a sampler and the batch reset counters, else its own). Async on the stream; device-side failures set the sticky status that mya_env_check reports: among them a
  * task id outside the table in batch->task_ids (the row is not stepped) or in next_task_ids (an autoresetting row
  * keeps its instance; DeviceEnv::step, include/mymyr/cuda/env.hpp:180-184). Over several instances the rows are
  * grouped by instance on the device first (a counting sort of task_ids into env-owned scratch, allocated on the

@@ -66,6 +66,10 @@ class EnvBatch(Structure):
         ("goal_pos", c_void_p),
         ("goal_neg", c_void_p),
         ("task_ids", c_void_p),
+        ("seeds", c_void_p),
+        ("env_ids", c_void_p),
+        ("reset_counts", c_void_p),
+        ("sampling_seeds", c_void_p),
     ]
 
 
@@ -183,6 +187,7 @@ def _load() -> ctypes.CDLL:
         "mya_hash_state": (c_uint64, [c_void_p, c_uint32]),
         "mya_philox": (None, [c_uint64, c_uint64, c_uint64, c_uint32, c_void_p]),
         "mya_successor_index": (c_uint32, [c_uint64, c_uint64, c_uint64, c_uint32]),
+        "mya_instance_draw": (c_int32, [c_uint64, c_uint64, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32]),
         "mya_hashset_create": (c_int, [c_uint64, c_uint32, c_double, c_uint64, POINTER(c_void_p)]),
         "mya_hashset_free": (None, [c_void_p]),
         "mya_hashset_insert": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p, POINTER(c_uint64), c_void_p]),
@@ -203,7 +208,8 @@ def _load() -> ctypes.CDLL:
         "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),
         "mya_env_create_table": (c_int, [c_void_p, c_uint32, POINTER(EnvConfig), POINTER(c_void_p)]),
         "mya_env_free": (None, [c_void_p]),
-        "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_void_p]),
+        "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_int, c_void_p]),
+        "mya_env_set_sampling": (c_int, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint32]),
         "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p, c_void_p]),
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_refresh": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),

@@ -186,6 +186,12 @@ uint32_t mya_successor_index(uint64_t seed, uint64_t env, uint64_t draw, uint32_
     return successor_index(seed, env, draw, count);
 }
 
+int32_t mya_instance_draw(uint64_t seed, uint64_t env, uint32_t reset_count, uint32_t instances, const uint32_t* thresholds,
+                          const int32_t* indices, uint32_t m)
+{
+    return instance_draw(seed, env, reset_count, instances, thresholds, indices, m);
+}
+
 int mya_hashset_create(uint64_t max_states, uint32_t words, double max_load, uint64_t batch, mya_hashset** out)
 {
     return guarded([&] {

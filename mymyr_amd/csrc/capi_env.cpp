@@ -41,6 +41,9 @@ struct mya_env
     u8* d_init_masks = nullptr;   // device [instances, num_schemas]
     u32* d_status = nullptr;
     u32* h_status = nullptr;
+    SamplerDev sampler{};          // the instance sampler (instances 0: off)
+    u32* d_thresholds = nullptr;   // device [m - 1]
+    i32* d_indices = nullptr;      // device [m]
     // grouped launches: per variant present, its block shape
     struct Launch
     {
@@ -137,7 +140,7 @@ std::string domain_mismatch(const TaskText& r, const TaskText& t)
 void free_env(mya_env* e)
 {
     for (void* p : std::initializer_list<void*>{e->d_status, e->d_inst, e->d_tasks, e->d_init, e->d_init_cache, e->d_init_masks, e->d_hist,
-                                                e->d_starts, e->d_chunks, e->d_order})
+                                                e->d_starts, e->d_chunks, e->d_order, e->d_thresholds, e->d_indices})
         dev_free(p);
     if (e->h_status)
         (void)hipHostFree(e->h_status);
@@ -286,6 +289,46 @@ void mya_env_free(mya_env* env)
         free_env(env);
 }
 
+int mya_env_set_sampling(mya_env* env, uint32_t instances, const uint32_t* thresholds, const int32_t* indices, uint32_t m)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        if (instances == 0)
+        {
+            env->sampler = SamplerDev{};
+            return;
+        }
+        // check_sampling (src/mymyr/rl/env.cpp:137-153)
+        if (instances != env->instances())
+            throw std::invalid_argument("mymyr: env: a sampler over " + std::to_string(instances) + " instances for " +
+                                        std::to_string(env->instances()));
+        if (m && (!thresholds || !indices))
+            throw std::invalid_argument("mymyr: env: a weighted sampler needs one threshold fewer than indices");
+        for (u32 k = 1; k + 1 < m; ++k)
+            if (thresholds[k] < thresholds[k - 1])
+                throw std::invalid_argument("mymyr: env: the sampler's thresholds are not ascending");
+        for (u32 k = 0; k < m; ++k)
+            if (indices[k] < 0 || static_cast<u32>(indices[k]) >= instances)
+                throw std::invalid_argument("mymyr: env: the sampler's instance " + std::to_string(indices[k]) + " is outside the " +
+                                            std::to_string(instances) + " instances");
+        dev_free(env->d_thresholds);
+        dev_free(env->d_indices);
+        env->d_thresholds = nullptr;
+        env->d_indices = nullptr;
+        env->sampler = SamplerDev{};
+        if (m)
+        {
+            env->d_thresholds = dev_alloc<u32>(std::max<u32>(1, m - 1), "sampler thresholds");
+            env->d_indices = dev_alloc<i32>(m, "sampler indices");
+            if (m > 1)
+                hip_check(hipMemcpy(env->d_thresholds, thresholds, (m - 1) * sizeof(u32), hipMemcpyHostToDevice), "sampler thresholds");
+            hip_check(hipMemcpy(env->d_indices, indices, m * sizeof(i32), hipMemcpyHostToDevice), "sampler indices");
+        }
+        env->sampler = SamplerDev{instances, m, env->d_thresholds, env->d_indices};
+    });
+}
+
 int mya_env_initial_count(const mya_env* env, uint32_t instance, uint32_t* count, uint8_t* goal)
 {
     return guarded([&] {
@@ -301,13 +344,20 @@ int mya_env_initial_count(const mya_env* env, uint32_t instance, uint32_t* count
     });
 }
 
-int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals, void* stream)
+int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, int32_t* count, int keep_goals, int sample,
+                  void* stream)
 {
     return guarded([&] {
         if (!env)
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
+        if (sample && !env->sampler.instances)
+            throw std::invalid_argument("mymyr: env: a sampling reset needs an instance sampler");
+        if (sample && batch->rows && !batch->reset_counts)
+            throw std::invalid_argument("mymyr: env: a sampling reset needs the reset counters");
         const auto s = static_cast<hipStream_t>(stream);
+        launch_env_reset_draw(env->sampler, env->cfg.seed, batch->first_env, batch->rows, mask, sample != 0, batch->task_ids, batch->reset_counts,
+                              batch->sampling_seeds, batch->env_ids, s);
         launch_env_reset(env->d_inst, env->instances(), batch->states, batch->rows, batch->words, mask, batch->task_ids, batch->steps,
                          batch->at_goal, count, batch->counts, cache_width(env->T0()), env->d_status, s);
         if (batch->goal_pos)
@@ -351,6 +401,11 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.words = batch->words;
         a.task_ids = batch->task_ids;
         a.next_task_ids = next_task_ids;
+        a.seeds = batch->seeds;
+        a.env_ids = batch->env_ids;
+        a.reset_counts = batch->reset_counts;
+        a.sampling_seeds = batch->sampling_seeds;
+        a.sampler = env->sampler;
         a.steps = batch->steps;
         a.draws = batch->draws;
         a.at_goal = batch->at_goal;

@@ -105,6 +105,36 @@ MYA_HD u32 below(u64 x, u32 n)
 
 MYA_HD u32 successor_index(u64 seed, u64 env, u64 draw, u32 count) { return below(philox_bits64(seed, env, draw, 0), count); }
 
+// ------------------------------------------------------------------------------------------------------ instance draws
+/// MurmurHash3's 32-bit finalizer.
+MYA_HD u32 fmix32(u32 x)
+{
+    x = (x ^ (x >> 16)) * 0x85EBCA6Bu;
+    x = (x ^ (x >> 13)) * 0xC2B2AE35u;
+    return x ^ (x >> 16);
+}
+
+/// The instance of env `env`'s draw number `reset_count` under `seed` (rl::rng::instance_draw,
+/// include/mymyr/rl/rng.hpp:94-115): a hash of the inputs; uniform over `instances` when m is 0, else indices[k] with k
+/// the number of the m - 1 ascending thresholds at most the draw's 32 bits.
+MYA_HD i32 instance_draw(u64 seed, u64 env, u32 reset_count, u32 instances, const u32* thresholds, const i32* indices, u32 m)
+{
+    const u32 key = fmix32(static_cast<u32>(seed) ^ fmix32(static_cast<u32>(seed >> 32) ^ 0x53414D50u));
+    const u32 bits = fmix32(key ^ fmix32(static_cast<u32>(env)) ^ fmix32(reset_count ^ 0x9E3779B9u));
+    if (m == 0)
+        return static_cast<i32>((static_cast<u64>(bits) * instances) >> 32);
+    u32 lo = 0, hi = m - 1;  // the first threshold above the draw
+    while (lo < hi)
+    {
+        const u32 mid = lo + (hi - lo) / 2;
+        if (thresholds[mid] <= bits)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return indices[lo];
+}
+
 // ------------------------------------------------------------------------------------------------------ errors
 /// Sticky device status bits (OR-ed into a device word, read by the host after the stream drains).
 enum StatusBit : u32

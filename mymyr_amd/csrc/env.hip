@@ -1228,7 +1228,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
                 a = static_cast<u32>(act);
         }
         else if (!already_goal)
-            a = successor_index(A.cfg.seed, A.first_env + i, A.draws[i], c);
+            a = successor_index(A.seeds ? A.seeds[i] : A.cfg.seed, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, A.draws[i], c);
         u32 rank = 0;
         if (st == kOk)
         {
@@ -1299,6 +1299,19 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     const bool reset = A.cfg.autoreset && (term || trunc);
     if (reset)
     {
+        // without next_task_ids the row restarts in its next sampled instance when the env has a sampler and the batch
+        // reset counters; every autoreset advances the row's counter
+        if (A.reset_counts)
+        {
+            const u32 rc = A.reset_counts[i];
+            if (!A.next_task_ids && A.sampler.instances)
+                next = static_cast<u32>(instance_draw(A.sampling_seeds ? A.sampling_seeds[i] : A.cfg.seed,
+                                                      A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, rc,
+                                                      A.sampler.instances, A.sampler.thresholds, A.sampler.indices, A.sampler.m));
+            wave_sync();  // every lane has read the counter before lane 0 advances it
+            if (lane == 0)
+                A.reset_counts[i] = rc + 1;
+        }
         const InstDev& J = A.inst[next];
         const u32 z = min(A.words, max(J.W, T.W));  // the words the row may have dirtied: its old and new instance's
         for (u32 q = lane; q < z; q += kWave)
@@ -1550,6 +1563,24 @@ __global__ void k_env_reset(const InstDev* inst, u32 instances, u64* states, u64
             if (count)
                 count[i] = static_cast<i32>(J.init_count);
         }
+    }
+}
+
+/// Per row before a reset: the drawn task id (sample) and the advanced reset counter.
+__global__ void k_env_reset_draw(SamplerDev sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, u32 sample, i32* task_ids,
+                                 u32* reset_counts, const u64* sampling_seeds, const u32* env_ids)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        if (mask && !mask[i])
+            continue;
+        if (!reset_counts)
+            continue;
+        const u32 rc = reset_counts[i];
+        if (sample && task_ids)
+            task_ids[i] = instance_draw(sampling_seeds ? sampling_seeds[i] : seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i, rc,
+                                        sampler.instances, sampler.thresholds, sampler.indices, sampler.m);
+        reset_counts[i] = rc + 1;
     }
 }
 
@@ -2188,6 +2219,16 @@ void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows,
                            stream, inst, instances, rows, cache_width, mask, task_ids, cache);
         launch_check("env reset cache");
     }
+}
+
+void launch_env_reset_draw(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
+                           u32* reset_counts, const u64* sampling_seeds, const u32* env_ids, hipStream_t stream)
+{
+    if (rows == 0 || !reset_counts)
+        return;
+    hipLaunchKernelGGL(k_env_reset_draw, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream,
+                       sampler, seed, first_env, rows, mask, sample ? 1u : 0u, task_ids, reset_counts, sampling_seeds, env_ids);
+    launch_check("env reset draw");
 }
 
 void launch_env_reset_goals(const InstDev* inst, u32 instances, u64 rows, u32 words, const u8* mask, const i32* task_ids, u64* goal_pos,

@@ -46,6 +46,15 @@ struct RowGroups
     const u32* starts;       // [instances + 1]
     const u32* chunk_start;  // [instances + 1]
 };
+/// An instance sampler on the device (rl/sampling.hpp): instances 0 is off; m 0 draws uniformly.
+struct SamplerDev
+{
+    u32 instances;
+    u32 m;
+    const u32* thresholds;  // [m - 1]
+    const i32* indices;     // [m]
+};
+
 constexpr u32 kChunkRows = 4;  // rows of a chunk: one block's share (one per wave of a block of 4 waves)
 constexpr u32 kMaxInstances = 65536;
 
@@ -62,7 +71,12 @@ struct EnvArgs
     u64 rows;
     u32 words;  // row words of the batch (>= every instance's W)
     i32* task_ids;             // [rows]: each row's instance (null: instance 0); an autoreset writes the new one
-    const i32* next_task_ids;  // [rows]: the instance an autoresetting row restarts in (null: its own)
+    const i32* next_task_ids;  // [rows]: the instance an autoresetting row restarts in (null: its sampled or own one)
+    const u64* seeds;          // [rows]: per-row keys of the random policy (null: cfg.seed)
+    const u32* env_ids;        // [rows]: per-row env ids (null: first_env + row)
+    u32* reset_counts;         // [rows]: the sampler's per-row counters (null: no counting, no sampling)
+    const u64* sampling_seeds; // [rows]: per-row sampling keys (null: cfg.seed)
+    SamplerDev sampler;
     i32* steps;
     u64* draws;
     u8* at_goal;
@@ -143,6 +157,11 @@ void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out
 /// row of the initial state; draws are kept (HostEnv::reset, src/mymyr/rl/env.cpp:179-205, 223-255).
 void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows, u32 words, const u8* mask, i32* task_ids, i32* steps,
                       u8* at_goal, i32* count, u32* cache, u32 cache_width, u32* status, hipStream_t stream);
+
+/// Before a reset of the rows with mask[i] != 0: with `sample` their task ids drawn from the sampler (with the rows'
+/// reset counters), then the counters advanced (HostEnv::reset, src/mymyr/rl/env.cpp:223-255).
+void launch_env_reset_draw(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
+                           u32* reset_counts, const u64* sampling_seeds, const u32* env_ids, hipStream_t stream);
 
 /// Per-env goal masks at a reset of the rows with mask[i] != 0: the instance's goal written into them, or with
 /// keep_goals the given masks kept, checked against the instance's fluent slots (kStatusGoalMask) and at_goal tested

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -27,6 +28,38 @@ def _p(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+class InstanceSampler:
+    """Draws the instance an env resets into (mymyr.rl.InstanceSampler, python/mymyr/rl/_sampling.py:16-104; the draw
+    is rl::rng::instance_draw, include/mymyr/rl/rng.hpp:94-115): uniform over num_instances, or weighted by `weights`
+    (finite, nonnegative, positive sum), as cumulative thresholds over 2^32 of the instances of positive weight."""
+
+    def __init__(self, num_instances: int, weights=None):
+        if num_instances < 1 or num_instances > 0x7FFFFFFF:
+            raise ValueError("mymyr: instance sampling needs between 1 and 2**31 - 1 instances")
+        self.num_instances = num_instances
+        self.weights = None
+        self.indices = np.empty(0, np.int32)
+        self.thresholds = np.empty(0, np.uint32)
+        if weights is not None:
+            values = np.asarray(weights, np.float64)
+            if values.shape != (num_instances,):
+                raise ValueError("mymyr: sampling weights need one value per instance")
+            if not np.isfinite(values).all() or (values < 0).any() or not (values > 0).any():
+                raise ValueError("mymyr: sampling weights must be finite, nonnegative and have a positive sum")
+            self.weights = tuple(float(v) for v in values)
+            self.indices = np.flatnonzero(values > 0).astype(np.int32)
+            positive = values[self.indices] / values.max()
+            cumulative = np.cumsum(positive / positive.sum())[:-1]
+            self.thresholds = np.minimum(np.floor(cumulative * 2**32), 0xFFFFFFFF).astype(np.uint32)
+
+    def sample(self, seed: int, env_id: int, reset_count: int) -> int:
+        """The instance of env `env_id`'s draw number `reset_count` under `seed` (host)."""
+        thr = np.ascontiguousarray(self.thresholds)
+        idx = np.ascontiguousarray(self.indices)
+        return int(lib.mya_instance_draw(seed & 0xFFFFFFFFFFFFFFFF, env_id, reset_count & 0xFFFFFFFF, self.num_instances,
+                                         thr.ctypes.data, idx.ctypes.data, len(idx)))
+
+
 class DeviceEnvPool:
     """num_envs environments over one task, or over a task table (a list of instances of one domain: TaskTable,
     include/mymyr/rl/task_table.hpp:1-28), stepped together on the device (random policy unless actions are given).
@@ -38,7 +71,8 @@ class DeviceEnvPool:
                  goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
                  witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda",
-                 count_cache: bool = True, goals: bool = False, task_ids=None):
+                 count_cache: bool = True, goals: bool = False, task_ids=None, sampler: InstanceSampler | None = None,
+                 env_ids=None, seeds=None, sampling_seeds=None, reset_counts: bool | None = None):
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
@@ -87,9 +121,35 @@ class DeviceEnvPool:
             self.task_ids = torch.zeros(N, dtype=torch.int32, device=dev)
             if task_ids is not None:
                 self.task_ids.copy_(torch.as_tensor(task_ids, dtype=torch.int32))
+        # per-row RNG keys and env ids (EnvBatch::seeds / env_ids), the sampler's per-row keys and reset counters
+        # (EnvBatch::sampling_seeds / reset_counts; on by default with a sampler)
+        def as_dev(a, unsigned, signed):  # unsigned words carried in a signed tensor with the same bits
+            if a is None:
+                return None
+            if isinstance(a, torch.Tensor):
+                return a.to(device=dev, dtype=torch.int64 if signed is np.int64 else torch.int32).contiguous()
+            return torch.from_numpy(np.ascontiguousarray(np.asarray(a).astype(unsigned)).view(signed)).to(dev)
+
+        self.seeds = as_dev(seeds, np.uint64, np.int64)
+        self.env_ids = as_dev(env_ids, np.uint32, np.int32)
+        self.sampling_seeds = as_dev(sampling_seeds, np.uint64, np.int64)
+        for name, t in (("seeds", self.seeds), ("env_ids", self.env_ids), ("sampling_seeds", self.sampling_seeds)):
+            if t is not None and t.shape != (N,):
+                raise ValueError(f"mymyr: env: {name} must have shape ({N},)")
+        self.reset_counts = None
+        if reset_counts or (reset_counts is None and sampler is not None):
+            self.reset_counts = torch.zeros(N, dtype=torch.int32, device=dev)
+        self.sampler = sampler
+        if sampler is not None:
+            if sampler.num_instances != len(self.tasks):
+                raise ValueError(f"mymyr: env: a sampler over {sampler.num_instances} instances for {len(self.tasks)}")
+            thr = np.ascontiguousarray(sampler.thresholds)
+            idx = np.ascontiguousarray(sampler.indices)
+            check(lib.mya_env_set_sampling(self._h, sampler.num_instances, thr.ctypes.data, idx.ctypes.data, len(idx)))
         self._batch = _lib.EnvBatch(self.states.data_ptr(), N, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
                                     self.at_goal.data_ptr(), first_env, _p(self.counts_cache), _p(self.goal_pos),
-                                    _p(self.goal_neg), _p(self.task_ids))
+                                    _p(self.goal_neg), _p(self.task_ids), _p(self.seeds), _p(self.env_ids), _p(self.reset_counts),
+                                    _p(self.sampling_seeds))
 
     def initial_count(self, instance: int = 0) -> tuple[int, bool]:
         c = ctypes.c_uint32()
@@ -97,11 +157,11 @@ class DeviceEnvPool:
         check(lib.mya_env_initial_count(self._h, instance, ctypes.byref(c), ctypes.byref(g)))
         return c.value, bool(g.value)
 
-    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False, task_ids=None) -> dict:
-        """Resets every env (or those with mask != 0) to the initial state of its instance; draws are kept. task_ids
-        (over a table) first sets the instances of the envs being reset. With per-env goals the instance's goal is
-        written into goal_pos / goal_neg unless keep_goals (the masks written there stay, and at_goal is their test on
-        the initial state)."""
+    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False, task_ids=None, sample: bool = False) -> dict:
+        """Resets every env (or those with mask != 0) to the initial state of its instance; draws are kept, reset
+        counters advance. task_ids (over a table) first sets the instances of the envs being reset; sample=True draws
+        them from the sampler instead. With per-env goals the instance's goal is written into goal_pos / goal_neg unless
+        keep_goals (the masks written there stay, and at_goal is their test on the initial state)."""
         if mask is not None:
             mask = mask.to(device=self.device, dtype=torch.uint8).contiguous()
         if task_ids is not None:
@@ -112,10 +172,13 @@ class DeviceEnvPool:
                 self.task_ids.copy_(ids)
             else:
                 self.task_ids.copy_(torch.where(mask != 0, ids, self.task_ids))
-        check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), int(keep_goals), _stream()))
+        check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), int(keep_goals), int(sample),
+                                _stream()))
         r = {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
         if self.task_ids is not None:
             r["task_ids"] = self.task_ids
+        if self.reset_counts is not None:
+            r["reset_counts"] = self.reset_counts
         if self.goal_pos is not None:
             r["goal_pos"] = self.goal_pos
             r["goal_neg"] = self.goal_neg

@@ -110,6 +110,24 @@ def successor_index(seed: int, env: int, draw: int, count: int) -> int:
 
 
 # ------------------------------------------------------------------------------------------------- task text
+def fmix32(x: int) -> int:
+    """MurmurHash3's 32-bit finalizer (rl::rng::fmix32, include/mymyr/rl/rng.hpp:86-92)."""
+    x &= M32
+    x = ((x ^ (x >> 16)) * 0x85EBCA6B) & M32
+    x = ((x ^ (x >> 13)) * 0xC2B2AE35) & M32
+    return x ^ (x >> 16)
+
+
+def instance_draw(seed: int, env: int, reset_count: int, instances: int, thresholds=(), indices=()) -> int:
+    """The instance of env's draw number reset_count (rl::rng::instance_draw, include/mymyr/rl/rng.hpp:94-115): uniform
+    over `instances` without indices, else indices[k] with k the number of thresholds at most the draw's 32 bits."""
+    value = fmix32((seed & M32) ^ fmix32(((seed >> 32) & M32) ^ 0x53414D50))
+    bits = fmix32(value ^ fmix32(env & M32) ^ fmix32((reset_count & M32) ^ 0x9E3779B9))
+    if len(indices) == 0:
+        return (bits * instances) >> 32
+    return int(indices[sum(1 for t in thresholds if int(t) <= bits)])
+
+
 class Task:
     """A classical task read from the text format (src/mymyr/formalism/text_format.cpp:22-197) and compiled to atom
     slots (src/mymyr/task/compile.cpp:803-915, 1363-1455; src/mymyr/task/task.cpp:106-143, 216-232)."""
@@ -678,7 +696,8 @@ class TableEnv:
     writes, and a reset zeroes only what it may have dirtied (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138)."""
 
     def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
-                 dead_end="no_successors", dead_end_terminal=True, autoreset=True):
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None):
+        """sampler: (instances, thresholds, indices) of an instance sampler (rl/sampling.hpp; empty arrays: uniform)."""
         if not tasks:
             raise ValueError("mymyr: TaskTable: no instances")
         for i, t in enumerate(tasks[1:], 1):
@@ -694,6 +713,18 @@ class TableEnv:
         self.seed, self.max_steps, self.autoreset = seed, max_steps, autoreset
         self.step_reward, self.goal_reward, self.dead_end_reward = e.step_reward, e.goal_reward, e.dead_end_reward
         self.dead_end, self.dead_end_terminal = dead_end, dead_end_terminal
+        self.sampler = sampler
+        if sampler is not None:
+            n, thr, idx = sampler
+            if n != len(tasks):
+                raise ValueError(f"mymyr: env: a sampler over {n} instances for {len(tasks)}")
+
+    def sample_row(self, b: dict, i: int) -> int:
+        """Row i's next sampled instance (HostEnv::sample_row, include/mymyr/rl/env.hpp:255-260)."""
+        n, thr, idx = self.sampler
+        key = int(b["sampling_seeds"][i]) if "sampling_seeds" in b else self.seed
+        env = int(b["env_ids"][i]) if "env_ids" in b else b.get("first_env", 0) + i
+        return instance_draw(key, env, int(b["reset_counts"][i]), n, thr, idx)
 
     def _check_ids(self, ids) -> None:
         bad = [(r, int(x)) for r, x in enumerate(ids) if x < 0 or x >= len(self.tasks)]
@@ -725,11 +756,20 @@ class TableEnv:
             return mask_goal(b["states"][i, :w], b["goal_pos"][i, :w], b["goal_neg"][i, :w])
         return is_goal(t, b["states"][i, :w])
 
-    def reset(self, b: dict, mask=None, keep_goals: bool = False) -> None:
-        """HostEnv::reset (env.cpp:223-255) of the rows with mask[i] != 0 into their instances task_ids[i]: count
-        receives the initial states' successor counts; with keep_goals the rows' goal masks stay (checked against the
-        instance's fluent slots) and at_goal is their test on the initial state."""
+    def reset(self, b: dict, mask=None, keep_goals: bool = False, sample: bool = False, first_env: int = 0) -> None:
+        """HostEnv::reset (env.cpp:223-255) of the rows with mask[i] != 0 into their instances task_ids[i] (with
+        `sample`, first drawn from the sampler): count receives the initial states' successor counts; with keep_goals
+        the rows' goal masks stay (checked against the instance's fluent slots) and at_goal is their test on the
+        initial state; reset counters advance for every reset row."""
         n = b["states"].shape[0]
+        if sample and self.sampler is None:
+            raise ValueError("mymyr: env: a sampling reset needs an instance sampler")
+        if sample and n and "reset_counts" not in b:
+            raise ValueError("mymyr: env: a sampling reset needs the reset counters")
+        if sample:
+            for i in range(n):
+                if mask is None or mask[i]:
+                    b["task_ids"][i] = self.sample_row(dict(b, first_env=first_env), i)
         self._check_ids(b["task_ids"])
         if keep_goals and "goal_pos" in b:
             for i in range(n):
@@ -744,6 +784,8 @@ class TableEnv:
                 continue
             inst = int(b["task_ids"][i])
             self._reset_row(b, i, inst, keep_goals, W)
+            if "reset_counts" in b:
+                b["reset_counts"][i] += np.uint32(1)
             b["count"][i] = self.envs[inst].init_count
             b["at_goal"][i] = 1 if (self._goal_row(b, i) if "goal_pos" in b else self.envs[inst].init_goal) else 0
 
@@ -779,7 +821,9 @@ class TableEnv:
                 else:
                     a = int(actions[i])
             elif not already:
-                a = successor_index(self.seed, first_env + i, int(b["draws"][i]), c)
+                key = int(b["seeds"][i]) if "seeds" in b else self.seed
+                env = int(b["env_ids"][i]) if "env_ids" in b else first_env + i
+                a = successor_index(key, env, int(b["draws"][i]), c)
             b["draws"][i] += np.uint64(1)
             if st == "ok":
                 out["schema"][i] = succ[a][0]
@@ -807,7 +851,14 @@ class TableEnv:
             out["goal"][i] = 1 if g else 0
             out["final_states"][i, :w] = s2
             if self.autoreset and (term or trunc):
-                nxt = int(next_task_ids[i]) if next_task_ids is not None else inst
+                if next_task_ids is not None:
+                    nxt = int(next_task_ids[i])
+                elif "reset_counts" in b and self.sampler is not None:
+                    nxt = self.sample_row(dict(b, first_env=first_env), i)
+                else:
+                    nxt = inst
+                if "reset_counts" in b:
+                    b["reset_counts"][i] += np.uint32(1)
                 self._reset_row(b, i, nxt, False, w)
                 out["count"][i] = self.envs[nxt].init_count
                 b["at_goal"][i] = 1 if (self._goal_row(b, i) if goals else self.envs[nxt].init_goal) else 0

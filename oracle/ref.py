@@ -93,12 +93,11 @@ def lib() -> ctypes.CDLL:
             "mref_env_reset": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64]),
             "mref_env_step": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p]),
-            "mref_table_env_create": (c_void_p, [c_void_p, c_uint32, POINTER(EnvConfig)]),
-            "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                             c_void_p, c_void_p, c_void_p, c_int]),
-            "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
-                                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+            "mref_table_env_create": (c_void_p, [c_void_p, c_uint32, POINTER(EnvConfig), c_uint32, c_void_p, c_void_p, c_uint32]),
+            "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int]),
+            "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32]),
+            "mref_instance_draw": (c_int32, [c_uint64, c_uint64, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32]),
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
             "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
         }
@@ -214,36 +213,55 @@ class RefEnv:
             self._h = c_void_p()
 
 
+class TableBatch(Structure):
+    _fields_ = [
+        ("states", c_void_p), ("rows", c_uint64), ("words", c_uint32), ("reserved", c_uint32), ("steps", c_void_p),
+        ("draws", c_void_p), ("at_goal", c_void_p), ("first_env", c_uint64), ("task_ids", c_void_p), ("goal_pos", c_void_p),
+        ("goal_neg", c_void_p), ("reset_counts", c_void_p), ("seeds", c_void_p), ("env_ids", c_void_p),
+        ("sampling_seeds", c_void_p),
+    ]
+
+
 class RefTableEnv:
-    """rl::HostEnv over TaskTable::create(tasks): several instances of one domain, per-row task ids."""
+    """rl::HostEnv over TaskTable::create(tasks): several instances of one domain, per-row task ids, with an instance
+    sampler when `sampler` = (instances, thresholds, indices) is given (thresholds / indices empty: uniform)."""
 
     def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
-                 dead_end="no_successors", dead_end_terminal=True, autoreset=True):
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None):
         self.tasks = tasks
         self.cfg = EnvConfig(seed, max_steps, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
                              int(dead_end_terminal), int(autoreset), 1, 0)
         arr = (c_void_p * len(tasks))(*[t._h.value for t in tasks])
-        h = lib().mref_table_env_create(arr, len(tasks), ctypes.byref(self.cfg))
+        inst, thr, idx = sampler if sampler is not None else (0, [], [])
+        self._thr = np.asarray(thr, np.uint32)
+        self._idx = np.asarray(idx, np.int32)
+        h = lib().mref_table_env_create(arr, len(tasks), ctypes.byref(self.cfg), inst, self._thr.ctypes.data, self._idx.ctypes.data,
+                                        len(self._idx))
         if not h:
             raise RuntimeError(_err())
         self._h = c_void_p(h)
 
-    def reset(self, states, steps, draws, at_goal, count, task_ids, goal_pos=None, goal_neg=None, mask=None, keep_goals=False):
-        rows, words = states.shape
-        if lib().mref_table_env_reset(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), _p(count),
-                                      _p(task_ids), _p(goal_pos), _p(goal_neg), _p(mask), int(keep_goals)) != 0:
+    @staticmethod
+    def batch(b: dict, first_env: int = 0) -> TableBatch:
+        """The harness batch over a dict of numpy arrays (states, steps, draws, at_goal, task_ids, and optionally
+        goal_pos, goal_neg, reset_counts, seeds, env_ids, sampling_seeds)."""
+        rows, words = b["states"].shape
+        g = lambda k: _p(b.get(k))
+        return TableBatch(b["states"].ctypes.data, rows, words, 0, g("steps"), g("draws"), g("at_goal"), first_env, g("task_ids"),
+                          g("goal_pos"), g("goal_neg"), g("reset_counts"), g("seeds"), g("env_ids"), g("sampling_seeds"))
+
+    def reset(self, b: dict, count, mask=None, keep_goals=False, sample=False, first_env=0):
+        tb = self.batch(b, first_env)
+        if lib().mref_table_env_reset(self._h, ctypes.byref(tb), _p(count), _p(mask), int(keep_goals), int(sample)) != 0:
             raise RuntimeError(_err())
 
-    def step(self, states, steps, draws, at_goal, task_ids, goal_pos=None, goal_neg=None, first_env=0, actions=None,
-             next_task_ids=None, reward=None, terminated=None, truncated=None, count=None, schema=None, binding=None, goal=None,
-             invalid=None, final_states=None):
-        rows, words = states.shape
+    def step(self, b: dict, first_env=0, actions=None, next_task_ids=None, reward=None, terminated=None, truncated=None, count=None,
+             schema=None, binding=None, goal=None, invalid=None, final_states=None):
+        tb = self.batch(b, first_env)
         lw = 0 if binding is None else binding.shape[1]
         fw = 0 if final_states is None else final_states.shape[1]
-        rc = lib().mref_table_env_step(self._h, states.ctypes.data, rows, words, _p(steps), _p(draws), _p(at_goal), first_env,
-                                       _p(task_ids), _p(goal_pos), _p(goal_neg), _p(actions), _p(next_task_ids), _p(reward),
-                                       _p(terminated), _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal), _p(invalid),
-                                       _p(final_states), fw)
+        rc = lib().mref_table_env_step(self._h, ctypes.byref(tb), _p(actions), _p(next_task_ids), _p(reward), _p(terminated),
+                                       _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal), _p(invalid), _p(final_states), fw)
         if rc != 0:
             raise RuntimeError(_err())
 
@@ -251,6 +269,12 @@ class RefTableEnv:
         if getattr(self, "_h", None) is not None and self._h.value:
             lib().mref_env_free(self._h)
             self._h = c_void_p()
+
+
+def instance_draw(seed, env, reset_count, instances, thresholds=(), indices=()) -> int:
+    thr = np.asarray(thresholds, np.uint32)
+    idx = np.asarray(indices, np.int32)
+    return int(lib().mref_instance_draw(seed, env, reset_count, instances, thr.ctypes.data, idx.ctypes.data, len(idx)))
 
 
 def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> tuple[float, int]:

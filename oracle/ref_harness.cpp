@@ -349,9 +349,11 @@ int mref_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, 
         -1);
 }
 
-// A HostEnv over TaskTable::create(tasks) (include/mymyr/rl/task_table.hpp:69-75): several instances of one domain.
-// Null (and the table's message in mref_last_error) when the tasks are not of one domain.
-mref_env* mref_table_env_create(mref_task* const* tasks, uint32_t n, const mref_env_config* c)
+// A HostEnv over TaskTable::create(tasks) (include/mymyr/rl/task_table.hpp:69-75): several instances of one domain,
+// with an instance sampler (rl/sampling.hpp) when sampled_instances > 0 (m = 0: uniform; else thresholds [m - 1] and
+// indices [m]). Null (and the table's message in mref_last_error) when the tasks are not of one domain.
+mref_env* mref_table_env_create(mref_task* const* tasks, uint32_t n, const mref_env_config* c, uint32_t sampled_instances,
+                                const uint32_t* thresholds, const int32_t* indices, uint32_t m)
 {
     return guarded(
         [&]() -> mref_env*
@@ -359,58 +361,84 @@ mref_env* mref_table_env_create(mref_task* const* tasks, uint32_t n, const mref_
             std::vector<TaskPtr> v;
             for (uint32_t i = 0; i < n; ++i)
                 v.push_back(tasks[i]->task);
+            rl::EnvConfig cfg = env_config(c);
+            cfg.sampling.instances = sampled_instances;
+            if (m)
+            {
+                cfg.sampling.thresholds.assign(thresholds, thresholds + m - 1);
+                cfg.sampling.indices.assign(indices, indices + m);
+            }
             auto e = new mref_env;
-            e->env = std::make_unique<rl::HostEnv>(rl::TaskTable::create(std::move(v)), env_config(c));
+            e->env = std::make_unique<rl::HostEnv>(rl::TaskTable::create(std::move(v)), cfg);
             return e;
         },
         nullptr);
 }
 
-// The batch of a table env: task_ids [rows] (null: instance 0), goal_pos / goal_neg [rows, words] (both or neither).
-static rl::EnvBatch table_batch(uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws, uint8_t* at_goal,
-                                uint64_t first_env, int32_t* task_ids, uint64_t* goal_pos, uint64_t* goal_neg)
+// The arrays of a table batch (rl::EnvBatch, include/mymyr/rl/env.hpp:96-135); null arrays are absent.
+struct mref_table_batch
+{
+    uint64_t* states;
+    uint64_t rows;
+    uint32_t words;
+    uint32_t reserved;
+    int32_t* steps;
+    uint64_t* draws;
+    uint8_t* at_goal;
+    uint64_t first_env;
+    int32_t* task_ids;
+    uint64_t* goal_pos;
+    uint64_t* goal_neg;
+    uint32_t* reset_counts;
+    const uint64_t* seeds;
+    const uint32_t* env_ids;
+    const uint64_t* sampling_seeds;
+};
+
+static rl::EnvBatch table_batch(const mref_table_batch* t)
 {
     rl::EnvBatch b;
-    b.states = states;
-    b.rows = rows;
-    b.words = words;
-    b.steps = steps;
-    b.draws = draws;
-    b.at_goal = at_goal;
-    b.first_env = first_env;
-    b.task_ids = task_ids;
-    b.goal_pos = goal_pos;
-    b.goal_neg = goal_neg;
+    b.states = t->states;
+    b.rows = t->rows;
+    b.words = t->words;
+    b.steps = t->steps;
+    b.draws = t->draws;
+    b.at_goal = t->at_goal;
+    b.first_env = t->first_env;
+    b.task_ids = t->task_ids;
+    b.goal_pos = t->goal_pos;
+    b.goal_neg = t->goal_neg;
+    b.reset_counts = t->reset_counts;
+    b.seeds = t->seeds;
+    b.env_ids = t->env_ids;
+    b.sampling_seeds = t->sampling_seeds;
     return b;
 }
 
-// HostEnv::reset over a table batch: mask [rows] (null: all), keep_goals.
-int mref_table_env_reset(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws,
-                         uint8_t* at_goal, int32_t* count, int32_t* task_ids, uint64_t* goal_pos, uint64_t* goal_neg,
-                         const uint8_t* mask, int keep_goals)
+// HostEnv::reset over a table batch: mask [rows] (null: all), keep_goals, sample (draw the reset rows' instances).
+int mref_table_env_reset(mref_env* e, const mref_table_batch* t, int32_t* count, const uint8_t* mask, int keep_goals, int sample)
 {
     return guarded(
         [&]() -> int
         {
-            rl::EnvBatch b = table_batch(states, rows, words, steps, draws, at_goal, 0, task_ids, goal_pos, goal_neg);
-            e->env->reset(b, mask, count, keep_goals != 0);
+            rl::EnvBatch b = table_batch(t);
+            e->env->reset(b, mask, count, keep_goals != 0, sample != 0);
             return 0;
         },
         -1);
 }
 
-// HostEnv::step over a table batch: actions (null: the random policy), next_task_ids [rows] (null: an autoreset keeps
-// the row's instance); final_states [rows, final_words] (final_words 0: the batch's words).
-int mref_table_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, int32_t* steps, uint64_t* draws,
-                        uint8_t* at_goal, uint64_t first_env, int32_t* task_ids, uint64_t* goal_pos, uint64_t* goal_neg,
-                        const int64_t* actions, const int32_t* next_task_ids, float* reward, uint8_t* terminated,
-                        uint8_t* truncated, int32_t* count, int32_t* schema, int32_t* binding, uint32_t label_width,
-                        uint8_t* goal, uint8_t* invalid, uint64_t* final_states, uint32_t final_words)
+// HostEnv::step over a table batch: actions (null: the random policy), next_task_ids [rows] (null: an autoreset restarts
+// in the row's next sampled instance with reset counters and a sampler, else in its own); final_states
+// [rows, final_words] (final_words 0: the batch's words).
+int mref_table_env_step(mref_env* e, const mref_table_batch* t, const int64_t* actions, const int32_t* next_task_ids, float* reward,
+                        uint8_t* terminated, uint8_t* truncated, int32_t* count, int32_t* schema, int32_t* binding,
+                        uint32_t label_width, uint8_t* goal, uint8_t* invalid, uint64_t* final_states, uint32_t final_words)
 {
     return guarded(
         [&]() -> int
         {
-            rl::EnvBatch b = table_batch(states, rows, words, steps, draws, at_goal, first_env, task_ids, goal_pos, goal_neg);
+            rl::EnvBatch b = table_batch(t);
             rl::StepOutputs o;
             o.reward = reward;
             o.terminated = terminated;
@@ -429,6 +457,13 @@ int mref_table_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t w
             return 0;
         },
         -1);
+}
+
+// rl::rng::instance_draw (include/mymyr/rl/rng.hpp:94-115)
+int32_t mref_instance_draw(uint64_t seed, uint64_t env, uint32_t reset_count, uint32_t instances, const uint32_t* thresholds,
+                           const int32_t* indices, uint32_t m)
+{
+    return rl::rng::instance_draw(seed, env, reset_count, instances, thresholds, indices, m);
 }
 
 // The CPU env pool (CpuEnvPool, `threads` workers) over `num_envs` envs: reset, then `steps` random-policy steps of

@@ -75,42 +75,88 @@ def arrays_digest(*arrays) -> str:
 
 
 # Task-table env trajectories (rl::HostEnv over TaskTable::create, src/mymyr/rl/env.cpp:179-255, 351-528): per-row
-# instances, autoresets into the instances of next_task_ids, masked resets that move rows to other instances, and
-# keep_goals resets with per-env goal masks. Every input of a case is drawn here from numpy's PCG64 with the case's
-# seed, so the golden script, the oracle test and the device test replay the same trajectory.
+# instances, autoresets into the instances of next_task_ids or of an instance sampler (rl/sampling.hpp), masked resets
+# that move rows to other instances or draw them, keep_goals resets with per-env goal masks, and per-row RNG keys and
+# env ids. Every input of a case is drawn here from numpy's PCG64 with the case's seed, so the golden script, the
+# oracle test and the device test replay the same trajectory.
 TABLE_CASES = {
-    # name: (table, rows, steps, env config, per-env goals, policy, seed)
-    "gridworld_ids": ("gridworld_table", 48, 40, {"seed": 3, "max_steps": 14, "step_reward": -1.0, "goal_reward": 5.0}, False,
-                      "random", 21),
-    "gridworld_goals": ("gridworld_table", 48, 40, {"seed": 4, "max_steps": 10, "step_reward": -0.5, "goal_reward": 2.0,
-                                                    "dead_end_reward": -3.0}, True, "given", 22),
-    "transport_ids": ("transport_table", 24, 16, {"seed": 5, "max_steps": 6}, True, "random", 23),
-    "gridworld_large": ("gridworld_table", 4096, 96, {"seed": 6, "max_steps": 30, "step_reward": -1.0, "goal_reward": 0.0}, False,
-                        "random", 24),
-    "transport_large": ("transport_table", 2048, 48, {"seed": 7, "max_steps": 16}, True, "given", 25),
+    "gridworld_ids": dict(table="gridworld_table", rows=48, steps=40, seed=21, policy="random",
+                          env={"seed": 3, "max_steps": 14, "step_reward": -1.0, "goal_reward": 5.0}),
+    "gridworld_goals": dict(table="gridworld_table", rows=48, steps=40, seed=22, policy="given", goals=True,
+                            env={"seed": 4, "max_steps": 10, "step_reward": -0.5, "goal_reward": 2.0, "dead_end_reward": -3.0}),
+    "transport_ids": dict(table="transport_table", rows=24, steps=16, seed=23, policy="random", goals=True,
+                          env={"seed": 5, "max_steps": 6}),
+    "gridworld_sampled": dict(table="gridworld_table", rows=40, steps=40, seed=26, policy="random", sampler="uniform", keys=True,
+                              env={"seed": 8, "max_steps": 9, "step_reward": -1.0}),
+    "transport_weighted": dict(table="transport_table", rows=24, steps=20, seed=27, policy="given", goals=True,
+                               sampler=[2.0, 0.0, 1.0], keys=True, env={"seed": 9, "max_steps": 5}),
+    "gridworld_large": dict(table="gridworld_table", rows=4096, steps=96, seed=24, policy="random",
+                            env={"seed": 6, "max_steps": 30, "step_reward": -1.0, "goal_reward": 0.0}),
+    "transport_large": dict(table="transport_table", rows=2048, steps=48, seed=25, policy="given", goals=True,
+                            env={"seed": 7, "max_steps": 16}),
+    "gridworld_sampled_large": dict(table="gridworld_table", rows=4096, steps=64, seed=28, policy="random", sampler=[1.0, 3.0, 2.0],
+                                    keys=True, env={"seed": 10, "max_steps": 20}),
 }
 # cases small enough for the oracle's pure-Python restatement
-TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids"]
+TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted"]
+
+
+def sampler_arrays(weights) -> tuple[np.ndarray, np.ndarray]:
+    """An instance sampler's arrays from its weights (mymyr.rl.InstanceSampler, python/mymyr/rl/_sampling.py:29-39):
+    indices = the instances of positive weight, thresholds = the cumulative distribution of their weights (scaled by the
+    largest) over 2^32, without its last entry. Uniform (None): both empty."""
+    if weights is None:
+        return np.empty(0, np.uint32), np.empty(0, np.int32)
+    w = np.asarray(weights, np.float64)
+    idx = np.flatnonzero(w > 0).astype(np.int32)
+    positive = w[idx] / w.max()
+    cum = np.cumsum(positive / positive.sum())[:-1]
+    return np.minimum(np.floor(cum * 2**32), 0xFFFFFFFF).astype(np.uint32), idx
+
+
+def case_sampler(case: str, instances: int):
+    """(instances, thresholds, indices) of the case's sampler, or None."""
+    spec = TABLE_CASES[case].get("sampler")
+    if spec is None:
+        return None
+    thr, idx = sampler_arrays(None if spec == "uniform" else spec)
+    return instances, thr, idx
 
 
 def table_inputs(case: str, instances: int) -> dict:
-    """The inputs of a table case: initial task ids, per step the next_task_ids (even steps; None on odd ones) and the
-    uniforms behind the given actions, and the two masked resets (step -> (mask, new task ids, keep_goals))."""
-    _, rows, steps, _, goals, _, seed = TABLE_CASES[case]
-    rng = np.random.default_rng(seed)
+    """The inputs of a table case: initial task ids, per step the next_task_ids (even steps without a sampler; None
+    otherwise) and the uniforms behind the given actions, the masked resets (step -> (mask, new task ids, keep_goals,
+    sample)), and with `keys` the per-row RNG keys, env ids and sampling keys."""
+    c = TABLE_CASES[case]
+    rows, steps, goals, sampler = c["rows"], c["steps"], c.get("goals", False), c.get("sampler")
+    rng = np.random.default_rng(c["seed"])
     out = {"task_ids": rng.integers(0, instances, rows, dtype=np.int32), "next": [], "u": []}
     for k in range(steps):
         nxt = rng.integers(0, instances, rows, dtype=np.int32)
-        out["next"].append(nxt if k % 2 == 0 else None)
+        given = k % 2 == 0 if sampler is None else k % 4 == 1
+        out["next"].append(nxt if given else None)
         out["u"].append(rng.random(rows))
     resets = {}
     m = rng.random(rows) < 0.25
-    resets[steps // 2] = (m.astype(np.uint8), rng.integers(0, instances, rows, dtype=np.int32), False)
+    resets[steps // 2] = (m.astype(np.uint8), rng.integers(0, instances, rows, dtype=np.int32), False, False)
     if goals:
         m = rng.random(rows) < 0.25
-        resets[steps // 4] = (m.astype(np.uint8), None, True)
+        resets[steps // 4] = (m.astype(np.uint8), None, True, False)
+    if sampler is not None:
+        m = rng.random(rows) < 0.4
+        resets[3 * steps // 4] = (m.astype(np.uint8), None, False, True)
     out["resets"] = resets
+    if c.get("keys"):
+        out["seeds"] = rng.integers(0, 2**63, rows, dtype=np.int64).view(np.uint64)
+        out["env_ids"] = rng.integers(0, 2**32, rows, dtype=np.uint64).astype(np.uint32)
+        out["sampling_seeds"] = rng.integers(0, 2**63, rows, dtype=np.int64).view(np.uint64)
     return out
+
+
+def table_state(b: dict) -> list:
+    """The batch arrays a table case's digests cover, in order (those the batch has)."""
+    keys = ("states", "task_ids", "steps", "draws", "at_goal", "goal_pos", "goal_neg", "reset_counts")
+    return [b[k] for k in keys if b.get(k) is not None]
 
 
 def given_actions(u, count) -> np.ndarray:

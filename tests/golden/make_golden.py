@@ -162,49 +162,64 @@ def make_env_small():
     dump("env_gridworld_small.json", env_trajectory(tiny, 16, 60))
 
 
+def table_batch_arrays(case: str, inp: dict, W: int) -> dict:
+    """The batch arrays of a table case, zeroed, with the case's task ids, per-row keys and reset counters."""
+    c = fx.TABLE_CASES[case]
+    rows = c["rows"]
+    b = {"states": np.zeros((rows, W), np.uint64), "steps": np.zeros(rows, np.int32), "draws": np.zeros(rows, np.uint64),
+         "at_goal": np.zeros(rows, np.uint8), "task_ids": inp["task_ids"].copy()}
+    if c.get("goals"):
+        b["goal_pos"] = np.zeros((rows, W), np.uint64)
+        b["goal_neg"] = np.zeros((rows, W), np.uint64)
+    if c.get("sampler") is not None:
+        b["reset_counts"] = np.zeros(rows, np.uint32)
+    for k in ("seeds", "env_ids", "sampling_seeds"):
+        if k in inp:
+            b[k] = inp[k]
+    return b
+
+
 def table_trajectory(case: str) -> dict:
     """A task-table env trajectory of the compiled reference (rl::HostEnv over TaskTable::create): the digest of the
     batch after the first reset, after each masked reset and after every step."""
-    table, rows, steps, env, goals, policy, _ = fx.TABLE_CASES[case]
+    c = fx.TABLE_CASES[case]
+    table, rows, steps, policy = c["table"], c["rows"], c["steps"], c["policy"]
     ts = [ref.RefTask(p) for p in workloads.table_files(table, fx.TASKS)]
     I, W = len(ts), max(t.words for t in ts)
     L = max(1, max(t.label_width for t in ts))
     inp = fx.table_inputs(case, I)
-    e = ref.RefTableEnv(ts, **env)
-    S = np.zeros((rows, W), np.uint64)
-    st, dr, ag, cnt = np.zeros(rows, np.int32), np.zeros(rows, np.uint64), np.zeros(rows, np.uint8), np.zeros(rows, np.int32)
-    tid = inp["task_ids"].copy()
-    gp = np.zeros((rows, W), np.uint64) if goals else None
-    gn = np.zeros((rows, W), np.uint64) if goals else None
+    e = ref.RefTableEnv(ts, sampler=fx.case_sampler(case, I), **c["env"])
+    b = table_batch_arrays(case, inp, W)
+    cnt = np.zeros(rows, np.int32)
     init = [t.initial_state(W) for t in ts]
-    e.reset(S, st, dr, ag, cnt, tid, gp, gn)
-    batch = lambda: [S, tid, st, dr, ag] + ([gp, gn] if goals else [])
-    resets = {"initial": fx.arrays_digest(*batch(), cnt)}
+    e.reset(b, cnt, first_env=5)
+    state = lambda: fx.table_state(b)
+    resets = {"initial": fx.arrays_digest(*state(), cnt)}
     digests = []
     totals = {"terminated": 0, "truncated": 0, "invalid": 0, "goal": 0, "instance_rows": [0] * I}
     for k in range(steps):
         if k in inp["resets"]:
-            mask, new_ids, keep = inp["resets"][k]
+            mask, new_ids, keep, sample = inp["resets"][k]
             if new_ids is not None:
-                tid[mask == 1] = new_ids[mask == 1]
+                b["task_ids"][mask == 1] = new_ids[mask == 1]
             if keep:
                 for i in np.nonzero(mask)[0]:
-                    gp[i] = init[tid[i]]
-                    gn[i] = 0
-            e.reset(S, st, dr, ag, cnt, tid, gp, gn, mask=mask, keep_goals=keep)
-            resets[str(k)] = fx.arrays_digest(*batch(), cnt)
+                    b["goal_pos"][i] = init[b["task_ids"][i]]
+                    b["goal_neg"][i] = 0
+            e.reset(b, cnt, mask=mask, keep_goals=keep, sample=sample, first_env=5)
+            resets[str(k)] = fx.arrays_digest(*state(), cnt)
         actions = fx.given_actions(inp["u"][k], cnt) if policy == "given" else None
         R, term, trunc = np.zeros(rows, np.float32), np.zeros(rows, np.uint8), np.zeros(rows, np.uint8)
-        c, sch, bnd = np.zeros(rows, np.int32), np.zeros(rows, np.int32), np.zeros((rows, L), np.int32)
+        cc, sch, bnd = np.zeros(rows, np.int32), np.zeros(rows, np.int32), np.zeros((rows, L), np.int32)
         g, inv, fs = np.zeros(rows, np.uint8), np.zeros(rows, np.uint8), np.zeros((rows, W), np.uint64)
-        e.step(S, st, dr, ag, tid, gp, gn, first_env=5, actions=actions, next_task_ids=inp["next"][k], reward=R, terminated=term,
-               truncated=trunc, count=c, schema=sch, binding=bnd, goal=g, invalid=inv, final_states=fs)
-        digests.append(fx.arrays_digest(*batch(), R, term, trunc, c, sch, bnd, g, inv, fs))
-        cnt = c
+        e.step(b, first_env=5, actions=actions, next_task_ids=inp["next"][k], reward=R, terminated=term, truncated=trunc, count=cc,
+               schema=sch, binding=bnd, goal=g, invalid=inv, final_states=fs)
+        digests.append(fx.arrays_digest(*state(), R, term, trunc, cc, sch, bnd, g, inv, fs))
+        cnt = cc
         for key, a in (("terminated", term), ("truncated", trunc), ("invalid", inv), ("goal", g)):
             totals[key] += int(a.sum())
         for i in range(I):
-            totals["instance_rows"][i] += int((tid == i).sum())
+            totals["instance_rows"][i] += int((b["task_ids"] == i).sum())
     return {"case": case, "table": table, "rows": rows, "steps": steps, "words": W, "label_width": L, "resets": resets,
             "digests": digests, "totals": totals}
 
@@ -220,6 +235,17 @@ def make_env_table():
         out["mismatch"] = None
     except RuntimeError as ex:
         out["mismatch"] = str(ex)
+    # instance draws (rl::rng::instance_draw, include/mymyr/rl/rng.hpp:94-115): uniform and weighted
+    rng = np.random.default_rng(31)
+    draws = []
+    for weights in (None, [1.0, 1.0], [1.0, 0.0, 3.0], [0.5, 2.0, 0.0, 1.5, 7.0]):
+        thr, idx = fx.sampler_arrays(weights)
+        n = 5 if weights is None else len(weights)
+        for _ in range(24):
+            seed, env, count = int(rng.integers(0, 2**63)), int(rng.integers(0, 2**32)), int(rng.integers(0, 2**32))
+            draws.append({"weights": weights, "seed": seed, "env": env, "reset_count": count, "instances": n,
+                          "draw": ref.instance_draw(seed, env, count, n, thr, idx)})
+    out["instance_draws"] = draws
     dump("env_table.json", out)
 
 

@@ -35,24 +35,34 @@ def replay(golden, case: str):
     from mymyr_amd import rl
 
     g = golden.load("env_table.json")[case]
-    table, rows, steps, env, goals, policy, _ = golden.TABLE_CASES[case]
-    ts = load_tasks(golden, table)
+    c = golden.TABLE_CASES[case]
+    rows, steps, goals = c["rows"], c["steps"], c.get("goals", False)
+    ts = load_tasks(golden, c["table"])
     inp = golden.table_inputs(case, len(ts))
     print(f"table case {case}: {rows} envs x {steps} steps", flush=True)
-    pool = rl.DeviceEnvPool(ts, rows, first_env=5, goals=goals, task_ids=inp["task_ids"], **env)
+    sampler = None
+    if c.get("sampler") is not None:
+        sampler = rl.InstanceSampler(len(ts), None if c["sampler"] == "uniform" else c["sampler"])
+    pool = rl.DeviceEnvPool(ts, rows, first_env=5, goals=goals, task_ids=inp["task_ids"], sampler=sampler, seeds=inp.get("seeds"),
+                            env_ids=inp.get("env_ids"), sampling_seeds=inp.get("sampling_seeds"), **c["env"])
     assert (pool.words, pool.label_width) == (g["words"], g["label_width"])
     W = pool.words
     init = initial_rows(ts, W)
 
-    def batch():
-        b = [u64(pool.states), host(pool.task_ids), host(pool.steps), u64(pool.draws), host(pool.at_goal)]
-        return b + ([u64(pool.goal_pos), u64(pool.goal_neg)] if goals else [])
+    def state():
+        b = {"states": u64(pool.states), "task_ids": host(pool.task_ids), "steps": host(pool.steps), "draws": u64(pool.draws),
+             "at_goal": host(pool.at_goal)}
+        if goals:
+            b["goal_pos"], b["goal_neg"] = u64(pool.goal_pos), u64(pool.goal_neg)
+        if pool.reset_counts is not None:
+            b["reset_counts"] = host(pool.reset_counts).view(np.uint32)
+        return golden.table_state(b)
 
     pool.reset()
-    assert golden.arrays_digest(*batch(), host(pool.count)) == g["resets"]["initial"], f"{case}: initial reset"
+    assert golden.arrays_digest(*state(), host(pool.count)) == g["resets"]["initial"], f"{case}: initial reset"
     for k in range(steps):
         if k in inp["resets"]:
-            mask, new, keep = inp["resets"][k]
+            mask, new, keep, sample = inp["resets"][k]
             if keep:
                 gp = u64(pool.goal_pos).copy()
                 ids = host(pool.task_ids)
@@ -60,21 +70,22 @@ def replay(golden, case: str):
                     gp[i] = init[ids[i]]
                 pool.goal_pos.copy_(torch.from_numpy(gp.view(np.int64)))
                 pool.goal_neg[torch.from_numpy(mask.astype(bool)).to(pool.device)] = 0
-            pool.reset(torch.from_numpy(mask), keep_goals=keep, task_ids=None if new is None else torch.from_numpy(new))
-            assert golden.arrays_digest(*batch(), host(pool.count)) == g["resets"][str(k)], f"{case}: reset at step {k}"
+            pool.reset(torch.from_numpy(mask), keep_goals=keep, task_ids=None if new is None else torch.from_numpy(new), sample=sample)
+            assert golden.arrays_digest(*state(), host(pool.count)) == g["resets"][str(k)], f"{case}: reset at step {k}"
         acts = None
-        if policy == "given":
+        if c["policy"] == "given":
             acts = torch.from_numpy(golden.given_actions(inp["u"][k], host(pool.count)))
         nxt = inp["next"][k]
         o = pool.step(actions=acts, final_states=True, next_task_ids=None if nxt is None else torch.from_numpy(nxt))
-        d = golden.arrays_digest(*batch(), host(o["reward"]), host(o["terminated"]), host(o["truncated"]), host(o["count"]),
+        d = golden.arrays_digest(*state(), host(o["reward"]), host(o["terminated"]), host(o["truncated"]), host(o["count"]),
                                  host(o["schema"]), host(o["binding"]), host(o["goal"]), host(o["invalid"]), u64(o["final_states"]))
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
     pool.check()
     return pool
 
 
-@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_large", "transport_large"])
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
+                                  "gridworld_large", "transport_large", "gridworld_sampled_large"])
 def test_table_env_matches_reference(golden, case):
     replay(golden, case)
 

@@ -14,25 +14,37 @@ def load_table(golden, table: str):
     return [port.Task(open(p).read()) for p in workloads.table_files(table, golden.TASKS)]
 
 
-def replay_oracle(golden, case: str) -> None:
-    g = golden.load("env_table.json")[case]
-    table, rows, steps, env, goals, policy, _ = golden.TABLE_CASES[case]
-    ts = load_table(golden, table)
-    e = port.TableEnv(ts, **env)
-    assert (e.words, e.label_width) == (g["words"], g["label_width"])
-    inp = golden.table_inputs(case, len(ts))
-    W = e.words
+def table_batch(golden, case: str, inp: dict, W: int) -> dict:
+    c = golden.TABLE_CASES[case]
+    rows = c["rows"]
     b = {"states": np.zeros((rows, W), np.uint64), "steps": np.zeros(rows, np.int32), "draws": np.zeros(rows, np.uint64),
-         "at_goal": np.zeros(rows, np.uint8), "count": np.zeros(rows, np.int32), "task_ids": inp["task_ids"].copy()}
-    if goals:
+         "at_goal": np.zeros(rows, np.uint8), "task_ids": inp["task_ids"].copy()}
+    if c.get("goals"):
         b["goal_pos"] = np.zeros((rows, W), np.uint64)
         b["goal_neg"] = np.zeros((rows, W), np.uint64)
-    batch = lambda: [b["states"], b["task_ids"], b["steps"], b["draws"], b["at_goal"]] + ([b["goal_pos"], b["goal_neg"]] if goals else [])
-    e.reset(b)
-    assert golden.arrays_digest(*batch(), b["count"]) == g["resets"]["initial"]
-    for k in range(steps):
+    if c.get("sampler") is not None:
+        b["reset_counts"] = np.zeros(rows, np.uint32)
+    for k in ("seeds", "env_ids", "sampling_seeds"):
+        if k in inp:
+            b[k] = inp[k]
+    return b
+
+
+def replay_oracle(golden, case: str) -> None:
+    g = golden.load("env_table.json")[case]
+    c = golden.TABLE_CASES[case]
+    ts = load_table(golden, c["table"])
+    e = port.TableEnv(ts, sampler=golden.case_sampler(case, len(ts)), **c["env"])
+    assert (e.words, e.label_width) == (g["words"], g["label_width"])
+    inp = golden.table_inputs(case, len(ts))
+    b = table_batch(golden, case, inp, e.words)
+    b["count"] = np.zeros(c["rows"], np.int32)
+    state = lambda: golden.table_state(b)
+    e.reset(b, first_env=5)
+    assert golden.arrays_digest(*state(), b["count"]) == g["resets"]["initial"]
+    for k in range(c["steps"]):
         if k in inp["resets"]:
-            mask, new, keep = inp["resets"][k]
+            mask, new, keep, sample = inp["resets"][k]
             if new is not None:
                 b["task_ids"][mask == 1] = new[mask == 1]
             if keep:
@@ -41,19 +53,51 @@ def replay_oracle(golden, case: str) -> None:
                     b["goal_pos"][i] = 0
                     b["goal_pos"][i, : t.words] = t.initial
                     b["goal_neg"][i] = 0
-            e.reset(b, mask=mask, keep_goals=keep)
-            assert golden.arrays_digest(*batch(), b["count"]) == g["resets"][str(k)], f"{case}: reset at step {k}"
-        acts = golden.given_actions(inp["u"][k], b["count"]) if policy == "given" else None
+            e.reset(b, mask=mask, keep_goals=keep, sample=sample, first_env=5)
+            assert golden.arrays_digest(*state(), b["count"]) == g["resets"][str(k)], f"{case}: reset at step {k}"
+        acts = golden.given_actions(inp["u"][k], b["count"]) if c["policy"] == "given" else None
         o = e.step(b, first_env=5, actions=acts, next_task_ids=inp["next"][k])
-        d = golden.arrays_digest(*batch(), o["reward"], o["terminated"], o["truncated"], o["count"], o["schema"], o["binding"],
+        d = golden.arrays_digest(*state(), o["reward"], o["terminated"], o["truncated"], o["count"], o["schema"], o["binding"],
                                  o["goal"], o["invalid"], o["final_states"])
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
         b["count"] = o["count"]
 
 
-@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids"])
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted"])
 def test_table_env_matches_reference(golden, case):
+    assert case in golden.TABLE_ORACLE_CASES
     replay_oracle(golden, case)
+
+
+def test_instance_draws(golden):
+    """rl::rng::instance_draw (include/mymyr/rl/rng.hpp:94-115) against the reference's draws, uniform and weighted."""
+    for d in golden.load("env_table.json")["instance_draws"]:
+        thr, idx = golden.sampler_arrays(d["weights"])
+        assert port.instance_draw(d["seed"], d["env"], d["reset_count"], d["instances"], thr, idx) == d["draw"]
+
+
+def test_library_instance_draws_and_sampler(golden):
+    """The library's host instance draw (mya_instance_draw) and InstanceSampler arrays against the reference's draws and
+    the fixture's restatement of mymyr.rl.InstanceSampler (no device needed)."""
+    from mymyr_amd import rl
+
+    for d in golden.load("env_table.json")["instance_draws"]:
+        s = rl.InstanceSampler(d["instances"], d["weights"])
+        thr, idx = golden.sampler_arrays(d["weights"])
+        assert np.array_equal(s.thresholds, thr) and np.array_equal(s.indices, idx)
+        assert s.sample(d["seed"], d["env"], d["reset_count"]) == d["draw"]
+    with pytest.raises(ValueError, match="positive sum"):
+        rl.InstanceSampler(2, [0.0, 0.0])
+
+
+def test_sampler_arrays_closed_form(golden):
+    """InstanceSampler's arrays (python/mymyr/rl/_sampling.py:29-39) on weights with known cumulative sums."""
+    thr, idx = golden.sampler_arrays([1.0, 1.0])
+    assert idx.tolist() == [0, 1] and thr.tolist() == [1 << 31]
+    thr, idx = golden.sampler_arrays([1.0, 0.0, 3.0])
+    assert idx.tolist() == [0, 2] and thr.tolist() == [1 << 30]
+    thr, idx = golden.sampler_arrays([0.0, 5.0])
+    assert idx.tolist() == [1] and thr.size == 0
 
 
 def test_table_fixture_exercises_the_rules(golden):
@@ -63,6 +107,7 @@ def test_table_fixture_exercises_the_rules(golden):
         t = g[case]["totals"]
         assert all(n > 0 for n in t["instance_rows"]), case
         assert t["truncated"] > 0, case
+        assert len(g[case]["resets"]) > 2 or golden.TABLE_CASES[case].get("sampler") is None, case
     assert g["gridworld_goals"]["totals"]["invalid"] > 0 and g["gridworld_large"]["totals"]["terminated"] > 0
     # instances of different widths: padding words exist in every table
     for table in workloads.TABLES:
