@@ -59,6 +59,8 @@ struct mya_env
     u32* d_starts = nullptr;  // [instances + 1]
     u32* d_chunks = nullptr;  // [instances + 1]
     u32* d_order = nullptr;   // [group_rows]
+    u64 sampled_rows = 0;
+    i32* d_sampled = nullptr;  // [sampled_rows]: the sampled next instances of a step
     std::mutex mutex;         // guards the scratch growth
 
     [[nodiscard]] u32 instances() const { return static_cast<u32>(inst.size()); }
@@ -95,21 +97,28 @@ void check_batch(const mya_env* e, const mya_env_batch* b)
 /// its task ids on the way).
 bool grouped(const mya_env* e) { return e->instances() > 1; }
 
+/// The env's per-row scratch array `member` (of `have` rows), grown under the env's lock to `rows` (a call with a batch
+/// no larger than before allocates nothing).
+template<class X>
+X* scratch_rows(mya_env* e, u64 rows, X* mya_env::*member, u64 mya_env::*have)
+{
+    std::lock_guard lock(e->mutex);
+    if (rows > e->*have)
+    {
+        dev_free(e->*member);
+        e->*member = nullptr;
+        e->*have = 0;
+        e->*member = dev_alloc<X>(rows, "env row scratch");
+        e->*have = rows;
+    }
+    return e->*member;
+}
+
 /// Groups the batch's rows by instance into the env's scratch (grown under the env's lock; a call with a batch no
 /// larger than before allocates nothing).
 RowGroups group_rows(mya_env* e, const mya_env_batch* b, hipStream_t stream)
 {
-    {
-        std::lock_guard lock(e->mutex);
-        if (b->rows > e->group_rows)
-        {
-            dev_free(e->d_order);
-            e->d_order = nullptr;
-            e->group_rows = 0;
-            e->d_order = dev_alloc<u32>(b->rows, "env row groups");
-            e->group_rows = b->rows;
-        }
-    }
+    scratch_rows(e, b->rows, &mya_env::d_order, &mya_env::group_rows);
     launch_group_rows(b->task_ids, b->rows, e->instances(), e->d_hist, e->d_order, e->d_starts, e->d_chunks, e->d_status, stream);
     return RowGroups{e->d_order, e->d_starts, e->d_chunks};
 }
@@ -140,7 +149,8 @@ std::string domain_mismatch(const TaskText& r, const TaskText& t)
 void free_env(mya_env* e)
 {
     for (void* p : std::initializer_list<void*>{e->d_status, e->d_inst, e->d_tasks, e->d_init, e->d_init_cache, e->d_init_masks, e->d_hist,
-                                                e->d_starts, e->d_chunks, e->d_order, e->d_thresholds, e->d_indices})
+                                                e->d_starts, e->d_chunks, e->d_order, e->d_thresholds, e->d_indices,
+                                                e->d_sampled})
         dev_free(p);
     if (e->h_status)
         (void)hipHostFree(e->h_status);
@@ -404,8 +414,6 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.seeds = batch->seeds;
         a.env_ids = batch->env_ids;
         a.reset_counts = batch->reset_counts;
-        a.sampling_seeds = batch->sampling_seeds;
-        a.sampler = env->sampler;
         a.steps = batch->steps;
         a.draws = batch->draws;
         a.at_goal = batch->at_goal;
@@ -430,17 +438,33 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.goal_neg = batch->goal_neg;
         a.status = env->d_status;
         const auto s = static_cast<hipStream_t>(stream);
+        // without next_task_ids, rows restart in their next sampled instances when the env has a sampler and the batch
+        // reset counters (drawn before the step, from the counters' values before its autoresets advance them)
+        if (!next_task_ids && batch->reset_counts && env->sampler.instances && env->cfg.autoreset && batch->rows)
+        {
+            a.next_task_ids = scratch_rows(env, batch->rows, &mya_env::d_sampled, &mya_env::sampled_rows);
+            launch_env_sample_next(env->sampler, env->cfg.seed, batch->first_env, batch->rows, batch->reset_counts, batch->sampling_seeds,
+                                   batch->env_ids, const_cast<i32*>(a.next_task_ids), s);
+        }
         if (!grouped(env))
         {
             launch_env_step(a, s);
             return;
         }
         a.groups = group_rows(env, batch, s);
-        for (const mya_env::Launch& l : env->launches)
-        {
-            a.wave_words = l.wave_words;
-            launch_env_step_grouped(a, l.variant, l.nw, l.lds, s);
-        }
+        if (env->instances() <= kPerInstanceLaunches)
+            for (u32 k = 0; k < env->instances(); ++k)
+            {
+                a.T = env->inst[k].T;
+                a.instance = k;
+                launch_env_step(a, s);
+            }
+        else
+            for (const mya_env::Launch& l : env->launches)
+            {
+                a.wave_words = l.wave_words;
+                launch_env_step_grouped(a, l.variant, l.nw, l.lds, s);
+            }
     });
 }
 
@@ -472,11 +496,19 @@ int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, vo
             return;
         }
         a.groups = group_rows(env, batch, s);
-        for (const mya_env::Launch& l : env->launches)
-        {
-            a.wave_words = l.wave_words;
-            launch_env_count_grouped(a, l.variant, l.nw, l.lds, s);
-        }
+        if (env->instances() <= kPerInstanceLaunches)
+            for (u32 k = 0; k < env->instances(); ++k)
+            {
+                a.T = env->inst[k].T;
+                a.instance = k;
+                launch_env_count(a, s);
+            }
+        else
+            for (const mya_env::Launch& l : env->launches)
+            {
+                a.wave_words = l.wave_words;
+                launch_env_count_grouped(a, l.variant, l.nw, l.lds, s);
+            }
     });
 }
 

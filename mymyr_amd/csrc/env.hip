@@ -1181,20 +1181,6 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         const u64 fp = state_fingerprint(L.row, T.W, lane) + salt;
         cached = (static_cast<u64>(crow[T.num_schemas]) | (static_cast<u64>(crow[T.num_schemas + 1]) << 32)) == fp;
     }
-    // the instance an autoreset restarts in; an id outside the table sets the status (every row's, as the reference
-    // checks next_task_ids over the whole batch) and keeps the row's instance
-    u32 next = k;
-    if (A.next_task_ids)
-    {
-        const i32 v = A.next_task_ids[i];
-        if (v < 0 || static_cast<u32>(v) >= A.instances)
-        {
-            if (lane == 0)
-                atomicOr(A.status, kStatusTaskId);
-        }
-        else
-            next = static_cast<u32>(v);
-    }
     enum
     {
         kOk = 0,
@@ -1295,23 +1281,28 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         for (u32 q = lane; q < FW; q += kWave)
             f[q] = q < T.W ? L.row[q] : 0;
     }
-    // 5. the autoreset, or the bookkeeping of the move (the LDS row holds s')
+    // 5. the autoreset, or the bookkeeping of the move (the LDS row holds s'). The instance an autoreset restarts in:
+    // next_task_ids[i], where an id outside the table sets the status (in every row, as the reference checks the whole
+    // array) and keeps the row's instance
+    u32 next = k;
+    if (A.next_task_ids)
+    {
+        const i32 v = A.next_task_ids[i];
+        if (v < 0 || static_cast<u32>(v) >= A.instances)
+        {
+            if (lane == 0)
+                atomicOr(A.status, kStatusTaskId);
+        }
+        else
+            next = static_cast<u32>(v);
+    }
     const bool reset = A.cfg.autoreset && (term || trunc);
     if (reset)
     {
-        // without next_task_ids the row restarts in its next sampled instance when the env has a sampler and the batch
-        // reset counters; every autoreset advances the row's counter
-        if (A.reset_counts)
-        {
-            const u32 rc = A.reset_counts[i];
-            if (!A.next_task_ids && A.sampler.instances)
-                next = static_cast<u32>(instance_draw(A.sampling_seeds ? A.sampling_seeds[i] : A.cfg.seed,
-                                                      A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, rc,
-                                                      A.sampler.instances, A.sampler.thresholds, A.sampler.indices, A.sampler.m));
-            wave_sync();  // every lane has read the counter before lane 0 advances it
-            if (lane == 0)
-                A.reset_counts[i] = rc + 1;
-        }
+        // every autoreset advances the row's reset counter (a sampled restart comes in as next_task_ids, drawn before the
+        // step with the counter's value before this advance)
+        if (A.reset_counts && lane == 0)
+            A.reset_counts[i] += 1;
         const InstDev& J = A.inst[next];
         const u32 z = min(A.words, max(J.W, T.W));  // the words the row may have dirtied: its old and new instance's
         for (u32 q = lane; q < z; q += kWave)
@@ -1373,27 +1364,51 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     wave_sync();
 }
 
-/// The step of a batch of one instance: every row in batch order with the kernel-argument tables. A row whose task id
-/// is not 0 names no instance: it sets kStatusTaskId and is not stepped.
-template<bool kStaged, bool kLevels>
-__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
+/// The step of a batch of one instance: every row in batch order with the kernel-argument tables (a row whose task id
+/// is not 0 names no instance: it sets kStatusTaskId and is not stepped); with kGroup, the rows of one instance's group
+/// of a batch grouped by instance.
+template<bool kStaged, bool kLevels, bool kGroup>
+__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kGroup ? 1 : (kLevels ? 3 : 4)))) void k_env_step(EnvArgs A)
 {
     extern __shared__ u64 smem[];
     const TaskDev& T = A.T;
-    Tab<kStaged> H;
-    lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
     const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
-    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
+    if constexpr (kGroup)
     {
-        if (A.task_ids && A.task_ids[i] != 0)
-        {
-            if (lane == 0)
-                atomicOr(A.status, kStatusTaskId);
-            continue;
-        }
-        step_row<kLevels>(A, T, H, L, i, 0, lane);
+        // the rows of instance A.instance of a batch grouped by instance; blocks past them leave before staging
+        const u32 lo = A.groups.starts[A.instance], hi = A.groups.starts[A.instance + 1];
+        if (lo + static_cast<u64>(blockIdx.x) * nw >= hi)
+            return;
+        Tab<kStaged> H;
+        lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+        const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+        for (u64 j = lo + static_cast<u64>(blockIdx.x) * nw + wave; j < hi; j += static_cast<u64>(gridDim.x) * nw)
+            step_row<kLevels>(A, T, H, L, A.groups.order[j], A.instance, lane);
     }
+    else
+    {
+        Tab<kStaged> H;
+        lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+        const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+        for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
+        {
+            if (A.task_ids && A.task_ids[i] != 0)
+            {
+                if (lane == 0)
+                    atomicOr(A.status, kStatusTaskId);
+                continue;
+            }
+            step_row<kLevels>(A, T, H, L, i, 0, lane);
+        }
+    }
+}
+
+/// Instance k's tables, read through the constant address space: loads of them are invariant, so the compiler
+/// re-reads a field with a scalar load where it needs it instead of holding the whole record in registers.
+__device__ __forceinline__ const TaskDev& instance_tables(const TaskDev* tasks, u32 k)
+{
+    typedef __attribute__((address_space(4))) const TaskDev ConstTaskDev;
+    return *(const TaskDev*)((const ConstTaskDev*)tasks + k);
 }
 
 /// The instance of chunk c: the last k with chunk_start[k] <= c (chunk_start is non-decreasing, chunk_start[0] = 0).
@@ -1424,7 +1439,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step_grouped(EnvArgs 
         const u32 k = chunk_instance(A.groups.chunk_start, A.instances, c);
         if (A.inst[k].variant != variant)
             continue;
-        const TaskDev T = A.tasks[k];
+        const TaskDev& T = instance_tables(A.tasks, k);
         __syncthreads();  // every wave is done with the tables of the block's previous chunk
         Tab<kStaged> H;
         lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
@@ -1477,26 +1492,40 @@ __device__ __forceinline__ void count_row(const CountArgs& A, const TaskDev& T, 
     wave_sync();
 }
 
-/// The count of a batch of one instance (A.instance) in batch order; rows whose task id is not 0 set kStatusTaskId and
-/// are not counted.
-template<bool kStaged, bool kLevels>
+/// The count of a batch of one instance (A.instance) in batch order (rows whose task id is not 0 set kStatusTaskId and
+/// are not counted); with kGroup, the rows of instance A.instance's group.
+template<bool kStaged, bool kLevels, bool kGroup>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count(CountArgs A)
 {
     extern __shared__ u64 smem[];
     const TaskDev& T = A.T;
-    Tab<kStaged> H;
-    lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
     const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
-    const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
-    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
+    if constexpr (kGroup)
     {
-        if (A.task_ids && A.task_ids[i] != 0)
+        const u32 lo = A.groups.starts[A.instance], hi = A.groups.starts[A.instance + 1];
+        if (lo + static_cast<u64>(blockIdx.x) * nw >= hi)
+            return;
+        Tab<kStaged> H;
+        lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+        const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+        for (u64 j = lo + static_cast<u64>(blockIdx.x) * nw + wave; j < hi; j += static_cast<u64>(gridDim.x) * nw)
+            count_row<kLevels>(A, T, H, L, A.groups.order[j], A.instance, lane);
+    }
+    else
+    {
+        Tab<kStaged> H;
+        lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
+        const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+        for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
         {
-            if (lane == 0 && A.status)
-                atomicOr(A.status, kStatusTaskId);
-            continue;
+            if (A.task_ids && A.task_ids[i] != 0)
+            {
+                if (lane == 0 && A.status)
+                    atomicOr(A.status, kStatusTaskId);
+                continue;
+            }
+            count_row<kLevels>(A, T, H, L, i, A.instance, lane);
         }
-        count_row<kLevels>(A, T, H, L, i, A.instance, lane);
     }
 }
 
@@ -1512,7 +1541,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_count_grouped(CountAr
         const u32 k = chunk_instance(A.groups.chunk_start, A.instances, c);
         if (A.inst[k].variant != variant)
             continue;
-        const TaskDev T = A.tasks[k];
+        const TaskDev& T = instance_tables(A.tasks, k);
         __syncthreads();
         Tab<kStaged> H;
         lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
@@ -1582,6 +1611,16 @@ __global__ void k_env_reset_draw(SamplerDev sampler, u64 seed, u64 first_env, u6
                                         sampler.instances, sampler.thresholds, sampler.indices, sampler.m);
         reset_counts[i] = rc + 1;
     }
+}
+
+/// Per row: the instance its next autoreset would draw (with the row's current reset counter), for a step without
+/// next_task_ids over a batch with reset counters and an env with a sampler.
+__global__ void k_env_sample_next(SamplerDev sampler, u64 seed, u64 first_env, u64 rows, const u32* reset_counts, const u64* sampling_seeds,
+                                  const u32* env_ids, i32* next)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
+        next[i] = instance_draw(sampling_seeds ? sampling_seeds[i] : seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i,
+                                reset_counts[i], sampler.instances, sampler.thresholds, sampler.indices, sampler.m);
 }
 
 /// Per row: the instance's goal into the row's goal masks, or (keep) the given masks checked against the instance's
@@ -2047,15 +2086,28 @@ void set_lds(const void* fn, size_t bytes)
 }
 }  // namespace
 
+/// Blocks of a one-instance launch: a row per wave in batch order; over one group of a grouped batch (whose size only the
+/// device knows) a bounded grid whose blocks stride over the group.
+unsigned one_instance_grid(u64 rows, unsigned nw, bool group)
+{
+    constexpr u64 kGroupBlocks = 8192;
+    const unsigned g = grid_for(rows, nw);
+    return group ? static_cast<unsigned>(std::min<u64>(g, kGroupBlocks)) : g;
+}
+
 void launch_env_step(const EnvArgs& a, hipStream_t stream)
 {
     if (a.rows == 0)
         return;
     size_t lds = 0;
     const unsigned nw = waves_per_block(a.T, &lds);
-    const auto fn = variant(a.T, k_env_step<true, false>, k_env_step<true, true>, k_env_step<false, false>, k_env_step<false, true>);
+    const bool group = a.groups.order != nullptr;
+    const auto fn = group ? variant(a.T, k_env_step<true, false, true>, k_env_step<true, true, true>, k_env_step<false, false, true>,
+                                    k_env_step<false, true, true>)
+                          : variant(a.T, k_env_step<true, false, false>, k_env_step<true, true, false>, k_env_step<false, false, false>,
+                                    k_env_step<false, true, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
     launch_check("env step");
 }
 
@@ -2065,9 +2117,13 @@ void launch_env_count(const CountArgs& a, hipStream_t stream)
         return;
     size_t lds = 0;
     const unsigned nw = waves_per_block(a.T, &lds);
-    const auto fn = variant(a.T, k_env_count<true, false>, k_env_count<true, true>, k_env_count<false, false>, k_env_count<false, true>);
+    const bool group = a.groups.order != nullptr;
+    const auto fn = group ? variant(a.T, k_env_count<true, false, true>, k_env_count<true, true, true>, k_env_count<false, false, true>,
+                                    k_env_count<false, true, true>)
+                          : variant(a.T, k_env_count<true, false, false>, k_env_count<true, true, false>, k_env_count<false, false, false>,
+                                    k_env_count<false, true, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
     launch_check("env count");
 }
 
@@ -2219,6 +2275,16 @@ void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows,
                            stream, inst, instances, rows, cache_width, mask, task_ids, cache);
         launch_check("env reset cache");
     }
+}
+
+void launch_env_sample_next(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u32* reset_counts,
+                            const u64* sampling_seeds, const u32* env_ids, i32* next, hipStream_t stream)
+{
+    if (rows == 0)
+        return;
+    hipLaunchKernelGGL(k_env_sample_next, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream,
+                       sampler, seed, first_env, rows, reset_counts, sampling_seeds, env_ids, next);
+    launch_check("env sample next");
 }
 
 void launch_env_reset_draw(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,

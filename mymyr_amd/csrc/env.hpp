@@ -65,18 +65,18 @@ struct EnvArgs
     const InstDev* inst;   // [instances] (device)
     u32 instances;
     u32 wave_words;        // LDS words per wave of a grouped launch (the largest of its instances)
-    RowGroups groups;
+    RowGroups groups;      // rows grouped by instance (order null: batch order, one instance)
+    u32 instance;          // with groups, a one-instance launch's instance (T's): it steps that group's rows
     EnvCfg cfg;
     u64* states;
     u64 rows;
     u32 words;  // row words of the batch (>= every instance's W)
     i32* task_ids;             // [rows]: each row's instance (null: instance 0); an autoreset writes the new one
-    const i32* next_task_ids;  // [rows]: the instance an autoresetting row restarts in (null: its sampled or own one)
+    const i32* next_task_ids;  // [rows]: the instance an autoresetting row restarts in (null: its own)
     const u64* seeds;          // [rows]: per-row keys of the random policy (null: cfg.seed)
     const u32* env_ids;        // [rows]: per-row env ids (null: first_env + row)
-    u32* reset_counts;         // [rows]: the sampler's per-row counters (null: no counting, no sampling)
-    const u64* sampling_seeds; // [rows]: per-row sampling keys (null: cfg.seed)
-    SamplerDev sampler;
+    u32* reset_counts;         // [rows]: per-row reset counters (null: none), advanced by every autoreset
+
     i32* steps;
     u64* draws;
     u8* at_goal;
@@ -126,7 +126,7 @@ struct CountArgs
     const u64* goal_pos;
     const u64* goal_neg;
     u32* status;
-    u32 instance;  // the instance of a one-instance count (its fingerprint salt)
+    u32 instance;  // the instance of a one-instance count (its fingerprint salt; with groups, the group it counts)
 };
 
 void launch_env_count(const CountArgs& a, hipStream_t stream);
@@ -139,6 +139,11 @@ void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, 
 /// with a task id outside [0, instances) set kStatusTaskId.
 void launch_group_rows(const i32* task_ids, u64 rows, u32 instances, u32* hist, u32* order, u32* starts, u32* chunk_start,
                        u32* status, hipStream_t stream);
+
+/// Tables of at most this many instances step with one launch per instance (the instance's tables as kernel arguments,
+/// its group's rows from the row groups); larger tables with one launch per kernel variant (each block reads its
+/// chunk's instance's tables from device memory).
+constexpr u32 kPerInstanceLaunches = 16;
 
 /// The kernel variant of an instance (InstDev::variant) and the block shape of a grouped launch over the instances of
 /// one variant: waves per block and dynamic LDS bytes, from the largest hot tables and per-wave region among them.
@@ -162,6 +167,11 @@ void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows,
 /// reset counters), then the counters advanced (HostEnv::reset, src/mymyr/rl/env.cpp:223-255).
 void launch_env_reset_draw(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
                            u32* reset_counts, const u64* sampling_seeds, const u32* env_ids, hipStream_t stream);
+
+/// next[i] = the instance row i's next autoreset draws from the sampler (its current reset counter, its sampling key or
+/// `seed`, its env id or first_env + i): the next_task_ids of a step that restarts rows in sampled instances.
+void launch_env_sample_next(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u32* reset_counts,
+                            const u64* sampling_seeds, const u32* env_ids, i32* next, hipStream_t stream);
 
 /// Per-env goal masks at a reset of the rows with mask[i] != 0: the instance's goal written into them, or with
 /// keep_goals the given masks kept, checked against the instance's fluent slots (kStatusGoalMask) and at_goal tested

@@ -57,6 +57,8 @@ TABLES = {
                         lambda: gen.gridworld(16, 16, 0.15, seed=3)],
     "transport_table": [lambda: gen.transport(8, 2, 4, goals=3, seed=1), lambda: gen.transport(24, 6, 40, goals=6, seed=2),
                         lambda: gen.transport(6, 2, 3, goals=2, seed=3)],
+    # more instances than one launch per instance serves: grids of 4x4 to 13x13 cells (rows of 1 to 3 words)
+    "gridworld_many": [(lambda w: (lambda: gen.gridworld(w, w - i % 3, 0.15, seed=10 + i)))(4 + (i * 7) % 10) for i in range(20)],
 }
 
 GRIDWORLD = EnvWorkload("gridworld", 1024, 256, {"seed": SEED, "step_reward": -1.0, "goal_reward": 0.0})

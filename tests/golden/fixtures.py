@@ -94,11 +94,15 @@ TABLE_CASES = {
                             env={"seed": 6, "max_steps": 30, "step_reward": -1.0, "goal_reward": 0.0}),
     "transport_large": dict(table="transport_table", rows=2048, steps=48, seed=25, policy="given", goals=True,
                             env={"seed": 7, "max_steps": 16}),
+    "gridworld_many": dict(table="gridworld_many", rows=96, steps=40, seed=29, policy="random", sampler="uniform",
+                           env={"seed": 11, "max_steps": 12, "step_reward": -1.0, "goal_reward": 3.0}),
+    "gridworld_many_large": dict(table="gridworld_many", rows=8192, steps=48, seed=30, policy="given", goals=True,
+                                 env={"seed": 12, "max_steps": 25}),
     "gridworld_sampled_large": dict(table="gridworld_table", rows=4096, steps=64, seed=28, policy="random", sampler=[1.0, 3.0, 2.0],
                                     keys=True, env={"seed": 10, "max_steps": 20}),
 }
 # cases small enough for the oracle's pure-Python restatement
-TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted"]
+TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted", "gridworld_many"]
 
 
 def sampler_arrays(weights) -> tuple[np.ndarray, np.ndarray]:

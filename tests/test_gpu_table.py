@@ -1,6 +1,7 @@
 """The device env over task tables (several instances of one domain, rows grouped by instance on the device) against
 the compiled reference's rl::HostEnv over TaskTable::create: every reset and step of the fixture's trajectories
-(tests/golden/env_table.json, from 24 to 4096 envs) digest-equal, through the C ABI (mymyr_amd.rl.DeviceEnvPool).
+(tests/golden/env_table.json, from 24 to 8192 envs; tables of 3 instances step with one launch per instance, the
+20-instance table with one launch per kernel variant) digest-equal, through the C ABI (mymyr_amd.rl.DeviceEnvPool).
 Also: a table whose rows all sit in one instance steps exactly as a one-instance env of that task, task ids outside
 the table raise through the sticky status, and a grouped step replays from a HIP graph."""
 
@@ -85,7 +86,8 @@ def replay(golden, case: str):
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
-                                  "gridworld_large", "transport_large", "gridworld_sampled_large"])
+                                  "gridworld_many", "gridworld_large", "transport_large", "gridworld_sampled_large",
+                                  "gridworld_many_large"])
 def test_table_env_matches_reference(golden, case):
     replay(golden, case)
 

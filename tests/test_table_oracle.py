@@ -63,7 +63,8 @@ def replay_oracle(golden, case: str) -> None:
         b["count"] = o["count"]
 
 
-@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted"])
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
+                                  "gridworld_many"])
 def test_table_env_matches_reference(golden, case):
     assert case in golden.TABLE_ORACLE_CASES
     replay_oracle(golden, case)
