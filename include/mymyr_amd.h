@@ -245,6 +245,22 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
  * first call with a larger batch). */
 int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
                  const int32_t* next_task_ids, void* stream);
+/* Sizes the env's scratch for batches of up to `rows` rows and sets its kernels' LDS limits now (the reference device
+ * env's reserve), so that later calls with such batches allocate nothing and make no runtime call besides kernel
+ * launches, as HIP graph capture of them requires. */
+int mya_env_reserve(mya_env* env, uint64_t rows);
+/* New RNG key of the random policy and of the sampler (BatchedEnv.set_seed, python/mymyr/rl/torch/_batched.py:549-556),
+ * written to the env's device word in stream order: steps enqueued before it draw with the old key, steps and graph
+ * replays after it with the new one. The caller restarts the draw and reset counters if it wants fresh streams. */
+int mya_env_set_seed(mya_env* env, uint64_t seed, void* stream);
+/* The random policy's next choices without a step (DeviceEnv::random_actions, include/mymyr/cuda/env.hpp:189-192):
+ * out[i] (device int64 [rows]) = the successor index a step would draw now for row i (batch->draws, the row's key and
+ * env id), among the first max_actions successors (0: no limit), 0 where count[i] (device int32 [rows]) is 0. Async. */
+int mya_env_random_actions(mya_env* env, const mya_env_batch* batch, const int32_t* count, uint32_t max_actions, int64_t* out,
+                           void* stream);
+/* Whether each row's current state is a goal of its instance (HostEnv::goal, src/mymyr/rl/env.cpp:272-281): the
+ * per-env masks' test when the batch has them, else the instance's goal test; goal (device uint8 [rows]). Async. */
+int mya_env_goal(mya_env* env, const mya_env_batch* batch, uint8_t* goal, void* stream);
 /* Reads and clears the sticky device status (synchronizes the env's status copy); -1 with a message if a step failed. */
 int mya_env_check(mya_env* env);
 /* Recomputes at_goal and the count cache (when the batch has one) of every row from its state and instance, after the

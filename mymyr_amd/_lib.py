@@ -210,6 +210,10 @@ def _load() -> ctypes.CDLL:
         "mya_env_free": (None, [c_void_p]),
         "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_int, c_void_p]),
         "mya_env_set_sampling": (c_int, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint32]),
+        "mya_env_set_seed": (c_int, [c_void_p, c_uint64, c_void_p]),
+        "mya_env_reserve": (c_int, [c_void_p, c_uint64]),
+        "mya_env_random_actions": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_uint32, c_void_p, c_void_p]),
+        "mya_env_goal": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),
         "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p, c_void_p]),
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_refresh": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),

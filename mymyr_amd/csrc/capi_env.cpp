@@ -41,6 +41,7 @@ struct mya_env
     u8* d_init_masks = nullptr;   // device [instances, num_schemas]
     u32* d_status = nullptr;
     u32* h_status = nullptr;
+    u64* d_seed = nullptr;        // device word: the RNG key of the random policy and of the sampler
     SamplerDev sampler{};          // the instance sampler (instances 0: off)
     u32* d_thresholds = nullptr;   // device [m - 1]
     i32* d_indices = nullptr;      // device [m]
@@ -146,11 +147,46 @@ std::string domain_mismatch(const TaskText& r, const TaskText& t)
     return {};
 }
 
+/// A count over the batch's rows (refresh, goal): in batch order over one instance, else grouped by instance.
+void run_count(mya_env* env, const mya_env_batch* batch, CountArgs& a, hipStream_t s)
+{
+    a.T = env->T0();
+    a.tasks = env->d_tasks;
+    a.inst = env->d_inst;
+    a.instances = env->instances();
+    a.states = batch->states;
+    a.rows = batch->rows;
+    a.words = batch->words;
+    a.task_ids = batch->task_ids;
+    a.goal_pos = batch->goal_pos;
+    a.goal_neg = batch->goal_neg;
+    a.status = env->d_status;
+    if (!grouped(env))
+    {
+        launch_env_count(a, s);
+        return;
+    }
+    a.groups = group_rows(env, batch, s);
+    if (env->instances() <= kPerInstanceLaunches)
+        for (u32 k = 0; k < env->instances(); ++k)
+        {
+            a.T = env->inst[k].T;
+            a.instance = k;
+            launch_env_count(a, s);
+        }
+    else
+        for (const mya_env::Launch& l : env->launches)
+        {
+            a.wave_words = l.wave_words;
+            launch_env_count_grouped(a, l.variant, l.nw, l.lds, s);
+        }
+}
+
 void free_env(mya_env* e)
 {
     for (void* p : std::initializer_list<void*>{e->d_status, e->d_inst, e->d_tasks, e->d_init, e->d_init_cache, e->d_init_masks, e->d_hist,
                                                 e->d_starts, e->d_chunks, e->d_order, e->d_thresholds, e->d_indices,
-                                                e->d_sampled})
+                                                e->d_sampled, e->d_seed})
         dev_free(p);
     if (e->h_status)
         (void)hipHostFree(e->h_status);
@@ -183,7 +219,6 @@ int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_c
         if (config->dead_end != 0 && config->dead_end != 1)
             throw std::invalid_argument("mymyr_amd: env: dead_end must be 0 (no_successors) or 1 (none)");
         std::unique_ptr<mya_env, void (*)(mya_env*)> e(new mya_env, free_env);
-        e->cfg.seed = config->seed;
         e->cfg.max_steps = config->max_steps;
         e->cfg.step_reward = config->step_reward;
         e->cfg.goal_reward = config->goal_reward;
@@ -204,6 +239,8 @@ int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_c
         e->num_schemas = e->T0().num_schemas;
         const u32 S = e->num_schemas, cw = cache_width(e->T0());
         e->d_status = dev_alloc<u32>(1, "env status");
+        e->d_seed = dev_alloc<u64>(1, "env seed");
+        hip_check(hipMemcpy(e->d_seed, &config->seed, sizeof(u64), hipMemcpyHostToDevice), "env seed");
         hip_check(hipHostMalloc(reinterpret_cast<void**>(&e->h_status), sizeof(u32), hipHostMallocDefault), "pinned status");
         hip_check(hipMemset(e->d_status, 0, sizeof(u32)), "env status");
         // per instance: the goal as masks over its words; then the initial states' counts, goal flags, masks and
@@ -366,7 +403,7 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         if (sample && batch->rows && !batch->reset_counts)
             throw std::invalid_argument("mymyr: env: a sampling reset needs the reset counters");
         const auto s = static_cast<hipStream_t>(stream);
-        launch_env_reset_draw(env->sampler, env->cfg.seed, batch->first_env, batch->rows, mask, sample != 0, batch->task_ids, batch->reset_counts,
+        launch_env_reset_draw(env->sampler, env->d_seed, batch->first_env, batch->rows, mask, sample != 0, batch->task_ids, batch->reset_counts,
                               batch->sampling_seeds, batch->env_ids, s);
         launch_env_reset(env->d_inst, env->instances(), batch->states, batch->rows, batch->words, mask, batch->task_ids, batch->steps,
                          batch->at_goal, count, batch->counts, cache_width(env->T0()), env->d_status, s);
@@ -411,6 +448,7 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.words = batch->words;
         a.task_ids = batch->task_ids;
         a.next_task_ids = next_task_ids;
+        a.seed = env->d_seed;
         a.seeds = batch->seeds;
         a.env_ids = batch->env_ids;
         a.reset_counts = batch->reset_counts;
@@ -443,7 +481,7 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         if (!next_task_ids && batch->reset_counts && env->sampler.instances && env->cfg.autoreset && batch->rows)
         {
             a.next_task_ids = scratch_rows(env, batch->rows, &mya_env::d_sampled, &mya_env::sampled_rows);
-            launch_env_sample_next(env->sampler, env->cfg.seed, batch->first_env, batch->rows, batch->reset_counts, batch->sampling_seeds,
+            launch_env_sample_next(env->sampler, env->d_seed, batch->first_env, batch->rows, batch->reset_counts, batch->sampling_seeds,
                                    batch->env_ids, const_cast<i32*>(a.next_task_ids), s);
         }
         if (!grouped(env))
@@ -475,40 +513,65 @@ int mya_env_refresh(mya_env* env, const mya_env_batch* batch, int32_t* count, vo
             throw std::invalid_argument("mymyr_amd: env: null env");
         check_batch(env, batch);
         CountArgs a{};
-        a.T = env->T0();
-        a.tasks = env->d_tasks;
-        a.inst = env->d_inst;
-        a.instances = env->instances();
-        a.states = batch->states;
-        a.rows = batch->rows;
-        a.words = batch->words;
-        a.task_ids = batch->task_ids;
         a.count = count;
         a.goal = batch->at_goal;
         a.cache = batch->counts;
-        a.goal_pos = batch->goal_pos;
-        a.goal_neg = batch->goal_neg;
-        a.status = env->d_status;
-        const auto s = static_cast<hipStream_t>(stream);
-        if (!grouped(env))
-        {
-            launch_env_count(a, s);
+        run_count(env, batch, a, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_reserve(mya_env* env, uint64_t rows)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        if (rows > 0x7FFFFFFFull)
+            throw std::invalid_argument("mymyr: env: more than 2^31 - 1 environments in one batch");
+        if (rows == 0)
             return;
-        }
-        a.groups = group_rows(env, batch, s);
-        if (env->instances() <= kPerInstanceLaunches)
-            for (u32 k = 0; k < env->instances(); ++k)
-            {
-                a.T = env->inst[k].T;
-                a.instance = k;
-                launch_env_count(a, s);
-            }
-        else
-            for (const mya_env::Launch& l : env->launches)
-            {
-                a.wave_words = l.wave_words;
-                launch_env_count_grouped(a, l.variant, l.nw, l.lds, s);
-            }
+        scratch_rows(env, rows, &mya_env::d_sampled, &mya_env::sampled_rows);
+        if (grouped(env))
+            scratch_rows(env, rows, &mya_env::d_order, &mya_env::group_rows);
+        for (const EnvInstance& in : env->inst)
+            prepare_env_launches(in.T);
+        for (const mya_env::Launch& l : env->launches)
+            prepare_grouped_launches(l.variant, l.lds);
+    });
+}
+
+int mya_env_set_seed(mya_env* env, uint64_t seed, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        launch_set_word(env->d_seed, seed, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_random_actions(mya_env* env, const mya_env_batch* batch, const int32_t* count, uint32_t max_actions, int64_t* out, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        check_batch(env, batch);
+        if (batch->rows && (!batch->draws || !count || !out))
+            throw std::invalid_argument("mymyr_amd: env: random_actions needs the draw counters, the counts and an output array");
+        launch_env_random_actions(env->d_seed, batch->seeds, batch->env_ids, batch->first_env, batch->draws, count, batch->rows,
+                                  max_actions ? max_actions : 0xFFFFFFFFu, out, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_goal(mya_env* env, const mya_env_batch* batch, uint8_t* goal, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        check_batch(env, batch);
+        if (batch->rows && !goal)
+            throw std::invalid_argument("mymyr: env: goal query needs an output array");
+        CountArgs a{};
+        a.goal = goal;
+        run_count(env, batch, a, static_cast<hipStream_t>(stream));
     });
 }
 

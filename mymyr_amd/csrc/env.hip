@@ -1214,7 +1214,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
                 a = static_cast<u32>(act);
         }
         else if (!already_goal)
-            a = successor_index(A.seeds ? A.seeds[i] : A.cfg.seed, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, A.draws[i], c);
+            a = successor_index(A.seeds ? A.seeds[i] : *A.seed, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, A.draws[i], c);
         u32 rank = 0;
         if (st == kOk)
         {
@@ -1596,7 +1596,7 @@ __global__ void k_env_reset(const InstDev* inst, u32 instances, u64* states, u64
 }
 
 /// Per row before a reset: the drawn task id (sample) and the advanced reset counter.
-__global__ void k_env_reset_draw(SamplerDev sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, u32 sample, i32* task_ids,
+__global__ void k_env_reset_draw(SamplerDev sampler, const u64* seed, u64 first_env, u64 rows, const u8* mask, u32 sample, i32* task_ids,
                                  u32* reset_counts, const u64* sampling_seeds, const u32* env_ids)
 {
     for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
@@ -1607,19 +1607,35 @@ __global__ void k_env_reset_draw(SamplerDev sampler, u64 seed, u64 first_env, u6
             continue;
         const u32 rc = reset_counts[i];
         if (sample && task_ids)
-            task_ids[i] = instance_draw(sampling_seeds ? sampling_seeds[i] : seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i, rc,
+            task_ids[i] = instance_draw(sampling_seeds ? sampling_seeds[i] : *seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i, rc,
                                         sampler.instances, sampler.thresholds, sampler.indices, sampler.m);
         reset_counts[i] = rc + 1;
     }
 }
 
+/// The random policy's next choices without a step (DeviceEnv::random_actions, include/mymyr/cuda/env.hpp:189-192):
+/// out[i] = successor_index(key, env id, draws[i], min(count[i], max_actions)), 0 where that is 0.
+__global__ void k_env_random_actions(const u64* seed, const u64* seeds, const u32* env_ids, u64 first_env, const u64* draws, const i32* count,
+                                     u64 rows, u32 max_actions, i64* out)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        const u32 c = min(static_cast<u32>(max(count[i], 0)), max_actions);
+        out[i] = c ? static_cast<i64>(successor_index(seeds ? seeds[i] : *seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i, draws[i], c))
+                   : 0;
+    }
+}
+
+/// The device seed word of an env, written in stream order.
+__global__ void k_set_word(u64* p, u64 v) { *p = v; }
+
 /// Per row: the instance its next autoreset would draw (with the row's current reset counter), for a step without
 /// next_task_ids over a batch with reset counters and an env with a sampler.
-__global__ void k_env_sample_next(SamplerDev sampler, u64 seed, u64 first_env, u64 rows, const u32* reset_counts, const u64* sampling_seeds,
+__global__ void k_env_sample_next(SamplerDev sampler, const u64* seed, u64 first_env, u64 rows, const u32* reset_counts, const u64* sampling_seeds,
                                   const u32* env_ids, i32* next)
 {
     for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
-        next[i] = instance_draw(sampling_seeds ? sampling_seeds[i] : seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i,
+        next[i] = instance_draw(sampling_seeds ? sampling_seeds[i] : *seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i,
                                 reset_counts[i], sampler.instances, sampler.thresholds, sampler.indices, sampler.m);
 }
 
@@ -2184,6 +2200,31 @@ F variant_of(u32 v, F gs, F ss, F gl, F sl)
 }
 }  // namespace
 
+void prepare_env_launches(const TaskDev& T)
+{
+    size_t lds = 0;
+    waves_per_block(T, &lds);
+    for (const void* fn : {reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false>, k_env_step<true, true, false>,
+                                                                 k_env_step<false, false, false>, k_env_step<false, true, false>)),
+                           reinterpret_cast<const void*>(variant(T, k_env_step<true, false, true>, k_env_step<true, true, true>,
+                                                                 k_env_step<false, false, true>, k_env_step<false, true, true>)),
+                           reinterpret_cast<const void*>(variant(T, k_env_count<true, false, false>, k_env_count<true, true, false>,
+                                                                 k_env_count<false, false, false>, k_env_count<false, true, false>)),
+                           reinterpret_cast<const void*>(variant(T, k_env_count<true, false, true>, k_env_count<true, true, true>,
+                                                                 k_env_count<false, false, true>, k_env_count<false, true, true>))})
+        set_lds(fn, lds);
+}
+
+void prepare_grouped_launches(u32 v, size_t lds)
+{
+    set_lds(reinterpret_cast<const void*>(variant_of(v, k_env_step_grouped<false, false>, k_env_step_grouped<true, false>,
+                                                     k_env_step_grouped<false, true>, k_env_step_grouped<true, true>)),
+            lds);
+    set_lds(reinterpret_cast<const void*>(variant_of(v, k_env_count_grouped<false, false>, k_env_count_grouped<true, false>,
+                                                     k_env_count_grouped<false, true>, k_env_count_grouped<true, true>)),
+            lds);
+}
+
 void launch_env_step_grouped(const EnvArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream)
 {
     if (a.rows == 0)
@@ -2277,7 +2318,23 @@ void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows,
     }
 }
 
-void launch_env_sample_next(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u32* reset_counts,
+void launch_env_random_actions(const u64* seed, const u64* seeds, const u32* env_ids, u64 first_env, const u64* draws, const i32* count,
+                               u64 rows, u32 max_actions, i64* out, hipStream_t stream)
+{
+    if (rows == 0)
+        return;
+    hipLaunchKernelGGL(k_env_random_actions, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream,
+                       seed, seeds, env_ids, first_env, draws, count, rows, max_actions, out);
+    launch_check("env random actions");
+}
+
+void launch_set_word(u64* p, u64 v, hipStream_t stream)
+{
+    hipLaunchKernelGGL(k_set_word, dim3(1), dim3(1), 0, stream, p, v);
+    launch_check("set word");
+}
+
+void launch_env_sample_next(const SamplerDev& sampler, const u64* seed, u64 first_env, u64 rows, const u32* reset_counts,
                             const u64* sampling_seeds, const u32* env_ids, i32* next, hipStream_t stream)
 {
     if (rows == 0)
@@ -2287,7 +2344,7 @@ void launch_env_sample_next(const SamplerDev& sampler, u64 seed, u64 first_env, 
     launch_check("env sample next");
 }
 
-void launch_env_reset_draw(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
+void launch_env_reset_draw(const SamplerDev& sampler, const u64* seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
                            u32* reset_counts, const u64* sampling_seeds, const u32* env_ids, hipStream_t stream)
 {
     if (rows == 0 || !reset_counts)

@@ -12,7 +12,6 @@ namespace mya
 {
 struct EnvCfg
 {
-    u64 seed;
     u32 max_steps;
     float step_reward, goal_reward, dead_end_reward;
     i32 dead_end_none;      // DeadEnd::None
@@ -73,7 +72,8 @@ struct EnvArgs
     u32 words;  // row words of the batch (>= every instance's W)
     i32* task_ids;             // [rows]: each row's instance (null: instance 0); an autoreset writes the new one
     const i32* next_task_ids;  // [rows]: the instance an autoresetting row restarts in (null: its own)
-    const u64* seeds;          // [rows]: per-row keys of the random policy (null: cfg.seed)
+    const u64* seed;           // device word: the env's RNG key (set_seed writes it in stream order)
+    const u64* seeds;          // [rows]: per-row keys of the random policy (null: *seed)
     const u32* env_ids;        // [rows]: per-row env ids (null: first_env + row)
     u32* reset_counts;         // [rows]: per-row reset counters (null: none), advanced by every autoreset
 
@@ -149,6 +149,10 @@ constexpr u32 kPerInstanceLaunches = 16;
 /// one variant: waves per block and dynamic LDS bytes, from the largest hot tables and per-wave region among them.
 u32 env_variant(const TaskDev& T);
 unsigned grouped_shape(const TaskDev* const* tasks, u32 n, size_t* lds_bytes, u32* wave_words);
+/// Raises the dynamic LDS limits of the step and count kernels an instance (or a variant's grouped launch) uses, so
+/// that later launches make no runtime call besides the launch (HIP graph capture).
+void prepare_env_launches(const TaskDev& T);
+void prepare_grouped_launches(u32 v, size_t lds);
 /// The grouped step / count of the rows of the instances of variant v (grid: enough blocks for every chunk).
 void launch_env_step_grouped(const EnvArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream);
 void launch_env_count_grouped(const CountArgs& a, u32 v, unsigned nw, size_t lds, hipStream_t stream);
@@ -165,13 +169,20 @@ void launch_env_reset(const InstDev* inst, u32 instances, u64* states, u64 rows,
 
 /// Before a reset of the rows with mask[i] != 0: with `sample` their task ids drawn from the sampler (with the rows'
 /// reset counters), then the counters advanced (HostEnv::reset, src/mymyr/rl/env.cpp:223-255).
-void launch_env_reset_draw(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
+void launch_env_reset_draw(const SamplerDev& sampler, const u64* seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,
                            u32* reset_counts, const u64* sampling_seeds, const u32* env_ids, hipStream_t stream);
 
 /// next[i] = the instance row i's next autoreset draws from the sampler (its current reset counter, its sampling key or
-/// `seed`, its env id or first_env + i): the next_task_ids of a step that restarts rows in sampled instances.
-void launch_env_sample_next(const SamplerDev& sampler, u64 seed, u64 first_env, u64 rows, const u32* reset_counts,
+/// *seed, its env id or first_env + i): the next_task_ids of a step that restarts rows in sampled instances.
+void launch_env_sample_next(const SamplerDev& sampler, const u64* seed, u64 first_env, u64 rows, const u32* reset_counts,
                             const u64* sampling_seeds, const u32* env_ids, i32* next, hipStream_t stream);
+
+/// The random policy's next choices without a step: out[i] = the successor index a step would draw now for row i,
+/// limited to max_actions, 0 where count[i] is 0 (DeviceEnv::random_actions, include/mymyr/cuda/env.hpp:189-192).
+void launch_env_random_actions(const u64* seed, const u64* seeds, const u32* env_ids, u64 first_env, const u64* draws, const i32* count,
+                               u64 rows, u32 max_actions, i64* out, hipStream_t stream);
+/// *p = v in stream order (one thread).
+void launch_set_word(u64* p, u64 v, hipStream_t stream);
 
 /// Per-env goal masks at a reset of the rows with mask[i] != 0: the instance's goal written into them, or with
 /// keep_goals the given masks kept, checked against the instance's fluent slots (kStatusGoalMask) and at_goal tested

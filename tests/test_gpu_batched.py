@@ -1,0 +1,161 @@
+"""The torch BatchedEnv drop-in (mymyr_amd.batched, the reference's mymyr.rl.torch.BatchedEnv and CapturedRollout)
+on the HIP env: the task-table trajectories of the compiled reference (tests/golden/env_table.json) replayed through
+BatchedEnv's reset / step / sampler calls, digest-equal; captured rollouts equal to eager steps, byte for byte;
+random_actions, set_seed and is_goal against their definitions."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def u64(t):
+    return host(t).view(np.uint64)
+
+
+def load_tasks(golden, table):
+    from mymyr_amd import workloads
+    from mymyr_amd.task import Task
+
+    return [Task.from_text_file(p) for p in workloads.table_files(table, golden.TASKS)]
+
+
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_many", "gridworld_many_large"])
+def test_batched_env_matches_reference(golden, case):
+    from mymyr_amd import rl
+    from mymyr_amd.batched import BatchedEnv
+
+    g = golden.load("env_table.json")[case]
+    c = golden.TABLE_CASES[case]
+    rows, goals = c["rows"], c.get("goals", False)
+    assert not c.get("keys"), "BatchedEnv has no per-row keys"
+    ts = load_tasks(golden, c["table"])
+    inp = golden.table_inputs(case, len(ts))
+    print(f"batched env case {case}: {rows} envs x {c['steps']} steps", flush=True)
+    sampler = None
+    if c.get("sampler") is not None:
+        sampler = rl.InstanceSampler(len(ts), None if c["sampler"] == "uniform" else c["sampler"])
+    env = BatchedEnv(ts, rows, task_ids=inp["task_ids"], sampler=sampler, first_env=5, goals=goals, **c["env"])
+    init = [t.initial_state(env.words) for t in ts]
+
+    def state():
+        b = {"states": u64(env.states), "task_ids": host(env.task_ids), "steps": host(env.steps), "draws": u64(env.draws),
+             "at_goal": host(env.at_goal).view(np.uint8)}
+        if goals:
+            b["goal_pos"], b["goal_neg"] = u64(env.goal_pos), u64(env.goal_neg)
+        if sampler is not None:
+            b["reset_counts"] = host(env.reset_counts).view(np.uint32)
+        return golden.table_state(b)
+
+    assert golden.arrays_digest(*state(), host(env.count)) == g["resets"]["initial"]
+    assert torch.equal(env.is_goal(), env.at_goal)
+    for k in range(c["steps"]):
+        if k in inp["resets"]:
+            mask, new, keep, sample = inp["resets"][k]
+            m = torch.from_numpy(mask.astype(bool))
+            if keep:
+                ids = host(env.task_ids)
+                gp = np.zeros((rows, env.words), np.uint64)
+                for i in range(rows):
+                    gp[i] = init[ids[i]]
+                env.reset(m, goal_pos=torch.from_numpy(gp.view(np.int64)).cuda(), goal_neg=torch.zeros_like(env.goal_neg))
+            else:
+                assert sample == (new is None)
+                env.reset(m, task_ids=None if new is None else torch.from_numpy(new))
+            assert golden.arrays_digest(*state(), host(env.count)) == g["resets"][str(k)], f"{case}: reset at step {k}"
+        acts = None
+        if c["policy"] == "given":
+            acts = torch.from_numpy(golden.given_actions(inp["u"][k], host(env.count)))
+        nxt = inp["next"][k]
+        r = env.step(acts, next_task_ids=None if nxt is None else torch.from_numpy(nxt), final=True)
+        d = golden.arrays_digest(*state(), host(r.reward), host(r.terminated).view(np.uint8), host(r.truncated).view(np.uint8),
+                                 host(r.count), host(r.schema), host(r.binding), host(r.goal).view(np.uint8),
+                                 host(r.invalid).view(np.uint8), u64(r.final_states))
+        assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
+        assert torch.equal(r.states, env.states) and torch.equal(r.at_goal, env.at_goal)
+    env.check_errors()
+
+
+def _twins(golden, **kw):
+    from mymyr_amd.batched import BatchedEnv
+
+    ts = load_tasks(golden, "transport_table")
+    n = 2000
+    return BatchedEnv(ts, n, **kw), BatchedEnv(ts, n, **kw)
+
+
+@pytest.mark.parametrize("policy", [None, "argmax"])
+def test_captured_rollout_equals_eager_steps(golden, policy):
+    """K steps captured into one HIP graph and replayed twice equal the same calls made eagerly on a twin env."""
+    a, b = _twins(golden, seed=3, max_steps=7, sampler="uniform")
+    pol = None
+    if policy == "argmax":
+        pol = lambda env: torch.clamp(env.count.to(torch.int64) - 1, min=0)  # the last successor: capturable, device only
+    K = 6
+    roll = a.capture(K, pol, final=True)
+    for rep in range(2):
+        out = roll.replay()
+        torch.cuda.synchronize()
+        for k in range(K):
+            act = None if pol is None else pol(b)
+            r = b.step(act, final=True)
+            for name in ("reward", "terminated", "truncated", "goal", "invalid", "schema", "binding", "final_states", "count",
+                         "states", "task_ids", "at_goal"):
+                assert torch.equal(getattr(out, name)[k], getattr(r, name)), f"replay {rep} step {k}: {name}"
+            if pol is not None:
+                assert torch.equal(out.action[k], act), f"replay {rep} step {k}: action"
+        for name in ("states", "task_ids", "steps", "draws", "reset_counts", "count", "at_goal", "counts"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), f"replay {rep}: env {name}"
+    a.check_errors()
+    b.check_errors()
+
+
+def test_random_actions_set_seed_and_goal(golden):
+    from mymyr_amd.batched import BatchedEnv
+
+    a, b = _twins(golden, seed=11, max_steps=9, sampler="uniform")
+    for k in range(5):
+        act = a.random_actions()
+        ra = a.step(act)
+        rb = b.step(None)
+        for name in ("reward", "schema", "binding", "count", "states", "task_ids"):
+            assert torch.equal(getattr(ra, name), getattr(rb, name)), f"step {k}: {name}"
+    capped = a.random_actions(max_actions=2)
+    assert bool(((capped >= 0) & (capped < 2)).all())
+    assert bool((capped[a.count == 0] == 0).all())
+    # set_seed: the draws restart with the new key, as a fresh env with that seed
+    ts = a.tasks
+    c = BatchedEnv(ts, a.num_envs, seed=99, max_steps=9, sampler="uniform")
+    a.set_seed(99)
+    assert int(a.draws.abs().sum()) == 0 and int(a.reset_counts.abs().sum()) == 0
+    ids = c.task_ids.clone()
+    a.reset(task_ids=ids)
+    c.reset(task_ids=ids)
+    a.reset_counts.copy_(c.reset_counts)
+    for k in range(4):
+        ra, rc = a.step(), c.step()
+        for name in ("reward", "states", "task_ids", "count"):
+            assert torch.equal(getattr(ra, name), getattr(rc, name)), f"after set_seed step {k}: {name}"
+    assert torch.equal(a.is_goal(), a.at_goal)
+    a.check_errors()
+    c.check_errors()
+
+
+def test_batched_env_argument_errors(golden):
+    from mymyr_amd.batched import BatchedEnv
+
+    ts = load_tasks(golden, "gridworld_table")
+    with pytest.raises(NotImplementedError):
+        BatchedEnv(ts, 8, actions="label")
+    with pytest.raises(ValueError, match="task id 3 of row 2 is outside the table's 3 instances"):
+        BatchedEnv(ts, 8, task_ids=[0, 1, 3, 0, 1, 2, 0, 1])
+    env = BatchedEnv(ts, 8, sampler=None, task_ids=0)
+    assert env.sampler is None and int(env.task_ids.sum()) == 0
+    with pytest.raises(TypeError):
+        env.step(torch.zeros(8, dtype=torch.float32))
