@@ -238,11 +238,12 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
                   void* stream);
 /* HostEnv::step (env.cpp:530-548 / step_row_impl 351-528): actions (device, int64 [rows], optional: the random policy
  * when null); next_task_ids (device, int32 [rows], optional: the instance an autoresetting row restarts in; null: its
- * next sampled instance when the env has a sampler and the batch reset counters, else its own). Async on the stream; device-side failures set the sticky status that mya_env_check reports: among them a
- * task id outside the table in batch->task_ids (the row is not stepped) or in next_task_ids (an autoresetting row
- * keeps its instance; DeviceEnv::step, include/mymyr/cuda/env.hpp:180-184). Over several instances the rows are
- * grouped by instance on the device first (a counting sort of task_ids into env-owned scratch, allocated on the
- * first call with a larger batch). */
+ * next sampled instance when the env has a sampler and the batch reset counters, else its own). Async on the stream;
+ * device-side failures set the sticky status that mya_env_check reports: among them a task id outside the table in
+ * batch->task_ids (over several instances the row is not stepped; a one-instance env steps every row as instance 0)
+ * or in next_task_ids (an autoresetting row keeps its instance; DeviceEnv::step, include/mymyr/cuda/env.hpp:180-184).
+ * Over several instances the rows are grouped by instance on the device first (a counting sort of task_ids into
+ * env-owned scratch, allocated on the first call with a larger batch). */
 int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
                  const int32_t* next_task_ids, void* stream);
 /* Sizes the env's scratch for batches of up to `rows` rows and sets its kernels' LDS limits now (the reference device
@@ -322,6 +323,13 @@ typedef struct mya_expansion
 
 int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, const mya_expand_options* options,
                mya_expansion* out, void* stream);
+/* rl::expand over the env's task table (include/mymyr/rl/expand.hpp:1-130: a batch over a TaskTable): row i is a state
+ * of instance task_ids[i] (device int32 [rows]; null only over a table of one instance), rows are at least the
+ * widest instance's words, and the successors of row i are states of its instance, labelled with its objects. The
+ * rows are grouped by instance on the device with the env's scratch. Same outputs, options and errors as mya_expand,
+ * plus an error for a task id outside the table. Synchronous. */
+int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids, uint64_t rows, uint32_t words,
+                   const mya_expand_options* options, mya_expansion* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------- BrFS */
 

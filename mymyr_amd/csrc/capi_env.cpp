@@ -117,10 +117,11 @@ X* scratch_rows(mya_env* e, u64 rows, X* mya_env::*member, u64 mya_env::*have)
 
 /// Groups the batch's rows by instance into the env's scratch (grown under the env's lock; a call with a batch no
 /// larger than before allocates nothing).
-RowGroups group_rows(mya_env* e, const mya_env_batch* b, hipStream_t stream)
+RowGroups group_rows(mya_env* e, const mya_env_batch* b, hipStream_t stream, u32* status = nullptr)
 {
     scratch_rows(e, b->rows, &mya_env::d_order, &mya_env::group_rows);
-    launch_group_rows(b->task_ids, b->rows, e->instances(), e->d_hist, e->d_order, e->d_starts, e->d_chunks, e->d_status, stream);
+    launch_group_rows(b->task_ids, b->rows, e->instances(), e->d_hist, e->d_order, e->d_starts, e->d_chunks, status ? status : e->d_status,
+                      stream);
     return RowGroups{e->d_order, e->d_starts, e->d_chunks};
 }
 
@@ -180,6 +181,152 @@ void run_count(mya_env* env, const mya_env_batch* batch, CountArgs& a, hipStream
             a.wave_words = l.wave_words;
             launch_env_count_grouped(a, l.variant, l.nw, l.lds, s);
         }
+}
+
+/// The flat expansion of rows over instances `inst` (one: batch order; several: grouped by instance with `env`'s
+/// scratch and the rows' task ids).
+void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const int32_t* task_ids, const uint64_t* states, uint64_t rows,
+                 uint32_t words, const mya_expand_options* options, mya_expansion* out, hipStream_t stream)
+{
+    {
+        if (!options || !out || (rows && !states))
+            throw std::invalid_argument("mymyr_amd: expand: null argument");
+        if (!options->canonical_order || options->witness_pruning)
+            throw std::invalid_argument("mymyr_amd: expand: the device expansion takes canonical_order on and witness_pruning off");
+        TaskDev T = *inst[0];  // the widest instance's words and label width stand for the table in the checks
+        for (const TaskDev* t : inst)
+        {
+            T.W = std::max(T.W, t->W);
+            T.label_width = std::max(T.label_width, t->label_width);
+        }
+        constexpr u64 kMaxRows = (u64{1} << 31) - 1;
+        if (rows > kMaxRows)
+            throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 states in one batch");
+        if (words < T.W)
+            throw std::invalid_argument("mymyr: expand: state rows of " + std::to_string(words) + " words; the task needs " +
+                                        std::to_string(T.W));
+        if (out->binding && out->label_width < T.label_width)
+            throw std::invalid_argument("mymyr: expand: label width " + std::to_string(out->label_width) +
+                                        " is below the largest schema arity " + std::to_string(T.label_width));
+        if (out->capacity > kMaxRows)
+            throw std::invalid_argument("mymyr: expand: capacity above 2^31 - 1 rows");
+        if (out->succ && out->words == 0 && out->capacity)
+            throw std::invalid_argument("mymyr: expand: successor rows of zero words");
+        if (out->goal && !out->succ)
+            throw std::invalid_argument("mymyr: expand: goal flags need the successor rows");
+        if (options->drop_noops && out->capacity && !out->index)
+            throw std::invalid_argument("mymyr: expand: drop_noops requires index");
+        out->generated = out->total = 0;
+        out->words_needed = 0;
+        // scratch: per-row counts and no-op counts, offsets before and after dropping, scan scratch, status words
+        const u64 n = std::max<u64>(rows, 1);
+        u32* counts = dev_alloc<u32>(n, "expand counts");
+        u32* noops = dev_alloc<u32>(n, "expand no-op counts");
+        u32* kept = dev_alloc<u32>(n, "expand kept counts");
+        u64* pre = dev_alloc<u64>(n + 1, "expand offsets");
+        u64* fin = dev_alloc<u64>(n + 1, "expand kept offsets");
+        u64* scratch = dev_alloc<u64>(scan_scratch_words(n), "expand scan scratch");
+        u32* words_status = dev_alloc<u32>(2, "expand status");  // [0] words needed, [1] status
+        struct Free
+        {
+            std::vector<void*> p;
+            ~Free()
+            {
+                for (void* q : p)
+                    dev_free(q);
+            }
+        } freeing{{counts, noops, kept, pre, fin, scratch, words_status}};
+        launch_fill_u32(words_status, 2, 0, stream);
+        ExpandArgs a{};
+        a.T = *inst[0];
+        if (inst.size() > 1)
+        {
+            mya_env_batch b{};
+            b.states = const_cast<uint64_t*>(states);
+            b.rows = rows;
+            b.words = words;
+            b.task_ids = const_cast<int32_t*>(task_ids);
+            a.groups = group_rows(env, &b, stream, words_status + 1);
+        }
+        // one launch over the batch, or one per instance over its group
+        auto launch = [&](ExpandArgs& x) {
+            if (!x.groups.order)
+            {
+                launch_expand(x, stream);
+                return;
+            }
+            for (u32 k = 0; k < inst.size(); ++k)
+            {
+                x.T = *inst[k];
+                x.instance = k;
+                launch_expand(x, stream);
+            }
+        };
+        a.states = states;
+        a.rows = rows;
+        a.words = words;
+        a.drop_noops = options->drop_noops ? 1 : 0;
+        a.out_words = out->words;
+        a.label_width = out->label_width;
+        a.counts = counts;
+        a.noops = noops;
+        a.words_needed = words_status;
+        a.status = words_status + 1;
+        a.pass = 0;
+        launch(a);
+        launch_exclusive_scan(counts, pre, rows, scratch, pre + rows, stream);
+        if (a.drop_noops)
+        {
+            launch_kept_counts(counts, noops, rows, kept, stream);
+            launch_exclusive_scan(kept, fin, rows, scratch, fin + rows, stream);
+        }
+        u64 totals[2] = {0, 0};
+        u32 st[2] = {0, 0};
+        hip_check(hipMemcpyAsync(&totals[0], pre + rows, sizeof(u64), hipMemcpyDeviceToHost, stream), "expand total");
+        if (a.drop_noops)
+            hip_check(hipMemcpyAsync(&totals[1], fin + rows, sizeof(u64), hipMemcpyDeviceToHost, stream), "expand total");
+        hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
+        hip_check(hipStreamSynchronize(stream), "expand");
+        if (options->validate && (st[1] & kStatusWideRow))
+            throw std::invalid_argument("mymyr: expand: a state has atoms past the task's slots");
+        if (st[1] & kStatusTaskId)
+            throw std::invalid_argument("mymyr: expand: a task id is outside the table's " + std::to_string(inst.size()) + " instances");
+        if (st[1] & ~kStatusWideRow)
+            throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
+        const u64 generated = totals[0];
+        if (generated > kMaxRows)
+            throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 successors in one batch");
+        // an overflow with drop_noops reports the counts before dropping
+        const bool dropping = a.drop_noops && generated <= out->capacity;
+        const u64* offs = dropping ? fin : pre;
+        out->generated = generated;
+        out->total = dropping ? totals[1] : generated;
+        if (out->offsets)
+            launch_offsets_i32(offs, rows + 1, out->offsets, stream);
+        const bool rows_out = out->succ || out->parent || out->schema || out->binding || out->goal || out->succ_hash || out->noop ||
+                              out->index;
+        if ((rows_out && out->capacity) || (out->succ && out->words < T.W))
+        {
+            a.pass = 1;
+            a.drop_noops = dropping ? 1 : 0;
+            a.offsets = offs;
+            a.capacity = out->capacity;
+            a.succ = out->succ;
+            a.parent = out->parent;
+            a.schema = out->schema;
+            a.binding = out->binding;
+            a.goal = out->goal;
+            a.succ_hash = out->succ_hash;
+            a.noop = out->noop;
+            a.index = out->index;
+            launch(a);
+        }
+        hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
+        hip_check(hipStreamSynchronize(stream), "expand");
+        if (st[1] & ~kStatusWideRow)
+            throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
+        out->words_needed = st[0];
+    }
 }
 
 void free_env(mya_env* e)
@@ -486,6 +633,9 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         }
         if (!grouped(env))
         {
+            // the batch-order step runs every row as instance 0: given ids are only checked
+            launch_check_ids(batch->task_ids, batch->rows, 1, env->d_status, s);
+            launch_check_ids(next_task_ids, batch->rows, 1, env->d_status, s);
             launch_env_step(a, s);
             return;
         }
@@ -650,118 +800,28 @@ int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32
 }
 
 int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, const mya_expand_options* options,
-               mya_expansion* out, void* stream_)
+               mya_expansion* out, void* stream)
 {
     return guarded([&] {
-        if (!task || !options || !out || (rows && !states))
+        if (!task)
             throw std::invalid_argument("mymyr_amd: expand: null argument");
-        if (!options->canonical_order || options->witness_pruning)
-            throw std::invalid_argument("mymyr_amd: expand: the device expansion takes canonical_order on and witness_pruning off");
-        const DeviceTask& d = device_task(task);
-        const TaskDev& T = *d.thost;
-        constexpr u64 kMaxRows = (u64{1} << 31) - 1;
-        if (rows > kMaxRows)
-            throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 states in one batch");
-        if (words < T.W)
-            throw std::invalid_argument("mymyr: expand: state rows of " + std::to_string(words) + " words; the task needs " +
-                                        std::to_string(T.W));
-        if (out->binding && out->label_width < T.label_width)
-            throw std::invalid_argument("mymyr: expand: label width " + std::to_string(out->label_width) +
-                                        " is below the largest schema arity " + std::to_string(T.label_width));
-        if (out->capacity > kMaxRows)
-            throw std::invalid_argument("mymyr: expand: capacity above 2^31 - 1 rows");
-        if (out->succ && out->words == 0 && out->capacity)
-            throw std::invalid_argument("mymyr: expand: successor rows of zero words");
-        if (out->goal && !out->succ)
-            throw std::invalid_argument("mymyr: expand: goal flags need the successor rows");
-        if (options->drop_noops && out->capacity && !out->index)
-            throw std::invalid_argument("mymyr: expand: drop_noops requires index");
-        const auto stream = static_cast<hipStream_t>(stream_);
-        out->generated = out->total = 0;
-        out->words_needed = 0;
-        // scratch: per-row counts and no-op counts, offsets before and after dropping, scan scratch, status words
-        const u64 n = std::max<u64>(rows, 1);
-        u32* counts = dev_alloc<u32>(n, "expand counts");
-        u32* noops = dev_alloc<u32>(n, "expand no-op counts");
-        u32* kept = dev_alloc<u32>(n, "expand kept counts");
-        u64* pre = dev_alloc<u64>(n + 1, "expand offsets");
-        u64* fin = dev_alloc<u64>(n + 1, "expand kept offsets");
-        u64* scratch = dev_alloc<u64>(scan_scratch_words(n), "expand scan scratch");
-        u32* words_status = dev_alloc<u32>(2, "expand status");  // [0] words needed, [1] status
-        struct Free
-        {
-            std::vector<void*> p;
-            ~Free()
-            {
-                for (void* q : p)
-                    dev_free(q);
-            }
-        } freeing{{counts, noops, kept, pre, fin, scratch, words_status}};
-        launch_fill_u32(words_status, 2, 0, stream);
-        ExpandArgs a{};
-        a.T = T;
-        a.states = states;
-        a.rows = rows;
-        a.words = words;
-        a.drop_noops = options->drop_noops ? 1 : 0;
-        a.out_words = out->words;
-        a.label_width = out->label_width;
-        a.counts = counts;
-        a.noops = noops;
-        a.words_needed = words_status;
-        a.status = words_status + 1;
-        a.pass = 0;
-        launch_expand(a, stream);
-        launch_exclusive_scan(counts, pre, rows, scratch, pre + rows, stream);
-        if (a.drop_noops)
-        {
-            launch_kept_counts(counts, noops, rows, kept, stream);
-            launch_exclusive_scan(kept, fin, rows, scratch, fin + rows, stream);
-        }
-        u64 totals[2] = {0, 0};
-        u32 st[2] = {0, 0};
-        hip_check(hipMemcpyAsync(&totals[0], pre + rows, sizeof(u64), hipMemcpyDeviceToHost, stream), "expand total");
-        if (a.drop_noops)
-            hip_check(hipMemcpyAsync(&totals[1], fin + rows, sizeof(u64), hipMemcpyDeviceToHost, stream), "expand total");
-        hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
-        hip_check(hipStreamSynchronize(stream), "expand");
-        if (options->validate && (st[1] & kStatusWideRow))
-            throw std::invalid_argument("mymyr: expand: a state has atoms past the task's slots");
-        if (st[1] & ~kStatusWideRow)
-            throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
-        const u64 generated = totals[0];
-        if (generated > kMaxRows)
-            throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 successors in one batch");
-        // an overflow with drop_noops reports the counts before dropping
-        const bool dropping = a.drop_noops && generated <= out->capacity;
-        const u64* offs = dropping ? fin : pre;
-        out->generated = generated;
-        out->total = dropping ? totals[1] : generated;
-        if (out->offsets)
-            launch_offsets_i32(offs, rows + 1, out->offsets, stream);
-        const bool rows_out = out->succ || out->parent || out->schema || out->binding || out->goal || out->succ_hash || out->noop ||
-                              out->index;
-        if ((rows_out && out->capacity) || (out->succ && out->words < T.W))
-        {
-            a.pass = 1;
-            a.drop_noops = dropping ? 1 : 0;
-            a.offsets = offs;
-            a.capacity = out->capacity;
-            a.succ = out->succ;
-            a.parent = out->parent;
-            a.schema = out->schema;
-            a.binding = out->binding;
-            a.goal = out->goal;
-            a.succ_hash = out->succ_hash;
-            a.noop = out->noop;
-            a.index = out->index;
-            launch_expand(a, stream);
-        }
-        hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
-        hip_check(hipStreamSynchronize(stream), "expand");
-        if (st[1] & ~kStatusWideRow)
-            throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
-        out->words_needed = st[0];
+        expand_rows({device_task(task).thost.get()}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream));
+    });
+}
+
+int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids, uint64_t rows, uint32_t words,
+                   const mya_expand_options* options, mya_expansion* out, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: expand: null env");
+        if (!task_ids && rows && env->instances() > 1)
+            throw std::invalid_argument("mymyr: expand: a batch over a table of " + std::to_string(env->instances()) +
+                                        " instances needs task ids");
+        std::vector<const TaskDev*> inst;
+        for (const EnvInstance& in : env->inst)
+            inst.push_back(&in.T);
+        expand_rows(inst, env, task_ids, states, rows, words, options, out, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -1162,8 +1162,8 @@ unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
 /// are T / H and whose wave region is L. An autoreset restarts the row in next_task_ids[i] when that names an instance
 /// (else in k), writing the new instance's initial state and goal masks over the words the row may have dirtied
 /// (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138) and its id into task_ids.
-template<bool kLevels>
-__device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane)
+template<bool kLevels, bool kOne>
+__device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane, u64 seed)
 {
     const u32 Lw = A.label_width;
     u64* grow = A.states + i * A.words;
@@ -1214,7 +1214,11 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
                 a = static_cast<u32>(act);
         }
         else if (!already_goal)
-            a = successor_index(A.seeds ? A.seeds[i] : *A.seed, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, A.draws[i], c);
+        {
+            // the key: the row's own, or the env's (read here in the batch-order path, which keeps fewer values live)
+            const u64 key = A.seeds ? A.seeds[i] : (kOne ? *A.seed : seed);
+            a = successor_index(key, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, A.draws[i], c);
+        }
         u32 rank = 0;
         if (st == kOk)
         {
@@ -1285,7 +1289,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     // next_task_ids[i], where an id outside the table sets the status (in every row, as the reference checks the whole
     // array) and keeps the row's instance
     u32 next = k;
-    if (A.next_task_ids)
+    if (!kOne && A.next_task_ids)
     {
         const i32 v = A.next_task_ids[i];
         if (v < 0 || static_cast<u32>(v) >= A.instances)
@@ -1303,7 +1307,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         // step with the counter's value before this advance)
         if (A.reset_counts && lane == 0)
             A.reset_counts[i] += 1;
-        const InstDev& J = A.inst[next];
+        const InstDev& J = A.inst[next];  // a one-instance env restarts in instance 0
         const u32 z = min(A.words, max(J.W, T.W));  // the words the row may have dirtied: its old and new instance's
         for (u32 q = lane; q < z; q += kWave)
             grow[q] = q < J.W ? J.initial[q] : 0;
@@ -1315,7 +1319,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             }
         if (lane == 0)
         {
-            if (A.task_ids)
+            if (!kOne && A.task_ids)
                 A.task_ids[i] = static_cast<i32>(next);
             if (A.count)
                 A.count[i] = static_cast<i32>(J.init_count);
@@ -1353,7 +1357,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (A.atoms)
         {
             if (reset)
-                encode_row(A.inst[next].initial, A.inst[next].W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
+                encode_row(A.inst[next].initial, A.inst[next].W, A.atoms + i * A.max_atoms,
+                           A.max_atoms, lane, A.status);
             else
                 encode_row(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
         }
@@ -1364,11 +1369,11 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     wave_sync();
 }
 
-/// The step of a batch of one instance: every row in batch order with the kernel-argument tables (a row whose task id
-/// is not 0 names no instance: it sets kStatusTaskId and is not stepped); with kGroup, the rows of one instance's group
-/// of a batch grouped by instance.
+/// The step of a batch of one instance: every row in batch order with the kernel-argument tables, as instance 0 (the
+/// host checks given task ids and next_task_ids with launch_check_ids first); with kGroup, the rows of one instance's
+/// group of a batch grouped by instance.
 template<bool kStaged, bool kLevels, bool kGroup>
-__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kGroup ? 1 : (kLevels ? 3 : 4)))) void k_env_step(EnvArgs A)
+__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
 {
     extern __shared__ u64 smem[];
     const TaskDev& T = A.T;
@@ -1382,8 +1387,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
         Tab<kStaged> H;
         lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
         const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
+        const u64 seed = *A.seed;
         for (u64 j = lo + static_cast<u64>(blockIdx.x) * nw + wave; j < hi; j += static_cast<u64>(gridDim.x) * nw)
-            step_row<kLevels>(A, T, H, L, A.groups.order[j], A.instance, lane);
+            step_row<kLevels, false>(A, T, H, L, A.groups.order[j], A.instance, lane, seed);
     }
     else
     {
@@ -1391,15 +1397,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
         lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
         const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
         for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
-        {
-            if (A.task_ids && A.task_ids[i] != 0)
-            {
-                if (lane == 0)
-                    atomicOr(A.status, kStatusTaskId);
-                continue;
-            }
-            step_row<kLevels>(A, T, H, L, i, 0, lane);
-        }
+            step_row<kLevels, true>(A, T, H, L, i, 0, lane, 0);
     }
 }
 
@@ -1446,8 +1444,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step_grouped(EnvArgs 
         const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * A.wave_words, T);
         const u32 r0 = A.groups.starts[k] + (c - A.groups.chunk_start[k]) * kChunkRows;
         const u32 r1 = min(r0 + kChunkRows, A.groups.starts[k + 1]);
+        const u64 seed = *A.seed;
         for (u32 j = r0 + wave; j < r1; j += nw)
-            step_row<kLevels>(A, T, H, L, A.groups.order[j], k, lane);
+            step_row<kLevels, false>(A, T, H, L, A.groups.order[j], k, lane, seed);
     }
 }
 
@@ -1624,6 +1623,16 @@ __global__ void k_env_random_actions(const u64* seed, const u64* seeds, const u3
         out[i] = c ? static_cast<i64>(successor_index(seeds ? seeds[i] : *seed, env_ids ? static_cast<u64>(env_ids[i]) : first_env + i, draws[i], c))
                    : 0;
     }
+}
+
+/// kStatusTaskId if some ids[i] is outside [0, instances).
+__global__ void k_check_ids(const i32* ids, u64 rows, u32 instances, u32* status)
+{
+    bool bad = false;
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += static_cast<u64>(gridDim.x) * blockDim.x)
+        bad = bad || ids[i] < 0 || static_cast<u32>(ids[i]) >= instances;
+    if (bad)
+        atomicOr(status, kStatusTaskId);
 }
 
 /// The device seed word of an env, written in stream order.
@@ -1892,115 +1901,131 @@ __device__ __forceinline__ u32 trimmed_words(const lds<u64>* row, u32 W, u32 lan
     return top;
 }
 
-template<bool kStaged, bool kLevels>
+/// The expansion of row i (pass 0: its counts and the validation of its words; pass 1: its successors from
+/// offsets[i] on) with the tables of its instance.
+template<bool kLevels>
+__device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 lane)
+{
+    const u32 Lw = A.label_width;
+    const u64* src = A.states + i * A.words;
+    if (A.pass == 0)
+    {
+        // rows must hold no atoms past the task's slots (ExpandOptions::validate)
+        bool wide = false;
+        for (u32 w = lane; w < A.words; w += kWave)
+        {
+            const u64 x = src[w];
+            if (w >= T.W)
+                wide = wide || x != 0;
+            else if (w == T.W - 1 && (T.fluent_slots & 63))
+                wide = wide || (x >> (T.fluent_slots & 63)) != 0;
+        }
+        if (__ballot(wide) && lane == 0)
+            atomicOr(A.status, kStatusWideRow);
+    }
+    load_row_lds(T, L, src, lane);
+    build_view(T, H, L, lane);
+    const u32 c = count_all<kLevels>(T, H, L, lane);
+    if (A.pass == 0 && !A.drop_noops)
+    {
+        if (lane == 0)
+            A.counts[i] = c;
+        return;
+    }
+    const bool keep_all = A.pass == 1 && A.drop_noops && A.noops[i] == c;
+    u32 noops = 0, kept = 0;
+    for (u32 k = 0; k < c; ++k)
+    {
+        u32 s = kNone, rank = 0;
+        select_schema(T, L, k, &s, &rank);
+        if (s == kNone || !pick<kLevels>(T, H, L, s, rank, lane))
+        {
+            if (lane == 0)
+                atomicOr(A.status, kStatusPickFailed);
+            break;
+        }
+        const bool noop = succ_apply(T, H, L, s, lane, A.status);
+        noops += noop ? 1 : 0;
+        if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
+        {
+            const u64 pos = A.offsets[i] + (A.drop_noops ? kept : k);
+            ++kept;
+            const u32 n = (A.succ || A.succ_hash) ? trimmed_words(L.row, T.W, lane) : 0;
+            const bool fits = n <= A.out_words;
+            if (A.succ && !fits && lane == 0)
+                atomicMax(A.words_needed, n);
+            if (pos < A.capacity)
+            {
+                if (A.succ)
+                {
+                    u64* dst = A.succ + pos * A.out_words;
+                    for (u32 w = lane; w < A.out_words; w += kWave)
+                        dst[w] = (fits && w < T.W) ? L.row[w] : 0;
+                }
+                if (A.goal)
+                {
+                    const bool g = goal_test(T, H, L.row, lane);
+                    if (lane == 0)
+                        A.goal[pos] = g ? 1 : 0;
+                }
+                if (lane == 0)
+                {
+                    if (A.succ_hash)
+                    {
+                        // hash_state over the trimmed words: the pairs chained in order
+                        u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
+                        for (u32 w = 0; w < n; w += 2)
+                            h = mulfold(h ^ L.row[w] ^ kHashP1, (w + 1 < n ? L.row[w + 1] : 0) ^ kHashP2);
+                        A.succ_hash[pos] = mix64(h);
+                    }
+                    if (A.noop)
+                        A.noop[pos] = noop ? 1 : 0;
+                    if (A.index)
+                        A.index[pos] = static_cast<i32>(k);
+                    if (A.parent)
+                        A.parent[pos] = static_cast<i32>(i);
+                    if (A.schema)
+                        A.schema[pos] = static_cast<i32>(s);
+                }
+                if (A.binding)
+                {
+                    const u32 arity = H.schemas[s].arity;
+                    for (u32 q = lane; q < Lw; q += kWave)
+                        A.binding[pos * Lw + q] = q < arity ? static_cast<i32>(L.ub[q]) : -1;
+                }
+            }
+        }
+        succ_revert(H, L, s, lane);
+    }
+    if (A.pass == 0 && lane == 0)
+    {
+        A.counts[i] = c;
+        A.noops[i] = noops;
+    }
+    wave_sync();
+}
+
+/// The expansion of a batch of one instance in batch order, or with kGroup of one instance's group of a batch grouped
+/// by instance.
+template<bool kStaged, bool kLevels, bool kGroup>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_expand(ExpandArgs A)
 {
     extern __shared__ u64 smem[];
     const TaskDev& T = A.T;
+    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    u64 lo = 0, hi = A.rows;
+    if constexpr (kGroup)
+    {
+        lo = A.groups.starts[A.instance];
+        hi = A.groups.starts[A.instance + 1];
+        if (lo + static_cast<u64>(blockIdx.x) * nw >= hi)
+            return;
+    }
     Tab<kStaged> H;
     lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
-    const u32 lane = lane_id(), wave = threadIdx.x / kWave, nw = blockDim.x / kWave;
     const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
-    const u32 Lw = A.label_width;
-    for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
-    {
-        const u64* src = A.states + i * A.words;
-        if (A.pass == 0)
-        {
-            // rows must hold no atoms past the task's slots (ExpandOptions::validate)
-            bool wide = false;
-            for (u32 w = lane; w < A.words; w += kWave)
-            {
-                const u64 x = src[w];
-                if (w >= T.W)
-                    wide = wide || x != 0;
-                else if (w == T.W - 1 && (T.fluent_slots & 63))
-                    wide = wide || (x >> (T.fluent_slots & 63)) != 0;
-            }
-            if (__ballot(wide) && lane == 0)
-                atomicOr(A.status, kStatusWideRow);
-        }
-        load_row_lds(T, L, src, lane);
-        build_view(T, H, L, lane);
-        const u32 c = count_all<kLevels>(T, H, L, lane);
-        if (A.pass == 0 && !A.drop_noops)
-        {
-            if (lane == 0)
-                A.counts[i] = c;
-            continue;
-        }
-        const bool keep_all = A.pass == 1 && A.drop_noops && A.noops[i] == c;
-        u32 noops = 0, kept = 0;
-        for (u32 k = 0; k < c; ++k)
-        {
-            u32 s = kNone, rank = 0;
-            select_schema(T, L, k, &s, &rank);
-            if (s == kNone || !pick<kLevels>(T, H, L, s, rank, lane))
-            {
-                if (lane == 0)
-                    atomicOr(A.status, kStatusPickFailed);
-                break;
-            }
-            const bool noop = succ_apply(T, H, L, s, lane, A.status);
-            noops += noop ? 1 : 0;
-            if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
-            {
-                const u64 pos = A.offsets[i] + (A.drop_noops ? kept : k);
-                ++kept;
-                const u32 n = (A.succ || A.succ_hash) ? trimmed_words(L.row, T.W, lane) : 0;
-                const bool fits = n <= A.out_words;
-                if (A.succ && !fits && lane == 0)
-                    atomicMax(A.words_needed, n);
-                if (pos < A.capacity)
-                {
-                    if (A.succ)
-                    {
-                        u64* dst = A.succ + pos * A.out_words;
-                        for (u32 w = lane; w < A.out_words; w += kWave)
-                            dst[w] = (fits && w < T.W) ? L.row[w] : 0;
-                    }
-                    if (A.goal)
-                    {
-                        const bool g = goal_test(T, H, L.row, lane);
-                        if (lane == 0)
-                            A.goal[pos] = g ? 1 : 0;
-                    }
-                    if (lane == 0)
-                    {
-                        if (A.succ_hash)
-                        {
-                            // hash_state over the trimmed words: the pairs chained in order
-                            u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
-                            for (u32 w = 0; w < n; w += 2)
-                                h = mulfold(h ^ L.row[w] ^ kHashP1, (w + 1 < n ? L.row[w + 1] : 0) ^ kHashP2);
-                            A.succ_hash[pos] = mix64(h);
-                        }
-                        if (A.noop)
-                            A.noop[pos] = noop ? 1 : 0;
-                        if (A.index)
-                            A.index[pos] = static_cast<i32>(k);
-                        if (A.parent)
-                            A.parent[pos] = static_cast<i32>(i);
-                        if (A.schema)
-                            A.schema[pos] = static_cast<i32>(s);
-                    }
-                    if (A.binding)
-                    {
-                        const u32 arity = H.schemas[s].arity;
-                        for (u32 q = lane; q < Lw; q += kWave)
-                            A.binding[pos * Lw + q] = q < arity ? static_cast<i32>(L.ub[q]) : -1;
-                    }
-                }
-            }
-            succ_revert(H, L, s, lane);
-        }
-        if (A.pass == 0 && lane == 0)
-        {
-            A.counts[i] = c;
-            A.noops[i] = noops;
-        }
-        wave_sync();
-    }
+    for (u64 j = lo + static_cast<u64>(blockIdx.x) * nw + wave; j < hi; j += static_cast<u64>(gridDim.x) * nw)
+        expand_row<kLevels>(A, T, H, L, kGroup ? A.groups.order[j] : j, lane);
 }
 
 __global__ void k_offsets_i32(const u64* src, u64 n, i32* dst)
@@ -2272,9 +2297,13 @@ void launch_expand(const ExpandArgs& a, hipStream_t stream)
         return;
     size_t lds = 0;
     const unsigned nw = waves_per_block(a.T, &lds);
-    const auto fn = variant(a.T, k_expand<true, false>, k_expand<true, true>, k_expand<false, false>, k_expand<false, true>);
+    const bool group = a.groups.order != nullptr;
+    const auto fn = group ? variant(a.T, k_expand<true, false, true>, k_expand<true, true, true>, k_expand<false, false, true>,
+                                    k_expand<false, true, true>)
+                          : variant(a.T, k_expand<true, false, false>, k_expand<true, true, false>, k_expand<false, false, false>,
+                                    k_expand<false, true, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
     launch_check("expand");
 }
 
@@ -2326,6 +2355,15 @@ void launch_env_random_actions(const u64* seed, const u64* seeds, const u32* env
     hipLaunchKernelGGL(k_env_random_actions, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream,
                        seed, seeds, env_ids, first_env, draws, count, rows, max_actions, out);
     launch_check("env random actions");
+}
+
+void launch_check_ids(const i32* ids, u64 rows, u32 instances, u32* status, hipStream_t stream)
+{
+    if (rows == 0 || !ids)
+        return;
+    hipLaunchKernelGGL(k_check_ids, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 1024))), dim3(256), 0, stream, ids, rows,
+                       instances, status);
+    launch_check("check task ids");
 }
 
 void launch_set_word(u64* p, u64 v, hipStream_t stream)

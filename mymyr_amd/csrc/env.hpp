@@ -181,6 +181,8 @@ void launch_env_sample_next(const SamplerDev& sampler, const u64* seed, u64 firs
 /// limited to max_actions, 0 where count[i] is 0 (DeviceEnv::random_actions, include/mymyr/cuda/env.hpp:189-192).
 void launch_env_random_actions(const u64* seed, const u64* seeds, const u32* env_ids, u64 first_env, const u64* draws, const i32* count,
                                u64 rows, u32 max_actions, i64* out, hipStream_t stream);
+/// kStatusTaskId if some ids[i] (device, [rows]; null: none) is outside [0, instances).
+void launch_check_ids(const i32* ids, u64 rows, u32 instances, u32* status, hipStream_t stream);
 /// *p = v in stream order (one thread).
 void launch_set_word(u64* p, u64 v, hipStream_t stream);
 
@@ -198,11 +200,14 @@ __host__ __device__ inline u64 instance_salt(u32 k) { return static_cast<u64>(k)
 __host__ __device__ inline u32 cache_width(const TaskDev& T) { return T.num_schemas + 2; }
 
 /// The flat expansion of rows (rl::expand, include/mymyr/rl/expand.hpp:1-130). Pass 0 counts each row's successors
-/// (and, with drop_noops, its no-op successors) and checks that rows have no atoms past the task's slots; pass 1 writes
-/// the successors of row i from offsets[i] on (kept rows only with drop_noops), up to capacity.
+/// (and, with drop_noops, its no-op successors) and checks that rows have no atoms past their instance's slots; pass 1
+/// writes the successors of row i from offsets[i] on (kept rows only with drop_noops), up to capacity. Over a table,
+/// one launch per instance expands that instance's group of rows.
 struct ExpandArgs
 {
     TaskDev T;
+    RowGroups groups;  // rows grouped by instance (order null: batch order, one instance)
+    u32 instance;      // with groups, the instance (T's) whose group this launch expands
     const u64* states;
     u64 rows;
     u32 words;

@@ -294,27 +294,77 @@ def successors(task: Task, states: torch.Tensor, cap: int = 4096) -> tuple[torch
     return count, schema, binding, rows
 
 
-def expand(task: Task, states: torch.Tensor, *, capacity: int | None = None, goal: bool = False, hashes: bool = False,
-           noops: bool = False, drop_noops: bool = False, index: bool = False, validate: bool = True,
-           words: int | None = None) -> dict:
+class TaskTable:
+    """Instances of one domain batched together (rl.TaskTable, include/mymyr/rl/task_table.hpp:1-28): created only if
+    every task has instance 0's action schemas and predicates in the same order; rows are the widest instance's words
+    and labels the largest schema arity wide. The table lives in a device env handle (the reference's default env
+    configuration), which table expansions run on."""
+
+    def __init__(self, tasks: list[Task]):
+        self.tasks = list(tasks)
+        if not self.tasks:
+            raise ValueError("mymyr: TaskTable: no instances")
+        cfg = _lib.EnvConfig(0, 0, 0.0, 1.0, 0.0, 0, 1, 1, 1, 0, 0)
+        handles = (ctypes.c_void_p * len(self.tasks))(*[t.handle.value for t in self.tasks])
+        h = ctypes.c_void_p()
+        check(lib.mya_env_create_table(handles, len(self.tasks), ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        self.num_instances = len(self.tasks)
+        self.words = max(t.words for t in self.tasks)
+        self.label_width = max(t.label_width for t in self.tasks)
+        self.num_schemas = self.tasks[0].num_schemas
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        try:
+            if h is not None and h.value:
+                lib.mya_env_free(h)
+                self._h = ctypes.c_void_p()
+        except Exception:
+            pass
+
+
+def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tensor | None = None, capacity: int | None = None,
+           goal: bool = False, hashes: bool = False, noops: bool = False, drop_noops: bool = False, index: bool = False,
+           validate: bool = True, words: int | None = None) -> dict:
     """The flat expansion of states [N, W] on the device (rl.expand, include/mymyr/rl/expand.hpp:1-130): successor rows
     "succ" [M, words], "parent", "schema" [M] int32, "binding" [M, label_width] int32 (-1 padded), "offsets" [N + 1]
     int32, with goal=True "goal" [M] uint8, hashes=True "succ_hash" [M] (uint64 bits in int64), noops=True "noop" [M]
     uint8, and "index" [M] int32 (the position in the parent's full successor order) with drop_noops or index=True;
     plus "generated", "total", "words_needed" and "overflow". capacity None sizes the buffers to every successor (a
     first call counts them). Canonical order, witness pruning off; drop_noops removes a state's no-op successors unless
-    all of them are no-ops."""
+    all of them are no-ops. Over a TaskTable, row i is a state of instance task_ids[i] ([N] int32 on the device)."""
     s = states.view(torch.int64) if states.dtype == torch.uint64 else states
     if not s.is_cuda or s.dim() != 2 or s.dtype != torch.int64:
         raise ValueError("mymyr_amd: expand: states must be a 2-d int64/uint64 device tensor")
     s = s.contiguous()
     rows, w = s.shape
+    table = isinstance(task, TaskTable)
+    ids = None
+    if table:
+        if task_ids is not None:
+            ids = torch.as_tensor(task_ids).to(device=s.device, dtype=torch.int32).contiguous()
+            if ids.shape != (rows,):
+                raise ValueError(f"mymyr: expand: task_ids must have shape ({rows},)")
+    elif task_ids is not None:
+        raise ValueError("mymyr: expand: task ids need a TaskTable")
     ow = task.words if words is None else words
     L = max(1, task.label_width)
     opts = _lib.ExpandOptions(1, 0, int(validate), int(drop_noops))
+
+    def run(x):
+        if table:
+            check(lib.mya_env_expand(task.handle, s.data_ptr(), _p(ids), rows, w, ctypes.byref(opts), ctypes.byref(x), _stream()))
+        else:
+            check(lib.mya_expand(task.handle, s.data_ptr(), rows, w, ctypes.byref(opts), ctypes.byref(x), _stream()))
+
     if capacity is None:
         probe = _lib.Expansion()
-        check(lib.mya_expand(task.handle, s.data_ptr(), rows, w, ctypes.byref(opts), ctypes.byref(probe), _stream()))
+        run(probe)
         capacity = probe.generated
     dev = s.device
     cap = int(capacity)
@@ -329,7 +379,7 @@ def expand(task: Task, states: torch.Tensor, *, capacity: int | None = None, goa
     ix = torch.empty(cap, dtype=torch.int32, device=dev) if (drop_noops or index) else None
     x = _lib.Expansion(cap, ow, L, succ.data_ptr(), parent.data_ptr(), schema.data_ptr(), binding.data_ptr(), _p(gl),
                        offsets.data_ptr(), _p(sh), _p(np_), _p(ix), 0, 0, 0, 0)
-    check(lib.mya_expand(task.handle, s.data_ptr(), rows, w, ctypes.byref(opts), ctypes.byref(x), _stream()))
+    run(x)
     kept = min(x.total, cap)
     out = {"succ": succ[:kept], "parent": parent[:kept], "schema": schema[:kept], "binding": binding[:kept],
            "offsets": offsets, "generated": x.generated, "total": x.total, "words_needed": x.words_needed,

@@ -558,6 +558,34 @@ def expand(task: Task, rows, capacity: int | None = None, drop_noops: bool = Fal
     return out
 
 
+def table_expand(tasks: list, rows, task_ids, drop_noops: bool = False) -> dict:
+    """rl::expand over a task table (include/mymyr/rl/expand.hpp:5-10, 133-150): row i is a state of instance
+    task_ids[i]; its successors are that instance's, in its canonical order, as rows of the batch's width (zeros past
+    the instance's words) with bindings padded to the table's label width (-1)."""
+    rows = np.asarray(rows, np.uint64)
+    W = rows.shape[1]
+    L = max(1, max(t.label_width for t in tasks))
+    out = {k: [] for k in ("succ", "parent", "schema", "binding", "goal", "succ_hash", "noop", "index")}
+    offsets, generated = [0], 0
+    for i, row in enumerate(rows):
+        t = tasks[int(task_ids[i])]
+        x = expand(t, [row[: t.words]], drop_noops=drop_noops)
+        generated += x["generated"]
+        for j in range(len(x["parent"])):
+            succ = np.zeros(W, np.uint64)
+            succ[: t.words] = x["succ"][j]
+            out["succ"].append(succ)
+            out["parent"].append(i)
+            out["binding"].append(list(x["binding"][j]) + [-1] * (L - len(x["binding"][j])))
+            for k in ("schema", "goal", "succ_hash", "noop", "index"):
+                out[k].append(x[k][j])
+        offsets.append(len(out["parent"]))
+    out["succ"] = np.array(out["succ"], np.uint64).reshape(-1, W)
+    out["binding"] = np.array(out["binding"], np.int32).reshape(-1, L)
+    out.update(offsets=offsets, generated=generated, total=offsets[-1])
+    return out
+
+
 def mask_goal(row, gp, gn) -> bool:
     """The per-env goal test over the words of the masks (mask_goal, src/mymyr/rl/env.cpp:55-61)."""
     row, gp, gn = (np.asarray(x, np.uint64) for x in (row, gp, gn))

@@ -97,6 +97,9 @@ def lib() -> ctypes.CDLL:
             "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int]),
             "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32]),
+            "mref_table_expand": (c_int64, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_uint32, c_int, c_uint64, c_void_p,
+                                            c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            POINTER(c_uint64)]),
             "mref_instance_draw": (c_int32, [c_uint64, c_uint64, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32]),
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
             "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
@@ -269,6 +272,36 @@ class RefTableEnv:
         if getattr(self, "_h", None) is not None and self._h.value:
             lib().mref_env_free(self._h)
             self._h = c_void_p()
+
+
+def table_expand(tasks: list, states: np.ndarray, task_ids: np.ndarray, drop_noops: bool = False) -> dict:
+    """rl::expand over TaskTable::create(tasks): every output of the flat expansion (capacity = every successor)."""
+    arr = (c_void_p * len(tasks))(*[t._h.value for t in tasks])
+    rows, words = states.shape
+    L = max(1, max(t.label_width for t in tasks))
+    total = c_uint64()
+    states = np.ascontiguousarray(states, np.uint64)
+    ids = np.ascontiguousarray(task_ids, np.int32)
+    off = np.zeros(rows + 1, np.int32)
+    gen = lib().mref_table_expand(arr, len(tasks), states.ctypes.data, ids.ctypes.data, rows, words, int(drop_noops), 0, None, None, None,
+                                  None, L, None, None, None, None, off.ctypes.data, ctypes.byref(total))
+    if gen < 0:
+        raise RuntimeError(_err())
+    cap = int(gen)
+    out = {"succ": np.zeros((cap, words), np.uint64), "parent": np.zeros(cap, np.int32), "schema": np.zeros(cap, np.int32),
+           "binding": np.zeros((cap, L), np.int32), "goal": np.zeros(cap, np.uint8), "succ_hash": np.zeros(cap, np.uint64),
+           "noop": np.zeros(cap, np.uint8), "index": np.zeros(cap, np.int32), "offsets": off}
+    g = lib().mref_table_expand(arr, len(tasks), states.ctypes.data, ids.ctypes.data, rows, words, int(drop_noops), cap,
+                                out["succ"].ctypes.data, out["parent"].ctypes.data, out["schema"].ctypes.data, out["binding"].ctypes.data,
+                                L, out["goal"].ctypes.data, out["succ_hash"].ctypes.data, out["noop"].ctypes.data, out["index"].ctypes.data,
+                                off.ctypes.data, ctypes.byref(total))
+    if g < 0:
+        raise RuntimeError(_err())
+    kept = int(total.value)
+    for k in ("succ", "parent", "schema", "binding", "goal", "succ_hash", "noop", "index"):
+        out[k] = out[k][:kept]
+    out["generated"], out["total"] = int(g), kept
+    return out
 
 
 def instance_draw(seed, env, reset_count, instances, thresholds=(), indices=()) -> int:

@@ -15,6 +15,7 @@
 
 #include "mymyr/core/hash.hpp"
 #include "mymyr/rl/env.hpp"
+#include "mymyr/rl/expand.hpp"
 #include "mymyr/rl/pool.hpp"
 #include "mymyr/rl/rng.hpp"
 #include "mymyr/rl/task_table.hpp"
@@ -455,6 +456,47 @@ int mref_table_env_step(mref_env* e, const mref_table_batch* t, const int64_t* a
             a.v64 = actions;
             e->env->step(b, o, a, next_task_ids, nullptr);
             return 0;
+        },
+        -1);
+}
+
+// rl::expand over TaskTable::create(tasks) (include/mymyr/rl/expand.hpp:133-150): states [rows, words], task_ids [rows];
+// outputs of `capacity` rows (succ [capacity, words], parent, schema, binding [capacity, label_width], goal, succ_hash,
+// noop, index) and offsets [rows + 1]. Returns generated; total through *total.
+int64_t mref_table_expand(mref_task* const* tasks, uint32_t n, const uint64_t* states, const int32_t* task_ids, uint64_t rows,
+                          uint32_t words, int drop_noops, uint64_t capacity, uint64_t* succ, int32_t* parent, int32_t* schema,
+                          int32_t* binding, uint32_t label_width, uint8_t* goal, uint64_t* succ_hash, uint8_t* noop, int32_t* index,
+                          int32_t* offsets, uint64_t* total)
+{
+    return guarded(
+        [&]() -> int64_t
+        {
+            std::vector<TaskPtr> v;
+            for (uint32_t i = 0; i < n; ++i)
+                v.push_back(tasks[i]->task);
+            const rl::TaskTablePtr table = rl::TaskTable::create(std::move(v));
+            rl::StateBatchView in;
+            in.data = states;
+            in.rows = rows;
+            in.words = words;
+            rl::Expansion out;
+            out.capacity = capacity;
+            out.words = words;
+            out.label_width = label_width;
+            out.succ = succ;
+            out.parent = parent;
+            out.schema = schema;
+            out.binding = binding;
+            out.goal = goal;
+            out.succ_hash = succ_hash;
+            out.noop = noop;
+            out.index = index;
+            out.offsets = offsets;
+            rl::ExpandOptions o;
+            o.drop_noops = drop_noops != 0;
+            rl::expand(*table, in, task_ids, out, o);
+            *total = out.total;
+            return static_cast<int64_t>(out.generated);
         },
         -1);
 }

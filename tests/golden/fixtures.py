@@ -157,6 +157,20 @@ def table_inputs(case: str, instances: int) -> dict:
     return out
 
 
+# table cases whose batch, after step TABLE_EXPAND_STEP, is also expanded by rl::expand over the table
+# (include/mymyr/rl/expand.hpp:133-150), with and without drop_noops
+TABLE_EXPAND_CASES = ["gridworld_ids", "transport_ids", "gridworld_many", "transport_large"]
+TABLE_EXPAND_STEP = 5
+
+
+def expansion_digest(x: dict) -> str:
+    """sha256 of a flat expansion's arrays in a fixed order and dtype (succ, parent, schema, binding, goal, succ_hash,
+    noop, index, offsets)."""
+    return arrays_digest(np.asarray(x["succ"], np.uint64), np.asarray(x["parent"], np.int32), np.asarray(x["schema"], np.int32),
+                         np.asarray(x["binding"], np.int32), np.asarray(x["goal"], np.uint8), np.asarray(x["succ_hash"], np.uint64),
+                         np.asarray(x["noop"], np.uint8), np.asarray(x["index"], np.int32), np.asarray(x["offsets"], np.int32))
+
+
 def table_state(b: dict) -> list:
     """The batch arrays a table case's digests cover, in order (those the batch has)."""
     keys = ("states", "task_ids", "steps", "draws", "at_goal", "goal_pos", "goal_neg", "reset_counts")

@@ -216,12 +216,21 @@ def table_trajectory(case: str) -> dict:
                schema=sch, binding=bnd, goal=g, invalid=inv, final_states=fs)
         digests.append(fx.arrays_digest(*state(), R, term, trunc, cc, sch, bnd, g, inv, fs))
         cnt = cc
+        if k == fx.TABLE_EXPAND_STEP and case in fx.TABLE_EXPAND_CASES:
+            expansions = {}
+            for drop in (False, True):
+                x = ref.table_expand(ts, b["states"], b["task_ids"], drop_noops=drop)
+                expansions["drop" if drop else "all"] = {"digest": fx.expansion_digest(x), "generated": x["generated"],
+                                                         "total": x["total"], "noops": int(np.asarray(x["noop"]).sum())}
         for key, a in (("terminated", term), ("truncated", trunc), ("invalid", inv), ("goal", g)):
             totals[key] += int(a.sum())
         for i in range(I):
             totals["instance_rows"][i] += int((b["task_ids"] == i).sum())
-    return {"case": case, "table": table, "rows": rows, "steps": steps, "words": W, "label_width": L, "resets": resets,
-            "digests": digests, "totals": totals}
+    out = {"case": case, "table": table, "rows": rows, "steps": steps, "words": W, "label_width": L, "resets": resets,
+           "digests": digests, "totals": totals}
+    if case in fx.TABLE_EXPAND_CASES:
+        out["expand"] = expansions
+    return out
 
 
 def make_env_table():

@@ -81,6 +81,17 @@ def replay(golden, case: str):
         d = golden.arrays_digest(*state(), host(o["reward"]), host(o["terminated"]), host(o["truncated"]), host(o["count"]),
                                  host(o["schema"]), host(o["binding"]), host(o["goal"]), host(o["invalid"]), u64(o["final_states"]))
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
+        if k == golden.TABLE_EXPAND_STEP and case in golden.TABLE_EXPAND_CASES:
+            # rl::expand over the table on the batch after this step (rows of several instances, grouped on the device)
+            table = rl.TaskTable(ts)
+            for key, drop in (("all", False), ("drop", True)):
+                x = rl.expand(table, pool.states, task_ids=pool.task_ids, goal=True, hashes=True, noops=True, index=True, drop_noops=drop)
+                want = g["expand"][key]
+                assert (x["generated"], x["total"]) == (want["generated"], want["total"]), f"{case}: expansion {key}"
+                got = {"succ": u64(x["succ"]), "parent": host(x["parent"]), "schema": host(x["schema"]), "binding": host(x["binding"]),
+                       "goal": host(x["goal"]), "succ_hash": u64(x["succ_hash"]), "noop": host(x["noop"]), "index": host(x["index"]),
+                       "offsets": host(x["offsets"])}
+                assert golden.expansion_digest(got) == want["digest"], f"{case}: expansion {key}"
     pool.check()
     return pool
 

@@ -61,6 +61,13 @@ def replay_oracle(golden, case: str) -> None:
                                  o["goal"], o["invalid"], o["final_states"])
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
         b["count"] = o["count"]
+        if k == golden.TABLE_EXPAND_STEP and case in golden.TABLE_EXPAND_CASES:
+            # rl::expand over the table on the batch after this step, with and without drop_noops
+            for key, drop in (("all", False), ("drop", True)):
+                x = port.table_expand(ts, b["states"], b["task_ids"], drop_noops=drop)
+                want = g["expand"][key]
+                assert (x["generated"], x["total"]) == (want["generated"], want["total"]), f"{case}: expansion {key}"
+                assert golden.expansion_digest(x) == want["digest"], f"{case}: expansion {key}"
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
