@@ -1010,9 +1010,49 @@ __device__ __forceinline__ void build_view(const TaskDev& T, const auto& H, cons
 /// Loads row i (W words of `words`) into the wave's LDS row.
 __device__ __forceinline__ void load_row_lds(const TaskDev& T, const Lds& L, const u64* src, u32 lane)
 {
-    for (u32 k = lane; k < T.W; k += kWave)
-        L.row[k] = src[k];
+    // up to 8 loads of a lane in flight before their LDS stores: a wide row arrives in about one load latency
+    constexpr u32 kBatch = 8;
+    for (u32 k0 = 0; k0 < T.W; k0 += kBatch * kWave)
+    {
+        u64 v[kBatch];
+#pragma unroll
+        for (u32 j = 0; j < kBatch; ++j)
+        {
+            const u32 k = k0 + j * kWave + lane;
+            v[j] = k < T.W ? src[k] : 0;
+        }
+#pragma unroll
+        for (u32 j = 0; j < kBatch; ++j)
+        {
+            const u32 k = k0 + j * kWave + lane;
+            if (k < T.W)
+                L.row[k] = v[j];
+        }
+    }
     wave_sync();
+}
+
+/// dst[k] = k < n ? src[k] : 0 for k < z (global to global), up to 8 loads of a lane in flight.
+__device__ __forceinline__ void copy_words(u64* dst, const u64* src, u32 n, u32 z, u32 lane)
+{
+    constexpr u32 kBatch = 8;
+    for (u32 k0 = 0; k0 < z; k0 += kBatch * kWave)
+    {
+        u64 v[kBatch];
+#pragma unroll
+        for (u32 j = 0; j < kBatch; ++j)
+        {
+            const u32 k = k0 + j * kWave + lane;
+            v[j] = k < n ? src[k] : 0;
+        }
+#pragma unroll
+        for (u32 j = 0; j < kBatch; ++j)
+        {
+            const u32 k = k0 + j * kWave + lane;
+            if (k < z)
+                dst[k] = v[j];
+        }
+    }
 }
 
 /// The ascending set-bit slots of `row` (W words) into out[0, max_atoms), -1 padded (all lanes).
@@ -1309,14 +1349,12 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             A.reset_counts[i] += 1;
         const InstDev& J = A.inst[next];  // a one-instance env restarts in instance 0
         const u32 z = min(A.words, max(J.W, T.W));  // the words the row may have dirtied: its old and new instance's
-        for (u32 q = lane; q < z; q += kWave)
-            grow[q] = q < J.W ? J.initial[q] : 0;
+        copy_words(grow, J.initial, J.W, z, lane);
         if (A.goal_pos)
-            for (u32 q = lane; q < z; q += kWave)
-            {
-                A.goal_pos[i * A.words + q] = q < J.W ? J.goal_pos[q] : 0;
-                A.goal_neg[i * A.words + q] = q < J.W ? J.goal_neg[q] : 0;
-            }
+        {
+            copy_words(A.goal_pos + i * A.words, J.goal_pos, J.W, z, lane);
+            copy_words(A.goal_neg + i * A.words, J.goal_neg, J.W, z, lane);
+        }
         if (lane == 0)
         {
             if (!kOne && A.task_ids)
