@@ -154,8 +154,9 @@ typedef struct mya_env_batch
     uint8_t* at_goal;
     uint64_t first_env;
     /* The count cache (the reference device env's EnvBatch::counts, include/mymyr/rl/env.hpp:106-110), optional:
-     * [rows, num_schemas + 2] uint32, each row's per-schema successor counts of its current state, then a 64-bit
-     * fingerprint of that state (low word first). reset, refresh and step keep it current, and a step takes the
+     * [rows, S + 2] uint32 with S the most schemas of any instance of the env, each row's per-schema successor counts
+     * of its current state (0 past its instance's schemas), then a 64-bit fingerprint of that state and its
+     * instance (low word first). reset, refresh and step keep it current, and a step takes the
      * counts of a row from it instead of counting the row's successors when the fingerprint matches the row's state
      * (a state written directly is counted again; refresh brings at_goal up to date for it). Null: every step counts. */
     uint32_t* counts;
@@ -217,6 +218,12 @@ int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out);
  * are at least the widest instance's words; the label width is the largest schema arity. The env keeps the tasks'
  * device images alive by reference: free the env before the tasks. */
 int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out);
+/* A device environment over a task suite: instances of several domains (TaskSuite::group,
+ * include/mymyr/rl/task_suite.hpp:1-30, 64): global task ids in the tasks' order, labels in each instance's own
+ * domain's schema ids and objects, rows the widest instance's words, the label width the largest arity; the count
+ * cache and schema masks have the most schemas of any instance (a narrower domain's columns past its own stay 0).
+ * No domain check; otherwise as mya_env_create_table. */
+int mya_env_create_suite(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out);
 void mya_env_free(mya_env* env);
 /* The env's instance sampler (EnvConfig::sampling, include/mymyr/rl/env.hpp:89-91; rl/sampling.hpp): `instances`
  * 0 turns it off, else it must be the table's instance count; m = 0 draws uniformly, else thresholds [m - 1]

@@ -207,6 +207,7 @@ def _load() -> ctypes.CDLL:
     optional = {
         "mya_env_create": (c_int, [c_void_p, POINTER(EnvConfig), POINTER(c_void_p)]),
         "mya_env_create_table": (c_int, [c_void_p, c_uint32, POINTER(EnvConfig), POINTER(c_void_p)]),
+        "mya_env_create_suite": (c_int, [c_void_p, c_uint32, POINTER(EnvConfig), POINTER(c_void_p)]),
         "mya_env_free": (None, [c_void_p]),
         "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_int, c_void_p]),
         "mya_env_set_sampling": (c_int, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint32]),

@@ -24,7 +24,7 @@ from torch import Tensor
 
 from . import _lib
 from ._lib import check, lib
-from .rl import InstanceSampler
+from .rl import InstanceSampler, TaskSuite, TaskTable
 from .task import Task
 
 __all__ = ["BatchedEnv", "CapturedRollout", "Observation", "Rollout", "StepResult"]
@@ -127,11 +127,11 @@ def _where(mask: Optional[Tensor], new: Tensor, old: Tensor) -> Tensor:
 
 
 class BatchedEnv:
-    """N environments over a task or a task table (a list of instances of one domain), stepped in lockstep on the
-    device. Keyword arguments and defaults are the reference's (seed 0, step_reward 0, goal_reward 1, dead_end
+    """N environments over a task, a task table (a list of instances of one domain, or an rl.TaskTable) or a suite of
+    several domains (rl.TaskSuite), stepped in lockstep on the device. Keyword arguments and defaults are the reference's (seed 0, step_reward 0, goal_reward 1, dead_end
     "no_successors", autoreset True, sampler "auto", first_env 0)."""
 
-    def __init__(self, table: Task | list[Task], num_envs: int, *, task_ids: Optional[Any] = None, sampler: Any = "auto",
+    def __init__(self, table: Task | list[Task] | TaskTable, num_envs: int, *, task_ids: Optional[Any] = None, sampler: Any = "auto",
                  device: str | torch.device = "cuda", goals: bool = False, seed: int = 0, max_steps: Optional[int] = None,
                  step_reward: float = 0.0, goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True, witness_pruning: bool = False,
@@ -149,6 +149,9 @@ class BatchedEnv:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
             raise ValueError("mymyr: dead_end must be 'no_successors' or 'none'")
+        suite = isinstance(table, TaskSuite)
+        if isinstance(table, TaskTable):
+            table = table.tasks
         self.tasks = list(table) if isinstance(table, (list, tuple)) else [table]
         self.num_envs, self.first_env = int(num_envs), int(first_env)
         self.device = torch.device(device)
@@ -164,8 +167,9 @@ class BatchedEnv:
                              int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning), 0)
         handles = (ctypes.c_void_p * I)(*[t.handle.value for t in self.tasks])
         h = ctypes.c_void_p()
+        create = lib.mya_env_create_suite if suite else lib.mya_env_create_table
         with torch.cuda.device(self.device):
-            check(lib.mya_env_create_table(handles, I, ctypes.byref(cfg), ctypes.byref(h)))
+            check(create(handles, I, ctypes.byref(cfg), ctypes.byref(h)))
         self._h = h
         if self.sampler is not None:
             thr = np.ascontiguousarray(self.sampler.thresholds)
@@ -179,7 +183,7 @@ class BatchedEnv:
         self.reset_counts = torch.zeros(n, dtype=torch.int32, device=d)
         self.steps = torch.zeros(n, dtype=torch.int32, device=d)
         self.draws = torch.zeros(n, dtype=torch.int64, device=d)
-        self.counts = torch.zeros((n, self.tasks[0].num_schemas + 2), dtype=torch.int32, device=d)
+        self.counts = torch.zeros((n, max(t.num_schemas for t in self.tasks) + 2), dtype=torch.int32, device=d)
         self.count = torch.zeros(n, dtype=torch.int32, device=d)
         self.at_goal = torch.zeros(n, dtype=torch.bool, device=d)
         self.goal_pos: Optional[Tensor] = None

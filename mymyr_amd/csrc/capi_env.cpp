@@ -33,12 +33,12 @@ struct mya_env
     EnvCfg cfg{};
     u32 words = 1;        // the widest instance's words
     u32 label_width = 0;  // the largest schema arity
-    u32 num_schemas = 0;
+    u32 num_schemas = 0;  // the most schemas of any instance (columns of masks; the count cache has 2 more)
     InstDev* d_inst = nullptr;    // device [instances]
     TaskDev* d_tasks = nullptr;   // device [instances]
     u64* d_init = nullptr;        // device: per instance its goal masks (positive, then negative) over its words
     u32* d_init_cache = nullptr;  // device [instances, num_schemas + 2]: the initial states' count-cache rows
-    u8* d_init_masks = nullptr;   // device [instances, num_schemas]
+    u8* d_init_masks = nullptr;   // device [instances, max(1, num_schemas)]
     u32* d_status = nullptr;
     u32* h_status = nullptr;
     u64* d_seed = nullptr;        // device word: the RNG key of the random policy and of the sampler
@@ -66,6 +66,7 @@ struct mya_env
 
     [[nodiscard]] u32 instances() const { return static_cast<u32>(inst.size()); }
     [[nodiscard]] const TaskDev& T0() const { return inst[0].T; }
+    [[nodiscard]] u32 cache_width() const { return num_schemas + 2; }
 };
 
 namespace
@@ -162,6 +163,8 @@ void run_count(mya_env* env, const mya_env_batch* batch, CountArgs& a, hipStream
     a.goal_pos = batch->goal_pos;
     a.goal_neg = batch->goal_neg;
     a.status = env->d_status;
+    a.cache_width = env->cache_width();
+    a.mask_width = env->num_schemas;
     if (!grouped(env))
     {
         launch_env_count(a, s);
@@ -341,11 +344,13 @@ void free_env(mya_env* e)
 }
 }  // namespace
 
-extern "C" {
-
-int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out)
+namespace
 {
-    return guarded([&] {
+/// An env over `count` instances; one_domain: a task table (TaskTable::create's domain check), else a suite of several
+/// domains (TaskSuite::group: global ids in the tasks' order, each domain's labels its own).
+void create_env(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out, bool one_domain)
+{
+    {
         if (!tasks || !config || !out)
             throw std::invalid_argument("mymyr_amd: env_create: null argument");
         if (count == 0)
@@ -355,7 +360,7 @@ int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_c
         for (u32 i = 0; i < count; ++i)
             if (!tasks[i])
                 throw std::invalid_argument("mymyr: TaskTable: instance " + std::to_string(i) + " is null");
-        for (u32 i = 1; i < count; ++i)
+        for (u32 i = 1; one_domain && i < count; ++i)
         {
             const std::string why = domain_mismatch(tasks[0]->compiled->text, tasks[i]->compiled->text);
             if (!why.empty())
@@ -382,9 +387,9 @@ int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_c
             in.variant = env_variant(in.T);
             e->words = std::max(e->words, in.T.W);
             e->label_width = std::max(e->label_width, in.T.label_width);
+            e->num_schemas = std::max(e->num_schemas, in.T.num_schemas);
         }
-        e->num_schemas = e->T0().num_schemas;
-        const u32 S = e->num_schemas, cw = cache_width(e->T0());
+        const u32 S = e->num_schemas, cw = e->cache_width();
         e->d_status = dev_alloc<u32>(1, "env status");
         e->d_seed = dev_alloc<u64>(1, "env seed");
         hip_check(hipMemcpy(e->d_seed, &config->seed, sizeof(u64), hipMemcpyHostToDevice), "env seed");
@@ -417,7 +422,7 @@ int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_c
             {
                 const TaskDev& T = e->inst[i].T;
                 launch_env_count(T, T.initial, 1, T.W, cnt + i, gl + i, e->d_init_masks + static_cast<size_t>(i) * std::max<u32>(1, S),
-                                 e->d_init_cache + static_cast<size_t>(i) * cw, nullptr, nullptr, nullptr, nullptr, i);
+                                 e->d_init_cache + static_cast<size_t>(i) * cw, nullptr, nullptr, nullptr, nullptr, i, S);
             }
             hip_check(hipMemcpy(hc.data(), cnt, count * sizeof(i32), hipMemcpyDeviceToHost), "initial counts");
             hip_check(hipMemcpy(hg.data(), gl, count * sizeof(u8), hipMemcpyDeviceToHost), "initial goals");
@@ -467,7 +472,21 @@ int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_c
             e->d_chunks = dev_alloc<u32>(count + 1, "env group chunks");
         }
         *out = e.release();
-    });
+    }
+}
+}  // namespace
+
+extern "C" {
+
+
+int mya_env_create_table(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out)
+{
+    return guarded([&] { create_env(tasks, count, config, out, true); });
+}
+
+int mya_env_create_suite(mya_task* const* tasks, uint32_t count, const mya_env_config* config, mya_env** out)
+{
+    return guarded([&] { create_env(tasks, count, config, out, false); });
 }
 
 int mya_env_create(mya_task* task, const mya_env_config* config, mya_env** out)
@@ -553,7 +572,7 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         launch_env_reset_draw(env->sampler, env->d_seed, batch->first_env, batch->rows, mask, sample != 0, batch->task_ids, batch->reset_counts,
                               batch->sampling_seeds, batch->env_ids, s);
         launch_env_reset(env->d_inst, env->instances(), batch->states, batch->rows, batch->words, mask, batch->task_ids, batch->steps,
-                         batch->at_goal, count, batch->counts, cache_width(env->T0()), env->d_status, s);
+                         batch->at_goal, count, batch->counts, env->cache_width(), env->d_status, s);
         if (batch->goal_pos)
             launch_env_reset_goals(env->d_inst, env->instances(), batch->rows, batch->words, mask, batch->task_ids, batch->goal_pos,
                                    batch->goal_neg, keep_goals != 0, batch->at_goal, env->d_status, s);
@@ -619,6 +638,8 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.max_atoms = out->max_atoms;
         a.masks = out->masks;
         a.counts = batch->counts;
+        a.cache_width = env->cache_width();
+        a.mask_width = env->num_schemas;
         a.goal_pos = batch->goal_pos;
         a.goal_neg = batch->goal_neg;
         a.status = env->d_status;

@@ -752,16 +752,17 @@ __device__ __forceinline__ u32 load_counts(const TaskDev& T, const Lds& L, const
     return wave_sum(part);
 }
 
-/// A count-cache row from the per-schema counts in LDS and the fingerprint of the LDS state (plus the instance's salt).
-__device__ __forceinline__ void store_counts(const TaskDev& T, const Lds& L, u32* crow, u32 lane, u64 salt)
+/// A count-cache row of `cw` words from the per-schema counts in LDS (zeros past the instance's schemas, as for a
+/// suite's narrower domains) and the fingerprint of the LDS state plus the instance's salt in its last two words.
+__device__ __forceinline__ void store_counts(const TaskDev& T, const Lds& L, u32* crow, u32 cw, u32 lane, u64 salt)
 {
     const u64 fp = state_fingerprint(L.row, T.W, lane) + salt;
-    for (u32 s = lane; s < T.num_schemas; s += kWave)
-        crow[s] = L.counts[s];
+    for (u32 s = lane; s < cw - 2; s += kWave)
+        crow[s] = s < T.num_schemas ? L.counts[s] : 0;
     if (lane == 0)
     {
-        crow[T.num_schemas] = static_cast<u32>(fp);
-        crow[T.num_schemas + 1] = static_cast<u32>(fp >> 32);
+        crow[cw - 2] = static_cast<u32>(fp);
+        crow[cw - 1] = static_cast<u32>(fp >> 32);
     }
 }
 
@@ -1212,14 +1213,14 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     const bool already_goal = A.at_goal[i] != 0;
     // the count cache row: its counts stand for the row's state (and instance) when its fingerprint matches (reset,
     // refresh and step write it; a state written directly since is counted again)
-    const u32 cw = cache_width(T);
+    const u32 cw = A.cache_width;
     u32* crow = A.counts ? A.counts + i * cw : nullptr;
     const u64 salt = instance_salt(k);
     bool cached = false;
     if (crow)
     {
         const u64 fp = state_fingerprint(L.row, T.W, lane) + salt;
-        cached = (static_cast<u64>(crow[T.num_schemas]) | (static_cast<u64>(crow[T.num_schemas + 1]) << 32)) == fp;
+        cached = (static_cast<u64>(crow[cw - 2]) | (static_cast<u64>(crow[cw - 1]) << 32)) == fp;
     }
     enum
     {
@@ -1385,7 +1386,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         // the count cache of the state the row now holds: the counts in LDS (of s' after a move, of s otherwise)
         // unless they came from the cache
         if (crow && (st == kOk || !cached))
-            store_counts(T, L, crow, lane, salt);
+            store_counts(T, L, crow, cw, lane, salt);
     }
     // 6. the observation's encoding: true-atom slots and applicable-schema masks (LDS holds the per-schema counts of
     // the state the row holds unless the row was reset)
@@ -1401,8 +1402,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
                 encode_row(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
         }
         if (A.masks)
-            for (u32 q = lane; q < T.num_schemas; q += kWave)
-                A.masks[i * T.num_schemas + q] = reset ? A.inst[next].init_masks[q] : (L.counts[q] > 0 ? 1 : 0);
+            for (u32 q = lane; q < A.mask_width; q += kWave)
+                A.masks[i * A.mask_width + q] = reset ? A.inst[next].init_masks[q] : (q < T.num_schemas && L.counts[q] > 0 ? 1 : 0);
     }
     wave_sync();
 }
@@ -1522,10 +1523,10 @@ __device__ __forceinline__ void count_row(const CountArgs& A, const TaskDev& T, 
             A.goal[i] = g ? 1 : 0;
     }
     if (A.masks)
-        for (u32 q = lane; q < T.num_schemas; q += kWave)
-            A.masks[i * T.num_schemas + q] = L.counts[q] > 0 ? 1 : 0;
+        for (u32 q = lane; q < A.mask_width; q += kWave)
+            A.masks[i * A.mask_width + q] = q < T.num_schemas && L.counts[q] > 0 ? 1 : 0;
     if (A.cache)
-        store_counts(T, L, A.cache + i * cache_width(T), lane, instance_salt(k));
+        store_counts(T, L, A.cache + i * A.cache_width, A.cache_width, lane, instance_salt(k));
     wave_sync();
 }
 
@@ -2207,10 +2208,12 @@ void launch_env_count(const CountArgs& a, hipStream_t stream)
 }
 
 void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
-                      hipStream_t stream, const u64* goal_pos, const u64* goal_neg, u32* status, u32 instance)
+                      hipStream_t stream, const u64* goal_pos, const u64* goal_neg, u32* status, u32 instance, u32 schemas)
 {
     CountArgs a{};
     a.T = T;
+    a.mask_width = schemas ? schemas : T.num_schemas;
+    a.cache_width = a.mask_width + 2;
     a.instances = 1;
     a.states = states;
     a.rows = rows;

@@ -96,7 +96,9 @@ struct EnvArgs
     i32* atoms;       // [rows, max_atoms]: ascending true-atom slots of the observed state, -1 padded (optional)
     u32 max_atoms;
     u8* masks;        // [rows, num_schemas]: schemas with an applicable binding in the observed state (optional)
-    u32* counts;      // [rows, num_schemas + 2]: the count cache (per-schema counts, then the state's fingerprint), optional
+    u32* counts;      // [rows, cache_width]: the count cache (per-schema counts, then the state's fingerprint), optional
+    u32 cache_width;  // the most schemas of any instance + 2
+    u32 mask_width;   // the most schemas of any instance (columns of masks)
     u64* goal_pos;    // [rows, words]: per-env goal masks (optional, with goal_neg)
     u64* goal_neg;
     u32* status;
@@ -121,8 +123,10 @@ struct CountArgs
     const i32* task_ids;
     i32* count;
     u8* goal;
-    u8* masks;
-    u32* cache;
+    u8* masks;        // [rows, mask_width]
+    u32* cache;       // [rows, cache_width]
+    u32 cache_width;  // the most schemas of any instance + 2
+    u32 mask_width;   // the most schemas of any instance
     const u64* goal_pos;
     const u64* goal_neg;
     u32* status;
@@ -130,10 +134,11 @@ struct CountArgs
 };
 
 void launch_env_count(const CountArgs& a, hipStream_t stream);
-/// A one-instance count of rows of instance `instance` (the common case of launch_env_count).
+/// A one-instance count of rows of instance `instance` (the common case of launch_env_count); masks and cache rows are
+/// laid out for `schemas` schemas (0: the task's).
 void launch_env_count(const TaskDev& T, const u64* states, u64 rows, u32 words, i32* count, u8* goal, u8* masks, u32* cache,
                       hipStream_t stream, const u64* goal_pos = nullptr, const u64* goal_neg = nullptr, u32* status = nullptr,
-                      u32 instance = 0);
+                      u32 instance = 0, u32 schemas = 0);
 
 /// Groups the rows by task id (RowGroups): hist [instances + 1] and the three group arrays are device scratch; rows
 /// with a task id outside [0, instances) set kStatusTaskId.

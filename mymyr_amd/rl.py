@@ -77,10 +77,14 @@ class DeviceEnvPool:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
             raise ValueError("mymyr: dead_end must be 'no_successors' or 'none'")
+        suite = isinstance(task, TaskSuite)
+        if isinstance(task, TaskTable):
+            task = task.tasks
         self.tasks = list(task) if isinstance(task, (list, tuple)) else [task]
         if not self.tasks:
             raise ValueError("mymyr: TaskTable: no instances")
         self.task = self.tasks[0]
+        self.num_schemas = max(t.num_schemas for t in self.tasks)
         self.num_envs = num_envs
         self.first_env = first_env
         widest = max(t.words for t in self.tasks)
@@ -93,7 +97,8 @@ class DeviceEnvPool:
                              int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning), 0)
         h = ctypes.c_void_p()
         handles = (ctypes.c_void_p * len(self.tasks))(*[t.handle.value for t in self.tasks])
-        check(lib.mya_env_create_table(handles, len(self.tasks), ctypes.byref(cfg), ctypes.byref(h)))
+        create = lib.mya_env_create_suite if suite else lib.mya_env_create_table
+        check(create(handles, len(self.tasks), ctypes.byref(cfg), ctypes.byref(h)))
         self._h = h
         N, W, L, dev = num_envs, self.words, self.label_width, self.device
         self.states = torch.zeros((N, W), dtype=torch.int64, device=dev)
@@ -111,7 +116,7 @@ class DeviceEnvPool:
         self.final_states: torch.Tensor | None = None
         # the count cache (the reference device env's EnvBatch::counts): per-schema successor counts of each row's
         # state plus its fingerprint, so a step counts only the reached states; zeros match no state
-        self.counts_cache = (torch.zeros((N, self.task.num_schemas + 2), dtype=torch.int32, device=dev) if count_cache else None)
+        self.counts_cache = (torch.zeros((N, self.num_schemas + 2), dtype=torch.int32, device=dev) if count_cache else None)
         # per-env goal masks (goals=True, CpuEnvPool's `goals`): goal_pos / goal_neg [N, W], the task's goal after a reset
         self.goal_pos = torch.zeros((N, W), dtype=torch.int64, device=dev) if goals else None
         self.goal_neg = torch.zeros((N, W), dtype=torch.int64, device=dev) if goals else None
@@ -232,7 +237,7 @@ class DeviceEnvPool:
         """The atom-index and mask outputs live in library-owned device buffers that torch takes over DLPack without a
         copy (the reference's pool arrays are DLPack-exported blocks, python/src/arrays.cpp:100-235)."""
         from .dlpack import DeviceBuffer
-        S = max(1, self.task.num_schemas)
+        S = max(1, self.num_schemas)
         with torch.cuda.device(self.device):
             ab = DeviceBuffer(self.num_envs * encode * 4)
             mb = DeviceBuffer(self.num_envs * S)
@@ -326,6 +331,26 @@ class TaskTable:
                 self._h = ctypes.c_void_p()
         except Exception:
             pass
+
+
+class TaskSuite(TaskTable):
+    """Instances of several domains batched together (rl.TaskSuite.group, include/mymyr/rl/task_suite.hpp:1-30):
+    global ids in the tasks' order, each instance's labels in its own domain's schemas and objects; rows the widest
+    instance's words, labels the largest arity wide, count caches and masks the most schemas of any instance."""
+
+    def __init__(self, tasks: list[Task]):
+        self.tasks = list(tasks)
+        if not self.tasks:
+            raise ValueError("mymyr: TaskSuite: no instances")
+        cfg = _lib.EnvConfig(0, 0, 0.0, 1.0, 0.0, 0, 1, 1, 1, 0, 0)
+        handles = (ctypes.c_void_p * len(self.tasks))(*[t.handle.value for t in self.tasks])
+        h = ctypes.c_void_p()
+        check(lib.mya_env_create_suite(handles, len(self.tasks), ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        self.num_instances = len(self.tasks)
+        self.words = max(t.words for t in self.tasks)
+        self.label_width = max(t.label_width for t in self.tasks)
+        self.num_schemas = max(t.num_schemas for t in self.tasks)
 
 
 def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tensor | None = None, capacity: int | None = None,

@@ -60,6 +60,9 @@ TABLES = {
     # more instances than one launch per instance serves: grids of 4x4 to 13x13 cells (rows of 1 to 3 words)
     "gridworld_many": [(lambda w: (lambda: gen.gridworld(w, w - i % 3, 0.15, seed=10 + i)))(4 + (i * 7) % 10) for i in range(20)],
 }
+# a suite of two domains: gridworld and transport instances interleaved (global ids in this order)
+TABLES["mixed_suite"] = [TABLES["gridworld_table"][0], TABLES["transport_table"][0], TABLES["gridworld_table"][1],
+                         TABLES["transport_table"][2], TABLES["gridworld_table"][2]]
 
 GRIDWORLD = EnvWorkload("gridworld", 1024, 256, {"seed": SEED, "step_reward": -1.0, "goal_reward": 0.0})
 TRANSPORT = EnvWorkload("transport", 65536, 512, {"seed": SEED})

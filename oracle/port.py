@@ -724,11 +724,13 @@ class TableEnv:
     writes, and a reset zeroes only what it may have dirtied (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138)."""
 
     def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
-                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None):
-        """sampler: (instances, thresholds, indices) of an instance sampler (rl/sampling.hpp; empty arrays: uniform)."""
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None, suite=False):
+        """sampler: (instances, thresholds, indices) of an instance sampler (rl/sampling.hpp; empty arrays: uniform).
+        suite: instances of several domains (TaskSuite::group, include/mymyr/rl/task_suite.hpp:62-64): no domain check;
+        each row steps in its own instance's domain."""
         if not tasks:
             raise ValueError("mymyr: TaskTable: no instances")
-        for i, t in enumerate(tasks[1:], 1):
+        for i, t in enumerate([] if suite else tasks[1:], 1):
             why = domain_mismatch(tasks[0], t)
             if why:
                 raise ValueError(f"mymyr: TaskTable: instance {i} is not of the domain of instance 0: {why}")

@@ -93,7 +93,7 @@ def lib() -> ctypes.CDLL:
             "mref_env_reset": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64]),
             "mref_env_step": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p,
                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p]),
-            "mref_table_env_create": (c_void_p, [c_void_p, c_uint32, POINTER(EnvConfig), c_uint32, c_void_p, c_void_p, c_uint32]),
+            "mref_table_env_create": (c_void_p, [c_void_p, c_uint32, POINTER(EnvConfig), c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
             "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int]),
             "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32]),
@@ -226,11 +226,11 @@ class TableBatch(Structure):
 
 
 class RefTableEnv:
-    """rl::HostEnv over TaskTable::create(tasks): several instances of one domain, per-row task ids, with an instance
-    sampler when `sampler` = (instances, thresholds, indices) is given (thresholds / indices empty: uniform)."""
+    """rl::HostEnv over TaskTable::create(tasks) (suite=True: TaskSuite::group(tasks), several domains): per-row task ids,
+    with an instance sampler when `sampler` = (instances, thresholds, indices) is given (empty arrays: uniform)."""
 
     def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
-                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None):
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None, suite=False):
         self.tasks = tasks
         self.cfg = EnvConfig(seed, max_steps, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
                              int(dead_end_terminal), int(autoreset), 1, 0)
@@ -239,7 +239,7 @@ class RefTableEnv:
         self._thr = np.asarray(thr, np.uint32)
         self._idx = np.asarray(idx, np.int32)
         h = lib().mref_table_env_create(arr, len(tasks), ctypes.byref(self.cfg), inst, self._thr.ctypes.data, self._idx.ctypes.data,
-                                        len(self._idx))
+                                        len(self._idx), int(suite))
         if not h:
             raise RuntimeError(_err())
         self._h = c_void_p(h)

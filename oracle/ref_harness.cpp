@@ -18,6 +18,7 @@
 #include "mymyr/rl/expand.hpp"
 #include "mymyr/rl/pool.hpp"
 #include "mymyr/rl/rng.hpp"
+#include "mymyr/rl/task_suite.hpp"
 #include "mymyr/rl/task_table.hpp"
 #include "mymyr/search/brfs.hpp"
 #include "mymyr/successor/successors.hpp"
@@ -350,11 +351,12 @@ int mref_env_step(mref_env* e, uint64_t* states, uint64_t rows, uint32_t words, 
         -1);
 }
 
-// A HostEnv over TaskTable::create(tasks) (include/mymyr/rl/task_table.hpp:69-75): several instances of one domain,
+// A HostEnv over TaskTable::create(tasks) (include/mymyr/rl/task_table.hpp:69-75): several instances of one domain
+// (suite: over TaskSuite::group(tasks), include/mymyr/rl/task_suite.hpp:62-64, instances of several domains),
 // with an instance sampler (rl/sampling.hpp) when sampled_instances > 0 (m = 0: uniform; else thresholds [m - 1] and
 // indices [m]). Null (and the table's message in mref_last_error) when the tasks are not of one domain.
 mref_env* mref_table_env_create(mref_task* const* tasks, uint32_t n, const mref_env_config* c, uint32_t sampled_instances,
-                                const uint32_t* thresholds, const int32_t* indices, uint32_t m)
+                                const uint32_t* thresholds, const int32_t* indices, uint32_t m, int suite)
 {
     return guarded(
         [&]() -> mref_env*
@@ -370,7 +372,10 @@ mref_env* mref_table_env_create(mref_task* const* tasks, uint32_t n, const mref_
                 cfg.sampling.indices.assign(indices, indices + m);
             }
             auto e = new mref_env;
-            e->env = std::make_unique<rl::HostEnv>(rl::TaskTable::create(std::move(v)), cfg);
+            if (suite)  // TaskSuite::group: several domains, global ids in task order
+                e->env = std::make_unique<rl::HostEnv>(rl::TaskSuite::group(std::move(v)), cfg);
+            else
+                e->env = std::make_unique<rl::HostEnv>(rl::TaskTable::create(std::move(v)), cfg);
             return e;
         },
         nullptr);
@@ -460,7 +465,7 @@ int mref_table_env_step(mref_env* e, const mref_table_batch* t, const int64_t* a
         -1);
 }
 
-// rl::expand over TaskTable::create(tasks) (include/mymyr/rl/expand.hpp:133-150): states [rows, words], task_ids [rows];
+// rl::expand over TaskSuite::group(tasks) (include/mymyr/rl/expand.hpp:133-150; one domain: its table): states [rows, words], task_ids [rows];
 // outputs of `capacity` rows (succ [capacity, words], parent, schema, binding [capacity, label_width], goal, succ_hash,
 // noop, index) and offsets [rows + 1]. Returns generated; total through *total.
 int64_t mref_table_expand(mref_task* const* tasks, uint32_t n, const uint64_t* states, const int32_t* task_ids, uint64_t rows,
@@ -474,7 +479,7 @@ int64_t mref_table_expand(mref_task* const* tasks, uint32_t n, const uint64_t* s
             std::vector<TaskPtr> v;
             for (uint32_t i = 0; i < n; ++i)
                 v.push_back(tasks[i]->task);
-            const rl::TaskTablePtr table = rl::TaskTable::create(std::move(v));
+            const rl::TaskSuitePtr suite = rl::TaskSuite::group(std::move(v));
             rl::StateBatchView in;
             in.data = states;
             in.rows = rows;
@@ -494,7 +499,7 @@ int64_t mref_table_expand(mref_task* const* tasks, uint32_t n, const uint64_t* s
             out.offsets = offsets;
             rl::ExpandOptions o;
             o.drop_noops = drop_noops != 0;
-            rl::expand(*table, in, task_ids, out, o);
+            rl::expand(*suite, in, task_ids, out, o);
             *total = out.total;
             return static_cast<int64_t>(out.generated);
         },

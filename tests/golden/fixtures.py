@@ -98,11 +98,16 @@ TABLE_CASES = {
                            env={"seed": 11, "max_steps": 12, "step_reward": -1.0, "goal_reward": 3.0}),
     "gridworld_many_large": dict(table="gridworld_many", rows=8192, steps=48, seed=30, policy="given", goals=True,
                                  env={"seed": 12, "max_steps": 25}),
+    "suite_mixed": dict(table="mixed_suite", suite=True, rows=40, steps=30, seed=31, policy="random", sampler="uniform", goals=True,
+                        env={"seed": 13, "max_steps": 8, "step_reward": -1.0, "goal_reward": 2.0}),
+    "suite_mixed_large": dict(table="mixed_suite", suite=True, rows=4096, steps=40, seed=32, policy="given", sampler=[1.0, 2.0, 1.0, 3.0, 1.0],
+                              env={"seed": 14, "max_steps": 12}),
     "gridworld_sampled_large": dict(table="gridworld_table", rows=4096, steps=64, seed=28, policy="random", sampler=[1.0, 3.0, 2.0],
                                     keys=True, env={"seed": 10, "max_steps": 20}),
 }
 # cases small enough for the oracle's pure-Python restatement
-TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted", "gridworld_many"]
+TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted", "gridworld_many",
+                      "suite_mixed"]
 
 
 def sampler_arrays(weights) -> tuple[np.ndarray, np.ndarray]:
@@ -159,7 +164,7 @@ def table_inputs(case: str, instances: int) -> dict:
 
 # table cases whose batch, after step TABLE_EXPAND_STEP, is also expanded by rl::expand over the table
 # (include/mymyr/rl/expand.hpp:133-150), with and without drop_noops
-TABLE_EXPAND_CASES = ["gridworld_ids", "transport_ids", "gridworld_many", "transport_large"]
+TABLE_EXPAND_CASES = ["gridworld_ids", "transport_ids", "gridworld_many", "transport_large", "suite_mixed", "suite_mixed_large"]
 TABLE_EXPAND_STEP = 5
 
 

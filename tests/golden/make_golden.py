@@ -188,7 +188,7 @@ def table_trajectory(case: str) -> dict:
     I, W = len(ts), max(t.words for t in ts)
     L = max(1, max(t.label_width for t in ts))
     inp = fx.table_inputs(case, I)
-    e = ref.RefTableEnv(ts, sampler=fx.case_sampler(case, I), **c["env"])
+    e = ref.RefTableEnv(ts, sampler=fx.case_sampler(case, I), suite=c.get("suite", False), **c["env"])
     b = table_batch_arrays(case, inp, W)
     cnt = np.zeros(rows, np.int32)
     init = [t.initial_state(W) for t in ts]

@@ -26,7 +26,8 @@ def load_tasks(golden, table):
     return [Task.from_text_file(p) for p in workloads.table_files(table, golden.TASKS)]
 
 
-@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_many", "gridworld_many_large"])
+@pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_many", "gridworld_many_large",
+                                  "suite_mixed", "suite_mixed_large"])
 def test_batched_env_matches_reference(golden, case):
     from mymyr_amd import rl
     from mymyr_amd.batched import BatchedEnv
@@ -41,7 +42,8 @@ def test_batched_env_matches_reference(golden, case):
     sampler = None
     if c.get("sampler") is not None:
         sampler = rl.InstanceSampler(len(ts), None if c["sampler"] == "uniform" else c["sampler"])
-    env = BatchedEnv(ts, rows, task_ids=inp["task_ids"], sampler=sampler, first_env=5, goals=goals, **c["env"])
+    table = rl.TaskSuite(ts) if c.get("suite") else ts
+    env = BatchedEnv(table, rows, task_ids=inp["task_ids"], sampler=sampler, first_env=5, goals=goals, **c["env"])
     init = [t.initial_state(env.words) for t in ts]
 
     def state():
@@ -64,7 +66,10 @@ def test_batched_env_matches_reference(golden, case):
                 gp = np.zeros((rows, env.words), np.uint64)
                 for i in range(rows):
                     gp[i] = init[ids[i]]
-                env.reset(m, goal_pos=torch.from_numpy(gp.view(np.int64)).cuda(), goal_neg=torch.zeros_like(env.goal_neg))
+                # the fixture's keep-goals reset keeps the rows' instances: with a sampler, name them (BatchedEnv samples
+                # the reset rows' instances unless task ids are given)
+                env.reset(m, task_ids=env.task_ids.clone() if sampler is not None else None,
+                          goal_pos=torch.from_numpy(gp.view(np.int64)).cuda(), goal_neg=torch.zeros_like(env.goal_neg))
             else:
                 assert sample == (new is None)
                 env.reset(m, task_ids=None if new is None else torch.from_numpy(new))

@@ -44,7 +44,8 @@ def replay(golden, case: str):
     sampler = None
     if c.get("sampler") is not None:
         sampler = rl.InstanceSampler(len(ts), None if c["sampler"] == "uniform" else c["sampler"])
-    pool = rl.DeviceEnvPool(ts, rows, first_env=5, goals=goals, task_ids=inp["task_ids"], sampler=sampler, seeds=inp.get("seeds"),
+    table = rl.TaskSuite(ts) if c.get("suite") else ts
+    pool = rl.DeviceEnvPool(table, rows, first_env=5, goals=goals, task_ids=inp["task_ids"], sampler=sampler, seeds=inp.get("seeds"),
                             env_ids=inp.get("env_ids"), sampling_seeds=inp.get("sampling_seeds"), **c["env"])
     assert (pool.words, pool.label_width) == (g["words"], g["label_width"])
     W = pool.words
@@ -83,9 +84,9 @@ def replay(golden, case: str):
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
         if k == golden.TABLE_EXPAND_STEP and case in golden.TABLE_EXPAND_CASES:
             # rl::expand over the table on the batch after this step (rows of several instances, grouped on the device)
-            table = rl.TaskTable(ts)
+            group = rl.TaskSuite(ts) if c.get("suite") else rl.TaskTable(ts)
             for key, drop in (("all", False), ("drop", True)):
-                x = rl.expand(table, pool.states, task_ids=pool.task_ids, goal=True, hashes=True, noops=True, index=True, drop_noops=drop)
+                x = rl.expand(group, pool.states, task_ids=pool.task_ids, goal=True, hashes=True, noops=True, index=True, drop_noops=drop)
                 want = g["expand"][key]
                 assert (x["generated"], x["total"]) == (want["generated"], want["total"]), f"{case}: expansion {key}"
                 got = {"succ": u64(x["succ"]), "parent": host(x["parent"]), "schema": host(x["schema"]), "binding": host(x["binding"]),
@@ -97,8 +98,8 @@ def replay(golden, case: str):
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
-                                  "gridworld_many", "gridworld_large", "transport_large", "gridworld_sampled_large",
-                                  "gridworld_many_large"])
+                                  "gridworld_many", "suite_mixed", "gridworld_large", "transport_large", "gridworld_sampled_large",
+                                  "gridworld_many_large", "suite_mixed_large"])
 def test_table_env_matches_reference(golden, case):
     replay(golden, case)
 

@@ -34,7 +34,7 @@ def replay_oracle(golden, case: str) -> None:
     g = golden.load("env_table.json")[case]
     c = golden.TABLE_CASES[case]
     ts = load_table(golden, c["table"])
-    e = port.TableEnv(ts, sampler=golden.case_sampler(case, len(ts)), **c["env"])
+    e = port.TableEnv(ts, sampler=golden.case_sampler(case, len(ts)), suite=c.get("suite", False), **c["env"])
     assert (e.words, e.label_width) == (g["words"], g["label_width"])
     inp = golden.table_inputs(case, len(ts))
     b = table_batch(golden, case, inp, e.words)
@@ -71,7 +71,7 @@ def replay_oracle(golden, case: str) -> None:
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
-                                  "gridworld_many"])
+                                  "gridworld_many", "suite_mixed"])
 def test_table_env_matches_reference(golden, case):
     assert case in golden.TABLE_ORACLE_CASES
     replay_oracle(golden, case)
