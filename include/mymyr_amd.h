@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 7
+#define MYA_ABI_VERSION 8
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -181,6 +181,17 @@ typedef struct mya_env_batch
      * reset_counts: no counting and no sampling. */
     uint32_t* reset_counts;
     const uint64_t* sampling_seeds;
+    /* Visited tables (EnvBatch::visited, include/mymyr/rl/env.hpp:126-130; rl/visited.hpp), device, optional (null
+     * visited: none): visited [rows, visited_capacity] u64 keys by linear probing (the reference's layout, word for
+     * word), visited_count [rows], visited_status [1] (or [rows] with visited_status_per_row) with sticky bit 0 for an
+     * overflowed row. visited_capacity is a power of two in [2, 2^20]. reset restarts a reset row's table with its
+     * initial state's key; a step inserts the reached state's key (unless the episode is over without autoreset) and
+     * an autoreset restarts the table. */
+    uint64_t* visited;
+    int32_t* visited_count;
+    int32_t* visited_status;
+    uint32_t visited_capacity;
+    int32_t visited_status_per_row;
 } mya_env_batch;
 
 /* StepOutputs (include/mymyr/rl/env.hpp:138-152), device pointers, null = not written. binding [rows, label_width];
@@ -205,6 +216,8 @@ typedef struct mya_step_outputs
     uint8_t* masks;
     uint32_t max_atoms;
     uint32_t reserved;
+    /* [rows]: the reached state's key was in the row's visited table before the step (StepOutputs::revisited) */
+    uint8_t* revisited;
 } mya_step_outputs;
 
 /* A device environment over one task (replaces cuda::DeviceEnv, include/mymyr/cuda/env.hpp:89, and
@@ -269,6 +282,9 @@ int mya_env_random_actions(mya_env* env, const mya_env_batch* batch, const int32
 /* Whether each row's current state is a goal of its instance (HostEnv::goal, src/mymyr/rl/env.cpp:272-281): the
  * per-env masks' test when the batch has them, else the instance's goal test; goal (device uint8 [rows]). Async. */
 int mya_env_goal(mya_env* env, const mya_env_batch* batch, uint8_t* goal, void* stream);
+/* HostEnv::clear_visited (include/mymyr/rl/env.hpp:210-211): the visited tables of the rows with mask[i] != 0 (device,
+ * optional: all rows) hold their current states' keys only; the overflow status is kept. Async on the stream. */
+int mya_env_clear_visited(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, void* stream);
 /* Reads and clears the sticky device status (synchronizes the env's status copy); -1 with a message if a step failed. */
 int mya_env_check(mya_env* env);
 /* Recomputes at_goal and the count cache (when the batch has one) of every row from its state and instance, after the

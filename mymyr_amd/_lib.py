@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 7  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 8  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -70,6 +70,11 @@ class EnvBatch(Structure):
         ("env_ids", c_void_p),
         ("reset_counts", c_void_p),
         ("sampling_seeds", c_void_p),
+        ("visited", c_void_p),
+        ("visited_count", c_void_p),
+        ("visited_status", c_void_p),
+        ("visited_capacity", c_uint32),
+        ("visited_status_per_row", c_int32),
     ]
 
 
@@ -90,6 +95,7 @@ class StepOutputs(Structure):
         ("masks", c_void_p),
         ("max_atoms", c_uint32),
         ("reserved", c_uint32),
+        ("revisited", c_void_p),
     ]
 
 
@@ -212,6 +218,7 @@ def _load() -> ctypes.CDLL:
         "mya_env_reset": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p, c_int, c_int, c_void_p]),
         "mya_env_set_sampling": (c_int, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint32]),
         "mya_env_set_seed": (c_int, [c_void_p, c_uint64, c_void_p]),
+        "mya_env_clear_visited": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),
         "mya_env_reserve": (c_int, [c_void_p, c_uint64]),
         "mya_env_random_actions": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_uint32, c_void_p, c_void_p]),
         "mya_env_goal": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),

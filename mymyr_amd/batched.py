@@ -9,8 +9,9 @@ The environments' tensors are ``states`` [N, row_words] int64 (the widest instan
 addresses: loops of steps capture into HIP graphs (:meth:`BatchedEnv.capture`, or ``torch.cuda.graph`` around the
 calls). Writing ``states``, ``task_ids`` or the goal masks directly needs :meth:`BatchedEnv.refresh`.
 
-The reference's observation encoders, label actions and visited tables are not part of this path; asking for them
-raises NotImplementedError.
+The reference's observation encoders and label actions are not part of this path; asking for them raises
+NotImplementedError. Visited tables (``track_visited``) are kept on the device: ``visited`` [N, H] int64, ``visited_count``
+[N] int32, ``visited_status`` [1] int32.
 """
 
 from __future__ import annotations
@@ -24,7 +25,7 @@ from torch import Tensor
 
 from . import _lib
 from ._lib import check, lib
-from .rl import InstanceSampler, TaskSuite, TaskTable
+from .rl import InstanceSampler, TaskSuite, TaskTable, visited_capacity
 from .task import Task
 
 __all__ = ["BatchedEnv", "CapturedRollout", "Observation", "Rollout", "StepResult"]
@@ -64,7 +65,7 @@ class StepResult(NamedTuple):
     at_goal: Tensor
     obs: Any = None
     final_obs: Any = None
-    revisited: Optional[Tensor] = None  # bool [N], all false (no visited tables)
+    revisited: Optional[Tensor] = None  # bool [N]: the reached state's key was in the env's visited table (false without tables)
     actions: Any = None
     action_visited: Any = None
 
@@ -141,8 +142,6 @@ class BatchedEnv:
             raise NotImplementedError("mymyr_amd: BatchedEnv: observation encoders are not part of the device expansion path")
         if actions != "index":
             raise NotImplementedError("mymyr_amd: BatchedEnv: label actions are not part of the device expansion path")
-        if track_visited:
-            raise NotImplementedError("mymyr_amd: BatchedEnv: visited tables are not part of the device expansion path")
         if path not in ("auto", "fast"):
             raise ValueError("mymyr_amd: BatchedEnv runs the device's fast path only")
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
@@ -191,10 +190,17 @@ class BatchedEnv:
         if goals:
             self.goal_pos = torch.zeros((n, W), dtype=torch.int64, device=d)
             self.goal_neg = torch.zeros((n, W), dtype=torch.int64, device=d)
+        # visited tables (track_visited): keys [N, H] int64, counts [N] int32, sticky status [1] int32
+        self.visited_capacity = visited_capacity(track_visited, max_steps)
+        H = self.visited_capacity
+        self.visited = torch.zeros((n, H), dtype=torch.int64, device=d) if H else None
+        self.visited_count = torch.zeros(n, dtype=torch.int32, device=d) if H else None
+        self.visited_status = torch.zeros(1, dtype=torch.int32, device=d) if H else None
         self._batch = _lib.EnvBatch(self.states.data_ptr(), n, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
                                     self.at_goal.data_ptr(), self.first_env, self.counts.data_ptr(), _p(self.goal_pos),
                                     _p(self.goal_neg), self.task_ids.data_ptr() if self.multi else None, None, None,
-                                    self.reset_counts.data_ptr() if self.sampler is not None else None, None)
+                                    self.reset_counts.data_ptr() if self.sampler is not None else None, None, _p(self.visited),
+                                    _p(self.visited_count), _p(self.visited_status), H, 0)
         # the scratch of N rows now: later calls allocate nothing, so they capture into graphs
         check(lib.mya_env_reserve(self._h, n))
         self.capturable = True
@@ -312,11 +318,12 @@ class BatchedEnv:
         ids = self._task_ids(next_task_ids, None, "next_task_ids")
         return ids if self.multi else None  # a table of one: every instance is 0
 
-    def _step_raw(self, outs: list[Tensor], action: Optional[Tensor], next_ids: Optional[Tensor], final: bool) -> None:
+    def _step_raw(self, outs: list[Tensor], action: Optional[Tensor], next_ids: Optional[Tensor], final: bool,
+                  revisited: Optional[Tensor] = None) -> None:
         reward, term, trunc, goal, invalid, schema, binding, fs = outs
         o = _lib.StepOutputs(reward.data_ptr(), term.data_ptr(), trunc.data_ptr(), self.count.data_ptr(), fs.data_ptr() if final else None,
                              schema.data_ptr(), binding.data_ptr(), self._label_width, self._words, invalid.data_ptr(),
-                             goal.data_ptr(), None, None, 0, 0)
+                             goal.data_ptr(), None, None, 0, 0, _p(revisited))
         check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(o), _p(action), _p(next_ids), _stream()))
 
     def step(self, action: Any = None, *, next_task_ids: Optional[Any] = None, final: bool = True, copy: bool = True) -> StepResult:
@@ -324,10 +331,19 @@ class BatchedEnv:
         random policy); ``next_task_ids`` [N] overrides sampling for autoresetting environments; ``final=True`` keeps
         the reached states before the autoreset; ``copy=False`` borrows the live observation tensors."""
         outs = self._outputs(final)
-        self._step_raw(outs, self._action(action), self._next_ids(next_task_ids), final)
-        obs = self.observation(copy=copy)
         revisited = torch.zeros(self.num_envs, dtype=torch.bool, device=self.device)
+        self._step_raw(outs, self._action(action), self._next_ids(next_task_ids), final, revisited if self.visited_capacity else None)
+        obs = self.observation(copy=copy)
         return StepResult(*outs, obs.count, obs.states, obs.task_ids, obs.goal_pos, obs.goal_neg, obs.at_goal, revisited=revisited)
+
+    def clear_visited(self, mask: Optional[Tensor] = None) -> None:
+        """Clear all visited tables, or rows selected by bool mask [N], and insert their current states."""
+        if not self.visited_capacity:
+            return
+        m8 = None
+        if mask is not None:
+            m8 = mask.reshape(self.num_envs).to(device=self.device, dtype=torch.bool).contiguous().view(torch.uint8)
+        check(lib.mya_env_clear_visited(self._h, ctypes.byref(self._batch), _p(m8), _stream()))
 
     def random_actions(self, max_actions: Optional[int] = None) -> Tensor:
         """The successors ``step(None)`` would take now, among the first ``max_actions`` (None: all); 0 where none."""
@@ -416,7 +432,7 @@ class CapturedRollout:
             action = env._action(self.policy(env))
             o.action[k].copy_(action)
         outs = [o.reward[k], o.terminated[k], o.truncated[k], o.goal[k], o.invalid[k], o.schema[k], o.binding[k], o.final_states[k]]
-        env._step_raw(outs, action, self.next_task_ids, self.final)
+        env._step_raw(outs, action, self.next_task_ids, self.final, o.revisited[k] if env.visited_capacity else None)
         o.count[k].copy_(env.count)
         o.states[k].copy_(env.states)
         o.task_ids[k].copy_(env.task_ids)

@@ -90,9 +90,25 @@ void check_batch(const mya_env* e, const mya_env_batch* b)
             if (e->inst[i].T.goal_unsat)
                 throw std::invalid_argument("mymyr: env: per-env goal masks cannot express the goal of instance " + std::to_string(i) +
                                             " (it is statically unsatisfiable); use the instances' goal tests (no goal masks)");
+    if (b->visited)
+    {
+        const u32 H = b->visited_capacity;
+        if (H < 2 || H > (1u << 20) || (H & (H - 1)))
+            throw std::invalid_argument("mymyr: env: visited capacity must be a power of two in [2, 2^20]");
+        if (b->rows && (!b->visited_count || !b->visited_status))
+            throw std::invalid_argument("mymyr: env: visited tracking needs table, count and status arrays");
+    }
     if (!b->task_ids && b->rows && e->instances() > 1)
         throw std::invalid_argument("mymyr: env: a batch over a table of " + std::to_string(e->instances()) +
                                     " instances needs task ids");
+}
+
+/// The batch's visited tables as the kernels take them (capacity 0: none).
+VisitedDev visited_of(const mya_env_batch* b)
+{
+    if (!b->visited)
+        return VisitedDev{};
+    return VisitedDev{b->visited, b->visited_count, b->visited_status, b->visited_capacity, b->visited_status_per_row ? 1u : 0u};
 }
 
 /// Whether a call runs grouped by instance: over several instances (a one-instance batch runs in batch order, checking
@@ -447,6 +463,7 @@ void create_env(mya_task* const* tasks, uint32_t count, const mya_env_config* co
             d.init_goal = in.init_goal;
             d.fluent_slots = in.T.fluent_slots;
             d.variant = in.variant;
+            d.init_hash = hash_state(tasks[i]->compiled->initial.data(), in.T.W);
             ht[i] = in.T;
         }
         e->d_inst = dev_alloc<InstDev>(count, "env instances");
@@ -576,6 +593,8 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
         if (batch->goal_pos)
             launch_env_reset_goals(env->d_inst, env->instances(), batch->rows, batch->words, mask, batch->task_ids, batch->goal_pos,
                                    batch->goal_neg, keep_goals != 0, batch->at_goal, env->d_status, s);
+        launch_visited_restart(visited_of(batch), env->d_inst, env->instances(), batch->states, batch->rows, batch->words, mask,
+                               batch->task_ids, false, s);
     });
 }
 
@@ -642,6 +661,8 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.mask_width = env->num_schemas;
         a.goal_pos = batch->goal_pos;
         a.goal_neg = batch->goal_neg;
+        a.visited = visited_of(batch);
+        a.revisited = out->revisited;
         a.status = env->d_status;
         const auto s = static_cast<hipStream_t>(stream);
         // without next_task_ids, rows restart in their next sampled instances when the env has a sampler and the batch
@@ -707,6 +728,19 @@ int mya_env_reserve(mya_env* env, uint64_t rows)
             prepare_env_launches(in.T);
         for (const mya_env::Launch& l : env->launches)
             prepare_grouped_launches(l.variant, l.lds);
+    });
+}
+
+int mya_env_clear_visited(mya_env* env, const mya_env_batch* batch, const uint8_t* mask, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        check_batch(env, batch);
+        if (env->instances() > 1 && batch->task_ids)
+            launch_check_ids(batch->task_ids, batch->rows, env->instances(), env->d_status, static_cast<hipStream_t>(stream));
+        launch_visited_restart(visited_of(batch), env->d_inst, env->instances(), batch->states, batch->rows, batch->words, mask,
+                               batch->task_ids, true, static_cast<hipStream_t>(stream));
     });
 }
 

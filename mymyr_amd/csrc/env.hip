@@ -1199,6 +1199,63 @@ unsigned waves_per_block(const TaskDev& T, size_t* lds_bytes)
     return block_shape(hot, wave, lds_bytes);
 }
 
+/// hash_state of a row (its trimmed words; include/mymyr/core/hash.hpp:56-60), one lane.
+template<class P>
+__device__ __forceinline__ u64 row_hash(P row, u32 W)
+{
+    u32 n = W;
+    while (n > 0 && row[n - 1] == 0)
+        --n;
+    u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
+    u32 k = 0;
+    for (; k + 1 < n; k += 2)
+        h = mulfold(h ^ row[k] ^ kHashP1, row[k + 1] ^ kHashP2);
+    if (k < n)
+        h = mulfold(h ^ row[k] ^ kHashP1, kHashP2);
+    return mix64(h);
+}
+
+constexpr u64 kVisitedZero = 0x9E3779B97F4A7C15ull;  // the key of hash 0 (0 marks an empty slot)
+
+/// visited_insert (include/mymyr/rl/visited.hpp:31-52), one lane: whether the key was present; a new key above
+/// floor(3H/4) entries is skipped and the count saturates at H.
+__device__ __forceinline__ bool visited_insert(u64* table, u32 H, i32& count, u64 hash)
+{
+    const u64 key = hash ? hash : kVisitedZero;
+    u32 at = static_cast<u32>(key) & (H - 1);
+    for (u32 probe = 0; probe < H; ++probe, at = (at + 1) & (H - 1))
+    {
+        const u64 x = table[at];
+        if (x == key)
+            return true;
+        if (!x)
+        {
+            if (count >= static_cast<i32>((static_cast<u64>(H) * 3) / 4))
+                count = static_cast<i32>(H);
+            else
+            {
+                table[at] = key;
+                ++count;
+            }
+            return false;
+        }
+    }
+    count = static_cast<i32>(H);
+    return false;
+}
+
+/// visited_clear + visited_insert of one hash over a row's table (all lanes; every slot written once, the key's own
+/// slot with the key); the count becomes 1 (lane 0).
+__device__ __forceinline__ void visited_restart(u64* table, u32 H, i32* count, u64 hash, u32 lane)
+{
+    const u64 key = hash ? hash : kVisitedZero;
+    const u32 at = static_cast<u32>(key) & (H - 1);
+    for (u32 q = lane; q < H; q += kWave)
+        table[q] = q == at ? key : 0;
+    if (lane == 0)
+        *count = 1;
+}
+
 /// One environment's step (HostEnv::step_row_impl, src/mymyr/rl/env.cpp:351-528): row i of instance k, whose tables
 /// are T / H and whose wave region is L. An autoreset restarts the row in next_task_ids[i] when that names an instance
 /// (else in k), writing the new instance's initial state and goal masks over the words the row may have dirtied
@@ -1326,6 +1383,24 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         for (u32 q = lane; q < FW; q += kWave)
             f[q] = q < T.W ? L.row[q] : 0;
     }
+    // the reached state's key into the row's visited table unless its episode is over without autoreset (env.cpp:487-499)
+    if (A.visited.capacity || A.revisited)
+    {
+        bool revisited = false;
+        const bool over = !A.cfg.autoreset && (absorbed || (A.cfg.max_steps && steps0 >= static_cast<i32>(A.cfg.max_steps)));
+        if (lane == 0 && A.visited.capacity && !over)
+        {
+            const u32 H = A.visited.capacity;
+            i32 cnt = A.visited.count[i];
+            revisited = visited_insert(A.visited.table + i * H, H, cnt, row_hash(L.row, T.W));
+            A.visited.count[i] = cnt;
+            if (cnt == static_cast<i32>(H))
+                atomicOr(A.visited.status + (A.visited.status_per_row ? i : 0), 1);
+        }
+        if (lane == 0 && A.revisited)
+            A.revisited[i] = revisited ? 1 : 0;
+        wave_sync();
+    }
     // 5. the autoreset, or the bookkeeping of the move (the LDS row holds s'). The instance an autoreset restarts in:
     // next_task_ids[i], where an id outside the table sets the status (in every row, as the reference checks the whole
     // array) and keeps the row's instance
@@ -1369,6 +1444,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (crow)
             for (u32 q = lane; q < cw; q += kWave)
                 crow[q] = J.init_cache[q];
+        if (A.visited.capacity)
+            visited_restart(A.visited.table + i * A.visited.capacity, A.visited.capacity, A.visited.count + i, J.init_hash, lane);
     }
     else
     {
@@ -1630,6 +1707,30 @@ __global__ void k_env_reset(const InstDev* inst, u32 instances, u64* states, u64
             if (count)
                 count[i] = static_cast<i32>(J.init_count);
         }
+    }
+}
+
+/// One wave per row: the masked rows' visited tables restarted with the initial state's key of the row's instance, or
+/// (current) the key of the row's state.
+__global__ __launch_bounds__(256) void k_visited_restart(VisitedDev v, const InstDev* inst, u32 instances, const u64* states, u64 rows,
+                                                         u32 words, const u8* mask, const i32* task_ids, u32 current)
+{
+    const u32 lane = lane_id(), nw = blockDim.x / kWave;
+    for (u64 i = static_cast<u64>(blockIdx.x) * nw + threadIdx.x / kWave; i < rows; i += static_cast<u64>(gridDim.x) * nw)
+    {
+        if (mask && !mask[i])
+            continue;
+        bool bad = false;
+        const InstDev& J = inst[reset_instance(task_ids, i, instances, &bad)];
+        u64 h = J.init_hash;
+        if (current)
+        {
+            u64 mine = 0;
+            if (lane == 0)
+                mine = row_hash(states + i * words, J.W);
+            h = __shfl(mine, 0, kWave);
+        }
+        visited_restart(v.table + i * v.capacity, v.capacity, v.count + i, h, lane);
     }
 }
 
@@ -2421,6 +2522,16 @@ void launch_env_sample_next(const SamplerDev& sampler, const u64* seed, u64 firs
     hipLaunchKernelGGL(k_env_sample_next, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 4096))), dim3(256), 0, stream,
                        sampler, seed, first_env, rows, reset_counts, sampling_seeds, env_ids, next);
     launch_check("env sample next");
+}
+
+void launch_visited_restart(const VisitedDev& v, const InstDev* inst, u32 instances, const u64* states, u64 rows, u32 words,
+                            const u8* mask, const i32* task_ids, bool current, hipStream_t stream)
+{
+    if (rows == 0 || !v.capacity)
+        return;
+    hipLaunchKernelGGL(k_visited_restart, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 4), 16384))), dim3(256), 0, stream, v, inst,
+                       instances, states, rows, words, mask, task_ids, current ? 1u : 0u);
+    launch_check("visited restart");
 }
 
 void launch_env_reset_draw(const SamplerDev& sampler, const u64* seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,

@@ -34,6 +34,18 @@ struct InstDev
     u32 fluent_slots;
     u32 variant;  // the kernel variant that runs the instance's rows (staged | levels << 1)
     u32 reserved;
+    u64 init_hash;  // hash_state of the initial state (its visited-table key)
+};
+
+/// Per-row visited tables (rl/visited.hpp): [rows, capacity] u64 keys by linear probing, counts [rows], a sticky
+/// overflow status word ([1], or [rows] per row).
+struct VisitedDev
+{
+    u64* table;
+    i32* count;
+    i32* status;
+    u32 capacity;  // 0: no tables
+    u32 status_per_row;
 };
 
 /// Rows of a batch over several instances grouped by instance (a counting sort of the task ids): order lists the rows
@@ -101,10 +113,17 @@ struct EnvArgs
     u32 mask_width;   // the most schemas of any instance (columns of masks)
     u64* goal_pos;    // [rows, words]: per-env goal masks (optional, with goal_neg)
     u64* goal_neg;
+    VisitedDev visited;
+    u8* revisited;    // [rows]: the reached state's key was in the row's table before the step (optional)
     u32* status;
 };
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream);
+
+/// The masked rows' visited tables restarted with one key each (visited_clear + visited_insert): the initial state's
+/// of the row's instance (a reset; run after launch_env_reset), or with `current` the hash of the row's state.
+void launch_visited_restart(const VisitedDev& v, const InstDev* inst, u32 instances, const u64* states, u64 rows, u32 words,
+                            const u8* mask, const i32* task_ids, bool current, hipStream_t stream);
 
 /// The arguments of a count over rows (refresh, the initial states, schema masks): count[i] (successors), goal[i],
 /// masks [rows, num_schemas] and the count cache [rows, num_schemas + 2] of the rows (each may be null); goal_pos /

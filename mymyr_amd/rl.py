@@ -28,6 +28,24 @@ def _p(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+def visited_capacity(track_visited: bool | int, max_steps: int | None) -> int:
+    """The capacity of an env's visited tables (python/src/py_pool.hpp:17-35): False 0; True the next power of two at
+    least 2 * (max_steps + 1) (max_steps in [1, 524287]); an int must be a power of two in [2, 2^20]."""
+    if isinstance(track_visited, bool):
+        if not track_visited:
+            return 0
+        if not max_steps or max_steps > (1 << 19) - 1:
+            raise ValueError("mymyr: track_visited=True needs max_steps in [1, 524287]; pass an explicit capacity otherwise")
+        H = 2
+        while H < 2 * (max_steps + 1):
+            H *= 2
+        return H
+    H = int(track_visited)
+    if H < 2 or H > (1 << 20) or (H & (H - 1)):
+        raise ValueError("mymyr: track_visited must be a power of two in [2, 2^20]")
+    return H
+
+
 class InstanceSampler:
     """Draws the instance an env resets into (mymyr.rl.InstanceSampler, python/mymyr/rl/_sampling.py:16-104; the draw
     is rl::rng::instance_draw, include/mymyr/rl/rng.hpp:94-115): uniform over num_instances, or weighted by `weights`
@@ -72,7 +90,7 @@ class DeviceEnvPool:
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
                  witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda",
                  count_cache: bool = True, goals: bool = False, task_ids=None, sampler: InstanceSampler | None = None,
-                 env_ids=None, seeds=None, sampling_seeds=None, reset_counts: bool | None = None):
+                 env_ids=None, seeds=None, sampling_seeds=None, reset_counts: bool | None = None, track_visited: bool | int = False):
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
         if dead_end not in ("no_successors", "none"):
@@ -151,10 +169,16 @@ class DeviceEnvPool:
             thr = np.ascontiguousarray(sampler.thresholds)
             idx = np.ascontiguousarray(sampler.indices)
             check(lib.mya_env_set_sampling(self._h, sampler.num_instances, thr.ctypes.data, idx.ctypes.data, len(idx)))
+        # visited tables (track_visited: rl/visited.hpp): keys [N, H] (uint64 bits in int64), counts [N], sticky status [1]
+        H = visited_capacity(track_visited, max_steps)
+        self.visited = torch.zeros((N, H), dtype=torch.int64, device=dev) if H else None
+        self.visited_count = torch.zeros(N, dtype=torch.int32, device=dev) if H else None
+        self.visited_status = torch.zeros(1, dtype=torch.int32, device=dev) if H else None
+        self.revisited = torch.zeros(N, dtype=torch.uint8, device=dev) if H else None
         self._batch = _lib.EnvBatch(self.states.data_ptr(), N, W, 0, self.steps.data_ptr(), self.draws.data_ptr(),
                                     self.at_goal.data_ptr(), first_env, _p(self.counts_cache), _p(self.goal_pos),
                                     _p(self.goal_neg), _p(self.task_ids), _p(self.seeds), _p(self.env_ids), _p(self.reset_counts),
-                                    _p(self.sampling_seeds))
+                                    _p(self.sampling_seeds), _p(self.visited), _p(self.visited_count), _p(self.visited_status), H, 0)
 
     def initial_count(self, instance: int = 0) -> tuple[int, bool]:
         c = ctypes.c_uint32()
@@ -218,11 +242,14 @@ class DeviceEnvPool:
             nxt = torch.as_tensor(next_task_ids, dtype=torch.int32).to(self.device).contiguous()
             if nxt.shape != (self.num_envs,):
                 raise ValueError(f"mymyr: env: next_task_ids must have shape ({self.num_envs},)")
+        out.revisited = _p(self.revisited)
         check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(out), _p(actions), _p(nxt), _stream()))
         r = {"states": self.states, "reward": self.reward, "terminated": self.terminated, "truncated": self.truncated,
              "count": self.count, "steps": self.steps, "at_goal": self.at_goal, "goal": self.goal, "invalid": self.invalid}
         if self.task_ids is not None:
             r["task_ids"] = self.task_ids
+        if self.revisited is not None:
+            r["revisited"] = self.revisited
         if labels:
             r["schema"] = self.schema
             r["binding"] = self.binding
@@ -266,6 +293,15 @@ class DeviceEnvPool:
         (DeviceEnv::refresh); returns the successor counts."""
         check(lib.mya_env_refresh(self._h, ctypes.byref(self._batch), self.count.data_ptr(), _stream()))
         return self.count
+
+    def clear_visited(self, mask: torch.Tensor | None = None) -> None:
+        """The visited tables of every env (or those with mask != 0) hold their current states' keys only
+        (HostEnv::clear_visited); the overflow status is kept."""
+        if self.visited is None:
+            return
+        if mask is not None:
+            mask = mask.to(device=self.device, dtype=torch.uint8).contiguous()
+        check(lib.mya_env_clear_visited(self._h, ctypes.byref(self._batch), _p(mask), _stream()))
 
     def check(self) -> None:
         """Raises if a step set the device's sticky error status."""

@@ -778,6 +778,15 @@ class TableEnv:
             b["goal_pos"][i, :w], b["goal_neg"][i, :w] = gp, gn
             b["goal_pos"][i, w:z] = 0
             b["goal_neg"][i, w:z] = 0
+        if b.get("visited") is not None:
+            b["visited_count"][i] = visited_restart(b["visited"][i], hash_state(t.initial))
+
+    def clear_visited(self, b: dict, mask=None) -> None:
+        """HostEnv::clear_visited (env.cpp:207-221): the masked rows' tables hold their current states' keys only."""
+        for i in range(b["states"].shape[0]):
+            if mask is None or mask[i]:
+                t = self.tasks[int(b["task_ids"][i])]
+                b["visited_count"][i] = visited_restart(b["visited"][i], hash_state(b["states"][i, : t.words]))
 
     def _goal_row(self, b: dict, i: int) -> bool:
         t = self.tasks[int(b["task_ids"][i])]
@@ -831,7 +840,7 @@ class TableEnv:
         out = {"reward": np.zeros(n, np.float32), "terminated": np.zeros(n, np.uint8), "truncated": np.zeros(n, np.uint8),
                "count": np.zeros(n, np.int32), "schema": np.full(n, -1, np.int32), "binding": np.full((n, L), -1, np.int32),
                "goal": np.zeros(n, np.uint8), "invalid": np.zeros(n, np.uint8),
-               "final_states": np.zeros((n, FW), np.uint64)}
+               "final_states": np.zeros((n, FW), np.uint64), "revisited": np.zeros(n, np.uint8)}
         goals = "goal_pos" in b
         for i in range(n):
             inst = int(b["task_ids"][i])
@@ -880,6 +889,15 @@ class TableEnv:
             out["truncated"][i] = 1 if trunc else 0
             out["goal"][i] = 1 if g else 0
             out["final_states"][i, :w] = s2
+            if b.get("visited") is not None:
+                # the reached state's key (env.cpp:487-499), unless the episode is over without autoreset
+                over = (not self.autoreset) and (absorbed or (self.max_steps and int(b["steps"][i]) >= self.max_steps))
+                rv = False
+                if not over:
+                    rv, b["visited_count"][i] = visited_insert(b["visited"][i], int(b["visited_count"][i]), hash_state(s2))
+                    if b["visited_count"][i] == b["visited"].shape[1]:
+                        b["visited_status"][0] |= 1
+                out["revisited"][i] = 1 if rv else 0
             if self.autoreset and (term or trunc):
                 if next_task_ids is not None:
                     nxt = int(next_task_ids[i])
@@ -898,6 +916,35 @@ class TableEnv:
             b["steps"][i] = t2
             out["count"][i] = c2
         return out
+
+
+VISITED_ZERO = 0x9E3779B97F4A7C15
+
+
+def visited_insert(table, count: int, h: int) -> tuple[bool, int]:
+    """The visited table's insert (include/mymyr/rl/visited.hpp:31-52): linear probing over H slots from key & (H - 1),
+    key = the hash (0 maps to a reserved key); a new key above floor(3H/4) entries is skipped and the count saturates
+    at H. Returns (whether the key was present, the new count); writes `table` in place."""
+    H = len(table)
+    key = h if h else VISITED_ZERO
+    at = key & (H - 1)
+    for _ in range(H):
+        if int(table[at]) == key:
+            return True, count
+        if int(table[at]) == 0:
+            if count >= (H * 3) // 4:
+                return False, H
+            table[at] = np.uint64(key)
+            return False, count + 1
+        at = (at + 1) & (H - 1)
+    return False, H
+
+
+def visited_restart(table, h: int) -> int:
+    """visited_clear then visited_insert of one hash (visited.hpp:55-61): returns the count, 1."""
+    table[:] = 0
+    _, c = visited_insert(table, 0, h)
+    return c
 
 
 def goal_masks_fit(gp, gn, fluent_slots: int) -> bool:

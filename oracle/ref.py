@@ -96,7 +96,8 @@ def lib() -> ctypes.CDLL:
             "mref_table_env_create": (c_void_p, [c_void_p, c_uint32, POINTER(EnvConfig), c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
             "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int]),
             "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                            c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32]),
+                                            c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
+            "mref_table_env_clear_visited": (c_int, [c_void_p, c_void_p, c_void_p]),
             "mref_table_expand": (c_int64, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_uint32, c_int, c_uint64, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             POINTER(c_uint64)]),
@@ -221,7 +222,8 @@ class TableBatch(Structure):
         ("states", c_void_p), ("rows", c_uint64), ("words", c_uint32), ("reserved", c_uint32), ("steps", c_void_p),
         ("draws", c_void_p), ("at_goal", c_void_p), ("first_env", c_uint64), ("task_ids", c_void_p), ("goal_pos", c_void_p),
         ("goal_neg", c_void_p), ("reset_counts", c_void_p), ("seeds", c_void_p), ("env_ids", c_void_p),
-        ("sampling_seeds", c_void_p),
+        ("sampling_seeds", c_void_p), ("visited", c_void_p), ("visited_count", c_void_p), ("visited_status", c_void_p),
+        ("visited_capacity", c_uint32), ("reserved2", c_uint32),
     ]
 
 
@@ -250,8 +252,15 @@ class RefTableEnv:
         goal_pos, goal_neg, reset_counts, seeds, env_ids, sampling_seeds)."""
         rows, words = b["states"].shape
         g = lambda k: _p(b.get(k))
+        H = b["visited"].shape[1] if b.get("visited") is not None else 0
         return TableBatch(b["states"].ctypes.data, rows, words, 0, g("steps"), g("draws"), g("at_goal"), first_env, g("task_ids"),
-                          g("goal_pos"), g("goal_neg"), g("reset_counts"), g("seeds"), g("env_ids"), g("sampling_seeds"))
+                          g("goal_pos"), g("goal_neg"), g("reset_counts"), g("seeds"), g("env_ids"), g("sampling_seeds"), g("visited"),
+                          g("visited_count"), g("visited_status"), H, 0)
+
+    def clear_visited(self, b: dict, mask=None):
+        tb = self.batch(b)
+        if lib().mref_table_env_clear_visited(self._h, ctypes.byref(tb), _p(mask)) != 0:
+            raise RuntimeError(_err())
 
     def reset(self, b: dict, count, mask=None, keep_goals=False, sample=False, first_env=0):
         tb = self.batch(b, first_env)
@@ -259,12 +268,13 @@ class RefTableEnv:
             raise RuntimeError(_err())
 
     def step(self, b: dict, first_env=0, actions=None, next_task_ids=None, reward=None, terminated=None, truncated=None, count=None,
-             schema=None, binding=None, goal=None, invalid=None, final_states=None):
+             schema=None, binding=None, goal=None, invalid=None, final_states=None, revisited=None):
         tb = self.batch(b, first_env)
         lw = 0 if binding is None else binding.shape[1]
         fw = 0 if final_states is None else final_states.shape[1]
         rc = lib().mref_table_env_step(self._h, ctypes.byref(tb), _p(actions), _p(next_task_ids), _p(reward), _p(terminated),
-                                       _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal), _p(invalid), _p(final_states), fw)
+                                       _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal), _p(invalid), _p(final_states), fw,
+                                       _p(revisited))
         if rc != 0:
             raise RuntimeError(_err())
 

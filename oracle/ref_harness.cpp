@@ -399,6 +399,11 @@ struct mref_table_batch
     const uint64_t* seeds;
     const uint32_t* env_ids;
     const uint64_t* sampling_seeds;
+    uint64_t* visited;        // [rows, visited_capacity] (null: no visited tables)
+    int32_t* visited_count;   // [rows]
+    int32_t* visited_status;  // [1]
+    uint32_t visited_capacity;
+    uint32_t reserved2;
 };
 
 static rl::EnvBatch table_batch(const mref_table_batch* t)
@@ -418,7 +423,24 @@ static rl::EnvBatch table_batch(const mref_table_batch* t)
     b.seeds = t->seeds;
     b.env_ids = t->env_ids;
     b.sampling_seeds = t->sampling_seeds;
+    b.visited = t->visited;
+    b.visited_count = t->visited_count;
+    b.visited_status = t->visited_status;
+    b.visited_capacity = t->visited ? t->visited_capacity : 0;
     return b;
+}
+
+// HostEnv::clear_visited over a table batch (include/mymyr/rl/env.hpp:210-211): mask [rows] (null: all rows).
+int mref_table_env_clear_visited(mref_env* e, const mref_table_batch* t, const uint8_t* mask)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::EnvBatch b = table_batch(t);
+            e->env->clear_visited(b, mask);
+            return 0;
+        },
+        -1);
 }
 
 // HostEnv::reset over a table batch: mask [rows] (null: all), keep_goals, sample (draw the reset rows' instances).
@@ -439,7 +461,8 @@ int mref_table_env_reset(mref_env* e, const mref_table_batch* t, int32_t* count,
 // [rows, final_words] (final_words 0: the batch's words).
 int mref_table_env_step(mref_env* e, const mref_table_batch* t, const int64_t* actions, const int32_t* next_task_ids, float* reward,
                         uint8_t* terminated, uint8_t* truncated, int32_t* count, int32_t* schema, int32_t* binding,
-                        uint32_t label_width, uint8_t* goal, uint8_t* invalid, uint64_t* final_states, uint32_t final_words)
+                        uint32_t label_width, uint8_t* goal, uint8_t* invalid, uint64_t* final_states, uint32_t final_words,
+                        uint8_t* revisited)
 {
     return guarded(
         [&]() -> int
@@ -457,6 +480,7 @@ int mref_table_env_step(mref_env* e, const mref_table_batch* t, const int64_t* a
             o.invalid = invalid;
             o.final_states = final_states;
             o.words = final_words;
+            o.revisited = revisited;
             rl::Actions a;
             a.v64 = actions;
             e->env->step(b, o, a, next_task_ids, nullptr);

@@ -102,12 +102,18 @@ TABLE_CASES = {
                         env={"seed": 13, "max_steps": 8, "step_reward": -1.0, "goal_reward": 2.0}),
     "suite_mixed_large": dict(table="mixed_suite", suite=True, rows=4096, steps=40, seed=32, policy="given", sampler=[1.0, 2.0, 1.0, 3.0, 1.0],
                               env={"seed": 14, "max_steps": 12}),
+    "gridworld_visited": dict(table="gridworld_table", rows=40, steps=40, seed=33, policy="random", visited=8,
+                              env={"seed": 15, "max_steps": 30, "step_reward": -1.0}),
+    "transport_visited": dict(table="transport_table", rows=24, steps=24, seed=34, policy="given", visited=16, goals=True,
+                              env={"seed": 16, "max_steps": 10, "autoreset": False}),
+    "gridworld_visited_large": dict(table="gridworld_table", rows=4096, steps=48, seed=35, policy="random", visited=64, sampler="uniform",
+                                    env={"seed": 17, "max_steps": 40}),
     "gridworld_sampled_large": dict(table="gridworld_table", rows=4096, steps=64, seed=28, policy="random", sampler=[1.0, 3.0, 2.0],
                                     keys=True, env={"seed": 10, "max_steps": 20}),
 }
 # cases small enough for the oracle's pure-Python restatement
 TABLE_ORACLE_CASES = ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted", "gridworld_many",
-                      "suite_mixed"]
+                      "suite_mixed", "gridworld_visited", "transport_visited"]
 
 
 def sampler_arrays(weights) -> tuple[np.ndarray, np.ndarray]:
@@ -155,6 +161,9 @@ def table_inputs(case: str, instances: int) -> dict:
         m = rng.random(rows) < 0.4
         resets[3 * steps // 4] = (m.astype(np.uint8), None, False, True)
     out["resets"] = resets
+    out["clears"] = {}
+    if c.get("visited"):
+        out["clears"][steps // 3] = (rng.random(rows) < 0.3).astype(np.uint8)
     if c.get("keys"):
         out["seeds"] = rng.integers(0, 2**63, rows, dtype=np.int64).view(np.uint64)
         out["env_ids"] = rng.integers(0, 2**32, rows, dtype=np.uint64).astype(np.uint32)
@@ -178,7 +187,8 @@ def expansion_digest(x: dict) -> str:
 
 def table_state(b: dict) -> list:
     """The batch arrays a table case's digests cover, in order (those the batch has)."""
-    keys = ("states", "task_ids", "steps", "draws", "at_goal", "goal_pos", "goal_neg", "reset_counts")
+    keys = ("states", "task_ids", "steps", "draws", "at_goal", "goal_pos", "goal_neg", "reset_counts", "visited", "visited_count",
+            "visited_status")
     return [b[k] for k in keys if b.get(k) is not None]
 
 

@@ -176,6 +176,10 @@ def table_batch_arrays(case: str, inp: dict, W: int) -> dict:
     for k in ("seeds", "env_ids", "sampling_seeds"):
         if k in inp:
             b[k] = inp[k]
+    if c.get("visited"):
+        b["visited"] = np.zeros((rows, c["visited"]), np.uint64)
+        b["visited_count"] = np.zeros(rows, np.int32)
+        b["visited_status"] = np.zeros(1, np.int32)
     return b
 
 
@@ -198,6 +202,9 @@ def table_trajectory(case: str) -> dict:
     digests = []
     totals = {"terminated": 0, "truncated": 0, "invalid": 0, "goal": 0, "instance_rows": [0] * I}
     for k in range(steps):
+        if k in inp["clears"]:
+            e.clear_visited(b, inp["clears"][k])
+            resets["clear" + str(k)] = fx.arrays_digest(*state())
         if k in inp["resets"]:
             mask, new_ids, keep, sample = inp["resets"][k]
             if new_ids is not None:
@@ -212,9 +219,12 @@ def table_trajectory(case: str) -> dict:
         R, term, trunc = np.zeros(rows, np.float32), np.zeros(rows, np.uint8), np.zeros(rows, np.uint8)
         cc, sch, bnd = np.zeros(rows, np.int32), np.zeros(rows, np.int32), np.zeros((rows, L), np.int32)
         g, inv, fs = np.zeros(rows, np.uint8), np.zeros(rows, np.uint8), np.zeros((rows, W), np.uint64)
+        rv = np.zeros(rows, np.uint8) if c.get("visited") else None
         e.step(b, first_env=5, actions=actions, next_task_ids=inp["next"][k], reward=R, terminated=term, truncated=trunc, count=cc,
-               schema=sch, binding=bnd, goal=g, invalid=inv, final_states=fs)
-        digests.append(fx.arrays_digest(*state(), R, term, trunc, cc, sch, bnd, g, inv, fs))
+               schema=sch, binding=bnd, goal=g, invalid=inv, final_states=fs, revisited=rv)
+        digests.append(fx.arrays_digest(*state(), R, term, trunc, cc, sch, bnd, g, inv, fs, *([] if rv is None else [rv])))
+        if rv is not None:
+            totals["revisited"] = totals.get("revisited", 0) + int(rv.sum())
         cnt = cc
         if k == fx.TABLE_EXPAND_STEP and case in fx.TABLE_EXPAND_CASES:
             expansions = {}

@@ -27,7 +27,8 @@ def load_tasks(golden, table):
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_many", "gridworld_many_large",
-                                  "suite_mixed", "suite_mixed_large"])
+                                  "suite_mixed", "suite_mixed_large", "gridworld_visited", "transport_visited",
+                                  "gridworld_visited_large"])
 def test_batched_env_matches_reference(golden, case):
     from mymyr_amd import rl
     from mymyr_amd.batched import BatchedEnv
@@ -43,7 +44,8 @@ def test_batched_env_matches_reference(golden, case):
     if c.get("sampler") is not None:
         sampler = rl.InstanceSampler(len(ts), None if c["sampler"] == "uniform" else c["sampler"])
     table = rl.TaskSuite(ts) if c.get("suite") else ts
-    env = BatchedEnv(table, rows, task_ids=inp["task_ids"], sampler=sampler, first_env=5, goals=goals, **c["env"])
+    env = BatchedEnv(table, rows, task_ids=inp["task_ids"], sampler=sampler, first_env=5, goals=goals,
+                     track_visited=c.get("visited", False), **c["env"])
     init = [t.initial_state(env.words) for t in ts]
 
     def state():
@@ -53,11 +55,16 @@ def test_batched_env_matches_reference(golden, case):
             b["goal_pos"], b["goal_neg"] = u64(env.goal_pos), u64(env.goal_neg)
         if sampler is not None:
             b["reset_counts"] = host(env.reset_counts).view(np.uint32)
+        if env.visited is not None:
+            b["visited"], b["visited_count"], b["visited_status"] = u64(env.visited), host(env.visited_count), host(env.visited_status)
         return golden.table_state(b)
 
     assert golden.arrays_digest(*state(), host(env.count)) == g["resets"]["initial"]
     assert torch.equal(env.is_goal(), env.at_goal)
     for k in range(c["steps"]):
+        if k in inp["clears"]:
+            env.clear_visited(torch.from_numpy(inp["clears"][k].astype(bool)))
+            assert golden.arrays_digest(*state()) == g["resets"]["clear" + str(k)], f"{case}: clear_visited at step {k}"
         if k in inp["resets"]:
             mask, new, keep, sample = inp["resets"][k]
             m = torch.from_numpy(mask.astype(bool))
@@ -79,9 +86,10 @@ def test_batched_env_matches_reference(golden, case):
             acts = torch.from_numpy(golden.given_actions(inp["u"][k], host(env.count)))
         nxt = inp["next"][k]
         r = env.step(acts, next_task_ids=None if nxt is None else torch.from_numpy(nxt), final=True)
+        extra = [host(r.revisited).view(np.uint8)] if env.visited is not None else []
         d = golden.arrays_digest(*state(), host(r.reward), host(r.terminated).view(np.uint8), host(r.truncated).view(np.uint8),
                                  host(r.count), host(r.schema), host(r.binding), host(r.goal).view(np.uint8),
-                                 host(r.invalid).view(np.uint8), u64(r.final_states))
+                                 host(r.invalid).view(np.uint8), u64(r.final_states), *extra)
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
         assert torch.equal(r.states, env.states) and torch.equal(r.at_goal, env.at_goal)
     env.check_errors()
@@ -98,7 +106,7 @@ def _twins(golden, **kw):
 @pytest.mark.parametrize("policy", [None, "argmax"])
 def test_captured_rollout_equals_eager_steps(golden, policy):
     """K steps captured into one HIP graph and replayed twice equal the same calls made eagerly on a twin env."""
-    a, b = _twins(golden, seed=3, max_steps=7, sampler="uniform")
+    a, b = _twins(golden, seed=3, max_steps=7, sampler="uniform", track_visited=16)
     pol = None
     if policy == "argmax":
         pol = lambda env: torch.clamp(env.count.to(torch.int64) - 1, min=0)  # the last successor: capturable, device only
@@ -111,11 +119,12 @@ def test_captured_rollout_equals_eager_steps(golden, policy):
             act = None if pol is None else pol(b)
             r = b.step(act, final=True)
             for name in ("reward", "terminated", "truncated", "goal", "invalid", "schema", "binding", "final_states", "count",
-                         "states", "task_ids", "at_goal"):
+                         "states", "task_ids", "at_goal", "revisited"):
                 assert torch.equal(getattr(out, name)[k], getattr(r, name)), f"replay {rep} step {k}: {name}"
             if pol is not None:
                 assert torch.equal(out.action[k], act), f"replay {rep} step {k}: action"
-        for name in ("states", "task_ids", "steps", "draws", "reset_counts", "count", "at_goal", "counts"):
+        for name in ("states", "task_ids", "steps", "draws", "reset_counts", "count", "at_goal", "counts", "visited", "visited_count",
+                     "visited_status"):
             assert torch.equal(getattr(a, name), getattr(b, name)), f"replay {rep}: env {name}"
     a.check_errors()
     b.check_errors()

@@ -46,7 +46,8 @@ def replay(golden, case: str):
         sampler = rl.InstanceSampler(len(ts), None if c["sampler"] == "uniform" else c["sampler"])
     table = rl.TaskSuite(ts) if c.get("suite") else ts
     pool = rl.DeviceEnvPool(table, rows, first_env=5, goals=goals, task_ids=inp["task_ids"], sampler=sampler, seeds=inp.get("seeds"),
-                            env_ids=inp.get("env_ids"), sampling_seeds=inp.get("sampling_seeds"), **c["env"])
+                            env_ids=inp.get("env_ids"), sampling_seeds=inp.get("sampling_seeds"), track_visited=c.get("visited", False),
+                            **c["env"])
     assert (pool.words, pool.label_width) == (g["words"], g["label_width"])
     W = pool.words
     init = initial_rows(ts, W)
@@ -58,11 +59,16 @@ def replay(golden, case: str):
             b["goal_pos"], b["goal_neg"] = u64(pool.goal_pos), u64(pool.goal_neg)
         if pool.reset_counts is not None:
             b["reset_counts"] = host(pool.reset_counts).view(np.uint32)
+        if pool.visited is not None:
+            b["visited"], b["visited_count"], b["visited_status"] = u64(pool.visited), host(pool.visited_count), host(pool.visited_status)
         return golden.table_state(b)
 
     pool.reset()
     assert golden.arrays_digest(*state(), host(pool.count)) == g["resets"]["initial"], f"{case}: initial reset"
     for k in range(steps):
+        if k in inp["clears"]:
+            pool.clear_visited(torch.from_numpy(inp["clears"][k]))
+            assert golden.arrays_digest(*state()) == g["resets"]["clear" + str(k)], f"{case}: clear_visited at step {k}"
         if k in inp["resets"]:
             mask, new, keep, sample = inp["resets"][k]
             if keep:
@@ -79,8 +85,10 @@ def replay(golden, case: str):
             acts = torch.from_numpy(golden.given_actions(inp["u"][k], host(pool.count)))
         nxt = inp["next"][k]
         o = pool.step(actions=acts, final_states=True, next_task_ids=None if nxt is None else torch.from_numpy(nxt))
+        extra = [host(o["revisited"])] if pool.visited is not None else []
         d = golden.arrays_digest(*state(), host(o["reward"]), host(o["terminated"]), host(o["truncated"]), host(o["count"]),
-                                 host(o["schema"]), host(o["binding"]), host(o["goal"]), host(o["invalid"]), u64(o["final_states"]))
+                                 host(o["schema"]), host(o["binding"]), host(o["goal"]), host(o["invalid"]), u64(o["final_states"]),
+                                 *extra)
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
         if k == golden.TABLE_EXPAND_STEP and case in golden.TABLE_EXPAND_CASES:
             # rl::expand over the table on the batch after this step (rows of several instances, grouped on the device)
@@ -99,7 +107,8 @@ def replay(golden, case: str):
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
                                   "gridworld_many", "suite_mixed", "gridworld_large", "transport_large", "gridworld_sampled_large",
-                                  "gridworld_many_large", "suite_mixed_large"])
+                                  "gridworld_many_large", "suite_mixed_large", "gridworld_visited", "transport_visited",
+                                  "gridworld_visited_large"])
 def test_table_env_matches_reference(golden, case):
     replay(golden, case)
 

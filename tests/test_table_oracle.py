@@ -27,6 +27,10 @@ def table_batch(golden, case: str, inp: dict, W: int) -> dict:
     for k in ("seeds", "env_ids", "sampling_seeds"):
         if k in inp:
             b[k] = inp[k]
+    if c.get("visited"):
+        b["visited"] = np.zeros((rows, c["visited"]), np.uint64)
+        b["visited_count"] = np.zeros(rows, np.int32)
+        b["visited_status"] = np.zeros(1, np.int32)
     return b
 
 
@@ -43,6 +47,9 @@ def replay_oracle(golden, case: str) -> None:
     e.reset(b, first_env=5)
     assert golden.arrays_digest(*state(), b["count"]) == g["resets"]["initial"]
     for k in range(c["steps"]):
+        if k in inp["clears"]:
+            e.clear_visited(b, inp["clears"][k])
+            assert golden.arrays_digest(*state()) == g["resets"]["clear" + str(k)], f"{case}: clear_visited at step {k}"
         if k in inp["resets"]:
             mask, new, keep, sample = inp["resets"][k]
             if new is not None:
@@ -57,8 +64,9 @@ def replay_oracle(golden, case: str) -> None:
             assert golden.arrays_digest(*state(), b["count"]) == g["resets"][str(k)], f"{case}: reset at step {k}"
         acts = golden.given_actions(inp["u"][k], b["count"]) if c["policy"] == "given" else None
         o = e.step(b, first_env=5, actions=acts, next_task_ids=inp["next"][k])
+        extra = [o["revisited"]] if c.get("visited") else []
         d = golden.arrays_digest(*state(), o["reward"], o["terminated"], o["truncated"], o["count"], o["schema"], o["binding"],
-                                 o["goal"], o["invalid"], o["final_states"])
+                                 o["goal"], o["invalid"], o["final_states"], *extra)
         assert d == g["digests"][k], f"{case}: step {k} differs from the reference"
         b["count"] = o["count"]
         if k == golden.TABLE_EXPAND_STEP and case in golden.TABLE_EXPAND_CASES:
@@ -71,7 +79,7 @@ def replay_oracle(golden, case: str) -> None:
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
-                                  "gridworld_many", "suite_mixed"])
+                                  "gridworld_many", "suite_mixed", "gridworld_visited", "transport_visited"])
 def test_table_env_matches_reference(golden, case):
     assert case in golden.TABLE_ORACLE_CASES
     replay_oracle(golden, case)
@@ -106,6 +114,26 @@ def test_sampler_arrays_closed_form(golden):
     assert idx.tolist() == [0, 2] and thr.tolist() == [1 << 30]
     thr, idx = golden.sampler_arrays([0.0, 5.0])
     assert idx.tolist() == [1] and thr.size == 0
+
+
+def test_visited_overflow_is_reported(golden):
+    """The small visited case overflows its 8-slot tables (a key past floor(3H/4) entries is skipped, the count
+    saturates and the sticky status is set), as the reference's fixture records."""
+    seen = {}
+    orig = port.TableEnv.step
+
+    def step(self, b, *a, **k):
+        seen["b"] = b
+        return orig(self, b, *a, **k)
+
+    port.TableEnv.step = step
+    try:
+        replay_oracle(golden, "gridworld_visited")
+    finally:
+        port.TableEnv.step = orig
+    b = seen["b"]
+    assert b["visited_status"][0] == 1 and (b["visited_count"] == 8).any()
+    assert golden.load("env_table.json")["gridworld_visited"]["totals"]["revisited"] > 0
 
 
 def test_table_fixture_exercises_the_rules(golden):
