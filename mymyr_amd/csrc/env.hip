@@ -1260,7 +1260,7 @@ __device__ __forceinline__ void visited_restart(u64* table, u32 H, i32* count, u
 /// are T / H and whose wave region is L. An autoreset restarts the row in next_task_ids[i] when that names an instance
 /// (else in k), writing the new instance's initial state and goal masks over the words the row may have dirtied
 /// (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138) and its id into task_ids.
-template<bool kLevels, bool kOne>
+template<bool kLevels, bool kOne, bool kVisited>
 __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane, u64 seed)
 {
     const u32 Lw = A.label_width;
@@ -1384,7 +1384,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             f[q] = q < T.W ? L.row[q] : 0;
     }
     // the reached state's key into the row's visited table unless its episode is over without autoreset (env.cpp:487-499)
-    if (A.visited.capacity || A.revisited)
+    if (kVisited && (A.visited.capacity || A.revisited))
     {
         bool revisited = false;
         const bool over = !A.cfg.autoreset && (absorbed || (A.cfg.max_steps && steps0 >= static_cast<i32>(A.cfg.max_steps)));
@@ -1444,7 +1444,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (crow)
             for (u32 q = lane; q < cw; q += kWave)
                 crow[q] = J.init_cache[q];
-        if (A.visited.capacity)
+        if (kVisited && A.visited.capacity)
             visited_restart(A.visited.table + i * A.visited.capacity, A.visited.capacity, A.visited.count + i, J.init_hash, lane);
     }
     else
@@ -1488,7 +1488,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
 /// The step of a batch of one instance: every row in batch order with the kernel-argument tables, as instance 0 (the
 /// host checks given task ids and next_task_ids with launch_check_ids first); with kGroup, the rows of one instance's
 /// group of a batch grouped by instance.
-template<bool kStaged, bool kLevels, bool kGroup>
+template<bool kStaged, bool kLevels, bool kGroup, bool kVisited>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
 {
     extern __shared__ u64 smem[];
@@ -1505,7 +1505,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
         const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
         const u64 seed = *A.seed;
         for (u64 j = lo + static_cast<u64>(blockIdx.x) * nw + wave; j < hi; j += static_cast<u64>(gridDim.x) * nw)
-            step_row<kLevels, false>(A, T, H, L, A.groups.order[j], A.instance, lane, seed);
+            step_row<kLevels, false, kVisited>(A, T, H, L, A.groups.order[j], A.instance, lane, seed);
     }
     else
     {
@@ -1513,7 +1513,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
         lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
         const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
         for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
-            step_row<kLevels, true>(A, T, H, L, i, 0, lane, 0);
+            step_row<kLevels, true, kVisited>(A, T, H, L, i, 0, lane, 0);
     }
 }
 
@@ -1562,7 +1562,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step_grouped(EnvArgs 
         const u32 r1 = min(r0 + kChunkRows, A.groups.starts[k + 1]);
         const u64 seed = *A.seed;
         for (u32 j = r0 + wave; j < r1; j += nw)
-            step_row<kLevels, false>(A, T, H, L, A.groups.order[j], k, lane, seed);
+            step_row<kLevels, false, true>(A, T, H, L, A.groups.order[j], k, lane, seed);
     }
 }
 
@@ -2283,10 +2283,14 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
     size_t lds = 0;
     const unsigned nw = waves_per_block(a.T, &lds);
     const bool group = a.groups.order != nullptr;
-    const auto fn = group ? variant(a.T, k_env_step<true, false, true>, k_env_step<true, true, true>, k_env_step<false, false, true>,
-                                    k_env_step<false, true, true>)
-                          : variant(a.T, k_env_step<true, false, false>, k_env_step<true, true, false>, k_env_step<false, false, false>,
-                                    k_env_step<false, true, false>);
+    // the visited tables' code only in the launches that use it (it keeps more kernel arguments live)
+    const bool visited = a.visited.capacity || a.revisited;
+    const auto fn = group     ? variant(a.T, k_env_step<true, false, true, true>, k_env_step<true, true, true, true>,
+                                        k_env_step<false, false, true, true>, k_env_step<false, true, true, true>)
+                    : visited ? variant(a.T, k_env_step<true, false, false, true>, k_env_step<true, true, false, true>,
+                                        k_env_step<false, false, false, true>, k_env_step<false, true, false, true>)
+                              : variant(a.T, k_env_step<true, false, false, false>, k_env_step<true, true, false, false>,
+                                        k_env_step<false, false, false, false>, k_env_step<false, true, false, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
     hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
     launch_check("env step");
@@ -2371,10 +2375,12 @@ void prepare_env_launches(const TaskDev& T)
 {
     size_t lds = 0;
     waves_per_block(T, &lds);
-    for (const void* fn : {reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false>, k_env_step<true, true, false>,
-                                                                 k_env_step<false, false, false>, k_env_step<false, true, false>)),
-                           reinterpret_cast<const void*>(variant(T, k_env_step<true, false, true>, k_env_step<true, true, true>,
-                                                                 k_env_step<false, false, true>, k_env_step<false, true, true>)),
+    for (const void* fn : {reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false, false>, k_env_step<true, true, false, false>,
+                                                                 k_env_step<false, false, false, false>, k_env_step<false, true, false, false>)),
+                           reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false, true>, k_env_step<true, true, false, true>,
+                                                                 k_env_step<false, false, false, true>, k_env_step<false, true, false, true>)),
+                           reinterpret_cast<const void*>(variant(T, k_env_step<true, false, true, true>, k_env_step<true, true, true, true>,
+                                                                 k_env_step<false, false, true, true>, k_env_step<false, true, true, true>)),
                            reinterpret_cast<const void*>(variant(T, k_env_count<true, false, false>, k_env_count<true, true, false>,
                                                                  k_env_count<false, false, false>, k_env_count<false, true, false>)),
                            reinterpret_cast<const void*>(variant(T, k_env_count<true, false, true>, k_env_count<true, true, true>,
