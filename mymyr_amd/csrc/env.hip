@@ -1011,6 +1011,13 @@ __device__ __forceinline__ void build_view(const TaskDev& T, const auto& H, cons
 /// Loads row i (W words of `words`) into the wave's LDS row.
 __device__ __forceinline__ void load_row_lds(const TaskDev& T, const Lds& L, const u64* src, u32 lane)
 {
+    if (T.W <= kWave)  // one load per lane
+    {
+        if (lane < T.W)
+            L.row[lane] = src[lane];
+        wave_sync();
+        return;
+    }
     // up to 8 loads of a lane in flight before their LDS stores: a wide row arrives in about one load latency
     constexpr u32 kBatch = 8;
     for (u32 k0 = 0; k0 < T.W; k0 += kBatch * kWave)
@@ -1036,6 +1043,12 @@ __device__ __forceinline__ void load_row_lds(const TaskDev& T, const Lds& L, con
 /// dst[k] = k < n ? src[k] : 0 for k < z (global to global), up to 8 loads of a lane in flight.
 __device__ __forceinline__ void copy_words(u64* dst, const u64* src, u32 n, u32 z, u32 lane)
 {
+    if (z <= kWave)  // one word per lane
+    {
+        if (lane < z)
+            dst[lane] = lane < n ? src[lane] : 0;
+        return;
+    }
     constexpr u32 kBatch = 8;
     for (u32 k0 = 0; k0 < z; k0 += kBatch * kWave)
     {
