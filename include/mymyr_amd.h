@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 8
+#define MYA_ABI_VERSION 9
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -353,6 +353,36 @@ int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t w
  * plus an error for a task id outside the table. Synchronous. */
 int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids, uint64_t rows, uint32_t words,
                    const mya_expand_options* options, mya_expansion* out, void* stream);
+
+/* PaddedExpansion (include/mymyr/rl/expand.hpp:162-181) without numeric and derived words: the [rows, k] view of a flat
+ * expansion. Device arrays; a null array is not written. index [rows, k] (flat row, -1 padding), mask [rows, k],
+ * count [rows] (the true successor counts, which may exceed k), succ [rows, k, words] (zero padding), schema (-1),
+ * binding [rows, k, label_width] (-1), goal (0), succ_hash (0), noop (0), canonical (the flat index, -1). */
+typedef struct mya_padded_expansion
+{
+    uint32_t k;
+    uint32_t words;       /* at least the flat expansion's words when succ is written from flat succ rows */
+    uint32_t label_width; /* at least the flat label width when binding is written from a flat binding */
+    uint32_t reserved;
+    int32_t* index;
+    uint8_t* mask;
+    int32_t* count;
+    uint64_t* succ;
+    int32_t* schema;
+    int32_t* binding;
+    uint8_t* goal;
+    uint64_t* succ_hash;
+    uint8_t* noop;
+    int32_t* canonical;
+    int32_t overflow;     /* out: a count above k, a successor past the flat capacity, or the flat expansion's overflow */
+    int32_t reserved2;
+} mya_padded_expansion;
+
+/* rl::pad (include/mymyr/rl/expand.hpp:183-186, src/mymyr/rl/expand.cpp:799-873): scatters the flat expansion of `rows`
+ * states (device arrays of `flat` as mya_expand wrote them; offsets [rows + 1] required; capacity, generated, total,
+ * words_needed as returned) into `out`. An array of `out` whose flat source is null is filled with its padding.
+ * Synchronous: out->overflow is set on return. */
+int mya_pad(const mya_expansion* flat, uint64_t rows, mya_padded_expansion* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------- BrFS */
 

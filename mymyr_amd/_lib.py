@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 8  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 9  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -164,6 +164,27 @@ class Expansion(Structure):
     ]
 
 
+class PaddedExpansion(Structure):
+    _fields_ = [
+        ("k", c_uint32),
+        ("words", c_uint32),
+        ("label_width", c_uint32),
+        ("reserved", c_uint32),
+        ("index", c_void_p),
+        ("mask", c_void_p),
+        ("count", c_void_p),
+        ("succ", c_void_p),
+        ("schema", c_void_p),
+        ("binding", c_void_p),
+        ("goal", c_void_p),
+        ("succ_hash", c_void_p),
+        ("noop", c_void_p),
+        ("canonical", c_void_p),
+        ("overflow", c_int32),
+        ("reserved2", c_int32),
+    ]
+
+
 def _load() -> ctypes.CDLL:
     # torch-ROCm ships its own libamdhip64.so.7. Loaded first, the library would bind the system's copy and the
     # process would hold two HIP runtimes (torch's then finds no device); with torch imported first, the library
@@ -232,6 +253,7 @@ def _load() -> ctypes.CDLL:
         "mya_expand": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion), c_void_p]),
         "mya_env_expand": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion),
                                    c_void_p]),
+        "mya_pad": (c_int, [POINTER(Expansion), c_uint64, POINTER(PaddedExpansion), c_void_p]),
         "mya_successors": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     }
     for name, (res, args) in list(sigs.items()) + list(optional.items()):

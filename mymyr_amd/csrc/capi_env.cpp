@@ -880,4 +880,62 @@ int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids
     });
 }
 
+int mya_pad(const mya_expansion* flat, uint64_t rows, mya_padded_expansion* out, void* stream)
+{
+    return guarded([&] {
+        if (!flat || !out)
+            throw std::invalid_argument("mymyr_amd: pad: null argument");
+        if (!flat->offsets)
+            throw std::invalid_argument("mymyr: pad: the flat expansion has no offsets");
+        if (out->succ && flat->succ && out->words < flat->words)
+            throw std::invalid_argument("mymyr: pad: padded rows narrower than the flat rows");
+        if (out->binding && flat->binding && out->label_width < flat->label_width)
+            throw std::invalid_argument("mymyr: pad: padded label width below the flat label width");
+        constexpr u64 kMaxRows = (u64{1} << 31) - 1;
+        if (rows > kMaxRows || flat->capacity > kMaxRows)
+            throw std::invalid_argument("mymyr_amd: pad: more than 2^31 - 1 states or flat rows");
+        const bool flat_overflow = flat->generated > flat->capacity || flat->total > flat->capacity || flat->words_needed > flat->words;
+        u32* d_over = dev_alloc<u32>(1, "pad overflow");
+        struct Free
+        {
+            u32* p;
+            ~Free() { dev_free(p); }
+        } freeing{d_over};
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        launch_fill_u32(d_over, 1, 0, s);
+        PadArgs a{};
+        a.rows = rows;
+        a.capacity = flat->capacity;
+        a.offsets = flat->offsets;
+        a.succ = flat->succ;
+        a.flat_words = flat->words;
+        a.flat_label_width = flat->label_width;
+        a.schema = flat->schema;
+        a.binding = flat->binding;
+        a.goal = flat->goal;
+        a.succ_hash = flat->succ_hash;
+        a.noop = flat->noop;
+        a.index = flat->index;
+        a.k = out->k;
+        a.words = out->words;
+        a.label_width = out->label_width;
+        a.out_index = out->index;
+        a.mask = out->mask;
+        a.count = out->count;
+        a.out_succ = out->succ;
+        a.out_schema = out->schema;
+        a.out_binding = out->binding;
+        a.out_goal = out->goal;
+        a.out_succ_hash = out->succ_hash;
+        a.out_noop = out->noop;
+        a.canonical = out->canonical;
+        a.overflow = d_over;
+        launch_pad(a, s);
+        u32 h = 0;
+        hip_check(hipMemcpyAsync(&h, d_over, sizeof(h), hipMemcpyDeviceToHost, s), "pad overflow");
+        hip_check(hipStreamSynchronize(s), "pad");
+        out->overflow = flat_overflow || h ? 1 : 0;
+    });
+}
+
 }  // extern "C"

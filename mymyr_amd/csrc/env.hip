@@ -2195,6 +2195,73 @@ __global__ void k_kept_counts(const u32* counts, const u32* noops, u64 rows, u32
         kept[i] = noops[i] == counts[i] ? counts[i] : counts[i] - noops[i];
 }
 
+// Padded view of a flat expansion, one wave per row: the row's k slots are contiguous in every output, so the lanes
+// walk each output row (scalars over the k slots, succ over k * words, binding over k * label_width) with coalesced
+// stores, reading the flat rows b .. b + k - 1 that are also contiguous.
+__global__ __launch_bounds__(256) void k_pad(PadArgs a)
+{
+    const u32 lane = lane_id();
+    const u64 nw = u64{gridDim.x} * (blockDim.x / kWave);
+    const u32 K = a.k;
+    for (u64 i = static_cast<u64>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave; i < a.rows; i += nw)
+    {
+        const u64 b = static_cast<u64>(static_cast<i64>(a.offsets[i]));
+        const u64 c = static_cast<u64>(static_cast<i64>(a.offsets[i + 1])) - b;
+        // valid slots: k < min(c, K) with b + k < capacity
+        const u64 room = b < a.capacity ? a.capacity - b : 0;
+        const u32 n = static_cast<u32>(std::min<u64>(std::min<u64>(c, K), room));
+        if (lane == 0)
+        {
+            if (a.count)
+                a.count[i] = static_cast<i32>(c);
+            if (c > K || n < std::min<u64>(c, K))
+                atomicOr(a.overflow, 1u);
+        }
+        const u64 base = i * K;
+        for (u32 k = lane; k < K; k += kWave)
+        {
+            const bool valid = k < n;
+            const u64 j = b + k, at = base + k;
+            if (a.out_index)
+                a.out_index[at] = valid ? static_cast<i32>(j) : -1;
+            if (a.mask)
+                a.mask[at] = valid ? 1 : 0;
+            if (a.canonical)
+                a.canonical[at] = valid && a.index ? a.index[j] : -1;
+            if (a.out_schema)
+                a.out_schema[at] = valid && a.schema ? a.schema[j] : -1;
+            if (a.out_goal)
+                a.out_goal[at] = valid && a.goal ? a.goal[j] : 0;
+            if (a.out_succ_hash)
+                a.out_succ_hash[at] = valid && a.succ_hash ? a.succ_hash[j] : 0;
+            if (a.out_noop)
+                a.out_noop[at] = valid && a.noop ? a.noop[j] : 0;
+        }
+        if (a.out_succ)
+        {
+            const u32 W = a.words, FW = a.succ ? a.flat_words : 0;
+            u64* dst = a.out_succ + base * W;
+            const u64 total = u64{K} * W;
+            for (u64 t = lane; t < total; t += kWave)
+            {
+                const u32 k = static_cast<u32>(t / W), w = static_cast<u32>(t - u64{k} * W);
+                dst[t] = k < n && w < FW ? a.succ[(b + k) * FW + w] : 0;
+            }
+        }
+        if (a.out_binding)
+        {
+            const u32 L = a.label_width, FL = a.binding ? a.flat_label_width : 0;
+            i32* dst = a.out_binding + base * L;
+            const u64 total = u64{K} * L;
+            for (u64 t = lane; t < total; t += kWave)
+            {
+                const u32 k = static_cast<u32>(t / L), w = static_cast<u32>(t - u64{k} * L);
+                dst[t] = k < n && w < FL ? a.binding[(b + k) * FL + w] : -1;
+            }
+        }
+    }
+}
+
 // Successor listing: successor k of row i is pick(k) applied to a copy of the row.
 template<bool kStaged, bool kLevels>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, const u64* states, u64 rows, u32 words, u32 cap, i32* count,
@@ -2480,6 +2547,15 @@ void launch_kept_counts(const u32* counts, const u32* noops, u64 rows, u32* kept
         return;
     hipLaunchKernelGGL(k_kept_counts, dim3(blocks_for(rows, 256)), dim3(256), 0, stream, counts, noops, rows, kept);
     launch_check("expand kept counts");
+}
+
+void launch_pad(const PadArgs& a, hipStream_t stream)
+{
+    if (a.rows == 0)
+        return;
+    constexpr unsigned nw = 4;
+    hipLaunchKernelGGL(k_pad, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), 0, stream, a);
+    launch_check("pad");
 }
 
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream)

@@ -258,6 +258,39 @@ struct ExpandArgs
 void launch_expand(const ExpandArgs& a, hipStream_t stream);
 /// kept[i] = counts[i] - noops[i], or counts[i] when every successor of row i is a no-op.
 void launch_kept_counts(const u32* counts, const u32* noops, u64 rows, u32* kept, hipStream_t stream);
+
+/// A flat expansion (device arrays; offsets [rows + 1]) and its padded [rows, k] view (rl::pad,
+/// src/mymyr/rl/expand.cpp:799-873). Null destinations are not written; a null flat source pads its destination.
+struct PadArgs
+{
+    u64 rows;
+    u64 capacity;          // rows the flat arrays hold: successor j of a row is valid only below it
+    const i32* offsets;    // [rows + 1]
+    const u64* succ;       // [capacity, flat_words]
+    u32 flat_words;
+    u32 flat_label_width;
+    const i32* schema;
+    const i32* binding;    // [capacity, flat_label_width]
+    const u8* goal;
+    const u64* succ_hash;
+    const u8* noop;
+    const i32* index;      // positions in the parents' full successor order
+    u32 k;
+    u32 words;             // words of the padded succ rows (>= flat_words)
+    u32 label_width;       // columns of the padded binding (>= flat_label_width)
+    i32* out_index;        // [rows, k]: flat row, -1 padding
+    u8* mask;
+    i32* count;            // [rows]
+    u64* out_succ;         // [rows, k, words], zero padding
+    i32* out_schema;       // -1 padding
+    i32* out_binding;      // [rows, k, label_width], -1 padding
+    u8* out_goal;
+    u64* out_succ_hash;
+    u8* out_noop;
+    i32* canonical;        // flat index, -1 padding
+    u32* overflow;         // device word: set when a count exceeds k or a successor lies past capacity
+};
+void launch_pad(const PadArgs& a, hipStream_t stream);
 /// dst[i] = src[i] for i < n (offsets fit int32 after the caller's checks).
 void launch_offsets_i32(const u64* src, u64 n, i32* dst, hipStream_t stream);
 

@@ -444,8 +444,52 @@ def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tens
     kept = min(x.total, cap)
     out = {"succ": succ[:kept], "parent": parent[:kept], "schema": schema[:kept], "binding": binding[:kept],
            "offsets": offsets, "generated": x.generated, "total": x.total, "words_needed": x.words_needed,
-           "overflow": x.generated > cap or x.total > cap or x.words_needed > ow}
+           "overflow": x.generated > cap or x.total > cap or x.words_needed > ow, "capacity": cap}
     for name, t in (("goal", gl), ("succ_hash", sh), ("noop", np_), ("index", ix)):
         if t is not None:
             out[name] = t[:kept]
+    return out
+
+
+def auto_k(offsets: torch.Tensor) -> int:
+    """The k of pad(k=None): the next power of two at or above the largest successor count (at least 1)."""
+    m = int((offsets[1:] - offsets[:-1]).max()) if offsets.numel() > 1 else 0
+    return 1 << (max(m, 1) - 1).bit_length()
+
+
+def pad(flat: dict, k: int | None = None, *, words: int | None = None, label_width: int | None = None) -> dict:
+    """The padded [N, k] view of a flat expansion of expand() (rl::pad, src/mymyr/rl/expand.cpp:799-873), scattered on
+    the device: "index" [N, k] int32 (flat row, -1 padding), "mask" [N, k] uint8, "count" [N] int32 (true counts, which
+    may exceed k), "succ" [N, k, words] (zero padding), "schema" [N, k] (-1), "binding" [N, k, label_width] (-1), and
+    "goal", "succ_hash", "noop" (0 padding) and "canonical" (the flat "index", -1 padding) when the flat expansion has
+    them; "overflow" is set by a count above k, a successor past the flat capacity or the flat expansion's own
+    overflow. k None sizes k to the next power of two at or above the largest count."""
+    offsets = flat["offsets"]
+    rows = offsets.numel() - 1
+    if k is None:
+        k = auto_k(offsets)
+    if k < 0:
+        raise ValueError("mymyr: pad: k must be non-negative")
+    fw, fl = flat["succ"].shape[1], flat["binding"].shape[1]
+    ow = fw if words is None else words
+    L = fl if label_width is None else label_width
+    dev = offsets.device
+    out = {"index": torch.empty((rows, k), dtype=torch.int32, device=dev), "mask": torch.empty((rows, k), dtype=torch.uint8, device=dev),
+           "count": torch.empty(rows, dtype=torch.int32, device=dev), "succ": torch.empty((rows, k, ow), dtype=torch.int64, device=dev),
+           "schema": torch.empty((rows, k), dtype=torch.int32, device=dev),
+           "binding": torch.empty((rows, k, L), dtype=torch.int32, device=dev)}
+    for name, dt in (("goal", torch.uint8), ("succ_hash", torch.int64), ("noop", torch.uint8)):
+        if name in flat:
+            out[name] = torch.empty((rows, k), dtype=dt, device=dev)
+    if "index" in flat:
+        out["canonical"] = torch.empty((rows, k), dtype=torch.int32, device=dev)
+    x = _lib.Expansion(flat["capacity"], fw, fl, flat["succ"].data_ptr(), flat["parent"].data_ptr(), flat["schema"].data_ptr(),
+                       flat["binding"].data_ptr(), _p(flat.get("goal")), offsets.data_ptr(), _p(flat.get("succ_hash")),
+                       _p(flat.get("noop")), _p(flat.get("index")), flat["generated"], flat["total"], flat["words_needed"], 0)
+    p = _lib.PaddedExpansion(k, ow, L, 0, out["index"].data_ptr(), out["mask"].data_ptr(), out["count"].data_ptr(), out["succ"].data_ptr(),
+                             out["schema"].data_ptr(), out["binding"].data_ptr(), _p(out.get("goal")), _p(out.get("succ_hash")),
+                             _p(out.get("noop")), _p(out.get("canonical")), 0, 0)
+    check(lib.mya_pad(ctypes.byref(x), rows, ctypes.byref(p), _stream()))
+    out["k"] = k
+    out["overflow"] = bool(p.overflow)
     return out

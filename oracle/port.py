@@ -586,6 +586,39 @@ def table_expand(tasks: list, rows, task_ids, drop_noops: bool = False) -> dict:
     return out
 
 
+def pad(flat: dict, rows: int, k: int, words: int | None = None, label_width: int | None = None, capacity: int | None = None) -> dict:
+    """rl::pad (src/mymyr/rl/expand.cpp:799-873) of a flat expansion (offsets required) into [rows, k] arrays: slot k of
+    row i is flat row j = offsets[i] + k when k < count and j < capacity (index j, mask 1, the flat row's fields, and
+    canonical = flat index[j]); other slots hold the padding (-1 for index, schema, binding, canonical; 0 otherwise).
+    Overflow: the flat expansion's own, a count above k, or a successor past capacity."""
+    off = np.asarray(flat["offsets"], np.int64)
+    succ = np.asarray(flat["succ"], np.uint64)
+    FW, FL = succ.shape[1], np.asarray(flat["binding"]).shape[1]
+    W = FW if words is None else words
+    L = FL if label_width is None else label_width
+    cap = len(succ) if capacity is None else capacity
+    c = off[1:rows + 1] - off[:rows]
+    kk = np.arange(k)
+    j = off[:rows, None] + kk[None, :]
+    listed = kk[None, :] < c[:, None]
+    valid = listed & (j < cap)
+    flat_over = flat.get("generated", 0) > cap or flat.get("total", 0) > cap or flat.get("words_needed", 0) > FW
+    out = {"count": c.astype(np.int32), "index": np.where(valid, j, -1).astype(np.int32), "mask": valid.astype(np.uint8),
+           "overflow": bool(flat_over or (c > k).any() or (listed & ~valid).any())}
+    jv = j[valid]
+    out["succ"] = np.zeros((rows, k, W), np.uint64)
+    out["succ"][valid, :FW] = succ[jv]
+    out["binding"] = np.full((rows, k, L), -1, np.int32)
+    out["binding"][valid, :FL] = np.asarray(flat["binding"], np.int32)[jv]
+    for name, fill, dt in (("schema", -1, np.int32), ("goal", 0, np.uint8), ("succ_hash", 0, np.uint64), ("noop", 0, np.uint8),
+                           ("index", -1, np.int32)):
+        dst = "canonical" if name == "index" else name
+        out[dst] = np.full((rows, k), fill, dt)
+        if flat.get(name) is not None:
+            out[dst][valid] = np.asarray(flat[name], dt)[jv]
+    return out
+
+
 def mask_goal(row, gp, gn) -> bool:
     """The per-env goal test over the words of the masks (mask_goal, src/mymyr/rl/env.cpp:55-61)."""
     row, gp, gn = (np.asarray(x, np.uint64) for x in (row, gp, gn))

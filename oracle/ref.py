@@ -101,6 +101,7 @@ def lib() -> ctypes.CDLL:
             "mref_table_expand": (c_int64, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_uint32, c_int, c_uint64, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             POINTER(c_uint64)]),
+            "mref_table_pad": (c_int, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_uint32, c_int, c_uint32, c_uint32] + [c_void_p] * 10),
             "mref_instance_draw": (c_int32, [c_uint64, c_uint64, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32]),
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
             "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
@@ -311,6 +312,26 @@ def table_expand(tasks: list, states: np.ndarray, task_ids: np.ndarray, drop_noo
     for k in ("succ", "parent", "schema", "binding", "goal", "succ_hash", "noop", "index"):
         out[k] = out[k][:kept]
     out["generated"], out["total"] = int(g), kept
+    return out
+
+
+def table_pad(tasks: list, states: np.ndarray, task_ids: np.ndarray, k: int, drop_noops: bool = False) -> dict:
+    """rl::pad of the full flat expansion of a batch over TaskSuite::group(tasks) into [rows, k] arrays."""
+    arr = (c_void_p * len(tasks))(*[t._h.value for t in tasks])
+    rows, words = states.shape
+    L = max(1, max(t.label_width for t in tasks))
+    out = {"index": np.zeros((rows, k), np.int32), "mask": np.zeros((rows, k), np.uint8), "count": np.zeros(rows, np.int32),
+           "succ": np.zeros((rows, k, words), np.uint64), "schema": np.zeros((rows, k), np.int32),
+           "binding": np.zeros((rows, k, L), np.int32), "goal": np.zeros((rows, k), np.uint8), "succ_hash": np.zeros((rows, k), np.uint64),
+           "noop": np.zeros((rows, k), np.uint8), "canonical": np.zeros((rows, k), np.int32)}
+    states = np.ascontiguousarray(states, np.uint64)
+    ids = np.ascontiguousarray(task_ids, np.int32)
+    r = lib().mref_table_pad(arr, len(tasks), states.ctypes.data, ids.ctypes.data, rows, words, int(drop_noops), k, L,
+                             *[out[n].ctypes.data for n in ("index", "mask", "count", "succ", "schema", "binding", "goal", "succ_hash",
+                                                           "noop", "canonical")])
+    if r < 0:
+        raise RuntimeError(_err())
+    out["overflow"] = bool(r)
     return out
 
 

@@ -530,6 +530,70 @@ int64_t mref_table_expand(mref_task* const* tasks, uint32_t n, const uint64_t* s
         -1);
 }
 
+// rl::pad (include/mymyr/rl/expand.hpp:155-183) of the full flat expansion of a suite batch (rl::expand with capacity for
+// every successor, drop_noops as given) into [rows, k] arrays: index, mask, count [rows], succ [rows, k, words], schema,
+// binding [rows, k, label_width], goal, succ_hash, noop, canonical. Returns the overflow flag (or -1).
+int mref_table_pad(mref_task* const* tasks, uint32_t n, const uint64_t* states, const int32_t* task_ids, uint64_t rows, uint32_t words,
+                   int drop_noops, uint32_t k, uint32_t label_width, int32_t* index, uint8_t* mask, int32_t* count, uint64_t* succ,
+                   int32_t* schema, int32_t* binding, uint8_t* goal, uint64_t* succ_hash, uint8_t* noop, int32_t* canonical)
+{
+    return guarded(
+        [&]() -> int
+        {
+            std::vector<TaskPtr> v;
+            for (uint32_t i = 0; i < n; ++i)
+                v.push_back(tasks[i]->task);
+            const rl::TaskSuitePtr suite = rl::TaskSuite::group(std::move(v));
+            rl::StateBatchView in;
+            in.data = states;
+            in.rows = rows;
+            in.words = words;
+            rl::ExpandOptions o;
+            o.drop_noops = drop_noops != 0;
+            std::vector<int32_t> off(rows + 1);
+            rl::Expansion probe;
+            probe.offsets = off.data();
+            probe.words = words;
+            rl::expand(*suite, in, task_ids, probe, o);
+            const u64 cap = probe.generated;
+            std::vector<u64> fs(cap * words);
+            std::vector<int32_t> fp(cap), fsch(cap), fb(cap * label_width), fix(cap);
+            std::vector<u8> fg(cap), fn(cap);
+            std::vector<u64> fh(cap);
+            rl::Expansion flat;
+            flat.capacity = cap;
+            flat.words = words;
+            flat.label_width = label_width;
+            flat.succ = fs.data();
+            flat.parent = fp.data();
+            flat.schema = fsch.data();
+            flat.binding = fb.data();
+            flat.goal = fg.data();
+            flat.succ_hash = fh.data();
+            flat.noop = fn.data();
+            flat.index = fix.data();
+            flat.offsets = off.data();
+            rl::expand(*suite, in, task_ids, flat, o);
+            rl::PaddedExpansion out;
+            out.k = k;
+            out.index = index;
+            out.mask = mask;
+            out.count = count;
+            out.words = words;
+            out.succ = succ;
+            out.schema = schema;
+            out.label_width = label_width;
+            out.binding = binding;
+            out.goal = goal;
+            out.succ_hash = succ_hash;
+            out.noop = noop;
+            out.canonical = canonical;
+            rl::pad(flat, rows, out);
+            return out.overflow ? 1 : 0;
+        },
+        -1);
+}
+
 // rl::rng::instance_draw (include/mymyr/rl/rng.hpp:94-115)
 int32_t mref_instance_draw(uint64_t seed, uint64_t env, uint32_t reset_count, uint32_t instances, const uint32_t* thresholds,
                            const int32_t* indices, uint32_t m)

@@ -185,6 +185,23 @@ def expansion_digest(x: dict) -> str:
                          np.asarray(x["noop"], np.uint8), np.asarray(x["index"], np.int32), np.asarray(x["offsets"], np.int32))
 
 
+def pad_ks(offsets) -> tuple:
+    """The k a table expansion is padded to: the automatic one (the next power of two at or above the largest count)
+    and 3 (below most counts: overflow and cut rows)."""
+    off = np.asarray(offsets, np.int64)
+    m = int((off[1:] - off[:-1]).max()) if len(off) > 1 else 0
+    return (1 << (max(m, 1) - 1).bit_length(), 3)
+
+
+def padded_digest(p: dict) -> str:
+    """sha256 of a padded expansion's arrays in a fixed order and dtype (index, mask, count, succ, schema, binding, goal,
+    succ_hash, noop, canonical)."""
+    return arrays_digest(np.asarray(p["index"], np.int32), np.asarray(p["mask"], np.uint8), np.asarray(p["count"], np.int32),
+                         np.asarray(p["succ"], np.uint64), np.asarray(p["schema"], np.int32), np.asarray(p["binding"], np.int32),
+                         np.asarray(p["goal"], np.uint8), np.asarray(p["succ_hash"], np.uint64), np.asarray(p["noop"], np.uint8),
+                         np.asarray(p["canonical"], np.int32))
+
+
 def table_state(b: dict) -> list:
     """The batch arrays a table case's digests cover, in order (those the batch has)."""
     keys = ("states", "task_ids", "steps", "draws", "at_goal", "goal_pos", "goal_neg", "reset_counts", "visited", "visited_count",

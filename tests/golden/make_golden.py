@@ -230,8 +230,12 @@ def table_trajectory(case: str) -> dict:
             expansions = {}
             for drop in (False, True):
                 x = ref.table_expand(ts, b["states"], b["task_ids"], drop_noops=drop)
+                pads = {}
+                for kp in fx.pad_ks(x["offsets"]):
+                    p = ref.table_pad(ts, b["states"], b["task_ids"], kp, drop_noops=drop)
+                    pads[str(kp)] = {"digest": fx.padded_digest(p), "overflow": p["overflow"]}
                 expansions["drop" if drop else "all"] = {"digest": fx.expansion_digest(x), "generated": x["generated"],
-                                                         "total": x["total"], "noops": int(np.asarray(x["noop"]).sum())}
+                                                         "total": x["total"], "noops": int(np.asarray(x["noop"]).sum()), "pad": pads}
         for key, a in (("terminated", term), ("truncated", trunc), ("invalid", inv), ("goal", g)):
             totals[key] += int(a.sum())
         for i in range(I):

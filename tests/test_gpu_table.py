@@ -101,6 +101,12 @@ def replay(golden, case: str):
                        "goal": host(x["goal"]), "succ_hash": u64(x["succ_hash"]), "noop": host(x["noop"]), "index": host(x["index"]),
                        "offsets": host(x["offsets"])}
                 assert golden.expansion_digest(got) == want["digest"], f"{case}: expansion {key}"
+                # the padded view (rl::pad) on the device, at the automatic k and at k = 3
+                for kp in golden.pad_ks(got["offsets"]):
+                    p = rl.pad(x, kp)
+                    hp = {n: (u64(t) if n in ("succ", "succ_hash") else host(t)) for n, t in p.items() if isinstance(t, torch.Tensor)}
+                    assert golden.padded_digest(hp) == want["pad"][str(kp)]["digest"], f"{case}: pad {key} k={kp}"
+                    assert p["overflow"] == want["pad"][str(kp)]["overflow"], f"{case}: pad {key} k={kp} overflow"
     pool.check()
     return pool
 
@@ -189,3 +195,41 @@ def test_grouped_step_graph_replay(golden):
             assert torch.equal(getattr(a, key), ob[key]), f"replay {r}: {key}"
     a.check()
     b.check()
+
+
+@pytest.mark.parametrize("k", [0, 1, 3, None, 40])
+def test_pad_edges(golden, k):
+    """rl::pad on the device against the oracle's pad on the same flat expansion: a flat capacity below the total (slots
+    past it invalid, overflow), k = 0 and k above every count, wider padded rows and labels, and an empty batch."""
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+    from mymyr_amd import workloads
+
+    ts = [Task.from_text_file(p) for p in workloads.table_files("transport_table", golden.TASKS)]
+    pool = rl.DeviceEnvPool(ts[0], 37, seed=4, max_steps=50)
+    for _ in range(3):
+        pool.step()
+    print(f"pad edges: 37 transport rows, k={k}", flush=True)
+    full = rl.expand(ts[0], pool.states, hashes=True, noops=True, drop_noops=True)
+    for cap in (None, full["generated"] // 2):
+        x = full if cap is None else rl.expand(ts[0], pool.states, capacity=cap, hashes=True, noops=True, drop_noops=True)
+        hx = {n: (u64(t) if n in ("succ", "succ_hash") else host(t)) if isinstance(t, torch.Tensor) else t for n, t in x.items()}
+        kk = rl.auto_k(x["offsets"]) if k is None else k
+        p = rl.pad(x, k, words=ts[0].words + 2, label_width=x["binding"].shape[1] + 1)
+        want = port_pad(hx, 37, kk, ts[0].words + 2, x["binding"].shape[1] + 1, x["capacity"])
+        for n in ("index", "mask", "count", "succ", "schema", "binding", "succ_hash", "noop", "canonical"):
+            got = u64(p[n]) if n in ("succ", "succ_hash") else host(p[n])
+            assert np.array_equal(got, want[n]), f"cap={cap} k={kk}: {n}"
+        assert p["overflow"] == want["overflow"]
+        if cap is not None:
+            assert p["overflow"]
+    empty = rl.expand(ts[0], pool.states[:0])
+    e = rl.pad(empty, k)
+    assert e["count"].numel() == 0 and e["succ"].shape[0] == 0 and not e["overflow"]
+    pool.check()
+
+
+def port_pad(*a):
+    from oracle import port
+
+    return port.pad(*a)

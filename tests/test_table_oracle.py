@@ -76,6 +76,11 @@ def replay_oracle(golden, case: str) -> None:
                 want = g["expand"][key]
                 assert (x["generated"], x["total"]) == (want["generated"], want["total"]), f"{case}: expansion {key}"
                 assert golden.expansion_digest(x) == want["digest"], f"{case}: expansion {key}"
+                # rl::pad of that expansion (src/mymyr/rl/expand.cpp:799-873) at the automatic k and at k = 3
+                for kp in golden.pad_ks(x["offsets"]):
+                    p = port.pad(x, len(b["states"]), kp)
+                    assert golden.padded_digest(p) == want["pad"][str(kp)]["digest"], f"{case}: pad {key} k={kp}"
+                    assert p["overflow"] == want["pad"][str(kp)]["overflow"]
 
 
 @pytest.mark.parametrize("case", ["gridworld_ids", "gridworld_goals", "transport_ids", "gridworld_sampled", "transport_weighted",
@@ -174,3 +179,33 @@ def test_task_id_checks(golden):
          "at_goal": np.zeros(2, np.uint8), "count": np.zeros(2, np.int32), "task_ids": np.array([0, 3], np.int32)}
     with pytest.raises(ValueError, match="task id 3 of row 1 is outside the table's 3 instances"):
         e.reset(b)
+
+
+def test_pad_round_trip_and_cuts():
+    """pad against what it must be, independent of the digests: with k at least every count, the valid slots read back
+    in row order are the flat expansion; a smaller k keeps each row's first k successors and flags the overflow; a flat
+    capacity below the total invalidates exactly the slots at or past it."""
+    rng = np.random.default_rng(5)
+    counts = np.array([0, 3, 1, 5, 0, 2], np.int64)
+    off = np.concatenate([[0], np.cumsum(counts)])
+    M, W, L = int(off[-1]), 3, 2
+    flat = {"offsets": off, "succ": rng.integers(0, 2**63, (M, W), dtype=np.uint64), "binding": rng.integers(0, 9, (M, L), dtype=np.int32),
+            "schema": rng.integers(0, 4, M, dtype=np.int32), "goal": rng.integers(0, 2, M, dtype=np.uint8),
+            "succ_hash": rng.integers(0, 2**63, M, dtype=np.uint64), "noop": rng.integers(0, 2, M, dtype=np.uint8),
+            "index": rng.integers(0, 50, M, dtype=np.int32), "generated": M, "total": M}
+    p = port.pad(flat, len(counts), 8, words=W + 1, label_width=L + 1)
+    assert not p["overflow"] and p["count"].tolist() == counts.tolist()
+    m = p["mask"].astype(bool)
+    assert (p["index"][m] == np.arange(M)).all() and (p["index"][~m] == -1).all()
+    assert (p["succ"][m][:, :W] == flat["succ"]).all() and (p["succ"][..., W] == 0).all() and (p["succ"][~m] == 0).all()
+    assert (p["binding"][m][:, :L] == flat["binding"]).all() and (p["binding"][..., L] == -1).all()
+    for name, fill in (("schema", -1), ("goal", 0), ("succ_hash", 0), ("noop", 0)):
+        assert (p[name][m] == flat[name]).all() and (p[name][~m] == fill).all()
+    assert (p["canonical"][m] == flat["index"]).all() and (p["canonical"][~m] == -1).all()
+    # k = 2: rows with 3 and 5 successors are cut to their first two
+    q = port.pad(flat, len(counts), 2)
+    assert q["overflow"] and q["mask"].sum(1).tolist() == [0, 2, 1, 2, 0, 2]
+    assert q["index"][3].tolist() == [4, 5]
+    # capacity 5: flat rows 5.. are missing; row 3 (rows 4..8) keeps only row 4
+    c = port.pad({**flat, "succ": flat["succ"][:5], "binding": flat["binding"][:5]}, len(counts), 8, capacity=5)
+    assert c["overflow"] and c["index"][3].tolist() == [4] + [-1] * 7 and c["mask"][5].sum() == 0
