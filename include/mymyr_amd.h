@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 9
+#define MYA_ABI_VERSION 10
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -383,6 +383,15 @@ typedef struct mya_padded_expansion
  * words_needed as returned) into `out`. An array of `out` whose flat source is null is filled with its padding.
  * Synchronous: out->overflow is set on return. */
 int mya_pad(const mya_expansion* flat, uint64_t rows, mya_padded_expansion* out, void* stream);
+
+/* rl::visited_mask (include/mymyr/rl/visited.hpp:63-74; the device launch of include/mymyr/cuda/rl_ops.hpp:53-58, the
+ * torch op mymyr::visited_mask of python/mymyr/rl/torch/_ops.py:464-486): out[j] = whether succ_hash[j] is in the
+ * visited table of row parent[j], or of rows[parent[j]] when `rows` ([parents] entries) is given (without it parents
+ * = table_rows). table [table_rows, capacity] and count [table_rows] as an env's visited tables hold them; capacity a
+ * power of two in [2, 2^20]. -1 is padding; a parent or mapped row outside [-1, parents) or [-1, table_rows) reads as
+ * not visited. Device arrays; asynchronous on `stream`. */
+int mya_visited_mask(const uint64_t* table, const int32_t* count, uint64_t table_rows, uint32_t capacity, const uint64_t* succ_hash,
+                     const int32_t* parent, const int32_t* rows, uint64_t parents, uint64_t size, uint8_t* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------- BrFS */
 

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 9  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 10  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -253,6 +253,8 @@ def _load() -> ctypes.CDLL:
         "mya_expand": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion), c_void_p]),
         "mya_env_expand": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion),
                                    c_void_p]),
+        "mya_visited_mask": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_void_p,
+                                     c_void_p]),
         "mya_pad": (c_int, [POINTER(Expansion), c_uint64, POINTER(PaddedExpansion), c_void_p]),
         "mya_successors": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     }

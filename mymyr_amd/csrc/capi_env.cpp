@@ -938,4 +938,19 @@ int mya_pad(const mya_expansion* flat, uint64_t rows, mya_padded_expansion* out,
     });
 }
 
+int mya_visited_mask(const uint64_t* table, const int32_t* count, uint64_t table_rows, uint32_t capacity, const uint64_t* succ_hash,
+                     const int32_t* parent, const int32_t* rows, uint64_t parents, uint64_t size, uint8_t* out, void* stream)
+{
+    return guarded([&] {
+        if (capacity < 2 || capacity > (1u << 20) || (capacity & (capacity - 1)))
+            throw std::invalid_argument("mymyr: visited capacity must be a power of two in [2, 2^20]");
+        if (size && (!succ_hash || !parent || !out || (table_rows && (!table || !count))))
+            throw std::invalid_argument("mymyr: visited_mask requires table, count, succ_hash, parent and out arrays");
+        if (!rows)
+            parents = table_rows;
+        launch_visited_mask(table, count, table_rows, capacity, succ_hash, parent, rows, parents, size, out,
+                            static_cast<hipStream_t>(stream));
+    });
+}
+
 }  // extern "C"

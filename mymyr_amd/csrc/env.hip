@@ -1269,6 +1269,38 @@ __device__ __forceinline__ void visited_restart(u64* table, u32 H, i32* count, u
         *count = 1;
 }
 
+/// visited_mask (include/mymyr/rl/visited.hpp:63-74), one lane per successor: whether succ_hash[j] is in the table of
+/// row parent[j] (or rows[parent[j]]). Padding (-1) and parents or rows outside the tables read as not visited.
+__global__ __launch_bounds__(256) void k_visited_mask(const u64* table, const i32* count, u64 table_rows, u32 H, const u64* succ_hash,
+                                                      const i32* parent, const i32* rows, u64 parents, u64 size, u8* out)
+{
+    const u64 stride = u64{gridDim.x} * blockDim.x;
+    for (u64 j = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; j < size; j += stride)
+    {
+        const i32 p = parent[j];
+        bool hit = false;
+        const i32 row = p < 0 || static_cast<u64>(p) >= parents ? -1 : rows ? rows[p] : p;
+        if (row >= 0 && static_cast<u64>(row) < table_rows && count[row])
+        {
+            const u64 h = succ_hash[j], key = h ? h : kVisitedZero;
+            const u64* t = table + static_cast<u64>(row) * H;
+            u32 at = static_cast<u32>(key) & (H - 1);
+            for (u32 probe = 0; probe < H; ++probe, at = (at + 1) & (H - 1))
+            {
+                const u64 x = t[at];
+                if (x == key)
+                {
+                    hit = true;
+                    break;
+                }
+                if (!x)
+                    break;
+            }
+        }
+        out[j] = hit ? 1 : 0;
+    }
+}
+
 /// One environment's step (HostEnv::step_row_impl, src/mymyr/rl/env.cpp:351-528): row i of instance k, whose tables
 /// are T / H and whose wave region is L. An autoreset restarts the row in next_task_ids[i] when that names an instance
 /// (else in k), writing the new instance's initial state and goal masks over the words the row may have dirtied
@@ -2627,6 +2659,16 @@ void launch_visited_restart(const VisitedDev& v, const InstDev* inst, u32 instan
     hipLaunchKernelGGL(k_visited_restart, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 4), 16384))), dim3(256), 0, stream, v, inst,
                        instances, states, rows, words, mask, task_ids, current ? 1u : 0u);
     launch_check("visited restart");
+}
+
+void launch_visited_mask(const u64* table, const i32* count, u64 table_rows, u32 capacity, const u64* succ_hash, const i32* parent,
+                         const i32* rows, u64 parents, u64 size, u8* out, hipStream_t stream)
+{
+    if (size == 0)
+        return;
+    hipLaunchKernelGGL(k_visited_mask, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(size, 256), 16384))), dim3(256), 0, stream, table,
+                       count, table_rows, capacity, succ_hash, parent, rows, parents, size, out);
+    launch_check("visited mask");
 }
 
 void launch_env_reset_draw(const SamplerDev& sampler, const u64* seed, u64 first_env, u64 rows, const u8* mask, bool sample, i32* task_ids,

@@ -125,6 +125,12 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream);
 void launch_visited_restart(const VisitedDev& v, const InstDev* inst, u32 instances, const u64* states, u64 rows, u32 words,
                             const u8* mask, const i32* task_ids, bool current, hipStream_t stream);
 
+/// Membership of successor hashes in visited tables (rl::visited_mask): out[j] = succ_hash[j] is in table row
+/// parent[j] (or rows[parent[j]], rows having `parents` entries; without rows parents = table_rows); -1 and
+/// out-of-range parents or rows read as not visited.
+void launch_visited_mask(const u64* table, const i32* count, u64 table_rows, u32 capacity, const u64* succ_hash, const i32* parent,
+                         const i32* rows, u64 parents, u64 size, u8* out, hipStream_t stream);
+
 /// The arguments of a count over rows (refresh, the initial states, schema masks): count[i] (successors), goal[i],
 /// masks [rows, num_schemas] and the count cache [rows, num_schemas + 2] of the rows (each may be null); goal_pos /
 /// goal_neg [rows, words]: per-env goal masks (null: the instances' goal tests).

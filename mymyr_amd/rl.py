@@ -493,3 +493,29 @@ def pad(flat: dict, k: int | None = None, *, words: int | None = None, label_wid
     out["k"] = k
     out["overflow"] = bool(p.overflow)
     return out
+
+
+def visited_mask(table: torch.Tensor, count: torch.Tensor, succ_hash: torch.Tensor, parent: torch.Tensor,
+                 rows: torch.Tensor | None = None) -> torch.Tensor:
+    """Membership of successor hashes in visited tables (the torch op mymyr::visited_mask, rl::visited_mask of
+    include/mymyr/rl/visited.hpp:63-74) on the device, on the current stream without a host synchronization: out[j] =
+    succ_hash[j] is in the table (table [n, H] int64/uint64, count [n] int32) of row parent[j], or of rows[parent[j]];
+    -1 is padding, and parents or rows outside the tables read as not visited."""
+    if table.dim() != 2 or not table.is_cuda:
+        raise ValueError("mymyr: visited_mask: table must be a 2-d device tensor")
+    n, H = table.shape
+    tab = table.view(torch.int64) if table.dtype == torch.uint64 else table
+    h = succ_hash.view(torch.int64) if succ_hash.dtype == torch.uint64 else succ_hash
+    if tab.dtype != torch.int64 or h.dtype != torch.int64:
+        raise TypeError("mymyr: visited_mask: table and succ_hash must be int64 or uint64")
+    for name, t in (("count", count), ("parent", parent)) + ((("rows", rows),) if rows is not None else ()):
+        if t.dtype != torch.int32 or t.device != table.device:
+            raise TypeError(f"mymyr: visited_mask: {name} must be an int32 tensor on the table's device")
+    if count.shape != (n,) or parent.shape != h.shape or h.dim() != 1:
+        raise ValueError("mymyr: visited_mask: count [n], succ_hash [size] and parent [size] expected")
+    tab, h, count, parent = tab.contiguous(), h.contiguous(), count.contiguous(), parent.contiguous()
+    rows = None if rows is None else rows.contiguous()
+    out = torch.empty(h.shape, dtype=torch.bool, device=table.device)
+    check(lib.mya_visited_mask(tab.data_ptr(), count.data_ptr(), n, H, h.data_ptr(), parent.data_ptr(), _p(rows),
+                               0 if rows is None else rows.numel(), h.numel(), out.data_ptr(), _stream()))
+    return out

@@ -980,6 +980,39 @@ def visited_restart(table, h: int) -> int:
     return c
 
 
+def visited_contains(table, count: int, h: int) -> bool:
+    """visited_contains (include/mymyr/rl/visited.hpp:12-28): an empty table (count 0) holds nothing; otherwise probe
+    from key & (H - 1) until the key or an empty slot, at most H slots."""
+    if not count:
+        return False
+    H = len(table)
+    key = h if h else VISITED_ZERO
+    at = key & (H - 1)
+    for _ in range(H):
+        if int(table[at]) == key:
+            return True
+        if int(table[at]) == 0:
+            return False
+        at = (at + 1) & (H - 1)
+    return False
+
+
+def visited_mask(table, count, succ_hash, parent, rows=None) -> np.ndarray:
+    """rl::visited_mask (include/mymyr/rl/visited.hpp:63-74): out[j] = succ_hash[j] is in the table of row parent[j]
+    (or rows[parent[j]]); -1 is padding. Parents or mapped rows outside the tables read as not visited (the device
+    contract of the reference's launch_visited_mask, include/mymyr/cuda/rl_ops.hpp:53-58)."""
+    table = np.asarray(table, np.uint64)
+    n = len(table)
+    out = np.zeros(len(succ_hash), np.uint8)
+    for j, (h, p) in enumerate(zip(np.asarray(succ_hash, np.uint64), np.asarray(parent, np.int64))):
+        if p < 0 or (rows is not None and p >= len(rows)) or (rows is None and p >= n):
+            continue
+        row = int(rows[p]) if rows is not None else int(p)
+        if 0 <= row < n:
+            out[j] = visited_contains(table[row], int(count[row]), int(h))
+    return out
+
+
 def goal_masks_fit(gp, gn, fluent_slots: int) -> bool:
     """Whether goal masks set no bit at or past fluent_slots (rl::goal_masks_fit, include/mymyr/rl/goal_masks.hpp:8-21)."""
     for wi, (p, q) in enumerate(zip(np.asarray(gp, np.uint64), np.asarray(gn, np.uint64))):

@@ -102,6 +102,8 @@ def lib() -> ctypes.CDLL:
                                             c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             POINTER(c_uint64)]),
             "mref_table_pad": (c_int, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_uint32, c_int, c_uint32, c_uint32] + [c_void_p] * 10),
+            "mref_visited_insert": (None, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_void_p]),
+            "mref_visited_mask": (None, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
             "mref_instance_draw": (c_int32, [c_uint64, c_uint64, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32]),
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
             "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
@@ -332,6 +334,28 @@ def table_pad(tasks: list, states: np.ndarray, task_ids: np.ndarray, k: int, dro
     if r < 0:
         raise RuntimeError(_err())
     out["overflow"] = bool(r)
+    return out
+
+
+def visited_insert(table: np.ndarray, count: int, hashes) -> tuple[np.ndarray, int]:
+    """rl::visited_insert of each hash into one table (uint64 [H], written in place): (present flags, new count)."""
+    h = np.ascontiguousarray(hashes, np.uint64)
+    c = np.array([count], np.int32)
+    present = np.zeros(len(h), np.uint8)
+    lib().mref_visited_insert(table.ctypes.data, len(table), c.ctypes.data, h.ctypes.data, len(h), present.ctypes.data)
+    return present, int(c[0])
+
+
+def visited_mask(table: np.ndarray, count: np.ndarray, succ_hash, parent, rows=None) -> np.ndarray:
+    """rl::visited_mask: table uint64 [n, H], count int32 [n]."""
+    table = np.ascontiguousarray(table, np.uint64)
+    count = np.ascontiguousarray(count, np.int32)
+    h = np.ascontiguousarray(succ_hash, np.uint64)
+    p = np.ascontiguousarray(parent, np.int32)
+    r = None if rows is None else np.ascontiguousarray(rows, np.int32)
+    out = np.zeros(len(h), np.uint8)
+    lib().mref_visited_mask(table.ctypes.data, count.ctypes.data, table.shape[1], h.ctypes.data, p.ctypes.data,
+                            None if r is None else r.ctypes.data, len(h), out.ctypes.data)
     return out
 
 

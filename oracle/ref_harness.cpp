@@ -20,6 +20,7 @@
 #include "mymyr/rl/rng.hpp"
 #include "mymyr/rl/task_suite.hpp"
 #include "mymyr/rl/task_table.hpp"
+#include "mymyr/rl/visited.hpp"
 #include "mymyr/search/brfs.hpp"
 #include "mymyr/successor/successors.hpp"
 #include "mymyr/task/task.hpp"
@@ -592,6 +593,20 @@ int mref_table_pad(mref_task* const* tasks, uint32_t n, const uint64_t* states, 
             return out.overflow ? 1 : 0;
         },
         -1);
+}
+
+// rl::visited_insert (include/mymyr/rl/visited.hpp:31-52) of `n` hashes into one table of H slots: present[i] for each.
+void mref_visited_insert(uint64_t* table, uint32_t H, int32_t* count, const uint64_t* hashes, uint64_t n, uint8_t* present)
+{
+    for (uint64_t i = 0; i < n; ++i)
+        present[i] = rl::visited_insert(table, H, *count, hashes[i]) ? 1 : 0;
+}
+
+// rl::visited_mask (include/mymyr/rl/visited.hpp:63-74).
+void mref_visited_mask(const uint64_t* table, const int32_t* count, uint32_t H, const uint64_t* succ_hash, const int32_t* parent,
+                       const int32_t* rows, uint64_t size, uint8_t* out)
+{
+    rl::visited_mask(table, count, H, succ_hash, parent, rows, size, out);
 }
 
 // rl::rng::instance_draw (include/mymyr/rl/rng.hpp:94-115)

@@ -272,6 +272,36 @@ def make_env_table():
     dump("env_table.json", out)
 
 
+def make_visited_mask():
+    """Visited tables filled by the reference's visited_insert (empty, short, at the 3H/4 threshold, saturated, probe
+    chains of one home slot, hash 0 and its reserved key) and rl::visited_mask over queries with -1 padding, with and
+    without a row mapping."""
+    rng = np.random.default_rng(17)
+    H, n = 16, 7
+    table = np.zeros((n, H), np.uint64)
+    count = np.zeros(n, np.int32)
+    inserts = [[], [0, 5, 77], list(range(1, 13)), list(range(100, 120)), [16 * i + 3 for i in range(1, 9)],
+               [int(x) for x in rng.integers(1, 2**63, 6, dtype=np.uint64)], [0x9E3779B97F4A7C15, 0]]
+    present = []
+    for r, hs in enumerate(inserts):
+        hs = [int(h) for h in hs]
+        p, count[r] = ref.visited_insert(table[r], 0, np.array(hs, np.uint64))
+        present.append(p.tolist())
+        inserts[r] = hs
+    q = [0, 5, 77, 13, 6, 12, 100, 115, 119, 19, 35, 147, 3, 0x9E3779B97F4A7C15] + [h for hs in inserts for h in hs]
+    q += [int(x) for x in rng.integers(0, 2**63, 20, dtype=np.uint64)]
+    hashes = np.array(q * 2, np.uint64)
+    parent = rng.integers(-1, n, len(hashes)).astype(np.int32)
+    rows = np.array([3, -1, 0, 6, 2, 1, 5, 4, 4, -1], np.int32)
+    parent_m = rng.integers(-1, len(rows), len(hashes)).astype(np.int32)
+    out = {"H": H, "inserts": [[str(h) for h in hs] for hs in inserts], "present": present, "table": [[str(int(x)) for x in t] for t in table],
+           "count": count.tolist(), "hashes": [str(int(h)) for h in hashes], "parent": parent.tolist(),
+           "mask": ref.visited_mask(table, count, hashes, parent).tolist(), "rows": rows.tolist(), "parent_mapped": parent_m.tolist(),
+           "mask_mapped": ref.visited_mask(table, count, hashes, parent_m, rows).tolist()}
+    print("visited_mask", sum(out["mask"]), sum(out["mask_mapped"]), count.tolist(), flush=True)
+    dump("visited_mask.json", out)
+
+
 def brfs_record(name, atoms="auto", **kw):
     t = ref.RefTask(fx.task_path(name), atoms)
     r = ref.brfs(t, **kw)
@@ -304,7 +334,7 @@ def main():
     a = ap.parse_args()
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
-             "env_small": make_env_small, "env_table": make_env_table, "brfs": lambda: make_brfs(a.quick)}
+             "env_small": make_env_small, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

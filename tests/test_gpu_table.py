@@ -233,3 +233,55 @@ def port_pad(*a):
     from oracle import port
 
     return port.pad(*a)
+
+
+def test_visited_mask_matches_reference(golden):
+    """rl.visited_mask on the device against the compiled reference's rl::visited_mask on the same tables and queries
+    (tests/golden/visited_mask.json), with and without a row mapping."""
+    from mymyr_amd import rl
+
+    g = golden.load("visited_mask.json")
+    u = lambda xs: torch.from_numpy(np.array([int(x) for x in xs], np.uint64).view(np.int64)).cuda()
+    table = torch.stack([u(t) for t in g["table"]])
+    count = torch.tensor(g["count"], dtype=torch.int32, device="cuda")
+    hashes = u(g["hashes"])
+    print(f"visited mask: {len(g['hashes'])} queries over {len(g['count'])} tables", flush=True)
+    got = rl.visited_mask(table, count, hashes, torch.tensor(g["parent"], dtype=torch.int32, device="cuda"))
+    assert host(got).astype(np.uint8).tolist() == g["mask"]
+    got = rl.visited_mask(table, count, hashes, torch.tensor(g["parent_mapped"], dtype=torch.int32, device="cuda"),
+                          torch.tensor(g["rows"], dtype=torch.int32, device="cuda"))
+    assert host(got).astype(np.uint8).tolist() == g["mask_mapped"]
+
+
+def test_visited_mask_of_an_expansion(golden):
+    """The successors of an env batch checked against the rows' own visited tables after a few steps (the novelty test
+    of an expansion), against the oracle's visited_mask; out-of-range parents and mapped rows read as not visited."""
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+    from mymyr_amd import workloads
+    from oracle import port
+
+    ts = [Task.from_text_file(p) for p in workloads.table_files("gridworld_table", golden.TASKS)]
+    n = 300
+    pool = rl.DeviceEnvPool(ts[0], n, seed=9, max_steps=40, track_visited=64)
+    for _ in range(12):
+        pool.step()
+    print(f"visited mask of an expansion: {n} gridworld rows", flush=True)
+    x = rl.expand(ts[0], pool.states, hashes=True)
+    tab, cnt = u64(pool.visited), host(pool.visited_count)
+    sh, par = u64(x["succ_hash"]), host(x["parent"])
+    got = host(rl.visited_mask(pool.visited, pool.visited_count, x["succ_hash"], x["parent"]))
+    want = port.visited_mask(tab, cnt, sh, par)
+    assert np.array_equal(got.astype(np.uint8), want) and 0 < want.sum() < len(want)
+    # padding, parents past the tables, and a row mapping with -1 and out-of-range rows
+    rng = np.random.default_rng(1)
+    p2 = rng.integers(-1, n + 5, len(sh)).astype(np.int32)
+    got = host(rl.visited_mask(pool.visited, pool.visited_count, x["succ_hash"], torch.from_numpy(p2).cuda()))
+    assert np.array_equal(got.astype(np.uint8), port.visited_mask(tab, cnt, sh, p2))
+    rows = rng.integers(-1, n + 3, 50).astype(np.int32)
+    p3 = rng.integers(-1, 55, len(sh)).astype(np.int32)
+    got = host(rl.visited_mask(pool.visited, pool.visited_count, x["succ_hash"], torch.from_numpy(p3).cuda(), torch.from_numpy(rows).cuda()))
+    assert np.array_equal(got.astype(np.uint8), port.visited_mask(tab, cnt, sh, p3, rows))
+    with pytest.raises(RuntimeError, match="power of two"):
+        rl.visited_mask(pool.visited[:, :48], pool.visited_count, x["succ_hash"], x["parent"])
+    pool.check()
