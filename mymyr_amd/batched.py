@@ -161,6 +161,7 @@ class BatchedEnv:
         I = len(self.tasks)
         self.multi = I > 1
         self.sampler = _instance_sampler(sampler, I, default_uniform=task_ids is None)
+        self.launch = "widest"
         self._seed = int(seed)
         cfg = _lib.EnvConfig(seed, max_steps or 0, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
                              int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning), 0)
@@ -366,6 +367,15 @@ class BatchedEnv:
                 next_task_ids: Optional[Tensor] = None, final: bool = False, pool: Any = None) -> "CapturedRollout":
         """``steps`` steps (actions from ``policy(self)``, or the random policy) captured into one HIP graph."""
         return CapturedRollout(self, steps, policy, next_task_ids=next_task_ids, final=final, pool=pool)
+
+    def set_launch(self, launch: str) -> None:
+        """'widest' or 'per_bucket' (BatchedEnv.set_launch, python/mymyr/rl/torch/_batched.py:573-575): how the
+        reference's device env launches over a table's row-width buckets. The HIP env picks its launch shape itself
+        (rows grouped by instance on the device, one launch per instance of a table of at most 16 instances, else one
+        per kernel variant); the outputs do not depend on it, so either value is accepted and recorded."""
+        if launch not in ("widest", "per_bucket"):
+            raise ValueError("mymyr: launch must be 'widest' or 'per_bucket'")
+        self.launch = launch
 
     def check_errors(self) -> None:
         """Waits for the device work and raises if a step met task ids outside the table, goal masks outside the

@@ -173,3 +173,6 @@ def test_batched_env_argument_errors(golden):
     assert env.sampler is None and int(env.task_ids.sum()) == 0
     with pytest.raises(TypeError):
         env.step(torch.zeros(8, dtype=torch.float32))
+    env.set_launch("per_bucket")
+    with pytest.raises(ValueError):
+        env.set_launch("fastest")
