@@ -29,6 +29,7 @@ class EnvConfig(Structure):
         ("autoreset", c_int32),
         ("canonical_order", c_int32),
         ("witness_pruning", c_int32),
+        ("label_actions", c_int32),
     ]
 
 
@@ -97,6 +98,8 @@ def lib() -> ctypes.CDLL:
             "mref_table_env_reset": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int]),
             "mref_table_env_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
+            "mref_table_env_step_labels": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                   c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p]),
             "mref_table_env_clear_visited": (c_int, [c_void_p, c_void_p, c_void_p]),
             "mref_table_expand": (c_int64, [c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_uint32, c_int, c_uint64, c_void_p,
                                             c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
@@ -235,10 +238,10 @@ class RefTableEnv:
     with an instance sampler when `sampler` = (instances, thresholds, indices) is given (empty arrays: uniform)."""
 
     def __init__(self, tasks: list, seed=0, max_steps=0, step_reward=0.0, goal_reward=1.0, dead_end_reward=0.0,
-                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None, suite=False):
+                 dead_end="no_successors", dead_end_terminal=True, autoreset=True, sampler=None, suite=False, labels=False):
         self.tasks = tasks
         self.cfg = EnvConfig(seed, max_steps, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
-                             int(dead_end_terminal), int(autoreset), 1, 0)
+                             int(dead_end_terminal), int(autoreset), 1, 0, int(labels))
         arr = (c_void_p * len(tasks))(*[t._h.value for t in tasks])
         inst, thr, idx = sampler if sampler is not None else (0, [], [])
         self._thr = np.asarray(thr, np.uint32)
@@ -271,10 +274,18 @@ class RefTableEnv:
             raise RuntimeError(_err())
 
     def step(self, b: dict, first_env=0, actions=None, next_task_ids=None, reward=None, terminated=None, truncated=None, count=None,
-             schema=None, binding=None, goal=None, invalid=None, final_states=None, revisited=None):
+             schema=None, binding=None, goal=None, invalid=None, final_states=None, revisited=None, labels=None):
         tb = self.batch(b, first_env)
         lw = 0 if binding is None else binding.shape[1]
         fw = 0 if final_states is None else final_states.shape[1]
+        if labels is not None:
+            ls, lb = np.ascontiguousarray(labels[0], np.int32), np.ascontiguousarray(labels[1], np.int32)
+            rc = lib().mref_table_env_step_labels(self._h, ctypes.byref(tb), ls.ctypes.data, lb.ctypes.data, lb.shape[1], _p(next_task_ids),
+                                                  _p(reward), _p(terminated), _p(truncated), _p(count), _p(schema), _p(binding), lw,
+                                                  _p(goal), _p(invalid), _p(final_states), fw, _p(revisited))
+            if rc != 0:
+                raise RuntimeError(_err())
+            return
         rc = lib().mref_table_env_step(self._h, ctypes.byref(tb), _p(actions), _p(next_task_ids), _p(reward), _p(terminated),
                                        _p(truncated), _p(count), _p(schema), _p(binding), lw, _p(goal), _p(invalid), _p(final_states), fw,
                                        _p(revisited))

@@ -85,6 +85,7 @@ struct mref_env_config
     int32_t autoreset;
     int32_t canonical_order;
     int32_t witness_pruning;
+    int32_t label_actions;  // ActionSpace::Label
 };
 
 struct mref_brfs_options
@@ -277,6 +278,7 @@ static rl::EnvConfig env_config(const mref_env_config* c)
     e.autoreset = c->autoreset != 0;
     e.canonical_order = c->canonical_order != 0;
     e.witness_pruning = c->witness_pruning != 0;
+    e.actions = c->label_actions ? rl::ActionSpace::Label : rl::ActionSpace::Index;
     return e;
 }
 
@@ -485,6 +487,37 @@ int mref_table_env_step(mref_env* e, const mref_table_batch* t, const int64_t* a
             rl::Actions a;
             a.v64 = actions;
             e->env->step(b, o, a, next_task_ids, nullptr);
+            return 0;
+        },
+        -1);
+}
+
+// HostEnv::step with explicit labels (include/mymyr/rl/env.hpp:216-219) on an env created with label actions: schema
+// [rows], binding [rows, stride].
+int mref_table_env_step_labels(mref_env* e, const mref_table_batch* t, const int32_t* label_schema, const int32_t* label_binding,
+                               uint32_t stride, const int32_t* next_task_ids, float* reward, uint8_t* terminated, uint8_t* truncated,
+                               int32_t* count, int32_t* schema, int32_t* binding, uint32_t label_width, uint8_t* goal, uint8_t* invalid,
+                               uint64_t* final_states, uint32_t final_words, uint8_t* revisited)
+{
+    return guarded(
+        [&]() -> int
+        {
+            rl::EnvBatch b = table_batch(t);
+            rl::StepOutputs o;
+            o.reward = reward;
+            o.terminated = terminated;
+            o.truncated = truncated;
+            o.count = count;
+            o.schema = schema;
+            o.binding = binding;
+            o.label_width = label_width;
+            o.goal = goal;
+            o.invalid = invalid;
+            o.final_states = final_states;
+            o.words = final_words;
+            o.revisited = revisited;
+            rl::Labels l{label_schema, label_binding, stride};
+            e->env->step(b, o, l, next_task_ids, nullptr);
             return 0;
         },
         -1);
