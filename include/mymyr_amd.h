@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 10
+#define MYA_ABI_VERSION 11
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -392,6 +392,15 @@ int mya_pad(const mya_expansion* flat, uint64_t rows, mya_padded_expansion* out,
  * not visited. Device arrays; asynchronous on `stream`. */
 int mya_visited_mask(const uint64_t* table, const int32_t* count, uint64_t table_rows, uint32_t capacity, const uint64_t* succ_hash,
                      const int32_t* parent, const int32_t* rows, uint64_t parents, uint64_t size, uint8_t* out, void* stream);
+
+/* The index form of label actions (HostEnv::step with Labels, src/mymyr/rl/env.cpp:376-426): actions[i] = the position
+ * of row i's label (label_schema [rows], label_binding [rows, stride], stride >= label_width; columns past the
+ * schema's arity are ignored) in the row's successors of a flat expansion in canonical order (offsets [rows + 1],
+ * schema, binding [., label_width] as mya_env_expand writes them without drop_noops), or -1 when the label is not
+ * applicable. An env step with these actions is the reference's label step, its counts clamped to 0/1. Device arrays;
+ * asynchronous on `stream`. */
+int mya_label_actions(const int32_t* offsets, const int32_t* schema, const int32_t* binding, uint32_t label_width, uint64_t rows,
+                      const int32_t* label_schema, const int32_t* label_binding, uint32_t stride, int64_t* actions, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------- BrFS */
 

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 10  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 11  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -255,6 +255,7 @@ def _load() -> ctypes.CDLL:
                                    c_void_p]),
         "mya_visited_mask": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_void_p,
                                      c_void_p]),
+        "mya_label_actions": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint64, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
         "mya_pad": (c_int, [POINTER(Expansion), c_uint64, POINTER(PaddedExpansion), c_void_p]),
         "mya_successors": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     }

@@ -9,8 +9,9 @@ The environments' tensors are ``states`` [N, row_words] int64 (the widest instan
 addresses: loops of steps capture into HIP graphs (:meth:`BatchedEnv.capture`, or ``torch.cuda.graph`` around the
 calls). Writing ``states``, ``task_ids`` or the goal masks directly needs :meth:`BatchedEnv.refresh`.
 
-The reference's observation encoders and label actions are not part of this path; asking for them raises
-NotImplementedError. Visited tables (``track_visited``) are kept on the device: ``visited`` [N, H] int64, ``visited_count``
+The reference's observation encoders are not part of this path; asking for them raises NotImplementedError. Label
+actions (``actions="label"``, ``step((schema, binding))``) run as the index step at each label's position in the
+row's canonical successor order, found in a flat expansion of the current states; counts are 0/1 in label mode. Visited tables (``track_visited``) are kept on the device: ``visited`` [N, H] int64, ``visited_count``
 [N] int32, ``visited_status`` [1] int32.
 """
 
@@ -23,7 +24,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, rl
 from ._lib import check, lib
 from .rl import InstanceSampler, TaskSuite, TaskTable, visited_capacity
 from .task import Task
@@ -140,8 +141,10 @@ class BatchedEnv:
                  path: str = "auto", threads: int = 1, **unsupported: Any) -> None:
         if observation is not None or unsupported:
             raise NotImplementedError("mymyr_amd: BatchedEnv: observation encoders are not part of the device expansion path")
-        if actions != "index":
-            raise NotImplementedError("mymyr_amd: BatchedEnv: label actions are not part of the device expansion path")
+        if actions not in ("index", "label"):
+            raise ValueError("mymyr: actions must be 'index' or 'label'")
+        self.actions = actions
+        self._expander = None
         if path not in ("auto", "fast"):
             raise ValueError("mymyr_amd: BatchedEnv runs the device's fast path only")
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
@@ -149,6 +152,7 @@ class BatchedEnv:
         if dead_end not in ("no_successors", "none"):
             raise ValueError("mymyr: dead_end must be 'no_successors' or 'none'")
         suite = isinstance(table, TaskSuite)
+        self._suite = suite
         if isinstance(table, TaskTable):
             table = table.tasks
         self.tasks = list(table) if isinstance(table, (list, tuple)) else [table]
@@ -288,11 +292,15 @@ class BatchedEnv:
             self.goal_neg.copy_(_where(mask, goal_neg.to(self.goal_neg).expand_as(self.goal_neg), self.goal_neg))
         m8 = None if mask is None else mask.view(torch.uint8)
         check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(m8), self.count.data_ptr(), int(keep), int(sample), _stream()))
+        if getattr(self, "actions", "index") == "label":
+            self.count.clamp_(max=1)
         return self.count
 
     def refresh(self) -> Tensor:
         """Recomputes the count cache, ``count`` and ``at_goal`` after the caller wrote states, task ids or goal masks."""
         check(lib.mya_env_refresh(self._h, ctypes.byref(self._batch), self.count.data_ptr(), _stream()))
+        if self.actions == "label":
+            self.count.clamp_(max=1)
         return self.count
 
     def _outputs(self, final: bool) -> list[Tensor]:
@@ -303,11 +311,28 @@ class BatchedEnv:
                 torch.empty(n, dtype=torch.bool, device=d), torch.empty(n, dtype=torch.int32, device=d),
                 torch.empty((n, self._label_width), dtype=torch.int32, device=d), fs]
 
+    def _label_action(self, action: Any) -> Tensor:
+        """Label mode: each row's (schema, binding) as its position in the row's canonical successor order (-1: not
+        applicable), found in the flat expansion of the current states; the index step with these positions is the
+        reference's label step (its counts clamped to 0/1)."""
+        if not isinstance(action, tuple) or len(action) != 2:
+            raise ValueError("mymyr: label mode requires action=(schema, binding); the random policy is unavailable")
+        schema, binding = action
+        if not isinstance(schema, Tensor) or not isinstance(binding, Tensor):
+            raise ValueError("mymyr: label actions require schema and binding tensors")
+        if self._expander is None:
+            self._expander = (rl.TaskSuite(self.tasks) if self._suite else rl.TaskTable(self.tasks)) if self.multi else self.tasks[0]
+        ids = self.task_ids if self.multi else None
+        flat = rl.expand(self._expander, self.states, task_ids=ids)
+        return rl.label_actions(flat, schema.to(self.device, torch.int32), binding.to(self.device, torch.int32))
+
     def _action(self, action: Any) -> Optional[Tensor]:
+        if self.actions == "label":
+            return self._label_action(action)
         if action is None:
             return None
         if isinstance(action, tuple):
-            raise NotImplementedError("mymyr_amd: BatchedEnv: label actions are not part of the device expansion path")
+            raise ValueError("mymyr: label actions require actions='label'")
         a = torch.as_tensor(action)
         if a.dtype.is_floating_point or a.dtype.is_complex or a.dtype == torch.bool:
             raise TypeError(f"mymyr: actions must be integer successor indices, not {a.dtype}")
@@ -334,6 +359,8 @@ class BatchedEnv:
         outs = self._outputs(final)
         revisited = torch.zeros(self.num_envs, dtype=torch.bool, device=self.device)
         self._step_raw(outs, self._action(action), self._next_ids(next_task_ids), final, revisited if self.visited_capacity else None)
+        if self.actions == "label":
+            self.count.clamp_(max=1)  # ActionSpace::Label: whether an applicable action exists
         obs = self.observation(copy=copy)
         return StepResult(*outs, obs.count, obs.states, obs.task_ids, obs.goal_pos, obs.goal_neg, obs.at_goal, revisited=revisited)
 
@@ -348,6 +375,8 @@ class BatchedEnv:
 
     def random_actions(self, max_actions: Optional[int] = None) -> Tensor:
         """The successors ``step(None)`` would take now, among the first ``max_actions`` (None: all); 0 where none."""
+        if self.actions == "label":
+            raise ValueError("mymyr: random_actions is unavailable in label mode")
         if max_actions is not None and int(max_actions) < 1:
             raise ValueError("mymyr: max_actions must be None or positive")
         out = torch.empty(self.num_envs, dtype=torch.int64, device=self.device)
@@ -366,6 +395,8 @@ class BatchedEnv:
     def capture(self, steps: int, policy: Optional[Callable[["BatchedEnv"], Tensor]] = None, *,
                 next_task_ids: Optional[Tensor] = None, final: bool = False, pool: Any = None) -> "CapturedRollout":
         """``steps`` steps (actions from ``policy(self)``, or the random policy) captured into one HIP graph."""
+        if self.actions == "label":
+            raise ValueError("mymyr_amd: label steps expand on the host's schedule (a synchronous expansion) and are not captured")
         return CapturedRollout(self, steps, policy, next_task_ids=next_task_ids, final=final, pool=pool)
 
     def set_launch(self, launch: str) -> None:

@@ -953,4 +953,18 @@ int mya_visited_mask(const uint64_t* table, const int32_t* count, uint64_t table
     });
 }
 
+int mya_label_actions(const int32_t* offsets, const int32_t* schema, const int32_t* binding, uint32_t label_width, uint64_t rows,
+                      const int32_t* label_schema, const int32_t* label_binding, uint32_t stride, int64_t* actions, void* stream)
+{
+    return guarded([&] {
+        if (stride < label_width)
+            throw std::invalid_argument("mymyr: env: label stride " + std::to_string(stride) + " is below the label width " +
+                                        std::to_string(label_width));
+        if (rows && (!offsets || !label_schema || !actions || (label_width && !label_binding)))
+            throw std::invalid_argument("mymyr: env: label mode requires explicit labels");
+        launch_label_actions(offsets, schema, binding, label_width, rows, label_schema, label_binding, stride, actions,
+                             static_cast<hipStream_t>(stream));
+    });
+}
+
 }  // extern "C"

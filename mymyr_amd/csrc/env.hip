@@ -2294,6 +2294,34 @@ __global__ __launch_bounds__(256) void k_pad(PadArgs a)
     }
 }
 
+// The position of each row's label in its flat expansion (canonical order): one lane per row scans the row's successors
+// for the label's schema and the objects of its binding (the flat binding's -1 columns lie past the arity and match
+// anything); -1 when no successor carries the label.
+__global__ __launch_bounds__(256) void k_label_actions(const i32* offsets, const i32* schema, const i32* binding, u32 L, u64 rows,
+                                                       const i32* label_schema, const i32* label_binding, u32 stride, i64* actions)
+{
+    const u64 step = u64{gridDim.x} * blockDim.x;
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows; i += step)
+    {
+        const i64 b = offsets[i], e = offsets[i + 1];
+        const i32 ls = label_schema[i];
+        const i32* lb = label_binding + i * stride;
+        i64 act = -1;
+        for (i64 j = b; j < e && act < 0; ++j)
+        {
+            if (schema[j] != ls)
+                continue;
+            const i32* fb = binding + static_cast<u64>(j) * L;
+            bool same = true;
+            for (u32 k = 0; k < L && same; ++k)
+                same = fb[k] < 0 || fb[k] == lb[k];
+            if (same)
+                act = j - b;
+        }
+        actions[i] = act;
+    }
+}
+
 // Successor listing: successor k of row i is pick(k) applied to a copy of the row.
 template<bool kStaged, bool kLevels>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, const u64* states, u64 rows, u32 words, u32 cap, i32* count,
@@ -2588,6 +2616,16 @@ void launch_pad(const PadArgs& a, hipStream_t stream)
     constexpr unsigned nw = 4;
     hipLaunchKernelGGL(k_pad, dim3(grid_for(a.rows, nw)), dim3(nw * kWave), 0, stream, a);
     launch_check("pad");
+}
+
+void launch_label_actions(const i32* offsets, const i32* schema, const i32* binding, u32 L, u64 rows, const i32* label_schema,
+                          const i32* label_binding, u32 stride, i64* actions, hipStream_t stream)
+{
+    if (rows == 0)
+        return;
+    hipLaunchKernelGGL(k_label_actions, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(rows, 256), 16384))), dim3(256), 0, stream, offsets,
+                       schema, binding, L, rows, label_schema, label_binding, stride, actions);
+    launch_check("label actions");
 }
 
 void launch_encode_atoms(const u64* states, u64 rows, u32 words, u32 W, i32* out, u32 max_atoms, u32* status, hipStream_t stream)

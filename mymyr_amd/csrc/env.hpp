@@ -297,6 +297,10 @@ struct PadArgs
     u32* overflow;         // device word: set when a count exceeds k or a successor lies past capacity
 };
 void launch_pad(const PadArgs& a, hipStream_t stream);
+/// actions[i] = the position of row i's label (label_schema[i], label_binding [rows, stride]) among its successors of a
+/// flat expansion (offsets [rows + 1], schema, binding [., L]), or -1 when no successor carries it.
+void launch_label_actions(const i32* offsets, const i32* schema, const i32* binding, u32 L, u64 rows, const i32* label_schema,
+                          const i32* label_binding, u32 stride, i64* actions, hipStream_t stream);
 /// dst[i] = src[i] for i < n (offsets fit int32 after the caller's checks).
 void launch_offsets_i32(const u64* src, u64 n, i32* dst, hipStream_t stream);
 

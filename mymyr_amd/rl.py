@@ -519,3 +519,22 @@ def visited_mask(table: torch.Tensor, count: torch.Tensor, succ_hash: torch.Tens
     check(lib.mya_visited_mask(tab.data_ptr(), count.data_ptr(), n, H, h.data_ptr(), parent.data_ptr(), _p(rows),
                                0 if rows is None else rows.numel(), h.numel(), out.data_ptr(), _stream()))
     return out
+
+
+def label_actions(flat: dict, schema: torch.Tensor, binding: torch.Tensor) -> torch.Tensor:
+    """The index form of label actions (HostEnv::step with Labels, src/mymyr/rl/env.cpp:376-426) on the device: int64
+    [N], the position of row i's label (schema [N] int32, binding [N, L'] int32 with L' at least the expansion's label
+    width; columns past the schema's arity are ignored) among its successors of the flat expansion `flat` (expand()
+    without drop_noops and without a capacity limit), or -1 when the label is not applicable."""
+    offsets = flat["offsets"]
+    rows = offsets.numel() - 1
+    L = flat["binding"].shape[1]
+    if schema.shape != (rows,) or schema.dtype != torch.int32 or binding.dtype != torch.int32 or binding.dim() != 2 or binding.shape[0] != rows:
+        raise ValueError(f"mymyr: label actions require schema int32 [{rows}] and binding int32 [{rows}, L] tensors")
+    if flat["overflow"] or "index" in flat:
+        raise ValueError("mymyr: label actions need a complete expansion without dropped no-ops")
+    schema, binding = schema.contiguous(), binding.contiguous()
+    out = torch.empty(rows, dtype=torch.int64, device=offsets.device)
+    check(lib.mya_label_actions(offsets.data_ptr(), flat["schema"].data_ptr(), flat["binding"].data_ptr(), L, rows, schema.data_ptr(),
+                                binding.data_ptr(), binding.shape[1], out.data_ptr(), _stream()))
+    return out

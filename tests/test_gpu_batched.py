@@ -165,8 +165,8 @@ def test_batched_env_argument_errors(golden):
     from mymyr_amd.batched import BatchedEnv
 
     ts = load_tasks(golden, "gridworld_table")
-    with pytest.raises(NotImplementedError):
-        BatchedEnv(ts, 8, actions="label")
+    with pytest.raises(ValueError):
+        BatchedEnv(ts, 8, actions="name")
     with pytest.raises(ValueError, match="task id 3 of row 2 is outside the table's 3 instances"):
         BatchedEnv(ts, 8, task_ids=[0, 1, 3, 0, 1, 2, 0, 1])
     env = BatchedEnv(ts, 8, sampler=None, task_ids=0)
@@ -176,3 +176,60 @@ def test_batched_env_argument_errors(golden):
     env.set_launch("per_bucket")
     with pytest.raises(ValueError):
         env.set_launch("fastest")
+
+
+@pytest.mark.parametrize("table", ["gridworld_table", "transport_table"])
+def test_label_steps_equal_index_steps(golden, table):
+    """actions="label": a label step equals the index step at the label's position in the row's canonical successor
+    order (-1, invalid, when the label is not applicable), with counts clamped to 0/1, as the reference's label steps
+    equal its index steps (tests/test_label_equivalence.py). Positions here come from a host scan of rl.expand's
+    output; labels are successors' labels with random objects past their arity, and 30% random garbage."""
+    from mymyr_amd import rl
+    from mymyr_amd.batched import BatchedEnv
+
+    ts = load_tasks(golden, table)
+    n = 256
+    kw = dict(seed=5, max_steps=9, sampler="uniform")
+    a, b = BatchedEnv(ts, n, actions="label", **kw), BatchedEnv(ts, n, **kw)
+    print(f"label steps: {table}, {n} envs", flush=True)
+    assert torch.equal(a.count, b.count.clamp(max=1))
+    rng = np.random.default_rng(2)
+    tt = rl.TaskTable(ts)
+    moved = invalid = 0
+    for k in range(10):
+        assert torch.equal(a.states, b.states) and torch.equal(a.task_ids, b.task_ids)
+        x = rl.expand(tt, b.states, task_ids=b.task_ids)
+        off, sch, bnd = host(x["offsets"]).astype(np.int64), host(x["schema"]), host(x["binding"])
+        L = bnd.shape[1]
+        c = off[1:] - off[:-1]
+        idx = (rng.random(n) * np.maximum(c, 1)).astype(np.int64)
+        ls = np.full(n, -1, np.int32)
+        lb = rng.integers(-1, 6, (n, L + 1)).astype(np.int32)
+        for i in range(n):
+            if c[i]:
+                ls[i] = sch[off[i] + idx[i]]
+                row = bnd[off[i] + idx[i]]
+                lb[i, :L] = np.where(row >= 0, row, lb[i, :L])
+        garbage = rng.random(n) < 0.3
+        ls[garbage] = rng.integers(-1, 8, int(garbage.sum()))
+        act = np.full(n, -1, np.int64)
+        for i in range(n):
+            for j in range(off[i], off[i + 1]):
+                if sch[j] == ls[i] and np.all((bnd[j] < 0) | (bnd[j] == lb[i, :L])):
+                    act[i] = j - off[i]
+                    break
+        ra = a.step((torch.from_numpy(ls).cuda(), torch.from_numpy(lb).cuda()))
+        rb = b.step(torch.from_numpy(act).cuda())
+        for name in ("reward", "terminated", "truncated", "goal", "invalid", "schema", "binding", "final_states", "states", "task_ids",
+                     "at_goal"):
+            assert torch.equal(getattr(ra, name), getattr(rb, name)), f"step {k}: {name}"
+        assert torch.equal(ra.count, rb.count.clamp(max=1)), f"step {k}: count"
+        moved += int((ra.schema >= 0).sum())
+        invalid += int(ra.invalid.sum())
+    assert moved > 0 and invalid > 0, (moved, invalid)
+    with pytest.raises(ValueError):
+        a.random_actions()
+    with pytest.raises(ValueError):
+        a.step(None)
+    a.check_errors()
+    b.check_errors()
