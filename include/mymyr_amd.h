@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 11
+#define MYA_ABI_VERSION 12
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -440,13 +440,34 @@ typedef struct mya_brfs_result
     double kernel_ms[8];
     uint64_t kernel_bytes[8];
     uint64_t kernel_launches[8];
+    uint64_t pruned;       /* successors not stored because they are blocked (no blocked states here: 0) */
+    uint64_t memory_bytes; /* device bytes of the search's buffers (state set, arena, nodes, chunk and layer arrays) */
 } mya_brfs_result;
+
+/* The plan of a solved search: BrfsResult::plan, cost and goal_state (include/mymyr/search/brfs.hpp:118-131), the
+ * actions from the start state to the first goal state tested, rebuilt from per-state node records (the first
+ * discovery of each state: its parent and action, src/mymyr/search/brfs.cpp:235-268). Host arrays, caller-owned;
+ * null arrays are not written. */
+typedef struct mya_brfs_plan
+{
+    int32_t* schema;       /* [cap] the actions' schemas */
+    int32_t* binding;      /* [cap, label_width] their objects, -1 past a schema's arity */
+    uint32_t cap;          /* actions the arrays hold */
+    uint32_t label_width;  /* columns of binding */
+    uint64_t* goal_state;  /* [goal_cap] the goal state's words */
+    uint32_t goal_cap;
+    uint32_t length;       /* out: actions of the plan (0 unless solved; those past cap are not written) */
+    uint32_t goal_words;   /* out: words of the goal state (0 unless solved) */
+    uint32_t reserved;
+    double cost;           /* out: the plan's cost (unit action costs: its length); 0 unless solved */
+} mya_brfs_plan;
 
 /* Layer-synchronous BrFS on the current device (replaces brfs(), include/mymyr/search/brfs.hpp:140, and
  * cuda::brfs, include/mymyr/cuda/brfs.hpp:89-123). layer_counts [cap, 3] (host, optional) receives
- * {expanded, generated, new} per expanded layer. Returns the number of layers, or -1. Synchronous. */
+ * {expanded, generated, new} per expanded layer; plan (optional) receives the plan of a solved search. Returns the
+ * number of layers, or -1. Synchronous. */
 int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts,
-             uint32_t cap);
+             uint32_t cap, mya_brfs_plan* plan);
 
 /* ---------------------------------------------------------------------------------------------------------- DLPack */
 

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 11  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 12  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -131,6 +131,23 @@ class BrfsResult(Structure):
         ("kernel_ms", c_double * 8),
         ("kernel_bytes", c_uint64 * 8),
         ("kernel_launches", c_uint64 * 8),
+        ("pruned", c_uint64),
+        ("memory_bytes", c_uint64),
+    ]
+
+
+class BrfsPlan(Structure):
+    _fields_ = [
+        ("schema", c_void_p),
+        ("binding", c_void_p),
+        ("cap", c_uint32),
+        ("label_width", c_uint32),
+        ("goal_state", c_void_p),
+        ("goal_cap", c_uint32),
+        ("length", c_uint32),
+        ("goal_words", c_uint32),
+        ("reserved", c_uint32),
+        ("cost", c_double),
     ]
 
 
@@ -247,7 +264,7 @@ def _load() -> ctypes.CDLL:
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_refresh": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),
         "mya_env_initial_count": (c_int, [c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_uint8)]),
-        "mya_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
+        "mya_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32, POINTER(BrfsPlan)]),
         "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p]),
         "mya_schema_masks": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),
         "mya_expand": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion), c_void_p]),

@@ -298,7 +298,12 @@ struct ParentRows
     template<int G, int K>
     __device__ __forceinline__ void load(u64 c, u32 q, Slice<G, K>& o) const
     {
-        const u64 pa = cand_pa[c];
+        load_pa<G, K>(cand_pa[c], q, o);
+    }
+    /// The row of the candidate with record pa.
+    template<int G, int K>
+    __device__ __forceinline__ void load_pa(u64 pa, u32 q, Slice<G, K>& o) const
+    {
         const u64* row = arena + (first + (pa >> 32)) * W;
         const u64* mk = masks + static_cast<u64>(static_cast<u32>(pa)) * (2 * W);
         Slice<G, K> r, d, a;
@@ -344,11 +349,13 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
 }
 
 // The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena
-// (rows recomputed from their records) and the table.
+// (rows recomputed from their records), with their search nodes: nodes[id] = (parent id << 32) | ground action, the
+// first discovery of the state (the reference's node records, src/mymyr/search/brfs.cpp:235-268). A winner at or past
+// `limit` sets kStatusCapacity.
 template<int W>
 __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 m, const u32* __restrict__ list,
-                                                       const u64* __restrict__ size_now,
-                                                       const u64* __restrict__ size_next, u64 limit, u32* __restrict__ status)
+                                                       const u64* __restrict__ size_now, const u64* __restrict__ size_next, u64 limit,
+                                                       u64* __restrict__ nodes, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
     const u32 q = lane_id() % G;
@@ -356,7 +363,21 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
     const u64 winners = min(m, *size_next - id0);
     // a grid sized for the whole chunk would mostly start waves that find no winner: a bounded grid strides instead
     for (u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G; w < winners; w += static_cast<u64>(gridDim.x) * (kLB / G))
-        compact_winner<G, kPairs<W>>(s, src, w, q, list, id0, limit, nullptr, status);
+    {
+        const u64 id = id0 + w;
+        if (id >= limit)
+        {
+            if (q == 0)
+                atomicOr(status, kStatusCapacity);
+            continue;
+        }
+        const u64 pa = src.cand_pa[list[w]];
+        Slice<G, kPairs<W>> r;
+        src.template load_pa<G, kPairs<W>>(pa, q, r);
+        store_row<G, kPairs<W>>(s.arena + id * W, W, q, r);
+        if (q == 0)
+            nodes[id] = ((src.first + (pa >> 32)) << 32) | static_cast<u32>(pa);
+    }
 }
 
 // The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
@@ -671,6 +692,9 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     } layer_guard{counts, goal_flags, offsets, scan_scratch};
     u64* cand_pa = b.alloc<u64>(chunk, "candidate records");
     u64* small = b.alloc<u64>(kSmall, "scalars");
+    // search nodes: per stored state its first discovery (parent id << 32 | ground action); the start state has none
+    u64* nodes = b.alloc<u64>(cap_states, "search nodes");
+    r.memory_bytes = set.v.capacity * 8 + cap_states * (R + 8) + chunk * (8 + 8 + 1 + 4) + layer_cap * (S * 4 + 1 + S * 8 + 8);
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
     enum
     {
@@ -700,6 +724,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         hip_check(hipMemcpyAsync(d_s0, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
         u64 nn = 0;
         state_set_insert(set, d_s0, 1, nullptr, nullptr, &nn, stream);
+        hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, nodes, ~u64{0});
+        launch_check("root node");
     }
     const auto td0 = Clock::now();
     bool stopped = false, budget_stopped = false;
@@ -883,7 +909,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 // (the store filled: the confirmation finds the cut)
                 tm.begin(kKCompact);
                 hipLaunchKernelGGL(k_ground_compact<W>, dim3(std::min<u64>(blocks_for(m * G, kLB), kStrideBlocks)), dim3(kLB), 0, stream, set.v, src, m, set.list,
-                                   state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states,
+                                   state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states, nodes,
                                    bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
                 launch_check("ground compact");
                 tm.end(kKCompact, 0);
@@ -950,6 +976,34 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         launch_check("fingerprint");
         sync_small();
         r.fingerprint = b.host[kFingerprint];
+    }
+    if (r.solved)
+    {
+        // the plan to the first goal state tested, from the node records (first discoveries), and that state's row
+        std::vector<u32> rev;
+        for (u64 v = static_cast<u64>(r.first_goal);;)
+        {
+            u64 nd = 0;
+            hip_check(hipMemcpy(&nd, nodes + v, sizeof(u64), hipMemcpyDeviceToHost), "plan node");
+            if (nd == ~u64{0})
+                break;
+            rev.push_back(static_cast<u32>(nd));
+            v = nd >> 32;
+            if (rev.size() > r.layers)
+                throw std::logic_error("mymyr_amd: brfs: the node records of the goal state form no path to the start");
+        }
+        const u32 L = ga.label_width;
+        r.plan_width = L;
+        for (auto it = rev.rbegin(); it != rev.rend(); ++it)
+        {
+            r.plan_schema.push_back(static_cast<i32>(ga.schema[*it]));
+            for (u32 k = 0; k < L; ++k)
+                r.plan_binding.push_back(static_cast<i32>(ga.binding[static_cast<size_t>(*it) * L + k]));
+        }
+        r.cost = static_cast<double>(rev.size());  // unit action costs (the device path takes tasks without a metric)
+        r.goal_state.resize(W);
+        hip_check(hipMemcpy(r.goal_state.data(), set.v.arena + static_cast<u64>(r.first_goal) * W, W * sizeof(u64), hipMemcpyDeviceToHost),
+                  "goal state");
     }
     r.search_s = std::chrono::duration<double>(Clock::now() - t0).count();
     return r;

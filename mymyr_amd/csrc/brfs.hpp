@@ -55,6 +55,14 @@ struct BrfsResultC
     double kernel_ms[kKClasses] = {};
     u64 kernel_bytes[kKClasses] = {};  // algorithmic bytes per class (the per-launch formulas in brfs.hip)
     u64 kernel_launches[kKClasses] = {};
+    u64 memory_bytes = 0;  // device bytes of the search's buffers (state set, arena, nodes, chunk and layer arrays)
+    // a solved search: the plan to the first goal state tested as (schema, binding) labels ([len], [len, plan_width]
+    // objects, -1 padded past a schema's arity), its cost and the goal state's words
+    std::vector<i32> plan_schema;
+    std::vector<i32> plan_binding;
+    u32 plan_width = 0;
+    double cost = 0;
+    std::vector<u64> goal_state;
 };
 
 enum SearchStatus : i32

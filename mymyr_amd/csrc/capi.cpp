@@ -261,7 +261,8 @@ int mya_dedup_rows(uint64_t start, uint64_t count, uint32_t words, uint64_t seed
     });
 }
 
-int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts, uint32_t cap)
+int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts, uint32_t cap,
+             mya_brfs_plan* plan)
 {
     int layers = -1;
     const int rc = guarded([&] {
@@ -300,6 +301,30 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         result->first_goal = r.first_goal;
         result->search_s = r.search_s;
         result->device_s = r.device_s;
+        result->pruned = 0;
+        result->memory_bytes = r.memory_bytes;
+        if (plan)
+        {
+            if (plan->binding && plan->label_width < r.plan_width)
+                throw std::invalid_argument("mymyr_amd: brfs: plan label width " + std::to_string(plan->label_width) +
+                                            " is below the task's " + std::to_string(r.plan_width));
+            const u32 len = static_cast<u32>(r.plan_schema.size());
+            plan->length = len;
+            plan->cost = r.cost;
+            plan->goal_words = static_cast<u32>(r.goal_state.size());
+            for (u32 i = 0; i < len && i < plan->cap; ++i)
+            {
+                if (plan->schema)
+                    plan->schema[i] = r.plan_schema[i];
+                if (plan->binding)
+                    for (u32 k = 0; k < plan->label_width; ++k)
+                        plan->binding[static_cast<size_t>(i) * plan->label_width + k] =
+                            k < r.plan_width ? r.plan_binding[static_cast<size_t>(i) * r.plan_width + k] : -1;
+            }
+            if (plan->goal_state)
+                for (u32 w = 0; w < plan->goal_cap; ++w)
+                    plan->goal_state[w] = w < r.goal_state.size() ? r.goal_state[w] : 0;
+        }
         for (int k = 0; k < kKClasses; ++k)
         {
             result->kernel_ms[k] = r.kernel_ms[k];

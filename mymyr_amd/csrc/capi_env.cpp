@@ -202,10 +202,45 @@ void run_count(mya_env* env, const mya_env_batch* batch, CountArgs& a, hipStream
         }
 }
 
+void free_env(mya_env* e)
+{
+    for (void* p : std::initializer_list<void*>{e->d_status, e->d_inst, e->d_tasks, e->d_init, e->d_init_cache, e->d_init_masks, e->d_hist,
+                                                e->d_starts, e->d_chunks, e->d_order, e->d_thresholds, e->d_indices,
+                                                e->d_sampled, e->d_seed})
+        dev_free(p);
+    if (e->h_status)
+        (void)hipHostFree(e->h_status);
+    delete e;
+}
+}  // namespace
+
+namespace mya
+{
+/// Carves the scratch of an expansion of n rows from a block of at least expand_scratch_bytes(n) bytes (256-aligned).
+ExpandScratch carve_expand_scratch(void* block, u64 n)
+{
+    unsigned char* p = static_cast<unsigned char*>(block);
+    auto next = [&]<class T>(size_t count) {
+        T* q = reinterpret_cast<T*>(p);
+        p += scratch_bytes<T>(count);
+        return q;
+    };
+    ExpandScratch x{};
+    x.counts = next.operator()<u32>(n);
+    x.noops = next.operator()<u32>(n);
+    x.kept = next.operator()<u32>(n);
+    x.pre = next.operator()<u64>(n + 1);
+    x.fin = next.operator()<u64>(n + 1);
+    x.scan = next.operator()<u64>(scan_scratch_words(n));
+    x.words_status = next.operator()<u32>(2);
+    return x;
+}
+
 /// The flat expansion of rows over instances `inst` (one: batch order; several: grouped by instance with `env`'s
-/// scratch and the rows' task ids).
+/// scratch and the rows' task ids). `block` (device, at least expand_scratch_bytes(max(rows, 1)) bytes) holds the
+/// expansion's scratch; the call synchronizes the stream before it returns, so the block is free again then.
 void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const int32_t* task_ids, const uint64_t* states, uint64_t rows,
-                 uint32_t words, const mya_expand_options* options, mya_expansion* out, hipStream_t stream)
+                 uint32_t words, const mya_expand_options* options, mya_expansion* out, hipStream_t stream, void* block)
 {
     {
         if (!options || !out || (rows && !states))
@@ -237,24 +272,15 @@ void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const in
             throw std::invalid_argument("mymyr: expand: drop_noops requires index");
         out->generated = out->total = 0;
         out->words_needed = 0;
-        // scratch: per-row counts and no-op counts, offsets before and after dropping, scan scratch, status words
         const u64 n = std::max<u64>(rows, 1);
-        u32* counts = dev_alloc<u32>(n, "expand counts");
-        u32* noops = dev_alloc<u32>(n, "expand no-op counts");
-        u32* kept = dev_alloc<u32>(n, "expand kept counts");
-        u64* pre = dev_alloc<u64>(n + 1, "expand offsets");
-        u64* fin = dev_alloc<u64>(n + 1, "expand kept offsets");
-        u64* scratch = dev_alloc<u64>(scan_scratch_words(n), "expand scan scratch");
-        u32* words_status = dev_alloc<u32>(2, "expand status");  // [0] words needed, [1] status
-        struct Free
-        {
-            std::vector<void*> p;
-            ~Free()
-            {
-                for (void* q : p)
-                    dev_free(q);
-            }
-        } freeing{{counts, noops, kept, pre, fin, scratch, words_status}};
+        const ExpandScratch x = carve_expand_scratch(block, n);
+        u32* const counts = x.counts;
+        u32* const noops = x.noops;
+        u32* const kept = x.kept;
+        u64* const pre = x.pre;
+        u64* const fin = x.fin;
+        u64* const scratch = x.scan;
+        u32* const words_status = x.words_status;
         launch_fill_u32(words_status, 2, 0, stream);
         ExpandArgs a{};
         a.T = *inst[0];
@@ -347,18 +373,7 @@ void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const in
         out->words_needed = st[0];
     }
 }
-
-void free_env(mya_env* e)
-{
-    for (void* p : std::initializer_list<void*>{e->d_status, e->d_inst, e->d_tasks, e->d_init, e->d_init_cache, e->d_init_masks, e->d_hist,
-                                                e->d_starts, e->d_chunks, e->d_order, e->d_thresholds, e->d_indices,
-                                                e->d_sampled, e->d_seed})
-        dev_free(p);
-    if (e->h_status)
-        (void)hipHostFree(e->h_status);
-    delete e;
-}
-}  // namespace
+}  // namespace mya
 
 namespace
 {
@@ -842,13 +857,13 @@ int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32
         if (words < T.W)
             throw std::invalid_argument("mymyr_amd: successors: rows of " + std::to_string(words) + " words; the task needs " +
                                         std::to_string(T.W));
-        u32* st = dev_alloc<u32>(1, "status");
-        hip_check(hipMemsetAsync(st, 0, sizeof(u32), static_cast<hipStream_t>(stream)), "status");
+        ScratchLease lease(scratch_bytes<u32>(1), "successors status");
+        u32* st = lease.take<u32>(1);
+        launch_fill_u32(st, 1, 0, static_cast<hipStream_t>(stream));
         launch_successors(T, states, rows, words, static_cast<u32>(cap), count, schema, binding, succ, st, static_cast<hipStream_t>(stream));
         u32 hs = 0;
         hip_check(hipMemcpyAsync(&hs, st, sizeof(u32), hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)), "status");
         hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "successors");
-        dev_free(st);
         if (hs)
             throw std::runtime_error("mymyr_amd: successors: device status " + std::to_string(hs));
     });
@@ -860,7 +875,9 @@ int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t w
     return guarded([&] {
         if (!task)
             throw std::invalid_argument("mymyr_amd: expand: null argument");
-        expand_rows({device_task(task).thost.get()}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream));
+        const TaskDev* T = device_task(task).thost.get();
+        ScratchLease lease(expand_scratch_bytes(std::max<u64>(rows, 1)), "expand scratch");
+        expand_rows({T}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream), lease.base());
     });
 }
 
@@ -876,7 +893,8 @@ int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids
         std::vector<const TaskDev*> inst;
         for (const EnvInstance& in : env->inst)
             inst.push_back(&in.T);
-        expand_rows(inst, env, task_ids, states, rows, words, options, out, static_cast<hipStream_t>(stream));
+        ScratchLease lease(expand_scratch_bytes(std::max<u64>(rows, 1)), "expand scratch");
+        expand_rows(inst, env, task_ids, states, rows, words, options, out, static_cast<hipStream_t>(stream), lease.base());
     });
 }
 
@@ -895,12 +913,8 @@ int mya_pad(const mya_expansion* flat, uint64_t rows, mya_padded_expansion* out,
         if (rows > kMaxRows || flat->capacity > kMaxRows)
             throw std::invalid_argument("mymyr_amd: pad: more than 2^31 - 1 states or flat rows");
         const bool flat_overflow = flat->generated > flat->capacity || flat->total > flat->capacity || flat->words_needed > flat->words;
-        u32* d_over = dev_alloc<u32>(1, "pad overflow");
-        struct Free
-        {
-            u32* p;
-            ~Free() { dev_free(p); }
-        } freeing{d_over};
+        ScratchLease lease(scratch_bytes<u32>(1), "pad overflow");
+        u32* d_over = lease.take<u32>(1);
         const hipStream_t s = static_cast<hipStream_t>(stream);
         launch_fill_u32(d_over, 1, 0, s);
         PadArgs a{};

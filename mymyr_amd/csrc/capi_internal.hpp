@@ -2,6 +2,8 @@
 // Internals shared by the C-ABI translation units: the opaque handle types and the exception guard.
 
 #include "brfs.hpp"
+#include "runtime.hpp"
+#include "scan.hpp"
 #include "state_set.hpp"
 #include "task.hpp"
 
@@ -12,6 +14,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <vector>
 
 namespace mya
 {
@@ -56,9 +59,40 @@ struct mya_task
     mya::BrfsCache brfs;  // the BrFS's device tables of the task's ground actions
 };
 
+struct mya_env;
+struct mya_expand_options;
+struct mya_expansion;
+
 namespace mya
 {
 const DeviceTask& device_task(mya_task* t);
+
+/// The device scratch of one flat expansion of n rows, carved from one block: per-row counts, no-op counts and kept
+/// counts, offsets before and after dropping no-ops, the scans' scratch, and two status words.
+struct ExpandScratch
+{
+    u32* counts;
+    u32* noops;
+    u32* kept;
+    u64* pre;
+    u64* fin;
+    u64* scan;
+    u32* words_status;  // [0] words needed, [1] status
+};
+
+constexpr size_t expand_scratch_bytes(u64 n)
+{
+    return 3 * scratch_bytes<u32>(n) + 2 * scratch_bytes<u64>(n + 1) + scratch_bytes<u64>(scan_scratch_words(n)) + scratch_bytes<u32>(2);
+}
+
+/// Carves the scratch of an expansion of n rows from a block of at least expand_scratch_bytes(n) bytes (256-aligned).
+ExpandScratch carve_expand_scratch(void* block, u64 n);
+
+/// The flat expansion of rows over instances `inst` (one: batch order; several: grouped by instance with `env`'s
+/// scratch and the rows' task ids). `block` (device, at least expand_scratch_bytes(max(rows, 1)) bytes) holds the
+/// expansion's scratch; the call synchronizes the stream before it returns, so the block is free again then.
+void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const int32_t* task_ids, const uint64_t* states, uint64_t rows,
+                 uint32_t words, const mya_expand_options* options, mya_expansion* out, hipStream_t stream, void* block);
 }
 
 /// A state set handle; mya_hashset_free drops the creator's reference and every exported rows tensor holds another.

@@ -2,6 +2,7 @@
 
 #include "runtime.hpp"
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <unordered_map>
@@ -19,11 +20,21 @@ struct Block
     size_t bytes;
 };
 
+/// A block freed on a stream: reusable once the event recorded after the stream's queued work has completed.
+struct Pending
+{
+    hipEvent_t event;
+    int device;
+    size_t bytes;
+    void* p;
+};
+
 struct Cache
 {
     std::mutex mutex;
     std::unordered_map<void*, Block> live;             // every block handed out
     std::multimap<std::pair<int, size_t>, void*> idle;  // freed blocks by (device, bytes)
+    std::vector<Pending> pending;                       // stream-ordered frees whose streams have not passed them yet
     size_t idle_bytes = 0;
 
     void release_idle()
@@ -32,6 +43,20 @@ struct Cache
             (void)hipFree(p);
         idle.clear();
         idle_bytes = 0;
+    }
+    /// Moves every pending block whose event completed (or, with wait, every pending block) to the idle blocks.
+    void collect(bool wait);
+    void make_idle(int device, size_t bytes, void* p)
+    {
+        if (idle_bytes + bytes > kCacheMax)
+            release_idle();
+        if (bytes > kCacheMax)
+        {
+            (void)hipFree(p);
+            return;
+        }
+        idle.emplace(std::make_pair(device, bytes), p);
+        idle_bytes += bytes;
     }
 };
 
@@ -43,6 +68,25 @@ Cache& cache()
 
 std::mutex g_event_mutex;
 std::vector<hipEvent_t>* g_events = new std::vector<hipEvent_t>();
+
+void Cache::collect(bool wait)
+{
+    for (size_t i = 0; i < pending.size();)
+    {
+        const hipError_t q = wait ? hipEventSynchronize(pending[i].event) : hipEventQuery(pending[i].event);
+        if (q == hipErrorNotReady)
+        {
+            (void)hipGetLastError();  // not an error: the stream has not reached the event yet
+            ++i;
+            continue;
+        }
+        const Pending b = pending[i];
+        pending[i] = pending.back();
+        pending.pop_back();
+        event_release(b.event);
+        make_idle(b.device, b.bytes, b.p);
+    }
+}
 }  // namespace
 
 void* device_alloc(size_t bytes, const char* what)
@@ -52,6 +96,8 @@ void* device_alloc(size_t bytes, const char* what)
     Cache& c = cache();
     {
         std::lock_guard lock(c.mutex);
+        if (!c.pending.empty())
+            c.collect(false);
         auto it = c.idle.find({dev, bytes});
         if (it != c.idle.end())
         {
@@ -69,6 +115,7 @@ void* device_alloc(size_t bytes, const char* what)
         (void)hipGetLastError();
         {
             std::lock_guard lock(c.mutex);
+            c.collect(true);
             c.release_idle();
         }
         e = hipMalloc(&p, bytes);
@@ -84,7 +131,7 @@ void* device_alloc(size_t bytes, const char* what)
 void device_free(void* p)
 {
     // the block may still be in use by queued work on any stream of the device: wait for it, as hipFree does, before
-    // the block can be handed out again
+    // the block can be handed out again (callers that know the stream use device_free_async)
     (void)hipDeviceSynchronize();
     Cache& c = cache();
     std::lock_guard lock(c.mutex);
@@ -96,22 +143,94 @@ void device_free(void* p)
     }
     const Block b = it->second;
     c.live.erase(it);
-    if (c.idle_bytes + b.bytes > kCacheMax)
-        c.release_idle();
-    if (b.bytes > kCacheMax)
+    c.make_idle(b.device, b.bytes, p);
+}
+
+void device_free_async(void* p, hipStream_t stream)
+{
+    Cache& c = cache();
+    Block b{};
     {
+        std::lock_guard lock(c.mutex);
+        auto it = c.live.find(p);
+        if (it == c.live.end())
+            b.device = -1;
+        else
+        {
+            b = it->second;
+            c.live.erase(it);
+        }
+    }
+    if (b.device < 0)
+    {
+        (void)hipStreamSynchronize(stream);
         (void)hipFree(p);
         return;
     }
-    c.idle.emplace(std::make_pair(b.device, b.bytes), p);
-    c.idle_bytes += b.bytes;
+    // the event marks the end of the work queued on the stream so far; the block is reused only after it completed
+    hipEvent_t e = event_acquire();
+    if (hipEventRecord(e, stream) != hipSuccess)
+    {
+        (void)hipGetLastError();
+        (void)hipStreamSynchronize(stream);
+        event_release(e);
+        std::lock_guard lock(c.mutex);
+        c.make_idle(b.device, b.bytes, p);
+        return;
+    }
+    std::lock_guard lock(c.mutex);
+    c.pending.push_back(Pending{e, b.device, b.bytes, p});
 }
 
 void device_cache_release()
 {
     Cache& c = cache();
     std::lock_guard lock(c.mutex);
+    c.collect(true);
     c.release_idle();
+}
+
+namespace
+{
+struct DeviceScratch
+{
+    std::mutex mutex;
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+DeviceScratch& device_scratch_of(int dev)
+{
+    static std::mutex m;
+    static auto* all = new std::map<int, DeviceScratch*>();  // never destroyed, as the cache
+    std::lock_guard lock(m);
+    DeviceScratch*& d = (*all)[dev];
+    if (!d)
+        d = new DeviceScratch();
+    return *d;
+}
+}  // namespace
+
+ScratchLease::ScratchLease(size_t bytes, const char* what)
+{
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    DeviceScratch& d = device_scratch_of(dev);
+    m_lock = std::unique_lock<std::mutex>(d.mutex);
+    if (d.bytes < bytes)
+    {
+        // grown to the largest request so far, in steps of at least 1 MiB (earlier calls have drained: every user
+        // synchronizes its stream before it returns)
+        if (d.p)
+            device_free(d.p);
+        d.p = nullptr;
+        d.bytes = 0;
+        const size_t want = std::max<size_t>((bytes + (size_t{1} << 20) - 1) & ~((size_t{1} << 20) - 1), size_t{1} << 20);
+        d.p = device_alloc(want, what);
+        d.bytes = want;
+    }
+    m_p = static_cast<unsigned char*>(d.p);
+    m_bytes = d.bytes;
 }
 
 hipEvent_t event_acquire()

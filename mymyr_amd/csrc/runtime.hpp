@@ -3,6 +3,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -23,7 +25,12 @@ inline void hip_check(hipError_t e, const char* what)
 /// of the same size on the same device (repeated searches and env pools reuse their buffers without hipMalloc / hipFree);
 /// the cache holds at most a fixed share of device memory and is released when an allocation fails.
 void* device_alloc(size_t bytes, const char* what);
+/// Returns a block to the cache after waiting for the device (for frees whose last stream is unknown).
 void device_free(void* p);
+/// Returns a block to the cache in stream order: an event recorded on `stream` marks the work queued so far, and the
+/// block is handed out again only once that event has completed (no device-wide wait). The block must not be used by
+/// work queued later on other streams.
+void device_free_async(void* p, hipStream_t stream);
 /// Frees every cached block (all devices).
 void device_cache_release();
 
@@ -39,6 +46,50 @@ inline void dev_free(void* p)
 {
     if (p)
         device_free(p);
+}
+
+inline void dev_free_async(void* p, hipStream_t stream)
+{
+    if (p)
+        device_free_async(p, stream);
+}
+
+/// Exclusive use of the current device's persistent scratch block for the lifetime of the lease, grown to at least
+/// `bytes` (the block is kept between calls: synchronous entry points that need per-call device scratch allocate
+/// nothing once it is large enough). The lease holds the device's scratch lock, so calls using it are serialized; a
+/// holder must have drained its work on the block (synchronized its stream) before the lease ends.
+class ScratchLease
+{
+public:
+    ScratchLease(size_t bytes, const char* what);
+    ScratchLease(const ScratchLease&) = delete;
+    ScratchLease& operator=(const ScratchLease&) = delete;
+    /// The whole block (256-byte aligned, at least the requested bytes).
+    void* base() const { return m_p; }
+    /// The next `count` elements of T from the block (aligned to 256 bytes).
+    template<class T>
+    T* take(size_t count)
+    {
+        m_used = (m_used + 255) & ~size_t{255};
+        T* p = reinterpret_cast<T*>(m_p + m_used);
+        m_used += std::max<size_t>(count, 1) * sizeof(T);
+        if (m_used > m_bytes)
+            throw std::logic_error("mymyr_amd: scratch lease overrun");
+        return p;
+    }
+
+private:
+    std::unique_lock<std::mutex> m_lock;
+    unsigned char* m_p = nullptr;
+    size_t m_bytes = 0;
+    size_t m_used = 0;
+};
+
+/// Bytes a lease needs for the given element counts of T (each aligned to 256 bytes).
+template<class T>
+constexpr size_t scratch_bytes(size_t count)
+{
+    return ((count == 0 ? 1 : count) * sizeof(T) + 255) & ~size_t{255};
 }
 
 /// HIP events from a process-wide pool (created once, reused).

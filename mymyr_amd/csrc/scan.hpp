@@ -84,7 +84,7 @@ __device__ __forceinline__ u32 block_exclusive(u32 v, u32* lds, u32* total)
 /// after the last offset, and `base` the total of the previous piece, to scan a sequence piece by piece).
 void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream,
                            const u64* base = nullptr);
-inline u64 scan_scratch_words(u64 n) { return (n + 1023) / 1024 + 2; }
+constexpr u64 scan_scratch_words(u64 n) { return (n + 1023) / 1024 + 2; }
 
 /// The indices j of the nonzero flags in order into list[0, winners) (flag bytes are 0 or 1; zero flags are reset to 1),
 /// id_of[j] = *total_base + rank for the winners (optional), is_new[j] = flags[j] (optional), and *total = *total_base +

@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
+from typing import NamedTuple
 
 import numpy as np
 
@@ -18,9 +19,18 @@ UNBOUNDED32 = 0xFFFFFFFF
 UNBOUNDED64 = (1 << 64) - 1
 
 
+class Action(NamedTuple):
+    """An action label (include/mymyr/successor/action.hpp:27-44): the schema and the objects of its full parameter list."""
+
+    schema: int
+    binding: tuple
+
+
 @dataclass
 class BrfsResult:
-    """The fields of the reference's BrfsResult (include/mymyr/search/brfs.hpp:103-138) that the device search fills."""
+    """The fields of the reference's BrfsResult (include/mymyr/search/brfs.hpp:103-138) that the device search fills.
+    A solved search has its plan (Actions from the start state to the first goal state tested), its cost (unit action
+    costs: the plan's length) and goal_state (the goal state's words, uint64); unsolved: [], 0.0 and None."""
 
     status: str
     states: int
@@ -36,6 +46,11 @@ class BrfsResult:
     device_s: float
     layer_counts: list = field(default_factory=list)
     kernels: dict = field(default_factory=dict)  # class -> {"ms", "bytes", "launches"} (ms with timings=True)
+    plan: list = field(default_factory=list)
+    cost: float = 0.0
+    goal_state: np.ndarray | None = None
+    pruned: int = 0
+    memory_bytes: int = 0
 
 
 KERNEL_CLASSES = ["count", "emit", "insert", "unused", "rank", "compact", "other"]
@@ -51,11 +66,24 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
                          int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
-    n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096)
+    L = max(1, task.label_width)
+    cap = 1 << 16
+    ps = np.zeros(cap, np.int32)
+    pb = np.zeros((cap, L), np.int32)
+    gs = np.zeros(max(1, task.words), np.uint64)
+    plan = _lib.BrfsPlan(ps.ctypes.data, pb.ctypes.data, cap, L, gs.ctypes.data, gs.size, 0, 0, 0, 0.0)
+    n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ctypes.byref(plan))
     if n < 0:
         check(-1)
     kernels = {c: {"ms": r.kernel_ms[i], "bytes": r.kernel_bytes[i], "launches": r.kernel_launches[i]}
                for i, c in enumerate(KERNEL_CLASSES)}
-    return BrfsResult(STATUS.get(r.status, str(r.status)), r.states, r.expanded, r.generated, r.goal_states, r.layers,
-                      bool(r.exhausted), bool(r.solved), r.fingerprint, r.first_goal, r.search_s, r.device_s,
-                      lc[:n].tolist() if layer_stats else [], kernels)
+    res = BrfsResult(STATUS.get(r.status, str(r.status)), r.states, r.expanded, r.generated, r.goal_states, r.layers,
+                     bool(r.exhausted), bool(r.solved), r.fingerprint, r.first_goal, r.search_s, r.device_s,
+                     lc[:n].tolist() if layer_stats else [], kernels, pruned=r.pruned, memory_bytes=r.memory_bytes)
+    if r.solved:
+        if plan.length > cap:
+            raise RuntimeError(f"mymyr_amd: brfs: a plan of {plan.length} actions (at most {cap} are read)")
+        res.plan = [Action(int(ps[i]), tuple(int(x) for x in pb[i] if x >= 0)) for i in range(plan.length)]
+        res.cost = plan.cost
+        res.goal_state = gs[: plan.goal_words].copy()
+    return res

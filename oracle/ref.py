@@ -42,6 +42,7 @@ class BrfsOptions(Structure):
         ("canonical_order", c_int32),
         ("stop_at_goal", c_int32),
         ("fingerprint", c_int32),
+        ("max_expanded", c_uint64),
     ]
 
 
@@ -57,6 +58,10 @@ class BrfsResult(Structure):
         ("solved", c_int32),
         ("exhausted", c_int32),
         ("seconds", c_double),
+        ("cost", c_double),
+        ("pruned", c_uint64),
+        ("plan_len", c_uint32),
+        ("goal_words", c_uint32),
     ]
 
 
@@ -109,7 +114,10 @@ def lib() -> ctypes.CDLL:
             "mref_visited_mask": (None, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
             "mref_instance_draw": (c_int32, [c_uint64, c_uint64, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32]),
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
-            "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32]),
+            "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32, c_void_p, c_void_p,
+                                  c_uint32, c_uint32, c_void_p, c_uint32]),
+            "mref_dedup_flat": (c_int, [c_void_p, c_uint64, c_uint32, POINTER(c_uint64), POINTER(c_double)]),
+            "mref_dedup_concurrent": (c_int, [c_void_p, c_uint64, c_uint32, c_uint32, c_uint64, POINTER(c_uint64), POINTER(c_double)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -391,18 +399,52 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 
 
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
-         stop_at_goal=False, fingerprint=True):
-    o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint))
+         stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1):
+    """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
+    (schema, binding) pairs, the goal state's words and the cost."""
+    o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
+                    max_expanded)
     r = BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
-    n = lib().mref_brfs(task._h, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096)
+    L = max(1, task.label_width)
+    cap = 4096
+    ps = np.zeros(cap, np.int32)
+    pb = np.zeros((cap, L), np.int32)
+    gs = np.zeros(max(1, task.words) + 64, np.uint64)
+    n = lib().mref_brfs(task._h, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ps.ctypes.data, pb.ctypes.data, L, cap,
+                        gs.ctypes.data, gs.size)
     if n < 0:
         raise RuntimeError(_err())
-    return {
+    out = {
         "states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.goal_states,
         "fingerprint": r.fingerprint, "layers": r.layers, "status": r.status, "solved": bool(r.solved),
-        "exhausted": bool(r.exhausted), "seconds": r.seconds, "layer_counts": lc[:n].tolist(),
+        "exhausted": bool(r.exhausted), "seconds": r.seconds, "layer_counts": lc[:n].tolist(), "pruned": r.pruned,
     }
+    if r.solved:
+        k = min(r.plan_len, cap)
+        out["plan"] = [[int(ps[i])] + [int(x) for x in pb[i] if x >= 0] for i in range(k)]
+        out["cost"] = r.cost
+        out["goal_state"] = [f"{int(x):016x}" for x in gs[:min(r.goal_words, gs.size)]]
+    return out
+
+
+def dedup_flat(rows: np.ndarray) -> tuple[int, float]:
+    """Unique count and insert seconds of the reference FlatStateStore over rows [n, words] (one thread)."""
+    rows = np.ascontiguousarray(rows, dtype=np.uint64)
+    u, s = c_uint64(), c_double()
+    if lib().mref_dedup_flat(rows.ctypes.data, rows.shape[0], rows.shape[1], ctypes.byref(u), ctypes.byref(s)) != 0:
+        raise RuntimeError(_err())
+    return u.value, s.value
+
+
+def dedup_concurrent(rows: np.ndarray, threads: int, batch: int = 1 << 20) -> tuple[int, float]:
+    """Unique count and insert seconds of the reference ConcurrentStateStore over rows [n, words] on `threads`
+    threads, in batches of `batch` rows."""
+    rows = np.ascontiguousarray(rows, dtype=np.uint64)
+    u, s = c_uint64(), c_double()
+    if lib().mref_dedup_concurrent(rows.ctypes.data, rows.shape[0], rows.shape[1], threads, batch, ctypes.byref(u), ctypes.byref(s)) != 0:
+        raise RuntimeError(_err())
+    return u.value, s.value
 
 
 def hash_words(w: np.ndarray, seed: int = 0x2D358DCCAA6C78A5) -> int:

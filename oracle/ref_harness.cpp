@@ -11,6 +11,8 @@
 //   env step / reset      rl::HostEnv                    include/mymyr/rl/env.hpp:181-278
 //   env pool              rl::CpuEnvPool                 include/mymyr/rl/pool.hpp:114-172
 //   BrFS                  brfs(Task, BrfsOptions)        include/mymyr/search/brfs.hpp:140
+//   dedup                 FlatStateStore::insert         include/mymyr/state/flat_store.hpp:44-115
+//                         ConcurrentStateStore::insert   include/mymyr/state/concurrent_store.hpp:79-177
 // Errors: functions return a negative value (or null) and mref_last_error() holds the message.
 
 #include "mymyr/core/hash.hpp"
@@ -21,11 +23,16 @@
 #include "mymyr/rl/task_suite.hpp"
 #include "mymyr/rl/task_table.hpp"
 #include "mymyr/rl/visited.hpp"
+#include "mymyr/core/team.hpp"
 #include "mymyr/search/brfs.hpp"
+#include "mymyr/state/concurrent_store.hpp"
+#include "mymyr/state/flat_store.hpp"
 #include "mymyr/successor/successors.hpp"
 #include "mymyr/task/task.hpp"
 #include "mymyr/task/workspace.hpp"
 
+#include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cstdint>
 #include <cstring>
@@ -97,6 +104,7 @@ struct mref_brfs_options
     int32_t canonical_order;
     int32_t stop_at_goal;
     int32_t fingerprint;
+    uint64_t max_expanded;
 };
 
 struct mref_brfs_result
@@ -107,6 +115,10 @@ struct mref_brfs_result
     int32_t solved;
     int32_t exhausted;
     double seconds;
+    double cost;
+    uint64_t pruned;
+    uint32_t plan_len;  // actions of the plan (those past plan_cap are not written)
+    uint32_t goal_words;  // words of goal_state (0: none)
 };
 
 const char* mref_last_error() { return g_error.c_str(); }
@@ -682,7 +694,11 @@ int mref_pool_run(mref_task* t, const mref_env_config* c, uint32_t num_envs, uin
 }
 
 // BrFS over the task; layer_counts [cap, 3] receives {expanded, generated, new} per expanded layer.
-int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uint64_t* layer_counts, uint32_t cap)
+// plan_schema [plan_cap], plan_binding [plan_cap, binding_width], goal_state [goal_cap] (all optional): the plan's
+// actions as (schema, objects padded with -1) and the goal state's words.
+int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uint64_t* layer_counts, uint32_t cap,
+              int32_t* plan_schema, int32_t* plan_binding, uint32_t binding_width, uint32_t plan_cap, uint64_t* goal_state,
+              uint32_t goal_cap)
 {
     return guarded(
         [&]() -> int
@@ -691,6 +707,7 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
             b.threads = o->threads;
             b.max_depth = o->max_depth;
             b.max_states = o->max_states;
+            b.max_expanded = o->max_expanded;
             b.witness_pruning = o->witness_pruning != 0;
             b.canonical_order = o->canonical_order != 0;
             b.stop_at_goal = o->stop_at_goal != 0;
@@ -708,10 +725,99 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
             r->status = static_cast<int32_t>(x.status);
             r->solved = x.solved;
             r->exhausted = x.exhausted;
+            r->cost = x.cost;
+            r->pruned = x.pruned;
+            r->plan_len = static_cast<uint32_t>(x.plan.size());
+            for (u32 i = 0; i < x.plan.size() && i < plan_cap; ++i)
+            {
+                const Action& a = x.plan[i];
+                if (plan_schema)
+                    plan_schema[i] = static_cast<int32_t>(a.schema.v);
+                if (plan_binding)
+                    for (u32 k = 0; k < binding_width; ++k)
+                        plan_binding[static_cast<usize>(i) * binding_width + k] =
+                            k < a.binding.size() ? static_cast<int32_t>(a.binding[k].v) : -1;
+            }
+            r->goal_words = 0;
+            if (x.goal_state)
+            {
+                const StateView g = x.goal_state->view();
+                r->goal_words = g.nw;
+                for (u32 w = 0; w < g.nw && w < goal_cap && goal_state; ++w)
+                    goal_state[w] = g.w[w];
+            }
             for (u32 i = 0; i < x.layer_counts.size() && i < cap; ++i)
                 for (u32 j = 0; j < 3; ++j)
                     layer_counts[i * 3 + j] = x.layer_counts[i][j];
             return static_cast<int>(x.layer_counts.size());
+        },
+        -1);
+}
+
+
+// Inserts rows [n, words] into the reference's FlatStateStore (single-threaded, grown at 70% load); unique = states
+// stored. seconds: the inserts alone.
+int mref_dedup_flat(const uint64_t* rows, uint64_t n, uint32_t words, uint64_t* unique, double* seconds)
+{
+    return guarded(
+        [&]() -> int
+        {
+            FlatStateStore store(words, 16);
+            const auto t0 = std::chrono::steady_clock::now();
+            for (uint64_t i = 0; i < n; ++i)
+                store.insert(rows + i * words, words);
+            *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            *unique = store.size();
+            return 0;
+        },
+        -1);
+}
+
+// Inserts rows [n, words] into the reference's ConcurrentStateStore on `threads` threads, in batches of `batch` rows
+// (each thread a contiguous slice of the batch; the store's stop-the-world rehash between batches when it asks for
+// one, and inside a batch a thread stops at the request until the batch ends and the rehash ran). unique = states
+// stored; seconds: the inserts and rehashes.
+int mref_dedup_concurrent(const uint64_t* rows, uint64_t n, uint32_t words, uint32_t threads, uint64_t batch,
+                          uint64_t* unique, double* seconds)
+{
+    return guarded(
+        [&]() -> int
+        {
+            Team team(threads);
+            const u32 T = team.size();
+            ConcurrentStateStore store(T);
+            std::vector<uint64_t> next(T);
+            std::atomic<uint64_t> stored{0};
+            const auto t0 = std::chrono::steady_clock::now();
+            for (uint64_t b0 = 0; b0 < n; b0 += batch)
+            {
+                const uint64_t b1 = std::min(n, b0 + batch);
+                for (u32 t = 0; t < T; ++t)
+                    next[t] = b0 + (b1 - b0) * t / T;
+                for (;;)
+                {
+                    team.run(
+                        [&](u32 t)
+                        {
+                            const uint64_t end = b0 + (b1 - b0) * (t + 1) / T;
+                            uint64_t i = next[t], added = 0;
+                            for (; i < end && !store.wants_rehash(); ++i)
+                                added += store.insert(t, rows + i * words, words, i).second ? 1 : 0;
+                            next[t] = i;
+                            stored.fetch_add(added, std::memory_order_relaxed);
+                        });
+                    bool done = true;
+                    for (u32 t = 0; t < T; ++t)
+                        done = done && next[t] >= b0 + (b1 - b0) * (t + 1) / T;
+                    if (store.wants_rehash())
+                        store.rehash(team);
+                    if (done)
+                        break;
+                }
+            }
+            *seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            *unique = stored.load();
+            return 0;
         },
         -1);
 }

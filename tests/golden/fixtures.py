@@ -213,3 +213,10 @@ def given_actions(u, count) -> np.ndarray:
     """The given policy's actions: uniform over [-1, count] (so some are invalid: -1 and count)."""
     c = np.asarray(count, np.int64)
     return np.floor(np.asarray(u) * (c + 2)).astype(np.int64) - 1
+
+
+# The dedup workload at its stated size: 2^26 rows of 16 words from the seeded stream (seed 0, 30% duplicates), inserted
+# in 2^20-row batches. Its exact unique count is the number of the stream's fresh rows (a duplicate copies an earlier
+# row, which resolves to a fresh one); tests/test_oracle.py recounts it from the generator's closed form.
+DEDUP_WORKLOAD = {"rows": 1 << 26, "words": 16, "seed": 0, "dup": 0.3, "batch": 1 << 20, "unique": 46975112}
+

@@ -150,10 +150,17 @@ def make_env():
     dump("env_gridworld.json", env_trajectory(g, g.num_envs, g.steps))
     dump("env_transport.json", env_trajectory(workloads.TRANSPORT, 2048, 64))
     dump("env_transport_xl.json", env_trajectory(workloads.TRANSPORT_XL, 128, 32))
+    make_env_long()
     # small instances with goals, truncation and dead ends reached often
     small = workloads.EnvWorkload("gridworld", 256, 200, {"seed": 3, "max_steps": 40, "step_reward": -1.0, "goal_reward": 5.0})
     dump("env_gridworld_truncated.json", env_trajectory(small, 256, 200))
     make_env_small()
+
+
+def make_env_long():
+    # the transport workloads over their whole horizons (512 and 128 steps) on their first rows
+    dump("env_transport_long.json", env_trajectory(workloads.TRANSPORT, 256, workloads.TRANSPORT.steps))
+    dump("env_transport_xl_long.json", env_trajectory(workloads.TRANSPORT_XL, 64, workloads.TRANSPORT_XL.steps))
 
 
 def make_env_small():
@@ -302,9 +309,13 @@ def make_visited_mask():
     dump("visited_mask.json", out)
 
 
-def brfs_record(name, atoms="auto", **kw):
+def brfs_record(name, atoms="auto", ref_threads=1, **kw):
+    """The reference brfs() on a task; `options` holds the BrfsOptions a device search repeats. Cuts are recorded
+    from the default single-threaded search (threads=1, the flat store for these widths): the reference's multi-threaded
+    search gives the same ids and counts on whole layers (tests/cpp/search/test_brfs.cpp:113-141) but not at a
+    max_states cut, where it neither records the cut layer nor stores the same states."""
     t = ref.RefTask(fx.task_path(name), atoms)
-    r = ref.brfs(t, **kw)
+    r = ref.brfs(t, threads=ref_threads, **kw)
     r.pop("seconds")
     r["options"] = kw
     return r
@@ -318,12 +329,17 @@ def make_brfs(quick: bool):
         out["suite"][name] = brfs_record(name, stop_at_goal=False)
         out["budget"][name] = brfs_record(name, stop_at_goal=False, max_states=20000)
         out["budget"][name + ":goal"] = brfs_record(name, stop_at_goal=True)
+        out["budget"][name + ":expanded"] = brfs_record(name, stop_at_goal=False, max_expanded=3000)
         print(name, out["suite"][name]["states"], flush=True)
-    for ms in ([1 << 20] if quick else [1 << 20, 1 << 22, 1 << 24]):
-        out["strips"][str(ms)] = brfs_record("strips", "dense", max_depth=12, max_states=ms, stop_at_goal=False)
+    for ms in ([1 << 20] if quick else [1 << 20, 1 << 22, 1 << 24, 1 << 26]):
+        out["strips"][str(ms)] = brfs_record("strips", "dense", max_depth=12, max_states=ms,
+                                             stop_at_goal=False)
         print("strips", ms, flush=True)
     out["strips"]["depth3"] = brfs_record("strips", "dense", max_depth=3, stop_at_goal=False)
-    out["strips"]["expanded5000"] = brfs_record("strips", "dense", max_depth=12, max_states=1 << 22, stop_at_goal=False)
+    out["strips"]["expanded5000"] = brfs_record("strips", "dense", max_depth=12, max_expanded=5000, stop_at_goal=False)
+    out["strips"]["expanded300000"] = brfs_record("strips", "dense", max_depth=12, max_expanded=300000,
+                                                  stop_at_goal=False)
+    out["strips"]["goal"] = brfs_record("strips", "dense", max_depth=12, max_states=1 << 24, stop_at_goal=True)
     dump("brfs.json", out)
 
 
@@ -334,7 +350,7 @@ def main():
     a = ap.parse_args()
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
-             "env_small": make_env_small, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
+             "env_small": make_env_small, "env_long": make_env_long, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

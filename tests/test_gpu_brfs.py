@@ -12,15 +12,34 @@ KEYS = ["states", "expanded", "generated", "goal_states", "layers", "fingerprint
 STATUS = {0: "solved", 1: "exhausted", 2: "out_of_states"}
 
 
-def device(golden, name, atoms="auto", **kw):
+def device(golden, name, atoms="auto", full=False, **kw):
     from mymyr_amd import search
     from mymyr_amd.task import Task
 
     t = Task.from_text_file(golden.task_path(name), atoms)
     r = search.brfs(t, fingerprint=True, **kw)
-    return {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
-            "layers": r.layers, "fingerprint": r.fingerprint, "status": r.status, "layer_counts": r.layer_counts,
-            "exhausted": r.exhausted, "solved": r.solved}
+    out = {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
+           "layers": r.layers, "fingerprint": r.fingerprint, "status": r.status, "layer_counts": r.layer_counts,
+           "exhausted": r.exhausted, "solved": r.solved}
+    if full:
+        out["result"] = r
+    return out
+
+
+def trimmed_hex(words):
+    w = [int(x, 16) if isinstance(x, str) else int(x) for x in words]
+    while w and w[-1] == 0:
+        w.pop()
+    return w
+
+
+def same_plan(r, exp):
+    """The device's plan, cost and goal state against the reference's (BrfsResult::plan, cost, goal_state)."""
+    res = r["result"]
+    if not exp["solved"]:
+        return res.plan == [] and res.cost == 0.0 and res.goal_state is None
+    return ([[a.schema, *a.binding] for a in res.plan] == exp["plan"] and res.cost == exp["cost"] and
+            trimmed_hex(res.goal_state) == trimmed_hex(exp["goal_state"]))
 
 
 def same(r, exp):
@@ -50,12 +69,39 @@ def test_reference_determinism_digests(golden, name):
 
 
 def test_budget_and_goal_stops(golden):
+    """max_states and max_expanded cuts and goal stops of the suite: counts, statuses and fingerprints, and for the
+    solved searches the plan (the first discoveries from the start state to the first goal state), its cost and the
+    goal state, all equal to the reference's."""
     g = golden.load("brfs.json")["budget"]
+    solved = 0
     for key, exp in g.items():
         name = key.split(":")[0]
         kw = dict(exp["options"])
-        r = device(golden, name, **kw)
+        r = device(golden, name, full=True, **kw)
         assert not same(r, exp), (key, same(r, exp))
+        assert same_plan(r, exp), (key, r["result"].plan[:4], exp.get("plan", [])[:4])
+        solved += bool(exp["solved"])
+    assert solved >= 10
+
+
+def test_plan_replays_to_the_goal_state(golden):
+    """A device plan applied step by step with the oracle's successor function from the initial state reaches the
+    reported goal state, which satisfies the goal; every step is an applicable action of the state before it."""
+    from mymyr_amd.task import Task
+    from oracle import port
+
+    for name in ("gripper__prob05", "depot__p02", "logistics00__probLOGISTICS-6-1"):
+        text = open(golden.task_path(name)).read()
+        r = device(golden, name, full=True, stop_at_goal=True)["result"]
+        assert r.solved and len(r.plan) == r.cost > 0
+        pt = port.Task(text)
+        row = pt.initial
+        for a in r.plan:
+            nxt = [s for (sc, b, s) in port.successors(pt, row) if sc == a.schema and tuple(b[: len(a.binding)]) == a.binding]
+            assert len(nxt) == 1, (name, a)
+            row = nxt[0]
+        assert trimmed_hex(row) == trimmed_hex(r.goal_state)
+        assert port.is_goal(pt, row)
 
 
 def test_strips_workload_cuts(golden):

@@ -17,23 +17,29 @@ def host(t):
     return t.cpu().numpy()
 
 
-def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0, **pool_kw):
-    from mymyr_amd import rl, workloads
+def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0, on_step=None, **pool_kw):
+    """Steps num_envs envs (default: the fixture's rows) for the fixture's steps and compares the first rows' per-step
+    digests with the reference's; on_step(k, outputs) sees each step's outputs (device tensors over every env)."""
+    from mymyr_amd import rl
     from mymyr_amd.task import Task
 
     g = golden.load(fixture)
     atoms = "dense" if g["workload"] == "strips" else "auto"
     t = Task.from_text_file(golden.task_path(g["workload"]), atoms)
     n = num_envs or g["rows"]
+    print(f"{fixture}: {n} envs x {g['steps']} steps", flush=True)
     pool = rl.DeviceEnvPool(t, n, **g["env"], **pool_kw)
     pool.reset()
     rows = g["rows"]
+    L = max(1, t.label_width)
     for k in range(g["steps"]):
         o = pool.step(encode=encode)
-        d = golden.step_digest(rows, host(o["states"]).view(np.uint64), host(o["reward"]), host(o["terminated"]),
-                               host(o["truncated"]), host(o["count"]), host(o["schema"]), host(o["binding"])[:, : max(1, t.label_width)],
-                               host(o["goal"]))
+        h = {key: host(o[key][:rows]) for key in ("states", "reward", "terminated", "truncated", "count", "schema", "binding", "goal")}
+        d = golden.step_digest(rows, h["states"].view(np.uint64), h["reward"], h["terminated"], h["truncated"], h["count"], h["schema"],
+                               h["binding"][:, :L], h["goal"])
         assert d == g["digests"][k], f"{fixture}: step {k} differs from the reference"
+        if on_step:
+            on_step(k, o)
     pool.check()
     return pool, t
 
@@ -57,6 +63,51 @@ def test_transport_full_batch_first_rows(golden):
 def test_transport_xl_first_rows_with_encoding(golden):
     """transport_xl with the encoding outputs on; the first rows match the reference's trajectory."""
     pool, t = run_env(golden, "env_transport_xl.json", num_envs=4096, encode=600)
+
+
+def test_transport_whole_horizon_full_batch(golden):
+    """The transport workload as run: 65536 envs for all 512 steps; the first 256 rows match the reference every step."""
+    run_env(golden, "env_transport_long.json", num_envs=65536)
+
+
+def reference_masks(rt, row):
+    """Per schema, whether the compiled reference generates a successor with it (rl::schema_masks semantics)."""
+    m = np.zeros(rt.num_schemas, np.uint8)
+    sc, _, _ = rt.successors(row)
+    m[np.asarray(sc, dtype=np.int64)] = 1
+    return m
+
+
+def test_transport_xl_full_workload_with_encoding(golden):
+    """The transport_xl workload as run: 262144 envs for all 128 steps with the encoding at the task's atom count (every
+    state holds 544 true atoms: 32 trucks and 512 packages, one position each). The first 64 rows match the
+    reference's trajectory every step; on sampled rows of the whole batch (the last rows included) at several steps,
+    the atom indices are the state's set slots in ascending order, padded with -1 (the closed form of State::slots),
+    and the schema masks equal the schemas of the compiled reference's successor listing of that state."""
+    from oracle import port, ref
+
+    rt = ref.RefTask(golden.task_path("transport_xl"))
+    max_atoms = 544
+    N = 262144
+    sample = np.array([0, 1, 63, 64, 1000, 65535, 131072, 200001, N - 2, N - 1])
+    idx = torch.as_tensor(sample, device="cuda")
+    checked = []
+
+    def on_step(k, o):
+        if k % 37 not in (0, 36) and k != 127:
+            return
+        states = host(o["states"].index_select(0, idx)).view(np.uint64)
+        atoms = host(o["atoms"].index_select(0, idx))
+        masks = host(o["masks"].index_select(0, idx))
+        for i in range(len(sample)):
+            row = states[i, : rt.words]
+            assert int(np.unpackbits(row.view(np.uint8)).sum()) == max_atoms
+            assert np.array_equal(atoms[i], port.encode_atoms(row, max_atoms)), (k, int(sample[i]))
+            assert np.array_equal(masks[i], reference_masks(rt, row)), (k, int(sample[i]))
+        checked.append(k)
+
+    pool, t = run_env(golden, "env_transport_xl_long.json", num_envs=N, encode=max_atoms, on_step=on_step)
+    assert len(checked) >= 6
 
 
 def test_encoding_closed_form(golden):

@@ -105,6 +105,33 @@ def test_state_set_dedup_closed_form_large():
     assert new == fresh == len(s)
 
 
+def test_state_set_dedup_workload_full_size():
+    """The dedup workload at its stated size: 2^26 rows of 1024 bits, about 30% duplicates, in 2^20-row batches into a
+    table at load 0.5 (a 1 GiB table and an 8.6 GB arena, so row and slot offsets pass 2^32 bytes). The unique count is
+    exact (the stream's fresh rows); inserting a batch again adds nothing and finds the ids of its first insert."""
+    from mymyr_amd import hip
+    from tests.golden import fixtures as fx
+
+    w = fx.DEDUP_WORKLOAD
+    total, batch = w["rows"], w["batch"]
+    print(f"dedup workload: {total} rows in batches of {batch}", flush=True)
+    s = hip.StateSet(total, w["words"], 0.5, batch=batch)
+    new = 0
+    again = {}
+    for b in range(0, total, batch):
+        keep = b in (0, total // 2, total - batch)
+        n, ids, _ = s.insert(hip.dedup_rows(b, batch, w["words"], seed=w["seed"], dup=w["dup"]), want_ids=keep)
+        if keep:
+            again[b] = ids.cpu().numpy()
+        new += n
+    assert new == w["unique"] == len(s)
+    for b, ids in again.items():
+        n2, ids2, is_new2 = s.insert(hip.dedup_rows(b, batch, w["words"], seed=w["seed"], dup=w["dup"]))
+        assert n2 == 0 and not bool(is_new2.any())
+        assert np.array_equal(ids2.cpu().numpy(), ids)
+        assert ids.min() >= 0 and ids.max() < w["unique"]
+
+
 def test_state_set_errors():
     from mymyr_amd import hip
     from mymyr_amd._lib import MyaError

@@ -109,6 +109,28 @@ def test_brfs_golden_budget(golden):
             assert r[k] == exp[k], (name, k)
 
 
+def test_dedup_workload_unique_count_closed_form():
+    """The dedup workload's unique count at its full size (2^26 rows): the generator's fresh rows, counted in chunks."""
+    from tests.golden import fixtures as fx
+
+    w = fx.DEDUP_WORKLOAD
+    fresh = 0
+    for b in range(0, w["rows"], 1 << 22):
+        fresh += int(gen.dedup_is_fresh(np.arange(b, b + (1 << 22), dtype=np.uint64), seed=w["seed"], dup=w["dup"]).sum())
+    assert fresh == w["unique"]
+
+
+def test_dedup_stream_against_reference_store():
+    """The reference FlatStateStore stores exactly the stream's fresh rows (2^18 rows of the workload's stream)."""
+    from oracle import ref
+
+    if not ref.available():
+        pytest.skip("reference build missing")
+    rows = gen.dedup_rows(0, 1 << 18, 16, seed=0)
+    unique, _ = ref.dedup_flat(rows)
+    assert unique == int(gen.dedup_is_fresh(np.arange(1 << 18, dtype=np.uint64), seed=0).sum())
+
+
 def test_dedup_closed_form():
     rows = gen.dedup_rows(0, 4000, 16, seed=5)
     n, ids = port.dedup_unique(rows)
