@@ -354,6 +354,17 @@ int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t w
 int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids, uint64_t rows, uint32_t words,
                    const mya_expand_options* options, mya_expansion* out, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code in tight serving loops,
+ * harnesses that forbid hipMalloc). mya_expand over at most MYA_EXPAND_NOALLOC_MAX_ROWS rows with the same arguments,
+ * outputs and errors, and no device allocation or free: the expansion's scratch (about 7 MiB) is a static device array
+ * that each device the library runs on holds until the process ends. The task must already have its device image on
+ * the current device (any earlier call with the task that reaches the device, e.g. mya_expand of 0 rows, uploads it).
+ * Calls are serialized within a process; they share the one array per device, so concurrent calls of several processes
+ * on one device are not supported. Synchronous on `stream`, as mya_expand. */
+#define MYA_EXPAND_NOALLOC_MAX_ROWS 262144u
+int mya_expand_noalloc(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, const mya_expand_options* options,
+                       mya_expansion* out, void* stream);
+
 /* PaddedExpansion (include/mymyr/rl/expand.hpp:162-181) without numeric and derived words: the [rows, k] view of a flat
  * expansion. Device arrays; a null array is not written. index [rows, k] (flat row, -1 padding), mask [rows, k],
  * count [rows] (the true successor counts, which may exceed k), succ [rows, k, words] (zero padding), schema (-1),

@@ -268,6 +268,7 @@ def _load() -> ctypes.CDLL:
         "mya_encode_atoms": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_uint32, c_void_p]),
         "mya_schema_masks": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p]),
         "mya_expand": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion), c_void_p]),
+        "mya_expand_noalloc": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion), c_void_p]),
         "mya_env_expand": (c_int, [c_void_p, c_void_p, c_void_p, c_uint64, c_uint32, POINTER(ExpandOptions), POINTER(Expansion),
                                    c_void_p]),
         "mya_visited_mask": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_uint64, c_uint64, c_void_p,
