@@ -10,8 +10,10 @@ reported under "workloads", each with env-steps/s (or rows/s) and the achieved H
 
 roofline: the dominant kernel class of the BrFS (by summed HIP-event time on the search's own stream): its
 algorithmic bytes (per launch, summed) / its summed duration, against the 8 TB/s HBM peak of MI355X.
-cpu_baseline: the reference's own CPU BrFS (oracle/_ref: ParallelBrfs with deterministic ids) on a bounded sample of
-the same task, timed on this host's cores.
+cpu_baseline: the reference's own CPU code (oracle/_ref, compiled from the reference's sources) on a bounded sample of
+the same workload, on every core allotted to this job (the CPU share of one GPU: OMP_NUM_THREADS when set, else the
+process's CPU affinity); `host` reports nproc, the affinity and the CPU model beside it. BrFS: ParallelBrfs with
+deterministic ids; env pools: CpuEnvPool; dedup: ConcurrentStateStore (and FlatStateStore on one core).
 """
 
 from __future__ import annotations
@@ -29,12 +31,35 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "env steps/sec + BrFS expanded states/sec on 1 GPU; % of HBM roofline"
 
 
-def cpu_threads() -> int:
+def affinity() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+def cpu_threads() -> int:
+    """The cores allotted to this job: OMP_NUM_THREADS when the launcher sets it (a GPU box's CPU share per GPU), else
+    every core of the process's affinity."""
+    try:
+        n = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        n = 0
+    return max(1, min(n, affinity()) if n > 0 else affinity())
+
+
+def host_info() -> dict:
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": affinity(), "threads_used": cpu_threads(), "cpu_model": model,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
 def load_traffic(kernel: str):
@@ -105,10 +130,11 @@ def cpu_strips(path, w):
     r = ref.brfs(rt, threads=T, max_depth=w.max_depth, max_states=sample, stop_at_goal=False, fingerprint=False)
     return {"value": r["expanded"] / r["seconds"], "unit": "expanded states/s", "cores": T, "kind": "reference",
             "sample": f"reference ParallelBrfs (deterministic ids) on the strips task, depth 12, max_states 2^22: "
-                      f"{r['expanded']} expanded, {r['generated']} generated in {r['seconds']:.2f} s"}
+                      f"{r['expanded']} expanded, {r['generated']} generated in {r['seconds']:.2f} s", "host": host_info()}
 
 
 def bench_env(name: str, steps: int, warmup: int, cpu: bool, num_envs: int | None = None):
+    import numpy as np
     import torch
 
     from mymyr_amd import rl, workloads
@@ -118,7 +144,9 @@ def bench_env(name: str, steps: int, warmup: int, cpu: bool, num_envs: int | Non
     path = workloads.task_file(name, os.path.join(ROOT, "tests", "golden", "tasks"))
     t = Task.from_text_file(path, w.atoms)
     N = num_envs or w.num_envs
-    encode = 600 if w.encode else 0
+    # the encoding's width: the task's true-atom count per state (transport: one position per truck and package; every
+    # state of the task holds the initial state's count)
+    encode = int(np.unpackbits(t.initial_state().view(np.uint8)).sum()) if w.encode else 0
     pool = rl.DeviceEnvPool(t, N, **w.env)
     pool.reset()
     for _ in range(warmup):
@@ -138,7 +166,7 @@ def bench_env(name: str, steps: int, warmup: int, cpu: bool, num_envs: int | Non
     per_step = 2 * R + 36 + (encode * 4 + t.num_schemas if encode else 0)
     achieved = per_step * N / (kms * 1e-3) / 1e9
     out = {"env_steps_per_s": N * steps / wall, "num_envs": N, "steps_timed": steps, "ms_per_step": wall * 1e3 / steps,
-           "words": t.words, "bytes_per_env_step": per_step,
+           "words": t.words, "bytes_per_env_step": per_step, "encode_atoms": encode,
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "env step", "ms_per_launch": round(kms, 4),
                         "traffic": load_traffic(f"env_{name}")}}
@@ -157,7 +185,7 @@ def cpu_env(path, w):
     n, k = {"gridworld": (1024, 256), "transport": (16384, 16), "transport_xl": (4096, 4)}[w.name]
     secs, _ = ref.pool_run(rt, n, T, k, **w.env)
     return {"value": n * k / secs, "unit": "env steps/s", "cores": T, "kind": "reference",
-            "sample": f"reference CpuEnvPool, {n} envs x {k} steps, {T} worker threads"}
+            "sample": f"reference CpuEnvPool, {n} envs x {k} steps, {T} worker threads", "host": host_info()}
 
 
 def bench_dedup(steps: int, warmup: int, cpu: bool):
@@ -191,16 +219,28 @@ def bench_dedup(steps: int, warmup: int, cpu: bool):
                         "bytes_per_launch": int(alg / nb), "ms_per_launch": round(wall * 1e3 / nb, 4),
                         "traffic": load_traffic("dedup_batch")}}
     if cpu:
-        from oracle import port
-
-        sample = 1 << 16
-        r = gen.dedup_rows(0, sample, words, seed=workloads.SEED, dup=workloads.DEDUP_DUP)
-        t0 = time.perf_counter()
-        port.dedup_unique(r)
-        dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": sample / dt, "unit": "rows/s", "cores": 1, "kind": "port",
-                               "sample": f"oracle restatement (dict-based first-occurrence ids), {sample} rows"}
+        out["cpu_baseline"] = cpu_dedup(words)
     return out
+
+
+def cpu_dedup(words: int):
+    """The reference's concurrent store (the store of its multi-threaded searches) on the workload's first 2^23 rows in
+    2^20-row batches, on the job's cores; the single-threaded flat store on the first 2^21 rows beside it."""
+    from mymyr_amd import gen, workloads
+    from oracle import ref
+
+    if not ref.available():
+        return None
+    T = cpu_threads()
+    sample = 1 << 23
+    rows = gen.dedup_rows(0, sample, words, seed=workloads.SEED, dup=workloads.DEDUP_DUP)
+    unique, secs = ref.dedup_concurrent(rows, T, workloads.DEDUP_BATCH)
+    flat_n = 1 << 21
+    flat_unique, flat_secs = ref.dedup_flat(rows[:flat_n])
+    return {"value": sample / secs, "unit": "rows/s", "cores": T, "kind": "reference",
+            "sample": f"reference ConcurrentStateStore, the dedup stream's first {sample} rows of {words} words in 2^20-row "
+                      f"batches on {T} threads: {unique} unique in {secs:.3f} s; reference FlatStateStore on one core, "
+                      f"first {flat_n} rows: {flat_n / flat_secs:.4g} rows/s", "host": host_info()}
 
 
 def copy_calibration(steps: int):
