@@ -326,10 +326,10 @@ constexpr int kPairs = W >= 4 ? 2 : 1;  // word pairs per lane
 
 // Candidates [0, m) of a chunk into the state set: a group of lanes per candidate forms its row, hashes it and probes
 // the table (a stored equal row drops it; a pending equal row takes part in the smallest-index rule; an empty slot
-// takes it as pending).
+// takes it as pending). Losers' flags are cleared, winners' stay 1.
 template<int W>
-__global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W> src, u64 m, u64* __restrict__ cand_slot,
-                                                      u8* __restrict__ flags, u32* __restrict__ status)
+__global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W> src, u64 m, u8* __restrict__ flags,
+                                                      u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
     const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
@@ -340,12 +340,8 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     src.load(j, q, me);
     const u64 h = group_hash<G, kPairs<W>>(me, q, gbase);
     const ProbeResult r = probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, flags, status);
-    if (q == 0)
-    {
-        cand_slot[j] = r.cand_slot;
-        if (r.lose)
-            flags[j] = 0;
-    }
+    if (q == 0 && r.lose)
+        flags[j] = 0;
 }
 
 // The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena
@@ -358,25 +354,41 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
                                                        u64* __restrict__ nodes, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
+    constexpr int K = kPairs<W>;
+    constexpr int kBatch = 4;  // winners per group in flight (the list, record and row loads of each are independent)
     const u32 q = lane_id() % G;
     const u64 id0 = *size_now;
     const u64 winners = min(m, *size_next - id0);
+    const u64 stride = static_cast<u64>(gridDim.x) * (kLB / G);
     // a grid sized for the whole chunk would mostly start waves that find no winner: a bounded grid strides instead
-    for (u64 w = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G; w < winners; w += static_cast<u64>(gridDim.x) * (kLB / G))
+    for (u64 w0 = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G; w0 < winners; w0 += kBatch * stride)
     {
-        const u64 id = id0 + w;
-        if (id >= limit)
+        u64 pa[kBatch];
+        bool live[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
         {
-            if (q == 0)
+            const u64 w = w0 + b * stride;
+            live[b] = w < winners && id0 + w < limit;
+            if (w < winners && id0 + w >= limit && q == 0)
                 atomicOr(status, kStatusCapacity);
-            continue;
+            pa[b] = live[b] ? list[w] : 0;
         }
-        const u64 pa = src.cand_pa[list[w]];
-        Slice<G, kPairs<W>> r;
-        src.template load_pa<G, kPairs<W>>(pa, q, r);
-        store_row<G, kPairs<W>>(s.arena + id * W, W, q, r);
-        if (q == 0)
-            nodes[id] = ((src.first + (pa >> 32)) << 32) | static_cast<u32>(pa);
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+            pa[b] = live[b] ? src.cand_pa[pa[b]] : 0;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+        {
+            if (!live[b])
+                continue;
+            const u64 id = id0 + w0 + b * stride;
+            Slice<G, K> r;
+            src.template load_pa<G, K>(pa[b], q, r);
+            store_row<G, K>(s.arena + id * W, W, q, r);
+            if (q == 0)
+                nodes[id] = ((src.first + (pa[b] >> 32)) << 32) | static_cast<u32>(pa[b]);
+        }
     }
 }
 
@@ -898,8 +910,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 tm.end(kKEmit, np * (R + 8) + m * 8);
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
-                hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.cand_slot,
-                                   set.flags, set.d_status);
+                hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.flags,
+                                   set.d_status);
                 launch_check("ground insert");
                 tm.end(kKInsert, 0);
                 tm.begin(kKRank);

@@ -66,7 +66,8 @@ __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __
     const ProbeResult r = probe_insert<G, K>(s, src, j, me, h, q, gbase, flags, status);
     if (q == 0)
     {
-        cand_slot[j] = r.cand_slot;
+        if (cand_slot)
+            cand_slot[j] = r.cand_slot;
         if (r.lose)
             flags[j] = 0;
     }
@@ -342,8 +343,9 @@ void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new,
             const u64 m = std::min(n - done, s.batch_cap);
             const u64* r = rows + done * W;
             state_set_begin_batch(s, stream);
-            hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, s.cand_slot, s.flags,
-                               s.d_status);
+            // the probe results are kept only for the ids
+            hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, ids ? s.cand_slot : nullptr,
+                               s.flags, s.d_status);
             launch_check("state set probe");
             state_set_rank(s, m, stream, is_new ? is_new + done : nullptr);
             hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, s.list,
