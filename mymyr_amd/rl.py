@@ -78,6 +78,40 @@ class InstanceSampler:
                                          thr.ctypes.data, idx.ctypes.data, len(idx)))
 
 
+class PoolBatch(dict):
+    """The results of one or more sends, or of a reset (PoolBatch, include/mymyr/rl/pool.hpp:92-112): device tensors of
+    B rows in the order of their env ids, under the reference's field names (env_ids, states, task_ids, count, steps,
+    at_goal, goal, terminated and, for a send's batch, reward, truncated, invalid, final_states, schema, binding,
+    revisited; goal_pos / goal_neg with per-env goals); the fields are also attributes. `step` tells a send's batch
+    from a reset's; `rows`, `words` and `label_width` give its shape."""
+
+    def __init__(self, fields: dict, rows: int, words: int, label_width: int, step: bool, goals: bool):
+        super().__init__(fields)
+        self.rows, self.words, self.label_width, self.step, self.goals = rows, words, label_width, step, goals
+
+    def __getattr__(self, name):
+        try:
+            return self[name]
+        except KeyError:
+            raise AttributeError(name) from None
+
+
+def resolve_sampler(sampler, instances: int) -> InstanceSampler | None:
+    """The pool's instance sampling from a `sampler` argument, as the reference resolves it
+    (python/mymyr/rl/_sampling.py: _instance_sampler): "auto" and "uniform" are uniform over the instances, None is
+    none, an InstanceSampler must cover the table; over one instance there is nothing to sample."""
+    if isinstance(sampler, str):
+        if sampler not in ("auto", "uniform"):
+            raise ValueError("mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None")
+        sampler = InstanceSampler(instances)
+    if sampler is not None:
+        if not isinstance(sampler, InstanceSampler):
+            raise TypeError("mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None")
+        if sampler.num_instances != instances:
+            raise ValueError(f"mymyr: env: a sampler over {sampler.num_instances} instances for {instances}")
+    return None if instances == 1 else sampler
+
+
 class DeviceEnvPool:
     """num_envs environments over one task, or over a task table (a list of instances of one domain: TaskTable,
     include/mymyr/rl/task_table.hpp:1-28), stepped together on the device (random policy unless actions are given).
@@ -89,7 +123,7 @@ class DeviceEnvPool:
                  goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
                  dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True,
                  witness_pruning: bool = False, first_env: int = 0, words: int | None = None, device: str | int = "cuda",
-                 count_cache: bool = True, goals: bool = False, task_ids=None, sampler: InstanceSampler | None = None,
+                 count_cache: bool = True, goals: bool = False, task_ids=None, sampler: InstanceSampler | str | None = None,
                  env_ids=None, seeds=None, sampling_seeds=None, reset_counts: bool | None = None, track_visited: bool | int = False):
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
             raise ValueError("mymyr: num_envs must be in [1, 2^31 - 1]")
@@ -111,6 +145,12 @@ class DeviceEnvPool:
             raise ValueError(f"mymyr: env: state rows of {self.words} words; the task needs {widest}")
         self.label_width = max(1, max(t.label_width for t in self.tasks))
         self.device = torch.device(device)
+        self._dead_end_none = dead_end == "none"
+        self._dead_end_terminal = bool(dead_end_terminal)
+        self._busy = np.zeros(num_envs, bool)  # envs with a send not yet received
+        self._sends = []  # (ticket, env ids, batch, event) in send order
+        self._next_ticket = 0
+        self._spare = {}  # rows -> recycled output arrays
         cfg = _lib.EnvConfig(seed, max_steps or 0, step_reward, goal_reward, dead_end_reward, 1 if dead_end == "none" else 0,
                              int(dead_end_terminal), int(autoreset), int(canonical_order), int(witness_pruning), 0)
         h = ctypes.c_void_p()
@@ -159,13 +199,12 @@ class DeviceEnvPool:
         for name, t in (("seeds", self.seeds), ("env_ids", self.env_ids), ("sampling_seeds", self.sampling_seeds)):
             if t is not None and t.shape != (N,):
                 raise ValueError(f"mymyr: env: {name} must have shape ({N},)")
+        sampler = resolve_sampler(sampler, len(self.tasks))
         self.reset_counts = None
         if reset_counts or (reset_counts is None and sampler is not None):
             self.reset_counts = torch.zeros(N, dtype=torch.int32, device=dev)
         self.sampler = sampler
         if sampler is not None:
-            if sampler.num_instances != len(self.tasks):
-                raise ValueError(f"mymyr: env: a sampler over {sampler.num_instances} instances for {len(self.tasks)}")
             thr = np.ascontiguousarray(sampler.thresholds)
             idx = np.ascontiguousarray(sampler.indices)
             check(lib.mya_env_set_sampling(self._h, sampler.num_instances, thr.ctypes.data, idx.ctypes.data, len(idx)))
@@ -186,41 +225,87 @@ class DeviceEnvPool:
         check(lib.mya_env_initial_count(self._h, instance, ctypes.byref(c), ctypes.byref(g)))
         return c.value, bool(g.value)
 
-    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False, task_ids=None, sample: bool = False) -> dict:
-        """Resets every env (or those with mask != 0) to the initial state of its instance; draws are kept, reset
-        counters advance. task_ids (over a table) first sets the instances of the envs being reset; sample=True draws
-        them from the sampler instead. With per-env goals the instance's goal is written into goal_pos / goal_neg unless
-        keep_goals (the masks written there stay, and at_goal is their test on the initial state)."""
+    def reset(self, mask: torch.Tensor | None = None, keep_goals: bool = False, task_ids=None, sample: bool = False, *,
+              env_ids=None, goal_pos=None, goal_neg=None) -> PoolBatch:
+        """Resets every env, those with mask != 0, or the envs env_ids to the initial state of its instance
+        (HostEnv::reset, include/mymyr/rl/env.hpp:208-219); draws are kept, reset counters advance. task_ids (over a
+        table) first sets the instances of the envs being reset (per env of env_ids, or over the whole batch with a
+        mask); sample=True draws them from the sampler instead. With per-env goals the instance's goal is written into
+        goal_pos / goal_neg unless keep_goals or goal masks are given (per env of env_ids; at_goal is their test on the
+        initial state). Returns the observations as a PoolBatch: the reset envs' rows in env_ids order, or views of the
+        whole batch."""
+        if self._busy.any():
+            raise ValueError("mymyr: DeviceEnvPool.reset: envs have a step in flight (recv first)")
+        ids = None
+        if env_ids is not None:
+            if mask is not None:
+                raise ValueError("mymyr: DeviceEnvPool.reset: give a mask or env ids, not both")
+            ids = self._env_ids_arg(env_ids, "reset")
+            mask = torch.zeros(self.num_envs, dtype=torch.uint8, device=self.device)
+            mask[ids] = 1
         if mask is not None:
             mask = mask.to(device=self.device, dtype=torch.uint8).contiguous()
+        if (goal_pos is None) != (goal_neg is None):
+            raise ValueError("mymyr: CpuEnvPool.reset: goals need both goal_pos and goal_neg")
+        if goal_pos is not None:
+            if self.goal_pos is None:
+                raise ValueError("mymyr: CpuEnvPool.reset: goal masks given, but the pool has no per-env goals")
+            rows = ids if ids is not None else torch.arange(self.num_envs, device=self.device)
+            for dst, src in ((self.goal_pos, goal_pos), (self.goal_neg, goal_neg)):
+                g = torch.as_tensor(np.ascontiguousarray(src).view(np.int64) if isinstance(src, np.ndarray) else src).to(self.device)
+                g = g.view(torch.int64) if g.dtype == torch.uint64 else g
+                if g.dim() != 2 or g.shape[0] != rows.numel() or g.shape[1] > self.words:
+                    raise ValueError("mymyr: CpuEnvPool.reset: goal masks must be [n, W] with W at most the pool's words")
+                full = torch.zeros((rows.numel(), self.words), dtype=torch.int64, device=self.device)
+                full[:, : g.shape[1]] = g
+                dst.index_copy_(0, rows, full)
+            keep_goals = True
         if task_ids is not None:
             if self.task_ids is None:
                 raise ValueError("mymyr: env: task ids need a table of several instances")
-            ids = torch.as_tensor(task_ids, dtype=torch.int32).to(self.device)
-            if mask is None:
-                self.task_ids.copy_(ids)
+            tid = torch.as_tensor(task_ids, dtype=torch.int32).to(self.device)
+            if ids is not None:
+                if tid.shape != (ids.numel(),):
+                    raise ValueError(f"mymyr: CpuEnvPool.reset: task_ids must have shape ({ids.numel()},)")
+                self.task_ids.index_copy_(0, ids, tid)
+            elif mask is None:
+                self.task_ids.copy_(tid)
             else:
-                self.task_ids.copy_(torch.where(mask != 0, ids, self.task_ids))
+                self.task_ids.copy_(torch.where(mask != 0, tid, self.task_ids))
         check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), _p(mask), self.count.data_ptr(), int(keep_goals), int(sample),
                                 _stream()))
-        r = {"states": self.states, "count": self.count, "steps": self.steps, "at_goal": self.at_goal}
-        if self.task_ids is not None:
-            r["task_ids"] = self.task_ids
+        goal = self.at_goal
+        dead_end_terminal = not self._dead_end_none and self._dead_end_terminal
+        term = (goal != 0) | ((self.count == 0) & dead_end_terminal)
+        r = {"env_ids": torch.arange(self.num_envs, dtype=torch.int32, device=self.device), "states": self.states,
+             "task_ids": self.task_ids if self.task_ids is not None else self._zero_ids(), "count": self.count, "steps": self.steps,
+             "at_goal": self.at_goal, "goal": goal, "terminated": term.to(torch.uint8)}
         if self.reset_counts is not None:
             r["reset_counts"] = self.reset_counts
         if self.goal_pos is not None:
             r["goal_pos"] = self.goal_pos
             r["goal_neg"] = self.goal_neg
-        return r
+        if ids is not None:
+            r = {k: (v.index_select(0, ids) if k != "env_ids" else ids.to(torch.int32)) for k, v in r.items()}
+        n = self.num_envs if ids is None else ids.numel()
+        return PoolBatch(r, n, self.words, self.label_width, False, self.goal_pos is not None)
 
-    def step(self, actions: torch.Tensor | None = None, final_states: bool = False, labels: bool = True,
-             encode: int = 0, next_task_ids=None) -> dict:
-        """One step of every env: actions [num_envs] int64 indices into the canonical successor order (None: the random
-        policy). next_task_ids [num_envs] (over a table): the instance each autoresetting env restarts in. encode > 0 also emits the observed states' true-atom slots ("atoms", int32 [num_envs, encode], -1
-        padded) and applicable-schema masks ("masks", uint8 [num_envs, num_schemas]), both in library-owned device
-        buffers taken over DLPack. Returns the step's arrays (views, overwritten by the next step)."""
+    def step(self, env_ids=None, actions=None, *, next_task_ids=None, final_states: bool = False, labels: bool = True,
+             encode: int = 0) -> PoolBatch:
+        """One step of every env (env_ids None: in place, the returned arrays are views that the next step overwrites) or
+        of envs env_ids (send + recv_ticket: the reference pool's step). actions [n] int64 indices into the canonical
+        successor order (None: the random policy). next_task_ids [n] (over a table): the instance each autoresetting env
+        restarts in. encode > 0 (whole-batch steps) also emits the observed states' true-atom slots ("atoms", int32
+        [num_envs, encode], -1 padded) and applicable-schema masks ("masks", uint8 [num_envs, num_schemas]), both in
+        library-owned device buffers taken over DLPack."""
+        if env_ids is not None:
+            if encode:
+                raise ValueError("mymyr_amd: DeviceEnvPool.step: the encoding outputs come with whole-batch steps")
+            return self.recv_ticket(self.send(env_ids, actions, next_task_ids=next_task_ids))
+        if self._busy.any():
+            raise ValueError("mymyr: CpuEnvPool.send: envs have a step in flight (recv first)")
         if actions is not None:
-            actions = actions.to(device=self.device, dtype=torch.int64).contiguous()
+            actions = torch.as_tensor(actions).to(device=self.device, dtype=torch.int64).contiguous()
             if actions.shape != (self.num_envs,):
                 raise ValueError(f"mymyr: env: actions must have shape ({self.num_envs},)")
         if final_states and self.final_states is None:
@@ -235,19 +320,12 @@ class DeviceEnvPool:
                                _p(fs), self.schema.data_ptr() if labels else None, self.binding.data_ptr() if labels else None,
                                self.label_width, self.words, self.invalid.data_ptr(), self.goal.data_ptr(), _p(atoms), _p(masks),
                                encode, 0)
-        nxt = None
-        if next_task_ids is not None:
-            if self.task_ids is None:
-                raise ValueError("mymyr: env: next_task_ids needs a table of several instances")
-            nxt = torch.as_tensor(next_task_ids, dtype=torch.int32).to(self.device).contiguous()
-            if nxt.shape != (self.num_envs,):
-                raise ValueError(f"mymyr: env: next_task_ids must have shape ({self.num_envs},)")
+        nxt = self._next_ids_arg(next_task_ids, self.num_envs)
         out.revisited = _p(self.revisited)
         check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(out), _p(actions), _p(nxt), _stream()))
-        r = {"states": self.states, "reward": self.reward, "terminated": self.terminated, "truncated": self.truncated,
-             "count": self.count, "steps": self.steps, "at_goal": self.at_goal, "goal": self.goal, "invalid": self.invalid}
-        if self.task_ids is not None:
-            r["task_ids"] = self.task_ids
+        r = {"env_ids": self._all_ids(), "states": self.states, "reward": self.reward, "terminated": self.terminated,
+             "truncated": self.truncated, "count": self.count, "steps": self.steps, "at_goal": self.at_goal, "goal": self.goal,
+             "invalid": self.invalid, "task_ids": self.task_ids if self.task_ids is not None else self._zero_ids()}
         if self.revisited is not None:
             r["revisited"] = self.revisited
         if labels:
@@ -258,7 +336,167 @@ class DeviceEnvPool:
         if encode:
             r["atoms"] = atoms
             r["masks"] = masks
-        return r
+        if self.goal_pos is not None:
+            r["goal_pos"] = self.goal_pos
+            r["goal_neg"] = self.goal_neg
+        return PoolBatch(r, self.num_envs, self.words, self.label_width, True, self.goal_pos is not None)
+
+    # ---- the reference pool's asynchronous API (CpuEnvPool send / recv / recv_ticket / recycle / pending,
+    # include/mymyr/rl/pool.hpp:114-172). A send steps its envs on the device at once, in stream order: their rows are
+    # gathered into a batch of their own (each keeping its env id's RNG and instance streams, so the results are those
+    # of stepping them with the whole batch), stepped by the HIP env step, and the envs' state is written back; the
+    # batch's arrays are the send's results. recv hands them out in send order.
+
+    def _all_ids(self) -> torch.Tensor:
+        if getattr(self, "_arange", None) is None:
+            self._arange = torch.arange(self.num_envs, dtype=torch.int32, device=self.device)
+        return self._arange
+
+    def _zero_ids(self) -> torch.Tensor:
+        if getattr(self, "_zeros", None) is None:
+            self._zeros = torch.zeros(self.num_envs, dtype=torch.int32, device=self.device)
+        return self._zeros
+
+    def _env_ids_arg(self, env_ids, what: str) -> torch.Tensor:
+        """env_ids as a device int64 tensor, checked: each an env of the pool, at most once, none in flight."""
+        a = env_ids.detach().cpu().numpy() if isinstance(env_ids, torch.Tensor) else np.asarray(env_ids)
+        a = a.astype(np.int64).reshape(-1)
+        if a.size and (a.min() < 0 or a.max() >= self.num_envs):
+            raise ValueError(f"mymyr: CpuEnvPool.{what}: env id out of range [0, {self.num_envs})")
+        if np.unique(a).size != a.size:
+            raise ValueError(f"mymyr: CpuEnvPool.{what}: an env id is repeated")
+        if self._busy[a].any():
+            raise ValueError(f"mymyr: CpuEnvPool.{what}: env {int(a[self._busy[a]][0])} has a step in flight")
+        return torch.from_numpy(a).to(self.device)
+
+    def _next_ids_arg(self, next_task_ids, rows: int):
+        if next_task_ids is None:
+            return None
+        if self.task_ids is None:
+            raise ValueError("mymyr: env: next_task_ids needs a table of several instances")
+        nxt = torch.as_tensor(next_task_ids, dtype=torch.int32).to(self.device).contiguous()
+        if nxt.shape != (rows,):
+            raise ValueError(f"mymyr: env: next_task_ids must have shape ({rows},)")
+        return nxt
+
+    def _batch_arrays(self, B: int) -> dict:
+        """The output arrays of a send of B rows: recycled ones of that size, or new."""
+        spare = self._spare.get(B)
+        if spare:
+            return spare.pop()
+        dev, W, L = self.device, self.words, self.label_width
+        a = {"reward": torch.empty(B, dtype=torch.float32, device=dev), "terminated": torch.empty(B, dtype=torch.uint8, device=dev),
+             "truncated": torch.empty(B, dtype=torch.uint8, device=dev), "count": torch.empty(B, dtype=torch.int32, device=dev),
+             "final_states": torch.empty((B, W), dtype=torch.int64, device=dev), "schema": torch.empty(B, dtype=torch.int32, device=dev),
+             "binding": torch.empty((B, L), dtype=torch.int32, device=dev), "invalid": torch.empty(B, dtype=torch.uint8, device=dev),
+             "goal": torch.empty(B, dtype=torch.uint8, device=dev)}
+        if self.revisited is not None:
+            a["revisited"] = torch.empty(B, dtype=torch.uint8, device=dev)
+        return a
+
+    def send(self, env_ids=None, actions=None, *, next_task_ids=None) -> int:
+        """Enqueues one step of envs env_ids [n] (None: every env) and returns its ticket at once: actions [n] (indices into
+        the canonical successor order; None: the random policy), next_task_ids [n] (over a table: the instances
+        autoresetting envs restart in). Raises for an unknown or repeated env id or one with a step in flight."""
+        if env_ids is None:
+            if self._busy.any():
+                raise ValueError("mymyr: CpuEnvPool.send: envs have a step in flight (recv first)")
+            ids = torch.arange(self.num_envs, dtype=torch.int64, device=self.device)
+        else:
+            ids = self._env_ids_arg(env_ids, "send")
+        B = ids.numel()
+        act = None
+        if actions is not None:
+            act = torch.as_tensor(np.asarray(actions) if not isinstance(actions, torch.Tensor) else actions)
+            act = act.to(device=self.device, dtype=torch.int64).contiguous()
+            if act.shape != (B,):
+                raise ValueError(f"mymyr: CpuEnvPool.send: actions must have shape ({B},)")
+        nxt = self._next_ids_arg(next_task_ids, B)
+        out = self._batch_arrays(B)
+        # the envs' rows as a batch of their own: their env ids carry their RNG streams
+        sub = {"states": self.states.index_select(0, ids), "steps": self.steps.index_select(0, ids),
+               "draws": self.draws.index_select(0, ids), "at_goal": self.at_goal.index_select(0, ids)}
+        rng_ids = self.env_ids.index_select(0, ids) if self.env_ids is not None else (ids + self.first_env).to(torch.int32)
+        opt = {}
+        for name in ("counts_cache", "goal_pos", "goal_neg", "task_ids", "seeds", "reset_counts", "sampling_seeds", "visited",
+                     "visited_count"):
+            t = getattr(self, name)
+            opt[name] = t.index_select(0, ids) if t is not None else None
+        H = 0 if self.visited is None else self.visited.shape[1]
+        batch = _lib.EnvBatch(sub["states"].data_ptr(), B, self.words, 0, sub["steps"].data_ptr(), sub["draws"].data_ptr(),
+                              sub["at_goal"].data_ptr(), self.first_env, _p(opt["counts_cache"]), _p(opt["goal_pos"]),
+                              _p(opt["goal_neg"]), _p(opt["task_ids"]), _p(opt["seeds"]), rng_ids.data_ptr(), _p(opt["reset_counts"]),
+                              _p(opt["sampling_seeds"]), _p(opt["visited"]), _p(opt["visited_count"]), _p(self.visited_status), H, 0)
+        so = _lib.StepOutputs(out["reward"].data_ptr(), out["terminated"].data_ptr(), out["truncated"].data_ptr(),
+                              out["count"].data_ptr(), out["final_states"].data_ptr(), out["schema"].data_ptr(), out["binding"].data_ptr(),
+                              self.label_width, self.words, out["invalid"].data_ptr(), out["goal"].data_ptr(), None, None, 0, 0)
+        so.revisited = _p(out.get("revisited"))
+        if B:
+            check(lib.mya_env_step(self._h, ctypes.byref(batch), ctypes.byref(so), _p(act), _p(nxt), _stream()))
+        # the envs' state back into the pool
+        for name, t in sub.items():
+            getattr(self, name).index_copy_(0, ids, t)
+        for name, t in opt.items():
+            if t is not None and name not in ("seeds", "sampling_seeds"):
+                getattr(self, name).index_copy_(0, ids, t)
+        res = dict(out)
+        res.update({"env_ids": ids.to(torch.int32), "states": sub["states"], "steps": sub["steps"], "at_goal": sub["at_goal"],
+                    "task_ids": opt["task_ids"] if opt["task_ids"] is not None else torch.zeros(B, dtype=torch.int32, device=self.device)})
+        if opt["goal_pos"] is not None:
+            res["goal_pos"], res["goal_neg"] = opt["goal_pos"], opt["goal_neg"]
+        ev = torch.cuda.Event()
+        ev.record()
+        ticket = self._next_ticket
+        self._next_ticket += 1
+        idx = ids.cpu().numpy()
+        self._busy[idx] = True
+        self._sends.append((ticket, idx, PoolBatch(res, B, self.words, self.label_width, True, opt["goal_pos"] is not None), ev))
+        return ticket
+
+    def _collect(self, taken: list) -> PoolBatch:
+        for _, idx, _, ev in taken:
+            ev.synchronize()
+            self._busy[idx] = False
+        if len(taken) == 1:
+            return taken[0][2]
+        parts = [t[2] for t in taken]
+        cat = {k: torch.cat([p[k] for p in parts]) for k in parts[0]}
+        return PoolBatch(cat, sum(p.rows for p in parts), self.words, self.label_width, True, parts[0].goals)
+
+    def recv(self, min_rows: int = 0) -> PoolBatch:
+        """The results of the oldest pending sends, in send order: whole sends with at least min_rows rows together
+        (0: exactly one send). Blocks until they are done; raises if fewer rows are pending."""
+        taken, rows = [], 0
+        for s in self._sends:
+            taken.append(s)
+            rows += s[2].rows
+            if rows >= min_rows:
+                break
+        if not taken or rows < min_rows:
+            raise ValueError(f"mymyr: CpuEnvPool.recv: {rows} rows pending, {max(min_rows, 1)} asked for (send first)")
+        del self._sends[: len(taken)]
+        return self._collect(taken)
+
+    def recv_ticket(self, ticket: int) -> PoolBatch:
+        """The results of the send with this ticket (blocks until it is done)."""
+        for k, s in enumerate(self._sends):
+            if s[0] == ticket:
+                del self._sends[k]
+                return self._collect([s])
+        raise ValueError(f"mymyr: CpuEnvPool.recv: no pending send has ticket {ticket}")
+
+    def recycle(self, batch: PoolBatch) -> None:
+        """Hands a send's batch back: a later send of as many rows fills its arrays instead of allocating new ones."""
+        if not isinstance(batch, PoolBatch) or not batch.step:
+            return
+        keys = ("reward", "terminated", "truncated", "count", "final_states", "schema", "binding", "invalid", "goal", "revisited")
+        arrays = {k: batch[k] for k in keys if k in batch}
+        self._spare.setdefault(batch.rows, []).append(arrays)
+
+    @property
+    def pending(self) -> int:
+        """Sends not yet received."""
+        return len(self._sends)
 
     def _encoding_outputs(self, encode: int) -> tuple[torch.Tensor, torch.Tensor]:
         """The atom-index and mask outputs live in library-owned device buffers that torch takes over DLPack without a
@@ -315,6 +553,54 @@ class DeviceEnvPool:
                 self._h = ctypes.c_void_p()
         except Exception:
             pass
+
+
+class EnvPool(DeviceEnvPool):
+    """The reference's rl.CpuEnvPool on the device (python/src/rl_bindings.cpp:2465-2600, include/mymyr/rl/pool.hpp:
+    114-172): num_envs envs over a task, a TaskTable or a TaskSuite, with its keyword arguments and defaults. reset(
+    env_ids, task_ids), send(env_ids, actions) / recv(min_rows) / recv_ticket(ticket), step(env_ids, actions) =
+    send + recv_ticket, recycle(batch) and pending behave as the reference pool's, with batches of device tensors
+    (PoolBatch). sampler ("auto" and "uniform": uniform over the instances, an InstanceSampler, or None) places every
+    env in a sampled instance and restarts it in its next one on each reset without task_ids and each autoreset
+    without next_task_ids, with the draws of the reference pool (seed, env id first_env + e, reset counter).
+    `threads` is accepted for the reference's signature (the device steps every env of a send at once); batch rows are
+    the widest instance's words (the reference's PoolOptions::words)."""
+
+    def __init__(self, table, num_envs: int, *, threads: int = 1, goals: bool = False, seed: int = 0, max_steps: int | None = None,
+                 step_reward: float = 0.0, goal_reward: float = 1.0, dead_end: str = "no_successors", dead_end_reward: float = 0.0,
+                 dead_end_terminal: bool = True, autoreset: bool = True, canonical_order: bool = True, witness_pruning: bool = False,
+                 framework=None, words: int | None = None, sampler="auto", track_visited: bool | int = False, first_env: int = 0,
+                 device: str | int = "cuda"):
+        if framework not in (None, "torch"):
+            raise ValueError("mymyr_amd: EnvPool: batches are device tensors (framework None or 'torch')")
+        n = len(table.tasks) if isinstance(table, TaskTable) else len(table) if isinstance(table, (list, tuple)) else 1
+        super().__init__(table, num_envs, seed=seed, max_steps=max_steps, step_reward=step_reward, goal_reward=goal_reward,
+                         dead_end=dead_end, dead_end_reward=dead_end_reward, dead_end_terminal=dead_end_terminal, autoreset=autoreset,
+                         canonical_order=canonical_order, witness_pruning=witness_pruning, first_env=first_env, words=words,
+                         device=device, goals=goals, sampler=resolve_sampler(sampler, n), track_visited=track_visited)
+        self.threads = threads
+        self.seed = seed
+        self.max_steps = max_steps
+        self.dead_end = dead_end
+        self.goals = goals
+        self.table = table
+        if self.sampler is not None:
+            # every env starts in a sampled instance (the draw of its reset counter 0, which then stands at 1)
+            check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), None, self.count.data_ptr(), 0, 1, _stream()))
+
+    def reset(self, env_ids=None, task_ids=None, *, goal_pos=None, goal_neg=None) -> PoolBatch:
+        """Resets envs env_ids [n] (None: every env) into instances task_ids [n] (None: sampled ones, or their current
+        ones without a sampler) with goal masks goal_pos / goal_neg [n, W] (per-env goals only; None: their instances'
+        goals); returns their observations. Draw counters are kept. Raises if one of them has a step in flight."""
+        sample = task_ids is None and self.sampler is not None
+        if env_ids is None and goal_pos is None:
+            return super().reset(task_ids=task_ids, sample=sample)
+        ids = np.arange(self.num_envs) if env_ids is None else env_ids
+        return super().reset(env_ids=ids, task_ids=task_ids, sample=sample, goal_pos=goal_pos, goal_neg=goal_neg)
+
+    def step(self, env_ids=None, actions=None, *, next_task_ids=None) -> PoolBatch:
+        """send + recv_ticket: one step of envs env_ids (None: every env), its results."""
+        return self.recv_ticket(self.send(env_ids, actions, next_task_ids=next_task_ids))
 
 
 def successors(task: Task, states: torch.Tensor, cap: int = 4096) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:

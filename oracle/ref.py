@@ -46,6 +46,15 @@ class BrfsOptions(Structure):
     ]
 
 
+class PoolOut(Structure):
+    _fields_ = [
+        ("cap", c_uint64),
+        ("words", c_uint32),
+        ("label_width", c_uint32),
+    ] + [(n, c_void_p) for n in ("env_ids", "states", "task_ids", "count", "steps", "at_goal", "terminated", "goal", "reward", "truncated",
+                                  "invalid", "final_states", "schema", "binding")]
+
+
 class BrfsResult(Structure):
     _fields_ = [
         ("states", c_uint64),
@@ -116,6 +125,13 @@ def lib() -> ctypes.CDLL:
             "mref_pool_run": (c_int, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint32, POINTER(c_double), POINTER(c_uint64)]),
             "mref_brfs": (c_int, [c_void_p, POINTER(BrfsOptions), POINTER(BrfsResult), c_void_p, c_uint32, c_void_p, c_void_p,
                                   c_uint32, c_uint32, c_void_p, c_uint32]),
+            "mref_pool_create": (c_void_p, [c_void_p, POINTER(EnvConfig), c_uint32, c_uint32, c_uint64]),
+            "mref_pool_free": (None, [c_void_p]),
+            "mref_pool_reset": (c_int64, [c_void_p, c_void_p, c_uint64, POINTER(PoolOut)]),
+            "mref_pool_send": (c_int64, [c_void_p, c_void_p, c_uint64, c_void_p]),
+            "mref_pool_recv": (c_int64, [c_void_p, c_uint64, POINTER(PoolOut)]),
+            "mref_pool_recv_ticket": (c_int64, [c_void_p, c_uint64, POINTER(PoolOut)]),
+            "mref_pool_pending": (c_int64, [c_void_p]),
             "mref_dedup_flat": (c_int, [c_void_p, c_uint64, c_uint32, POINTER(c_uint64), POINTER(c_double)]),
             "mref_dedup_concurrent": (c_int, [c_void_p, c_uint64, c_uint32, c_uint32, c_uint64, POINTER(c_uint64), POINTER(c_double)]),
         }
@@ -426,6 +442,82 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         out["cost"] = r.cost
         out["goal_state"] = [f"{int(x):016x}" for x in gs[:min(r.goal_words, gs.size)]]
     return out
+
+
+class RefPool:
+    """The reference CpuEnvPool (rl/pool.hpp:114-172) over one task: reset, send, recv, recv_ticket, pending. Batches come
+    back as dicts of numpy arrays in the reference's PoolBatch field names."""
+
+    STEP_FIELDS = ("reward", "truncated", "invalid", "final_states", "schema", "binding")
+
+    def __init__(self, task: RefTask, num_envs: int, threads: int = 4, first_env: int = 0, **cfg):
+        c = EnvConfig(cfg.get("seed", 0), cfg.get("max_steps", 0) or 0, cfg.get("step_reward", 0.0), cfg.get("goal_reward", 1.0),
+                      cfg.get("dead_end_reward", 0.0), 1 if cfg.get("dead_end") == "none" else 0, int(cfg.get("dead_end_terminal", True)),
+                      int(cfg.get("autoreset", True)), 1, 0, 0)
+        h = lib().mref_pool_create(task._h, ctypes.byref(c), num_envs, threads, first_env)
+        if not h:
+            raise RuntimeError(_err())
+        self._h = c_void_p(h)
+        self.N, self.W, self.L = num_envs, task.table_words, max(1, task.label_width)
+
+    def _out(self):
+        N, W, L = self.N, self.W, self.L
+        a = {"env_ids": np.zeros(N, np.uint32), "states": np.zeros((N, W), np.uint64), "task_ids": np.zeros(N, np.int32),
+             "count": np.zeros(N, np.int32), "steps": np.zeros(N, np.int32), "at_goal": np.zeros(N, np.uint8),
+             "terminated": np.zeros(N, np.uint8), "goal": np.zeros(N, np.uint8), "reward": np.zeros(N, np.float32),
+             "truncated": np.zeros(N, np.uint8), "invalid": np.zeros(N, np.uint8), "final_states": np.zeros((N, W), np.uint64),
+             "schema": np.zeros(N, np.int32), "binding": np.zeros((N, L), np.int32)}
+        o = PoolOut(N, W, L, *[a[n].ctypes.data for n in ("env_ids", "states", "task_ids", "count", "steps", "at_goal", "terminated", "goal",
+                                                           "reward", "truncated", "invalid", "final_states", "schema", "binding")])
+        return a, o
+
+    @staticmethod
+    def _ids(env_ids):
+        return None if env_ids is None else np.ascontiguousarray(env_ids, np.uint32)
+
+    def _batch(self, a, rows, step):
+        keys = [k for k in a if step or k not in self.STEP_FIELDS]
+        return {k: a[k][:rows].copy() for k in keys}
+
+    def reset(self, env_ids=None) -> dict:
+        ids = self._ids(env_ids)
+        a, o = self._out()
+        n = lib().mref_pool_reset(self._h, _p(ids), 0 if ids is None else ids.size, ctypes.byref(o))
+        if n < 0:
+            raise RuntimeError(_err())
+        return self._batch(a, n, False)
+
+    def send(self, env_ids=None, actions=None) -> int:
+        ids = self._ids(env_ids)
+        act = None if actions is None else np.ascontiguousarray(actions, np.int64)
+        t = lib().mref_pool_send(self._h, _p(ids), 0 if ids is None else ids.size, _p(act))
+        if t < 0:
+            raise RuntimeError(_err())
+        return t
+
+    def recv(self, min_rows: int = 0) -> dict:
+        a, o = self._out()
+        n = lib().mref_pool_recv(self._h, min_rows, ctypes.byref(o))
+        if n < 0:
+            raise RuntimeError(_err())
+        return self._batch(a, n, True)
+
+    def recv_ticket(self, ticket: int) -> dict:
+        a, o = self._out()
+        n = lib().mref_pool_recv_ticket(self._h, ticket, ctypes.byref(o))
+        if n < 0:
+            raise RuntimeError(_err())
+        return self._batch(a, n, True)
+
+    @property
+    def pending(self) -> int:
+        return int(lib().mref_pool_pending(self._h))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            lib().mref_pool_free(h)
+            self._h = c_void_p()
 
 
 def dedup_flat(rows: np.ndarray) -> tuple[int, float]:

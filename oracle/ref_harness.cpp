@@ -9,7 +9,7 @@
 //   hashes                hash::words / hash::state      include/mymyr/core/hash.hpp:38-60
 //   Philox                rl::rng::block                 include/mymyr/rl/rng.hpp:45-83
 //   env step / reset      rl::HostEnv                    include/mymyr/rl/env.hpp:181-278
-//   env pool              rl::CpuEnvPool                 include/mymyr/rl/pool.hpp:114-172
+//   env pool              rl::CpuEnvPool                 include/mymyr/rl/pool.hpp:114-172 (reset, send, recv, recv_ticket)
 //   BrFS                  brfs(Task, BrfsOptions)        include/mymyr/search/brfs.hpp:140
 //   dedup                 FlatStateStore::insert         include/mymyr/state/flat_store.hpp:44-115
 //                         ConcurrentStateStore::insert   include/mymyr/state/concurrent_store.hpp:79-177
@@ -820,6 +820,128 @@ int mref_dedup_concurrent(const uint64_t* rows, uint64_t n, uint32_t words, uint
             return 0;
         },
         -1);
+}
+
+
+// ---- the reference pool's asynchronous API over a scripted sequence of calls (CpuEnvPool, rl/pool.hpp:114-172)
+
+struct mref_pool
+{
+    std::unique_ptr<rl::CpuEnvPool> pool;
+};
+
+// A PoolBatch's arrays copied out (caller-owned, `cap` rows; null arrays are not written): env ids, states [rows, words]
+// (zero padded), instances, counts, step counts, and for a step's batch the rewards, flags, final states and labels.
+struct mref_pool_out
+{
+    uint64_t cap;
+    uint32_t words, label_width;
+    uint32_t* env_ids;
+    uint64_t* states;
+    int32_t* task_ids;
+    int32_t* count;
+    int32_t* steps;
+    uint8_t* at_goal;
+    uint8_t* terminated;
+    uint8_t* goal;
+    float* reward;
+    uint8_t* truncated;
+    uint8_t* invalid;
+    uint64_t* final_states;
+    int32_t* schema;
+    int32_t* binding;
+};
+
+static int64_t copy_pool_batch(const rl::PoolBatch& b, mref_pool_out* o)
+{
+    if (b.rows > o->cap)
+        throw std::invalid_argument("harness: pool batch of " + std::to_string(b.rows) + " rows, buffers hold " + std::to_string(o->cap));
+    const u32 BW = b.row_words(), OW = o->words;
+    for (u64 r = 0; r < b.rows; ++r)
+    {
+        if (o->env_ids)
+            o->env_ids[r] = b.env_ids[r];
+        if (o->task_ids)
+            o->task_ids[r] = b.task_ids[r];
+        if (o->count)
+            o->count[r] = b.count[r];
+        if (o->steps)
+            o->steps[r] = b.steps[r];
+        if (o->at_goal)
+            o->at_goal[r] = b.at_goal[r];
+        if (o->terminated)
+            o->terminated[r] = b.terminated[r];
+        if (o->goal)
+            o->goal[r] = b.goal[r];
+        for (u32 w = 0; w < OW && o->states; ++w)
+            o->states[r * OW + w] = w < BW ? b.states[r * BW + w] : 0;
+        if (!b.step)
+            continue;
+        if (o->reward)
+            o->reward[r] = b.reward[r];
+        if (o->truncated)
+            o->truncated[r] = b.truncated[r];
+        if (o->invalid)
+            o->invalid[r] = b.invalid[r];
+        if (o->schema)
+            o->schema[r] = b.schema[r];
+        for (u32 w = 0; w < OW && o->final_states; ++w)
+            o->final_states[r * OW + w] = w < BW ? b.final_states[r * BW + w] : 0;
+        for (u32 k = 0; k < o->label_width && o->binding; ++k)
+            o->binding[r * o->label_width + k] = k < b.label_width ? b.binding[r * b.label_width + k] : -1;
+    }
+    return static_cast<int64_t>(b.rows);
+}
+
+mref_pool* mref_pool_create(mref_task* t, const mref_env_config* c, uint32_t num_envs, uint32_t threads, uint64_t first_env)
+{
+    return guarded(
+        [&]() -> mref_pool*
+        {
+            rl::PoolOptions po;
+            po.threads = threads;
+            po.first_env = first_env;
+            auto p = new mref_pool;
+            p->pool = std::make_unique<rl::CpuEnvPool>(t->table, env_config(c), num_envs, po);
+            return p;
+        },
+        nullptr);
+}
+
+void mref_pool_free(mref_pool* p) { delete p; }
+
+// env_ids [n] (null: every env). Returns the rows of the reset's batch.
+int64_t mref_pool_reset(mref_pool* p, const uint32_t* env_ids, uint64_t n, mref_pool_out* o)
+{
+    return guarded([&]() -> int64_t { return copy_pool_batch(p->pool->reset(env_ids, n, nullptr), o); }, -1);
+}
+
+// env_ids [n] (null: every env), actions [n] (null: the random policy). Returns the send's ticket.
+int64_t mref_pool_send(mref_pool* p, const uint32_t* env_ids, uint64_t n, const int64_t* actions)
+{
+    return guarded(
+        [&]() -> int64_t
+        {
+            rl::Actions a;
+            a.v64 = actions;
+            return static_cast<int64_t>(p->pool->send(env_ids, n, a, nullptr));
+        },
+        -1);
+}
+
+int64_t mref_pool_recv(mref_pool* p, uint64_t min_rows, mref_pool_out* o)
+{
+    return guarded([&]() -> int64_t { return copy_pool_batch(p->pool->recv(min_rows), o); }, -1);
+}
+
+int64_t mref_pool_recv_ticket(mref_pool* p, uint64_t ticket, mref_pool_out* o)
+{
+    return guarded([&]() -> int64_t { return copy_pool_batch(p->pool->recv_ticket(ticket), o); }, -1);
+}
+
+int64_t mref_pool_pending(mref_pool* p)
+{
+    return guarded([&]() -> int64_t { return static_cast<int64_t>(p->pool->pending()); }, -1);
 }
 
 }  // extern "C"

@@ -220,3 +220,98 @@ def given_actions(u, count) -> np.ndarray:
 # row, which resolves to a fresh one); tests/test_oracle.py recounts it from the generator's closed form.
 DEDUP_WORKLOAD = {"rows": 1 << 26, "words": 16, "seed": 0, "dup": 0.3, "batch": 1 << 20, "unique": 46975112}
 
+
+# The pool's asynchronous API (CpuEnvPool reset / send / recv / recv_ticket, include/mymyr/rl/pool.hpp:114-172) over a
+# scripted sequence of calls: resets of all and of some envs, sends of subsets (shuffled env ids, given actions with
+# invalid ones among them, the random policy), received whole (recv), several at once (recv with min_rows) and by ticket.
+# The calls are drawn here from the case's seed, so the golden script and the device test make the same ones; every
+# batch a call returns is recorded as a digest of its arrays in PoolBatch order.
+POOL_CASES = {
+    "gridworld": {"num_envs": 256, "first_env": 3, "rounds": 24, "seed": 41,
+                  "env": {"seed": 7, "max_steps": 12, "step_reward": -1.0, "goal_reward": 2.0}},
+    "transport": {"num_envs": 192, "first_env": 0, "rounds": 16, "seed": 43, "env": {"seed": 1}},
+}
+
+POOL_FIELDS = (("env_ids", np.uint32), ("states", np.uint64), ("task_ids", np.int32), ("count", np.int32), ("steps", np.int32),
+               ("at_goal", np.uint8), ("terminated", np.uint8), ("goal", np.uint8))
+POOL_STEP_FIELDS = (("reward", np.float32), ("truncated", np.uint8), ("invalid", np.uint8), ("final_states", np.uint64),
+                    ("schema", np.int32), ("binding", np.int32))
+
+
+def pool_batch_digest(b, step: bool, label_width: int) -> str:
+    """Digest of a pool batch (a mapping of arrays: numpy, or tensors with .cpu()) in PoolBatch field order."""
+    def arr(k, dt):
+        a = b[k]
+        a = a.cpu().numpy() if hasattr(a, "cpu") else np.asarray(a)
+        if k == "binding":
+            a = a[:, :label_width]
+        return np.ascontiguousarray(a).view(dt) if a.dtype.itemsize == np.dtype(dt).itemsize else a.astype(dt)
+    fields = POOL_FIELDS + (POOL_STEP_FIELDS if step else ())
+    return arrays_digest(*[arr(k, dt) for k, dt in fields])
+
+
+def pool_script(case: str) -> list:
+    """The calls of a pool case: ("reset", ids | None), ("send", ids | None, actions | None), ("recv", min_rows) and
+    ("recv_ticket", k) for the k-th send. Each round sends some idle envs and receives every pending send; only idle
+    envs are sent or reset."""
+    c = POOL_CASES[case]
+    N = c["num_envs"]
+    rng = np.random.default_rng(c["seed"])
+    calls = [("reset", None)]
+    busy = np.zeros(N, bool)
+    pending = []  # (send index, ids or None: every env), in send order
+    nsend = 0
+    for r in range(c["rounds"]):
+        kind = r % 4
+        if kind == 3 and r % 8 == 3:
+            calls.append(("send", None, None))
+            pending.append((nsend, None))
+            nsend += 1
+            busy[:] = True
+        else:
+            for _ in range(1 + int(rng.integers(0, 3))):
+                idle = np.flatnonzero(~busy)
+                if idle.size == 0:
+                    break
+                take = max(1, int(rng.integers(1, idle.size + 1)) // 2)
+                ids = rng.permutation(idle)[:take]
+                busy[ids] = True
+                acts = rng.integers(-1, 5, ids.size) if kind == 1 else None
+                calls.append(("send", ids.tolist(), None if acts is None else acts.tolist()))
+                pending.append((nsend, ids))
+                nsend += 1
+        while pending:
+            if kind == 2 and len(pending) > 1:
+                calls.append(("recv_ticket", pending.pop(-1)[0]))  # a later send first
+            elif kind == 0 and len(pending) > 1:
+                rows = sum(N if ids is None else ids.size for _, ids in pending[:2])
+                calls.append(("recv", rows))  # the two oldest sends together
+                pending = pending[2:]
+            else:
+                pending.pop(0)
+                calls.append(("recv", 0))
+        busy[:] = False
+        if r % 5 == 4:
+            calls.append(("reset", rng.permutation(N)[: int(rng.integers(1, N // 3))].tolist()))
+    return calls
+
+
+def run_pool_script(pool, case: str, label_width: int) -> list:
+    """Digests of the batches the calls of a pool case return, on a pool with the reference's reset / send / recv /
+    recv_ticket methods (env ids and actions as numpy arrays)."""
+    out = []
+    tickets = []
+    for call in pool_script(case):
+        if call[0] == "reset":
+            ids = None if call[1] is None else np.asarray(call[1], np.uint32)
+            out.append(pool_batch_digest(pool.reset(ids), False, label_width))
+        elif call[0] == "send":
+            ids = None if call[1] is None else np.asarray(call[1], np.uint32)
+            acts = None if call[2] is None else np.asarray(call[2], np.int64)
+            tickets.append(pool.send(ids, acts))
+        elif call[0] == "recv":
+            out.append(pool_batch_digest(pool.recv(call[1]), True, label_width))
+        else:
+            out.append(pool_batch_digest(pool.recv_ticket(tickets[call[1]]), True, label_width))
+    return out
+

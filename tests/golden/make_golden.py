@@ -309,6 +309,19 @@ def make_visited_mask():
     dump("visited_mask.json", out)
 
 
+def make_pool():
+    """Digests of every batch the reference CpuEnvPool returns over each pool case's scripted calls."""
+    out = {}
+    for case, c in fx.POOL_CASES.items():
+        t = ref.RefTask(fx.task_path(case))
+        pool = ref.RefPool(t, c["num_envs"], threads=4, first_env=c["first_env"], **c["env"])
+        digests = fx.run_pool_script(pool, case, max(1, t.label_width))
+        assert pool.pending == 0
+        out[case] = {"digests": digests, "label_width": max(1, t.label_width)}
+        print("pool", case, len(digests), flush=True)
+    dump("pool.json", out)
+
+
 def brfs_record(name, atoms="auto", ref_threads=1, **kw):
     """The reference brfs() on a task; `options` holds the BrfsOptions a device search repeats. Cuts are recorded
     from the default single-threaded search (threads=1, the flat store for these widths): the reference's multi-threaded
@@ -350,7 +363,7 @@ def main():
     a = ap.parse_args()
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
-             "env_small": make_env_small, "env_long": make_env_long, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
+             "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

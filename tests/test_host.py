@@ -100,3 +100,21 @@ def test_generators_deterministic():
     a = gen.dedup_rows(100, 50, 16, seed=3)
     b = gen.dedup_rows(0, 150, 16, seed=3)[100:]
     assert np.array_equal(a, b)
+
+
+def test_pool_sampler_resolution():
+    """sampler="auto" (the reference pool's default) and "uniform" sample every instance uniformly over a table of several
+    instances and nothing over one; other strings and mismatched samplers are refused (python/mymyr/rl/_sampling.py)."""
+    import pytest
+
+    from mymyr_amd.rl import InstanceSampler, resolve_sampler
+
+    assert resolve_sampler("auto", 1) is None
+    s = resolve_sampler("auto", 3)
+    assert isinstance(s, InstanceSampler) and s.num_instances == 3 and s.weights is None
+    assert isinstance(resolve_sampler("uniform", 2), InstanceSampler)
+    assert resolve_sampler(None, 4) is None
+    with pytest.raises(ValueError):
+        resolve_sampler("weighted", 2)
+    with pytest.raises(ValueError):
+        resolve_sampler(InstanceSampler(2), 3)
