@@ -89,6 +89,14 @@ struct BrfsCache
     ~BrfsCache();
 };
 
+struct TaskDev;
+
+/// Rows of at most 16 words: over the ground actions (brfs.hip). Wider rows: over the lifted expansion (brfs_wide.hip),
+/// which needs the task's device tables `dev`.
 BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts,
-                        BrfsCache* cache = nullptr);
+                        BrfsCache* cache = nullptr, const TaskDev* dev = nullptr);
+
+/// The BrFS of a task with rows wider than 16 words over the lifted expansion (witness pruning only for tasks without
+/// witness parameters).
+BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts);
 }  // namespace mya

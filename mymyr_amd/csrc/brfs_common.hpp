@@ -1,0 +1,177 @@
+#pragma once
+// Pieces shared by the device BrFS drivers (brfs.hip over ground actions, brfs_wide.hip over the lifted expansion): the
+// drivers' device scalars and small kernels (chunk ends, goal-flag sums and searches, the fingerprint), owned device
+// buffers, and HIP-event timing of kernel classes. Included by one driver translation unit each; everything here has
+// internal linkage.
+
+#include "brfs.hpp"
+#include "device_common.hpp"
+#include "runtime.hpp"
+#include "scan.hpp"
+
+#include <chrono>
+#include <vector>
+
+namespace mya
+{
+namespace
+{
+// The chunk end: the largest parent p in (p0, hi] whose first successor offset offsets[p * stride] <= bound, at least
+// p0 + 1 (one parent's successors always fit). out[0] = p, out[1] = offsets[p * stride].
+__global__ void k_chunk_end(const u64* __restrict__ offsets, u32 stride, u64 p0, u64 hi, u64 bound, u64* __restrict__ out)
+{
+    u64 a = p0 + 1, b = hi + 1;  // the first parent in [p0 + 1, hi + 1) past the bound
+    while (a < b)
+    {
+        const u64 mid = a + (b - a) / 2;
+        if (offsets[mid * stride] <= bound)
+            a = mid + 1;
+        else
+            b = mid;
+    }
+    const u64 p = a - 1 < p0 + 1 ? p0 + 1 : a - 1;
+    out[0] = p;
+    out[1] = offsets[p * stride];
+}
+
+// The driver's scalars that a synchronization reads, gathered in one launch: the set's current size and status, and
+// (optional) a counted block's offset total.
+__global__ void k_gather_small(u64* __restrict__ small, int size_at, const u64* __restrict__ size_now, int status_at,
+                               const u32* __restrict__ status, int total_at, const u64* __restrict__ total)
+{
+    small[size_at] = *size_now;
+    small[status_at] = *status;
+    if (total)
+        small[total_at] = *total;
+}
+
+__global__ void k_sum_u8(const u8* __restrict__ v, u64 n, u64* __restrict__ out)
+{
+    u64 s = 0;
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += static_cast<u64>(gridDim.x) * blockDim.x)
+        s += v[i];
+    s = wave_sum64(s);
+    if (lane_id() == 0 && s)
+        atomicAdd(reinterpret_cast<unsigned long long*>(out), static_cast<unsigned long long>(s));
+}
+
+__global__ void k_first_u8(const u8* __restrict__ v, u64 n, u64* __restrict__ out)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += static_cast<u64>(gridDim.x) * blockDim.x)
+        if (v[i])
+            atomicMin(reinterpret_cast<unsigned long long*>(out), static_cast<unsigned long long>(i));
+}
+
+__global__ void k_fingerprint(const u64* __restrict__ arena, u64 n, u32 W, const u64* __restrict__ slot_cid, u64* __restrict__ out)
+{
+    u64 acc = 0;
+    for (u64 id = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; id < n; id += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        const u64* row = arena + id * W;
+        u64 ch = 0;
+        for (u32 w = 0; w < W; ++w)
+        {
+            u64 x = row[w];
+            while (x)
+            {
+                const u32 s = w * 64 + static_cast<u32>(__builtin_ctzll(x));
+                x &= x - 1;
+                const u64 cid = slot_cid ? slot_cid[s] : s;
+                ch ^= mix64(cid + 0x1234567ULL);
+            }
+        }
+        acc ^= mix64(id * 0x9E3779B97F4A7C15ULL ^ ch);
+    }
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1)
+        acc ^= __shfl_xor(acc, d, kWave);
+    if (lane_id() == 0 && acc)
+        atomicXor(reinterpret_cast<unsigned long long*>(out), static_cast<unsigned long long>(acc));
+}
+
+__global__ void k_set_u64(u64* p, u64 v) { *p = v; }
+
+constexpr int kSmall = 16;  // device scalars of the driver
+
+struct Buffers
+{
+    std::vector<void*> owned;
+    u64* host = nullptr;  // pinned mirror of the device scalars
+    template<class T>
+    T* alloc(size_t n, const char* what)
+    {
+        T* p = dev_alloc<T>(n, what);
+        owned.push_back(p);
+        return p;
+    }
+    ~Buffers()
+    {
+        for (void* p : owned)
+            dev_free(p);
+        if (host)
+            (void)hipHostFree(host);
+    }
+};
+
+using Clock = std::chrono::steady_clock;
+
+/// HIP-event timing of kernel classes on one stream; durations are read once the stream has drained.
+class Timers
+{
+public:
+    Timers(bool on, hipStream_t s, BrfsResultC& r) : m_on(on), m_s(s), m_r(r) {}
+    ~Timers()
+    {
+        for (auto& e : m_ev)
+        {
+            event_release(e.a);
+            event_release(e.b);
+        }
+    }
+    void begin(int k)
+    {
+        if (!m_on)
+            return;
+        Pair p{k, nullptr, nullptr};
+        p.a = event_acquire();
+        p.b = event_acquire();
+        hip_check(hipEventRecord(p.a, m_s), "event");
+        m_ev.push_back(p);
+    }
+    void end(int k, u64 bytes)
+    {
+        m_r.kernel_bytes[k] += bytes;
+        m_r.kernel_launches[k] += 1;
+        if (!m_on)
+            return;
+        hip_check(hipEventRecord(m_ev.back().b, m_s), "event");
+    }
+    void bytes(int k, u64 b) { m_r.kernel_bytes[k] += b; }
+    /// Adds the durations of the recorded pairs (the stream must have drained).
+    void collect()
+    {
+        for (auto& e : m_ev)
+        {
+            float ms = 0;
+            hip_check(hipEventElapsedTime(&ms, e.a, e.b), "event time");
+            m_r.kernel_ms[e.k] += ms;
+            event_release(e.a);
+            event_release(e.b);
+        }
+        m_ev.clear();
+    }
+
+private:
+    struct Pair
+    {
+        int k;
+        hipEvent_t a, b;
+    };
+    bool m_on;
+    hipStream_t m_s;
+    BrfsResultC& m_r;
+    std::vector<Pair> m_ev;
+};
+
+}  // namespace
+}  // namespace mya

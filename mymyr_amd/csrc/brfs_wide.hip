@@ -1,0 +1,473 @@
+// Device BrFS over rows wider than the ground driver's 16 words (brfs.hpp), for lifted tasks whose ground action lists
+// are too large to test per parent (a transport instance grounds to hundreds of thousands of actions, few of them
+// applicable in a state). A layer's parents are expanded by the lifted successor generator of the env path (the flat
+// expansion's kernels: per parent a wave builds the state's view, counts the applicable bindings and writes each
+// successor row in canonical order), in chunks whose successor rows fit the candidate buffer:
+//   count    expansion pass 0 over the layer's parents: successor counts, an exclusive scan gives their offsets
+//   emit     expansion pass 1 over a chunk of parents: successor rows, their parents, indices and goal flags
+//   insert   the state set's probe over the candidate rows (stored equal rows drop a candidate; equal candidates keep
+//            the smallest index), the winner list, and compaction: winner rows into the arena with their node records
+//            (parent id, successor index: the reference's discoverer keys, src/mymyr/search/brfs.cpp:1362-1388) and
+//            goal flags
+// Every stored state's goal flag is written when the state is stored, so a layer's goal test reads flags. Ids, counts,
+// cuts and statuses follow the ground driver (brfs.hip) and the reference's run_flat (brfs.cpp:274-404). The lifted
+// expansion takes witness pruning off; a task whose schemas have witness parameters needs witness_pruning off here.
+
+#include "brfs.hpp"
+#include "brfs_common.hpp"
+#include "env.hpp"
+#include "runtime.hpp"
+#include "scan.hpp"
+#include "state_set.hpp"
+
+#include <algorithm>
+#include <cstring>
+
+namespace mya
+{
+namespace
+{
+constexpr int kWB = 256;
+constexpr u64 kWideStrideBlocks = 4096;
+
+/// Calls f.template operator()<G, K>() for the lane-group shape of rows of W > 16 words.
+template<class F>
+void wide_shape(u32 W, F&& f)
+{
+    if (W <= 32)
+        f.template operator()<16, 1>();
+    else if (W <= 128)
+        f.template operator()<64, 1>();
+    else if (W <= 256)
+        f.template operator()<64, 2>();
+    else if (W <= 512)
+        f.template operator()<64, 4>();
+    else if (W <= 1024)
+        f.template operator()<64, 8>();
+    else if (W <= 2048)
+        f.template operator()<64, 16>();
+    else
+        throw std::invalid_argument("mymyr_amd: brfs: states of more than 2048 words");
+}
+
+// The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena:
+// candidate row list[w] becomes state id0 + w with its node record (parent id << 32 | successor index) and goal flag.
+// A winner at or past `limit` sets kStatusCapacity.
+template<int G, int K>
+__global__ __launch_bounds__(kWB) void k_wide_compact(StateSetView s, const u64* __restrict__ rows, u64 m, const u32* __restrict__ list,
+                                                     const u64* __restrict__ size_now, const u64* __restrict__ size_next, u64 limit,
+                                                     const i32* __restrict__ parent, const i32* __restrict__ index,
+                                                     const u8* __restrict__ goal, u64 first, u64* __restrict__ nodes,
+                                                     u8* __restrict__ goal_id, u32* __restrict__ status)
+{
+    const u32 q = lane_id() % G;
+    const u64 id0 = *size_now;
+    const u64 winners = min(m, *size_next - id0);
+    for (u64 w = (static_cast<u64>(blockIdx.x) * kWB + threadIdx.x) / G; w < winners; w += static_cast<u64>(gridDim.x) * (kWB / G))
+    {
+        const u64 id = id0 + w;
+        if (id >= limit)
+        {
+            if (q == 0)
+                atomicOr(status, kStatusCapacity);
+            continue;
+        }
+        const u64 j = list[w];
+        Slice<G, K> r;
+        load_row<G, K>(rows + j * s.words, s.words, q, r);
+        store_row<G, K>(s.arena + id * s.words, s.words, q, r);
+        if (q == 0)
+        {
+            nodes[id] = ((first + static_cast<u64>(parent[j])) << 32) | static_cast<u32>(index[j]);
+            goal_id[id] = goal[j];
+        }
+    }
+}
+
+__global__ void k_read_u32(const u32* __restrict__ src, u64* __restrict__ dst) { *dst = *src; }
+
+/// Whether the task's goal holds in a row (host; the compiled goal lists).
+bool goal_holds(const CompiledTask& task, const std::vector<u64>& row)
+{
+    if (task.goal_unsat)
+        return false;
+    auto bit = [&](u32 s) { return s / 64 < row.size() && ((row[s / 64] >> (s % 64)) & 1); };
+    for (u32 s : task.goal_pos)
+        if (!bit(s))
+            return false;
+    for (u32 s : task.goal_neg)
+        if (bit(s))
+            return false;
+    return true;
+}
+
+/// The name of a schema with a parameter that no effect mentions (a witness parameter), or "" if none has one.
+std::string witness_schema(const CompiledTask& task)
+{
+    for (const SchemaText& s : task.text.schemas)
+    {
+        std::vector<u8> rel(s.arity, 0);
+        for (const Literal& l : s.eff)
+            for (i32 x : l.terms)
+                if (x >= 0)
+                    rel[static_cast<u32>(x)] = 1;
+        if (std::find(rel.begin(), rel.end(), 0) != rel.end())
+            return s.name;
+    }
+    return "";
+}
+}  // namespace
+
+BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc)
+{
+    const u32 W = task.words;
+    if (o.witness_pruning)
+    {
+        const std::string ws = witness_schema(task);
+        if (!ws.empty())
+            throw std::invalid_argument("mymyr_amd: brfs: states of " + std::to_string(W) + " words are expanded by the lifted "
+                                        "successor generator, which does not prune witness parameters, and schema " + ws +
+                                        " has one (run with witness_pruning off)");
+    }
+    BrfsResultC r;
+    const auto t0 = Clock::now();
+    hipStream_t stream = nullptr;
+    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "stream");
+    struct StreamGuard
+    {
+        hipStream_t s;
+        ~StreamGuard() { (void)hipStreamDestroy(s); }
+    } sg{stream};
+    Timers tm(o.timings != 0, stream, r);
+    const u64 R = static_cast<u64>(W) * 8;
+    Buffers b;
+    const bool bounded = o.max_states != ~u64{0};
+    // unbounded searches: an arena of at most 32 GiB by default
+    const u64 cap_states = bounded ? std::max<u64>(1, o.max_states)
+                                   : (o.memory_states ? o.memory_states : std::min<u64>(u64{1} << 26, (u64{32} << 30) / R));
+    // candidate rows per chunk: about 4 GiB of them by default
+    u64 chunk = o.chunk ? o.chunk : std::clamp<u64>((u64{4} << 30) / R, u64{1} << 12, u64{1} << 22);
+    chunk = std::min<u64>(chunk, kMaxBatch - 1);
+    StateSet set;
+    state_set_create(set, cap_states, W, 0.5, chunk, stream, chunk);
+    struct SetGuard
+    {
+        StateSet& s;
+        ~SetGuard() { state_set_destroy(s); }
+    } setg{set};
+    const u64 layer_cap = cap_states;
+    u32* counts = b.alloc<u32>(layer_cap, "layer counts");
+    u64* offsets = b.alloc<u64>(layer_cap + 1, "layer offsets");
+    u64* scan_scratch = b.alloc<u64>(scan_scratch_words(layer_cap), "scan scratch");
+    u8* goal_id = b.alloc<u8>(cap_states, "goal flags");
+    u64* nodes = b.alloc<u64>(cap_states, "search nodes");
+    u64* small = b.alloc<u64>(kSmall, "scalars");
+    u32* xstatus = b.alloc<u32>(2, "expansion status");  // [0] words needed, [1] status
+    hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
+    // candidate buffers of one chunk (the state set's batch arrays hold as many)
+    u64* cand_rows = b.alloc<u64>(chunk * W, "candidate rows");
+    i32* cand_parent = b.alloc<i32>(chunk, "candidate parents");
+    i32* cand_index = b.alloc<i32>(chunk, "candidate indices");
+    u8* cand_goal = b.alloc<u8>(chunk, "candidate goal flags");
+    r.memory_bytes = set.v.capacity * 8 + cap_states * (R + 8 + 1) + layer_cap * (4 + 8 + 8) + chunk * (R + 4 + 4 + 1 + 1 + 4);
+    enum
+    {
+        kFirstGoal = 0,
+        kChunkP = 1,  // chunk end parent, then its offset
+        kChunkOff = 2,
+        kSizeNow = 3,
+        kStatus = 4,
+        kTotal = 5,
+        kGoalSum = 6,
+        kFingerprint = 7,
+        kSpare = 8,  // the capacity status of a cut chunk's compaction (expected there, not an error)
+        kXStatus = 9,
+    };
+    auto set_small = [&](int idx, u64 v) { hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, small + idx, v); };
+    auto sync_small = [&] {
+        hip_check(hipMemcpyAsync(b.host, small, kSmall * sizeof(u64), hipMemcpyDeviceToHost, stream), "read scalars");
+        hip_check(hipStreamSynchronize(stream), "sync");
+    };
+    auto read_state = [&](const u64* total) {
+        hipLaunchKernelGGL(k_gather_small, dim3(1), dim3(1), 0, stream, small, int{kSizeNow}, state_set_size_now(set), int{kStatus},
+                           set.d_status, int{kTotal}, total);
+        hipLaunchKernelGGL(k_read_u32, dim3(1), dim3(1), 0, stream, xstatus + 1, small + kXStatus);
+        launch_check("gather");
+    };
+    auto check_expansion = [&] {
+        if (b.host[kXStatus] & ~u64{kStatusWideRow})
+            throw std::runtime_error("mymyr_amd: brfs: expansion status " + std::to_string(b.host[kXStatus]));
+        if (b.host[kStatus] & kStatusTableFull)
+            throw std::length_error("mymyr_amd: brfs: state table full");
+    };
+    launch_fill_u32(xstatus, 2, 0, stream);
+    // the start state
+    {
+        std::vector<u64> s0(W, 0);
+        std::copy(task.initial.begin(), task.initial.end(), s0.begin());
+        u64* d_s0 = b.alloc<u64>(W, "start state");
+        hip_check(hipMemcpyAsync(d_s0, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
+        u64 nn = 0;
+        state_set_insert(set, d_s0, 1, nullptr, nullptr, &nn, stream);
+        hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, nodes, ~u64{0});
+        const u8 g0 = goal_holds(task, s0) ? 1 : 0;
+        hip_check(hipMemcpyAsync(goal_id, &g0, 1, hipMemcpyHostToDevice, stream), "start goal");
+        hip_check(hipStreamSynchronize(stream), "start state");
+    }
+    ExpandArgs base_args{};
+    base_args.T = T;
+    base_args.words = W;
+    base_args.out_words = W;
+    base_args.label_width = 0;
+    base_args.status = xstatus + 1;
+    base_args.words_needed = xstatus;
+    const auto td0 = Clock::now();
+    bool stopped = false, budget_stopped = false;
+    r.status = kExhausted;
+    u64 pos = 0;
+    while (!stopped)
+    {
+        if (pos >= set.size)
+            break;
+        if (bounded && set.size >= o.max_states)
+        {
+            r.status = kOutOfStates;
+            break;
+        }
+        if (r.expanded >= o.max_expanded)
+        {
+            r.status = kOutOfStates;
+            budget_stopped = true;
+            break;
+        }
+        if (r.layers == o.max_depth)
+            break;
+        ++r.layers;
+        const u64 lb = pos, le = set.size, ln = le - lb;
+        std::array<u64, 3> row{0, 0, 0};
+        const u64 size0 = set.size;
+        const u64 budget = o.max_expanded == ~u64{0} ? ~u64{0} : o.max_expanded - r.expanded;
+        u64 lim = std::min(ln, budget);
+        // the layer's first goal state among the parents to expand, and their successor counts
+        set_small(kFirstGoal, ~u64{0});
+        hipLaunchKernelGGL(k_first_u8, dim3(std::min<u64>(blocks_for(lim, 256), 4096)), dim3(256), 0, stream, goal_id + lb, lim,
+                           small + kFirstGoal);
+        launch_check("goal search");
+        tm.begin(kKCount);
+        ExpandArgs a = base_args;
+        a.states = set.v.arena + lb * W;
+        a.rows = lim;
+        a.pass = 0;
+        a.counts = counts;
+        launch_expand(a, stream);
+        tm.end(kKCount, lim * (R + 4));
+        tm.begin(kKOther);
+        launch_exclusive_scan(counts, offsets, lim, scan_scratch, offsets + lim, stream);
+        tm.end(kKOther, 0);
+        read_state(offsets + lim);
+        sync_small();
+        check_expansion();
+        const u64 first_goal = b.host[kFirstGoal];
+        bool goal_stop = false;
+        if (first_goal != ~u64{0} && o.stop_at_goal && first_goal < lim)
+        {
+            lim = first_goal;
+            goal_stop = true;
+        }
+        u64 layer_goals = 0;
+        u64 p0 = 0, base = 0;
+        while (p0 < lim && !stopped)
+        {
+            hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, 1u, p0, lim, base + chunk, small + kChunkP);
+            launch_check("chunk end");
+            sync_small();
+            const u64 p1 = b.host[kChunkP], end_off = b.host[kChunkOff];
+            const u64 m = end_off - base;
+            if (m > chunk)
+                throw std::length_error("mymyr_amd: brfs: a state has " + std::to_string(m) + " successors, more than a chunk of " +
+                                        std::to_string(chunk) + " candidates holds (raise the chunk option)");
+            if (m > 0)
+            {
+                tm.begin(kKEmit);
+                ExpandArgs e = base_args;
+                e.states = set.v.arena + (lb + p0) * W;
+                e.rows = p1 - p0;
+                e.pass = 1;
+                e.offsets = offsets + p0;
+                e.offset_base = base;
+                e.capacity = m;
+                e.succ = cand_rows;
+                e.parent = cand_parent;
+                e.index = cand_index;
+                e.goal = cand_goal;
+                e.counts = counts + p0;
+                launch_expand(e, stream);
+                tm.end(kKEmit, (p1 - p0) * R + m * (R + 9));
+                tm.begin(kKInsert);
+                state_set_begin_batch(set, stream);
+                state_set_probe(set, cand_rows, m, stream);
+                tm.end(kKInsert, m * (R + 8));
+                tm.begin(kKRank);
+                state_set_rank(set, m, stream);
+                tm.end(kKRank, m * 9);
+                tm.begin(kKCompact);
+                set_small(kSpare, 0);
+                wide_shape(W, [&]<int G, int K>() {
+                    hipLaunchKernelGGL((k_wide_compact<G, K>), dim3(std::min<u64>(blocks_for(m * G, kWB), kWideStrideBlocks)), dim3(kWB), 0, stream,
+                                       set.v, cand_rows, m, set.list, state_set_size_now(set), state_set_size_next(set),
+                                       bounded ? o.max_states : cap_states, cand_parent, cand_index, cand_goal, lb + p0, nodes, goal_id,
+                                       bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
+                });
+                launch_check("wide compact");
+                tm.end(kKCompact, 0);
+                state_set_flip(set);
+            }
+            // the chunk's goal parents, its outcome and the expansion's status in one synchronization
+            set_small(kGoalSum, 0);
+            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(p1 - p0, 256), 1024)), dim3(256), 0, stream, goal_id + lb + p0,
+                               p1 - p0, small + kGoalSum);
+            read_state(nullptr);
+            sync_small();
+            check_expansion();
+            const u64 size_dev = b.host[kSizeNow];
+            const u64 winners = size_dev - set.size;
+            const u64 room = (bounded ? o.max_states : cap_states) - set.size;
+            tm.bytes(kKCompact, std::min(winners, room) * (2 * R + 21));
+            if (bounded && winners >= room && winners > 0)
+            {
+                // the store filled at winner room - 1 (id max_states - 1): the search stops inside its parent's expansion
+                u32 jc = 0;
+                hip_check(hipMemcpy(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost), "cut");
+                i32 pc = 0;
+                hip_check(hipMemcpy(&pc, cand_parent + jc, sizeof(i32), hipMemcpyDeviceToHost), "cut parent");
+                row[0] += static_cast<u64>(pc) + 1;
+                row[1] += u64{jc} + 1;
+                set_small(kGoalSum, 0);
+                hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(static_cast<u64>(pc) + 1, 256), 1024)), dim3(256), 0, stream,
+                                   goal_id + lb + p0, static_cast<u64>(pc) + 1, small + kGoalSum);
+                sync_small();
+                layer_goals += b.host[kGoalSum];
+                set.size = o.max_states;
+                r.status = kOutOfStates;
+                stopped = true;
+                break;
+            }
+            if (winners > room)
+                throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
+                                        " states of device memory (set max_states or memory_states)");
+            set.size = size_dev;
+            row[0] += p1 - p0;
+            row[1] += m;
+            layer_goals += b.host[kGoalSum];
+            p0 = p1;
+            base = end_off;
+        }
+        r.goal_states += layer_goals;
+        pos = lb + row[0];
+        r.expanded += row[0];
+        r.generated += row[1];
+        row[2] = set.size - size0;
+        const u64 tested = row[0] + ((goal_stop && !stopped) ? 1 : 0);
+        if (first_goal != ~u64{0} && first_goal < tested && r.first_goal < 0)
+            r.first_goal = static_cast<i64>(lb + first_goal);
+        if (goal_stop && !stopped)
+        {
+            r.goal_states += 1;
+            r.status = kSolved;
+            stopped = true;
+        }
+        if (!goal_stop && !stopped && lim < ln)
+        {
+            r.status = kOutOfStates;
+            budget_stopped = true;
+            stopped = true;
+        }
+        lc.push_back(row);
+        if (!stopped)
+            pos = le;
+    }
+    r.states = set.size;
+    r.exhausted = (!stopped && pos >= set.size) ? 1 : 0;
+    r.solved = r.first_goal >= 0 ? 1 : 0;
+    if (r.solved)
+        r.status = kSolved;
+    else if (!budget_stopped)
+        r.status = (r.exhausted || r.layers >= o.max_depth) ? kExhausted : kOutOfStates;
+    hip_check(hipStreamSynchronize(stream), "brfs");
+    r.device_s = std::chrono::duration<double>(Clock::now() - td0).count();
+    tm.collect();
+    if (o.fingerprint)
+    {
+        const u64* d_slot_cid = nullptr;
+        if (task.mode != AtomMode::Dense)
+        {
+            u64* c = b.alloc<u64>(task.slot_cid.size(), "slot canonical ids");
+            hip_check(hipMemcpy(c, task.slot_cid.data(), task.slot_cid.size() * sizeof(u64), hipMemcpyHostToDevice), "slot ids");
+            d_slot_cid = c;
+        }
+        set_small(kFingerprint, 0);
+        hipLaunchKernelGGL(k_fingerprint, dim3(std::min<u64>(blocks_for(set.size, 256), 2048)), dim3(256), 0, stream, set.v.arena,
+                           set.size, W, d_slot_cid, small + kFingerprint);
+        launch_check("fingerprint");
+        sync_small();
+        r.fingerprint = b.host[kFingerprint];
+    }
+    if (r.solved)
+    {
+        // the plan from the node records: each names its parent and the successor's index in the parent's canonical
+        // order; the label is that successor of the parent's expansion, generated again (brfs.cpp:1362-1388)
+        std::vector<std::pair<u64, u32>> rev;
+        for (u64 v = static_cast<u64>(r.first_goal);;)
+        {
+            u64 nd = 0;
+            hip_check(hipMemcpy(&nd, nodes + v, sizeof(u64), hipMemcpyDeviceToHost), "plan node");
+            if (nd == ~u64{0})
+                break;
+            rev.push_back({nd >> 32, static_cast<u32>(nd)});
+            v = nd >> 32;
+            if (rev.size() > r.layers)
+                throw std::logic_error("mymyr_amd: brfs: the node records of the goal state form no path to the start");
+        }
+        const u32 L = std::max<u32>(1, task.label_width);
+        r.plan_width = L;
+        u64* zero = b.alloc<u64>(1, "plan offset");
+        hip_check(hipMemset(zero, 0, sizeof(u64)), "plan offset");
+        for (auto it = rev.rbegin(); it != rev.rend(); ++it)
+        {
+            ExpandArgs a = base_args;
+            a.states = set.v.arena + it->first * W;
+            a.rows = 1;
+            a.pass = 0;
+            a.counts = counts;
+            launch_expand(a, stream);
+            u32 c = 0;
+            hip_check(hipMemcpyAsync(&c, counts, sizeof(u32), hipMemcpyDeviceToHost, stream), "plan count");
+            hip_check(hipStreamSynchronize(stream), "plan count");
+            if (it->second >= c)
+                throw std::logic_error("mymyr_amd: brfs: a node record names a successor its parent does not have");
+            i32* sch = b.alloc<i32>(c, "plan schemas");
+            i32* bnd = b.alloc<i32>(static_cast<u64>(c) * L, "plan bindings");
+            ExpandArgs e = a;
+            e.pass = 1;
+            e.offsets = zero;
+            e.capacity = c;
+            e.schema = sch;
+            e.binding = bnd;
+            e.label_width = L;
+            launch_expand(e, stream);
+            std::vector<i32> lab(1 + L);
+            hip_check(hipMemcpyAsync(lab.data(), sch + it->second, sizeof(i32), hipMemcpyDeviceToHost, stream), "plan schema");
+            hip_check(hipMemcpyAsync(lab.data() + 1, bnd + static_cast<u64>(it->second) * L, L * sizeof(i32), hipMemcpyDeviceToHost, stream),
+                      "plan binding");
+            hip_check(hipStreamSynchronize(stream), "plan label");
+            r.plan_schema.push_back(lab[0]);
+            r.plan_binding.insert(r.plan_binding.end(), lab.begin() + 1, lab.end());
+        }
+        r.cost = static_cast<double>(rev.size());
+        r.goal_state.resize(W);
+        hip_check(hipMemcpy(r.goal_state.data(), set.v.arena + static_cast<u64>(r.first_goal) * W, R, hipMemcpyDeviceToHost), "goal state");
+    }
+    r.search_s = std::chrono::duration<double>(Clock::now() - t0).count();
+    return r;
+}
+}  // namespace mya

@@ -287,7 +287,7 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
             r.states = 1;
         }
         else
-            r = brfs_device(*task->compiled, o, lc, &task->brfs);
+            r = brfs_device(*task->compiled, o, lc, &task->brfs, task->compiled->words > 16 ? device_task(task).thost.get() : nullptr);
         std::memset(result, 0, sizeof(*result));
         result->status = r.status;
         result->solved = r.solved;

@@ -2133,7 +2133,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
         noops += noop ? 1 : 0;
         if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
         {
-            const u64 pos = A.offsets[i] + (A.drop_noops ? kept : k);
+            const u64 pos = A.offsets[i] - A.offset_base + (A.drop_noops ? kept : k);
             ++kept;
             const u32 n = (A.succ || A.succ_hash) ? trimmed_words(L.row, T.W, lane) : 0;
             const bool fits = n <= A.out_words;

@@ -248,6 +248,7 @@ struct ExpandArgs
     u32* counts;      // [rows]
     u32* noops;       // [rows]
     const u64* offsets;  // [rows]
+    u64 offset_base;     // subtracted from offsets (a chunk of a longer expansion writes from its own position 0)
     u64 capacity;
     u64* succ;
     i32* parent;

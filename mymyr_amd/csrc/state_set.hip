@@ -316,6 +316,18 @@ void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
     launch_check("state set rank");
 }
 
+void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream)
+{
+    if (m == 0)
+        return;
+    with_shape(s.v.words, [&]<int G, int K>() {
+        hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, rows, m, nullptr, s.flags,
+                           s.d_status);
+    });
+    launch_check("state set probe");
+    s.last = stream;
+}
+
 void state_set_sync(StateSet& s)
 {
     // the size and status words are read here only (an asynchronous insert copies nothing back)

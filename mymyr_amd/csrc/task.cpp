@@ -1403,6 +1403,77 @@ u32 CompiledTask::slot_of_atom(u32 pred, const u32* objs) const
     return c < layout.fluent_count ? slot_of[c] : kNone;
 }
 
+namespace
+{
+/// The witness parameters of schema si (those no effect mentions) in the order the reference's successor matcher binds
+/// them (src/mymyr/task/compile.cpp:916-946): after every effect-relevant parameter, greedily the one with the most
+/// binary constraints to placed parameters, then the most fluent unary constraints, then the fewest dom0 objects, ties
+/// to the smallest parameter. The constraints are counted as the matcher builds them with every parameter free
+/// (compile.cpp:826-907): a binary per arity-2 literal over two distinct parameters, and per pair i < j of distinct
+/// parameters of a positive static literal of arity 3 or more; a fluent unary per arity-1 fluent literal and per
+/// arity-2 fluent literal of one parameter and one constant.
+std::vector<u32> witness_order(const CompiledTask& task, u32 si, const std::vector<u8>& relevant)
+{
+    const TaskText& T = task.text;
+    const SchemaText& s = T.schemas[si];
+    std::vector<std::pair<u32, u32>> bin;
+    std::vector<long> unary(s.arity, 0);
+    for (const Literal& l : s.pre)
+    {
+        const PredicateText& P = T.preds[l.pred];
+        const bool fluent = P.kind != 'S';
+        const auto& t = l.terms;
+        if (std::none_of(t.begin(), t.end(), [](i32 x) { return x >= 0; }))
+            continue;
+        if (P.arity == 1)
+        {
+            if (fluent)
+                ++unary[static_cast<u32>(t[0])];
+            continue;
+        }
+        if (P.arity == 2 && t[0] != t[1])
+        {
+            if (t[0] >= 0 && t[1] >= 0)
+                bin.push_back({static_cast<u32>(t[0]), static_cast<u32>(t[1])});
+            else if (fluent)
+                ++unary[static_cast<u32>(t[0] >= 0 ? t[0] : t[1])];
+            continue;
+        }
+        if (!fluent && l.positive && P.arity >= 3)
+            for (u32 i = 0; i < P.arity; ++i)
+                for (u32 j = i + 1; j < P.arity; ++j)
+                    if (t[i] >= 0 && t[j] >= 0 && t[i] != t[j])
+                        bin.push_back({static_cast<u32>(t[i]), static_cast<u32>(t[j])});
+    }
+    std::vector<u8> placed(relevant.begin(), relevant.end());
+    std::vector<u32> order;
+    for (;;)
+    {
+        int best = -1;
+        long best_score = 0;
+        for (u32 v = 0; v < s.arity; ++v)
+        {
+            if (placed[v])
+                continue;
+            long links = 0;
+            for (const auto& [a, b] : bin)
+                links += (a == v && placed[b]) || (b == v && placed[a]);
+            long pc = 0;
+            for (u64 w : task.dom0[si][v])
+                pc += std::popcount(w);
+            const long score = links * 1000000 + unary[v] * 10000 - pc;
+            if (best < 0 || score > best_score)
+                best = static_cast<int>(v), best_score = score;
+        }
+        if (best < 0)
+            break;
+        placed[static_cast<u32>(best)] = 1;
+        order.push_back(static_cast<u32>(best));
+    }
+    return order;
+}
+}  // namespace
+
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit)
 {
     const TaskText& T = task.text;
@@ -1415,26 +1486,20 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
         return kNone;
     }();
     (void)eq;  // the successor engine reads "=" as a static relation over its initial atoms, as the reference does
-    std::map<std::vector<u32>, std::vector<u32>> groups;  // (schema, relevant objects) -> members, witness ascending
+    // (schema, effect-relevant objects) -> members with their witness objects in the matcher's witness order
+    std::map<std::vector<u32>, std::vector<std::pair<std::vector<u32>, u32>>> groups;
     for (u32 si = 0; si < T.schemas.size(); ++si)
     {
         const SchemaText& s = T.schemas[si];
-        i32 witness = -1;
+        std::vector<u8> rel(s.arity, 0);
+        std::vector<u32> wit;  // witness parameters in the matcher's order
         if (witness_pruning)
         {
-            std::vector<u8> rel(s.arity, 0);
             for (const Literal& l : s.eff)
                 for (i32 x : l.terms)
                     if (x >= 0)
                         rel[x] = 1;
-            for (u32 v = 0; v < s.arity; ++v)
-                if (!rel[v])
-                {
-                    if (witness >= 0)
-                        throw Error("schema " + s.name + " has several parameters no effect mentions; the device BrFS prunes one "
-                                    "witness parameter per schema (run with witness_pruning off)");
-                    witness = static_cast<i32>(v);
-                }
+            wit = witness_order(task, si, rel);
         }
         if (task.never[si])
             continue;
@@ -1523,24 +1588,33 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
             }
         };
         rec(0);
-        if (witness >= 0)
+        if (!wit.empty())
             for (u32 a = first_action; a < g.meta.size(); ++a)
             {
+                const u32* b = g.binding.data() + static_cast<size_t>(a) * g.label_width;
                 std::vector<u32> key{si};
                 for (u32 v = 0; v < s.arity; ++v)
-                    if (static_cast<i32>(v) != witness)
-                        key.push_back(g.binding[static_cast<size_t>(a) * g.label_width + v]);
-                groups[key].push_back(a);
+                    if (rel[v])
+                        key.push_back(b[v]);
+                std::vector<u32> w;
+                for (u32 v : wit)
+                    w.push_back(b[v]);
+                groups[key].push_back({std::move(w), a});
             }
     }
     if (witness_pruning)
     {
-        // dominators: the group's members with a smaller witness object. Members are in lexicographic binding order,
-        // so within a group (fixed effect-relevant objects) they ascend in the witness object.
+        // dominators: the group's members (fixed effect-relevant objects) whose witness objects come first in the
+        // matcher's witness order; an action is a successor only if none of them applies (the matcher emits the first
+        // witness binding it finds, include/mymyr/successor/detail/engine.hpp:345-356)
         std::vector<std::vector<u32>> doms(g.meta.size());
-        for (const auto& [key, members] : groups)
+        for (auto& [key, members] : groups)
+        {
+            std::sort(members.begin(), members.end());
             for (size_t i = 1; i < members.size(); ++i)
-                doms[members[i]].assign(members.begin(), members.begin() + static_cast<long>(i));
+                for (size_t k = 0; k < i; ++k)
+                    doms[members[i].second].push_back(members[k].second);
+        }
         g.dom_off.assign(g.meta.size() + 1, 0);
         for (u32 a = 0; a < g.meta.size(); ++a)
         {

@@ -294,10 +294,10 @@ struct GroundActions
 };
 
 /// Grounds every schema (static literals filter the bindings). Throws if more than `limit` actions result, or if an
-/// action has more than 255 atoms in one list. With `witness_pruning`, a schema may have at most one parameter that
-/// no effect mentions (a witness): among the applicable actions with one effect-relevant binding the one with the
-/// smallest witness object is the successor, the binding the reference's matcher finds first when the witness is its
-/// only unbound parameter (include/mymyr/successor/detail/engine.hpp:345-356). More witnesses throw.
+/// action has more than 255 atoms in one list. With `witness_pruning`, the parameters no effect mentions (witnesses)
+/// are pruned as the reference's matcher does: among the applicable actions with one effect-relevant binding the
+/// successor is the one whose witness objects come first in the matcher's witness order, the binding it finds first
+/// (include/mymyr/successor/detail/engine.hpp:345-356; the order: src/mymyr/task/compile.cpp:916-946).
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit);
 
 inline u32 words_for(u64 bits) { return static_cast<u32>((bits + 63) >> 6); }

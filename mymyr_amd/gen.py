@@ -136,6 +136,35 @@ def gridworld(width: int = 32, height: int = 32, blocked: float = 0.2, seed: int
     return "\n".join(lines) + "\n"
 
 
+def witness_task(items: int = 6, places: int = 6, seed: int = 0) -> str:
+    """A task whose actions have two witness parameters (parameters no effect mentions) that the successor matcher binds
+    in an order other than the parameter order: work(?x ?w1 ?w2) with pre todo(?x), link(?w1 ?w2), tool(?w2), effect
+    del todo(?x), add done(?x); the fluent unary tool(?w2) makes the matcher bind ?w2 first. toggle(?t ?u) moves a tool
+    along static near(?t ?u); relink(?a ?b ?c) moves a link's end along near. Objects: items [0, items), places
+    after. Goal: every item done."""
+    rng = Xoshiro256(seed)
+    P0 = items
+    places_ = list(range(P0, P0 + places))
+    near = sorted({(a, b) for a in places_ for b in places_ if a != b and rng.uniform() < 0.4})
+    links = sorted({(places_[rng.bounded(places)], places_[rng.bounded(places)]) for _ in range(places)})
+    tools = sorted({places_[rng.bounded(places)] for _ in range(2)})
+    # predicates: 0 S near, 1 S item, 2 F todo, 3 F done, 4 F tool, 5 F link
+    lines = [f"O {items + places}", "P 6", "S 2 near", "S 1 item", "F 1 todo", "F 1 done", "F 1 tool", "F 2 link",
+             f"SI {len(near) + items}"]
+    lines += [f"0 {a} {b}" for a, b in near] + [f"1 {x}" for x in range(items)]
+    lines += [f"FI {items + len(tools) + len(links)}"] + [f"2 {x}" for x in range(items)] + [f"4 {t}" for t in tools]
+    lines += [f"5 {a} {b}" for a, b in links]
+    lines += [f"G {items}"] + [f"3 1 {x}" for x in range(items)]
+    lines += ["A 3"]
+    lines += ["work 3", "L 4", _lit(2, True, [0]), _lit(1, True, [0]), _lit(5, True, [1, 2]), _lit(4, True, [2]),
+              "E 1", "0", "L 0", "F 2", _lit(2, False, [0]), _lit(3, True, [0])]
+    lines += ["toggle 2", "L 2", _lit(4, True, [0]), _lit(0, True, [0, 1]),
+              "E 1", "0", "L 0", "F 2", _lit(4, False, [0]), _lit(4, True, [1])]
+    lines += ["relink 3", "L 2", _lit(5, True, [0, 1]), _lit(0, True, [1, 2]),
+              "E 1", "0", "L 0", "F 2", _lit(5, False, [0, 1]), _lit(5, True, [0, 2])]
+    return "\n".join(lines) + "\n"
+
+
 def random_strips(props: int = 512, actions: int = 4096, init_atoms: int = 64, goal_atoms: int = 8, walk: int = 32,
                   seed: int = 0) -> str:
     """A random ground STRIPS task: `props` nullary fluents, `actions` nullary schemas with 1-4 precondition atoms,

@@ -30,7 +30,8 @@ SUITE_COUNTS = {
     "pegsol-08-strips__p22": (99457, 189967, 2),
     "pathways__p02": (669078, 11237052, 12288),
 }
-# rovers__p02 has schemas with two witness parameters (device witness pruning takes one): env and layout only
+# suite tasks outside the published counts whose slot tables are pinned too (rovers__p02's schemas have two witness
+# parameters; its BrFS is pinned in brfs_witness.json)
 LAYOUT_ONLY = ["rovers__p02"]
 
 # the reference's own determinism digests of search.brfs(max_states=20000, fingerprint=True, stop_at_goal=False):

@@ -21,7 +21,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
 
-from mymyr_amd import workloads  # noqa: E402
+from mymyr_amd import gen, workloads  # noqa: E402
 from oracle import ref  # noqa: E402
 from tests.golden import fixtures as fx  # noqa: E402
 
@@ -309,6 +309,48 @@ def make_visited_mask():
     dump("visited_mask.json", out)
 
 
+WITNESS_TASKS = {"witness_order_5": 5, "witness_order_0": 0}
+
+
+def make_brfs_witness():
+    """BrFS with witness pruning over schemas with several witness parameters (bound by the matcher in an order other
+    than the parameter order): counts, fingerprints and the plans whose labels carry the witness choices."""
+    for name, seed in WITNESS_TASKS.items():
+        with open(fx.task_path(name), "w") as f:
+            f.write(gen.witness_task(seed=seed))
+    out = {"witness_order_5": brfs_record("witness_order_5", stop_at_goal=False),
+           "witness_order_5:goal": brfs_record("witness_order_5", stop_at_goal=True),
+           "witness_order_0:goal": brfs_record("witness_order_0", stop_at_goal=True),
+           "witness_order_0:cut": brfs_record("witness_order_0", stop_at_goal=False, max_states=50000),
+           "rovers__p02": brfs_record("rovers__p02", stop_at_goal=False),
+           "rovers__p02:goal": brfs_record("rovers__p02", stop_at_goal=True),
+           "rovers__p02:expanded": brfs_record("rovers__p02", stop_at_goal=False, max_expanded=20000)}
+    dump("brfs_witness.json", out)
+
+
+WIDE_TASKS = {"transport_w20_3": dict(locations=20, trucks=4, packages=50, goals=1, seed=3),
+              "transport_w20_7": dict(locations=20, trucks=4, packages=50, goals=1, seed=7)}
+
+
+def make_brfs_wide():
+    """BrFS over rows wider than 16 words (the lifted-expansion driver): typed transport instances of 20 words (plans of
+    3 and 4 actions, cuts, an expansion budget), the transport workload's 176-word rows at max_states and depth cuts,
+    and a 19-word task with witness parameters searched with witness pruning off."""
+    for name, kw in WIDE_TASKS.items():
+        with open(fx.task_path(name), "w") as f:
+            f.write(gen.transport(**kw))
+    with open(fx.task_path("witness_wide"), "w") as f:
+        f.write(gen.witness_task(items=60, places=32, seed=2))
+    out = {"transport_w20_3:goal": brfs_record("transport_w20_3", stop_at_goal=True),
+           "transport_w20_7:goal": brfs_record("transport_w20_7", stop_at_goal=True),
+           "transport_w20_3:cut": brfs_record("transport_w20_3", stop_at_goal=False, max_states=200000),
+           "transport_w20_7:expanded": brfs_record("transport_w20_7", stop_at_goal=False, max_expanded=5000),
+           "transport:cut": brfs_record("transport", stop_at_goal=False, max_depth=12, max_states=100000),
+           "transport:depth2": brfs_record("transport", stop_at_goal=False, max_depth=2),
+           "witness_wide:cut": brfs_record("witness_wide", "dense", stop_at_goal=False, witness_pruning=False, max_states=50000)}
+    dump("brfs_wide.json", out)
+
+
 def make_pool():
     """Digests of every batch the reference CpuEnvPool returns over each pool case's scripted calls."""
     out = {}
@@ -363,7 +405,8 @@ def main():
     a = ap.parse_args()
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
-             "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
+             "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool,
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -118,8 +118,39 @@ def test_small_chunks_do_not_change_results(golden):
     assert a == b
 
 
-def test_unsupported_witness_pattern_refused(golden):
+
+
+@pytest.mark.parametrize("key", ["witness_order_5", "witness_order_5:goal", "witness_order_0:goal", "witness_order_0:cut",
+                                 "rovers__p02", "rovers__p02:goal", "rovers__p02:expanded"])
+def test_several_witness_parameters(golden, key):
+    """Witness pruning over schemas with two witness parameters, which the reference's matcher binds in its own order
+    (here not the parameter order): counts, fingerprints, statuses and, for solved searches, plans (whose labels carry
+    the witness objects the matcher finds first) equal to the reference's."""
+    exp = golden.load("brfs_witness.json")[key]
+    name = key.split(":")[0]
+    r = device(golden, name, full=True, **exp["options"])
+    assert not same(r, exp), (key, same(r, exp))
+    assert same_plan(r, exp), (key, r["result"].plan[:6], exp.get("plan", [])[:6])
+
+
+WIDE_ATOMS = {"witness_wide": "dense"}
+
+
+@pytest.mark.parametrize("key", ["transport_w20_3:goal", "transport_w20_7:goal", "transport_w20_3:cut", "transport_w20_7:expanded",
+                                 "transport:cut", "transport:depth2", "witness_wide:cut"])
+def test_wide_rows(golden, key):
+    """Rows wider than 16 words (typed transport of 20 and of 176 words, a 19-word dense task) take the driver over the
+    lifted expansion: layer counts, fingerprints, statuses, cuts and plans equal to the reference's."""
+    exp = golden.load("brfs_wide.json")[key]
+    name = key.split(":")[0]
+    print(f"wide brfs: {key}", flush=True)
+    r = device(golden, name, WIDE_ATOMS.get(name, "auto"), full=True, **exp["options"])
+    assert not same(r, exp), (key, same(r, exp))
+    assert same_plan(r, exp), (key, r["result"].plan[:6], exp.get("plan", [])[:6])
+
+
+def test_wide_rows_refuse_witness_pruning_over_witness_parameters(golden):
     from mymyr_amd._lib import MyaError
 
     with pytest.raises(MyaError, match="witness"):
-        device(golden, "rovers__p02", stop_at_goal=False)
+        device(golden, "witness_wide", "dense", stop_at_goal=False, max_states=1000)
