@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 12
+#define MYA_ABI_VERSION 13
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -428,10 +428,26 @@ typedef struct mya_brfs_options
     uint64_t memory_states;  /* state capacity when max_states is unbounded (0: 2^26) */
     int32_t timings;         /* time each kernel class with HIP events (mya_brfs_result.kernel_ms) */
     int32_t reserved;
+    /* BrfsOptions::start and blocked_states (brfs.hpp:82-83): host rows of `words` words (the task's row words,
+     * mya_task_info.words). start (null: the task's initial state) replaces the initial state; the blocked_count
+     * rows are never stored: a successor equal to one of them counts as generated and pruned (the start state is
+     * exempt: it is stored even if blocked). */
+    const uint64_t* start;
+    const uint64_t* blocked;
+    uint64_t blocked_count;
+    uint32_t words;
+    /* BrfsOptions::max_seconds and cancel (brfs.hpp:97-98): with timed != 0 the search stops with status 3
+     * (OutOfTime) once max_seconds of wall time have passed (max_seconds <= 0: before the first expansion); cancel
+     * (null: none) is a flag that another thread sets nonzero to stop the search with status 4 (Cancelled). Both are
+     * checked between device batches (the reference checks every 8 expansions), so a stopped search's counts stop at
+     * a batch boundary. */
+    int32_t timed;
+    double max_seconds;
+    const volatile int32_t* cancel;
 } mya_brfs_options;
 
 /* BrfsResult fields (include/mymyr/search/brfs.hpp:103-138). status: the reference's SearchStatus codes
- * (0 solved, 1 exhausted, 2 out of states, 5 failed, 6 unsolvable). */
+ * (0 solved, 1 exhausted, 2 out of states, 3 out of time, 4 cancelled, 5 failed, 6 unsolvable). */
 typedef struct mya_brfs_result
 {
     int32_t status;
@@ -451,7 +467,7 @@ typedef struct mya_brfs_result
     double kernel_ms[8];
     uint64_t kernel_bytes[8];
     uint64_t kernel_launches[8];
-    uint64_t pruned;       /* successors not stored because they are blocked (no blocked states here: 0) */
+    uint64_t pruned;       /* successors not stored because they are blocked states */
     uint64_t memory_bytes; /* device bytes of the search's buffers (state set, arena, nodes, chunk and layer arrays) */
 } mya_brfs_result;
 

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 12  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 13  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -111,6 +111,13 @@ class BrfsOptions(Structure):
         ("memory_states", c_uint64),
         ("timings", c_int32),
         ("reserved", c_int32),
+        ("start", c_void_p),
+        ("blocked", c_void_p),
+        ("blocked_count", c_uint64),
+        ("words", c_uint32),
+        ("timed", c_int32),
+        ("max_seconds", c_double),
+        ("cancel", c_void_p),
     ]
 
 

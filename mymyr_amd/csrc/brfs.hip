@@ -330,7 +330,7 @@ constexpr int kPairs = W >= 4 ? 2 : 1;  // word pairs per lane
 // takes it as pending). Losers' flags are cleared, winners' stay 1.
 template<int W>
 __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W> src, u64 m, u8* __restrict__ flags,
-                                                      u32* __restrict__ status)
+                                                      u32* __restrict__ status, BlockedView blocked)
 {
     constexpr int G = kGroup<W>;
     const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
@@ -340,6 +340,19 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     Slice<G, kPairs<W>> me;
     src.load(j, q, me);
     const u64 h = group_hash<G, kPairs<W>>(me, q, gbase);
+    if (blocked.capacity)
+    {
+        // the blocked test precedes the store (brfs.cpp:350-361): a blocked candidate takes no entry and no id
+        const bool hit = group_blocked<G, kPairs<W>>(blocked, me, h, q, gbase);
+        if (q == 0)
+        {
+            blocked.hit[j] = hit ? 1 : 0;
+            if (hit)
+                flags[j] = 0;
+        }
+        if (hit)
+            return;
+    }
     const ProbeResult r = probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, flags, status);
     if (q == 0 && r.lose)
         flags[j] = 0;
@@ -565,6 +578,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         kCut = 5,       // the candidate of the state that fills the store
         kBlockTotal = 6,
         kFingerprint = 7,
+        kChunkPruned = 11,  // blocked candidates of a chunk (read at the synchronization that confirms it)
+        kCutPruned = 12,    // blocked candidates of a cut chunk up to the cut
     };
     auto set_small = [&](int idx, u64 v) { hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, small + idx, v); };
     auto sync_small = [&] {
@@ -572,10 +587,10 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         hip_check(hipStreamSynchronize(stream), "sync");
     };
 
-    // the start state
+    const BlockedView blocked = upload_blocked(o.blocked, task.words, W, chunk, b, stream);
+    // the start state (stored even if blocked)
     {
-        std::vector<u64> s0(W, 0);
-        std::copy(task.initial.begin(), task.initial.end(), s0.begin());
+        const std::vector<u64> s0 = start_row(task, o, W);
         u64* d_s0 = b.alloc<u64>(W, "start state");
         hip_check(hipMemcpyAsync(d_s0, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
         u64 nn = 0;
@@ -584,6 +599,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         launch_check("root node");
     }
     const auto td0 = Clock::now();
+    Halt halt(o, t0);
     bool stopped = false, budget_stopped = false;
     r.status = kExhausted;
     u64 pos = 0;                           // states expanded or passed (the reference's queue position)
@@ -603,6 +619,11 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             budget_stopped = true;
             break;
         }
+        if (halt.check())
+        {
+            stopped = true;
+            break;
+        }
         if (r.layers == o.max_depth)
             break;
         ++r.layers;
@@ -618,6 +639,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         u64 first_goal = ~u64{0};
         bool goal_stop = false;
         u64 layer_goals = 0;   // goal states among the layer's expanded parents (confirmed chunks)
+        u64 layer_pruned = 0;  // blocked successors of the confirmed chunks
         u64 p0 = 0, base = 0;  // base = offsets[p0 * S]
         constexpr int G = kGroup<W>;
         // The chunk whose kernels are queued but whose outcome (its winners) the host has not read yet: it is confirmed
@@ -658,8 +680,16 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 set_small(kGoalSum, 0);
                 hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(pc + 1, 256), 1024)), dim3(256), 0, stream, goal_flags + pend.p0,
                                    pc + 1, small + kGoalSum);
+                if (blocked.capacity)
+                {
+                    set_small(kCutPruned, 0);
+                    hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(u64{jc} + 1, 256), 1024)), dim3(256), 0, stream, blocked.hit,
+                                       u64{jc} + 1, small + kCutPruned);
+                }
                 sync_small();
                 layer_goals += b.host[kGoalSum];
+                if (blocked.capacity)
+                    layer_pruned += b.host[kCutPruned];
                 set.size = o.max_states;
                 r.status = kOutOfStates;
                 stopped = true;
@@ -673,6 +703,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             row[0] += pend.np;
             row[1] += pend.m;
             layer_goals += b.host[kChunkGoal];
+            if (blocked.capacity)
+                layer_pruned += b.host[kChunkPruned];
             return false;
         };
         auto read_state = [&](const u64* block_total = nullptr) {
@@ -682,6 +714,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         };
         while (p0 < lim && !stopped)
         {
+            if (halt.check())
+                break;  // the pending chunk is confirmed below; the layer ends at its last parent
             // count ahead when the counted parents past p0 hold less than a full chunk (and the layer has more)
             const bool count_now = counted < lim && counted_total - base < chunk;
             u64 nb = 0;
@@ -755,7 +789,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
                 hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.flags,
-                                   set.d_status);
+                                   set.d_status, blocked);
                 launch_check("ground insert");
                 tm.end(kKInsert, 0);
                 tm.begin(kKRank);
@@ -775,6 +809,13 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             set_small(kChunkGoal, 0);
             hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(np, 256), 1024)), dim3(256), 0, stream, goal_flags + p0, u64{np},
                                small + kChunkGoal);
+            if (blocked.capacity)
+            {
+                set_small(kChunkPruned, 0);
+                if (m > 0)
+                    hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(m, 256), 1024)), dim3(256), 0, stream, blocked.hit, m,
+                                       small + kChunkPruned);
+            }
             pend = Pending{true, p0, np, m};
             p0 = p1;
             base = end_off;
@@ -787,7 +828,10 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             sync_small();
             confirm(b.host[kSizeNow], static_cast<u32>(b.host[kCut]));
         }
+        if (halt.why)
+            stopped = true;  // the time or the cancellation ended the layer after its confirmed chunks
         r.goal_states += layer_goals;
+        r.pruned += layer_pruned;
         pos = layer_begin + row[0];
         r.expanded += row[0];
         r.generated += row[1];
@@ -819,6 +863,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     r.solved = r.first_goal >= 0 ? 1 : 0;
     if (r.solved)
         r.status = kSolved;
+    else if (halt.why && !(set.size >= o.max_states && bounded))
+        r.status = halt.why;
     else if (!budget_stopped)
         r.status = (r.exhausted || r.layers >= o.max_depth) ? kExhausted : kOutOfStates;
     hip_check(hipStreamSynchronize(stream), "brfs");

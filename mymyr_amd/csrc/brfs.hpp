@@ -27,6 +27,11 @@ struct BrfsOptionsC
     u64 chunk = 0;          // candidates per device batch (0: automatic)
     u64 memory_states = 0;  // arena capacity when max_states is unbounded (0: automatic)
     i32 timings = 0;        // time every kernel class with HIP events on the search's stream
+    std::vector<u64> start;    // [task words] the start state (empty: the task's initial state)
+    std::vector<u64> blocked;  // [k, task words] states never stored (the start state exempt)
+    bool timed = false;        // stop with OutOfTime once max_seconds have passed
+    double max_seconds = 0;
+    const volatile i32* cancel = nullptr;  // stop with Cancelled once another thread sets it nonzero
 };
 
 /// Kernel classes of the device BrFS (timed with HIP events when BrfsOptionsC::timings is set).
@@ -55,6 +60,7 @@ struct BrfsResultC
     double kernel_ms[kKClasses] = {};
     u64 kernel_bytes[kKClasses] = {};  // algorithmic bytes per class (the per-launch formulas in brfs.hip)
     u64 kernel_launches[kKClasses] = {};
+    u64 pruned = 0;        // successors equal to a blocked state
     u64 memory_bytes = 0;  // device bytes of the search's buffers (state set, arena, nodes, chunk and layer arrays)
     // a solved search: the plan to the first goal state tested as (schema, binding) labels ([len], [len, plan_width]
     // objects, -1 padded past a schema's arity), its cost and the goal state's words

@@ -8,8 +8,11 @@
 #include "device_common.hpp"
 #include "runtime.hpp"
 #include "scan.hpp"
+#include "state_set_device.hpp"
 
+#include <algorithm>
 #include <chrono>
+#include <stdexcept>
 #include <vector>
 
 namespace mya
@@ -114,6 +117,87 @@ struct Buffers
 };
 
 using Clock = std::chrono::steady_clock;
+
+/// The blocked states of a search on the device (BlockedView): the rows padded to the set's row width W, duplicates
+/// dropped, the table built here with the state set's hash, slot and tag.
+inline BlockedView upload_blocked(const std::vector<u64>& rows, u32 task_words, u32 W, u64 batch, Buffers& b, hipStream_t stream)
+{
+    const u64 k = task_words ? rows.size() / task_words : 0;
+    if (k == 0)
+        return BlockedView{};
+    if (task_words > W)
+        throw std::invalid_argument("mymyr_amd: brfs: blocked rows wider than the search's rows");
+    std::vector<u64> uniq;
+    std::vector<u64> table(2 * k + 2, 0);
+    const u64 cap = table.size();
+    std::vector<u64> row(W);
+    for (u64 i = 0; i < k; ++i)
+    {
+        std::fill(row.begin(), row.end(), 0);
+        std::copy(rows.begin() + i * task_words, rows.begin() + (i + 1) * task_words, row.begin());
+        const u64 h = hash_state(row.data(), W);
+        const u64 tag = h >> 32;
+        u64 slot = slot_of_hash(h, cap);
+        bool dup = false;
+        for (; table[slot]; slot = slot + 1 == cap ? 0 : slot + 1)
+            if ((table[slot] >> 32) == tag &&
+                std::equal(row.begin(), row.end(), uniq.begin() + (static_cast<u32>(table[slot]) - 1) * W))
+            {
+                dup = true;
+                break;
+            }
+        if (dup)
+            continue;
+        table[slot] = (tag << 32) | (uniq.size() / W + 1);
+        uniq.insert(uniq.end(), row.begin(), row.end());
+    }
+    BlockedView v{};
+    u64* d_table = b.alloc<u64>(cap, "blocked table");
+    u64* d_rows = b.alloc<u64>(uniq.size(), "blocked rows");
+    hip_check(hipMemcpyAsync(d_table, table.data(), cap * sizeof(u64), hipMemcpyHostToDevice, stream), "blocked table");
+    hip_check(hipMemcpyAsync(d_rows, uniq.data(), uniq.size() * sizeof(u64), hipMemcpyHostToDevice, stream), "blocked rows");
+    hip_check(hipStreamSynchronize(stream), "blocked states");
+    v.table = d_table;
+    v.capacity = cap;
+    v.rows = d_rows;
+    v.words = W;
+    v.hit = b.alloc<u8>(batch, "blocked flags");
+    return v;
+}
+
+/// The start state as a row of W words (BrfsOptionsC::start, else the task's initial state).
+inline std::vector<u64> start_row(const CompiledTask& task, const BrfsOptionsC& o, u32 W)
+{
+    const std::vector<u64>& s = o.start.empty() ? task.initial : o.start;
+    std::vector<u64> row(W, 0);
+    std::copy(s.begin(), s.begin() + std::min<size_t>(s.size(), W), row.begin());
+    return row;
+}
+
+/// max_seconds and the cancellation flag (the reference's Control::check, src/mymyr/search/brfs.cpp:168-181): checked
+/// by the drivers before every batch; `why` keeps the first reason (OutOfTime or Cancelled).
+struct Halt
+{
+    bool timed;
+    Clock::time_point deadline;
+    const volatile i32* cancel;
+    i32 why = 0;
+    Halt(const BrfsOptionsC& o, Clock::time_point t0) : timed(o.timed), cancel(o.cancel)
+    {
+        const double s = std::min(std::max(0.0, o.max_seconds), 1e9);
+        deadline = t0 + std::chrono::duration_cast<Clock::duration>(std::chrono::duration<double>(s));
+    }
+    bool check()
+    {
+        if (why)
+            return true;
+        if (timed && Clock::now() >= deadline)
+            why = kOutOfTime;
+        else if (cancel && *cancel)
+            why = kCancelled;
+        return why != 0;
+    }
+};
 
 /// HIP-event timing of kernel classes on one stream; durations are read once the stream has drained.
 class Timers

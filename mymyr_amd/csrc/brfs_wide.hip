@@ -182,6 +182,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
         kFingerprint = 7,
         kSpare = 8,  // the capacity status of a cut chunk's compaction (expected there, not an error)
         kXStatus = 9,
+        kPruned = 10,  // blocked candidates of a chunk (up to the cut of a cut chunk)
     };
     auto set_small = [&](int idx, u64 v) { hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, small + idx, v); };
     auto sync_small = [&] {
@@ -201,10 +202,10 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
             throw std::length_error("mymyr_amd: brfs: state table full");
     };
     launch_fill_u32(xstatus, 2, 0, stream);
-    // the start state
+    const BlockedView blocked = upload_blocked(o.blocked, task.words, W, chunk, b, stream);
+    // the start state (stored even if blocked)
     {
-        std::vector<u64> s0(W, 0);
-        std::copy(task.initial.begin(), task.initial.end(), s0.begin());
+        const std::vector<u64> s0 = start_row(task, o, W);
         u64* d_s0 = b.alloc<u64>(W, "start state");
         hip_check(hipMemcpyAsync(d_s0, s0.data(), W * sizeof(u64), hipMemcpyHostToDevice, stream), "start state");
         u64 nn = 0;
@@ -222,6 +223,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     base_args.status = xstatus + 1;
     base_args.words_needed = xstatus;
     const auto td0 = Clock::now();
+    Halt halt(o, t0);
     bool stopped = false, budget_stopped = false;
     r.status = kExhausted;
     u64 pos = 0;
@@ -238,6 +240,11 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
         {
             r.status = kOutOfStates;
             budget_stopped = true;
+            break;
+        }
+        if (halt.check())
+        {
+            stopped = true;
             break;
         }
         if (r.layers == o.max_depth)
@@ -274,10 +281,12 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
             lim = first_goal;
             goal_stop = true;
         }
-        u64 layer_goals = 0;
+        u64 layer_goals = 0, layer_pruned = 0;
         u64 p0 = 0, base = 0;
         while (p0 < lim && !stopped)
         {
+            if (halt.check())
+                break;
             hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, 1u, p0, lim, base + chunk, small + kChunkP);
             launch_check("chunk end");
             sync_small();
@@ -305,7 +314,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
                 tm.end(kKEmit, (p1 - p0) * R + m * (R + 9));
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
-                state_set_probe(set, cand_rows, m, stream);
+                state_set_probe(set, cand_rows, m, stream, blocked.capacity ? &blocked : nullptr);
                 tm.end(kKInsert, m * (R + 8));
                 tm.begin(kKRank);
                 state_set_rank(set, m, stream);
@@ -326,6 +335,13 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
             set_small(kGoalSum, 0);
             hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(p1 - p0, 256), 1024)), dim3(256), 0, stream, goal_id + lb + p0,
                                p1 - p0, small + kGoalSum);
+            if (blocked.capacity)
+            {
+                set_small(kPruned, 0);
+                if (m > 0)
+                    hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(m, 256), 1024)), dim3(256), 0, stream, blocked.hit, m,
+                                       small + kPruned);
+            }
             read_state(nullptr);
             sync_small();
             check_expansion();
@@ -345,8 +361,16 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
                 set_small(kGoalSum, 0);
                 hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(static_cast<u64>(pc) + 1, 256), 1024)), dim3(256), 0, stream,
                                    goal_id + lb + p0, static_cast<u64>(pc) + 1, small + kGoalSum);
+                if (blocked.capacity)
+                {
+                    set_small(kPruned, 0);
+                    hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(u64{jc} + 1, 256), 1024)), dim3(256), 0, stream, blocked.hit,
+                                       u64{jc} + 1, small + kPruned);
+                }
                 sync_small();
                 layer_goals += b.host[kGoalSum];
+                if (blocked.capacity)
+                    layer_pruned += b.host[kPruned];
                 set.size = o.max_states;
                 r.status = kOutOfStates;
                 stopped = true;
@@ -359,10 +383,15 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
             row[0] += p1 - p0;
             row[1] += m;
             layer_goals += b.host[kGoalSum];
+            if (blocked.capacity)
+                layer_pruned += b.host[kPruned];
             p0 = p1;
             base = end_off;
         }
+        if (halt.why)
+            stopped = true;  // the time or the cancellation ended the layer after its last full chunk
         r.goal_states += layer_goals;
+        r.pruned += layer_pruned;
         pos = lb + row[0];
         r.expanded += row[0];
         r.generated += row[1];
@@ -391,6 +420,8 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     r.solved = r.first_goal >= 0 ? 1 : 0;
     if (r.solved)
         r.status = kSolved;
+    else if (halt.why && !(bounded && set.size >= o.max_states))
+        r.status = halt.why;
     else if (!budget_stopped)
         r.status = (r.exhausted || r.layers >= o.max_depth) ? kExhausted : kOutOfStates;
     hip_check(hipStreamSynchronize(stream), "brfs");

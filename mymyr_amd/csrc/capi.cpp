@@ -278,6 +278,19 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         o.chunk = options->chunk;
         o.memory_states = options->memory_states;
         o.timings = options->timings;
+        const u32 TW = task->compiled->words;
+        if ((options->start || options->blocked_count) && options->words != TW)
+            throw std::invalid_argument("mymyr_amd: brfs: start and blocked rows have " + std::to_string(options->words) +
+                                        " words, the task's rows " + std::to_string(TW));
+        if (options->blocked_count && !options->blocked)
+            throw std::invalid_argument("mymyr_amd: brfs: blocked_count without blocked rows");
+        if (options->start)
+            o.start.assign(options->start, options->start + TW);
+        if (options->blocked_count)
+            o.blocked.assign(options->blocked, options->blocked + options->blocked_count * TW);
+        o.timed = options->timed != 0;
+        o.max_seconds = options->max_seconds;
+        o.cancel = options->cancel;
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
         if (o.stop_at_goal && task->compiled->goal_unsat)
@@ -301,7 +314,7 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         result->first_goal = r.first_goal;
         result->search_s = r.search_s;
         result->device_s = r.device_s;
-        result->pruned = 0;
+        result->pruned = r.pruned;
         result->memory_bytes = r.memory_bytes;
         if (plan)
         {

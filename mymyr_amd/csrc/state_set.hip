@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kBlock) void k_hash_rows(const u64* __restrict__ ro
 
 template<int G, int K>
 __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __restrict__ rows, u64 n, u64* __restrict__ cand_slot,
-                                                  u8* __restrict__ flags, u32* __restrict__ status)
+                                                  u8* __restrict__ flags, u32* __restrict__ status, BlockedView blocked)
 {
     u64 j;
     u32 q, gbase;
@@ -63,6 +63,19 @@ __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __
     Slice<G, K> me;
     src.load(j, q, me);
     const u64 h = group_hash<G, K>(me, q, gbase);
+    if (blocked.capacity)
+    {
+        // a blocked candidate is dropped before the table is probed (it takes no entry and no id)
+        const bool hit = group_blocked<G, K>(blocked, me, h, q, gbase);
+        if (q == 0)
+        {
+            blocked.hit[j] = hit ? 1 : 0;
+            if (hit)
+                flags[j] = 0;
+        }
+        if (hit)
+            return;
+    }
     const ProbeResult r = probe_insert<G, K>(s, src, j, me, h, q, gbase, flags, status);
     if (q == 0)
     {
@@ -316,13 +329,14 @@ void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
     launch_check("state set rank");
 }
 
-void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream)
+void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked)
 {
     if (m == 0)
         return;
+    const BlockedView bl = blocked ? *blocked : BlockedView{};
     with_shape(s.v.words, [&]<int G, int K>() {
         hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, rows, m, nullptr, s.flags,
-                           s.d_status);
+                           s.d_status, bl);
     });
     launch_check("state set probe");
     s.last = stream;
@@ -357,7 +371,7 @@ void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new,
             state_set_begin_batch(s, stream);
             // the probe results are kept only for the ids
             hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, m, ids ? s.cand_slot : nullptr,
-                               s.flags, s.d_status);
+                               s.flags, s.d_status, BlockedView{});
             launch_check("state set probe");
             state_set_rank(s, m, stream, is_new ? is_new + done : nullptr);
             hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, s.list,

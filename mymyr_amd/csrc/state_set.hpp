@@ -75,8 +75,9 @@ void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new = nullptr
 
 /// The probe of a batch begun with state_set_begin_batch over candidate rows [m, words] (device) that the caller produced:
 /// a stored equal row drops a candidate, equal candidates keep the smallest index, the others take pending entries
-/// (the losers' flags are cleared). state_set_rank and the caller's compaction follow.
-void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream);
+/// (the losers' flags are cleared). state_set_rank and the caller's compaction follow. With `blocked`, a candidate equal
+/// to a blocked state is dropped first (flag cleared, blocked->hit[j] = 1; every other candidate's hit byte is 0).
+void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked = nullptr);
 
 /// hash_state of every row (a group of lanes per row).
 void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t stream);

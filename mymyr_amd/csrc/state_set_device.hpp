@@ -259,6 +259,43 @@ __device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const
     return {kProbeFailed, true};
 }
 
+/// States a search never stores (the reference's BlockedSet, src/mymyr/search/iw_detail.hpp:95-105, compared by
+/// content): rows [count, words] and a linear-probing table of (hash tag << 32) | (row index + 1) entries over
+/// `capacity` slots (at most half of them taken, so every probe ends at an empty slot), slot and tag as the state
+/// set's. hit [batch] receives per candidate whether it was blocked. capacity 0: nothing is blocked.
+struct BlockedView
+{
+    const u64* table;
+    u64 capacity;
+    const u64* rows;
+    u32 words;
+    u8* hit;
+};
+
+/// Whether the group's row `me` (hash h) is a blocked state (group-uniform).
+template<int G, int K>
+__device__ __forceinline__ bool group_blocked(const BlockedView& b, const Slice<G, K>& me, u64 h, u32 q, u32 gbase)
+{
+    const u64 tag = h >> 32;
+    u64 slot = slot_of_hash(h, b.capacity);
+    for (u64 probes = 0; probes < b.capacity; ++probes)
+    {
+        u64 e = q == 0 ? b.table[slot] : 0;
+        e = group_bcast<G>(e, gbase, 0);
+        if (e == 0)
+            return false;
+        if ((e >> 32) == tag)
+        {
+            Slice<G, K> o;
+            load_row<G, K>(b.rows + (static_cast<u64>(static_cast<u32>(e)) - 1) * b.words, b.words, q, o);
+            if (group_equal<G, K>(me, o, gbase))
+                return true;
+        }
+        slot = slot + 1 == b.capacity ? 0 : slot + 1;
+    }
+    return false;
+}
+
 /// Winner w of the batch (candidate j = list[w], id = id0 + w): below `limit` its row into the arena; at or past it,
 /// kStatusCapacity (and is_new[j] = 0). The winner's table entry keeps its candidate code: the batch's epoch maps it to
 /// the id (id_of), so no entry is rewritten.

@@ -56,14 +56,66 @@ class BrfsResult:
 KERNEL_CLASSES = ["count", "emit", "insert", "unused", "rank", "compact", "other"]
 
 
+class CancelToken:
+    """The reference's mymyr.search.CancelToken (python/src/search_bindings.cpp:2277-2287, search::CancelToken,
+    include/mymyr/search/control.hpp:81-90): request() from any thread stops a search that holds the token (status
+    "cancelled"). The flag is a 32-bit word the device search reads between batches."""
+
+    def __init__(self):
+        self._flag = ctypes.c_int32(0)
+
+    def request(self) -> None:
+        self._flag.value = 1
+
+    @property
+    def requested(self) -> bool:
+        return bool(self._flag.value)
+
+    @property
+    def address(self) -> int:
+        return ctypes.addressof(self._flag)
+
+    def __repr__(self) -> str:
+        return f"CancelToken(requested={self.requested})"
+
+
+def _rows(task: Task, rows, what: str) -> np.ndarray:
+    """States as [k, task.words] uint64 rows (the task's state words)."""
+    a = np.ascontiguousarray(np.asarray(rows, dtype=np.uint64))
+    if a.ndim == 1:
+        a = a.reshape(1, -1)
+    if a.ndim != 2 or a.shape[1] != task.words:
+        raise ValueError(f"mymyr_amd: brfs: {what} must have {task.words} words per state, got shape {a.shape}")
+    return a
+
+
 def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None, max_expanded: int | None = None,
          witness_pruning: bool = True, stop_at_goal: bool = True, fingerprint: bool = False, layer_stats: bool = True,
-         chunk: int = 0, memory_states: int = 0, timings: bool = False) -> BrfsResult:
+         chunk: int = 0, memory_states: int = 0, timings: bool = False, start=None, blocked_states=None,
+         max_seconds: float | None = None, cancel: CancelToken | None = None) -> BrfsResult:
     """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
-    (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer."""
+    (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer.
+
+    start: the start state's words (default: the task's initial state). blocked_states: states never stored ([k, words]
+    or a list of rows); a successor equal to one counts as generated and pruned (the start state is exempt).
+    max_seconds (None: unlimited) and cancel (a CancelToken) stop the search between device batches with status
+    "out_of_time" or "cancelled" (python/src/search_bindings.cpp:516-538, 2135-2145)."""
+    if max_seconds is not None and not max_seconds >= 0:
+        raise ValueError("mymyr_amd: brfs: max_seconds must be >= 0")
+    if cancel is not None and not isinstance(cancel, CancelToken):
+        raise TypeError("mymyr_amd: cancel must be a mymyr_amd.search.CancelToken")
+    st = None if start is None else _rows(task, start, "start")
+    if st is not None and st.shape[0] != 1:
+        raise ValueError("mymyr_amd: brfs: start must be one state")
+    bl = None if blocked_states is None else _rows(task, np.zeros((0, task.words), np.uint64) if len(blocked_states) == 0
+                                                   else blocked_states, "blocked_states")
+    timed = max_seconds is not None and np.isfinite(max_seconds)
     o = _lib.BrfsOptions(UNBOUNDED32 if max_depth is None else max_depth, int(witness_pruning),
                          UNBOUNDED64 if max_states is None else max_states, UNBOUNDED64 if max_expanded is None else max_expanded,
-                         int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0)
+                         int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0,
+                         None if st is None else st.ctypes.data, None if bl is None or bl.shape[0] == 0 else bl.ctypes.data,
+                         0 if bl is None else bl.shape[0], task.words, int(timed), float(max_seconds) if timed else 0.0,
+                         None if cancel is None else cancel.address)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)

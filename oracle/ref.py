@@ -43,6 +43,12 @@ class BrfsOptions(Structure):
         ("stop_at_goal", c_int32),
         ("fingerprint", c_int32),
         ("max_expanded", c_uint64),
+        ("start", c_void_p),
+        ("blocked", c_void_p),
+        ("blocked_count", c_uint64),
+        ("words", c_uint32),
+        ("reserved", c_uint32),
+        ("max_seconds", c_double),
     ]
 
 
@@ -415,11 +421,15 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 
 
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
-         stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1):
+         stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf")):
     """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
-    (schema, binding) pairs, the goal state's words and the cost."""
+    (schema, binding) pairs, the goal state's words and the cost. start [words] and blocked_states [k, words] are
+    rows of the task's table words."""
+    W = task.table_words
+    st = None if start is None else np.ascontiguousarray(np.asarray(start, np.uint64).reshape(-1)[:W])
+    bl = None if blocked_states is None else np.ascontiguousarray(np.asarray(blocked_states, np.uint64).reshape(-1, W))
     o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
-                    max_expanded)
+                    max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds)
     r = BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -436,6 +446,7 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         "fingerprint": r.fingerprint, "layers": r.layers, "status": r.status, "solved": bool(r.solved),
         "exhausted": bool(r.exhausted), "seconds": r.seconds, "layer_counts": lc[:n].tolist(), "pruned": r.pruned,
     }
+    del st, bl
     if r.solved:
         k = min(r.plan_len, cap)
         out["plan"] = [[int(ps[i])] + [int(x) for x in pb[i] if x >= 0] for i in range(k)]

@@ -105,6 +105,12 @@ struct mref_brfs_options
     int32_t stop_at_goal;
     int32_t fingerprint;
     uint64_t max_expanded;
+    const uint64_t* start;    // [words] (null: the task's initial state)
+    const uint64_t* blocked;  // [blocked_count, words]
+    uint64_t blocked_count;
+    uint32_t words;
+    uint32_t reserved;
+    double max_seconds;       // BrfsOptions::max_seconds (infinity: unbounded)
 };
 
 struct mref_brfs_result
@@ -709,6 +715,11 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
             b.max_states = o->max_states;
             b.max_expanded = o->max_expanded;
             b.witness_pruning = o->witness_pruning != 0;
+            if (o->start)
+                b.start = State(std::span<const u64>(o->start, o->words));
+            for (uint64_t k = 0; k < o->blocked_count; ++k)
+                b.blocked_states.push_back(State(std::span<const u64>(o->blocked + k * o->words, o->words)));
+            b.max_seconds = o->max_seconds;
             b.canonical_order = o->canonical_order != 0;
             b.stop_at_goal = o->stop_at_goal != 0;
             b.fingerprint = o->fingerprint != 0;

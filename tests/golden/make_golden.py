@@ -351,6 +351,68 @@ def make_brfs_wide():
     dump("brfs_wide.json", out)
 
 
+def walk_states(t, depths, seed):
+    """One state per entry of `depths`: the end of a seeded random walk of that many steps from the initial state (a walk
+    that reaches a dead end stops there)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for d in depths:
+        row = t.initial_state()
+        for _ in range(d):
+            _, _, rows = t.successors(row)
+            if len(rows) == 0:
+                break
+            row = rows[rng.integers(len(rows))]
+        out.append(row.copy())
+    return out
+
+
+OPTION_CASES = {
+    # key: (task, atoms, start walk depth or None, blocked walk depths, include the start among the blocked, options)
+    "gripper__prob05:blocked_goal": ("gripper__prob05", "auto", None, [1, 1, 3, 3, 3, 4], False, dict(stop_at_goal=True)),
+    "gripper__prob05:blocked_all": ("gripper__prob05", "auto", None, [2, 3, 4, 5, 6, 6, 8, 10], True, dict(stop_at_goal=False)),
+    "gripper__prob05:start_goal": ("gripper__prob05", "auto", 4, [], False, dict(stop_at_goal=True)),
+    "gripper__prob05:blocked_cut": ("gripper__prob05", "auto", None, [3, 4, 5, 5, 6, 7, 8, 9], False,
+                                    dict(stop_at_goal=False, max_states=20000)),
+    "gripper__prob05:start_blocked_expanded": ("gripper__prob05", "auto", 2, [3, 4, 4, 5, 6, 7], False,
+                                               dict(stop_at_goal=False, max_expanded=3000)),
+    "gripper__prob05:timed0": ("gripper__prob05", "auto", None, [], False, dict(stop_at_goal=False, max_seconds=0.0)),
+    "blocks__probBLOCKS-8-0:blocked_goal": ("blocks__probBLOCKS-8-0", "auto", None, [1, 2, 2, 3, 4, 5, 5, 6, 8, 10], False,
+                                           dict(stop_at_goal=True)),
+    "logistics00__probLOGISTICS-6-1:start_blocked": ("logistics00__probLOGISTICS-6-1", "auto", 3, [1, 2, 3, 4, 5, 6], True,
+                                                     dict(stop_at_goal=True)),
+    "strips:blocked_cut": ("strips", "dense", None, [2, 3, 4, 5, 6, 6, 7, 7, 8, 8, 9, 10, 11, 11, 12, 12], False,
+                           dict(stop_at_goal=False, max_depth=12, max_states=1 << 20)),
+    "transport_w20_3:blocked_goal": ("transport_w20_3", "auto", None, [1, 1, 2, 2, 2, 3], False, dict(stop_at_goal=True)),
+    "transport_w20_3:start_goal": ("transport_w20_3", "auto", 2, [], False, dict(stop_at_goal=True)),
+    "transport_w20_3:blocked_cut": ("transport_w20_3", "auto", 1, [2, 3, 3, 4, 5, 6], True,
+                                    dict(stop_at_goal=False, max_states=200000)),
+}
+
+
+def make_brfs_options():
+    """BrfsOptions::start and blocked_states (and max_seconds 0) of the reference brfs(): the start state and the
+    blocked states are ends of seeded random walks from the initial state; the results (counts, pruned, statuses,
+    fingerprints, plans) of the reference's single-threaded search."""
+    out = {}
+    for i, (key, (name, atoms, start_d, blocked_d, block_start, kw)) in enumerate(OPTION_CASES.items()):
+        t = ref.RefTask(fx.task_path(name), atoms)
+        start = None if start_d is None else walk_states(t, [start_d], 100 + i)[0]
+        blocked = walk_states(t, blocked_d, 200 + i)
+        if block_start:
+            blocked.append(t.initial_state() if start is None else start)
+        bl = np.array(blocked, dtype=np.uint64).reshape(-1, t.table_words)
+        r = ref.brfs(t, start=start, blocked_states=bl if len(bl) else None, **kw)
+        r.pop("seconds")
+        r["options"] = kw
+        r["start"] = None if start is None else hex_row(start)
+        r["blocked"] = [hex_row(b) for b in bl]
+        r["atoms"] = atoms
+        out[key] = r
+        print(key, r["states"], r["pruned"], r["status"], len(r.get("plan", [])), flush=True)
+    dump("brfs_options.json", out)
+
+
 def make_pool():
     """Digests of every batch the reference CpuEnvPool returns over each pool case's scripted calls."""
     out = {}
@@ -406,7 +468,7 @@ def main():
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool,
-             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "brfs_options": make_brfs_options, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -9,7 +9,7 @@ pytestmark = pytest.mark.gpu
 pytest.importorskip("torch")
 
 KEYS = ["states", "expanded", "generated", "goal_states", "layers", "fingerprint", "status", "layer_counts", "exhausted", "solved"]
-STATUS = {0: "solved", 1: "exhausted", 2: "out_of_states"}
+STATUS = {0: "solved", 1: "exhausted", 2: "out_of_states", 3: "out_of_time", 4: "cancelled"}
 
 
 def device(golden, name, atoms="auto", full=False, **kw):
@@ -154,3 +154,91 @@ def test_wide_rows_refuse_witness_pruning_over_witness_parameters(golden):
 
     with pytest.raises(MyaError, match="witness"):
         device(golden, "witness_wide", "dense", stop_at_goal=False, max_states=1000)
+
+
+def _rows(words, hexrows):
+    import numpy as np
+
+    out = np.zeros((len(hexrows), words), np.uint64)
+    for i, r in enumerate(hexrows):
+        w = trimmed_hex(r)
+        assert len(w) <= words
+        out[i, : len(w)] = w
+    return out
+
+
+OPTION_KEYS = [
+    "gripper__prob05:blocked_goal", "gripper__prob05:blocked_all", "gripper__prob05:start_goal", "gripper__prob05:blocked_cut",
+    "gripper__prob05:start_blocked_expanded", "gripper__prob05:timed0", "blocks__probBLOCKS-8-0:blocked_goal",
+    "logistics00__probLOGISTICS-6-1:start_blocked", "strips:blocked_cut", "transport_w20_3:blocked_goal",
+    "transport_w20_3:start_goal", "transport_w20_3:blocked_cut"]
+
+
+@pytest.mark.parametrize("key", OPTION_KEYS)
+def test_start_and_blocked_states(golden, key):
+    """BrfsOptions::start and blocked_states (and max_seconds 0): a successor equal to a blocked state counts as
+    generated and pruned and is never stored (the start state is exempt, a successor equal to it and blocked is
+    pruned), the search and its plan start at `start`; counts, pruned, statuses, fingerprints and plans equal to the
+    reference's, on the ground-action driver and on the wide-row driver, at goal stops and at max_states and
+    max_expanded cuts."""
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    exp = golden.load("brfs_options.json")[key]
+    name = key.split(":")[0]
+    t = Task.from_text_file(golden.task_path(name), exp["atoms"])
+    kw = dict(exp["options"])
+    if exp["start"] is not None:
+        kw["start"] = _rows(t.words, [exp["start"]])[0]
+    if exp["blocked"]:
+        kw["blocked_states"] = _rows(t.words, exp["blocked"])
+    print(f"brfs options: {key}", flush=True)
+    for chunk in ((0, 4096) if name == "strips" else (0,)):
+        r = search.brfs(t, fingerprint=True, chunk=chunk, **kw)
+        got = {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
+               "layers": r.layers, "fingerprint": r.fingerprint, "status": r.status, "layer_counts": r.layer_counts,
+               "exhausted": r.exhausted, "solved": r.solved, "result": r}
+        assert not same(got, exp), (key, chunk, same(got, exp))
+        assert r.pruned == exp["pruned"], (key, chunk, r.pruned, exp["pruned"])
+        assert same_plan(got, exp), (key, r.plan[:6], exp.get("plan", [])[:6])
+
+
+def _consistent(r):
+    lc = r.layer_counts
+    return (sum(x[0] for x in lc) == r.expanded and sum(x[1] for x in lc) == r.generated and
+            sum(x[2] for x in lc) + 1 == r.states and len(lc) == r.layers)
+
+
+def test_cancel_and_time_stop_between_batches(golden):
+    """A CancelToken requested before the search stops it before the first expansion; one requested from another thread
+    and a max_seconds budget stop a long search between device batches: status "cancelled" / "out_of_time", the
+    layers before the last equal to the uncut search's, and counts that add up."""
+    import threading
+    import time
+
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("strips"), "dense")
+    full = golden.load("brfs.json")["strips"][str(1 << 24)]
+    tok = search.CancelToken()
+    tok.request()
+    r = search.brfs(t, max_depth=12, max_states=1 << 24, stop_at_goal=False, cancel=tok)
+    assert (r.status, r.states, r.expanded, r.layers) == ("cancelled", 1, 0, 0)
+
+    r = search.brfs(t, max_depth=12, max_states=1 << 24, stop_at_goal=False, max_seconds=0.02, chunk=1 << 16)
+    assert r.status == "out_of_time" and r.states < full["states"] and _consistent(r), (r.status, r.states)
+    assert r.layer_counts[:-1] == full["layer_counts"][: max(0, r.layers - 1)]
+
+    tok = search.CancelToken()
+    timer = threading.Timer(0.02, tok.request)
+    t0 = time.perf_counter()
+    timer.start()
+    r = search.brfs(t, max_depth=12, max_states=1 << 24, stop_at_goal=False, cancel=tok, chunk=1 << 16)
+    timer.join()
+    if r.status != "cancelled":
+        # the whole search finished inside the timer's delay: nothing to stop
+        assert r.status == "out_of_states" and time.perf_counter() - t0 < 0.5
+    else:
+        assert r.states < full["states"] and _consistent(r)
+        assert r.layer_counts[:-1] == full["layer_counts"][: max(0, r.layers - 1)]

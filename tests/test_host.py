@@ -118,3 +118,28 @@ def test_pool_sampler_resolution():
         resolve_sampler("weighted", 2)
     with pytest.raises(ValueError):
         resolve_sampler(InstanceSampler(2), 3)
+
+
+def test_brfs_option_arguments_checked_on_the_host(golden):
+    """search.brfs checks start / blocked_states widths, max_seconds and the cancel type before any device call, and a
+    CancelToken behaves as the reference's (request() once, requested stays True)."""
+    import numpy as np
+
+    from mymyr_amd import search
+
+    tok = search.CancelToken()
+    assert not tok.requested and repr(tok) == "CancelToken(requested=False)"
+    tok.request()
+    tok.request()
+    assert tok.requested and repr(tok) == "CancelToken(requested=True)"
+    t = Task.from_text_file(golden.task_path("gripper__prob05"))
+    with pytest.raises(ValueError, match="words per state"):
+        search.brfs(t, start=np.zeros(t.words + 1, np.uint64))
+    with pytest.raises(ValueError, match="one state"):
+        search.brfs(t, start=np.zeros((2, t.words), np.uint64))
+    with pytest.raises(ValueError, match="words per state"):
+        search.brfs(t, blocked_states=np.zeros((3, t.words + 2), np.uint64))
+    with pytest.raises(ValueError, match="max_seconds"):
+        search.brfs(t, max_seconds=-1.0)
+    with pytest.raises(TypeError, match="CancelToken"):
+        search.brfs(t, cancel=True)
