@@ -149,8 +149,8 @@ struct Lds
     lds<u32>* bind;    // [A][64]: lane columns of the per-lane nested loop (count_from)
     lds<u64>* cur_m;   // [A][64]: its enumeration cursors (candidate bits left)
     lds<u32>* cur_w;   // [A][64]: its enumeration cursors (word index)
-    lds<u32>* eff;     // [kMaxEff]: effect slots (lane 0)
-    lds<u32>* before;  // [kMaxEff]: effect atoms' bits before the move (lane 0)
+    lds<u32>* eff;     // [kMaxEff]: effect slots of a successor (lane k: effect k)
+    lds<u32>* before;  // [kMaxEff]: their bits before the move
     lds<u32>* counts;  // [num_schemas]
 };
 
@@ -1108,47 +1108,46 @@ __device__ __forceinline__ bool goal_test(const TaskDev& T, const auto& H, P row
     return !T.goal_unsat && __ballot(!ok) == 0;
 }
 
-/// Applies the effects of the picked binding of schema s to the LDS row and the view: delete, then add.
+/// Applies the effects of the picked binding of schema s to the LDS row and the view: delete, then add. One effect per
+/// lane: its slot (the table reads of the effects overlap instead of following each other), then the deletes, the adds,
+/// and the view bits of the atoms whose bit changed. View pairs exist for predicates of arity 1 and 2 only, so a view bit
+/// stands for one atom: lanes that list the same slot write the same value.
 __device__ __forceinline__ void apply_effects(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane, u32* status)
 {
     const auto& S = H.schemas[s];
-    if (lane == 0)
+    const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
+    if (lane == 0 && S.eff_end - S.eff_begin > kMaxEff)
+        atomicOr(status, kStatusCapacity);
+    const bool mine = lane < ne;
+    const bool add = lane < S.nadd;
+    u32 sl = kNone;
+    bool before = false;
+    if (mine)
     {
-        lds<u32>* slot = L.eff;
-        lds<u32>* before = L.before;
-        const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
-        if (S.eff_end - S.eff_begin > kMaxEff)
-            atomicOr(status, kStatusCapacity);
-        for (u32 k = 0; k < ne; ++k)
+        sl = effect_slot(T, L, H.effects[S.eff_begin + lane]);
+        before = sl != kNone && row_bit(L.row, sl);
+        if (add && sl == kNone)
+            atomicOr(status, kStatusNoSlot);
+    }
+    wave_sync();
+    if (mine && !add && sl != kNone)
+        __hip_atomic_fetch_and(L.row + (sl >> 6), ~(u64{1} << (sl & 63)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    wave_sync();
+    if (mine && add && sl != kNone)
+        __hip_atomic_fetch_or(L.row + (sl >> 6), u64{1} << (sl & 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    wave_sync();
+    if (mine && sl != kNone && sl < T.fluent_slots)
+    {
+        const bool now = row_bit(L.row, sl);
+        if (now != before)
         {
-            slot[k] = effect_slot(T, L, H.effects[S.eff_begin + k]);
-            before[k] = slot[k] != kNone && row_bit(L.row, slot[k]);
-            if (k < S.nadd && slot[k] == kNone)
-                atomicOr(status, kStatusNoSlot);
-        }
-        for (u32 k = S.nadd; k < ne; ++k)
-            if (slot[k] != kNone)
-                L.row[slot[k] >> 6] &= ~(u64{1} << (slot[k] & 63));
-        for (u32 k = 0; k < S.nadd && k < ne; ++k)
-            if (slot[k] != kNone)
-                L.row[slot[k] >> 6] |= u64{1} << (slot[k] & 63);
-        // the view follows the atoms whose bit changed
-        for (u32 k = 0; k < ne; ++k)
-        {
-            const u32 sl = slot[k];
-            if (sl == kNone || sl >= T.fluent_slots)
-                continue;
-            const bool now = row_bit(L.row, sl);
-            if (now == (before[k] != 0))
-                continue;
-            before[k] = now ? 1u : 0u;  // a slot listed twice changes once
             u32 pred, a0, a1;
             decode_slot(T, H, sl, &pred, &a0, &a1);
             for_view_bits(H, L, pred, a0, a1, [now](lds<u64>* word, u64 bit) {
                 if (now)
-                    *word |= bit;
+                    __hip_atomic_fetch_or(word, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
                 else
-                    *word &= ~bit;
+                    __hip_atomic_fetch_and(word, ~bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             });
         }
     }
@@ -1310,20 +1309,23 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
 {
     const u32 Lw = A.label_width;
     u64* grow = A.states + i * A.words;
-    load_row_lds(T, L, grow, lane);
-    build_view(T, H, L, lane);
+    // the row's scalars are read before its words, so that their latencies overlap with the row's
     const bool already_goal = A.at_goal[i] != 0;
+    const i64 act_in = A.actions ? A.actions[i] : 0;
+    const u64 draws0 = A.draws ? A.draws[i] : 0;
+    const i32 steps0 = A.steps ? A.steps[i] : 0;
+    const i32 next_in = (!kOne && A.next_task_ids) ? A.next_task_ids[i] : 0;
     // the count cache row: its counts stand for the row's state (and instance) when its fingerprint matches (reset,
     // refresh and step write it; a state written directly since is counted again)
     const u32 cw = A.cache_width;
     u32* crow = A.counts ? A.counts + i * cw : nullptr;
+    const u64 fp_cached = crow ? (static_cast<u64>(crow[cw - 2]) | (static_cast<u64>(crow[cw - 1]) << 32)) : 0;
+    load_row_lds(T, L, grow, lane);
+    build_view(T, H, L, lane);
     const u64 salt = instance_salt(k);
     bool cached = false;
     if (crow)
-    {
-        const u64 fp = state_fingerprint(L.row, T.W, lane) + salt;
-        cached = (static_cast<u64>(crow[cw - 2]) | (static_cast<u64>(crow[cw - 1]) << 32)) == fp;
-    }
+        cached = fp_cached == state_fingerprint(L.row, T.W, lane) + salt;
     enum
     {
         kOk = 0,
@@ -1350,7 +1352,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             st = kStuck;
         else if (!already_goal && A.actions)
         {
-            const i64 act = A.actions[i];
+            const i64 act = act_in;
             if (act < 0 || static_cast<u64>(act) >= c)
                 st = kInvalid;
             else
@@ -1360,7 +1362,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         {
             // the key: the row's own, or the env's (read here in the batch-order path, which keeps fewer values live)
             const u64 key = A.seeds ? A.seeds[i] : (kOne ? *A.seed : seed);
-            a = successor_index(key, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, A.draws[i], c);
+            a = successor_index(key, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, draws0, c);
         }
         u32 rank = 0;
         if (st == kOk)
@@ -1376,7 +1378,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (lane == 0)
         {
             if (A.draws)
-                A.draws[i] += 1;
+                A.draws[i] = draws0 + 1;
             if (A.schema)
                 A.schema[i] = st == kOk ? static_cast<i32>(schema) : -1;
             if (A.invalid)
@@ -1399,7 +1401,6 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     const bool dead = !A.cfg.dead_end_none && !g && ((st == kOk && c2 == 0) || st == kStuck);
     const bool term = g || (dead && A.cfg.dead_end_terminal);
     const bool absorbed = already_goal || (st == kStuck && dead && A.cfg.dead_end_terminal);
-    const i32 steps0 = A.steps ? A.steps[i] : 0;
     const i32 t2 = A.steps ? steps0 + (absorbed ? 0 : 1) : 0;
     const bool trunc = !term && A.cfg.max_steps && t2 >= static_cast<i32>(A.cfg.max_steps);
     if (lane == 0)
@@ -1452,7 +1453,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     u32 next = k;
     if (!kOne && A.next_task_ids)
     {
-        const i32 v = A.next_task_ids[i];
+        const i32 v = next_in;
         if (v < 0 || static_cast<u32>(v) >= A.instances)
         {
             if (lane == 0)
@@ -1530,11 +1531,17 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     wave_sync();
 }
 
+/// Waves per SIMD the env step is compiled for: the split count (transport-like tasks) holds 5 at the price of a few
+/// spilled registers, faster than the 4 its register use gives unconstrained; the level-synchronous count keeps the 3
+/// its registers allow (spills cost it more than a wave gains).
+template<bool kLevels>
+constexpr int kEnvStepWaves = kLevels ? 3 : 5;
+
 /// The step of a batch of one instance: every row in batch order with the kernel-argument tables, as instance 0 (the
 /// host checks given task ids and next_task_ids with launch_check_ids first); with kGroup, the rows of one instance's
 /// group of a batch grouped by instance.
 template<bool kStaged, bool kLevels, bool kGroup, bool kVisited>
-__global__ __launch_bounds__(kMaxWaves * kWave) void k_env_step(EnvArgs A)
+__global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kEnvStepWaves<kLevels>))) void k_env_step(EnvArgs A)
 {
     extern __shared__ u64 smem[];
     const TaskDev& T = A.T;
@@ -2021,53 +2028,52 @@ __global__ __launch_bounds__(kGroupBlock) void k_group_scatter(const i32* task_i
 }
 
 /// Applies the effects of the picked binding of schema s to the LDS row only (the view stays the parent's), keeping
-/// the effect slots and their prior bits for succ_revert. Returns whether no bit changed (a no-op successor).
+/// the effect slots and their prior bits for succ_revert. Returns whether no bit changed (a no-op successor). One effect
+/// per lane (lane k: slot L.eff[k], prior bit L.before[k]); deletes, then adds.
 __device__ __forceinline__ bool succ_apply(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane, u32* status)
 {
     const auto& S = H.schemas[s];
-    bool noop = true;
-    if (lane == 0)
+    const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
+    if (lane == 0 && S.eff_end - S.eff_begin > kMaxEff)
+        atomicOr(status, kStatusCapacity);
+    const bool mine = lane < ne;
+    const bool add = lane < S.nadd;
+    u32 sl = kNone;
+    bool before = false;
+    if (mine)
     {
-        const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
-        if (S.eff_end - S.eff_begin > kMaxEff)
-            atomicOr(status, kStatusCapacity);
-        for (u32 k = 0; k < ne; ++k)
-        {
-            L.eff[k] = effect_slot(T, L, H.effects[S.eff_begin + k]);
-            L.before[k] = L.eff[k] != kNone && row_bit(L.row, L.eff[k]);
-            if (k < S.nadd && L.eff[k] == kNone)
-                atomicOr(status, kStatusNoSlot);
-        }
-        for (u32 k = S.nadd; k < ne; ++k)
-            if (L.eff[k] != kNone)
-                L.row[L.eff[k] >> 6] &= ~(u64{1} << (L.eff[k] & 63));
-        for (u32 k = 0; k < S.nadd && k < ne; ++k)
-            if (L.eff[k] != kNone)
-                L.row[L.eff[k] >> 6] |= u64{1} << (L.eff[k] & 63);
-        for (u32 k = 0; k < ne; ++k)
-            if (L.eff[k] != kNone && row_bit(L.row, L.eff[k]) != (L.before[k] != 0))
-                noop = false;
+        sl = effect_slot(T, L, H.effects[S.eff_begin + lane]);
+        before = sl != kNone && row_bit(L.row, sl);
+        L.eff[lane] = sl;
+        L.before[lane] = before ? 1u : 0u;
+        if (add && sl == kNone)
+            atomicOr(status, kStatusNoSlot);
     }
     wave_sync();
-    return __shfl(noop ? 1 : 0, 0, kWave) != 0;
+    if (mine && !add && sl != kNone)
+        __hip_atomic_fetch_and(L.row + (sl >> 6), ~(u64{1} << (sl & 63)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    wave_sync();
+    if (mine && add && sl != kNone)
+        __hip_atomic_fetch_or(L.row + (sl >> 6), u64{1} << (sl & 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    wave_sync();
+    const bool changed = mine && sl != kNone && row_bit(L.row, sl) != before;
+    return __ballot(changed) == 0;
 }
 
-/// Restores the parent row after succ_apply.
+/// Restores the parent row after succ_apply (lanes listing one slot hold the same prior bit).
 __device__ __forceinline__ void succ_revert(const auto& H, const Lds& L, u32 s, u32 lane)
 {
-    if (lane == 0)
+    const auto& S = H.schemas[s];
+    const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
+    if (lane < ne)
     {
-        const auto& S = H.schemas[s];
-        const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
-        for (u32 k = 0; k < ne; ++k)
+        const u32 sl = L.eff[lane];
+        if (sl != kNone)
         {
-            const u32 sl = L.eff[k];
-            if (sl == kNone)
-                continue;
-            if (L.before[k])
-                L.row[sl >> 6] |= u64{1} << (sl & 63);
+            if (L.before[lane])
+                __hip_atomic_fetch_or(L.row + (sl >> 6), u64{1} << (sl & 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             else
-                L.row[sl >> 6] &= ~(u64{1} << (sl & 63));
+                __hip_atomic_fetch_and(L.row + (sl >> 6), ~(u64{1} << (sl & 63)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
         }
     }
     wave_sync();
@@ -2409,11 +2415,39 @@ void set_lds(const void* fn, size_t bytes)
 
 /// Blocks of a one-instance launch: a row per wave in batch order; over one group of a grouped batch (whose size only the
 /// device knows) a bounded grid whose blocks stride over the group.
-unsigned one_instance_grid(u64 rows, unsigned nw, bool group)
+/// Compute units of the current device (queried once per device).
+unsigned device_cus()
+{
+    static std::mutex mu;
+    static std::unordered_map<int, unsigned> cus;
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "device");
+    std::lock_guard lock(mu);
+    unsigned& n = cus[dev];
+    if (n == 0)
+    {
+        int v = 0;
+        hip_check(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "compute units");
+        n = static_cast<unsigned>(std::max(1, v));
+    }
+    return n;
+}
+
+/// The grid of a one-instance launch. `resident`: the blocks that are resident at once (LDS bytes `lds` and nw waves per
+/// block), each looping over rows, so that a block stages the hot tables once for many rows of equal work (env steps
+/// and counts); else one block per nw rows. A grouped launch keeps its cap.
+unsigned one_instance_grid(u64 rows, unsigned nw, bool group, size_t lds, bool resident = true)
 {
     constexpr u64 kGroupBlocks = 8192;
+    constexpr size_t kCuLds = 160 * 1024;
+    constexpr unsigned kCuWaves = 24;
     const unsigned g = grid_for(rows, nw);
-    return group ? static_cast<unsigned>(std::min<u64>(g, kGroupBlocks)) : g;
+    if (group)
+        return static_cast<unsigned>(std::min<u64>(g, kGroupBlocks));
+    if (!resident)
+        return g;
+    const unsigned per_cu = std::max<unsigned>(1, std::min<unsigned>(lds ? static_cast<unsigned>(kCuLds / lds) : kCuWaves, kCuWaves / nw));
+    return std::min<unsigned>(g, per_cu * device_cus());
 }
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream)
@@ -2432,7 +2466,7 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
                               : variant(a.T, k_env_step<true, false, false, false>, k_env_step<true, true, false, false>,
                                         k_env_step<false, false, false, false>, k_env_step<false, true, false, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group, lds)), dim3(nw * kWave), lds, stream, a);
     launch_check("env step");
 }
 
@@ -2448,7 +2482,7 @@ void launch_env_count(const CountArgs& a, hipStream_t stream)
                           : variant(a.T, k_env_count<true, false, false>, k_env_count<true, true, false>, k_env_count<false, false, false>,
                                     k_env_count<false, true, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group, lds)), dim3(nw * kWave), lds, stream, a);
     launch_check("env count");
 }
 
@@ -2591,7 +2625,8 @@ void launch_expand(const ExpandArgs& a, hipStream_t stream)
                           : variant(a.T, k_expand<true, false, false>, k_expand<true, true, false>, k_expand<false, false, false>,
                                     k_expand<false, true, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group)), dim3(nw * kWave), lds, stream, a);
+    // one block per nw rows: rows differ widely in successors, and the dispatcher balances them as blocks finish
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group, 0, false)), dim3(nw * kWave), lds, stream, a);
     launch_check("expand");
 }
 
