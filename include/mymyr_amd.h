@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 13
+#define MYA_ABI_VERSION 14
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
@@ -266,6 +266,14 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
  * env-owned scratch, allocated on the first call with a larger batch). */
 int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
                  const int32_t* next_task_ids, void* stream);
+/* The label-mode step (DeviceEnv::step(EnvBatch&, const StepOutputs&, rl::Labels, next_task_ids),
+ * include/mymyr/cuda/env.hpp:185-188; rl::HostEnv's Labels step, src/mymyr/rl/env.cpp:376-426): row i's action is the
+ * label (schema[i], binding[i * binding_stride + k] for k below the schema's arity; device int32 arrays), applied where
+ * it is applicable in the row's state; elsewhere the row does not move and out->invalid is set (a row with no
+ * applicable action is stuck first). out->count is the reached state's full successor count (the caller clamps it to
+ * 0/1 for ActionSpace::Label). No host synchronization: capturable into a HIP graph like mya_env_step. Async. */
+int mya_env_step_labels(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int32_t* schema,
+                        const int32_t* binding, uint32_t binding_stride, const int32_t* next_task_ids, void* stream);
 /* Sizes the env's scratch for batches of up to `rows` rows and sets its kernels' LDS limits now (the reference device
  * env's reserve), so that later calls with such batches allocate nothing and make no runtime call besides kernel
  * launches, as HIP graph capture of them requires. */

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 13  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 14  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -268,6 +268,8 @@ def _load() -> ctypes.CDLL:
         "mya_env_random_actions": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_uint32, c_void_p, c_void_p]),
         "mya_env_goal": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),
         "mya_env_step": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p, c_void_p]),
+        "mya_env_step_labels": (c_int, [c_void_p, POINTER(EnvBatch), POINTER(StepOutputs), c_void_p, c_void_p, c_uint32, c_void_p,
+                                        c_void_p]),
         "mya_env_check": (c_int, [c_void_p]),
         "mya_env_refresh": (c_int, [c_void_p, POINTER(EnvBatch), c_void_p, c_void_p]),
         "mya_env_initial_count": (c_int, [c_void_p, c_uint32, POINTER(c_uint32), POINTER(c_uint8)]),

@@ -10,8 +10,9 @@ addresses: loops of steps capture into HIP graphs (:meth:`BatchedEnv.capture`, o
 calls). Writing ``states``, ``task_ids`` or the goal masks directly needs :meth:`BatchedEnv.refresh`.
 
 The reference's observation encoders are not part of this path; asking for them raises NotImplementedError. Label
-actions (``actions="label"``, ``step((schema, binding))``) run as the index step at each label's position in the
-row's canonical successor order, found in a flat expansion of the current states; counts are 0/1 in label mode. Visited tables (``track_visited``) are kept on the device: ``visited`` [N, H] int64, ``visited_count``
+actions (``actions="label"``, ``step((schema, binding))``) move each row by its label where the label is applicable in
+the row's state (else the row is invalid), in the step kernel itself, so label steps are captured like index steps;
+counts are 0/1 in label mode. Visited tables (``track_visited``) are kept on the device: ``visited`` [N, H] int64, ``visited_count``
 [N] int32, ``visited_status`` [1] int32.
 """
 
@@ -144,7 +145,6 @@ class BatchedEnv:
         if actions not in ("index", "label"):
             raise ValueError("mymyr: actions must be 'index' or 'label'")
         self.actions = actions
-        self._expander = None
         if path not in ("auto", "fast"):
             raise ValueError("mymyr_amd: BatchedEnv runs the device's fast path only")
         if num_envs < 1 or num_envs > 0x7FFFFFFF:
@@ -311,20 +311,22 @@ class BatchedEnv:
                 torch.empty(n, dtype=torch.bool, device=d), torch.empty(n, dtype=torch.int32, device=d),
                 torch.empty((n, self._label_width), dtype=torch.int32, device=d), fs]
 
-    def _label_action(self, action: Any) -> Tensor:
-        """Label mode: each row's (schema, binding) as its position in the row's canonical successor order (-1: not
-        applicable), found in the flat expansion of the current states; the index step with these positions is the
-        reference's label step (its counts clamped to 0/1)."""
+    def _label_action(self, action: Any) -> tuple:
+        """Label mode: each row's (schema int32 [N], binding int32 [N, L]) as device tensors; the step applies a row's
+        label where it is applicable (the reference's label step, its counts clamped to 0/1)."""
         if not isinstance(action, tuple) or len(action) != 2:
             raise ValueError("mymyr: label mode requires action=(schema, binding); the random policy is unavailable")
         schema, binding = action
         if not isinstance(schema, Tensor) or not isinstance(binding, Tensor):
             raise ValueError("mymyr: label actions require schema and binding tensors")
-        if self._expander is None:
-            self._expander = (rl.TaskSuite(self.tasks) if self._suite else rl.TaskTable(self.tasks)) if self.multi else self.tasks[0]
-        ids = self.task_ids if self.multi else None
-        flat = rl.expand(self._expander, self.states, task_ids=ids)
-        return rl.label_actions(flat, schema.to(self.device, torch.int32), binding.to(self.device, torch.int32))
+        n = self.num_envs
+        schema = schema.reshape(n).to(device=self.device, dtype=torch.int32).contiguous()
+        binding = binding.to(device=self.device, dtype=torch.int32)
+        if binding.dim() != 2 or binding.shape[0] != n:
+            raise ValueError(f"mymyr: label actions require a binding tensor of shape [{n}, L]")
+        if binding.shape[1] < self._label_width:
+            raise ValueError(f"mymyr: label bindings have {binding.shape[1]} columns; the largest schema arity is {self._label_width}")
+        return schema, binding.contiguous()
 
     def _action(self, action: Any) -> Optional[Tensor]:
         if self.actions == "label":
@@ -344,13 +346,19 @@ class BatchedEnv:
         ids = self._task_ids(next_task_ids, None, "next_task_ids")
         return ids if self.multi else None  # a table of one: every instance is 0
 
-    def _step_raw(self, outs: list[Tensor], action: Optional[Tensor], next_ids: Optional[Tensor], final: bool,
+    def _step_raw(self, outs: list[Tensor], action: Any, next_ids: Optional[Tensor], final: bool,
                   revisited: Optional[Tensor] = None) -> None:
+        """One step into `outs`: action None (the random policy), int64 [N] indices, or a (schema, binding) label pair."""
         reward, term, trunc, goal, invalid, schema, binding, fs = outs
         o = _lib.StepOutputs(reward.data_ptr(), term.data_ptr(), trunc.data_ptr(), self.count.data_ptr(), fs.data_ptr() if final else None,
                              schema.data_ptr(), binding.data_ptr(), self._label_width, self._words, invalid.data_ptr(),
                              goal.data_ptr(), None, None, 0, 0, _p(revisited))
-        check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(o), _p(action), _p(next_ids), _stream()))
+        if isinstance(action, tuple):
+            ls, lb = action
+            check(lib.mya_env_step_labels(self._h, ctypes.byref(self._batch), ctypes.byref(o), ls.data_ptr(), lb.data_ptr(), lb.shape[1],
+                                          _p(next_ids), _stream()))
+        else:
+            check(lib.mya_env_step(self._h, ctypes.byref(self._batch), ctypes.byref(o), _p(action), _p(next_ids), _stream()))
 
     def step(self, action: Any = None, *, next_task_ids: Optional[Any] = None, final: bool = True, copy: bool = True) -> StepResult:
         """One step of every environment: ``action`` [N] int64 indexes the canonical successor order (None: the
@@ -395,8 +403,6 @@ class BatchedEnv:
     def capture(self, steps: int, policy: Optional[Callable[["BatchedEnv"], Tensor]] = None, *,
                 next_task_ids: Optional[Tensor] = None, final: bool = False, pool: Any = None) -> "CapturedRollout":
         """``steps`` steps (actions from ``policy(self)``, or the random policy) captured into one HIP graph."""
-        if self.actions == "label":
-            raise ValueError("mymyr_amd: label steps expand on the host's schedule (a synchronous expansion) and are not captured")
         return CapturedRollout(self, steps, policy, next_task_ids=next_task_ids, final=final, pool=pool)
 
     def set_launch(self, launch: str) -> None:
@@ -439,6 +445,9 @@ class CapturedRollout:
                  next_task_ids: Optional[Tensor] = None, final: bool = False, pool: Any = None) -> None:
         if steps < 1:
             raise ValueError("mymyr: a captured rollout needs at least one step")
+        self.labels = env.actions == "label"
+        if self.labels and policy is None:
+            raise ValueError("mymyr: label mode has no random policy; pass a policy returning (schema, binding)")
         if next_task_ids is not None and (not isinstance(next_task_ids, Tensor) or next_task_ids.device != env.device):
             raise ValueError("mymyr: a captured rollout's next_task_ids must be a tensor on the environments' device")
         self.env, self.steps, self.policy, self.final = env, int(steps), policy, final
@@ -446,8 +455,9 @@ class CapturedRollout:
         K, n, W, d = self.steps, env.num_envs, env.words, env.device
         z = lambda *shape, dtype: torch.zeros(shape, dtype=dtype, device=d)
         gw = W if env.goals else 0
+        self.label_schema, self.label_binding = None, None
         self.out = Rollout(
-            z(K, n, dtype=torch.int64) if policy is not None else None, z(K, n, dtype=torch.float32), z(K, n, dtype=torch.bool),
+            z(K, n, dtype=torch.int64) if policy is not None and not self.labels else None, z(K, n, dtype=torch.float32), z(K, n, dtype=torch.bool),
             z(K, n, dtype=torch.bool), z(K, n, dtype=torch.bool), z(K, n, dtype=torch.bool), z(K, n, dtype=torch.int32),
             z(K, n, env.label_width, dtype=torch.int32), z(K, n if final else 0, W, dtype=torch.int64), z(K, n, dtype=torch.int32),
             z(K, n, W, dtype=torch.int64), z(K, n, dtype=torch.int32), z(K, n, gw, dtype=torch.int64), z(K, n, gw, dtype=torch.int64),
@@ -465,15 +475,29 @@ class CapturedRollout:
         with torch.cuda.graph(self.graph, pool=pool):
             for k in range(K):
                 self._step(k)
+        if self.labels:
+            self.out = self.out._replace(action_schema=self.label_schema, action_binding=self.label_binding)
 
     def _step(self, k: int) -> None:
         env, o = self.env, self.out
         action = None
-        if self.policy is not None:
+        if self.labels:
+            # the policy's labels into the rollout's label arrays (allocated at the first step, with its binding width)
+            ls, lb = env._action(self.policy(env))
+            if self.label_binding is None:
+                K, n = self.steps, env.num_envs
+                self.label_schema = torch.empty((K, n), dtype=torch.int32, device=env.device)
+                self.label_binding = torch.empty((K, n, lb.shape[1]), dtype=torch.int32, device=env.device)
+            self.label_schema[k].copy_(ls)
+            self.label_binding[k].copy_(lb)
+            action = (self.label_schema[k], self.label_binding[k])
+        elif self.policy is not None:
             action = env._action(self.policy(env))
             o.action[k].copy_(action)
         outs = [o.reward[k], o.terminated[k], o.truncated[k], o.goal[k], o.invalid[k], o.schema[k], o.binding[k], o.final_states[k]]
         env._step_raw(outs, action, self.next_task_ids, self.final, o.revisited[k] if env.visited_capacity else None)
+        if self.labels:
+            env.count.clamp_(max=1)  # ActionSpace::Label: whether an applicable action exists
         o.count[k].copy_(env.count)
         o.states[k].copy_(env.states)
         o.task_ids[k].copy_(env.task_ids)

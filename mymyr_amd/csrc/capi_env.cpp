@@ -613,16 +613,19 @@ int mya_env_reset(mya_env* env, const mya_env_batch* batch, const uint8_t* mask,
     });
 }
 
-int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
-                 const int32_t* next_task_ids, void* stream)
+namespace
 {
-    return guarded([&] {
+/// The step of mya_env_step (actions: index actions, null: the random policy) and of mya_env_step_labels (labels).
+void env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions, const int32_t* label_schema,
+              const int32_t* label_binding, uint32_t label_stride, const int32_t* next_task_ids, void* stream)
+{
+    {
         if (!env || !out)
             throw std::invalid_argument("mymyr_amd: env: null argument");
         check_batch(env, batch);
         if (batch->rows && !batch->at_goal)
             throw std::invalid_argument("mymyr_amd: env: the device step needs the at_goal array");
-        if (!actions && batch->rows && !batch->draws)
+        if (!actions && !label_schema && batch->rows && !batch->draws)
             throw std::invalid_argument("mymyr: env: the random policy needs the draw counters");
         if (env->cfg.max_steps && batch->rows && !batch->steps)
             throw std::invalid_argument("mymyr: env: truncation (max_steps) needs the step counters");
@@ -657,6 +660,9 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
         a.at_goal = batch->at_goal;
         a.first_env = batch->first_env;
         a.actions = actions;
+        a.label_schema = label_schema;
+        a.label_binding = label_binding;
+        a.label_stride = label_stride;
         a.reward = out->reward;
         a.terminated = out->terminated;
         a.truncated = out->truncated;
@@ -710,6 +716,28 @@ int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_output
                 a.wave_words = l.wave_words;
                 launch_env_step_grouped(a, l.variant, l.nw, l.lds, s);
             }
+    }
+}
+}  // namespace
+
+int mya_env_step(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int64_t* actions,
+                 const int32_t* next_task_ids, void* stream)
+{
+    return guarded([&] { env_step(env, batch, out, actions, nullptr, nullptr, 0, next_task_ids, stream); });
+}
+
+int mya_env_step_labels(mya_env* env, const mya_env_batch* batch, const mya_step_outputs* out, const int32_t* schema,
+                        const int32_t* binding, uint32_t binding_stride, const int32_t* next_task_ids, void* stream)
+{
+    return guarded([&] {
+        if (!env)
+            throw std::invalid_argument("mymyr_amd: env: null env");
+        if (batch && batch->rows && (!schema || (!binding && env->label_width)))
+            throw std::invalid_argument("mymyr: label actions require schema and binding arrays");
+        if (binding && binding_stride < env->label_width)
+            throw std::invalid_argument("mymyr: label binding rows of " + std::to_string(binding_stride) + " columns; the largest schema arity is " +
+                                        std::to_string(env->label_width));
+        env_step(env, batch, out, nullptr, schema, binding, binding_stride, next_task_ids, stream);
     });
 }
 

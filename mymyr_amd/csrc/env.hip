@@ -897,6 +897,28 @@ __device__ __forceinline__ bool pick_lanes(const TaskDev& T, const auto& H, cons
     return true;
 }
 
+/// Whether the binding in L.ub (parameters [0, arity)) of schema s is applicable, for a schema with at least one
+/// applicable binding (its ground preconditions hold): parameter i's object is a candidate of its filter step given
+/// parameters [0, i), the test that makes a picked binding applicable (every precondition is checked at the step of its
+/// last parameter). Wave-uniform.
+__device__ __forceinline__ bool label_applicable(const TaskDev& T, const auto& H, const Lds& L, u32 s)
+{
+    const auto& S = H.schemas[s];
+    for (u32 i = 0; i < S.arity; ++i)
+    {
+        const DevStep F = ld(H.steps + S.filter_step[i]);
+        const u32 o = L.ub[i];
+        if (o < F.lo || o - F.lo >= 64 * F.words)
+            return false;
+        const u32 w = (o - F.lo) >> 6, b = (o - F.lo) & 63;
+        if (!((cand_word(T, H, L, F, w, L.ub, 1) >> b) & 1))
+            return false;
+        if (F.check_begin != F.check_end && !checks_ok(T, H, L, F.check_begin, F.check_end, L.ub, 1))
+            return false;
+    }
+    return true;
+}
+
 template<bool kLevels>
 __device__ __forceinline__ bool pick(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 rank, u32 lane)
 {
@@ -1315,6 +1337,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     const u64 draws0 = A.draws ? A.draws[i] : 0;
     const i32 steps0 = A.steps ? A.steps[i] : 0;
     const i32 next_in = (!kOne && A.next_task_ids) ? A.next_task_ids[i] : 0;
+    const i32 label_in = A.label_schema ? A.label_schema[i] : -1;
     // the count cache row: its counts stand for the row's state (and instance) when its fingerprint matches (reset,
     // refresh and step write it; a state written directly since is counted again)
     const u32 cw = A.cache_width;
@@ -1348,8 +1371,29 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         // 2. the choice (env.cpp:416-440)
         st = already_goal ? kGoal : kOk;
         u32 a = 0;
+        bool labelled = false;  // the move is the row's label (no pick)
         if (!already_goal && c == 0)
             st = kStuck;
+        else if (!already_goal && A.label_schema)
+        {
+            // label mode (env.cpp:376-398, 423-425): the label moves where it is applicable, else the row is invalid
+            bool ok = label_in >= 0 && static_cast<u32>(label_in) < T.num_schemas && L.counts[label_in] > 0;
+            if (ok)
+            {
+                const u32 arity = H.schemas[label_in].arity;
+                if (lane < arity)
+                    L.ub[lane] = static_cast<u32>(A.label_binding[i * A.label_stride + lane]);
+                wave_sync();
+                ok = label_applicable(T, H, L, static_cast<u32>(label_in));
+            }
+            if (ok)
+            {
+                schema = static_cast<u32>(label_in);
+                labelled = true;
+            }
+            else
+                st = kInvalid;
+        }
         else if (!already_goal && A.actions)
         {
             const i64 act = act_in;
@@ -1365,7 +1409,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             a = successor_index(key, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, draws0, c);
         }
         u32 rank = 0;
-        if (st == kOk)
+        if (st == kOk && !labelled)
         {
             select_schema(T, L, a, &schema, &rank);
             if (schema == kNone || !pick<kLevels>(T, H, L, schema, rank, lane))

@@ -94,6 +94,11 @@ struct EnvArgs
     u8* at_goal;
     u64 first_env;
     const i64* actions;  // null: the random policy
+    // label mode (DeviceEnv::step with rl::Labels): row i's action is the label (label_schema[i], label_binding[i *
+    // label_stride + k] for k below the schema's arity), applied where it is applicable (else the row is invalid)
+    const i32* label_schema;
+    const i32* label_binding;
+    u32 label_stride;
     float* reward;
     u8* terminated;
     u8* truncated;

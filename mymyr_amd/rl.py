@@ -11,6 +11,7 @@ the next call overwrites, as the reference's recycled batches.
 from __future__ import annotations
 
 import ctypes
+from typing import Optional
 
 import numpy as np
 import torch
@@ -783,10 +784,17 @@ def pad(flat: dict, k: int | None = None, *, words: int | None = None, label_wid
 
 def visited_mask(table: torch.Tensor, count: torch.Tensor, succ_hash: torch.Tensor, parent: torch.Tensor,
                  rows: torch.Tensor | None = None) -> torch.Tensor:
-    """Membership of successor hashes in visited tables (the torch op mymyr::visited_mask, rl::visited_mask of
-    include/mymyr/rl/visited.hpp:63-74) on the device, on the current stream without a host synchronization: out[j] =
-    succ_hash[j] is in the table (table [n, H] int64/uint64, count [n] int32) of row parent[j], or of rows[parent[j]];
-    -1 is padding, and parents or rows outside the tables read as not visited."""
+    """Membership of successor hashes in visited tables (rl::visited_mask of include/mymyr/rl/visited.hpp:63-74) on the
+    device, on the current stream without a host synchronization: out[j] = succ_hash[j] is in the table (table [n, H]
+    int64/uint64, count [n] int32) of row parent[j], or of rows[parent[j]]; -1 is padding, and parents or rows outside
+    the tables read as not visited. The same as torch.ops.mymyr.visited_mask (registered below with a fake
+    implementation, so torch.compile traces it; python/mymyr/rl/torch/_ops.py:464-486)."""
+    return torch.ops.mymyr.visited_mask(table, count, succ_hash, parent, rows)
+
+
+@torch.library.custom_op("mymyr::visited_mask", mutates_args=())
+def _visited_mask_op(table: torch.Tensor, count: torch.Tensor, succ_hash: torch.Tensor, parent: torch.Tensor,
+                     rows: Optional[torch.Tensor]) -> torch.Tensor:
     if table.dim() != 2 or not table.is_cuda:
         raise ValueError("mymyr: visited_mask: table must be a 2-d device tensor")
     n, H = table.shape
@@ -805,6 +813,11 @@ def visited_mask(table: torch.Tensor, count: torch.Tensor, succ_hash: torch.Tens
     check(lib.mya_visited_mask(tab.data_ptr(), count.data_ptr(), n, H, h.data_ptr(), parent.data_ptr(), _p(rows),
                                0 if rows is None else rows.numel(), h.numel(), out.data_ptr(), _stream()))
     return out
+
+
+@_visited_mask_op.register_fake
+def _visited_mask_fake(table, count, succ_hash, parent, rows):
+    return torch.empty(succ_hash.shape, dtype=torch.bool, device=succ_hash.device)
 
 
 def label_actions(flat: dict, schema: torch.Tensor, binding: torch.Tensor) -> torch.Tensor:

@@ -67,6 +67,6 @@ class Task:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value:
+        if h is not None and h.value and lib is not None:  # at interpreter exit the module's globals may be gone
             lib.mya_task_free(h)
             self._h = ctypes.c_void_p()

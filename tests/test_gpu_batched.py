@@ -178,58 +178,125 @@ def test_batched_env_argument_errors(golden):
         env.set_launch("fastest")
 
 
-@pytest.mark.parametrize("table", ["gridworld_table", "transport_table"])
-def test_label_steps_equal_index_steps(golden, table):
+def _labels(rng, x, n, nobj):
+    """Labels for the rows of expansion x: a successor's label with random objects past its arity (70%), 20% of those
+    with one object within the arity replaced by a random object (applicable or not), and 30% random garbage; and each
+    label's position in its row's canonical successor order (-1: not applicable)."""
+    off, sch, bnd = host(x["offsets"]).astype(np.int64), host(x["schema"]), host(x["binding"])
+    L = bnd.shape[1]
+    c = off[1:] - off[:-1]
+    idx = (rng.random(n) * np.maximum(c, 1)).astype(np.int64)
+    ls = np.full(n, -1, np.int32)
+    lb = rng.integers(-1, 6, (n, L + 1)).astype(np.int32)
+    for i in range(n):
+        if c[i]:
+            ls[i] = sch[off[i] + idx[i]]
+            row = bnd[off[i] + idx[i]]
+            lb[i, :L] = np.where(row >= 0, row, lb[i, :L])
+            arity = int((row >= 0).sum())
+            if arity and rng.random() < 0.2:
+                lb[i, rng.integers(arity)] = rng.integers(nobj)
+    garbage = rng.random(n) < 0.3
+    ls[garbage] = rng.integers(-1, 8, int(garbage.sum()))
+    act = np.full(n, -1, np.int64)
+    for i in range(n):
+        for j in range(off[i], off[i + 1]):
+            if sch[j] == ls[i] and np.all((bnd[j] < 0) | (bnd[j] == lb[i, :L])):
+                act[i] = j - off[i]
+                break
+    return ls, lb, act
+
+
+LABEL_CASES = [("gridworld_table", {}), ("transport_table", {}), ("transport_table", {"goals": True, "track_visited": 16}),
+               ("gridworld_table", {"track_visited": 8}), ("mixed_suite", {"suite": True, "goals": True})]
+
+
+@pytest.mark.parametrize("table,extra", LABEL_CASES)
+def test_label_steps_equal_index_steps(golden, table, extra):
     """actions="label": a label step equals the index step at the label's position in the row's canonical successor
     order (-1, invalid, when the label is not applicable), with counts clamped to 0/1, as the reference's label steps
-    equal its index steps (tests/test_label_equivalence.py). Positions here come from a host scan of rl.expand's
-    output; labels are successors' labels with random objects past their arity, and 30% random garbage."""
+    equal its index steps (tests/test_label_equivalence.py), also with per-env goals and visited tables. Positions come
+    from a host scan of rl.expand's output; labels are successors' labels with random objects past their arity, some
+    with a random object within it, and 30% random garbage."""
     from mymyr_amd import rl
     from mymyr_amd.batched import BatchedEnv
 
     ts = load_tasks(golden, table)
     n = 256
-    kw = dict(seed=5, max_steps=9, sampler="uniform")
-    a, b = BatchedEnv(ts, n, actions="label", **kw), BatchedEnv(ts, n, **kw)
-    print(f"label steps: {table}, {n} envs", flush=True)
+    extra = dict(extra)
+    suite = extra.pop("suite", False)
+    tt = rl.TaskSuite(ts) if suite else rl.TaskTable(ts)  # a suite's labels carry each domain's own schema ids
+    kw = dict(seed=5, max_steps=9, sampler="uniform", **extra)
+    a, b = BatchedEnv(tt if suite else ts, n, actions="label", **kw), BatchedEnv(tt if suite else ts, n, **kw)
+    print(f"label steps: {table} {extra} suite={suite}, {n} envs", flush=True)
     assert torch.equal(a.count, b.count.clamp(max=1))
     rng = np.random.default_rng(2)
-    tt = rl.TaskTable(ts)
+    nobj = max(t.num_objects for t in ts)
     moved = invalid = 0
+    names = ["reward", "terminated", "truncated", "goal", "invalid", "schema", "binding", "final_states", "states", "task_ids", "at_goal"]
+    if extra.get("track_visited"):
+        names.append("revisited")
     for k in range(10):
         assert torch.equal(a.states, b.states) and torch.equal(a.task_ids, b.task_ids)
         x = rl.expand(tt, b.states, task_ids=b.task_ids)
-        off, sch, bnd = host(x["offsets"]).astype(np.int64), host(x["schema"]), host(x["binding"])
-        L = bnd.shape[1]
-        c = off[1:] - off[:-1]
-        idx = (rng.random(n) * np.maximum(c, 1)).astype(np.int64)
-        ls = np.full(n, -1, np.int32)
-        lb = rng.integers(-1, 6, (n, L + 1)).astype(np.int32)
-        for i in range(n):
-            if c[i]:
-                ls[i] = sch[off[i] + idx[i]]
-                row = bnd[off[i] + idx[i]]
-                lb[i, :L] = np.where(row >= 0, row, lb[i, :L])
-        garbage = rng.random(n) < 0.3
-        ls[garbage] = rng.integers(-1, 8, int(garbage.sum()))
-        act = np.full(n, -1, np.int64)
-        for i in range(n):
-            for j in range(off[i], off[i + 1]):
-                if sch[j] == ls[i] and np.all((bnd[j] < 0) | (bnd[j] == lb[i, :L])):
-                    act[i] = j - off[i]
-                    break
+        ls, lb, act = _labels(rng, x, n, nobj)
         ra = a.step((torch.from_numpy(ls).cuda(), torch.from_numpy(lb).cuda()))
         rb = b.step(torch.from_numpy(act).cuda())
-        for name in ("reward", "terminated", "truncated", "goal", "invalid", "schema", "binding", "final_states", "states", "task_ids",
-                     "at_goal"):
+        for name in names:
             assert torch.equal(getattr(ra, name), getattr(rb, name)), f"step {k}: {name}"
         assert torch.equal(ra.count, rb.count.clamp(max=1)), f"step {k}: count"
         moved += int((ra.schema >= 0).sum())
         invalid += int(ra.invalid.sum())
     assert moved > 0 and invalid > 0, (moved, invalid)
+    if extra.get("track_visited"):
+        assert torch.equal(a.visited, b.visited) and torch.equal(a.visited_count, b.visited_count)
     with pytest.raises(ValueError):
         a.random_actions()
     with pytest.raises(ValueError):
         a.step(None)
+    with pytest.raises(ValueError, match="columns"):
+        a.step((torch.zeros(n, dtype=torch.int32).cuda(), torch.zeros((n, 0), dtype=torch.int32).cuda()))
+    a.check_errors()
+    b.check_errors()
+
+
+def test_captured_label_rollout_equals_eager_steps(golden):
+    """Label mode captured into one HIP graph (a label policy computed on the device from the states): replays equal the
+    same label steps made eagerly on a twin env, and the rollout keeps the policy's labels."""
+    from mymyr_amd.batched import BatchedEnv
+
+    ts = load_tasks(golden, "transport_table")
+    n = 512
+    kw = dict(seed=4, max_steps=7, sampler="uniform", actions="label", track_visited=8)
+    a, b = BatchedEnv(ts, n, **kw), BatchedEnv(ts, n, **kw)
+    S = max(t.num_schemas for t in ts)
+    nobj = max(t.num_objects for t in ts)
+    L = a.label_width
+
+    def pol(env):
+        h = env.states[:, : 2 * L].to(torch.int64)
+        schema = (h.sum(1) % S).to(torch.int32)
+        binding = ((h[:, :L] ^ h[:, L : 2 * L]).abs() % nobj).to(torch.int32)
+        return schema, binding
+
+    with pytest.raises(ValueError, match="policy"):
+        a.capture(3, None)
+    K = 5
+    roll = a.capture(K, pol, final=True)
+    moved = 0
+    for rep in range(2):
+        out = roll.replay()
+        torch.cuda.synchronize()
+        for k in range(K):
+            ls, lb = pol(b)
+            r = b.step((ls, lb), final=True)
+            assert torch.equal(out.action_schema[k], ls) and torch.equal(out.action_binding[k], lb), f"replay {rep} step {k}: labels"
+            for name in ("reward", "terminated", "truncated", "goal", "invalid", "schema", "binding", "final_states", "count",
+                         "states", "task_ids", "at_goal", "revisited"):
+                assert torch.equal(getattr(out, name)[k], getattr(r, name)), f"replay {rep} step {k}: {name}"
+            moved += int((r.schema >= 0).sum())
+        for name in ("states", "task_ids", "steps", "count", "at_goal", "counts", "visited", "visited_count"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), f"replay {rep}: env {name}"
+    assert out.action is None
     a.check_errors()
     b.check_errors()

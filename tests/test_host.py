@@ -143,3 +143,18 @@ def test_brfs_option_arguments_checked_on_the_host(golden):
         search.brfs(t, max_seconds=-1.0)
     with pytest.raises(TypeError, match="CancelToken"):
         search.brfs(t, cancel=True)
+
+
+def test_visited_mask_is_a_registered_torch_op():
+    """rl.visited_mask is the torch op mymyr::visited_mask, with a fake implementation (bool [size]) for tracing."""
+    torch = pytest.importorskip("torch")
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from mymyr_amd import rl  # noqa: F401  (registers the op)
+
+    assert hasattr(torch.ops.mymyr, "visited_mask")
+    with FakeTensorMode():
+        tab, cnt = torch.empty((4, 8), dtype=torch.int64), torch.empty(4, dtype=torch.int32)
+        h, par = torch.empty(10, dtype=torch.int64), torch.empty(10, dtype=torch.int32)
+        out = torch.ops.mymyr.visited_mask(tab, cnt, h, par, None)
+        assert out.shape == (10,) and out.dtype == torch.bool
