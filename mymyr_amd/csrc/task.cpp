@@ -62,45 +62,81 @@ public:
         const u32 ns = u();
         for (u32 i = 0; i < ns; ++i)
             t.schemas.push_back(schema(t));
-        while (!at_end())
+        // the optional sections, in the reference's order: X, C, EG (text_format.cpp:122-187)
+        tag = at_end() ? std::string_view{} : word();
+        if (tag == "X")
         {
-            tag = word();
-            if (tag == "X")
-            {
-                if (u() != 0)
-                    fail("axioms (derived predicates) are not supported by the device path");
-            }
-            else if (tag == "C")
-            {
-                // collapsed parameters: the schemas bind the other parameters only (labels as the reference's)
-                const u32 k = u();
-                for (u32 i = 0; i < k; ++i)
-                {
-                    const u32 s = u();
-                    if (s >= t.schemas.size())
-                        fail("collapsed parameter of an unknown schema");
-                    (void)u();
-                    (void)u();
-                    (void)i32v();
-                }
-            }
-            else if (tag == "EG")
-            {
-                (void)u();
-                const u32 k = u();
-                for (u32 i = 0; i < k; ++i)
-                {
-                    const u32 p = u();
-                    if (p >= t.preds.size())
-                        fail("encoding goal literal of an unknown predicate");
-                    (void)u();
-                    for (u32 j = 0; j < t.preds[p].arity; ++j)
-                        (void)u();
-                }
-            }
-            else
-                fail("unexpected section " + std::string(tag));
+            if (u() != 0)
+                fail("axioms (derived predicates) are not supported by the device path");
+            tag = at_end() ? std::string_view{} : word();
         }
+        if (tag == "C")
+        {
+            // collapsed parameters: "C <k>", then k lines "<schema> <position> <written> <representative or -1>"
+            t.unused_parameters_collapsed = true;
+            const u32 k = u();
+            for (u32 i = 0; i < k; ++i)
+            {
+                CollapsedText c;
+                c.schema = u();
+                if (c.schema >= t.schemas.size())
+                    fail("collapsed parameter of an unknown schema");
+                c.position = u();
+                c.written = u() != 0;
+                c.representative = i32v();
+                t.collapsed.push_back(c);
+            }
+            // the reference's checks (task_data.cpp:136-147): per schema, positions ascend and lie among the parameters
+            // before collapsing; a representative is an object
+            std::stable_sort(t.collapsed.begin(), t.collapsed.end(), [](const CollapsedText& a, const CollapsedText& b) { return a.schema < b.schema; });
+            for (size_t a = 0; a < t.collapsed.size();)
+            {
+                size_t b = a;
+                while (b < t.collapsed.size() && t.collapsed[b].schema == t.collapsed[a].schema)
+                    ++b;
+                const u32 before = t.schemas[t.collapsed[a].schema].arity + static_cast<u32>(b - a);
+                for (size_t j = a; j < b; ++j)
+                {
+                    const CollapsedText& c = t.collapsed[j];
+                    if (c.position >= before || (j > a && t.collapsed[j - 1].position >= c.position))
+                        fail("collapsed parameter positions must ascend within the schema's parameters before collapsing");
+                    if (c.representative >= 0 && static_cast<u32>(c.representative) >= t.objects)
+                        fail("collapsed parameter representative out of range");
+                    if (c.representative < -1)
+                        fail("collapsed parameter representative out of range");
+                }
+                a = b;
+            }
+            tag = at_end() ? std::string_view{} : word();
+        }
+        if (tag == "EG")
+        {
+            // the encoding goal: "EG <complete> <k>", then k ground literals "<pred> <positive> <objects...>"
+            t.encoding_goal_recorded = true;
+            t.encoding_goal_complete = u() != 0;
+            const u32 k = u();
+            for (u32 i = 0; i < k; ++i)
+            {
+                GroundLiteralText g;
+                g.pred = u();
+                if (g.pred >= t.preds.size())
+                    fail("encoding goal: predicate out of range");
+                g.positive = u() != 0;
+                for (u32 j = 0; j < t.preds[g.pred].arity; ++j)
+                {
+                    const u32 o = u();
+                    if (o >= t.objects)
+                        fail("encoding goal: object out of range");
+                    g.objects.push_back(o);
+                }
+                t.encoding_goal.push_back(std::move(g));
+            }
+            std::sort(t.encoding_goal.begin(), t.encoding_goal.end());
+            t.encoding_goal.erase(std::unique(t.encoding_goal.begin(), t.encoding_goal.end()), t.encoding_goal.end());
+            // the reference's reader stops after the encoding goal: what follows it is not read
+        }
+        else if (!tag.empty())
+            fail("unexpected section " + std::string(tag));
         for (const auto& p : t.preds)
             if (p.kind == 'D')
                 fail("derived predicates are not supported by the device path");
@@ -462,6 +498,11 @@ private:
             }
             for (u32 v = 0; v < s.arity; ++v)
                 if (!any_bit(dom[v]))
+                    never = true;
+            // a collapsed parameter without a representative (no object of its type): the schema has no action
+            // (src/mymyr/task/compile.cpp:1171-1181)
+            for (const CollapsedText& c : T->collapsed)
+                if (c.schema == si && c.representative < 0)
                     never = true;
             C->never[si] = never ? 1 : 0;
         }

@@ -60,6 +60,34 @@ struct PredicateText
     std::string name;
 };
 
+/// A parameter that normalization removed from its schema because nothing but its type mentions it (the reference's
+/// CollapsedParameter, include/mymyr/formalism/task_data.hpp:194-206): the schema's actions bind the other parameters,
+/// and the action as written names the representative at `position` of the parameter list before collapsing.
+struct CollapsedText
+{
+    u32 schema = 0;
+    u32 position = 0;
+    bool written = false;
+    i32 representative = -1;  // -1: none
+};
+
+/// A ground literal of the encoding goal (the goal that observation encodings show; the search goal is `goal`).
+struct GroundLiteralText
+{
+    u32 pred = 0;
+    bool positive = true;
+    std::vector<u32> objects;
+    bool operator<(const GroundLiteralText& o) const
+    {
+        if (positive != o.positive)
+            return positive;  // positive literals first
+        if (pred != o.pred)
+            return pred < o.pred;
+        return objects < o.objects;
+    }
+    bool operator==(const GroundLiteralText& o) const { return positive == o.positive && pred == o.pred && objects == o.objects; }
+};
+
 struct TaskText
 {
     u32 objects = 0;
@@ -67,6 +95,12 @@ struct TaskText
     std::vector<std::vector<u32>> static_init, fluent_init;  // [pred, args...]
     std::vector<Literal> goal;                                // ground
     std::vector<SchemaText> schemas;
+    // the C section: collapsed parameters ascending in (schema, position); labels bind the schemas' own parameters
+    bool unused_parameters_collapsed = false;
+    std::vector<CollapsedText> collapsed;
+    // the EG section: sorted and unique (positive first, predicate, objects)
+    bool encoding_goal_recorded = false, encoding_goal_complete = false;
+    std::vector<GroundLiteralText> encoding_goal;
 };
 
 /// Parses the reference's task text format (classical subset: no numeric sections, no axioms, no conditional

@@ -413,6 +413,38 @@ def make_brfs_options():
     dump("brfs_options.json", out)
 
 
+def goal_lines(text):
+    lines = text.rstrip("\n").split("\n")
+    gi = [i for i, l in enumerate(lines) if l.startswith("G ")][0]
+    return lines[gi + 1: gi + 1 + int(lines[gi].split()[1])]
+
+
+# tasks with the optional C (collapsed parameters) and EG (encoding goal) sections: a suite task's text with the sections
+# appended; a collapsed parameter without a representative (-1) leaves its schema without actions
+SECTION_TASKS = {
+    "sections_gripper_rep": ("gripper__prob05", "C 2\n0 2 1 0\n1 0 0 5\n", True),
+    "sections_gripper_norep": ("gripper__prob05", "C 1\n1 0 0 -1\n", True),
+    "sections_blocks_norep": ("blocks__probBLOCKS-8-0", "C 2\n0 1 1 3\n2 0 1 -1\n", False),
+    "sections_logistics_eg": ("logistics00__probLOGISTICS-6-1", "", True),
+}
+
+
+def make_sections():
+    """BrFS of the reference on suite tasks with C and EG sections (tests/golden/tasks/sections_*.txt, written here)."""
+    out = {}
+    for name, (base, c, eg) in SECTION_TASKS.items():
+        text = open(fx.task_path(base)).read().rstrip("\n") + "\n" + c
+        if eg:
+            g = goal_lines(text)
+            text += "EG 1 %d\n" % len(g) + "\n".join(reversed(g)) + "\n"
+        with open(fx.task_path(name), "w") as f:
+            f.write(text)
+        out[name + ":goal"] = brfs_record(name, stop_at_goal=True)
+        out[name + ":all"] = brfs_record(name, stop_at_goal=False, max_states=200000)
+        print(name, out[name + ":all"]["states"], out[name + ":goal"]["status"], flush=True)
+    dump("brfs_sections.json", out)
+
+
 def make_pool():
     """Digests of every batch the reference CpuEnvPool returns over each pool case's scripted calls."""
     out = {}
@@ -468,7 +500,7 @@ def main():
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool,
-             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "brfs_options": make_brfs_options, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

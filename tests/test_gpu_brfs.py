@@ -242,3 +242,18 @@ def test_cancel_and_time_stop_between_batches(golden):
     else:
         assert r.states < full["states"] and _consistent(r)
         assert r.layer_counts[:-1] == full["layer_counts"][: max(0, r.layers - 1)]
+
+
+@pytest.mark.parametrize("key", ["sections_gripper_rep:goal", "sections_gripper_rep:all", "sections_gripper_norep:goal",
+                                 "sections_gripper_norep:all", "sections_blocks_norep:goal", "sections_blocks_norep:all",
+                                 "sections_logistics_eg:goal", "sections_logistics_eg:all"])
+def test_tasks_with_collapsed_parameters_and_encoding_goal(golden, key):
+    """Tasks with the C (collapsed parameters) and EG (encoding goal) sections: a collapsed parameter without a
+    representative leaves its schema without actions (src/mymyr/task/compile.cpp:1171-1181), one with a representative
+    changes nothing, and the encoding goal does not touch the search; counts, fingerprints and plans equal to the
+    reference's on the same text."""
+    exp = golden.load("brfs_sections.json")[key]
+    name = key.split(":")[0]
+    r = device(golden, name, full=True, **exp["options"])
+    assert not same(r, exp), (key, same(r, exp))
+    assert same_plan(r, exp), (key, r["result"].plan[:4], exp.get("plan", [])[:4])

@@ -158,3 +158,40 @@ def test_visited_mask_is_a_registered_torch_op():
         h, par = torch.empty(10, dtype=torch.int64), torch.empty(10, dtype=torch.int32)
         out = torch.ops.mymyr.visited_mask(tab, cnt, h, par, None)
         assert out.shape == (10,) and out.dtype == torch.bool
+
+
+SECTION_ERRORS = [
+    ("C 1\n0 5 1 0\n", "ascend"),           # a position past the parameters before collapsing
+    ("C 2\n0 1 1 0\n0 0 1 0\n", "ascend"),  # positions of one schema not ascending
+    ("C 1\n9 0 1 0\n", "unknown schema"),
+    ("C 1\n0 0 1 999\n", "representative"),
+    ("EG 1 1\n99 1 0\n", "predicate"),
+    ("EG 1 1\n6 1 999 1\n", "object"),
+    ("C 0\nX 0\n", "unexpected section"),  # the sections' order is X, C, EG (what follows EG is not read)
+    ("Z 1\n", "unexpected section"),
+]
+
+
+@pytest.mark.parametrize("appendix,match", SECTION_ERRORS)
+def test_malformed_c_and_eg_sections_are_refused_as_the_reference_does(golden, appendix, match, tmp_path):
+    """The reader checks the C and EG sections as the reference's reader and validator do (text_format.cpp:140-187,
+    task_data.cpp:129-147): both refuse each of these appendices to a valid task."""
+    from mymyr_amd._lib import MyaError
+    from oracle import ref
+
+    text = open(golden.task_path("gripper__prob05")).read().rstrip("\n") + "\n" + appendix
+    with pytest.raises(MyaError, match=match):
+        Task.from_text(text)
+    if ref.available():
+        p = tmp_path / "t.txt"
+        p.write_text(text)
+        with pytest.raises(Exception):
+            ref.RefTask(str(p))
+
+
+def test_c_and_eg_sections_are_read(golden):
+    """Valid C and EG sections load; a schema whose collapsed parameter has no representative has no successors."""
+    from mymyr_amd import gen  # noqa: F401
+
+    for name in ("sections_gripper_rep", "sections_gripper_norep", "sections_blocks_norep", "sections_logistics_eg"):
+        Task.from_text_file(golden.task_path(name))
