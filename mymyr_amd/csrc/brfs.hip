@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
         return;
     Slice<G, kPairs<W>> me;
     src.load(j, q, me);
-    const u64 h = group_hash<G, kPairs<W>>(me, q, gbase);
+    const u64 h = group_set_hash<G, kPairs<W>>(me, q, gbase);
     if (blocked.capacity)
     {
         // the blocked test precedes the store (brfs.cpp:350-361): a blocked candidate takes no entry and no id

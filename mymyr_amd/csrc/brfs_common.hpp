@@ -119,7 +119,7 @@ struct Buffers
 using Clock = std::chrono::steady_clock;
 
 /// The blocked states of a search on the device (BlockedView): the rows padded to the set's row width W, duplicates
-/// dropped, the table built here with the state set's hash, slot and tag.
+/// dropped, the table built here with the state set's table hash (set_hash), slot and tag.
 inline BlockedView upload_blocked(const std::vector<u64>& rows, u32 task_words, u32 W, u64 batch, Buffers& b, hipStream_t stream)
 {
     const u64 k = task_words ? rows.size() / task_words : 0;
@@ -135,7 +135,7 @@ inline BlockedView upload_blocked(const std::vector<u64>& rows, u32 task_words, 
     {
         std::fill(row.begin(), row.end(), 0);
         std::copy(rows.begin() + i * task_words, rows.begin() + (i + 1) * task_words, row.begin());
-        const u64 h = hash_state(row.data(), W);
+        const u64 h = set_hash(row.data(), W);
         const u64 tag = h >> 32;
         u64 slot = slot_of_hash(h, cap);
         bool dup = false;

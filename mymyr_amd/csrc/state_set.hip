@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kBlock) void k_insert(StateSetView s, const u64* __
     const BufferRows src{rows, s.words};
     Slice<G, K> me;
     src.load(j, q, me);
-    const u64 h = group_hash<G, K>(me, q, gbase);
+    const u64 h = group_set_hash<G, K>(me, q, gbase);
     if (blocked.capacity)
     {
         // a blocked candidate is dropped before the table is probed (it takes no entry and no id)

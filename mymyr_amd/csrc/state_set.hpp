@@ -6,8 +6,9 @@
 // A batch insert keeps the reference's id rule (include/mymyr/cuda/state_set.hpp:2-18, the CPU stores'
 // first-discovery ids: src/mymyr/search/brfs.cpp:1657-1780): among equal candidates of one batch the smallest
 // candidate index wins (64-bit atomicMin on the pending entry), and new ids follow candidate order (an exclusive scan
-// of the winner flags). The probe hash is the public state hash (hash_state); slot = fastrange of its low 32 bits over
-// the capacity, tag = its high 32 bits, linear probing.
+// of the winner flags). The probe hash (set_hash) is the public state hash (hash_state) for rows of at most 32 words
+// and an order-free sum of mixed words above (set_hash_wide); slot = fastrange of its low 32 bits over the capacity,
+// tag = its high 32 bits, linear probing.
 //
 // A batch is three steps on one stream: probe (group of lanes per row: hash, probe, CAS or atomicMin, loser flags),
 // the winner list (a scan of the flags: winner w gets id = the set's size + w, recorded per candidate in the batch's

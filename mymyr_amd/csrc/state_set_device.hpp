@@ -5,10 +5,10 @@
 // coalesced request of the whole group, and the group's lanes follow one control path (every branch depends on
 // group-uniform values only).
 //
-// The state hash is the public hash_state (include/mymyr/core/hash.hpp:38-60) over the trimmed words, chained over the
-// pairs in order with the pair broadcast from its lane; the table probe keeps the reference's id rule
-// (include/mymyr/cuda/state_set.hpp:2-18): among equal candidates the smallest candidate index wins (64-bit atomicMin
-// on the pending entry), new ids follow candidate order.
+// The table hash of rows of at most 32 words is the public hash_state (include/mymyr/core/hash.hpp:38-60) over the
+// trimmed words, chained over the pairs in order with the pair broadcast from its lane (wider rows: set_hash_wide);
+// the table probe keeps the reference's id rule (include/mymyr/cuda/state_set.hpp:2-18): among equal candidates the
+// smallest candidate index wins (64-bit atomicMin on the pending entry), new ids follow candidate order.
 //
 // Entries are never rewritten after the probe: a batch's pending entries keep the candidate code of their winner, and
 // the batch's epoch (one of up to 64, 6 bits of the code) maps candidate indices to ids through id_of, written by the
@@ -186,6 +186,48 @@ __device__ __forceinline__ u64 group_hash(const Slice<G, K>& s, u32 q, u32 gbase
                 h = mulfold(h ^ a ^ kHashP1, b ^ kHashP2);
         }
     return mix64(h);
+}
+
+/// Rows wider than this many words are placed in the table by set_hash_wide instead of hash_state.
+constexpr u32 kWideHashWords = 32;
+
+/// The table hash of rows wider than kWideHashWords words: mix64 of the seed xor the sum over the row's nonzero words w
+/// of mix64(word + (w + 1) * phi). A row's table slot and tag only place it (ids follow candidate order, and the public
+/// state hash has its own kernels), so wide rows take this order-free sum, which the lanes of a group add up in
+/// parallel, instead of hash_state's chain of one dependent multiply-fold per word pair. Trailing zero words add
+/// nothing, as in hash_state.
+MYA_HD inline u64 set_hash_wide(const u64* w, u32 n)
+{
+    u64 acc = 0;
+    for (u32 i = 0; i < n; ++i)
+        if (w[i])
+            acc += mix64(w[i] + static_cast<u64>(i + 1) * 0x9E3779B97F4A7C15ull);
+    return mix64(acc ^ kHashSeed);
+}
+
+/// The table hash of a row of `words` words (host side of group_set_hash).
+MYA_HD inline u64 set_hash(const u64* w, u32 words) { return words > kWideHashWords ? set_hash_wide(w, words) : hash_state(w, words); }
+
+/// set_hash of the group's row (group-uniform): set_hash_wide for the 64-lane groups of rows above 32 words.
+template<int G, int K>
+__device__ __forceinline__ u64 group_set_hash(const Slice<G, K>& s, u32 q, u32 gbase)
+{
+    if constexpr (G == kWave)
+    {
+        u64 acc = 0;
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+        {
+            const u64 w = 2 * static_cast<u64>(k * G + q);
+            if (s.lo[k])
+                acc += mix64(s.lo[k] + (w + 1) * 0x9E3779B97F4A7C15ull);
+            if (s.hi[k])
+                acc += mix64(s.hi[k] + (w + 2) * 0x9E3779B97F4A7C15ull);
+        }
+        return mix64(wave_sum64(acc) ^ kHashSeed);
+    }
+    else
+        return group_hash<G, K>(s, q, gbase);
 }
 
 __device__ __forceinline__ u64 load_entry(const u64* e) { return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
