@@ -152,6 +152,8 @@ struct Lds
     lds<u32>* eff;     // [kMaxEff]: effect slots of a successor (lane k: effect k)
     lds<u32>* before;  // [kMaxEff]: their bits before the move
     lds<u32>* counts;  // [num_schemas]
+    lds<u64>* dfs_m;   // [8] the successor enumeration's per-parameter candidates left in the current word
+    lds<u32>* dfs_w;   // [8] and that word
 };
 
 template<bool kLevels>
@@ -178,6 +180,10 @@ __device__ __forceinline__ Lds lds_of(lds<u64>* base, const TaskDev& T)
     p += kMaxEff / 2;
     l.counts = reinterpret_cast<lds<u32>*>(p);
     p += (T.num_schemas + 1) / 2;
+    l.dfs_m = p;
+    p += 8;
+    l.dfs_w = reinterpret_cast<lds<u32>*>(p);
+    p += 4;
     if constexpr (kLevels)
     {
         l.qa = reinterpret_cast<lds<u32>*>(p);
@@ -917,6 +923,105 @@ __device__ __forceinline__ bool label_applicable(const TaskDev& T, const auto& H
             return false;
     }
     return true;
+}
+
+/// Calls emit(k, s) for the successors of the state in canonical order (schema, then lexicographic binding),
+/// k = 0, 1, ...; L.ub holds the binding during the call, and emit returns false to stop. Each schema with successors
+/// (L.counts from count_all) is enumerated depth first over its parameters in order, so the bindings come in the order
+/// pick(rank) finds them for rank 0, 1, .... A level takes the window words of its parameter's filter step one at a
+/// time: lane b tests candidate b against the step's checks and counts its completions over the rest of the plan (as
+/// pick does), and only candidates with completions are visited, lowest first; the leaf level emits its candidates.
+/// Counting thus happens once per node of the binding tree instead of once per successor and parameter. The levels'
+/// words and candidates left live in L.dfs_w / L.dfs_m; L.bind holds the binding's prefix in every lane's column.
+/// Returns the successors enumerated.
+template<class Emit>
+__device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& H, const Lds& L, u32 lane, Emit&& emit)
+{
+    const u32 A = T.label_width ? T.label_width : 1;
+    u32 k = 0;
+    for (u32 s = 0; s < T.num_schemas; ++s)
+    {
+        if (L.counts[s] == 0)
+            continue;
+        const auto& S = H.schemas[s];
+        if (S.arity == 0)
+        {
+            if (!emit(k++, s))
+                return k;
+            continue;
+        }
+        // the candidates of parameter i in word w with at least one completion (wave-uniform mask)
+        auto word_mask = [&](u32 i, u32 w) -> u64 {
+            const DevStep F = ld(H.steps + S.filter_step[i]);
+            const u64 m = cand_word(T, H, L, F, w, L.bind + lane, 64);
+            bool live = false;
+            if ((m >> lane) & 1)
+            {
+                L.bind[i * 64 + lane] = F.lo + 64 * w + lane;
+                live = F.check_begin == F.check_end || checks_ok(T, H, L, F.check_begin, F.check_end, L.bind + lane, 64);
+                if (live && i + 1 < S.arity)
+                    live = count_from(T, H, L, S.plan_begin[i + 1], S.plan_begin[i + 2], lane) != 0;
+            }
+            return __ballot(live);
+        };
+        // parameter i from its first word with live candidates (false: none)
+        auto open = [&](u32 i, u32 w0) -> bool {
+            const DevStep F = ld(H.steps + S.filter_step[i]);
+            for (u32 w = w0; w < F.words; ++w)
+            {
+                const u64 m = word_mask(i, w);
+                if (m)
+                {
+                    wave_sync();
+                    if (lane == 0)
+                    {
+                        L.dfs_m[i] = m;
+                        L.dfs_w[i] = w;
+                    }
+                    wave_sync();
+                    return true;
+                }
+            }
+            return false;
+        };
+        u32 i = 0;
+        bool have = open(0, 0);
+        for (;;)
+        {
+            if (!have)
+            {
+                if (i == 0)
+                    break;
+                --i;
+                have = L.dfs_m[i] != 0 || open(i, L.dfs_w[i] + 1);
+                continue;
+            }
+            // the level's lowest live candidate
+            const u64 m = L.dfs_m[i];
+            const u32 w = L.dfs_w[i];
+            const u32 o = ld(H.steps + S.filter_step[i]).lo + 64 * w + static_cast<u32>(__builtin_ctzll(m));
+            wave_sync();
+            if (lane == 0)
+            {
+                L.dfs_m[i] = m & (m - 1);
+                L.ub[i] = o;
+            }
+            L.bind[i * 64 + lane] = o;
+            for (u32 q = 0; q < i && q < A; ++q)
+                L.bind[q * 64 + lane] = L.ub[q];
+            wave_sync();
+            if (i + 1 == S.arity)
+            {
+                if (!emit(k++, s))
+                    return k;
+                have = L.dfs_m[i] != 0 || open(i, w + 1);
+                continue;
+            }
+            ++i;
+            have = open(i, 0);
+        }
+    }
+    return k;
 }
 
 template<bool kLevels>
@@ -2169,16 +2274,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
     }
     const bool keep_all = A.pass == 1 && A.drop_noops && A.noops[i] == c;
     u32 noops = 0, kept = 0;
-    for (u32 k = 0; k < c; ++k)
-    {
-        u32 s = kNone, rank = 0;
-        select_schema(T, L, k, &s, &rank);
-        if (s == kNone || !pick<kLevels>(T, H, L, s, rank, lane))
-        {
-            if (lane == 0)
-                atomicOr(A.status, kStatusPickFailed);
-            break;
-        }
+    const u32 listed = for_each_successor(T, H, L, lane, [&](u32 k, u32 s) {
         const bool noop = succ_apply(T, H, L, s, lane, A.status);
         noops += noop ? 1 : 0;
         if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
@@ -2231,7 +2327,10 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
             }
         }
         succ_revert(H, L, s, lane);
-    }
+        return true;
+    });
+    if (listed != c && lane == 0)
+        atomicOr(A.status, kStatusPickFailed);
     if (A.pass == 0 && lane == 0)
     {
         A.counts[i] = c;
@@ -2390,17 +2489,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
         const u32 c = count_all<kLevels>(T, H, L, lane);
         if (lane == 0 && count)
             count[i] = static_cast<i32>(c);
-        for (u32 k = 0; k < c && k < cap; ++k)
-        {
-            u32 s = kNone, rank = 0;
-            select_schema(T, L, k, &s, &rank);
-            const bool ok = s != kNone && pick<kLevels>(T, H, L, s, rank, lane);
-            if (!ok)
-            {
-                if (lane == 0)
-                    atomicOr(status, kStatusPickFailed);
-                break;
-            }
+        const u32 listed = cap == 0 ? 0 : for_each_successor(T, H, L, lane, [&](u32 k, u32 s) {
             const u64 o = i * cap + k;
             if (lane == 0 && schema)
                 schema[o] = static_cast<i32>(s);
@@ -2410,30 +2499,18 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
                     binding[o * Lw + q] = q < S.arity ? static_cast<i32>(L.ub[q]) : -1;
             if (succ)
             {
+                // the successor on the LDS row (one effect per lane), copied out, then the row restored
+                succ_apply(T, H, L, s, lane, status);
                 u64* dst = succ + o * words;
                 for (u32 q = lane; q < words; q += kWave)
                     dst[q] = q < T.W ? L.row[q] : 0;
-                __threadfence_block();
-                wave_sync();
-                if (lane == 0)
-                {
-                    // delete, then add, on the copy
-                    for (u32 e = S.eff_begin + S.nadd; e < S.eff_end; ++e)
-                    {
-                        const u32 sl = effect_slot(T, L, H.effects[e]);
-                        if (sl != kNone)
-                            dst[sl >> 6] &= ~(u64{1} << (sl & 63));
-                    }
-                    for (u32 e = S.eff_begin; e < S.eff_begin + S.nadd; ++e)
-                    {
-                        const u32 sl = effect_slot(T, L, H.effects[e]);
-                        if (sl != kNone)
-                            dst[sl >> 6] |= u64{1} << (sl & 63);
-                    }
-                }
+                succ_revert(H, L, s, lane);
             }
             wave_sync();
-        }
+            return k + 1 < cap;
+        });
+        if (listed != min(c, cap) && lane == 0)
+            atomicOr(status, kStatusPickFailed);
         wave_sync();
     }
 }
