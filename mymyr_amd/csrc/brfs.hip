@@ -604,6 +604,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     r.status = kExhausted;
     u64 pos = 0;                           // states expanded or passed (the reference's queue position)
     u64 seen_parents = 0, seen_cands = 0;  // counted so far (the successors-per-parent estimate)
+    double new_rate = 1.0;                 // new states per candidate of the last confirmed chunk
     while (!stopped)
     {
         if (pos >= set.size)
@@ -699,6 +700,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
                                         " states of device memory (set max_states or memory_states)");
             tm.bytes(kKCompact, winners * (2 * R + 28));
+            if (pend.m)
+                new_rate = static_cast<double>(winners) / static_cast<double>(pend.m);
             set.size = size_dev;
             row[0] += pend.np;
             row[1] += pend.m;
@@ -775,6 +778,22 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 hip_check(hipMemcpyAsync(b.host + kChunkOff, offsets + lim * S, sizeof(u64), hipMemcpyDeviceToHost, stream), "chunk end");
                 hip_check(hipStreamSynchronize(stream), "sync");
                 end_off = b.host[kChunkOff];
+            }
+            if (bounded && p1 > p0 + 1)
+            {
+                // near the max_states cut, a chunk of about the candidates the store's room needs at the last chunk's
+                // rate of new states (with a margin): the chunk the store fills in then probes few candidates past the
+                // cut (chunk boundaries change no result)
+                const double room = static_cast<double>(o.max_states - set.size);
+                const double want = room / std::max(new_rate, 1.0 / 1024) * 1.25 + 65536.0;
+                if (want < static_cast<double>(end_off - base))
+                {
+                    hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, p1, base + static_cast<u64>(want), small + kChunkP);
+                    launch_check("chunk end");
+                    sync_small();
+                    p1 = b.host[kChunkP];
+                    end_off = b.host[kChunkOff];
+                }
             }
             const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
