@@ -209,6 +209,17 @@ class PaddedExpansion(Structure):
     ]
 
 
+def current_stream() -> int:
+    """torch's current HIP stream on the current device as a raw hipStream_t: torch.cuda.current_stream().cuda_stream
+    without building the Stream object (a few microseconds per call, which a per-step call would pay every step)."""
+    import torch
+
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is None:
+        return torch.cuda.current_stream().cuda_stream
+    return raw(torch._C._cuda_getDevice())
+
+
 def _load() -> ctypes.CDLL:
     # torch-ROCm ships its own libamdhip64.so.7. Loaded first, the library would bind the system's copy and the
     # process would hold two HIP runtimes (torch's then finds no device); with torch imported first, the library

@@ -115,7 +115,7 @@ def _instance_sampler(value: Any, num_instances: int, default_uniform: bool) -> 
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return _lib.current_stream()
 
 
 def _p(t: Optional[Tensor]):

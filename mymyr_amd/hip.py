@@ -12,11 +12,12 @@ import ctypes
 
 import torch
 
+from . import _lib
 from ._lib import check, lib
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return _lib.current_stream()
 
 
 def _require(t: torch.Tensor, name: str, dtype=None, ndim=None) -> None:

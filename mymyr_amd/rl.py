@@ -22,7 +22,7 @@ from .task import Task
 
 
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return _lib.current_stream()
 
 
 def _p(t: torch.Tensor | None):
