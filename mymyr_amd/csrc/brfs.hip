@@ -243,11 +243,12 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_count(const u64* __restr
 }
 
 // (parent, action) records of the successors of parents [first, first + n) at their offsets (candidate index =
-// offsets[t] - cand_base + rank in action order): the parent index relative to `first` in the high 32 bits, the action in
-// the low.
+// offsets[t] - cand_base + rank in action order), 32 bits each: the parent index relative to `first` above the low
+// `abits` bits, which hold the action (the driver keeps a chunk's parents below 2^(32 - abits)).
 template<int W>
 __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
-                                                            const u64* __restrict__ offsets, u64 cand_base, u64* __restrict__ cand_pa)
+                                                            const u64* __restrict__ offsets, u64 cand_base, u32 abits,
+                                                            u32* __restrict__ cand_pa)
 {
     __shared__ u64 Bs[kTW][Slices<W>::kWords];
     const u32 lane = lane_id(), wave = threadIdx.x / kWave;
@@ -259,7 +260,7 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restri
     const u32 t = base + lane;
     const bool valid = t < n;
     u64 k = valid ? offsets[t] - cand_base : 0;
-    const u64 hi = static_cast<u64>(t) << 32;
+    const u32 hi = t << abits;
     for (u32 a0 = 0; a0 < g.num_padded; a0 += 4 * kWave)
     {
         // four groups in flight (num_padded is a multiple of 64; groups past it are empty)
@@ -294,8 +295,11 @@ struct ParentRows
 {
     const u64* arena;
     u64 first;            // arena id of the chunk's first parent (records hold the parent relative to it)
-    const u64* cand_pa;   // (parent << 32) | action
+    const u32* cand_pa;   // (parent << abits) | action
     const u64* masks;     // [actions, 2W]: delete mask, then add mask
+    u32 abits;            // action bits of a record
+    __device__ __forceinline__ u32 parent_of(u32 pa) const { return pa >> abits; }
+    __device__ __forceinline__ u32 action_of(u32 pa) const { return pa & ((1u << abits) - 1); }
     template<int G, int K>
     __device__ __forceinline__ void load(u64 c, u32 q, Slice<G, K>& o) const
     {
@@ -303,10 +307,10 @@ struct ParentRows
     }
     /// The row of the candidate with record pa.
     template<int G, int K>
-    __device__ __forceinline__ void load_pa(u64 pa, u32 q, Slice<G, K>& o) const
+    __device__ __forceinline__ void load_pa(u32 pa, u32 q, Slice<G, K>& o) const
     {
-        const u64* row = arena + (first + (pa >> 32)) * W;
-        const u64* mk = masks + static_cast<u64>(static_cast<u32>(pa)) * (2 * W);
+        const u64* row = arena + (first + parent_of(pa)) * W;
+        const u64* mk = masks + static_cast<u64>(action_of(pa)) * (2 * W);
         Slice<G, K> r, d, a;
         load_row<G, K>(row, W, q, r);
         load_row<G, K>(mk, W, q, d);
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
     // a grid sized for the whole chunk would mostly start waves that find no winner: a bounded grid strides instead
     for (u64 w0 = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G; w0 < winners; w0 += kBatch * stride)
     {
-        u64 pa[kBatch];
+        u32 pa[kBatch];
         bool live[kBatch];
 #pragma unroll
         for (int b = 0; b < kBatch; ++b)
@@ -401,7 +405,7 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
             src.template load_pa<G, K>(pa[b], q, r);
             store_row<G, K>(s.arena + id * W, W, q, r);
             if (q == 0)
-                nodes[id] = ((src.first + (pa[b] >> 32)) << 32) | static_cast<u32>(pa[b]);
+                nodes[id] = ((src.first + src.parent_of(pa[b])) << 32) | src.action_of(pa[b]);
         }
     }
 }
@@ -559,11 +563,16 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             dev_free(s);
         }
     } layer_guard{counts, goal_flags, offsets, scan_scratch};
-    u64* cand_pa = b.alloc<u64>(chunk, "candidate records");
+    // 32-bit candidate records: the action in the low abits bits, the parent relative to the chunk's first above them
+    u32 abits = 1;
+    while ((u64{1} << abits) < g.num_padded)
+        ++abits;
+    const u64 max_chunk_parents = u64{1} << (32 - abits);
+    u32* cand_pa = b.alloc<u32>(chunk, "candidate records");
     u64* small = b.alloc<u64>(kSmall, "scalars");
     // search nodes: per stored state its first discovery (parent id << 32 | ground action); the start state has none
     u64* nodes = b.alloc<u64>(cap_states, "search nodes");
-    r.memory_bytes = set.v.capacity * 8 + cap_states * (R + 8) + chunk * (8 + 8 + 1 + 4) + layer_cap * (S * 4 + 1 + S * 8 + 8);
+    r.memory_bytes = set.v.capacity * 8 + cap_states * (R + 8) + chunk * (4 + 8 + 1 + 4) + layer_cap * (S * 4 + 1 + S * 8 + 8);
     hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
     enum
     {
@@ -663,19 +672,20 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             const u64 room = (bounded ? o.max_states : cap_states) - set.size;
             // insert: every candidate's record, probe entry and slot, the parent rows, and the row each non-winner
             // compared equal to; compaction: per winner its list entry, record, slot, arena row and entry
-            tm.bytes(kKInsert, pend.m * 24 + pend.np * R + (pend.m - std::min(winners, pend.m)) * R);
+            tm.bytes(kKInsert, pend.m * 20 + pend.np * R + (pend.m - std::min(winners, pend.m)) * R);
             tm.bytes(kKRank, pend.m * 9 + winners * 4);
             if (bounded && winners >= room && winners > 0)
             {
                 // the store filled at winner room - 1 (id max_states - 1): the search stops inside its parent's
                 // expansion; the compaction wrote ids below max_states only
-                tm.bytes(kKCompact, room * (2 * R + 28));
+                tm.bytes(kKCompact, room * (2 * R + 24));
                 u32 jc = 0;
                 hip_check(hipMemcpyAsync(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost, stream), "cut");
                 hip_check(hipStreamSynchronize(stream), "sync");
-                hip_check(hipMemcpyAsync(b.host + kCut, cand_pa + jc, sizeof(u64), hipMemcpyDeviceToHost, stream), "parent");
+                u32 rec = 0;
+                hip_check(hipMemcpyAsync(&rec, cand_pa + jc, sizeof(u32), hipMemcpyDeviceToHost, stream), "parent");
                 hip_check(hipStreamSynchronize(stream), "sync");
-                const u64 pc = b.host[kCut] >> 32;  // the parent, relative to the chunk's first
+                const u64 pc = rec >> abits;  // the parent, relative to the chunk's first
                 row[0] += pc + 1;
                 row[1] += u64{jc} + 1;
                 set_small(kGoalSum, 0);
@@ -699,7 +709,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             if (winners > room)
                 throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
                                         " states of device memory (set max_states or memory_states)");
-            tm.bytes(kKCompact, winners * (2 * R + 28));
+            tm.bytes(kKCompact, winners * (2 * R + 24));
             if (pend.m)
                 new_rate = static_cast<double>(winners) / static_cast<double>(pend.m);
             set.size = size_dev;
@@ -741,7 +751,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 tm.end(kKOther, 0);
             }
             // the chunk end over what is counted, and the pending chunk's outcome, in one synchronization
-            hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, std::min(counted + nb, lim), base + chunk, small + kChunkP);
+            hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, S, p0, std::min({counted + nb, lim, p0 + max_chunk_parents}),
+                               base + chunk, small + kChunkP);
             launch_check("chunk end");
             read_state(count_now ? offsets + (counted + nb) * S : nullptr);
             sync_small();
@@ -797,14 +808,14 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             }
             const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
-            const ParentRows<W> src{set.v.arena, layer_begin + p0, cand_pa, d_masks};
+            const ParentRows<W> src{set.v.arena, layer_begin + p0, cand_pa, d_masks, abits};
             if (m > 0)
             {
                 tm.begin(kKEmit);
                 hipLaunchKernelGGL(k_ground_emit<W>, dim3(blocks_for(np, kTW * kWave)), dim3(kTW * kWave), 0, stream, set.v.arena, layer_begin + p0, np, g,
-                                   offsets + p0 * S, base, cand_pa);
+                                   offsets + p0 * S, base, abits, cand_pa);
                 launch_check("ground emit");
-                tm.end(kKEmit, np * (R + 8) + m * 8);
+                tm.end(kKEmit, np * (R + 8) + m * 4);
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
                 hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.flags,
