@@ -505,13 +505,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     const GroundActions& ga = tb.ga;
     BrfsResultC r;
     const auto t0 = Clock::now();
-    hipStream_t stream = nullptr;
-    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "stream");
-    struct StreamGuard
-    {
-        hipStream_t s;
-        ~StreamGuard() { (void)hipStreamDestroy(s); }
-    } sg{stream};
+    hipStream_t stream = thread_stream();
     Timers tm(o.timings != 0, stream, r);
     constexpr u64 R = W * 8;  // row bytes
     Buffers b;
@@ -573,7 +567,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     // search nodes: per stored state its first discovery (parent id << 32 | ground action); the start state has none
     u64* nodes = b.alloc<u64>(cap_states, "search nodes");
     r.memory_bytes = set.v.capacity * 8 + cap_states * (R + 8) + chunk * (4 + 8 + 1 + 4) + layer_cap * (S * 4 + 1 + S * 8 + 8);
-    hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
+    b.host = static_cast<u64*>(pinned_acquire(kSmall * sizeof(u64)));
     enum
     {
         kGoalSum = 0,   // goal states among the layer's expanded parents

@@ -111,8 +111,7 @@ struct Buffers
     {
         for (void* p : owned)
             dev_free(p);
-        if (host)
-            (void)hipHostFree(host);
+        pinned_release(host);
     }
 };
 

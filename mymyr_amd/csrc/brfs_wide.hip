@@ -131,13 +131,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     }
     BrfsResultC r;
     const auto t0 = Clock::now();
-    hipStream_t stream = nullptr;
-    hip_check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "stream");
-    struct StreamGuard
-    {
-        hipStream_t s;
-        ~StreamGuard() { (void)hipStreamDestroy(s); }
-    } sg{stream};
+    hipStream_t stream = thread_stream();
     Timers tm(o.timings != 0, stream, r);
     const u64 R = static_cast<u64>(W) * 8;
     Buffers b;
@@ -163,7 +157,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     u64* nodes = b.alloc<u64>(cap_states, "search nodes");
     u64* small = b.alloc<u64>(kSmall, "scalars");
     u32* xstatus = b.alloc<u32>(2, "expansion status");  // [0] words needed, [1] status
-    hip_check(hipHostMalloc(reinterpret_cast<void**>(&b.host), kSmall * sizeof(u64), hipHostMallocDefault), "pinned");
+    b.host = static_cast<u64*>(pinned_acquire(kSmall * sizeof(u64)));
     // candidate buffers of one chunk (the state set's batch arrays hold as many)
     u64* cand_rows = b.alloc<u64>(chunk * W, "candidate rows");
     i32* cand_parent = b.alloc<i32>(chunk, "candidate parents");

@@ -254,4 +254,48 @@ void event_release(hipEvent_t e)
     std::lock_guard lock(g_event_mutex);
     g_events->push_back(e);
 }
+
+namespace
+{
+constexpr size_t kPinnedBlock = 4096;
+std::mutex g_pinned_mutex;
+std::vector<void*>* g_pinned = new std::vector<void*>();  // never destroyed: blocks live until the process ends
+}  // namespace
+
+void* pinned_acquire(size_t bytes)
+{
+    if (bytes > kPinnedBlock)
+        throw std::invalid_argument("mymyr_amd: pinned scalar blocks hold at most 4 KiB");
+    {
+        std::lock_guard lock(g_pinned_mutex);
+        if (!g_pinned->empty())
+        {
+            void* p = g_pinned->back();
+            g_pinned->pop_back();
+            return p;
+        }
+    }
+    void* p = nullptr;
+    hip_check(hipHostMalloc(&p, kPinnedBlock, hipHostMallocDefault), "pinned block");
+    return p;
+}
+
+void pinned_release(void* p)
+{
+    if (!p)
+        return;
+    std::lock_guard lock(g_pinned_mutex);
+    g_pinned->push_back(p);
+}
+
+hipStream_t thread_stream()
+{
+    thread_local std::unordered_map<int, hipStream_t> streams;
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    hipStream_t& s = streams[dev];
+    if (!s)
+        hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "stream");
+    return s;
+}
 }  // namespace mya

@@ -96,6 +96,15 @@ constexpr size_t scratch_bytes(size_t count)
 hipEvent_t event_acquire();
 void event_release(hipEvent_t e);
 
+/// Pinned host blocks of at most 4 KiB from a process-wide pool (hipHostMalloc once per block, reused): the drivers'
+/// scalar readbacks take one per call without pinning and unpinning host memory each time.
+void* pinned_acquire(size_t bytes);
+void pinned_release(void* p);
+
+/// A non-blocking stream of the current device for the calling thread (created on first use, kept until the process
+/// ends): a synchronous driver runs on it without creating and destroying a stream per call.
+hipStream_t thread_stream();
+
 /// Launch check: the error of the last launch, if any.
 inline void launch_check(const char* what) { hip_check(hipGetLastError(), what); }
 

@@ -273,7 +273,7 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
     s.scan_scratch = dev_alloc<u64>(scan_scratch_words(s.batch_cap), "state set scan scratch");
     s.d_size = dev_alloc<u64>(2, "state set size");
     s.d_status = dev_alloc<u32>(1, "state set status");
-    hip_check(hipHostMalloc(reinterpret_cast<void**>(&s.h_pinned), sizeof(u64) * 4, hipHostMallocDefault), "pinned words");
+    s.h_pinned = static_cast<u64*>(pinned_acquire(sizeof(u64) * 4));
     launch_fill_u32(reinterpret_cast<u32*>(s.flags), (s.batch_cap + 15) / 16 * 4, 0x01010101u, stream);  // flag bytes 1
     state_set_clear(s, stream);
 }
@@ -292,7 +292,7 @@ void state_set_destroy(StateSet& s)
     dev_free(s.d_status);
     dev_free(s.id_of);
     if (s.h_pinned)
-        (void)hipHostFree(s.h_pinned);
+        pinned_release(s.h_pinned);
     s = StateSet{};
 }
 
