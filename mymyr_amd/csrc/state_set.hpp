@@ -6,7 +6,7 @@
 // A batch insert keeps the reference's id rule (include/mymyr/cuda/state_set.hpp:2-18, the CPU stores'
 // first-discovery ids: src/mymyr/search/brfs.cpp:1657-1780): among equal candidates of one batch the smallest
 // candidate index wins (64-bit atomicMin on the pending entry), and new ids follow candidate order (an exclusive scan
-// of the winner flags). The probe hash (set_hash) is the public state hash (hash_state) for rows of at most 32 words
+// of the winner flags). The probe hash (set_hash) is the public state hash (hash_state) for rows of at most 8 words
 // and an order-free sum of mixed words above (set_hash_wide); slot = fastrange of its low 32 bits over the capacity,
 // tag = its high 32 bits, linear probing.
 //

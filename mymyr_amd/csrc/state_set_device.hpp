@@ -5,7 +5,7 @@
 // coalesced request of the whole group, and the group's lanes follow one control path (every branch depends on
 // group-uniform values only).
 //
-// The table hash of rows of at most 32 words is the public hash_state (include/mymyr/core/hash.hpp:38-60) over the
+// The table hash of rows of at most 8 words is the public hash_state (include/mymyr/core/hash.hpp:38-60) over the
 // trimmed words, chained over the pairs in order with the pair broadcast from its lane (wider rows: set_hash_wide);
 // the table probe keeps the reference's id rule (include/mymyr/cuda/state_set.hpp:2-18): among equal candidates the
 // smallest candidate index wins (64-bit atomicMin on the pending entry), new ids follow candidate order.
@@ -189,13 +189,13 @@ __device__ __forceinline__ u64 group_hash(const Slice<G, K>& s, u32 q, u32 gbase
 }
 
 /// Rows wider than this many words are placed in the table by set_hash_wide instead of hash_state.
-constexpr u32 kWideHashWords = 32;
+constexpr u32 kWideHashWords = 8;
 
 /// The table hash of rows wider than kWideHashWords words: mix64 of the seed xor the sum over the row's nonzero words w
 /// of mix64(word + (w + 1) * phi). A row's table slot and tag only place it (ids follow candidate order, and the public
 /// state hash has its own kernels), so wide rows take this order-free sum, which the lanes of a group add up in
-/// parallel, instead of hash_state's chain of one dependent multiply-fold per word pair. Trailing zero words add
-/// nothing, as in hash_state.
+/// parallel, instead of hash_state's chain of one dependent multiply-fold per word pair with a cross-lane broadcast
+/// each. Trailing zero words add nothing, as in hash_state.
 MYA_HD inline u64 set_hash_wide(const u64* w, u32 n)
 {
     u64 acc = 0;
@@ -208,11 +208,21 @@ MYA_HD inline u64 set_hash_wide(const u64* w, u32 n)
 /// The table hash of a row of `words` words (host side of group_set_hash).
 MYA_HD inline u64 set_hash(const u64* w, u32 words) { return words > kWideHashWords ? set_hash_wide(w, words) : hash_state(w, words); }
 
-/// set_hash of the group's row (group-uniform): set_hash_wide for the 64-lane groups of rows above 32 words.
+template<int G>
+__device__ __forceinline__ u64 group_sum64(u64 v)
+{
+#pragma unroll
+    for (int d = 1; d < G; d <<= 1)
+        v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+/// set_hash of the group's row (group-uniform): set_hash_wide for the groups of rows above 8 words (the lanes' sums
+/// added across the group), hash_state below.
 template<int G, int K>
 __device__ __forceinline__ u64 group_set_hash(const Slice<G, K>& s, u32 q, u32 gbase)
 {
-    if constexpr (G == kWave)
+    if constexpr (G * K * 2 > kWideHashWords)
     {
         u64 acc = 0;
 #pragma unroll
@@ -224,7 +234,7 @@ __device__ __forceinline__ u64 group_set_hash(const Slice<G, K>& s, u32 q, u32 g
             if (s.hi[k])
                 acc += mix64(s.hi[k] + (w + 2) * 0x9E3779B97F4A7C15ull);
         }
-        return mix64(wave_sum64(acc) ^ kHashSeed);
+        return mix64(group_sum64<G>(acc) ^ kHashSeed);
     }
     else
         return group_hash<G, K>(s, q, gbase);
