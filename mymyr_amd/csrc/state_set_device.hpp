@@ -258,53 +258,121 @@ __device__ __forceinline__ ProbeResult probe_insert(const StateSetView& s, const
 {
     const u64 tag = h >> 32;
     const u64 mine = (tag << 32) | cand_code(s.epoch, j);
-    u64 slot = slot_of_hash(h, s.capacity);
-    for (u64 probes = 0; probes < s.capacity; ++probes)
+    // groups of 4 lanes or more load 4 consecutive entries per round (lane q: slot + q) and examine them in probe order,
+    // so a probe that crosses occupied entries waits for one load per 4 of them; smaller groups load one at a time (their
+    // probes are decided at the first entry often enough that more loads cost more)
+    if constexpr (G < 4)
     {
-        u64 e = q == 0 ? load_entry(s.table + slot) : 0;
-        e = group_bcast<G>(e, gbase, 0);
-        if (e == 0)
+        u64 slot = slot_of_hash(h, s.capacity);
+        for (u64 probes = 0; probes < s.capacity; ++probes)
         {
-            u64 old = 0;
-            if (q == 0)
-                old = atomicCAS(reinterpret_cast<unsigned long long*>(s.table + slot), 0ull, static_cast<unsigned long long>(mine));
-            old = group_bcast<G>(old, gbase, 0);
-            if (old == 0)
-                return {(tag << 32) | slot, false};
-            e = old;
-        }
-        if ((e >> 32) == tag)
-        {
-            // a pending entry holds a candidate of this batch (its row comes from the row source); any other entry a
-            // stored state (its row is in the arena; an id past the arena was cut by a capacity overflow and matches
-            // nothing)
-            const u32 code = static_cast<u32>(e);
-            const bool pending = (code & kPending) && code_epoch(code) == s.epoch;
-            const u64 id = pending ? 0 : committed_id(s, code);
-            Slice<G, K> o;
-            if (pending)
-                src.load(code & kJMask, q, o);
-            else if (id < s.max_rows)
-                load_row<G, K>(s.arena + id * s.words, s.words, q, o);
-            if ((pending || id < s.max_rows) && group_equal<G, K>(me, o, gbase))
+            u64 e = q == 0 ? load_entry(s.table + slot) : 0;
+            e = group_bcast<G>(e, gbase, 0);
+            if (e == 0)
             {
-                if (!pending)
-                    return {(id << 32) | kNoSlot, true};
-                // a smaller candidate holding the entry already makes this one lose without an atomic (a pending
-                // entry only ever decreases, so a stale read shows a value at least as large as the current one)
-                if ((code & kJMask) < j)
-                    return {(tag << 32) | slot, true};
                 u64 old = 0;
                 if (q == 0)
-                    old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
+                    old = atomicCAS(reinterpret_cast<unsigned long long*>(s.table + slot), 0ull, static_cast<unsigned long long>(mine));
                 old = group_bcast<G>(old, gbase, 0);
-                const u64 other = static_cast<u32>(old) & kJMask;
-                if (other > j && q == 0)
-                    flags[other] = 0;
-                return {(tag << 32) | slot, other < j};
+                if (old == 0)
+                    return {(tag << 32) | slot, false};
+                e = old;
             }
+            if ((e >> 32) == tag)
+            {
+                // a pending entry holds a candidate of this batch (its row comes from the row source); any other entry a
+                // stored state (its row is in the arena; an id past the arena was cut by a capacity overflow and matches
+                // nothing)
+                const u32 code = static_cast<u32>(e);
+                const bool pending = (code & kPending) && code_epoch(code) == s.epoch;
+                const u64 id = pending ? 0 : committed_id(s, code);
+                Slice<G, K> o;
+                if (pending)
+                    src.load(code & kJMask, q, o);
+                else if (id < s.max_rows)
+                    load_row<G, K>(s.arena + id * s.words, s.words, q, o);
+                if ((pending || id < s.max_rows) && group_equal<G, K>(me, o, gbase))
+                {
+                    if (!pending)
+                        return {(id << 32) | kNoSlot, true};
+                    // a smaller candidate holding the entry already makes this one lose without an atomic (a pending
+                    // entry only ever decreases, so a stale read shows a value at least as large as the current one)
+                    if ((code & kJMask) < j)
+                        return {(tag << 32) | slot, true};
+                    u64 old = 0;
+                    if (q == 0)
+                        old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
+                    old = group_bcast<G>(old, gbase, 0);
+                    const u64 other = static_cast<u32>(old) & kJMask;
+                    if (other > j && q == 0)
+                        flags[other] = 0;
+                    return {(tag << 32) | slot, other < j};
+                }
+            }
+            slot = slot + 1 == s.capacity ? 0 : slot + 1;
         }
-        slot = slot + 1 == s.capacity ? 0 : slot + 1;
+    }
+    else
+    {
+        constexpr int P = 4;
+        u64 base = slot_of_hash(h, s.capacity);
+        for (u64 probes = 0; probes < s.capacity; probes += P)
+        {
+            u64 mine_e = 0;
+            if (q < P)
+            {
+                const u64 sq = base + q >= s.capacity ? base + q - s.capacity : base + q;
+                mine_e = load_entry(s.table + sq);
+            }
+    #pragma unroll
+            for (int r = 0; r < P; ++r)
+            {
+                const u64 slot = base + r >= s.capacity ? base + r - s.capacity : base + r;
+                u64 e = group_bcast<G>(mine_e, gbase, r);
+                if (e == 0)
+                {
+                    u64 old = 0;
+                    if (q == 0)
+                        old = atomicCAS(reinterpret_cast<unsigned long long*>(s.table + slot), 0ull, static_cast<unsigned long long>(mine));
+                    old = group_bcast<G>(old, gbase, 0);
+                    if (old == 0)
+                        return {(tag << 32) | slot, false};
+                    e = old;
+                }
+                if ((e >> 32) == tag)
+                {
+                    // a pending entry holds a candidate of this batch (its row comes from the row source); any other entry
+                    // a stored state (its row is in the arena; an id past the arena was cut by a capacity overflow and
+                    // matches nothing)
+                    const u32 code = static_cast<u32>(e);
+                    const bool pending = (code & kPending) && code_epoch(code) == s.epoch;
+                    const u64 id = pending ? 0 : committed_id(s, code);
+                    Slice<G, K> o;
+                    if (pending)
+                        src.load(code & kJMask, q, o);
+                    else if (id < s.max_rows)
+                        load_row<G, K>(s.arena + id * s.words, s.words, q, o);
+                    if ((pending || id < s.max_rows) && group_equal<G, K>(me, o, gbase))
+                    {
+                        if (!pending)
+                            return {(id << 32) | kNoSlot, true};
+                        // a smaller candidate holding the entry already makes this one lose without an atomic (a pending
+                        // entry only ever decreases, so a stale read shows a value at least as large as the current one)
+                        if ((code & kJMask) < j)
+                            return {(tag << 32) | slot, true};
+                        u64 old = 0;
+                        if (q == 0)
+                            old = atomicMin(reinterpret_cast<unsigned long long*>(s.table + slot), static_cast<unsigned long long>(mine));
+                        old = group_bcast<G>(old, gbase, 0);
+                        const u64 other = static_cast<u32>(old) & kJMask;
+                        if (other > j && q == 0)
+                            flags[other] = 0;
+                        return {(tag << 32) | slot, other < j};
+                    }
+                }
+            }
+            base = base + P >= s.capacity ? base + P - s.capacity : base + P;
+        }
     }
     if (q == 0)
         atomicOr(status, kStatusTableFull);
