@@ -32,15 +32,21 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 14
+#define MYA_ABI_VERSION 15
 int mya_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
 
-/* Atom slot modes (reference TaskOptions::Atoms, include/mymyr/task/task.hpp:88-101). */
+/* Atom slot modes (reference TaskOptions::Atoms, include/mymyr/task/task.hpp:88-104). Lazy slots
+ * (include/mymyr/task/atom_index.hpp:19-22) start with the initial state's atoms, in its atom order; the device BrFS,
+ * mya_expand, mya_expand_noalloc and mya_successors give the atoms their successors add without a slot the next
+ * slots, in ascending canonical id, between device launches (include/mymyr/cuda/generator.hpp:20-24), so a lazy
+ * task's words and fluent_slots grow with use. Such calls on one lazy task run one at a time. Environments and task
+ * tables refuse lazy tasks, as the reference's TaskTable does (src/mymyr/rl/task_table.cpp:120-123). */
 #define MYA_ATOMS_AUTO 0
 #define MYA_ATOMS_REACHABLE 1
 #define MYA_ATOMS_DENSE 2
+#define MYA_ATOMS_LAZY 3
 
 /* Loads a task from the reference's text format (replaces Task::from_text_file / Task::create over
  * read_task_text, include/mymyr/task/task.hpp:166-167, include/mymyr/formalism/text_format.hpp:23-24).
@@ -51,14 +57,14 @@ void mya_task_free(mya_task* task);
 
 typedef struct mya_task_info
 {
-    uint32_t words;         /* state words W (Task::words(), at least 1) */
-    uint32_t fluent_slots;  /* atom slots */
-    uint32_t atom_mode;     /* 0 reachable, 1 dense (AtomMode) */
+    uint32_t words;         /* state words W (Task::words(), at least 1; lazy slots: the current width) */
+    uint32_t fluent_slots;  /* atom slots (lazy slots: those assigned so far) */
+    uint32_t atom_mode;     /* 0 reachable, 1 dense, 2 lazy (AtomMode) */
     uint32_t num_schemas;
     uint32_t label_width;   /* largest schema arity */
     uint32_t num_objects;
     uint32_t max_arity;     /* largest fluent predicate arity */
-    uint32_t goal_unsat;    /* the goal can never hold */
+    uint32_t goal_unsat;    /* no state is a goal under the current slots */
     uint64_t dense_fluent;  /* size of the typed-dense canonical fluent space */
     uint64_t reachable_fluent; /* relaxed-reachable fluent atoms (0 when not computed: dense option) */
     uint32_t view_words;    /* per-state device view size in u64 words */
@@ -69,7 +75,8 @@ int mya_task_info_get(const mya_task* task, mya_task_info* out);
 
 /* Slot records: rec [fluent_slots, 1 + max(1, max_arity)] u32 = predicate then arguments (zero padded);
  * cid [fluent_slots] u64 canonical ids (AtomIndex::record / canonical, include/mymyr/task/atom_index.hpp:167-172).
- * Either may be null. */
+ * Either may be null. Lazy slots: fluent_slots as mya_task_info_get last reported it, with no call that interns
+ * between the two. */
 int mya_task_slots(const mya_task* task, uint32_t* rec, uint64_t* cid);
 
 /* The initial state, zero padded to `words` (>= the task's words). Host memory. */

@@ -970,9 +970,15 @@ BrfsResultC run_cached(const CompiledTask& task, const BrfsOptionsC& o, std::vec
 }  // namespace
 
 BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts, BrfsCache* cache,
-                        const TaskDev* dev)
+                        const TaskDev* dev, const LazyResolve* lazy)
 {
     const u32 W = task.words;
+    if (lazy)
+    {
+        if (!dev)
+            throw std::invalid_argument("mymyr_amd: brfs: a task with lazy slots needs its device tables");
+        return brfs_wide(task, *dev, o, layer_counts, lazy);
+    }
     if (W <= 1)
         return run_cached<1>(task, o, layer_counts, cache);
     if (W <= 2)

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <array>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <vector>
@@ -97,12 +98,30 @@ struct BrfsCache
 
 struct TaskDev;
 
-/// Rows of at most 16 words: over the ground actions (brfs.hip). Wider rows: over the lifted expansion (brfs_wide.hip),
-/// which needs the task's device tables `dev`.
-BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts,
-                        BrfsCache* cache = nullptr, const TaskDev* dev = nullptr);
+/// Lazy slots: interns the atoms the successor kernels recorded without a slot, brings the task's device image up to
+/// date and stores its new pointer table in *T; returns whether any atom was interned.
+using LazyResolve = std::function<bool(hipStream_t, TaskDev*)>;
 
-/// The BrFS of a task with rows wider than 16 words over the lifted expansion (witness pruning only for tasks without
-/// witness parameters).
-BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts);
+/// Rows of at most 16 words: over the ground actions (brfs.hip). Wider rows, and tasks with lazy slots (`lazy` set):
+/// over the lifted expansion (brfs_wide.hip), which needs the task's device tables `dev`.
+BrfsResultC brfs_device(const CompiledTask& task, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts,
+                        BrfsCache* cache = nullptr, const TaskDev* dev = nullptr, const LazyResolve* lazy = nullptr);
+
+/// The BrFS over the lifted expansion (witness pruning only for tasks without witness parameters). With lazy slots the
+/// rows start at the task's current width (rounded up: lazy_row_words) and are widened, the stored states moved to
+/// a set of the new width, when interned atoms outgrow them.
+BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& layer_counts,
+                      const LazyResolve* lazy = nullptr);
+
+/// Row words of a search over a task with lazy slots whose states have `words` words: powers of two through 64 words,
+/// then whole multiples of 64 (the reference's arena buckets, cuda/src/brfs.cpp:33-34).
+inline u32 lazy_row_words(u32 words)
+{
+    if (words > 64)
+        return (words + 63) / 64 * 64;
+    u32 w = 1;
+    while (w < words)
+        w *= 2;
+    return w;
+}
 }  // namespace mya

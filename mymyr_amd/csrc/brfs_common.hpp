@@ -107,6 +107,15 @@ struct Buffers
         owned.push_back(p);
         return p;
     }
+    /// Frees one buffer of alloc() before the others (stream-ordered, as dev_free).
+    void release(void* p)
+    {
+        const auto it = std::find(owned.begin(), owned.end(), p);
+        if (it == owned.end())
+            return;
+        owned.erase(it);
+        dev_free(p);
+    }
     ~Buffers()
     {
         for (void* p : owned)

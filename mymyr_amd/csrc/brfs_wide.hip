@@ -86,6 +86,17 @@ __global__ __launch_bounds__(kWB) void k_wide_compact(StateSetView s, const u64*
 
 __global__ void k_read_u32(const u32* __restrict__ src, u64* __restrict__ dst) { *dst = *src; }
 
+/// Rows [n, sw] into rows [n, dw] (dw >= sw), zero-padded.
+__global__ void k_relayout(const u64* __restrict__ src, u32 sw, u64* __restrict__ dst, u32 dw, u64 n)
+{
+    for (u64 t = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; t < n * dw; t += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        const u64 i = t / dw;
+        const u32 w = static_cast<u32>(t - i * dw);
+        dst[t] = w < sw ? src[i * sw + w] : 0;
+    }
+}
+
 /// Whether the task's goal holds in a row (host; the compiled goal lists).
 bool goal_holds(const CompiledTask& task, const std::vector<u64>& row)
 {
@@ -118,9 +129,12 @@ std::string witness_schema(const CompiledTask& task)
 }
 }  // namespace
 
-BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc)
+BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc,
+                      const LazyResolve* lazy)
 {
-    const u32 W = task.words;
+    TaskDev T = dev;  // lazy slots: refreshed after each interning
+    const u32 TW0 = task.words;  // the width of the start and blocked rows
+    u32 W = lazy ? lazy_row_words(TW0) : TW0;
     if (o.witness_pruning)
     {
         const std::string ws = witness_schema(task);
@@ -133,15 +147,19 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     const auto t0 = Clock::now();
     hipStream_t stream = thread_stream();
     Timers tm(o.timings != 0, stream, r);
-    const u64 R = static_cast<u64>(W) * 8;
+    u64 R = static_cast<u64>(W) * 8;
     Buffers b;
     const bool bounded = o.max_states != ~u64{0};
-    // unbounded searches: an arena of at most 32 GiB by default
+    // unbounded searches: an arena of at most 32 GiB by default (lazy slots: for rows of the task's largest width)
+    const u64 R_max = lazy ? static_cast<u64>(lazy_row_words(words_for(task.layout.fluent_count))) * 8 : R;
     const u64 cap_states = bounded ? std::max<u64>(1, o.max_states)
-                                   : (o.memory_states ? o.memory_states : std::min<u64>(u64{1} << 26, (u64{32} << 30) / R));
+                                   : (o.memory_states ? o.memory_states : std::min<u64>(u64{1} << 26, (u64{32} << 30) / R_max));
     // candidate rows per chunk: about 4 GiB of them by default
-    u64 chunk = o.chunk ? o.chunk : std::clamp<u64>((u64{4} << 30) / R, u64{1} << 12, u64{1} << 22);
-    chunk = std::min<u64>(chunk, kMaxBatch - 1);
+    auto chunk_for = [&](u64 row_bytes) {
+        const u64 c = o.chunk ? o.chunk : std::clamp<u64>((u64{4} << 30) / row_bytes, u64{1} << 12, u64{1} << 22);
+        return std::min<u64>(c, kMaxBatch - 1);
+    };
+    u64 chunk = chunk_for(R);
     StateSet set;
     state_set_create(set, cap_states, W, 0.5, chunk, stream, chunk);
     struct SetGuard
@@ -163,7 +181,8 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     i32* cand_parent = b.alloc<i32>(chunk, "candidate parents");
     i32* cand_index = b.alloc<i32>(chunk, "candidate indices");
     u8* cand_goal = b.alloc<u8>(chunk, "candidate goal flags");
-    r.memory_bytes = set.v.capacity * 8 + cap_states * (R + 8 + 1) + layer_cap * (4 + 8 + 8) + chunk * (R + 4 + 4 + 1 + 1 + 4);
+    auto memory_bytes = [&] { return set.v.capacity * 8 + cap_states * (R + 8 + 1) + layer_cap * (4 + 8 + 8) + chunk * (R + 4 + 4 + 1 + 1 + 4); };
+    r.memory_bytes = memory_bytes();
     enum
     {
         kFirstGoal = 0,
@@ -196,7 +215,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
             throw std::length_error("mymyr_amd: brfs: state table full");
     };
     launch_fill_u32(xstatus, 2, 0, stream);
-    const BlockedView blocked = upload_blocked(o.blocked, task.words, W, chunk, b, stream);
+    BlockedView blocked = upload_blocked(o.blocked, TW0, W, chunk, b, stream);
     // the start state (stored even if blocked)
     {
         const std::vector<u64> s0 = start_row(task, o, W);
@@ -216,6 +235,36 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
     base_args.label_width = 0;
     base_args.status = xstatus + 1;
     base_args.words_needed = xstatus;
+    // lazy slots: the stored states move to a set of rows of nw words in id order (so their ids stay), a chunk at a
+    // time through new candidate rows of that width; the blocked table follows the width
+    auto widen = [&](u32 nw) {
+        const u64 nchunk = chunk_for(static_cast<u64>(nw) * 8);
+        u64* rows = b.alloc<u64>(nchunk * nw, "candidate rows");
+        StateSet grown;
+        state_set_create(grown, cap_states, nw, 0.5, nchunk, stream, nchunk);
+        for (u64 i = 0; i < set.size; i += nchunk)
+        {
+            const u64 k = std::min(nchunk, set.size - i);
+            hipLaunchKernelGGL(k_relayout, dim3(std::min<u64>(blocks_for(k * nw, 256), 4096)), dim3(256), 0, stream, set.v.arena + i * W, W,
+                               rows, nw, k);
+            launch_check("relayout");
+            u64 nn = 0;
+            state_set_insert(grown, rows, k, nullptr, nullptr, &nn, stream);
+            if (nn != k)
+                throw std::logic_error("mymyr_amd: brfs: stored states merged when their rows were widened");
+        }
+        state_set_destroy(set);
+        set = grown;
+        b.release(cand_rows);
+        cand_rows = rows;
+        W = nw;
+        R = static_cast<u64>(nw) * 8;
+        chunk = nchunk;
+        blocked = upload_blocked(o.blocked, TW0, W, chunk, b, stream);
+        base_args.words = W;
+        base_args.out_words = W;
+        r.memory_bytes = std::max(r.memory_bytes, memory_bytes());
+    };
     const auto td0 = Clock::now();
     Halt halt(o, t0);
     bool stopped = false, budget_stopped = false;
@@ -306,6 +355,23 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
                 e.counts = counts + p0;
                 launch_expand(e, stream);
                 tm.end(kKEmit, (p1 - p0) * R + m * (R + 9));
+                if (lazy)
+                {
+                    // added atoms without a slot: intern them (ascending canonical id), widen the rows if the task's
+                    // rows outgrew them, and expand the chunk again (nothing of it is stored yet)
+                    read_state(nullptr);
+                    sync_small();
+                    if (b.host[kXStatus] & kStatusNoSlot)
+                    {
+                        launch_fill_u32(xstatus, 2, 0, stream);
+                        if (!(*lazy)(stream, &T))
+                            throw std::logic_error("mymyr_amd: brfs: an added atom without a slot was not recorded");
+                        base_args.T = T;
+                        if (lazy_row_words(task.words) > W)
+                            widen(lazy_row_words(task.words));
+                        continue;
+                    }
+                }
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
                 state_set_probe(set, cand_rows, m, stream, blocked.capacity ? &blocked : nullptr);
@@ -489,8 +555,9 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& T, const BrfsOpti
             r.plan_binding.insert(r.plan_binding.end(), lab.begin() + 1, lab.end());
         }
         r.cost = static_cast<double>(rev.size());
-        r.goal_state.resize(W);
-        hip_check(hipMemcpy(r.goal_state.data(), set.v.arena + static_cast<u64>(r.first_goal) * W, R, hipMemcpyDeviceToHost), "goal state");
+        r.goal_state.resize(task.words);
+        hip_check(hipMemcpy(r.goal_state.data(), set.v.arena + static_cast<u64>(r.first_goal) * W, task.words * sizeof(u64),
+                            hipMemcpyDeviceToHost), "goal state");
     }
     r.search_s = std::chrono::duration<double>(Clock::now() - t0).count();
     return r;

@@ -34,8 +34,41 @@ const DeviceTask& device_task(mya_task* t)
         t->dev.device = dev;
         t->dev.words = img.size();
         t->dev.thost = std::make_unique<TaskDev>(task_dev(t->dev.image, t->compiled->header()));
+        if (t->compiled->mode == AtomMode::Lazy)
+        {
+            const u64 nw = std::max<u64>(1, words_for(t->compiled->layout.fluent_count));
+            t->dev.missing = dev_alloc<u64>(nw, "lazy slot bitmap");
+            hip_check(hipMemset(t->dev.missing, 0, nw * sizeof(u64)), "lazy slot bitmap");
+            t->dev.thost->missing = t->dev.missing;
+        }
     }
     return t->dev;
+}
+
+bool resolve_missing(mya_task* t, hipStream_t s)
+{
+    const DeviceTask& d = device_task(t);
+    std::lock_guard lock(t->mutex);
+    CompiledTask& C = *t->compiled;
+    const u64 nw = std::max<u64>(1, words_for(C.layout.fluent_count));
+    std::vector<u64> bits(nw);
+    hip_check(hipMemcpyAsync(bits.data(), d.missing, nw * sizeof(u64), hipMemcpyDeviceToHost, s), "lazy slot bitmap");
+    hip_check(hipStreamSynchronize(s), "lazy slot bitmap");
+    std::vector<u64> cids;
+    for (u64 w = 0; w < nw; ++w)
+        for (u64 x = bits[w]; x; x &= x - 1)
+            cids.push_back(w * 64 + static_cast<u64>(__builtin_ctzll(x)));
+    if (cids.empty())
+        return false;
+    launch_fill_u32(reinterpret_cast<u32*>(d.missing), 2 * nw, 0, s);
+    const auto ranges = intern_atoms(C, cids);
+    for (const auto& [a, b] : ranges)
+        if (b > a)
+            hip_check(hipMemcpyAsync(d.image + a, C.image.data() + a, (b - a) * sizeof(u64), hipMemcpyHostToDevice, s), "task image");
+    hip_check(hipStreamSynchronize(s), "task image");
+    *t->dev.thost = task_dev(d.image, C.header());
+    t->dev.thost->missing = d.missing;
+    return true;
 }
 }  // namespace mya
 
@@ -52,8 +85,8 @@ int mya_task_load_text(const char* text, size_t len, int atoms, mya_task** out)
     return guarded([&] {
         if (!text || !out)
             throw std::invalid_argument("mymyr_amd: task_load_text: null argument");
-        if (atoms < 0 || atoms > 2)
-            throw std::invalid_argument("mymyr_amd: task_load_text: atoms must be 0 (auto), 1 (reachable) or 2 (dense)");
+        if (atoms < 0 || atoms > 3)
+            throw std::invalid_argument("mymyr_amd: task_load_text: atoms must be 0 (auto), 1 (reachable), 2 (dense) or 3 (lazy)");
         auto t = std::make_unique<mya_task>();
         t->compiled = compile_task(parse_task_text(std::string_view(text, len)), static_cast<AtomsOption>(atoms));
         *out = t.release();
@@ -81,6 +114,7 @@ void mya_task_free(mya_task* task)
     if (!task)
         return;
     dev_free(task->dev.image);
+    dev_free(task->dev.missing);
     delete task;
 }
 
@@ -89,6 +123,7 @@ int mya_task_info_get(const mya_task* task, mya_task_info* out)
     return guarded([&] {
         if (!task || !out)
             throw std::invalid_argument("mymyr_amd: task_info: null argument");
+        std::lock_guard lock(const_cast<mya_task*>(task)->mutex);  // lazy slots change words and fluent_slots
         const CompiledTask& c = *task->compiled;
         std::memset(out, 0, sizeof(*out));
         out->words = c.words;
@@ -114,6 +149,7 @@ int mya_task_slots(const mya_task* task, uint32_t* rec, uint64_t* cid)
     return guarded([&] {
         if (!task)
             throw std::invalid_argument("mymyr_amd: task_slots: null task");
+        std::lock_guard lock(const_cast<mya_task*>(task)->mutex);
         const CompiledTask& c = *task->compiled;
         u32 ma = 0;
         for (const auto& p : c.text.preds)
@@ -152,6 +188,7 @@ int mya_task_initial(const mya_task* task, uint64_t* row, uint32_t words)
     return guarded([&] {
         if (!task || !row)
             throw std::invalid_argument("mymyr_amd: task_initial: null argument");
+        std::lock_guard lock(const_cast<mya_task*>(task)->mutex);
         const CompiledTask& c = *task->compiled;
         if (words < c.words)
             throw std::invalid_argument("mymyr_amd: task_initial: rows of " + std::to_string(words) + " words; the task needs " +
@@ -268,6 +305,18 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
     const int rc = guarded([&] {
         if (!task || !options || !result)
             throw std::invalid_argument("mymyr_amd: brfs: null argument");
+        // lazy slots: the search interns atoms into the task; it holds the task for its whole run
+        std::unique_lock<std::mutex> lazy_lock;
+        LazyResolve resolve;
+        if (lazy_task(task))
+        {
+            lazy_lock = std::unique_lock<std::mutex>(task->lazy_mutex);
+            resolve = [task](hipStream_t s, TaskDev* T) {
+                const bool any = resolve_missing(task, s);
+                *T = *device_task(task).thost;
+                return any;
+            };
+        }
         BrfsOptionsC o;
         o.max_depth = options->max_depth;
         o.witness_pruning = options->witness_pruning;
@@ -293,14 +342,18 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         o.cancel = options->cancel;
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
-        if (o.stop_at_goal && task->compiled->goal_unsat)
+        if (o.stop_at_goal && task->compiled->goal_fixed_unsat)
         {
-            // no state is a goal: the start state alone, nothing expanded (brfs.cpp:1864-1876)
+            // the goal fails in every state: the start state alone, nothing expanded (brfs.cpp:1851-1861)
             r.status = kUnsolvable;
             r.states = 1;
         }
         else
-            r = brfs_device(*task->compiled, o, lc, &task->brfs, task->compiled->words > 16 ? device_task(task).thost.get() : nullptr);
+        {
+            const bool lifted = resolve || task->compiled->words > 16;
+            r = brfs_device(*task->compiled, o, lc, &task->brfs, lifted ? device_task(task).thost.get() : nullptr,
+                            resolve ? &resolve : nullptr);
+        }
         std::memset(result, 0, sizeof(*result));
         result->status = r.status;
         result->solved = r.solved;

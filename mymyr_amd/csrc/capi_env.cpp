@@ -240,7 +240,7 @@ ExpandScratch carve_expand_scratch(void* block, u64 n)
 /// scratch and the rows' task ids). `block` (device, at least expand_scratch_bytes(max(rows, 1)) bytes) holds the
 /// expansion's scratch; the call synchronizes the stream before it returns, so the block is free again then.
 void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const int32_t* task_ids, const uint64_t* states, uint64_t rows,
-                 uint32_t words, const mya_expand_options* options, mya_expansion* out, hipStream_t stream, void* block)
+                 uint32_t words, const mya_expand_options* options, mya_expansion* out, hipStream_t stream, void* block, mya_task* lazy)
 {
     {
         if (!options || !out || (rows && !states))
@@ -256,7 +256,8 @@ void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const in
         constexpr u64 kMaxRows = (u64{1} << 31) - 1;
         if (rows > kMaxRows)
             throw std::invalid_argument("mymyr: expand: more than 2^31 - 1 states in one batch");
-        if (words < T.W)
+        // lazy slots: rows narrower than the task's current width hold no atom past them (src/mymyr/rl/expand.cpp:53)
+        if (words < T.W && !lazy)
             throw std::invalid_argument("mymyr: expand: state rows of " + std::to_string(words) + " words; the task needs " +
                                         std::to_string(T.W));
         if (out->binding && out->label_width < T.label_width)
@@ -368,6 +369,18 @@ void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const in
         }
         hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
         hip_check(hipStreamSynchronize(stream), "expand");
+        // lazy slots: successors that added atoms without a slot are written again once those atoms are interned
+        // (ascending canonical id; a row past `words` then counts in words_needed)
+        while (lazy && (st[1] & kStatusNoSlot))
+        {
+            if (!resolve_missing(lazy, stream))
+                throw std::logic_error("mymyr_amd: expand: an added atom without a slot was not recorded");
+            a.T = *device_task(lazy).thost;
+            launch_fill_u32(words_status, 2, 0, stream);
+            launch(a);
+            hip_check(hipMemcpyAsync(st, words_status, sizeof(st), hipMemcpyDeviceToHost, stream), "expand status");
+            hip_check(hipStreamSynchronize(stream), "expand");
+        }
         if (st[1] & ~kStatusWideRow)
             throw std::runtime_error("mymyr_amd: expand: device status " + std::to_string(st[1]));
         out->words_needed = st[0];
@@ -391,6 +404,11 @@ void create_env(mya_task* const* tasks, uint32_t count, const mya_env_config* co
         for (u32 i = 0; i < count; ++i)
             if (!tasks[i])
                 throw std::invalid_argument("mymyr: TaskTable: instance " + std::to_string(i) + " is null");
+            else if (lazy_task(tasks[i]))
+                // the reference's table refusal (src/mymyr/rl/task_table.cpp:120-123)
+                throw std::invalid_argument("mymyr: TaskTable: instance " + std::to_string(i) +
+                                            " has lazy atom slots, numbered in the order searches meet its atoms; the rows of a table "
+                                            "need a fixed slot layout (atoms 'auto', 'reachable' or 'dense')");
         for (u32 i = 1; one_domain && i < count; ++i)
         {
             const std::string why = domain_mismatch(tasks[0]->compiled->text, tasks[i]->compiled->text);
@@ -880,18 +898,32 @@ int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32
             throw std::invalid_argument("mymyr_amd: successors: null argument");
         if (cap < 0)
             throw std::invalid_argument("mymyr_amd: successors: negative cap");
+        std::unique_lock<std::mutex> lazy_lock;
+        if (lazy_task(task))
+            lazy_lock = std::unique_lock<std::mutex>(task->lazy_mutex);
         const DeviceTask& d = device_task(task);
-        const TaskDev& T = *d.thost;
-        if (words < T.W)
+        if (words < d.thost->W && !lazy_task(task))
             throw std::invalid_argument("mymyr_amd: successors: rows of " + std::to_string(words) + " words; the task needs " +
-                                        std::to_string(T.W));
+                                        std::to_string(d.thost->W));
+        const hipStream_t s = static_cast<hipStream_t>(stream);
         ScratchLease lease(scratch_bytes<u32>(1), "successors status");
         u32* st = lease.take<u32>(1);
-        launch_fill_u32(st, 1, 0, static_cast<hipStream_t>(stream));
-        launch_successors(T, states, rows, words, static_cast<u32>(cap), count, schema, binding, succ, st, static_cast<hipStream_t>(stream));
         u32 hs = 0;
-        hip_check(hipMemcpyAsync(&hs, st, sizeof(u32), hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream)), "status");
-        hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "successors");
+        for (;;)
+        {
+            launch_fill_u32(st, 1, 0, s);
+            launch_successors(*d.thost, states, rows, words, static_cast<u32>(cap), count, schema, binding, succ, st, s);
+            hip_check(hipMemcpyAsync(&hs, st, sizeof(u32), hipMemcpyDeviceToHost, s), "status");
+            hip_check(hipStreamSynchronize(s), "successors");
+            // lazy slots: the listing again once the added atoms without a slot are interned
+            if (!(lazy_task(task) && (hs & kStatusNoSlot) && succ))
+                break;
+            if (!resolve_missing(task, s))
+                throw std::logic_error("mymyr_amd: successors: an added atom without a slot was not recorded");
+        }
+        if (hs & kStatusWideRow)
+            throw std::invalid_argument("mymyr: successors: a successor has atoms past the rows' " + std::to_string(words) +
+                                        " words (the task's lazy slots now need " + std::to_string(d.thost->W) + ")");
         if (hs)
             throw std::runtime_error("mymyr_amd: successors: device status " + std::to_string(hs));
     });
@@ -903,9 +935,13 @@ int mya_expand(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t w
     return guarded([&] {
         if (!task)
             throw std::invalid_argument("mymyr_amd: expand: null argument");
+        std::unique_lock<std::mutex> lazy_lock;
+        if (lazy_task(task))
+            lazy_lock = std::unique_lock<std::mutex>(task->lazy_mutex);
         const TaskDev* T = device_task(task).thost.get();
         ScratchLease lease(expand_scratch_bytes(std::max<u64>(rows, 1)), "expand scratch");
-        expand_rows({T}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream), lease.base());
+        expand_rows({T}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream), lease.base(),
+                    lazy_task(task) ? task : nullptr);
     });
 }
 

@@ -55,6 +55,8 @@ TaskDev task_dev(const u64* img, const DevTaskHeader& h)
     t.num_decode = h.num_decode;
     t.decode_arith = h.decode_arith;
     t.max_step_words = h.max_step_words;
+    t.lazy = h.lazy;
+    t.missing = nullptr;
     return t;
 }
 
@@ -1033,14 +1035,25 @@ __device__ __forceinline__ bool pick(const TaskDev& T, const auto& H, const Lds&
         return pick_lanes(T, H, L, s, rank, lane);
 }
 
-__device__ __forceinline__ u32 effect_slot(const TaskDev& T, const Lds& L, const auto& e)
+/// The slot of an effect's atom under the wave's binding (kNone: none); its canonical id in *cid.
+__device__ __forceinline__ u32 effect_slot(const TaskDev& T, const Lds& L, const auto& e, u64* cid_out)
 {
     u64 cid = e.base;
     for (u32 v = 0; v < e.nvar; ++v)
         cid += T.rs[static_cast<u64>(e.var_pos[v]) * T.n + L.ub[e.var_param[v]]];
+    *cid_out = cid;
     if (cid >= T.fluent_count)
         return kNone;
     return T.dense ? static_cast<u32>(cid) : T.slot_of[cid];
+}
+
+/// An added atom without a slot: an error under frozen slots; lazy slots record it for the host to intern (the
+/// successor written is then incomplete, and the launch is repeated once the atom has a slot).
+__device__ __forceinline__ void missing_atom(const TaskDev& T, u64 cid, u32* status)
+{
+    if (T.missing && cid < T.fluent_count)
+        atomicOr(reinterpret_cast<unsigned long long*>(T.missing + (cid >> 6)), 1ull << (cid & 63));
+    atomicOr(status, kStatusNoSlot);
 }
 
 /// Predicate and the first two arguments of atom slot s: arithmetic for dense slots over contiguous domains, else the
@@ -1167,6 +1180,15 @@ __device__ __forceinline__ void load_row_lds(const TaskDev& T, const Lds& L, con
     wave_sync();
 }
 
+/// Loads the first n words of a row into the wave's LDS row and zeroes the rest of its T.W words (rows narrower than
+/// the task: a lazy task's rows grow as atoms intern).
+__device__ __forceinline__ void load_row_lds_n(const TaskDev& T, const Lds& L, const u64* src, u32 n, u32 lane)
+{
+    for (u32 k = lane; k < T.W; k += kWave)
+        L.row[k] = k < n ? src[k] : 0;
+    wave_sync();
+}
+
 /// dst[k] = k < n ? src[k] : 0 for k < z (global to global), up to 8 loads of a lane in flight.
 __device__ __forceinline__ void copy_words(u64* dst, const u64* src, u32 n, u32 z, u32 lane)
 {
@@ -1251,10 +1273,11 @@ __device__ __forceinline__ void apply_effects(const TaskDev& T, const auto& H, c
     bool before = false;
     if (mine)
     {
-        sl = effect_slot(T, L, H.effects[S.eff_begin + lane]);
+        u64 cid;
+        sl = effect_slot(T, L, H.effects[S.eff_begin + lane], &cid);
         before = sl != kNone && row_bit(L.row, sl);
         if (add && sl == kNone)
-            atomicOr(status, kStatusNoSlot);
+            missing_atom(T, cid, status);
     }
     wave_sync();
     if (mine && !add && sl != kNone)
@@ -2191,12 +2214,13 @@ __device__ __forceinline__ bool succ_apply(const TaskDev& T, const auto& H, cons
     bool before = false;
     if (mine)
     {
-        sl = effect_slot(T, L, H.effects[S.eff_begin + lane]);
+        u64 cid;
+        sl = effect_slot(T, L, H.effects[S.eff_begin + lane], &cid);
         before = sl != kNone && row_bit(L.row, sl);
         L.eff[lane] = sl;
         L.before[lane] = before ? 1u : 0u;
         if (add && sl == kNone)
-            atomicOr(status, kStatusNoSlot);
+            missing_atom(T, cid, status);
     }
     wave_sync();
     if (mine && !add && sl != kNone)
@@ -2263,7 +2287,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
         if (__ballot(wide) && lane == 0)
             atomicOr(A.status, kStatusWideRow);
     }
-    load_row_lds(T, L, src, lane);
+    load_row_lds_n(T, L, src, min(A.words, T.W), lane);
     build_view(T, H, L, lane);
     const u32 c = count_all<kLevels>(T, H, L, lane);
     if (A.pass == 0 && !A.drop_noops)
@@ -2484,7 +2508,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
     const u32 Lw = T.label_width;
     for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < rows; i += static_cast<u64>(gridDim.x) * nw)
     {
-        load_row_lds(T, L, states + i * words, lane);
+        load_row_lds_n(T, L, states + i * words, min(words, T.W), lane);
         build_view(T, H, L, lane);
         const u32 c = count_all<kLevels>(T, H, L, lane);
         if (lane == 0 && count)
@@ -2504,6 +2528,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
                 u64* dst = succ + o * words;
                 for (u32 q = lane; q < words; q += kWave)
                     dst[q] = q < T.W ? L.row[q] : 0;
+                // a successor with atoms past the rows' words (a lazy task's rows outgrew them) is an error
+                bool wide = false;
+                for (u32 q = words + lane; q < T.W; q += kWave)
+                    wide = wide || L.row[q] != 0;
+                if (__ballot(wide) && lane == 0)
+                    atomicOr(status, kStatusWideRow);
                 succ_revert(H, L, s, lane);
             }
             wave_sync();

@@ -59,6 +59,9 @@ int mya_expand_noalloc(mya_task* task, const uint64_t* states, uint64_t rows, ui
                                         std::to_string(kNoallocRows) + " (use mya_expand)");
         int dev = 0;
         hip_check(hipGetDevice(&dev), "hipGetDevice");
+        std::unique_lock<std::mutex> lazy_lock;
+        if (lazy_task(task))
+            lazy_lock = std::unique_lock<std::mutex>(task->lazy_mutex);
         const TaskDev* T = nullptr;
         {
             // the task's device image must be there already: uploading it would allocate
@@ -70,7 +73,8 @@ int mya_expand_noalloc(mya_task* task, const uint64_t* states, uint64_t rows, ui
         }
         std::lock_guard lock(g_mutex);
         void* block = scratch_ptr(dev);
-        expand_rows({T}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream), block);
+        expand_rows({T}, nullptr, nullptr, states, rows, words, options, out, static_cast<hipStream_t>(stream), block,
+                    lazy_task(task) ? task : nullptr);
     });
 }
 

@@ -40,6 +40,8 @@ struct TaskDev
     u32 n, ow, W, num_schemas, num_pairs, view_words, ngp, ngn, goal_unsat, dense, label_width, fluent_slots;
     u32 num_decode, decode_arith;
     u32 max_step_words;
+    u32 lazy;      // lazy slots: an added atom without a slot is recorded in `missing`
+    u64* missing;  // lazy slots: bit per canonical fluent atom (device; set by the successor kernels), else null
 };
 
 /// Pointers into an uploaded image (host helper).

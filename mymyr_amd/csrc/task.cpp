@@ -13,6 +13,9 @@
 
 namespace mya
 {
+/// The goal's slot lists and goal_unsat from goal_fluent under the current slots.
+void resolve_goal(CompiledTask& C);
+
 namespace
 {
 // ------------------------------------------------------------------------------------------------- text reader
@@ -858,6 +861,19 @@ private:
             return atoms * per + (L.fluent_count + 1) * 4;
         };
         constexpr u64 kMaxBytes = u64{4} << 30;
+        if (m_opt == AtomsOption::Lazy)
+        {
+            // no slots yet: the initial state's atoms take the first ones (build_state_tables); the tables are sized for
+            // every canonical atom, as the reference's lazy index is (atom_index.cpp:60-70)
+            if (frozen_bytes(L.fluent_count) + L.fluent_count * 8 > kMaxBytes)
+                throw Error("lazy atom slots over " + std::to_string(L.fluent_count) + " canonical atoms need more than 4 GiB of records");
+            C->mode = AtomMode::Lazy;
+            C->slot_of.assign(L.fluent_count, kNone);
+            C->fluent_slots = 0;
+            C->slot_cid.clear();
+            C->words = 1;
+            return;
+        }
         std::vector<u64> reach;
         AtomMode mode = AtomMode::Dense;
         if (m_opt != AtomsOption::Dense)
@@ -895,6 +911,22 @@ private:
 
     void build_state_tables()
     {
+        if (C->mode == AtomMode::Lazy)
+        {
+            // the initial state's atoms intern first, in the order of its atom list (task.cpp:214-224)
+            for (const auto& a : T->fluent_init)
+            {
+                const u64 c = cid_of(a[0], a.data() + 1);
+                if (c >= C->layout.fluent_count)
+                    throw Error("an initial atom lies outside the typed-dense domains");
+                if (C->slot_of[c] == kNone)
+                {
+                    C->slot_of[c] = C->fluent_slots++;
+                    C->slot_cid.push_back(c);
+                }
+            }
+            C->words = std::max<u32>(1, words_for(C->fluent_slots));
+        }
         C->initial.assign(C->words, 0);
         for (const auto& a : T->fluent_init)
         {
@@ -903,7 +935,8 @@ private:
                 throw Error("an initial atom has no slot");
             C->initial[s >> 6] |= u64{1} << (s & 63);
         }
-        // goal: static literals folded, fluent ones as slot masks (a positive atom without a slot never holds)
+        // goal: static literals folded, fluent ones kept by canonical id and resolved to slot lists (a positive atom
+        // without a slot holds in no state)
         std::set<std::vector<u32>> pos_atoms;
         for (const Literal& l : T->goal)
         {
@@ -913,21 +946,15 @@ private:
             if (T->preds[l.pred].kind == 'S')
             {
                 if (static_holds(l.pred, objs.data()) != l.positive)
-                    C->goal_unsat = true;
+                    C->goal_fixed_unsat = true;
                 continue;
             }
             std::vector<u32> key{l.pred};
             key.insert(key.end(), objs.begin(), objs.end());
             if (l.positive)
                 pos_atoms.insert(key);
-            const u32 s = slot_of_cid(cid_of(l.pred, objs.data()));
-            if (s == kNone)
-            {
-                if (l.positive)
-                    C->goal_unsat = true;
-                continue;
-            }
-            (l.positive ? C->goal_pos : C->goal_neg).push_back(s);
+            const u64 c = cid_of(l.pred, objs.data());
+            C->goal_fluent.emplace_back(l.positive, c < C->layout.fluent_count ? c : C->layout.fluent_count);
         }
         for (const Literal& l : T->goal)
             if (!l.positive && T->preds[l.pred].kind != 'S')
@@ -936,8 +963,9 @@ private:
                 for (i32 x : l.terms)
                     key.push_back(term_object(x));
                 if (pos_atoms.count(key))
-                    C->goal_unsat = true;
+                    C->goal_fixed_unsat = true;
             }
+        resolve_goal(*C);
         C->label_width = 0;
         for (const auto& s : T->schemas)
             C->label_width = std::max(C->label_width, s.arity);
@@ -1258,41 +1286,12 @@ private:
             decode.push_back(d);
         }
 
-        // slot records (pred | a0 << 16 | a1 << 32 | a2 << 48) for the view build and the atom listing
-        std::vector<u64> records(C->fluent_slots, 0);
-        {
-            std::vector<u32> by_offset;
-            for (u32 p = 0; p < m; ++p)
-                if (T->preds[p].kind == 'F' && C->layout.size[p] > 0)
-                    by_offset.push_back(p);
-            for (u32 s = 0; s < C->fluent_slots; ++s)
-            {
-                const u64 c = C->slot_cid[s];
-                u32 p = by_offset[0];
-                for (u32 q : by_offset)
-                    if (C->layout.offset[q] <= c)
-                        p = q;
-                u64 rem = c - C->layout.offset[p];
-                const u32 ar = T->preds[p].arity;
-                u64 rec = p;
-                // decode ranks: last position has stride 1
-                std::vector<u32> args(ar, 0);
-                for (u32 i = ar; i-- > 0;)
-                {
-                    const auto& dom = C->layout.domain[C->layout.pos_begin[p] + i];
-                    const u64 dsz = std::max<u64>(1, dom.size());
-                    args[i] = dom[rem % dsz];
-                    rem /= dsz;
-                }
-                for (u32 i = 0; i < ar && i < 3; ++i)
-                {
-                    if (args[i] >= 65536)
-                        throw Error("objects beyond 65535 are not supported by the device path");
-                    rec |= static_cast<u64>(args[i]) << (16 * (i + 1));
-                }
-                records[s] = rec;
-            }
-        }
+        // slot records (pred | a0 << 16 | a1 << 32 | a2 << 48) for the view build and the atom listing; lazy slots
+        // reserve one per canonical atom
+        const bool lazy = C->mode == AtomMode::Lazy;
+        std::vector<u64> records(lazy ? C->layout.fluent_count : C->fluent_slots, 0);
+        for (u32 s = 0; s < C->fluent_slots; ++s)
+            records[s] = atom_record(*C, C->slot_cid[s]);
 
         // per predicate: its view pairs (unary/forward, backward) for the view build
         std::vector<u64> pred_pairs(m, ~u64{0});
@@ -1346,8 +1345,20 @@ private:
         h.decode_arith = decode_arith ? 1 : 0;
         h.off_decode = put(decode.data(), decode.size() * sizeof(DevPredDecode));
         h.off_dom0 = put(dom0_words.data(), dom0_words.size() * sizeof(u64));
-        h.off_goal_pos = put(C->goal_pos.data(), C->goal_pos.size() * sizeof(u32));
-        h.off_goal_neg = put(C->goal_neg.data(), C->goal_neg.size() * sizeof(u32));
+        {
+            // lazy slots: room for every fluent goal literal (the lists grow as their atoms intern)
+            std::vector<u32> gp = C->goal_pos, gn = C->goal_neg;
+            if (lazy)
+            {
+                u32 np = 0, nn = 0;
+                for (const auto& [pos, c] : C->goal_fluent)
+                    ++(pos ? np : nn);
+                gp.resize(np, 0);
+                gn.resize(nn, 0);
+            }
+            h.off_goal_pos = put(gp.data(), gp.size() * sizeof(u32));
+            h.off_goal_neg = put(gn.data(), gn.size() * sizeof(u32));
+        }
         {
             std::vector<u32> ar(m);
             for (u32 p = 0; p < m; ++p)
@@ -1388,7 +1399,13 @@ private:
         for (auto& meta : static_meta)
             meta.keys += h.off_static_keys;
         h.off_static_meta = put(static_meta.data(), static_meta.size() * sizeof(DevStaticMeta));
-        h.off_initial = put(C->initial.data(), C->initial.size() * sizeof(u64));
+        {
+            std::vector<u64> init = C->initial;
+            if (lazy)
+                init.resize(std::max<u32>(1, words_for(C->layout.fluent_count)), 0);
+            h.off_initial = put(init.data(), init.size() * sizeof(u64));
+        }
+        h.lazy = lazy ? 1 : 0;
         std::memcpy(img.data(), &h, sizeof(h));
         C->image = std::move(img);
     }
@@ -1668,4 +1685,95 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
 }
 
 std::unique_ptr<CompiledTask> compile_task(TaskText text, AtomsOption atoms) { return Compiler(std::move(text), atoms).run(); }
+
+u64 atom_record(const CompiledTask& C, u64 c)
+{
+    // the predicate whose canonical block holds c, then its mixed-radix ranks (the last position has stride 1)
+    u32 p = kNone;
+    for (u32 q = 0; q < C.text.preds.size(); ++q)
+        if (C.text.preds[q].kind == 'F' && C.layout.size[q] > 0 && C.layout.offset[q] <= c && c < C.layout.offset[q] + C.layout.size[q])
+            p = q;
+    if (p == kNone)
+        throw std::logic_error("mymyr_amd: canonical atom " + std::to_string(c) + " outside the fluent predicates' blocks");
+    u64 rem = c - C.layout.offset[p];
+    const u32 ar = C.text.preds[p].arity;
+    u32 args[8] = {};
+    for (u32 i = ar; i-- > 0;)
+    {
+        const auto& dom = C.layout.domain[C.layout.pos_begin[p] + i];
+        const u64 dsz = std::max<u64>(1, dom.size());
+        args[i] = dom[rem % dsz];
+        rem /= dsz;
+    }
+    u64 rec = p;
+    for (u32 i = 0; i < ar && i < 3; ++i)
+    {
+        if (args[i] >= 65536)
+            throw Error("objects beyond 65535 are not supported by the device path");
+        rec |= static_cast<u64>(args[i]) << (16 * (i + 1));
+    }
+    return rec;
+}
+
+void resolve_goal(CompiledTask& C)
+{
+    C.goal_pos.clear();
+    C.goal_neg.clear();
+    C.goal_unsat = C.goal_fixed_unsat;
+    for (const auto& [pos, c] : C.goal_fluent)
+    {
+        const u32 s = c < C.layout.fluent_count ? C.slot_of[c] : kNone;
+        if (s == kNone)
+        {
+            if (pos)
+                C.goal_unsat = true;
+            continue;
+        }
+        (pos ? C.goal_pos : C.goal_neg).push_back(s);
+    }
+}
+
+std::vector<std::pair<u64, u64>> intern_atoms(CompiledTask& C, const std::vector<u64>& cids)
+{
+    if (C.mode != AtomMode::Lazy)
+        throw std::logic_error("mymyr_amd: atoms interned into a task with frozen slots");
+    std::vector<std::pair<u64, u64>> ranges;
+    DevTaskHeader h;
+    std::memcpy(&h, C.image.data(), sizeof(h));
+    const u32 first = C.fluent_slots;
+    u64 lo = ~u64{0}, hi = 0;
+    u32* slot_img = reinterpret_cast<u32*>(C.image.data() + h.off_slot_of);
+    for (const u64 c : cids)
+    {
+        if (c >= C.layout.fluent_count)
+            throw std::logic_error("mymyr_amd: an atom outside the typed-dense domains met without a slot");
+        if (C.slot_of[c] != kNone)
+            continue;
+        const u32 s = C.fluent_slots++;
+        C.slot_of[c] = s;
+        C.slot_cid.push_back(c);
+        C.image[h.off_records + s] = atom_record(C, c);
+        slot_img[c] = s;
+        lo = std::min(lo, c);
+        hi = std::max(hi, c);
+    }
+    if (C.fluent_slots == first)
+        return ranges;
+    C.words = std::max<u32>(1, words_for(C.fluent_slots));
+    C.initial.resize(C.words, 0);
+    resolve_goal(C);
+    std::memcpy(reinterpret_cast<u32*>(C.image.data() + h.off_goal_pos), C.goal_pos.data(), C.goal_pos.size() * sizeof(u32));
+    std::memcpy(reinterpret_cast<u32*>(C.image.data() + h.off_goal_neg), C.goal_neg.data(), C.goal_neg.size() * sizeof(u32));
+    h.words = C.words;
+    h.fluent_slots = C.fluent_slots;
+    h.num_goal_pos = static_cast<u32>(C.goal_pos.size());
+    h.num_goal_neg = static_cast<u32>(C.goal_neg.size());
+    h.goal_unsat = C.goal_unsat ? 1 : 0;
+    std::memcpy(C.image.data(), &h, sizeof(h));
+    // the header and the goal lists (hot section), the slot table's changed words, the new records
+    ranges.emplace_back(0, h.hot_words);
+    ranges.emplace_back(h.off_slot_of + lo / 2, h.off_slot_of + hi / 2 + 1);
+    ranges.emplace_back(h.off_records + first, h.off_records + C.fluent_slots);
+    return ranges;
+}
 }  // namespace mya

@@ -107,16 +107,22 @@ struct TaskText
 /// effects). Throws mya::Error naming what is unsupported or malformed.
 TaskText parse_task_text(std::string_view text);
 
+/// Atom slots (include/mymyr/task/atom_index.hpp:12-22): Reachable and Dense are frozen (the slot table is a function of
+/// the task); Lazy slots are assigned as atoms are met: the initial state's atoms at load, in the order of its atom
+/// list (task.cpp:214-224), then the atoms that successors add without a slot, interned between device launches in
+/// ascending canonical id (include/mymyr/cuda/generator.hpp:20-24).
 enum class AtomMode : u32
 {
     Reachable = 0,
     Dense = 1,
+    Lazy = 2,
 };
 enum class AtomsOption : u32
 {
     Auto = 0,
     Reachable = 1,
     Dense = 2,
+    Lazy = 3,
 };
 
 /// Typed-dense canonical ids: cid(p, a) = offset[p] + sum_i rs[pos_begin[p] + i][a_i].
@@ -272,7 +278,7 @@ struct DevTaskHeader
     u32 decode_arith;     // 1: slots decode arithmetically (dense slots, contiguous domains)
     u32 init_count;     // successors of the initial state (filled once the device has counted them)
     u32 max_step_words; // the widest candidate window of any plan or filter step, in words
-    u32 pad_header;
+    u32 lazy;           // 1: lazy slots (slot_of, records, goal lists and initial row sized for every canonical atom)
 };
 
 /// Static k-ary relation: sorted keys sum(obj_i * n^(ar-1-i)) at [keys, keys + count).
@@ -296,7 +302,12 @@ struct CompiledTask
     std::vector<u64> slot_cid;    // per slot
     std::vector<u64> initial;     // [words]
     std::vector<u32> goal_pos, goal_neg;  // goal slots
-    bool goal_unsat = false;
+    bool goal_unsat = false;              // no state is a goal under the current slots
+    // the goal's fluent literals in order (polarity, canonical id: at least fluent_count for an atom outside the
+    // typed-dense domains), and whether the goal fails whatever the state (a static literal that fails, or one atom
+    // wanted both true and false: the reference's compiled goal.unsatisfiable, compile.cpp:1322-1343)
+    std::vector<std::pair<bool, u64>> goal_fluent;
+    bool goal_fixed_unsat = false;
     u32 label_width = 0;
     std::vector<std::vector<std::vector<u64>>> dom0;  // per schema, per parameter: object bits (ow words)
     std::vector<u8> never;                            // per schema
@@ -308,6 +319,14 @@ struct CompiledTask
 };
 
 std::unique_ptr<CompiledTask> compile_task(TaskText text, AtomsOption atoms);
+
+/// The device record of canonical fluent atom `cid`: predicate | a0 << 16 | a1 << 32 | a2 << 48.
+u64 atom_record(const CompiledTask& task, u64 cid);
+
+/// Lazy slots: gives the next slots to the atoms `cids` (canonical fluent ids without a slot, ascending), in that order,
+/// and brings the slot tables, the goal, the initial row's width and the device image up to date. Returns the image's
+/// changed word ranges [first, end), for the device copy.
+std::vector<std::pair<u64, u64>> intern_atoms(CompiledTask& task, const std::vector<u64>& cids);
 
 /// Ground actions in canonical order (schema, then lexicographic binding), with their static preconditions evaluated
 /// and fluent ones resolved to slots. An action whose positive fluent precondition has no slot is dropped (it never

@@ -685,7 +685,9 @@ def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tens
     uint8, and "index" [M] int32 (the position in the parent's full successor order) with drop_noops or index=True;
     plus "generated", "total", "words_needed" and "overflow". capacity None sizes the buffers to every successor (a
     first call counts them). Canonical order, witness pruning off; drop_noops removes a state's no-op successors unless
-    all of them are no-ops. Over a TaskTable, row i is a state of instance task_ids[i] ([N] int32 on the device)."""
+    all of them are no-ops. Over a TaskTable, row i is a state of instance task_ids[i] ([N] int32 on the device).
+    A task with lazy slots interns the atoms its successors add without a slot (ascending canonical id); with words
+    None the rows then take the task's new width (the expansion runs once more when its successors outgrew them)."""
     s = states.view(torch.int64) if states.dtype == torch.uint64 else states
     if not s.is_cuda or s.dim() != 2 or s.dtype != torch.int64:
         raise ValueError("mymyr_amd: expand: states must be a 2-d int64/uint64 device tensor")
@@ -728,6 +730,10 @@ def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tens
     x = _lib.Expansion(cap, ow, L, succ.data_ptr(), parent.data_ptr(), schema.data_ptr(), binding.data_ptr(), _p(gl),
                        offsets.data_ptr(), _p(sh), _p(np_), _p(ix), 0, 0, 0, 0)
     run(x)
+    if words is None and not table and not task.frozen and x.words_needed > ow:
+        # lazy slots grew the rows: their atoms have slots now, so the successors fit rows of the task's new width
+        return expand(task, states, capacity=cap, goal=goal, hashes=hashes, noops=noops, drop_noops=drop_noops, index=index,
+                      validate=validate, words=max(task.words, int(x.words_needed)))
     kept = min(x.total, cap)
     out = {"succ": succ[:kept], "parent": parent[:kept], "schema": schema[:kept], "binding": binding[:kept],
            "offsets": offsets, "generated": x.generated, "total": x.total, "words_needed": x.words_needed,

@@ -122,7 +122,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     cap = 1 << 16
     ps = np.zeros(cap, np.int32)
     pb = np.zeros((cap, L), np.int32)
-    gs = np.zeros(max(1, task.words), np.uint64)
+    # lazy slots: the goal state may be as wide as the task's canonical atoms make it
+    gs = np.zeros(max(1, task.words if task.frozen else (task.dense_fluent + 63) // 64), np.uint64)
     plan = _lib.BrfsPlan(ps.ctypes.data, pb.ctypes.data, cap, L, gs.ctypes.data, gs.size, 0, 0, 0, 0.0)
     n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ctypes.byref(plan))
     if n < 0:

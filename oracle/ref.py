@@ -160,13 +160,17 @@ def _p(a: np.ndarray | None):
 class RefTask:
     """A reference Task (Task::from_text_file) plus its one-instance TaskTable."""
 
-    MODES = {"auto": 0, "reachable": 1, "dense": 2}
+    MODES = {"auto": 0, "reachable": 1, "dense": 2, "lazy": 3}
 
     def __init__(self, path: str, atoms: str = "auto"):
         h = lib().mref_task_load(str(path).encode(), self.MODES[atoms])
         if not h:
             raise RuntimeError(_err())
         self._h = c_void_p(h)
+        self.refresh()
+
+    def refresh(self):
+        """Reads the task's sizes again (lazy slots grow as searches meet atoms)."""
         info = np.zeros(9, dtype=np.uint64)
         assert lib().mref_task_info(self._h, info.ctypes.data) == 0
         (self.words, self.fluent_slots, mode, self.num_schemas, self.label_width, self.num_objects, self.max_arity,
@@ -436,7 +440,7 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
     cap = 4096
     ps = np.zeros(cap, np.int32)
     pb = np.zeros((cap, L), np.int32)
-    gs = np.zeros(max(1, task.words) + 64, np.uint64)
+    gs = np.zeros(max(1, task.words, (task.dense_fluent + 63) // 64) + 64, np.uint64)
     n = lib().mref_brfs(task._h, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ps.ctypes.data, pb.ctypes.data, L, cap,
                         gs.ctypes.data, gs.size)
     if n < 0:
@@ -447,6 +451,7 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         "exhausted": bool(r.exhausted), "seconds": r.seconds, "layer_counts": lc[:n].tolist(), "pruned": r.pruned,
     }
     del st, bl
+    task.refresh()
     if r.solved:
         k = min(r.plan_len, cap)
         out["plan"] = [[int(ps[i])] + [int(x) for x in pb[i] if x >= 0] for i in range(k)]

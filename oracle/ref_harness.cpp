@@ -129,17 +129,21 @@ struct mref_brfs_result
 
 const char* mref_last_error() { return g_error.c_str(); }
 
-// atoms: 0 auto, 1 reachable, 2 dense
+// atoms: 0 auto, 1 reachable, 2 dense, 3 lazy (a lazy task has no table: TaskTable refuses lazy slots)
 mref_task* mref_task_load(const char* path, int atoms)
 {
     return guarded(
         [&]() -> mref_task*
         {
             TaskOptions o;
-            o.atoms = atoms == 1 ? TaskOptions::Atoms::Reachable : atoms == 2 ? TaskOptions::Atoms::Dense : TaskOptions::Atoms::Auto;
+            o.atoms = atoms == 1   ? TaskOptions::Atoms::Reachable
+                      : atoms == 2 ? TaskOptions::Atoms::Dense
+                      : atoms == 3 ? TaskOptions::Atoms::Lazy
+                                   : TaskOptions::Atoms::Auto;
             auto t = new mref_task;
             t->task = Task::from_text_file(path, o);
-            t->table = rl::TaskTable::single(t->task);
+            if (atoms != 3)
+                t->table = rl::TaskTable::single(t->task);
             return t;
         },
         nullptr);
@@ -159,10 +163,13 @@ int mref_task_info(mref_task* t, uint64_t* out)
             out[1] = k.atoms().fluent_slots();
             out[2] = static_cast<uint64_t>(k.atoms().mode());
             out[3] = k.num_schemas();
-            out[4] = t->table->label_width();
+            u32 lw = 0;
+            for (const auto& sc : k.data().schemas)
+                lw = std::max(lw, sc.arity());
+            out[4] = t->table ? t->table->label_width() : lw;
             out[5] = k.data().num_objects();
             out[6] = k.atoms().layout().max_arity;
-            out[7] = t->table->words();
+            out[7] = t->table ? t->table->words() : k.words();
             out[8] = k.atoms().layout().fluent_count;
             return 0;
         },

@@ -492,6 +492,58 @@ def make_brfs(quick: bool):
     dump("brfs.json", out)
 
 
+LAZY_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "pegsol-08-strips__p22", "visitall__visitall_x-6_y-3_r-100"]
+
+
+def goal_cids(t, words_hex):
+    """The canonical ids of a goal state's atoms (its words as hex strings) under the task's current slots, ascending."""
+    _, cid = t.slot_records()
+    out = []
+    for w, x in enumerate(words_hex):
+        v = int(x, 16)
+        while v:
+            b = (v & -v).bit_length() - 1
+            v &= v - 1
+            out.append(int(cid[w * 64 + b]))
+    return sorted(out)
+
+
+def lazy_record(name, **kw):
+    """The reference brfs() over a task loaded with lazy slots (witness pruning off, as the lifted expansion runs it):
+    counts, fingerprint and plan, plus what does not depend on the order the slots were numbered in: the number of
+    slots the search left, the sha256 of their canonical ids sorted, and the goal state's atoms by canonical id."""
+    t = ref.RefTask(fx.task_path(name), "lazy")
+    r = ref.brfs(t, witness_pruning=False, **kw)
+    r.pop("seconds")
+    _, cid = t.slot_records()
+    r["slots"] = t.fluent_slots
+    r["slot_cids_sha"] = hashlib.sha256(np.sort(cid.astype(np.uint64)).tobytes()).hexdigest()
+    if "goal_state" in r:
+        r["goal_cids"] = goal_cids(t, r.pop("goal_state"))
+    r["options"] = dict(kw, witness_pruning=False)
+    return r
+
+
+def make_lazy():
+    """Lazy atom slots: the slot table right after loading (the initial state's atoms in its atom order), and BrFS runs
+    whose states' atoms intern as the search meets them (exhaustive, to the first goal, and a max_states cut)."""
+    out = {"initial": {}, "brfs": {}}
+    for name in LAZY_TASKS + ["transport_w20_3", "rovers__p02", "transport"]:
+        t = ref.RefTask(fx.task_path(name), "lazy")
+        rec, cid = t.slot_records()
+        out["initial"][name] = {"words": t.words, "slots": t.fluent_slots, "cid": [int(x) for x in cid],
+                                "rec_sha": hashlib.sha256(rec.astype(np.uint32).tobytes()).hexdigest(),
+                                "initial": hex_row(t.initial_state(t.words))}
+    for name in LAZY_TASKS:
+        out["brfs"][name] = lazy_record(name, stop_at_goal=False, fingerprint=True)
+        out["brfs"][name + ":goal"] = lazy_record(name, stop_at_goal=True, fingerprint=True)
+        print("lazy", name, out["brfs"][name]["states"], out["brfs"][name]["slots"], flush=True)
+    out["brfs"]["transport_w20_3:goal"] = lazy_record("transport_w20_3", stop_at_goal=True, fingerprint=True)
+    out["brfs"]["gripper__prob05:cut"] = lazy_record("gripper__prob05", stop_at_goal=False, fingerprint=True, max_states=20000)
+    out["brfs"]["blocks__probBLOCKS-8-0:depth"] = lazy_record("blocks__probBLOCKS-8-0", stop_at_goal=False, fingerprint=True, max_depth=6)
+    dump("lazy.json", out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--quick", action="store_true")
@@ -500,7 +552,7 @@ def main():
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool,
-             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "brfs": lambda: make_brfs(a.quick)}
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

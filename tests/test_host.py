@@ -195,3 +195,32 @@ def test_c_and_eg_sections_are_read(golden):
 
     for name in ("sections_gripper_rep", "sections_gripper_norep", "sections_blocks_norep", "sections_logistics_eg"):
         Task.from_text_file(golden.task_path(name))
+
+
+def test_lazy_slots_after_load_equal_the_reference(golden):
+    """atoms="lazy": the slots start with the initial state's atoms, in its atom order (src/mymyr/task/task.cpp:214-224),
+    record for record the reference's lazy AtomIndex right after loading."""
+    init = golden.load("lazy.json")["initial"]
+    for name, g in init.items():
+        t = Task.from_text_file(golden.task_path(name), "lazy")
+        assert (t.atom_mode, t.words, t.fluent_slots, t.frozen) == ("lazy", g["words"], g["slots"], False), name
+        rec, cid = t.slot_records()
+        assert [int(x) for x in cid] == g["cid"], name
+        assert hashlib.sha256(rec.astype(np.uint32).tobytes()).hexdigest() == g["rec_sha"], name
+        assert [f"{int(x):016x}" for x in t.initial_state()] == g["initial"], name
+
+
+def test_lazy_tasks_refused_by_env_tables(golden):
+    """Environments and task tables need a fixed slot layout (src/mymyr/rl/task_table.cpp:120-123): the refusal comes
+    before any device work."""
+    t = Task.from_text_file(golden.task_path("gripper__prob05"), "lazy")
+    cfg = _lib.EnvConfig(0, 0, 0.0, 1.0, 0.0, 0, 1, 1, 1, 0, 0)
+    h = ctypes.c_void_p()
+    assert lib.mya_env_create(t.handle, ctypes.byref(cfg), ctypes.byref(h)) != 0
+    assert "lazy atom slots" in lib.mya_last_error().decode()
+    with pytest.raises(MyaError, match="atoms 'auto', 'reachable' or 'dense'"):
+        from mymyr_amd import rl
+
+        rl.TaskTable([Task.from_text_file(golden.task_path("gripper__prob05")), t])
+    with pytest.raises(MyaError, match="atoms must be"):
+        _lib.check(lib.mya_task_load_file(golden.task_path("gripper__prob05").encode(), 4, ctypes.byref(h)))
