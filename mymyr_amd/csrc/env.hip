@@ -310,6 +310,28 @@ __device__ __forceinline__ u64 cand_word(const TaskDev& T, const auto& H, const 
     return a;
 }
 
+/// Calls f(w, m) for the window words w >= w0 of step st whose candidate word m is nonzero, ascending, until f returns
+/// true (then returns true). The binding b (stride bs) must hold the same prefix in every lane (the parameters before
+/// st's): the words are evaluated 64 at a time, one per lane, and the nonzero ones taken from a ballot, so a wide
+/// window with few candidates costs one evaluation instead of one per word.
+template<class F>
+__device__ __forceinline__ bool for_nonzero_words(const TaskDev& T, const auto& H, const Lds& L, const auto& st, u32 w0, auto b, u32 bs,
+                                                  u32 lane, F&& f)
+{
+    for (u32 base = w0; base < st.words; base += kWave)
+    {
+        const u32 wl = base + lane;
+        const u64 mine = wl < st.words ? cand_word(T, H, L, st, wl, b, bs) : 0;
+        for (u64 nz = __ballot(mine != 0); nz; nz &= nz - 1)
+        {
+            const u32 k = static_cast<u32>(__builtin_ctzll(nz));
+            if (f(base + k, __shfl(mine, static_cast<int>(k), kWave)))
+                return true;
+        }
+    }
+    return false;
+}
+
 __device__ __forceinline__ bool check_holds(const TaskDev& T, const auto& H, const Lds& L, const auto& c, auto b, u32 bs)
 {
     u32 objs[6];
@@ -805,11 +827,8 @@ __device__ __forceinline__ bool pick_levels(const TaskDev& T, const auto& H, con
         const DevStep F = ld(H.steps + S.filter_step[i]);
         const u32 pb = S.plan_begin[i + 1], pe = S.plan_begin[i + 2];
         const bool chk = F.check_begin != F.check_end;
-        bool found = false;
-        for (u32 w = 0; w < F.words && !found; ++w)
-        {
-            u64 m = cand_word(T, H, L, F, w, L.ub, 1);
-            if (chk && m)
+        const bool found = for_nonzero_words(T, H, L, F, 0, L.ub, 1, lane, [&](u32 w, u64 m) {
+            if (chk)
             {
                 // lane b checks candidate b
                 bool ok = false;
@@ -823,7 +842,7 @@ __device__ __forceinline__ bool pick_levels(const TaskDev& T, const auto& H, con
                 m = __ballot(ok);
             }
             if (m == 0)
-                continue;
+                return false;
             const u32 nr = static_cast<u32>(__popcll(m));
             // root r = the r-th candidate in object order
             if ((m >> lane) & 1)
@@ -839,6 +858,7 @@ __device__ __forceinline__ bool pick_levels(const TaskDev& T, const auto& H, con
             const u32 c = lane < nr ? L.rc[lane] : 0;
             const u32 incl = wave_inclusive(c);
             const u32 tot = __shfl(incl, kWave - 1, kWave);
+            bool hit = false;
             if (a < tot)
             {
                 const u64 over = __ballot(incl > a);
@@ -848,12 +868,13 @@ __device__ __forceinline__ bool pick_levels(const TaskDev& T, const auto& H, con
                 wave_sync();
                 if (lane == 0)
                     L.ub[i] = obj;
-                found = true;
+                hit = true;
             }
             else
                 a -= tot;
             wave_sync();
-        }
+            return hit;
+        });
         if (!found)
             return false;
     }
@@ -936,7 +957,7 @@ __device__ __forceinline__ bool label_applicable(const TaskDev& T, const auto& H
 /// Counting thus happens once per node of the binding tree instead of once per successor and parameter. The levels'
 /// words and candidates left live in L.dfs_w / L.dfs_m; L.bind holds the binding's prefix in every lane's column.
 /// Returns the successors enumerated.
-template<class Emit>
+template<bool kLevels, class Emit>
 __device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& H, const Lds& L, u32 lane, Emit&& emit)
 {
     const u32 A = T.label_width ? T.label_width : 1;
@@ -952,7 +973,19 @@ __device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& 
                 return k;
             continue;
         }
-        // the candidates of parameter i in word w with at least one completion (wave-uniform mask)
+        // the candidates of parameter i in word w (candidate word m) with at least one completion (wave-uniform mask)
+        auto live_mask = [&](u32 i, u32 w, u64 m) -> u64 {
+            const DevStep F = ld(H.steps + S.filter_step[i]);
+            bool live = false;
+            if ((m >> lane) & 1)
+            {
+                L.bind[i * 64 + lane] = F.lo + 64 * w + lane;
+                live = F.check_begin == F.check_end || checks_ok(T, H, L, F.check_begin, F.check_end, L.bind + lane, 64);
+                if (live && i + 1 < S.arity)
+                    live = count_from(T, H, L, S.plan_begin[i + 1], S.plan_begin[i + 2], lane) != 0;
+            }
+            return __ballot(live);
+        };
         auto word_mask = [&](u32 i, u32 w) -> u64 {
             const DevStep F = ld(H.steps + S.filter_step[i]);
             const u64 m = cand_word(T, H, L, F, w, L.bind + lane, 64);
@@ -966,14 +999,15 @@ __device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& 
             }
             return __ballot(live);
         };
-        // parameter i from its first word with live candidates (false: none)
+        // parameter i from its first word with live candidates (false: none). Tasks with wide candidate windows (the
+        // level-synchronous kernels) skip empty words 64 at a time; the split kernels' narrow windows go word by word.
         auto open = [&](u32 i, u32 w0) -> bool {
             const DevStep F = ld(H.steps + S.filter_step[i]);
-            for (u32 w = w0; w < F.words; ++w)
-            {
-                const u64 m = word_mask(i, w);
-                if (m)
-                {
+            if constexpr (kLevels)
+                return for_nonzero_words(T, H, L, F, w0, L.bind + lane, 64, lane, [&](u32 w, u64 cm) {
+                    const u64 m = live_mask(i, w, cm);
+                    if (!m)
+                        return false;
                     wave_sync();
                     if (lane == 0)
                     {
@@ -982,9 +1016,26 @@ __device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& 
                     }
                     wave_sync();
                     return true;
+                });
+            else
+            {
+                for (u32 w = w0; w < F.words; ++w)
+                {
+                    const u64 m = word_mask(i, w);
+                    if (m)
+                    {
+                        wave_sync();
+                        if (lane == 0)
+                        {
+                            L.dfs_m[i] = m;
+                            L.dfs_w[i] = w;
+                        }
+                        wave_sync();
+                        return true;
+                    }
                 }
+                return false;
             }
-            return false;
         };
         u32 i = 0;
         bool have = open(0, 0);
@@ -2298,7 +2349,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
     }
     const bool keep_all = A.pass == 1 && A.drop_noops && A.noops[i] == c;
     u32 noops = 0, kept = 0;
-    const u32 listed = for_each_successor(T, H, L, lane, [&](u32 k, u32 s) {
+    const u32 listed = for_each_successor<kLevels>(T, H, L, lane, [&](u32 k, u32 s) {
         const bool noop = succ_apply(T, H, L, s, lane, A.status);
         noops += noop ? 1 : 0;
         if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
@@ -2513,7 +2564,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
         const u32 c = count_all<kLevels>(T, H, L, lane);
         if (lane == 0 && count)
             count[i] = static_cast<i32>(c);
-        const u32 listed = cap == 0 ? 0 : for_each_successor(T, H, L, lane, [&](u32 k, u32 s) {
+        const u32 listed = cap == 0 ? 0 : for_each_successor<kLevels>(T, H, L, lane, [&](u32 k, u32 s) {
             const u64 o = i * cap + k;
             if (lane == 0 && schema)
                 schema[o] = static_cast<i32>(s);
