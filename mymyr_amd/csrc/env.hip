@@ -1269,26 +1269,34 @@ __device__ __forceinline__ void copy_words(u64* dst, const u64* src, u32 n, u32 
     }
 }
 
-/// The ascending set-bit slots of `row` (W words) into out[0, max_atoms), -1 padded (all lanes).
-template<class P>
+/// The ascending set-bit slots of `row` (W words) into out[0, max_atoms), -1 padded (all lanes). A lane takes kPer
+/// consecutive words per round (one wave scan per kPer * 64 words; wide rows take 4); a lane's atoms are consecutive
+/// in the output, and the lanes' ranges follow each other.
+template<u32 kPer = 1, class P>
 __device__ __forceinline__ void encode_row(P row, u32 W, i32* out, u32 max_atoms, u32 lane, u32* status)
 {
     u32 base = 0;
-    for (u32 w0 = 0; w0 < W; w0 += kWave)
+    for (u32 w0 = 0; w0 < W; w0 += kWave * kPer)
     {
-        const u32 w = w0 + lane;
-        u64 x = w < W ? row[w] : 0;
-        const u32 c = static_cast<u32>(__popcll(x));
+        const u32 wl = w0 + lane * kPer;
+        u64 x[kPer];
+        u32 c = 0;
+#pragma unroll
+        for (u32 j = 0; j < kPer; ++j)
+        {
+            x[j] = wl + j < W ? row[wl + j] : 0;
+            c += static_cast<u32>(__popcll(x[j]));
+        }
         const u32 incl = wave_inclusive(c);
         u32 k = base + incl - c;
-        while (x)
-        {
-            const u32 b = static_cast<u32>(__builtin_ctzll(x));
-            x &= x - 1;
-            if (k < max_atoms)
-                out[k] = static_cast<i32>(w * 64 + b);
-            ++k;
-        }
+#pragma unroll
+        for (u32 j = 0; j < kPer; ++j)
+            for (u64 y = x[j]; y; y &= y - 1)
+            {
+                if (k < max_atoms)
+                    out[k] = static_cast<i32>((wl + j) * 64 + static_cast<u32>(__builtin_ctzll(y)));
+                ++k;
+            }
         base += __shfl(incl, kWave - 1, kWave);
     }
     for (u32 k = base + lane; k < max_atoms; k += kWave)
@@ -1742,10 +1750,10 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (A.atoms)
         {
             if (reset)
-                encode_row(A.inst[next].initial, A.inst[next].W, A.atoms + i * A.max_atoms,
+                encode_row<kLevels ? 4 : 1>(A.inst[next].initial, A.inst[next].W, A.atoms + i * A.max_atoms,
                            A.max_atoms, lane, A.status);
             else
-                encode_row(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
+                encode_row<kLevels ? 4 : 1>(L.row, T.W, A.atoms + i * A.max_atoms, A.max_atoms, lane, A.status);
         }
         if (A.masks)
             for (u32 q = lane; q < A.mask_width; q += kWave)
@@ -1845,7 +1853,7 @@ __global__ __launch_bounds__(kWave) void k_encode(const u64* states, u64 rows, u
 {
     const u32 lane = threadIdx.x;
     for (u64 i = blockIdx.x; i < rows; i += gridDim.x)
-        encode_row(states + i * words, W, out + i * max_atoms, max_atoms, lane, status);
+        encode_row<4>(states + i * words, W, out + i * max_atoms, max_atoms, lane, status);
 }
 
 /// The count of row i of instance k (HostEnv::refresh / count_row, src/mymyr/rl/env.cpp:283-322): successors, goal
