@@ -126,3 +126,30 @@ def test_lazy_successor_listing_equals_frozen(golden):
     _, fcid = frozen.slot_records()
     _, lcid = lazy.slot_records()
     assert atoms_of(fcid, fr[0, :n].cpu().numpy().view(np.uint64)) == atoms_of(lcid, lr[0, :n].cpu().numpy().view(np.uint64))
+
+
+def test_lazy_task_searched_again(golden):
+    """A second search over a lazy task starts with the slots the first left (wider rows from the start) and finds the
+    same counts, fingerprint and plan; a search after an expansion that interned atoms too."""
+    from mymyr_amd import rl, search
+    from mymyr_amd.task import Task
+
+    exp = golden.load("lazy.json")["brfs"]["blocks__probBLOCKS-8-0:goal"]
+    t = Task.from_text_file(golden.task_path("blocks__probBLOCKS-8-0"), "lazy")
+    first = search.brfs(t, **exp["options"])
+    words = t.words
+    again = search.brfs(t, **exp["options"])
+    assert t.words == words and t.fluent_slots == exp["slots"]
+    for r in (first, again):
+        assert (r.states, r.expanded, r.generated, r.fingerprint, r.layer_counts) == \
+            (exp["states"], exp["expanded"], exp["generated"], exp["fingerprint"], exp["layer_counts"])
+        assert [[a.schema, *a.binding] for a in r.plan] == exp["plan"]
+    # an expansion first: its atoms take slots in another order, which changes nothing the search reports
+    t2 = Task.from_text_file(golden.task_path("blocks__probBLOCKS-8-0"), "lazy")
+    s0 = torch.from_numpy(t2.initial_state().view(np.int64)).reshape(1, -1).to("cuda:0")
+    x = rl.expand(t2, s0)
+    rl.expand(t2, x["succ"].contiguous())
+    r = search.brfs(t2, **exp["options"])
+    assert (r.states, r.generated, r.fingerprint) == (exp["states"], exp["generated"], exp["fingerprint"])
+    _, cid = t2.slot_records()
+    assert atoms_of(cid, [r.goal_state])[0] == exp["goal_cids"]
