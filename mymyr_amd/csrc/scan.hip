@@ -227,14 +227,30 @@ __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ fla
     u64 off = sums[blockIdx.x] + excl;
     const u64 id0 = base ? *base : 0;
     const u32 w[4] = {v.x, v.y, v.z, v.w};
+    // a full thread writes all 16 of its id_of entries (a loser's is never read: only winners hold table entries), as
+    // four whole 16-byte stores instead of a scattered 4-byte store per winner
+    // (first is a multiple of 16 entries, so the id map's base decides the 16-byte alignment of every thread's stores)
+    const bool whole = id_of && full && (reinterpret_cast<uintptr_t>(id_of) & 15) == 0;
+    u32 ids[kFlagsPerThread];
 #pragma unroll
     for (int k = 0; k < kFlagsPerThread; ++k)
+    {
+        ids[k] = ~0u;
         if ((w[k / 4] >> (8 * (k % 4))) & 1)
         {
-            if (id_of)
-                id_of[first + k] = static_cast<u32>(id0 + off);
+            ids[k] = static_cast<u32>(id0 + off);
+            if (id_of && !whole)
+                id_of[first + k] = ids[k];
             list[off++] = static_cast<u32>(first + k);
         }
+    }
+    if (whole)
+    {
+        uint4* d = reinterpret_cast<uint4*>(id_of + first);
+#pragma unroll
+        for (int k = 0; k < kFlagsPerThread / 4; ++k)
+            d[k] = uint4{ids[4 * k], ids[4 * k + 1], ids[4 * k + 2], ids[4 * k + 3]};
+    }
     if (full)
     {
         if (s != kFlagsPerThread)
