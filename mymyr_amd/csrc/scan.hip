@@ -212,19 +212,42 @@ __global__ __launch_bounds__(kScanBlock) void k_flag_sums(const u8* __restrict__
 }
 
 // The winners' indices in order (list[rank] = j for flags[j] != 0), their ids base + rank into id_of[j] (optional),
-// is_new[j] = flags[j] (optional), and the losers' flags reset to 1.
+// is_new[j] = flags[j] (optional), and the losers' flags reset to 1. kFused: `sums` holds the raw block sums, each
+// block adds up those before it itself (few blocks), and the last block writes *total = *base + the grand total;
+// else `sums` holds their exclusive scan.
+template<bool kFused>
 __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ flags, u64 n, const u64* __restrict__ sums,
                                                            const u64* __restrict__ base, u32* __restrict__ list,
-                                                           u32* __restrict__ id_of, u8* __restrict__ is_new)
+                                                           u32* __restrict__ id_of, u8* __restrict__ is_new, u64* __restrict__ total_out)
 {
     __shared__ u32 lds[kScanBlock / kWave + 1];
+    __shared__ u64 pre[kScanBlock / kWave];
     const u64 first = static_cast<u64>(blockIdx.x) * kFlagsPerBlock + threadIdx.x * kFlagsPerThread;
     uint4 v;
     bool full;
     const u32 s = load_flags(flags, first, n, v, full);
+    u64 prefix;
+    if constexpr (kFused)
+    {
+        u64 part = 0;
+        for (u64 i = threadIdx.x; i < blockIdx.x; i += kScanBlock)
+            part += sums[i];
+        part = wave_sum64(part);
+        if (lane_id() == 0)
+            pre[threadIdx.x / kWave] = part;
+        __syncthreads();
+        prefix = 0;
+        for (int w = 0; w < kScanBlock / kWave; ++w)
+            prefix += pre[w];
+    }
+    else
+        prefix = sums[blockIdx.x];
     u32 total;
     const u32 excl = block_exclusive<kScanBlock>(s, lds, &total);
-    u64 off = sums[blockIdx.x] + excl;
+    if constexpr (kFused)
+        if (blockIdx.x + 1 == gridDim.x && threadIdx.x == 0)
+            *total_out = (base ? *base : 0) + prefix + total;
+    u64 off = prefix + excl;
     const u64 id0 = base ? *base : 0;
     const u32 w[4] = {v.x, v.y, v.z, v.w};
     // a full thread writes all 16 of its id_of entries (a loser's is never read: only winners hold table entries), as
@@ -272,12 +295,21 @@ void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* t
                         hipStream_t stream)
 {
     const u64 nb = (n + kFlagsPerBlock - 1) / kFlagsPerBlock;
+    // up to 1024 blocks (2^22 flags), each block adds up the block sums before it (at most 8 KiB, from L2) instead of a
+    // third launch scanning them
+    constexpr u64 kFusedBlocks = 1024;
     if (nb > 0)
         hipLaunchKernelGGL(k_flag_sums, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch);
+    if (nb > 0 && nb <= kFusedBlocks)
+    {
+        hipLaunchKernelGGL(k_winner_list<true>, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, total_base, list,
+                           id_of, is_new, total);
+        return;
+    }
     hipLaunchKernelGGL(k_scan_sums_rel, dim3(1), dim3(1024), 0, stream, scratch, nb, total, total_base);
     if (nb > 0)
-        hipLaunchKernelGGL(k_winner_list, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, total_base, list,
-                           id_of, is_new);
+        hipLaunchKernelGGL(k_winner_list<false>, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, total_base,
+                           list, id_of, is_new, total);
 }
 
 void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream, const u64* base)
