@@ -39,7 +39,7 @@ def affinity() -> int:
 
 
 def cpu_threads() -> int:
-    """The cores allotted to this job: OMP_NUM_THREADS when the launcher sets it (a GPU box's CPU share per GPU), else
+    """The cores allotted to this job: OMP_NUM_THREADS when the launcher sets it (the host's CPU share of one GPU), else
     every core of the process's affinity."""
     try:
         n = int(os.environ.get("OMP_NUM_THREADS", "0"))

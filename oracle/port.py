@@ -1,6 +1,6 @@
 """Test infrastructure, not product code: a CPU restatement of the reference algorithm of the state-expansion path
 (maichmueller/mymyr), written from the reference's semantics in plain Python with numpy for row arithmetic. Only
-tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, as the checker; the product never imports it.
+tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, to check results; the product never imports it.
 
 Every function cites the reference file:line it restates. How each part is pinned (tests/test_oracle.py):
   hash_words / hash_state / mix64   closed form (include/mymyr/core/hash.hpp:12-60) + the compiled reference

@@ -1,7 +1,7 @@
 """Test infrastructure, not product code: ctypes binding of oracle/_ref/libmymyr_ref.so, the reference CPU core
 (maichmueller/mymyr) compiled from its own sources by oracle/Makefile, with the harness oracle/ref_harness.cpp.
 
-Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, as the checker or the timed CPU
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it, to check results or as the timed CPU
 baseline; the product never imports it.
 """
 
