@@ -204,6 +204,17 @@ void with_shape(u32 W, F&& f)
         throw std::invalid_argument("mymyr_amd: state set rows hold at most 2048 words");
 }
 
+/// The lane-group shape of the compaction: the probe's, except that rows of 9-16 words are copied by eight lanes of
+/// one word pair (their probe takes four lanes of two).
+template<class F>
+void with_copy_shape(u32 W, F&& f)
+{
+    if (W > 8 && W <= 16)
+        f.template operator()<8, 1>();
+    else
+        with_shape(W, f);
+}
+
 template<int G>
 unsigned group_blocks(u64 n)
 {
@@ -374,8 +385,11 @@ void state_set_insert(StateSet& s, const u64* rows, u64 n, i64* ids, u8* is_new,
                                s.flags, s.d_status, BlockedView{});
             launch_check("state set probe");
             state_set_rank(s, m, stream, is_new ? is_new + done : nullptr);
-            hipLaunchKernelGGL((k_compact<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, r, s.list,
-                               state_set_size_now(s), state_set_size_next(s), s.max_states, is_new ? is_new + done : nullptr, s.d_status);
+            with_copy_shape(W, [&]<int G2, int K2>() {
+                hipLaunchKernelGGL((k_compact<G2, K2>), dim3(group_blocks<G2>(m)), dim3(kBlock), 0, stream, s.v, r, s.list,
+                                   state_set_size_now(s), state_set_size_next(s), s.max_states, is_new ? is_new + done : nullptr,
+                                   s.d_status);
+            });
             launch_check("state set compact");
             if (ids)
             {
