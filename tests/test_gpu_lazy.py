@@ -153,3 +153,17 @@ def test_lazy_task_searched_again(golden):
     assert (r.states, r.generated, r.fingerprint) == (exp["states"], exp["generated"], exp["fingerprint"])
     _, cid = t2.slot_records()
     assert atoms_of(cid, [r.goal_state])[0] == exp["goal_cids"]
+
+
+def test_lazy_search_refuses_witness_pruning_over_witness_parameters(golden):
+    """A lazy task's search runs over the lifted expansion, which prunes no witness parameters: a task whose schemas have
+    one is refused with witness pruning on, as wide rows are."""
+    from mymyr_amd import search
+    from mymyr_amd._lib import MyaError
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("rovers__p02"), "lazy")
+    with pytest.raises(MyaError, match="witness"):
+        search.brfs(t, stop_at_goal=False, max_states=1000)
+    r = search.brfs(t, stop_at_goal=False, max_states=1000, witness_pruning=False)
+    assert r.states == 1000 and r.status == "out_of_states"
