@@ -167,3 +167,35 @@ def test_lazy_search_refuses_witness_pruning_over_witness_parameters(golden):
         search.brfs(t, stop_at_goal=False, max_states=1000)
     r = search.brfs(t, stop_at_goal=False, max_states=1000, witness_pruning=False)
     assert r.states == 1000 and r.status == "out_of_states"
+
+
+@pytest.mark.parametrize("key", ["transport:cut", "transport:depth2", "transport_w20_3:cut", "transport_w20_7:expanded",
+                                 "transport_w20_7:goal"])
+def test_lazy_wide_rows_equal_the_frozen_reference(golden, key):
+    """Transport tasks of 20 and 176 words loaded with lazy slots: the rows start at 1 to 4 words and widen several times
+    (every stored state moved to the wider set in id order) while the search runs to a max_states cut, a depth bound,
+    an expansion budget or a goal. Counts, fingerprints and plans do not depend on the slots, so they equal the
+    compiled reference's over the frozen task (tests/golden/brfs_wide.json), and the goal state holds the same atoms."""
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    exp = golden.load("brfs_wide.json")[key]
+    name = key.split(":")[0]
+    print(f"lazy wide brfs: {key}", flush=True)
+    t = Task.from_text_file(golden.task_path(name), "lazy")
+    words0 = t.words
+    r = search.brfs(t, fingerprint=True, **exp["options"])
+    got = {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
+           "layers": r.layers, "fingerprint": r.fingerprint, "layer_counts": r.layer_counts, "exhausted": r.exhausted,
+           "solved": r.solved}
+    bad = {k: (got[k], exp[k]) for k in KEYS if got[k] != exp[k]}
+    assert not bad, (key, bad)
+    assert r.status == STATUS[exp["status"]]
+    assert t.words > words0
+    if exp["solved"]:
+        assert [[a.schema, *a.binding] for a in r.plan] == exp["plan"] and r.cost == exp["cost"]
+        frozen = Task.from_text_file(golden.task_path(name), "auto")
+        _, fcid = frozen.slot_records()
+        _, lcid = t.slot_records()
+        want = np.array([int(x, 16) for x in exp["goal_state"]], dtype=np.uint64)
+        assert atoms_of(lcid, [r.goal_state])[0] == atoms_of(fcid, [want])[0]
