@@ -269,6 +269,39 @@ def copy_calibration(steps: int):
                       "gbs": 2 * n * 4 / (ms * 1e-3) / 1e9}))
 
 
+def random_ops(steps: int):
+    """The random 8-byte operation rates that bound the state set's probes (mya_random_ops): loads, compare-and-swaps,
+    atomic mins and stores at seeded random addresses of a 1 GiB table (in HBM) and of a 256 MiB one (the Infinity
+    Cache's size), 2^28 operations each, HIP-event timed; one JSON line."""
+    import torch
+
+    from mymyr_amd._lib import check, lib
+
+    n = 1 << 28
+    sink = torch.empty(1 << 20, dtype=torch.int64, device="cuda")
+    out = {}
+    for label, words in (("1 GiB", 1 << 27), ("256 MiB", 1 << 25)):
+        table = torch.zeros(words, dtype=torch.int64, device="cuda")
+        rates = {}
+        for kind, name in enumerate(("load", "cas", "atomic_min", "store")):
+            best = None
+            for it in range(steps + 1):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                check(lib.mya_random_ops(table.data_ptr(), words, n, kind, 12345 + it, sink.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream))
+                b.record()
+                torch.cuda.synchronize()
+                if it:
+                    ms = a.elapsed_time(b)
+                    best = ms if best is None else min(best, ms)
+            rates[name] = round(n / (best * 1e-3) / 1e9, 2)
+        out[label] = rates
+        del table
+    print(json.dumps({"metric": "random 8-byte operations per second (G/s), 2^28 per launch, 4 in flight per thread",
+                      "threads": 1 << 20, "random_ops": out}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -278,6 +311,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (the reference kernel for scaling PMC byte counters)")
+    ap.add_argument("--random-ops", action="store_true",
+                    help="run only the random 8-byte load / CAS / atomic-min / store rates (the state set's ceilings)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for {a.gpus}); the env pool shards by env range and the "
@@ -291,6 +326,9 @@ def main():
     torch.cuda.set_device(0)
     if a.copy_calibration:
         copy_calibration(max(1, a.steps))
+        return
+    if a.random_ops:
+        random_ops(max(1, a.steps))
         return
     only = set(x for x in a.only.split(",") if x)
     cpu = not a.no_cpu

@@ -129,6 +129,14 @@ int mya_hashset_clear(mya_hashset* set, void* stream);
  * mix64(seed + (16 i + k + 1) * 0x9E3779B97F4A7C15). out [count, words]: device. Async on the stream. */
 int mya_dedup_rows(uint64_t start, uint64_t count, uint32_t words, uint64_t seed, double dup, uint64_t* out, void* stream);
 
+/* No reference counterpart: the random-access rates the state set's probes are bound by, for measurement. n operations
+ * of one kind (0 load, 1 compare-and-swap, 2 atomic min, 3 store; the atomics' old values are used, as the probes use
+ * them) on 8-byte words at seeded random addresses of table [words] (device; words a power of two), 4 independent
+ * operations per thread in flight over MYA_RANDOM_OPS_THREADS threads, whose folded load and atomic results go to
+ * sink [MYA_RANDOM_OPS_THREADS] (device). Async on the stream. */
+#define MYA_RANDOM_OPS_THREADS 1048576u
+int mya_random_ops(uint64_t* table, uint64_t words, uint64_t n, int kind, uint64_t seed, uint64_t* sink, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------- env */
 
 /* EnvConfig (include/mymyr/rl/env.hpp:76-92), index action space. dead_end: 0 no_successors, 1 none.

@@ -257,6 +257,7 @@ def _load() -> ctypes.CDLL:
         "mya_hashset_rows": (c_int, [c_void_p, POINTER(c_void_p)]),
         "mya_hashset_clear": (c_int, [c_void_p, c_void_p]),
         "mya_dedup_rows": (c_int, [c_uint64, c_uint64, c_uint32, c_uint64, c_double, c_void_p, c_void_p]),
+        "mya_random_ops": (c_int, [c_void_p, c_uint64, c_uint64, c_int, c_uint64, c_void_p, c_void_p]),
         "mya_buffer_create": (c_int, [c_uint64, POINTER(c_void_p)]),
         "mya_buffer_data": (c_void_p, [c_void_p]),
         "mya_buffer_bytes": (c_uint64, [c_void_p]),

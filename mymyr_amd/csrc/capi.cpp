@@ -298,6 +298,19 @@ int mya_dedup_rows(uint64_t start, uint64_t count, uint32_t words, uint64_t seed
     });
 }
 
+int mya_random_ops(uint64_t* table, uint64_t words, uint64_t n, int kind, uint64_t seed, uint64_t* sink, void* stream)
+{
+    return guarded([&] {
+        if (!table || !sink)
+            throw std::invalid_argument("mymyr_amd: random_ops: null array");
+        if (words == 0 || (words & (words - 1)))
+            throw std::invalid_argument("mymyr_amd: random_ops: the table's words must be a power of two");
+        if (kind < 0 || kind > 3)
+            throw std::invalid_argument("mymyr_amd: random_ops: kind must be 0 (load), 1 (CAS), 2 (atomic min) or 3 (store)");
+        launch_random_ops(table, words, n, kind, seed, sink, static_cast<hipStream_t>(stream));
+    });
+}
+
 int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts, uint32_t cap,
              mya_brfs_plan* plan)
 {

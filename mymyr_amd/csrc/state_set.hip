@@ -176,6 +176,41 @@ __global__ __launch_bounds__(kBlock) void k_dedup_rows(u64 start, u64 count, u32
     out[t] = mix64(seed + (cur * 16 + k + 1) * kGamma);
 }
 
+/// n random 8-byte operations of kind kKind (0 load, 1 CAS, 2 atomicMin, 3 store) on table[mix64(seed + i * gamma) & mask],
+/// four independent ones per thread in flight; the loads' and atomics' results fold into sink[thread].
+template<int kKind>
+__global__ __launch_bounds__(kBlock) void k_random_ops(u64* __restrict__ table, u64 mask, u64 n, u64 seed, u64* __restrict__ sink)
+{
+    constexpr int kIn = 4;
+    const u64 t = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x;
+    const u64 threads = static_cast<u64>(gridDim.x) * kBlock;
+    u64 acc = 0;
+    for (u64 i0 = t * kIn; i0 < n; i0 += threads * kIn)
+    {
+        u64 a[kIn];
+#pragma unroll
+        for (int k = 0; k < kIn; ++k)
+            a[k] = mix64(seed + (i0 + k) * kGamma) & mask;
+#pragma unroll
+        for (int k = 0; k < kIn; ++k)
+        {
+            if (i0 + k >= n)
+                break;
+            unsigned long long* p = reinterpret_cast<unsigned long long*>(table + a[k]);
+            if constexpr (kKind == 0)
+                acc ^= *p;
+            else if constexpr (kKind == 1)
+                acc ^= atomicCAS(p, 0ull, static_cast<unsigned long long>(a[k] | 1));
+            else if constexpr (kKind == 2)
+                acc ^= atomicMin(p, static_cast<unsigned long long>(~a[k]));
+            else
+                *p = i0 + k;
+        }
+    }
+    if constexpr (kKind != 3)
+        sink[t] = acc;
+}
+
 /// Calls f.template operator()<G, K>() for the lane-group shape of rows of W words.
 template<class F>
 void with_shape(u32 W, F&& f)
@@ -228,6 +263,21 @@ void launch_fill_u32(u32* p, u64 n, u32 v, hipStream_t stream)
         return;
     hipLaunchKernelGGL(k_fill_u32, dim3(std::min<u64>(blocks_for(n, kBlock), 8192)), dim3(kBlock), 0, stream, p, n, v);
     launch_check("fill");
+}
+
+void launch_random_ops(u64* table, u64 words, u64 n, int kind, u64 seed, u64* sink, hipStream_t stream)
+{
+    const dim3 grid(kRandomOpsThreads / kBlock), block(kBlock);
+    const u64 mask = words - 1;
+    if (kind == 0)
+        hipLaunchKernelGGL(k_random_ops<0>, grid, block, 0, stream, table, mask, n, seed, sink);
+    else if (kind == 1)
+        hipLaunchKernelGGL(k_random_ops<1>, grid, block, 0, stream, table, mask, n, seed, sink);
+    else if (kind == 2)
+        hipLaunchKernelGGL(k_random_ops<2>, grid, block, 0, stream, table, mask, n, seed, sink);
+    else
+        hipLaunchKernelGGL(k_random_ops<3>, grid, block, 0, stream, table, mask, n, seed, sink);
+    launch_check("random ops");
 }
 
 void launch_dedup_rows(u64 start, u64 count, u32 words, u64 seed, double dup, u64* out, hipStream_t stream)

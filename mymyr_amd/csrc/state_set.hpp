@@ -86,6 +86,12 @@ void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t s
 /// Fills n u32 words with v.
 void launch_fill_u32(u32* p, u64 n, u32 v, hipStream_t stream);
 
+/// Threads of launch_random_ops (its sink's length).
+constexpr u64 kRandomOpsThreads = u64{1} << 20;
+/// n random 8-byte operations (0 load, 1 CAS, 2 atomicMin, 3 store) on table [words] (a power of two), results into
+/// sink [kRandomOpsThreads]: the random-access rates of the probes' memory operations.
+void launch_random_ops(u64* table, u64 words, u64 n, int kind, u64 seed, u64* sink, hipStream_t stream);
+
 /// Rows [start, start + count) of the seeded dedup stream (the dedup workload's synthetic input).
 void launch_dedup_rows(u64 start, u64 count, u32 words, u64 seed, double dup, u64* out, hipStream_t stream);
 }  // namespace mya
