@@ -88,7 +88,8 @@ MYA_HD Block4 philox4x32_10(Block4 c, u32 k0, u32 k1)
     return c;
 }
 
-/// 64 random bits of (seed; draw, env, purpose): the block's first two words, low first.
+/// Philox over the counter (draw low, draw high, env low, purpose) with the seed's halves as key; output words 0 and 1
+/// joined into one 64-bit value (word 0 in the low half).
 MYA_HD u64 philox_bits64(u64 seed, u64 env, u64 draw, u32 purpose)
 {
     const Block4 b = philox4x32_10(Block4{{static_cast<u32>(draw), static_cast<u32>(draw >> 32), static_cast<u32>(env), purpose}},
@@ -96,7 +97,8 @@ MYA_HD u64 philox_bits64(u64 seed, u64 env, u64 draw, u32 purpose)
     return static_cast<u64>(b.v[0]) | (static_cast<u64>(b.v[1]) << 32);
 }
 
-/// high64(x * n) from 32x32-bit partial products: an index in [0, n).
+/// Lemire's multiply-shift reduction of a 64-bit draw onto [0, n): the upper 64 bits of the 128-bit product x * n,
+/// assembled from x's two 32-bit halves so that host and device compute the same value.
 MYA_HD u32 below(u64 x, u32 n)
 {
     const u64 hi = (x >> 32) * n, lo = (x & 0xFFFFFFFFull) * n;
@@ -114,16 +116,16 @@ MYA_HD u32 fmix32(u32 x)
     return x ^ (x >> 16);
 }
 
-/// The instance of env `env`'s draw number `reset_count` under `seed` (rl::rng::instance_draw,
-/// include/mymyr/rl/rng.hpp:94-115): a hash of the inputs; uniform over `instances` when m is 0, else indices[k] with k
-/// the number of the m - 1 ascending thresholds at most the draw's 32 bits.
+/// Which instance an env restarts in (rl::rng::instance_draw, include/mymyr/rl/rng.hpp:94-115). The seed, the env
+/// number and its reset count are mixed into 32 bits; with m == 0 they scale uniformly onto [0, instances), otherwise
+/// the draw selects indices[k], k being how many of the m - 1 sorted thresholds do not exceed it.
 MYA_HD i32 instance_draw(u64 seed, u64 env, u32 reset_count, u32 instances, const u32* thresholds, const i32* indices, u32 m)
 {
     const u32 key = fmix32(static_cast<u32>(seed) ^ fmix32(static_cast<u32>(seed >> 32) ^ 0x53414D50u));
     const u32 bits = fmix32(key ^ fmix32(static_cast<u32>(env)) ^ fmix32(reset_count ^ 0x9E3779B9u));
     if (m == 0)
         return static_cast<i32>((static_cast<u64>(bits) * instances) >> 32);
-    u32 lo = 0, hi = m - 1;  // the first threshold above the draw
+    u32 lo = 0, hi = m - 1;  // bisection for the first threshold greater than bits
     while (lo < hi)
     {
         const u32 mid = lo + (hi - lo) / 2;
