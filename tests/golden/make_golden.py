@@ -492,7 +492,8 @@ def make_brfs(quick: bool):
     dump("brfs.json", out)
 
 
-LAZY_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "pegsol-08-strips__p22", "visitall__visitall_x-6_y-3_r-100"]
+LAZY_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "pegsol-08-strips__p22", "visitall__visitall_x-6_y-3_r-100",
+              "miconic__s7-4", "logistics00__probLOGISTICS-6-1", "driverlog__p03", "rovers__p02"]
 
 
 def goal_cids(t, words_hex):
@@ -528,7 +529,7 @@ def make_lazy():
     """Lazy atom slots: the slot table right after loading (the initial state's atoms in its atom order), and BrFS runs
     whose states' atoms intern as the search meets them (exhaustive, to the first goal, and a max_states cut)."""
     out = {"initial": {}, "brfs": {}}
-    for name in LAZY_TASKS + ["transport_w20_3", "rovers__p02", "transport"]:
+    for name in LAZY_TASKS + ["transport_w20_3", "transport"]:
         t = ref.RefTask(fx.task_path(name), "lazy")
         rec, cid = t.slot_records()
         out["initial"][name] = {"words": t.words, "slots": t.fluent_slots, "cid": [int(x) for x in cid],
