@@ -732,6 +732,30 @@ __device__ __forceinline__ u32 count_all(const TaskDev& T, const auto& H, const 
     return total;
 }
 
+/// The successor counts after a move by an action of schema `applied` from the state whose counts L.counts holds: a
+/// schema the action cannot affect (DevSchema::affects) keeps its count, the others are counted again.
+template<bool kLevels>
+__device__ __forceinline__ u32 count_after(const TaskDev& T, const auto& H, const Lds& L, u32 lane, u32 applied)
+{
+    const u32 mask = H.schemas[applied].affects;
+    u32 total = 0;
+    for (u32 s = 0; s < T.num_schemas; ++s)
+    {
+        u32 c;
+        if (s >= 32 || ((mask >> s) & 1))
+        {
+            c = schema_count<kLevels>(T, H, L, s, lane);
+            if (lane == 0)
+                L.counts[s] = c;
+        }
+        else
+            c = L.counts[s];
+        total += c;
+    }
+    wave_sync();
+    return total;
+}
+
 /// The per-env goal test (mask_goal, src/mymyr/rl/env.cpp:55-61): the LDS row against a row of goal masks.
 __device__ __forceinline__ bool mask_goal(const lds<u64>* row, const u64* gp, const u64* gn, u32 W, u32 lane)
 {
@@ -1548,7 +1572,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     bool g = already_goal;
     for (u32 phase = 0; phase < 2; ++phase)
     {
-        const u32 cc = (phase == 0 && cached) ? load_counts(T, L, crow, lane) : count_all<kLevels>(T, H, L, lane);
+        const u32 cc = (phase == 1 && T.num_schemas > 1) ? count_after<kLevels>(T, H, L, lane, schema)
+                       : ((phase == 0 && cached) ? load_counts(T, L, crow, lane) : count_all<kLevels>(T, H, L, lane));
         if (phase == 1)
         {
             c2 = cc;

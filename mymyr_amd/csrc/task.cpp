@@ -1219,6 +1219,48 @@ private:
                 ds.nadd += l.positive ? 1 : 0;
             schemas.push_back(ds);
         }
+        // which schemas' successor counts an action of schema a can change: an add or delete effect of a that can be an
+        // atom of a fluent precondition literal of s (the same predicate, and at every position the two terms can take
+        // a common object: a constant, or a parameter's static domain); a schema no action of a can touch keeps its
+        // count across the move. With more than 32 schemas every schema counts as changed.
+        {
+            const u32 S = static_cast<u32>(schemas.size());
+            auto dom_of = [&](u32 si, i32 t) {
+                Bits b(ow, 0);
+                if (t < 0)
+                    set_bit(b, term_object(t));
+                else
+                    b = C->dom0[si][static_cast<u32>(t)];
+                return b;
+            };
+            auto meet = [](const Bits& x, const Bits& y) {
+                for (size_t w = 0; w < x.size() && w < y.size(); ++w)
+                    if (x[w] & y[w])
+                        return true;
+                return false;
+            };
+            for (u32 a = 0; a < S; ++a)
+            {
+                u32 mask = S > 32 ? ~0u : 0u;
+                for (u32 s2 = 0; s2 < S && S <= 32; ++s2)
+                {
+                    bool hit = false;
+                    for (const Literal& e : T->schemas[a].eff)
+                        for (const Literal& l : T->schemas[s2].pre)
+                        {
+                            if (hit || l.pred != e.pred || T->preds[l.pred].kind != 'F' || l.terms.size() != e.terms.size())
+                                continue;
+                            bool all = true;
+                            for (size_t i = 0; i < l.terms.size() && all; ++i)
+                                all = meet(dom_of(a, e.terms[i]), dom_of(s2, l.terms[i]));
+                            hit = all;
+                        }
+                    if (hit)
+                        mask |= 1u << s2;
+                }
+                schemas[a].affects = mask;
+            }
+        }
 
         // view pairs: windows and offsets
         std::vector<DevPair> pairs;

@@ -207,7 +207,7 @@ struct DevSchema
     u32 filter_step[kMaxParams];     // the DevStep of filter i
     u32 eff_begin, eff_end;          // into effects
     u32 nadd;                        // effects [eff_begin, eff_begin + nadd) add, the rest delete
-    u32 pad;
+    u32 affects;  // bit s: an action of this schema can change schema s's successor count (every bit past 32 schemas)
 };
 
 /// An effect pattern: cid = base + sum over parameter terms of rs[pos][object].
