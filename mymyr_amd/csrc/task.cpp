@@ -1804,8 +1804,10 @@ std::vector<std::pair<u64, u64>> intern_atoms(CompiledTask& C, const std::vector
     C.words = std::max<u32>(1, words_for(C.fluent_slots));
     C.initial.resize(C.words, 0);
     resolve_goal(C);
-    std::memcpy(reinterpret_cast<u32*>(C.image.data() + h.off_goal_pos), C.goal_pos.data(), C.goal_pos.size() * sizeof(u32));
-    std::memcpy(reinterpret_cast<u32*>(C.image.data() + h.off_goal_neg), C.goal_neg.data(), C.goal_neg.size() * sizeof(u32));
+    if (!C.goal_pos.empty())
+        std::memcpy(reinterpret_cast<u32*>(C.image.data() + h.off_goal_pos), C.goal_pos.data(), C.goal_pos.size() * sizeof(u32));
+    if (!C.goal_neg.empty())
+        std::memcpy(reinterpret_cast<u32*>(C.image.data() + h.off_goal_neg), C.goal_neg.data(), C.goal_neg.size() * sizeof(u32));
     h.words = C.words;
     h.fluent_slots = C.fluent_slots;
     h.num_goal_pos = static_cast<u32>(C.goal_pos.size());
