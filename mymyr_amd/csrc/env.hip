@@ -1343,8 +1343,9 @@ __device__ __forceinline__ bool goal_test(const TaskDev& T, const auto& H, P row
 /// Applies the effects of the picked binding of schema s to the LDS row and the view: delete, then add. One effect per
 /// lane: its slot (the table reads of the effects overlap instead of following each other), then the deletes, the adds,
 /// and the view bits of the atoms whose bit changed. View pairs exist for predicates of arity 1 and 2 only, so a view bit
-/// stands for one atom: lanes that list the same slot write the same value.
-__device__ __forceinline__ void apply_effects(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane, u32* status)
+/// stands for one atom: lanes that list the same slot write the same value. Returns the lane's effect slot (kNone: no
+/// effect or no slot): the row words that can have changed are the words of these slots.
+__device__ __forceinline__ u32 apply_effects(const TaskDev& T, const auto& H, const Lds& L, u32 s, u32 lane, u32* status)
 {
     const auto& S = H.schemas[s];
     const u32 ne = min(S.eff_end - S.eff_begin, kMaxEff);
@@ -1385,6 +1386,7 @@ __device__ __forceinline__ void apply_effects(const TaskDev& T, const auto& H, c
         }
     }
     wave_sync();
+    return sl;
 }
 
 /// Whether the task's hot tables are staged in LDS.
@@ -1569,6 +1571,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     };
     // phase 0 counts s, chooses, picks and moves; phase 1 counts the reached state s' (one copy of the count)
     u32 c = 0, c2 = 0, st = kOk, schema = kNone;
+    u32 moved_slot = kNone;  // the lane's effect slot of the applied move (its word is the only one it can change)
     bool g = already_goal;
     for (u32 phase = 0; phase < 2; ++phase)
     {
@@ -1649,7 +1652,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (st != kOk)
             break;
         // 3. the move, goal and (next phase) the successor count of the reached state
-        apply_effects(T, H, L, schema, lane, A.status);
+        moved_slot = apply_effects(T, H, L, schema, lane, A.status);
         g = A.goal_pos ? mask_goal(L.row, A.goal_pos + i * A.words, A.goal_neg + i * A.words, T.W, lane)
                        : goal_test(T, H, L.row, lane);
     }
@@ -1751,7 +1754,16 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     }
     else
     {
-        if (st == kOk)
+        // a move changes only the words of its effects' slots. The level-synchronous kernel (wide candidate windows,
+        // rows of up to thousands of words) writes back just those, one per effect lane (lanes sharing a word write the
+        // same value); the split kernel copies its row whole, which keeps the slot out of the registers it holds
+        // across the count of s' (an extra live value there costs it more than the few stores)
+        if constexpr (kLevels)
+        {
+            if (st == kOk && moved_slot != kNone)
+                grow[moved_slot >> 6] = L.row[moved_slot >> 6];
+        }
+        else if (st == kOk)
             for (u32 q = lane; q < T.W; q += kWave)
                 grow[q] = L.row[q];
         if (lane == 0)
