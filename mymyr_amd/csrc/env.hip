@@ -1198,12 +1198,99 @@ __device__ __forceinline__ void for_view_bits(const auto& H, const Lds& L, u32 p
     }
 }
 
-/// Builds the view of the wave's row (all lanes).
+/// Builds the view of the wave's row (all lanes). With kByPredicate and arithmetic slot decoding the row is read
+/// predicate by predicate: only the slot ranges of predicates with scattered view rows, each with its decoding and its
+/// two pairs read once (the level-synchronous kernels, whose wide rows hold many atoms); otherwise every set bit is
+/// decoded on its own (the split kernels keep this shorter code: the other costs them registers for little).
+template<bool kByPredicate>
 __device__ __forceinline__ void build_view(const TaskDev& T, const auto& H, const Lds& L, u32 lane)
 {
     for (u32 k = lane; k < T.view_words; k += kWave)
         L.view[k] = 0;
     wave_sync();
+    if (kByPredicate && T.decode_arith)
+    {
+        for (u32 k = 0; k < T.num_decode; ++k)
+        {
+            const DevPredDecode d = ld(H.decode + k);
+            const u64 end = min(d.offset + d.size, static_cast<u64>(T.fluent_slots));
+            if (!d.has_scatter || end <= d.offset)
+                continue;
+            // the predicate's scattered pairs: forward (or unary) and backward
+            const u64 pp = H.pred_pairs[d.pred];
+            const u32 ar = H.pred_arity[d.pred];
+            u32 on[2], off[2], src_lo[2], dst_lo[2], dst_words[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+            {
+                const u32 pi = q == 0 ? static_cast<u32>(pp) : static_cast<u32>(pp >> 32);
+                on[q] = 0;
+                off[q] = src_lo[q] = dst_lo[q] = dst_words[q] = 0;
+                if (pp != ~u64{0} && pi != kNone)
+                {
+                    const DevPair P = ld(H.pairs + pi);
+                    on[q] = P.bulk ? 0 : 1;
+                    off[q] = P.offset;
+                    src_lo[q] = P.src_lo;
+                    dst_lo[q] = P.dst_lo;
+                    dst_words[q] = P.dst_words;
+                }
+            }
+            const u32 w0 = static_cast<u32>(d.offset >> 6), w1 = static_cast<u32>((end - 1) >> 6);
+            for (u32 w = w0 + lane; w <= w1; w += kWave)
+            {
+                u64 x = L.row[w];
+                if (w == w0)
+                    x &= ~u64{0} << (d.offset & 63);
+                if (w == w1 && (end & 63))
+                    x &= (u64{1} << (end & 63)) - 1;
+                while (x)
+                {
+                    const u32 rem = static_cast<u32>(w * 64 + static_cast<u32>(__builtin_ctzll(x)) - d.offset);
+                    x &= x - 1;
+                    u32 a0, a1;
+                    if (d.arity >= 2)
+                    {
+                        const u32 r0 = rem / d.d1;
+                        a0 = d.lo0 + r0;
+                        a1 = d.lo1 + (rem - r0 * d.d1);
+                    }
+                    else
+                    {
+                        a0 = d.lo0 + rem;
+                        a1 = 0;
+                    }
+                    // the atom's bits in the pairs' rows, as for_view_bits places them
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                    {
+                        if (!on[q])
+                            continue;
+                        u32 ri, bi;
+                        if (ar == 1)
+                        {
+                            ri = 0;
+                            bi = a0 - dst_lo[q];
+                        }
+                        else if (q == 0)
+                        {
+                            ri = a0 - src_lo[q];
+                            bi = a1 - dst_lo[q];
+                        }
+                        else
+                        {
+                            ri = a1 - src_lo[q];
+                            bi = a0 - dst_lo[q];
+                        }
+                        __hip_atomic_fetch_or(L.view + off[q] + static_cast<u64>(ri) * dst_words[q] + (bi >> 6), u64{1} << (bi & 63),
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                    }
+                }
+            }
+        }
+        wave_sync();
+        return;
+    }
     for (u32 w = lane; w < T.W; w += kWave)
     {
         u64 x = L.row[w];
@@ -1557,7 +1644,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     u32* crow = A.counts ? A.counts + i * cw : nullptr;
     const u64 fp_cached = crow ? (static_cast<u64>(crow[cw - 2]) | (static_cast<u64>(crow[cw - 1]) << 32)) : 0;
     load_row_lds(T, L, grow, lane);
-    build_view(T, H, L, lane);
+    build_view<kLevels>(T, H, L, lane);
     const u64 salt = instance_salt(k);
     bool cached = false;
     if (crow)
@@ -1899,7 +1986,7 @@ template<bool kLevels>
 __device__ __forceinline__ void count_row(const CountArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane)
 {
     load_row_lds(T, L, A.states + i * A.words, lane);
-    build_view(T, H, L, lane);
+    build_view<kLevels>(T, H, L, lane);
     const u32 c = count_all<kLevels>(T, H, L, lane);
     bool g;
     if (A.goal_pos)
@@ -2384,7 +2471,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
             atomicOr(A.status, kStatusWideRow);
     }
     load_row_lds_n(T, L, src, min(A.words, T.W), lane);
-    build_view(T, H, L, lane);
+    build_view<kLevels>(T, H, L, lane);
     const u32 c = count_all<kLevels>(T, H, L, lane);
     if (A.pass == 0 && !A.drop_noops)
     {
@@ -2605,7 +2692,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_successors(TaskDev T, con
     for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < rows; i += static_cast<u64>(gridDim.x) * nw)
     {
         load_row_lds_n(T, L, states + i * words, min(words, T.W), lane);
-        build_view(T, H, L, lane);
+        build_view<kLevels>(T, H, L, lane);
         const u32 c = count_all<kLevels>(T, H, L, lane);
         if (lane == 0 && count)
             count[i] = static_cast<i32>(c);
