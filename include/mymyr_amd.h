@@ -32,8 +32,23 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 15
+#define MYA_ABI_VERSION 16
 int mya_abi_version(void);
+
+/* Device memory held by the library (replaces DeviceContext::usage(), include/mymyr/cuda/runtime.hpp:140-146, 183):
+ * freed blocks are kept for reuse, so `reserved` (bytes taken from the driver: handed out, idle, or waiting for a
+ * stream-ordered free) can exceed `used` (bytes handed out). `allocations` counts the device blocks the library has
+ * handed out (from its cache or the driver), `driver_allocations` its hipMalloc calls; both only grow. */
+typedef struct mya_memory_usage
+{
+    uint64_t reserved;
+    uint64_t used;
+    uint64_t reserved_high;
+    uint64_t used_high;
+    uint64_t allocations;
+    uint64_t driver_allocations;
+} mya_memory_usage;
+int mya_memory_usage_get(mya_memory_usage* out);
 
 /* ---------------------------------------------------------------------------------------------------------- tasks */
 
@@ -338,11 +353,12 @@ int mya_successors(mya_task* task, const uint64_t* states, uint64_t rows, uint32
  * counted, not written: generated (all successors) > capacity is the overflow. With drop_noops the no-op successors of
  * a row are removed unless all of its successors are no-ops (then all are kept), index gives each kept row's position
  * in its row's full order, and an overflow reports the counts before dropping (offsets[rows] == total == generated).
- * Successors in canonical order; witness pruning off. Synchronous: generated, total and words_needed are set on return. */
+ * Successors in canonical order, with witness pruning when asked. Synchronous: generated, total and words_needed are set on
+ * return. */
 typedef struct mya_expand_options
 {
     int32_t canonical_order; /* must be 1 */
-    int32_t witness_pruning; /* must be 0 */
+    int32_t witness_pruning; /* 1: one successor per effect-relevant binding (ExpandOptions::witness_pruning); 0 over a task table */
     int32_t validate;        /* reject rows with atoms past the task's slots */
     int32_t drop_noops;
 } mya_expand_options;
@@ -382,8 +398,8 @@ int mya_env_expand(mya_env* env, const uint64_t* states, const int32_t* task_ids
  * outputs and errors, and no device allocation or free: the expansion's scratch (about 7 MiB) is a static device array
  * that each device the library runs on holds until the process ends. The task must already have its device image on
  * the current device (any earlier call with the task that reaches the device, e.g. mya_expand of 0 rows, uploads it).
- * Calls are serialized within a process; they share the one array per device, so concurrent calls of several processes
- * on one device are not supported. Synchronous on `stream`, as mya_expand. */
+ * The calls of one process share its one array per device and run one at a time (a process-wide lock; each process
+ * that loads the library holds its own copies). Synchronous on `stream`, as mya_expand. */
 #define MYA_EXPAND_NOALLOC_MAX_ROWS 262144u
 int mya_expand_noalloc(mya_task* task, const uint64_t* states, uint64_t rows, uint32_t words, const mya_expand_options* options,
                        mya_expansion* out, void* stream);

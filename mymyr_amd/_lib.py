@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 15  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 16  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -158,6 +158,25 @@ class BrfsPlan(Structure):
     ]
 
 
+class MemoryUsage(Structure):
+    _fields_ = [
+        ("reserved", c_uint64),
+        ("used", c_uint64),
+        ("reserved_high", c_uint64),
+        ("used_high", c_uint64),
+        ("allocations", c_uint64),
+        ("driver_allocations", c_uint64),
+    ]
+
+
+def memory_usage() -> dict:
+    """The library's device memory figures (mya_memory_usage_get): reserved / used bytes, their high-water marks, and
+    the blocks handed out and taken from the driver so far."""
+    u = MemoryUsage()
+    check(lib.mya_memory_usage_get(ctypes.byref(u)))
+    return {k: int(getattr(u, k)) for k, _ in MemoryUsage._fields_}
+
+
 class ExpandOptions(Structure):
     _fields_ = [
         ("canonical_order", c_int32),
@@ -238,6 +257,7 @@ def _load() -> ctypes.CDLL:
     sigs = {
         "mya_last_error": (c_char_p, []),
         "mya_abi_version": (c_int, []),
+        "mya_memory_usage_get": (c_int, [POINTER(MemoryUsage)]),
         "mya_task_load_text": (c_int, [c_char_p, c_size_t, c_int, POINTER(c_void_p)]),
         "mya_task_load_file": (c_int, [c_char_p, c_int, POINTER(c_void_p)]),
         "mya_task_free": (None, [c_void_p]),

@@ -508,7 +508,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     hipStream_t stream = thread_stream();
     Timers tm(o.timings != 0, stream, r);
     constexpr u64 R = W * 8;  // row bytes
-    Buffers b;
+    Buffers b(stream);
 
     // ground tables and goal (device copies kept with the task)
     constexpr u32 S = 1;  // one count and one offset per parent
@@ -529,8 +529,9 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     struct SetGuard
     {
         StateSet& s;
-        ~SetGuard() { state_set_destroy(s); }
-    } setg{set};
+        hipStream_t st;
+        ~SetGuard() { state_set_destroy(s, st); }
+    } setg{set, stream};
     // per-layer arrays (grown with the largest layer): counts [parents * S] per (parent, slice), goal flags per parent,
     // successor offsets [parents * S + 1] (layer-relative candidate indices)
     u32* counts = nullptr;
@@ -549,14 +550,15 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         u8*& g;
         u64*& o;
         u64*& s;
+        hipStream_t st;
         ~LayerGuard()
         {
-            dev_free(c);
-            dev_free(g);
-            dev_free(o);
-            dev_free(s);
+            dev_free_async(c, st);
+            dev_free_async(g, st);
+            dev_free_async(o, st);
+            dev_free_async(s, st);
         }
-    } layer_guard{counts, goal_flags, offsets, scan_scratch};
+    } layer_guard{counts, goal_flags, offsets, scan_scratch, stream};
     // 32-bit candidate records: the action in the low abits bits, the parent relative to the chunk's first above them
     u32 abits = 1;
     while ((u64{1} << abits) < g.num_padded)

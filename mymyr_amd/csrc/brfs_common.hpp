@@ -96,8 +96,14 @@ __global__ void k_set_u64(u64* p, u64 v) { *p = v; }
 
 constexpr int kSmall = 16;  // device scalars of the driver
 
+/// A search's device buffers, freed in the order of its stream: a freed block is reused only once the work queued on
+/// the stream before the free has completed, so ending a search waits for nothing and stalls no other stream.
 struct Buffers
 {
+    explicit Buffers(hipStream_t s) : stream(s) {}
+    Buffers(const Buffers&) = delete;
+    Buffers& operator=(const Buffers&) = delete;
+    hipStream_t stream;
     std::vector<void*> owned;
     u64* host = nullptr;  // pinned mirror of the device scalars
     template<class T>
@@ -107,20 +113,25 @@ struct Buffers
         owned.push_back(p);
         return p;
     }
-    /// Frees one buffer of alloc() before the others (stream-ordered, as dev_free).
+    /// Frees one buffer of alloc() before the others (stream-ordered).
     void release(void* p)
     {
         const auto it = std::find(owned.begin(), owned.end(), p);
         if (it == owned.end())
             return;
         owned.erase(it);
-        dev_free(p);
+        dev_free_async(p, stream);
     }
     ~Buffers()
     {
         for (void* p : owned)
-            dev_free(p);
-        pinned_release(host);
+            dev_free_async(p, stream);
+        if (host)
+        {
+            // the pinned scalar block is handed to the next search only after this one's copies into it have landed
+            (void)hipStreamSynchronize(stream);
+            pinned_release(host);
+        }
     }
 };
 

@@ -10,8 +10,9 @@
 //            (parent id, successor index: the reference's discoverer keys, src/mymyr/search/brfs.cpp:1362-1388) and
 //            goal flags
 // Every stored state's goal flag is written when the state is stored, so a layer's goal test reads flags. Ids, counts,
-// cuts and statuses follow the ground driver (brfs.hip) and the reference's run_flat (brfs.cpp:274-404). The lifted
-// expansion takes witness pruning off; a task whose schemas have witness parameters needs witness_pruning off here.
+// cuts and statuses follow the ground driver (brfs.hip) and the reference's run_flat (brfs.cpp:274-404). With witness
+// pruning on (the reference's default, include/mymyr/search/brfs.hpp:76) the expansion keeps, per effect-relevant
+// binding of a schema with witness parameters, the one binding whose witnesses the reference's matcher finds first.
 
 #include "brfs.hpp"
 #include "brfs_common.hpp"
@@ -112,21 +113,6 @@ bool goal_holds(const CompiledTask& task, const std::vector<u64>& row)
     return true;
 }
 
-/// The name of a schema with a parameter that no effect mentions (a witness parameter), or "" if none has one.
-std::string witness_schema(const CompiledTask& task)
-{
-    for (const SchemaText& s : task.text.schemas)
-    {
-        std::vector<u8> rel(s.arity, 0);
-        for (const Literal& l : s.eff)
-            for (i32 x : l.terms)
-                if (x >= 0)
-                    rel[static_cast<u32>(x)] = 1;
-        if (std::find(rel.begin(), rel.end(), 0) != rel.end())
-            return s.name;
-    }
-    return "";
-}
 }  // namespace
 
 BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc,
@@ -135,20 +121,12 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
     TaskDev T = dev;  // lazy slots: refreshed after each interning
     const u32 TW0 = task.words;  // the width of the start and blocked rows
     u32 W = lazy ? lazy_row_words(TW0) : TW0;
-    if (o.witness_pruning)
-    {
-        const std::string ws = witness_schema(task);
-        if (!ws.empty())
-            throw std::invalid_argument("mymyr_amd: brfs: states of " + std::to_string(W) + " words are expanded by the lifted "
-                                        "successor generator, which does not prune witness parameters, and schema " + ws +
-                                        " has one (run with witness_pruning off)");
-    }
     BrfsResultC r;
     const auto t0 = Clock::now();
     hipStream_t stream = thread_stream();
     Timers tm(o.timings != 0, stream, r);
     u64 R = static_cast<u64>(W) * 8;
-    Buffers b;
+    Buffers b(stream);
     const bool bounded = o.max_states != ~u64{0};
     // unbounded searches: an arena of at most 32 GiB by default (lazy slots: for rows of the task's largest width)
     const u64 R_max = lazy ? static_cast<u64>(lazy_row_words(words_for(task.layout.fluent_count))) * 8 : R;
@@ -165,8 +143,9 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
     struct SetGuard
     {
         StateSet& s;
-        ~SetGuard() { state_set_destroy(s); }
-    } setg{set};
+        hipStream_t st;
+        ~SetGuard() { state_set_destroy(s, st); }
+    } setg{set, stream};
     const u64 layer_cap = cap_states;
     u32* counts = b.alloc<u32>(layer_cap, "layer counts");
     u64* offsets = b.alloc<u64>(layer_cap + 1, "layer offsets");
@@ -235,6 +214,9 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
     base_args.label_width = 0;
     base_args.status = xstatus + 1;
     base_args.words_needed = xstatus;
+    // witness pruning (the reference's default): one successor per effect-relevant binding, with the witnesses the
+    // matcher binds first (tasks whose schemas have no witness parameter expand the same either way)
+    base_args.witness = o.witness_pruning && T.witness ? 1 : 0;
     // lazy slots: the stored states move to a set of rows of nw words in id order (so their ids stay), a chunk at a
     // time through new candidate rows of that width; the blocked table follows the width
     auto widen = [&](u32 nw) {
@@ -253,7 +235,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
             if (nn != k)
                 throw std::logic_error("mymyr_amd: brfs: stored states merged when their rows were widened");
         }
-        state_set_destroy(set);
+        state_set_destroy(set, stream);
         set = grown;
         b.release(cand_rows);
         cand_rows = rows;

@@ -80,6 +80,16 @@ const char* mya_last_error(void) { return g_error.c_str(); }
 
 int mya_abi_version(void) { return MYA_ABI_VERSION; }
 
+int mya_memory_usage_get(mya_memory_usage* out)
+{
+    return guarded([&] {
+        if (!out)
+            throw std::invalid_argument("mymyr_amd: memory_usage_get: null argument");
+        const MemoryUsage u = memory_usage();
+        *out = mya_memory_usage{u.reserved, u.used, u.reserved_high, u.used_high, u.allocations, u.driver_allocations};
+    });
+}
+
 int mya_task_load_text(const char* text, size_t len, int atoms, mya_task** out)
 {
     return guarded([&] {

@@ -245,8 +245,10 @@ void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const in
     {
         if (!options || !out || (rows && !states))
             throw std::invalid_argument("mymyr_amd: expand: null argument");
-        if (!options->canonical_order || options->witness_pruning)
-            throw std::invalid_argument("mymyr_amd: expand: the device expansion takes canonical_order on and witness_pruning off");
+        if (!options->canonical_order)
+            throw std::invalid_argument("mymyr_amd: expand: the device expansion takes canonical_order on");
+        if (options->witness_pruning && inst.size() > 1)
+            throw std::invalid_argument("mymyr_amd: expand: the device expansion over a task table takes witness_pruning off");
         TaskDev T = *inst[0];  // the widest instance's words and label width stand for the table in the checks
         for (const TaskDev* t : inst)
         {
@@ -285,6 +287,7 @@ void expand_rows(const std::vector<const TaskDev*>& inst, mya_env* env, const in
         launch_fill_u32(words_status, 2, 0, stream);
         ExpandArgs a{};
         a.T = *inst[0];
+        a.witness = options->witness_pruning && a.T.witness ? 1 : 0;
         if (inst.size() > 1)
         {
             mya_env_batch b{};
@@ -475,8 +478,9 @@ void create_env(mya_task* const* tasks, uint32_t count, const mya_env_config* co
             }
             hip_check(hipMemcpy(hc.data(), cnt, count * sizeof(i32), hipMemcpyDeviceToHost), "initial counts");
             hip_check(hipMemcpy(hg.data(), gl, count * sizeof(u8), hipMemcpyDeviceToHost), "initial goals");
-            dev_free(cnt);
-            dev_free(gl);
+            // the synchronous copies above have drained the null stream: the blocks are free in its order
+            dev_free_async(cnt, nullptr);
+            dev_free_async(gl, nullptr);
         }
         std::vector<InstDev> hi(count);
         std::vector<TaskDev> ht(count);

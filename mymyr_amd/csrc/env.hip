@@ -38,6 +38,7 @@ TaskDev task_dev(const u64* img, const DevTaskHeader& h)
     t.static_meta = reinterpret_cast<const DevStaticMeta*>(img + h.off_static_meta);
     t.static_words = img;
     t.initial = img + h.off_initial;
+    t.witness = h.off_witness ? reinterpret_cast<const DevWitness*>(img + h.off_witness) : nullptr;
     t.fluent_count = h.fluent_count;
     t.hot_words = static_cast<u32>(h.hot_words);
     t.n = h.num_objects;
@@ -972,6 +973,48 @@ __device__ __forceinline__ bool label_applicable(const TaskDev& T, const auto& H
     return true;
 }
 
+/// Witness pruning (include/mymyr/successor/detail/engine.hpp:345-356): whether the witness objects of the full binding
+/// in L.ub are the ones the reference's matcher binds first for its effect-relevant objects, i.e. the first completion
+/// of the witnesses in the matcher's witness order, each witness taking its lowest object that the later ones can
+/// complete. Per witness t, lane b tests candidate b of each window word (its checks, then whether the count plan of
+/// the later witnesses finds a completion); the lowest passing candidate is the matcher's, and the binding is not the
+/// one emitted as soon as one differs. The lanes' binding columns hold L.ub again on return. Wave-uniform.
+__device__ __forceinline__ bool witness_first(const TaskDev& T, const auto& H, const Lds& L, const DevWitness* X, u32 arity, u32 lane)
+{
+    for (u32 q = 0; q < arity; ++q)
+        L.bind[q * 64 + lane] = L.ub[q];
+    const u32 n = X->n;
+    bool first = true;
+    for (u32 t = 0; t < n && first; ++t)
+    {
+        const u32 v = X->param[t];
+        const DevStep F = ld(H.steps + X->filter[t]);
+        const u32 lo = X->plan_lo[t], hi = X->plan_hi[t];
+        u32 found = kNone;
+        for (u32 w = 0; w < F.words && found == kNone; ++w)
+        {
+            const u64 m = cand_word(T, H, L, F, w, L.bind + lane, 64);
+            bool ok = false;
+            if ((m >> lane) & 1)
+            {
+                L.bind[v * 64 + lane] = F.lo + 64 * w + lane;
+                ok = F.check_begin == F.check_end || checks_ok(T, H, L, F.check_begin, F.check_end, L.bind + lane, 64);
+                if (ok && lo != hi)
+                    ok = count_from(T, H, L, lo, hi, lane) != 0;
+            }
+            const u64 okm = __ballot(ok);
+            if (okm)
+                found = F.lo + 64 * w + static_cast<u32>(__builtin_ctzll(okm));
+        }
+        first = found == L.ub[v];
+        L.bind[v * 64 + lane] = found;
+    }
+    for (u32 q = 0; q < arity; ++q)
+        L.bind[q * 64 + lane] = L.ub[q];
+    wave_sync();
+    return first;
+}
+
 /// Calls emit(k, s) for the successors of the state in canonical order (schema, then lexicographic binding),
 /// k = 0, 1, ...; L.ub holds the binding during the call, and emit returns false to stop. Each schema with successors
 /// (L.counts from count_all) is enumerated depth first over its parameters in order, so the bindings come in the order
@@ -981,16 +1024,21 @@ __device__ __forceinline__ bool label_applicable(const TaskDev& T, const auto& H
 /// Counting thus happens once per node of the binding tree instead of once per successor and parameter. The levels'
 /// words and candidates left live in L.dfs_w / L.dfs_m; L.bind holds the binding's prefix in every lane's column.
 /// Returns the successors enumerated.
-template<bool kLevels, class Emit>
-__device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& H, const Lds& L, u32 lane, Emit&& emit)
+template<bool kLevels, bool kWitness = false, class Emit>
+__device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& H, const Lds& L, u32 lane, Emit&& emit, u32 s_begin = 0,
+                                                  u32 s_end = kNone)
 {
     const u32 A = T.label_width ? T.label_width : 1;
     u32 k = 0;
-    for (u32 s = 0; s < T.num_schemas; ++s)
+    for (u32 s = s_begin; s < T.num_schemas && s < s_end; ++s)
     {
         if (L.counts[s] == 0)
             continue;
         const auto& S = H.schemas[s];
+        // witness pruning: only the full bindings whose witnesses the matcher binds first are successors
+        [[maybe_unused]] const DevWitness* X = nullptr;
+        if constexpr (kWitness)
+            X = (T.witness && T.witness[s].n) ? T.witness + s : nullptr;
         if (S.arity == 0)
         {
             if (!emit(k++, s))
@@ -1089,7 +1137,10 @@ __device__ __forceinline__ u32 for_each_successor(const TaskDev& T, const auto& 
             wave_sync();
             if (i + 1 == S.arity)
             {
-                if (!emit(k++, s))
+                bool take = true;
+                if constexpr (kWitness)
+                    take = !X || witness_first(T, H, L, X, S.arity, lane);
+                if (take && !emit(k++, s))
                     return k;
                 have = L.dfs_m[i] != 0 || open(i, w + 1);
                 continue;
@@ -2448,9 +2499,32 @@ __device__ __forceinline__ u32 trimmed_words(const lds<u64>* row, u32 W, u32 lan
     return top;
 }
 
+/// Witness pruning (include/mymyr/successor/successors.hpp:154-248 with witness pruning on): the successor counts of
+/// the schemas with witness parameters become the number of full bindings whose witnesses the matcher binds first (one
+/// per effect-relevant binding), counted by enumerating those schemas; `total` (count_all's) is corrected to match.
+template<bool kLevels>
+__device__ __forceinline__ u32 witness_counts(const TaskDev& T, const auto& H, const Lds& L, u32 lane, u32 total)
+{
+    if (!T.witness)
+        return total;
+    for (u32 s = 0; s < T.num_schemas; ++s)
+    {
+        const u32 all = L.counts[s];
+        if (T.witness[s].n == 0 || all == 0)
+            continue;
+        const u32 kept = for_each_successor<kLevels, true>(T, H, L, lane, [](u32, u32) { return true; }, s, s + 1);
+        wave_sync();
+        if (lane == 0)
+            L.counts[s] = kept;
+        wave_sync();
+        total = total - all + kept;
+    }
+    return total;
+}
+
 /// The expansion of row i (pass 0: its counts and the validation of its words; pass 1: its successors from
 /// offsets[i] on) with the tables of its instance.
-template<bool kLevels>
+template<bool kLevels, bool kWitness>
 __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 lane)
 {
     const u32 Lw = A.label_width;
@@ -2472,7 +2546,9 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
     }
     load_row_lds_n(T, L, src, min(A.words, T.W), lane);
     build_view<kLevels>(T, H, L, lane);
-    const u32 c = count_all<kLevels>(T, H, L, lane);
+    u32 c = count_all<kLevels>(T, H, L, lane);
+    if constexpr (kWitness)
+        c = witness_counts<kLevels>(T, H, L, lane, c);
     if (A.pass == 0 && !A.drop_noops)
     {
         if (lane == 0)
@@ -2481,7 +2557,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
     }
     const bool keep_all = A.pass == 1 && A.drop_noops && A.noops[i] == c;
     u32 noops = 0, kept = 0;
-    const u32 listed = for_each_successor<kLevels>(T, H, L, lane, [&](u32 k, u32 s) {
+    const u32 listed = for_each_successor<kLevels, kWitness>(T, H, L, lane, [&](u32 k, u32 s) {
         const bool noop = succ_apply(T, H, L, s, lane, A.status);
         noops += noop ? 1 : 0;
         if (A.pass == 1 && (!A.drop_noops || !noop || keep_all))
@@ -2548,7 +2624,7 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
 
 /// The expansion of a batch of one instance in batch order, or with kGroup of one instance's group of a batch grouped
 /// by instance.
-template<bool kStaged, bool kLevels, bool kGroup>
+template<bool kStaged, bool kLevels, bool kGroup, bool kWitness = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) void k_expand(ExpandArgs A)
 {
     extern __shared__ u64 smem[];
@@ -2566,7 +2642,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void k_expand(ExpandArgs A)
     lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
     const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
     for (u64 j = lo + static_cast<u64>(blockIdx.x) * nw + wave; j < hi; j += static_cast<u64>(gridDim.x) * nw)
-        expand_row<kLevels>(A, T, H, L, kGroup ? A.groups.order[j] : j, lane);
+        expand_row<kLevels, kWitness>(A, T, H, L, kGroup ? A.groups.order[j] : j, lane);
 }
 
 __global__ void k_offsets_i32(const u64* src, u64 n, i32* dst)
@@ -2954,10 +3030,14 @@ void launch_expand(const ExpandArgs& a, hipStream_t stream)
     size_t lds = 0;
     const unsigned nw = waves_per_block(a.T, &lds);
     const bool group = a.groups.order != nullptr;
+    if (a.witness && group)
+        throw std::invalid_argument("mymyr_amd: expand: witness pruning over a task table is not supported by the device expansion");
     const auto fn = group ? variant(a.T, k_expand<true, false, true>, k_expand<true, true, true>, k_expand<false, false, true>,
                                     k_expand<false, true, true>)
-                          : variant(a.T, k_expand<true, false, false>, k_expand<true, true, false>, k_expand<false, false, false>,
-                                    k_expand<false, true, false>);
+                    : a.witness ? variant(a.T, k_expand<true, false, false, true>, k_expand<true, true, false, true>,
+                                          k_expand<false, false, false, true>, k_expand<false, true, false, true>)
+                                : variant(a.T, k_expand<true, false, false>, k_expand<true, true, false>, k_expand<false, false, false>,
+                                          k_expand<false, true, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
     // one block per nw rows: rows differ widely in successors, and the dispatcher balances them as blocks finish
     hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group, 0, false)), dim3(nw * kWave), lds, stream, a);

@@ -265,6 +265,7 @@ struct ExpandArgs
     i32* index;
     u32* words_needed;  // device word: the widest trimmed successor that did not fit out_words
     u32* status;
+    u32 witness;        // witness pruning (one-instance launches): one successor per effect-relevant binding
 };
 
 void launch_expand(const ExpandArgs& a, hipStream_t stream);

@@ -42,6 +42,7 @@ struct TaskDev
     u32 max_step_words;
     u32 lazy;      // lazy slots: an added atom without a slot is recorded in `missing`
     u64* missing;  // lazy slots: bit per canonical fluent atom (device; set by the successor kernels), else null
+    const DevWitness* witness;  // per schema its witness parameters and plans (null: no schema has a witness)
 };
 
 /// Pointers into an uploaded image (host helper).

@@ -36,12 +36,27 @@ struct Cache
     std::multimap<std::pair<int, size_t>, void*> idle;  // freed blocks by (device, bytes)
     std::vector<Pending> pending;                       // stream-ordered frees whose streams have not passed them yet
     size_t idle_bytes = 0;
+    MemoryUsage usage;  // reserved / used bytes (held under `mutex`) and the allocation counts
+
+    void on_reserve(size_t bytes)
+    {
+        usage.reserved += bytes;
+        usage.reserved_high = std::max(usage.reserved_high, usage.reserved);
+        ++usage.driver_allocations;
+    }
+    void on_use(size_t bytes)
+    {
+        usage.used += bytes;
+        usage.used_high = std::max(usage.used_high, usage.used);
+        ++usage.allocations;
+    }
 
     void release_idle()
     {
         for (auto& [key, p] : idle)
             (void)hipFree(p);
         idle.clear();
+        usage.reserved -= idle_bytes;
         idle_bytes = 0;
     }
     /// Moves every pending block whose event completed (or, with wait, every pending block) to the idle blocks.
@@ -53,6 +68,7 @@ struct Cache
         if (bytes > kCacheMax)
         {
             (void)hipFree(p);
+            usage.reserved -= bytes;
             return;
         }
         idle.emplace(std::make_pair(device, bytes), p);
@@ -105,6 +121,7 @@ void* device_alloc(size_t bytes, const char* what)
             c.idle.erase(it);
             c.idle_bytes -= bytes;
             c.live.emplace(p, Block{dev, bytes});
+            c.on_use(bytes);
             return p;
         }
     }
@@ -125,6 +142,8 @@ void* device_alloc(size_t bytes, const char* what)
                        hipGetErrorString(e));
     std::lock_guard lock(c.mutex);
     c.live.emplace(p, Block{dev, bytes});
+    c.on_reserve(bytes);
+    c.on_use(bytes);
     return p;
 }
 
@@ -143,6 +162,7 @@ void device_free(void* p)
     }
     const Block b = it->second;
     c.live.erase(it);
+    c.usage.used -= b.bytes;
     c.make_idle(b.device, b.bytes, p);
 }
 
@@ -159,6 +179,7 @@ void device_free_async(void* p, hipStream_t stream)
         {
             b = it->second;
             c.live.erase(it);
+            c.usage.used -= b.bytes;
         }
     }
     if (b.device < 0)
@@ -188,6 +209,13 @@ void device_cache_release()
     std::lock_guard lock(c.mutex);
     c.collect(true);
     c.release_idle();
+}
+
+MemoryUsage memory_usage()
+{
+    Cache& c = cache();
+    std::lock_guard lock(c.mutex);
+    return c.usage;
 }
 
 namespace

@@ -4,12 +4,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <mutex>
 #include <stdexcept>
 #include <string>
 
 namespace mya
 {
+using u64 = std::uint64_t;
 struct HipError : std::runtime_error
 {
     using std::runtime_error::runtime_error;
@@ -33,6 +35,20 @@ void device_free(void* p);
 void device_free_async(void* p, hipStream_t stream);
 /// Frees every cached block (all devices).
 void device_cache_release();
+
+/// Process-wide device memory figures of the cache (the reference's PoolUsage, include/mymyr/cuda/runtime.hpp:140-146):
+/// bytes held from the driver (handed out, idle or awaiting a stream-ordered free), bytes handed out, their high-water
+/// marks, and how many blocks the library has handed out (cache hits included) and taken from the driver.
+struct MemoryUsage
+{
+    u64 reserved = 0;
+    u64 used = 0;
+    u64 reserved_high = 0;
+    u64 used_high = 0;
+    u64 allocations = 0;
+    u64 driver_allocations = 0;
+};
+MemoryUsage memory_usage();
 
 template<class T>
 T* dev_alloc(size_t count, const char* what)

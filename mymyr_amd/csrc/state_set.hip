@@ -339,21 +339,24 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
     state_set_clear(s, stream);
 }
 
-void state_set_destroy(StateSet& s)
+void state_set_destroy(StateSet& s, hipStream_t stream)
 {
-    if (s.last)
-        (void)hipStreamSynchronize(s.last);
-    dev_free(s.v.table);
-    dev_free(s.v.arena);
-    dev_free(s.cand_slot);
-    dev_free(s.flags);
-    dev_free(s.list);
-    dev_free(s.scan_scratch);
-    dev_free(s.d_size);
-    dev_free(s.d_status);
-    dev_free(s.id_of);
+    for (void* p : {static_cast<void*>(s.v.table), static_cast<void*>(s.v.arena), static_cast<void*>(s.cand_slot),
+                    static_cast<void*>(s.flags), static_cast<void*>(s.list), static_cast<void*>(s.scan_scratch),
+                    static_cast<void*>(s.d_size), static_cast<void*>(s.d_status), static_cast<void*>(s.id_of)})
+    {
+        if (stream)
+            dev_free_async(p, stream);
+        else
+            dev_free(p);
+    }
     if (s.h_pinned)
+    {
+        // the pinned words are reused by the next set only after this one's last copies into them have landed
+        if (stream)
+            (void)hipStreamSynchronize(stream);
         pinned_release(s.h_pinned);
+    }
     s = StateSet{};
 }
 

@@ -47,7 +47,9 @@ struct StateSet
 /// max_states (a driver that cuts a batch at max_states after probing it).
 void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u64 batch_cap, hipStream_t stream,
                       u64 pending = 0);
-void state_set_destroy(StateSet& s);
+/// Frees the set's device memory: with a stream, in that stream's order (the blocks are reused only after the work
+/// queued on it so far, which must include every use of the set); without one, after the device has finished all work.
+void state_set_destroy(StateSet& s, hipStream_t stream = nullptr);
 /// Clears the set (size 0) without freeing.
 void state_set_clear(StateSet& s, hipStream_t stream);
 

@@ -1017,6 +1017,8 @@ private:
         const u32 eq = equality_pred();
         (void)eq;
         std::vector<DevSchema> schemas;
+        std::vector<DevWitness> witness;  // per schema
+        bool any_witness = false;
         std::vector<DevStep> steps;
         std::vector<DevCons> cons;
         std::vector<DevCheck> checks;
@@ -1186,6 +1188,36 @@ private:
                     bound[v] = 1;
                 ds.filter_step[i] = static_cast<u32>(steps.size());
                 steps.push_back(make_step(i, bound));
+            }
+            // witness pruning: the witnesses in the matcher's order, each one's filter with the effect-relevant
+            // parameters and the earlier witnesses bound, and the count plan of the later witnesses
+            {
+                DevWitness wd{};
+                std::vector<u8> rel(s.arity, 0);
+                for (const Literal& l : s.eff)
+                    for (i32 x : l.terms)
+                        if (x >= 0)
+                            rel[static_cast<u32>(x)] = 1;
+                const std::vector<u32> wit = witness_order(*C, si, rel);
+                wd.n = static_cast<u32>(wit.size());
+                std::vector<u8> bound = rel;
+                for (u32 t = 0; t < wd.n; ++t)
+                {
+                    wd.param[t] = wit[t];
+                    wd.filter[t] = static_cast<u32>(steps.size());
+                    steps.push_back(make_step(wit[t], bound));
+                    bound[wit[t]] = 1;
+                    std::vector<u8> b2 = bound;
+                    wd.plan_lo[t] = static_cast<u32>(steps.size());
+                    for (u32 t2 = t + 1; t2 < wd.n; ++t2)
+                    {
+                        steps.push_back(make_step(wit[t2], b2));
+                        b2[wit[t2]] = 1;
+                    }
+                    wd.plan_hi[t] = static_cast<u32>(steps.size());
+                }
+                witness.push_back(wd);
+                any_witness = any_witness || wd.n > 0;
             }
             // effects: adds first, then deletes
             ds.eff_begin = static_cast<u32>(effects.size());
@@ -1447,6 +1479,7 @@ private:
                 init.resize(std::max<u32>(1, words_for(C->layout.fluent_count)), 0);
             h.off_initial = put(init.data(), init.size() * sizeof(u64));
         }
+        h.off_witness = any_witness ? put(witness.data(), witness.size() * sizeof(DevWitness)) : 0;
         h.lazy = lazy ? 1 : 0;
         std::memcpy(img.data(), &h, sizeof(h));
         C->image = std::move(img);
@@ -1503,8 +1536,6 @@ u32 CompiledTask::slot_of_atom(u32 pred, const u32* objs) const
     return c < layout.fluent_count ? slot_of[c] : kNone;
 }
 
-namespace
-{
 /// The witness parameters of schema si (those no effect mentions) in the order the reference's successor matcher binds
 /// them (src/mymyr/task/compile.cpp:916-946): after every effect-relevant parameter, greedily the one with the most
 /// binary constraints to placed parameters, then the most fluent unary constraints, then the fewest dom0 objects, ties
@@ -1572,7 +1603,6 @@ std::vector<u32> witness_order(const CompiledTask& task, u32 si, const std::vect
     }
     return order;
 }
-}  // namespace
 
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit)
 {

@@ -210,6 +210,20 @@ struct DevSchema
     u32 affects;  // bit s: an action of this schema can change schema s's successor count (every bit past 32 schemas)
 };
 
+/// Witness pruning of a schema (the parameters no effect mentions, witnesses, bound last and only once per binding of
+/// the others), in the order the reference's matcher binds the witnesses: filter[t] gives the candidates of param[t]
+/// with the effect-relevant parameters and witnesses [0, t) bound; steps [plan_lo[t], plan_hi[t]) count the completions
+/// of witnesses (t, n) once witnesses [0, t] are bound (empty for the last).
+struct DevWitness
+{
+    u32 n;  // witness parameters (0: none)
+    u32 param[kMaxParams];
+    u32 filter[kMaxParams];
+    u32 plan_lo[kMaxParams];
+    u32 plan_hi[kMaxParams];
+    u32 pad;
+};
+
 /// An effect pattern: cid = base + sum over parameter terms of rs[pos][object].
 struct DevEffect
 {
@@ -279,6 +293,8 @@ struct DevTaskHeader
     u32 init_count;     // successors of the initial state (filled once the device has counted them)
     u32 max_step_words; // the widest candidate window of any plan or filter step, in words
     u32 lazy;           // 1: lazy slots (slot_of, records, goal lists and initial row sized for every canonical atom)
+    u32 pad;
+    u64 off_witness;    // DevWitness per schema (0: no schema has a witness parameter)
 };
 
 /// Static k-ary relation: sorted keys sum(obj_i * n^(ar-1-i)) at [keys, keys + count).
@@ -352,6 +368,10 @@ struct GroundActions
 /// successor is the one whose witness objects come first in the matcher's witness order, the binding it finds first
 /// (include/mymyr/successor/detail/engine.hpp:345-356; the order: src/mymyr/task/compile.cpp:916-946).
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit);
+
+/// The witness parameters of schema si (those `relevant` does not mark) in the order the reference's matcher binds them
+/// (src/mymyr/task/compile.cpp:916-946).
+std::vector<u32> witness_order(const CompiledTask& task, u32 si, const std::vector<u8>& relevant);
 
 inline u32 words_for(u64 bits) { return static_cast<u32>((bits + 63) >> 6); }
 }  // namespace mya

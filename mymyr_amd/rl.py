@@ -678,14 +678,16 @@ class TaskSuite(TaskTable):
 
 def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tensor | None = None, capacity: int | None = None,
            goal: bool = False, hashes: bool = False, noops: bool = False, drop_noops: bool = False, index: bool = False,
-           validate: bool = True, words: int | None = None) -> dict:
+           validate: bool = True, words: int | None = None, witness_pruning: bool = False) -> dict:
     """The flat expansion of states [N, W] on the device (rl.expand, include/mymyr/rl/expand.hpp:1-130): successor rows
     "succ" [M, words], "parent", "schema" [M] int32, "binding" [M, label_width] int32 (-1 padded), "offsets" [N + 1]
     int32, with goal=True "goal" [M] uint8, hashes=True "succ_hash" [M] (uint64 bits in int64), noops=True "noop" [M]
     uint8, and "index" [M] int32 (the position in the parent's full successor order) with drop_noops or index=True;
     plus "generated", "total", "words_needed" and "overflow". capacity None sizes the buffers to every successor (a
-    first call counts them). Canonical order, witness pruning off; drop_noops removes a state's no-op successors unless
-    all of them are no-ops. Over a TaskTable, row i is a state of instance task_ids[i] ([N] int32 on the device).
+    first call counts them). Canonical order; witness_pruning keeps one successor per effect-relevant binding of a schema
+    with witness parameters (the binding the reference's matcher finds first; one task only, as the reference's default
+    is off); drop_noops removes a state's no-op successors unless all of them are no-ops. Over a TaskTable, row i is a
+    state of instance task_ids[i] ([N] int32 on the device).
     A task with lazy slots interns the atoms its successors add without a slot (ascending canonical id); with words
     None the rows then take the task's new width (the expansion runs once more when its successors outgrew them)."""
     s = states.view(torch.int64) if states.dtype == torch.uint64 else states
@@ -704,7 +706,7 @@ def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tens
         raise ValueError("mymyr: expand: task ids need a TaskTable")
     ow = task.words if words is None else words
     L = max(1, task.label_width)
-    opts = _lib.ExpandOptions(1, 0, int(validate), int(drop_noops))
+    opts = _lib.ExpandOptions(1, int(witness_pruning), int(validate), int(drop_noops))
 
     def run(x):
         if table:
@@ -733,7 +735,7 @@ def expand(task: Task | TaskTable, states: torch.Tensor, *, task_ids: torch.Tens
     if words is None and not table and not task.frozen and x.words_needed > ow:
         # lazy slots grew the rows: their atoms have slots now, so the successors fit rows of the task's new width
         return expand(task, states, capacity=cap, goal=goal, hashes=hashes, noops=noops, drop_noops=drop_noops, index=index,
-                      validate=validate, words=max(task.words, int(x.words_needed)))
+                      validate=validate, words=max(task.words, int(x.words_needed)), witness_pruning=witness_pruning)
     kept = min(x.total, cap)
     out = {"succ": succ[:kept], "parent": parent[:kept], "schema": schema[:kept], "binding": binding[:kept],
            "offsets": offsets, "generated": x.generated, "total": x.total, "words_needed": x.words_needed,

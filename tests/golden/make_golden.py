@@ -115,7 +115,9 @@ def make_successors():
     dump("successors.json", out)
 
 
-def env_trajectory(w: workloads.EnvWorkload, rows: int, steps: int, threads: int = 8):
+def env_trajectory(w: workloads.EnvWorkload, rows: int, steps: int, threads: int = 8, first_env: int = 0):
+    """The reference HostEnv's per-step digests of `rows` envs with ids first_env, first_env + 1, ... (a batch's rows
+    [first_env, first_env + rows): an env's trajectory depends only on its row and its env id)."""
     t = ref.RefTask(fx.task_path(w.name), w.atoms)
     e = ref.RefEnv(t, threads=threads, **w.env)
     N, W, L = rows, t.table_words, max(1, t.label_width)
@@ -124,7 +126,7 @@ def env_trajectory(w: workloads.EnvWorkload, rows: int, steps: int, threads: int
     dr = np.zeros(N, np.uint64)
     ag = np.zeros(N, np.uint8)
     cnt = np.zeros(N, np.int32)
-    e.reset(S, st, dr, ag, cnt)
+    e.reset(S, st, dr, ag, cnt, first_env=first_env)
     digests = []
     totals = {"terminated": 0, "truncated": 0, "reward": 0.0}
     t0 = time.time()
@@ -136,13 +138,13 @@ def env_trajectory(w: workloads.EnvWorkload, rows: int, steps: int, threads: int
         sch = np.zeros(N, np.int32)
         bnd = np.zeros((N, L), np.int32)
         g = np.zeros(N, np.uint8)
-        e.step(S, st, dr, ag, reward=R, terminated=term, truncated=trunc, count=c, schema=sch, binding=bnd, goal=g)
+        e.step(S, st, dr, ag, first_env=first_env, reward=R, terminated=term, truncated=trunc, count=c, schema=sch, binding=bnd, goal=g)
         digests.append(fx.step_digest(N, S, R, term, trunc, c, sch, bnd, g))
         totals["terminated"] += int(term.sum())
         totals["truncated"] += int(trunc.sum())
         totals["reward"] += float(R.astype(np.float64).sum())
     return {"workload": w.name, "rows": N, "steps": steps, "env": w.env, "digests": digests, "totals": totals,
-            "ref_seconds": time.time() - t0}
+            "first_env": first_env, "ref_seconds": time.time() - t0}
 
 
 def make_env():
@@ -161,6 +163,15 @@ def make_env_long():
     # the transport workloads over their whole horizons (512 and 128 steps) on their first rows
     dump("env_transport_long.json", env_trajectory(workloads.TRANSPORT, 256, workloads.TRANSPORT.steps))
     dump("env_transport_xl_long.json", env_trajectory(workloads.TRANSPORT_XL, 64, workloads.TRANSPORT_XL.steps))
+    make_env_tail()
+
+
+def make_env_tail():
+    # the transport workloads over their whole horizons on their last 64 rows (env ids N - 64 .. N - 1 of the full
+    # batches)
+    tr, xl = workloads.TRANSPORT, workloads.TRANSPORT_XL
+    dump("env_transport_long_tail.json", env_trajectory(tr, 64, tr.steps, first_env=tr.num_envs - 64))
+    dump("env_transport_xl_long_tail.json", env_trajectory(xl, 64, xl.steps, first_env=xl.num_envs - 64))
 
 
 def make_env_small():
@@ -347,8 +358,35 @@ def make_brfs_wide():
            "transport_w20_7:expanded": brfs_record("transport_w20_7", stop_at_goal=False, max_expanded=5000),
            "transport:cut": brfs_record("transport", stop_at_goal=False, max_depth=12, max_states=100000),
            "transport:depth2": brfs_record("transport", stop_at_goal=False, max_depth=2),
-           "witness_wide:cut": brfs_record("witness_wide", "dense", stop_at_goal=False, witness_pruning=False, max_states=50000)}
+           "witness_wide:cut": brfs_record("witness_wide", "dense", stop_at_goal=False, witness_pruning=False, max_states=50000),
+           "witness_wide:witness_cut": brfs_record("witness_wide", "dense", stop_at_goal=False, max_states=50000),
+           "witness_wide:witness_goal": brfs_record("witness_wide", "dense", stop_at_goal=True, max_states=300000),
+           "witness_wide:witness_depth": brfs_record("witness_wide", "dense", stop_at_goal=False, max_depth=2)}
     dump("brfs_wide.json", out)
+
+
+def make_successors_witness():
+    """Canonical successor listings with witness pruning on (the reference's Successors::generate, one successor per
+    effect-relevant binding, the witness the matcher binds first) along seeded random walks of tasks with witness
+    parameters: per state its schema and binding order and the successors' hash_state."""
+    out = {}
+    for name, atoms, steps in [("rovers__p02", "auto", 10), ("witness_wide", "dense", 10), ("witness_order_5", "auto", 10),
+                               ("witness_order_0", "auto", 10)]:
+        t = ref.RefTask(fx.task_path(name), atoms)
+        rng = np.random.default_rng(5)
+        row = t.initial_state()
+        states = []
+        for _ in range(steps):
+            sc, bd, rs = t.successors(row, witness=True)
+            full, _, frs = t.successors(row)
+            states.append({"row": hex_row(row), "count": int(len(sc)), "schema": [int(x) for x in sc],
+                           "binding": bd.tolist(), "succ_hash": [f"{ref.hash_state(r):016x}" for r in rs],
+                           "all": int(len(full))})
+            if len(full) == 0:
+                break
+            row = frs[int(rng.integers(len(full)))]
+        out[name] = {"atoms": atoms, "states": states}
+    dump("successors_witness.json", out)
 
 
 def walk_states(t, depths, seed):
@@ -552,8 +590,8 @@ def main():
     a = ap.parse_args()
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
-             "env_small": make_env_small, "env_long": make_env_long, "pool": make_pool,
-             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick)}
+             "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

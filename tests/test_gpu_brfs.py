@@ -137,23 +137,19 @@ WIDE_ATOMS = {"witness_wide": "dense"}
 
 
 @pytest.mark.parametrize("key", ["transport_w20_3:goal", "transport_w20_7:goal", "transport_w20_3:cut", "transport_w20_7:expanded",
-                                 "transport:cut", "transport:depth2", "witness_wide:cut"])
+                                 "transport:cut", "transport:depth2", "witness_wide:cut", "witness_wide:witness_cut",
+                                 "witness_wide:witness_depth", "witness_wide:witness_goal"])
 def test_wide_rows(golden, key):
     """Rows wider than 16 words (typed transport of 20 and of 176 words, a 19-word dense task) take the driver over the
-    lifted expansion: layer counts, fingerprints, statuses, cuts and plans equal to the reference's."""
+    lifted expansion: layer counts, fingerprints, statuses, cuts and plans equal to the reference's. The 19-word task's
+    schemas have witness parameters: with witness pruning on (the reference's default) the expansion keeps one
+    successor per effect-relevant binding, with the witnesses the reference's matcher binds first."""
     exp = golden.load("brfs_wide.json")[key]
     name = key.split(":")[0]
     print(f"wide brfs: {key}", flush=True)
     r = device(golden, name, WIDE_ATOMS.get(name, "auto"), full=True, **exp["options"])
     assert not same(r, exp), (key, same(r, exp))
     assert same_plan(r, exp), (key, r["result"].plan[:6], exp.get("plan", [])[:6])
-
-
-def test_wide_rows_refuse_witness_pruning_over_witness_parameters(golden):
-    from mymyr_amd._lib import MyaError
-
-    with pytest.raises(MyaError, match="witness"):
-        device(golden, "witness_wide", "dense", stop_at_goal=False, max_states=1000)
 
 
 def _rows(words, hexrows):

@@ -18,8 +18,9 @@ def host(t):
 
 
 def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0, on_step=None, **pool_kw):
-    """Steps num_envs envs (default: the fixture's rows) for the fixture's steps and compares the first rows' per-step
-    digests with the reference's; on_step(k, outputs) sees each step's outputs (device tensors over every env)."""
+    """Steps num_envs envs (default: the fixture's rows) for the fixture's steps and compares the per-step digests of
+    the rows whose env ids the fixture holds (first_env, first_env + 1, ...; the first rows unless it says otherwise)
+    with the reference's; on_step(k, outputs) sees each step's outputs (device tensors over every env)."""
     from mymyr_amd import rl
     from mymyr_amd.task import Task
 
@@ -31,10 +32,12 @@ def run_env(golden, fixture: str, num_envs: int | None = None, encode: int = 0, 
     pool = rl.DeviceEnvPool(t, n, **g["env"], **pool_kw)
     pool.reset()
     rows = g["rows"]
+    r0 = g.get("first_env", 0)
+    assert r0 + rows <= n
     L = max(1, t.label_width)
     for k in range(g["steps"]):
         o = pool.step(encode=encode)
-        h = {key: host(o[key][:rows]) for key in ("states", "reward", "terminated", "truncated", "count", "schema", "binding", "goal")}
+        h = {key: host(o[key][r0:r0 + rows]) for key in ("states", "reward", "terminated", "truncated", "count", "schema", "binding", "goal")}
         d = golden.step_digest(rows, h["states"].view(np.uint64), h["reward"], h["terminated"], h["truncated"], h["count"], h["schema"],
                                h["binding"][:, :L], h["goal"])
         assert d == g["digests"][k], f"{fixture}: step {k} differs from the reference"
@@ -68,6 +71,20 @@ def test_transport_xl_first_rows_with_encoding(golden):
 def test_transport_whole_horizon_full_batch(golden):
     """The transport workload as run: 65536 envs for all 512 steps; the first 256 rows match the reference every step."""
     run_env(golden, "env_transport_long.json", num_envs=65536)
+
+
+def test_transport_whole_horizon_last_rows(golden):
+    """The transport workload as run (65536 envs, 512 steps): its last 64 rows (env ids 65472 to 65535, whose Philox
+    counters, row offsets and places in the resident grid differ most from the first rows') match the reference's
+    trajectory of those env ids every step."""
+    run_env(golden, "env_transport_long_tail.json", num_envs=65536)
+
+
+def test_transport_xl_whole_horizon_last_rows(golden):
+    """The transport_xl workload as run (262144 envs, 128 steps, encoding on at 544 atoms): its last 64 rows (env ids
+    262080 to 262143, whose rows start 2.8 GB into the batch, past 2^31 bytes) match the reference's trajectory every
+    step."""
+    run_env(golden, "env_transport_xl_long_tail.json", num_envs=262144, encode=544)
 
 
 def reference_masks(rt, row):

@@ -154,3 +154,34 @@ def test_expand_argument_errors(golden):
     x.capacity = 8
     assert lib.mya_expand(t.handle, rows.data_ptr(), 4, t.words, ctypes.byref(opts), ctypes.byref(x), None) != 0
     assert b"drop_noops requires index" in lib.mya_last_error()
+
+
+@pytest.mark.parametrize("name", ["witness_wide", "rovers__p02", "witness_order_5", "witness_order_0"])
+def test_expand_with_witness_pruning_matches_reference_listing(golden, name):
+    """rl.expand with witness_pruning (the reference's ExpandOptions::witness_pruning, include/mymyr/rl/expand.hpp:81):
+    along a seeded walk, per state the count, schemas, bindings (whose witness objects are the ones the reference's
+    matcher binds first) and successor hashes equal the compiled reference's Successors::generate with witness pruning
+    on; the 19-word task's listings are shorter than its full ones."""
+    from mymyr_amd import rl
+    from mymyr_amd.task import Task
+
+    g = golden.load("successors_witness.json")[name]
+    t = Task.from_text_file(golden.task_path(name), g["atoms"])
+    states = g["states"]
+    rows = np.array([[int(x, 16) for x in s["row"]][: t.words] + [0] * max(0, t.words - len(s["row"])) for s in states],
+                    dtype=np.uint64)
+    print(f"witness expand: {name} rows {len(rows)}", flush=True)
+    x = rl.expand(t, dev(rows), hashes=True, witness_pruning=True)
+    off = host(x["offsets"])
+    assert list(np.diff(off)) == [s["count"] for s in states]
+    sch, bnd, hsh = host(x["schema"]), host(x["binding"]), host(x["succ_hash"]).view(np.uint64)
+    for i, s in enumerate(states):
+        a, b = off[i], off[i + 1]
+        assert list(sch[a:b]) == s["schema"], (i, list(sch[a:b])[:8], s["schema"][:8])
+        if b > a:
+            assert bnd[a:b, : len(s["binding"][0])].tolist() == s["binding"], i
+        assert [f"{int(h):016x}" for h in hsh[a:b]] == s["succ_hash"], i
+    full = rl.expand(t, dev(rows))
+    assert list(np.diff(host(full["offsets"]))) == [s["all"] for s in states]
+    if name == "witness_wide":
+        assert all(s["count"] < s["all"] for s in states)

@@ -155,18 +155,34 @@ def test_lazy_task_searched_again(golden):
     assert atoms_of(cid, [r.goal_state])[0] == exp["goal_cids"]
 
 
-def test_lazy_search_refuses_witness_pruning_over_witness_parameters(golden):
-    """A lazy task's search runs over the lifted expansion, which prunes no witness parameters: a task whose schemas have
-    one is refused with witness pruning on, as wide rows are."""
+@pytest.mark.parametrize("key", ["rovers__p02", "rovers__p02:goal", "rovers__p02:expanded", "witness_order_5:goal",
+                                 "witness_order_0:goal", "witness_order_0:cut"])
+def test_lazy_search_with_witness_pruning(golden, key):
+    """A lazy task's search runs over the lifted expansion, which prunes witness parameters as the reference's matcher
+    does (the reference's default options): over rovers and tasks whose two witness parameters the matcher binds in an
+    order other than the parameter order, counts, statuses, fingerprints and plans (whose labels carry the witness
+    objects found first) equal the compiled reference's over the frozen task (tests/golden/brfs_witness.json)."""
     from mymyr_amd import search
-    from mymyr_amd._lib import MyaError
     from mymyr_amd.task import Task
 
-    t = Task.from_text_file(golden.task_path("rovers__p02"), "lazy")
-    with pytest.raises(MyaError, match="witness"):
-        search.brfs(t, stop_at_goal=False, max_states=1000)
-    r = search.brfs(t, stop_at_goal=False, max_states=1000, witness_pruning=False)
-    assert r.states == 1000 and r.status == "out_of_states"
+    exp = golden.load("brfs_witness.json")[key]
+    name = key.split(":")[0]
+    print(f"lazy witness brfs: {key}", flush=True)
+    t = Task.from_text_file(golden.task_path(name), "lazy")
+    r = search.brfs(t, fingerprint=True, **exp["options"])
+    got = {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
+           "layers": r.layers, "fingerprint": r.fingerprint, "layer_counts": r.layer_counts, "exhausted": r.exhausted,
+           "solved": r.solved}
+    bad = {k: (got[k], exp[k]) for k in KEYS if got[k] != exp[k]}
+    assert not bad, (key, bad)
+    assert r.status == STATUS[exp["status"]]
+    if exp["solved"]:
+        assert [[a.schema, *a.binding] for a in r.plan] == exp["plan"] and r.cost == exp["cost"]
+    # the same search with witness pruning off generates every binding: at least as many successors
+    if key == "rovers__p02:expanded":
+        off = search.brfs(Task.from_text_file(golden.task_path(name), "lazy"), fingerprint=True, witness_pruning=False,
+                          **exp["options"])
+        assert off.generated >= r.generated
 
 
 @pytest.mark.parametrize("key", ["transport:cut", "transport:depth2", "transport_w20_3:cut", "transport_w20_7:expanded",

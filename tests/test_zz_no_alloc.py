@@ -1,6 +1,7 @@
 """mya_expand_noalloc (the flat expansion whose scratch is a static device array) against mya_expand on the same
 inputs, through the C ABI: every output array bit-equal, on two calls in a row with the second on fewer rows (the
-static scratch keeps the first call's contents), for a lifted and a ground task and the no-op filter."""
+static scratch keeps the first call's contents), for a lifted and a ground task and the no-op filter; and the
+library's allocation count (mya_memory_usage_get) unchanged across every no-alloc call."""
 
 import ctypes
 
@@ -70,10 +71,16 @@ def test_noalloc_expand_equals_expand(golden, name, atoms, rows, steps):
     states = walk_states(task, rows, steps, seed=11)
     # the task's device image goes up with the first allocating call
     _ = run(lib.mya_expand, task, states[:0], False, cap=0)
+    from mymyr_amd._lib import memory_usage
+
     for drop in (False, True):
         for n in (rows, rows // 3 + 1):  # the second call on fewer rows: the static scratch holds the first call's data
             a = run(lib.mya_expand, task, states[:n], drop)
+            before = memory_usage()
             b = run(lib.mya_expand_noalloc, task, states[:n], drop)
+            after = memory_usage()
+            # no device block handed out (from the driver or the library's cache) and none taken from the driver
+            assert (after["allocations"], after["driver_allocations"]) == (before["allocations"], before["driver_allocations"]), (n, drop)
             assert a["counts"] == b["counts"], (n, drop)
             for k in a:
                 if k != "counts":
