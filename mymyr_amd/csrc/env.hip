@@ -1677,18 +1677,33 @@ __global__ __launch_bounds__(256) void k_visited_mask(const u64* table, const i3
 /// are T / H and whose wave region is L. An autoreset restarts the row in next_task_ids[i] when that names an instance
 /// (else in k), writing the new instance's initial state and goal masks over the words the row may have dirtied
 /// (TaskSuite::initial_row, src/mymyr/rl/task_suite.cpp:130-138) and its id into task_ids.
-template<bool kLevels, bool kOne, bool kVisited>
+template<bool kLevels, bool kOne, bool kVisited, bool kPlain = false>
 __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, const auto& H, const Lds& L, u64 i, u32 k, u32 lane, u64 seed)
 {
+    static_assert(!kPlain || (kOne && !kVisited), "the plain step is a one-instance step without visited tables");
+    // the plain step (an env pool's step: the random policy over one instance, the env's RNG key and env ids first_env +
+    // row, the task's goal, steps and draws kept, no labels or final states) knows the optional inputs it does not
+    // take at compile time, so their pointers and tests take no registers
+    const i64* const actions = kPlain ? nullptr : A.actions;
+    const i32* const label_schema = kPlain ? nullptr : A.label_schema;
+    const u64* const seeds = kPlain ? nullptr : A.seeds;
+    const u32* const env_ids = kPlain ? nullptr : A.env_ids;
+    const u64* const goal_pos = kPlain ? nullptr : A.goal_pos;
+    u64* const final_states = kPlain ? nullptr : A.final_states;
+    u32* const reset_counts = kPlain ? nullptr : A.reset_counts;
+    i32* const steps = A.steps;
+    u64* const draws = A.draws;
+    const bool have_steps = kPlain || A.steps != nullptr;
+    const bool have_draws = kPlain || A.draws != nullptr;
     const u32 Lw = A.label_width;
     u64* grow = A.states + i * A.words;
     // the row's scalars are read before its words, so that their latencies overlap with the row's
     const bool already_goal = A.at_goal[i] != 0;
-    const i64 act_in = A.actions ? A.actions[i] : 0;
-    const u64 draws0 = A.draws ? A.draws[i] : 0;
-    const i32 steps0 = A.steps ? A.steps[i] : 0;
+    const i64 act_in = actions ? actions[i] : 0;
+    const u64 draws0 = have_draws ? draws[i] : 0;
+    const i32 steps0 = have_steps ? steps[i] : 0;
     const i32 next_in = (!kOne && A.next_task_ids) ? A.next_task_ids[i] : 0;
-    const i32 label_in = A.label_schema ? A.label_schema[i] : -1;
+    const i32 label_in = label_schema ? label_schema[i] : -1;
     // the count cache row: its counts stand for the row's state (and instance) when its fingerprint matches (reset,
     // refresh and step write it; a state written directly since is counted again)
     const u32 cw = A.cache_width;
@@ -1727,7 +1742,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         bool labelled = false;  // the move is the row's label (no pick)
         if (!already_goal && c == 0)
             st = kStuck;
-        else if (!already_goal && A.label_schema)
+        else if (!already_goal && label_schema)
         {
             // label mode (env.cpp:376-398, 423-425): the label moves where it is applicable, else the row is invalid
             bool ok = label_in >= 0 && static_cast<u32>(label_in) < T.num_schemas && L.counts[label_in] > 0;
@@ -1747,7 +1762,7 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             else
                 st = kInvalid;
         }
-        else if (!already_goal && A.actions)
+        else if (!already_goal && actions)
         {
             const i64 act = act_in;
             if (act < 0 || static_cast<u64>(act) >= c)
@@ -1758,8 +1773,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         else if (!already_goal)
         {
             // the key: the row's own, or the env's (read here in the batch-order path, which keeps fewer values live)
-            const u64 key = A.seeds ? A.seeds[i] : (kOne ? *A.seed : seed);
-            a = successor_index(key, A.env_ids ? static_cast<u64>(A.env_ids[i]) : A.first_env + i, draws0, c);
+            const u64 key = seeds ? seeds[i] : (kOne ? *A.seed : seed);
+            a = successor_index(key, env_ids ? static_cast<u64>(env_ids[i]) : A.first_env + i, draws0, c);
         }
         u32 rank = 0;
         if (st == kOk && !labelled)
@@ -1774,8 +1789,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         }
         if (lane == 0)
         {
-            if (A.draws)
-                A.draws[i] = draws0 + 1;
+            if (have_draws)
+                draws[i] = draws0 + 1;
             if (A.schema)
                 A.schema[i] = st == kOk ? static_cast<i32>(schema) : -1;
             if (A.invalid)
@@ -1791,14 +1806,14 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             break;
         // 3. the move, goal and (next phase) the successor count of the reached state
         moved_slot = apply_effects(T, H, L, schema, lane, A.status);
-        g = A.goal_pos ? mask_goal(L.row, A.goal_pos + i * A.words, A.goal_neg + i * A.words, T.W, lane)
-                       : goal_test(T, H, L.row, lane);
+        g = goal_pos ? mask_goal(L.row, goal_pos + i * A.words, A.goal_neg + i * A.words, T.W, lane)
+                     : goal_test(T, H, L.row, lane);
     }
     // 4. rewards, termination, truncation (env.cpp:466-485)
     const bool dead = !A.cfg.dead_end_none && !g && ((st == kOk && c2 == 0) || st == kStuck);
     const bool term = g || (dead && A.cfg.dead_end_terminal);
     const bool absorbed = already_goal || (st == kStuck && dead && A.cfg.dead_end_terminal);
-    const i32 t2 = A.steps ? steps0 + (absorbed ? 0 : 1) : 0;
+    const i32 t2 = have_steps ? steps0 + (absorbed ? 0 : 1) : 0;
     const bool trunc = !term && A.cfg.max_steps && t2 >= static_cast<i32>(A.cfg.max_steps);
     if (lane == 0)
     {
@@ -1819,10 +1834,10 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (A.goal)
             A.goal[i] = g ? 1 : 0;
     }
-    if (A.final_states)
+    if (final_states)
     {
         const u32 FW = A.final_words;
-        u64* f = A.final_states + i * FW;
+        u64* f = final_states + i * FW;
         for (u32 q = lane; q < FW; q += kWave)
             f[q] = q < T.W ? L.row[q] : 0;
     }
@@ -1864,12 +1879,12 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
     {
         // every autoreset advances the row's reset counter (a sampled restart comes in as next_task_ids, drawn before the
         // step with the counter's value before this advance)
-        if (A.reset_counts && lane == 0)
-            A.reset_counts[i] += 1;
+        if (reset_counts && lane == 0)
+            reset_counts[i] += 1;
         const InstDev& J = A.inst[next];  // a one-instance env restarts in instance 0
         const u32 z = min(A.words, max(J.W, T.W));  // the words the row may have dirtied: its old and new instance's
         copy_words(grow, J.initial, J.W, z, lane);
-        if (A.goal_pos)
+        if (goal_pos)
         {
             copy_words(A.goal_pos + i * A.words, J.goal_pos, J.W, z, lane);
             copy_words(A.goal_neg + i * A.words, J.goal_neg, J.W, z, lane);
@@ -1881,8 +1896,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
             if (A.count)
                 A.count[i] = static_cast<i32>(J.init_count);
             A.at_goal[i] = J.init_goal ? 1 : 0;
-            if (A.steps)
-                A.steps[i] = 0;
+            if (have_steps)
+                steps[i] = 0;
         }
         if (crow)
             for (u32 q = lane; q < cw; q += kWave)
@@ -1907,8 +1922,8 @@ __device__ __forceinline__ void step_row(const EnvArgs& A, const TaskDev& T, con
         if (lane == 0)
         {
             A.at_goal[i] = g ? 1 : 0;
-            if (A.steps)
-                A.steps[i] = t2;
+            if (have_steps)
+                steps[i] = t2;
             if (A.count)
                 A.count[i] = static_cast<i32>(c2);
         }
@@ -1946,7 +1961,7 @@ constexpr int kEnvStepWaves = kLevels ? 3 : 5;
 /// The step of a batch of one instance: every row in batch order with the kernel-argument tables, as instance 0 (the
 /// host checks given task ids and next_task_ids with launch_check_ids first); with kGroup, the rows of one instance's
 /// group of a batch grouped by instance.
-template<bool kStaged, bool kLevels, bool kGroup, bool kVisited>
+template<bool kStaged, bool kLevels, bool kGroup, bool kVisited, bool kPlain = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_eu(kEnvStepWaves<kLevels>))) void k_env_step(EnvArgs A)
 {
     extern __shared__ u64 smem[];
@@ -1971,7 +1986,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) __attribute__((amdgpu_waves_per_
         lds<u64>* waves = stage_hot<kStaged>(smem, T, &H);
         const Lds L = lds_of<kLevels>(waves + static_cast<u64>(wave) * wave_lds_words(T, kLevels), T);
         for (u64 i = static_cast<u64>(blockIdx.x) * nw + wave; i < A.rows; i += static_cast<u64>(gridDim.x) * nw)
-            step_row<kLevels, true, kVisited>(A, T, H, L, i, 0, lane, 0);
+            step_row<kLevels, true, kVisited, kPlain>(A, T, H, L, i, 0, lane, 0);
     }
 }
 
@@ -2867,12 +2882,17 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
     size_t lds = 0;
     const unsigned nw = waves_per_block(a.T, &lds);
     const bool group = a.groups.order != nullptr;
-    // the visited tables' code only in the launches that use it (it keeps more kernel arguments live)
+    // the visited tables' code only in the launches that use it (it keeps more kernel arguments live); the plain step
+    // (an env pool's random-policy step over one instance) compiles the optional inputs it does not take away
     const bool visited = a.visited.capacity || a.revisited;
+    const bool plain = !group && !visited && !a.actions && !a.label_schema && !a.seeds && !a.env_ids && !a.goal_pos && !a.final_states &&
+                       !a.reset_counts && !a.next_task_ids && a.steps && a.draws;
     const auto fn = group     ? variant(a.T, k_env_step<true, false, true, true>, k_env_step<true, true, true, true>,
                                         k_env_step<false, false, true, true>, k_env_step<false, true, true, true>)
                     : visited ? variant(a.T, k_env_step<true, false, false, true>, k_env_step<true, true, false, true>,
                                         k_env_step<false, false, false, true>, k_env_step<false, true, false, true>)
+                    : plain   ? variant(a.T, k_env_step<true, false, false, false, true>, k_env_step<true, true, false, false, true>,
+                                        k_env_step<false, false, false, false, true>, k_env_step<false, true, false, false, true>)
                               : variant(a.T, k_env_step<true, false, false, false>, k_env_step<true, true, false, false>,
                                         k_env_step<false, false, false, false>, k_env_step<false, true, false, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
@@ -2961,6 +2981,8 @@ void prepare_env_launches(const TaskDev& T)
     waves_per_block(T, &lds);
     for (const void* fn : {reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false, false>, k_env_step<true, true, false, false>,
                                                                  k_env_step<false, false, false, false>, k_env_step<false, true, false, false>)),
+                           reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false, false, true>, k_env_step<true, true, false, false, true>,
+                                                                 k_env_step<false, false, false, false, true>, k_env_step<false, true, false, false, true>)),
                            reinterpret_cast<const void*>(variant(T, k_env_step<true, false, false, true>, k_env_step<true, true, false, true>,
                                                                  k_env_step<false, false, false, true>, k_env_step<false, true, false, true>)),
                            reinterpret_cast<const void*>(variant(T, k_env_step<true, false, true, true>, k_env_step<true, true, true, true>,
