@@ -63,14 +63,27 @@ def host_info() -> dict:
 
 
 def load_traffic(kernel: str):
-    """HBM bytes per launch of a kernel, measured by rocprofv3 PMC counters (FETCH_SIZE, WRITE_SIZE, scaled by a plain
-    copy of known size) and committed in profiles/pmc_traffic.json; None if not measured."""
+    """HBM bytes per launch of a kernel, measured by rocprofv3 PMC counters (FETCH_SIZE, WRITE_SIZE, each scaled by what
+    it reads for a kernel of known traffic and the same access pattern: a plain copy for streaming kernels, the
+    random 8-byte loads of bench.py --random-ops for the state set's probes) and committed in
+    profiles/pmc_traffic.json; None if not measured."""
     p = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         k = json.load(f).get("kernels", {}).get(kernel)
     return k.get("traffic_bytes_per_launch") if k else None
+
+
+def load_bound(kernel: str):
+    """The counter evidence of what bounds a kernel, committed in profiles/pmc_bounds.json (from rocprofv3 PMC runs of
+    this bench): for the state set's probes the share of the measured random-access capacity their reads and atomics
+    use, for the env steps the share of the VALU issue slots; None if not measured."""
+    p = os.path.join(ROOT, "profiles", "pmc_bounds.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("kernels", {}).get(kernel)
 
 
 def bench_strips(steps: int, warmup: int, cpu: bool):
@@ -103,7 +116,8 @@ def bench_strips(steps: int, warmup: int, cpu: bool):
     traffic = load_traffic(f"brfs_{dom}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": f"brfs {dom}",
-                "bytes_per_launch": int(by[dom] / max(1, launches[dom])), "ms_per_launch": round(ms[dom] / max(1, launches[dom]), 4)}
+                "bytes_per_launch": int(by[dom] / max(1, launches[dom])), "ms_per_launch": round(ms[dom] / max(1, launches[dom]), 4),
+                "bound_evidence": load_bound(f"brfs_{dom}")}
     out = {
         "value": value, "unit": "expanded states/s", "ms_per_step": wall * 1e3 / steps, "roofline": roofline,
         "detail": {"states": r.states, "expanded": r.expanded, "generated": r.generated, "layers": r.layers, "status": r.status,
@@ -151,8 +165,9 @@ def bench_env(name: str, steps: int, warmup: int, cpu: bool, num_envs: int | Non
     pool.reset()
     for _ in range(warmup):
         pool.step(encode=encode, labels=False)
+    # the rate: the workload's whole horizon from reset, back-to-back steps, synchronized on both sides
+    pool.reset()
     torch.cuda.synchronize()
-    # the rate: back-to-back steps, synchronized on both sides
     t0 = time.perf_counter()
     for _ in range(steps):
         pool.step(encode=encode, labels=False)
@@ -172,10 +187,11 @@ def bench_env(name: str, steps: int, warmup: int, cpu: bool, num_envs: int | Non
     per_step = 2 * R + 36 + (encode * 4 + t.num_schemas if encode else 0)
     achieved = per_step * N / (kms * 1e-3) / 1e9
     out = {"env_steps_per_s": N * steps / wall, "num_envs": N, "steps_timed": steps, "ms_per_step": wall * 1e3 / steps,
-           "words": t.words, "bytes_per_env_step": per_step, "encode_atoms": encode,
+           "timed": f"the whole horizon from reset: {steps} steps of {N} envs", "words": t.words,
+           "bytes_per_env_step": per_step, "encode_atoms": encode,
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "env step", "ms_per_launch": round(kms, 4),
-                        "traffic": load_traffic(f"env_{name}")}}
+                        "traffic": load_traffic(f"env_{name}"), "bound_evidence": load_bound(f"env_{name}")}}
     if cpu:
         out["cpu_baseline"] = cpu_env(path, w)
     return out
@@ -223,7 +239,7 @@ def bench_dedup(steps: int, warmup: int, cpu: bool):
                         "frac": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4),
                         "kernel": "state-set batch insert (probe, winner scan, compaction) per 2^20-row batch",
                         "bytes_per_launch": int(alg / nb), "ms_per_launch": round(wall * 1e3 / nb, 4),
-                        "traffic": load_traffic("dedup_batch")}}
+                        "traffic": load_traffic("dedup_batch"), "bound_evidence": load_bound("dedup_probe")}}
     if cpu:
         out["cpu_baseline"] = cpu_dedup(words)
     return out
@@ -335,12 +351,13 @@ def main():
     steps, warmup = max(1, a.steps), max(0, a.warmup)
     head = bench_strips(steps, warmup, cpu) if (not only or "strips" in only) else None
     wl = {}
-    if not only or "gridworld" in only:
-        wl["gridworld"] = bench_env("gridworld", 256, 16, cpu)
-    if not only or "transport" in only:
-        wl["transport"] = bench_env("transport", 32, 4, cpu)
-    if not only or "transport_xl" in only:
-        wl["transport_xl"] = bench_env("transport_xl", 4, 1, cpu)
+    # each env workload over its stated horizon (gridworld 256, transport 512, transport_xl 128 steps) from reset
+    from mymyr_amd import workloads
+
+    for name, w, wu in (("gridworld", workloads.GRIDWORLD, 16), ("transport", workloads.TRANSPORT, 4),
+                        ("transport_xl", workloads.TRANSPORT_XL, 1)):
+        if not only or name in only:
+            wl[name] = bench_env(name, w.steps, wu, cpu)
     if not only or "dedup" in only:
         wl["dedup"] = bench_dedup(steps, min(warmup, 1), cpu)
     line = {

@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 16
+#define MYA_ABI_VERSION 17
 int mya_abi_version(void);
 
 /* Device memory held by the library (replaces DeviceContext::usage(), include/mymyr/cuda/runtime.hpp:140-146, 183):
@@ -483,7 +483,21 @@ typedef struct mya_brfs_options
     int32_t timed;
     double max_seconds;
     const volatile int32_t* cancel;
+    /* BrfsOptions::goal (brfs.hpp:87-91) as GoalSpec::AnyOf of ground conditions (include/mymyr/search/control.hpp:93-118,
+     * search::any_of, include/mymyr/search/goal.hpp:35): with goal_kind 1 a state is a goal iff one of goal_count
+     * conditions holds in it (goal_kind 0: the task's goal). Condition k's literals are the records
+     * [goal_offsets[k], goal_offsets[k + 1]) of goal_literals, MYA_GOAL_LITERAL_INTS int32 each: predicate, positive
+     * (0 or 1), the number of objects, then the objects. As the reference resolves them (src/mymyr/search/goal.cpp:14-60):
+     * a static literal is decided against the task's static facts (a false one leaves its condition out), a fluent atom
+     * outside its predicate's domains or without a slot makes a positive literal's condition impossible (left out) and
+     * a negative literal true (dropped). Host arrays. An invalid literal (predicate, object count or object out of
+     * range) is an error. */
+    int32_t goal_kind;
+    uint32_t goal_count;
+    const uint32_t* goal_offsets;
+    const int32_t* goal_literals;
 } mya_brfs_options;
+#define MYA_GOAL_LITERAL_INTS 9
 
 /* BrfsResult fields (include/mymyr/search/brfs.hpp:103-138). status: the reference's SearchStatus codes
  * (0 solved, 1 exhausted, 2 out of states, 3 out of time, 4 cancelled, 5 failed, 6 unsolvable). */
@@ -508,6 +522,12 @@ typedef struct mya_brfs_result
     uint64_t kernel_launches[8];
     uint64_t pruned;       /* successors not stored because they are blocked states */
     uint64_t memory_bytes; /* device bytes of the search's buffers (state set, arena, nodes, chunk and layer arrays) */
+    uint32_t words;        /* the task's state words at the end (BrfsResult::words; lazy slots: after interning) */
+    uint32_t fluent_slots; /* assigned fluent atom slots at the end (BrfsResult::fluent_slots) */
+    uint32_t threads_used; /* host threads the search ran on (BrfsResult::threads_used): 1, the calling thread */
+    uint32_t reserved2;
+    char store[16];        /* the store (BrfsResult::store): "device" (the device state set), "none" when nothing was searched */
+    char message[256];     /* why the search stopped early or ran otherwise than asked (BrfsResult::message); "" if neither */
 } mya_brfs_result;
 
 /* The plan of a solved search: BrfsResult::plan, cost and goal_state (include/mymyr/search/brfs.hpp:118-131), the

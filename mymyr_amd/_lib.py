@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 16  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 17  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -118,7 +118,14 @@ class BrfsOptions(Structure):
         ("timed", c_int32),
         ("max_seconds", c_double),
         ("cancel", c_void_p),
+        ("goal_kind", c_int32),
+        ("goal_count", c_uint32),
+        ("goal_offsets", c_void_p),
+        ("goal_literals", c_void_p),
     ]
+
+
+GOAL_LITERAL_INTS = 9  # MYA_GOAL_LITERAL_INTS
 
 
 class BrfsResult(Structure):
@@ -140,6 +147,12 @@ class BrfsResult(Structure):
         ("kernel_launches", c_uint64 * 8),
         ("pruned", c_uint64),
         ("memory_bytes", c_uint64),
+        ("words", c_uint32),
+        ("fluent_slots", c_uint32),
+        ("threads_used", c_uint32),
+        ("reserved2", c_uint32),
+        ("store", ctypes.c_char * 16),
+        ("message", ctypes.c_char * 256),
     ]
 
 

@@ -54,6 +54,7 @@ struct GoalDev
     const u32* neg;
     u32 npos, nneg;
     u32 unsat;
+    AnyOfDev any;  // BrfsOptions::goal as GoalSpec::AnyOf (any.any set): it decides instead of the task's goal
 };
 
 /// Slot words of 64 parents, bit-sliced: word s holds bit s of each of the wave's 64 parents (bit t: parent t), for
@@ -182,11 +183,28 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_count(const u64* __restr
         return;
     u64* B = Bs[wave];
     const u64 vm = load_slices<W>(B, arena, first, base, n, lane);
-    u64 gm = goal.unsat ? 0 : vm;
-    for (u32 i = 0; i < goal.npos; ++i)
-        gm &= B[goal.pos[i]];
-    for (u32 i = 0; i < goal.nneg; ++i)
-        gm &= ~B[goal.neg[i]];
+    u64 gm = 0;
+    if (goal.any.any)
+    {
+        // AnyOf: the parents for which one of the goals holds, goal by goal over the bit slices
+        for (u32 k = 0; k < goal.any.count; ++k)
+        {
+            u64 m = vm;
+            for (u32 i = goal.any.off[2 * k]; i < goal.any.off[2 * k + 1]; ++i)
+                m &= B[goal.any.slots[i]];
+            for (u32 i = goal.any.off[2 * k + 1]; i < goal.any.off[2 * k + 2]; ++i)
+                m &= ~B[goal.any.slots[i]];
+            gm |= m;
+        }
+    }
+    else
+    {
+        gm = goal.unsat ? 0 : vm;
+        for (u32 i = 0; i < goal.npos; ++i)
+            gm &= B[goal.pos[i]];
+        for (u32 i = 0; i < goal.nneg; ++i)
+            gm &= ~B[goal.neg[i]];
+    }
     // Per lane (one action of each group), a bit-sliced counter over the 64 parents: plane k holds bit k of how many of
     // the lane's actions so far apply to each parent. Adding a group's mask is a ripple carry through the planes, and
     // only the final planes are transposed (bit k of parent t's count over the lanes = popcount of plane k's column t),
@@ -514,7 +532,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     constexpr u32 S = 1;  // one count and one offset per parent
     const GroundDev& g = tb.g;
     const u64* d_masks = tb.masks;
-    const GoalDev& goal = tb.goal;
+    GoalDev goal = tb.goal;
+    goal.any = upload_any_of(o, b, stream);
     const u64* d_slot_cid = tb.slot_cid;
 
     // capacity: the arena holds every stored state

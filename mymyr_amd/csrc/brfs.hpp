@@ -33,7 +33,15 @@ struct BrfsOptionsC
     bool timed = false;        // stop with OutOfTime once max_seconds have passed
     double max_seconds = 0;
     const volatile i32* cancel = nullptr;  // stop with Cancelled once another thread sets it nonzero
+    // BrfsOptions::goal as GoalSpec::AnyOf (include/mymyr/search/control.hpp:93-118): a state is a goal iff one of the
+    // goals' positive slots all hold and its negative ones none (the goals that can never hold left out, so no goal at
+    // all makes no state a goal); any_of false: the task's goal
+    bool any_of = false;
+    std::vector<std::vector<u32>> goal_pos, goal_neg;
 };
+
+/// Whether one of the AnyOf goals holds in a row of `words` words (host).
+bool any_of_holds(const BrfsOptionsC& o, const u64* row, u32 words);
 
 /// Kernel classes of the device BrFS (timed with HIP events when BrfsOptionsC::timings is set).
 enum BrfsKernel : int

@@ -184,6 +184,33 @@ inline BlockedView upload_blocked(const std::vector<u64>& rows, u32 task_words, 
     return v;
 }
 
+/// The AnyOf goals of the options on the device (AnyOfDev{} when the task's goal decides).
+inline AnyOfDev upload_any_of(const BrfsOptionsC& o, Buffers& b, hipStream_t stream)
+{
+    AnyOfDev d{};
+    if (!o.any_of)
+        return d;
+    std::vector<u32> off{0}, slots;
+    for (size_t k = 0; k < o.goal_pos.size(); ++k)
+    {
+        slots.insert(slots.end(), o.goal_pos[k].begin(), o.goal_pos[k].end());
+        off.push_back(static_cast<u32>(slots.size()));
+        slots.insert(slots.end(), o.goal_neg[k].begin(), o.goal_neg[k].end());
+        off.push_back(static_cast<u32>(slots.size()));
+    }
+    u32* d_off = b.alloc<u32>(off.size(), "goal offsets");
+    u32* d_slots = b.alloc<u32>(std::max<size_t>(1, slots.size()), "goal slots");
+    hip_check(hipMemcpyAsync(d_off, off.data(), off.size() * sizeof(u32), hipMemcpyHostToDevice, stream), "goal offsets");
+    if (!slots.empty())
+        hip_check(hipMemcpyAsync(d_slots, slots.data(), slots.size() * sizeof(u32), hipMemcpyHostToDevice, stream), "goal slots");
+    hip_check(hipStreamSynchronize(stream), "goals");
+    d.off = d_off;
+    d.slots = d_slots;
+    d.count = static_cast<u32>(o.goal_pos.size());
+    d.any = 1;
+    return d;
+}
+
 /// The start state as a row of W words (BrfsOptionsC::start, else the task's initial state).
 inline std::vector<u64> start_row(const CompiledTask& task, const BrfsOptionsC& o, u32 W)
 {

@@ -115,6 +115,22 @@ bool goal_holds(const CompiledTask& task, const std::vector<u64>& row)
 
 }  // namespace
 
+bool any_of_holds(const BrfsOptionsC& o, const u64* row, u32 words)
+{
+    auto bit = [&](u32 s) { return s / 64 < words && ((row[s / 64] >> (s % 64)) & 1); };
+    for (size_t k = 0; k < o.goal_pos.size(); ++k)
+    {
+        bool ok = true;
+        for (u32 s : o.goal_pos[k])
+            ok = ok && bit(s);
+        for (u32 s : o.goal_neg[k])
+            ok = ok && !bit(s);
+        if (ok)
+            return true;
+    }
+    return false;
+}
+
 BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOptionsC& o, std::vector<std::array<u64, 3>>& lc,
                       const LazyResolve* lazy)
 {
@@ -203,7 +219,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         u64 nn = 0;
         state_set_insert(set, d_s0, 1, nullptr, nullptr, &nn, stream);
         hipLaunchKernelGGL(k_set_u64, dim3(1), dim3(1), 0, stream, nodes, ~u64{0});
-        const u8 g0 = goal_holds(task, s0) ? 1 : 0;
+        const u8 g0 = (o.any_of ? any_of_holds(o, s0.data(), static_cast<u32>(s0.size())) : goal_holds(task, s0)) ? 1 : 0;
         hip_check(hipMemcpyAsync(goal_id, &g0, 1, hipMemcpyHostToDevice, stream), "start goal");
         hip_check(hipStreamSynchronize(stream), "start state");
     }
@@ -217,6 +233,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
     // witness pruning (the reference's default): one successor per effect-relevant binding, with the witnesses the
     // matcher binds first (tasks whose schemas have no witness parameter expand the same either way)
     base_args.witness = o.witness_pruning && T.witness ? 1 : 0;
+    base_args.any_goal = upload_any_of(o, b, stream);
     // lazy slots: the stored states move to a set of rows of nw words in id order (so their ids stay), a chunk at a
     // time through new candidate rows of that width; the blocked table follows the width
     auto widen = [&](u32 nw) {

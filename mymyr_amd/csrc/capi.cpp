@@ -11,6 +11,7 @@
 #include "lifted.hpp"
 #include "task.hpp"
 
+#include <cstdio>
 #include <cstring>
 #include <fstream>
 #include <sstream>
@@ -321,6 +322,113 @@ int mya_random_ops(uint64_t* table, uint64_t words, uint64_t n, int kind, uint64
     });
 }
 
+namespace
+{
+[[noreturn]] void condition_error(const std::string& what) { throw std::invalid_argument("mymyr: condition: " + what); }
+
+/// BrfsOptions::goal as GoalSpec::AnyOf (search::any_of, src/mymyr/search/goal.cpp:14-70): each condition's literals
+/// are checked first (GroundCondition::validate, src/mymyr/successor/conditions.cpp:757-766), then resolved in order: a
+/// static literal decided against the static facts (false: the condition can never hold and is left out), a fluent
+/// atom outside its predicate's domains or without a slot is never true (a positive literal leaves its condition out, a
+/// negative one is dropped), any other fluent literal becomes its slot.
+/// Lazy slots: the slot of canonical atom `cid`, interned now (the next slot) if it has none, with the task's device
+/// image brought up to date when it is on the device (AtomIndex::slot_if_any, include/mymyr/task/atom_index.hpp:169).
+u32 intern_goal_atom(mya_task* t, u64 cid)
+{
+    std::lock_guard lock(t->mutex);
+    CompiledTask& C = *t->compiled;
+    if (C.slot_of[cid] != kNone)
+        return C.slot_of[cid];
+    const auto ranges = intern_atoms(C, {cid});
+    if (t->dev.image)
+    {
+        for (const auto& [a, b] : ranges)
+            if (b > a)
+                hip_check(hipMemcpy(t->dev.image + a, C.image.data() + a, (b - a) * sizeof(u64), hipMemcpyHostToDevice), "task image");
+        *t->dev.thost = task_dev(t->dev.image, C.header());
+        t->dev.thost->missing = t->dev.missing;
+    }
+    return C.slot_of[cid];
+}
+
+void resolve_any_of(mya_task* task, const mya_brfs_options& op, BrfsOptionsC& o)
+{
+    const CompiledTask& C = *task->compiled;
+    if (op.goal_kind == 0)
+        return;
+    if (op.goal_kind != 1)
+        throw std::invalid_argument("mymyr_amd: brfs: goal_kind must be 0 (the task's goal) or 1 (any of goal_count conditions)");
+    if (op.goal_count && !op.goal_offsets)
+        throw std::invalid_argument("mymyr_amd: brfs: goal_count without goal_offsets");
+    const TaskText& T = C.text;
+    o.any_of = true;
+    for (u32 k = 0; k < op.goal_count; ++k)
+    {
+        const u32 lo = op.goal_offsets[k], hi = op.goal_offsets[k + 1];
+        if (hi < lo)
+            throw std::invalid_argument("mymyr_amd: brfs: goal_offsets must not decrease");
+        if (hi > lo && !op.goal_literals)
+            throw std::invalid_argument("mymyr_amd: brfs: goal literals missing");
+        auto rec = [&](u32 l) { return op.goal_literals + static_cast<size_t>(l) * MYA_GOAL_LITERAL_INTS; };
+        for (u32 l = lo; l < hi; ++l)
+        {
+            const int32_t* r = rec(l);
+            const std::string where = "literal " + std::to_string(l - lo);
+            if (r[0] < 0 || static_cast<u32>(r[0]) >= T.preds.size())
+                condition_error(where + ": predicate index " + std::to_string(r[0]) + " out of range");
+            const PredicateText& P = T.preds[static_cast<u32>(r[0])];
+            if (r[2] < 0 || static_cast<u32>(r[2]) != P.arity)
+                condition_error(where + ": " + P.name + " takes " + std::to_string(P.arity) + " arguments, got " + std::to_string(r[2]));
+            if (P.arity > MYA_GOAL_LITERAL_INTS - 3)
+                throw std::invalid_argument("mymyr_amd: brfs: goal literals hold at most 6 objects");
+            for (u32 i = 0; i < P.arity; ++i)
+                if (r[3 + i] < 0 || static_cast<u32>(r[3 + i]) >= T.objects)
+                    condition_error(where + ": object index " + std::to_string(r[3 + i]) + " out of range");
+        }
+        std::vector<u32> pos, neg;
+        bool possible = true;
+        for (u32 l = lo; l < hi && possible; ++l)
+        {
+            const int32_t* r = rec(l);
+            const u32 p = static_cast<u32>(r[0]);
+            const bool positive = r[1] != 0;
+            const PredicateText& P = T.preds[p];
+            u32 objs[6] = {};
+            for (u32 i = 0; i < P.arity; ++i)
+                objs[i] = static_cast<u32>(r[3 + i]);
+            if (P.kind == 'S')
+            {
+                if (C.static_holds(p, objs) != positive)
+                    possible = false;
+                continue;
+            }
+            if (P.kind != 'F')
+                throw std::invalid_argument("mymyr_amd: brfs: goal literals over derived predicates are not supported");
+            u32 slot = kNone;
+            if (C.layout.size[p])
+            {
+                // frozen slots: the atom's slot if it has one; lazy slots: interned now, in the literals' order
+                const u64 cid = C.layout.encode(p, objs, P.arity);
+                if (cid < C.layout.fluent_count)
+                    slot = lazy_task(task) ? intern_goal_atom(task, cid) : C.slot_of[cid];
+            }
+            if (slot == kNone)
+            {
+                if (positive)
+                    possible = false;
+                continue;
+            }
+            (positive ? pos : neg).push_back(slot);
+        }
+        if (possible)
+        {
+            o.goal_pos.push_back(std::move(pos));
+            o.goal_neg.push_back(std::move(neg));
+        }
+    }
+}
+}  // namespace
+
 int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* result, uint64_t* layer_counts, uint32_t cap,
              mya_brfs_plan* plan)
 {
@@ -363,13 +471,16 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         o.timed = options->timed != 0;
         o.max_seconds = options->max_seconds;
         o.cancel = options->cancel;
+        resolve_any_of(task, *options, o);
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
-        if (o.stop_at_goal && task->compiled->goal_fixed_unsat)
+        bool searched = true;
+        if (o.stop_at_goal && !o.any_of && task->compiled->goal_fixed_unsat)
         {
-            // the goal fails in every state: the start state alone, nothing expanded (brfs.cpp:1851-1861)
+            // the task's goal fails in every state: the start state alone, nothing expanded (brfs.cpp:1851-1861)
             r.status = kUnsolvable;
             r.states = 1;
+            searched = false;
         }
         else
         {
@@ -392,6 +503,10 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         result->device_s = r.device_s;
         result->pruned = r.pruned;
         result->memory_bytes = r.memory_bytes;
+        result->words = task->compiled->words;
+        result->fluent_slots = task->compiled->fluent_slots;
+        result->threads_used = 1;
+        std::snprintf(result->store, sizeof(result->store), "%s", searched ? "device" : "none");
         if (plan)
         {
             if (plan->binding && plan->label_width < r.plan_width)

@@ -149,4 +149,31 @@ enum StatusBit : u32
     kStatusGoalMask = 1u << 5,      // per-env goal masks set bits past the task's fluent slots
     kStatusTaskId = 1u << 6,        // a task id (of a row or of next_task_ids) names no instance of the table
 };
+/// GoalSpec::AnyOf on the device: goal k holds in a state iff the slots slots[off[2k], off[2k + 1]) are set and the
+/// slots [off[2k + 1], off[2k + 2]) clear (count 0 with `any` set: no state is a goal).
+struct AnyOfDev
+{
+    const u32* off;    // [2 count + 1]
+    const u32* slots;
+    u32 count;
+    u32 any;           // 1: the AnyOf goals decide (0: the task's goal)
+};
+
+/// Whether one of the AnyOf goals holds in a row (one lane's view of it: bit s of the row).
+template<class Bit>
+__device__ __forceinline__ bool any_of_holds_dev(const AnyOfDev& g, Bit&& bit)
+{
+    for (u32 k = 0; k < g.count; ++k)
+    {
+        bool ok = true;
+        for (u32 i = g.off[2 * k]; i < g.off[2 * k + 1] && ok; ++i)
+            ok = bit(g.slots[i]);
+        for (u32 i = g.off[2 * k + 1]; i < g.off[2 * k + 2] && ok; ++i)
+            ok = !bit(g.slots[i]);
+        if (ok)
+            return true;
+    }
+    return false;
+}
+
 }  // namespace mya

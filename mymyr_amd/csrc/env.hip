@@ -2593,7 +2593,9 @@ __device__ __forceinline__ void expand_row(const ExpandArgs& A, const TaskDev& T
                 }
                 if (A.goal)
                 {
-                    const bool g = goal_test(T, H, L.row, lane);
+                    const bool g = A.any_goal.any
+                                       ? any_of_holds_dev(A.any_goal, [&](u32 s) { return s < 64 * T.W && row_bit(L.row, s); })
+                                       : goal_test(T, H, L.row, lane);
                     if (lane == 0)
                         A.goal[pos] = g ? 1 : 0;
                 }

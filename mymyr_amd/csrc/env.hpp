@@ -266,6 +266,7 @@ struct ExpandArgs
     u32* words_needed;  // device word: the widest trimmed successor that did not fit out_words
     u32* status;
     u32 witness;        // witness pruning (one-instance launches): one successor per effect-relevant binding
+    AnyOfDev any_goal;  // the goal flags' goal when any_goal.any is set (a search's GoalSpec::AnyOf), else the task's
 };
 
 void launch_expand(const ExpandArgs& a, hipStream_t stream);

@@ -51,6 +51,11 @@ class BrfsResult:
     goal_state: np.ndarray | None = None
     pruned: int = 0
     memory_bytes: int = 0
+    words: int = 0          # the task's state words at the end (lazy slots: after interning)
+    fluent_slots: int = 0   # assigned fluent atom slots at the end
+    threads_used: int = 1   # host threads the search ran on (the calling thread; the work runs on the device)
+    store: str = ""         # "device" (the device state set), "none" when nothing was searched
+    message: str = ""       # why the search stopped early or ran otherwise than asked ("" if neither)
 
 
 KERNEL_CLASSES = ["count", "emit", "insert", "unused", "rank", "compact", "other"]
@@ -89,17 +94,38 @@ def _rows(task: Task, rows, what: str) -> np.ndarray:
     return a
 
 
+def _goal_records(task: Task, goal) -> tuple[np.ndarray, np.ndarray]:
+    """AnyOf goal conditions as the C ABI's offsets [k + 1] and literal records (predicate, positive, object count,
+    objects). A condition is a sequence of (predicate index, positive, objects) literals."""
+    if isinstance(goal, (str, bytes)) or not hasattr(goal, "__iter__"):
+        raise TypeError("mymyr: goal= takes a sequence of ground conditions (each a sequence of (predicate, positive, objects))")
+    offs, recs = [0], []
+    for cond in goal:
+        for lit in cond:
+            pred, pos, objs = lit
+            objs = [int(o) for o in objs]
+            if len(objs) > _lib.GOAL_LITERAL_INTS - 3:
+                raise ValueError("mymyr_amd: brfs: goal literals hold at most 6 objects")
+            recs.append([int(pred), int(bool(pos)), len(objs)] + objs + [0] * (_lib.GOAL_LITERAL_INTS - 3 - len(objs)))
+        offs.append(len(recs))
+    return np.array(offs, np.uint32), np.array(recs, np.int32).reshape(-1, _lib.GOAL_LITERAL_INTS)
+
+
 def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None, max_expanded: int | None = None,
          witness_pruning: bool = True, stop_at_goal: bool = True, fingerprint: bool = False, layer_stats: bool = True,
          chunk: int = 0, memory_states: int = 0, timings: bool = False, start=None, blocked_states=None,
-         max_seconds: float | None = None, cancel: CancelToken | None = None) -> BrfsResult:
+         max_seconds: float | None = None, cancel: CancelToken | None = None, goal=None) -> BrfsResult:
     """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
     (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer.
 
     start: the start state's words (default: the task's initial state). blocked_states: states never stored ([k, words]
     or a list of rows); a successor equal to one counts as generated and pruned (the start state is exempt).
     max_seconds (None: unlimited) and cancel (a CancelToken) stop the search between device batches with status
-    "out_of_time" or "cancelled" (python/src/search_bindings.cpp:516-538, 2135-2145)."""
+    "out_of_time" or "cancelled" (python/src/search_bindings.cpp:516-538, 2135-2145).
+    goal (None: the task's goal): BrfsOptions::goal as GoalSpec::AnyOf, a sequence of ground conditions, each a sequence
+    of (predicate index, positive, object indices) literals; a state is a goal iff one of them holds in it (the
+    reference's goal= with GroundConditions, python/src/search_bindings.cpp:439-505; conditions that can never hold are
+    left out)."""
     if max_seconds is not None and not max_seconds >= 0:
         raise ValueError("mymyr_amd: brfs: max_seconds must be >= 0")
     if cancel is not None and not isinstance(cancel, CancelToken):
@@ -110,12 +136,14 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     bl = None if blocked_states is None else _rows(task, np.zeros((0, task.words), np.uint64) if len(blocked_states) == 0
                                                    else blocked_states, "blocked_states")
     timed = max_seconds is not None and np.isfinite(max_seconds)
+    go, gl = _goal_records(task, goal) if goal is not None else (None, None)
     o = _lib.BrfsOptions(UNBOUNDED32 if max_depth is None else max_depth, int(witness_pruning),
                          UNBOUNDED64 if max_states is None else max_states, UNBOUNDED64 if max_expanded is None else max_expanded,
                          int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0,
                          None if st is None else st.ctypes.data, None if bl is None or bl.shape[0] == 0 else bl.ctypes.data,
                          0 if bl is None else bl.shape[0], task.words, int(timed), float(max_seconds) if timed else 0.0,
-                         None if cancel is None else cancel.address)
+                         None if cancel is None else cancel.address, 0 if goal is None else 1, 0 if goal is None else len(go) - 1,
+                         None if go is None else go.ctypes.data, None if gl is None or gl.size == 0 else gl.ctypes.data)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -132,7 +160,9 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
                for i, c in enumerate(KERNEL_CLASSES)}
     res = BrfsResult(STATUS.get(r.status, str(r.status)), r.states, r.expanded, r.generated, r.goal_states, r.layers,
                      bool(r.exhausted), bool(r.solved), r.fingerprint, r.first_goal, r.search_s, r.device_s,
-                     lc[:n].tolist() if layer_stats else [], kernels, pruned=r.pruned, memory_bytes=r.memory_bytes)
+                     lc[:n].tolist() if layer_stats else [], kernels, pruned=r.pruned, memory_bytes=r.memory_bytes,
+                     words=r.words, fluent_slots=r.fluent_slots, threads_used=r.threads_used, store=r.store.decode(),
+                     message=r.message.decode())
     if r.solved:
         if plan.length > cap:
             raise RuntimeError(f"mymyr_amd: brfs: a plan of {plan.length} actions (at most {cap} are read)")

@@ -49,7 +49,26 @@ class BrfsOptions(Structure):
         ("words", c_uint32),
         ("reserved", c_uint32),
         ("max_seconds", c_double),
+        ("goal_kind", c_int32),
+        ("goal_count", c_uint32),
+        ("goal_offsets", c_void_p),
+        ("goal_literals", c_void_p),
     ]
+
+
+def goal_records(goal) -> tuple[np.ndarray, np.ndarray]:
+    """AnyOf goal conditions (a list of conditions, each a list of (predicate, positive, objects) literals) as the
+    harness's offsets [k + 1] and 8-int32 literal records (predicate, positive, objects, zero padded)."""
+    offs = [0]
+    recs = []
+    for cond in goal:
+        for pred, pos, objs in cond:
+            objs = list(objs)
+            if len(objs) > 6:
+                raise ValueError("goal literals of more than 6 objects")
+            recs.append([int(pred), int(bool(pos))] + [int(o) for o in objs] + [0] * (6 - len(objs)))
+        offs.append(len(recs))
+    return np.array(offs, np.uint32), np.array(recs if recs else np.zeros((0, 8)), np.int32).reshape(-1, 8)
 
 
 class PoolOut(Structure):
@@ -77,6 +96,12 @@ class BrfsResult(Structure):
         ("pruned", c_uint64),
         ("plan_len", c_uint32),
         ("goal_words", c_uint32),
+        ("words", c_uint32),
+        ("fluent_slots", c_uint32),
+        ("threads_used", c_uint32),
+        ("reserved", c_uint32),
+        ("store", ctypes.c_char * 16),
+        ("message", ctypes.c_char * 256),
     ]
 
 
@@ -425,15 +450,19 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 
 
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
-         stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf")):
+         stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf"),
+         goal=None):
     """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
-    (schema, binding) pairs, the goal state's words and the cost. start [words] and blocked_states [k, words] are
-    rows of the task's table words."""
+    (schema, binding) pairs, the goal state's words and the cost; the result's words, fluent_slots, threads_used, store
+    and message. start [words] and blocked_states [k, words] are rows of the task's table words; goal (None: the task's)
+    is BrfsOptions::goal = search::any_of over ground conditions, each a list of (predicate, positive, objects)."""
     W = task.table_words
     st = None if start is None else np.ascontiguousarray(np.asarray(start, np.uint64).reshape(-1)[:W])
     bl = None if blocked_states is None else np.ascontiguousarray(np.asarray(blocked_states, np.uint64).reshape(-1, W))
+    go, gl = goal_records(goal) if goal is not None else (None, None)
     o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
-                    max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds)
+                    max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds,
+                    0 if goal is None else 1, 0 if goal is None else len(goal), _p(go), _p(gl))
     r = BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -449,8 +478,10 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         "states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.goal_states,
         "fingerprint": r.fingerprint, "layers": r.layers, "status": r.status, "solved": bool(r.solved),
         "exhausted": bool(r.exhausted), "seconds": r.seconds, "layer_counts": lc[:n].tolist(), "pruned": r.pruned,
+        "words": r.words, "fluent_slots": r.fluent_slots, "threads_used": r.threads_used, "store": r.store.decode(),
+        "message": r.message.decode(),
     }
-    del st, bl
+    del st, bl, go, gl
     task.refresh()
     if r.solved:
         k = min(r.plan_len, cap)

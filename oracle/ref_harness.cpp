@@ -25,6 +25,7 @@
 #include "mymyr/rl/visited.hpp"
 #include "mymyr/core/team.hpp"
 #include "mymyr/search/brfs.hpp"
+#include "mymyr/search/goal.hpp"
 #include "mymyr/state/concurrent_store.hpp"
 #include "mymyr/state/flat_store.hpp"
 #include "mymyr/successor/successors.hpp"
@@ -35,6 +36,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -111,6 +113,12 @@ struct mref_brfs_options
     uint32_t words;
     uint32_t reserved;
     double max_seconds;       // BrfsOptions::max_seconds (infinity: unbounded)
+    // BrfsOptions::goal: goal_kind 1 = search::any_of over goal_count ground conditions, condition k's literals the
+    // 8-int32 records [goal_offsets[k], goal_offsets[k + 1]) of goal_literals: predicate, positive, then the objects
+    int32_t goal_kind;
+    uint32_t goal_count;
+    const uint32_t* goal_offsets;
+    const int32_t* goal_literals;
 };
 
 struct mref_brfs_result
@@ -125,6 +133,12 @@ struct mref_brfs_result
     uint64_t pruned;
     uint32_t plan_len;  // actions of the plan (those past plan_cap are not written)
     uint32_t goal_words;  // words of goal_state (0: none)
+    uint32_t words;         // BrfsResult::words
+    uint32_t fluent_slots;  // BrfsResult::fluent_slots
+    uint32_t threads_used;  // BrfsResult::threads_used
+    uint32_t reserved;
+    char store[16];         // BrfsResult::store
+    char message[256];      // BrfsResult::message
 };
 
 const char* mref_last_error() { return g_error.c_str(); }
@@ -727,6 +741,24 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
             for (uint64_t k = 0; k < o->blocked_count; ++k)
                 b.blocked_states.push_back(State(std::span<const u64>(o->blocked + k * o->words, o->words)));
             b.max_seconds = o->max_seconds;
+            if (o->goal_kind == 1)
+            {
+                std::vector<GroundCondition> conds(o->goal_count);
+                const formalism::TaskData& td = t->task->data();
+                for (u32 k = 0; k < o->goal_count; ++k)
+                    for (u32 l = o->goal_offsets[k]; l < o->goal_offsets[k + 1]; ++l)
+                    {
+                        const int32_t* rec = o->goal_literals + static_cast<usize>(l) * 8;
+                        GroundLiteral gl;
+                        gl.atom.predicate = PredicateId{static_cast<u32>(rec[0])};
+                        gl.positive = rec[1] != 0;
+                        const u32 ar = td.predicates.at(static_cast<u32>(rec[0])).arity;
+                        for (u32 i = 0; i < ar; ++i)
+                            gl.atom.objects.push_back(ObjectId{static_cast<u32>(rec[2 + i])});
+                        conds[k].literals.push_back(std::move(gl));
+                    }
+                b.goal = search::any_of(*t->task, conds);
+            }
             b.canonical_order = o->canonical_order != 0;
             b.stop_at_goal = o->stop_at_goal != 0;
             b.fingerprint = o->fingerprint != 0;
@@ -745,6 +777,11 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
             r->exhausted = x.exhausted;
             r->cost = x.cost;
             r->pruned = x.pruned;
+            r->words = x.words;
+            r->fluent_slots = x.fluent_slots;
+            r->threads_used = x.threads_used;
+            std::snprintf(r->store, sizeof(r->store), "%s", x.store.c_str());
+            std::snprintf(r->message, sizeof(r->message), "%s", x.message.c_str());
             r->plan_len = static_cast<uint32_t>(x.plan.size());
             for (u32 i = 0; i < x.plan.size() && i < plan_cap; ++i)
             {

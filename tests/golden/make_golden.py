@@ -389,6 +389,88 @@ def make_successors_witness():
     dump("successors_witness.json", out)
 
 
+def task_predicates(path):
+    """(kind, arity) per predicate of a task file (its P section: "<kind> <arity> <name>" lines)."""
+    preds = []
+    with open(path) as f:
+        lines = f.read().split("\n")
+    i = next(k for k, l in enumerate(lines) if l.startswith("P "))
+    for l in lines[i + 1: i + 1 + int(lines[i].split()[1])]:
+        kind, ar = l.split()[:2]
+        preds.append((kind, int(ar)))
+    return preds
+
+
+def goal_conditions(name, atoms, seed):
+    """AnyOf goal conditions for a task: per random walk of 3, 5 and 8 steps from the initial state, two or three of the
+    reached state's atoms that the initial state does not hold (positive) and one atom it does not hold (negative); then a condition with a false static
+    literal and its negation (never holds: left out)."""
+    t = ref.RefTask(fx.task_path(name), atoms)
+    preds = task_predicates(fx.task_path(name))
+    rng = np.random.default_rng(seed)
+    rec, _ = t.slot_records()
+    conds = []
+    for depth in (3, 5, 8):
+        row = t.initial_state()
+        for _ in range(depth):
+            sc, _, rs = t.successors(row)
+            if len(sc) == 0:
+                break
+            row = rs[int(rng.integers(len(sc)))]
+        t.refresh()
+        rec, _ = t.slot_records()
+        init = t.initial_state(len(row))
+        bits = [s for s in range(len(rec)) if (int(row[s // 64]) >> (s % 64)) & 1]
+        new_bits = [s for s in bits if not (int(init[s // 64]) >> (s % 64)) & 1] or bits
+        off = [s for s in range(len(rec)) if s not in set(bits)]
+        lits = []
+        for s in rng.choice(new_bits, size=min(len(new_bits), 2 + depth % 2), replace=False):
+            p = int(rec[s][0])
+            lits.append([p, True, [int(x) for x in rec[s][1:1 + preds[p][1]]]])
+        if off:
+            s = int(rng.choice(off))
+            p = int(rec[s][0])
+            lits.append([p, False, [int(x) for x in rec[s][1:1 + preds[p][1]]]])
+        conds.append(lits)
+    # a static literal and its negation: one of them is false, so the condition never holds (left out)
+    static = [p for p, (k, a) in enumerate(preds) if k == "S" and a == 1]
+    if static:
+        p = static[0]
+        conds.append([[p, False, [0]], [p, True, [0]]] + conds[0])
+    return conds
+
+
+def make_brfs_goals():
+    """BrfsOptions::goal as GoalSpec::AnyOf (search::any_of over ground conditions): goal stops, plans and goal states,
+    counts of goal states over whole searches, a max_states cut, the lazy slots' resolution of goal atoms at the search's
+    start, and the result's words, fluent_slots, threads_used, store and message."""
+    out = {}
+    for name, atoms, seed, kws in [
+            ("gripper__prob05", "auto", 1, [dict(stop_at_goal=True), dict(stop_at_goal=False, max_states=30000)]),
+            ("blocks__probBLOCKS-8-0", "auto", 2, [dict(stop_at_goal=True), dict(stop_at_goal=False, max_depth=6)]),
+            ("transport_w20_3", "auto", 3, [dict(stop_at_goal=True), dict(stop_at_goal=False, max_states=60000)]),
+            ("blocks__probBLOCKS-8-0", "lazy", 2, [dict(stop_at_goal=True), dict(stop_at_goal=False, max_depth=5)])]:
+        conds = goal_conditions(name, "auto", seed)
+        for i, kw in enumerate(kws):
+            t = ref.RefTask(fx.task_path(name), atoms)
+            r = ref.brfs(t, goal=conds, fingerprint=True, **kw)
+            r.pop("seconds")
+            r["options"] = kw
+            r["goal"] = conds
+            r["atoms"] = atoms
+            out[f"{name}:{atoms}:{i}"] = r
+            print("goals", name, atoms, kw, r["states"], r["status"], r["goal_states"], flush=True)
+        # no condition can hold: every state is tested, none is a goal
+        t = ref.RefTask(fx.task_path(name), atoms)
+        r = ref.brfs(t, goal=[conds[-1][:2]], fingerprint=True, stop_at_goal=True, max_states=5000)
+        r.pop("seconds")
+        r["options"] = dict(stop_at_goal=True, max_states=5000)
+        r["goal"] = [conds[-1][:2]]
+        r["atoms"] = atoms
+        out[f"{name}:{atoms}:never"] = r
+    dump("brfs_goals.json", out)
+
+
 def walk_states(t, depths, seed):
     """One state per entry of `depths`: the end of a seeded random walk of that many steps from the initial state (a walk
     that reaches a dead end stops there)."""
@@ -591,7 +673,7 @@ def main():
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
-             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick)}
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick)}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

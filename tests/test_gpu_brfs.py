@@ -253,3 +253,52 @@ def test_tasks_with_collapsed_parameters_and_encoding_goal(golden, key):
     r = device(golden, name, full=True, **exp["options"])
     assert not same(r, exp), (key, same(r, exp))
     assert same_plan(r, exp), (key, r["result"].plan[:4], exp.get("plan", [])[:4])
+
+
+GOAL_KEYS = sorted(__import__("json").load(open(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                                                          "brfs_goals.json"))))
+
+
+@pytest.mark.parametrize("key", GOAL_KEYS)
+def test_any_of_goals(golden, key):
+    """BrfsOptions::goal as GoalSpec::AnyOf over ground conditions (search::any_of: static literals decided, fluent atoms
+    resolved to slots, interned at the search's start under lazy slots; impossible conditions left out): goal stops with
+    their plans and goal states, goal-state counts over whole searches, a max_states cut and conditions that can never
+    hold, on the ground-action driver (gripper, blocks), the wide-row driver (20-word transport) and lazy slots; and the
+    result's words, fluent_slots, threads_used and message, all equal to the compiled reference's (words as its flat
+    store reports them)."""
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    exp = golden.load("brfs_goals.json")[key]
+    name = key.split(":")[0]
+    print(f"any-of goals: {key}", flush=True)
+    t = Task.from_text_file(golden.task_path(name), exp["atoms"])
+    goal = [[(p, pos, objs) for p, pos, objs in cond] for cond in exp["goal"]]
+    r = search.brfs(t, fingerprint=True, goal=goal, **exp["options"])
+    got = {"states": r.states, "expanded": r.expanded, "generated": r.generated, "goal_states": r.num_goal_states,
+           "layers": r.layers, "fingerprint": r.fingerprint, "status": r.status, "layer_counts": r.layer_counts,
+           "exhausted": r.exhausted, "solved": r.solved, "result": r}
+    assert not same(got, exp), (key, same(got, exp))
+    assert same_plan(got, exp), (key, r.plan[:6], exp.get("plan", [])[:6])
+    assert (r.fluent_slots, r.threads_used, r.message) == (exp["fluent_slots"], exp["threads_used"], exp["message"])
+    # words: the fluent width of the stored rows at the end; the reference's flat store reports the same, its chunked
+    # store (rows above 8 words) its width rounded up to whole 8-word chunks
+    assert r.words == t.words
+    assert r.words == exp["words"] if exp["store"] == "flat" else exp["words"] == (r.words + 7) // 8 * 8
+    assert r.store == "device"
+
+
+def test_any_of_goal_errors(golden):
+    """Invalid goal literals are refused with the reference's GroundCondition::validate messages."""
+    from mymyr_amd import search
+    from mymyr_amd._lib import MyaError
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("gripper__prob05"))
+    with pytest.raises(MyaError, match="predicate index 99 out of range"):
+        search.brfs(t, goal=[[(99, True, [0])]])
+    with pytest.raises(MyaError, match="takes 2 arguments, got 1"):
+        search.brfs(t, goal=[[(6, True, [0])]])
+    with pytest.raises(MyaError, match="object index 1000 out of range"):
+        search.brfs(t, goal=[[(6, True, [0, 1000])]])
