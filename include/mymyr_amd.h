@@ -81,7 +81,8 @@ typedef struct mya_task_info
     uint32_t max_arity;     /* largest fluent predicate arity */
     uint32_t goal_unsat;    /* no state is a goal under the current slots */
     uint64_t dense_fluent;  /* size of the typed-dense canonical fluent space */
-    uint64_t reachable_fluent; /* relaxed-reachable fluent atoms (0 when not computed: dense option) */
+    uint64_t reachable_fluent; /* relaxed-reachable fluent atoms (0 when not computed: dense option; under auto the count
+                                * stops once it fills the dense layout's words, which decides the mode) */
     uint32_t view_words;    /* per-state device view size in u64 words */
     uint32_t reserved;
 } mya_task_info;

@@ -148,15 +148,15 @@ struct Lds
     lds<u32>* rc;      // [kCap] per-root counts
     lds<u32>* robj;    // [kCap] the objects of a pick round's roots
     lds<u32>* own;     // [kCap] the lane that makes each item of a level-expansion round
-    lds<u32>* ub;      // [8] the wave-uniform binding (pick prefix, then the picked action)
+    lds<u32>* ub;      // [A] the wave-uniform binding (pick prefix, then the picked action)
     lds<u32>* bind;    // [A][64]: lane columns of the per-lane nested loop (count_from)
     lds<u64>* cur_m;   // [A][64]: its enumeration cursors (candidate bits left)
     lds<u32>* cur_w;   // [A][64]: its enumeration cursors (word index)
     lds<u32>* eff;     // [kMaxEff]: effect slots of a successor (lane k: effect k)
     lds<u32>* before;  // [kMaxEff]: their bits before the move
     lds<u32>* counts;  // [num_schemas]
-    lds<u64>* dfs_m;   // [8] the successor enumeration's per-parameter candidates left in the current word
-    lds<u32>* dfs_w;   // [8] and that word
+    lds<u64>* dfs_m;   // [A] the successor enumeration's per-parameter candidates left in the current word
+    lds<u32>* dfs_w;   // [A] and that word
 };
 
 template<bool kLevels>
@@ -170,7 +170,7 @@ __device__ __forceinline__ Lds lds_of(lds<u64>* base, const TaskDev& T)
     l.view = p;
     p += T.view_words;
     l.ub = reinterpret_cast<lds<u32>*>(p);
-    p += 4;
+    p += (A + 1) / 2;
     l.bind = reinterpret_cast<lds<u32>*>(p);
     p += 32 * A;
     l.cur_m = p;
@@ -184,9 +184,9 @@ __device__ __forceinline__ Lds lds_of(lds<u64>* base, const TaskDev& T)
     l.counts = reinterpret_cast<lds<u32>*>(p);
     p += (T.num_schemas + 1) / 2;
     l.dfs_m = p;
-    p += 8;
+    p += A;
     l.dfs_w = reinterpret_cast<lds<u32>*>(p);
-    p += 4;
+    p += (A + 1) / 2;
     if constexpr (kLevels)
     {
         l.qa = reinterpret_cast<lds<u32>*>(p);

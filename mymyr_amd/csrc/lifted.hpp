@@ -53,14 +53,14 @@ constexpr u32 kCap = 64;           // items per level of the level-synchronous c
 
 /// Per-wave LDS words: the state row, the view, the uniform binding, the bindings and per-level enumeration cursors of
 /// the 64 lanes' nested loops (A = the largest schema arity, at least 1), the effect scratch, the per-schema counts and
-/// the successor enumeration's level cursors (8 masks, 8 words);
+/// the successor enumeration's level cursors (A masks, A words);
 /// with `levels`, also the two item levels of the level-synchronous count with their roots, root counts, root objects
 /// and item makers.
 __host__ __device__ inline u32 wave_lds_words(const TaskDev& t, bool levels)
 {
     const u32 A = t.label_width ? t.label_width : 1;
     const u32 S = t.num_schemas;
-    u32 w = t.W + t.view_words + 4 + 32 * A + 64 * A + 32 * A + 32 + (S + 1) / 2 + 12;
+    u32 w = t.W + t.view_words + (A + 1) / 2 + 32 * A + 64 * A + 32 * A + 32 + (S + 1) / 2 + A + (A + 1) / 2;
     if (levels)
         w += kCap * A + 5 * kCap / 2;
     return (w + 1) & ~1u;

@@ -591,7 +591,7 @@ private:
     // static precondition as its body; negative fluent literals dropped; "=" by object identity; a variable no
     // positive literal binds ranges over every object (relaxed_reachability.hpp:3-12). Evaluated by naive rounds of
     // a bitset join until no new atom appears.
-    std::vector<u64> reachable_fluents()
+    std::vector<u64> reachable_fluents(u64 stop_at = ~u64{0})
     {
         const u32 m = static_cast<u32>(T->preds.size());
         std::vector<u8> reached(C->layout.fluent_count, 0);
@@ -636,8 +636,16 @@ private:
         };
         for (const auto& a : T->fluent_init)
             add_atom(a[0], a.data() + 1);
+        if (list.size() >= stop_at)
+        {
+            std::sort(list.begin(), list.end());
+            return list;
+        }
 
         const u32 eq = equality_pred();
+        Bits all_objects(ow, 0);
+        for (u32 o = 0; o < n; ++o)
+            set_bit(all_objects, o);
         for (bool changed = true; changed;)
         {
             changed = false;
@@ -693,43 +701,100 @@ private:
                     }
                 if (!ok)
                     continue;
-                // order: greedy by constraints to placed variables
-                std::vector<u32> order;
-                std::vector<u8> placed(s.arity, 0);
-                while (order.size() < vars.size())
-                {
-                    int best = -1;
-                    long best_score = 0;
-                    for (u32 v : vars)
+                // one rule per positive effect literal (its head): the head's variables are enumerated, and each head
+                // atom not reached yet is added if some binding of the remaining variables satisfies the body (a
+                // search that stops at the first one); schemas with many parameters thus cost one existence search
+                // per new head atom instead of an enumeration of all their bindings
+                auto greedy = [&](const std::vector<u32>& cand, std::vector<u8>& placed) {
+                    std::vector<u32> order;
+                    while (order.size() < cand.size())
                     {
-                        if (placed[v])
-                            continue;
-                        long links = 0, un = 0;
-                        for (const Literal* l : body)
+                        int best = -1;
+                        long best_score = 0;
+                        for (u32 v : cand)
                         {
-                            const auto ps = distinct_params(l->terms);
-                            if (std::find(ps.begin(), ps.end(), v) == ps.end())
+                            if (placed[v])
                                 continue;
-                            if (ps.size() == 1)
-                                ++un;
-                            for (u32 q : ps)
-                                if (q != v && placed[q])
-                                    ++links;
+                            long links = 0, un = 0;
+                            for (const Literal* l : body)
+                            {
+                                const auto ps = distinct_params(l->terms);
+                                if (std::find(ps.begin(), ps.end(), v) == ps.end())
+                                    continue;
+                                if (ps.size() == 1)
+                                    ++un;
+                                for (u32 q : ps)
+                                    if (q != v && placed[q])
+                                        ++links;
+                            }
+                            const long score = links * 1000000 + un * 10000;
+                            if (best < 0 || score > best_score)
+                                best = static_cast<int>(v), best_score = score;
                         }
-                        const long score = links * 1000000 + un * 10000;
-                        if (best < 0 || score > best_score)
-                            best = static_cast<int>(v), best_score = score;
+                        placed[best] = 1;
+                        order.push_back(static_cast<u32>(best));
                     }
-                    placed[best] = 1;
-                    order.push_back(static_cast<u32>(best));
+                    return order;
+                };
+                for (const Literal& head : s.eff)
+                {
+                    if (!head.positive)
+                        continue;
+                    const std::vector<u32> hv = distinct_params(head.terms);
+                    std::vector<u8> placed(s.arity, 0);
+                    const std::vector<u32> order_head = greedy(hv, placed);
+                    // the remaining variables that the body constrains (a variable only another head mentions does
+                    // not change whether this head's body is satisfiable)
+                    std::vector<u8> in_body(s.arity, 0);
+                    for (const Literal* l : body)
+                        for (i32 x : l->terms)
+                            if (x >= 0)
+                                in_body[x] = 1;
+                    std::vector<u32> rest;
+                    for (u32 v : vars)
+                        if (!placed[v] && in_body[v])
+                            rest.push_back(v);
+                    const std::vector<u32> order_rest = greedy(rest, placed);
+                    std::vector<u32> bind(s.arity, 0);
+                    std::vector<u8> bound(s.arity, 0);
+                    std::vector<std::vector<u32>> found;
+                    std::vector<u32> h;
+                    // the variables' domains, arc consistent over the body (a rule whose body cannot hold adds nothing)
+                    std::vector<Bits> dom(s.arity, all_objects);
+                    if (!arc_consistent(body, dom, unary, fwd, bwd, eq))
+                        continue;
+                    std::vector<Bits> fixed;
+                    enumerate(s, body, order_head, 0, bind, bound, unary, fwd, bwd, reached, eq, dom, [&] {
+                        h.assign(1, head.pred);
+                        for (i32 x : head.terms)
+                            h.push_back(x < 0 ? term_object(x) : bind[x]);
+                        if (holds(h[0], h.data() + 1))
+                            return true;  // reached already
+                        // the head's variables fixed: the remaining domains made arc consistent again, then a search
+                        // for one binding of the rest
+                        fixed = dom;
+                        for (u32 v : hv)
+                        {
+                            std::fill(fixed[v].begin(), fixed[v].end(), 0);
+                            set_bit(fixed[v], bind[v]);
+                        }
+                        if (!arc_consistent(body, fixed, unary, fwd, bwd, eq))
+                            return true;
+                        const bool stopped = !enumerate(s, body, order_rest, 0, bind, bound, unary, fwd, bwd, reached, eq, fixed,
+                                                        [] { return false; });
+                        if (stopped)
+                            found.push_back(h);
+                        return true;
+                    });
+                    for (const auto& a : found)
+                        if (add_atom(a[0], a.data() + 1))
+                            changed = true;
+                    if (list.size() >= stop_at)
+                    {
+                        std::sort(list.begin(), list.end());
+                        return list;
+                    }
                 }
-                std::vector<u32> bind(s.arity, 0);
-                std::vector<u8> bound(s.arity, 0);
-                std::vector<std::vector<u32>> heads;
-                enumerate(s, body, order, 0, bind, bound, unary, fwd, bwd, reached, eq, heads);
-                for (const auto& h : heads)
-                    if (add_atom(h[0], h.data() + 1))
-                        changed = true;
             }
         }
         std::sort(list.begin(), list.end());
@@ -744,27 +809,80 @@ private:
         return kNone;
     }
 
-    void enumerate(const SchemaText& s, const std::vector<const Literal*>& body, const std::vector<u32>& order, u32 d,
+    /// Arc consistency over a rule body's variables: D[v] (object bits) keeps only the objects that satisfy v's unary
+    /// literals and have support in every positive binary literal with another variable (the fluent relation as
+    /// reached so far, or the static one), repeated until nothing changes. Only objects that no binding of the body
+    /// can use are removed, so a search over the domains finds the same bindings. Returns false if a domain emptied
+    /// (the body cannot hold).
+    bool arc_consistent(const std::vector<const Literal*>& body, std::vector<Bits>& D, const std::vector<Bits>& unary,
+                        const std::vector<Bits>& fwd, const std::vector<Bits>& bwd, u32 eq)
+    {
+        auto empty = [&](const Bits& b) { return std::all_of(b.begin(), b.end(), [](u64 w) { return w == 0; }); };
+        for (const Literal* l : body)
+        {
+            const auto ps = distinct_params(l->terms);
+            const bool fluent = T->preds[l->pred].kind != 'S';
+            if (ps.size() == 1 && T->preds[l->pred].arity == 1 && l->pred != eq)
+                and_bits(D[ps[0]], fluent ? unary[l->pred] : s_unary[l->pred], !l->positive);
+        }
+        for (bool changed = true; changed;)
+        {
+            changed = false;
+            for (const Literal* l : body)
+            {
+                if (!l->positive || T->preds[l->pred].arity != 2 || l->terms[0] < 0 || l->terms[1] < 0 || l->terms[0] == l->terms[1])
+                    continue;
+                const u32 x = static_cast<u32>(l->terms[0]), y = static_cast<u32>(l->terms[1]);
+                for (int dir = 0; dir < 2; ++dir)
+                {
+                    // revise: the objects of `to` with support in some object of `from`
+                    const u32 from = dir == 0 ? x : y, to = dir == 0 ? y : x;
+                    Bits sup(ow, 0);
+                    if (l->pred == eq)
+                        sup = D[from];
+                    else
+                    {
+                        const bool fluent = T->preds[l->pred].kind != 'S';
+                        const Bits* tab = fluent ? (dir == 0 ? &fwd[l->pred] : &bwd[l->pred])
+                                                 : &m_row_data[static_rows(l->pred, dir == 0 ? 0 : 1, dir == 0 ? 1 : 0)];
+                        for (u32 w = 0; w < ow; ++w)
+                            for (u64 bits = D[from][w]; bits; bits &= bits - 1)
+                            {
+                                const u32 o = w * 64 + static_cast<u32>(std::countr_zero(bits));
+                                for (u32 k = 0; k < ow; ++k)
+                                    sup[k] |= (*tab)[static_cast<size_t>(o) * ow + k];
+                            }
+                    }
+                    for (u32 k = 0; k < ow; ++k)
+                    {
+                        const u64 nv = D[to][k] & sup[k];
+                        if (nv != D[to][k])
+                        {
+                            D[to][k] = nv;
+                            changed = true;
+                        }
+                    }
+                    if (empty(D[to]))
+                        return false;
+                }
+            }
+        }
+        return std::none_of(D.begin(), D.end(), empty);
+    }
+
+    /// Binds the variables order[d..] (the earlier ones bound in `bind` / `bound`) in every way the body literals whose
+    /// variables are then bound allow, calling leaf() per complete binding; leaf returning false stops the search, and
+    /// then so does this (returns false; true: the search ran to its end).
+    template<class Leaf>
+    bool enumerate(const SchemaText& s, const std::vector<const Literal*>& body, const std::vector<u32>& order, u32 d,
                    std::vector<u32>& bind, std::vector<u8>& bound, const std::vector<Bits>& unary,
                    const std::vector<Bits>& fwd, const std::vector<Bits>& bwd, const std::vector<u8>& reached, u32 eq,
-                   std::vector<std::vector<u32>>& heads)
+                   const std::vector<Bits>& dom, Leaf&& leaf)
     {
         if (d == order.size())
-        {
-            for (const Literal& l : s.eff)
-                if (l.positive)
-                {
-                    std::vector<u32> h{l.pred};
-                    for (i32 x : l.terms)
-                        h.push_back(x < 0 ? term_object(x) : bind[x]);
-                    heads.push_back(std::move(h));
-                }
-            return;
-        }
+            return leaf();
         const u32 v = order[d];
-        Bits cand(ow, 0);
-        for (u32 o = 0; o < n; ++o)
-            set_bit(cand, o);
+        Bits cand = dom[v];
         std::vector<const Literal*> checks;
         for (const Literal* l : body)
         {
@@ -837,11 +955,17 @@ private:
                         break;
                     }
                 }
-                if (ok)
-                    enumerate(s, body, order, d + 1, bind, bound, unary, fwd, bwd, reached, eq, heads);
+                if (!ok)
+                    continue;
+                if (!enumerate(s, body, order, d + 1, bind, bound, unary, fwd, bwd, reached, eq, dom, leaf))
+                {
+                    bound[v] = 0;
+                    return false;
+                }
             }
         }
         bound[v] = 0;
+        return true;
     }
 
     // --------------------------------------------------------------------------------------------- atom mode
@@ -878,7 +1002,10 @@ private:
         AtomMode mode = AtomMode::Dense;
         if (m_opt != AtomsOption::Dense)
         {
-            reach = reachable_fluents();
+            // under auto, the fixpoint stops once the reachable atoms fill as many words as the dense layout: the
+            // dense layout is then not wider (its other conditions aside), which is all the choice needs
+            const u64 decided = m_opt == AtomsOption::Auto ? u64{64} * (words_for(L.fluent_count) - 1) + 1 : ~u64{0};
+            reach = reachable_fluents(decided);
             C->reachable_fluent = reach.size();
             const bool dense_fits = words_for(L.fluent_count) <= words_for(reach.size()) && frozen_bytes(L.fluent_count) <= kMaxBytes;
             mode = m_opt == AtomsOption::Auto && dense_fits ? AtomMode::Dense : AtomMode::Reachable;

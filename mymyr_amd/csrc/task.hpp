@@ -194,7 +194,7 @@ struct DevStep
     u32 pad;
 };
 
-constexpr u32 kMaxParams = 6;
+constexpr u32 kMaxParams = 32;
 
 /// Per schema: plans P_j (j = 0..arity) count the bindings with parameters [0, j) bound; filters F_i (i < arity) give
 /// the candidates of parameter i with [0, i) bound (the lexicographic pick).

@@ -29,6 +29,9 @@ SUITE_COUNTS = {
     "parcprinter-opt11-strips__p03": (173942, 488868, 1),
     "pegsol-08-strips__p22": (99457, 189967, 2),
     "pathways__p02": (669078, 11237052, 12288),
+    "freecell__p02": (159924, 1371273, 1),
+    "folding-opt23-adl__p01": (148260, 170776, 1),
+    "organic-synthesis-opt18-strips__p20": (41311, 52548, 24),
 }
 # suite tasks outside the published counts whose slot tables are pinned too (rovers__p02's schemas have two witness
 # parameters; its BrFS is pinned in brfs_witness.json)

@@ -40,7 +40,8 @@ def test_symbols_are_plain_c():
 ALL_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "driverlog__p03", "logistics00__probLOGISTICS-6-1",
              "miconic__s7-4", "parcprinter-opt11-strips__p03", "pathways__p02", "pegsol-08-strips__p22", "rovers__p02",
              "snake-opt18-strips__p05", "sokoban-opt08-strips__p14", "transport-opt08-strips__p23",
-             "visitall__visitall_x-6_y-3_r-100", "zenotravel__p05", "gridworld", "strips", "transport", "transport_xl"]
+             "visitall__visitall_x-6_y-3_r-100", "zenotravel__p05", "gridworld", "strips", "transport", "transport_xl",
+             "freecell__p02", "folding-opt23-adl__p01"]
 
 
 @pytest.mark.parametrize("name", ALL_TASKS)
@@ -85,7 +86,7 @@ def test_task_errors():
     with pytest.raises(MyaError, match="object out of range"):
         Task.from_text("O 1\nP 1\nF 1 p\nSI 0\nFI 1\n0 3\nG 0\nA 0\n")
     with pytest.raises(MyaError, match="parameters; the device path supports at most"):
-        Task.from_text("O 2\nP 1\nF 1 p\nSI 0\nFI 0\nG 0\nA 1\nbig 7\nL 0\nE 1\n0\nL 0\nF 1\n0 1 0\n")
+        Task.from_text("O 2\nP 1\nF 1 p\nSI 0\nFI 0\nG 0\nA 1\nbig 33\nL 0\nE 1\n0\nL 0\nF 1\n0 1 0\n")
 
 
 def test_conditional_effects_and_axioms_refused():
