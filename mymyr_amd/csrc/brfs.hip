@@ -44,6 +44,10 @@ struct GroundDev
     const u32* slots;    // pos..., neg..., add..., del...
     const u32* dom_off;  // witness pruning: dominators of each action (null: none)
     const u32* dom;
+    const u32* ce_off;   // conditional effects (null: none): action a's ground instances [ce_off[a], ce_off[a + 1])
+    const u32* ce_meta;  // npos | nneg << 8 | nadd << 16 | ndel << 24 of each instance
+    const u32* ce_soff;  // into ce_slots
+    const u32* ce_slots; // pos..., neg..., add..., del...
     u32 num;
     u32 num_padded;      // a multiple of 64; the padding records never apply
 };
@@ -308,7 +312,11 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restri
 /// The successor rows of (parent, action) records as the row source of the state set's probe and compaction:
 /// candidate c's row = (parent row & ~delete mask) | add mask, recomputed wherever it is needed (the probe compares a
 /// pending entry against it, the compaction writes it), so candidate rows are never stored before they are new states.
-template<int W>
+///
+/// With conditional effects (kCE), the instances of the candidate's action whose conditions hold in the parent row add
+/// their deletes and adds to the masks before the row is formed: every effect of the action is applied as "delete, then
+/// add", the adds winning (include/mymyr/successor/successors.hpp:361-385).
+template<int W, bool kCE = false>
 struct ParentRows
 {
     const u64* arena;
@@ -316,6 +324,10 @@ struct ParentRows
     const u32* cand_pa;   // (parent << abits) | action
     const u64* masks;     // [actions, 2W]: delete mask, then add mask
     u32 abits;            // action bits of a record
+    const u32* ce_off;    // kCE: GroundDev's conditional effect tables
+    const u32* ce_meta;
+    const u32* ce_soff;
+    const u32* ce_slots;
     __device__ __forceinline__ u32 parent_of(u32 pa) const { return pa >> abits; }
     __device__ __forceinline__ u32 action_of(u32 pa) const { return pa & ((1u << abits) - 1); }
     template<int G, int K>
@@ -333,11 +345,58 @@ struct ParentRows
         load_row<G, K>(row, W, q, r);
         load_row<G, K>(mk, W, q, d);
         load_row<G, K>(mk + W, W, q, a);
+        if constexpr (kCE)
+            fire_ces<G, K>(row, action_of(pa), q, d, a);
 #pragma unroll
         for (int k = 0; k < K; ++k)
         {
             o.lo[k] = (r.lo[k] & ~d.lo[k]) | a.lo[k];
             o.hi[k] = (r.hi[k] & ~d.hi[k]) | a.hi[k];
+        }
+    }
+    /// Sets slot s's bit in x if lane q holds its word (word w is in pair w / 2, pair p at lane p % G, index p / G).
+    template<int G, int K>
+    __device__ __forceinline__ static void set_slot(Slice<G, K>& x, u32 s, u32 q)
+    {
+        const u32 w = s >> 6, p = w >> 1;
+        if (p % G != q)
+            return;
+        const u64 bit = u64{1} << (s & 63);
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (p / G == static_cast<u32>(k))
+            {
+                if (w & 1)
+                    x.hi[k] |= bit;
+                else
+                    x.lo[k] |= bit;
+            }
+    }
+    /// The deletes and adds of action a's conditional effect instances whose conditions hold in `row` into d and a.
+    template<int G, int K>
+    __device__ __forceinline__ void fire_ces(const u64* row, u32 act, u32 q, Slice<G, K>& d, Slice<G, K>& a) const
+    {
+        for (u32 i = ce_off[act], e = ce_off[act + 1]; i < e; ++i)
+        {
+            const u32 m = ce_meta[i], o = ce_soff[i];
+            const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF, nadd = (m >> 16) & 0xFF, ndel = m >> 24;
+            bool fires = true;
+            for (u32 k = 0; k < npos && fires; ++k)
+            {
+                const u32 s = ce_slots[o + k];
+                fires = (row[s >> 6] >> (s & 63)) & 1;
+            }
+            for (u32 k = 0; k < nneg && fires; ++k)
+            {
+                const u32 s = ce_slots[o + npos + k];
+                fires = !((row[s >> 6] >> (s & 63)) & 1);
+            }
+            if (!fires)
+                continue;
+            for (u32 k = 0; k < nadd; ++k)
+                set_slot<G, K>(a, ce_slots[o + npos + nneg + k], q);
+            for (u32 k = 0; k < ndel; ++k)
+                set_slot<G, K>(d, ce_slots[o + npos + nneg + nadd + k], q);
         }
     }
 };
@@ -350,8 +409,8 @@ constexpr int kPairs = W >= 4 ? 2 : 1;  // word pairs per lane
 // Candidates [0, m) of a chunk into the state set: a group of lanes per candidate forms its row, hashes it and probes
 // the table (a stored equal row drops it; a pending equal row takes part in the smallest-index rule; an empty slot
 // takes it as pending). Losers' flags are cleared, winners' stay 1.
-template<int W>
-__global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W> src, u64 m, u8* __restrict__ flags,
+template<int W, bool kCE>
+__global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W, kCE> src, u64 m, u8* __restrict__ flags,
                                                       u32* __restrict__ status, BlockedView blocked)
 {
     constexpr int G = kGroup<W>;
@@ -384,8 +443,8 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
 // (rows recomputed from their records), with their search nodes: nodes[id] = (parent id << 32) | ground action, the
 // first discovery of the state (the reference's node records, src/mymyr/search/brfs.cpp:235-268). A winner at or past
 // `limit` sets kStatusCapacity.
-template<int W>
-__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W> src, u64 m, const u32* __restrict__ list,
+template<int W, bool kCE>
+__global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W, kCE> src, u64 m, const u32* __restrict__ list,
                                                        const u64* __restrict__ size_now, const u64* __restrict__ size_next, u64 limit,
                                                        u64* __restrict__ nodes, u32* __restrict__ status)
 {
@@ -508,8 +567,21 @@ std::unique_ptr<BrfsTables> build_tables(const CompiledTask& task, bool witness,
     const GroundActions& ga = tb->ga;
     std::vector<u64> fast, masks;
     build_action_tables<W>(ga, fast, masks);
-    tb->g = GroundDev{tb->upload(fast), tb->upload(ga.meta), tb->upload(ga.off), tb->upload(ga.slots), tb->upload(ga.dom_off),
-                      tb->upload(ga.dom), ga.size(), static_cast<u32>(fast.size())};
+    // an action's conditional effect instances are evaluated where its successor rows are formed; tables without any
+    // instance take the plain kernels
+    const bool ces = !ga.ce_meta.empty();
+    tb->g = GroundDev{tb->upload(fast),
+                      tb->upload(ga.meta),
+                      tb->upload(ga.off),
+                      tb->upload(ga.slots),
+                      tb->upload(ga.dom_off),
+                      tb->upload(ga.dom),
+                      ces ? tb->upload(ga.ce_off) : nullptr,
+                      ces ? tb->upload(ga.ce_meta) : nullptr,
+                      ces ? tb->upload(ga.ce_soff) : nullptr,
+                      ces ? tb->upload(ga.ce_slots) : nullptr,
+                      ga.size(),
+                      static_cast<u32>(fast.size())};
     tb->masks = tb->upload(masks);
     tb->goal = GoalDev{tb->upload(task.goal_pos), tb->upload(task.goal_neg), static_cast<u32>(task.goal_pos.size()),
                        static_cast<u32>(task.goal_neg.size()), task.goal_unsat ? 1u : 0u};
@@ -823,7 +895,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             }
             const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
-            const ParentRows<W> src{set.v.arena, layer_begin + p0, cand_pa, d_masks, abits};
+            const ParentRows<W, false> src{set.v.arena, layer_begin + p0, cand_pa, d_masks, abits};
+            const ParentRows<W, true> src_ce{set.v.arena, layer_begin + p0, cand_pa, d_masks, abits, g.ce_off, g.ce_meta, g.ce_soff, g.ce_slots};
             if (m > 0)
             {
                 tm.begin(kKEmit);
@@ -833,8 +906,12 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 tm.end(kKEmit, np * (R + 8) + m * 4);
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
-                hipLaunchKernelGGL(k_ground_insert<W>, dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m, set.flags,
-                                   set.d_status, blocked);
+                if (g.ce_off)
+                    hipLaunchKernelGGL((k_ground_insert<W, true>), dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src_ce, m,
+                                       set.flags, set.d_status, blocked);
+                else
+                    hipLaunchKernelGGL((k_ground_insert<W, false>), dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m,
+                                       set.flags, set.d_status, blocked);
                 launch_check("ground insert");
                 tm.end(kKInsert, 0);
                 tm.begin(kKRank);
@@ -843,9 +920,17 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 // the winners' count is on the device (size next - size now); ids from max_states on are not written
                 // (the store filled: the confirmation finds the cut)
                 tm.begin(kKCompact);
-                hipLaunchKernelGGL(k_ground_compact<W>, dim3(std::min<u64>(blocks_for(m * G, kLB), kStrideBlocks)), dim3(kLB), 0, stream, set.v, src, m, set.list,
-                                   state_set_size_now(set), state_set_size_next(set), bounded ? o.max_states : cap_states, nodes,
-                                   bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
+                {
+                    const dim3 grid(std::min<u64>(blocks_for(m * G, kLB), kStrideBlocks));
+                    u32* const cstat = bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status;
+                    const u64 climit = bounded ? o.max_states : cap_states;
+                    if (g.ce_off)
+                        hipLaunchKernelGGL((k_ground_compact<W, true>), grid, dim3(kLB), 0, stream, set.v, src_ce, m, set.list,
+                                           state_set_size_now(set), state_set_size_next(set), climit, nodes, cstat);
+                    else
+                        hipLaunchKernelGGL((k_ground_compact<W, false>), grid, dim3(kLB), 0, stream, set.v, src, m, set.list,
+                                           state_set_size_now(set), state_set_size_next(set), climit, nodes, cstat);
+                }
                 launch_check("ground compact");
                 tm.end(kKCompact, 0);
                 state_set_flip(set);

@@ -24,6 +24,11 @@ void set_error(const std::string& m) { g_error = m; }
 
 const DeviceTask& device_task(mya_task* t)
 {
+    // the lifted device tables (environment, successor listing, the wide and lazy searches) carry no conditional
+    // effects: only the ground search (states of at most 16 words) evaluates them
+    if (t->compiled->has_ce)
+        throw std::invalid_argument("mymyr_amd: conditional effects are supported by the ground breadth-first search only (states of "
+                                    "at most 16 words); the environment, the successor listing and the wide search refuse them");
     std::lock_guard lock(t->mutex);
     if (!t->dev.image)
     {

@@ -255,20 +255,36 @@ private:
         const u32 ne = u();
         for (u32 i = 0; i < ne; ++i)
         {
-            const u32 extra = u();
+            // an effect without forall parameters and condition is unconditional (text_format.cpp's schema(), and
+            // compile.cpp's split of them from the conditional ones)
+            CondEffectText ce;
+            ce.extra = u();
+            if (ce.extra > 1024)
+                fail("more than 1024 forall parameters");
+            const u32 total = s.arity + ce.extra;
             expect("L");
             const u32 nc = u();
-            if (extra != 0 || nc != 0)
-                fail("conditional effects are not supported by the device path (schema " + s.name + ")");
+            for (u32 j = 0; j < nc; ++j)
+            {
+                Literal l = literal(t, false, total);
+                if (t.preds[l.pred].kind == 'D')
+                    fail("derived literals in effect conditions are not supported (schema " + s.name + ")");
+                ce.cond.push_back(std::move(l));
+            }
             expect("F");
             const u32 nf = u();
             for (u32 j = 0; j < nf; ++j)
             {
-                Literal l = literal(t, false, s.arity);
+                Literal l = literal(t, false, total);
                 if (t.preds[l.pred].kind != 'F')
                     fail("effect on a non-fluent predicate");
-                s.eff.push_back(std::move(l));
+                ce.eff.push_back(std::move(l));
             }
+            if (ce.extra == 0 && ce.cond.empty())
+                for (Literal& l : ce.eff)
+                    s.eff.push_back(std::move(l));
+            else
+                s.ces.push_back(std::move(ce));
         }
         return s;
     }
@@ -428,86 +444,104 @@ private:
     // --------------------------------------------------------------------------------------------- dom0
     // The static domain of each schema parameter: every object, AND static unary literals, AND static binary
     // literals with one constant, AND projections of positive static k-ary literals (compile.cpp:803-915).
+    /// Static domains of the variables [0, total) of a literal list: every object, AND static unary literals, AND static
+    /// binary literals with one constant, AND projections of positive static k-ary literals (compile.cpp:803-915).
+    /// *never: a ground static literal fails or a domain is empty.
+    std::vector<Bits> static_domains(const std::vector<Literal>& lits, u32 total, bool* never)
+    {
+        std::vector<Bits> dom(total, Bits(ow, 0));
+        for (u32 v = 0; v < total; ++v)
+            for (u32 o = 0; o < n; ++o)
+                set_bit(dom[v], o);
+        for (const Literal& l : lits)
+        {
+            const PredicateText& P = T->preds[l.pred];
+            if (P.kind == 'D')
+                throw Error("derived precondition literals are not supported");
+            const bool fluent = P.kind != 'S';
+            const auto vars = distinct_params(l.terms);
+            if (vars.empty())
+            {
+                if (!fluent && static_ground_holds(l) != l.positive)
+                    *never = true;
+                continue;
+            }
+            if (P.arity == 1)
+            {
+                if (!fluent)
+                    and_bits(dom[vars[0]], s_unary[l.pred], !l.positive);
+                continue;
+            }
+            if (P.arity == 2 && l.terms[0] != l.terms[1])
+            {
+                const bool f0 = l.terms[0] >= 0, f1 = l.terms[1] >= 0;
+                if (f0 && f1)
+                    continue;
+                const u32 fpos = f0 ? 0 : 1, opos = 1 - fpos;
+                const u32 v = static_cast<u32>(l.terms[fpos]);
+                const u32 cobj = term_object(l.terms[opos]);
+                if (!fluent)
+                {
+                    const u32 tab = static_rows(l.pred, opos, fpos);
+                    Bits row(m_row_data[tab].begin() + static_cast<size_t>(cobj) * ow,
+                             m_row_data[tab].begin() + static_cast<size_t>(cobj + 1) * ow);
+                    and_bits(dom[v], row, !l.positive);
+                }
+                continue;
+            }
+            if (!fluent && l.positive && P.arity >= 3)
+            {
+                for (u32 i = 0; i < P.arity; ++i)
+                    if (l.terms[i] >= 0)
+                    {
+                        Bits proj(ow, 0);
+                        for (const auto* a : static_atoms[l.pred])
+                        {
+                            bool ok = true;
+                            for (u32 j = 0; j < P.arity && ok; ++j)
+                                if (l.terms[j] < 0 && (*a)[1 + j] != term_object(l.terms[j]))
+                                    ok = false;
+                            if (ok)
+                                set_bit(proj, (*a)[1 + i]);
+                        }
+                        and_bits(dom[static_cast<u32>(l.terms[i])], proj, false);
+                    }
+            }
+        }
+        for (u32 v = 0; v < total; ++v)
+            if (!any_bit(dom[v]))
+                *never = true;
+        return dom;
+    }
+
     void compute_dom0()
     {
         C->dom0.resize(T->schemas.size());
         C->never.assign(T->schemas.size(), 0);
+        C->ce_dom0.assign(T->schemas.size(), {});
         for (u32 si = 0; si < T->schemas.size(); ++si)
         {
             const SchemaText& s = T->schemas[si];
             if (s.arity > kMaxParams)
                 throw Error("schema " + s.name + " has " + std::to_string(s.arity) + " parameters; the device path supports at most " +
                             std::to_string(kMaxParams));
-            auto& dom = C->dom0[si];
-            dom.assign(s.arity, Bits(ow, 0));
-            for (u32 v = 0; v < s.arity; ++v)
-                for (u32 o = 0; o < n; ++o)
-                    set_bit(dom[v], o);
             bool never = false;
-            for (const Literal& l : s.pre)
-            {
-                const PredicateText& P = T->preds[l.pred];
-                if (P.kind == 'D')
-                    throw Error("derived precondition literals are not supported");
-                const bool fluent = P.kind != 'S';
-                const auto vars = distinct_params(l.terms);
-                if (vars.empty())
-                {
-                    if (!fluent && static_ground_holds(l) != l.positive)
-                        never = true;
-                    continue;
-                }
-                if (P.arity == 1)
-                {
-                    if (!fluent)
-                        and_bits(dom[vars[0]], s_unary[l.pred], !l.positive);
-                    continue;
-                }
-                if (P.arity == 2 && l.terms[0] != l.terms[1])
-                {
-                    const bool f0 = l.terms[0] >= 0, f1 = l.terms[1] >= 0;
-                    if (f0 && f1)
-                        continue;
-                    const u32 fpos = f0 ? 0 : 1, opos = 1 - fpos;
-                    const u32 v = static_cast<u32>(l.terms[fpos]);
-                    const u32 cobj = term_object(l.terms[opos]);
-                    if (!fluent)
-                    {
-                        const u32 tab = static_rows(l.pred, opos, fpos);
-                        Bits row(m_row_data[tab].begin() + static_cast<size_t>(cobj) * ow,
-                                 m_row_data[tab].begin() + static_cast<size_t>(cobj + 1) * ow);
-                        and_bits(dom[v], row, !l.positive);
-                    }
-                    continue;
-                }
-                if (!fluent && l.positive && P.arity >= 3)
-                {
-                    for (u32 i = 0; i < P.arity; ++i)
-                        if (l.terms[i] >= 0)
-                        {
-                            Bits proj(ow, 0);
-                            for (const auto* a : static_atoms[l.pred])
-                            {
-                                bool ok = true;
-                                for (u32 j = 0; j < P.arity && ok; ++j)
-                                    if (l.terms[j] < 0 && (*a)[1 + j] != term_object(l.terms[j]))
-                                        ok = false;
-                                if (ok)
-                                    set_bit(proj, (*a)[1 + i]);
-                            }
-                            and_bits(dom[static_cast<u32>(l.terms[i])], proj, false);
-                        }
-                }
-            }
-            for (u32 v = 0; v < s.arity; ++v)
-                if (!any_bit(dom[v]))
-                    never = true;
+            C->dom0[si] = static_domains(s.pre, s.arity, &never);
             // a collapsed parameter without a representative (no object of its type): the schema has no action
             // (src/mymyr/task/compile.cpp:1171-1181)
             for (const CollapsedText& c : T->collapsed)
                 if (c.schema == si && c.representative < 0)
                     never = true;
             C->never[si] = never ? 1 : 0;
+            // the forall parameters of its conditional effects: the static domains their conditions give them (the
+            // condition's matcher, compile.cpp:1208-1216)
+            for (const CondEffectText& ce : s.ces)
+            {
+                bool ce_never = false;
+                std::vector<Bits> d = static_domains(ce.cond, s.arity + ce.extra, &ce_never);
+                C->ce_dom0[si].emplace_back(d.begin() + s.arity, d.end());
+                C->has_ce = true;
+            }
         }
     }
     void and_bits(Bits& d, const Bits& s, bool neg)
@@ -527,16 +561,29 @@ private:
             if (T->preds[p].kind == 'F')
                 bits[p].assign(T->preds[p].arity, Bits(ow, 0));
         for (u32 si = 0; si < T->schemas.size(); ++si)
-            for (const Literal& l : T->schemas[si].eff)
+        {
+            const SchemaText& s = T->schemas[si];
+            // a term's objects: a constant, a schema parameter's dom0, or a forall parameter's conditional dom0
+            auto add_term = [&](u32 p, u32 i, i32 t, const std::vector<Bits>* ce_dom) {
+                if (t < 0)
+                    set_bit(bits[p][i], term_object(t));
+                else
+                {
+                    const Bits& d = static_cast<u32>(t) < s.arity ? C->dom0[si][static_cast<u32>(t)] : (*ce_dom)[static_cast<u32>(t) - s.arity];
+                    for (u32 w = 0; w < ow; ++w)
+                        bits[p][i][w] |= d[w];
+                }
+            };
+            for (const Literal& l : s.eff)
                 if (l.positive)
                     for (u32 i = 0; i < l.terms.size(); ++i)
-                    {
-                        if (l.terms[i] < 0)
-                            set_bit(bits[l.pred][i], term_object(l.terms[i]));
-                        else
-                            for (u32 w = 0; w < ow; ++w)
-                                bits[l.pred][i][w] |= C->dom0[si][static_cast<u32>(l.terms[i])][w];
-                    }
+                        add_term(l.pred, i, l.terms[i], nullptr);
+            for (u32 k = 0; k < s.ces.size(); ++k)
+                for (const Literal& l : s.ces[k].eff)
+                    if (l.positive)
+                        for (u32 i = 0; i < l.terms.size(); ++i)
+                            add_term(l.pred, i, l.terms[i], &C->ce_dom0[si][k]);
+        }
         for (const auto& a : T->fluent_init)
             for (u32 i = 0; i + 1 < a.size(); ++i)
                 set_bit(bits[a[0]][i], a[1 + i]);
@@ -646,12 +693,25 @@ private:
         Bits all_objects(ow, 0);
         for (u32 o = 0; o < n; ++o)
             set_bit(all_objects, o);
+        // the rules: one per schema (its precondition, its unconditional effects) and one per conditional effect (the
+        // schema's precondition and the effect's condition over the schema's and the forall parameters, its effects)
+        std::vector<SchemaText> rules;
+        for (const SchemaText& sc : T->schemas)
+        {
+            rules.push_back(SchemaText{sc.name, sc.arity, sc.pre, sc.eff, {}});
+            for (const CondEffectText& ce : sc.ces)
+            {
+                SchemaText r{sc.name, sc.arity + ce.extra, sc.pre, ce.eff, {}};
+                r.pre.insert(r.pre.end(), ce.cond.begin(), ce.cond.end());
+                rules.push_back(std::move(r));
+            }
+        }
         for (bool changed = true; changed;)
         {
             changed = false;
-            for (u32 si = 0; si < T->schemas.size(); ++si)
+            for (u32 ri = 0; ri < rules.size(); ++ri)
             {
-                const SchemaText& s = T->schemas[si];
+                const SchemaText& s = rules[ri];
                 std::vector<const Literal*> body;
                 bool has_head = false;
                 for (const Literal& l : s.eff)
@@ -985,6 +1045,8 @@ private:
             return atoms * per + (L.fluent_count + 1) * 4;
         };
         constexpr u64 kMaxBytes = u64{4} << 30;
+        if (m_opt == AtomsOption::Lazy && C->has_ce)
+            throw Error("conditional effects are supported by the ground search over frozen atom slots, not with lazy slots");
         if (m_opt == AtomsOption::Lazy)
         {
             // no slots yet: the initial state's atoms take the first ones (build_state_tables); the tables are sized for
@@ -1320,11 +1382,7 @@ private:
             // parameters and the earlier witnesses bound, and the count plan of the later witnesses
             {
                 DevWitness wd{};
-                std::vector<u8> rel(s.arity, 0);
-                for (const Literal& l : s.eff)
-                    for (i32 x : l.terms)
-                        if (x >= 0)
-                            rel[static_cast<u32>(x)] = 1;
+                const std::vector<u8> rel = effect_relevant(s);
                 const std::vector<u32> wit = witness_order(*C, si, rel);
                 wd.n = static_cast<u32>(wit.size());
                 std::vector<u8> bound = rel;
@@ -1663,6 +1721,24 @@ u32 CompiledTask::slot_of_atom(u32 pred, const u32* objs) const
     return c < layout.fluent_count ? slot_of[c] : kNone;
 }
 
+std::vector<u8> effect_relevant(const SchemaText& s)
+{
+    std::vector<u8> rel(s.arity, 0);
+    auto mark = [&](const std::vector<Literal>& ls) {
+        for (const Literal& l : ls)
+            for (i32 x : l.terms)
+                if (x >= 0 && static_cast<u32>(x) < s.arity)
+                    rel[static_cast<u32>(x)] = 1;
+    };
+    mark(s.eff);
+    for (const CondEffectText& ce : s.ces)
+    {
+        mark(ce.cond);
+        mark(ce.eff);
+    }
+    return rel;
+}
+
 /// The witness parameters of schema si (those no effect mentions) in the order the reference's successor matcher binds
 /// them (src/mymyr/task/compile.cpp:916-946): after every effect-relevant parameter, greedily the one with the most
 /// binary constraints to placed parameters, then the most fluent unary constraints, then the fewest dom0 objects, ties
@@ -1731,6 +1807,88 @@ std::vector<u32> witness_order(const CompiledTask& task, u32 si, const std::vect
     return order;
 }
 
+namespace
+{
+/// The ground instances of schema si's conditional effects for the action with parameters `bind` into g (the
+/// reference's collect_literals, include/mymyr/successor/successors.hpp:321-385): per effect, every binding of its
+/// forall parameters over their static domains whose static condition literals hold; the fluent condition literals
+/// become slots (a positive one without a slot never holds: the instance is dropped; a negative one always holds), the
+/// effects slots (an add without a slot belongs to an instance that never fires in a reachable state: dropped; a
+/// delete without one changes nothing).
+void ground_ces(const CompiledTask& task, u32 si, const std::vector<u32>& bind, GroundActions& g)
+{
+    const TaskText& T = task.text;
+    const SchemaText& s = T.schemas[si];
+    for (u32 k = 0; k < s.ces.size(); ++k)
+    {
+        const CondEffectText& ce = s.ces[k];
+        const auto& dom = task.ce_dom0[si][k];
+        std::vector<u32> ext(ce.extra, 0);
+        auto obj = [&](i32 x) { return x < 0 ? term_object(x) : static_cast<u32>(x) < s.arity ? bind[x] : ext[x - s.arity]; };
+        std::function<void(u32)> rec = [&](u32 d) {
+            if (d < ce.extra)
+            {
+                for (u32 o = 0; o < task.n; ++o)
+                    if ((dom[d][o >> 6] >> (o & 63)) & 1)
+                    {
+                        ext[d] = o;
+                        rec(d + 1);
+                    }
+                return;
+            }
+            std::vector<u32> pos, neg, add, del;
+            std::vector<u32> objs;
+            for (const Literal& l : ce.cond)
+            {
+                objs.clear();
+                for (i32 x : l.terms)
+                    objs.push_back(obj(x));
+                if (T.preds[l.pred].kind == 'S')
+                {
+                    if (task.static_holds(l.pred, objs.data()) != l.positive)
+                        return;
+                    continue;
+                }
+                const u32 slot = task.slot_of_atom(l.pred, objs.data());
+                if (slot == kNone)
+                {
+                    if (l.positive)
+                        return;
+                    continue;
+                }
+                (l.positive ? pos : neg).push_back(slot);
+            }
+            for (const Literal& l : ce.eff)
+            {
+                objs.clear();
+                for (i32 x : l.terms)
+                    objs.push_back(obj(x));
+                const u32 slot = task.slot_of_atom(l.pred, objs.data());
+                if (slot == kNone)
+                {
+                    if (l.positive)
+                        return;
+                    continue;
+                }
+                (l.positive ? add : del).push_back(slot);
+            }
+            if (add.empty() && del.empty())
+                return;  // changes nothing where it fires
+            if (pos.size() > 255 || neg.size() > 255 || add.size() > 255 || del.size() > 255)
+                throw Error("ground conditional effect with more than 255 atoms in one list");
+            g.ce_meta.push_back(static_cast<u32>(pos.size()) | static_cast<u32>(neg.size()) << 8 | static_cast<u32>(add.size()) << 16 |
+                                static_cast<u32>(del.size()) << 24);
+            g.ce_soff.push_back(static_cast<u32>(g.ce_slots.size()));
+            for (auto* v : {&pos, &neg, &add, &del})
+                g.ce_slots.insert(g.ce_slots.end(), v->begin(), v->end());
+            if (g.ce_slots.size() > (u64{1} << 31))
+                throw Error("the ground conditional effects hold more than 2^31 atoms");
+        };
+        rec(0);
+    }
+}
+}  // namespace
+
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit)
 {
     const TaskText& T = task.text;
@@ -1748,16 +1906,10 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
     for (u32 si = 0; si < T.schemas.size(); ++si)
     {
         const SchemaText& s = T.schemas[si];
-        std::vector<u8> rel(s.arity, 0);
+        const std::vector<u8> rel = effect_relevant(s);
         std::vector<u32> wit;  // witness parameters in the matcher's order
         if (witness_pruning)
-        {
-            for (const Literal& l : s.eff)
-                for (i32 x : l.terms)
-                    if (x >= 0)
-                        rel[x] = 1;
             wit = witness_order(task, si, rel);
-        }
         if (task.never[si])
             continue;
         const u32 first_action = static_cast<u32>(g.meta.size());
@@ -1832,6 +1984,11 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
                 g.schema.push_back(si);
                 for (u32 k = 0; k < g.label_width; ++k)
                     g.binding.push_back(k < s.arity ? bind[k] : kNone);
+                if (task.has_ce)
+                {
+                    g.ce_off.push_back(static_cast<u32>(g.ce_meta.size()));
+                    ground_ces(task, si, bind, g);
+                }
                 return;
             }
             const auto& dom = task.dom0[si][d];
@@ -1859,6 +2016,8 @@ GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64
                 groups[key].push_back({std::move(w), a});
             }
     }
+    if (task.has_ce)
+        g.ce_off.push_back(static_cast<u32>(g.ce_meta.size()));
     if (witness_pruning)
     {
         // dominators: the group's members (fixed effect-relevant objects) whose witness objects come first in the

@@ -45,12 +45,23 @@ struct Literal
     std::vector<i32> terms;
 };
 
+/// A conditional effect (the reference's ConditionalEffect, include/mymyr/formalism/task_data.hpp): for every binding of
+/// its `extra` forall parameters (terms arity .. arity + extra - 1) under which `cond` holds in the state, the
+/// literals `eff` apply (deletes, then adds, with the schema's own effects).
+struct CondEffectText
+{
+    u32 extra = 0;
+    std::vector<Literal> cond;
+    std::vector<Literal> eff;
+};
+
 struct SchemaText
 {
     std::string name;
     u32 arity = 0;
     std::vector<Literal> pre;
-    std::vector<Literal> eff;  // positive = add, negative = delete
+    std::vector<Literal> eff;           // the unconditional effects: positive = add, negative = delete
+    std::vector<CondEffectText> ces;    // effects with a condition or forall parameters
 };
 
 struct PredicateText
@@ -103,8 +114,8 @@ struct TaskText
     std::vector<GroundLiteralText> encoding_goal;
 };
 
-/// Parses the reference's task text format (classical subset: no numeric sections, no axioms, no conditional
-/// effects). Throws mya::Error naming what is unsupported or malformed.
+/// Parses the reference's task text format (classical subset: no numeric sections, no axioms). Throws mya::Error naming
+/// what is unsupported or malformed.
 TaskText parse_task_text(std::string_view text);
 
 /// Atom slots (include/mymyr/task/atom_index.hpp:12-22): Reachable and Dense are frozen (the slot table is a function of
@@ -324,6 +335,9 @@ struct CompiledTask
     // wanted both true and false: the reference's compiled goal.unsatisfiable, compile.cpp:1322-1343)
     std::vector<std::pair<bool, u64>> goal_fluent;
     bool goal_fixed_unsat = false;
+    // conditional effects: per schema, per conditional effect, the static domains of its forall parameters
+    bool has_ce = false;
+    std::vector<std::vector<std::vector<std::vector<u64>>>> ce_dom0;
     u32 label_width = 0;
     std::vector<std::vector<std::vector<u64>>> dom0;  // per schema, per parameter: object bits (ow words)
     std::vector<u8> never;                            // per schema
@@ -358,6 +372,13 @@ struct GroundActions
     /// its effect-relevant binding and a smaller witness object). Empty without witness pruning.
     std::vector<u32> dom_off;
     std::vector<u32> dom;
+    /// Conditional effects: action a's ground instances are [ce_off[a], ce_off[a + 1]) (empty without conditional
+    /// effects); instance k fires in a state where its condition slots ce_slots[ce_soff[k] ..] hold (npos positive, then
+    /// nneg negative; ce_meta[k] = npos | nneg << 8 | nadd << 16 | ndel << 24), and then adds and deletes its slots.
+    std::vector<u32> ce_off;
+    std::vector<u32> ce_meta;
+    std::vector<u32> ce_soff;
+    std::vector<u32> ce_slots;
     u32 label_width = 0;
     [[nodiscard]] u32 size() const { return static_cast<u32>(meta.size()); }
 };
@@ -368,6 +389,10 @@ struct GroundActions
 /// successor is the one whose witness objects come first in the matcher's witness order, the binding it finds first
 /// (include/mymyr/successor/detail/engine.hpp:345-356; the order: src/mymyr/task/compile.cpp:916-946).
 GroundActions ground_actions(const CompiledTask& task, bool witness_pruning, u64 limit);
+
+/// The effect-relevant parameters of a schema: those its effects or its conditional effects' conditions and effects
+/// mention (src/mymyr/task/compile.cpp:1140-1162); the others are witnesses.
+std::vector<u8> effect_relevant(const SchemaText& s);
 
 /// The witness parameters of schema si (those `relevant` does not mark) in the order the reference's matcher binds them
 /// (src/mymyr/task/compile.cpp:916-946).

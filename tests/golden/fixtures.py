@@ -32,7 +32,11 @@ SUITE_COUNTS = {
     "freecell__p02": (159924, 1371273, 1),
     "folding-opt23-adl__p01": (148260, 170776, 1),
     "organic-synthesis-opt18-strips__p20": (41311, 52548, 24),
+    "miconic-simpleadl__s10-2": (316680, 6333600, 20),
+    "caldera-split-opt18-adl__p04": (468041, 630395, 4472),
 }
+# suite tasks with conditional effects: searched by the ground driver only (the lifted entry points refuse them)
+CE_TASKS = ["miconic-simpleadl__s10-2", "caldera-split-opt18-adl__p04"]
 # suite tasks outside the published counts whose slot tables are pinned too (rovers__p02's schemas have two witness
 # parameters; its BrFS is pinned in brfs_witness.json)
 LAYOUT_ONLY = ["rovers__p02"]

@@ -612,6 +612,28 @@ def make_brfs(quick: bool):
     dump("brfs.json", out)
 
 
+def make_brfs_suite_add():
+    """Adds the suite, budget, goal and expanded-cut records of the suite tasks that brfs.json does not hold yet (the
+    step keeps the existing records, whose strips cuts take long to regenerate)."""
+    path = os.path.join(fx.GOLDEN, "brfs.json")
+    with open(path) as f:
+        out = json.load(f)
+    for name in fx.SUITE_COUNTS:
+        if name in out["suite"]:
+            continue
+        out["suite"][name] = brfs_record(name, stop_at_goal=False)
+        out["budget"][name] = brfs_record(name, stop_at_goal=False, max_states=20000)
+        out["budget"][name + ":goal"] = brfs_record(name, stop_at_goal=True)
+        out["budget"][name + ":expanded"] = brfs_record(name, stop_at_goal=False, max_expanded=3000)
+        print(name, out["suite"][name]["states"], flush=True)
+    # the goal states of the solved budget records (auto slots) as canonical atom ids: a device search over other slots
+    # (dense) compares its goal state through them
+    for key, rec in out["budget"].items():
+        if rec["solved"] and "goal_cids" not in rec:
+            rec["goal_cids"] = goal_cids(ref.RefTask(fx.task_path(key.split(":")[0]), "auto"), rec["goal_state"])
+    dump("brfs.json", out)
+
+
 LAZY_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "pegsol-08-strips__p22", "visitall__visitall_x-6_y-3_r-100",
               "miconic__s7-4", "logistics00__probLOGISTICS-6-1", "driverlog__p03", "rovers__p02"]
 
@@ -673,7 +695,8 @@ def main():
     workload_tasks()
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
-             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick)}
+             "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
+             "brfs_suite_add": make_brfs_suite_add}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -41,7 +41,7 @@ ALL_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "driverl
              "miconic__s7-4", "parcprinter-opt11-strips__p03", "pathways__p02", "pegsol-08-strips__p22", "rovers__p02",
              "snake-opt18-strips__p05", "sokoban-opt08-strips__p14", "transport-opt08-strips__p23",
              "visitall__visitall_x-6_y-3_r-100", "zenotravel__p05", "gridworld", "strips", "transport", "transport_xl",
-             "freecell__p02", "folding-opt23-adl__p01"]
+             "freecell__p02", "folding-opt23-adl__p01", "miconic-simpleadl__s10-2", "caldera-split-opt18-adl__p04"]
 
 
 @pytest.mark.parametrize("name", ALL_TASKS)
@@ -89,10 +89,14 @@ def test_task_errors():
         Task.from_text("O 2\nP 1\nF 1 p\nSI 0\nFI 0\nG 0\nA 1\nbig 33\nL 0\nE 1\n0\nL 0\nF 1\n0 1 0\n")
 
 
-def test_conditional_effects_and_axioms_refused():
+def test_conditional_effects_load_frozen_and_refuse_lazy():
+    """A schema with a conditional effect (one effect with a condition) loads with frozen slots; lazy slots refuse it,
+    as the lifted entry points do (the ground search is the one path that evaluates conditional effects)."""
     txt = "O 1\nP 1\nF 1 p\nSI 0\nFI 0\nG 0\nA 1\nx 1\nL 0\nE 1\n0\nL 1\n0 1 0\nF 1\n0 1 0\n"
+    for atoms in ("auto", "dense", "reachable"):
+        assert Task.from_text(txt, atoms).words == 1
     with pytest.raises(MyaError, match="conditional effects"):
-        Task.from_text(txt)
+        Task.from_text(txt, "lazy")
 
 
 def test_generators_deterministic():
