@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 17
+#define MYA_ABI_VERSION 18
 int mya_abi_version(void);
 
 /* Device memory held by the library (replaces DeviceContext::usage(), include/mymyr/cuda/runtime.hpp:140-146, 183):
@@ -497,8 +497,45 @@ typedef struct mya_brfs_options
     uint32_t goal_count;
     const uint32_t* goal_offsets;
     const int32_t* goal_literals;
+    /* BrfsOptions::observer and progress_interval (brfs.hpp:99-100; the events of search::SearchObserver,
+     * include/mymyr/search/control.hpp:157-186): null for none. progress_interval 0 means the reference's default,
+     * 2^16 expansions. */
+    const struct mya_search_observer* observer;
+    uint64_t progress_interval;
 } mya_brfs_options;
 #define MYA_GOAL_LITERAL_INTS 9
+
+/* search::SearchStatistics (include/mymyr/search/control.hpp:129-139): the counts of a layer (on_pass), of the search
+ * so far (on_progress) or of the whole search (on_end, with pruned); seconds of wall time since the search (on_pass:
+ * the layer) started. memory_bytes is 0 in events, as in the reference. */
+typedef struct mya_search_statistics
+{
+    uint64_t expanded;
+    uint64_t generated;
+    uint64_t states;
+    uint64_t pruned;
+    double seconds;
+    uint64_t memory_bytes;
+} mya_search_statistics;
+
+/* The events of search::SearchObserver (include/mymyr/search/control.hpp:157-186) that the device search sends, each
+ * on the thread that called mya_brfs; a null function is skipped. on_start: the start state's row (`words` words);
+ * on_pass: the end of BrFS layer `layer` (0 first) with that layer's counts; on_progress: before a device batch once
+ * `progress_interval` more states were expanded (the reference asks every progress_interval expansions; the device
+ * search asks at its batch boundaries), returning 0 stops the search with status 4 (Cancelled); on_solution: the plan
+ * (schemas[i], bindings[i * label_width ..], -1 padded) and its cost; on_end: the final status and statistics. The
+ * per-state events (on_expand, on_generate, on_prune, on_transition) are not sent: the device search does not bring
+ * its states and transitions to the host. */
+typedef struct mya_search_observer
+{
+    void* user;
+    void (*on_start)(void* user, const uint64_t* state, uint32_t words);
+    void (*on_pass)(void* user, uint32_t layer, const mya_search_statistics* pass);
+    int32_t (*on_progress)(void* user, const mya_search_statistics* so_far);
+    void (*on_solution)(void* user, const int32_t* schemas, const int32_t* bindings, uint32_t length, uint32_t label_width,
+                        double cost);
+    void (*on_end)(void* user, int32_t status, const mya_search_statistics* total);
+} mya_search_observer;
 
 /* BrfsResult fields (include/mymyr/search/brfs.hpp:103-138). status: the reference's SearchStatus codes
  * (0 solved, 1 exhausted, 2 out of states, 3 out of time, 4 cancelled, 5 failed, 6 unsolvable). */

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 17  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 18  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -122,10 +122,29 @@ class BrfsOptions(Structure):
         ("goal_count", c_uint32),
         ("goal_offsets", c_void_p),
         ("goal_literals", c_void_p),
+        ("observer", c_void_p),
+        ("progress_interval", c_uint64),
     ]
 
 
 GOAL_LITERAL_INTS = 9  # MYA_GOAL_LITERAL_INTS
+
+
+class SearchStatistics(Structure):
+    _fields_ = [("expanded", c_uint64), ("generated", c_uint64), ("states", c_uint64), ("pruned", c_uint64),
+                ("seconds", c_double), ("memory_bytes", c_uint64)]
+
+
+ON_START = ctypes.CFUNCTYPE(None, c_void_p, ctypes.POINTER(c_uint64), c_uint32)
+ON_PASS = ctypes.CFUNCTYPE(None, c_void_p, c_uint32, ctypes.POINTER(SearchStatistics))
+ON_PROGRESS = ctypes.CFUNCTYPE(c_int32, c_void_p, ctypes.POINTER(SearchStatistics))
+ON_SOLUTION = ctypes.CFUNCTYPE(None, c_void_p, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), c_uint32, c_uint32, c_double)
+ON_END = ctypes.CFUNCTYPE(None, c_void_p, c_int32, ctypes.POINTER(SearchStatistics))
+
+
+class SearchObserver(Structure):
+    _fields_ = [("user", c_void_p), ("on_start", ON_START), ("on_pass", ON_PASS), ("on_progress", ON_PROGRESS),
+                ("on_solution", ON_SOLUTION), ("on_end", ON_END)]
 
 
 class BrfsResult(Structure):

@@ -716,7 +716,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             budget_stopped = true;
             break;
         }
-        if (halt.check())
+        if (halt.check(r.expanded, r.generated, set.size))
         {
             stopped = true;
             break;
@@ -727,6 +727,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         const u64 layer_begin = pos, layer_end = set.size;
         const u64 ln = layer_end - layer_begin;
         std::array<u64, 3> row{0, 0, 0};
+        const auto layer_t0 = Clock::now();
         const u64 size0 = set.size;
         // the budget check precedes the goal test of each state (brfs.cpp:138-144): parents at or past the remaining
         // budget are neither tested nor expanded
@@ -814,7 +815,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         };
         while (p0 < lim && !stopped)
         {
-            if (halt.check())
+            if (halt.check(r.expanded + row[0], r.generated + row[1], set.size))
                 break;  // the pending chunk is confirmed below; the layer ends at its last parent
             // count ahead when the counted parents past p0 hold less than a full chunk (and the layer has more)
             const bool count_now = counted < lim && counted_total - base < chunk;
@@ -984,6 +985,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             stopped = true;
         }
         lc.push_back(row);
+        if (o.on_pass)
+            o.on_pass(static_cast<u32>(lc.size() - 1), row, std::chrono::duration<double>(Clock::now() - layer_t0).count());
         if (!stopped)
             pos = layer_end;
     }

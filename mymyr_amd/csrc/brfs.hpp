@@ -38,6 +38,12 @@ struct BrfsOptionsC
     // all makes no state a goal); any_of false: the task's goal
     bool any_of = false;
     std::vector<std::vector<u32>> goal_pos, goal_neg;
+    // the observer's events sent from inside the search (SearchObserver::on_pass and on_progress,
+    // include/mymyr/search/control.hpp:157-186): the end of a layer with its {expanded, generated, new} counts and
+    // seconds; before a batch once progress_interval more states were expanded, false stopping the search (Cancelled)
+    std::function<void(u32 layer, const std::array<u64, 3>& counts, double seconds)> on_pass;
+    std::function<bool(u64 expanded, u64 generated, u64 states, double seconds)> on_progress;
+    u64 progress_interval = u64{1} << 16;
 };
 
 /// Whether one of the AnyOf goals holds in a row of `words` words (host).

@@ -220,27 +220,35 @@ inline std::vector<u64> start_row(const CompiledTask& task, const BrfsOptionsC& 
     return row;
 }
 
-/// max_seconds and the cancellation flag (the reference's Control::check, src/mymyr/search/brfs.cpp:168-181): checked
-/// by the drivers before every batch; `why` keeps the first reason (OutOfTime or Cancelled).
+/// max_seconds, the cancellation flag and the observer's on_progress (the reference's Control::check and keep_going,
+/// src/mymyr/search/brfs.cpp:137-181): checked by the drivers before every batch with the counts so far; `why` keeps
+/// the first reason (OutOfTime or Cancelled).
 struct Halt
 {
-    bool timed;
-    Clock::time_point deadline;
-    const volatile i32* cancel;
+    const BrfsOptionsC& o;
+    Clock::time_point t0, deadline;
+    u64 next_progress;  // on_progress is asked once this many states were expanded
     i32 why = 0;
-    Halt(const BrfsOptionsC& o, Clock::time_point t0) : timed(o.timed), cancel(o.cancel)
+    Halt(const BrfsOptionsC& opt, Clock::time_point start)
+        : o(opt), t0(start), next_progress(std::max<u64>(1, opt.progress_interval))
     {
         const double s = std::min(std::max(0.0, o.max_seconds), 1e9);
         deadline = t0 + std::chrono::duration_cast<Clock::duration>(std::chrono::duration<double>(s));
     }
-    bool check()
+    bool check(u64 expanded, u64 generated, u64 states)
     {
         if (why)
             return true;
-        if (timed && Clock::now() >= deadline)
+        if (o.timed && Clock::now() >= deadline)
             why = kOutOfTime;
-        else if (cancel && *cancel)
+        else if (o.cancel && *o.cancel)
             why = kCancelled;
+        else if (o.on_progress && expanded >= next_progress)
+        {
+            next_progress = expanded + std::max<u64>(1, o.progress_interval);
+            if (!o.on_progress(expanded, generated, states, std::chrono::duration<double>(Clock::now() - t0).count()))
+                why = kCancelled;
+        }
         return why != 0;
     }
 };

@@ -284,7 +284,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
             budget_stopped = true;
             break;
         }
-        if (halt.check())
+        if (halt.check(r.expanded, r.generated, set.size))
         {
             stopped = true;
             break;
@@ -294,6 +294,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         ++r.layers;
         const u64 lb = pos, le = set.size, ln = le - lb;
         std::array<u64, 3> row{0, 0, 0};
+        const auto layer_t0 = Clock::now();
         const u64 size0 = set.size;
         const u64 budget = o.max_expanded == ~u64{0} ? ~u64{0} : o.max_expanded - r.expanded;
         u64 lim = std::min(ln, budget);
@@ -327,7 +328,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         u64 p0 = 0, base = 0;
         while (p0 < lim && !stopped)
         {
-            if (halt.check())
+            if (halt.check(r.expanded + row[0], r.generated + row[1], set.size))
                 break;
             hipLaunchKernelGGL(k_chunk_end, dim3(1), dim3(1), 0, stream, offsets, 1u, p0, lim, base + chunk, small + kChunkP);
             launch_check("chunk end");
@@ -471,6 +472,8 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
             stopped = true;
         }
         lc.push_back(row);
+        if (o.on_pass)
+            o.on_pass(static_cast<u32>(lc.size() - 1), row, std::chrono::duration<double>(Clock::now() - layer_t0).count());
         if (!stopped)
             pos = le;
     }

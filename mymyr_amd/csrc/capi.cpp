@@ -477,6 +477,26 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         o.max_seconds = options->max_seconds;
         o.cancel = options->cancel;
         resolve_any_of(task, *options, o);
+        // the observer (search::SearchObserver, include/mymyr/search/control.hpp:157-186): on_start here, on_pass and
+        // on_progress from inside the drivers, on_solution and on_end once the result is known (Control::finish,
+        // src/mymyr/search/brfs.cpp:193-211)
+        const mya_search_observer* obs = options->observer;
+        o.progress_interval = options->progress_interval ? options->progress_interval : u64{1} << 16;
+        if (obs && obs->on_pass)
+            o.on_pass = [obs](u32 layer, const std::array<u64, 3>& c, double seconds) {
+                const mya_search_statistics st{c[0], c[1], c[2], 0, seconds, 0};
+                obs->on_pass(obs->user, layer, &st);
+            };
+        if (obs && obs->on_progress)
+            o.on_progress = [obs](u64 expanded, u64 generated, u64 states, double seconds) {
+                const mya_search_statistics st{expanded, generated, states, 0, seconds, 0};
+                return obs->on_progress(obs->user, &st) != 0;
+            };
+        if (obs && obs->on_start)
+        {
+            const std::vector<u64>& s0 = o.start.empty() ? task->compiled->initial : o.start;
+            obs->on_start(obs->user, s0.data(), static_cast<u32>(s0.size()));
+        }
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
         bool searched = true;
@@ -545,6 +565,14 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
                 for (int j = 0; j < 3; ++j)
                     layer_counts[i * 3 + j] = lc[i][j];
         layers = static_cast<int>(lc.size());
+        if (obs && obs->on_solution && r.solved)
+            obs->on_solution(obs->user, r.plan_schema.data(), r.plan_binding.data(), static_cast<u32>(r.plan_schema.size()),
+                             r.plan_width, r.cost);
+        if (obs && obs->on_end)
+        {
+            const mya_search_statistics st{r.expanded, r.generated, r.states, r.pruned, r.search_s, 0};
+            obs->on_end(obs->user, r.status, &st);
+        }
     });
     return rc == 0 ? layers : -1;
 }

@@ -27,6 +27,148 @@ class Action(NamedTuple):
 
 
 @dataclass
+class Statistics:
+    """search::SearchStatistics (include/mymyr/search/control.hpp:129-139) as the observer's events carry it."""
+
+    expanded: int = 0
+    generated: int = 0
+    states: int = 0
+    pruned: int = 0
+    seconds: float = 0.0
+    memory_bytes: int = 0
+
+
+def _default_event(fn):
+    # an event a subclass does not override carries this attribute and is not installed (python/mymyr/search/
+    # _observer.py:17-20)
+    fn._mymyr_default_event = True
+    return fn
+
+
+class Observer:
+    """Base class of search observers (the reference's mymyr.search.Observer, python/mymyr/search/_observer.py:23-120):
+    pass an instance (or any object with some of these methods) as ``observer=`` to :func:`brfs` and override the
+    events of interest; events a subclass does not override are never called. The device search sends ``on_start``,
+    ``on_pass`` after every layer, ``on_progress`` at its batch boundaries once ``progress_interval`` more states were
+    expanded, ``on_solution`` and ``on_end``, all on the calling thread. It does not bring states and transitions to the
+    host, so an observer that defines ``on_expand``, ``on_generate``, ``on_prune`` or ``on_transition`` is refused. The
+    first exception an event raises stops the search (status "cancelled") and is raised when the search returns."""
+
+    @_default_event
+    def on_start(self, state: np.ndarray) -> None:
+        """The search starts from ``state`` (its words)."""
+
+    @_default_event
+    def on_expand(self, id: int, state) -> None:
+        """Not sent by the device search."""
+
+    @_default_event
+    def on_generate(self, parent: int, action: Action, child, state, is_new: bool) -> None:
+        """Not sent by the device search."""
+
+    @_default_event
+    def on_prune(self, parent: int, action: Action, state) -> None:
+        """Not sent by the device search."""
+
+    @_default_event
+    def on_transition(self, parent: int, action: Action, child, state, outcome) -> None:
+        """Not sent by the device search."""
+
+    @_default_event
+    def on_pass(self, width: int, stats: Statistics) -> None:
+        """The brfs layer of this depth ended; ``stats`` are its own counts."""
+
+    @_default_event
+    def on_solution(self, plan: list, cost: float) -> None:
+        """A plan was found."""
+
+    @_default_event
+    def on_progress(self, stats: Statistics) -> bool:
+        """The statistics so far; return False to stop the search (status "cancelled")."""
+        return True
+
+    @_default_event
+    def on_end(self, status: str, stats: Statistics) -> None:
+        """The search ended with ``status`` and the total ``stats``."""
+
+
+_PER_STATE_EVENTS = ("on_expand", "on_generate", "on_prune", "on_transition")
+
+
+def _event(obj, name: str):
+    fn = getattr(obj, name, None)
+    if fn is None or getattr(fn, "_mymyr_default_event", False):
+        return None
+    return fn
+
+
+def _stats(p) -> Statistics:
+    v = p.contents
+    return Statistics(int(v.expanded), int(v.generated), int(v.states), int(v.pruned), float(v.seconds), int(v.memory_bytes))
+
+
+class _ObserverBridge:
+    """The C observer (mya_search_observer) forwarding to a Python object's events; keeps the ctypes callbacks alive for
+    the search and records the first exception an event raised."""
+
+    def __init__(self, obj, interval: int):
+        for name in _PER_STATE_EVENTS:
+            if _event(obj, name) is not None:
+                raise ValueError(f"mymyr_amd: brfs: the device search does not send {name} (per-state events stay on the "
+                                 "device); observers may define on_start, on_pass, on_progress, on_solution and on_end")
+        self.error: BaseException | None = None
+        ev = {n: _event(obj, n) for n in ("on_start", "on_pass", "on_progress", "on_solution", "on_end")}
+        self.defines_any = any(f is not None for f in ev.values())
+
+        def guard(fn):
+            def run(*args):
+                if self.error is not None:
+                    return None
+                try:
+                    return fn(*args)
+                except BaseException as e:  # noqa: BLE001 - re-raised when the search returns
+                    self.error = e
+                    return None
+            return run
+
+        def on_start(_u, state, words):
+            ev["on_start"](np.ctypeslib.as_array(state, shape=(words,)).copy())
+
+        def on_pass(_u, layer, stats):
+            ev["on_pass"](int(layer), _stats(stats))
+
+        # the C side asks at every batch boundary (interval 1), so that an exception in any event stops the search at
+        # the next batch; the observer's on_progress is called every `interval` expansions
+        self.next_progress = max(1, interval)
+
+        def on_progress(_u, stats):
+            if self.error is not None:
+                return 0
+            if ev["on_progress"] is None or stats.contents.expanded < self.next_progress:
+                return 1
+            self.next_progress = int(stats.contents.expanded) + max(1, interval)
+            r = guard(lambda: ev["on_progress"](_stats(stats)))()
+            return 0 if self.error is not None or (r is not None and not r) else 1
+
+        def on_solution(_u, schemas, bindings, length, width, cost):
+            plan = [Action(int(schemas[i]), tuple(int(bindings[i * width + k]) for k in range(width) if bindings[i * width + k] >= 0))
+                    for i in range(length)]
+            ev["on_solution"](plan, float(cost))
+
+        def on_end(_u, status, stats):
+            ev["on_end"](STATUS.get(int(status), str(int(status))), _stats(stats))
+
+        # on_progress is always installed: an exception in another event stops the search at the next batch
+        self.c = _lib.SearchObserver(
+            None,
+            _lib.ON_START(guard(on_start)) if ev["on_start"] else _lib.ON_START(),
+            _lib.ON_PASS(guard(on_pass)) if ev["on_pass"] else _lib.ON_PASS(),
+            _lib.ON_PROGRESS(on_progress),
+            _lib.ON_SOLUTION(guard(on_solution)) if ev["on_solution"] else _lib.ON_SOLUTION(),
+            _lib.ON_END(guard(on_end)) if ev["on_end"] else _lib.ON_END())
+
+
+@dataclass
 class BrfsResult:
     """The fields of the reference's BrfsResult (include/mymyr/search/brfs.hpp:103-138) that the device search fills.
     A solved search has its plan (Actions from the start state to the first goal state tested), its cost (unit action
@@ -114,7 +256,8 @@ def _goal_records(task: Task, goal) -> tuple[np.ndarray, np.ndarray]:
 def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None, max_expanded: int | None = None,
          witness_pruning: bool = True, stop_at_goal: bool = True, fingerprint: bool = False, layer_stats: bool = True,
          chunk: int = 0, memory_states: int = 0, timings: bool = False, start=None, blocked_states=None,
-         max_seconds: float | None = None, cancel: CancelToken | None = None, goal=None) -> BrfsResult:
+         max_seconds: float | None = None, cancel: CancelToken | None = None, goal=None, observer=None,
+         progress_interval: int | None = None) -> BrfsResult:
     """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
     (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer.
 
@@ -125,7 +268,9 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     goal (None: the task's goal): BrfsOptions::goal as GoalSpec::AnyOf, a sequence of ground conditions, each a sequence
     of (predicate index, positive, object indices) literals; a state is a goal iff one of them holds in it (the
     reference's goal= with GroundConditions, python/src/search_bindings.cpp:439-505; conditions that can never hold are
-    left out)."""
+    left out).
+    observer (an :class:`Observer`, or any object with some of its methods) and progress_interval (expansions between
+    on_progress calls; None: 2^16): BrfsOptions::observer and progress_interval (include/mymyr/search/brfs.hpp:99-100)."""
     if max_seconds is not None and not max_seconds >= 0:
         raise ValueError("mymyr_amd: brfs: max_seconds must be >= 0")
     if cancel is not None and not isinstance(cancel, CancelToken):
@@ -137,13 +282,19 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
                                                    else blocked_states, "blocked_states")
     timed = max_seconds is not None and np.isfinite(max_seconds)
     go, gl = _goal_records(task, goal) if goal is not None else (None, None)
+    if progress_interval is not None and not 0 <= int(progress_interval) < (1 << 64):
+        raise ValueError("mymyr_amd: brfs: progress_interval must be a non-negative 64-bit count")
+    bridge = _ObserverBridge(observer, (1 << 16) if progress_interval is None else int(progress_interval)) if observer is not None else None
+    if bridge is not None and not bridge.defines_any:
+        bridge = None  # an observer that defines no event is not installed
     o = _lib.BrfsOptions(UNBOUNDED32 if max_depth is None else max_depth, int(witness_pruning),
                          UNBOUNDED64 if max_states is None else max_states, UNBOUNDED64 if max_expanded is None else max_expanded,
                          int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0,
                          None if st is None else st.ctypes.data, None if bl is None or bl.shape[0] == 0 else bl.ctypes.data,
                          0 if bl is None else bl.shape[0], task.words, int(timed), float(max_seconds) if timed else 0.0,
                          None if cancel is None else cancel.address, 0 if goal is None else 1, 0 if goal is None else len(go) - 1,
-                         None if go is None else go.ctypes.data, None if gl is None or gl.size == 0 else gl.ctypes.data)
+                         None if go is None else go.ctypes.data, None if gl is None or gl.size == 0 else gl.ctypes.data,
+                         None if bridge is None else ctypes.addressof(bridge.c), 1)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -156,6 +307,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ctypes.byref(plan))
     if n < 0:
         check(-1)
+    if bridge is not None and bridge.error is not None:
+        raise bridge.error
     kernels = {c: {"ms": r.kernel_ms[i], "bytes": r.kernel_bytes[i], "launches": r.kernel_launches[i]}
                for i, c in enumerate(KERNEL_CLASSES)}
     res = BrfsResult(STATUS.get(r.status, str(r.status)), r.states, r.expanded, r.generated, r.goal_states, r.layers,

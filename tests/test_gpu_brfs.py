@@ -343,3 +343,80 @@ def test_conditional_effects_refused_by_lifted_entry_points(golden):
         rl.successors(t, rows)
     with pytest.raises(MyaError, match="conditional effects"):
         rl.EnvPool(t, 4)
+
+
+def test_observer_events(golden):
+    """BrfsOptions::observer (include/mymyr/search/control.hpp:157-186) on the device search: on_start with the start
+    state, on_pass per layer with the reference-pinned layer counts, on_solution with the plan and on_end with the
+    result's status and totals (Control::finish, src/mymyr/search/brfs.cpp:193-211); on_progress every
+    progress_interval expansions, False stopping the search as cancelled; an exception in an event stops the search and
+    is raised; per-state events are refused."""
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("gripper__prob05"))
+
+    class Rec(search.Observer):
+        def __init__(self):
+            self.ev = []
+
+        def on_start(self, state):
+            self.ev.append(("start", [int(x) for x in state]))
+
+        def on_pass(self, width, stats):
+            self.ev.append(("pass", width, stats.expanded, stats.generated, stats.states))
+
+        def on_progress(self, stats):
+            self.ev.append(("progress", stats.expanded, stats.generated, stats.states))
+            return True
+
+        def on_solution(self, plan, cost):
+            self.ev.append(("solution", plan, cost))
+
+        def on_end(self, status, stats):
+            self.ev.append(("end", status, stats.expanded, stats.generated, stats.states, stats.pruned))
+
+    # gripper over the ground driver (to its goal and exhaustively), a 20-word transport task over the lifted one
+    for name, stop in (("gripper__prob05", True), ("gripper__prob05", False), ("transport_w20_3", True)):
+        t = Task.from_text_file(golden.task_path(name))
+        o = Rec()
+        r = search.brfs(t, stop_at_goal=stop, observer=o, progress_interval=5000)
+        assert o.ev[0] == ("start", [int(x) for x in t.initial_state()])
+        passes = [e for e in o.ev if e[0] == "pass"]
+        assert [p[1] for p in passes] == list(range(len(r.layer_counts)))
+        assert [list(p[2:]) for p in passes] == r.layer_counts
+        prog = [e for e in o.ev if e[0] == "progress"]
+        assert (prog or r.expanded < 100000) and all(b[1] - a[1] >= 5000 for a, b in zip(prog, prog[1:]))
+        assert all(p[1] >= 5000 and p[1] <= r.expanded for p in prog)
+        sol = [e for e in o.ev if e[0] == "solution"]
+        assert (len(sol) == 1 and sol[0][1] == r.plan and sol[0][2] == r.cost) if r.solved else not sol
+        assert o.ev[-1] == ("end", r.status, r.expanded, r.generated, r.states, r.pruned)
+
+    class Stop(search.Observer):
+        def __init__(self):
+            self.calls = 0
+
+        def on_progress(self, stats):
+            self.calls += 1
+            return False
+
+    t = Task.from_text_file(golden.task_path("gripper__prob05"))
+    o = Stop()
+    r = search.brfs(t, stop_at_goal=False, observer=o, progress_interval=1)
+    full = search.brfs(t, stop_at_goal=False)
+    assert r.status == "cancelled" and o.calls == 1 and r.expanded < full.expanded
+
+    class Boom(search.Observer):
+        def on_pass(self, width, stats):
+            if width == 3:
+                raise RuntimeError("boom")
+
+    with pytest.raises(RuntimeError, match="boom"):
+        search.brfs(t, stop_at_goal=False, observer=Boom())
+
+    class PerState(search.Observer):
+        def on_generate(self, parent, action, child, state, is_new):
+            pass
+
+    with pytest.raises(ValueError, match="on_generate"):
+        search.brfs(t, observer=PerState())
