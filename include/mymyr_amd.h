@@ -502,6 +502,25 @@ typedef struct mya_brfs_options
      * 2^16 expansions. */
     const struct mya_search_observer* observer;
     uint64_t progress_interval;
+    /* BrfsOptions::layers (search::LayerOrdering, include/mymyr/search/layer_ordering.hpp:63-113). layer_kind: 0 queue
+     * (the plain BrFS), 1 in order, 2 reverse, 3 randomized (SplitMix64 of layer_seed), 4 goal count (by the task goal's
+     * satisfied literals, most first unless prefer_fewer_satisfied_goals), 5 scored (layer_scorer: scores[i] of the
+     * layer's host rows [n, words], lower first; NaN is an error). With an ordered kind each next layer is reordered
+     * before it is expanded (state ids follow the expansion order; the start layer keeps its order). max_next_layer_states
+     * (0: no limit) cuts a layer's generation once the next layer holds that many states, dropping the rest of the
+     * layer; beam_width (0: no beam) keeps the first beam_width states of each ordered layer, the others stay stored
+     * and are never expanded; randomize_ties breaks equal scores by SplitMix64 tokens drawn in generation order. The
+     * reference's checks apply (check_layers, layer_ordering.hpp:117-134); beam_novelty is accepted as 0 (all tested)
+     * or 1 (survivors only, the same in a BrFS), relaxed survivors-only (2) is refused. */
+    int32_t layer_kind;
+    int32_t prefer_fewer_satisfied_goals;
+    uint64_t layer_seed;
+    uint32_t max_next_layer_states;
+    uint32_t beam_width;
+    int32_t randomize_ties;
+    int32_t beam_novelty;
+    void (*layer_scorer)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, double* scores);
+    void* layer_scorer_user;
 } mya_brfs_options;
 #define MYA_GOAL_LITERAL_INTS 9
 

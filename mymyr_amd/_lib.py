@@ -99,6 +99,10 @@ class StepOutputs(Structure):
     ]
 
 
+# BrfsOptions::layers' scorer: (user, rows [n, words], n, words, scores [n])
+LAYER_SCORER = ctypes.CFUNCTYPE(None, c_void_p, POINTER(c_uint64), c_uint64, c_uint32, POINTER(c_double))
+
+
 class BrfsOptions(Structure):
     _fields_ = [
         ("max_depth", c_uint32),
@@ -124,6 +128,15 @@ class BrfsOptions(Structure):
         ("goal_literals", c_void_p),
         ("observer", c_void_p),
         ("progress_interval", c_uint64),
+        ("layer_kind", c_int32),
+        ("prefer_fewer_satisfied_goals", c_int32),
+        ("layer_seed", c_uint64),
+        ("max_next_layer_states", c_uint32),
+        ("beam_width", c_uint32),
+        ("randomize_ties", c_int32),
+        ("beam_novelty", c_int32),
+        ("layer_scorer", LAYER_SCORER),
+        ("layer_scorer_user", c_void_p),
     ]
 
 

@@ -446,7 +446,7 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
 template<int W, bool kCE>
 __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRows<W, kCE> src, u64 m, const u32* __restrict__ list,
                                                        const u64* __restrict__ size_now, const u64* __restrict__ size_next, u64 limit,
-                                                       u64* __restrict__ nodes, u32* __restrict__ status)
+                                                       const u64* __restrict__ parent_ids, u64* __restrict__ nodes, u32* __restrict__ status)
 {
     constexpr int G = kGroup<W>;
     constexpr int K = kPairs<W>;
@@ -482,7 +482,11 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
             src.template load_pa<G, K>(pa[b], q, r);
             store_row<G, K>(s.arena + id * W, W, q, r);
             if (q == 0)
-                nodes[id] = ((src.first + src.parent_of(pa[b])) << 32) | src.action_of(pa[b]);
+            {
+                // parent rows gathered in an ordered layer's expansion order carry their ids in parent_ids
+                const u64 p = src.first + src.parent_of(pa[b]);
+                nodes[id] = ((parent_ids ? parent_ids[p] : p) << 32) | src.action_of(pa[b]);
+            }
         }
     }
 }
@@ -696,6 +700,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     }
     const auto td0 = Clock::now();
     Halt halt(o, t0);
+    LayerOrder lorder(o);
+    LayerRows lrows(stream);
     bool stopped = false, budget_stopped = false;
     r.status = kExhausted;
     u64 pos = 0;                           // states expanded or passed (the reference's queue position)
@@ -729,10 +735,34 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         std::array<u64, 3> row{0, 0, 0};
         const auto layer_t0 = Clock::now();
         const u64 size0 = set.size;
+        // parent rows: the layer's rows in the arena, or an ordered layer's rows gathered in its expansion order (the
+        // positions below are then expansion positions, pids their state ids)
+        const u64* par = set.v.arena;
+        u64 pbase = layer_begin;
+        const u64* pids = nullptr;
+        u64 keep = ln;
+        if (lorder.ordered() && layer_begin > 0)
+        {
+            lrows.order(lorder, o, task, set.v.arena, layer_begin, ln, W, stream);
+            par = lrows.rows.p;
+            pbase = 0;
+            pids = lrows.d_ids.p;
+            keep = lrows.ids.size();
+        }
+        auto id_at = [&](u64 p) { return pids ? lrows.ids[p] : layer_begin + p; };
+        // the id at which the store takes no more states: max_states, and with max_next_layer_states the layer's end
+        // plus the limit (the layer is cut there and the search goes on, brfs.cpp:360-365)
+        u64 cut_at = bounded ? o.max_states : ~u64{0};
+        bool layer_cut = false, truncated = false;
+        if (lorder.limited() && layer_end + o.max_next_layer_states < cut_at)
+        {
+            cut_at = layer_end + o.max_next_layer_states;
+            layer_cut = true;
+        }
         // the budget check precedes the goal test of each state (brfs.cpp:138-144): parents at or past the remaining
         // budget are neither tested nor expanded
         const u64 budget = o.max_expanded == ~u64{0} ? ~u64{0} : o.max_expanded - r.expanded;
-        u64 lim = std::min(ln, budget);
+        u64 lim = std::min(keep, budget);
         u64 counted = 0, counted_total = 0;  // parents [0, counted) counted; offsets[counted * S] on the host
         u64 first_goal = ~u64{0};
         bool goal_stop = false;
@@ -757,15 +787,16 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             if (status & kStatusTableFull)
                 throw std::length_error("mymyr_amd: brfs: state table full");
             const u64 winners = size_dev - set.size;
-            const u64 room = (bounded ? o.max_states : cap_states) - set.size;
+            const bool cuts = cut_at <= cap_states;  // a cut inside the arena (else only its capacity bounds the store)
+            const u64 room = (cuts ? cut_at : cap_states) - set.size;
             // insert: every candidate's record, probe entry and slot, the parent rows, and the row each non-winner
             // compared equal to; compaction: per winner its list entry, record, slot, arena row and entry
             tm.bytes(kKInsert, pend.m * 20 + pend.np * R + (pend.m - std::min(winners, pend.m)) * R);
             tm.bytes(kKRank, pend.m * 9 + winners * 4);
-            if (bounded && winners >= room && winners > 0)
+            if (cuts && winners >= room && winners > 0)
             {
-                // the store filled at winner room - 1 (id max_states - 1): the search stops inside its parent's
-                // expansion; the compaction wrote ids below max_states only
+                // the store filled at winner room - 1 (id cut_at - 1): the search (max_states) or the layer
+                // (max_next_layer_states) stops inside its parent's expansion; the compaction wrote ids below cut_at only
                 tm.bytes(kKCompact, room * (2 * R + 24));
                 u32 jc = 0;
                 hip_check(hipMemcpyAsync(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost, stream), "cut");
@@ -789,6 +820,13 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 layer_goals += b.host[kGoalSum];
                 if (blocked.capacity)
                     layer_pruned += b.host[kCutPruned];
+                if (layer_cut)
+                {
+                    // the search goes on with the next layer: the cut winners' entries must not stand for states
+                    state_set_cut(set, cut_at, room, winners, stream);
+                    truncated = true;
+                    return true;
+                }
                 set.size = o.max_states;
                 r.status = kOutOfStates;
                 stopped = true;
@@ -825,7 +863,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 const u64 est = seen_parents ? std::max<u64>(1, (seen_cands + seen_parents - 1) / seen_parents) : 1;
                 nb = std::min<u64>(lim - counted, std::max<u64>(u64{1} << 18, chunk / est));
                 tm.begin(kKCount);
-                hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kTW * kWave)), dim3(kTW * kWave), 0, stream, set.v.arena, layer_begin + counted,
+                hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kTW * kWave)), dim3(kTW * kWave), 0, stream, par, pbase + counted,
                                    static_cast<u32>(nb), g, goal, counts + counted * S, goal_flags + counted);
                 launch_check("ground count");
                 tm.end(kKCount, nb * (R + 5));
@@ -878,12 +916,12 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 hip_check(hipStreamSynchronize(stream), "sync");
                 end_off = b.host[kChunkOff];
             }
-            if (bounded && p1 > p0 + 1)
+            if (cut_at <= cap_states && p1 > p0 + 1)
             {
-                // near the max_states cut, a chunk of about the candidates the store's room needs at the last chunk's
-                // rate of new states (with a margin): the chunk the store fills in then probes few candidates past the
-                // cut (chunk boundaries change no result)
-                const double room = static_cast<double>(o.max_states - set.size);
+                // near a cut, a chunk of about the candidates the store's room needs at the last chunk's rate of new
+                // states (with a margin): the chunk the store fills in then probes few candidates past the cut (chunk
+                // boundaries change no result)
+                const double room = static_cast<double>(cut_at - set.size);
                 const double want = room / std::max(new_rate, 1.0 / 1024) * 1.25 + 65536.0;
                 if (want < static_cast<double>(end_off - base))
                 {
@@ -896,12 +934,12 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             }
             const u64 m = end_off - base;
             const u32 np = static_cast<u32>(p1 - p0);
-            const ParentRows<W, false> src{set.v.arena, layer_begin + p0, cand_pa, d_masks, abits};
-            const ParentRows<W, true> src_ce{set.v.arena, layer_begin + p0, cand_pa, d_masks, abits, g.ce_off, g.ce_meta, g.ce_soff, g.ce_slots};
+            const ParentRows<W, false> src{par, pbase + p0, cand_pa, d_masks, abits};
+            const ParentRows<W, true> src_ce{par, pbase + p0, cand_pa, d_masks, abits, g.ce_off, g.ce_meta, g.ce_soff, g.ce_slots};
             if (m > 0)
             {
                 tm.begin(kKEmit);
-                hipLaunchKernelGGL(k_ground_emit<W>, dim3(blocks_for(np, kTW * kWave)), dim3(kTW * kWave), 0, stream, set.v.arena, layer_begin + p0, np, g,
+                hipLaunchKernelGGL(k_ground_emit<W>, dim3(blocks_for(np, kTW * kWave)), dim3(kTW * kWave), 0, stream, par, pbase + p0, np, g,
                                    offsets + p0 * S, base, abits, cand_pa);
                 launch_check("ground emit");
                 tm.end(kKEmit, np * (R + 8) + m * 4);
@@ -923,14 +961,15 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 tm.begin(kKCompact);
                 {
                     const dim3 grid(std::min<u64>(blocks_for(m * G, kLB), kStrideBlocks));
-                    u32* const cstat = bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status;
-                    const u64 climit = bounded ? o.max_states : cap_states;
+                    // winners past a cut are expected (the cut is confirmed on the host); past the arena an error
+                    u32* const cstat = cut_at <= cap_states ? reinterpret_cast<u32*>(small + kSpare) : set.d_status;
+                    const u64 climit = std::min(cut_at, cap_states);
                     if (g.ce_off)
                         hipLaunchKernelGGL((k_ground_compact<W, true>), grid, dim3(kLB), 0, stream, set.v, src_ce, m, set.list,
-                                           state_set_size_now(set), state_set_size_next(set), climit, nodes, cstat);
+                                           state_set_size_now(set), state_set_size_next(set), climit, pids, nodes, cstat);
                     else
                         hipLaunchKernelGGL((k_ground_compact<W, false>), grid, dim3(kLB), 0, stream, set.v, src, m, set.list,
-                                           state_set_size_now(set), state_set_size_next(set), climit, nodes, cstat);
+                                           state_set_size_now(set), state_set_size_next(set), climit, pids, nodes, cstat);
                 }
                 launch_check("ground compact");
                 tm.end(kKCompact, 0);
@@ -968,16 +1007,16 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
         r.generated += row[1];
         row[2] = set.size - size0;
         // the states this layer goal-tested: the expanded ones, plus the goal state a goal stop ends at
-        const u64 tested = row[0] + ((goal_stop && !stopped) ? 1 : 0);
+        const u64 tested = row[0] + ((goal_stop && !stopped && !truncated) ? 1 : 0);
         if (first_goal != ~u64{0} && first_goal < tested && r.first_goal < 0)
-            r.first_goal = static_cast<i64>(layer_begin + first_goal);
-        if (goal_stop && !stopped)
+            r.first_goal = static_cast<i64>(id_at(first_goal));
+        if (goal_stop && !stopped && !truncated)
         {
             r.goal_states += 1;  // the goal state is tested (and counted), then the search stops
             r.status = kSolved;
             stopped = true;
         }
-        if (!goal_stop && !stopped && lim < ln)
+        if (!goal_stop && !stopped && !truncated && lim < keep)
         {
             // the expansion budget ran out inside this layer
             r.status = kOutOfStates;

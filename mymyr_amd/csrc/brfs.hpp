@@ -44,6 +44,16 @@ struct BrfsOptionsC
     std::function<void(u32 layer, const std::array<u64, 3>& counts, double seconds)> on_pass;
     std::function<bool(u64 expanded, u64 generated, u64 states, double seconds)> on_progress;
     u64 progress_interval = u64{1} << 16;
+    // BrfsOptions::layers (include/mymyr/search/layer_ordering.hpp:63-113): kind 0 queue, 1 in order, 2 reverse,
+    // 3 randomized, 4 goal count, 5 scored (the reference's Kind order); ~0: no limit / no beam
+    i32 layer_kind = 0;
+    u64 layer_seed = 0;
+    u32 max_next_layer_states = ~u32{0};
+    bool prefer_more_satisfied_goals = true;
+    u32 beam_width = ~u32{0};
+    bool randomize_ties = false;
+    // scored layers: scores[i] of the layer's rows [n, words] (host), lower first
+    std::function<void(const u64* rows, u64 n, u32 words, double* scores)> scorer;
 };
 
 /// Whether one of the AnyOf goals holds in a row of `words` words (host).

@@ -12,6 +12,8 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cmath>
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
@@ -309,6 +311,246 @@ private:
     hipStream_t m_s;
     BrfsResultC& m_r;
     std::vector<Pair> m_ev;
+};
+
+/// SplitMix64 as the reference specifies it (include/mymyr/core/random.hpp:1-16, bit for bit): the state advances by
+/// the golden gamma and each output is its mix64; bounded(n) is Lemire's multiply-shift with rejection; shuffle is
+/// Fisher-Yates from the back (for i = n down to 2: swap a[i - 1] with a[bounded(i)]).
+class SplitMix64
+{
+public:
+    explicit SplitMix64(u64 seed) : m_state(seed) {}
+    u64 next()
+    {
+        m_state += kGamma;
+        return mix64(m_state);
+    }
+    u64 bounded(u64 n)
+    {
+        unsigned __int128 m = static_cast<unsigned __int128>(next()) * n;
+        u64 low = static_cast<u64>(m);
+        if (low < n)
+        {
+            const u64 threshold = (u64{0} - n) % n;  // 2^64 mod n
+            while (low < threshold)
+            {
+                m = static_cast<unsigned __int128>(next()) * n;
+                low = static_cast<u64>(m);
+            }
+        }
+        return static_cast<u64>(m >> 64);
+    }
+    template<class T>
+    void shuffle(std::vector<T>& a)
+    {
+        for (u64 i = a.size(); i > 1; --i)
+            std::swap(a[i - 1], a[bounded(i)]);
+    }
+
+private:
+    static constexpr u64 kGamma = 0x9e3779b97f4a7c15ull;
+    u64 m_state;
+};
+
+/// The expansion order of BrFS layers under BrfsOptions::layers (the reference's LayerOrderer,
+/// src/mymyr/search/layer_order_detail.hpp:26-200): a layer of n states (positions in id order) is reordered by the
+/// kind and, with a beam, cut to its first beam_width entries. The generator persists across the layers of a search.
+class LayerOrder
+{
+public:
+    enum Kind : i32
+    {
+        kQueue = 0,
+        kInOrder = 1,
+        kReverse = 2,
+        kRandomized = 3,
+        kGoalCount = 4,
+        kScored = 5,
+    };
+    explicit LayerOrder(const BrfsOptionsC& o) : m_o(o), m_rng(o.layer_seed) {}
+    [[nodiscard]] bool ordered() const { return m_o.layer_kind != kQueue; }
+    [[nodiscard]] bool limited() const { return ordered() && m_o.max_next_layer_states != ~u32{0}; }
+    [[nodiscard]] bool ranked() const { return m_o.layer_kind == kGoalCount || m_o.layer_kind == kScored; }
+    /// The positions of a layer of n states in expansion order (cut to the beam); `keys` (ranked kinds): each state's
+    /// rank key, smaller first, ties by a random token (randomize_ties, drawn in position order) and then position.
+    std::vector<u32> order(u32 n, const std::vector<u64>& keys)
+    {
+        std::vector<u32> out(n);
+        for (u32 i = 0; i < n; ++i)
+            out[i] = i;
+        if (m_o.layer_kind == kReverse)
+            std::reverse(out.begin(), out.end());
+        else if (m_o.layer_kind == kRandomized)
+            m_rng.shuffle(out);
+        else if (ranked())
+        {
+            struct Ranked
+            {
+                u64 key, tie;
+                u32 pos;
+            };
+            std::vector<Ranked> rk(n);
+            for (u32 i = 0; i < n; ++i)
+                rk[i] = {keys[i], m_o.randomize_ties ? m_rng.next() : 0, i};
+            std::sort(rk.begin(), rk.end(), [](const Ranked& a, const Ranked& b) {
+                return a.key != b.key ? a.key < b.key : a.tie != b.tie ? a.tie < b.tie : a.pos < b.pos;
+            });
+            for (u32 i = 0; i < n; ++i)
+                out[i] = rk[i].pos;
+        }
+        if (m_o.beam_width != ~u32{0} && out.size() > m_o.beam_width)
+            out.resize(m_o.beam_width);
+        return out;
+    }
+    /// The rank key of a score: doubles ordered as unsigned integers (-inf first, +inf last; -0 as 0).
+    static u64 score_key(double v)
+    {
+        u64 bits = 0;
+        const double z = v == 0 ? 0.0 : v;
+        std::memcpy(&bits, &z, sizeof(bits));
+        return (bits >> 63) ? ~bits : bits | (u64{1} << 63);
+    }
+
+private:
+    const BrfsOptionsC& m_o;
+    SplitMix64 m_rng;
+};
+
+/// out[k] = v[ids[k] - first]: per-state bytes of a layer in its expansion order.
+__global__ void k_gather_u8(const u8* __restrict__ v, const u64* __restrict__ ids, u64 first, u64 n, u8* __restrict__ out)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += static_cast<u64>(gridDim.x) * blockDim.x)
+        out[i] = v[ids[i] - first];
+}
+
+/// GoalCount rank keys of rows [0, n) of W words: the task goal's unsatisfied literals (positive slots not set,
+/// negative slots set; the masks hold each literal once), or their complement with prefer_less (fewest satisfied first).
+__global__ void k_goal_keys(const u64* __restrict__ rows, u64 n, u32 W, const u64* __restrict__ pos, const u64* __restrict__ neg,
+                            u32 prefer_less, u32* __restrict__ keys)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        const u64* r = rows + i * W;
+        u32 unsat = 0;
+        for (u32 w = 0; w < W; ++w)
+            unsat += __popcll(pos[w] & ~r[w]) + __popcll(neg[w] & r[w]);
+        keys[i] = prefer_less ? ~unsat : unsat;
+    }
+}
+
+/// out[k] = rows[ids[k]] (W words each): a layer's rows in expansion order.
+__global__ void k_gather_rows(const u64* __restrict__ rows, const u64* __restrict__ ids, u64 n, u32 W, u64* __restrict__ out)
+{
+    for (u64 i = static_cast<u64>(blockIdx.x) * blockDim.x + threadIdx.x; i < n * W; i += static_cast<u64>(gridDim.x) * blockDim.x)
+    {
+        const u64 k = i / W, w = i % W;
+        out[i] = rows[ids[k] * W + w];
+    }
+}
+
+/// A device buffer grown to the largest request of a search, freed in the order of its stream.
+template<class T>
+struct GrowBuf
+{
+    hipStream_t stream;
+    T* p = nullptr;
+    u64 cap = 0;
+    explicit GrowBuf(hipStream_t s) : stream(s) {}
+    GrowBuf(const GrowBuf&) = delete;
+    GrowBuf& operator=(const GrowBuf&) = delete;
+    T* get(u64 n, const char* what)
+    {
+        if (n > cap)
+        {
+            if (p)
+                dev_free_async(p, stream);
+            p = dev_alloc<T>(std::max<u64>(n, 1), what);
+            cap = std::max<u64>(n, 1);
+        }
+        return p;
+    }
+    ~GrowBuf()
+    {
+        if (p)
+            dev_free_async(p, stream);
+    }
+};
+
+/// The expansion order of an ordered layer (BrfsOptions::layers): `ids` (host and device) holds the layer's state ids
+/// in the order they are expanded, cut to the beam, and `rows` their rows gathered in that order, so that the
+/// drivers expand positions [0, ids.size()) of it as they expand a layer of the arena. The start layer is never
+/// reordered (src/mymyr/search/brfs.cpp:316-318).
+struct LayerRows
+{
+    explicit LayerRows(hipStream_t s) : d_ids(s), rows(s), keys(s), masks(s) {}
+    std::vector<u64> ids;
+    GrowBuf<u64> d_ids;
+    GrowBuf<u64> rows;
+    GrowBuf<u32> keys;
+    GrowBuf<u64> masks;
+
+    /// Orders the layer [first, first + n) of the arena (W words per row) and gathers its rows.
+    void order(LayerOrder& lo, const BrfsOptionsC& o, const CompiledTask& task, const u64* arena, u64 first, u64 n, u32 W, hipStream_t stream)
+    {
+        if (n > 0xFFFFFFFFull)
+            throw std::length_error("mymyr_amd: brfs: an ordered layer of more than 2^32 - 1 states");
+        std::vector<u64> key;
+        if (o.layer_kind == LayerOrder::kGoalCount && n > 0)
+        {
+            // the task's goal (also under another search goal), each literal once (layer_ordering.hpp:93-96)
+            std::vector<u64> m(2 * static_cast<size_t>(W), 0);
+            for (u32 sl : task.goal_pos)
+                if (sl < 64 * W)
+                    m[sl >> 6] |= u64{1} << (sl & 63);
+            for (u32 sl : task.goal_neg)
+                if (sl < 64 * W)
+                    m[W + (sl >> 6)] |= u64{1} << (sl & 63);
+            u64* dm = masks.get(2 * W, "goal count masks");
+            hip_check(hipMemcpyAsync(dm, m.data(), m.size() * sizeof(u64), hipMemcpyHostToDevice, stream), "goal count masks");
+            u32* dk = keys.get(n, "goal count keys");
+            hipLaunchKernelGGL(k_goal_keys, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(n, 256), 4096))), dim3(256), 0, stream,
+                               arena + first * W, n, W, dm, dm + W, o.prefer_more_satisfied_goals ? 0u : 1u, dk);
+            launch_check("goal count keys");
+            std::vector<u32> hk(n);
+            hip_check(hipMemcpyAsync(hk.data(), dk, n * sizeof(u32), hipMemcpyDeviceToHost, stream), "goal count keys");
+            hip_check(hipStreamSynchronize(stream), "goal count keys");
+            key.assign(hk.begin(), hk.end());
+        }
+        else if (o.layer_kind == LayerOrder::kScored && n > 0)
+        {
+            // one call of the scorer per layer with the layer's states in generation order (layer_ordering.hpp:98-104)
+            std::vector<u64> hr(n * W);
+            hip_check(hipMemcpyAsync(hr.data(), arena + first * W, hr.size() * sizeof(u64), hipMemcpyDeviceToHost, stream), "layer rows");
+            hip_check(hipStreamSynchronize(stream), "layer rows");
+            std::vector<double> sc(n, 0.0);
+            o.scorer(hr.data(), n, W, sc.data());
+            key.resize(n);
+            for (u64 i = 0; i < n; ++i)
+            {
+                if (std::isnan(sc[i]))
+                    throw std::invalid_argument("mymyr: a layer score is NaN");
+                key[i] = LayerOrder::score_key(sc[i]);
+            }
+        }
+        const std::vector<u32> pos = lo.order(static_cast<u32>(n), key);
+        ids.resize(pos.size());
+        for (size_t k = 0; k < pos.size(); ++k)
+            ids[k] = first + pos[k];
+        gather(arena, W, stream);
+    }
+    /// The ordered rows from the arena again (after the arena's rows were widened).
+    void gather(const u64* arena, u32 W, hipStream_t stream)
+    {
+        const u64 k = ids.size();
+        u64* di = d_ids.get(k, "layer order");
+        u64* dr = rows.get(k * W, "ordered layer rows");
+        if (k == 0)
+            return;
+        hip_check(hipMemcpyAsync(di, ids.data(), k * sizeof(u64), hipMemcpyHostToDevice, stream), "layer order");
+        hipLaunchKernelGGL(k_gather_rows, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(k * W, 256), 8192))), dim3(256), 0, stream, arena,
+                           di, k, W, dr);
+        launch_check("ordered layer rows");
+    }
 };
 
 }  // namespace

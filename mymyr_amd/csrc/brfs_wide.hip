@@ -58,8 +58,8 @@ template<int G, int K>
 __global__ __launch_bounds__(kWB) void k_wide_compact(StateSetView s, const u64* __restrict__ rows, u64 m, const u32* __restrict__ list,
                                                      const u64* __restrict__ size_now, const u64* __restrict__ size_next, u64 limit,
                                                      const i32* __restrict__ parent, const i32* __restrict__ index,
-                                                     const u8* __restrict__ goal, u64 first, u64* __restrict__ nodes,
-                                                     u8* __restrict__ goal_id, u32* __restrict__ status)
+                                                     const u8* __restrict__ goal, u64 first, const u64* __restrict__ parent_ids,
+                                                     u64* __restrict__ nodes, u8* __restrict__ goal_id, u32* __restrict__ status)
 {
     const u32 q = lane_id() % G;
     const u64 id0 = *size_now;
@@ -79,7 +79,9 @@ __global__ __launch_bounds__(kWB) void k_wide_compact(StateSetView s, const u64*
         store_row<G, K>(s.arena + id * s.words, s.words, q, r);
         if (q == 0)
         {
-            nodes[id] = ((first + static_cast<u64>(parent[j])) << 32) | static_cast<u32>(index[j]);
+            // parents gathered in an ordered layer's expansion order carry their ids in parent_ids
+            const u64 p = first + static_cast<u64>(parent[j]);
+            nodes[id] = ((parent_ids ? parent_ids[p] : p) << 32) | static_cast<u32>(index[j]);
             goal_id[id] = goal[j];
         }
     }
@@ -266,6 +268,9 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
     };
     const auto td0 = Clock::now();
     Halt halt(o, t0);
+    LayerOrder lorder(o);
+    LayerRows lrows(stream);
+    GrowBuf<u8> lgoal(stream);  // an ordered layer's goal flags in its expansion order
     bool stopped = false, budget_stopped = false;
     r.status = kExhausted;
     u64 pos = 0;
@@ -296,16 +301,41 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         std::array<u64, 3> row{0, 0, 0};
         const auto layer_t0 = Clock::now();
         const u64 size0 = set.size;
+        // parent rows and goal flags: the layer's in the arena, or an ordered layer's gathered in its expansion order
+        // (positions below are then expansion positions)
+        const bool ordered = lorder.ordered() && lb > 0;
+        u64 keep = ln;
+        const u8* gflags = goal_id + lb;
+        if (ordered)
+        {
+            lrows.order(lorder, o, task, set.v.arena, lb, ln, W, stream);
+            keep = lrows.ids.size();
+            u8* g = lgoal.get(keep, "ordered layer goal flags");
+            if (keep)
+                hipLaunchKernelGGL(k_gather_u8, dim3(std::min<u64>(blocks_for(keep, 256), 4096)), dim3(256), 0, stream, goal_id + lb,
+                                   lrows.d_ids.p, lb, keep, g);
+            launch_check("ordered layer goal flags");
+            gflags = g;
+        }
+        auto parents = [&](u64 p) { return ordered ? lrows.rows.p + p * W : set.v.arena + (lb + p) * W; };
+        auto id_at = [&](u64 p) { return ordered ? lrows.ids[p] : lb + p; };
+        u64 cut_at = bounded ? o.max_states : ~u64{0};
+        bool layer_cut = false, truncated = false;
+        if (lorder.limited() && le + o.max_next_layer_states < cut_at)
+        {
+            cut_at = le + o.max_next_layer_states;
+            layer_cut = true;
+        }
         const u64 budget = o.max_expanded == ~u64{0} ? ~u64{0} : o.max_expanded - r.expanded;
-        u64 lim = std::min(ln, budget);
+        u64 lim = std::min(keep, budget);
         // the layer's first goal state among the parents to expand, and their successor counts
         set_small(kFirstGoal, ~u64{0});
-        hipLaunchKernelGGL(k_first_u8, dim3(std::min<u64>(blocks_for(lim, 256), 4096)), dim3(256), 0, stream, goal_id + lb, lim,
+        hipLaunchKernelGGL(k_first_u8, dim3(std::min<u64>(blocks_for(lim, 256), 4096)), dim3(256), 0, stream, gflags, lim,
                            small + kFirstGoal);
         launch_check("goal search");
         tm.begin(kKCount);
         ExpandArgs a = base_args;
-        a.states = set.v.arena + lb * W;
+        a.states = parents(0);
         a.rows = lim;
         a.pass = 0;
         a.counts = counts;
@@ -342,7 +372,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
             {
                 tm.begin(kKEmit);
                 ExpandArgs e = base_args;
-                e.states = set.v.arena + (lb + p0) * W;
+                e.states = parents(p0);
                 e.rows = p1 - p0;
                 e.pass = 1;
                 e.offsets = offsets + p0;
@@ -368,7 +398,11 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                             throw std::logic_error("mymyr_amd: brfs: an added atom without a slot was not recorded");
                         base_args.T = T;
                         if (lazy_row_words(task.words) > W)
+                        {
                             widen(lazy_row_words(task.words));
+                            if (ordered)
+                                lrows.gather(set.v.arena, W, stream);  // the ordered rows at the new width
+                        }
                         continue;
                     }
                 }
@@ -384,8 +418,9 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 wide_shape(W, [&]<int G, int K>() {
                     hipLaunchKernelGGL((k_wide_compact<G, K>), dim3(std::min<u64>(blocks_for(m * G, kWB), kWideStrideBlocks)), dim3(kWB), 0, stream,
                                        set.v, cand_rows, m, set.list, state_set_size_now(set), state_set_size_next(set),
-                                       bounded ? o.max_states : cap_states, cand_parent, cand_index, cand_goal, lb + p0, nodes, goal_id,
-                                       bounded ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
+                                       std::min(cut_at, cap_states), cand_parent, cand_index, cand_goal, ordered ? p0 : lb + p0,
+                                       ordered ? lrows.d_ids.p : nullptr, nodes, goal_id,
+                                       cut_at <= cap_states ? reinterpret_cast<u32*>(small + kSpare) : set.d_status);
                 });
                 launch_check("wide compact");
                 tm.end(kKCompact, 0);
@@ -393,7 +428,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
             }
             // the chunk's goal parents, its outcome and the expansion's status in one synchronization
             set_small(kGoalSum, 0);
-            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(p1 - p0, 256), 1024)), dim3(256), 0, stream, goal_id + lb + p0,
+            hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(p1 - p0, 256), 1024)), dim3(256), 0, stream, gflags + p0,
                                p1 - p0, small + kGoalSum);
             if (blocked.capacity)
             {
@@ -407,11 +442,13 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
             check_expansion();
             const u64 size_dev = b.host[kSizeNow];
             const u64 winners = size_dev - set.size;
-            const u64 room = (bounded ? o.max_states : cap_states) - set.size;
+            const bool cuts = cut_at <= cap_states;  // a cut inside the arena (else only its capacity bounds the store)
+            const u64 room = (cuts ? cut_at : cap_states) - set.size;
             tm.bytes(kKCompact, std::min(winners, room) * (2 * R + 21));
-            if (bounded && winners >= room && winners > 0)
+            if (cuts && winners >= room && winners > 0)
             {
-                // the store filled at winner room - 1 (id max_states - 1): the search stops inside its parent's expansion
+                // the store filled at winner room - 1 (id cut_at - 1): the search (max_states) or the layer
+                // (max_next_layer_states) stops inside its parent's expansion
                 u32 jc = 0;
                 hip_check(hipMemcpy(&jc, set.list + (room - 1), sizeof(u32), hipMemcpyDeviceToHost), "cut");
                 i32 pc = 0;
@@ -420,7 +457,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 row[1] += u64{jc} + 1;
                 set_small(kGoalSum, 0);
                 hipLaunchKernelGGL(k_sum_u8, dim3(std::min<u64>(blocks_for(static_cast<u64>(pc) + 1, 256), 1024)), dim3(256), 0, stream,
-                                   goal_id + lb + p0, static_cast<u64>(pc) + 1, small + kGoalSum);
+                                   gflags + p0, static_cast<u64>(pc) + 1, small + kGoalSum);
                 if (blocked.capacity)
                 {
                     set_small(kPruned, 0);
@@ -431,6 +468,13 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 layer_goals += b.host[kGoalSum];
                 if (blocked.capacity)
                     layer_pruned += b.host[kPruned];
+                if (layer_cut)
+                {
+                    // the search goes on with the next layer: the cut winners' entries must not stand for states
+                    state_set_cut(set, cut_at, room, winners, stream);
+                    truncated = true;
+                    break;
+                }
                 set.size = o.max_states;
                 r.status = kOutOfStates;
                 stopped = true;
@@ -456,16 +500,16 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         r.expanded += row[0];
         r.generated += row[1];
         row[2] = set.size - size0;
-        const u64 tested = row[0] + ((goal_stop && !stopped) ? 1 : 0);
+        const u64 tested = row[0] + ((goal_stop && !stopped && !truncated) ? 1 : 0);
         if (first_goal != ~u64{0} && first_goal < tested && r.first_goal < 0)
-            r.first_goal = static_cast<i64>(lb + first_goal);
-        if (goal_stop && !stopped)
+            r.first_goal = static_cast<i64>(id_at(first_goal));
+        if (goal_stop && !stopped && !truncated)
         {
             r.goal_states += 1;
             r.status = kSolved;
             stopped = true;
         }
-        if (!goal_stop && !stopped && lim < ln)
+        if (!goal_stop && !stopped && !truncated && lim < keep)
         {
             r.status = kOutOfStates;
             budget_stopped = true;

@@ -497,6 +497,47 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
             const std::vector<u64>& s0 = o.start.empty() ? task->compiled->initial : o.start;
             obs->on_start(obs->user, s0.data(), static_cast<u32>(s0.size()));
         }
+        // BrfsOptions::layers with the reference's checks (check_layers, include/mymyr/search/layer_ordering.hpp:117-134)
+        {
+            const i32 k = options->layer_kind;
+            const u32 limit = options->max_next_layer_states ? options->max_next_layer_states : ~u32{0};
+            const u32 beam = options->beam_width ? options->beam_width : ~u32{0};
+            auto bad = [](const std::string& m) { throw std::invalid_argument("mymyr brfs: " + m); };
+            if (k < 0 || k > 5)
+                bad("layer_kind must be 0 (queue) .. 5 (scored)");
+            if (k == 0 && limit != ~u32{0})
+                bad("max_next_layer_states needs an ordered layer order (any but the queue)");
+            if (beam != ~u32{0} && k == 0)
+                bad("beam_width needs an ordered layer order (any but the queue)");
+            if (beam != ~u32{0} && limit != ~u32{0})
+                bad("beam_width and max_next_layer_states exclude each other");
+            if (options->beam_novelty < 0 || options->beam_novelty > 2)
+                bad("beam_novelty must be 0 (all tested), 1 (survivors only) or 2 (relaxed survivors only)");
+            if (beam == ~u32{0} && options->beam_novelty != 0)
+                bad("a beam novelty other than all-tested needs a beam (beam_width)");
+            if (options->randomize_ties && k != 4 && k != 5)
+                bad("randomize_ties needs a layer order with scores (goal count or a scorer)");
+            if ((k == 5) != (options->layer_scorer != nullptr))
+                bad("a scorer is needed by the scored layer order and taken by no other");
+            if (options->beam_novelty == 2)
+            {
+                if (k != 4)
+                    bad("the relaxed survivors-only beam novelty needs the goal-count layer order (it ranks by score)");
+                throw std::invalid_argument("mymyr_amd: brfs: the relaxed survivors-only beam is not supported by the device search");
+            }
+            o.layer_kind = k;
+            o.layer_seed = options->layer_seed;
+            o.max_next_layer_states = limit;
+            o.prefer_more_satisfied_goals = options->prefer_fewer_satisfied_goals == 0;
+            o.beam_width = beam;
+            o.randomize_ties = options->randomize_ties != 0;
+            if (k == 5)
+            {
+                auto fn = options->layer_scorer;
+                void* user = options->layer_scorer_user;
+                o.scorer = [fn, user](const u64* rows, u64 n, u32 words, double* scores) { fn(user, rows, n, words, scores); };
+            }
+        }
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
         bool searched = true;

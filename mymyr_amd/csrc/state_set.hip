@@ -144,6 +144,16 @@ __global__ __launch_bounds__(kBlock) void k_settle(u64* __restrict__ table, u64 
     }
 }
 
+/// The epoch ids of the winners list[kept, winners) of a cut batch: an id past every arena (sets hold fewer than
+/// 2^31 - 2 states), so their entries match nothing, also once settled (code id + 1 keeps the pending bit clear).
+__global__ __launch_bounds__(kBlock) void k_forget_winners(const u32* __restrict__ list, u64 kept, u64 winners, u32* __restrict__ id_of)
+{
+    for (u64 w = kept + static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x; w < winners; w += static_cast<u64>(gridDim.x) * kBlock)
+        id_of[list[w]] = 0x7FFFFFFEu;
+}
+
+__global__ void k_set_size(u64* __restrict__ size, u64 v) { *size = v; }
+
 __global__ __launch_bounds__(kBlock) void k_fill_u32(u32* __restrict__ p, u64 n, u32 v)
 {
     for (u64 i = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += static_cast<u64>(gridDim.x) * kBlock)
@@ -391,6 +401,16 @@ void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
     launch_winner_list(s.flags, n, s.scan_scratch, state_set_size_next(s), state_set_size_now(s), s.list,
                        s.id_of + static_cast<u64>(s.v.epoch) * s.batch_cap, is_new, stream);
     launch_check("state set rank");
+}
+
+void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t stream)
+{
+    if (winners > kept)
+        hipLaunchKernelGGL(k_forget_winners, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(winners - kept, kBlock), 4096))), dim3(kBlock),
+                           0, stream, s.list, kept, winners, s.id_of + static_cast<u64>(s.v.epoch) * s.batch_cap);
+    hipLaunchKernelGGL(k_set_size, dim3(1), dim3(1), 0, stream, state_set_size_now(s), size);
+    launch_check("state set cut");
+    s.size = size;
 }
 
 void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked)

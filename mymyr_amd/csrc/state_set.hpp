@@ -76,6 +76,11 @@ inline void state_set_flip(StateSet& s) { s.cur ^= 1; }
 /// epoch of id_of, is_new[j] (optional) the flags, and next size = size + winners.
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new = nullptr);
 
+/// A cut inside the last ranked batch whose search goes on (a BrFS layer cut by max_next_layer_states): of its
+/// `winners` winners only the first `kept` are stored, so the set's size becomes `size` and the table entries of the
+/// others (pending codes of the batch's epoch) stand for no state from now on (their epoch ids point past the arena).
+void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t stream);
+
 /// The probe of a batch begun with state_set_begin_batch over candidate rows [m, words] (device) that the caller produced:
 /// a stored equal row drops a candidate, equal candidates keep the smallest index, the others take pending entries
 /// (the losers' flags are cleared). state_set_rank and the caller's compaction follow. With `blocked`, a candidate equal

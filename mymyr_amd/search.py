@@ -168,6 +168,63 @@ class _ObserverBridge:
             _lib.ON_END(guard(on_end)) if ev["on_end"] else _lib.ON_END())
 
 
+_LAYER_KINDS = {"queue": 0, "in_order": 1, "reverse": 2, "randomized": 3, "goal_count": 4}
+_BEAM_NOVELTY = {"all_tested": 0, "survivors_only": 1, "relaxed_survivors_only": 2}
+
+
+class _Layers:
+    """BrfsOptions::layers from search.brfs's arguments (python/src/search_bindings.cpp:1638-1680): the kind, the
+    limits (None: none; 0 is refused, as the reference's check_layers refuses it) and, for a scorer, the C callback
+    that hands it the layer's rows; the first exception the scorer raises is raised when the search returns."""
+
+    def __init__(self, order, seed, max_next, prefer_more, beam_width, novelty, randomize_ties, beam_chunk):
+        self.error: BaseException | None = None
+        self.c_scorer = _lib.LAYER_SCORER()
+        if isinstance(order, str):
+            if order not in _LAYER_KINDS:
+                raise ValueError("mymyr: layer_order must be 'queue', 'in_order', 'reverse', 'randomized', 'goal_count' or an "
+                                 "evaluator (scores, lower first)")
+            self.kind = _LAYER_KINDS[order]
+        else:
+            score = getattr(order, "evaluate_batch", order)
+            if not callable(score):
+                raise TypeError("mymyr_amd: layer_order must be a kind name or a scorer")
+            self.kind = 5
+
+            def call(_u, rows, n, words, out):
+                if self.error is not None:
+                    for i in range(n):
+                        out[i] = float("nan")
+                    return
+                try:
+                    states = np.ctypeslib.as_array(rows, shape=(n, words)).copy() if n else np.zeros((0, words), np.uint64)
+                    v = np.asarray(score(states), dtype=np.float64).reshape(-1)
+                    if v.size != n:
+                        raise ValueError(f"mymyr_amd: the layer scorer returned {v.size} scores for {n} states")
+                    for i in range(n):
+                        out[i] = float(v[i])
+                except BaseException as e:  # noqa: BLE001 - raised when the search returns
+                    self.error = e
+                    for i in range(n):
+                        out[i] = float("nan")
+
+            self.c_scorer = _lib.LAYER_SCORER(call)
+        if not 0 <= int(seed) < (1 << 64):
+            raise ValueError("mymyr: seed must be a 64-bit unsigned integer")
+        self.seed = int(seed)
+        for name, v in (("max_next_layer_states", max_next), ("beam_width", beam_width)):
+            if v is not None and not 0 < int(v) < (1 << 32) - 1:
+                raise ValueError(f"mymyr brfs: {name} must be positive" if v is not None and int(v) <= 0 else
+                                 f"mymyr: {name} must be below 2^32 - 1")
+        self.limit = 0 if max_next is None else int(max_next)
+        self.beam = 0 if beam_width is None else int(beam_width)
+        if novelty not in _BEAM_NOVELTY:
+            raise ValueError("mymyr: beam_novelty must be 'all_tested', 'survivors_only' or 'relaxed_survivors_only'")
+        self.novelty = _BEAM_NOVELTY[novelty]
+        if int(beam_chunk) <= 0:
+            raise ValueError("mymyr brfs: beam_chunk must be positive")
+
+
 @dataclass
 class BrfsResult:
     """The fields of the reference's BrfsResult (include/mymyr/search/brfs.hpp:103-138) that the device search fills.
@@ -257,7 +314,9 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
          witness_pruning: bool = True, stop_at_goal: bool = True, fingerprint: bool = False, layer_stats: bool = True,
          chunk: int = 0, memory_states: int = 0, timings: bool = False, start=None, blocked_states=None,
          max_seconds: float | None = None, cancel: CancelToken | None = None, goal=None, observer=None,
-         progress_interval: int | None = None) -> BrfsResult:
+         progress_interval: int | None = None, layer_order="queue", seed: int = 0, max_next_layer_states: int | None = None,
+         prefer_more_satisfied_goals: bool = True, beam_width: int | None = None, beam_novelty: str = "all_tested",
+         randomize_ties: bool = False, beam_chunk: int = 1024) -> BrfsResult:
     """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
     (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer.
 
@@ -270,7 +329,12 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     reference's goal= with GroundConditions, python/src/search_bindings.cpp:439-505; conditions that can never hold are
     left out).
     observer (an :class:`Observer`, or any object with some of its methods) and progress_interval (expansions between
-    on_progress calls; None: 2^16): BrfsOptions::observer and progress_interval (include/mymyr/search/brfs.hpp:99-100)."""
+    on_progress calls; None: 2^16): BrfsOptions::observer and progress_interval (include/mymyr/search/brfs.hpp:99-100).
+    layer_order, seed, max_next_layer_states, prefer_more_satisfied_goals, beam_width, beam_novelty, randomize_ties and
+    beam_chunk: BrfsOptions::layers (include/mymyr/search/layer_ordering.hpp; python/src/search_bindings.cpp:1638-1680,
+    2206-2233): 'queue' (the default), 'in_order', 'reverse', 'randomized', 'goal_count', or a scorer (a callable
+    taking the layer's states [n, words] uint64 and returning n scores, lower first, or an object with evaluate_batch);
+    'relaxed_survivors_only' is refused by the device search."""
     if max_seconds is not None and not max_seconds >= 0:
         raise ValueError("mymyr_amd: brfs: max_seconds must be >= 0")
     if cancel is not None and not isinstance(cancel, CancelToken):
@@ -285,6 +349,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     if progress_interval is not None and not 0 <= int(progress_interval) < (1 << 64):
         raise ValueError("mymyr_amd: brfs: progress_interval must be a non-negative 64-bit count")
     bridge = _ObserverBridge(observer, (1 << 16) if progress_interval is None else int(progress_interval)) if observer is not None else None
+    lay = _Layers(layer_order, seed, max_next_layer_states, prefer_more_satisfied_goals, beam_width, beam_novelty, randomize_ties,
+                  beam_chunk)
     if bridge is not None and not bridge.defines_any:
         bridge = None  # an observer that defines no event is not installed
     o = _lib.BrfsOptions(UNBOUNDED32 if max_depth is None else max_depth, int(witness_pruning),
@@ -294,7 +360,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
                          0 if bl is None else bl.shape[0], task.words, int(timed), float(max_seconds) if timed else 0.0,
                          None if cancel is None else cancel.address, 0 if goal is None else 1, 0 if goal is None else len(go) - 1,
                          None if go is None else go.ctypes.data, None if gl is None or gl.size == 0 else gl.ctypes.data,
-                         None if bridge is None else ctypes.addressof(bridge.c), 1)
+                         None if bridge is None else ctypes.addressof(bridge.c), 1, lay.kind, int(not prefer_more_satisfied_goals),
+                         lay.seed, lay.limit, lay.beam, int(bool(randomize_ties)), lay.novelty, lay.c_scorer, None)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -305,6 +372,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     gs = np.zeros(max(1, task.words if task.frozen else (task.dense_fluent + 63) // 64), np.uint64)
     plan = _lib.BrfsPlan(ps.ctypes.data, pb.ctypes.data, cap, L, gs.ctypes.data, gs.size, 0, 0, 0, 0.0)
     n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ctypes.byref(plan))
+    if lay.error is not None:
+        raise lay.error
     if n < 0:
         check(-1)
     if bridge is not None and bridge.error is not None:

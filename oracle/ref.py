@@ -53,7 +53,20 @@ class BrfsOptions(Structure):
         ("goal_count", c_uint32),
         ("goal_offsets", c_void_p),
         ("goal_literals", c_void_p),
+        ("layer_kind", c_int32),
+        ("prefer_fewer", c_int32),
+        ("layer_seed", c_uint64),
+        ("max_next_layer_states", c_uint32),
+        ("beam_width", c_uint32),
+        ("randomize_ties", c_int32),
+        ("reserved2", c_int32),
+        ("scorer", ctypes.CFUNCTYPE(None, c_void_p, ctypes.POINTER(c_uint64), c_uint64, c_uint32, ctypes.POINTER(ctypes.c_double))),
+        ("scorer_user", c_void_p),
     ]
+
+
+SCORER = BrfsOptions._fields_[-2][1]
+LAYER_KINDS = {"queue": 0, "in_order": 1, "reverse": 2, "randomized": 3, "goal_count": 4}
 
 
 def goal_records(goal) -> tuple[np.ndarray, np.ndarray]:
@@ -451,7 +464,8 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
          stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf"),
-         goal=None):
+         goal=None, layer_order="queue", seed=0, max_next_layer_states=None, prefer_more_satisfied_goals=True, beam_width=None,
+         randomize_ties=False):
     """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
     (schema, binding) pairs, the goal state's words and the cost; the result's words, fluent_slots, threads_used, store
     and message. start [words] and blocked_states [k, words] are rows of the task's table words; goal (None: the task's)
@@ -460,9 +474,21 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
     st = None if start is None else np.ascontiguousarray(np.asarray(start, np.uint64).reshape(-1)[:W])
     bl = None if blocked_states is None else np.ascontiguousarray(np.asarray(blocked_states, np.uint64).reshape(-1, W))
     go, gl = goal_records(goal) if goal is not None else (None, None)
+    if callable(layer_order):
+        score = layer_order
+
+        def call(_u, rows, n, words, out):
+            v = np.asarray(score(np.ctypeslib.as_array(rows, shape=(n, words)).copy()), np.float64).reshape(-1)
+            for i in range(n):
+                out[i] = float(v[i])
+
+        kind, cb = 5, SCORER(call)
+    else:
+        kind, cb = LAYER_KINDS[layer_order], SCORER()
     o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
                     max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds,
-                    0 if goal is None else 1, 0 if goal is None else len(goal), _p(go), _p(gl))
+                    0 if goal is None else 1, 0 if goal is None else len(goal), _p(go), _p(gl), kind, int(not prefer_more_satisfied_goals),
+                    seed, max_next_layer_states or 0, beam_width or 0, int(randomize_ties), 0, cb, None)
     r = BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)

@@ -119,6 +119,17 @@ struct mref_brfs_options
     uint32_t goal_count;
     const uint32_t* goal_offsets;
     const int32_t* goal_literals;
+    // BrfsOptions::layers: kind (LayerOrdering::Kind order), seed, max_next_layer_states / beam_width (0: none),
+    // prefer_fewer (prefer_more_satisfied_goals false), randomize_ties, and for the scored kind a scorer over host rows
+    int32_t layer_kind;
+    int32_t prefer_fewer;
+    uint64_t layer_seed;
+    uint32_t max_next_layer_states;
+    uint32_t beam_width;
+    int32_t randomize_ties;
+    int32_t reserved2;
+    void (*scorer)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, double* scores);
+    void* scorer_user;
 };
 
 struct mref_brfs_result
@@ -763,6 +774,30 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
             b.stop_at_goal = o->stop_at_goal != 0;
             b.fingerprint = o->fingerprint != 0;
             b.layer_stats = true;
+            b.layers.kind = static_cast<search::LayerOrdering::Kind>(o->layer_kind);
+            b.layers.seed = o->layer_seed;
+            if (o->max_next_layer_states)
+                b.layers.max_next_layer_states = o->max_next_layer_states;
+            if (o->beam_width)
+                b.layers.beam_width = o->beam_width;
+            b.layers.prefer_more_satisfied_goals = o->prefer_fewer == 0;
+            b.layers.randomize_ties = o->randomize_ties != 0;
+            if (o->scorer)
+            {
+                // the views' rows padded to a common width for the callback
+                auto fn = o->scorer;
+                void* user = o->scorer_user;
+                b.layers.scorer = [fn, user](std::span<const StateView> states, std::span<f64> scores)
+                {
+                    u32 w = 1;
+                    for (const StateView& v : states)
+                        w = std::max(w, v.nw);
+                    std::vector<u64> rows(states.size() * w, 0);
+                    for (usize i = 0; i < states.size(); ++i)
+                        std::copy(states[i].w, states[i].w + states[i].nw, rows.begin() + static_cast<std::ptrdiff_t>(i * w));
+                    fn(user, rows.data(), states.size(), w, scores.data());
+                };
+            }
             const auto t0 = std::chrono::steady_clock::now();
             const BrfsResult x = brfs(*t->task, b);
             r->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();

@@ -41,6 +41,13 @@ CE_TASKS = ["miconic-simpleadl__s10-2", "caldera-split-opt18-adl__p04"]
 # parameters; its BrFS is pinned in brfs_witness.json)
 LAYOUT_ONLY = ["rovers__p02"]
 
+# layer scorers of the scored-layer fixtures (brfs_layers.json), by name; the tests pass the same functions to the
+# device search. They depend on the number of set atoms only, so they score a state alike under every slot numbering.
+LAYER_SCORERS = {
+    "popcount": lambda rows: [sum(bin(int(w)).count("1") for w in r) for r in rows],
+    "neg_popcount_mod3": lambda rows: [-(sum(bin(int(w)).count("1") for w in r) % 3) for r in rows],
+}
+
 # the reference's own determinism digests of search.brfs(max_states=20000, fingerprint=True, stop_at_goal=False):
 # sha256(json.dumps([states, expanded, generated, layers, fingerprint], sort_keys=True))[:16]
 # (tests/data/determinism.json, tests/python/test_determinism.py:63-104)

@@ -634,6 +634,53 @@ def make_brfs_suite_add():
     dump("brfs.json", out)
 
 
+LAYER_CASES = [
+    ("gripper__prob05", "auto", dict(layer_order="in_order", beam_width=50)),
+    ("gripper__prob05", "auto", dict(layer_order="reverse")),
+    ("gripper__prob05", "auto", dict(layer_order="randomized", seed=5)),
+    ("gripper__prob05", "auto", dict(layer_order="randomized", seed=5, stop_at_goal=True)),
+    ("gripper__prob05", "auto", dict(layer_order="goal_count")),
+    ("gripper__prob05", "auto", dict(layer_order="goal_count", prefer_more_satisfied_goals=False, randomize_ties=True, seed=11,
+                                     beam_width=100)),
+    ("gripper__prob05", "auto", dict(layer_order="in_order", max_next_layer_states=300)),
+    ("gripper__prob05", "auto", dict(layer_order="randomized", seed=9, max_next_layer_states=1000, stop_at_goal=True)),
+    ("gripper__prob05", "auto", dict(layer_order="popcount", beam_width=40)),
+    ("blocks__probBLOCKS-8-0", "auto", dict(layer_order="goal_count", beam_width=200, stop_at_goal=True)),
+    ("blocks__probBLOCKS-8-0", "auto", dict(layer_order="reverse", max_states=20000)),
+    ("blocks__probBLOCKS-8-0", "auto", dict(layer_order="neg_popcount_mod3", randomize_ties=True, seed=2, max_next_layer_states=5000)),
+    ("logistics00__probLOGISTICS-6-1", "auto", dict(layer_order="goal_count", beam_width=1000, stop_at_goal=True)),
+    ("depot__p02", "auto", dict(layer_order="goal_count", randomize_ties=True, seed=4, max_next_layer_states=2000, max_expanded=30000)),
+    ("transport_w20_3", "auto", dict(layer_order="goal_count", beam_width=64, stop_at_goal=True)),
+    ("transport_w20_3", "auto", dict(layer_order="randomized", seed=3, max_next_layer_states=2000, max_depth=6)),
+    ("transport_w20_3", "auto", dict(layer_order="reverse", max_depth=4)),
+    ("blocks__probBLOCKS-8-0", "lazy", dict(layer_order="goal_count", beam_width=200, stop_at_goal=True)),
+    ("gripper__prob05", "lazy", dict(layer_order="randomized", seed=7, max_next_layer_states=800)),
+]
+
+
+def make_brfs_layers():
+    """The reference brfs() under BrfsOptions::layers (ordered layers, randomized orders, goal-count and scored ranks,
+    beams and max_next_layer_states) on ground, wide-row and lazy tasks: counts, layer counts, fingerprints, plans."""
+    out = {}
+    for name, atoms, kw in LAYER_CASES:
+        opts = dict(kw)
+        opts.setdefault("stop_at_goal", False)
+        ref_kw = dict(opts)
+        if ref_kw["layer_order"] in fx.LAYER_SCORERS:
+            ref_kw["layer_order"] = fx.LAYER_SCORERS[ref_kw["layer_order"]]
+        t = ref.RefTask(fx.task_path(name), atoms)
+        r = ref.brfs(t, witness_pruning=atoms != "lazy", **ref_kw)
+        r.pop("seconds")
+        if atoms == "lazy" and r["solved"]:
+            r["goal_cids"] = goal_cids(t, r["goal_state"])
+        r["options"] = opts
+        r["atoms"] = atoms
+        key = f"{name}:{atoms}:" + ",".join(f"{k}={v}" for k, v in sorted(opts.items()))
+        out[key] = r
+        print(key, r["states"], r["expanded"], r["status"], flush=True)
+    dump("brfs_layers.json", out)
+
+
 LAZY_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "pegsol-08-strips__p22", "visitall__visitall_x-6_y-3_r-100",
               "miconic__s7-4", "logistics00__probLOGISTICS-6-1", "driverlog__p03", "rovers__p02"]
 
@@ -696,7 +743,7 @@ def main():
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
-             "brfs_suite_add": make_brfs_suite_add}
+             "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -420,3 +420,71 @@ def test_observer_events(golden):
 
     with pytest.raises(ValueError, match="on_generate"):
         search.brfs(t, observer=PerState())
+
+
+@pytest.mark.parametrize("key", list(__import__("json").load(open(__import__("os").path.join(
+    __import__("os").path.dirname(__file__), "golden", "brfs_layers.json")))))
+def test_layer_orders(golden, key):
+    """BrfsOptions::layers (include/mymyr/search/layer_ordering.hpp; src/mymyr/search/brfs.cpp:300-382 with
+    layer_order_detail.hpp): in-order, reverse and SplitMix64-randomized layers, goal-count ranks (most or fewest
+    satisfied first, random tie tokens) and scored ranks, beams and max_next_layer_states cuts, over ground, wide-row
+    and lazy tasks: counts, layer counts, fingerprints, statuses and plans equal to the compiled reference's."""
+    from mymyr_amd.task import Task
+
+    exp = golden.load("brfs_layers.json")[key]
+    name = key.split(":")[0]
+    kw = dict(exp["options"])
+    if kw["layer_order"] in golden.LAYER_SCORERS:
+        kw["layer_order"] = golden.LAYER_SCORERS[kw["layer_order"]]
+    print(f"layers: {key}", flush=True)
+    if exp["atoms"] != "lazy":
+        r = device(golden, name, exp["atoms"], full=True, **kw)
+        assert not same(r, exp), same(r, exp)
+        assert same_plan(r, exp)
+        return
+    # lazy slots: the plan and the goal state's atoms by canonical id (the slots the search interned are the task's)
+    from mymyr_amd import search
+
+    t = Task.from_text_file(golden.task_path(name), "lazy")
+    res = search.brfs(t, fingerprint=True, witness_pruning=False, **kw)
+    r = {"states": res.states, "expanded": res.expanded, "generated": res.generated, "goal_states": res.num_goal_states,
+         "layers": res.layers, "fingerprint": res.fingerprint, "status": res.status, "layer_counts": res.layer_counts,
+         "exhausted": res.exhausted, "solved": res.solved}
+    assert not same(r, exp), same(r, exp)
+    assert [[a.schema, *a.binding] for a in res.plan] == exp.get("plan", [])
+    if exp["solved"]:
+        assert goal_cids(t, res.goal_state) == exp["goal_cids"]
+
+
+def test_layer_order_errors(golden):
+    """The reference's check_layers messages (include/mymyr/search/layer_ordering.hpp:117-134) and the device's refusal of
+    the relaxed survivors-only beam."""
+    from mymyr_amd import search
+    from mymyr_amd._lib import MyaError
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("gripper__prob05"))
+    for kw, msg in [(dict(max_next_layer_states=10), "needs an ordered layer order"),
+                    (dict(beam_width=10), "needs an ordered layer order"),
+                    (dict(layer_order="in_order", beam_width=10, max_next_layer_states=10), "exclude each other"),
+                    (dict(layer_order="in_order", beam_novelty="survivors_only"), "needs a beam"),
+                    (dict(layer_order="reverse", randomize_ties=True), "randomize_ties needs"),
+                    (dict(layer_order="in_order", beam_width=5, beam_novelty="relaxed_survivors_only"), "needs the goal-count"),
+                    (dict(layer_order="goal_count", beam_width=5, beam_novelty="relaxed_survivors_only"), "not supported")]:
+        with pytest.raises(MyaError, match=msg):
+            search.brfs(t, **kw)
+    for kw in (dict(layer_order="sideways"), dict(layer_order="in_order", beam_width=0),
+               dict(layer_order="in_order", max_next_layer_states=0), dict(beam_novelty="none")):
+        with pytest.raises(ValueError):
+            search.brfs(t, **kw)
+    with pytest.raises(MyaError, match="NaN"):
+        search.brfs(t, stop_at_goal=False, layer_order=lambda rows: [float("nan")] * len(rows))
+
+    class Fail(RuntimeError):
+        pass
+
+    def bad(rows):
+        raise Fail("scorer")
+
+    with pytest.raises(Fail):
+        search.brfs(t, stop_at_goal=False, layer_order=bad)
