@@ -316,7 +316,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
          max_seconds: float | None = None, cancel: CancelToken | None = None, goal=None, observer=None,
          progress_interval: int | None = None, layer_order="queue", seed: int = 0, max_next_layer_states: int | None = None,
          prefer_more_satisfied_goals: bool = True, beam_width: int | None = None, beam_novelty: str = "all_tested",
-         randomize_ties: bool = False, beam_chunk: int = 1024) -> BrfsResult:
+         randomize_ties: bool = False, beam_chunk: int = 1024, threads: int = 1, store: str = "auto", canonical_order: bool = True,
+         deterministic_ids: bool = True) -> BrfsResult:
     """Breadth-first search on the current HIP device. Defaults follow the reference's BrfsOptions
     (witness_pruning and stop_at_goal on). layer_counts holds [expanded, generated, new] per expanded layer.
 
@@ -334,9 +335,19 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     beam_chunk: BrfsOptions::layers (include/mymyr/search/layer_ordering.hpp; python/src/search_bindings.cpp:1638-1680,
     2206-2233): 'queue' (the default), 'in_order', 'reverse', 'randomized', 'goal_count', or a scorer (a callable
     taking the layer's states [n, words] uint64 and returning n scores, lower first, or an object with evaluate_batch);
-    'relaxed_survivors_only' is refused by the device search."""
+    'relaxed_survivors_only' is refused by the device search.
+    threads, store and deterministic_ids are the reference's host-side choices (python/src/search_bindings.cpp:3396-3398):
+    they are checked and the device state set is used (its ids are the single-threaded search's, which every thread
+    count of the reference's deterministic search gives); canonical_order=False (the matcher's own order) is refused."""
     if max_seconds is not None and not max_seconds >= 0:
         raise ValueError("mymyr_amd: brfs: max_seconds must be >= 0")
+    if store not in ("auto", "flat", "chunked", "compact", "concurrent"):
+        raise ValueError("mymyr: store must be 'auto', 'flat', 'chunked', 'compact' or 'concurrent'")
+    if int(threads) < 0:
+        raise ValueError("mymyr: threads must be >= 0")
+    if not canonical_order:
+        raise ValueError("mymyr_amd: brfs: the device search generates successors in canonical order only "
+                         "(canonical_order=False is not supported)")
     if cancel is not None and not isinstance(cancel, CancelToken):
         raise TypeError("mymyr_amd: cancel must be a mymyr_amd.search.CancelToken")
     st = None if start is None else _rows(task, start, "start")
