@@ -45,10 +45,10 @@ void wide_shape(u32 W, F&& f)
         f.template operator()<64, 4>();
     else if (W <= 1024)
         f.template operator()<64, 8>();
-    else if (W <= 2048)
+    else if (W <= kLongRowWords)
         f.template operator()<64, 16>();
     else
-        throw std::invalid_argument("mymyr_amd: brfs: states of more than 2048 words");
+        f.template operator()<64, 0>();  // long rows: copied from memory by a 64-lane group
 }
 
 // The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena:

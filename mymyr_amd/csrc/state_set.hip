@@ -243,10 +243,10 @@ void with_shape(u32 W, F&& f)
         f.template operator()<64, 4>();
     else if (W <= 1024)
         f.template operator()<64, 8>();
-    else if (W <= 2048)
+    else if (W <= kLongRowWords)
         f.template operator()<64, 16>();
     else
-        throw std::invalid_argument("mymyr_amd: state set rows hold at most 2048 words");
+        f.template operator()<64, 0>();  // long rows: compared, hashed and copied from memory by a 64-lane group
 }
 
 /// The lane-group shape of the compaction: the probe's, except that rows of 9-16 words are copied by eight lanes of
@@ -313,8 +313,6 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
 {
     if (words == 0)
         throw std::invalid_argument("mymyr_amd: state set rows need at least one word");
-    if (words > 2048)
-        throw std::invalid_argument("mymyr_amd: state set rows hold at most 2048 words");
     if (!(max_load > 0.0 && max_load <= 0.95))
         throw std::invalid_argument("mymyr_amd: state set load must be in (0, 0.95]");
     if (max_states >= (u64{1} << 31) - 1)

@@ -74,24 +74,42 @@ struct Slice
     u64 lo[K], hi[K];  // pair k * G + q: words 2p (lo) and 2p + 1 (hi)
 };
 
+/// Rows above kLongRowWords words (K = 0) stay in memory: the slice is the row's address, and the group's lanes stride
+/// over its word pairs wherever the row is compared, hashed or copied (lane q: pairs q, q + G, ...).
+constexpr u32 kLongRowWords = 2048;
+template<int G>
+struct Slice<G, 0>
+{
+    const u64* row;
+    u32 W;
+};
+
 /// Lane q's words of a row of W words (zeros past W).
 template<int G, int K>
 __device__ __forceinline__ void load_row(const u64* __restrict__ row, u32 W, u32 q, Slice<G, K>& s)
 {
-#pragma unroll
-    for (int k = 0; k < K; ++k)
+    if constexpr (K == 0)
     {
-        const u32 w = 2 * (k * G + q);
-        if (w + 1 < W && (W & 1) == 0)
+        s.row = row;
+        s.W = W;
+    }
+    else
+    {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
         {
-            const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(row + w);
-            s.lo[k] = v.x;
-            s.hi[k] = v.y;
-        }
-        else
-        {
-            s.lo[k] = w < W ? row[w] : 0;
-            s.hi[k] = w + 1 < W ? row[w + 1] : 0;
+            const u32 w = 2 * (k * G + q);
+            if (w + 1 < W && (W & 1) == 0)
+            {
+                const ulonglong2 v = *reinterpret_cast<const ulonglong2*>(row + w);
+                s.lo[k] = v.x;
+                s.hi[k] = v.y;
+            }
+            else
+            {
+                s.lo[k] = w < W ? row[w] : 0;
+                s.hi[k] = w + 1 < W ? row[w + 1] : 0;
+            }
         }
     }
 }
@@ -99,18 +117,29 @@ __device__ __forceinline__ void load_row(const u64* __restrict__ row, u32 W, u32
 template<int G, int K>
 __device__ __forceinline__ void store_row(u64* __restrict__ row, u32 W, u32 q, const Slice<G, K>& s)
 {
-#pragma unroll
-    for (int k = 0; k < K; ++k)
+    if constexpr (K == 0)
     {
-        const u32 w = 2 * (k * G + q);
-        if (w + 1 < W && (W & 1) == 0)
-            *reinterpret_cast<ulonglong2*>(row + w) = ulonglong2{s.lo[k], s.hi[k]};
-        else
+        // W (even for these widths: multiples of 64 words) copied pair by pair across the group
+        for (u32 w = 2 * q; w + 1 < W; w += 2 * G)
+            *reinterpret_cast<ulonglong2*>(row + w) = *reinterpret_cast<const ulonglong2*>(s.row + w);
+        if ((W & 1) && q == 0)
+            row[W - 1] = s.row[W - 1];
+    }
+    else
+    {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
         {
-            if (w < W)
-                row[w] = s.lo[k];
-            if (w + 1 < W)
-                row[w + 1] = s.hi[k];
+            const u32 w = 2 * (k * G + q);
+            if (w + 1 < W && (W & 1) == 0)
+                *reinterpret_cast<ulonglong2*>(row + w) = ulonglong2{s.lo[k], s.hi[k]};
+            else
+            {
+                if (w < W)
+                    row[w] = s.lo[k];
+                if (w + 1 < W)
+                    row[w + 1] = s.hi[k];
+            }
         }
     }
 }
@@ -152,9 +181,18 @@ template<int G, int K>
 __device__ __forceinline__ bool group_equal(const Slice<G, K>& a, const Slice<G, K>& b, u32 gbase)
 {
     bool eq = true;
+    if constexpr (K == 0)
+    {
+        const u32 q = lane_id() - gbase;
+        for (u32 w = 2 * q; w < a.W && eq; w += 2 * G)
+            eq = a.row[w] == b.row[w] && (w + 1 >= a.W || a.row[w + 1] == b.row[w + 1]);
+    }
+    else
+    {
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-        eq = eq && a.lo[k] == b.lo[k] && a.hi[k] == b.hi[k];
+        for (int k = 0; k < K; ++k)
+            eq = eq && a.lo[k] == b.lo[k] && a.hi[k] == b.hi[k];
+    }
     return group_all<G>(eq, gbase);
 }
 
@@ -162,30 +200,41 @@ __device__ __forceinline__ bool group_equal(const Slice<G, K>& a, const Slice<G,
 template<int G, int K>
 __device__ __forceinline__ u64 group_hash(const Slice<G, K>& s, u32 q, u32 gbase)
 {
-    u32 top = 0;  // 1 + index of the lane's highest nonzero word
-#pragma unroll
-    for (int k = 0; k < K; ++k)
+    if constexpr (K == 0)
     {
-        const u32 w = 2 * (k * G + q);
-        if (s.hi[k])
-            top = w + 2;
-        else if (s.lo[k])
-            top = w + 1;
+        // the serial chain of hash_state over the trimmed words, on the group's first lane
+        u64 h = 0;
+        if (q == 0)
+            h = hash_state(s.row, s.W);
+        return group_bcast<G>(h, gbase, 0);
     }
-    const u32 n = group_max<G>(top);
-    u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
+    else
+    {
+        u32 top = 0;  // 1 + index of the lane's highest nonzero word
 #pragma unroll
-    for (int k = 0; k < K; ++k)
-#pragma unroll
-        for (int r = 0; r < G; ++r)
+        for (int k = 0; k < K; ++k)
         {
-            const u32 p = k * G + r;
-            const u64 a = group_bcast<G>(s.lo[k], gbase, r);
-            const u64 b = group_bcast<G>(s.hi[k], gbase, r);
-            if (2 * p < n)
-                h = mulfold(h ^ a ^ kHashP1, b ^ kHashP2);
+            const u32 w = 2 * (k * G + q);
+            if (s.hi[k])
+                top = w + 2;
+            else if (s.lo[k])
+                top = w + 1;
         }
-    return mix64(h);
+        const u32 n = group_max<G>(top);
+        u64 h = kHashSeed ^ (static_cast<u64>(n) * kHashP1);
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+#pragma unroll
+            for (int r = 0; r < G; ++r)
+            {
+                const u32 p = k * G + r;
+                const u64 a = group_bcast<G>(s.lo[k], gbase, r);
+                const u64 b = group_bcast<G>(s.hi[k], gbase, r);
+                if (2 * p < n)
+                    h = mulfold(h ^ a ^ kHashP1, b ^ kHashP2);
+            }
+        return mix64(h);
+    }
 }
 
 /// Rows wider than this many words are placed in the table by set_hash_wide instead of hash_state.
@@ -222,7 +271,16 @@ __device__ __forceinline__ u64 group_sum64(u64 v)
 template<int G, int K>
 __device__ __forceinline__ u64 group_set_hash(const Slice<G, K>& s, u32 q, u32 gbase)
 {
-    if constexpr (G * K * 2 > kWideHashWords)
+    if constexpr (K == 0)
+    {
+        // set_hash_wide with the lanes striding over the row's words
+        u64 acc = 0;
+        for (u32 w = q; w < s.W; w += G)
+            if (const u64 v = s.row[w])
+                acc += mix64(v + static_cast<u64>(w + 1) * 0x9E3779B97F4A7C15ull);
+        return mix64(group_sum64<G>(acc) ^ kHashSeed);
+    }
+    else if constexpr (G * K * 2 > kWideHashWords)
     {
         u64 acc = 0;
 #pragma unroll

@@ -341,6 +341,23 @@ def make_brfs_witness():
 
 WIDE_TASKS = {"transport_w20_3": dict(locations=20, trucks=4, packages=50, goals=1, seed=3),
               "transport_w20_7": dict(locations=20, trucks=4, packages=50, goals=1, seed=7)}
+# a transport task of 2208-word rows (141,312 atoms), past the 2048 words the state set keeps in registers
+LONG_TASKS = {"transport_w2208": dict(locations=128, trucks=48, packages=768, goals=32, seed=5)}
+
+
+def make_brfs_long():
+    """BrFS over rows of more than 2048 words (the state set's long-row shape): the 2208-word transport task to a
+    depth bound, a max_states cut and a goal-count beam."""
+    for name, kw in LONG_TASKS.items():
+        with open(fx.task_path(name), "w") as f:
+            f.write(gen.transport(**kw))
+    out = {"transport_w2208:depth2": brfs_record("transport_w2208", stop_at_goal=False, max_depth=2),
+           "transport_w2208:cut": brfs_record("transport_w2208", stop_at_goal=False, max_states=30000),
+           "transport_w2208:beam": brfs_record("transport_w2208", stop_at_goal=False, max_depth=8, layer_order="goal_count",
+                                               beam_width=64)}
+    for k, v in out.items():
+        print(k, v["states"], v["expanded"], v["status"], flush=True)
+    dump("brfs_long.json", out)
 
 
 def make_brfs_wide():
@@ -743,7 +760,7 @@ def main():
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
-             "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers}
+             "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -488,3 +488,14 @@ def test_layer_order_errors(golden):
 
     with pytest.raises(Fail):
         search.brfs(t, stop_at_goal=False, layer_order=bad)
+
+
+@pytest.mark.parametrize("key", ["transport_w2208:depth2", "transport_w2208:cut", "transport_w2208:beam"])
+def test_rows_beyond_2048_words(golden, key):
+    """A transport task of 2208-word rows (141,312 atoms), past the rows the state set keeps in registers: the lifted
+    driver's probe, compaction and blocked test compare, hash and copy them from memory (the reference's set takes any
+    width, cuda/src/state_set.cu:456-464). Counts, layer counts, fingerprints and statuses equal the reference's."""
+    exp = golden.load("brfs_long.json")[key]
+    print(f"long rows: {key}", flush=True)
+    r = device(golden, "transport_w2208", **exp["options"])
+    assert not same(r, exp), same(r, exp)

@@ -36,7 +36,7 @@ def test_hash_rows_random_vs_oracle():
     from oracle import port
 
     rng = np.random.default_rng(1)
-    for words in (1, 3, 8, 13, 16, 176):
+    for words in (1, 3, 8, 13, 16, 176, 2049, 3000):
         rows = rng.integers(0, 2**63, size=(257, words), dtype=np.int64).view(np.uint64)
         rows[::4, words // 2:] = 0
         rows[7] = 0
@@ -143,3 +143,29 @@ def test_state_set_errors():
         s.insert(torch.arange(64, dtype=torch.int64, device="cuda").view(16, 4))
     with pytest.raises(MyaError, match="load"):
         hip.StateSet(10, 4, 1.5)
+
+
+@pytest.mark.parametrize("words", [2049, 3000])
+def test_state_set_rows_beyond_2048_words(words):
+    """Rows wider than 2048 words stay in memory (a 64-lane group compares, hashes and copies them): ids, unique count and
+    stored rows equal the oracle's first occurrences over several batches, and rows that differ only in their last
+    or a middle word stay apart."""
+    from mymyr_amd import gen, hip
+    from oracle import port
+
+    rows = gen.dedup_rows(0, 3000, words, seed=8)
+    a = rows[0].copy()
+    b = a.copy()
+    b[-1] ^= 1
+    c = a.copy()
+    c[words // 2] ^= 1 << 63
+    rows = np.concatenate([rows, np.stack([a, b, a, c, b])])
+    s = hip.StateSet(4000, words, 0.5, batch=700)
+    n, ids, _ = s.insert(dev(rows))
+    exp_n, exp_ids = port.dedup_unique(rows)
+    assert n == exp_n == len(s)
+    assert np.array_equal(ids.cpu().numpy(), exp_ids)
+    got = ids.cpu().numpy()[-5:]
+    assert got[0] == got[2] and got[1] == got[4] and len({got[0], got[1], got[3]}) == 3
+    stored = torch.from_dlpack(s.rows()).cpu().numpy().view(np.uint64)
+    assert np.array_equal(stored, rows[np.unique(exp_ids, return_index=True)[1]])
