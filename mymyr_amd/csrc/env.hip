@@ -2860,10 +2860,10 @@ unsigned device_cus()
     return n;
 }
 
-/// The grid of a one-instance launch. `resident`: the blocks that are resident at once (LDS bytes `lds` and nw waves per
-/// block), each looping over rows, so that a block stages the hot tables once for many rows of equal work (env steps
-/// and counts); else one block per nw rows. A grouped launch keeps its cap.
-unsigned one_instance_grid(u64 rows, unsigned nw, bool group, size_t lds, bool resident = true)
+/// The grid of a one-instance launch. `resident`: `over` times the blocks that are resident at once (LDS bytes `lds` and
+/// nw waves per block), each looping over rows, so that a block stages the hot tables once for many rows (env steps and
+/// counts); else one block per nw rows. A grouped launch keeps its cap.
+unsigned one_instance_grid(u64 rows, unsigned nw, bool group, size_t lds, bool resident = true, unsigned over = 1)
 {
     constexpr u64 kGroupBlocks = 8192;
     constexpr size_t kCuLds = 160 * 1024;
@@ -2874,7 +2874,7 @@ unsigned one_instance_grid(u64 rows, unsigned nw, bool group, size_t lds, bool r
     if (!resident)
         return g;
     const unsigned per_cu = std::max<unsigned>(1, std::min<unsigned>(lds ? static_cast<unsigned>(kCuLds / lds) : kCuWaves, kCuWaves / nw));
-    return std::min<unsigned>(g, per_cu * device_cus());
+    return std::min<unsigned>(g, per_cu * device_cus() * over);
 }
 
 void launch_env_step(const EnvArgs& a, hipStream_t stream)
@@ -2898,7 +2898,10 @@ void launch_env_step(const EnvArgs& a, hipStream_t stream)
                               : variant(a.T, k_env_step<true, false, false, false>, k_env_step<true, true, false, false>,
                                         k_env_step<false, false, false, false>, k_env_step<false, true, false, false>);
     set_lds(reinterpret_cast<const void*>(fn), lds);
-    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group, lds)), dim3(nw * kWave), lds, stream, a);
+    // several resident grids' worth of blocks: a block whose rows take longer no longer holds the launch's end, the
+    // dispatcher hands its CU the next block (transport_xl, 262,144 envs: 24.2 ms per step on one resident grid, 15.7 ms
+    // on 16; transport's lane-split step is best at 4)
+    hipLaunchKernelGGL(fn, dim3(one_instance_grid(a.rows, nw, group, lds, true, levels(a.T) ? 16 : 4)), dim3(nw * kWave), lds, stream, a);
     launch_check("env step");
 }
 
