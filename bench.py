@@ -75,6 +75,17 @@ def load_traffic(kernel: str):
     return k.get("traffic_bytes_per_launch") if k else None
 
 
+def load_traffic_copy_scaled(kernel: str):
+    """The same kernel's traffic with every FETCH_SIZE byte scaled by the plain copy's factor (an upper bound for the
+    probes, whose random reads the copy's 128-byte streaming requests overstate); None if not measured."""
+    p = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        k = json.load(f).get("kernels", {}).get(kernel)
+    return k.get("traffic_upper_bytes_per_launch", k.get("traffic_bytes_per_launch")) if k else None
+
+
 def load_bound(kernel: str):
     """The counter evidence of what bounds a kernel, committed in profiles/pmc_bounds.json (from rocprofv3 PMC runs of
     this bench): for the state set's probes the share of the measured random-access capacity their reads and atomics
@@ -115,7 +126,8 @@ def bench_strips(steps: int, warmup: int, cpu: bool):
     achieved = by[dom] / (ms[dom] * 1e-3) / 1e9 if ms[dom] > 0 else 0.0
     traffic = load_traffic(f"brfs_{dom}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": f"brfs {dom}",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_copy_scaled": load_traffic_copy_scaled(f"brfs_{dom}"), "kernel": f"brfs {dom}",
                 "bytes_per_launch": int(by[dom] / max(1, launches[dom])), "ms_per_launch": round(ms[dom] / max(1, launches[dom]), 4),
                 "bound_evidence": load_bound(f"brfs_{dom}")}
     out = {
