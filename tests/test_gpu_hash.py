@@ -169,3 +169,24 @@ def test_state_set_rows_beyond_2048_words(words):
     assert got[0] == got[2] and got[1] == got[4] and len({got[0], got[1], got[3]}) == 3
     stored = torch.from_dlpack(s.rows()).cpu().numpy().view(np.uint64)
     assert np.array_equal(stored, rows[np.unique(exp_ids, return_index=True)[1]])
+
+
+def test_state_set_ids_at_4m_rows():
+    """Ids at 2^22 rows of 1,024 bits in 2^20-row batches (four batches, 7% of the 2^26-row workload), against the ids
+    numpy derives from the rows themselves: each distinct row's id is the rank of its first occurrence."""
+    from mymyr_amd import gen, hip
+
+    total, batch = 1 << 22, 1 << 20
+    rows = gen.dedup_rows(0, total, 16, seed=12)
+    _, first, inverse = np.unique(np.ascontiguousarray(rows).view(np.dtype((np.void, 128))).reshape(-1), return_index=True,
+                                  return_inverse=True)
+    rank = np.empty(len(first), np.int64)
+    rank[np.argsort(first, kind="stable")] = np.arange(len(first))
+    exp = rank[inverse.reshape(-1)]
+    s = hip.StateSet(total, 16, 0.5, batch=batch)
+    got = np.empty(total, np.int64)
+    for b in range(0, total, batch):
+        _, ids, _ = s.insert(dev(rows[b:b + batch]))
+        got[b:b + batch] = ids.cpu().numpy()
+    assert len(s) == len(first)
+    assert np.array_equal(got, exp)
