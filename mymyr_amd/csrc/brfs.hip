@@ -450,7 +450,7 @@ __global__ __launch_bounds__(kLB) void k_ground_compact(StateSetView s, ParentRo
 {
     constexpr int G = kGroup<W>;
     constexpr int K = kPairs<W>;
-    constexpr int kBatch = 4;  // winners per group in flight (the list, record and row loads of each are independent)
+    constexpr int kBatch = 16;  // winners per group in flight (the list, record and row loads of each are independent)
     const u32 q = lane_id() % G;
     const u64 id0 = *size_now;
     const u64 winners = min(m, *size_next - id0);
