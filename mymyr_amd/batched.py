@@ -27,7 +27,7 @@ from torch import Tensor
 
 from . import _lib, rl
 from ._lib import check, lib
-from .rl import InstanceSampler, TaskSuite, TaskTable, visited_capacity
+from .rl import InstanceSampler, TaskSuite, TaskTable, resolve_sampler, visited_capacity
 from .task import Task
 
 __all__ = ["BatchedEnv", "CapturedRollout", "Observation", "Rollout", "StepResult"]
@@ -100,18 +100,9 @@ class Rollout(NamedTuple):
 
 
 def _instance_sampler(value: Any, num_instances: int, default_uniform: bool) -> Optional[InstanceSampler]:
-    """The sampler a BatchedEnv draws with (python/mymyr/rl/_sampling.py:153-163): "auto" is uniform unless task ids
-    pin the assignment, "uniform" always, None never; a table of one instance samples nothing."""
-    if isinstance(value, str):
-        if value not in ("auto", "uniform"):
-            raise ValueError("mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None")
-        value = InstanceSampler(num_instances) if value == "uniform" or default_uniform else None
-    if value is not None:
-        if not isinstance(value, InstanceSampler):
-            raise TypeError("mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None")
-        if value.num_instances != num_instances:
-            raise ValueError("mymyr: sampler instance count does not match the environment's table or suite")
-    return None if num_instances == 1 else value
+    """The sampler a BatchedEnv draws with: "auto" is uniform unless task ids pin the assignment (rl.resolve_sampler)."""
+    return resolve_sampler(value, num_instances, auto_uniform=default_uniform,
+                           mismatch="mymyr: sampler instance count does not match the environment's table or suite")
 
 
 def _stream() -> int:

@@ -47,29 +47,42 @@ def visited_capacity(track_visited: bool | int, max_steps: int | None) -> int:
     return H
 
 
+def _checked_weights(weights, n: int) -> tuple:
+    """The weights as floats, one per instance, finite and nonnegative with a positive sum (the reference's messages)."""
+    w = np.asarray(weights, np.float64)
+    if w.shape != (n,):
+        raise ValueError("mymyr: sampling weights need one value per instance")
+    ok = bool(np.isfinite(w).all()) and not bool((w < 0).any()) and bool((w > 0).any())
+    if not ok:
+        raise ValueError("mymyr: sampling weights must be finite, nonnegative and have a positive sum")
+    return tuple(float(x) for x in w)
+
+
+def _draw_tables(weights) -> tuple[np.ndarray, np.ndarray]:
+    """The instances of positive weight and the cumulative thresholds over 2^32 between them that rl::rng::instance_draw
+    compares a draw against (include/mymyr/rl/rng.hpp:94-115); the float64 steps (weights over their maximum, each
+    over the sum, the running sum, scaled by 2^32 and floored) must match the reference's bit for bit. None (uniform):
+    empty tables."""
+    if weights is None:
+        return np.empty(0, np.int32), np.empty(0, np.uint32)
+    w = np.asarray(weights, np.float64)
+    kept = np.flatnonzero(w > 0).astype(np.int32)
+    scaled = w[kept] / w.max()
+    running = np.cumsum(scaled / scaled.sum())[:-1]
+    return kept, np.minimum(np.floor(running * 2**32), 0xFFFFFFFF).astype(np.uint32)
+
+
 class InstanceSampler:
     """Draws the instance an env resets into (mymyr.rl.InstanceSampler, python/mymyr/rl/_sampling.py:16-104; the draw
     is rl::rng::instance_draw, include/mymyr/rl/rng.hpp:94-115): uniform over num_instances, or weighted by `weights`
     (finite, nonnegative, positive sum), as cumulative thresholds over 2^32 of the instances of positive weight."""
 
     def __init__(self, num_instances: int, weights=None):
-        if num_instances < 1 or num_instances > 0x7FFFFFFF:
+        if not 1 <= num_instances <= 0x7FFFFFFF:
             raise ValueError("mymyr: instance sampling needs between 1 and 2**31 - 1 instances")
         self.num_instances = num_instances
-        self.weights = None
-        self.indices = np.empty(0, np.int32)
-        self.thresholds = np.empty(0, np.uint32)
-        if weights is not None:
-            values = np.asarray(weights, np.float64)
-            if values.shape != (num_instances,):
-                raise ValueError("mymyr: sampling weights need one value per instance")
-            if not np.isfinite(values).all() or (values < 0).any() or not (values > 0).any():
-                raise ValueError("mymyr: sampling weights must be finite, nonnegative and have a positive sum")
-            self.weights = tuple(float(v) for v in values)
-            self.indices = np.flatnonzero(values > 0).astype(np.int32)
-            positive = values[self.indices] / values.max()
-            cumulative = np.cumsum(positive / positive.sum())[:-1]
-            self.thresholds = np.minimum(np.floor(cumulative * 2**32), 0xFFFFFFFF).astype(np.uint32)
+        self.weights = None if weights is None else _checked_weights(weights, num_instances)
+        self.indices, self.thresholds = _draw_tables(self.weights)
 
     def sample(self, seed: int, env_id: int, reset_count: int) -> int:
         """The instance of env `env_id`'s draw number `reset_count` under `seed` (host)."""
@@ -97,20 +110,29 @@ class PoolBatch(dict):
             raise AttributeError(name) from None
 
 
-def resolve_sampler(sampler, instances: int) -> InstanceSampler | None:
-    """The pool's instance sampling from a `sampler` argument, as the reference resolves it
-    (python/mymyr/rl/_sampling.py: _instance_sampler): "auto" and "uniform" are uniform over the instances, None is
-    none, an InstanceSampler must cover the table; over one instance there is nothing to sample."""
-    if isinstance(sampler, str):
-        if sampler not in ("auto", "uniform"):
-            raise ValueError("mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None")
-        sampler = InstanceSampler(instances)
-    if sampler is not None:
-        if not isinstance(sampler, InstanceSampler):
-            raise TypeError("mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None")
+_SAMPLER_ARG = "mymyr: sampler must be 'auto', 'uniform', an InstanceSampler or None"
+
+
+def resolve_sampler(sampler, instances: int, *, auto_uniform: bool = True, mismatch: str | None = None) -> InstanceSampler | None:
+    """The instance sampling a `sampler` argument asks for, with the reference's rules and messages
+    (python/mymyr/rl/_sampling.py:153-163): "uniform" samples uniformly, "auto" too unless `auto_uniform` is off (a
+    BatchedEnv given task ids), None not at all, and an InstanceSampler as it is if it covers the `instances`; a
+    table of one instance never samples. `mismatch`: the message for a sampler over another number of instances."""
+    if isinstance(sampler, InstanceSampler):
         if sampler.num_instances != instances:
-            raise ValueError(f"mymyr: env: a sampler over {sampler.num_instances} instances for {instances}")
-    return None if instances == 1 else sampler
+            raise ValueError(mismatch or f"mymyr: env: a sampler over {sampler.num_instances} instances for {instances}")
+        chosen = sampler
+    elif sampler is None:
+        chosen = None
+    elif not isinstance(sampler, str):
+        raise TypeError(_SAMPLER_ARG)
+    elif sampler == "uniform" or (sampler == "auto" and auto_uniform):
+        chosen = InstanceSampler(instances)
+    elif sampler == "auto":
+        chosen = None
+    else:
+        raise ValueError(_SAMPLER_ARG)
+    return chosen if instances > 1 else None
 
 
 class DeviceEnvPool:
