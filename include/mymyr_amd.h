@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 18
+#define MYA_ABI_VERSION 19
 int mya_abi_version(void);
 
 /* Device memory held by the library (replaces DeviceContext::usage(), include/mymyr/cuda/runtime.hpp:140-146, 183):
@@ -537,14 +537,18 @@ typedef struct mya_search_statistics
     uint64_t memory_bytes;
 } mya_search_statistics;
 
-/* The events of search::SearchObserver (include/mymyr/search/control.hpp:157-186) that the device search sends, each
- * on the thread that called mya_brfs; a null function is skipped. on_start: the start state's row (`words` words);
- * on_pass: the end of BrFS layer `layer` (0 first) with that layer's counts; on_progress: before a device batch once
- * `progress_interval` more states were expanded (the reference asks every progress_interval expansions; the device
- * search asks at its batch boundaries), returning 0 stops the search with status 4 (Cancelled); on_solution: the plan
- * (schemas[i], bindings[i * label_width ..], -1 padded) and its cost; on_end: the final status and statistics. The
- * per-state events (on_expand, on_generate, on_prune, on_transition) are not sent: the device search does not bring
- * its states and transitions to the host. */
+/* The events of search::SearchObserver (include/mymyr/search/control.hpp:157-186), each on the thread that called
+ * mya_brfs; a null function is skipped. on_start: the start state's row (`words` words); on_pass: the end of BrFS layer
+ * `layer` (0 first) with that layer's counts; on_progress: before a device batch once `progress_interval` more states
+ * were expanded (the reference asks every progress_interval expansions; the device search asks at its batch
+ * boundaries), returning 0 stops the search with status 4 (Cancelled); on_solution: the plan (schemas[i],
+ * bindings[i * label_width ..], -1 padded) and its cost; on_end: the final status and statistics.
+ * on_expand (state `id` expanded), on_generate (a transition of `parent` by the action (schema, binding[arity]) to
+ * `child`, UINT64_MAX when the successor got no id (a blocked state), with the successor's row and whether the
+ * transition entered it) and on_prune (a blocked successor, after its on_generate) come in the reference's order,
+ * state by state and successor by successor, but a device batch at a time once the batch is confirmed: with any of
+ * them set, the search brings each batch's parents, transitions and successor rows to the host (slower; for
+ * analysis and tests). on_transition is not sent by a BrFS, as in the reference. */
 typedef struct mya_search_observer
 {
     void* user;
@@ -554,6 +558,11 @@ typedef struct mya_search_observer
     void (*on_solution)(void* user, const int32_t* schemas, const int32_t* bindings, uint32_t length, uint32_t label_width,
                         double cost);
     void (*on_end)(void* user, int32_t status, const mya_search_statistics* total);
+    void (*on_expand)(void* user, uint64_t id, const uint64_t* state, uint32_t words);
+    void (*on_generate)(void* user, uint64_t parent, int32_t schema, const int32_t* binding, uint32_t arity, uint64_t child,
+                        const uint64_t* state, uint32_t words, int32_t is_new);
+    void (*on_prune)(void* user, uint64_t parent, int32_t schema, const int32_t* binding, uint32_t arity, const uint64_t* state,
+                     uint32_t words);
 } mya_search_observer;
 
 /* BrfsResult fields (include/mymyr/search/brfs.hpp:103-138). status: the reference's SearchStatus codes

@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 18  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 19  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -153,11 +153,16 @@ ON_PASS = ctypes.CFUNCTYPE(None, c_void_p, c_uint32, ctypes.POINTER(SearchStatis
 ON_PROGRESS = ctypes.CFUNCTYPE(c_int32, c_void_p, ctypes.POINTER(SearchStatistics))
 ON_SOLUTION = ctypes.CFUNCTYPE(None, c_void_p, ctypes.POINTER(c_int32), ctypes.POINTER(c_int32), c_uint32, c_uint32, c_double)
 ON_END = ctypes.CFUNCTYPE(None, c_void_p, c_int32, ctypes.POINTER(SearchStatistics))
+ON_EXPAND = ctypes.CFUNCTYPE(None, c_void_p, c_uint64, ctypes.POINTER(c_uint64), c_uint32)
+ON_GENERATE = ctypes.CFUNCTYPE(None, c_void_p, c_uint64, c_int32, ctypes.POINTER(c_int32), c_uint32, c_uint64, ctypes.POINTER(c_uint64),
+                               c_uint32, c_int32)
+ON_PRUNE = ctypes.CFUNCTYPE(None, c_void_p, c_uint64, c_int32, ctypes.POINTER(c_int32), c_uint32, ctypes.POINTER(c_uint64), c_uint32)
 
 
 class SearchObserver(Structure):
     _fields_ = [("user", c_void_p), ("on_start", ON_START), ("on_pass", ON_PASS), ("on_progress", ON_PROGRESS),
-                ("on_solution", ON_SOLUTION), ("on_end", ON_END)]
+                ("on_solution", ON_SOLUTION), ("on_end", ON_END), ("on_expand", ON_EXPAND), ("on_generate", ON_GENERATE),
+                ("on_prune", ON_PRUNE)]
 
 
 class BrfsResult(Structure):

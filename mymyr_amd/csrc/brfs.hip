@@ -411,7 +411,7 @@ constexpr int kPairs = W >= 4 ? 2 : 1;  // word pairs per lane
 // takes it as pending). Losers' flags are cleared, winners' stay 1.
 template<int W, bool kCE>
 __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRows<W, kCE> src, u64 m, u8* __restrict__ flags,
-                                                      u32* __restrict__ status, BlockedView blocked)
+                                                      u32* __restrict__ status, BlockedView blocked, u64* __restrict__ cand_slot)
 {
     constexpr int G = kGroup<W>;
     const u64 j = (static_cast<u64>(blockIdx.x) * kLB + threadIdx.x) / G;
@@ -437,6 +437,8 @@ __global__ __launch_bounds__(kLB) void k_ground_insert(StateSetView s, ParentRow
     const ProbeResult r = probe_insert<G, kPairs<W>>(s, src, j, me, h, q, gbase, flags, status);
     if (q == 0 && r.lose)
         flags[j] = 0;
+    if (q == 0 && cand_slot)
+        cand_slot[j] = r.cand_slot;  // an observed search resolves every candidate's state id from it
 }
 
 // The chunk's winners (list order, ids from *size_now, their count size_next - size_now) below `limit` into the arena
@@ -528,6 +530,45 @@ void build_action_tables(const GroundActions& ga, std::vector<u64>& fast, std::v
 
 }  // namespace
 
+struct BrfsTables;
+
+namespace
+{
+/// Successor row of ground action a from a parent row on the host (an observed search's events): the instances of
+/// its conditional effects that fire in the parent add their deletes and adds, then "delete, then add".
+void host_successor(const std::vector<u64>& masks, const GroundActions& ga, const u64* parent, u32 a, u32 W, u64* out)
+{
+    std::vector<u64> del(masks.begin() + static_cast<size_t>(a) * 2 * W, masks.begin() + static_cast<size_t>(a) * 2 * W + W);
+    std::vector<u64> add(masks.begin() + static_cast<size_t>(a) * 2 * W + W, masks.begin() + static_cast<size_t>(a + 1) * 2 * W);
+    auto bit = [&](u32 sl) { return (parent[sl >> 6] >> (sl & 63)) & 1; };
+    if (!ga.ce_meta.empty())
+        for (u32 i = ga.ce_off[a]; i < ga.ce_off[a + 1]; ++i)
+        {
+            const u32 m = ga.ce_meta[i], o = ga.ce_soff[i];
+            const u32 npos = m & 0xFF, nneg = (m >> 8) & 0xFF, nadd = (m >> 16) & 0xFF, ndel = m >> 24;
+            bool fires = true;
+            for (u32 k = 0; k < npos && fires; ++k)
+                fires = bit(ga.ce_slots[o + k]);
+            for (u32 k = 0; k < nneg && fires; ++k)
+                fires = !bit(ga.ce_slots[o + npos + k]);
+            if (!fires)
+                continue;
+            for (u32 k = 0; k < nadd; ++k)
+            {
+                const u32 sl = ga.ce_slots[o + npos + nneg + k];
+                add[sl >> 6] |= u64{1} << (sl & 63);
+            }
+            for (u32 k = 0; k < ndel; ++k)
+            {
+                const u32 sl = ga.ce_slots[o + npos + nneg + nadd + k];
+                del[sl >> 6] |= u64{1} << (sl & 63);
+            }
+        }
+    for (u32 w = 0; w < W; ++w)
+        out[w] = (parent[w] & ~del[w]) | add[w];
+}
+}  // namespace
+
 struct BrfsTables
 {
     int device = -1;
@@ -537,6 +578,7 @@ struct BrfsTables
     GoalDev goal{};
     const u64* masks = nullptr;
     const u64* slot_cid = nullptr;
+    std::vector<u64> host_masks;  // the delete and add masks on the host (an observed search's successor rows)
     std::vector<void*> owned;
 
     template<class T>
@@ -587,6 +629,7 @@ std::unique_ptr<BrfsTables> build_tables(const CompiledTask& task, bool witness,
                       ga.size(),
                       static_cast<u32>(fast.size())};
     tb->masks = tb->upload(masks);
+    tb->host_masks = std::move(masks);
     tb->goal = GoalDev{tb->upload(task.goal_pos), tb->upload(task.goal_neg), static_cast<u32>(task.goal_pos.size()),
                        static_cast<u32>(task.goal_neg.size()), task.goal_unsat ? 1u : 0u};
     tb->slot_cid = task.mode == AtomMode::Dense ? nullptr : tb->upload(task.slot_cid);
@@ -688,6 +731,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
     };
 
     const BlockedView blocked = upload_blocked(o.blocked, task.words, W, chunk, b, stream);
+    EventBuffers ev;
+    ev.init(o.observed(), chunk, b);
     // the start state (stored even if blocked)
     {
         const std::vector<u64> s0 = start_row(task, o, W);
@@ -778,6 +823,39 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             bool live = false;
             u64 p0 = 0, np = 0, m = 0;
         } pend;
+        // an observed search's events of a confirmed chunk: parents [p0e, p0e + npe) and candidates [0, me)
+        auto emit = [&](u64 p0e, u64 npe, u64 me) {
+            if (!ev.on)
+                return;
+            const std::vector<u64> prow = to_host(par + (pbase + p0e) * W, npe * W, stream);
+            std::vector<u64> pid(npe);
+            for (u64 p = 0; p < npe; ++p)
+                pid[p] = id_at(p0e + p);
+            const std::vector<u32> pa = to_host(cand_pa, me, stream);
+            const std::vector<i64> ids = to_host(ev.ids, me, stream);
+            const std::vector<u8> isn = to_host(ev.is_new, me, stream);
+            const std::vector<u8> hit = blocked.capacity ? to_host(blocked.hit, me, stream) : std::vector<u8>{};
+            std::vector<u32> cp(me);
+            for (u64 j = 0; j < me; ++j)
+                cp[j] = pa[j] >> abits;
+            const u32 L = ga.label_width;
+            std::vector<i32> bind(std::max<u32>(L, 1));
+            std::vector<u64> crow(W);
+            emit_batch(
+                o, W, npe, prow, pid, me, cp, ids, isn, hit,
+                [&](u64 j, u32* sc, const i32** bd, u32* ar) {
+                    const u32 a = pa[j] & ((1u << abits) - 1);
+                    *sc = ga.schema[a];
+                    *ar = task.text.schemas[*sc].arity;
+                    for (u32 k = 0; k < L; ++k)
+                        bind[k] = static_cast<i32>(ga.binding[static_cast<size_t>(a) * L + k]);
+                    *bd = bind.data();
+                },
+                [&](u64 j, const u64* parent) {
+                    host_successor(tb.host_masks, ga, parent, pa[j] & ((1u << abits) - 1), W, crow.data());
+                    return static_cast<const u64*>(crow.data());
+                });
+        };
         // confirms the pending chunk from the set's size and status read at the last synchronization; true if the
         // store filled inside it (the search stops there)
         auto confirm = [&](u64 size_dev, u32 status) {
@@ -820,6 +898,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 layer_goals += b.host[kGoalSum];
                 if (blocked.capacity)
                     layer_pruned += b.host[kCutPruned];
+                emit(pend.p0, pc + 1, u64{jc} + 1);
                 if (layer_cut)
                 {
                     // the search goes on with the next layer: the cut winners' entries must not stand for states
@@ -839,6 +918,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
             if (pend.m)
                 new_rate = static_cast<double>(winners) / static_cast<double>(pend.m);
             set.size = size_dev;
+            emit(pend.p0, pend.np, pend.m);
             row[0] += pend.np;
             row[1] += pend.m;
             layer_goals += b.host[kChunkGoal];
@@ -947,14 +1027,14 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 state_set_begin_batch(set, stream);
                 if (g.ce_off)
                     hipLaunchKernelGGL((k_ground_insert<W, true>), dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src_ce, m,
-                                       set.flags, set.d_status, blocked);
+                                       set.flags, set.d_status, blocked, ev.cand_slot);
                 else
                     hipLaunchKernelGGL((k_ground_insert<W, false>), dim3(blocks_for(m * G, kLB)), dim3(kLB), 0, stream, set.v, src, m,
-                                       set.flags, set.d_status, blocked);
+                                       set.flags, set.d_status, blocked, ev.cand_slot);
                 launch_check("ground insert");
                 tm.end(kKInsert, 0);
                 tm.begin(kKRank);
-                state_set_rank(set, m, stream);
+                state_set_rank(set, m, stream, ev.is_new);
                 tm.end(kKRank, 0);
                 // the winners' count is on the device (size next - size now); ids from max_states on are not written
                 // (the store filled: the confirmation finds the cut)
@@ -973,6 +1053,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 }
                 launch_check("ground compact");
                 tm.end(kKCompact, 0);
+                if (ev.on)
+                    state_set_resolve_ids(set, ev.cand_slot, m, ev.ids, stream);
                 state_set_flip(set);
             }
             // the chunk's goal states, read at the synchronization that confirms it

@@ -44,6 +44,13 @@ struct BrfsOptionsC
     std::function<void(u32 layer, const std::array<u64, 3>& counts, double seconds)> on_pass;
     std::function<bool(u64 expanded, u64 generated, u64 states, double seconds)> on_progress;
     u64 progress_interval = u64{1} << 16;
+    // the per-state events (SearchObserver::on_expand, on_generate, on_prune), sent batch by batch in the reference's
+    // order; child ~0: none (a blocked successor)
+    std::function<void(u64 id, const u64* row, u32 words)> on_expand;
+    std::function<void(u64 parent, u32 schema, const i32* binding, u32 arity, u64 child, const u64* row, u32 words, bool is_new)>
+        on_generate;
+    std::function<void(u64 parent, u32 schema, const i32* binding, u32 arity, const u64* row, u32 words)> on_prune;
+    [[nodiscard]] bool observed() const { return on_expand || on_generate || on_prune; }
     // BrfsOptions::layers (include/mymyr/search/layer_ordering.hpp:63-113): kind 0 queue, 1 in order, 2 reverse,
     // 3 randomized, 4 goal count, 5 scored (the reference's Kind order); ~0: no limit / no beam
     i32 layer_kind = 0;

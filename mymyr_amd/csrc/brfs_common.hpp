@@ -448,6 +448,70 @@ __global__ void k_gather_rows(const u64* __restrict__ rows, const u64* __restric
     }
 }
 
+/// The device buffers of an observed search's per-state events (BrfsOptionsC::observed): per candidate of a batch its
+/// probe result, its state's id and whether it entered the store. All null when the search is not observed.
+struct EventBuffers
+{
+    bool on = false;
+    u64* cand_slot = nullptr;
+    i64* ids = nullptr;
+    u8* is_new = nullptr;
+    void init(bool observed, u64 chunk, Buffers& b)
+    {
+        on = observed;
+        if (!on)
+            return;
+        cand_slot = b.alloc<u64>(chunk, "event probe results");
+        ids = b.alloc<i64>(chunk, "event ids");
+        is_new = b.alloc<u8>(chunk, "event new flags");
+    }
+};
+
+/// A confirmed batch's events in the reference's order (src/mymyr/search/brfs.cpp:335-372): per parent p < np its
+/// on_expand, then per successor of it (candidates in order; cand_parent[j] is j's parent) its on_generate and, for a
+/// blocked one (hit[j]), its on_prune. ids [m] and is_new [m] come from the device; label(j, &schema, &binding,
+/// &arity) gives a candidate's action and row(j, parent row) its successor row (host, W words).
+template<class Label, class Row>
+void emit_batch(const BrfsOptionsC& o, u32 W, u64 np, const std::vector<u64>& parent_rows, const std::vector<u64>& parent_ids,
+                u64 m, const std::vector<u32>& cand_parent, const std::vector<i64>& ids, const std::vector<u8>& is_new,
+                const std::vector<u8>& hit, Label&& label, Row&& row)
+{
+    u64 j = 0;
+    for (u64 p = 0; p < np; ++p)
+    {
+        const u64* prow = parent_rows.data() + p * W;
+        const u64 pid = parent_ids[p];
+        if (o.on_expand)
+            o.on_expand(pid, prow, W);
+        for (; j < m && cand_parent[j] == p; ++j)
+        {
+            u32 schema = 0, arity = 0;
+            const i32* binding = nullptr;
+            label(j, &schema, &binding, &arity);
+            const u64* crow = row(j, prow);
+            const bool blocked = !hit.empty() && hit[j];
+            if (o.on_generate)
+                o.on_generate(pid, schema, binding, arity, blocked || ids[j] < 0 ? ~u64{0} : static_cast<u64>(ids[j]), crow, W,
+                              !blocked && is_new[j] != 0);
+            if (blocked && o.on_prune)
+                o.on_prune(pid, schema, binding, arity, crow, W);
+        }
+    }
+}
+
+/// Device to host copy of n elements on the stream (synchronous).
+template<class T>
+std::vector<T> to_host(const T* d, u64 n, hipStream_t stream)
+{
+    std::vector<T> h(n);
+    if (n)
+    {
+        hip_check(hipMemcpyAsync(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost, stream), "event copy");
+        hip_check(hipStreamSynchronize(stream), "event copy");
+    }
+    return h;
+}
+
 /// A device buffer grown to the largest request of a search, freed in the order of its stream.
 template<class T>
 struct GrowBuf

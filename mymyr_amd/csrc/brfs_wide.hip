@@ -213,6 +213,12 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
     };
     launch_fill_u32(xstatus, 2, 0, stream);
     BlockedView blocked = upload_blocked(o.blocked, TW0, W, chunk, b, stream);
+    // an observed search's events: per candidate its probe result, id, new flag and action label
+    EventBuffers ev;
+    ev.init(o.observed(), chunk, b);
+    const u32 EL = std::max<u32>(1, task.label_width);
+    i32* ev_schema = ev.on ? b.alloc<i32>(chunk, "event schemas") : nullptr;
+    i32* ev_binding = ev.on ? b.alloc<i32>(chunk * EL, "event bindings") : nullptr;
     // the start state (stored even if blocked)
     {
         const std::vector<u64> s0 = start_row(task, o, W);
@@ -319,6 +325,31 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         }
         auto parents = [&](u64 p) { return ordered ? lrows.rows.p + p * W : set.v.arena + (lb + p) * W; };
         auto id_at = [&](u64 p) { return ordered ? lrows.ids[p] : lb + p; };
+        // an observed search's events of a confirmed chunk: parents [p0e, p0e + npe) and candidates [0, me)
+        auto emit = [&](u64 p0e, u64 npe, u64 me) {
+            if (!ev.on)
+                return;
+            const std::vector<u64> prow = to_host(parents(p0e), npe * W, stream);
+            std::vector<u64> pid(npe);
+            for (u64 p = 0; p < npe; ++p)
+                pid[p] = id_at(p0e + p);
+            const std::vector<i32> par_rel = to_host(cand_parent, me, stream);
+            std::vector<u32> cp(par_rel.begin(), par_rel.end());
+            const std::vector<i64> ids = to_host(ev.ids, me, stream);
+            const std::vector<u8> isn = to_host(ev.is_new, me, stream);
+            const std::vector<u8> hit = blocked.capacity ? to_host(blocked.hit, me, stream) : std::vector<u8>{};
+            const std::vector<i32> sch = to_host(ev_schema, me, stream);
+            const std::vector<i32> bnd = to_host(ev_binding, me * EL, stream);
+            const std::vector<u64> rows = to_host(cand_rows, me * W, stream);
+            emit_batch(
+                o, W, npe, prow, pid, me, cp, ids, isn, hit,
+                [&](u64 j, u32* sc, const i32** bd, u32* ar) {
+                    *sc = static_cast<u32>(sch[j]);
+                    *ar = task.text.schemas[*sc].arity;
+                    *bd = bnd.data() + j * EL;
+                },
+                [&](u64 j, const u64*) { return rows.data() + j * W; });
+        };
         u64 cut_at = bounded ? o.max_states : ~u64{0};
         bool layer_cut = false, truncated = false;
         if (lorder.limited() && le + o.max_next_layer_states < cut_at)
@@ -383,6 +414,12 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 e.index = cand_index;
                 e.goal = cand_goal;
                 e.counts = counts + p0;
+                if (ev.on)
+                {
+                    e.schema = ev_schema;
+                    e.binding = ev_binding;
+                    e.label_width = EL;
+                }
                 launch_expand(e, stream);
                 tm.end(kKEmit, (p1 - p0) * R + m * (R + 9));
                 if (lazy)
@@ -408,10 +445,10 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 }
                 tm.begin(kKInsert);
                 state_set_begin_batch(set, stream);
-                state_set_probe(set, cand_rows, m, stream, blocked.capacity ? &blocked : nullptr);
+                state_set_probe(set, cand_rows, m, stream, blocked.capacity ? &blocked : nullptr, ev.cand_slot);
                 tm.end(kKInsert, m * (R + 8));
                 tm.begin(kKRank);
-                state_set_rank(set, m, stream);
+                state_set_rank(set, m, stream, ev.is_new);
                 tm.end(kKRank, m * 9);
                 tm.begin(kKCompact);
                 set_small(kSpare, 0);
@@ -424,6 +461,8 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 });
                 launch_check("wide compact");
                 tm.end(kKCompact, 0);
+                if (ev.on)
+                    state_set_resolve_ids(set, ev.cand_slot, m, ev.ids, stream);
                 state_set_flip(set);
             }
             // the chunk's goal parents, its outcome and the expansion's status in one synchronization
@@ -468,6 +507,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 layer_goals += b.host[kGoalSum];
                 if (blocked.capacity)
                     layer_pruned += b.host[kPruned];
+                emit(p0, static_cast<u64>(pc) + 1, u64{jc} + 1);
                 if (layer_cut)
                 {
                     // the search goes on with the next layer: the cut winners' entries must not stand for states
@@ -484,6 +524,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 throw std::length_error("mymyr_amd: brfs: the search needs more than " + std::to_string(cap_states) +
                                         " states of device memory (set max_states or memory_states)");
             set.size = size_dev;
+            emit(p0, p1 - p0, m);
             row[0] += p1 - p0;
             row[1] += m;
             layer_goals += b.host[kGoalSum];

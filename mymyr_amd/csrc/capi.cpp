@@ -492,6 +492,16 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
                 const mya_search_statistics st{expanded, generated, states, 0, seconds, 0};
                 return obs->on_progress(obs->user, &st) != 0;
             };
+        if (obs && obs->on_expand)
+            o.on_expand = [obs](u64 id, const u64* row, u32 words) { obs->on_expand(obs->user, id, row, words); };
+        if (obs && obs->on_generate)
+            o.on_generate = [obs](u64 parent, u32 schema, const i32* binding, u32 arity, u64 child, const u64* row, u32 words, bool is_new) {
+                obs->on_generate(obs->user, parent, static_cast<i32>(schema), binding, arity, child, row, words, is_new ? 1 : 0);
+            };
+        if (obs && obs->on_prune)
+            o.on_prune = [obs](u64 parent, u32 schema, const i32* binding, u32 arity, const u64* row, u32 words) {
+                obs->on_prune(obs->user, parent, static_cast<i32>(schema), binding, arity, row, words);
+            };
         if (obs && obs->on_start)
         {
             const std::vector<u64>& s0 = o.start.empty() ? task->compiled->initial : o.start;

@@ -401,6 +401,14 @@ void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
     launch_check("state set rank");
 }
 
+void state_set_resolve_ids(StateSet& s, const u64* cand_slot, u64 n, i64* ids, hipStream_t stream)
+{
+    if (n == 0)
+        return;
+    hipLaunchKernelGGL(k_resolve_ids, dim3(blocks_for(n, kBlock)), dim3(kBlock), 0, stream, s.v, cand_slot, n, ids);
+    launch_check("state set ids");
+}
+
 void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t stream)
 {
     if (winners > kept)
@@ -411,13 +419,13 @@ void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t str
     s.size = size;
 }
 
-void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked)
+void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked, u64* cand_slot)
 {
     if (m == 0)
         return;
     const BlockedView bl = blocked ? *blocked : BlockedView{};
     with_shape(s.v.words, [&]<int G, int K>() {
-        hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, rows, m, nullptr, s.flags,
+        hipLaunchKernelGGL((k_insert<G, K>), dim3(group_blocks<G>(m)), dim3(kBlock), 0, stream, s.v, rows, m, cand_slot, s.flags,
                            s.d_status, bl);
     });
     launch_check("state set probe");

@@ -85,7 +85,13 @@ void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t str
 /// a stored equal row drops a candidate, equal candidates keep the smallest index, the others take pending entries
 /// (the losers' flags are cleared). state_set_rank and the caller's compaction follow. With `blocked`, a candidate equal
 /// to a blocked state is dropped first (flag cleared, blocked->hit[j] = 1; every other candidate's hit byte is 0).
-void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked = nullptr);
+void state_set_probe(StateSet& s, const u64* rows, u64 m, hipStream_t stream, const BlockedView* blocked = nullptr,
+                     u64* cand_slot = nullptr);
+
+/// After a batch's rank and compaction: ids[j] = the id of candidate j's state (its own as a winner, the equal one's
+/// otherwise; -1 when it got none: blocked, or past a cut), from the probe results cand_slot [n] (blocked candidates'
+/// entries are not read by callers).
+void state_set_resolve_ids(StateSet& s, const u64* cand_slot, u64 n, i64* ids, hipStream_t stream);
 
 /// hash_state of every row (a group of lanes per row).
 void launch_hash_rows(const u64* rows, u64 n, u32 words, u64* out, hipStream_t stream);

@@ -49,30 +49,33 @@ class Observer:
     """Base class of search observers (the reference's mymyr.search.Observer, python/mymyr/search/_observer.py:23-120):
     pass an instance (or any object with some of these methods) as ``observer=`` to :func:`brfs` and override the
     events of interest; events a subclass does not override are never called. The device search sends ``on_start``,
-    ``on_pass`` after every layer, ``on_progress`` at its batch boundaries once ``progress_interval`` more states were
-    expanded, ``on_solution`` and ``on_end``, all on the calling thread. It does not bring states and transitions to the
-    host, so an observer that defines ``on_expand``, ``on_generate``, ``on_prune`` or ``on_transition`` is refused. The
-    first exception an event raises stops the search (status "cancelled") and is raised when the search returns."""
+    ``on_expand`` per expanded state, ``on_generate`` per successor (``on_prune`` after it for a blocked one), ``on_pass``
+    after every layer, ``on_progress`` at its batch boundaries once ``progress_interval`` more states were expanded,
+    ``on_solution`` and ``on_end``, all on the calling thread and in the reference's order; the per-state events come a
+    device batch at a time (with any of them defined, each batch's parents, transitions and successor rows are brought
+    to the host). A BrFS sends no ``on_transition``, as the reference's. The first exception an event raises stops the
+    search (status "cancelled") at the next batch and is raised when the search returns."""
 
     @_default_event
     def on_start(self, state: np.ndarray) -> None:
         """The search starts from ``state`` (its words)."""
 
     @_default_event
-    def on_expand(self, id: int, state) -> None:
-        """Not sent by the device search."""
+    def on_expand(self, id: int, state: np.ndarray) -> None:
+        """State ``id`` is expanded."""
 
     @_default_event
-    def on_generate(self, parent: int, action: Action, child, state, is_new: bool) -> None:
-        """Not sent by the device search."""
+    def on_generate(self, parent: int, action: Action, child, state: np.ndarray, is_new: bool) -> None:
+        """``action`` leads from ``parent`` to ``state``; ``child`` is its id (None for a blocked successor); ``is_new``:
+        the state was entered by this transition."""
 
     @_default_event
-    def on_prune(self, parent: int, action: Action, state) -> None:
-        """Not sent by the device search."""
+    def on_prune(self, parent: int, action: Action, state: np.ndarray) -> None:
+        """The successor ``state`` of ``parent`` is not entered (a blocked state)."""
 
     @_default_event
     def on_transition(self, parent: int, action: Action, child, state, outcome) -> None:
-        """Not sent by the device search."""
+        """Not sent by a BrFS (the reference's BrFS does not send it either)."""
 
     @_default_event
     def on_pass(self, width: int, stats: Statistics) -> None:
@@ -92,9 +95,6 @@ class Observer:
         """The search ended with ``status`` and the total ``stats``."""
 
 
-_PER_STATE_EVENTS = ("on_expand", "on_generate", "on_prune", "on_transition")
-
-
 def _event(obj, name: str):
     fn = getattr(obj, name, None)
     if fn is None or getattr(fn, "_mymyr_default_event", False):
@@ -112,12 +112,9 @@ class _ObserverBridge:
     the search and records the first exception an event raised."""
 
     def __init__(self, obj, interval: int):
-        for name in _PER_STATE_EVENTS:
-            if _event(obj, name) is not None:
-                raise ValueError(f"mymyr_amd: brfs: the device search does not send {name} (per-state events stay on the "
-                                 "device); observers may define on_start, on_pass, on_progress, on_solution and on_end")
         self.error: BaseException | None = None
-        ev = {n: _event(obj, n) for n in ("on_start", "on_pass", "on_progress", "on_solution", "on_end")}
+        ev = {n: _event(obj, n) for n in ("on_start", "on_pass", "on_progress", "on_solution", "on_end", "on_expand", "on_generate",
+                                          "on_prune")}
         self.defines_any = any(f is not None for f in ev.values())
 
         def guard(fn):
@@ -158,6 +155,22 @@ class _ObserverBridge:
         def on_end(_u, status, stats):
             ev["on_end"](STATUS.get(int(status), str(int(status))), _stats(stats))
 
+        def row(p, words):
+            return np.ctypeslib.as_array(p, shape=(words,)).copy()
+
+        def action(schema, binding, arity):
+            return Action(int(schema), tuple(int(binding[k]) for k in range(arity)))
+
+        def on_expand(_u, sid, state, words):
+            ev["on_expand"](int(sid), row(state, words))
+
+        def on_generate(_u, parent, schema, binding, arity, child, state, words, is_new):
+            ev["on_generate"](int(parent), action(schema, binding, arity), None if child == (1 << 64) - 1 else int(child),
+                              row(state, words), bool(is_new))
+
+        def on_prune(_u, parent, schema, binding, arity, state, words):
+            ev["on_prune"](int(parent), action(schema, binding, arity), row(state, words))
+
         # on_progress is always installed: an exception in another event stops the search at the next batch
         self.c = _lib.SearchObserver(
             None,
@@ -165,7 +178,10 @@ class _ObserverBridge:
             _lib.ON_PASS(guard(on_pass)) if ev["on_pass"] else _lib.ON_PASS(),
             _lib.ON_PROGRESS(on_progress),
             _lib.ON_SOLUTION(guard(on_solution)) if ev["on_solution"] else _lib.ON_SOLUTION(),
-            _lib.ON_END(guard(on_end)) if ev["on_end"] else _lib.ON_END())
+            _lib.ON_END(guard(on_end)) if ev["on_end"] else _lib.ON_END(),
+            _lib.ON_EXPAND(guard(on_expand)) if ev["on_expand"] else _lib.ON_EXPAND(),
+            _lib.ON_GENERATE(guard(on_generate)) if ev["on_generate"] else _lib.ON_GENERATE(),
+            _lib.ON_PRUNE(guard(on_prune)) if ev["on_prune"] else _lib.ON_PRUNE())
 
 
 _LAYER_KINDS = {"queue": 0, "in_order": 1, "reverse": 2, "randomized": 3, "goal_count": 4}

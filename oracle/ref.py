@@ -59,7 +59,7 @@ class BrfsOptions(Structure):
         ("max_next_layer_states", c_uint32),
         ("beam_width", c_uint32),
         ("randomize_ties", c_int32),
-        ("reserved2", c_int32),
+        ("record_events", c_int32),
         ("scorer", ctypes.CFUNCTYPE(None, c_void_p, ctypes.POINTER(c_uint64), c_uint64, c_uint32, ctypes.POINTER(ctypes.c_double))),
         ("scorer_user", c_void_p),
     ]
@@ -141,6 +141,7 @@ def lib() -> ctypes.CDLL:
             "mref_task_goal": (c_int, [c_void_p, c_void_p, c_uint32]),
             "mref_canonical_hash": (c_uint64, [c_void_p, c_void_p, c_uint32]),
             "mref_successors": (c_int64, [c_void_p, c_void_p, c_uint32, c_int, c_int, c_void_p, c_void_p, c_uint32, c_void_p, c_uint32, c_uint64]),
+            "mref_brfs_events": (c_uint64, [c_void_p, c_uint64]),
             "mref_hash_words": (c_uint64, [c_void_p, c_uint32, c_uint64]),
             "mref_hash_state": (c_uint64, [c_void_p, c_uint32]),
             "mref_hash_mix64": (c_uint64, [c_uint64]),
@@ -465,7 +466,7 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
          stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf"),
          goal=None, layer_order="queue", seed=0, max_next_layer_states=None, prefer_more_satisfied_goals=True, beam_width=None,
-         randomize_ties=False):
+         randomize_ties=False, record_events=False):
     """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
     (schema, binding) pairs, the goal state's words and the cost; the result's words, fluent_slots, threads_used, store
     and message. start [words] and blocked_states [k, words] are rows of the task's table words; goal (None: the task's)
@@ -488,7 +489,7 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
     o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
                     max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds,
                     0 if goal is None else 1, 0 if goal is None else len(goal), _p(go), _p(gl), kind, int(not prefer_more_satisfied_goals),
-                    seed, max_next_layer_states or 0, beam_width or 0, int(randomize_ties), 0, cb, None)
+                    seed, max_next_layer_states or 0, beam_width or 0, int(randomize_ties), int(record_events), cb, None)
     r = BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -508,6 +509,11 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         "message": r.message.decode(),
     }
     del st, bl, go, gl
+    if record_events:
+        ne = lib().mref_brfs_events(None, 0)
+        ev = np.zeros((ne, 7), np.uint64)
+        lib().mref_brfs_events(ev.ctypes.data, ne)
+        out["events"] = ev
     task.refresh()
     if r.solved:
         k = min(r.plan_len, cap)

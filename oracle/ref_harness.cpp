@@ -127,10 +127,62 @@ struct mref_brfs_options
     uint32_t max_next_layer_states;
     uint32_t beam_width;
     int32_t randomize_ties;
-    int32_t reserved2;
+    int32_t record_events;  // record the observer's events (mref_brfs_events)
     void (*scorer)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, double* scores);
     void* scorer_user;
 };
+
+namespace
+{
+/// The events of search::SearchObserver as 7-word records: kind (0 start, 1 expand, 2 generate, 3 prune, 4 pass,
+/// 5 solution, 6 end) then its fields; states by their hash_state, bindings by a polynomial hash of their objects
+/// (h = arity, then h = h * 1000003 + object).
+struct EventLog final : search::SearchObserver
+{
+    std::vector<uint64_t> ev;
+    void rec(uint64_t a, uint64_t b = 0, uint64_t c = 0, uint64_t d = 0, uint64_t e = 0, uint64_t f = 0, uint64_t g = 0)
+    {
+        ev.insert(ev.end(), {a, b, c, d, e, f, g});
+    }
+    static uint64_t sh(StateView s) { return hash::state(s.w, s.nw, s.num, s.nnum); }
+    static uint64_t bh(const Action& a)
+    {
+        uint64_t h = a.binding.size();
+        for (ObjectId o : a.binding)
+            h = h * 1000003ull + o.v;
+        return h;
+    }
+    void on_start(StateView s) override { rec(0, sh(s)); }
+    void on_expand(u64 id, StateView s) override { rec(1, id, sh(s)); }
+    void on_generate(u64 parent, const Action& a, u64 child, StateView s, bool is_new) override
+    {
+        rec(2, parent, a.schema.v, bh(a), child, sh(s), is_new ? 1 : 0);
+    }
+    void on_prune(u64 parent, const Action& a, StateView s) override { rec(3, parent, a.schema.v, bh(a), 0, sh(s)); }
+    void on_pass(u32 layer, const search::SearchStatistics& st) override { rec(4, layer, st.expanded, st.generated, st.states); }
+    void on_solution(std::span<const Action> plan, double cost) override
+    {
+        uint64_t h = plan.size();
+        for (const Action& a : plan)
+            h = h * 1000003ull + a.schema.v * 7919ull + bh(a);
+        rec(5, plan.size(), h, static_cast<uint64_t>(cost));
+    }
+    void on_end(search::SearchStatus status, const search::SearchStatistics& st) override
+    {
+        rec(6, static_cast<uint64_t>(status), st.expanded, st.generated, st.states, st.pruned);
+    }
+};
+thread_local std::vector<uint64_t> g_events;
+}  // namespace
+
+/// The events recorded by the last mref_brfs with record_events: count records of 7 words (copied up to cap records).
+uint64_t mref_brfs_events(uint64_t* out, uint64_t cap)
+{
+    const uint64_t n = g_events.size() / 7;
+    if (out)
+        std::memcpy(out, g_events.data(), std::min(n, cap) * 7 * sizeof(uint64_t));
+    return n;
+}
 
 struct mref_brfs_result
 {
@@ -798,8 +850,15 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
                     fn(user, rows.data(), states.size(), w, scores.data());
                 };
             }
+            EventLog log;
+            if (o->record_events)
+            {
+                b.observer = &log;
+                b.progress_interval = ~u64{0};
+            }
             const auto t0 = std::chrono::steady_clock::now();
             const BrfsResult x = brfs(*t->task, b);
+            g_events = std::move(log.ev);
             r->seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
             r->states = x.states;
             r->expanded = x.expanded;

@@ -698,6 +698,44 @@ def make_brfs_layers():
     dump("brfs_layers.json", out)
 
 
+EVENT_CASES = [
+    ("gripper__prob05", dict(stop_at_goal=False, max_states=3000)),
+    ("caldera-split-opt18-adl__p04", dict(stop_at_goal=True)),
+    ("parcprinter-opt11-strips__p03", dict(stop_at_goal=True)),
+    ("transport_w20_3", dict(stop_at_goal=True)),
+    ("blocks__probBLOCKS-8-0", dict(stop_at_goal=False, max_states=2000, blocked=3)),
+    ("gripper__prob05", dict(stop_at_goal=False, layer_order="reverse", beam_width=30, max_depth=6)),
+    ("depot__p02", dict(stop_at_goal=False, layer_order="in_order", max_next_layer_states=200, max_depth=5)),
+    ("miconic-simpleadl__s10-2", dict(stop_at_goal=False, max_states=2000)),
+]
+
+
+def make_brfs_events():
+    """The reference observer's events (search::SearchObserver, include/mymyr/search/control.hpp:157-186) of small
+    searches, as the harness records them (7-word records: start, expand, generate, prune, pass, solution, end; states
+    by hash_state, bindings by a polynomial hash): per case the count of each kind, the sha256 of all records and the
+    first 60 records. blocked=k blocks the first k successors of the initial state."""
+    out = {}
+    for name, kw in EVENT_CASES:
+        kw = dict(kw)
+        t = ref.RefTask(fx.task_path(name), "auto")
+        blocked = None
+        if "blocked" in kw:
+            k = kw.pop("blocked")
+            _, _, rows = t.successors(t.initial_state())
+            blocked = rows[:k]
+        r = ref.brfs(t, record_events=True, blocked_states=blocked, **kw)
+        ev = r["events"]
+        key = f"{name}:" + ",".join(f"{a}={b}" for a, b in sorted(kw.items())) + (f",blocked={len(blocked)}" if blocked is not None else "")
+        out[key] = {"options": kw, "blocked": None if blocked is None else [hex_row(x) for x in blocked],
+                    "counts": {str(int(k)): int((ev[:, 0] == k).sum()) for k in range(7)},
+                    "sha256": hashlib.sha256(np.ascontiguousarray(ev).astype("<u8").tobytes()).hexdigest(),
+                    "head": [[f"{int(x):x}" for x in row] for row in ev[:60]],
+                    "states": r["states"], "expanded": r["expanded"], "generated": r["generated"], "status": r["status"]}
+        print(key, out[key]["counts"], flush=True)
+    dump("brfs_events.json", out)
+
+
 LAZY_TASKS = ["gripper__prob05", "blocks__probBLOCKS-8-0", "depot__p02", "pegsol-08-strips__p22", "visitall__visitall_x-6_y-3_r-100",
               "miconic__s7-4", "logistics00__probLOGISTICS-6-1", "driverlog__p03", "rovers__p02"]
 
@@ -760,7 +798,8 @@ def main():
     steps = {"hash": make_hash, "philox": make_philox, "slots": make_slots, "successors": make_successors, "env": make_env,
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
-             "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long}
+             "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long,
+             "brfs_events": make_brfs_events}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

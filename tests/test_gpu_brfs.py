@@ -414,12 +414,13 @@ def test_observer_events(golden):
     with pytest.raises(RuntimeError, match="boom"):
         search.brfs(t, stop_at_goal=False, observer=Boom())
 
-    class PerState(search.Observer):
+    class Boom2(search.Observer):
         def on_generate(self, parent, action, child, state, is_new):
-            pass
+            if child is not None and child > 100:
+                raise KeyError("late")
 
-    with pytest.raises(ValueError, match="on_generate"):
-        search.brfs(t, observer=PerState())
+    with pytest.raises(KeyError, match="late"):
+        search.brfs(t, stop_at_goal=False, observer=Boom2())
 
 
 @pytest.mark.parametrize("key", list(__import__("json").load(open(__import__("os").path.join(
@@ -499,3 +500,87 @@ def test_rows_beyond_2048_words(golden, key):
     print(f"long rows: {key}", flush=True)
     r = device(golden, "transport_w2208", **exp["options"])
     assert not same(r, exp), same(r, exp)
+
+
+class EventLog:
+    """The observer's events as the reference harness records them (tests/golden/make_golden.py, make_brfs_events):
+    7-word records, states by hash_state, bindings by h = arity, then h * 1000003 + object (mod 2^64)."""
+
+    M = (1 << 64) - 1
+    CODES = {"solved": 0, "exhausted": 1, "out_of_states": 2, "out_of_time": 3, "cancelled": 4, "failed": 5, "unsolvable": 6}
+
+    def __init__(self):
+        from mymyr_amd._lib import lib
+
+        self.lib = lib
+        self.ev = []
+
+    def sh(self, row):
+        import numpy as np
+
+        r = np.ascontiguousarray(row, dtype=np.uint64)
+        return int(self.lib.mya_hash_state(r.ctypes.data, r.size))
+
+    def bh(self, a):
+        h = len(a.binding)
+        for o in a.binding:
+            h = (h * 1000003 + o) & self.M
+        return h
+
+    def rec(self, *v):
+        self.ev.append(list(v) + [0] * (7 - len(v)))
+
+    def on_start(self, state):
+        self.rec(0, self.sh(state))
+
+    def on_expand(self, sid, state):
+        self.rec(1, sid, self.sh(state))
+
+    def on_generate(self, parent, action, child, state, is_new):
+        self.rec(2, parent, action.schema, self.bh(action), self.M if child is None else child, self.sh(state), int(is_new))
+
+    def on_prune(self, parent, action, state):
+        self.rec(3, parent, action.schema, self.bh(action), 0, self.sh(state))
+
+    def on_pass(self, layer, st):
+        self.rec(4, layer, st.expanded, st.generated, st.states)
+
+    def on_solution(self, plan, cost):
+        h = len(plan)
+        for a in plan:
+            h = (h * 1000003 + a.schema * 7919 + self.bh(a)) & self.M
+        self.rec(5, len(plan), h, int(cost))
+
+    def on_end(self, status, st):
+        self.rec(6, self.CODES[status], st.expanded, st.generated, st.states, st.pruned)
+
+
+@pytest.mark.parametrize("key", list(__import__("json").load(open(__import__("os").path.join(
+    __import__("os").path.dirname(__file__), "golden", "brfs_events.json")))))
+def test_observer_per_state_events(golden, key):
+    """Every observer event of a search, on_expand, on_generate (child ids, new flags, successor states) and on_prune
+    included, in order, equal to the compiled reference's (src/mymyr/search/brfs.cpp:274-404): ground, conditional-effect,
+    wide-row, blocked-state, beam and layer-cut searches, compared by the sha256 of their event records."""
+    import hashlib
+
+    import numpy as np
+
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    exp = golden.load("brfs_events.json")[key]
+    name = key.split(":")[0]
+    t = Task.from_text_file(golden.task_path(name))
+    kw = dict(exp["options"])
+    if exp["blocked"]:
+        kw["blocked_states"] = np.array([[int(x, 16) for x in r][: t.words] + [0] * max(0, t.words - len(r)) for r in exp["blocked"]],
+                                        dtype=np.uint64)
+    log = EventLog()
+    print(f"events: {key}", flush=True)
+    search.brfs(t, observer=log, **kw)
+    ev = np.array(log.ev, dtype=np.uint64)
+    counts = {str(k): int((ev[:, 0] == k).sum()) for k in range(7)}
+    head = [[f"{int(x):x}" for x in row] for row in ev[:60]]
+    assert counts == exp["counts"], (counts, exp["counts"])
+    assert head == exp["head"]
+    assert hashlib.sha256(np.ascontiguousarray(ev).astype("<u8").tobytes()).hexdigest() == exp["sha256"]
