@@ -267,21 +267,34 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_count(const u64* __restr
 // (parent, action) records of the successors of parents [first, first + n) at their offsets (candidate index =
 // offsets[t] - cand_base + rank in action order), 32 bits each: the parent index relative to `first` above the low
 // `abits` bits, which hold the action (the driver keeps a chunk's parents below 2^(32 - abits)).
+//
+// Each parent's records are a run of its own (about 9 per parent and group of 256 actions here), so a lane writing its
+// parent's records straight out makes every store touch as many memory lines as there are lanes. The wave stages the
+// records of each 256-action step in LDS instead, parent after parent (a wave prefix sum of the parents' counts places
+// them), with their candidate indices beside them, and writes them out in staging order: 64 consecutive staged records
+// lie in a few parents' runs, a few lines per store. A step with more records than the stage holds writes directly.
+constexpr u32 kEmitStage = 1024;  // staged records per wave (8 KiB of LDS with their indices)
+
 template<int W>
 __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restrict__ arena, u64 first, u32 n, GroundDev g,
                                                             const u64* __restrict__ offsets, u64 cand_base, u32 abits,
                                                             u32* __restrict__ cand_pa)
 {
     __shared__ u64 Bs[kTW][Slices<W>::kWords];
+    __shared__ u32 Sk[kTW][kEmitStage], Sr[kTW][kEmitStage];
     const u32 lane = lane_id(), wave = threadIdx.x / kWave;
     const u32 base = (blockIdx.x * kTW + wave) * kWave;
     if (base >= n)
         return;
     u64* B = Bs[wave];
+    u32* sk = Sk[wave];
+    u32* sr = Sr[wave];
     const u64 vm = load_slices<W>(B, arena, first, base, n, lane);
     const u32 t = base + lane;
     const bool valid = t < n;
-    u64 k = valid ? offsets[t] - cand_base : 0;
+    // candidate indices relative to the wave's first parent's (a wave holds at most 64 times the actions, below 2^32)
+    const u64 kbase = offsets[base] - cand_base;
+    u32 k = valid ? static_cast<u32>(offsets[t] - cand_base - kbase) : 0;
     const u32 hi = t << abits;
     for (u32 a0 = 0; a0 < g.num_padded; a0 += 4 * kWave)
     {
@@ -293,19 +306,47 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restri
             const u32 a = a0 + q * kWave + lane;
             mt[q] = a0 + q * kWave < g.num_padded ? action_mask<W>(B, g, g.fast[a], a, vm) : 0;
         }
+        // every lane takes part in the transposes (cross-lane moves), invalid parents' masks cleared after them
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             mt[q] = transpose64(mt[q], lane);
-        if (!valid)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            mt[q] = valid ? mt[q] : 0;
+        const u32 c = static_cast<u32>(__popcll(mt[0]) + __popcll(mt[1]) + __popcll(mt[2]) + __popcll(mt[3]));
+        const u32 inc = wave_inclusive(c);
+        const u32 total = __shfl(inc, kWave - 1, kWave);
+        if (total > kEmitStage)
+        {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                while (mt[q])
+                {
+                    const u32 bit = static_cast<u32>(__builtin_ctzll(mt[q]));
+                    mt[q] &= mt[q] - 1;
+                    cand_pa[kbase + k++] = hi | (a0 + q * kWave + bit);
+                }
             continue;
+        }
+        u32 pos = inc - c;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             while (mt[q])
             {
                 const u32 bit = static_cast<u32>(__builtin_ctzll(mt[q]));
                 mt[q] &= mt[q] - 1;
-                cand_pa[k++] = hi | (a0 + q * kWave + bit);
+                sk[pos] = k++;
+                sr[pos++] = hi | (a0 + q * kWave + bit);
             }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (u32 r = lane; r < total; r += kWave)
+            cand_pa[kbase + sk[r]] = sr[r];
+        // the next step overwrites the stage only after every lane has read its share
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
