@@ -140,6 +140,20 @@ def bench_strips(steps: int, warmup: int, cpu: bool):
                    "search_ms": round(sum(x.search_s for x in results) * 1e3 / steps, 3),
                    "device_ms": round(sum(x.device_s for x in results) * 1e3 / steps, 3)},
     }
+    # the same search at four times the budget (max_states 2^28: a 4 GiB table, a 16 GiB arena, the cut late in the
+    # fifth layer), one untimed and one timed search: how the rate holds as the table outgrows the caches' reach
+    big = dict(kw, max_states=w.max_states << 2)
+    search.brfs(t, **big)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    rb = search.brfs(t, timings=True, **big)
+    torch.cuda.synchronize()
+    wb = time.perf_counter() - t0
+    out["detail"]["larger_budget"] = {
+        "max_states": big["max_states"], "ms": round(wb * 1e3, 2), "expanded_per_s": rb.expanded / wb,
+        "generated_per_s": rb.generated / wb, "expanded": rb.expanded, "generated": rb.generated, "states": rb.states,
+        "layer_counts": rb.layer_counts, "kernel_ms": {c: round(rb.kernels[c]["ms"], 3) for c in classes},
+        "insert_candidates_per_s": rb.generated / (rb.kernels["insert"]["ms"] * 1e-3)}
     if cpu:
         out["cpu_baseline"] = cpu_strips(path, w)
     return out

@@ -651,6 +651,18 @@ def make_brfs_suite_add():
     dump("brfs.json", out)
 
 
+def make_brfs_strips_large():
+    """Adds the strips workload's cut at max_states = 2^28 to brfs.json (the single-threaded reference search: about
+    1.2 G successors and 25 GB of host memory, some 20 minutes), keeping the existing records."""
+    path = os.path.join(fx.GOLDEN, "brfs.json")
+    with open(path) as f:
+        out = json.load(f)
+    ms = 1 << 28
+    out["strips"][str(ms)] = brfs_record("strips", "dense", max_depth=12, max_states=ms, stop_at_goal=False)
+    print("strips", ms, flush=True)
+    dump("brfs.json", out)
+
+
 LAYER_CASES = [
     ("gripper__prob05", "auto", dict(layer_order="in_order", beam_width=50)),
     ("gripper__prob05", "auto", dict(layer_order="reverse")),
@@ -799,7 +811,7 @@ def main():
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
              "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long,
-             "brfs_events": make_brfs_events}
+             "brfs_events": make_brfs_events, "brfs_strips_large": make_brfs_strips_large}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -127,6 +127,9 @@ def test_plan_replays_to_the_goal_state(golden):
 
 
 def test_strips_workload_cuts(golden):
+    """The strips workload's searches (512 fluents, 4096 actions) at max_states 2^20, 2^22, 2^24, 2^26 and 2^28 (1.18 G
+    successors, a 4 GiB table), its depth, expansion and goal cuts: counts, layers and fingerprints equal to the
+    reference's single-threaded search."""
     g = golden.load("brfs.json")["strips"]
     for key, exp in g.items():
         r = device(golden, "strips", "dense", **exp["options"])
