@@ -313,8 +313,9 @@ def copy_calibration(steps: int):
 
 def random_ops(steps: int):
     """The random 8-byte operation rates that bound the state set's probes (mya_random_ops): loads, compare-and-swaps,
-    atomic mins and stores at seeded random addresses of a 1 GiB table (in HBM) and of a 256 MiB one (the Infinity
-    Cache's size), 2^28 operations each, HIP-event timed; one JSON line."""
+    atomic mins and stores at seeded random addresses of a 1 GiB table (in HBM), of a 256 MiB one (the Infinity Cache's
+    size) and of 4 GiB and 16 GiB ones (the strips search's table and arena at 2^28 states), 2^28 operations each,
+    HIP-event timed; one JSON line."""
     import torch
 
     from mymyr_amd._lib import check, lib
@@ -322,7 +323,7 @@ def random_ops(steps: int):
     n = 1 << 28
     sink = torch.empty(1 << 20, dtype=torch.int64, device="cuda")
     out = {}
-    for label, words in (("1 GiB", 1 << 27), ("256 MiB", 1 << 25)):
+    for label, words in (("1 GiB", 1 << 27), ("256 MiB", 1 << 25), ("4 GiB", 1 << 29), ("16 GiB", 1 << 31)):
         table = torch.zeros(words, dtype=torch.int64, device="cuda")
         rates = {}
         for kind, name in enumerate(("load", "cas", "atomic_min", "store")):
