@@ -97,7 +97,7 @@ def load_bound(kernel: str):
         return json.load(f).get("kernels", {}).get(kernel)
 
 
-def bench_strips(steps: int, warmup: int, cpu: bool):
+def bench_strips(steps: int, warmup: int, cpu: bool, larger: bool = True):
     import torch
 
     from mymyr_amd import search, workloads
@@ -142,6 +142,10 @@ def bench_strips(steps: int, warmup: int, cpu: bool):
     }
     # the same search at four times the budget (max_states 2^28: a 4 GiB table, a 16 GiB arena, the cut late in the
     # fifth layer), one untimed and one timed search: how the rate holds as the table outgrows the caches' reach
+    if not larger:
+        if cpu:
+            out["cpu_baseline"] = cpu_strips(path, w)
+        return out
     big = dict(kw, max_states=w.max_states << 2)
     search.brfs(t, **big)
     torch.cuda.synchronize()
@@ -352,6 +356,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-larger-budget", action="store_true",
+                    help="leave out the strips search at max_states 2^28 (profiles of the headline search alone)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (the reference kernel for scaling PMC byte counters)")
     ap.add_argument("--random-ops", action="store_true",
@@ -376,7 +382,7 @@ def main():
     only = set(x for x in a.only.split(",") if x)
     cpu = not a.no_cpu
     steps, warmup = max(1, a.steps), max(0, a.warmup)
-    head = bench_strips(steps, warmup, cpu) if (not only or "strips" in only) else None
+    head = bench_strips(steps, warmup, cpu, not a.no_larger_budget) if (not only or "strips" in only) else None
     wl = {}
     # each env workload over its stated horizon (gridworld 256, transport 512, transport_xl 128 steps) from reset
     from mymyr_amd import workloads

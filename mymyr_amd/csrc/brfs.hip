@@ -281,14 +281,13 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restri
                                                             u32* __restrict__ cand_pa)
 {
     __shared__ u64 Bs[kTW][Slices<W>::kWords];
-    __shared__ u32 Sk[kTW][kEmitStage], Sr[kTW][kEmitStage];
+    __shared__ u64 Stage[kTW][kEmitStage];  // (candidate index << 32) | record
     const u32 lane = lane_id(), wave = threadIdx.x / kWave;
     const u32 base = (blockIdx.x * kTW + wave) * kWave;
     if (base >= n)
         return;
     u64* B = Bs[wave];
-    u32* sk = Sk[wave];
-    u32* sr = Sr[wave];
+    u64* stage = Stage[wave];
     const u64 vm = load_slices<W>(B, arena, first, base, n, lane);
     const u32 t = base + lane;
     const bool valid = t < n;
@@ -335,14 +334,16 @@ __global__ __launch_bounds__(kTW * kWave) void k_ground_emit(const u64* __restri
             {
                 const u32 bit = static_cast<u32>(__builtin_ctzll(mt[q]));
                 mt[q] &= mt[q] - 1;
-                sk[pos] = k++;
-                sr[pos++] = hi | (a0 + q * kWave + bit);
+                stage[pos++] = (static_cast<u64>(k++) << 32) | (hi | (a0 + q * kWave + bit));
             }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         for (u32 r = lane; r < total; r += kWave)
-            cand_pa[kbase + sk[r]] = sr[r];
+        {
+            const u64 e = stage[r];
+            cand_pa[kbase + (e >> 32)] = static_cast<u32>(e);
+        }
         // the next step overwrites the stage only after every lane has read its share
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
