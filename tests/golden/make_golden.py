@@ -651,6 +651,31 @@ def make_brfs_suite_add():
     dump("brfs.json", out)
 
 
+# small budgets at the edges (the reference's own checks: python tests/python/test_search.py:120-136), over the ground
+# driver (gripper), the wide one (20-word transport rows) and lazy slots
+EDGE_OPTIONS = {
+    "states1": dict(max_states=1, stop_at_goal=False), "states2": dict(max_states=2, stop_at_goal=False),
+    "states50": dict(max_states=50, stop_at_goal=False), "expanded0": dict(max_expanded=0, stop_at_goal=False),
+    "expanded1": dict(max_expanded=1, stop_at_goal=False), "expanded5": dict(max_expanded=5, stop_at_goal=False),
+    "depth0": dict(max_depth=0, stop_at_goal=False), "depth1": dict(max_depth=1, stop_at_goal=False),
+    "depth2": dict(max_depth=2, stop_at_goal=False), "depth0_goal": dict(max_depth=0, stop_at_goal=True),
+    "depth2_goal": dict(max_depth=2, stop_at_goal=True), "states2_goal": dict(max_states=2, stop_at_goal=True),
+}
+EDGE_TASKS = [("gripper__prob05", "auto"), ("transport_w20_3", "auto"), ("gripper__prob05", "lazy")]
+
+
+def make_brfs_edges():
+    """The reference brfs() at budgets of zero, one and a few states, expansions and layers (brfs_edges.json)."""
+    out = {}
+    for name, atoms in EDGE_TASKS:
+        for key, kw in EDGE_OPTIONS.items():
+            r = lazy_record(name, **kw) if atoms == "lazy" else brfs_record(name, atoms, **kw)
+            r["atoms"] = atoms
+            out[f"{name}:{atoms}:{key}"] = r
+            print(name, atoms, key, r["states"], r["expanded"], r["status"], flush=True)
+    dump("brfs_edges.json", out)
+
+
 def make_brfs_strips_large():
     """Adds the strips workload's cut at max_states = 2^28 to brfs.json (the single-threaded reference search: about
     1.2 G successors and 25 GB of host memory, some 20 minutes), keeping the existing records."""
@@ -811,7 +836,8 @@ def main():
              "env_small": make_env_small, "env_long": make_env_long, "env_tail": make_env_tail, "pool": make_pool,
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
              "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long,
-             "brfs_events": make_brfs_events, "brfs_strips_large": make_brfs_strips_large}
+             "brfs_events": make_brfs_events, "brfs_strips_large": make_brfs_strips_large,
+             "brfs_edges": make_brfs_edges}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

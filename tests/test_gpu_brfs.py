@@ -136,6 +136,26 @@ def test_strips_workload_cuts(golden):
         assert not same(r, exp), (key, same(r, exp))
 
 
+def edge_keys():
+    from tests.golden import fixtures
+
+    return sorted(fixtures.load("brfs_edges.json"))
+
+
+@pytest.mark.parametrize("key", edge_keys())
+def test_budgets_at_the_edges(golden, key):
+    """max_states of 1, 2 and 50, max_expanded of 0, 1 and 5 and max_depth of 0, 1 and 2 (with and without the goal
+    stop) through the ground driver, the wide one (20-word rows) and lazy slots: counts, layers, statuses and
+    fingerprints equal to the reference's (its own checks of these budgets: tests/python/test_search.py:120-136)."""
+    exp = golden.load("brfs_edges.json")[key]
+    name, atoms = key.split(":")[:2]
+    print(f"edge budget: {key}", flush=True)
+    r = device(golden, name, atoms, **exp["options"])
+    assert not same(r, exp), (key, same(r, exp))
+    if "max_states" in exp["options"]:
+        assert r["states"] == exp["options"]["max_states"]
+
+
 def test_small_chunks_do_not_change_results(golden):
     """Chunked layers (tiny candidate buffers) give the same ids and counts."""
     a = device(golden, "gripper__prob05", stop_at_goal=False)
