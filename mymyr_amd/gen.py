@@ -288,9 +288,17 @@ def _dup_and_src(idx: np.ndarray, seed: int, dup: float):
 
 
 def _resolve_sources(idx: np.ndarray, seed: int, dup: float) -> np.ndarray:
+    """The fresh row each row copies (itself when fresh): duplicates' sources followed until a fresh row, only the rows
+    still on a duplicate being drawn again."""
     cur = idx.copy()
-    while True:
-        d, s = _dup_and_src(cur, seed, dup)
-        if not d.any():
-            return cur
-        cur = np.where(d, s, cur)
+    live = np.arange(len(idx))
+    while live.size:
+        d, s = _dup_and_src(cur[live], seed, dup)
+        live = live[d]
+        cur[live] = s[d]
+    return cur
+
+
+def dedup_sources(start: int, count: int, seed: int = 0, dup: float = 0.3) -> np.ndarray:
+    """For rows [start, start + count) of the dedup stream, the index of the fresh row each one equals (uint64)."""
+    return _resolve_sources(np.arange(start, start + count, dtype=np.uint64), seed, dup)

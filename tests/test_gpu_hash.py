@@ -108,21 +108,28 @@ def test_state_set_dedup_closed_form_large():
 def test_state_set_dedup_workload_full_size():
     """The dedup workload at its stated size: 2^26 rows of 1024 bits, about 30% duplicates, in 2^20-row batches into a
     table at load 0.5 (a 1 GiB table and an 8.6 GB arena, so row and slot offsets pass 2^32 bytes). The unique count is
-    exact (the stream's fresh rows); inserting a batch again adds nothing and finds the ids of its first insert."""
-    from mymyr_amd import hip
+    exact (the stream's fresh rows), and so is every row's id: the stream makes each duplicate a copy of an earlier
+    fresh row, so a row's id is that fresh row's rank among the fresh rows (ids are first-occurrence ranks). Inserting
+    a batch again adds nothing and finds the ids of its first insert."""
+    from mymyr_amd import gen, hip
     from tests.golden import fixtures as fx
 
     w = fx.DEDUP_WORKLOAD
     total, batch = w["rows"], w["batch"]
     print(f"dedup workload: {total} rows in batches of {batch}", flush=True)
+    src = gen.dedup_sources(0, total, seed=w["seed"], dup=w["dup"])
+    fresh = src == np.arange(total, dtype=np.uint64)
+    exp_ids = (np.cumsum(fresh, dtype=np.int64) - 1)[src.astype(np.int64)]
+    del fresh
     s = hip.StateSet(total, w["words"], 0.5, batch=batch)
     new = 0
     again = {}
     for b in range(0, total, batch):
-        keep = b in (0, total // 2, total - batch)
-        n, ids, _ = s.insert(hip.dedup_rows(b, batch, w["words"], seed=w["seed"], dup=w["dup"]), want_ids=keep)
-        if keep:
-            again[b] = ids.cpu().numpy()
+        n, ids, _ = s.insert(hip.dedup_rows(b, batch, w["words"], seed=w["seed"], dup=w["dup"]))
+        got = ids.cpu().numpy()
+        assert np.array_equal(got, exp_ids[b:b + batch]), b
+        if b in (0, total // 2, total - batch):
+            again[b] = got
         new += n
     assert new == w["unique"] == len(s)
     for b, ids in again.items():
