@@ -1,12 +1,13 @@
 """Benchmark of the state-expansion path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only strips,gridworld,...] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only strips,gridworld,...] [--no-cpu] [--no-larger-budget]
 
 Prints ONE JSON line. The headline (`value`) is the strips workload: BrFS expanded states per second of a random
 ground STRIPS task (512 fluents, 4096 actions) from its initial state, depth bound 12, stopped by max_states = 2^26
 (the frontier grows ~40x per layer, so the depth bound is never reached; the stop is the reference's own max_states
-rule). One step = one whole BrFS. The other workloads (gridworld / transport / transport_xl env pools, dedup) are
-reported under "workloads", each with env-steps/s (or rows/s) and the achieved HBM bandwidth of its dominant kernel.
+rule). One step = one whole BrFS; `detail.larger_budget` times the same search once at max_states = 2^28. The other
+workloads (gridworld / transport / transport_xl env pools, dedup) are reported under "workloads", each with
+env-steps/s (or rows/s) and the achieved HBM bandwidth of its dominant kernel.
 
 roofline: the dominant kernel class of the BrFS (by summed HIP-event time on the search's own stream): its
 algorithmic bytes (per launch, summed) / its summed duration, against the 8 TB/s HBM peak of MI355X.
