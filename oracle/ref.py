@@ -144,6 +144,7 @@ def lib() -> ctypes.CDLL:
             "mref_brfs_events": (c_uint64, [c_void_p, c_uint64]),
             "mref_hash_words": (c_uint64, [c_void_p, c_uint32, c_uint64]),
             "mref_hash_state": (c_uint64, [c_void_p, c_uint32]),
+            "mref_hash_rows": (None, [c_void_p, c_uint64, c_uint32, c_uint32, c_void_p]),
             "mref_hash_mix64": (c_uint64, [c_uint64]),
             "mref_philox": (None, [c_uint64, c_uint64, c_uint64, c_uint32, c_void_p]),
             "mref_philox_raw": (None, [c_void_p, c_uint32, c_uint32, c_void_p]),
@@ -626,6 +627,15 @@ def hash_words(w: np.ndarray, seed: int = 0x2D358DCCAA6C78A5) -> int:
 def hash_state(w: np.ndarray) -> int:
     w = np.ascontiguousarray(w, dtype=np.uint64)
     return int(lib().mref_hash_state(w.ctypes.data, w.size))
+
+
+def hash_rows(rows: np.ndarray, words: int | None = None) -> np.ndarray:
+    """hash::state of every row of a [n, W] array (its first `words` words; default all), uint64 [n]."""
+    rows = np.ascontiguousarray(rows, dtype=np.uint64)
+    n, W = rows.shape
+    out = np.zeros(n, np.uint64)
+    lib().mref_hash_rows(rows.ctypes.data, n, W if words is None else words, W, out.ctypes.data)
+    return out
 
 
 def philox(seed: int, env: int, draw: int, purpose: int = 0) -> list[int]:

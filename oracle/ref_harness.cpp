@@ -346,6 +346,12 @@ int64_t mref_successors(mref_task* t, const uint64_t* row, uint32_t nw, int witn
 
 uint64_t mref_hash_words(const uint64_t* w, uint32_t n, uint64_t seed) { return hash::words(w, n, seed); }
 uint64_t mref_hash_state(const uint64_t* w, uint32_t n) { return hash::state(w, n, nullptr, 0); }
+// hash_state of each of n rows of `words` words, `stride` words apart
+void mref_hash_rows(const uint64_t* rows, uint64_t n, uint32_t words, uint32_t stride, uint64_t* out)
+{
+    for (uint64_t i = 0; i < n; ++i)
+        out[i] = hash::state(rows + i * stride, words, nullptr, 0);
+}
 uint64_t mref_hash_mix64(uint64_t x) { return hash::mix64(x); }
 
 void mref_philox(uint64_t seed, uint64_t env, uint64_t draw, uint32_t purpose, uint32_t* out)

@@ -72,6 +72,16 @@ def step_digest(n: int, states, reward, terminated, truncated, count, schema, bi
     return h.hexdigest()[:16]
 
 
+def rows_digest(row_hashes, reward, terminated, truncated, count, schema, binding, goal) -> str:
+    """sha256 of one step over a whole batch: each row's state as its 64-bit state hash, then the other arrays, in a
+    fixed order and dtype."""
+    h = hashlib.sha256()
+    for a, dt in ((row_hashes, np.uint64), (reward, np.float32), (terminated, np.uint8), (truncated, np.uint8),
+                  (count, np.int32), (schema, np.int32), (binding, np.int32), (goal, np.uint8)):
+        h.update(np.ascontiguousarray(np.asarray(a)).astype(dt, copy=False).tobytes())
+    return h.hexdigest()[:16]
+
+
 def load(name: str):
     with open(os.path.join(GOLDEN, name)) as f:
         return json.load(f)

@@ -174,6 +174,35 @@ def make_env_tail():
     dump("env_transport_xl_long_tail.json", env_trajectory(xl, 64, xl.steps, first_env=xl.num_envs - 64))
 
 
+def env_batch_digests(w: workloads.EnvWorkload, threads: int = 8):
+    """The reference HostEnv over a workload's whole batch and horizon: per step, the digest of every row (states as
+    their state hashes, fixtures.rows_digest)."""
+    t = ref.RefTask(fx.task_path(w.name), w.atoms)
+    e = ref.RefEnv(t, threads=threads, **w.env)
+    N, W, L = w.num_envs, t.table_words, max(1, t.label_width)
+    S = np.zeros((N, W), np.uint64)
+    st = np.zeros(N, np.int32)
+    dr = np.zeros(N, np.uint64)
+    ag = np.zeros(N, np.uint8)
+    e.reset(S, st, dr, ag, np.zeros(N, np.int32))
+    R, term, trunc = np.zeros(N, np.float32), np.zeros(N, np.uint8), np.zeros(N, np.uint8)
+    c, sch, bnd, g = np.zeros(N, np.int32), np.zeros(N, np.int32), np.zeros((N, L), np.int32), np.zeros(N, np.uint8)
+    digests = []
+    t0 = time.time()
+    for k in range(w.steps):
+        e.step(S, st, dr, ag, reward=R, terminated=term, truncated=trunc, count=c, schema=sch, binding=bnd, goal=g)
+        digests.append(fx.rows_digest(ref.hash_rows(S, t.words), R, term, trunc, c, sch, bnd, g))
+        if k % 32 == 0:
+            print(w.name, "step", k, round(time.time() - t0, 1), flush=True)
+    return {"workload": w.name, "rows": N, "steps": w.steps, "env": w.env, "digests": digests, "ref_seconds": time.time() - t0}
+
+
+def make_env_batch():
+    """Whole-batch digests of the transport workloads over their whole horizons (every env id, every step)."""
+    dump("env_transport_batch.json", env_batch_digests(workloads.TRANSPORT))
+    dump("env_transport_xl_batch.json", env_batch_digests(workloads.TRANSPORT_XL))
+
+
 def make_env_small():
     # a trajectory short enough for the oracle's pure-Python restatement
     tiny = workloads.EnvWorkload("gridworld", 16, 60, {"seed": 3, "max_steps": 20, "step_reward": -1.0, "goal_reward": 5.0})
@@ -837,7 +866,7 @@ def main():
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
              "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long,
              "brfs_events": make_brfs_events, "brfs_strips_large": make_brfs_strips_large,
-             "brfs_edges": make_brfs_edges}
+             "brfs_edges": make_brfs_edges, "env_batch": make_env_batch}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

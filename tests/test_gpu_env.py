@@ -87,6 +87,39 @@ def test_transport_xl_whole_horizon_last_rows(golden):
     run_env(golden, "env_transport_xl_long_tail.json", num_envs=262144, encode=544)
 
 
+def run_batch(golden, fixture: str, encode: int = 0):
+    """Steps a workload's whole batch over its whole horizon and compares, every step, the digest of every row (states
+    as their state hashes, computed on the device; rewards, terminations, truncations, counts, labels and goals) with
+    the reference's."""
+    from mymyr_amd import hip, rl
+    from mymyr_amd.task import Task
+
+    g = golden.load(fixture)
+    t = Task.from_text_file(golden.task_path(g["workload"]))
+    n, L = g["rows"], max(1, t.label_width)
+    print(f"{fixture}: {n} envs x {g['steps']} steps, every row", flush=True)
+    pool = rl.DeviceEnvPool(t, n, **g["env"])
+    pool.reset()
+    for k in range(g["steps"]):
+        o = pool.step(encode=encode)
+        hashes = host(hip.hash_rows(o["states"][:, : t.words].contiguous())).view(np.uint64)
+        d = golden.rows_digest(hashes, host(o["reward"]), host(o["terminated"]), host(o["truncated"]), host(o["count"]),
+                               host(o["schema"]), host(o["binding"])[:, :L], host(o["goal"]))
+        assert d == g["digests"][k], f"{fixture}: step {k} differs from the reference"
+    pool.check()
+
+
+def test_transport_every_row_whole_horizon(golden):
+    """The transport workload as run (65536 envs, 512 steps): every row equals the reference's every step."""
+    run_batch(golden, "env_transport_batch.json")
+
+
+def test_transport_xl_every_row_whole_horizon(golden):
+    """The transport_xl workload as run (262144 envs, 128 steps, the encoding on at its 544 atoms): every row equals the
+    reference's every step."""
+    run_batch(golden, "env_transport_xl_batch.json", encode=544)
+
+
 def reference_masks(rt, row):
     """Per schema, whether the compiled reference generates a successor with it (rl::schema_masks semantics)."""
     m = np.zeros(rt.num_schemas, np.uint8)

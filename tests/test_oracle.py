@@ -164,6 +164,13 @@ def test_port_against_reference_random_rows():
     for _ in range(200):
         s, e, d, c = (int(x) for x in rng.integers(1, 2**31, size=4))
         assert port.successor_index(s, e, d, c) == ref.successor_index(s, e, d, c)
+    # the whole-batch row hash the env batch fixtures are written with: hash_state row by row, zero tails trimmed
+    rows = rng.integers(0, 2**63, size=(64, 9), dtype=np.int64).view(np.uint64)
+    rows[5:20, 6:] = 0
+    rows[30] = 0
+    h = ref.hash_rows(rows)
+    assert all(int(h[i]) == port.hash_state(rows[i]) for i in range(len(rows)))
+    assert all(int(x) == port.hash_state(rows[i, :7]) for i, x in enumerate(ref.hash_rows(rows, 7)))
 
 
 def test_expand_noop_filter_closed_form(golden):
