@@ -39,6 +39,21 @@ def test_philox_known_answers(golden):
         assert port.successor_index(d["seed"], d["env"], d["draw"], d["count"]) == d["index"]
 
 
+def test_below_is_the_high_word_of_the_product():
+    """rng::below takes the high 64 bits of the 128-bit product x * n from 32x32 partial products (rng.hpp:73-78): the
+    mathematics fixes it as floor(x * n / 2^64). The golden draws' counts (< 5000) leave the low partial product's
+    carry almost never visible, so random and extreme x and n pin it here."""
+    rng = np.random.default_rng(17)
+    xs = [int(x) for x in rng.integers(0, 2**63, size=2000, dtype=np.int64)] + [2**64 - 1, 2**63, 2**32 - 1, 2**32, 1, 0]
+    ns = [int(n) for n in rng.integers(1, 2**32, size=2000, dtype=np.int64)] + [2**32 - 1, 2**31, 65536, 3, 1, 2]
+    for x in xs:
+        x2 = x | ((x & 1) << 63)  # top bit set for half of them
+        for n in ns[:: 97]:
+            assert port.below(x2, n) == (x2 * n) >> 64
+    for x, n in zip(xs, ns):
+        assert port.below(x, n) == (x * n) >> 64
+
+
 def test_index_in_range():
     for n in (1, 2, 3, 7, 1000, 0xFFFFFFFF):
         for d in range(50):
