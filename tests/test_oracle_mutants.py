@@ -145,10 +145,16 @@ def test_env_step_pins(golden, monkeypatch):
 
 # ------------------------------------------------------------------------------------------------- BrFS
 def brfs_check(golden):
+    """The reference's searches of gripper to depth 2 and to a 50-state cut (brfs_edges.json): counts and fingerprints."""
     t = port.Task(open(golden.task_path("gripper__prob05")).read())
-    r = port.brfs(t, max_states=20000, stop_at_goal=False)
-    d = golden.determinism_digest(r["states"], r["expanded"], r["generated"], r["layers"], r["fingerprint"])
-    return d == golden.DETERMINISM_BRFS["gripper__prob05"]
+    edges = golden.load("brfs_edges.json")
+    for key in ("gripper__prob05:auto:depth2", "gripper__prob05:auto:states50"):
+        exp = edges[key]
+        opts = {k: v for k, v in exp["options"].items() if k in ("max_depth", "max_states", "stop_at_goal")}
+        r = port.brfs(t, **opts)
+        if any(r[k] != exp[k] for k in ("states", "expanded", "generated", "layers", "fingerprint", "layer_counts")):
+            return False
+    return True
 
 
 _canonical_hash, _mix = port.canonical_hash, port.mix64
