@@ -76,6 +76,19 @@ def test_host_hash_and_philox(golden):
         assert lib.mya_successor_index(d["seed"], d["env"], d["draw"], d["count"]) == d["index"]
 
 
+def test_successor_index_large_counts():
+    """The library's successor index at counts up to 2^32 - 1: the high word of the 128-bit product of the draw's 64
+    Philox bits and the count (rng.hpp:73-84), whose low partial product's carry small counts almost never show."""
+    from oracle import port
+
+    rng = np.random.default_rng(23)
+    for _ in range(3000):
+        seed, env, draw = (int(x) for x in rng.integers(0, 2**63, size=3, dtype=np.int64))
+        count = int(rng.integers(1, 2**32, dtype=np.int64))
+        b = port.philox_block(seed, env & 0xFFFFFFFF, draw, 0)
+        assert lib.mya_successor_index(seed, env & 0xFFFFFFFF, draw, count) == ((b[0] | (b[1] << 32)) * count) >> 64
+
+
 def test_task_errors():
     with pytest.raises(MyaError, match="expected"):
         Task.from_text("O 1\nQ 0\n")
