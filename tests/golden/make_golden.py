@@ -319,6 +319,26 @@ def make_env_table():
     dump("env_table.json", out)
 
 
+def make_instance_draw_edges():
+    """Instance draws whose sampler thresholds sit on the draw's own 32 bits, one below and one above them: the rule
+    counts the thresholds at most the bits (include/mymyr/rl/rng.hpp:94-115), which a random draw almost never tests.
+    The oracle only places the thresholds; the draws are the reference's."""
+    from oracle import port
+
+    rng = np.random.default_rng(41)
+    out = []
+    for _ in range(24):
+        seed, env, count = int(rng.integers(0, 2**63)), int(rng.integers(0, 2**32)), int(rng.integers(0, 2**32))
+        bits = port.fmix32(port.fmix32((seed & 0xFFFFFFFF) ^ port.fmix32(((seed >> 32) & 0xFFFFFFFF) ^ 0x53414D50))
+                           ^ port.fmix32(env) ^ port.fmix32(count ^ 0x9E3779B9))
+        for thr in ([bits], [max(bits, 1) - 1], [min(bits + 1, 0xFFFFFFFF)], [max(bits, 1) - 1, bits, min(bits + 1, 0xFFFFFFFF)]):
+            t = np.array(sorted(thr), np.uint32)
+            idx = np.arange(10, 10 + len(t) + 1, dtype=np.int32)
+            out.append({"seed": seed, "env": env, "reset_count": count, "instances": 16, "thresholds": [int(x) for x in t],
+                        "indices": [int(x) for x in idx], "draw": ref.instance_draw(seed, env, count, 16, t, idx)})
+    dump("instance_draw_edges.json", out)
+
+
 def make_visited_mask():
     """Visited tables filled by the reference's visited_insert (empty, short, at the 3H/4 threshold, saturated, probe
     chains of one home slot, hash 0 and its reserved key) and rl::visited_mask over queries with -1 padding, with and
@@ -866,7 +886,8 @@ def main():
              "brfs_witness": make_brfs_witness, "brfs_wide": make_brfs_wide, "successors_witness": make_successors_witness, "brfs_goals": make_brfs_goals, "brfs_options": make_brfs_options, "sections": make_sections, "env_table": make_env_table, "visited_mask": make_visited_mask, "lazy": make_lazy, "brfs": lambda: make_brfs(a.quick),
              "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long,
              "brfs_events": make_brfs_events, "brfs_strips_large": make_brfs_strips_large,
-             "brfs_edges": make_brfs_edges, "env_batch": make_env_batch}
+             "brfs_edges": make_brfs_edges, "env_batch": make_env_batch,
+             "instance_draw_edges": make_instance_draw_edges}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

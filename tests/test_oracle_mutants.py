@@ -242,9 +242,81 @@ def test_dedup_and_encoding_pins(golden, monkeypatch):
     ])
 
 
+# ------------------------------------------------------------------------------------------------- task tables
+def table_check(*cases):
+    def check(golden):
+        from tests.test_table_oracle import replay_oracle
+
+        for d in golden.load("env_table.json")["instance_draws"]:
+            thr, idx = golden.sampler_arrays(d["weights"])
+            if port.instance_draw(d["seed"], d["env"], d["reset_count"], d["instances"], thr, idx) != d["draw"]:
+                return False
+        for d in golden.load("instance_draw_edges.json"):
+            if port.instance_draw(d["seed"], d["env"], d["reset_count"], d["instances"], d["thresholds"], d["indices"]) != d["draw"]:
+                return False
+        for case in cases:
+            replay_oracle(golden, case)
+        return True
+    return check
+
+
+_instance_draw, _fmix32, _visited_insert, _mask_goal, _pad = (port.instance_draw, port.fmix32, port.visited_insert,
+                                                              port.mask_goal, port.pad)
+
+
+def fmix32_constant(x):
+    x &= M32
+    x = ((x ^ (x >> 16)) * 0x85EBCA6C) & M32  # 0x85EBCA6B
+    x = ((x ^ (x >> 13)) * 0xC2B2AE35) & M32
+    return x ^ (x >> 16)
+
+
+def instance_draw_strict(seed, env, reset_count, instances, thresholds=(), indices=()):
+    # thresholds compared with < where the draw counts those at most its bits
+    if len(indices) == 0:
+        return _instance_draw(seed, env, reset_count, instances)
+    value = _fmix32((seed & M32) ^ _fmix32(((seed >> 32) & M32) ^ 0x53414D50))
+    bits = _fmix32(value ^ _fmix32(env & M32) ^ _fmix32((reset_count & M32) ^ 0x9E3779B9))
+    return int(indices[sum(1 for t in thresholds if int(t) < bits)])
+
+
+def visited_insert_late_overflow(table, count, h):
+    H = len(table)
+    key = h if h else port.VISITED_ZERO
+    at = key & (H - 1)
+    for _ in range(H):
+        if int(table[at]) == key:
+            return True, count
+        if int(table[at]) == 0:
+            if count >= (H * 3) // 4 + 1:  # (H * 3) // 4
+                return False, H
+            table[at] = np.uint64(key)
+            return False, count + 1
+        at = (at + 1) & (H - 1)
+    return False, H
+
+
+def test_task_table_pins(golden, monkeypatch):
+    assert_pins(golden, monkeypatch, table_check("gridworld_sampled", "transport_weighted"), [
+        ("fmix32 constant", "fmix32", fmix32_constant),
+        ("thresholds compared strictly", "instance_draw", instance_draw_strict),
+        ("env and reset count swapped", "instance_draw",
+         lambda seed, env, rc, n, thr=(), idx=(): _instance_draw(seed, rc, env, n, thr, idx)),
+    ])
+    assert_pins(golden, monkeypatch, table_check("gridworld_visited"), [
+        ("overflow one entry late", "visited_insert", visited_insert_late_overflow),
+    ])
+    assert_pins(golden, monkeypatch, table_check("gridworld_goals"), [
+        ("goal masks transposed", "mask_goal", lambda row, gp, gn: _mask_goal(row, gn, gp)),
+    ])
+    assert_pins(golden, monkeypatch, table_check("gridworld_ids"), [
+        ("one slot fewer", "pad", lambda flat, rows, k, *a, **kw: _pad(flat, rows, max(0, k - 1), *a, **kw)),
+    ])
+
+
 @pytest.mark.parametrize("attr", ["mix64", "mulfold", "hash_words", "hash_state", "philox4x32_10", "philox_block", "below",
                                   "successor_index", "successors", "is_goal", "canonical_hash", "dedup_unique",
-                                  "encode_atoms"])
+                                  "encode_atoms", "fmix32", "instance_draw", "visited_insert", "mask_goal", "pad"])
 def test_every_pinned_function_has_a_mutant(attr):
     """Each function named here is mutated by at least one of the tests above."""
     import inspect

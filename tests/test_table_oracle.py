@@ -95,6 +95,9 @@ def test_instance_draws(golden):
     for d in golden.load("env_table.json")["instance_draws"]:
         thr, idx = golden.sampler_arrays(d["weights"])
         assert port.instance_draw(d["seed"], d["env"], d["reset_count"], d["instances"], thr, idx) == d["draw"]
+    # thresholds on, just below and just above the draw's bits (the rule counts those at most the bits)
+    for d in golden.load("instance_draw_edges.json"):
+        assert port.instance_draw(d["seed"], d["env"], d["reset_count"], d["instances"], d["thresholds"], d["indices"]) == d["draw"]
 
 
 def test_library_instance_draws_and_sampler(golden):
@@ -109,6 +112,12 @@ def test_library_instance_draws_and_sampler(golden):
         assert s.sample(d["seed"], d["env"], d["reset_count"]) == d["draw"]
     with pytest.raises(ValueError, match="positive sum"):
         rl.InstanceSampler(2, [0.0, 0.0])
+    from mymyr_amd._lib import lib
+
+    for d in golden.load("instance_draw_edges.json"):
+        thr, idx = np.array(d["thresholds"], np.uint32), np.array(d["indices"], np.int32)
+        assert lib.mya_instance_draw(d["seed"], d["env"], d["reset_count"], d["instances"], thr.ctypes.data, idx.ctypes.data,
+                                     len(idx)) == d["draw"]
 
 
 def test_sampler_arrays_closed_form(golden):
