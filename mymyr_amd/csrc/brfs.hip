@@ -944,7 +944,7 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 if (layer_cut)
                 {
                     // the search goes on with the next layer: the cut winners' entries must not stand for states
-                    state_set_cut(set, cut_at, room, winners, stream);
+                    state_set_cut(set, cut_at, stream);
                     truncated = true;
                     return true;
                 }

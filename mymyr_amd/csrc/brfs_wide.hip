@@ -511,7 +511,7 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
                 if (layer_cut)
                 {
                     // the search goes on with the next layer: the cut winners' entries must not stand for states
-                    state_set_cut(set, cut_at, room, winners, stream);
+                    state_set_cut(set, cut_at, stream);
                     truncated = true;
                     break;
                 }

@@ -211,14 +211,15 @@ __global__ __launch_bounds__(kScanBlock) void k_flag_sums(const u8* __restrict__
     }
 }
 
-// The winners' indices in order (list[rank] = j for flags[j] != 0), their ids base + rank into id_of[j] (optional),
-// is_new[j] = flags[j] (optional), and the losers' flags reset to 1. kFused: `sums` holds the raw block sums, each
-// block adds up those before it itself (few blocks), and the last block writes *total = *base + the grand total;
-// else `sums` holds their exclusive scan.
+// The winners' indices in order (list[rank] = j for flags[j] != 0), their ids base + rank as WinnerBlocks (optional;
+// *id_limit reset to ~0), is_new[j] = flags[j] (optional), and the losers' flags reset to 1. kFused: `sums` holds the
+// raw block sums, each block adds up those before it itself (few blocks), and the last block writes *total = *base +
+// the grand total; else `sums` holds their exclusive scan.
 template<bool kFused>
 __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ flags, u64 n, const u64* __restrict__ sums,
                                                            const u64* __restrict__ base, u32* __restrict__ list,
-                                                           u32* __restrict__ id_of, u8* __restrict__ is_new, u64* __restrict__ total_out)
+                                                           WinnerBlock* __restrict__ ids, u64* __restrict__ id_limit,
+                                                           u8* __restrict__ is_new, u64* __restrict__ total_out)
 {
     __shared__ u32 lds[kScanBlock / kWave + 1];
     __shared__ u64 pre[kScanBlock / kWave];
@@ -250,30 +251,28 @@ __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ fla
     u64 off = prefix + excl;
     const u64 id0 = base ? *base : 0;
     const u32 w[4] = {v.x, v.y, v.z, v.w};
-    // a full thread writes all 16 of its id_of entries (a loser's is never read: only winners hold table entries), as
-    // four whole 16-byte stores instead of a scattered 4-byte store per winner
-    // (first is a multiple of 16 entries, so the id map's base decides the 16-byte alignment of every thread's stores)
-    const bool whole = id_of && full && (reinterpret_cast<uintptr_t>(id_of) & 15) == 0;
-    u32 ids[kFlagsPerThread];
+    if (ids)
+    {
+        // four consecutive threads hold 64 consecutive candidates: their 16-bit winner masks make the block's bits and
+        // the first thread's first rank its base (the block's first winner, if any, is that thread's or a later one's)
+        u32 m16 = 0;
+#pragma unroll
+        for (int k = 0; k < kFlagsPerThread; ++k)
+            m16 |= ((w[k / 4] >> (8 * (k % 4))) & 1) << k;
+        const u32 l0 = lane_id() & ~3u;
+        u64 bits = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            bits |= static_cast<u64>(static_cast<u32>(__shfl(static_cast<int>(m16), static_cast<int>(l0 + r), kWave))) << (16 * r);
+        if ((lane_id() & 3u) == 0 && first < n)
+            ids[first / 64] = WinnerBlock{bits, static_cast<u32>(id0 + off), 0u};
+        if (id_limit && blockIdx.x == 0 && threadIdx.x == 0)
+            *id_limit = ~u64{0};
+    }
 #pragma unroll
     for (int k = 0; k < kFlagsPerThread; ++k)
-    {
-        ids[k] = ~0u;
         if ((w[k / 4] >> (8 * (k % 4))) & 1)
-        {
-            ids[k] = static_cast<u32>(id0 + off);
-            if (id_of && !whole)
-                id_of[first + k] = ids[k];
             list[off++] = static_cast<u32>(first + k);
-        }
-    }
-    if (whole)
-    {
-        uint4* d = reinterpret_cast<uint4*>(id_of + first);
-#pragma unroll
-        for (int k = 0; k < kFlagsPerThread / 4; ++k)
-            d[k] = uint4{ids[4 * k], ids[4 * k + 1], ids[4 * k + 2], ids[4 * k + 3]};
-    }
     if (full)
     {
         if (s != kFlagsPerThread)
@@ -291,8 +290,8 @@ __global__ __launch_bounds__(kScanBlock) void k_winner_list(u8* __restrict__ fla
 }
 }  // namespace
 
-void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u32* id_of, u8* is_new,
-                        hipStream_t stream)
+void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, WinnerBlock* ids,
+                        u64* id_limit, u8* is_new, hipStream_t stream)
 {
     const u64 nb = (n + kFlagsPerBlock - 1) / kFlagsPerBlock;
     // up to 1024 blocks (2^22 flags), each block adds up the block sums before it (at most 8 KiB, from L2) instead of a
@@ -303,13 +302,13 @@ void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* t
     if (nb > 0 && nb <= kFusedBlocks)
     {
         hipLaunchKernelGGL(k_winner_list<true>, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, total_base, list,
-                           id_of, is_new, total);
+                           ids, id_limit, is_new, total);
         return;
     }
     hipLaunchKernelGGL(k_scan_sums_rel, dim3(1), dim3(1024), 0, stream, scratch, nb, total, total_base);
     if (nb > 0)
         hipLaunchKernelGGL(k_winner_list<false>, dim3(static_cast<u32>(nb)), dim3(kScanBlock), 0, stream, flags, n, scratch, total_base,
-                           list, id_of, is_new, total);
+                           list, ids, id_limit, is_new, total);
 }
 
 void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch, u64* total, hipStream_t stream, const u64* base)

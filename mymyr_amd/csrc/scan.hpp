@@ -86,9 +86,26 @@ void launch_exclusive_scan(const u32* counts, u64* offsets, u64 n, u64* scratch,
                            const u64* base = nullptr);
 constexpr u64 scan_scratch_words(u64 n) { return (n + 1023) / 1024 + 2; }
 
+/// The ids of the winners among 64 consecutive candidates of a batch: bit t of `bits` marks candidate 64k + t a winner
+/// and `base` is the id of the block's first winner. Winners take consecutive ids in candidate order, so a winner's id
+/// is base + the winners before it in the block: 16 bytes per 64 candidates where an id per candidate takes 256.
+struct alignas(16) WinnerBlock
+{
+    u64 bits;
+    u32 base;
+    u32 reserved;
+};
+constexpr u64 winner_blocks(u64 n) { return (n + 63) / 64; }
+/// The id of winner j (j's bit set in its block b = blocks[j / 64]).
+__host__ __device__ inline u64 winner_id(const WinnerBlock& b, u32 j)
+{
+    return b.base + static_cast<u64>(__builtin_popcountll(b.bits & ((u64{1} << (j & 63)) - 1)));
+}
+
 /// The indices j of the nonzero flags in order into list[0, winners) (flag bytes are 0 or 1; zero flags are reset to 1),
-/// id_of[j] = *total_base + rank for the winners (optional), is_new[j] = flags[j] (optional), and *total = *total_base +
-/// winners. Three launches; scratch as for launch_exclusive_scan. flags must be 16-byte aligned.
-void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, u32* id_of, u8* is_new,
-                        hipStream_t stream);
+/// the winners' ids as WinnerBlocks from *total_base on (optional; *id_limit, when given, is reset to ~0 for a cut to
+/// lower), is_new[j] = flags[j] (optional), and *total = *total_base + winners. Three launches; scratch as for
+/// launch_exclusive_scan. flags must be 16-byte aligned.
+void launch_winner_list(u8* flags, u64 n, u64* scratch, u64* total, const u64* total_base, u32* list, WinnerBlock* ids,
+                        u64* id_limit, u8* is_new, hipStream_t stream);
 }  // namespace mya

@@ -122,7 +122,8 @@ __global__ __launch_bounds__(kBlock) void k_resolve_ids(StateSetView s, const u6
 }
 
 // Settles every candidate-coded entry to id + 1 (two entries per thread per step).
-__global__ __launch_bounds__(kBlock) void k_settle(u64* __restrict__ table, u64 capacity, const u32* __restrict__ id_of, u64 stride)
+__global__ __launch_bounds__(kBlock) void k_settle(u64* __restrict__ table, u64 capacity, const WinnerBlock* __restrict__ id_map, u64 stride,
+                                                  const u64* __restrict__ id_limit)
 {
     const u64 pairs = capacity / 2;
     for (u64 i = static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x; i < pairs; i += static_cast<u64>(gridDim.x) * kBlock)
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(kBlock) void k_settle(u64* __restrict__ table, u64 
             const u32 code = static_cast<u32>(e[k]);
             if (code & kPending)
             {
-                e[k] = (e[k] & 0xFFFFFFFF00000000ull) | (id_of[code_epoch(code) * stride + (code & kJMask)] + 1u);
+                e[k] = (e[k] & 0xFFFFFFFF00000000ull) | (epoch_winner_id(id_map, stride, id_limit, code_epoch(code), code & kJMask) + 1u);
                 dirty = true;
             }
         }
@@ -144,15 +145,13 @@ __global__ __launch_bounds__(kBlock) void k_settle(u64* __restrict__ table, u64 
     }
 }
 
-/// The epoch ids of the winners list[kept, winners) of a cut batch: an id past every arena (sets hold fewer than
-/// 2^31 - 2 states), so their entries match nothing, also once settled (code id + 1 keeps the pending bit clear).
-__global__ __launch_bounds__(kBlock) void k_forget_winners(const u32* __restrict__ list, u64 kept, u64 winners, u32* __restrict__ id_of)
+/// A cut batch keeps the winners below the set's new size: ids from `size` on stand for kCutId (an id past every arena, so
+/// their entries match nothing, also once settled: code id + 1 keeps the pending bit clear).
+__global__ void k_cut_words(u64* __restrict__ size_now, u64* __restrict__ limit, u64 size)
 {
-    for (u64 w = kept + static_cast<u64>(blockIdx.x) * kBlock + threadIdx.x; w < winners; w += static_cast<u64>(gridDim.x) * kBlock)
-        id_of[list[w]] = 0x7FFFFFFEu;
+    *size_now = size;
+    *limit = size;
 }
-
-__global__ void k_set_size(u64* __restrict__ size, u64 v) { *size = v; }
 
 __global__ __launch_bounds__(kBlock) void k_fill_u32(u32* __restrict__ p, u64 n, u32 v)
 {
@@ -328,11 +327,14 @@ void state_set_create(StateSet& s, u64 max_states, u32 words, double max_load, u
     s.v.capacity = cap;
     s.max_states = max_states;
     s.batch_cap = std::clamp<u64>(batch_cap, 1, kMaxBatch);
-    // epochs in rotation: as many as fit 2 GiB of id maps (the 2^25-candidate batches of the BrFS: 16), at least 4
-    s.epochs = static_cast<u32>(std::clamp<u64>((u64{1} << 31) / (s.batch_cap * sizeof(u32)), 4, kMaxEpochs));
-    s.id_of = dev_alloc<u32>(s.epochs * s.batch_cap, "state set epoch ids");
-    s.v.id_of = s.id_of;
-    s.v.id_stride = s.batch_cap;
+    // epochs in rotation: as many as fit 512 MiB of id maps (the 2^25-candidate batches of the BrFS: 64), at least 4
+    const u64 blocks = winner_blocks(s.batch_cap);
+    s.epochs = static_cast<u32>(std::clamp<u64>((u64{1} << 29) / (blocks * sizeof(WinnerBlock)), 4, kMaxEpochs));
+    s.id_map = dev_alloc<WinnerBlock>(s.epochs * blocks, "state set epoch ids");
+    s.id_limit = dev_alloc<u64>(s.epochs, "state set epoch cuts");
+    s.v.id_map = s.id_map;
+    s.v.id_limit = s.id_limit;
+    s.v.id_stride = blocks;
     s.v.max_rows = max_states;
     s.v.table = dev_alloc<u64>(cap, "state set table");
     s.v.arena = dev_alloc<u64>(max_states * words, "state set arena");
@@ -351,7 +353,8 @@ void state_set_destroy(StateSet& s, hipStream_t stream)
 {
     for (void* p : {static_cast<void*>(s.v.table), static_cast<void*>(s.v.arena), static_cast<void*>(s.cand_slot),
                     static_cast<void*>(s.flags), static_cast<void*>(s.list), static_cast<void*>(s.scan_scratch),
-                    static_cast<void*>(s.d_size), static_cast<void*>(s.d_status), static_cast<void*>(s.id_of)})
+                    static_cast<void*>(s.d_size), static_cast<void*>(s.d_status), static_cast<void*>(s.id_map),
+                    static_cast<void*>(s.id_limit)})
     {
         if (stream)
             dev_free_async(p, stream);
@@ -387,7 +390,7 @@ void state_set_begin_batch(StateSet& s, hipStream_t stream)
     {
         // every epoch is taken: one streaming pass settles all candidate-coded entries, and the rotation restarts
         hipLaunchKernelGGL(k_settle, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(s.v.capacity / 2, kBlock), 8192))), dim3(kBlock),
-                           0, stream, s.v.table, s.v.capacity, s.id_of, s.batch_cap);
+                           0, stream, s.v.table, s.v.capacity, s.id_map, s.v.id_stride, s.id_limit);
         launch_check("state set settle");
         s.batches = 0;
     }
@@ -397,7 +400,7 @@ void state_set_begin_batch(StateSet& s, hipStream_t stream)
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new)
 {
     launch_winner_list(s.flags, n, s.scan_scratch, state_set_size_next(s), state_set_size_now(s), s.list,
-                       s.id_of + static_cast<u64>(s.v.epoch) * s.batch_cap, is_new, stream);
+                       s.id_map + static_cast<u64>(s.v.epoch) * s.v.id_stride, s.id_limit + s.v.epoch, is_new, stream);
     launch_check("state set rank");
 }
 
@@ -409,12 +412,9 @@ void state_set_resolve_ids(StateSet& s, const u64* cand_slot, u64 n, i64* ids, h
     launch_check("state set ids");
 }
 
-void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t stream)
+void state_set_cut(StateSet& s, u64 size, hipStream_t stream)
 {
-    if (winners > kept)
-        hipLaunchKernelGGL(k_forget_winners, dim3(static_cast<unsigned>(std::min<u64>(blocks_for(winners - kept, kBlock), 4096))), dim3(kBlock),
-                           0, stream, s.list, kept, winners, s.id_of + static_cast<u64>(s.v.epoch) * s.batch_cap);
-    hipLaunchKernelGGL(k_set_size, dim3(1), dim3(1), 0, stream, state_set_size_now(s), size);
+    hipLaunchKernelGGL(k_cut_words, dim3(1), dim3(1), 0, stream, state_set_size_now(s), s.id_limit + s.v.epoch, size);
     launch_check("state set cut");
     s.size = size;
 }

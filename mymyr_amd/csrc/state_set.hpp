@@ -11,8 +11,8 @@
 // tag = its high 32 bits, linear probing.
 //
 // A batch is three steps on one stream: probe (group of lanes per row: hash, probe, CAS or atomicMin, loser flags),
-// the winner list (a scan of the flags: winner w gets id = the set's size + w, recorded per candidate in the batch's
-// epoch of id_of), and compaction over the winners (rows into the arena; the entries keep their epoch codes). The set's size lives on the device in two words used alternately (the scan of a batch
+// the winner list (a scan of the flags: winner w gets id = the set's size + w, recorded as winner bits and a first id
+// per 64 candidates in the batch's epoch of id_map), and compaction over the winners (rows into the arena; the entries keep their epoch codes). The set's size lives on the device in two words used alternately (the scan of a batch
 // writes next = current + winners), so batches need no host synchronization; the host copy is refreshed by the
 // calls that synchronize.
 
@@ -37,7 +37,8 @@ struct StateSet
     u64* h_pinned = nullptr;   // [4] size before, size after, status of the last insert
     int cur = 0;               // d_size[cur] is the current size
     hipStream_t last = nullptr;
-    u32* id_of = nullptr;      // [epochs, batch_cap] winner ids per epoch (v.id_of)
+    WinnerBlock* id_map = nullptr;  // [epochs, winner_blocks(batch_cap)] winner ids per epoch (v.id_map)
+    u64* id_limit = nullptr;        // [epochs] the epochs' cut ids (v.id_limit)
     u32 epochs = 0;            // epochs in rotation (at most kMaxEpochs)
     u64 batches = 0;           // epochs taken since the last clear or settling pass
 };
@@ -73,13 +74,13 @@ inline u64* state_set_size_next(StateSet& s) { return s.d_size + (s.cur ^ 1); }
 inline void state_set_flip(StateSet& s) { s.cur ^= 1; }
 
 /// The winners of a batch of n candidates in order into s.list (losers' flags reset), their ids into the batch's
-/// epoch of id_of, is_new[j] (optional) the flags, and next size = size + winners.
+/// epoch of id_map, is_new[j] (optional) the flags, and next size = size + winners.
 void state_set_rank(StateSet& s, u64 n, hipStream_t stream, u8* is_new = nullptr);
 
-/// A cut inside the last ranked batch whose search goes on (a BrFS layer cut by max_next_layer_states): of its
-/// `winners` winners only the first `kept` are stored, so the set's size becomes `size` and the table entries of the
-/// others (pending codes of the batch's epoch) stand for no state from now on (their epoch ids point past the arena).
-void state_set_cut(StateSet& s, u64 size, u64 kept, u64 winners, hipStream_t stream);
+/// A cut inside the last ranked batch whose search goes on (a BrFS layer cut by max_next_layer_states): only the
+/// batch's winners below `size` are stored, so the set's size becomes `size` and the table entries of the others
+/// (pending codes of the batch's epoch) stand for no state from now on (the epoch's ids from `size` on are cut).
+void state_set_cut(StateSet& s, u64 size, hipStream_t stream);
 
 /// The probe of a batch begun with state_set_begin_batch over candidate rows [m, words] (device) that the caller produced:
 /// a stored equal row drops a candidate, equal candidates keep the smallest index, the others take pending entries

@@ -53,15 +53,25 @@ struct StateSetView
     u64* arena;         // [max_rows, words]
     u32 words;
     u32 epoch;          // the epoch of the batch being inserted
-    const u32* id_of;   // [epochs, id_stride]: the id of each batch winner j of the epoch (written by the winner list)
-    u64 id_stride;
+    const WinnerBlock* id_map;  // [epochs, id_stride]: the ids of each epoch's batch winners (written by the winner list)
+    u64 id_stride;              // winner blocks per epoch
+    const u64* id_limit;        // [epochs]: ids at or past an epoch's limit were cut (they stand for no stored state)
     u64 max_rows;       // rows of the arena: ids at or past it were never stored
 };
+
+/// The id candidate j of epoch e's batch (a winner) took, or kCutId past the epoch's cut.
+constexpr u64 kCutId = 0x7FFFFFFEu;  // past every arena (sets hold fewer than 2^31 - 2 states): matches nothing
+__host__ __device__ inline u64 epoch_winner_id(const WinnerBlock* id_map, u64 stride, const u64* id_limit, u32 e, u32 j)
+{
+    const u64 id = winner_id(id_map[e * stride + (j >> 6)], j);
+    return id < id_limit[e] ? id : kCutId;
+}
 
 /// The id a committed entry code stands for: id + 1 for settled codes, the epoch's winner id for candidate codes.
 __device__ __forceinline__ u64 committed_id(const StateSetView& s, u32 code)
 {
-    return (code & kPending) ? s.id_of[code_epoch(code) * s.id_stride + (code & kJMask)] : static_cast<u64>(code) - 1;
+    return (code & kPending) ? epoch_winner_id(s.id_map, s.id_stride, s.id_limit, code_epoch(code), code & kJMask)
+                             : static_cast<u64>(code) - 1;
 }
 
 /// cand_slot encodings written by the probe: (tag << 32) | slot for a candidate that holds or held a pending entry;
