@@ -11,10 +11,10 @@
 // smallest candidate index wins (64-bit atomicMin on the pending entry), new ids follow candidate order.
 //
 // Entries are never rewritten after the probe: a batch's pending entries keep the candidate code of their winner, and
-// the batch's epoch (one of up to 64, 6 bits of the code) maps candidate indices to ids through id_of, written by the
-// winner list. When every epoch is taken, one streaming pass settles all entries to id + 1. This trades the random
-// 8-byte rewrite of every new state's entry (a read-modify-write of a memory line) for a 4-byte id_of read on the
-// probes that compare against a recent state.
+// the batch's epoch (one of up to 64, 6 bits of the code) maps candidate indices to ids through its winner blocks,
+// written by the winner list. When every epoch is taken, one streaming pass settles all entries to id + 1. This trades
+// the random 8-byte rewrite of every new state's entry (a read-modify-write of a memory line) for a 16-byte winner-block
+// read on the probes that compare against a recent state.
 //
 // Winner flags need no second pass over the table: every candidate starts at flag 1 (the winner list of the previous
 // batch resets the zeros), and only zeros are written during the probe: a candidate equal to a stored state, a candidate
@@ -486,7 +486,7 @@ __device__ __forceinline__ bool group_blocked(const BlockedView& b, const Slice<
 
 /// Winner w of the batch (candidate j = list[w], id = id0 + w): below `limit` its row into the arena; at or past it,
 /// kStatusCapacity (and is_new[j] = 0). The winner's table entry keeps its candidate code: the batch's epoch maps it to
-/// the id (id_of), so no entry is rewritten.
+/// the id (its winner block), so no entry is rewritten.
 template<int G, int K, class Src>
 __device__ __forceinline__ void compact_winner(const StateSetView& s, const Src& src, u64 w, u32 q, const u32* __restrict__ list,
                                                u64 id0, u64 limit, u8* __restrict__ is_new, u32* __restrict__ status)
