@@ -32,7 +32,7 @@ typedef struct mya_hashset mya_hashset;
 const char* mya_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
-#define MYA_ABI_VERSION 19
+#define MYA_ABI_VERSION 20
 int mya_abi_version(void);
 
 /* Device memory held by the library (replaces DeviceContext::usage(), include/mymyr/cuda/runtime.hpp:140-146, 183):
@@ -521,6 +521,14 @@ typedef struct mya_brfs_options
     int32_t beam_novelty;
     void (*layer_scorer)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, double* scores);
     void* layer_scorer_user;
+    /* BrfsOptions::goal as GoalSpec::Custom (include/mymyr/search/control.hpp:99-121): goal_test(user, rows, n, words,
+     * out) sets out[i] to 1 when host row i ([n, words], the task's slot layout) is a goal state and to 0 otherwise;
+     * a nonzero return stops the search with an error. It decides instead of the task's goal and of goal_kind (which
+     * must be 0). The ground search calls it on each batch of parents it counts, the lifted one on each layer before
+     * expanding it; a state is tested before its expansion, as the reference tests a state popped for expansion
+     * (src/mymyr/search/brfs.cpp:332-339). Null: none. */
+    int32_t (*goal_test)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, uint8_t* out);
+    void* goal_test_user;
 } mya_brfs_options;
 #define MYA_GOAL_LITERAL_INTS 9
 

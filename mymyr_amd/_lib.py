@@ -12,7 +12,7 @@ from ctypes import POINTER, Structure, c_char_p, c_double, c_int, c_int32, c_int
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmymyr_amd.so")
-ABI_VERSION = 19  # MYA_ABI_VERSION of include/mymyr_amd.h
+ABI_VERSION = 20  # MYA_ABI_VERSION of include/mymyr_amd.h
 
 
 class MyaError(RuntimeError):
@@ -101,6 +101,7 @@ class StepOutputs(Structure):
 
 # BrfsOptions::layers' scorer: (user, rows [n, words], n, words, scores [n])
 LAYER_SCORER = ctypes.CFUNCTYPE(None, c_void_p, POINTER(c_uint64), c_uint64, c_uint32, POINTER(c_double))
+GOAL_TEST = ctypes.CFUNCTYPE(ctypes.c_int32, c_void_p, POINTER(c_uint64), c_uint64, c_uint32, POINTER(ctypes.c_uint8))
 
 
 class BrfsOptions(Structure):
@@ -137,6 +138,8 @@ class BrfsOptions(Structure):
         ("beam_novelty", c_int32),
         ("layer_scorer", LAYER_SCORER),
         ("layer_scorer_user", c_void_p),
+        ("goal_test", GOAL_TEST),
+        ("goal_test_user", c_void_p),
     ]
 
 

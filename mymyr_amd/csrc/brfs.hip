@@ -988,6 +988,8 @@ BrfsResultC run(const CompiledTask& task, const BrfsTables& tb, const BrfsOption
                 hipLaunchKernelGGL(k_ground_count<W>, dim3(blocks_for(nb, kTW * kWave)), dim3(kTW * kWave), 0, stream, par, pbase + counted,
                                    static_cast<u32>(nb), g, goal, counts + counted * S, goal_flags + counted);
                 launch_check("ground count");
+                if (o.goal_test)
+                    custom_goal_flags(o, par + (pbase + counted) * W, nb, W, goal_flags + counted, stream);
                 tm.end(kKCount, nb * (R + 5));
                 tm.begin(kKOther);
                 launch_exclusive_scan(counts + counted * S, offsets + counted * S, nb * S, scan_scratch, offsets + (counted + nb) * S, stream,

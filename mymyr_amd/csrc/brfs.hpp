@@ -61,7 +61,13 @@ struct BrfsOptionsC
     bool randomize_ties = false;
     // scored layers: scores[i] of the layer's rows [n, words] (host), lower first
     std::function<void(const u64* rows, u64 n, u32 words, double* scores)> scorer;
+    // GoalSpec::Custom: out[i] = whether host row i of [n, words] is a goal (instead of the task's goal or any_of); false
+    // from it is an error that stops the search
+    std::function<bool(const u64* rows, u64 n, u32 words, u8* out)> goal_test;
 };
+
+/// The custom goal test of rows [n, words] on the device into goal flags (device): a host round trip (BrfsOptionsC::goal_test).
+void custom_goal_flags(const BrfsOptionsC& o, const u64* rows, u64 n, u32 words, u8* flags, hipStream_t stream);
 
 /// Whether one of the AnyOf goals holds in a row of `words` words (host).
 bool any_of_holds(const BrfsOptionsC& o, const u64* row, u32 words);

@@ -117,6 +117,25 @@ bool goal_holds(const CompiledTask& task, const std::vector<u64>& row)
 
 }  // namespace
 
+void custom_goal_flags(const BrfsOptionsC& o, const u64* rows, u64 n, u32 words, u8* flags, hipStream_t stream)
+{
+    // in pieces of at most 2^20 rows, so that the host copies stay bounded
+    constexpr u64 kPiece = u64{1} << 20;
+    std::vector<u8> f;
+    for (u64 i0 = 0; i0 < n; i0 += kPiece)
+    {
+        const u64 m = std::min(kPiece, n - i0);
+        const std::vector<u64> h = to_host(rows + i0 * words, m * words, stream);
+        f.assign(m, 0);
+        if (!o.goal_test(h.data(), m, words, f.data()))
+            throw std::runtime_error("mymyr_amd: brfs: the goal test failed");
+        for (u8& x : f)
+            x = x ? 1 : 0;
+        hip_check(hipMemcpyAsync(flags + i0, f.data(), m, hipMemcpyHostToDevice, stream), "goal flags");
+        hip_check(hipStreamSynchronize(stream), "goal flags");
+    }
+}
+
 bool any_of_holds(const BrfsOptionsC& o, const u64* row, u32 words)
 {
     auto bit = [&](u32 s) { return s / 64 < words && ((row[s / 64] >> (s % 64)) & 1); };
@@ -311,6 +330,8 @@ BrfsResultC brfs_wide(const CompiledTask& task, const TaskDev& dev, const BrfsOp
         // (positions below are then expansion positions)
         const bool ordered = lorder.ordered() && lb > 0;
         u64 keep = ln;
+        if (o.goal_test)
+            custom_goal_flags(o, set.v.arena + lb * W, ln, W, goal_id + lb, stream);
         const u8* gflags = goal_id + lb;
         if (ordered)
         {

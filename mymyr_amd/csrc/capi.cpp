@@ -359,6 +359,16 @@ u32 intern_goal_atom(mya_task* t, u64 cid)
 void resolve_any_of(mya_task* task, const mya_brfs_options& op, BrfsOptionsC& o)
 {
     const CompiledTask& C = *task->compiled;
+    if (op.goal_test)
+    {
+        // GoalSpec::Custom: the caller's test decides (brfs.cpp:43-52)
+        if (op.goal_kind != 0)
+            throw std::invalid_argument("mymyr_amd: brfs: a custom goal test takes goal_kind 0 (no goal conditions)");
+        auto fn = op.goal_test;
+        void* user = op.goal_test_user;
+        o.goal_test = [fn, user](const u64* rows, u64 n, u32 words, u8* out) { return fn(user, rows, n, words, out) == 0; };
+        return;
+    }
     if (op.goal_kind == 0)
         return;
     if (op.goal_kind != 1)
@@ -551,7 +561,7 @@ int mya_brfs(mya_task* task, const mya_brfs_options* options, mya_brfs_result* r
         std::vector<std::array<u64, 3>> lc;
         BrfsResultC r;
         bool searched = true;
-        if (o.stop_at_goal && !o.any_of && task->compiled->goal_fixed_unsat)
+        if (o.stop_at_goal && !o.any_of && !o.goal_test && task->compiled->goal_fixed_unsat)
         {
             // the task's goal fails in every state: the start state alone, nothing expanded (brfs.cpp:1851-1861)
             r.status = kUnsolvable;

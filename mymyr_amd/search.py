@@ -309,6 +309,28 @@ def _rows(task: Task, rows, what: str) -> np.ndarray:
     return a
 
 
+class _GoalTest:
+    """A callable goal (state words -> bool) as the C goal test: each row of a batch is passed as a uint64 array of the
+    task's words (the reference passes its State view); the first exception stops the search and is raised again."""
+
+    def __init__(self, fn):
+        self.fn, self.error = fn, None
+
+        def call(_user, rows, n, words, out):
+            if self.error is not None:
+                return 1
+            try:
+                a = np.ctypeslib.as_array(rows, shape=(n, words))
+                for i in range(n):
+                    out[i] = 1 if self.fn(a[i].copy()) else 0
+                return 0
+            except BaseException as e:  # noqa: BLE001 (raised again after the search)
+                self.error = e
+                return 1
+
+        self.c = _lib.GOAL_TEST(call)
+
+
 def _goal_records(task: Task, goal) -> tuple[np.ndarray, np.ndarray]:
     """AnyOf goal conditions as the C ABI's offsets [k + 1] and literal records (predicate, positive, object count,
     objects). A condition is a sequence of (predicate index, positive, objects) literals."""
@@ -344,7 +366,9 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     goal (None: the task's goal): BrfsOptions::goal as GoalSpec::AnyOf, a sequence of ground conditions, each a sequence
     of (predicate index, positive, object indices) literals; a state is a goal iff one of them holds in it (the
     reference's goal= with GroundConditions, python/src/search_bindings.cpp:439-505; conditions that can never hold are
-    left out).
+    left out). Or a callable (GoalSpec::Custom, python/src/search_bindings.cpp:444-448; threads=1): goal(words) -> bool
+    on a state's uint64 words in the task's slot layout (the reference passes its State view), called on each state
+    before it is expanded; an exception in it stops the search and is raised again.
     observer (an :class:`Observer`, or any object with some of its methods) and progress_interval (expansions between
     on_progress calls; None: 2^16): BrfsOptions::observer and progress_interval (include/mymyr/search/brfs.hpp:99-100).
     layer_order, seed, max_next_layer_states, prefer_more_satisfied_goals, beam_width, beam_novelty, randomize_ties and
@@ -372,7 +396,15 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     bl = None if blocked_states is None else _rows(task, np.zeros((0, task.words), np.uint64) if len(blocked_states) == 0
                                                    else blocked_states, "blocked_states")
     timed = max_seconds is not None and np.isfinite(max_seconds)
-    go, gl = _goal_records(task, goal) if goal is not None else (None, None)
+    goal_test = None
+    if goal is not None and callable(goal) and not isinstance(goal, (str, bytes)):
+        # GoalSpec::Custom: the callable decides on each state's words (python/src/search_bindings.cpp:444-448)
+        if int(threads) > 1:
+            raise ValueError("mymyr brfs: a custom goal test needs threads == 1 and a test function")
+        goal_test = _GoalTest(goal)
+        go, gl = None, None
+    else:
+        go, gl = _goal_records(task, goal) if goal is not None else (None, None)
     if progress_interval is not None and not 0 <= int(progress_interval) < (1 << 64):
         raise ValueError("mymyr_amd: brfs: progress_interval must be a non-negative 64-bit count")
     bridge = _ObserverBridge(observer, (1 << 16) if progress_interval is None else int(progress_interval)) if observer is not None else None
@@ -385,10 +417,11 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
                          int(stop_at_goal), int(fingerprint), chunk, memory_states, int(timings), 0,
                          None if st is None else st.ctypes.data, None if bl is None or bl.shape[0] == 0 else bl.ctypes.data,
                          0 if bl is None else bl.shape[0], task.words, int(timed), float(max_seconds) if timed else 0.0,
-                         None if cancel is None else cancel.address, 0 if goal is None else 1, 0 if goal is None else len(go) - 1,
+                         None if cancel is None else cancel.address, 0 if go is None else 1, 0 if go is None else len(go) - 1,
                          None if go is None else go.ctypes.data, None if gl is None or gl.size == 0 else gl.ctypes.data,
                          None if bridge is None else ctypes.addressof(bridge.c), 1, lay.kind, int(not prefer_more_satisfied_goals),
-                         lay.seed, lay.limit, lay.beam, int(bool(randomize_ties)), lay.novelty, lay.c_scorer, None)
+                         lay.seed, lay.limit, lay.beam, int(bool(randomize_ties)), lay.novelty, lay.c_scorer, None,
+                         _lib.GOAL_TEST() if goal_test is None else goal_test.c, None)
     r = _lib.BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)
@@ -399,6 +432,8 @@ def brfs(task: Task, max_depth: int | None = None, max_states: int | None = None
     gs = np.zeros(max(1, task.words if task.frozen else (task.dense_fluent + 63) // 64), np.uint64)
     plan = _lib.BrfsPlan(ps.ctypes.data, pb.ctypes.data, cap, L, gs.ctypes.data, gs.size, 0, 0, 0, 0.0)
     n = lib.mya_brfs(task.handle, ctypes.byref(o), ctypes.byref(r), lc.ctypes.data, 4096, ctypes.byref(plan))
+    if goal_test is not None and goal_test.error is not None:
+        raise goal_test.error
     if lay.error is not None:
         raise lay.error
     if n < 0:

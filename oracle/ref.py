@@ -62,10 +62,12 @@ class BrfsOptions(Structure):
         ("record_events", c_int32),
         ("scorer", ctypes.CFUNCTYPE(None, c_void_p, ctypes.POINTER(c_uint64), c_uint64, c_uint32, ctypes.POINTER(ctypes.c_double))),
         ("scorer_user", c_void_p),
+        ("goal_mod", c_uint64),
+        ("goal_res", c_uint64),
     ]
 
 
-SCORER = BrfsOptions._fields_[-2][1]
+SCORER = dict(BrfsOptions._fields_)["scorer"]
 LAYER_KINDS = {"queue": 0, "in_order": 1, "reverse": 2, "randomized": 3, "goal_count": 4}
 
 
@@ -467,15 +469,18 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
          stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf"),
          goal=None, layer_order="queue", seed=0, max_next_layer_states=None, prefer_more_satisfied_goals=True, beam_width=None,
-         randomize_ties=False, record_events=False):
+         randomize_ties=False, record_events=False, goal_hash=None):
     """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
     (schema, binding) pairs, the goal state's words and the cost; the result's words, fluent_slots, threads_used, store
     and message. start [words] and blocked_states [k, words] are rows of the task's table words; goal (None: the task's)
-    is BrfsOptions::goal = search::any_of over ground conditions, each a list of (predicate, positive, objects)."""
+    is BrfsOptions::goal = search::any_of over ground conditions, each a list of (predicate, positive, objects);
+    goal_hash = (m, r) makes it a custom goal test instead (GoalSpec::Custom): hash_state(state) % m == r."""
+    if goal_hash is not None:
+        goal = []
     W = task.table_words
     st = None if start is None else np.ascontiguousarray(np.asarray(start, np.uint64).reshape(-1)[:W])
     bl = None if blocked_states is None else np.ascontiguousarray(np.asarray(blocked_states, np.uint64).reshape(-1, W))
-    go, gl = goal_records(goal) if goal is not None else (None, None)
+    go, gl = goal_records(goal) if goal is not None and goal_hash is None else (None, None)
     if callable(layer_order):
         score = layer_order
 
@@ -489,8 +494,10 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         kind, cb = LAYER_KINDS[layer_order], SCORER()
     o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
                     max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds,
-                    0 if goal is None else 1, 0 if goal is None else len(goal), _p(go), _p(gl), kind, int(not prefer_more_satisfied_goals),
-                    seed, max_next_layer_states or 0, beam_width or 0, int(randomize_ties), int(record_events), cb, None)
+                    0 if goal is None else (2 if goal_hash is not None else 1), 0 if goal is None or goal_hash is not None else len(goal),
+                    _p(go), _p(gl), kind, int(not prefer_more_satisfied_goals),
+                    seed, max_next_layer_states or 0, beam_width or 0, int(randomize_ties), int(record_events), cb, None,
+                    goal_hash[0] if goal_hash else 0, goal_hash[1] if goal_hash else 0)
     r = BrfsResult()
     lc = np.zeros((4096, 3), dtype=np.uint64)
     L = max(1, task.label_width)

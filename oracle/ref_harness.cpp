@@ -130,6 +130,10 @@ struct mref_brfs_options
     int32_t record_events;  // record the observer's events (mref_brfs_events)
     void (*scorer)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, double* scores);
     void* scorer_user;
+    // goal_kind 2: GoalSpec::Custom, a state is a goal iff its hash_state % goal_mod == goal_res (a test that no atom
+    // goal expresses)
+    uint64_t goal_mod;
+    uint64_t goal_res;
 };
 
 namespace
@@ -827,6 +831,12 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
                         conds[k].literals.push_back(std::move(gl));
                     }
                 b.goal = search::any_of(*t->task, conds);
+            }
+            else if (o->goal_kind == 2)
+            {
+                b.goal.kind = search::GoalSpec::Kind::Custom;
+                const uint64_t m = o->goal_mod, res = o->goal_res;
+                b.goal.test = [m, res](StateView s) { return s.hash() % m == res; };
             }
             b.canonical_order = o->canonical_order != 0;
             b.stop_at_goal = o->stop_at_goal != 0;

@@ -725,6 +725,28 @@ def make_brfs_edges():
     dump("brfs_edges.json", out)
 
 
+# BrfsOptions::goal as GoalSpec::Custom: a state is a goal iff hash_state(state) % m == r (no atom goal expresses it),
+# through the ground driver (gripper) and the wide one (20-word transport rows)
+CUSTOM_GOAL_CASES = {
+    "gripper__prob05:goal": ("gripper__prob05", (1000, 7), dict(stop_at_goal=True)),
+    "gripper__prob05:all": ("gripper__prob05", (1000, 7), dict(stop_at_goal=False)),
+    "gripper__prob05:cut": ("gripper__prob05", (97, 5), dict(stop_at_goal=False, max_states=30000)),
+    "transport_w20_3:goal": ("transport_w20_3", (500, 3), dict(stop_at_goal=True)),
+    "transport_w20_3:cut": ("transport_w20_3", (61, 2), dict(stop_at_goal=False, max_states=40000)),
+}
+
+
+def make_brfs_custom_goal():
+    """The reference brfs() with a custom goal test (brfs_custom_goal.json)."""
+    out = {}
+    for key, (name, gh, kw) in CUSTOM_GOAL_CASES.items():
+        r = brfs_record(name, "auto", goal_hash=gh, **kw)
+        r["goal_hash"] = list(gh)
+        out[key] = r
+        print(key, r["states"], r["expanded"], r["goal_states"], r["status"], len(r.get("plan", [])), flush=True)
+    dump("brfs_custom_goal.json", out)
+
+
 def make_brfs_strips_large():
     """Adds the strips workload's cut at max_states = 2^28 to brfs.json (the single-threaded reference search: about
     1.2 G successors and 25 GB of host memory, some 20 minutes), keeping the existing records."""
@@ -887,7 +909,8 @@ def main():
              "brfs_suite_add": make_brfs_suite_add, "brfs_layers": make_brfs_layers, "brfs_long": make_brfs_long,
              "brfs_events": make_brfs_events, "brfs_strips_large": make_brfs_strips_large,
              "brfs_edges": make_brfs_edges, "env_batch": make_env_batch,
-             "instance_draw_edges": make_instance_draw_edges}
+             "instance_draw_edges": make_instance_draw_edges,
+             "brfs_custom_goal": make_brfs_custom_goal}
     for k, f in steps.items():
         if not a.only or k in a.only.split(","):
             f()

@@ -136,6 +136,54 @@ def test_strips_workload_cuts(golden):
         assert not same(r, exp), (key, same(r, exp))
 
 
+def custom_goal_keys():
+    from tests.golden import fixtures
+
+    return sorted(fixtures.load("brfs_custom_goal.json"))
+
+
+@pytest.mark.parametrize("key", custom_goal_keys())
+def test_custom_goal_test(golden, key):
+    """BrfsOptions::goal as a callable (GoalSpec::Custom): a state is a goal iff its hash_state % m == r, which no atom
+    goal expresses, through the ground driver (gripper) and the wide one (20-word rows), with the goal stop, over the
+    whole space and at a cut: counts, fingerprints, statuses and plans equal to the reference's with the same test."""
+    from oracle import port
+
+    exp = golden.load("brfs_custom_goal.json")[key]
+    m, res = exp["goal_hash"]
+    calls = [0]
+
+    def goal(row):
+        calls[0] += 1
+        return port.hash_state(row) % m == res
+
+    print(f"custom goal: {key}", flush=True)
+    opts = {k: v for k, v in exp["options"].items() if k != "goal_hash"}  # the reference's form of the same test
+    r = device(golden, key.split(":")[0], "auto", full=True, goal=goal, **opts)
+    assert not same(r, exp), (key, same(r, exp))
+    assert same_plan(r, exp)
+    assert calls[0] >= exp["expanded"]  # every expanded state was tested
+
+
+def test_custom_goal_test_errors(golden):
+    """An exception in the goal test stops the search and is raised again; the threads check is the reference's."""
+    from mymyr_amd import search
+    from mymyr_amd.task import Task
+
+    t = Task.from_text_file(golden.task_path("gripper__prob05"))
+
+    class Stop(Exception):
+        pass
+
+    def goal(row):
+        raise Stop()
+
+    with pytest.raises(Stop):
+        search.brfs(t, goal=goal, stop_at_goal=False, max_states=5000)
+    # the search runs again afterwards
+    assert search.brfs(t, goal=lambda row: False, stop_at_goal=False, max_states=5000).states == 5000
+
+
 def edge_keys():
     from tests.golden import fixtures
 

@@ -161,6 +161,8 @@ def test_brfs_option_arguments_checked_on_the_host(golden):
         search.brfs(t, max_seconds=-1.0)
     with pytest.raises(TypeError, match="CancelToken"):
         search.brfs(t, cancel=True)
+    with pytest.raises(ValueError, match="custom goal test needs threads == 1"):
+        search.brfs(t, goal=lambda row: False, threads=2)
 
 
 def test_visited_mask_is_a_registered_torch_op():
