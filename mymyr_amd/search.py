@@ -5,6 +5,7 @@
 from __future__ import annotations
 
 import ctypes
+import enum
 from dataclasses import dataclass, field
 from typing import NamedTuple
 
@@ -15,6 +16,22 @@ from ._lib import check, lib
 from .task import Task
 
 STATUS = {0: "solved", 1: "exhausted", 2: "out_of_states", 3: "out_of_time", 4: "cancelled", 5: "failed", 6: "unsolvable"}
+
+
+class Status(str, enum.Enum):
+    """The reference's mymyr.search.Status (search::SearchStatus, python/src/search_bindings.cpp:2240-2248): its members
+    are the strings a result's status holds, so `result.status == Status.EXHAUSTED` reads as with the reference."""
+
+    SOLVED = "solved"
+    EXHAUSTED = "exhausted"
+    OUT_OF_STATES = "out_of_states"
+    OUT_OF_TIME = "out_of_time"
+    CANCELLED = "cancelled"
+    FAILED = "failed"
+    UNSOLVABLE = "unsolvable"
+
+    def __str__(self) -> str:
+        return self.value
 UNBOUNDED32 = 0xFFFFFFFF
 UNBOUNDED64 = (1 << 64) - 1
 
@@ -271,6 +288,13 @@ class BrfsResult:
     threads_used: int = 1   # host threads the search ran on (the calling thread; the work runs on the device)
     store: str = ""         # "device" (the device state set), "none" when nothing was searched
     message: str = ""       # why the search stopped early or ran otherwise than asked ("" if neither)
+
+    @property
+    def stats(self) -> Statistics:
+        """The search's counts and time as Statistics (the reference's result.stats, brfs_stats in
+        python/src/search_bindings.cpp:661-670): expanded, generated, states, pruned, seconds (search_s) and
+        memory_bytes."""
+        return Statistics(self.expanded, self.generated, self.states, self.pruned, self.search_s, self.memory_bytes)
 
 
 KERNEL_CLASSES = ["count", "emit", "insert", "unused", "rank", "compact", "other"]

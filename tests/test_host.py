@@ -165,6 +165,20 @@ def test_brfs_option_arguments_checked_on_the_host(golden):
         search.brfs(t, goal=lambda row: False, threads=2)
 
 
+def test_brfs_result_stats_and_status():
+    """BrfsResult.stats (the reference's result.stats: expanded, generated, states, pruned, seconds, memory_bytes) and
+    search.Status, whose members equal the result's status strings (mymyr.search.Status)."""
+    from mymyr_amd import search
+
+    r = search.BrfsResult("out_of_states", 50, 4, 61, 0, 2, False, False, 0, 0, 0.25, 0.2, pruned=3, memory_bytes=4096)
+    st = r.stats
+    assert (st.expanded, st.generated, st.states, st.pruned, st.seconds, st.memory_bytes) == (4, 61, 50, 3, 0.25, 4096)
+    assert r.status == search.Status.OUT_OF_STATES and r.status != search.Status.EXHAUSTED
+    assert [s.name for s in search.Status] == ["SOLVED", "EXHAUSTED", "OUT_OF_STATES", "OUT_OF_TIME", "CANCELLED", "FAILED",
+                                               "UNSOLVABLE"]
+    assert all(search.Status(v) == v for v in search.STATUS.values())
+
+
 def test_visited_mask_is_a_registered_torch_op():
     """rl.visited_mask is the torch op mymyr::visited_mask, with a fake implementation (bool [size]) for tracing."""
     torch = pytest.importorskip("torch")
