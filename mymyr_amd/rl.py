@@ -607,6 +607,8 @@ class EnvPool(DeviceEnvPool):
         self.dead_end = dead_end
         self.goals = goals
         self.table = table
+        self.framework = framework  # the reference's framework argument (batches are device tensors either way)
+        self.numeric_words = 0      # classical tasks: no numeric words after the atom words
         if self.sampler is not None:
             # every env starts in a sampled instance (the draw of its reset counter 0, which then stands at 1)
             check(lib.mya_env_reset(self._h, ctypes.byref(self._batch), None, self.count.data_ptr(), 0, 1, _stream()))
