@@ -105,3 +105,6 @@ def test_env_pool_samples_instances_like_the_reference_default(golden):
     assert pool.reset_counts.cpu().numpy().tolist() == [2] * 64
     still = rl.EnvPool(ts, 64, seed=5, first_env=2, sampler=None)
     assert still.reset().task_ids.cpu().numpy().tolist() == [0] * 64
+    # the reference pool's read-only properties (python/src/rl_bindings.cpp:2465-2600)
+    assert (pool.num_envs, pool.first_env, pool.seed, pool.threads, pool.goals, pool.dead_end) == (64, 2, 5, 1, False, "no_successors")
+    assert (pool.framework, pool.numeric_words, pool.max_steps, pool.pending) == (None, 0, None, 0)
