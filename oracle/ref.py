@@ -469,12 +469,16 @@ def pool_run(task: RefTask, num_envs: int, threads: int, steps: int, **cfg) -> t
 def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 1, witness_pruning=True, canonical_order=True,
          stop_at_goal=False, fingerprint=True, max_expanded=(1 << 64) - 1, start=None, blocked_states=None, max_seconds=float("inf"),
          goal=None, layer_order="queue", seed=0, max_next_layer_states=None, prefer_more_satisfied_goals=True, beam_width=None,
-         randomize_ties=False, record_events=False, goal_hash=None):
+         randomize_ties=False, record_events=False, goal_hash=None, goal_atoms=None):
     """brfs(Task, BrfsOptions) of the reference: counts, status, fingerprint, and for a solved search the plan
     (schema, binding) pairs, the goal state's words and the cost; the result's words, fluent_slots, threads_used, store
     and message. start [words] and blocked_states [k, words] are rows of the task's table words; goal (None: the task's)
     is BrfsOptions::goal = search::any_of over ground conditions, each a list of (predicate, positive, objects);
-    goal_hash = (m, r) makes it a custom goal test instead (GoalSpec::Custom): hash_state(state) % m == r."""
+    goal_hash = (m, r) makes it a custom goal test instead (GoalSpec::Custom): hash_state(state) % m == r;
+    goal_atoms = k the custom test that the state has k true atoms."""
+    if goal_atoms is not None:
+        goal_hash = (0, int(goal_atoms))
+    custom = 3 if goal_atoms is not None else 2
     if goal_hash is not None:
         goal = []
     W = task.table_words
@@ -494,7 +498,7 @@ def brfs(task: RefTask, threads=1, max_depth=0xFFFFFFFF, max_states=(1 << 64) - 
         kind, cb = LAYER_KINDS[layer_order], SCORER()
     o = BrfsOptions(threads, max_depth, max_states, int(witness_pruning), int(canonical_order), int(stop_at_goal), int(fingerprint),
                     max_expanded, _p(st), _p(bl), 0 if bl is None else bl.shape[0], W, 0, max_seconds,
-                    0 if goal is None else (2 if goal_hash is not None else 1), 0 if goal is None or goal_hash is not None else len(goal),
+                    0 if goal is None else (custom if goal_hash is not None else 1), 0 if goal is None or goal_hash is not None else len(goal),
                     _p(go), _p(gl), kind, int(not prefer_more_satisfied_goals),
                     seed, max_next_layer_states or 0, beam_width or 0, int(randomize_ties), int(record_events), cb, None,
                     goal_hash[0] if goal_hash else 0, goal_hash[1] if goal_hash else 0)

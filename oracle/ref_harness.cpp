@@ -131,7 +131,7 @@ struct mref_brfs_options
     void (*scorer)(void* user, const uint64_t* rows, uint64_t n, uint32_t words, double* scores);
     void* scorer_user;
     // goal_kind 2: GoalSpec::Custom, a state is a goal iff its hash_state % goal_mod == goal_res (a test that no atom
-    // goal expresses)
+    // goal expresses); goal_kind 3: GoalSpec::Custom, iff the state has goal_res true atoms
     uint64_t goal_mod;
     uint64_t goal_res;
 };
@@ -837,6 +837,13 @@ int mref_brfs(mref_task* t, const mref_brfs_options* o, mref_brfs_result* r, uin
                 b.goal.kind = search::GoalSpec::Kind::Custom;
                 const uint64_t m = o->goal_mod, res = o->goal_res;
                 b.goal.test = [m, res](StateView s) { return s.hash() % m == res; };
+            }
+            else if (o->goal_kind == 3)
+            {
+                // a custom test that no slot numbering changes: the number of true atoms is goal_res
+                b.goal.kind = search::GoalSpec::Kind::Custom;
+                const uint64_t k = o->goal_res;
+                b.goal.test = [k](StateView s) { return s.count() == k; };
             }
             b.canonical_order = o->canonical_order != 0;
             b.stop_at_goal = o->stop_at_goal != 0;

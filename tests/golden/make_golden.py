@@ -726,22 +726,32 @@ def make_brfs_edges():
 
 
 # BrfsOptions::goal as GoalSpec::Custom: a state is a goal iff hash_state(state) % m == r (no atom goal expresses it),
-# through the ground driver (gripper) and the wide one (20-word transport rows)
+# through the ground driver (gripper) and the wide one (20-word transport rows); and, under lazy slots (whose row layout
+# is the device's own), iff the state has k true atoms, a test no slot numbering changes
 CUSTOM_GOAL_CASES = {
-    "gripper__prob05:goal": ("gripper__prob05", (1000, 7), dict(stop_at_goal=True)),
-    "gripper__prob05:all": ("gripper__prob05", (1000, 7), dict(stop_at_goal=False)),
-    "gripper__prob05:cut": ("gripper__prob05", (97, 5), dict(stop_at_goal=False, max_states=30000)),
-    "transport_w20_3:goal": ("transport_w20_3", (500, 3), dict(stop_at_goal=True)),
-    "transport_w20_3:cut": ("transport_w20_3", (61, 2), dict(stop_at_goal=False, max_states=40000)),
+    "gripper__prob05:goal": ("gripper__prob05", "auto", {"goal_hash": (1000, 7)}, dict(stop_at_goal=True)),
+    "gripper__prob05:all": ("gripper__prob05", "auto", {"goal_hash": (1000, 7)}, dict(stop_at_goal=False)),
+    "gripper__prob05:cut": ("gripper__prob05", "auto", {"goal_hash": (97, 5)}, dict(stop_at_goal=False, max_states=30000)),
+    "transport_w20_3:goal": ("transport_w20_3", "auto", {"goal_hash": (500, 3)}, dict(stop_at_goal=True)),
+    "transport_w20_3:cut": ("transport_w20_3", "auto", {"goal_hash": (61, 2)}, dict(stop_at_goal=False, max_states=40000)),
+    "blocks__probBLOCKS-8-0:lazy_goal": ("blocks__probBLOCKS-8-0", "lazy", {"goal_atoms": 10}, dict(stop_at_goal=True)),
+    "blocks__probBLOCKS-8-0:lazy_cut": ("blocks__probBLOCKS-8-0", "lazy", {"goal_atoms": 12},
+                                        dict(stop_at_goal=False, max_states=30000)),
 }
 
 
 def make_brfs_custom_goal():
     """The reference brfs() with a custom goal test (brfs_custom_goal.json)."""
     out = {}
-    for key, (name, gh, kw) in CUSTOM_GOAL_CASES.items():
-        r = brfs_record(name, "auto", goal_hash=gh, **kw)
-        r["goal_hash"] = list(gh)
+    for key, (name, atoms, test, kw) in CUSTOM_GOAL_CASES.items():
+        r = brfs_record(name, atoms, **test, **kw)
+        r.update({k: list(v) if isinstance(v, tuple) else v for k, v in test.items()})
+        r["atoms"] = atoms
+        if atoms == "lazy" and "goal_state" in r:
+            # the goal state's atoms by canonical id (the device numbers lazy slots in its own order)
+            t = ref.RefTask(fx.task_path(name), "lazy")
+            ref.brfs(t, **test, **kw)
+            r["goal_cids"] = goal_cids(t, r["goal_state"])
         out[key] = r
         print(key, r["states"], r["expanded"], r["goal_states"], r["status"], len(r.get("plan", [])), flush=True)
     dump("brfs_custom_goal.json", out)
